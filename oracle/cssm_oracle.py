@@ -1,0 +1,722 @@
+"""CPU restatement of the CSSM spectral state-space layer (gated and GDN cells).
+
+TEST INFRASTRUCTURE ONLY.  This module is the parity checker for the HIP
+kernels in ``cssm_amd``.  Only ``tests/``, ``__graft_entry__.smoke()`` and the
+``cpu_baseline`` leg of ``bench.py`` may import it, and only as the checker or
+the reported CPU baseline -- never as the thing that is measured or shipped.
+The product path (``cssm_amd``) never imports this file.
+
+It restates, in float64 numpy, the algorithm of the reference JAX/Flax code
+(``/root/reference`` = drewlinsley/CSSM, read as text; JAX/Flax are not
+installed here, so the reference itself cannot be run).  Every function cites
+the reference lines it follows.
+
+Pinning (see ``tests/test_oracle.py``): numpy pocketfft vs a brute-force DFT
+matrix evaluation (incl. odd / non-power-of-2 sizes), the K=1 closed form of
+the spectral kernel, the T=1 closed form of the gated core, the static-gate
+geometric-series closed form of the recurrence, a faithful GOOM log-space scan
+(to_goom / log_add_exp with the reference floors) against the linear scan,
+circular-shift equivariance, causality, the GDN T=1 closed form, the unit
+key-norm invariant, and the reference's published parameter counts.
+"""
+from __future__ import annotations
+
+import math
+from dataclasses import dataclass, field
+from typing import Dict, Optional
+
+import numpy as np
+
+# ---------------------------------------------------------------------------
+# numerics helpers
+# ---------------------------------------------------------------------------
+
+GOOM_EPS = 1e-7                                   # goom.py:161 (to_goom eps)
+FLT_MIN = float(np.finfo(np.float32).tiny)        # jnp.finfo(float32).smallest_normal
+GOOM_FINITE_FLOOR = 2.0 * math.log(FLT_MIN)       # goom.py:99-100  (= -174.67)
+
+
+def silu(x):
+    """jax.nn.silu: x * sigmoid(x)."""
+    return x * sigmoid(x)
+
+
+def sigmoid(x):
+    x = np.asarray(x, dtype=np.float64)
+    return 0.5 * (1.0 + np.tanh(0.5 * x))
+
+
+def softplus(x):
+    """jax.nn.softplus = logaddexp(x, 0)."""
+    return np.logaddexp(x, 0.0)
+
+
+def gate_activation(x, kind: str):
+    """GatedCSSM._compute_gate (cssm.py:432-441)."""
+    if kind == 'softplus':
+        return softplus(x)
+    if kind == 'sigmoid':
+        return sigmoid(x) * 2.0
+    if kind == 'exp':
+        return np.exp(np.clip(x, -4.0, 2.0))
+    return softplus(x)
+
+
+def stable_spectral_magnitude(K, rho=0.999):
+    """_stable_spectral_magnitude (cssm.py:29-46): K * rho / (1 + |K|)."""
+    return K * rho / (1.0 + np.abs(K))
+
+
+def rms_norm(x, weight, eps=1e-6):
+    """_rms_norm (cssm.py:49-52): x * rsqrt(mean(x^2, -1) + eps) * weight."""
+    ms = np.mean(x ** 2, axis=-1, keepdims=True)
+    return x / np.sqrt(ms + eps) * weight
+
+
+def layer_norm(x, scale, bias, eps=1e-6):
+    """flax.linen.LayerNorm over the last axis (epsilon 1e-6)."""
+    mu = np.mean(x, axis=-1, keepdims=True)
+    var = np.mean((x - mu) ** 2, axis=-1, keepdims=True)
+    return (x - mu) / np.sqrt(var + eps) * scale + bias
+
+
+def goom_floor(x):
+    """to_goom's complex-safe floor (goom.py:161-174): |x| < 1e-7 -> 1e-7 + 0j."""
+    x = np.asarray(x, dtype=np.complex128)
+    return np.where(np.abs(x) < GOOM_EPS, GOOM_EPS + 0j, x)
+
+
+def to_goom(x):
+    """to_goom + goom_log (goom.py:89-137, 144-178): floored complex log."""
+    lg = np.log(goom_floor(x))
+    re = np.where(lg.real < GOOM_FINITE_FLOOR, GOOM_FINITE_FLOOR, lg.real)
+    return re + 1j * lg.imag
+
+
+def from_goom(lx):
+    """from_goom (goom.py:181-196): complex exp."""
+    return np.exp(lx)
+
+
+def log_add_exp(a, b):
+    """operations.log_add_exp (operations.py:17-41): max shift, exp, add, floored log."""
+    c = np.maximum(a.real, b.real)
+    s = from_goom(a - c) + from_goom(b - c)
+    return to_goom(s) + c
+
+
+def dense(x, p):
+    """flax.linen.Dense: x @ kernel + bias (kernel shape (in, out))."""
+    y = np.tensordot(x, p['kernel'], axes=([-1], [0]))
+    if 'bias' in p:
+        y = y + p['bias']
+    return y
+
+
+def same_pad(k):
+    """lax 'SAME' padding for stride 1: low=(k-1)//2, high=k//2."""
+    return (k - 1) // 2, k // 2
+
+
+def depthwise_conv2d_same(x, p):
+    """nn.Conv(C, (k,k), feature_group_count=C, padding='SAME') on (N,H,W,C).
+
+    Cross-correlation (no flip); kernel HWIO (k,k,1,C); bias (C,).
+    """
+    kern = p['kernel']
+    kh, kw = kern.shape[0], kern.shape[1]
+    lo_h, hi_h = same_pad(kh)
+    lo_w, hi_w = same_pad(kw)
+    N, H, W, C = x.shape
+    xp = np.pad(x, ((0, 0), (lo_h, hi_h), (lo_w, hi_w), (0, 0)))
+    out = np.zeros_like(x, dtype=np.float64)
+    for i in range(kh):
+        for j in range(kw):
+            out += xp[:, i:i + H, j:j + W, :] * kern[i, j, 0, :]
+    if 'bias' in p:
+        out = out + p['bias']
+    return out
+
+
+def full_conv2d_same(x, p):
+    """nn.Conv(Cout, (k,k), padding='SAME') with full channel mixing; kernel (k,k,Cin,Cout)."""
+    kern = p['kernel']
+    kh, kw = kern.shape[0], kern.shape[1]
+    lo_h, hi_h = same_pad(kh)
+    lo_w, hi_w = same_pad(kw)
+    N, H, W, C = x.shape
+    xp = np.pad(x, ((0, 0), (lo_h, hi_h), (lo_w, hi_w), (0, 0)))
+    out = np.zeros((N, H, W, kern.shape[3]), dtype=np.float64)
+    for i in range(kh):
+        for j in range(kw):
+            out += np.tensordot(xp[:, i:i + H, j:j + W, :], kern[i, j], axes=([-1], [0]))
+    if 'bias' in p:
+        out = out + p['bias']
+    return out
+
+
+def causal_conv_t(x5, p):
+    """Causal depthwise temporal conv (cssm.py:494-500, 4766-4776).
+
+    x5 (B,T,H,W,C); kernel (k,1,C); out[t] = sum_j w_j x[t-k+1+j] + b, zeros for t<0.
+    """
+    kern = p['kernel']
+    k = kern.shape[0]
+    B, T, H, W, C = x5.shape
+    xp = np.concatenate([np.zeros((B, k - 1, H, W, C)), x5], axis=1)
+    out = np.zeros_like(x5, dtype=np.float64)
+    for j in range(k):
+        out += xp[:, j:j + T] * kern[j, 0, :]
+    if 'bias' in p:
+        out = out + p['bias']
+    return out
+
+
+# ---------------------------------------------------------------------------
+# FFT conventions (jnp.fft.rfft2 / irfft2 = numpy pocketfft semantics)
+# ---------------------------------------------------------------------------
+
+def rfft2(x):
+    """Unnormalised forward real 2-D FFT over the last two axes (cssm.py:533)."""
+    return np.fft.rfft2(np.asarray(x, dtype=np.float64), axes=(-2, -1))
+
+
+def irfft2(X, H, W):
+    """irfft2(X, s=(H,W)) over the last two axes (cssm.py:577).
+
+    C2R rule: complex inverse over H, then a real inverse over W that keeps only
+    Re of the v=0 column (and of v=W/2 for even W).
+    """
+    return np.fft.irfft2(np.asarray(X, dtype=np.complex128), s=(H, W), axes=(-2, -1))
+
+
+def rfft2_bruteforce(x):
+    """Brute-force DFT-matrix evaluation of rfft2 (for pinning pocketfft)."""
+    x = np.asarray(x, dtype=np.float64)
+    H, W = x.shape[-2:]
+    Wf = W // 2 + 1
+    FH = np.exp(-2j * np.pi * np.outer(np.arange(H), np.arange(H)) / H)
+    FW = np.exp(-2j * np.pi * np.outer(np.arange(W), np.arange(Wf)) / W)
+    return np.einsum('uh,...hw,wv->...uv', FH, x, FW)
+
+
+def irfft2_bruteforce(X, H, W):
+    """Brute-force evaluation of the C2R rule written out in closed form.
+
+    Z[h,v] = (1/H) sum_u X[u,v] e^{+2pi i u h/H}
+    y[h,w] = (1/W) [Re Z[h,0] + 2 sum_{0<v<W/2} Re(Z[h,v] e^{2pi i v w/W})
+                    + (W even) (-1)^w Re Z[h,W/2]]
+    """
+    X = np.asarray(X, dtype=np.complex128)
+    Wf = W // 2 + 1
+    FHi = np.exp(2j * np.pi * np.outer(np.arange(H), np.arange(H)) / H) / H
+    Z = np.einsum('hu,...uv->...hv', FHi, X)
+    w = np.arange(W)
+    y = np.repeat(Z[..., :, 0:1].real, W, axis=-1).astype(np.float64)
+    vmax = (W - 1) // 2  # last fully doubled bin
+    for v in range(1, vmax + 1):
+        y = y + 2.0 * (Z[..., :, v:v + 1] * np.exp(2j * np.pi * v * w / W)).real
+    if W % 2 == 0:
+        y = y + Z[..., :, Wf - 1:Wf].real * ((-1.0) ** w)
+    return y / W
+
+
+# ---------------------------------------------------------------------------
+# spectral kernel
+# ---------------------------------------------------------------------------
+
+def pad_kernel(k, H, W):
+    """Kernel pad / crop rule (cssm.py:510-526, GDN pad_kernel 4698-4709).
+
+    K <= H: zero-pad with pad_before = (H-K)//2; K > H: centre crop at (K-H)//2.
+    k: (C, K, K) -> (C, H, W).
+    """
+    K = k.shape[-1]
+    if K > H or K > W:
+        sh = (K - H) // 2
+        sw = (K - W) // 2
+        return k[:, sh:sh + H, sw:sw + W]
+    ph = max(0, (H - K) // 2)
+    pw = max(0, (W - K) // 2)
+    return np.pad(k, ((0, 0), (ph, max(0, H - K - ph)), (pw, max(0, W - K - pw))))
+
+
+def spectral_kernel(k, H, W, rho=0.999, squash=True):
+    """K_hat = rho * F / (1 + |F|), F = rfft2(pad(k)) (cssm.py:505-529, 4711-4716)."""
+    F = rfft2(pad_kernel(np.asarray(k, dtype=np.float64), H, W))
+    return stable_spectral_magnitude(F, rho) if squash else F
+
+
+# ---------------------------------------------------------------------------
+# scans
+# ---------------------------------------------------------------------------
+
+def linear_scalar_scan(A, V):
+    """h_t = A_t h_{t-1} + V_t over axis 1, h_{-1} = 0 (the algebra of cssm.py:570-575)."""
+    h = np.zeros_like(V[:, 0])
+    out = np.empty_like(V)
+    for t in range(V.shape[1]):
+        h = A[:, t] * h + V[:, t]
+        out[:, t] = h
+    return out
+
+
+def goom_scalar_scan(K_log, U_log):
+    """Faithful log-space prefix over axis 1 with cssm_scalar_scan_op (math.py:24-54).
+
+    Evaluated sequentially (the associative scan computes the same prefix up to
+    rounding order): (k, u) o (k', u') = (k + k', log_add_exp(k' + u, u')).
+    """
+    k = K_log[:, 0]
+    u = U_log[:, 0]
+    out = np.empty_like(U_log)
+    out[:, 0] = u
+    for t in range(1, U_log.shape[1]):
+        kj, uj = K_log[:, t], U_log[:, t]
+        u = log_add_exp(kj + u, uj)
+        k = kj + k
+        out[:, t] = u
+    return out
+
+
+# ---------------------------------------------------------------------------
+# gated cell (GatedCSSM._forward_depthwise, cssm.py:476-585)
+# ---------------------------------------------------------------------------
+
+@dataclass
+class GatedConfig:
+    """GatedCSSM attributes (cssm.py:416-430) + the build's `expand` (A.6 of the design)."""
+    channels: int
+    kernel_size: int = 15
+    spectral_rho: float = 0.999
+    gate_activation: str = 'softplus'
+    rope_mode: str = 'none'
+    short_conv_size: int = 4
+    short_conv_spatial_size: int = 3
+    gate_type: str = 'dense'
+    dense_mixing: bool = False
+    expand: int = 1
+
+
+def gated_gates(ctx, params, cfg: GatedConfig, H, W):
+    """Per-frequency gates from ctx (cssm.py:536-556): returns (Delta, G_B, G_C), each (B,T,H,Wf)."""
+    Wf = W // 2 + 1
+    B, T, _ = ctx.shape
+
+    def make(name):
+        if cfg.gate_type == 'factored':
+            gh = dense(ctx, params[f'{name}_h'])
+            gw = dense(ctx, params[f'{name}_w'])
+            return gh[..., :, None] * gw[..., None, :]
+        return dense(ctx, params[name]).reshape(B, T, H, Wf)
+
+    delta = gate_activation(make('delta_proj'), cfg.gate_activation)
+    return delta, make('B_proj'), make('C_proj')
+
+
+def gated_core(xm_act, z_gate, khat, delta, gB, gC, scan='linear'):
+    """The spectral core between the in_proj split and out_proj (cssm.py:531-581).
+
+    xm_act: (B,T,C,H,W) post-activation x_main (plane-major)
+    z_gate: (B,T,C,H,W) multiplier applied after irfft2 (= SiLU(z)), or None
+    khat  : (C,H,Wf) complex squashed spectral kernel
+    delta, gB, gC: (B,T,H,Wf) gates (broadcast over C)
+    Returns (B,T,C,H,W) = irfft2(gC * h) * z_gate with h_t = A_t h_{t-1} + V_t,
+    A = floor(K_hat) e^{-Delta}, V = (Delta + 1e-8) floor(gB * U_hat).
+    scan='goom' evaluates the recurrence exactly as the reference does, in GOOM log space.
+    """
+    B, T, C, H, W = xm_act.shape
+    U = rfft2(xm_act)                                   # (B,T,C,H,Wf)
+    d = delta[:, :, None]
+    if scan == 'goom':
+        K_log = to_goom(khat)[None, None]               # cssm.py:559-560
+        K_log = np.broadcast_to(K_log, U.shape)
+        U_log = to_goom(U * gB[:, :, None])             # cssm.py:562-563
+        K_g = (K_log.real - d) + 1j * K_log.imag        # cssm.py:566
+        U_g = (U_log.real + np.log(d + 1e-8)) + 1j * U_log.imag  # cssm.py:567
+        X = from_goom(goom_scalar_scan(K_g, U_g))       # cssm.py:570-575
+    else:
+        A = goom_floor(khat)[None, None] * np.exp(-d)
+        V = (d + 1e-8) * goom_floor(U * gB[:, :, None])
+        X = linear_scalar_scan(A, V)
+    Y = X * gC[:, :, None]                              # cssm.py:576
+    y = irfft2(Y, H, W)                                 # cssm.py:577
+    if z_gate is not None:
+        y = y * z_gate
+    return y
+
+
+def gated_forward(params, x, cfg: GatedConfig, scan='linear', return_intermediates=False):
+    """GatedCSSM forward (cssm.py:443-474, 476-585); x (B,T,H,W,C_in) channels-last."""
+    if cfg.rope_mode != 'none':
+        raise NotImplementedError('rope_mode != none is outside the restated path')
+    if cfg.dense_mixing:
+        raise NotImplementedError('dense_mixing is outside the restated path')
+    x = np.asarray(x, dtype=np.float64)
+    B, T, H, W, Cin = x.shape
+    Ci = cfg.channels * cfg.expand
+    xz = dense(x, params['in_proj'])                    # cssm.py:481
+    x_main, z = xz[..., :Ci], xz[..., Ci:]              # cssm.py:483-484
+    if cfg.short_conv_spatial_size > 0:                 # cssm.py:487-492
+        x_main = depthwise_conv2d_same(x_main.reshape(B * T, H, W, Ci),
+                                       params['short_conv_spatial']).reshape(B, T, H, W, Ci)
+    if cfg.short_conv_size > 0:                         # cssm.py:494-500
+        x_main = causal_conv_t(x_main, params['short_conv_temporal'])
+    x_main = silu(x_main)                               # cssm.py:502
+    khat = spectral_kernel(params['kernel'], H, W, cfg.spectral_rho)   # cssm.py:505-529
+    ctx = x_main.mean(axis=(2, 3))                      # cssm.py:536
+    delta, gB, gC = gated_gates(ctx, params, cfg, H, W)
+    xm_pm = x_main.transpose(0, 1, 4, 2, 3)             # cssm.py:532
+    zg_pm = silu(z).transpose(0, 1, 4, 2, 3)            # cssm.py:581 (SiLU(z))
+    y_pm = gated_core(xm_pm, zg_pm, khat, delta, gB, gC, scan=scan)
+    y = y_pm.transpose(0, 1, 3, 4, 2)                   # cssm.py:578
+    out = dense(y, params['out_proj'])                  # cssm.py:584
+    if return_intermediates:
+        return out, dict(x_main=x_main, z=z, ctx=ctx, khat=khat, delta=delta, gB=gB, gC=gC,
+                         y_core=y_pm)
+    return out
+
+
+def gated_param_shapes(cfg: GatedConfig, c_in, H, W) -> Dict[str, Dict[str, tuple]]:
+    """Parameter tree of GatedCSSM (Flax names; Dense kernel (in,out), Conv HWIO)."""
+    Ci = cfg.channels * cfg.expand
+    Wf = W // 2 + 1
+    s = {'in_proj': {'kernel': (c_in, 2 * Ci), 'bias': (2 * Ci,)}}
+    if cfg.short_conv_spatial_size > 0:
+        k = cfg.short_conv_spatial_size
+        s['short_conv_spatial'] = {'kernel': (k, k, 1, Ci), 'bias': (Ci,)}
+    if cfg.short_conv_size > 0:
+        s['short_conv_temporal'] = {'kernel': (cfg.short_conv_size, 1, Ci), 'bias': (Ci,)}
+    s['kernel'] = (Ci, cfg.kernel_size, cfg.kernel_size)
+    for g in ('delta_proj', 'B_proj', 'C_proj'):
+        if cfg.gate_type == 'factored':
+            s[f'{g}_h'] = {'kernel': (Ci, H), 'bias': (H,)}
+            s[f'{g}_w'] = {'kernel': (Ci, Wf), 'bias': (Wf,)}
+        else:
+            s[g] = {'kernel': (Ci, H * Wf), 'bias': (H * Wf,)}
+    s['out_proj'] = {'kernel': (Ci, cfg.channels), 'bias': (cfg.channels,)}
+    return s
+
+
+# ---------------------------------------------------------------------------
+# GDN cell (GatedDeltaNetCSSM slow path, cssm.py:4685-5141)
+# ---------------------------------------------------------------------------
+
+@dataclass
+class GDNConfig:
+    """GatedDeltaNetCSSM attributes used by the slow path (cssm.py:4298-4338)."""
+    channels: int
+    delta_key_dim: int = 2
+    kernel_size: int = 11
+    rope_mode: str = 'none'
+    rope_base: float = 10000.0
+    spectral_rho: float = 0.999
+    gate_type: str = 'channel'
+    use_goom: bool = True
+    use_log: bool = True
+    short_conv_size: int = 4
+    output_norm: str = 'rms'
+    use_input_gates: bool = True
+    output_gate_act: str = 'silu'
+    use_spectral_l2_norm: bool = True
+    qkv_conv_size: int = 1
+    qkv_conv_separable: bool = True
+    cross_freq_conv_size: int = 0
+    no_spectral_clamp: bool = False
+    int_attention_mode: str = 'none'
+    gate_proj_bias_init: float = 0.0
+
+
+def temporal_context_encoding(T, C, base=10000.0):
+    """apply_temporal_rope_to_context's additive table E (cssm.py:353-383): E[t,2j]=sin, E[t,2j+1]=cos."""
+    t_pos = np.arange(T, dtype=np.float64)
+    dim = np.arange(0, C, 2, dtype=np.float64)
+    inv_freq = 1.0 / (base ** (dim / C))
+    theta = np.outer(t_pos, inv_freq)
+    return np.stack([np.sin(theta), np.cos(theta)], axis=-1).reshape(T, C)
+
+
+def gdn_gate(name, params, cfg: GDNConfig, ctx, gate_input, H, W, bounded=False, spatial=False):
+    """_gate (cssm.py:4798-4842)."""
+    B, T, C = ctx.shape
+    dk = cfg.delta_key_dim
+    nh = C // dk
+    Wf = W // 2 + 1
+    gt = cfg.gate_type
+    if gt == 'channel':
+        if spatial:
+            # nn.Conv(C, (1,1)) on the gate input: a per-pixel Dense C->C (kernel (1,1,C,C))
+            pc = params[name]
+            p2 = {'kernel': pc['kernel'].reshape(pc['kernel'].shape[-2], pc['kernel'].shape[-1]),
+                  'bias': pc['bias']}
+            return sigmoid(dense(gate_input, p2))                       # (B,T,H,W,C)
+        raw = sigmoid(dense(ctx, params[name])).reshape(B, T, nh, 1, 1)
+        return 0.1 + 0.89 * raw if bounded else raw
+    if gt == 'factored':
+        if spatial:
+            row = dense(ctx, params[f'{name}_h'])
+            col = dense(ctx, params[f'{name}_w'])
+            return sigmoid(row[..., :, None] + col[..., None, :]).reshape(B, T, H, W, 1)
+        row = dense(ctx, params[f'{name}_h'])
+        col = dense(ctx, params[f'{name}_w'])
+        raw = sigmoid(row[..., :, None] + col[..., None, :]).reshape(B, T, 1, H, Wf)
+        return 0.1 + 0.89 * raw if bounded else raw
+    if gt == 'scalar':
+        raw = sigmoid(dense(ctx, params[name])).reshape(B, T, 1, 1, 1)
+        if spatial:
+            return raw
+        return 0.1 + 0.89 * raw if bounded else raw
+    # 'dense'
+    if spatial:
+        return sigmoid(dense(ctx, params[name])).reshape(B, T, H, W, 1)
+    raw = sigmoid(dense(ctx, params[name])).reshape(B, T, 1, H, Wf)
+    return 0.1 + 0.89 * raw if bounded else raw
+
+
+def gdn_prologue(params, x, cfg: GDNConfig):
+    """Everything of the GDN slow path before the rfft2 (cssm.py:4713-4869).
+
+    Returns dict with q_in, k_in, v_in (B,T,H,W,C), gate_val (B,T,H,W,C),
+    alpha, beta (broadcastable to (B,T,n_h|1,H|1,Wf|1)), W_hat (n_h,H,Wf).
+    """
+    if cfg.rope_mode not in ('none', 'learned_t'):
+        raise NotImplementedError('rope_mode other than none/learned_t is outside the restated path')
+    x = np.asarray(x, dtype=np.float64)
+    B, T, H, W, C = x.shape
+    dk = cfg.delta_key_dim
+    assert C % dk == 0
+    W_hat = spectral_kernel(params['kernel'], H, W, cfg.spectral_rho,
+                            squash=not cfg.no_spectral_clamp)          # cssm.py:4711-4716
+    x_flat = x.reshape(B * T, H, W, C)
+    if cfg.qkv_conv_size > 1:                                           # cssm.py:4740-4754
+        if cfg.qkv_conv_separable:
+            qkv = dense(depthwise_conv2d_same(x_flat, params['qkv_dw']), params['qkv_proj'])
+        else:
+            qkv = full_conv2d_same(x_flat, params['qkv_proj'])
+    else:
+        qkv = dense(x_flat, params['qkv_proj'])
+    qkv = qkv.reshape(B, T, H, W, 3 * C)
+    q_in, k_in, v_in = qkv[..., :C], qkv[..., C:2 * C], qkv[..., 2 * C:]
+    if cfg.short_conv_size > 0:                                          # cssm.py:4763-4780
+        q_in = silu(causal_conv_t(q_in, params['short_conv_q']))
+        k_in = silu(causal_conv_t(k_in, params['short_conv_k']))
+        v_in = silu(causal_conv_t(v_in, params['short_conv_v']))
+    ctx = x.mean(axis=(2, 3))                                            # cssm.py:4785
+    if cfg.rope_mode == 'learned_t':
+        ctx = ctx + params['temporal_embed'][None]                       # cssm.py:4787-4791
+    else:
+        ctx = ctx + temporal_context_encoding(T, C, cfg.rope_base)[None]  # cssm.py:4793
+    if cfg.use_input_gates:                                              # cssm.py:4844-4848
+        k_in = k_in * gdn_gate('B_k', params, cfg, ctx, x, H, W, spatial=True)
+        v_in = v_in * gdn_gate('B_v', params, cfg, ctx, x, H, W, spatial=True)
+    gv = dense(x_flat, params['gate_proj']).reshape(B, T, H, W, C)      # cssm.py:4853-4855
+    gate_val = silu(gv) if cfg.output_gate_act == 'silu' else sigmoid(gv)
+    alpha = gdn_gate('alpha', params, cfg, ctx, x, H, W, bounded=True)   # cssm.py:4864
+    beta = gdn_gate('beta', params, cfg, ctx, x, H, W)                   # cssm.py:4865
+    return dict(q_in=q_in, k_in=k_in, v_in=v_in, gate_val=gate_val, alpha=alpha,
+                beta=beta, W_hat=W_hat, ctx=ctx)
+
+
+def _gate_bins(g, B, T, nh, H, Wf):
+    """alpha/beta broadcast to (B,T,n_h,H,Wf): 'channel' gates are (B,T,n_h,1,1),
+    the others (B,T,1,H,Wf) or (B,T,1,1,1) (cssm.py:4918-4923)."""
+    return np.broadcast_to(g, (B, T, nh, H, Wf))
+
+
+def gdn_spectral_norms(q_spec, k_spec, cfg: GDNConfig):
+    """Spectral and key-vector L2 norms (cssm.py:4890-4906); specs (B,T,nh,dk,H,Wf)."""
+    def spec_norm(z):
+        if not cfg.use_spectral_l2_norm:
+            return z
+        n = np.sqrt(np.sum(np.abs(z) ** 2, axis=(4, 5), keepdims=True) + 1e-6)
+        return z / n
+    k = spec_norm(k_spec)
+    k = k / np.sqrt(np.sum(np.abs(k) ** 2, axis=3, keepdims=True) + 1e-6)
+    return spec_norm(q_spec), k
+
+
+def gdn_core(q_in, k_in, v_in, alpha, beta, W_hat, cfg: GDNConfig, scan='linear'):
+    """rfft2 -> norms -> delta-rule matrix scan -> readout -> irfft2 (cssm.py:4875-5025).
+
+    q_in/k_in/v_in: (B,T,H,W,C) channels-last; returns o_spatial (B,T,C,H,W).
+    scan='linear': materialises M_t and Delta_t with the GOOM floors and runs the
+    complex linear recurrence s_t = M_t s_{t-1} + Delta_t[i,:] (exact algebra of the
+    log-space scan); scan='rank1': the same recurrence in rank-1 form without
+    materialising M (no floors on M entries), as the HIP kernel evaluates it.
+    """
+    B, T, H, W, C = q_in.shape
+    dk = cfg.delta_key_dim
+    dv = dk
+    nh = C // dk
+    Wf = W // 2 + 1
+
+    def heads(z):
+        return z.reshape(B, T, H, W, nh, dk).transpose(0, 1, 4, 5, 2, 3)
+    q_spec, k_spec, v_spec = rfft2(heads(q_in)), rfft2(heads(k_in)), rfft2(heads(v_in))
+    q_n, k_n = gdn_spectral_norms(q_spec, k_spec, cfg)
+    al = _gate_bins(alpha, B, T, nh, H, Wf)
+    be = _gate_bins(beta, B, T, nh, H, Wf)
+    if scan == 'linear':
+        a_bc = al[:, :, :, None, None]                                         # (B,T,nh,1,1,H,Wf)
+        b_bc = be[:, :, :, None, None]
+        Wh = W_hat[None, None, :, None, None, :, :]
+        k_outer = k_n[..., :, None, :, :] * np.conj(k_n[..., None, :, :, :])   # (B,T,nh,dk,dk,H,Wf)
+        I = np.eye(dk).reshape(1, 1, 1, dk, dk, 1, 1)
+        M = a_bc * Wh * (I - b_bc * k_outer)                                   # cssm.py:4925
+        vk = v_spec[..., :, None, :, :] * np.conj(k_n[..., None, :, :, :])    # (B,T,nh,dv,dk,H,Wf)
+        D = b_bc * vk                                                          # cssm.py:4927-4929
+        if cfg.use_log and cfg.use_goom:
+            M = goom_floor(M)                                                  # to_goom floors
+            D = goom_floor(D)
+        Mt = np.moveaxis(M, (3, 4), (5, 6))     # (B,T,nh,H,Wf,dk,dk)
+        Dt = np.moveaxis(D, (4,), (6,))         # (B,T,nh,dv,H,Wf,dk)
+        s = np.zeros((B, nh, dv, H, Wf, dk), dtype=np.complex128)
+        S = np.empty((B, T, nh, dv, H, Wf, dk), dtype=np.complex128)
+        for t in range(T):                      # s_t = M_t s_{t-1} + Delta_t[i,:] (math.py:384-411)
+            s = np.einsum('znuvab,zniuvb->zniuva', Mt[:, t], s) + Dt[:, t]
+            S[:, t] = s
+    else:
+        s = np.zeros((B, nh, dv, dk, H, Wf), dtype=np.complex128)   # s[..., i, a, u, v]
+        S = np.empty((B, T, nh, dv, H, Wf, dk), dtype=np.complex128)
+        for t in range(T):
+            kk = k_n[:, t]                                             # (B,nh,dk,H,Wf)
+            a_t = al[:, t][:, :, None, None]                           # (B,nh,1,1,H,Wf)
+            b_t = be[:, t][:, :, None, None]
+            khs = np.einsum('bnauv,bniauv->bniuv', np.conj(kk), s)     # k^H s_i
+            s = a_t * W_hat[None, :, None, None] * (s - b_t * kk[:, :, None] * khs[:, :, :, None])
+            s = s + b_t * v_spec[:, t][:, :, :, None] * np.conj(kk)[:, :, None]
+            S[:, t] = np.moveaxis(s, 3, 5)
+    q_read = q_n.transpose(0, 1, 2, 4, 5, 3)[:, :, :, None]              # cssm.py:4998
+    o_hat = np.sum(S * q_read, axis=-1).reshape(B, T, C, H, Wf)          # cssm.py:4999-5000
+    if cfg.cross_freq_conv_size > 0:
+        raise NotImplementedError('cross_freq_conv is outside the restated path')
+    return irfft2(o_hat, H, W)                                           # cssm.py:5025
+
+
+def gdn_forward(params, x, cfg: GDNConfig, scan='linear', return_intermediates=False):
+    """GatedDeltaNetCSSM slow-path forward (cssm.py:4685-5141)."""
+    if cfg.int_attention_mode != 'none':
+        raise NotImplementedError('InT attention modes are outside the restated path')
+    pro = gdn_prologue(params, x, cfg)
+    o = gdn_core(pro['q_in'], pro['k_in'], pro['v_in'], pro['alpha'], pro['beta'],
+                 pro['W_hat'], cfg, scan=scan)
+    out = o.transpose(0, 1, 3, 4, 2)                                     # cssm.py:5026
+    if cfg.output_norm == 'rms':
+        out = rms_norm(out, params['rms_scale'])                         # cssm.py:5029-5031
+    elif cfg.output_norm == 'layer':
+        out = layer_norm(out, params['output_layernorm']['scale'], params['output_layernorm']['bias'])
+    out = out * pro['gate_val']                                          # cssm.py:5126
+    res = dense(out, params['output_proj'])                              # cssm.py:5141
+    if return_intermediates:
+        pro['o_spatial'] = o
+        return res, pro
+    return res
+
+
+def gdn_param_shapes(cfg: GDNConfig, H, W) -> Dict[str, object]:
+    """Parameter tree of GatedDeltaNetCSSM's slow path (Flax names)."""
+    C = cfg.channels
+    dk = cfg.delta_key_dim
+    nh = C // dk
+    Wf = W // 2 + 1
+    s: Dict[str, object] = {'kernel': (nh, cfg.kernel_size, cfg.kernel_size)}
+    q = cfg.qkv_conv_size
+    if q > 1:
+        if cfg.qkv_conv_separable:
+            s['qkv_dw'] = {'kernel': (q, q, 1, C), 'bias': (C,)}
+            s['qkv_proj'] = {'kernel': (C, 3 * C), 'bias': (3 * C,)}
+        else:
+            s['qkv_proj'] = {'kernel': (q, q, C, 3 * C), 'bias': (3 * C,)}
+    else:
+        s['qkv_proj'] = {'kernel': (C, 3 * C), 'bias': (3 * C,)}
+    if cfg.short_conv_size > 0:
+        for n in ('q', 'k', 'v'):
+            s[f'short_conv_{n}'] = {'kernel': (cfg.short_conv_size, 1, C), 'bias': (C,)}
+    if cfg.rope_mode == 'learned_t':
+        s['temporal_embed'] = None   # (T, C): resolution of T known only at init
+    gt = cfg.gate_type
+
+    def gate(name, spatial):
+        if gt == 'channel':
+            if spatial:
+                s[name] = {'kernel': (1, 1, C, C), 'bias': (C,)}
+            else:
+                s[name] = {'kernel': (C, nh), 'bias': (nh,)}
+        elif gt == 'factored':
+            s[f'{name}_h'] = {'kernel': (C, H), 'bias': (H,)}
+            s[f'{name}_w'] = {'kernel': (C, W if spatial else Wf), 'bias': (W if spatial else Wf,)}
+        elif gt == 'scalar':
+            s[name] = {'kernel': (C, 1), 'bias': (1,)}
+        else:
+            n = H * W if spatial else H * Wf
+            s[name] = {'kernel': (C, n), 'bias': (n,)}
+    if cfg.use_input_gates:
+        gate('B_k', True)
+        gate('B_v', True)
+    s['gate_proj'] = {'kernel': (C, C), 'bias': (C,)}
+    gate('alpha', False)
+    gate('beta', False)
+    if cfg.output_norm == 'rms':
+        s['rms_scale'] = (C,)
+    elif cfg.output_norm == 'layer':
+        s['output_layernorm'] = {'scale': (C,), 'bias': (C,)}
+    s['output_proj'] = {'kernel': (C, C), 'bias': (C,)}
+    return s
+
+
+def count_params(shapes) -> int:
+    n = 0
+    for v in shapes.values():
+        if isinstance(v, dict):
+            n += count_params(v)
+        elif v is not None:
+            n += int(np.prod(v))
+    return n
+
+
+# ---------------------------------------------------------------------------
+# seeded parameter draws (reference init *distributions*; numpy PCG64)
+# ---------------------------------------------------------------------------
+
+def _fan_in(shape):
+    if len(shape) == 2:
+        return shape[0]
+    if len(shape) == 4:          # HWIO
+        return shape[0] * shape[1] * shape[2]
+    if len(shape) == 3:          # (k, 1, C) temporal conv: fan_in = k * 1
+        return shape[0] * shape[1]
+    return shape[0]
+
+
+def init_params(shapes, rng: np.random.Generator, bias_std=0.1, spectral_std=None,
+                spectral_init='normal', gate_proj_bias_init=None):
+    """Draw a parameter tree: lecun-normal kernels, N(0, bias_std^2) biases
+    (non-zero so the bias paths are exercised), spectral `kernel` N(0,0.02^2) (gated,
+    cssm.py:506-510) or xavier-normal (GDN, cssm.py:4717), `rms_scale` around 1."""
+    out = {}
+    for name, v in shapes.items():
+        if isinstance(v, dict):
+            sub = {}
+            for pn, shp in v.items():
+                if pn == 'kernel':
+                    std = 1.0 / math.sqrt(max(1, _fan_in(shp)))
+                    sub[pn] = rng.standard_normal(shp) * std
+                elif pn == 'scale':
+                    sub[pn] = 1.0 + 0.1 * rng.standard_normal(shp)
+                else:
+                    sub[pn] = rng.standard_normal(shp) * bias_std
+            out[name] = sub
+        elif v is None:
+            continue
+        elif name == 'kernel':
+            if spectral_init == 'xavier':
+                nh, K, _ = v
+                std = math.sqrt(2.0 / (2.0 * K * nh))
+            else:
+                std = 0.02 if spectral_std is None else spectral_std
+            out[name] = rng.standard_normal(v) * std
+        elif name == 'rms_scale':
+            out[name] = 1.0 + 0.1 * rng.standard_normal(v)
+        else:
+            out[name] = rng.standard_normal(v) * 0.1
+    return out
