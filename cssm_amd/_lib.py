@@ -1,0 +1,90 @@
+"""ctypes binding of libcssm_hip.so (the C ABI in include/cssm_amd.h).
+
+The library is built in-tree by ``cssm_amd.build``.  There is no fallback:
+if the library is missing or fails to load, every call raises.
+"""
+from __future__ import annotations
+
+import ctypes
+import os
+import threading
+
+LIB_PATH = os.path.join(os.path.dirname(os.path.abspath(__file__)), "libcssm_hip.so")
+
+CSSM_OK = 0
+F32, BF16 = 0, 1
+GATE_DENSE, GATE_FACTORED = 0, 1
+ACT_SOFTPLUS, ACT_SIGMOID2, ACT_EXP = 0, 1, 2
+LOAD_IDENTITY, LOAD_SILU = 0, 1
+
+_c_float_p = ctypes.POINTER(ctypes.c_float)
+
+
+class GateParams(ctypes.Structure):
+    """cssm_gate_params (include/cssm_amd.h)."""
+    _fields_ = [
+        ("gate_type", ctypes.c_int),
+        ("activation", ctypes.c_int),
+        ("kernel", ctypes.c_void_p * 3),
+        ("bias", ctypes.c_void_p * 3),
+        ("kernel_w", ctypes.c_void_p * 3),
+        ("bias_w", ctypes.c_void_p * 3),
+    ]
+
+
+# name -> (restype, argtypes); every symbol declared in include/cssm_amd.h
+SIGNATURES = {
+    "cssm_abi_version": (ctypes.c_int, []),
+    "cssm_strerror": (ctypes.c_char_p, [ctypes.c_int]),
+    "cssm_last_error": (ctypes.c_char_p, []),
+    "cssm_spectral_kernel": (ctypes.c_int, [ctypes.c_void_p, ctypes.c_int, ctypes.c_int, ctypes.c_int,
+                                            ctypes.c_int, ctypes.c_float, ctypes.c_int, ctypes.c_int,
+                                            ctypes.c_void_p, ctypes.c_void_p]),
+    "cssm_plane_mean": (ctypes.c_int, [ctypes.c_void_p, ctypes.c_int, ctypes.c_longlong, ctypes.c_int,
+                                       ctypes.c_int, ctypes.c_int, ctypes.c_void_p, ctypes.c_void_p]),
+    "cssm_gated_gates": (ctypes.c_int, [ctypes.c_void_p, ctypes.c_int, ctypes.c_int, ctypes.c_int,
+                                        ctypes.c_int, ctypes.c_int, ctypes.POINTER(GateParams),
+                                        ctypes.c_float, ctypes.c_void_p, ctypes.c_void_p]),
+    "cssm_gated_scan_fwd": (ctypes.c_int, [ctypes.c_void_p, ctypes.c_void_p, ctypes.c_void_p, ctypes.c_int,
+                                           ctypes.c_int, ctypes.c_int, ctypes.c_int, ctypes.c_int,
+                                           ctypes.c_int, ctypes.c_void_p, ctypes.c_void_p, ctypes.c_int,
+                                           ctypes.c_int, ctypes.c_void_p]),
+    "cssm_gated_scan_supported": (ctypes.c_int, [ctypes.c_int, ctypes.c_int]),
+}
+
+_lock = threading.Lock()
+_lib = None
+
+
+class CssmError(RuntimeError):
+    def __init__(self, fn: str, status: int, detail: str):
+        super().__init__(f"{fn} failed ({status}): {detail}")
+        self.status = status
+
+
+def load() -> ctypes.CDLL:
+    """Load (once) and return the HIP library; raises if it is not built."""
+    global _lib
+    with _lock:
+        if _lib is None:
+            if not os.path.exists(LIB_PATH):
+                raise RuntimeError(f"{LIB_PATH} is missing: build it with `python -m cssm_amd.build`")
+            lib = ctypes.CDLL(LIB_PATH)
+            for name, (res, args) in SIGNATURES.items():
+                fn = getattr(lib, name)
+                fn.restype = res
+                fn.argtypes = args
+            _lib = lib
+    return _lib
+
+
+def check(fn_name: str, status: int) -> None:
+    if status != CSSM_OK:
+        lib = load()
+        detail = lib.cssm_last_error().decode() or lib.cssm_strerror(status).decode()
+        raise CssmError(fn_name, status, detail)
+
+
+def call(fn_name: str, *args) -> None:
+    """Call an int-returning entry point and raise CssmError on failure."""
+    check(fn_name, getattr(load(), fn_name)(*args))

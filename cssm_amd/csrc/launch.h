@@ -1,0 +1,28 @@
+// Internal launcher declarations shared by the kernel files and the C ABI.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+namespace cssm {
+
+struct GateWeights {
+  const float* kd[3];
+  const float* bd[3];
+  const float* kw[3];
+  const float* bw[3];
+};
+
+hipError_t launch_spectral_kernel(const float* k, int C, int K, int H, int W, float rho, int squash,
+                                  int goom_floor, float2* khat, hipStream_t s);
+hipError_t launch_plane_mean(const void* x, int dtype, long long nplanes, int HW, int act, float* out,
+                             hipStream_t s);
+hipError_t launch_gated_gates(const float* ctx, int BT, int C, int H, int W, int factored, int act,
+                              const GateWeights& w, float c_scale, float4* gates, hipStream_t s);
+// returns hipErrorInvalidValue if no kernel exists for the shape
+bool gated_scan_has_kernel(int H, int W);
+hipError_t launch_gated_scan(const void* u, const void* z, void* y, int dtype, int B, int T, int C, int H,
+                             int W, const float4* gates, const float2* khat, int u_act, int z_act,
+                             hipStream_t s);
+
+}  // namespace cssm

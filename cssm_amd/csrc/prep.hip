@@ -1,0 +1,224 @@
+// Weight- and context-side kernels of the spectral layer (gfx950):
+//   * spectral kernel K_hat = rho * F / (1 + |F|), F = rfft2(pad(k))
+//   * per-frequency gates from the spatial mean ctx (dense or factored)
+//   * spatial mean of a plane-major tensor
+// These are small next to the fused scan; they run once per layer call.
+#include <hip/hip_runtime.h>
+#include <math.h>
+#include <stdint.h>
+
+#include "launch.h"
+
+namespace cssm {
+
+// ---------------------------------------------------------------------------
+// K_hat (cssm.py:505-529 gated, 4711-4716 GDN; _stable_spectral_magnitude :29-46)
+//
+// pad rule: K <= H -> zero pad with pad_before = (H-K)//2 (the tap (i,j) lands
+// at (i + ph, j + pw)); K > H -> centre crop starting at (K-H)//2.  The DFT of
+// the padded plane only needs the K x K (or cropped) taps, evaluated separably
+// in double precision.  One block per channel.
+// out: (C, H, W/2+1) complex, optionally GOOM-floored (|x| < 1e-7 -> 1e-7+0j).
+// ---------------------------------------------------------------------------
+__global__ void spectral_kernel_prep(const float* __restrict__ k, int K, int H, int W, float rho,
+                                     int squash, int goom_floor, float2* __restrict__ out) {
+  extern __shared__ double sm_d[];   // rows x WF complex (re, im)
+  const int c = blockIdx.x;
+  const int WF = W / 2 + 1;
+  // taps that survive: rows [r0, r0+nr) of k land on padded rows [oh, oh+nr)
+  // (the host rejects K between H and W, which the reference cannot run either)
+  int r0, nr, oh, q0, nq, ow;
+  if (K > H || K > W) {   // centre crop of both axes
+    r0 = (K - H) / 2; nr = H; oh = 0;
+    q0 = (K - W) / 2; nq = W; ow = 0;
+  } else {                // zero pad, tap (i, j) -> (i + (H-K)//2, j + (W-K)//2)
+    r0 = 0; nr = K; oh = (H - K) / 2;
+    q0 = 0; nq = K; ow = (W - K) / 2;
+  }
+  const float* kc = k + size_t(c) * K * K;
+  // stage 1: R[i][v] = sum_j k[i][j] e^{-2 pi i v (j') / W}
+  for (int idx = threadIdx.x; idx < nr * WF; idx += blockDim.x) {
+    const int i = idx / WF, v = idx % WF;
+    double re = 0.0, im = 0.0;
+    for (int j = 0; j < nq; ++j) {
+      const int jp = j + ow;
+      const long long m = (long long)v * jp % W;
+      double sn, cs;
+      sincospi(2.0 * double(m) / double(W), &sn, &cs);
+      const double kv = double(kc[(r0 + i) * K + (q0 + j)]);
+      re += kv * cs;
+      im -= kv * sn;
+    }
+    sm_d[2 * idx] = re;
+    sm_d[2 * idx + 1] = im;
+  }
+  __syncthreads();
+  // stage 2: F[u][v] = sum_i R[i][v] e^{-2 pi i u (i') / H}
+  for (int idx = threadIdx.x; idx < H * WF; idx += blockDim.x) {
+    const int u = idx / WF, v = idx % WF;
+    double re = 0.0, im = 0.0;
+    for (int i = 0; i < nr; ++i) {
+      const int ip = i + oh;
+      const long long m = (long long)u * ip % H;
+      double sn, cs;
+      sincospi(2.0 * double(m) / double(H), &sn, &cs);
+      const double ar = sm_d[2 * (i * WF + v)], ai = sm_d[2 * (i * WF + v) + 1];
+      // (ar + i ai)(cs - i sn)
+      re += ar * cs + ai * sn;
+      im += ai * cs - ar * sn;
+    }
+    if (squash) {
+      const double mag = sqrt(re * re + im * im);
+      const double f = double(rho) / (1.0 + mag);
+      re *= f;
+      im *= f;
+    }
+    float2 o = make_float2(float(re), float(im));
+    if (goom_floor) {
+      const float m2 = o.x * o.x + o.y * o.y;
+      if (m2 < 1e-14f) o = make_float2(1e-7f, 0.0f);
+    }
+    out[size_t(c) * H * WF + idx] = o;
+  }
+}
+
+// ---------------------------------------------------------------------------
+// Gates (cssm.py:536-556, _compute_gate :432-441, GOOM shifts :559-567).
+// One block per (b, t).  Output per bin (u, v) of the (H, W/2+1) half
+// spectrum, float4 = (exp(-Delta), Delta + 1e-8, B, C * c_scale), where
+//   Delta = act(G_delta), act in {softplus, 2*sigmoid, exp(clip(-4, 2))}
+//   dense:    G_x[u, v] = ctx . kernel[:, u*WF + v] + bias[u*WF + v]
+//   factored: G_x[u, v] = (ctx . kh[:, u] + bh[u]) * (ctx . kw[:, v] + bw[v])
+// ---------------------------------------------------------------------------
+// GateWeights (launch.h): kd/bd = dense kernel (C, H*WF) / bias (H*WF), or the
+// factored row kernel (C, H) / bias (H); kw/bw = factored column kernel (C, WF) / bias (WF).
+
+__device__ __forceinline__ float softplus_f(float x) {
+  // jax.nn.softplus = logaddexp(x, 0) = max(x, 0) + log1p(exp(-|x|))
+  return fmaxf(x, 0.0f) + log1pf(expf(-fabsf(x)));
+}
+
+__device__ __forceinline__ float gate_act(float x, int act) {
+  if (act == 1) return 2.0f / (1.0f + expf(-x));            // sigmoid * 2
+  if (act == 2) return expf(fminf(fmaxf(x, -4.0f), 2.0f));  // bounded exp
+  return softplus_f(x);
+}
+
+__global__ void gated_gates_kernel(const float* __restrict__ ctx, int C, int H, int W, int factored,
+                                   int act, GateWeights gw, float c_scale, float4* __restrict__ out) {
+  extern __shared__ float sm_f[];
+  const int WF = W / 2 + 1;
+  const int bt = blockIdx.x;
+  float* cx = sm_f;              // C
+  float* fac = sm_f + C;         // 3 * (H + WF) factored vectors
+  for (int i = threadIdx.x; i < C; i += blockDim.x) cx[i] = ctx[size_t(bt) * C + i];
+  __syncthreads();
+  const int nbin = H * WF;
+  if (factored) {
+    const int nv = 3 * (H + WF);
+    for (int idx = threadIdx.x; idx < nv; idx += blockDim.x) {
+      const int g = idx / (H + WF), r = idx % (H + WF);
+      float acc;
+      if (r < H) {
+        acc = gw.bd[g][r];
+        for (int c = 0; c < C; ++c) acc = fmaf(cx[c], gw.kd[g][size_t(c) * H + r], acc);
+      } else {
+        const int v = r - H;
+        acc = gw.bw[g][v];
+        for (int c = 0; c < C; ++c) acc = fmaf(cx[c], gw.kw[g][size_t(c) * WF + v], acc);
+      }
+      fac[idx] = acc;
+    }
+    __syncthreads();
+    for (int o = threadIdx.x; o < nbin; o += blockDim.x) {
+      const int u = o / WF, v = o % WF;
+      float gr[3];
+      for (int g = 0; g < 3; ++g) gr[g] = fac[g * (H + WF) + u] * fac[g * (H + WF) + H + v];
+      const float d = gate_act(gr[0], act);
+      out[size_t(bt) * nbin + o] = make_float4(expf(-d), d + 1e-8f, gr[1], gr[2] * c_scale);
+    }
+  } else {
+    for (int o = threadIdx.x; o < nbin; o += blockDim.x) {
+      float gr[3];
+      for (int g = 0; g < 3; ++g) {
+        float acc = gw.bd[g][o];
+        const float* kk = gw.kd[g] + o;
+        for (int c = 0; c < C; ++c) acc = fmaf(cx[c], kk[size_t(c) * nbin], acc);
+        gr[g] = acc;
+      }
+      const float d = gate_act(gr[0], act);
+      out[size_t(bt) * nbin + o] = make_float4(expf(-d), d + 1e-8f, gr[1], gr[2] * c_scale);
+    }
+  }
+}
+
+// ---------------------------------------------------------------------------
+// mean over (H, W) of each plane of a plane-major tensor (cssm.py:536),
+// optionally after SiLU.  One block per plane; bf16 or f32 input.
+// ---------------------------------------------------------------------------
+template <class TIN>
+__device__ __forceinline__ float load_as_f32(const TIN* p, size_t i);
+template <>
+__device__ __forceinline__ float load_as_f32<float>(const float* p, size_t i) { return p[i]; }
+template <>
+__device__ __forceinline__ float load_as_f32<uint16_t>(const uint16_t* p, size_t i) {
+  return __uint_as_float(uint32_t(p[i]) << 16);
+}
+
+template <class TIN>
+__global__ void plane_mean_kernel(const TIN* __restrict__ x, int HW, int act, float* __restrict__ out) {
+  __shared__ float red[32];
+  const size_t base = size_t(blockIdx.x) * HW;
+  float acc = 0.0f;
+  for (int i = threadIdx.x; i < HW; i += blockDim.x) {
+    float v = load_as_f32<TIN>(x, base + i);
+    if (act == 1) v = v / (1.0f + expf(-v));
+    acc += v;
+  }
+  for (int off = 32; off > 0; off >>= 1) acc += __shfl_down(acc, off, 64);
+  const int lane = threadIdx.x & 63, wid = threadIdx.x >> 6;
+  if (lane == 0) red[wid] = acc;
+  __syncthreads();
+  if (threadIdx.x == 0) {
+    float s = 0.0f;
+    for (int w = 0; w < int(blockDim.x >> 6); ++w) s += red[w];
+    out[blockIdx.x] = s / float(HW);
+  }
+}
+
+// ----------------------------------------------------------------- launchers
+
+hipError_t launch_spectral_kernel(const float* k, int C, int K, int H, int W, float rho, int squash,
+                                  int goom_floor, float2* khat, hipStream_t s) {
+  const int WF = W / 2 + 1;
+  const int rows = (K > H || K > W) ? H : K;
+  const size_t shm = size_t(rows) * WF * 2 * sizeof(double);
+  if (shm > 64 * 1024) return hipErrorInvalidValue;
+  hipLaunchKernelGGL(spectral_kernel_prep, dim3(C), dim3(256), shm, s, k, K, H, W, rho, squash,
+                     goom_floor, khat);
+  return hipGetLastError();
+}
+
+hipError_t launch_plane_mean(const void* x, int dtype, long long nplanes, int HW, int act, float* out,
+                             hipStream_t s) {
+  if (nplanes <= 0) return hipSuccess;
+  if (dtype == 0)
+    hipLaunchKernelGGL(plane_mean_kernel<float>, dim3(unsigned(nplanes)), dim3(256), 0, s,
+                       static_cast<const float*>(x), HW, act, out);
+  else
+    hipLaunchKernelGGL(plane_mean_kernel<uint16_t>, dim3(unsigned(nplanes)), dim3(256), 0, s,
+                       static_cast<const uint16_t*>(x), HW, act, out);
+  return hipGetLastError();
+}
+
+hipError_t launch_gated_gates(const float* ctx, int BT, int C, int H, int W, int factored, int act,
+                              const GateWeights& w, float c_scale, float4* gates, hipStream_t s) {
+  const int WF = W / 2 + 1;
+  const size_t shm = (size_t(C) + 3 * size_t(H + WF)) * sizeof(float);
+  if (shm > 64 * 1024) return hipErrorInvalidValue;
+  hipLaunchKernelGGL(gated_gates_kernel, dim3(BT), dim3(256), shm, s, ctx, C, H, W, factored, act, w,
+                     c_scale, gates);
+  return hipGetLastError();
+}
+
+}  // namespace cssm

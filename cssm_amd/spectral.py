@@ -1,0 +1,122 @@
+"""Torch-tensor wrappers over the C ABI: one function per ABI entry point.
+
+Tensors must live on the GPU; each call is enqueued on torch's current HIP
+stream.  Nothing here computes on the CPU and there is no fallback path.
+"""
+from __future__ import annotations
+
+from typing import Dict, Optional
+
+import torch
+
+from . import _lib
+
+_DTYPES = {torch.float32: _lib.F32, torch.bfloat16: _lib.BF16}
+_GATE_ACTS = {"softplus": _lib.ACT_SOFTPLUS, "sigmoid": _lib.ACT_SIGMOID2, "exp": _lib.ACT_EXP}
+
+
+def _stream() -> int:
+    return torch.cuda.current_stream().cuda_stream
+
+
+def _dev(t: torch.Tensor, name: str, dtype=None) -> torch.Tensor:
+    if not isinstance(t, torch.Tensor) or t.device.type != "cuda":
+        raise ValueError(f"{name} must be a GPU tensor")
+    if dtype is not None and t.dtype != dtype:
+        raise ValueError(f"{name} must be {dtype}, got {t.dtype}")
+    if not t.is_contiguous():
+        raise ValueError(f"{name} must be contiguous")
+    return t
+
+
+def spectral_kernel(k: torch.Tensor, H: int, W: int, rho: float = 0.999, squash: bool = True,
+                    goom_floor: bool = True) -> torch.Tensor:
+    """K_hat (C, H, W//2+1) complex64 from k (C, K, K) (cssm.py:505-529, 4711-4716)."""
+    _dev(k, "k", torch.float32)
+    C, K, K2 = k.shape
+    if K != K2:
+        raise ValueError("spectral kernel must be square (C, K, K)")
+    out = torch.empty((C, H, W // 2 + 1), dtype=torch.complex64, device=k.device)
+    _lib.call("cssm_spectral_kernel", k.data_ptr(), C, K, H, W, float(rho), int(squash),
+              int(goom_floor), out.data_ptr(), _stream())
+    return out
+
+
+def plane_mean(x: torch.Tensor, silu: bool = False) -> torch.Tensor:
+    """Mean over the last two axes of a plane-major tensor (cssm.py:536)."""
+    _dev(x, "x")
+    if x.dtype not in _DTYPES:
+        raise ValueError(f"unsupported dtype {x.dtype}")
+    H, W = x.shape[-2:]
+    out = torch.empty(x.shape[:-2], dtype=torch.float32, device=x.device)
+    _lib.call("cssm_plane_mean", x.data_ptr(), _DTYPES[x.dtype], out.numel(), H, W,
+              _lib.LOAD_SILU if silu else _lib.LOAD_IDENTITY, out.data_ptr(), _stream())
+    return out
+
+
+def gate_params_struct(gp: Dict[str, Dict[str, torch.Tensor]], gate_type: str,
+                       activation: str) -> _lib.GateParams:
+    """cssm_gate_params from a Flax-named parameter dict (delta_proj / B_proj / C_proj)."""
+    s = _lib.GateParams()
+    s.gate_type = _lib.GATE_FACTORED if gate_type == "factored" else _lib.GATE_DENSE
+    s.activation = _GATE_ACTS.get(activation, _lib.ACT_SOFTPLUS)   # unknown -> softplus (cssm.py:441)
+    for i, name in enumerate(("delta_proj", "B_proj", "C_proj")):
+        if gate_type == "factored":
+            ph, pw = gp[f"{name}_h"], gp[f"{name}_w"]
+            s.kernel[i] = _dev(ph["kernel"], f"{name}_h.kernel", torch.float32).data_ptr()
+            s.bias[i] = _dev(ph["bias"], f"{name}_h.bias", torch.float32).data_ptr()
+            s.kernel_w[i] = _dev(pw["kernel"], f"{name}_w.kernel", torch.float32).data_ptr()
+            s.bias_w[i] = _dev(pw["bias"], f"{name}_w.bias", torch.float32).data_ptr()
+        else:
+            p = gp[name]
+            s.kernel[i] = _dev(p["kernel"], f"{name}.kernel", torch.float32).data_ptr()
+            s.bias[i] = _dev(p["bias"], f"{name}.bias", torch.float32).data_ptr()
+    return s
+
+
+def gated_gates(ctx: torch.Tensor, params: Dict, H: int, W: int, gate_type: str = "dense",
+                activation: str = "softplus", c_scale: float = 1.0,
+                out: Optional[torch.Tensor] = None) -> torch.Tensor:
+    """(B, T, H, Wf, 4) = [exp(-Delta), Delta + 1e-8, B, C * c_scale] (cssm.py:536-567)."""
+    _dev(ctx, "ctx", torch.float32)
+    B, T, C = ctx.shape
+    if out is None:
+        out = torch.empty((B, T, H, W // 2 + 1, 4), dtype=torch.float32, device=ctx.device)
+    _dev(out, "out", torch.float32)
+    s = gate_params_struct(params, gate_type, activation)
+    _lib.call("cssm_gated_gates", ctx.data_ptr(), B, T, C, H, W, s, float(c_scale), out.data_ptr(),
+              _stream())
+    return out
+
+
+def gated_scan(u: torch.Tensor, z: torch.Tensor, gates: torch.Tensor, khat: torch.Tensor,
+               u_silu: bool = False, z_silu: bool = False,
+               out: Optional[torch.Tensor] = None) -> torch.Tensor:
+    """Fused rfft2 -> recurrence -> irfft2 -> x z for plane-major (B, T, C, H, W) u, z.
+
+    ``gates`` must come from :func:`gated_gates` with ``c_scale = 1/(H*W)``;
+    ``khat`` from :func:`spectral_kernel` with ``goom_floor=True``.
+    """
+    _dev(u, "u")
+    _dev(z, "z", u.dtype)
+    if u.dtype not in _DTYPES:
+        raise ValueError(f"unsupported dtype {u.dtype}")
+    B, T, C, H, W = u.shape
+    if z.shape != u.shape:
+        raise ValueError("u and z must have the same shape")
+    _dev(gates, "gates", torch.float32)
+    if tuple(gates.shape) != (B, T, H, W // 2 + 1, 4):
+        raise ValueError(f"gates shape {tuple(gates.shape)} != {(B, T, H, W // 2 + 1, 4)}")
+    _dev(khat, "khat", torch.complex64)
+    if tuple(khat.shape) != (C, H, W // 2 + 1):
+        raise ValueError(f"khat shape {tuple(khat.shape)} != {(C, H, W // 2 + 1)}")
+    if out is None:
+        out = torch.empty_like(u)
+    _dev(out, "out", u.dtype)
+    _lib.call("cssm_gated_scan_fwd", u.data_ptr(), z.data_ptr(), out.data_ptr(), _DTYPES[u.dtype],
+              B, T, C, H, W, gates.data_ptr(), khat.data_ptr(), int(u_silu), int(z_silu), _stream())
+    return out
+
+
+def gated_scan_supported(H: int, W: int) -> bool:
+    return bool(_lib.load().cssm_gated_scan_supported(H, W))

@@ -1,0 +1,149 @@
+/*
+ * cssm_amd.h -- C ABI of the MI355X (gfx950) spectral state-space layer.
+ *
+ * Drop-in boundary for the hot path of drewlinsley/CSSM: the `gated`
+ * (GatedCSSM, Mamba-SCSSM) and `gdn` (GatedDeltaNetCSSM) cells of
+ * src/models/cssm.py.  The reference is pure JAX/Flax and has no native FFI;
+ * each entry point below replaces the span of reference code cited beside it,
+ * so a binding (ctypes, jax.ffi custom call) can swap that span for one call.
+ *
+ * Conventions
+ *   - Plain pointers to DEVICE memory, sizes as ints; no torch/JAX types.
+ *   - `stream` is a hipStream_t passed as void* (NULL = default stream).  All
+ *     work is enqueued on it; no entry point synchronises the device.
+ *   - Entry points never allocate device memory and never abort or throw: they
+ *     return CSSM_OK (0) or a negative cssm_status; cssm_last_error() gives a
+ *     message for the calling thread.
+ *   - Tensors are row-major.  "plane-major" means (B, T, C, H, W): every
+ *     (b, t, c) plane is one contiguous H x W image.  The reference layout is
+ *     channels-last (B, T, H, W, C); the projection entry points convert.
+ *   - Complex tensors are interleaved (re, im) float32.  Wf = W/2 + 1.
+ *   - Stateless and re-entrant; calls on one stream are ordered.
+ */
+#ifndef CSSM_AMD_H_
+#define CSSM_AMD_H_
+
+#include <stddef.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define CSSM_ABI_VERSION 1
+
+typedef enum cssm_status {
+  CSSM_OK = 0,
+  CSSM_ERR_NULL = -1,        /* a required pointer is NULL */
+  CSSM_ERR_SHAPE = -2,       /* non-positive or inconsistent sizes */
+  CSSM_ERR_UNSUPPORTED = -3, /* valid request this build has no kernel for */
+  CSSM_ERR_ARG = -4,         /* bad enum value or flag */
+  CSSM_ERR_ALIGN = -5,       /* pointer not aligned as the kernel requires */
+  CSSM_ERR_HIP = -6          /* HIP runtime reported an error at launch */
+} cssm_status;
+
+typedef enum cssm_dtype { CSSM_F32 = 0, CSSM_BF16 = 1 } cssm_dtype;
+
+/* gate_type of GatedCSSM (cssm.py:430, :538-545) */
+typedef enum cssm_gate_type { CSSM_GATE_DENSE = 0, CSSM_GATE_FACTORED = 1 } cssm_gate_type;
+
+/* gate_activation of GatedCSSM._compute_gate (cssm.py:432-441) */
+typedef enum cssm_gate_act {
+  CSSM_ACT_SOFTPLUS = 0, /* softplus(x)            */
+  CSSM_ACT_SIGMOID2 = 1, /* 2 * sigmoid(x)         */
+  CSSM_ACT_EXP = 2       /* exp(clip(x, -4, 2))    */
+} cssm_gate_act;
+
+/* elementwise activation applied when an input plane is loaded */
+typedef enum cssm_load_act { CSSM_LOAD_IDENTITY = 0, CSSM_LOAD_SILU = 1 } cssm_load_act;
+
+/*
+ * Gate projection weights of GatedCSSM (Flax parameter names in brackets).
+ * Index 0 = delta_proj, 1 = B_proj, 2 = C_proj.
+ *   dense    (cssm.py:545): kernel[i] (C, H*Wf) [<name>/kernel], bias[i] (H*Wf) [<name>/bias];
+ *            kernel_w / bias_w unused.
+ *   factored (cssm.py:541-543): kernel[i] (C, H) [<name>_h/kernel], bias[i] (H) [<name>_h/bias],
+ *            kernel_w[i] (C, Wf) [<name>_w/kernel], bias_w[i] (Wf) [<name>_w/bias].
+ */
+typedef struct cssm_gate_params {
+  int gate_type;  /* cssm_gate_type */
+  int activation; /* cssm_gate_act */
+  const float* kernel[3];
+  const float* bias[3];
+  const float* kernel_w[3];
+  const float* bias_w[3];
+} cssm_gate_params;
+
+/* ABI version of the loaded library (CSSM_ABI_VERSION it was built with). */
+int cssm_abi_version(void);
+
+/* Static description of a status code. */
+const char* cssm_strerror(int status);
+
+/* Message of the last failing call made by this thread ("" if none). */
+const char* cssm_last_error(void);
+
+/*
+ * Spectral kernel K_hat = rho * F / (1 + |F|), F = rfft2(pad(k)).
+ * Replaces cssm.py:505-529 (GatedCSSM kernel pad + rfft2 + squash, helper
+ * _stable_spectral_magnitude :29-46) and cssm.py:4711-4716 (GatedDeltaNetCSSM).
+ *   k     (C, K, K) float32 spatial kernel [params 'kernel']
+ *   khat  (C, H, Wf) complex64 out
+ *   squash      1 = apply rho/(1+|F|) (0 = GDN no_spectral_clamp, cssm.py:4715)
+ *   goom_floor  1 = replace |K_hat| < 1e-7 by 1e-7+0j (to_goom floor, goom.py:161-174),
+ *               which is what the scan consumes.
+ * Pad rule: K <= H, W zero-pads with (H-K)//2 before; K >= H and K >= W
+ * centre-crops from (K-H)//2.  K between H and W is rejected (the reference
+ * produces mismatched shapes there).
+ */
+int cssm_spectral_kernel(const float* k, int C, int K, int H, int W, float rho, int squash,
+                         int goom_floor, float* khat, void* stream);
+
+/*
+ * Spatial mean of every H x W plane: out[i] = mean(act(x[i, :, :])).
+ * Replaces cssm.py:536 (ctx = x_main.mean(axis=(2, 3))) for plane-major x.
+ *   x (nplanes, H, W) of dtype; out (nplanes) float32; act = cssm_load_act.
+ */
+int cssm_plane_mean(const void* x, int dtype, long long nplanes, int H, int W, int act,
+                    float* out, void* stream);
+
+/*
+ * Per-frequency gates of GatedCSSM from ctx, with the GOOM shifts folded in.
+ * Replaces cssm.py:538-556 (_make_gate for delta_proj, B_proj, C_proj and
+ * _compute_gate) and the Delta terms of cssm.py:559-567.
+ *   ctx   (B, T, C) float32
+ *   gates (B, T, H, Wf, 4) float32 out, per bin:
+ *         [exp(-Delta), Delta + 1e-8, B, C * c_scale]
+ * c_scale = 1 gives the reference values; cssm_gated_scan_fwd expects
+ * c_scale = 1 / (H * W) (the irfft2 normalisation folded into C).
+ */
+int cssm_gated_gates(const float* ctx, int B, int T, int C, int H, int W,
+                     const cssm_gate_params* params, float c_scale, float* gates, void* stream);
+
+/*
+ * Fused spectral scan of GatedCSSM for one layer call:
+ *   U_t = rfft2(u_t); h_t = floor(K_hat) e^{-Delta_t} h_{t-1} + (Delta_t + 1e-8) floor(U_t B_t);
+ *   y_t = irfft2(C_t h_t, s=(H, W)) * z_t          (h_{-1} = 0, all t in [0, T))
+ * Replaces cssm.py:531-533 and 559-581 (rfft2, to_goom, Delta shifts,
+ * jax.lax.associative_scan(cssm_scalar_scan_op), from_goom, x C, irfft2,
+ * x SiLU(z)); math.py:24-54 and operations.py:17-41 are the combiner it
+ * evaluates exactly (the log-space scan is this linear recurrence).
+ *   u, z, y  (B, T, C, H, W) plane-major of dtype; u = x_main after the short
+ *            convolutions, z = the gate branch; u_act / z_act select SiLU on
+ *            load (the reference applies SiLU to both, cssm.py:502, :581).
+ *   gates    from cssm_gated_gates with c_scale = 1/(H*W)
+ *   khat     from cssm_spectral_kernel with goom_floor = 1, C channels
+ * Supported planes: H = W in {4, 8, 16, 32, 64, 128}.  Pointers u, z, y must
+ * be 16-byte aligned (f32) or 8-byte aligned (bf16); gates 16, khat 8.
+ */
+int cssm_gated_scan_fwd(const void* u, const void* z, void* y, int dtype, int B, int T, int C,
+                        int H, int W, const float* gates, const float* khat, int u_act,
+                        int z_act, void* stream);
+
+/* 1 if cssm_gated_scan_fwd has a kernel for (H, W), else 0. */
+int cssm_gated_scan_supported(int H, int W);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* CSSM_AMD_H_ */

@@ -1,0 +1,201 @@
+"""GPU parity of the gated-cell kernels against the float64 oracle.
+
+Bar: max|y_gpu - y_ref| / RMS(y_ref) <= 1e-4 for
+fp32 I/O and <= 5e-3 for bf16 I/O.  All calls go through the C ABI.
+"""
+import math
+
+import numpy as np
+import pytest
+
+from oracle import cssm_oracle as O
+from tests.gpu_util import bf16_excess_err, print_case, rel_err, to_np
+
+torch = pytest.importorskip("torch")
+pytestmark = pytest.mark.gpu
+
+TOL_F32 = 1e-4
+TOL_BF16 = 5e-3
+
+
+@pytest.fixture(scope="module")
+def S():
+    if not torch.cuda.is_available():
+        pytest.skip("no GPU")
+    from cssm_amd import spectral
+    return spectral
+
+
+def _dev(a, dtype=torch.float32):
+    return torch.from_numpy(np.ascontiguousarray(a)).to("cuda", dtype)
+
+
+def _rand_gates(rng, B, T, H, W, zero_rows=False):
+    Wf = W // 2 + 1
+    delta = O.softplus(rng.standard_normal((B, T, H, Wf)))
+    gB = rng.standard_normal((B, T, H, Wf))
+    gC = rng.standard_normal((B, T, H, Wf))
+    if zero_rows:
+        gB[:, :, 1, :] = 0.0
+    return delta, gB, gC
+
+
+def _pack_gates(delta, gB, gC, H, W):
+    g = np.stack([np.exp(-delta), delta + 1e-8, gB, gC / (H * W)], axis=-1)
+    return _dev(g)
+
+
+# ------------------------------------------------------------- spectral kernel
+
+@pytest.mark.parametrize("C,K,H,W", [(3, 11, 128, 128), (5, 11, 32, 32), (2, 1, 32, 32), (4, 15, 8, 8),
+                                     (2, 3, 7, 7), (3, 11, 14, 14), (2, 5, 4, 4), (2, 11, 16, 16)])
+def test_spectral_kernel_matches_oracle(S, C, K, H, W):
+    print_case(test="spectral_kernel", C=C, K=K, H=H, W=W)
+    rng = np.random.default_rng(7)
+    k = rng.standard_normal((C, K, K)) * 0.3
+    got = S.spectral_kernel(_dev(k), H, W, rho=0.999, squash=True, goom_floor=False)
+    torch.cuda.synchronize()
+    ref = O.spectral_kernel(k, H, W, 0.999)
+    err = np.max(np.abs(got.cpu().numpy().astype(np.complex128) - ref))
+    assert err < 1e-6 * max(1.0, np.max(np.abs(ref)))
+
+
+def test_spectral_kernel_goom_floor(S):
+    print_case(test="spectral_kernel_floor")
+    k = np.zeros((2, 3, 3))
+    k[1, 1, 1] = 0.5
+    got = S.spectral_kernel(_dev(k), 8, 8, goom_floor=True).cpu().numpy()
+    assert np.all(got[0] == np.complex64(1e-7))       # all-zero kernel -> every bin floored
+    assert np.allclose(np.abs(got[1]), 0.999 * 0.5 / 1.5, rtol=1e-6)
+
+
+# ------------------------------------------------------------------ plane mean
+
+@pytest.mark.parametrize("silu", [False, True])
+def test_plane_mean(S, silu):
+    print_case(test="plane_mean", silu=silu)
+    rng = np.random.default_rng(3)
+    x = rng.standard_normal((2, 3, 5, 32, 32))
+    got = to_np(S.plane_mean(_dev(x), silu=silu))
+    ref = (O.silu(x) if silu else x).mean(axis=(-2, -1))
+    assert np.max(np.abs(got - ref)) < 1e-6
+
+
+# ----------------------------------------------------------------------- gates
+
+@pytest.mark.parametrize("gate_type", ["dense", "factored"])
+@pytest.mark.parametrize("act", ["softplus", "sigmoid", "exp"])
+def test_gated_gates_match_oracle(S, gate_type, act):
+    print_case(test="gated_gates", gate_type=gate_type, act=act)
+    rng = np.random.default_rng(11)
+    B, T, C, H, W = 2, 3, 16, 16, 16
+    cfg = O.GatedConfig(channels=C, gate_type=gate_type, gate_activation=act, short_conv_size=0,
+                        short_conv_spatial_size=0, kernel_size=3)
+    p = O.init_params(O.gated_param_shapes(cfg, C, H, W), rng)
+    ctx = rng.standard_normal((B, T, C))
+    delta, gB, gC = O.gated_gates(ctx, p, cfg, H, W)
+    pd = {k: ({kk: _dev(vv) for kk, vv in v.items()} if isinstance(v, dict) else _dev(v))
+          for k, v in p.items()}
+    got = to_np(S.gated_gates(_dev(ctx), pd, H, W, gate_type, act, c_scale=0.5))
+    assert np.max(np.abs(got[..., 0] - np.exp(-delta))) < 1e-5
+    assert np.max(np.abs(got[..., 1] - (delta + 1e-8))) < 1e-5 * max(1, np.max(delta))
+    assert rel_err(got[..., 2], gB) < 1e-5
+    assert rel_err(got[..., 3], 0.5 * gC) < 1e-5
+
+
+# --------------------------------------------------------------- fused scan
+
+SCAN_CASES = [
+    # (B, T, C, H, W)
+    (2, 1, 64, 4, 4), (1, 3, 128, 4, 4), (2, 3, 32, 8, 8), (2, 4, 16, 16, 16), (1, 3, 8, 32, 32),
+    (2, 5, 8, 32, 32), (1, 3, 4, 64, 64), (2, 2, 2, 64, 64), (1, 3, 2, 128, 128), (2, 8, 1, 128, 128),
+]
+
+
+@pytest.mark.parametrize("B,T,C,H,W", SCAN_CASES)
+def test_gated_scan_matches_oracle(S, B, T, C, H, W):
+    print_case(test="gated_scan", B=B, T=T, C=C, H=H, W=W)
+    rng = np.random.default_rng(1000 + H + T)
+    xm = rng.standard_normal((B, T, C, H, W))
+    z = rng.standard_normal((B, T, C, H, W))
+    khat = O.goom_floor(O.spectral_kernel(rng.standard_normal((C, 5, 5)) * 0.3, H, W))
+    delta, gB, gC = _rand_gates(rng, B, T, H, W)
+    y = S.gated_scan(_dev(xm), _dev(z), _pack_gates(delta, gB, gC, H, W), _dev(khat, torch.complex64),
+                     u_silu=True, z_silu=True)
+    torch.cuda.synchronize()
+    ref = O.gated_core(O.silu(xm), O.silu(z), khat, delta, gB, gC)
+    assert rel_err(to_np(y), ref) <= TOL_F32
+
+
+@pytest.mark.parametrize("H", [8, 32, 128])
+def test_gated_scan_goom_floor_zero_inputs(S, H):
+    """Exact zeros (a zero frame, a zero B row) take to_goom's 1e-7 floor."""
+    print_case(test="gated_scan_floor", H=H)
+    rng = np.random.default_rng(5)
+    B, T, W = 1, 4, H
+    C = {8: 32, 32: 8, 128: 2}[H]
+    xm = rng.standard_normal((B, T, C, H, W))
+    xm[:, 0] = 0.0
+    zg = rng.standard_normal((B, T, C, H, W))
+    khat = O.goom_floor(O.spectral_kernel(rng.standard_normal((C, 3, 3)) * 0.3, H, W))
+    delta, gB, gC = _rand_gates(rng, B, T, H, W, zero_rows=True)
+    y = S.gated_scan(_dev(xm), _dev(zg), _pack_gates(delta, gB, gC, H, W), _dev(khat, torch.complex64))
+    ref = O.gated_core(xm, zg, khat, delta, gB, gC)
+    assert rel_err(to_np(y), ref) <= TOL_F32
+    # the all-zero first frame is pure floor: gC (Delta + 1e-8) 1e-7 through irfft2
+    y0 = to_np(y)[:, 0]
+    assert rel_err(y0, ref[:, 0]) <= TOL_F32
+
+
+@pytest.mark.parametrize("B,T,C,H,W", [(2, 4, 8, 32, 32), (1, 3, 2, 128, 128), (2, 2, 16, 16, 16)])
+def test_gated_scan_bf16_io(S, B, T, C, H, W):
+    print_case(test="gated_scan_bf16", B=B, T=T, C=C, H=H, W=W)
+    rng = np.random.default_rng(99)
+    xm = rng.standard_normal((B, T, C, H, W))
+    z = rng.standard_normal((B, T, C, H, W))
+    xm_b = _dev(xm, torch.bfloat16)
+    z_b = _dev(z, torch.bfloat16)
+    khat = O.goom_floor(O.spectral_kernel(rng.standard_normal((C, 5, 5)) * 0.3, H, W))
+    delta, gB, gC = _rand_gates(rng, B, T, H, W)
+    y = S.gated_scan(xm_b, z_b, _pack_gates(delta, gB, gC, H, W), _dev(khat, torch.complex64),
+                     u_silu=True, z_silu=True)
+    assert y.dtype == torch.bfloat16
+    # reference on the bf16-rounded inputs, exact arithmetic; the bar applies beyond the
+    # output's own bf16 rounding
+    ref = O.gated_core(O.silu(to_np(xm_b)), O.silu(to_np(z_b)), khat, delta, gB, gC)
+    assert bf16_excess_err(to_np(y), ref) <= TOL_BF16
+    assert np.sqrt(np.mean((to_np(y) - ref) ** 2)) <= TOL_BF16 * np.sqrt(np.mean(ref ** 2))
+
+
+def test_gated_scan_c2_full_size_sampled(S):
+    """BASELINE config 2 shape (B=128, T=8, 128x128, C=64) run whole; sampled planes vs oracle,
+    and the scan must not depend on the frames being repeated."""
+    print_case(test="gated_scan_c2_full")
+    B, T, C, H, W = 128, 8, 64, 128, 128
+    g = torch.Generator(device="cuda").manual_seed(0)
+    img = torch.randn((B, 1, C, H, W), generator=g, device="cuda")
+    u = img.expand(B, T, C, H, W).contiguous()
+    del img
+    z = torch.randn((B, T, C, H, W), generator=g, device="cuda")
+    rng = np.random.default_rng(0)
+    khat = O.goom_floor(O.spectral_kernel(rng.standard_normal((C, 11, 11)) * 0.02, H, W))
+    delta, gB, gC = _rand_gates(rng, B, T, H, W)
+    y = S.gated_scan(u, z, _pack_gates(delta, gB, gC, H, W), _dev(khat, torch.complex64),
+                     u_silu=True, z_silu=True)
+    torch.cuda.synchronize()
+    for (b, c) in [(0, 0), (17, 33), (127, 63), (64, 1)]:
+        ub = to_np(u[b:b + 1, :, c:c + 1])
+        zb = to_np(z[b:b + 1, :, c:c + 1])
+        ref = O.gated_core(O.silu(ub), O.silu(zb), khat[c:c + 1], delta[b:b + 1], gB[b:b + 1], gC[b:b + 1])
+        assert rel_err(to_np(y[b:b + 1, :, c:c + 1]), ref) <= TOL_F32, (b, c)
+    assert torch.isfinite(y).all().item()
+
+
+def test_gated_scan_rejects_bad_input(S):
+    from cssm_amd._lib import CssmError
+    print_case(test="gated_scan_errors")
+    u = torch.zeros((1, 1, 1, 12, 12), device="cuda")
+    gates = torch.zeros((1, 1, 12, 7, 4), device="cuda")
+    kh = torch.zeros((1, 12, 7), dtype=torch.complex64, device="cuda")
+    with pytest.raises(CssmError, match="no fused kernel"):
+        S.gated_scan(u, u, gates, kh)
