@@ -115,6 +115,8 @@ int cssm_gated_gates(const float* ctx, int B, int T, int C, int H, int W, const 
 
 int cssm_gated_scan_supported(int H, int W) { return cssm::gated_scan_has_kernel(H, W) ? 1 : 0; }
 
+int cssm_gated_scan_min_group(int H, int W) { return cssm::gated_scan_min_group(H, W); }
+
 int cssm_gated_scan_fwd(const void* u, const void* z, void* y, int dtype, int B, int T, int C, int H, int W,
                         const float* gates, const float* khat, int u_act, int z_act, void* stream) {
   if (!u || !z || !y || !gates || !khat)
@@ -127,18 +129,20 @@ int cssm_gated_scan_fwd(const void* u, const void* z, void* y, int dtype, int B,
     return fail(CSSM_ERR_ARG, "cssm_gated_scan_fwd: u_act=%d z_act=%d", u_act, z_act);
   if (!cssm::gated_scan_has_kernel(H, W))
     return fail(CSSM_ERR_UNSUPPORTED, "cssm_gated_scan_fwd: no fused kernel for %dx%d planes", H, W);
+  const int g = cssm::gated_scan_min_group(H, W);
+  if (C % g != 0)
+    return fail(CSSM_ERR_UNSUPPORTED, "cssm_gated_scan_fwd: C=%d is not a multiple of %d for %dx%d planes", C, g,
+                H, W);
   const size_t va = dtype == CSSM_F32 ? 16 : 8;
   if (!aligned(u, va) || !aligned(z, va) || !aligned(y, va) || !aligned(gates, 16) || !aligned(khat, 8))
     return fail(CSSM_ERR_ALIGN, "cssm_gated_scan_fwd: misaligned tensor pointer");
   if ((long long)B * T * C * H * W > (1LL << 40))
     return fail(CSSM_ERR_SHAPE, "cssm_gated_scan_fwd: tensor too large");
-  const hipError_t e = cssm::launch_gated_scan(u, z, y, dtype, B, T, C, H, W,
-                                               reinterpret_cast<const float4*>(gates),
+  const hipError_t e = cssm::launch_gated_scan(u, z, y, dtype, B, T, C, H, W, reinterpret_cast<const float4*>(gates),
                                                reinterpret_cast<const float2*>(khat), u_act, z_act,
                                                static_cast<hipStream_t>(stream));
   if (e == hipErrorInvalidValue)
-    return fail(CSSM_ERR_UNSUPPORTED, "cssm_gated_scan_fwd: B*C=%lld has no plane-group split for %dx%d",
-                (long long)B * C, H, W);
+    return fail(CSSM_ERR_UNSUPPORTED, "cssm_gated_scan_fwd: no plane-group split of C=%d for %dx%d", C, H, W);
   return hip_status(e, "cssm_gated_scan_fwd");
 }
 

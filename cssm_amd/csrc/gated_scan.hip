@@ -17,7 +17,9 @@
 // floor(a) = 1e-7 + 0j where |a| < 1e-7 (goom.py:161-174).
 //
 // FFT organisation (H = H1*H2, W = W1*W2, all passes in-register radix-H1/H2/
-// W1/W2 with an LDS transpose between them):
+// W1/W2 with an LDS exchange between them; every pass writes its results back
+// into exactly the LDS slots it read, so one plane-sized buffer suffices and
+// a workgroup needs well under half of LDS):
 //   R1/R2  row transforms: rows r and r+H/2 are packed as one complex row,
 //          separated after the DFT; the real DC and Nyquist bins of each row
 //          are packed into one complex "column 0".
@@ -68,7 +70,9 @@ struct IoBF16 {
   }
 };
 
-__device__ __forceinline__ float silu_f(float x) { return x / (1.0f + __expf(-x)); }
+__device__ __forceinline__ float silu_f(float x) {
+  return x * __builtin_amdgcn_rcpf(1.0f + __expf(-x));
+}
 
 __device__ __forceinline__ float4 act4(float4 v, int act) {
   if (act == 1) {
@@ -79,16 +83,19 @@ __device__ __forceinline__ float4 act4(float4 v, int act) {
 
 // ------------------------------------------------------------------ geometry
 
-constexpr int cmax(int a, int b) { return a > b ? a : b; }
 constexpr int fft_radix1(int n) { return n >= 128 ? 16 : (n >= 32 ? 8 : (n >= 8 ? 4 : 2)); }
 
-template <int LH, int LW, int NP>
+// LH, LW: log2 of the plane; NP planes per workgroup; PPT real samples per
+// thread per plane load (64 for large planes: a 128x128 plane is one 256-thread
+// workgroup, two of which share a CU so one's barriers and memory waits hide
+// behind the other's arithmetic).
+template <int LH, int LW, int NP, int PPT>
 struct Geom {
   static constexpr int H = 1 << LH, W = 1 << LW;
   static constexpr int HP = H / 2, WH = W / 2, WF = WH + 1;
   static constexpr int W1 = fft_radix1(W), W2 = W / W1;
   static constexpr int H1 = fft_radix1(H), H2 = H / H1;
-  static constexpr int NT = NP * H * W / 32;
+  static constexpr int NT = NP * H * W / PPT;
   static constexpr int NR1 = NP * HP * W2, NR2 = NP * HP * (W1 / 2);
   static constexpr int NC1 = NP * WH * H2, NC2 = NP * WH * (H1 / 2);
   static constexpr int JR1 = NR1 / NT, JR2 = NR2 / NT, JC1 = NC1 / NT, JC2 = NC2 / NT;
@@ -96,52 +103,82 @@ struct Geom {
   static constexpr int JE = (NE + NT - 1) / NT;
   static constexpr int NV4 = NP * H * W / 4;
   static constexpr int JLD = NV4 / NT;
-  static constexpr int NBIN = JC2 * 2 * H2;   // regular state bins per thread
 
-  // LDS layouts.  Offsets are in floats for REAL, in float2 for the others.
-  static constexpr int RS = W + (W2 < 4 ? 4 : W2);
-  static constexpr int HPP = HP + 4;
-  static constexpr int RSP = WH + 1;
-  static constexpr int SZ_REAL = NP * H * RS;
-  static constexpr int SZ_RA = 2 * NP * W1 * W2 * HPP;
-  static constexpr int SZ_P = 2 * NP * H * RSP;
-  static constexpr int SZ_CA = 2 * NP * H2 * H1 * WH;
-  static constexpr int BUF = (cmax(cmax(SZ_REAL, SZ_RA), cmax(SZ_P, SZ_CA)) + 3) / 4 * 4;
+  // LDS (floats): the plane buffer (row stride RS), the packed DC/Nyquist
+  // column of each plane and four twiddle tables laid out so one thread's
+  // entries are contiguous (rows padded by one entry against bank conflicts):
+  //   R1 [s][k] = w_W^{s k}, C1 [s][k] = w_H^{s k},
+  //   I1 [k][s] = conj w_H^{s k}, I3 [k][s] = conj w_W^{s k}.
+  static constexpr int RS = W + 4;
+  static constexpr int SZ_BUF = (NP * H * RS + 3) / 4 * 4;
   static constexpr int SZ_EDGE = 2 * NP * H;
-  static constexpr int SZ_TW = 2 * (H + W);
-  static constexpr int LDS_FLOATS = 2 * BUF + SZ_EDGE + SZ_TW;
-  static_assert(LDS_FLOATS * 4 <= 160 * 1024, "plane group does not fit gfx950 LDS");
+  static constexpr int TR1 = W1 + 1, TC1 = H1, TI1 = H2, TI3 = W2 + 1;   // table row lengths
+  static constexpr int N_R1 = W2 * TR1, N_C1 = H2 * TC1, N_I1 = H1 * TI1, N_I3 = W1 * TI3;
+  static constexpr int SZ_TW = 2 * (N_R1 + N_C1 + N_I1 + N_I3);
+  static constexpr int OFF_EDGE = SZ_BUF, OFF_TW = OFF_EDGE + SZ_EDGE;
+  static constexpr int LDS_FLOATS = OFF_TW + SZ_TW;
 
+  static_assert(LDS_FLOATS * 4 <= 160 * 1024, "plane group does not fit gfx950 LDS");
   static_assert(NT % 64 == 0 && NT <= 1024, "workgroup must be whole waves, <= 1024 threads");
   static_assert(JR1 * NT == NR1 && JR2 * NT == NR2 && JC1 * NT == NC1 && JC2 * NT == NC2,
                 "every FFT pass must split evenly over the workgroup");
   static_assert(JLD * NT == NV4, "plane group must split into whole 4-vectors per thread");
   static_assert(W2 % 2 == 0 && H2 % 2 == 0 && W1 % 2 == 0 && H1 % 2 == 0, "radix split");
 
-  static __device__ __forceinline__ int real_off(int pl, int r, int w) { return (pl * H + r) * RS + w; }
-  static __device__ __forceinline__ int ra_off(int pl, int k, int s, int p) {
-    return ((pl * W1 + k) * W2 + s) * HPP + p;
+  // Sample (pl, r, w) lives at row (pl, r), column w, except that in the
+  // upper half of each row's W2-float blocks (block index >= W1/2) the two
+  // halves of the block are swapped.  With RS = W + 4 the passes are free of
+  // LDS bank conflicts on 64 banks except the row-pair gather (2-way):
+  // R1/I4 (scalar, rows two apart within a wave), R2/I3 (whole blocks),
+  // C1/C2/I1/I2 (one packed-spectrum slot per lane along a row), load/store.
+  static constexpr int HALF = W2 >= 4 ? W2 / 2 : 0;
+  static __device__ __forceinline__ int row_off(int pl, int r) { return (pl * H + r) * RS; }
+  // block blk < W1/2 (lo: halves in place) or >= W1/2 (hi: halves swapped), position pos < W2
+  static __device__ __forceinline__ int lo_off(int pl, int r, int blk, int pos) {
+    return row_off(pl, r) + blk * W2 + pos;
   }
-  static __device__ __forceinline__ int p_off(int pl, int r, int v) { return (pl * H + r) * RSP + v; }
-  static __device__ __forceinline__ int ca_off(int pl, int s, int k, int v) {
-    return ((pl * H2 + s) * H1 + k) * WH + v;
+  static __device__ __forceinline__ int hi_off(int pl, int r, int blk, int pos) {
+    return row_off(pl, r) + blk * W2 + (pos ^ HALF);
+  }
+  // column of the packed-row spectrum P(pl, r, v), v < W/2: complex pair 2 (v / W1)
+  // of block v % W1 (the slots the row pass that produces it has just read)
+  static __device__ __forceinline__ int p_col(int v) {
+    const int blk = v % W1, pos = 2 * (v / W1);
+    return blk * W2 + (blk >= W1 / 2 ? (pos ^ HALF) : pos);
+  }
+  // 4-vector c4 of row r: contiguous unless the block is split by the swap
+  static constexpr bool V4_SPLIT = (HALF == 2);
+  // R1/I4 job jb -> (pl, p, s): s fastest; consecutive row groups of one wave
+  // are two rows apart so the row stride's bank shift (4) becomes 8
+  static constexpr int RG = 64 / W2;
+  static constexpr bool R1_STRIDE2 = (RG >= 2) && (HP % (2 * RG) == 0);
+  static __device__ __forceinline__ void r1_job(unsigned jb, int& pl, int& p, int& s) {
+    s = int(jb % W2);
+    const unsigned t1 = jb / W2;
+    pl = int(t1 / HP);
+    const unsigned tp = t1 % HP;
+    p = int(R1_STRIDE2 ? ((tp % RG) * 2 + (tp / RG) % 2 + 2 * RG * (tp / (2 * RG))) : tp);
   }
 };
 
-__device__ __forceinline__ float2 goom_floor(float2 a) {
-  // |a| < 1e-7  ->  1e-7 + 0j   (goom.py:161-174)
-  const float m2 = a.x * a.x + a.y * a.y;
-  return (m2 < 1e-14f) ? make_float2(1e-7f, 0.0f) : a;
-}
-
-// one bin of the recurrence; returns C * h (C already carries 1/(H W))
+// The forward row pass skips the 1/2 of the packed-row separation, so the
+// spectrum the recurrence sees is U' = 2U for every bin (the edge unpack keeps
+// its 1/2 and inherits the factor from the doubled DC/Nyquist column).  The
+// state is then h' = 2h; the GOOM floor is applied at the doubled scale and
+// C is halved, so y is unchanged.
+//
+// gate g = (E, DB, VF, GC): E = exp(-Delta), DB = (Delta + 1e-8) B,
+// VF = (Delta + 1e-8) 1e-7 (the input term when |U B| < 1e-7), GC = C c_scale.
+// |DB U| < VF  <=>  |U B| < 1e-7 since Delta + 1e-8 > 0.
 __device__ __forceinline__ float2 scan_bin(float2& h, float2 U, float4 g, float2 kh) {
-  const float2 P = goom_floor(make_float2(U.x * g.z, U.y * g.z));   // floor(U * B)
-  const float2 A = make_float2(kh.x * g.x, kh.y * g.x);            // floor(K) e^{-D}
-  const float2 hn = make_float2(A.x * h.x - A.y * h.y + g.y * P.x,
-                                A.x * h.y + A.y * h.x + g.y * P.y);
+  float2 V = make_float2(U.x * g.y, U.y * g.y);
+  const float vf = g.z + g.z;
+  if (V.x * V.x + V.y * V.y < vf * vf) V = make_float2(vf, 0.0f);
+  const float2 A = make_float2(kh.x * g.x, kh.y * g.x);
+  const float2 hn = make_float2(fmaf(A.x, h.x, fmaf(-A.y, h.y, V.x)), fmaf(A.x, h.y, fmaf(A.y, h.x, V.y)));
   h = hn;
-  return make_float2(hn.x * g.w, hn.y * g.w);
+  const float gc = 0.5f * g.w;
+  return make_float2(hn.x * gc, hn.y * gc);
 }
 
 // pair-unit decode: pair jj of radix N1 -> units (kA, kB) with kB = -kA mod N1
@@ -152,40 +189,72 @@ __device__ __forceinline__ void pair_units(int jj, int& kA, int& kB) {
   kB = (jj == 0) ? (N1 / 2) : (N1 - jj);
 }
 
-template <int LH, int LW, int NP, class IO>
-__global__ void __launch_bounds__((NP << (LH + LW)) / 32, 1)
-gated_scan_pow2(const typename IO::T* __restrict__ u, const typename IO::T* __restrict__ z,
-                typename IO::T* __restrict__ y, const float4* __restrict__ gates,
-                const float2* __restrict__ khat, int T, int C, int u_act, int z_act) {
-  using G = Geom<LH, LW, NP>;
-  static_assert(G::NT == (NP << (LH + LW)) / 32, "launch bound");
-  constexpr int H = G::H, W = G::W, HP = G::HP, WH = G::WH, WF = G::WF;
+// raw buffer access: 32-bit offsets from a uniform base (cheaper addressing
+// than 64-bit pointers, and out-of-range reads return 0)
+struct Buf {
+  __amdgpu_buffer_rsrc_t r;
+  __device__ __forceinline__ Buf(const void* p, unsigned bytes)
+      : r(__builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(p), 0, int(bytes), 0x00020000)) {}
+  __device__ __forceinline__ float4 ld4(unsigned off) const {
+    return __builtin_bit_cast(float4, __builtin_amdgcn_raw_buffer_load_b128(r, int(off), 0, 0));
+  }
+  __device__ __forceinline__ float2 ld2(unsigned off) const {
+    return __builtin_bit_cast(float2, __builtin_amdgcn_raw_buffer_load_b64(r, int(off), 0, 0));
+  }
+};
+
+struct ScanArgs {
+  const void* u;
+  const void* z;
+  void* y;
+  const float4* gates;   // (B, T, H, WF) per-bin (E, DB, VF, GC)
+  const float2* khat;    // (C, H, WF), GOOM-floored
+  int T, C, u_act, z_act;
+};
+
+template <int LH, int LW, int NP, int PPT, class IO>
+__global__ void __launch_bounds__((NP << (LH + LW)) / PPT, PPT >= 64 ? 2 : 1)
+gated_scan_pow2(const ScanArgs a) {
+  using G = Geom<LH, LW, NP, PPT>;
+  static_assert(G::NT == (NP << (LH + LW)) / PPT, "launch bound");
+  constexpr int H = G::H, HP = G::HP, WH = G::WH, WF = G::WF, W = G::W;
   constexpr int W1 = G::W1, W2 = G::W2, H1 = G::H1, H2 = G::H2, NT = G::NT;
   using V4 = typename IO::V4;
+  using TE = typename IO::T;
 
   __shared__ __attribute__((aligned(16))) float smem[G::LDS_FLOATS];
-  float* const bufX = smem;
-  float* const bufY = smem + G::BUF;
-  float2* const edge = reinterpret_cast<float2*>(smem + 2 * G::BUF);
-  float2* const twW = reinterpret_cast<float2*>(smem + 2 * G::BUF + G::SZ_EDGE);
-  float2* const twH = twW + W;
+  float* const buf = smem;
+  float2* const edge = reinterpret_cast<float2*>(smem + G::OFF_EDGE);
+  float2* const twR1 = reinterpret_cast<float2*>(smem + G::OFF_TW);
+  float2* const twC1 = twR1 + G::N_R1;
+  float2* const twI1 = twC1 + G::N_C1;
+  float2* const twI3 = twI1 + G::N_I1;
+  auto cplx = [&](int off) -> float2& { return *reinterpret_cast<float2*>(buf + off); };
 
-  const int tid = threadIdx.x;
-  // planes of this group: flattened (b * C + c) = blockIdx.x * NP + pl
-  const long gp0 = long(blockIdx.x) * NP;
-  auto plane_b = [&](int pl) -> int { return int((gp0 + pl) / C); };
-  auto plane_c = [&](int pl) -> int { return int((gp0 + pl) % C); };
+  const int T = a.T, C = a.C;
+  // this workgroup: batch b, channels c0 .. c0 + NP - 1 (C % NP == 0)
+  const int groups = C / NP;
+  const int b = blockIdx.x / groups;
+  const int c0 = (blockIdx.x % groups) * NP;
+  const size_t HWs = size_t(H) * W;
+  auto group_elems = [&](int t) -> size_t { return ((size_t(b) * T + t) * C + c0) * HWs; };
+  const TE* __restrict__ up = static_cast<const TE*>(a.u);
+  const TE* __restrict__ zp = static_cast<const TE*>(a.z);
+  TE* __restrict__ yp = static_cast<TE*>(a.y);
+  const Buf kbuf(a.khat + size_t(c0) * H * WF, unsigned(NP * H * WF * sizeof(float2)));
 
-  // twiddle tables w_N^i = exp(-2 pi i i / N), from double precision
-  for (int i = tid; i < W; i += NT) {
-    double sn, cs;
-    sincospi(2.0 * double(i) / double(W), &sn, &cs);
-    twW[i] = make_float2(float(cs), float(-sn));
-  }
-  for (int i = tid; i < H; i += NT) {
-    double sn, cs;
-    sincospi(2.0 * double(i) / double(H), &sn, &cs);
-    twH[i] = make_float2(float(cs), float(-sn));
+  {
+    const int tid = threadIdx.x;
+    // twiddles w_N^m = exp(-2 pi i m / N) from double precision
+    auto tw = [](int m, int n) -> float2 {
+      double sn, cs;
+      sincospi(2.0 * double(m) / double(n), &sn, &cs);
+      return make_float2(float(cs), float(-sn));
+    };
+    for (int i = tid; i < G::N_R1; i += NT) twR1[i] = tw((i / G::TR1) * (i % G::TR1), W);
+    for (int i = tid; i < G::N_C1; i += NT) twC1[i] = tw((i / G::TC1) * (i % G::TC1), H);
+    for (int i = tid; i < G::N_I1; i += NT) twI1[i] = cconj(tw((i % G::TI1) * (i / G::TI1), H));
+    for (int i = tid; i < G::N_I3; i += NT) twI3[i] = cconj(tw((i % G::TI3) * (i / G::TI3), W));
   }
 
   float2 h[G::JC2][2][H2];
@@ -193,201 +262,226 @@ gated_scan_pow2(const typename IO::T* __restrict__ u, const typename IO::T* __re
 #pragma unroll
   for (int j = 0; j < G::JC2; ++j)
 #pragma unroll
-    for (int a = 0; a < 2; ++a)
-#pragma unroll
-      for (int q = 0; q < H2; ++q) h[j][a][q] = make_float2(0.f, 0.f);
+    for (int q = 0; q < H2; ++q) h[j][0][q] = h[j][1][q] = make_float2(0.f, 0.f);
 #pragma unroll
   for (int j = 0; j < G::JE; ++j)
 #pragma unroll
-    for (int a = 0; a < 4; ++a) hE[j][a] = make_float2(0.f, 0.f);
+    for (int k = 0; k < 4; ++k) hE[j][k] = make_float2(0.f, 0.f);
 
-  const size_t plane_elems = size_t(H) * W;
-  // element offset of 4-vector f (of the NP-plane group) at step t
-  auto vec_off = [&](int f, int t) -> size_t {
-    const int pl = f / (H * W / 4), rem = f % (H * W / 4);
-    return ((size_t(plane_b(pl)) * T + t) * C + plane_c(pl)) * plane_elems + size_t(rem) * 4;
+  // LDS slot of 4-vector f of the group (row-major over planes and rows)
+  auto v4_store = [&](unsigned f, float4 v) {
+    const int pl = int(f / (H * W / 4)), rem = int(f % (H * W / 4));
+    const int r = rem / (W / 4), w = 4 * (rem % (W / 4));
+    const int blk = w / W2, pos = w % W2;
+    if (G::V4_SPLIT && blk >= W1 / 2) {
+      cplx(G::row_off(pl, r) + blk * W2 + (pos ^ 2)) = make_float2(v.x, v.y);
+      cplx(G::row_off(pl, r) + blk * W2 + pos) = make_float2(v.z, v.w);
+    } else {
+      const int o = blk >= W1 / 2 ? (pos ^ G::HALF) : pos;
+      *reinterpret_cast<float4*>(buf + G::row_off(pl, r) + blk * W2 + o) = v;
+    }
   };
-  auto gates_at = [&](int pl, int t) -> const float4* {
-    return gates + (size_t(plane_b(pl)) * T + t) * size_t(H) * WF;
+  auto v4_load = [&](unsigned f) -> float4 {
+    const int pl = int(f / (H * W / 4)), rem = int(f % (H * W / 4));
+    const int r = rem / (W / 4), w = 4 * (rem % (W / 4));
+    const int blk = w / W2, pos = w % W2;
+    if (G::V4_SPLIT && blk >= W1 / 2) {
+      const float2 lo = cplx(G::row_off(pl, r) + blk * W2 + (pos ^ 2));
+      const float2 hi = cplx(G::row_off(pl, r) + blk * W2 + pos);
+      return make_float4(lo.x, lo.y, hi.x, hi.y);
+    }
+    const int o = blk >= W1 / 2 ? (pos ^ G::HALF) : pos;
+    return *reinterpret_cast<const float4*>(buf + G::row_off(pl, r) + blk * W2 + o);
   };
 
-  V4 ldu[G::JLD];
+  // u_0 into the plane buffer
+  {
+    const unsigned tid = threadIdx.x;
+    const V4* src = reinterpret_cast<const V4*>(up + group_elems(0));
+    V4 ld[G::JLD];
 #pragma unroll
-  for (int i = 0; i < G::JLD; ++i)
-    ldu[i] = *reinterpret_cast<const V4*>(u + vec_off(i * NT + tid, 0));
+    for (int i = 0; i < G::JLD; ++i) ld[i] = src[i * NT + tid];
+#pragma unroll
+    for (int i = 0; i < G::JLD; ++i) v4_store(i * NT + tid, act4(IO::to_f4(ld[i]), a.u_act));
+  }
+  __syncthreads();
 
   for (int t = 0; t < T; ++t) {
-    // ---------------------------------------------------------- LOAD u_t
-#pragma unroll
-    for (int i = 0; i < G::JLD; ++i) {
-      const int f = i * NT + tid;
-      const int pl = f / (H * W / 4);
-      const int rem = f % (H * W / 4);
-      const int r = rem / (W / 4), c4 = rem % (W / 4);
-      const float4 v = act4(IO::to_f4(ldu[i]), u_act);
-      *reinterpret_cast<float4*>(bufX + G::real_off(pl, r, 4 * c4)) = v;
-    }
-    V4 ldg[G::JLD];
-#pragma unroll
-    for (int i = 0; i < G::JLD; ++i)
-      ldg[i] = *reinterpret_cast<const V4*>(z + vec_off(i * NT + tid, t));
-    __syncthreads();
+    // Re-derive the thread index inside the loop so the compiler rebuilds the
+    // (cheap, base + constant) LDS addresses per step instead of hoisting
+    // hundreds of them into registers for the whole scan.
+    unsigned tid = threadIdx.x;
+    asm volatile("" : "+v"(tid));
+    const Buf gbuf(a.gates + (size_t(b) * T + t) * size_t(H) * WF, unsigned(H * WF * sizeof(float4)));
 
     // ---------------------------------------------- R1: DFT-W1 over m, twiddle
-    {
-      float2* Y = reinterpret_cast<float2*>(bufY);
 #pragma unroll
-      for (int j = 0; j < G::JR1; ++j) {
-        const int jb = j * NT + tid;
-        const int s = jb % W2, p = (jb / W2) % HP, pl = jb / (W2 * HP);
-        float2 zz[W1];
+    for (int j = 0; j < G::JR1; ++j) {
+      int pl, p, s;
+      G::r1_job(j * NT + tid, pl, p, s);
+      float2 zz[W1];
 #pragma unroll
-        for (int m = 0; m < W1; ++m)
-          zz[m] = make_float2(bufX[G::real_off(pl, p, s + W2 * m)],
-                              bufX[G::real_off(pl, p + HP, s + W2 * m)]);
-        Dft<W1, false>::run(zz);
-#pragma unroll
-        for (int k = 0; k < W1; ++k) Y[G::ra_off(pl, k, s, p)] = cmul(zz[k], twW[s * k]);
+      for (int m = 0; m < W1; ++m) {
+        const int o = (m >= W1 / 2) ? (s ^ G::HALF) : s;
+        zz[m] = make_float2(buf[G::row_off(pl, p) + m * W2 + o], buf[G::row_off(pl, p + HP) + m * W2 + o]);
       }
+      Dft<W1, false>::run(zz);
+#pragma unroll
+      for (int k = 0; k < W1; ++k) {
+        const float2 v = k ? cmul(zz[k], twR1[s * G::TR1 + k]) : zz[0];
+        const int o = (k >= W1 / 2) ? (s ^ G::HALF) : s;
+        buf[G::row_off(pl, p) + k * W2 + o] = v.x;
+        buf[G::row_off(pl, p + HP) + k * W2 + o] = v.y;
+      }
+      __builtin_amdgcn_sched_barrier(0);
     }
     __syncthreads();
 
-    // ------------------------- R2: DFT-W2 over s, separate packed row pairs
-    {
-      const float2* Yc = reinterpret_cast<const float2*>(bufY);
-      float2* X = reinterpret_cast<float2*>(bufX);
+    // ----------------- R2: DFT-W2 over s, separate packed row pairs (x2 scale)
 #pragma unroll
-      for (int j = 0; j < G::JR2; ++j) {
-        const int jb = j * NT + tid;
-        const int p = jb % HP, jj = (jb / HP) % (W1 / 2), pl = jb / (HP * (W1 / 2));
-        int kA, kB;
-        pair_units<W1>(jj, kA, kB);
-        float2 za[W2], zb[W2];
+    for (int j = 0; j < G::JR2; ++j) {
+      const unsigned jb = j * NT + tid;
+      const int jj = int(jb % (W1 / 2)), p = int((jb / (W1 / 2)) % HP), pl = int(jb / (HP * (W1 / 2)));
+      int kA, kB;
+      pair_units<W1>(jj, kA, kB);
+      float2 za[W2], zb[W2];
 #pragma unroll
-        for (int s = 0; s < W2; ++s) {
-          za[s] = Yc[G::ra_off(pl, kA, s, p)];
-          zb[s] = Yc[G::ra_off(pl, kB, s, p)];
-        }
-        Dft<W2, false>::run(za);
-        Dft<W2, false>::run(zb);
-        // Z[kA + W1 q] = za[q], Z[kB + W1 q] = zb[q]
-        auto emit = [&](int v, float2 zv, float2 zm) {
-          // X_p[v] = (Z[v] + conj Z[-v]) / 2 ; X_{p+HP}[v] = -i (Z[v] - conj Z[-v]) / 2
-          const float2 xa = make_float2(0.5f * (zv.x + zm.x), 0.5f * (zv.y - zm.y));
-          const float2 xb = make_float2(0.5f * (zv.y + zm.y), -0.5f * (zv.x - zm.x));
-          X[G::p_off(pl, p, v)] = xa;
-          X[G::p_off(pl, p + HP, v)] = xb;
-        };
-        if (jj != 0) {
-#pragma unroll
-          for (int q = 0; q < W2 / 2; ++q) {
-            emit(kA + W1 * q, za[q], zb[W2 - 1 - q]);
-            emit(kB + W1 * q, zb[q], za[W2 - 1 - q]);
-          }
-        } else {
-          // packed column 0: DC + i * Nyquist of both rows
-          const float2 z0 = za[0], zn = za[W2 / 2];
-          X[G::p_off(pl, p, 0)] = make_float2(z0.x, zn.x);
-          X[G::p_off(pl, p + HP, 0)] = make_float2(z0.y, zn.y);
-#pragma unroll
-          for (int q = 1; q < W2 / 2; ++q) emit(W1 * q, za[q], za[W2 - q]);
-#pragma unroll
-          for (int q = 0; q < W2 / 2; ++q) emit(W1 / 2 + W1 * q, zb[q], zb[W2 - 1 - q]);
-        }
+      for (int s = 0; s < W2; ++s) {
+        za[s] = make_float2(buf[G::lo_off(pl, p, kA, s)], buf[G::lo_off(pl, p + HP, kA, s)]);
+        zb[s] = make_float2(buf[G::hi_off(pl, p, kB, s)], buf[G::hi_off(pl, p + HP, kB, s)]);
       }
+      Dft<W2, false>::run(za);
+      Dft<W2, false>::run(zb);
+      // Z[kA + W1 q] = za[q], Z[kB + W1 q] = zb[q]
+      // 2 X_p[v] = Z[v] + conj Z[-v] ; 2 X_{p+HP}[v] = -i (Z[v] - conj Z[-v])
+      // v = kA + W1 q sits in (lo) block kA, v = kB + W1 q in (hi) block kB
+      auto emit = [&](bool hi, int blk, int q, float2 zv, float2 zm) {
+        const int o0 = hi ? G::hi_off(pl, p, blk, 2 * q) : G::lo_off(pl, p, blk, 2 * q);
+        const int o1 = hi ? G::hi_off(pl, p + HP, blk, 2 * q) : G::lo_off(pl, p + HP, blk, 2 * q);
+        cplx(o0) = make_float2(zv.x + zm.x, zv.y - zm.y);
+        cplx(o1) = make_float2(zv.y + zm.y, zm.x - zv.x);
+      };
+      if (jj != 0) {
+#pragma unroll
+        for (int q = 0; q < W2 / 2; ++q) {
+          emit(false, kA, q, za[q], zb[W2 - 1 - q]);
+          emit(true, kB, q, zb[q], za[W2 - 1 - q]);
+        }
+      } else {
+        // packed column 0: 2 (DC + i Nyquist) of both rows
+        const float2 z0 = za[0], zn = za[W2 / 2];
+        cplx(G::lo_off(pl, p, 0, 0)) = make_float2(z0.x + z0.x, zn.x + zn.x);
+        cplx(G::lo_off(pl, p + HP, 0, 0)) = make_float2(z0.y + z0.y, zn.y + zn.y);
+#pragma unroll
+        for (int q = 1; q < W2 / 2; ++q) emit(false, 0, q, za[q], za[W2 - q]);
+#pragma unroll
+        for (int q = 0; q < W2 / 2; ++q) emit(true, W1 / 2, q, zb[q], zb[W2 - 1 - q]);
+      }
+      __builtin_amdgcn_sched_barrier(0);
     }
     __syncthreads();
 
     // ------------------------------------------ C1: DFT-H1 over m, twiddle
-    {
-      const float2* X = reinterpret_cast<const float2*>(bufX);
-      float2* Y = reinterpret_cast<float2*>(bufY);
 #pragma unroll
-      for (int j = 0; j < G::JC1; ++j) {
-        const int jb = j * NT + tid;
-        const int v = jb % WH, s = (jb / WH) % H2, pl = jb / (WH * H2);
-        float2 zz[H1];
+    for (int j = 0; j < G::JC1; ++j) {
+      const unsigned jb = j * NT + tid;
+      const int v = int(jb % WH), s = int((jb / WH) % H2), pl = int(jb / (WH * H2));
+      const int col = G::p_col(v);
+      float2 zz[H1];
 #pragma unroll
-        for (int m = 0; m < H1; ++m) zz[m] = X[G::p_off(pl, s + H2 * m, v)];
-        Dft<H1, false>::run(zz);
+      for (int m = 0; m < H1; ++m) zz[m] = cplx(G::row_off(pl, s + H2 * m) + col);
+      Dft<H1, false>::run(zz);
 #pragma unroll
-        for (int k = 0; k < H1; ++k) Y[G::ca_off(pl, s, k, v)] = cmul(zz[k], twH[s * k]);
-      }
+      for (int k = 0; k < H1; ++k)
+        cplx(G::row_off(pl, s + H2 * k) + col) = k ? cmul(zz[k], twC1[s * G::TC1 + k]) : zz[0];
+      __builtin_amdgcn_sched_barrier(0);
     }
     __syncthreads();
 
-    // ------------- C2: DFT-H2 over s -> spectrum; recurrence; inverse DFT-H2
-    float2 spec[G::JC2][2][H2];
-    {
-      const float2* Y = reinterpret_cast<const float2*>(bufY);
+    // ------ C2: DFT-H2 over s -> spectrum; recurrence; inverse DFT-H2 (I1)
 #pragma unroll
-      for (int j = 0; j < G::JC2; ++j) {
-        const int jb = j * NT + tid;
-        const int v = jb % WH, jj = (jb / WH) % (H1 / 2), pl = jb / (WH * (H1 / 2));
-        int kA, kB;
-        pair_units<H1>(jj, kA, kB);
+    for (int j = 0; j < G::JC2; ++j) {
+      const unsigned jb = j * NT + tid;
+      const int v = int(jb % WH), pl = int(jb / (WH * (H1 / 2)));
+      int kA, kB;
+      pair_units<H1>(int((jb / WH) % (H1 / 2)), kA, kB);
+      const int col = G::p_col(v);
+      float2 sa[H2], sb[H2];
+#pragma unroll
+      for (int s = 0; s < H2; ++s) {
+        sa[s] = cplx(G::row_off(pl, s + H2 * kA) + col);
+        sb[s] = cplx(G::row_off(pl, s + H2 * kB) + col);
+      }
+      Dft<H2, false>::run(sa);
+      Dft<H2, false>::run(sb);
+      if (v == 0) {
+        // packed DC/Nyquist column: hand to the edge pass
+#pragma unroll
+        for (int q = 0; q < H2; ++q) {
+          edge[pl * H + kA + H1 * q] = sa[q];
+          edge[pl * H + kB + H1 * q] = sb[q];
+        }
+      } else {
+        // gates of (b, t) and the spectral kernel of this plane, bins (kA|kB + H1 q, v)
+        const unsigned ga = unsigned(kA * WF + v), gb = unsigned(kB * WF + v);
+        const unsigned ka = unsigned(pl * H * WF) + ga, kb = unsigned(pl * H * WF) + gb;
+        float4 gra[H2], grb[H2];
+        float2 kra[H2], krb[H2];
+#pragma unroll
+        for (int q = 0; q < H2; ++q) {
+          gra[q] = gbuf.ld4((ga + q * H1 * WF) * 16u);
+          grb[q] = gbuf.ld4((gb + q * H1 * WF) * 16u);
+          kra[q] = kbuf.ld2((ka + q * H1 * WF) * 8u);
+          krb[q] = kbuf.ld2((kb + q * H1 * WF) * 8u);
+        }
+#pragma unroll
+        for (int q = 0; q < H2; ++q) {
+          sa[q] = scan_bin(h[j][0][q], sa[q], gra[q], kra[q]);
+          sb[q] = scan_bin(h[j][1][q], sb[q], grb[q], krb[q]);
+        }
+        Dft<H2, true>::run(sa);
+        Dft<H2, true>::run(sb);
 #pragma unroll
         for (int s = 0; s < H2; ++s) {
-          spec[j][0][s] = Y[G::ca_off(pl, s, kA, v)];
-          spec[j][1][s] = Y[G::ca_off(pl, s, kB, v)];
-        }
-        Dft<H2, false>::run(spec[j][0]);
-        Dft<H2, false>::run(spec[j][1]);
-        const float2* kc = khat + size_t(plane_c(pl)) * H * WF;
-        const float4* gt = gates_at(pl, t);
-        if (v == 0) {
-          // packed DC/Nyquist column: hand to the edge pass
-#pragma unroll
-          for (int q = 0; q < H2; ++q) {
-            edge[pl * H + kA + H1 * q] = spec[j][0][q];
-            edge[pl * H + kB + H1 * q] = spec[j][1][q];
-          }
-        } else {
-#pragma unroll
-          for (int a = 0; a < 2; ++a) {
-            const int k = a ? kB : kA;
-#pragma unroll
-            for (int q = 0; q < H2; ++q) {
-              const int uu = k + H1 * q;
-              const float4 g = gt[uu * WF + v];
-              const float2 kh = kc[uu * WF + v];
-              spec[j][a][q] = scan_bin(h[j][a][q], spec[j][a][q], g, kh);
-            }
-          }
+          cplx(G::row_off(pl, s + H2 * kA) + col) = s ? cmul(sa[s], twI1[kA * G::TI1 + s]) : sa[0];
+          cplx(G::row_off(pl, s + H2 * kB) + col) = s ? cmul(sb[s], twI1[kB * G::TI1 + s]) : sb[0];
         }
       }
-    }
-    // prefetch u_{t+1} while the inverse runs
-    if (t + 1 < T) {
-#pragma unroll
-      for (int i = 0; i < G::JLD; ++i)
-        ldu[i] = *reinterpret_cast<const V4*>(u + vec_off(i * NT + tid, t + 1));
+      __builtin_amdgcn_sched_barrier(0);
     }
     __syncthreads();
 
     // ------------------- edge pass: DC and Nyquist columns (unpack, scan, repack)
 #pragma unroll
     for (int j = 0; j < G::JE; ++j) {
-      const int jb = j * NT + tid;
-      if (jb < G::NE) {
-        const int e = jb % HP, pl = jb / HP;
+      const unsigned jb = j * NT + tid;
+      if (jb < unsigned(G::NE)) {
+        const int e = int(jb % HP), pl = int(jb / HP);
         const int uA = e, uB = (e == 0) ? HP : H - e;
-        const int pA = (H - uA) % H, pB = (H - uB) % H;   // partners (-u mod H)
-        const float2 cA = edge[pl * H + uA], cAm = edge[pl * H + pA];
-        const float2 cB = edge[pl * H + uB], cBm = edge[pl * H + pB];
+        float4 ge[4];
+        float2 ke[4];
+        const unsigned kp = unsigned(pl * H * WF);
+        ge[0] = gbuf.ld4(unsigned(uA * WF) * 16u);
+        ge[1] = gbuf.ld4(unsigned(uA * WF + WH) * 16u);
+        ge[2] = gbuf.ld4(unsigned(uB * WF) * 16u);
+        ge[3] = gbuf.ld4(unsigned(uB * WF + WH) * 16u);
+        ke[0] = kbuf.ld2((kp + uA * WF) * 8u);
+        ke[1] = kbuf.ld2((kp + uA * WF + WH) * 8u);
+        ke[2] = kbuf.ld2((kp + uB * WF) * 8u);
+        ke[3] = kbuf.ld2((kp + uB * WF + WH) * 8u);
+        // partners -u mod H: uB for uA when e > 0; both self-partnered when e == 0
+        const float2 cA = edge[pl * H + uA], cB = edge[pl * H + uB];
+        const float2 cAm = (e == 0) ? cA : cB, cBm = (e == 0) ? cB : cA;
         // U(u,0) = (C[u] + conj C[-u]) / 2 ; U(u,W/2) = -i (C[u] - conj C[-u]) / 2
         const float2 u0A = make_float2(0.5f * (cA.x + cAm.x), 0.5f * (cA.y - cAm.y));
-        const float2 uNA = make_float2(0.5f * (cA.y + cAm.y), -0.5f * (cA.x - cAm.x));
+        const float2 uNA = make_float2(0.5f * (cA.y + cAm.y), 0.5f * (cAm.x - cA.x));
         const float2 u0B = make_float2(0.5f * (cB.x + cBm.x), 0.5f * (cB.y - cBm.y));
-        const float2 uNB = make_float2(0.5f * (cB.y + cBm.y), -0.5f * (cB.x - cBm.x));
-        const float2* kc = khat + size_t(plane_c(pl)) * H * WF;
-        const float4* gt = gates_at(pl, t);
-        const float2 y0A = scan_bin(hE[j][0], u0A, gt[uA * WF + 0], kc[uA * WF + 0]);
-        const float2 yNA = scan_bin(hE[j][1], uNA, gt[uA * WF + WH], kc[uA * WF + WH]);
-        const float2 y0B = scan_bin(hE[j][2], u0B, gt[uB * WF + 0], kc[uB * WF + 0]);
-        const float2 yNB = scan_bin(hE[j][3], uNB, gt[uB * WF + WH], kc[uB * WF + WH]);
-        // repack: c[u] = Herm(Y0)[u] + i Herm(YN)[u], Herm(X)[u] = (X[u] + conj X[-u]) / 2.
-        // partner of uA is uB for e > 0; for e == 0 both are self-partnered.
+        const float2 uNB = make_float2(0.5f * (cB.y + cBm.y), 0.5f * (cBm.x - cB.x));
+        const float2 y0A = scan_bin(hE[j][0], u0A, ge[0], ke[0]);
+        const float2 yNA = scan_bin(hE[j][1], uNA, ge[1], ke[1]);
+        const float2 y0B = scan_bin(hE[j][2], u0B, ge[2], ke[2]);
+        const float2 yNB = scan_bin(hE[j][3], uNB, ge[3], ke[3]);
+        // repack: c[u] = Herm(Y0)[u] + i Herm(YN)[u], Herm(X)[u] = (X[u] + conj X[-u]) / 2
         float2 cOutA, cOutB;
         if (e != 0) {
           const float2 h0A = make_float2(0.5f * (y0A.x + y0B.x), 0.5f * (y0A.y - y0B.y));
@@ -406,180 +500,196 @@ gated_scan_pow2(const typename IO::T* __restrict__ u, const typename IO::T* __re
     }
     __syncthreads();
 
-    // ---------------------- I1: inverse DFT-H2 over q, conj twiddle -> CA
-    {
-      float2* X = reinterpret_cast<float2*>(bufX);
+    // ---------------- I1 for the packed column: inverse DFT-H2, conj twiddle
 #pragma unroll
-      for (int j = 0; j < G::JC2; ++j) {
-        const int jb = j * NT + tid;
-        const int v = jb % WH, jj = (jb / WH) % (H1 / 2), pl = jb / (WH * (H1 / 2));
+    for (int j = 0; j < G::JC2; ++j) {
+      const unsigned jb = j * NT + tid;
+      const int v = int(jb % WH), pl = int(jb / (WH * (H1 / 2)));
+      if (v == 0) {
         int kA, kB;
-        pair_units<H1>(jj, kA, kB);
-        if (v == 0) {
+        pair_units<H1>(int((jb / WH) % (H1 / 2)), kA, kB);
+        float2 sa[H2], sb[H2];
 #pragma unroll
-          for (int q = 0; q < H2; ++q) {
-            spec[j][0][q] = edge[pl * H + kA + H1 * q];
-            spec[j][1][q] = edge[pl * H + kB + H1 * q];
-          }
+        for (int q = 0; q < H2; ++q) {
+          sa[q] = edge[pl * H + kA + H1 * q];
+          sb[q] = edge[pl * H + kB + H1 * q];
         }
-        Dft<H2, true>::run(spec[j][0]);
-        Dft<H2, true>::run(spec[j][1]);
+        Dft<H2, true>::run(sa);
+        Dft<H2, true>::run(sb);
+        const int col = G::p_col(0);
 #pragma unroll
         for (int s = 0; s < H2; ++s) {
-          X[G::ca_off(pl, s, kA, v)] = cmulc(spec[j][0][s], twH[s * kA]);
-          X[G::ca_off(pl, s, kB, v)] = cmulc(spec[j][1][s], twH[s * kB]);
+          cplx(G::row_off(pl, s + H2 * kA) + col) = s ? cmul(sa[s], twI1[kA * G::TI1 + s]) : sa[0];
+          cplx(G::row_off(pl, s + H2 * kB) + col) = s ? cmul(sb[s], twI1[kB * G::TI1 + s]) : sb[0];
         }
       }
     }
     __syncthreads();
 
-    // ----------------------------- I2: inverse DFT-H1 over k -> rows (P layout)
-    {
-      const float2* X = reinterpret_cast<const float2*>(bufX);
-      float2* Y = reinterpret_cast<float2*>(bufY);
+    // ----------------------------- I2: inverse DFT-H1 over k -> rows (P slots)
 #pragma unroll
-      for (int j = 0; j < G::JC1; ++j) {
-        const int jb = j * NT + tid;
-        const int v = jb % WH, s = (jb / WH) % H2, pl = jb / (WH * H2);
-        float2 zz[H1];
+    for (int j = 0; j < G::JC1; ++j) {
+      const unsigned jb = j * NT + tid;
+      const int v = int(jb % WH), s = int((jb / WH) % H2), pl = int(jb / (WH * H2));
+      const int col = G::p_col(v);
+      float2 zz[H1];
 #pragma unroll
-        for (int k = 0; k < H1; ++k) zz[k] = X[G::ca_off(pl, s, k, v)];
-        Dft<H1, true>::run(zz);
+      for (int k = 0; k < H1; ++k) zz[k] = cplx(G::row_off(pl, s + H2 * k) + col);
+      Dft<H1, true>::run(zz);
 #pragma unroll
-        for (int m = 0; m < H1; ++m) Y[G::p_off(pl, s + H2 * m, v)] = zz[m];
-      }
+      for (int m = 0; m < H1; ++m) cplx(G::row_off(pl, s + H2 * m) + col) = zz[m];
+      __builtin_amdgcn_sched_barrier(0);
     }
     __syncthreads();
 
     // ------------- I3: build packed Hermitian row pair, inverse DFT-W2, twiddle
-    {
-      const float2* Yc = reinterpret_cast<const float2*>(bufY);
-      float2* X = reinterpret_cast<float2*>(bufX);
 #pragma unroll
-      for (int j = 0; j < G::JR2; ++j) {
-        const int jb = j * NT + tid;
-        const int p = jb % HP, jj = (jb / HP) % (W1 / 2), pl = jb / (HP * (W1 / 2));
-        int kA, kB;
-        pair_units<W1>(jj, kA, kB);
-        float2 za[W2], zb[W2];
-        // Q[v] = Zp[v] + i Zq[v]; Q[W-v] = conj Zp[v] + i conj Zq[v]  (0 < v < W/2)
-        auto fetch = [&](int v, float2& qv, float2& qm) {
-          const float2 a = Yc[G::p_off(pl, p, v)], c = Yc[G::p_off(pl, p + HP, v)];
-          qv = make_float2(a.x - c.y, a.y + c.x);
-          qm = make_float2(a.x + c.y, c.x - a.y);
-        };
-        if (jj != 0) {
+    for (int j = 0; j < G::JR2; ++j) {
+      const unsigned jb = j * NT + tid;
+      const int jj = int(jb % (W1 / 2)), p = int((jb / (W1 / 2)) % HP), pl = int(jb / (HP * (W1 / 2)));
+      int kA, kB;
+      pair_units<W1>(jj, kA, kB);
+      float2 za[W2], zb[W2];
+      // Q[v] = Zp[v] + i Zq[v]; Q[W-v] = conj Zp[v] + i conj Zq[v]  (0 < v < W/2)
+      auto fetch = [&](bool hi, int blk, int q, float2& qv, float2& qm) {
+        const int o0 = hi ? G::hi_off(pl, p, blk, 2 * q) : G::lo_off(pl, p, blk, 2 * q);
+        const int o1 = hi ? G::hi_off(pl, p + HP, blk, 2 * q) : G::lo_off(pl, p + HP, blk, 2 * q);
+        const float2 x = cplx(o0), c = cplx(o1);
+        qv = make_float2(x.x - c.y, x.y + c.x);
+        qm = make_float2(x.x + c.y, c.x - x.y);
+      };
+      if (jj != 0) {
 #pragma unroll
-          for (int q = 0; q < W2 / 2; ++q) {
-            fetch(kA + W1 * q, za[q], zb[W2 - 1 - q]);
-            fetch(kB + W1 * q, zb[q], za[W2 - 1 - q]);
-          }
-        } else {
-          const float2 cp = Yc[G::p_off(pl, p, 0)], cq = Yc[G::p_off(pl, p + HP, 0)];
-          za[0] = make_float2(cp.x, cq.x);          // Q[0]   = Re c_p + i Re c_q
-          za[W2 / 2] = make_float2(cp.y, cq.y);     // Q[W/2] = Im c_p + i Im c_q
-#pragma unroll
-          for (int q = 1; q < W2 / 2; ++q) fetch(W1 * q, za[q], za[W2 - q]);
-#pragma unroll
-          for (int q = 0; q < W2 / 2; ++q) fetch(W1 / 2 + W1 * q, zb[q], zb[W2 - 1 - q]);
+        for (int q = 0; q < W2 / 2; ++q) {
+          fetch(false, kA, q, za[q], zb[W2 - 1 - q]);
+          fetch(true, kB, q, zb[q], za[W2 - 1 - q]);
         }
-        Dft<W2, true>::run(za);
-        Dft<W2, true>::run(zb);
+      } else {
+        const float2 cp = cplx(G::lo_off(pl, p, 0, 0)), cq = cplx(G::lo_off(pl, p + HP, 0, 0));
+        za[0] = make_float2(cp.x, cq.x);          // Q[0]   = Re c_p + i Re c_q
+        za[W2 / 2] = make_float2(cp.y, cq.y);     // Q[W/2] = Im c_p + i Im c_q
 #pragma unroll
-        for (int s = 0; s < W2; ++s) {
-          X[G::ra_off(pl, kA, s, p)] = cmulc(za[s], twW[s * kA]);
-          X[G::ra_off(pl, kB, s, p)] = cmulc(zb[s], twW[s * kB]);
-        }
+        for (int q = 1; q < W2 / 2; ++q) fetch(false, 0, q, za[q], za[W2 - q]);
+#pragma unroll
+        for (int q = 0; q < W2 / 2; ++q) fetch(true, W1 / 2, q, zb[q], zb[W2 - 1 - q]);
       }
+      Dft<W2, true>::run(za);
+      Dft<W2, true>::run(zb);
+#pragma unroll
+      for (int s = 0; s < W2; ++s) {
+        const float2 oa = s ? cmul(za[s], twI3[kA * G::TI3 + s]) : za[0];
+        const float2 ob = s ? cmul(zb[s], twI3[kB * G::TI3 + s]) : zb[0];
+        buf[G::lo_off(pl, p, kA, s)] = oa.x;
+        buf[G::lo_off(pl, p + HP, kA, s)] = oa.y;
+        buf[G::hi_off(pl, p, kB, s)] = ob.x;
+        buf[G::hi_off(pl, p + HP, kB, s)] = ob.y;
+      }
+      __builtin_amdgcn_sched_barrier(0);
     }
     __syncthreads();
 
     // ------------------------ I4: inverse DFT-W1 over k -> real rows p, p+H/2
-    {
-      const float2* X = reinterpret_cast<const float2*>(bufX);
 #pragma unroll
-      for (int j = 0; j < G::JR1; ++j) {
-        const int jb = j * NT + tid;
-        const int s = jb % W2, p = (jb / W2) % HP, pl = jb / (W2 * HP);
-        float2 zz[W1];
+    for (int j = 0; j < G::JR1; ++j) {
+      int pl, p, s;
+      G::r1_job(j * NT + tid, pl, p, s);
+      float2 zz[W1];
 #pragma unroll
-        for (int k = 0; k < W1; ++k) zz[k] = X[G::ra_off(pl, k, s, p)];
-        Dft<W1, true>::run(zz);
-#pragma unroll
-        for (int m = 0; m < W1; ++m) {
-          bufY[G::real_off(pl, p, s + W2 * m)] = zz[m].x;
-          bufY[G::real_off(pl, p + HP, s + W2 * m)] = zz[m].y;
-        }
+      for (int k = 0; k < W1; ++k) {
+        const int o = (k >= W1 / 2) ? (s ^ G::HALF) : s;
+        zz[k] = make_float2(buf[G::row_off(pl, p) + k * W2 + o], buf[G::row_off(pl, p + HP) + k * W2 + o]);
       }
+      Dft<W1, true>::run(zz);
+#pragma unroll
+      for (int m = 0; m < W1; ++m) {
+        const int o = (m >= W1 / 2) ? (s ^ G::HALF) : s;
+        buf[G::row_off(pl, p) + m * W2 + o] = zz[m].x;
+        buf[G::row_off(pl, p + HP) + m * W2 + o] = zz[m].y;
+      }
+      __builtin_amdgcn_sched_barrier(0);
     }
     __syncthreads();
 
-    // ----------------------------------------------- STORE y_t = y * z_gate
+    // ---------- STORE y_t = y * z_gate, and LOAD u_{t+1} into the same slots
+    // (in chunks of CH vectors to bound the registers in flight)
     {
+      constexpr int CH = G::JLD < 8 ? G::JLD : 8;
+      const V4* zsrc = reinterpret_cast<const V4*>(zp + group_elems(t));
+      const V4* usrc = reinterpret_cast<const V4*>(up + group_elems(t + 1 < T ? t + 1 : t));
+      V4* dst = reinterpret_cast<V4*>(yp + group_elems(t));
 #pragma unroll
-      for (int i = 0; i < G::JLD; ++i) {
-        const int f = i * NT + tid;
-        const int pl = f / (H * W / 4);
-        const int rem = f % (H * W / 4);
-        const int r = rem / (W / 4), c4 = rem % (W / 4);
-        const float4 yv = *reinterpret_cast<const float4*>(bufY + G::real_off(pl, r, 4 * c4));
-        const float4 gv = act4(IO::to_f4(ldg[i]), z_act);
-        *reinterpret_cast<V4*>(y + vec_off(f, t)) =
-            IO::from_f4(make_float4(yv.x * gv.x, yv.y * gv.y, yv.z * gv.z, yv.w * gv.w));
+      for (int c = 0; c < G::JLD; c += CH) {
+        V4 ldg[CH], ldu[CH];
+#pragma unroll
+        for (int i = 0; i < CH; ++i) ldg[i] = zsrc[(c + i) * NT + tid];
+        if (t + 1 < T) {
+#pragma unroll
+          for (int i = 0; i < CH; ++i) ldu[i] = usrc[(c + i) * NT + tid];
+        }
+#pragma unroll
+        for (int i = 0; i < CH; ++i) {
+          const unsigned f = (c + i) * NT + tid;
+          const float4 yv = v4_load(f);
+          const float4 gv = act4(IO::to_f4(ldg[i]), a.z_act);
+          dst[f] = IO::from_f4(make_float4(yv.x * gv.x, yv.y * gv.y, yv.z * gv.z, yv.w * gv.w));
+        }
+        if (t + 1 < T) {
+#pragma unroll
+          for (int i = 0; i < CH; ++i) v4_store((c + i) * NT + tid, act4(IO::to_f4(ldu[i]), a.u_act));
+        }
+        __builtin_amdgcn_sched_barrier(0);
       }
     }
+    __syncthreads();
   }
 }
 
 // ----------------------------------------------------------------- launchers
 
-template <int LH, int LW, int NP, class IO>
-static hipError_t run_scan(const void* u, const void* z, void* y, int B, int T, int C,
-                           const float4* gates, const float2* khat, int u_act, int z_act, hipStream_t s) {
-  using G = Geom<LH, LW, NP>;
-  const long long blocks = (long long)B * C / NP;
-  hipLaunchKernelGGL((gated_scan_pow2<LH, LW, NP, IO>), dim3(unsigned(blocks)), dim3(G::NT), 0, s,
-                     static_cast<const typename IO::T*>(u), static_cast<const typename IO::T*>(z),
-                     static_cast<typename IO::T*>(y), gates, khat, T, C, u_act, z_act);
+template <int LH, int LW, int NP, int PPT, class IO>
+static hipError_t run_scan(const ScanArgs& a, int B, hipStream_t s) {
+  using G = Geom<LH, LW, NP, PPT>;
+  const long long blocks = (long long)B * a.C / NP;
+  hipLaunchKernelGGL((gated_scan_pow2<LH, LW, NP, PPT, IO>), dim3(unsigned(blocks)), dim3(G::NT), 0, s, a);
   return hipGetLastError();
 }
 
 // plane-group sizes per plane size, largest first; a variant is usable when it
-// divides B * C.  Large groups amortise the per-workgroup set-up on small planes.
+// divides C (one batch element per workgroup).  The largest group that still
+// gives >= 512 workgroups wins; small planes need large groups to fill a
+// workgroup with whole waves.
 template <class IO>
-static hipError_t dispatch_scan(const void* u, const void* z, void* y, int B, int T, int C, int H, int W,
-                                const float4* gates, const float2* khat, int ua, int za, hipStream_t s) {
-  const long long P = (long long)B * C;
+static hipError_t dispatch_scan(const ScanArgs& a, int B, int H, int W, hipStream_t s) {
+  const int C = a.C;
   auto pick = [&](std::initializer_list<int> nps) -> int {
     int best = 0;
-    for (int np : nps) {        // largest group that still leaves >= 512 workgroups
-      if (P % np) continue;
-      if (best == 0) best = np;
-      if (P / np >= 512) return np;
+    for (int np : nps) {
+      if (C % np) continue;
       best = np;
+      if ((long long)B * C / np >= 512) return np;
     }
     return best;
   };
-#define CSSM_SCAN_CASE(LH, NP_) \
-  if (np == NP_) return run_scan<LH, LH, NP_, IO>(u, z, y, B, T, C, gates, khat, ua, za, s);
+#define CSSM_SCAN_CASE(LH, NP_, PPT_) \
+  if (np == NP_) return run_scan<LH, LH, NP_, PPT_, IO>(a, B, s);
   if (H == 128 && W == 128) {
     const int np = pick({1});
-    CSSM_SCAN_CASE(7, 1)
+    CSSM_SCAN_CASE(7, 1, 64)
   } else if (H == 64 && W == 64) {
     const int np = pick({4, 2, 1});
-    CSSM_SCAN_CASE(6, 4) CSSM_SCAN_CASE(6, 2) CSSM_SCAN_CASE(6, 1)
+    CSSM_SCAN_CASE(6, 4, 64) CSSM_SCAN_CASE(6, 2, 64) CSSM_SCAN_CASE(6, 1, 64)
   } else if (H == 32 && W == 32) {
     const int np = pick({8, 4, 2});
-    CSSM_SCAN_CASE(5, 8) CSSM_SCAN_CASE(5, 4) CSSM_SCAN_CASE(5, 2)
+    CSSM_SCAN_CASE(5, 8, 32) CSSM_SCAN_CASE(5, 4, 32) CSSM_SCAN_CASE(5, 2, 32)
   } else if (H == 16 && W == 16) {
     const int np = pick({16, 8});
-    CSSM_SCAN_CASE(4, 16) CSSM_SCAN_CASE(4, 8)
+    CSSM_SCAN_CASE(4, 16, 32) CSSM_SCAN_CASE(4, 8, 32)
   } else if (H == 8 && W == 8) {
     const int np = pick({32});
-    CSSM_SCAN_CASE(3, 32)
+    CSSM_SCAN_CASE(3, 32, 32)
   } else if (H == 4 && W == 4) {
     const int np = pick({128});
-    CSSM_SCAN_CASE(2, 128)
+    CSSM_SCAN_CASE(2, 128, 32)
   }
 #undef CSSM_SCAN_CASE
   return hipErrorInvalidValue;
@@ -589,11 +699,34 @@ bool gated_scan_has_kernel(int H, int W) {
   return H == W && (H == 4 || H == 8 || H == 16 || H == 32 || H == 64 || H == 128);
 }
 
+int gated_scan_min_group(int H, int W) {
+  if (H != W) return 0;
+  switch (H) {
+    case 128: return 1;
+    case 64: return 1;
+    case 32: return 2;
+    case 16: return 8;
+    case 8: return 32;
+    case 4: return 128;
+    default: return 0;
+  }
+}
+
 hipError_t launch_gated_scan(const void* u, const void* z, void* y, int dtype, int B, int T, int C, int H,
                              int W, const float4* gates, const float2* khat, int u_act, int z_act,
                              hipStream_t s) {
-  if (dtype == 0) return dispatch_scan<IoF32>(u, z, y, B, T, C, H, W, gates, khat, u_act, z_act, s);
-  return dispatch_scan<IoBF16>(u, z, y, B, T, C, H, W, gates, khat, u_act, z_act, s);
+  ScanArgs a;
+  a.u = u;
+  a.z = z;
+  a.y = y;
+  a.gates = gates;
+  a.khat = khat;
+  a.T = T;
+  a.C = C;
+  a.u_act = u_act;
+  a.z_act = z_act;
+  if (dtype == 0) return dispatch_scan<IoF32>(a, B, H, W, s);
+  return dispatch_scan<IoBF16>(a, B, H, W, s);
 }
 
 }  // namespace cssm

@@ -19,8 +19,10 @@ hipError_t launch_plane_mean(const void* x, int dtype, long long nplanes, int HW
                              hipStream_t s);
 hipError_t launch_gated_gates(const float* ctx, int BT, int C, int H, int W, int factored, int act,
                               const GateWeights& w, float c_scale, float4* gates, hipStream_t s);
-// returns hipErrorInvalidValue if no kernel exists for the shape
+// fused scan: plane sizes with a kernel, and the smallest plane group (C must be a multiple)
 bool gated_scan_has_kernel(int H, int W);
+int gated_scan_min_group(int H, int W);
+// returns hipErrorInvalidValue if no kernel exists for the shape
 hipError_t launch_gated_scan(const void* u, const void* z, void* y, int dtype, int B, int T, int C, int H,
                              int W, const float4* gates, const float2* khat, int u_act, int z_act,
                              hipStream_t s);

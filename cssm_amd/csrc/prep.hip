@@ -85,7 +85,9 @@ __global__ void spectral_kernel_prep(const float* __restrict__ k, int K, int H, 
 // ---------------------------------------------------------------------------
 // Gates (cssm.py:536-556, _compute_gate :432-441, GOOM shifts :559-567).
 // One block per (b, t).  Output per bin (u, v) of the (H, W/2+1) half
-// spectrum, float4 = (exp(-Delta), Delta + 1e-8, B, C * c_scale), where
+// spectrum, float4 = (exp(-Delta), (Delta + 1e-8) B, (Delta + 1e-8) 1e-7, C * c_scale):
+// the decay, the input gain, the input term that replaces (Delta + 1e-8) U B
+// when |U B| < 1e-7 (the to_goom floor), and the readout gain; where
 //   Delta = act(G_delta), act in {softplus, 2*sigmoid, exp(clip(-4, 2))}
 //   dense:    G_x[u, v] = ctx . kernel[:, u*WF + v] + bias[u*WF + v]
 //   factored: G_x[u, v] = (ctx . kh[:, u] + bh[u]) * (ctx . kw[:, v] + bw[v])
@@ -134,8 +136,8 @@ __global__ void gated_gates_kernel(const float* __restrict__ ctx, int C, int H, 
       const int u = o / WF, v = o % WF;
       float gr[3];
       for (int g = 0; g < 3; ++g) gr[g] = fac[g * (H + WF) + u] * fac[g * (H + WF) + H + v];
-      const float d = gate_act(gr[0], act);
-      out[size_t(bt) * nbin + o] = make_float4(expf(-d), d + 1e-8f, gr[1], gr[2] * c_scale);
+      const float d = gate_act(gr[0], act), dd = d + 1e-8f;
+      out[size_t(bt) * nbin + o] = make_float4(expf(-d), dd * gr[1], dd * 1e-7f, gr[2] * c_scale);
     }
   } else {
     for (int o = threadIdx.x; o < nbin; o += blockDim.x) {
@@ -146,8 +148,8 @@ __global__ void gated_gates_kernel(const float* __restrict__ ctx, int C, int H, 
         for (int c = 0; c < C; ++c) acc = fmaf(cx[c], kk[size_t(c) * nbin], acc);
         gr[g] = acc;
       }
-      const float d = gate_act(gr[0], act);
-      out[size_t(bt) * nbin + o] = make_float4(expf(-d), d + 1e-8f, gr[1], gr[2] * c_scale);
+      const float d = gate_act(gr[0], act), dd = d + 1e-8f;
+      out[size_t(bt) * nbin + o] = make_float4(expf(-d), dd * gr[1], dd * 1e-7f, gr[2] * c_scale);
     }
   }
 }

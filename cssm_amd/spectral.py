@@ -77,7 +77,8 @@ def gate_params_struct(gp: Dict[str, Dict[str, torch.Tensor]], gate_type: str,
 def gated_gates(ctx: torch.Tensor, params: Dict, H: int, W: int, gate_type: str = "dense",
                 activation: str = "softplus", c_scale: float = 1.0,
                 out: Optional[torch.Tensor] = None) -> torch.Tensor:
-    """(B, T, H, Wf, 4) = [exp(-Delta), Delta + 1e-8, B, C * c_scale] (cssm.py:536-567)."""
+    """(B, T, H, Wf, 4) = [exp(-Delta), (Delta + 1e-8) B, (Delta + 1e-8) 1e-7, C * c_scale]
+    (cssm.py:536-567)."""
     _dev(ctx, "ctx", torch.float32)
     B, T, C = ctx.shape
     if out is None:
@@ -94,22 +95,24 @@ def gated_scan(u: torch.Tensor, z: torch.Tensor, gates: torch.Tensor, khat: torc
                out: Optional[torch.Tensor] = None) -> torch.Tensor:
     """Fused rfft2 -> recurrence -> irfft2 -> x z for plane-major (B, T, C, H, W) u, z.
 
-    ``gates`` must come from :func:`gated_gates` with ``c_scale = 1/(H*W)``;
-    ``khat`` from :func:`spectral_kernel` with ``goom_floor=True``.
+    ``gates`` are the per-bin planes (B, T, H, Wf, 4) from :func:`gated_gates`
+    made with ``c_scale = 1/(H*W)``; ``khat`` comes from
+    :func:`spectral_kernel` with ``goom_floor=True``.
     """
     _dev(u, "u")
     _dev(z, "z", u.dtype)
     if u.dtype not in _DTYPES:
         raise ValueError(f"unsupported dtype {u.dtype}")
     B, T, C, H, W = u.shape
+    Wf = W // 2 + 1
     if z.shape != u.shape:
         raise ValueError("u and z must have the same shape")
     _dev(gates, "gates", torch.float32)
-    if tuple(gates.shape) != (B, T, H, W // 2 + 1, 4):
-        raise ValueError(f"gates shape {tuple(gates.shape)} != {(B, T, H, W // 2 + 1, 4)}")
+    if tuple(gates.shape) != (B, T, H, Wf, 4):
+        raise ValueError(f"gates shape {tuple(gates.shape)} != {(B, T, H, Wf, 4)}")
     _dev(khat, "khat", torch.complex64)
-    if tuple(khat.shape) != (C, H, W // 2 + 1):
-        raise ValueError(f"khat shape {tuple(khat.shape)} != {(C, H, W // 2 + 1)}")
+    if tuple(khat.shape) != (C, H, Wf):
+        raise ValueError(f"khat shape {tuple(khat.shape)} != {(C, H, Wf)}")
     if out is None:
         out = torch.empty_like(u)
     _dev(out, "out", u.dtype)
@@ -120,3 +123,7 @@ def gated_scan(u: torch.Tensor, z: torch.Tensor, gates: torch.Tensor, khat: torc
 
 def gated_scan_supported(H: int, W: int) -> bool:
     return bool(_lib.load().cssm_gated_scan_supported(H, W))
+
+
+def gated_scan_min_group(H: int, W: int) -> int:
+    return int(_lib.load().cssm_gated_scan_min_group(H, W))

@@ -112,7 +112,9 @@ int cssm_plane_mean(const void* x, int dtype, long long nplanes, int H, int W, i
  * _compute_gate) and the Delta terms of cssm.py:559-567.
  *   ctx   (B, T, C) float32
  *   gates (B, T, H, Wf, 4) float32 out, per bin:
- *         [exp(-Delta), Delta + 1e-8, B, C * c_scale]
+ *         [exp(-Delta), (Delta + 1e-8) B, (Delta + 1e-8) 1e-7, C * c_scale]
+ *         = decay, input gain, the input term that replaces (Delta + 1e-8) U B
+ *         when |U B| < 1e-7 (the to_goom floor), readout gain.
  * c_scale = 1 gives the reference values; cssm_gated_scan_fwd expects
  * c_scale = 1 / (H * W) (the irfft2 normalisation folded into C).
  */
@@ -127,13 +129,16 @@ int cssm_gated_gates(const float* ctx, int B, int T, int C, int H, int W,
  * jax.lax.associative_scan(cssm_scalar_scan_op), from_goom, x C, irfft2,
  * x SiLU(z)); math.py:24-54 and operations.py:17-41 are the combiner it
  * evaluates exactly (the log-space scan is this linear recurrence).
- *   u, z, y  (B, T, C, H, W) plane-major of dtype; u = x_main after the short
- *            convolutions, z = the gate branch; u_act / z_act select SiLU on
- *            load (the reference applies SiLU to both, cssm.py:502, :581).
- *   gates    from cssm_gated_gates with c_scale = 1/(H*W)
- *   khat     from cssm_spectral_kernel with goom_floor = 1, C channels
- * Supported planes: H = W in {4, 8, 16, 32, 64, 128}.  Pointers u, z, y must
- * be 16-byte aligned (f32) or 8-byte aligned (bf16); gates 16, khat 8.
+ *   u, z, y   (B, T, C, H, W) plane-major of dtype; u = x_main after the short
+ *             convolutions, z = the gate branch; u_act / z_act select SiLU on
+ *             load (the reference applies SiLU to both, cssm.py:502, :581).
+ *   gates     (B, T, H, Wf, 4) from cssm_gated_gates with c_scale = 1/(H*W)
+ *             (the irfft2 normalisation folded into C); dense and factored
+ *             gate_type both arrive in this per-bin form.
+ *   khat      from cssm_spectral_kernel with goom_floor = 1, C channels
+ * Supported planes: H = W in {4, 8, 16, 32, 64, 128}, with C a multiple of
+ * cssm_gated_scan_min_group(H, W).  u, z, y must be 16-byte aligned (f32) or
+ * 8-byte aligned (bf16); gates 16; khat 8.
  */
 int cssm_gated_scan_fwd(const void* u, const void* z, void* y, int dtype, int B, int T, int C,
                         int H, int W, const float* gates, const float* khat, int u_act,
@@ -141,6 +146,9 @@ int cssm_gated_scan_fwd(const void* u, const void* z, void* y, int dtype, int B,
 
 /* 1 if cssm_gated_scan_fwd has a kernel for (H, W), else 0. */
 int cssm_gated_scan_supported(int H, int W);
+
+/* Channel-count granule of the fused scan for (H, W): C must be a multiple (0 = unsupported). */
+int cssm_gated_scan_min_group(int H, int W);
 
 #ifdef __cplusplus
 }

@@ -41,7 +41,8 @@ def _rand_gates(rng, B, T, H, W, zero_rows=False):
 
 
 def _pack_gates(delta, gB, gC, H, W):
-    g = np.stack([np.exp(-delta), delta + 1e-8, gB, gC / (H * W)], axis=-1)
+    d = delta + 1e-8
+    g = np.stack([np.exp(-delta), d * gB, d * 1e-7, gC / (H * W)], axis=-1)
     return _dev(g)
 
 
@@ -97,9 +98,10 @@ def test_gated_gates_match_oracle(S, gate_type, act):
     pd = {k: ({kk: _dev(vv) for kk, vv in v.items()} if isinstance(v, dict) else _dev(v))
           for k, v in p.items()}
     got = to_np(S.gated_gates(_dev(ctx), pd, H, W, gate_type, act, c_scale=0.5))
+    d = delta + 1e-8
     assert np.max(np.abs(got[..., 0] - np.exp(-delta))) < 1e-5
-    assert np.max(np.abs(got[..., 1] - (delta + 1e-8))) < 1e-5 * max(1, np.max(delta))
-    assert rel_err(got[..., 2], gB) < 1e-5
+    assert rel_err(got[..., 1], d * gB) < 1e-5
+    assert np.max(np.abs(got[..., 2] - d * 1e-7)) < 1e-12 * max(1, np.max(delta))
     assert rel_err(got[..., 3], 0.5 * gC) < 1e-5
 
 
@@ -107,7 +109,7 @@ def test_gated_gates_match_oracle(S, gate_type, act):
 
 SCAN_CASES = [
     # (B, T, C, H, W)
-    (2, 1, 64, 4, 4), (1, 3, 128, 4, 4), (2, 3, 32, 8, 8), (2, 4, 16, 16, 16), (1, 3, 8, 32, 32),
+    (2, 1, 128, 4, 4), (1, 3, 128, 4, 4), (2, 3, 32, 8, 8), (2, 4, 16, 16, 16), (1, 3, 8, 32, 32),
     (2, 5, 8, 32, 32), (1, 3, 4, 64, 64), (2, 2, 2, 64, 64), (1, 3, 2, 128, 128), (2, 8, 1, 128, 128),
 ]
 
