@@ -146,4 +146,74 @@ int cssm_gated_scan_fwd(const void* u, const void* z, void* y, int dtype, int B,
   return hip_status(e, "cssm_gated_scan_fwd");
 }
 
+size_t cssm_proj_in_workspace_size(int F, int HW, int N) {
+  if (F <= 0 || HW <= 0 || N <= 0) return 0;
+  const int tm = cssm::proj_in_tile_rows();
+  if (HW % tm != 0) return 0;
+  return size_t(F) * (HW / tm) * (N / 2) * sizeof(float);
+}
+
+int cssm_proj_in(const void* x, int in_dtype, int F, int HW, int K, int N, const float* kernel, const float* bias,
+                 void* out_lo, void* out_hi, int out_dtype, int act_lo, int act_hi, float* ctx, void* workspace,
+                 size_t workspace_bytes, void* stream) {
+  if (!x || !kernel || !bias || !out_lo || !out_hi)
+    return fail(CSSM_ERR_NULL, "cssm_proj_in: x, kernel, bias, out_lo and out_hi must be non-null");
+  if (F <= 0 || HW <= 0 || K <= 0 || N <= 0 || (N % 2) != 0)
+    return fail(CSSM_ERR_SHAPE, "cssm_proj_in: F=%d HW=%d K=%d N=%d (N must be even)", F, HW, K, N);
+  if ((long long)F * HW > 0x7fffffffLL) return fail(CSSM_ERR_SHAPE, "cssm_proj_in: F*HW exceeds 2^31");
+  if ((in_dtype != CSSM_F32 && in_dtype != CSSM_BF16) || (out_dtype != CSSM_F32 && out_dtype != CSSM_BF16))
+    return fail(CSSM_ERR_ARG, "cssm_proj_in: dtypes %d/%d", in_dtype, out_dtype);
+  if ((act_lo != CSSM_LOAD_IDENTITY && act_lo != CSSM_LOAD_SILU) || (act_hi != CSSM_LOAD_IDENTITY && act_hi != CSSM_LOAD_SILU))
+    return fail(CSSM_ERR_ARG, "cssm_proj_in: act_lo=%d act_hi=%d", act_lo, act_hi);
+  if (out_dtype == CSSM_F32 && (!aligned(out_lo, 16) || !aligned(out_hi, 16)))
+    return fail(CSSM_ERR_ALIGN, "cssm_proj_in: f32 outputs must be 16-byte aligned");
+  const hipStream_t s = static_cast<hipStream_t>(stream);
+  const int M = F * HW;
+  const int tm = cssm::proj_in_tile_rows();
+  const bool fused_ctx = ctx != nullptr && (HW % tm) == 0;
+  float* partial = nullptr;
+  if (fused_ctx) {
+    const size_t need = cssm_proj_in_workspace_size(F, HW, N);
+    if (!workspace || workspace_bytes < need)
+      return fail(CSSM_ERR_ARG, "cssm_proj_in: ctx needs a %zu-byte workspace (got %zu)", need, workspace_bytes);
+    partial = static_cast<float*>(workspace);
+  }
+  hipError_t e = cssm::launch_proj_in(x, in_dtype, M, K, N, kernel, bias, HW, out_lo, out_hi, out_dtype, act_lo,
+                                      act_hi, partial, s);
+  if (e != hipSuccess) return hip_status(e, "cssm_proj_in");
+  if (ctx != nullptr) {
+    e = fused_ctx ? cssm::launch_ctx_reduce(partial, F, HW / tm, N / 2, 1.0f / float(HW), ctx, s)
+                  : cssm::launch_plane_mean(out_lo, out_dtype, (long long)F * (N / 2), HW, 0, ctx, s);
+  }
+  return hip_status(e, "cssm_proj_in");
+}
+
+int cssm_proj_out(const void* y, int in_dtype, int F, int HW, int K, int N, const float* kernel, const float* bias,
+                  void* out, int out_dtype, void* stream) {
+  if (!y || !kernel || !bias || !out)
+    return fail(CSSM_ERR_NULL, "cssm_proj_out: y, kernel, bias and out must be non-null");
+  if (F <= 0 || HW <= 0 || K <= 0 || N <= 0) return fail(CSSM_ERR_SHAPE, "cssm_proj_out: F=%d HW=%d K=%d N=%d", F, HW, K, N);
+  if ((long long)F * HW > 0x7fffffffLL) return fail(CSSM_ERR_SHAPE, "cssm_proj_out: F*HW exceeds 2^31");
+  if ((in_dtype != CSSM_F32 && in_dtype != CSSM_BF16) || (out_dtype != CSSM_F32 && out_dtype != CSSM_BF16))
+    return fail(CSSM_ERR_ARG, "cssm_proj_out: dtypes %d/%d", in_dtype, out_dtype);
+  return hip_status(cssm::launch_proj_out(y, in_dtype, F * HW, K, N, kernel, bias, HW, out, out_dtype,
+                                          static_cast<hipStream_t>(stream)),
+                    "cssm_proj_out");
+}
+
+int cssm_short_conv(const void* x, int in_dtype, int B, int T, int C, int H, int W, int ks, const float* ws,
+                    const float* bs, int kt, const float* wt, const float* bt, void* u, int out_dtype, float* ctx,
+                    void* stream) {
+  if (!x || !u) return fail(CSSM_ERR_NULL, "cssm_short_conv: x and u must be non-null");
+  if ((ks > 0 && (!ws || !bs)) || (kt > 0 && (!wt || !bt)))
+    return fail(CSSM_ERR_NULL, "cssm_short_conv: weights of an enabled convolution are missing");
+  if (B <= 0 || T <= 0 || C <= 0 || H <= 0 || W <= 0 || ks < 0 || kt < 0 || ks > 15 || kt > 16)
+    return fail(CSSM_ERR_SHAPE, "cssm_short_conv: B=%d T=%d C=%d H=%d W=%d ks=%d kt=%d", B, T, C, H, W, ks, kt);
+  if ((in_dtype != CSSM_F32 && in_dtype != CSSM_BF16) || (out_dtype != CSSM_F32 && out_dtype != CSSM_BF16))
+    return fail(CSSM_ERR_ARG, "cssm_short_conv: dtypes %d/%d", in_dtype, out_dtype);
+  return hip_status(cssm::launch_short_conv(x, in_dtype, B, T, C, H, W, ks, ws, bs, kt, wt, bt, u, out_dtype, ctx,
+                                            static_cast<hipStream_t>(stream)),
+                    "cssm_short_conv");
+}
+
 }  // extern "C"

@@ -27,4 +27,18 @@ hipError_t launch_gated_scan(const void* u, const void* z, void* y, int dtype, i
                              int W, const float4* gates, const float2* khat, int u_act, int z_act,
                              hipStream_t s);
 
+// projection GEMMs (fp32 MFMA)
+int proj_in_tile_rows();
+hipError_t launch_proj_in(const void* X, int in_dtype, int M, int K, int N, const float* W, const float* b, int HW,
+                          void* out_lo, void* out_hi, int out_dtype, int act_lo, int act_hi, float* partial,
+                          hipStream_t s);
+hipError_t launch_proj_out(const void* Y, int in_dtype, int M, int K, int N, const float* W, const float* b, int HW,
+                           void* out, int out_dtype, hipStream_t s);
+hipError_t launch_ctx_reduce(const float* partial, int F, int tiles_per_frame, int C, float inv_hw, float* ctx,
+                             hipStream_t s);
+
+hipError_t launch_short_conv(const void* x, int in_dtype, int B, int T, int C, int H, int W, int ks, const float* ws,
+                             const float* bs, int kt, const float* wt, const float* bt, void* u, int out_dtype,
+                             float* ctx, hipStream_t s);
+
 }  // namespace cssm

@@ -1,0 +1,289 @@
+// Projection GEMMs of the spectral layer on fp32 MFMA (gfx950), with the
+// layout change between the reference's channels-last tensors and the scan's
+// plane-major planes fused into the GEMM:
+//   proj_in : X (M, K) channels-last  ->  two plane-major outputs (the two
+//             halves of the N output channels), bias, optional SiLU on each
+//             half, optional per-tile channel sums of the first half (the
+//             spatial mean ctx), cssm.py:480-484 + :502 + :536 + :581.
+//   proj_out: Y plane-major (F, K, HW) ->  out (M, N) channels-last, bias,
+//             cssm.py:584.
+// M = F * HW rows (F frames of HW pixels).  fp32 accumulation throughout.
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+#include "launch.h"
+
+namespace cssm {
+
+typedef float floatx4 __attribute__((ext_vector_type(4)));
+
+__device__ __forceinline__ float ld_el(const float* p, size_t i) { return p[i]; }
+__device__ __forceinline__ float ld_el(const uint16_t* p, size_t i) { return __uint_as_float(uint32_t(p[i]) << 16); }
+__device__ __forceinline__ void st_el(float* p, size_t i, float v) { p[i] = v; }
+__device__ __forceinline__ void st_el(uint16_t* p, size_t i, float v) {
+  uint32_t x = __float_as_uint(v);
+  if ((x & 0x7f800000u) == 0x7f800000u) {
+    p[i] = uint16_t((x >> 16) | ((x & 0x007fffffu) ? 0x40u : 0u));
+  } else {
+    x += 0x7fffu + ((x >> 16) & 1u);
+    p[i] = uint16_t(x >> 16);
+  }
+}
+__device__ __forceinline__ float silu_acc(float x) { return x / (1.0f + expf(-x)); }
+__device__ __forceinline__ void st4(float* p, size_t i, const float* v) {
+  *reinterpret_cast<float4*>(p + i) = make_float4(v[0], v[1], v[2], v[3]);
+}
+__device__ __forceinline__ void st4(uint16_t* p, size_t i, const float* v) {
+  for (int r = 0; r < 4; ++r) st_el(p, i + r, v[r]);
+}
+
+// Block tile TM rows x TN output channels, K staged through LDS in chunks of
+// KC.  Wave layout WMW x WNW waves, each owning (TM / WMW) x (TN / WNW)
+// outputs as 16x16 MFMA tiles (v_mfma_f32_16x16x4f32: lane l holds
+// A[l % 16][l / 16], B[l / 16][l % 16] and D rows 4 (l / 16) .. +3 of column l % 16).
+template <int TM, int TN, int WMW, int WNW>
+struct ProjTile {
+  static constexpr int KC = 32;
+  static constexpr int NT = 64 * WMW * WNW;
+  static constexpr int MT = TM / WMW / 16, NTL = TN / WNW / 16;   // 16x16 tiles per wave
+  static constexpr int AP = KC + 1;     // A tile row pitch (rows = TM), padded
+  static constexpr int BP = TN + 4;     // B tile row pitch (rows = KC)
+};
+
+// ---------------------------------------------------------------------------
+// proj_in: out_lo[f][c][p] = act_lo(sum_k X[f*HW+p][k] W[k][c] + b[c]),   c < N/2
+//          out_hi[f][c][p] = act_hi(... c + N/2 ...)
+// partial (optional): partial[tile][c] = sum over the tile's rows of out_lo
+// (requires HW % TM == 0 so a tile lies in one frame).
+// ---------------------------------------------------------------------------
+template <int TM, int TN, int WMW, int WNW, class TI, class TO>
+__global__ void __launch_bounds__(64 * WMW * WNW)
+proj_in_kernel(const TI* __restrict__ X, int M, int K, int N, const float* __restrict__ Wt,
+               const float* __restrict__ bias, int HW, TO* __restrict__ out_lo, TO* __restrict__ out_hi,
+               int act_lo, int act_hi, float* __restrict__ partial) {
+  using P = ProjTile<TM, TN, WMW, WNW>;
+  __shared__ float As[TM * P::AP];
+  __shared__ float Bs[P::KC * P::BP];
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int wm = wave / WNW, wn = wave % WNW;
+  const int m0 = blockIdx.x * TM, n0 = blockIdx.y * TN;
+  const int NH = N / 2;
+
+  floatx4 acc[P::MT][P::NTL];
+#pragma unroll
+  for (int i = 0; i < P::MT; ++i)
+#pragma unroll
+    for (int j = 0; j < P::NTL; ++j) acc[i][j] = floatx4{0.f, 0.f, 0.f, 0.f};
+
+  for (int k0 = 0; k0 < K; k0 += P::KC) {
+    // stage A (TM x KC) and B (KC x TN); zero-fill outside the matrix
+    for (int i = tid; i < TM * P::KC; i += P::NT) {
+      const int r = i / P::KC, kk = i % P::KC;
+      const int gm = m0 + r, gk = k0 + kk;
+      As[r * P::AP + kk] = (gm < M && gk < K) ? ld_el(X, size_t(gm) * K + gk) : 0.0f;
+    }
+    for (int i = tid; i < P::KC * TN; i += P::NT) {
+      const int kk = i / TN, c = i % TN;
+      const int gk = k0 + kk, gn = n0 + c;
+      Bs[kk * P::BP + c] = (gk < K && gn < N) ? Wt[size_t(gk) * N + gn] : 0.0f;
+    }
+    __syncthreads();
+#pragma unroll
+    for (int kk = 0; kk < P::KC; kk += 4) {
+      float a[P::MT], b[P::NTL];
+#pragma unroll
+      for (int i = 0; i < P::MT; ++i)
+        a[i] = As[((wm * P::MT + i) * 16 + (lane & 15)) * P::AP + kk + (lane >> 4)];
+#pragma unroll
+      for (int j = 0; j < P::NTL; ++j) b[j] = Bs[(kk + (lane >> 4)) * P::BP + (wn * P::NTL + j) * 16 + (lane & 15)];
+#pragma unroll
+      for (int i = 0; i < P::MT; ++i)
+#pragma unroll
+        for (int j = 0; j < P::NTL; ++j) acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x4f32(a[i], b[j], acc[i][j], 0, 0, 0);
+    }
+    __syncthreads();
+  }
+
+  // epilogue: lane holds rows 4 (lane / 16) + r of column lane % 16 of each
+  // tile; with HW % 4 == 0 those 4 rows are 4 consecutive pixels of one plane.
+  static_assert(WMW == 1, "proj_in keeps a whole row tile per wave (channel sums stay in-wave)");
+  const bool vec = (HW % 4) == 0;
+#pragma unroll
+  for (int j = 0; j < P::NTL; ++j) {
+    const int gn = n0 + (wn * P::NTL + j) * 16 + (lane & 15);
+    const bool nok = gn < N;
+    const float bv = nok ? bias[gn] : 0.0f;
+    const bool lo = gn < NH;
+    const int c = lo ? gn : gn - NH;
+    TO* dst = lo ? out_lo : out_hi;
+    const int act = lo ? act_lo : act_hi;
+    float csum = 0.0f;
+#pragma unroll
+    for (int i = 0; i < P::MT; ++i) {
+      const int gm0 = m0 + (wm * P::MT + i) * 16 + (lane >> 4) * 4;
+      float v[4];
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        v[r] = acc[i][j][r] + bv;
+        if (act == 1) v[r] = silu_acc(v[r]);
+      }
+      if (nok && vec && gm0 + 3 < M) {
+        const int f = gm0 / HW, p = gm0 % HW;
+        st4(dst, (size_t(f) * NH + c) * HW + p, v);
+        csum += (v[0] + v[1]) + (v[2] + v[3]);
+      } else if (nok) {
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+          const int gm = gm0 + r;
+          if (gm < M) {
+            const int f = gm / HW, p = gm % HW;
+            st_el(dst, (size_t(f) * NH + c) * HW + p, v[r]);
+            csum += v[r];
+          }
+        }
+      }
+    }
+    if (partial != nullptr && lo) {
+      // the wave holds all TM rows of the tile: reduce the 4 row groups
+      csum += __shfl_xor(csum, 16, 64);
+      csum += __shfl_xor(csum, 32, 64);
+      if (lane < 16 && nok) partial[size_t(blockIdx.x) * NH + c] = csum;
+    }
+  }
+}
+
+// ---------------------------------------------------------------------------
+// proj_out: out[f*HW + p][n] = sum_k Y[f][k][p] W[k][n] + b[n]
+// ---------------------------------------------------------------------------
+template <int TM, int TN, int WMW, int WNW, class TI, class TO>
+__global__ void __launch_bounds__(64 * WMW * WNW)
+proj_out_kernel(const TI* __restrict__ Y, int M, int K, int N, const float* __restrict__ Wt,
+                const float* __restrict__ bias, int HW, TO* __restrict__ out) {
+  using P = ProjTile<TM, TN, WMW, WNW>;
+  __shared__ float As[TM * P::AP];
+  __shared__ float Bs[P::KC * P::BP];
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int wm = wave / WNW, wn = wave % WNW;
+  const int m0 = blockIdx.x * TM, n0 = blockIdx.y * TN;
+
+  floatx4 acc[P::MT][P::NTL];
+#pragma unroll
+  for (int i = 0; i < P::MT; ++i)
+#pragma unroll
+    for (int j = 0; j < P::NTL; ++j) acc[i][j] = floatx4{0.f, 0.f, 0.f, 0.f};
+
+  for (int k0 = 0; k0 < K; k0 += P::KC) {
+    // A tile from plane-major Y: consecutive threads walk the pixels of one channel
+    for (int i = tid; i < TM * P::KC; i += P::NT) {
+      const int kk = i / TM, r = i % TM;
+      const int gm = m0 + r, gk = k0 + kk;
+      float v = 0.0f;
+      if (gm < M && gk < K) {
+        const int f = gm / HW, p = gm % HW;
+        v = ld_el(Y, (size_t(f) * K + gk) * HW + p);
+      }
+      As[r * P::AP + kk] = v;
+    }
+    for (int i = tid; i < P::KC * TN; i += P::NT) {
+      const int kk = i / TN, c = i % TN;
+      const int gk = k0 + kk, gn = n0 + c;
+      Bs[kk * P::BP + c] = (gk < K && gn < N) ? Wt[size_t(gk) * N + gn] : 0.0f;
+    }
+    __syncthreads();
+#pragma unroll
+    for (int kk = 0; kk < P::KC; kk += 4) {
+      float a[P::MT], b[P::NTL];
+#pragma unroll
+      for (int i = 0; i < P::MT; ++i)
+        a[i] = As[((wm * P::MT + i) * 16 + (lane & 15)) * P::AP + kk + (lane >> 4)];
+#pragma unroll
+      for (int j = 0; j < P::NTL; ++j) b[j] = Bs[(kk + (lane >> 4)) * P::BP + (wn * P::NTL + j) * 16 + (lane & 15)];
+#pragma unroll
+      for (int i = 0; i < P::MT; ++i)
+#pragma unroll
+        for (int j = 0; j < P::NTL; ++j) acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x4f32(a[i], b[j], acc[i][j], 0, 0, 0);
+    }
+    __syncthreads();
+  }
+#pragma unroll
+  for (int j = 0; j < P::NTL; ++j) {
+    const int gn = n0 + (wn * P::NTL + j) * 16 + (lane & 15);
+    if (gn >= N) continue;
+    const float bv = bias[gn];
+#pragma unroll
+    for (int i = 0; i < P::MT; ++i)
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        const int gm = m0 + (wm * P::MT + i) * 16 + (lane >> 4) * 4 + r;
+        if (gm < M) st_el(out, size_t(gm) * N + gn, acc[i][j][r] + bv);
+      }
+  }
+}
+
+// ctx[f][c] = sum_t partial[f * tiles_per_frame + t][c] / HW
+__global__ void ctx_reduce_kernel(const float* __restrict__ partial, int F, int tiles_per_frame, int C, float inv_hw,
+                                  float* __restrict__ ctx) {
+  const int i = blockIdx.x * blockDim.x + threadIdx.x;
+  if (i >= F * C) return;
+  const int f = i / C, c = i % C;
+  float s = 0.0f;
+  for (int t = 0; t < tiles_per_frame; ++t) s += partial[(size_t(f) * tiles_per_frame + t) * C + c];
+  ctx[i] = s * inv_hw;
+}
+
+// ----------------------------------------------------------------- launchers
+
+constexpr int kProjTM = 64;
+
+int proj_in_tile_rows() { return kProjTM; }
+
+template <class TI, class TO>
+static void launch_in(const void* X, int M, int K, int N, const float* W, const float* b, int HW, void* lo, void* hi,
+                      int act_lo, int act_hi, float* partial, hipStream_t s) {
+  const dim3 grid((M + kProjTM - 1) / kProjTM, (N + 127) / 128);
+  hipLaunchKernelGGL((proj_in_kernel<kProjTM, 128, 1, 4, TI, TO>), grid, dim3(256), 0, s, static_cast<const TI*>(X), M,
+                     K, N, W, b, HW, static_cast<TO*>(lo), static_cast<TO*>(hi), act_lo, act_hi, partial);
+}
+
+hipError_t launch_proj_in(const void* X, int in_dtype, int M, int K, int N, const float* W, const float* b, int HW,
+                          void* out_lo, void* out_hi, int out_dtype, int act_lo, int act_hi, float* partial,
+                          hipStream_t s) {
+  if (in_dtype == 0 && out_dtype == 0) launch_in<float, float>(X, M, K, N, W, b, HW, out_lo, out_hi, act_lo, act_hi, partial, s);
+  else if (in_dtype == 0) launch_in<float, uint16_t>(X, M, K, N, W, b, HW, out_lo, out_hi, act_lo, act_hi, partial, s);
+  else if (out_dtype == 0) launch_in<uint16_t, float>(X, M, K, N, W, b, HW, out_lo, out_hi, act_lo, act_hi, partial, s);
+  else launch_in<uint16_t, uint16_t>(X, M, K, N, W, b, HW, out_lo, out_hi, act_lo, act_hi, partial, s);
+  return hipGetLastError();
+}
+
+template <class TI, class TO>
+static void launch_out(const void* Y, int M, int K, int N, const float* W, const float* b, int HW, void* out,
+                       hipStream_t s) {
+  if (N <= 64) {
+    const dim3 grid((M + kProjTM - 1) / kProjTM, (N + 63) / 64);
+    hipLaunchKernelGGL((proj_out_kernel<kProjTM, 64, 2, 2, TI, TO>), grid, dim3(256), 0, s, static_cast<const TI*>(Y), M,
+                       K, N, W, b, HW, static_cast<TO*>(out));
+  } else {
+    const dim3 grid((M + kProjTM - 1) / kProjTM, (N + 127) / 128);
+    hipLaunchKernelGGL((proj_out_kernel<kProjTM, 128, 1, 4, TI, TO>), grid, dim3(256), 0, s, static_cast<const TI*>(Y),
+                       M, K, N, W, b, HW, static_cast<TO*>(out));
+  }
+}
+
+hipError_t launch_proj_out(const void* Y, int in_dtype, int M, int K, int N, const float* W, const float* b, int HW,
+                           void* out, int out_dtype, hipStream_t s) {
+  if (in_dtype == 0 && out_dtype == 0) launch_out<float, float>(Y, M, K, N, W, b, HW, out, s);
+  else if (in_dtype == 0) launch_out<float, uint16_t>(Y, M, K, N, W, b, HW, out, s);
+  else if (out_dtype == 0) launch_out<uint16_t, float>(Y, M, K, N, W, b, HW, out, s);
+  else launch_out<uint16_t, uint16_t>(Y, M, K, N, W, b, HW, out, s);
+  return hipGetLastError();
+}
+
+hipError_t launch_ctx_reduce(const float* partial, int F, int tiles_per_frame, int C, float inv_hw, float* ctx,
+                             hipStream_t s) {
+  const int n = F * C;
+  hipLaunchKernelGGL(ctx_reduce_kernel, dim3((n + 255) / 256), dim3(256), 0, s, partial, F, tiles_per_frame, C, inv_hw,
+                     ctx);
+  return hipGetLastError();
+}
+
+}  // namespace cssm

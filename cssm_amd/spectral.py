@@ -127,3 +127,83 @@ def gated_scan_supported(H: int, W: int) -> bool:
 
 def gated_scan_min_group(H: int, W: int) -> int:
     return int(_lib.load().cssm_gated_scan_min_group(H, W))
+
+
+def proj_in(x: torch.Tensor, kernel: torch.Tensor, bias: torch.Tensor, frames: int, hw: int,
+            silu_lo: bool = False, silu_hi: bool = False, want_ctx: bool = False,
+            out_dtype: Optional[torch.dtype] = None):
+    """Dense(N) on channels-last rows with the plane-major split (cssm.py:480-484).
+
+    x: (..., K) with frames * hw rows.  Returns (lo, hi, ctx): lo, hi are
+    (frames, N/2, hw) plane-major; ctx (frames, N/2) = spatial mean of lo, or None.
+    """
+    _dev(x, "x")
+    if x.dtype not in _DTYPES:
+        raise ValueError(f"unsupported dtype {x.dtype}")
+    K = x.shape[-1]
+    if x.numel() != frames * hw * K:
+        raise ValueError("x does not hold frames * hw rows")
+    _dev(kernel, "kernel", torch.float32)
+    _dev(bias, "bias", torch.float32)
+    Kk, N = kernel.shape
+    if Kk != K or bias.shape != (N,) or N % 2:
+        raise ValueError(f"kernel {tuple(kernel.shape)} / bias {tuple(bias.shape)} do not match K={K}")
+    od = out_dtype or x.dtype
+    lo = torch.empty((frames, N // 2, hw), dtype=od, device=x.device)
+    hi = torch.empty_like(lo)
+    ctx = ws = None
+    nbytes = 0
+    if want_ctx:
+        ctx = torch.empty((frames, N // 2), dtype=torch.float32, device=x.device)
+        nbytes = int(_lib.load().cssm_proj_in_workspace_size(frames, hw, N))
+        if nbytes:
+            ws = torch.empty(nbytes // 4, dtype=torch.float32, device=x.device)
+    _lib.call("cssm_proj_in", x.data_ptr(), _DTYPES[x.dtype], frames, hw, K, N, kernel.data_ptr(),
+              bias.data_ptr(), lo.data_ptr(), hi.data_ptr(), _DTYPES[od], int(silu_lo), int(silu_hi),
+              ctx.data_ptr() if ctx is not None else None, ws.data_ptr() if ws is not None else None,
+              nbytes, _stream())
+    return lo, hi, ctx
+
+
+def proj_out(y: torch.Tensor, kernel: torch.Tensor, bias: torch.Tensor,
+             out_dtype: Optional[torch.dtype] = None) -> torch.Tensor:
+    """Dense(N) from plane-major (frames, K, hw) to channels-last (frames * hw, N) (cssm.py:584)."""
+    _dev(y, "y")
+    if y.dtype not in _DTYPES:
+        raise ValueError(f"unsupported dtype {y.dtype}")
+    F, K, hw = y.shape
+    _dev(kernel, "kernel", torch.float32)
+    _dev(bias, "bias", torch.float32)
+    if kernel.shape[0] != K or bias.shape != (kernel.shape[1],):
+        raise ValueError(f"kernel {tuple(kernel.shape)} does not match K={K}")
+    N = kernel.shape[1]
+    od = out_dtype or y.dtype
+    out = torch.empty((F * hw, N), dtype=od, device=y.device)
+    _lib.call("cssm_proj_out", y.data_ptr(), _DTYPES[y.dtype], F, hw, K, N, kernel.data_ptr(), bias.data_ptr(),
+              out.data_ptr(), _DTYPES[od], _stream())
+    return out
+
+
+def short_conv(x: torch.Tensor, spatial: Optional[Dict[str, torch.Tensor]],
+               temporal: Optional[Dict[str, torch.Tensor]], want_ctx: bool = True,
+               out_dtype: Optional[torch.dtype] = None):
+    """SiLU(causal temporal conv(depthwise spatial conv(x))) on plane-major (B, T, C, H, W)
+    x, plus its spatial mean (cssm.py:487-502, 536).  Returns (u, ctx)."""
+    _dev(x, "x")
+    B, T, C, H, W = x.shape
+    od = out_dtype or x.dtype
+    u = torch.empty((B, T, C, H, W), dtype=od, device=x.device)
+    ctx = torch.empty((B, T, C), dtype=torch.float32, device=x.device) if want_ctx else None
+    ks = kt = 0
+    ws = bs = wt = bt = None
+    if spatial is not None:
+        ks = spatial["kernel"].shape[0]
+        ws = _dev(spatial["kernel"], "short_conv_spatial.kernel", torch.float32).data_ptr()
+        bs = _dev(spatial["bias"], "short_conv_spatial.bias", torch.float32).data_ptr()
+    if temporal is not None:
+        kt = temporal["kernel"].shape[0]
+        wt = _dev(temporal["kernel"], "short_conv_temporal.kernel", torch.float32).data_ptr()
+        bt = _dev(temporal["bias"], "short_conv_temporal.bias", torch.float32).data_ptr()
+    _lib.call("cssm_short_conv", x.data_ptr(), _DTYPES[x.dtype], B, T, C, H, W, ks, ws, bs, kt, wt, bt,
+              u.data_ptr(), _DTYPES[od], ctx.data_ptr() if ctx is not None else None, _stream())
+    return u, ctx

@@ -144,6 +144,55 @@ int cssm_gated_scan_fwd(const void* u, const void* z, void* y, int dtype, int B,
                         int H, int W, const float* gates, const float* khat, int u_act,
                         int z_act, void* stream);
 
+/*
+ * Input projection with the layout change to plane-major fused in.
+ * Replaces cssm.py:480-484 (in_proj = Dense(2C) on channels-last x, split
+ * into x_main and z), with the SiLU of cssm.py:502 / :581 optionally applied
+ * to each half and the spatial mean ctx of the first half (cssm.py:536)
+ * optionally produced.  Also serves the GDN projections (cssm.py:4753-4758,
+ * 4853) with N = 3C or C.
+ *   x        (F * HW, K) channels-last of in_dtype (F = B * T frames)
+ *   kernel   (K, N) float32 [in_proj/kernel], bias (N) [in_proj/bias]
+ *   out_lo   (F, N/2, HW) plane-major of out_dtype: output channels [0, N/2)
+ *   out_hi   (F, N/2, HW): output channels [N/2, N) (N must be even)
+ *   act_lo, act_hi  cssm_load_act applied to each half
+ *   ctx      (F, N/2) float32 out = mean over HW of the stored out_lo, or NULL
+ *   workspace  device scratch of cssm_proj_in_workspace_size(F, HW, N) bytes
+ *              (used only when ctx is requested)
+ */
+int cssm_proj_in(const void* x, int in_dtype, int F, int HW, int K, int N, const float* kernel,
+                 const float* bias, void* out_lo, void* out_hi, int out_dtype, int act_lo, int act_hi,
+                 float* ctx, void* workspace, size_t workspace_bytes, void* stream);
+
+/* Bytes of device workspace cssm_proj_in needs to produce ctx. */
+size_t cssm_proj_in_workspace_size(int F, int HW, int N);
+
+/*
+ * Output projection from plane-major planes back to channels-last.
+ * Replaces cssm.py:584 (out_proj = Dense(C) on the channels-last transpose
+ * of the scan output, cssm.py:578).
+ *   y       (F, K, HW) plane-major of in_dtype
+ *   kernel  (K, N) float32, bias (N)
+ *   out     (F * HW, N) channels-last of out_dtype
+ */
+int cssm_proj_out(const void* y, int in_dtype, int F, int HW, int K, int N, const float* kernel,
+                  const float* bias, void* out, int out_dtype, void* stream);
+
+/*
+ * Factored short convolution + SiLU + spatial mean of GatedCSSM.
+ * Replaces cssm.py:487-502 and :536 for plane-major x_main:
+ *   s_t = DWConv_{ks x ks, SAME}(x_t) + b_s; o_t = sum_j w_t[j] s_{t-kt+1+j} + b_t;
+ *   u_t = SiLU(o_t); ctx_t = mean_{h,w} u_t.
+ *   x   (B, T, C, H, W) of in_dtype; u (B, T, C, H, W) of out_dtype; ctx (B, T, C) or NULL
+ *   ks = 0 skips the spatial stage (ws, bs unused): kernel (ks, ks, 1, C)
+ *        [short_conv_spatial/kernel], bias (C)
+ *   kt = 0 skips the temporal stage (wt, bt unused): kernel (kt, 1, C)
+ *        [short_conv_temporal/kernel], bias (C)
+ */
+int cssm_short_conv(const void* x, int in_dtype, int B, int T, int C, int H, int W, int ks,
+                    const float* ws, const float* bs, int kt, const float* wt, const float* bt,
+                    void* u, int out_dtype, float* ctx, void* stream);
+
 /* 1 if cssm_gated_scan_fwd has a kernel for (H, W), else 0. */
 int cssm_gated_scan_supported(int H, int W);
 
