@@ -146,9 +146,9 @@ int cssm_gated_scan_fwd(const void* u, const void* z, void* y, int dtype, int B,
   return hip_status(e, "cssm_gated_scan_fwd");
 }
 
-size_t cssm_proj_in_workspace_size(int F, int HW, int N) {
-  if (F <= 0 || HW <= 0 || N <= 0) return 0;
-  const int tm = cssm::proj_in_tile_rows();
+size_t cssm_proj_in_workspace_size(int F, int HW, int K, int N) {
+  if (F <= 0 || HW <= 0 || K <= 0 || N <= 0) return 0;
+  const int tm = cssm::proj_in_tile_rows(K);
   if (HW % tm != 0) return 0;
   return size_t(F) * (HW / tm) * (N / 2) * sizeof(float);
 }
@@ -169,11 +169,11 @@ int cssm_proj_in(const void* x, int in_dtype, int F, int HW, int K, int N, const
     return fail(CSSM_ERR_ALIGN, "cssm_proj_in: f32 outputs must be 16-byte aligned");
   const hipStream_t s = static_cast<hipStream_t>(stream);
   const int M = F * HW;
-  const int tm = cssm::proj_in_tile_rows();
+  const int tm = cssm::proj_in_tile_rows(K);
   const bool fused_ctx = ctx != nullptr && (HW % tm) == 0;
   float* partial = nullptr;
   if (fused_ctx) {
-    const size_t need = cssm_proj_in_workspace_size(F, HW, N);
+    const size_t need = cssm_proj_in_workspace_size(F, HW, K, N);
     if (!workspace || workspace_bytes < need)
       return fail(CSSM_ERR_ARG, "cssm_proj_in: ctx needs a %zu-byte workspace (got %zu)", need, workspace_bytes);
     partial = static_cast<float*>(workspace);

@@ -28,7 +28,8 @@ hipError_t launch_gated_scan(const void* u, const void* z, void* y, int dtype, i
                              hipStream_t s);
 
 // projection GEMMs (fp32 MFMA)
-int proj_in_tile_rows();
+// rows per proj_in tile (the channel partial sums come one per tile)
+int proj_in_tile_rows(int K);
 hipError_t launch_proj_in(const void* X, int in_dtype, int M, int K, int N, const float* W, const float* b, int HW,
                           void* out_lo, void* out_hi, int out_dtype, int act_lo, int act_hi, float* partial,
                           hipStream_t s);

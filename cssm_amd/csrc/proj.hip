@@ -30,6 +30,13 @@ __device__ __forceinline__ void st_el(uint16_t* p, size_t i, float v) {
   }
 }
 __device__ __forceinline__ float silu_acc(float x) { return x / (1.0f + expf(-x)); }
+// 4 consecutive elements at a 4-element-aligned index
+__device__ __forceinline__ float4 ld4(const float* p, size_t i) { return *reinterpret_cast<const float4*>(p + i); }
+__device__ __forceinline__ float4 ld4(const uint16_t* p, size_t i) {
+  const uint2 v = *reinterpret_cast<const uint2*>(p + i);
+  return make_float4(__uint_as_float(v.x << 16), __uint_as_float(v.x & 0xffff0000u), __uint_as_float(v.y << 16),
+                     __uint_as_float(v.y & 0xffff0000u));
+}
 __device__ __forceinline__ void st4(float* p, size_t i, const float* v) {
   *reinterpret_cast<float4*>(p + i) = make_float4(v[0], v[1], v[2], v[3]);
 }
@@ -231,11 +238,203 @@ __global__ void ctx_reduce_kernel(const float* __restrict__ partial, int F, int 
   ctx[i] = s * inv_hw;
 }
 
+// ---------------------------------------------------------------------------
+// Persistent small-K GEMM (K <= KMAX, the layer's projections): the weight
+// block (K x 128 columns) stays in LDS for the whole launch; each workgroup
+// walks 128-row tiles, prefetching the next tile's A rows into registers while
+// the MFMAs run on the current one.  Four waves split the 128 columns (32
+// each) and keep all 128 rows, so every per-channel reduction stays in-wave.
+//   PLANE_A = false: A is channels-last (M, K) rows; true: A is plane-major
+//   (F, K, HW) (the scan output).  OUT_SPLIT = true: plane-major split output
+//   with SiLU / channel sums (proj_in); false: channels-last (M, N) (proj_out).
+// ---------------------------------------------------------------------------
+template <int KMAX, bool PLANE_A, bool OUT_SPLIT, int WN, class TI, class TO>
+__global__ void __launch_bounds__(256, 2)
+proj_persist_kernel(const TI* __restrict__ A, int M, int K, int N, const float* __restrict__ Wt,
+                    const float* __restrict__ bias, int HW, TO* __restrict__ out_lo, TO* __restrict__ out_hi,
+                    int act_lo, int act_hi, float* __restrict__ partial) {
+  // WN waves along the TN = 32 WN columns, WM = 4 / WN along the TM = 128 rows;
+  // a wave owns (128 / WM) rows x 32 columns = MI x 2 MFMA tiles
+  constexpr int TM = 128, TN = 32 * WN, NT = 256, WM = 4 / WN, MI = TM / WM / 16;
+  static_assert(!OUT_SPLIT || WM == 1, "channel sums of proj_in need whole row tiles per wave");
+  constexpr int AP = PLANE_A ? (TM + 16) : (KMAX + 2);   // pitch: rows of A (row-major) or k-rows (plane)
+  constexpr int BP = TN + 16;
+  constexpr int A_FLOATS = PLANE_A ? KMAX * AP : TM * AP;
+  constexpr int OP = TN + 4;                              // output staging pitch (channels-last out)
+  constexpr int AS_FLOATS = (!OUT_SPLIT && TM * OP > A_FLOATS) ? TM * OP : A_FLOATS;  // staging reuses As
+  constexpr int PF = TM * KMAX / 4 / NT;                 // float4 of A prefetched per thread
+  __shared__ __attribute__((aligned(16))) float As[AS_FLOATS];
+  __shared__ float Bs[KMAX * BP];
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int wm = wave / WN, wn = wave % WN;
+  const int n0 = blockIdx.y * TN;
+  const int NH = N / 2;
+  const int tiles = (M + TM - 1) / TM;
+
+  for (int i = tid; i < KMAX * TN; i += NT) {
+    const int kk = i / TN, c = i % TN;
+    const int gn = n0 + c;
+    Bs[kk * BP + c] = (kk < K && gn < N) ? Wt[size_t(kk) * N + gn] : 0.0f;
+  }
+  // A prefetch: float4 f of the tile -> (row, k4) or (k, row4)
+  auto fetch = [&](int tile, float4* pf) {
+    const int m0 = tile * TM;
+#pragma unroll
+    for (int i = 0; i < PF; ++i) {
+      const int f = i * NT + tid;
+      float4 v = make_float4(0.f, 0.f, 0.f, 0.f);
+      if (!PLANE_A) {
+        const int r = f / (KMAX / 4), k4 = (f % (KMAX / 4)) * 4;
+        const int gm = m0 + r;
+        if (gm < M && k4 < K) v = ld4(A, size_t(gm) * K + k4);
+      } else {
+        const int kk = f / (TM / 4), r4 = (f % (TM / 4)) * 4;
+        const int gm = m0 + r4;
+        if (kk < K && gm < M) {
+          const int fr = gm / HW, p = gm % HW;
+          v = ld4(A, (size_t(fr) * K + kk) * HW + p);
+        }
+      }
+      pf[i] = v;
+    }
+  };
+  auto stash = [&](const float4* pf) {
+#pragma unroll
+    for (int i = 0; i < PF; ++i) {
+      const int f = i * NT + tid;
+      if (!PLANE_A) {
+        const int r = f / (KMAX / 4), k4 = (f % (KMAX / 4)) * 4;
+        *reinterpret_cast<float2*>(&As[r * AP + k4]) = make_float2(pf[i].x, pf[i].y);
+        *reinterpret_cast<float2*>(&As[r * AP + k4 + 2]) = make_float2(pf[i].z, pf[i].w);
+      } else {
+        const int kk = f / (TM / 4), r4 = (f % (TM / 4)) * 4;
+        *reinterpret_cast<float4*>(&As[kk * AP + r4]) = pf[i];
+      }
+    }
+  };
+
+  float4 pf[PF];
+  int tile = blockIdx.x;
+  if (tile < tiles) fetch(tile, pf);
+  for (; tile < tiles; tile += gridDim.x) {
+    __syncthreads();            // previous tile is done with As (and Bs is staged)
+    stash(pf);
+    __syncthreads();
+    const int next = tile + gridDim.x;
+    if (next < tiles) fetch(next, pf);
+
+    floatx4 acc[MI][2];
+#pragma unroll
+    for (int i = 0; i < MI; ++i) acc[i][0] = acc[i][1] = floatx4{0.f, 0.f, 0.f, 0.f};
+    const int kend = (K + 3) / 4 * 4;
+    for (int kk = 0; kk < kend; kk += 4) {
+      const int ka = kk + (lane >> 4);
+      float a[MI], b[2];
+#pragma unroll
+      for (int i = 0; i < MI; ++i) {
+        const int r = (wm * MI + i) * 16 + (lane & 15);
+        a[i] = PLANE_A ? As[ka * AP + r] : As[r * AP + ka];
+      }
+#pragma unroll
+      for (int j = 0; j < 2; ++j) b[j] = Bs[ka * BP + wn * 32 + j * 16 + (lane & 15)];
+#pragma unroll
+      for (int i = 0; i < MI; ++i)
+#pragma unroll
+        for (int j = 0; j < 2; ++j) acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x4f32(a[i], b[j], acc[i][j], 0, 0, 0);
+    }
+
+    // epilogue: lane holds rows 16 i + 4 (lane / 16) + r of column lane % 16 of n-tile j
+    const int m0 = tile * TM;
+    if (OUT_SPLIT) {
+      // 4 consecutive pixels of one channel per lane and MFMA tile: 16 B stores
+#pragma unroll
+      for (int j = 0; j < 2; ++j) {
+        const int gn = n0 + wn * 32 + j * 16 + (lane & 15);
+        const bool nok = gn < N;
+        const float bv = nok ? bias[gn] : 0.0f;
+        const bool lo = gn < NH;
+        const int c = lo ? gn : gn - NH;
+        TO* dst = lo ? out_lo : out_hi;
+        const int act = lo ? act_lo : act_hi;
+        float csum = 0.0f;
+#pragma unroll
+        for (int i = 0; i < MI; ++i) {
+          const int gm0 = m0 + (wm * MI + i) * 16 + (lane >> 4) * 4;
+          float v[4];
+#pragma unroll
+          for (int r = 0; r < 4; ++r) {
+            v[r] = acc[i][j][r] + bv;
+            if (act == 1) v[r] = v[r] * __builtin_amdgcn_rcpf(1.0f + __expf(-v[r]));
+          }
+          if (nok && gm0 + 3 < M && (HW % 4) == 0) {
+            const int fr = gm0 / HW, p = gm0 % HW;
+            st4(dst, (size_t(fr) * NH + c) * HW + p, v);
+            csum += (v[0] + v[1]) + (v[2] + v[3]);
+          } else if (nok) {
+#pragma unroll
+            for (int r = 0; r < 4; ++r) {
+              const int gm = gm0 + r;
+              if (gm < M) {
+                const int fr = gm / HW, p = gm % HW;
+                st_el(dst, (size_t(fr) * NH + c) * HW + p, v[r]);
+                csum += v[r];
+              }
+            }
+          }
+        }
+        if (partial != nullptr && lo) {
+          csum += __shfl_xor(csum, 16, 64);
+          csum += __shfl_xor(csum, 32, 64);
+          if (lane < 16 && nok) partial[size_t(tile) * NH + c] = csum;
+        }
+      }
+    } else {
+      // stage the tile in LDS (over the A tile) and store whole rows: 16 B per lane
+      __syncthreads();
+#pragma unroll
+      for (int j = 0; j < 2; ++j) {
+        const int cl = wn * 32 + j * 16 + (lane & 15);
+        const int gn = n0 + cl;
+        const float bv = gn < N ? bias[gn] : 0.0f;
+#pragma unroll
+        for (int i = 0; i < MI; ++i)
+#pragma unroll
+          for (int r = 0; r < 4; ++r) As[((wm * MI + i) * 16 + (lane >> 4) * 4 + r) * OP + cl] = acc[i][j][r] + bv;
+      }
+      __syncthreads();
+      constexpr int C4 = TN / 4;
+      for (int f = tid; f < TM * C4; f += NT) {
+        const int r = f / C4, c4 = (f % C4) * 4;
+        const int gm = m0 + r, gn = n0 + c4;
+        if (gm >= M) continue;
+        const float* src = &As[r * OP + c4];
+        if (gn + 3 < N && (N % 4) == 0) {
+          float v[4] = {src[0], src[1], src[2], src[3]};
+          st4(out_lo, size_t(gm) * N + gn, v);
+        } else {
+          for (int e = 0; e < 4; ++e)
+            if (gn + e < N) st_el(out_lo, size_t(gm) * N + gn + e, src[e]);
+        }
+      }
+    }
+  }
+}
+
 // ----------------------------------------------------------------- launchers
 
-constexpr int kProjTM = 64;
+constexpr int kProjTM = 64;      // row tile of the general kernels
+constexpr int kPersistTM = 128;  // row tile of the persistent small-K kernels
 
-int proj_in_tile_rows() { return kProjTM; }
+static int persistent_grid(int tiles) {
+  int dev = 0, cus = 256;
+  if (hipGetDevice(&dev) == hipSuccess) {
+    hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev);
+  }
+  const int g = 2 * cus;   // two workgroups per CU
+  return tiles < g ? tiles : g;
+}
+
+int proj_in_tile_rows(int K) { return K <= 128 ? kPersistTM : kProjTM; }
 
 template <class TI, class TO>
 static void launch_in(const void* X, int M, int K, int N, const float* W, const float* b, int HW, void* lo, void* hi,
@@ -245,9 +444,49 @@ static void launch_in(const void* X, int M, int K, int N, const float* W, const 
                      K, N, W, b, HW, static_cast<TO*>(lo), static_cast<TO*>(hi), act_lo, act_hi, partial);
 }
 
+template <int KMAX, bool PLANE_A, bool OUT_SPLIT, class TI, class TO>
+static void launch_persist(const void* A, int M, int K, int N, const float* W, const float* b, int HW, void* lo,
+                           void* hi, int act_lo, int act_hi, float* partial, hipStream_t s) {
+  const int tiles = (M + kPersistTM - 1) / kPersistTM;
+  // narrow outputs (N <= 64) split the rows between wave pairs instead of idling half the waves
+  if constexpr (!OUT_SPLIT) {
+    if (N <= 64) {
+      const dim3 grid(unsigned(persistent_grid(tiles)), unsigned((N + 63) / 64));
+      hipLaunchKernelGGL((proj_persist_kernel<KMAX, PLANE_A, OUT_SPLIT, 2, TI, TO>), grid, dim3(256), 0, s,
+                         static_cast<const TI*>(A), M, K, N, W, b, HW, static_cast<TO*>(lo), static_cast<TO*>(hi),
+                         act_lo, act_hi, partial);
+      return;
+    }
+  }
+  const dim3 grid(unsigned(persistent_grid(tiles)), unsigned((N + 127) / 128));
+  hipLaunchKernelGGL((proj_persist_kernel<KMAX, PLANE_A, OUT_SPLIT, 4, TI, TO>), grid, dim3(256), 0, s,
+                     static_cast<const TI*>(A), M, K, N, W, b, HW, static_cast<TO*>(lo), static_cast<TO*>(hi),
+                     act_lo, act_hi, partial);
+}
+
+template <bool PLANE_A, bool OUT_SPLIT, class TI, class TO>
+static bool try_persist(const void* A, int M, int K, int N, const float* W, const float* b, int HW, void* lo,
+                        void* hi, int act_lo, int act_hi, float* partial, hipStream_t s) {
+  if (K % 4 != 0 || K > 128) return false;
+  if (K <= 64) launch_persist<64, PLANE_A, OUT_SPLIT, TI, TO>(A, M, K, N, W, b, HW, lo, hi, act_lo, act_hi, partial, s);
+  else launch_persist<128, PLANE_A, OUT_SPLIT, TI, TO>(A, M, K, N, W, b, HW, lo, hi, act_lo, act_hi, partial, s);
+  return true;
+}
+
 hipError_t launch_proj_in(const void* X, int in_dtype, int M, int K, int N, const float* W, const float* b, int HW,
                           void* out_lo, void* out_hi, int out_dtype, int act_lo, int act_hi, float* partial,
                           hipStream_t s) {
+  if (K <= 128 && K % 4 == 0) {
+    if (in_dtype == 0 && out_dtype == 0)
+      try_persist<false, true, float, float>(X, M, K, N, W, b, HW, out_lo, out_hi, act_lo, act_hi, partial, s);
+    else if (in_dtype == 0)
+      try_persist<false, true, float, uint16_t>(X, M, K, N, W, b, HW, out_lo, out_hi, act_lo, act_hi, partial, s);
+    else if (out_dtype == 0)
+      try_persist<false, true, uint16_t, float>(X, M, K, N, W, b, HW, out_lo, out_hi, act_lo, act_hi, partial, s);
+    else
+      try_persist<false, true, uint16_t, uint16_t>(X, M, K, N, W, b, HW, out_lo, out_hi, act_lo, act_hi, partial, s);
+    return hipGetLastError();
+  }
   if (in_dtype == 0 && out_dtype == 0) launch_in<float, float>(X, M, K, N, W, b, HW, out_lo, out_hi, act_lo, act_hi, partial, s);
   else if (in_dtype == 0) launch_in<float, uint16_t>(X, M, K, N, W, b, HW, out_lo, out_hi, act_lo, act_hi, partial, s);
   else if (out_dtype == 0) launch_in<uint16_t, float>(X, M, K, N, W, b, HW, out_lo, out_hi, act_lo, act_hi, partial, s);
@@ -271,6 +510,17 @@ static void launch_out(const void* Y, int M, int K, int N, const float* W, const
 
 hipError_t launch_proj_out(const void* Y, int in_dtype, int M, int K, int N, const float* W, const float* b, int HW,
                            void* out, int out_dtype, hipStream_t s) {
+  if (K <= 128 && K % 4 == 0 && HW % 4 == 0) {
+    if (in_dtype == 0 && out_dtype == 0)
+      try_persist<true, false, float, float>(Y, M, K, N, W, b, HW, out, nullptr, 0, 0, nullptr, s);
+    else if (in_dtype == 0)
+      try_persist<true, false, float, uint16_t>(Y, M, K, N, W, b, HW, out, nullptr, 0, 0, nullptr, s);
+    else if (out_dtype == 0)
+      try_persist<true, false, uint16_t, float>(Y, M, K, N, W, b, HW, out, nullptr, 0, 0, nullptr, s);
+    else
+      try_persist<true, false, uint16_t, uint16_t>(Y, M, K, N, W, b, HW, out, nullptr, 0, 0, nullptr, s);
+    return hipGetLastError();
+  }
   if (in_dtype == 0 && out_dtype == 0) launch_out<float, float>(Y, M, K, N, W, b, HW, out, s);
   else if (in_dtype == 0) launch_out<float, uint16_t>(Y, M, K, N, W, b, HW, out, s);
   else if (out_dtype == 0) launch_out<uint16_t, float>(Y, M, K, N, W, b, HW, out, s);

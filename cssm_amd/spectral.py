@@ -155,7 +155,7 @@ def proj_in(x: torch.Tensor, kernel: torch.Tensor, bias: torch.Tensor, frames: i
     nbytes = 0
     if want_ctx:
         ctx = torch.empty((frames, N // 2), dtype=torch.float32, device=x.device)
-        nbytes = int(_lib.load().cssm_proj_in_workspace_size(frames, hw, N))
+        nbytes = int(_lib.load().cssm_proj_in_workspace_size(frames, hw, K, N))
         if nbytes:
             ws = torch.empty(nbytes // 4, dtype=torch.float32, device=x.device)
     _lib.call("cssm_proj_in", x.data_ptr(), _DTYPES[x.dtype], frames, hw, K, N, kernel.data_ptr(),

@@ -157,7 +157,7 @@ int cssm_gated_scan_fwd(const void* u, const void* z, void* y, int dtype, int B,
  *   out_hi   (F, N/2, HW): output channels [N/2, N) (N must be even)
  *   act_lo, act_hi  cssm_load_act applied to each half
  *   ctx      (F, N/2) float32 out = mean over HW of the stored out_lo, or NULL
- *   workspace  device scratch of cssm_proj_in_workspace_size(F, HW, N) bytes
+ *   workspace  device scratch of cssm_proj_in_workspace_size(F, HW, K, N) bytes
  *              (used only when ctx is requested)
  */
 int cssm_proj_in(const void* x, int in_dtype, int F, int HW, int K, int N, const float* kernel,
@@ -165,7 +165,7 @@ int cssm_proj_in(const void* x, int in_dtype, int F, int HW, int K, int N, const
                  float* ctx, void* workspace, size_t workspace_bytes, void* stream);
 
 /* Bytes of device workspace cssm_proj_in needs to produce ctx. */
-size_t cssm_proj_in_workspace_size(int F, int HW, int N);
+size_t cssm_proj_in_workspace_size(int F, int HW, int K, int N);
 
 /*
  * Output projection from plane-major planes back to channels-last.
