@@ -399,6 +399,8 @@ gated_scan_pow2(const ScanArgs a) {
     __syncthreads();
 
     // ------ C2: DFT-H2 over s -> spectrum; recurrence; inverse DFT-H2 (I1)
+    // one unit (kA, then kB) at a time keeps the live registers to one unit's
+    // spectrum, gates and spectral kernel on top of the state
 #pragma unroll
     for (int j = 0; j < G::JC2; ++j) {
       const unsigned jb = j * NT + tid;
@@ -406,48 +408,36 @@ gated_scan_pow2(const ScanArgs a) {
       int kA, kB;
       pair_units<H1>(int((jb / WH) % (H1 / 2)), kA, kB);
       const int col = G::p_col(v);
-      float2 sa[H2], sb[H2];
 #pragma unroll
-      for (int s = 0; s < H2; ++s) {
-        sa[s] = cplx(G::row_off(pl, s + H2 * kA) + col);
-        sb[s] = cplx(G::row_off(pl, s + H2 * kB) + col);
+      for (int a2 = 0; a2 < 2; ++a2) {
+        const int k = a2 ? kB : kA;
+        float2 sp[H2];
+#pragma unroll
+        for (int s = 0; s < H2; ++s) sp[s] = cplx(G::row_off(pl, s + H2 * k) + col);
+        Dft<H2, false>::run(sp);
+        if (v == 0) {
+          // packed DC/Nyquist column: hand to the edge pass
+#pragma unroll
+          for (int q = 0; q < H2; ++q) edge[pl * H + k + H1 * q] = sp[q];
+        } else {
+          // gates of (b, t) and the spectral kernel of this plane at bins (k + H1 q, v)
+          const unsigned gi = unsigned(k * WF + v), ki = unsigned(pl * H * WF) + gi;
+          float4 gq[H2];
+          float2 kq[H2];
+#pragma unroll
+          for (int q = 0; q < H2; ++q) {
+            gq[q] = gbuf.ld4((gi + q * H1 * WF) * 16u);
+            kq[q] = kbuf.ld2((ki + q * H1 * WF) * 8u);
+          }
+#pragma unroll
+          for (int q = 0; q < H2; ++q) sp[q] = scan_bin(h[j][a2][q], sp[q], gq[q], kq[q]);
+          Dft<H2, true>::run(sp);
+#pragma unroll
+          for (int s = 0; s < H2; ++s)
+            cplx(G::row_off(pl, s + H2 * k) + col) = s ? cmul(sp[s], twI1[k * G::TI1 + s]) : sp[0];
+        }
+        __builtin_amdgcn_sched_barrier(0);
       }
-      Dft<H2, false>::run(sa);
-      Dft<H2, false>::run(sb);
-      if (v == 0) {
-        // packed DC/Nyquist column: hand to the edge pass
-#pragma unroll
-        for (int q = 0; q < H2; ++q) {
-          edge[pl * H + kA + H1 * q] = sa[q];
-          edge[pl * H + kB + H1 * q] = sb[q];
-        }
-      } else {
-        // gates of (b, t) and the spectral kernel of this plane, bins (kA|kB + H1 q, v)
-        const unsigned ga = unsigned(kA * WF + v), gb = unsigned(kB * WF + v);
-        const unsigned ka = unsigned(pl * H * WF) + ga, kb = unsigned(pl * H * WF) + gb;
-        float4 gra[H2], grb[H2];
-        float2 kra[H2], krb[H2];
-#pragma unroll
-        for (int q = 0; q < H2; ++q) {
-          gra[q] = gbuf.ld4((ga + q * H1 * WF) * 16u);
-          grb[q] = gbuf.ld4((gb + q * H1 * WF) * 16u);
-          kra[q] = kbuf.ld2((ka + q * H1 * WF) * 8u);
-          krb[q] = kbuf.ld2((kb + q * H1 * WF) * 8u);
-        }
-#pragma unroll
-        for (int q = 0; q < H2; ++q) {
-          sa[q] = scan_bin(h[j][0][q], sa[q], gra[q], kra[q]);
-          sb[q] = scan_bin(h[j][1][q], sb[q], grb[q], krb[q]);
-        }
-        Dft<H2, true>::run(sa);
-        Dft<H2, true>::run(sb);
-#pragma unroll
-        for (int s = 0; s < H2; ++s) {
-          cplx(G::row_off(pl, s + H2 * kA) + col) = s ? cmul(sa[s], twI1[kA * G::TI1 + s]) : sa[0];
-          cplx(G::row_off(pl, s + H2 * kB) + col) = s ? cmul(sb[s], twI1[kB * G::TI1 + s]) : sb[0];
-        }
-      }
-      __builtin_amdgcn_sched_barrier(0);
     }
     __syncthreads();
 
