@@ -115,10 +115,13 @@ def main():
     B, T, H, W, C = args.batch, w["T"], w["H"], w["W"], w["C"]
     dev = "cuda"
     if args.copy_calibration > 0:
+        # a streaming kernel of known traffic (read n*4 B, write n*4 B): torch's neg, which
+        # nothing else in this run launches, so its dispatch is easy to find in the counters
         n = args.copy_calibration // 4
         src = torch.ones(n, dtype=torch.float32, device=dev)
         dst = torch.empty_like(src)
-        dst.copy_(src)
+        torch.cuda.synchronize()
+        torch.neg(src, out=dst)
         torch.cuda.synchronize()
         del src, dst
     torch.manual_seed(0)
