@@ -16,6 +16,9 @@ F32, BF16 = 0, 1
 GATE_DENSE, GATE_FACTORED = 0, 1
 ACT_SOFTPLUS, ACT_SIGMOID2, ACT_EXP = 0, 1, 2
 LOAD_IDENTITY, LOAD_SILU = 0, 1
+ACT_IDENTITY, ACT_SILU, ACT_SIGMOID = 0, 1, 2
+GDN_GATE_DENSE, GDN_GATE_FACTORED, GDN_GATE_CHANNEL, GDN_GATE_SCALAR = 0, 1, 2, 3
+NORM_NONE, NORM_RMS, NORM_LAYER = 0, 1, 2
 
 _c_float_p = ctypes.POINTER(ctypes.c_float)
 
@@ -31,6 +34,21 @@ class GateParams(ctypes.Structure):
         ("bias_w", ctypes.c_void_p * 3),
     ]
 
+
+class GdnGateParams(ctypes.Structure):
+    """cssm_gdn_gate_params (include/cssm_amd.h): 0 alpha, 1 beta, 2 B_k, 3 B_v."""
+    _fields_ = [
+        ("gate_type", ctypes.c_int),
+        ("kernel", ctypes.c_void_p * 4),
+        ("bias", ctypes.c_void_p * 4),
+        ("kernel_w", ctypes.c_void_p * 4),
+        ("bias_w", ctypes.c_void_p * 4),
+    ]
+
+
+_P = ctypes.c_void_p
+_I = ctypes.c_int
+_LL = ctypes.c_longlong
 
 # name -> (restype, argtypes); every symbol declared in include/cssm_amd.h
 SIGNATURES = {
@@ -61,6 +79,17 @@ SIGNATURES = {
                                        ctypes.c_int, ctypes.c_int, ctypes.c_int, ctypes.c_void_p, ctypes.c_void_p,
                                        ctypes.c_int, ctypes.c_void_p, ctypes.c_void_p, ctypes.c_void_p,
                                        ctypes.c_int, ctypes.c_void_p, ctypes.c_void_p]),
+    "cssm_proj_planes": (_I, [_P, _I, _I, _I, _I, _I, _P, _P, _P, _I, _I, _P]),
+    "cssm_frame_mean": (_I, [_P, _I, _I, _I, _I, _P, _P]),
+    "cssm_depthwise_conv": (_I, [_P, _I, _I, _I, _I, _I, _I, _P, _P, _P, _I, _P]),
+    "cssm_gdn_gates": (_I, [_P, _I, _I, _I, _I, _I, _I, ctypes.POINTER(GdnGateParams), _I, ctypes.c_float, _P,
+                            _P, _P, _P]),
+    "cssm_gdn_qkv_post": (_I, [_P, _I, _I, _I, _I, _I, _I, _I, _P, _P, _I, _P, _P]),
+    "cssm_rfft2": (_I, [_P, _I, _LL, _I, _I, _P, _P, _P]),
+    "cssm_irfft2": (_I, [_P, _LL, _I, _I, _P, _I, _P]),
+    "cssm_fft_min_group": (_I, [_I, _I]),
+    "cssm_gdn_scan_bins": (_I, [_P, _P, _P, _LL, _I, _I, _P, _I, _I, _I, _I, _I, _I, _P, _P]),
+    "cssm_gdn_proj_out": (_I, [_P, _P, _I, _I, _I, _I, _I, _I, _P, _P, _P, _P, _P, _I, _P]),
     "cssm_gated_scan_supported": (ctypes.c_int, [ctypes.c_int, ctypes.c_int]),
     "cssm_gated_scan_min_group": (ctypes.c_int, [ctypes.c_int, ctypes.c_int]),
 }

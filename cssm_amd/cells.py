@@ -173,3 +173,245 @@ class GatedCSSM:
         return out.view(B, T, H, W, self.channels)
 
     __call__ = apply
+
+
+class GatedDeltaNetCSSM:
+    """GatedDeltaNetCSSM (cssm.py:4264-5141), slow path: the `gdn` cell.
+
+    x -> [qkv_dw] -> qkv_proj -> causal short conv + SiLU -> input gates B_k, B_v
+    -> rfft2 -> spectral / key L2 norms -> delta-rule recurrence over T with the
+    d_k x d_k complex state per (head, bin) -> readout S q -> irfft2 -> RMSNorm
+    -> x SiLU(gate_proj(x)) -> output_proj.  Gates alpha / beta / B_k / B_v come
+    from the spatial mean of x plus the temporal context encoding.
+
+    Not part of this build (NotImplementedError): rope_mode other than 'none',
+    int_attention_mode, cross_freq_conv_size > 0, ssl_proj_dim > 0, the
+    static-image fast path, bf16 / fp8 split-precision scans (use_complex32/16),
+    and a non-separable qkv conv.  scan_mode and use_goom / use_log select
+    numerically equivalent evaluations of the same recurrence; the kernels apply
+    to_goom's floors on every M / Delta entry.
+    """
+
+    def __init__(self, channels: int, delta_key_dim: int = 2, kernel_size: int = 11, rope_mode: str = "none",
+                 rope_base: float = 10000.0, spectral_rho: float = 0.999, position_independent_gates: bool = False,
+                 block_size: int = 1, gate_type: str = "channel", use_goom: bool = True, use_log: bool = True,
+                 use_complex32: bool = False, use_complex16: bool = False, scan_mode: str = "associative",
+                 ssd_chunk_size: int = 8, learned_init: bool = False, short_conv_size: int = 4,
+                 output_norm: str = "rms", use_input_gates: bool = True, output_gate_act: str = "silu",
+                 use_spectral_l2_norm: bool = True, qkv_conv_size: int = 1, qkv_conv_separable: bool = True,
+                 cross_freq_conv_size: int = 0, no_spectral_clamp: bool = False, int_attention_mode: str = "none",
+                 attn_kernel_size: int = 7, int_attn_dim: int = 16, static_image_fast_path: bool = False,
+                 num_timesteps: int = 0, ssl_proj_dim: int = 0, gate_proj_bias_init: float = 0.0,
+                 dtype=None, param_dtype=None, name: Optional[str] = None):
+        unsupported = []
+        if rope_mode != "none":
+            unsupported.append(f"rope_mode={rope_mode!r}")
+        if int_attention_mode != "none":
+            unsupported.append(f"int_attention_mode={int_attention_mode!r}")
+        if cross_freq_conv_size > 0:
+            unsupported.append("cross_freq_conv_size > 0")
+        if ssl_proj_dim > 0:
+            unsupported.append("ssl_proj_dim > 0")
+        if static_image_fast_path:
+            unsupported.append("static_image_fast_path")
+        if (use_complex32 or use_complex16) and not use_log:
+            unsupported.append("split-precision scans (use_complex32/16)")
+        if qkv_conv_size > 1 and not qkv_conv_separable:
+            unsupported.append("non-separable qkv conv")
+        if gate_type not in ("dense", "factored", "channel", "scalar"):
+            unsupported.append(f"gate_type={gate_type!r}")
+        if output_norm not in ("rms", "layer", "none"):
+            unsupported.append(f"output_norm={output_norm!r}")
+        if unsupported:
+            raise NotImplementedError("GatedDeltaNetCSSM: not part of this build: " + ", ".join(unsupported))
+        if not 1 <= delta_key_dim <= 4 or channels % delta_key_dim:
+            raise ValueError(f"channels={channels} must be divisible by delta_key_dim={delta_key_dim} (1..4)")
+        self.channels = channels
+        self.delta_key_dim = delta_key_dim
+        self.kernel_size = kernel_size
+        self.rope_mode = rope_mode
+        self.rope_base = rope_base
+        self.spectral_rho = spectral_rho
+        self.position_independent_gates = position_independent_gates
+        self.block_size = block_size
+        self.gate_type = gate_type
+        self.use_goom = use_goom
+        self.use_log = use_log
+        self.use_complex32 = use_complex32
+        self.use_complex16 = use_complex16
+        self.scan_mode = scan_mode
+        self.ssd_chunk_size = ssd_chunk_size
+        self.learned_init = learned_init
+        self.short_conv_size = short_conv_size
+        self.output_norm = output_norm
+        self.use_input_gates = use_input_gates
+        self.output_gate_act = output_gate_act
+        self.use_spectral_l2_norm = use_spectral_l2_norm
+        self.qkv_conv_size = qkv_conv_size
+        self.qkv_conv_separable = qkv_conv_separable
+        self.cross_freq_conv_size = cross_freq_conv_size
+        self.no_spectral_clamp = no_spectral_clamp
+        self.int_attention_mode = int_attention_mode
+        self.attn_kernel_size = attn_kernel_size
+        self.int_attn_dim = int_attn_dim
+        self.static_image_fast_path = static_image_fast_path
+        self.num_timesteps = num_timesteps
+        self.ssl_proj_dim = ssl_proj_dim
+        self.gate_proj_bias_init = gate_proj_bias_init
+        self.dtype = dtype
+        self.param_dtype = param_dtype
+        self.name = name
+        self._cache: Dict[Any, Any] = {}
+
+    # ------------------------------------------------------------- parameters
+    def param_shapes(self, H: int, W: int) -> Dict[str, Any]:
+        """Flax parameter tree of the slow path (cssm.py:4717-5141)."""
+        C, dk = self.channels, self.delta_key_dim
+        nh, Wf = C // dk, W // 2 + 1
+        s: Dict[str, Any] = {"kernel": (nh, self.kernel_size, self.kernel_size)}
+        q = self.qkv_conv_size
+        if q > 1:
+            s["qkv_dw"] = {"kernel": (q, q, 1, C), "bias": (C,)}
+        s["qkv_proj"] = {"kernel": (C, 3 * C), "bias": (3 * C,)}
+        if self.short_conv_size > 0:
+            for n in ("q", "k", "v"):
+                s[f"short_conv_{n}"] = {"kernel": (self.short_conv_size, 1, C), "bias": (C,)}
+
+        def gate(name, spatial):
+            gt = self.gate_type
+            if gt == "channel":
+                s[name] = {"kernel": (1, 1, C, C), "bias": (C,)} if spatial else {"kernel": (C, nh), "bias": (nh,)}
+            elif gt == "factored":
+                s[f"{name}_h"] = {"kernel": (C, H), "bias": (H,)}
+                n = W if spatial else Wf
+                s[f"{name}_w"] = {"kernel": (C, n), "bias": (n,)}
+            elif gt == "scalar":
+                s[name] = {"kernel": (C, 1), "bias": (1,)}
+            else:
+                n = H * W if spatial else H * Wf
+                s[name] = {"kernel": (C, n), "bias": (n,)}
+        if self.use_input_gates:
+            gate("B_k", True)
+            gate("B_v", True)
+        s["gate_proj"] = {"kernel": (C, C), "bias": (C,)}
+        gate("alpha", False)
+        gate("beta", False)
+        if self.output_norm == "rms":
+            s["rms_scale"] = (C,)
+        elif self.output_norm == "layer":
+            s["output_layernorm"] = {"scale": (C,), "bias": (C,)}
+        s["output_proj"] = {"kernel": (C, C), "bias": (C,)}
+        return s
+
+    def init(self, seed: int, x_shape, device="cuda") -> Params:
+        """Fresh parameters for inputs (B, T, H, W, C): lecun-normal Dense/Conv kernels,
+        zero biases (gate_proj: gate_proj_bias_init), xavier-normal spectral kernel, unit scales."""
+        _, _, H, W, _ = x_shape
+        gen = torch.Generator(device=device).manual_seed(int(seed))
+        params: Dict[str, Any] = {}
+        for name, v in self.param_shapes(H, W).items():
+            if name == "kernel":
+                nh, K, _ = v
+                std = math.sqrt(2.0 / (K * nh + K * nh))   # xavier_normal over (K, K) fans of (n_h, K, K)
+                params[name] = torch.randn(v, generator=gen, device=device, dtype=torch.float32) * std
+                continue
+            if name == "rms_scale":
+                params[name] = torch.ones(v, dtype=torch.float32, device=device)
+                continue
+            sub = {}
+            for pn, shp in v.items():
+                if pn == "kernel":
+                    fan_in = shp[0] if len(shp) == 2 else int(np.prod(shp[:-1]))
+                    sub[pn] = _lecun_normal(shp, fan_in, gen, device)
+                elif pn == "scale":
+                    sub[pn] = torch.ones(shp, dtype=torch.float32, device=device)
+                else:
+                    fill = self.gate_proj_bias_init if name == "gate_proj" else 0.0
+                    sub[pn] = torch.full(shp, float(fill), dtype=torch.float32, device=device)
+            params[name] = sub
+        return {"params": params}
+
+    load_params = staticmethod(GatedCSSM.load_params)
+
+    # ---------------------------------------------------------------- forward
+    def spectral_kernel(self, p: Dict[str, Any], H: int, W: int) -> torch.Tensor:
+        """W_hat (n_h, H, Wf) (cssm.py:4711-4734); cached per kernel tensor version."""
+        k = p["kernel"]
+        key = ("what", k.data_ptr(), k._version, H, W, self.spectral_rho)
+        kh = self._cache.get(key)
+        if kh is None:
+            kh = S.spectral_kernel(k, H, W, self.spectral_rho, squash=not self.no_spectral_clamp, goom_floor=False)
+            self._cache = {k_: v for k_, v in self._cache.items() if k_[0] != "what"}
+            self._cache[key] = kh
+        return kh
+
+    def _channel_input_gate_weights(self, p):
+        """B_k | B_v 1x1-conv kernels concatenated to one (C, 2C) Dense (cached)."""
+        kk, kv = p["B_k"]["kernel"], p["B_v"]["kernel"]
+        key = ("bkv", kk.data_ptr(), kk._version, kv.data_ptr(), kv._version)
+        w = self._cache.get(key)
+        if w is None:
+            C = self.channels
+            w = (torch.cat([kk.reshape(C, C), kv.reshape(C, C)], dim=1).contiguous(),
+                 torch.cat([p["B_k"]["bias"], p["B_v"]["bias"]]).contiguous())
+            self._cache = {k_: v for k_, v in self._cache.items() if k_[0] != "bkv"}
+            self._cache[key] = w
+        return w
+
+    def apply(self, variables: Params, x: torch.Tensor, injected_qkv_spatial=None) -> torch.Tensor:
+        """y = GatedDeltaNetCSSM(x); x (B, T, H, W, C) float32 or bfloat16 on the GPU, y same dtype."""
+        p = variables["params"]
+        B, T, H, W, C = x.shape
+        if C != self.channels:
+            raise ValueError(f"input has {C} channels, the cell {self.channels}")
+        dk = self.delta_key_dim
+        F, HW = B * T, H * W
+        if not S.fft_supported(H, W):
+            raise NotImplementedError(f"no spectral transform kernel for {H}x{W} planes")
+        x = x.contiguous()
+        # intermediates stay float32 whatever the I/O dtype (the reference computes in fp32 params'
+        # precision); only x is read and the output written in the I/O dtype
+        f32 = torch.float32
+        what = self.spectral_kernel(p, H, W)
+        # gates from the spatial mean of the layer input (+ temporal encoding)
+        ctx = S.frame_mean(x)
+        temporal = "none" if self.position_independent_gates else "sinusoid"
+        ab, bkv = S.gdn_gates(ctx, p, H, W, dk, self.gate_type, self.use_input_gates, temporal, self.rope_base)
+        # q, k, v in plane-major blocks (B, T, 3C, H, W)
+        xq = (S.depthwise_conv(x, p["qkv_dw"]["kernel"], p["qkv_dw"]["bias"], out_dtype=f32)
+              if self.qkv_conv_size > 1 else x)
+        qkv = S.proj_planes(xq, p["qkv_proj"]["kernel"], p["qkv_proj"]["bias"], F, HW,
+                            out_dtype=f32).view(B, T, 3 * C, H, W)
+        del xq
+        gate_mode, gates = 0, None
+        if self.use_input_gates:
+            if self.gate_type == "channel":
+                wk, bk = self._channel_input_gate_weights(p)
+                gates, gate_mode = S.proj_planes(x, wk, bk, F, HW, act="sigmoid", out_dtype=torch.float32), 3
+            else:
+                gates, gate_mode = bkv, (2 if self.gate_type == "scalar" else 1)
+        convs = None
+        if self.short_conv_size > 0:
+            convs = [p["short_conv_q"], p["short_conv_k"], p["short_conv_v"]]
+        S.gdn_qkv_post(qkv, convs, gate_mode, gates)
+        del gates
+        gv = S.proj_planes(x, p["gate_proj"]["kernel"], p["gate_proj"]["bias"], F, HW,
+                           act="silu" if self.output_gate_act == "silu" else "sigmoid", out_dtype=f32)
+        # spectral core: rfft2 -> delta-rule recurrence -> irfft2
+        spec, norms = S.rfft2(qkv, want_norms=self.use_spectral_l2_norm)
+        del qkv
+        ohat = S.gdn_scan_bins(spec, norms, ab, self.gate_type, what, dk)
+        del spec
+        o = S.irfft2(ohat, W, out_dtype=f32)
+        del ohat
+        if self.output_norm == "rms":
+            ns, nb = p["rms_scale"], None
+        elif self.output_norm == "layer":
+            ns, nb = p["output_layernorm"]["scale"], p["output_layernorm"]["bias"]
+        else:
+            ns = nb = None
+        out = S.gdn_proj_out(o.view(F, C, HW), gv, self.output_norm, ns, nb, p["output_proj"]["kernel"],
+                             p["output_proj"]["bias"], out_dtype=x.dtype)
+        return out.view(B, T, H, W, C)
+
+    __call__ = apply

@@ -217,3 +217,160 @@ int cssm_short_conv(const void* x, int in_dtype, int B, int T, int C, int H, int
 }
 
 }  // extern "C"
+
+namespace {
+bool dtype_ok(int d) { return d == CSSM_F32 || d == CSSM_BF16; }
+}  // namespace
+
+extern "C" {
+
+int cssm_proj_planes(const void* x, int in_dtype, int F, int HW, int K, int N, const float* kernel, const float* bias,
+                     void* out, int out_dtype, int act, void* stream) {
+  if (!x || !kernel || !bias || !out) return fail(CSSM_ERR_NULL, "cssm_proj_planes: x, kernel, bias and out must be non-null");
+  if (F <= 0 || HW <= 0 || K <= 0 || N <= 0) return fail(CSSM_ERR_SHAPE, "cssm_proj_planes: F=%d HW=%d K=%d N=%d", F, HW, K, N);
+  if ((long long)F * HW > 0x7fffffffLL) return fail(CSSM_ERR_SHAPE, "cssm_proj_planes: F*HW exceeds 2^31");
+  if (!dtype_ok(in_dtype) || !dtype_ok(out_dtype)) return fail(CSSM_ERR_ARG, "cssm_proj_planes: dtypes %d/%d", in_dtype, out_dtype);
+  if (act < 0 || act > 2) return fail(CSSM_ERR_ARG, "cssm_proj_planes: act=%d", act);
+  if (out_dtype == CSSM_F32 && !aligned(out, 16)) return fail(CSSM_ERR_ALIGN, "cssm_proj_planes: f32 out must be 16-byte aligned");
+  return hip_status(cssm::launch_proj_planes(x, in_dtype, F * HW, K, N, kernel, bias, HW, out, out, out_dtype, act, act,
+                                             nullptr, N, static_cast<hipStream_t>(stream)),
+                    "cssm_proj_planes");
+}
+
+int cssm_frame_mean(const void* x, int dtype, int F, int HW, int C, float* out, void* stream) {
+  if (!x || !out) return fail(CSSM_ERR_NULL, "cssm_frame_mean: x and out must be non-null");
+  if (F <= 0 || HW <= 0 || C <= 0) return fail(CSSM_ERR_SHAPE, "cssm_frame_mean: F=%d HW=%d C=%d", F, HW, C);
+  if (!dtype_ok(dtype)) return fail(CSSM_ERR_ARG, "cssm_frame_mean: dtype=%d", dtype);
+  return hip_status(cssm::launch_frame_mean(x, dtype, F, HW, C, out, static_cast<hipStream_t>(stream)), "cssm_frame_mean");
+}
+
+int cssm_depthwise_conv(const void* x, int dtype, int F, int H, int W, int C, int ks, const float* kernel,
+                        const float* bias, void* out, int out_dtype, void* stream) {
+  if (!x || !kernel || !bias || !out) return fail(CSSM_ERR_NULL, "cssm_depthwise_conv: null argument");
+  if (F <= 0 || H <= 0 || W <= 0 || C <= 0 || ks <= 0 || ks > 31)
+    return fail(CSSM_ERR_SHAPE, "cssm_depthwise_conv: F=%d H=%d W=%d C=%d ks=%d", F, H, W, C, ks);
+  if (!dtype_ok(dtype) || !dtype_ok(out_dtype))
+    return fail(CSSM_ERR_ARG, "cssm_depthwise_conv: dtypes %d/%d", dtype, out_dtype);
+  if (x == out) return fail(CSSM_ERR_ARG, "cssm_depthwise_conv: out must not alias x");
+  return hip_status(cssm::launch_depthwise_conv(x, dtype, F, H, W, C, ks, kernel, bias, out, out_dtype,
+                                                static_cast<hipStream_t>(stream)),
+                    "cssm_depthwise_conv");
+}
+
+int cssm_gdn_gates(const float* ctx, int B, int T, int C, int H, int W, int dk, const cssm_gdn_gate_params* p,
+                   int temporal, float rope_base, const float* temporal_table, float* ab, float* bkv, void* stream) {
+  if (!ctx || !p || !ab) return fail(CSSM_ERR_NULL, "cssm_gdn_gates: ctx, params and ab must be non-null");
+  if (B <= 0 || T <= 0 || C <= 0 || H <= 0 || W <= 0 || dk <= 0 || C % dk)
+    return fail(CSSM_ERR_SHAPE, "cssm_gdn_gates: B=%d T=%d C=%d H=%d W=%d d_k=%d", B, T, C, H, W, dk);
+  if (p->gate_type < CSSM_GDN_GATE_DENSE || p->gate_type > CSSM_GDN_GATE_SCALAR)
+    return fail(CSSM_ERR_ARG, "cssm_gdn_gates: gate_type=%d", p->gate_type);
+  if (temporal < 0 || temporal > 2 || (temporal == 2 && !temporal_table))
+    return fail(CSSM_ERR_ARG, "cssm_gdn_gates: temporal=%d (table %p)", temporal, (const void*)temporal_table);
+  const bool fac = p->gate_type == CSSM_GDN_GATE_FACTORED;
+  const bool spatial = p->kernel[2] != nullptr;
+  if (spatial && p->gate_type == CSSM_GDN_GATE_CHANNEL)
+    return fail(CSSM_ERR_ARG, "cssm_gdn_gates: channel input gates are 1x1 convolutions (cssm_proj_planes)");
+  if (spatial && !bkv) return fail(CSSM_ERR_NULL, "cssm_gdn_gates: bkv must be non-null with input gates");
+  cssm::GdnGateWeights w;
+  w.kind = p->gate_type;
+  for (int g = 0; g < 4; ++g) {
+    const bool need = g < 2 || spatial;
+    if (need && (!p->kernel[g] || !p->bias[g] || (fac && (!p->kernel_w[g] || !p->bias_w[g]))))
+      return fail(CSSM_ERR_NULL, "cssm_gdn_gates: gate %d weights missing", g);
+    w.kd[g] = need ? p->kernel[g] : nullptr;
+    w.bd[g] = need ? p->bias[g] : nullptr;
+    w.kw[g] = need && fac ? p->kernel_w[g] : nullptr;
+    w.bw[g] = need && fac ? p->bias_w[g] : nullptr;
+  }
+  const hipError_t e = cssm::launch_gdn_gates(ctx, B, T, C, H, W, C / dk, w, temporal, rope_base, temporal_table,
+                                              reinterpret_cast<float2*>(ab), reinterpret_cast<float2*>(bkv),
+                                              static_cast<hipStream_t>(stream));
+  if (e == hipErrorInvalidValue)
+    return fail(CSSM_ERR_UNSUPPORTED, "cssm_gdn_gates: C=%d with %dx%d planes exceeds the staging buffer", C, H, W);
+  return hip_status(e, "cssm_gdn_gates");
+}
+
+int cssm_gdn_qkv_post(void* qkv, int dtype, int B, int T, int C, int H, int W, int kt, const float* const* conv_kernel,
+                      const float* const* conv_bias, int gate_mode, const void* gates, void* stream) {
+  if (!qkv) return fail(CSSM_ERR_NULL, "cssm_gdn_qkv_post: qkv must be non-null");
+  if (B <= 0 || T <= 0 || C <= 0 || H <= 0 || W <= 0 || kt < 0 || kt > 8)
+    return fail(CSSM_ERR_SHAPE, "cssm_gdn_qkv_post: B=%d T=%d C=%d H=%d W=%d kt=%d (kt <= 8)", B, T, C, H, W, kt);
+  if (!dtype_ok(dtype)) return fail(CSSM_ERR_ARG, "cssm_gdn_qkv_post: dtype=%d", dtype);
+  if (gate_mode < 0 || gate_mode > 3) return fail(CSSM_ERR_ARG, "cssm_gdn_qkv_post: gate_mode=%d", gate_mode);
+  if (gate_mode != 0 && !gates) return fail(CSSM_ERR_NULL, "cssm_gdn_qkv_post: gates must be non-null");
+  cssm::GdnShortConv sc{};
+  if (kt > 0) {
+    if (!conv_kernel || !conv_bias) return fail(CSSM_ERR_NULL, "cssm_gdn_qkv_post: short-conv weights missing");
+    for (int i = 0; i < 3; ++i) {
+      if (!conv_kernel[i] || !conv_bias[i]) return fail(CSSM_ERR_NULL, "cssm_gdn_qkv_post: short-conv %d missing", i);
+      sc.w[i] = conv_kernel[i];
+      sc.b[i] = conv_bias[i];
+    }
+  }
+  if (gate_mode == 1 && !aligned(gates, 8)) return fail(CSSM_ERR_ALIGN, "cssm_gdn_qkv_post: gates must be 8-byte aligned");
+  return hip_status(cssm::launch_gdn_qkv_post(qkv, dtype, B, T, C, H * W, kt, sc, gate_mode, gates,
+                                              static_cast<hipStream_t>(stream)),
+                    "cssm_gdn_qkv_post");
+}
+
+int cssm_fft_min_group(int H, int W) { return cssm::fft_planes_min_group(H, W); }
+
+int cssm_rfft2(const void* x, int dtype, long long P, int H, int W, float* spec, float* norms, void* stream) {
+  if (!x || !spec) return fail(CSSM_ERR_NULL, "cssm_rfft2: x and spec must be non-null");
+  if (P <= 0 || H <= 0 || W <= 0 || P > 0x7fffffffLL) return fail(CSSM_ERR_SHAPE, "cssm_rfft2: P=%lld H=%d W=%d", P, H, W);
+  if (!dtype_ok(dtype)) return fail(CSSM_ERR_ARG, "cssm_rfft2: dtype=%d", dtype);
+  if (!cssm::fft_planes_min_group(H, W)) return fail(CSSM_ERR_UNSUPPORTED, "cssm_rfft2: no kernel for %dx%d planes", H, W);
+  if (!aligned(x, dtype == CSSM_F32 ? 16 : 8) || !aligned(spec, 8))
+    return fail(CSSM_ERR_ALIGN, "cssm_rfft2: misaligned tensor pointer");
+  return hip_status(cssm::launch_rfft2(x, dtype, P, H, W, reinterpret_cast<float2*>(spec), norms,
+                                       static_cast<hipStream_t>(stream)),
+                    "cssm_rfft2");
+}
+
+int cssm_irfft2(const float* spec, long long P, int H, int W, void* y, int dtype, void* stream) {
+  if (!spec || !y) return fail(CSSM_ERR_NULL, "cssm_irfft2: spec and y must be non-null");
+  if (P <= 0 || H <= 0 || W <= 0 || P > 0x7fffffffLL) return fail(CSSM_ERR_SHAPE, "cssm_irfft2: P=%lld H=%d W=%d", P, H, W);
+  if (!dtype_ok(dtype)) return fail(CSSM_ERR_ARG, "cssm_irfft2: dtype=%d", dtype);
+  if (!cssm::fft_planes_min_group(H, W)) return fail(CSSM_ERR_UNSUPPORTED, "cssm_irfft2: no kernel for %dx%d planes", H, W);
+  if (!aligned(y, dtype == CSSM_F32 ? 16 : 8) || !aligned(spec, 8))
+    return fail(CSSM_ERR_ALIGN, "cssm_irfft2: misaligned tensor pointer");
+  return hip_status(cssm::launch_irfft2(reinterpret_cast<const float2*>(spec), P, H, W, y, dtype,
+                                        static_cast<hipStream_t>(stream)),
+                    "cssm_irfft2");
+}
+
+int cssm_gdn_scan_bins(const float* spec, const float* norms, const float* ab, long long ab_frame, int ab_head,
+                       int ab_bin, const float* what, int B, int T, int C, int H, int W, int dk, float* ohat,
+                       void* stream) {
+  if (!spec || !ab || !what || !ohat) return fail(CSSM_ERR_NULL, "cssm_gdn_scan_bins: spec, ab, what and ohat must be non-null");
+  if (B <= 0 || T <= 0 || C <= 0 || H <= 0 || W <= 0 || dk < 1 || dk > 4 || C % dk)
+    return fail(CSSM_ERR_SHAPE, "cssm_gdn_scan_bins: B=%d T=%d C=%d H=%d W=%d d_k=%d (1..4, divides C)", B, T, C, H, W, dk);
+  if (ab_frame < 0 || ab_head < 0 || ab_bin < 0) return fail(CSSM_ERR_ARG, "cssm_gdn_scan_bins: negative gate stride");
+  if (B > 65535 || C / dk > 65535) return fail(CSSM_ERR_SHAPE, "cssm_gdn_scan_bins: grid too large");
+  if (!aligned(spec, 8) || !aligned(ab, 8) || !aligned(what, 8) || !aligned(ohat, 8))
+    return fail(CSSM_ERR_ALIGN, "cssm_gdn_scan_bins: complex tensors must be 8-byte aligned");
+  return hip_status(cssm::launch_gdn_scan_bins(reinterpret_cast<const float2*>(spec), norms,
+                                               reinterpret_cast<const float2*>(ab), ab_frame, ab_head, ab_bin,
+                                               reinterpret_cast<const float2*>(what), B, T, C, H, W, dk,
+                                               reinterpret_cast<float2*>(ohat), static_cast<hipStream_t>(stream)),
+                    "cssm_gdn_scan_bins");
+}
+
+int cssm_gdn_proj_out(const void* o, const void* gate, int in_dtype, int F, int HW, int K, int N, int norm,
+                      const float* norm_scale, const float* norm_bias, const float* kernel, const float* bias, void* out,
+                      int out_dtype, void* stream) {
+  if (!o || !gate || !kernel || !bias || !out) return fail(CSSM_ERR_NULL, "cssm_gdn_proj_out: null argument");
+  if (F <= 0 || HW <= 0 || K <= 0 || N <= 0) return fail(CSSM_ERR_SHAPE, "cssm_gdn_proj_out: F=%d HW=%d K=%d N=%d", F, HW, K, N);
+  if (K > 128 || K % 4 || HW % 4)
+    return fail(CSSM_ERR_UNSUPPORTED, "cssm_gdn_proj_out: needs K <= 128, K %% 4 == 0, HW %% 4 == 0 (K=%d HW=%d)", K, HW);
+  if ((long long)F * HW > 0x7fffffffLL) return fail(CSSM_ERR_SHAPE, "cssm_gdn_proj_out: F*HW exceeds 2^31");
+  if (!dtype_ok(in_dtype) || !dtype_ok(out_dtype)) return fail(CSSM_ERR_ARG, "cssm_gdn_proj_out: dtypes %d/%d", in_dtype, out_dtype);
+  if (norm < CSSM_NORM_NONE || norm > CSSM_NORM_LAYER) return fail(CSSM_ERR_ARG, "cssm_gdn_proj_out: norm=%d", norm);
+  const size_t va = in_dtype == CSSM_F32 ? 16 : 8;
+  if (!aligned(o, va) || !aligned(gate, va)) return fail(CSSM_ERR_ALIGN, "cssm_gdn_proj_out: misaligned o / gate");
+  return hip_status(cssm::launch_proj_out_norm_gate(o, gate, in_dtype, F * HW, K, N, norm, norm_scale, norm_bias, kernel,
+                                                    bias, HW, out, out_dtype, static_cast<hipStream_t>(stream)),
+                    "cssm_gdn_proj_out");
+}
+
+}  // extern "C"

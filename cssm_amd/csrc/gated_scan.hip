@@ -16,150 +16,16 @@
 //   y_t = irfft2(C_t * h_t, s=(H,W)) * z_gate_t           :576-581
 // floor(a) = 1e-7 + 0j where |a| < 1e-7 (goom.py:161-174).
 //
-// FFT organisation (H = H1*H2, W = W1*W2, all passes in-register radix-H1/H2/
-// W1/W2 with an LDS exchange between them; every pass writes its results back
-// into exactly the LDS slots it read, so one plane-sized buffer suffices and
-// a workgroup needs well under half of LDS):
-//   R1/R2  row transforms: rows r and r+H/2 are packed as one complex row,
-//          separated after the DFT; the real DC and Nyquist bins of each row
-//          are packed into one complex "column 0".
-//   C1/C2  column transforms over the W/2 packed columns; column 0 carries
-//          DC + i*Nyquist and is unpacked by the edge pass.
-//   the inverse mirrors these passes (I1..I4); column 0 is re-packed from
-//   the Hermitian parts of the DC and Nyquist columns, which is exactly the
-//   information irfft2's C2R step keeps.
+// The 2-D real FFT passes (and their LDS layout) are those of fft_plane.h.
 #include <hip/hip_runtime.h>
 #include <stdint.h>
 
 #include <initializer_list>
 
-#include "fft_reg.h"
+#include "fft_plane.h"
 #include "launch.h"
 
 namespace cssm {
-
-// ---------------------------------------------------------------- I/O types
-
-struct IoF32 {
-  using T = float;
-  using V4 = float4;
-  static __device__ __forceinline__ float4 to_f4(const float4 v) { return v; }
-  static __device__ __forceinline__ float4 from_f4(const float4 v) { return v; }
-};
-
-__device__ __forceinline__ float bf16_to_f32(uint32_t bits16) { return __uint_as_float(bits16 << 16); }
-__device__ __forceinline__ uint32_t f32_to_bf16(float f) {
-  uint32_t x = __float_as_uint(f);
-  if ((x & 0x7f800000u) == 0x7f800000u) {          // inf / nan: keep, force quiet nan
-    return (x >> 16) | ((x & 0x007fffffu) ? 0x40u : 0u);
-  }
-  x += 0x7fffu + ((x >> 16) & 1u);                   // round to nearest even
-  return x >> 16;
-}
-
-struct IoBF16 {
-  using T = uint16_t;
-  using V4 = uint2;   // 4 x bf16
-  static __device__ __forceinline__ float4 to_f4(const uint2 v) {
-    return make_float4(bf16_to_f32(v.x & 0xffffu), bf16_to_f32(v.x >> 16),
-                       bf16_to_f32(v.y & 0xffffu), bf16_to_f32(v.y >> 16));
-  }
-  static __device__ __forceinline__ uint2 from_f4(const float4 f) {
-    return make_uint2(f32_to_bf16(f.x) | (f32_to_bf16(f.y) << 16),
-                      f32_to_bf16(f.z) | (f32_to_bf16(f.w) << 16));
-  }
-};
-
-__device__ __forceinline__ float silu_f(float x) {
-  return x * __builtin_amdgcn_rcpf(1.0f + __expf(-x));
-}
-
-__device__ __forceinline__ float4 act4(float4 v, int act) {
-  if (act == 1) {
-    v.x = silu_f(v.x); v.y = silu_f(v.y); v.z = silu_f(v.z); v.w = silu_f(v.w);
-  }
-  return v;
-}
-
-// ------------------------------------------------------------------ geometry
-
-constexpr int fft_radix1(int n) { return n >= 128 ? 16 : (n >= 32 ? 8 : (n >= 8 ? 4 : 2)); }
-
-// LH, LW: log2 of the plane; NP planes per workgroup; PPT real samples per
-// thread per plane load (64 for large planes: a 128x128 plane is one 256-thread
-// workgroup, two of which share a CU so one's barriers and memory waits hide
-// behind the other's arithmetic).
-template <int LH, int LW, int NP, int PPT>
-struct Geom {
-  static constexpr int H = 1 << LH, W = 1 << LW;
-  static constexpr int HP = H / 2, WH = W / 2, WF = WH + 1;
-  static constexpr int W1 = fft_radix1(W), W2 = W / W1;
-  static constexpr int H1 = fft_radix1(H), H2 = H / H1;
-  static constexpr int NT = NP * H * W / PPT;
-  static constexpr int NR1 = NP * HP * W2, NR2 = NP * HP * (W1 / 2);
-  static constexpr int NC1 = NP * WH * H2, NC2 = NP * WH * (H1 / 2);
-  static constexpr int JR1 = NR1 / NT, JR2 = NR2 / NT, JC1 = NC1 / NT, JC2 = NC2 / NT;
-  static constexpr int NE = NP * HP;
-  static constexpr int JE = (NE + NT - 1) / NT;
-  static constexpr int NV4 = NP * H * W / 4;
-  static constexpr int JLD = NV4 / NT;
-
-  // LDS (floats): the plane buffer (row stride RS), the packed DC/Nyquist
-  // column of each plane and four twiddle tables laid out so one thread's
-  // entries are contiguous (rows padded by one entry against bank conflicts):
-  //   R1 [s][k] = w_W^{s k}, C1 [s][k] = w_H^{s k},
-  //   I1 [k][s] = conj w_H^{s k}, I3 [k][s] = conj w_W^{s k}.
-  static constexpr int RS = W + 4;
-  static constexpr int SZ_BUF = (NP * H * RS + 3) / 4 * 4;
-  static constexpr int SZ_EDGE = 2 * NP * H;
-  static constexpr int TR1 = W1 + 1, TC1 = H1, TI1 = H2, TI3 = W2 + 1;   // table row lengths
-  static constexpr int N_R1 = W2 * TR1, N_C1 = H2 * TC1, N_I1 = H1 * TI1, N_I3 = W1 * TI3;
-  static constexpr int SZ_TW = 2 * (N_R1 + N_C1 + N_I1 + N_I3);
-  static constexpr int OFF_EDGE = SZ_BUF, OFF_TW = OFF_EDGE + SZ_EDGE;
-  static constexpr int LDS_FLOATS = OFF_TW + SZ_TW;
-
-  static_assert(LDS_FLOATS * 4 <= 160 * 1024, "plane group does not fit gfx950 LDS");
-  static_assert(NT % 64 == 0 && NT <= 1024, "workgroup must be whole waves, <= 1024 threads");
-  static_assert(JR1 * NT == NR1 && JR2 * NT == NR2 && JC1 * NT == NC1 && JC2 * NT == NC2,
-                "every FFT pass must split evenly over the workgroup");
-  static_assert(JLD * NT == NV4, "plane group must split into whole 4-vectors per thread");
-  static_assert(W2 % 2 == 0 && H2 % 2 == 0 && W1 % 2 == 0 && H1 % 2 == 0, "radix split");
-
-  // Sample (pl, r, w) lives at row (pl, r), column w, except that in the
-  // upper half of each row's W2-float blocks (block index >= W1/2) the two
-  // halves of the block are swapped.  With RS = W + 4 the passes are free of
-  // LDS bank conflicts on 64 banks except the row-pair gather (2-way):
-  // R1/I4 (scalar, rows two apart within a wave), R2/I3 (whole blocks),
-  // C1/C2/I1/I2 (one packed-spectrum slot per lane along a row), load/store.
-  static constexpr int HALF = W2 >= 4 ? W2 / 2 : 0;
-  static __device__ __forceinline__ int row_off(int pl, int r) { return (pl * H + r) * RS; }
-  // block blk < W1/2 (lo: halves in place) or >= W1/2 (hi: halves swapped), position pos < W2
-  static __device__ __forceinline__ int lo_off(int pl, int r, int blk, int pos) {
-    return row_off(pl, r) + blk * W2 + pos;
-  }
-  static __device__ __forceinline__ int hi_off(int pl, int r, int blk, int pos) {
-    return row_off(pl, r) + blk * W2 + (pos ^ HALF);
-  }
-  // column of the packed-row spectrum P(pl, r, v), v < W/2: complex pair 2 (v / W1)
-  // of block v % W1 (the slots the row pass that produces it has just read)
-  static __device__ __forceinline__ int p_col(int v) {
-    const int blk = v % W1, pos = 2 * (v / W1);
-    return blk * W2 + (blk >= W1 / 2 ? (pos ^ HALF) : pos);
-  }
-  // 4-vector c4 of row r: contiguous unless the block is split by the swap
-  static constexpr bool V4_SPLIT = (HALF == 2);
-  // R1/I4 job jb -> (pl, p, s): s fastest; consecutive row groups of one wave
-  // are two rows apart so the row stride's bank shift (4) becomes 8
-  static constexpr int RG = 64 / W2;
-  static constexpr bool R1_STRIDE2 = (RG >= 2) && (HP % (2 * RG) == 0);
-  static __device__ __forceinline__ void r1_job(unsigned jb, int& pl, int& p, int& s) {
-    s = int(jb % W2);
-    const unsigned t1 = jb / W2;
-    pl = int(t1 / HP);
-    const unsigned tp = t1 % HP;
-    p = int(R1_STRIDE2 ? ((tp % RG) * 2 + (tp / RG) % 2 + 2 * RG * (tp / (2 * RG))) : tp);
-  }
-};
 
 // The forward row pass skips the 1/2 of the packed-row separation, so the
 // spectrum the recurrence sees is U' = 2U for every bin (the edge unpack keeps
@@ -181,28 +47,6 @@ __device__ __forceinline__ float2 scan_bin(float2& h, float2 U, float4 g, float2
   return make_float2(hn.x * gc, hn.y * gc);
 }
 
-// pair-unit decode: pair jj of radix N1 -> units (kA, kB) with kB = -kA mod N1
-// (jj = 0 groups the two self-paired units 0 and N1/2)
-template <int N1>
-__device__ __forceinline__ void pair_units(int jj, int& kA, int& kB) {
-  kA = jj;
-  kB = (jj == 0) ? (N1 / 2) : (N1 - jj);
-}
-
-// raw buffer access: 32-bit offsets from a uniform base (cheaper addressing
-// than 64-bit pointers, and out-of-range reads return 0)
-struct Buf {
-  __amdgpu_buffer_rsrc_t r;
-  __device__ __forceinline__ Buf(const void* p, unsigned bytes)
-      : r(__builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(p), 0, int(bytes), 0x00020000)) {}
-  __device__ __forceinline__ float4 ld4(unsigned off) const {
-    return __builtin_bit_cast(float4, __builtin_amdgcn_raw_buffer_load_b128(r, int(off), 0, 0));
-  }
-  __device__ __forceinline__ float2 ld2(unsigned off) const {
-    return __builtin_bit_cast(float2, __builtin_amdgcn_raw_buffer_load_b64(r, int(off), 0, 0));
-  }
-};
-
 struct ScanArgs {
   const void* u;
   const void* z;
@@ -212,24 +56,50 @@ struct ScanArgs {
   int T, C, u_act, z_act;
 };
 
+
+// C2 / edge policy of the fused scan: the state of the thread's bins lives in
+// registers for the whole launch (h: C2 units, hE: DC / Nyquist bins).
+template <class G>
+struct GatedScanOp {
+  static constexpr int H = G::H, WH = G::WH, WF = G::WF, H1 = G::H1, H2 = G::H2;
+  float2 (&h)[G::JC2][2][G::H2];
+  float2 (&hE)[G::JE][4];
+  Buf gbuf;   // gates of (b, t): (H, WF) float4
+  Buf kbuf;   // K_hat of the group's planes: (NP, H, WF) float2
+
+  // gates of (b, t) and the spectral kernel of this plane at bins (k + H1 q, v)
+  __device__ __forceinline__ void bins(int j, int a2, int pl, int k, int v, float2 (&sp)[G::H2]) const {
+    const unsigned gi = unsigned(k * WF + v), ki = unsigned(pl * H * WF) + gi;
+    float4 gq[H2];
+    float2 kq[H2];
+#pragma unroll
+    for (int q = 0; q < H2; ++q) {
+      gq[q] = gbuf.ld4((gi + q * H1 * WF) * 16u);
+      kq[q] = kbuf.ld2((ki + q * H1 * WF) * 8u);
+    }
+#pragma unroll
+    for (int q = 0; q < H2; ++q) sp[q] = scan_bin(h[j][a2][q], sp[q], gq[q], kq[q]);
+  }
+
+  __device__ __forceinline__ void edge(int j, int pl, int uA, int uB, int, float2 (&v4)[4]) const {
+    const unsigned kp = unsigned(pl * H * WF);
+    const unsigned bi[4] = {unsigned(uA * WF), unsigned(uA * WF + WH), unsigned(uB * WF), unsigned(uB * WF + WH)};
+#pragma unroll
+    for (int i = 0; i < 4; ++i) v4[i] = scan_bin(hE[j][i], v4[i], gbuf.ld4(bi[i] * 16u), kbuf.ld2((kp + bi[i]) * 8u));
+  }
+};
+
 template <int LH, int LW, int NP, int PPT, class IO>
 __global__ void __launch_bounds__((NP << (LH + LW)) / PPT, PPT >= 64 ? 2 : 1)
 gated_scan_pow2(const ScanArgs a) {
   using G = Geom<LH, LW, NP, PPT>;
   static_assert(G::NT == (NP << (LH + LW)) / PPT, "launch bound");
-  constexpr int H = G::H, HP = G::HP, WH = G::WH, WF = G::WF, W = G::W;
-  constexpr int W1 = G::W1, W2 = G::W2, H1 = G::H1, H2 = G::H2, NT = G::NT;
+  constexpr int H = G::H, WF = G::WF, W = G::W, H2 = G::H2, NT = G::NT;
   using V4 = typename IO::V4;
   using TE = typename IO::T;
 
   __shared__ __attribute__((aligned(16))) float smem[G::LDS_FLOATS];
-  float* const buf = smem;
-  float2* const edge = reinterpret_cast<float2*>(smem + G::OFF_EDGE);
-  float2* const twR1 = reinterpret_cast<float2*>(smem + G::OFF_TW);
-  float2* const twC1 = twR1 + G::N_R1;
-  float2* const twI1 = twC1 + G::N_C1;
-  float2* const twI3 = twI1 + G::N_I1;
-  auto cplx = [&](int off) -> float2& { return *reinterpret_cast<float2*>(buf + off); };
+  const PlaneFft<G> fft(smem);
 
   const int T = a.T, C = a.C;
   // this workgroup: batch b, channels c0 .. c0 + NP - 1 (C % NP == 0)
@@ -241,21 +111,8 @@ gated_scan_pow2(const ScanArgs a) {
   const TE* __restrict__ up = static_cast<const TE*>(a.u);
   const TE* __restrict__ zp = static_cast<const TE*>(a.z);
   TE* __restrict__ yp = static_cast<TE*>(a.y);
-  const Buf kbuf(a.khat + size_t(c0) * H * WF, unsigned(NP * H * WF * sizeof(float2)));
 
-  {
-    const int tid = threadIdx.x;
-    // twiddles w_N^m = exp(-2 pi i m / N) from double precision
-    auto tw = [](int m, int n) -> float2 {
-      double sn, cs;
-      sincospi(2.0 * double(m) / double(n), &sn, &cs);
-      return make_float2(float(cs), float(-sn));
-    };
-    for (int i = tid; i < G::N_R1; i += NT) twR1[i] = tw((i / G::TR1) * (i % G::TR1), W);
-    for (int i = tid; i < G::N_C1; i += NT) twC1[i] = tw((i / G::TC1) * (i % G::TC1), H);
-    for (int i = tid; i < G::N_I1; i += NT) twI1[i] = cconj(tw((i % G::TI1) * (i / G::TI1), H));
-    for (int i = tid; i < G::N_I3; i += NT) twI3[i] = cconj(tw((i % G::TI3) * (i / G::TI3), W));
-  }
+  fft.init_twiddles(threadIdx.x);
 
   float2 h[G::JC2][2][H2];
   float2 hE[G::JE][4];
@@ -268,32 +125,6 @@ gated_scan_pow2(const ScanArgs a) {
 #pragma unroll
     for (int k = 0; k < 4; ++k) hE[j][k] = make_float2(0.f, 0.f);
 
-  // LDS slot of 4-vector f of the group (row-major over planes and rows)
-  auto v4_store = [&](unsigned f, float4 v) {
-    const int pl = int(f / (H * W / 4)), rem = int(f % (H * W / 4));
-    const int r = rem / (W / 4), w = 4 * (rem % (W / 4));
-    const int blk = w / W2, pos = w % W2;
-    if (G::V4_SPLIT && blk >= W1 / 2) {
-      cplx(G::row_off(pl, r) + blk * W2 + (pos ^ 2)) = make_float2(v.x, v.y);
-      cplx(G::row_off(pl, r) + blk * W2 + pos) = make_float2(v.z, v.w);
-    } else {
-      const int o = blk >= W1 / 2 ? (pos ^ G::HALF) : pos;
-      *reinterpret_cast<float4*>(buf + G::row_off(pl, r) + blk * W2 + o) = v;
-    }
-  };
-  auto v4_load = [&](unsigned f) -> float4 {
-    const int pl = int(f / (H * W / 4)), rem = int(f % (H * W / 4));
-    const int r = rem / (W / 4), w = 4 * (rem % (W / 4));
-    const int blk = w / W2, pos = w % W2;
-    if (G::V4_SPLIT && blk >= W1 / 2) {
-      const float2 lo = cplx(G::row_off(pl, r) + blk * W2 + (pos ^ 2));
-      const float2 hi = cplx(G::row_off(pl, r) + blk * W2 + pos);
-      return make_float4(lo.x, lo.y, hi.x, hi.y);
-    }
-    const int o = blk >= W1 / 2 ? (pos ^ G::HALF) : pos;
-    return *reinterpret_cast<const float4*>(buf + G::row_off(pl, r) + blk * W2 + o);
-  };
-
   // u_0 into the plane buffer
   {
     const unsigned tid = threadIdx.x;
@@ -302,7 +133,7 @@ gated_scan_pow2(const ScanArgs a) {
 #pragma unroll
     for (int i = 0; i < G::JLD; ++i) ld[i] = src[i * NT + tid];
 #pragma unroll
-    for (int i = 0; i < G::JLD; ++i) v4_store(i * NT + tid, act4(IO::to_f4(ld[i]), a.u_act));
+    for (int i = 0; i < G::JLD; ++i) fft.v4_store(i * NT + tid, act4(IO::to_f4(ld[i]), a.u_act));
   }
   __syncthreads();
 
@@ -312,293 +143,18 @@ gated_scan_pow2(const ScanArgs a) {
     // hundreds of them into registers for the whole scan.
     unsigned tid = threadIdx.x;
     asm volatile("" : "+v"(tid));
-    const Buf gbuf(a.gates + (size_t(b) * T + t) * size_t(H) * WF, unsigned(H * WF * sizeof(float4)));
+    GatedScanOp<G> op{h, hE, Buf(a.gates + (size_t(b) * T + t) * size_t(H) * WF, unsigned(H * WF * sizeof(float4))),
+                      Buf(a.khat + size_t(c0) * H * WF, unsigned(NP * H * WF * sizeof(float2)))};
 
-    // ---------------------------------------------- R1: DFT-W1 over m, twiddle
-#pragma unroll
-    for (int j = 0; j < G::JR1; ++j) {
-      int pl, p, s;
-      G::r1_job(j * NT + tid, pl, p, s);
-      float2 zz[W1];
-#pragma unroll
-      for (int m = 0; m < W1; ++m) {
-        const int o = (m >= W1 / 2) ? (s ^ G::HALF) : s;
-        zz[m] = make_float2(buf[G::row_off(pl, p) + m * W2 + o], buf[G::row_off(pl, p + HP) + m * W2 + o]);
-      }
-      Dft<W1, false>::run(zz);
-#pragma unroll
-      for (int k = 0; k < W1; ++k) {
-        const float2 v = k ? cmul(zz[k], twR1[s * G::TR1 + k]) : zz[0];
-        const int o = (k >= W1 / 2) ? (s ^ G::HALF) : s;
-        buf[G::row_off(pl, p) + k * W2 + o] = v.x;
-        buf[G::row_off(pl, p + HP) + k * W2 + o] = v.y;
-      }
-      __builtin_amdgcn_sched_barrier(0);
-    }
-    __syncthreads();
-
-    // ----------------- R2: DFT-W2 over s, separate packed row pairs (x2 scale)
-#pragma unroll
-    for (int j = 0; j < G::JR2; ++j) {
-      const unsigned jb = j * NT + tid;
-      const int jj = int(jb % (W1 / 2)), p = int((jb / (W1 / 2)) % HP), pl = int(jb / (HP * (W1 / 2)));
-      int kA, kB;
-      pair_units<W1>(jj, kA, kB);
-      float2 za[W2], zb[W2];
-#pragma unroll
-      for (int s = 0; s < W2; ++s) {
-        za[s] = make_float2(buf[G::lo_off(pl, p, kA, s)], buf[G::lo_off(pl, p + HP, kA, s)]);
-        zb[s] = make_float2(buf[G::hi_off(pl, p, kB, s)], buf[G::hi_off(pl, p + HP, kB, s)]);
-      }
-      Dft<W2, false>::run(za);
-      Dft<W2, false>::run(zb);
-      // Z[kA + W1 q] = za[q], Z[kB + W1 q] = zb[q]
-      // 2 X_p[v] = Z[v] + conj Z[-v] ; 2 X_{p+HP}[v] = -i (Z[v] - conj Z[-v])
-      // v = kA + W1 q sits in (lo) block kA, v = kB + W1 q in (hi) block kB
-      auto emit = [&](bool hi, int blk, int q, float2 zv, float2 zm) {
-        const int o0 = hi ? G::hi_off(pl, p, blk, 2 * q) : G::lo_off(pl, p, blk, 2 * q);
-        const int o1 = hi ? G::hi_off(pl, p + HP, blk, 2 * q) : G::lo_off(pl, p + HP, blk, 2 * q);
-        cplx(o0) = make_float2(zv.x + zm.x, zv.y - zm.y);
-        cplx(o1) = make_float2(zv.y + zm.y, zm.x - zv.x);
-      };
-      if (jj != 0) {
-#pragma unroll
-        for (int q = 0; q < W2 / 2; ++q) {
-          emit(false, kA, q, za[q], zb[W2 - 1 - q]);
-          emit(true, kB, q, zb[q], za[W2 - 1 - q]);
-        }
-      } else {
-        // packed column 0: 2 (DC + i Nyquist) of both rows
-        const float2 z0 = za[0], zn = za[W2 / 2];
-        cplx(G::lo_off(pl, p, 0, 0)) = make_float2(z0.x + z0.x, zn.x + zn.x);
-        cplx(G::lo_off(pl, p + HP, 0, 0)) = make_float2(z0.y + z0.y, zn.y + zn.y);
-#pragma unroll
-        for (int q = 1; q < W2 / 2; ++q) emit(false, 0, q, za[q], za[W2 - q]);
-#pragma unroll
-        for (int q = 0; q < W2 / 2; ++q) emit(true, W1 / 2, q, zb[q], zb[W2 - 1 - q]);
-      }
-      __builtin_amdgcn_sched_barrier(0);
-    }
-    __syncthreads();
-
-    // ------------------------------------------ C1: DFT-H1 over m, twiddle
-#pragma unroll
-    for (int j = 0; j < G::JC1; ++j) {
-      const unsigned jb = j * NT + tid;
-      const int v = int(jb % WH), s = int((jb / WH) % H2), pl = int(jb / (WH * H2));
-      const int col = G::p_col(v);
-      float2 zz[H1];
-#pragma unroll
-      for (int m = 0; m < H1; ++m) zz[m] = cplx(G::row_off(pl, s + H2 * m) + col);
-      Dft<H1, false>::run(zz);
-#pragma unroll
-      for (int k = 0; k < H1; ++k)
-        cplx(G::row_off(pl, s + H2 * k) + col) = k ? cmul(zz[k], twC1[s * G::TC1 + k]) : zz[0];
-      __builtin_amdgcn_sched_barrier(0);
-    }
-    __syncthreads();
-
-    // ------ C2: DFT-H2 over s -> spectrum; recurrence; inverse DFT-H2 (I1)
-    // one unit (kA, then kB) at a time keeps the live registers to one unit's
-    // spectrum, gates and spectral kernel on top of the state
-#pragma unroll
-    for (int j = 0; j < G::JC2; ++j) {
-      const unsigned jb = j * NT + tid;
-      const int v = int(jb % WH), pl = int(jb / (WH * (H1 / 2)));
-      int kA, kB;
-      pair_units<H1>(int((jb / WH) % (H1 / 2)), kA, kB);
-      const int col = G::p_col(v);
-#pragma unroll
-      for (int a2 = 0; a2 < 2; ++a2) {
-        const int k = a2 ? kB : kA;
-        float2 sp[H2];
-#pragma unroll
-        for (int s = 0; s < H2; ++s) sp[s] = cplx(G::row_off(pl, s + H2 * k) + col);
-        Dft<H2, false>::run(sp);
-        if (v == 0) {
-          // packed DC/Nyquist column: hand to the edge pass
-#pragma unroll
-          for (int q = 0; q < H2; ++q) edge[pl * H + k + H1 * q] = sp[q];
-        } else {
-          // gates of (b, t) and the spectral kernel of this plane at bins (k + H1 q, v)
-          const unsigned gi = unsigned(k * WF + v), ki = unsigned(pl * H * WF) + gi;
-          float4 gq[H2];
-          float2 kq[H2];
-#pragma unroll
-          for (int q = 0; q < H2; ++q) {
-            gq[q] = gbuf.ld4((gi + q * H1 * WF) * 16u);
-            kq[q] = kbuf.ld2((ki + q * H1 * WF) * 8u);
-          }
-#pragma unroll
-          for (int q = 0; q < H2; ++q) sp[q] = scan_bin(h[j][a2][q], sp[q], gq[q], kq[q]);
-          Dft<H2, true>::run(sp);
-#pragma unroll
-          for (int s = 0; s < H2; ++s)
-            cplx(G::row_off(pl, s + H2 * k) + col) = s ? cmul(sp[s], twI1[k * G::TI1 + s]) : sp[0];
-        }
-        __builtin_amdgcn_sched_barrier(0);
-      }
-    }
-    __syncthreads();
-
-    // ------------------- edge pass: DC and Nyquist columns (unpack, scan, repack)
-#pragma unroll
-    for (int j = 0; j < G::JE; ++j) {
-      const unsigned jb = j * NT + tid;
-      if (jb < unsigned(G::NE)) {
-        const int e = int(jb % HP), pl = int(jb / HP);
-        const int uA = e, uB = (e == 0) ? HP : H - e;
-        float4 ge[4];
-        float2 ke[4];
-        const unsigned kp = unsigned(pl * H * WF);
-        ge[0] = gbuf.ld4(unsigned(uA * WF) * 16u);
-        ge[1] = gbuf.ld4(unsigned(uA * WF + WH) * 16u);
-        ge[2] = gbuf.ld4(unsigned(uB * WF) * 16u);
-        ge[3] = gbuf.ld4(unsigned(uB * WF + WH) * 16u);
-        ke[0] = kbuf.ld2((kp + uA * WF) * 8u);
-        ke[1] = kbuf.ld2((kp + uA * WF + WH) * 8u);
-        ke[2] = kbuf.ld2((kp + uB * WF) * 8u);
-        ke[3] = kbuf.ld2((kp + uB * WF + WH) * 8u);
-        // partners -u mod H: uB for uA when e > 0; both self-partnered when e == 0
-        const float2 cA = edge[pl * H + uA], cB = edge[pl * H + uB];
-        const float2 cAm = (e == 0) ? cA : cB, cBm = (e == 0) ? cB : cA;
-        // U(u,0) = (C[u] + conj C[-u]) / 2 ; U(u,W/2) = -i (C[u] - conj C[-u]) / 2
-        const float2 u0A = make_float2(0.5f * (cA.x + cAm.x), 0.5f * (cA.y - cAm.y));
-        const float2 uNA = make_float2(0.5f * (cA.y + cAm.y), 0.5f * (cAm.x - cA.x));
-        const float2 u0B = make_float2(0.5f * (cB.x + cBm.x), 0.5f * (cB.y - cBm.y));
-        const float2 uNB = make_float2(0.5f * (cB.y + cBm.y), 0.5f * (cBm.x - cB.x));
-        const float2 y0A = scan_bin(hE[j][0], u0A, ge[0], ke[0]);
-        const float2 yNA = scan_bin(hE[j][1], uNA, ge[1], ke[1]);
-        const float2 y0B = scan_bin(hE[j][2], u0B, ge[2], ke[2]);
-        const float2 yNB = scan_bin(hE[j][3], uNB, ge[3], ke[3]);
-        // repack: c[u] = Herm(Y0)[u] + i Herm(YN)[u], Herm(X)[u] = (X[u] + conj X[-u]) / 2
-        float2 cOutA, cOutB;
-        if (e != 0) {
-          const float2 h0A = make_float2(0.5f * (y0A.x + y0B.x), 0.5f * (y0A.y - y0B.y));
-          const float2 hNA = make_float2(0.5f * (yNA.x + yNB.x), 0.5f * (yNA.y - yNB.y));
-          const float2 h0B = make_float2(0.5f * (y0B.x + y0A.x), 0.5f * (y0B.y - y0A.y));
-          const float2 hNB = make_float2(0.5f * (yNB.x + yNA.x), 0.5f * (yNB.y - yNA.y));
-          cOutA = make_float2(h0A.x - hNA.y, h0A.y + hNA.x);
-          cOutB = make_float2(h0B.x - hNB.y, h0B.y + hNB.x);
-        } else {
-          cOutA = make_float2(y0A.x, yNA.x);
-          cOutB = make_float2(y0B.x, yNB.x);
-        }
-        edge[pl * H + uA] = cOutA;
-        edge[pl * H + uB] = cOutB;
-      }
-    }
-    __syncthreads();
-
-    // ---------------- I1 for the packed column: inverse DFT-H2, conj twiddle
-#pragma unroll
-    for (int j = 0; j < G::JC2; ++j) {
-      const unsigned jb = j * NT + tid;
-      const int v = int(jb % WH), pl = int(jb / (WH * (H1 / 2)));
-      if (v == 0) {
-        int kA, kB;
-        pair_units<H1>(int((jb / WH) % (H1 / 2)), kA, kB);
-        float2 sa[H2], sb[H2];
-#pragma unroll
-        for (int q = 0; q < H2; ++q) {
-          sa[q] = edge[pl * H + kA + H1 * q];
-          sb[q] = edge[pl * H + kB + H1 * q];
-        }
-        Dft<H2, true>::run(sa);
-        Dft<H2, true>::run(sb);
-        const int col = G::p_col(0);
-#pragma unroll
-        for (int s = 0; s < H2; ++s) {
-          cplx(G::row_off(pl, s + H2 * kA) + col) = s ? cmul(sa[s], twI1[kA * G::TI1 + s]) : sa[0];
-          cplx(G::row_off(pl, s + H2 * kB) + col) = s ? cmul(sb[s], twI1[kB * G::TI1 + s]) : sb[0];
-        }
-      }
-    }
-    __syncthreads();
-
-    // ----------------------------- I2: inverse DFT-H1 over k -> rows (P slots)
-#pragma unroll
-    for (int j = 0; j < G::JC1; ++j) {
-      const unsigned jb = j * NT + tid;
-      const int v = int(jb % WH), s = int((jb / WH) % H2), pl = int(jb / (WH * H2));
-      const int col = G::p_col(v);
-      float2 zz[H1];
-#pragma unroll
-      for (int k = 0; k < H1; ++k) zz[k] = cplx(G::row_off(pl, s + H2 * k) + col);
-      Dft<H1, true>::run(zz);
-#pragma unroll
-      for (int m = 0; m < H1; ++m) cplx(G::row_off(pl, s + H2 * m) + col) = zz[m];
-      __builtin_amdgcn_sched_barrier(0);
-    }
-    __syncthreads();
-
-    // ------------- I3: build packed Hermitian row pair, inverse DFT-W2, twiddle
-#pragma unroll
-    for (int j = 0; j < G::JR2; ++j) {
-      const unsigned jb = j * NT + tid;
-      const int jj = int(jb % (W1 / 2)), p = int((jb / (W1 / 2)) % HP), pl = int(jb / (HP * (W1 / 2)));
-      int kA, kB;
-      pair_units<W1>(jj, kA, kB);
-      float2 za[W2], zb[W2];
-      // Q[v] = Zp[v] + i Zq[v]; Q[W-v] = conj Zp[v] + i conj Zq[v]  (0 < v < W/2)
-      auto fetch = [&](bool hi, int blk, int q, float2& qv, float2& qm) {
-        const int o0 = hi ? G::hi_off(pl, p, blk, 2 * q) : G::lo_off(pl, p, blk, 2 * q);
-        const int o1 = hi ? G::hi_off(pl, p + HP, blk, 2 * q) : G::lo_off(pl, p + HP, blk, 2 * q);
-        const float2 x = cplx(o0), c = cplx(o1);
-        qv = make_float2(x.x - c.y, x.y + c.x);
-        qm = make_float2(x.x + c.y, c.x - x.y);
-      };
-      if (jj != 0) {
-#pragma unroll
-        for (int q = 0; q < W2 / 2; ++q) {
-          fetch(false, kA, q, za[q], zb[W2 - 1 - q]);
-          fetch(true, kB, q, zb[q], za[W2 - 1 - q]);
-        }
-      } else {
-        const float2 cp = cplx(G::lo_off(pl, p, 0, 0)), cq = cplx(G::lo_off(pl, p + HP, 0, 0));
-        za[0] = make_float2(cp.x, cq.x);          // Q[0]   = Re c_p + i Re c_q
-        za[W2 / 2] = make_float2(cp.y, cq.y);     // Q[W/2] = Im c_p + i Im c_q
-#pragma unroll
-        for (int q = 1; q < W2 / 2; ++q) fetch(false, 0, q, za[q], za[W2 - q]);
-#pragma unroll
-        for (int q = 0; q < W2 / 2; ++q) fetch(true, W1 / 2, q, zb[q], zb[W2 - 1 - q]);
-      }
-      Dft<W2, true>::run(za);
-      Dft<W2, true>::run(zb);
-#pragma unroll
-      for (int s = 0; s < W2; ++s) {
-        const float2 oa = s ? cmul(za[s], twI3[kA * G::TI3 + s]) : za[0];
-        const float2 ob = s ? cmul(zb[s], twI3[kB * G::TI3 + s]) : zb[0];
-        buf[G::lo_off(pl, p, kA, s)] = oa.x;
-        buf[G::lo_off(pl, p + HP, kA, s)] = oa.y;
-        buf[G::hi_off(pl, p, kB, s)] = ob.x;
-        buf[G::hi_off(pl, p + HP, kB, s)] = ob.y;
-      }
-      __builtin_amdgcn_sched_barrier(0);
-    }
-    __syncthreads();
-
-    // ------------------------ I4: inverse DFT-W1 over k -> real rows p, p+H/2
-#pragma unroll
-    for (int j = 0; j < G::JR1; ++j) {
-      int pl, p, s;
-      G::r1_job(j * NT + tid, pl, p, s);
-      float2 zz[W1];
-#pragma unroll
-      for (int k = 0; k < W1; ++k) {
-        const int o = (k >= W1 / 2) ? (s ^ G::HALF) : s;
-        zz[k] = make_float2(buf[G::row_off(pl, p) + k * W2 + o], buf[G::row_off(pl, p + HP) + k * W2 + o]);
-      }
-      Dft<W1, true>::run(zz);
-#pragma unroll
-      for (int m = 0; m < W1; ++m) {
-        const int o = (m >= W1 / 2) ? (s ^ G::HALF) : s;
-        buf[G::row_off(pl, p) + m * W2 + o] = zz[m].x;
-        buf[G::row_off(pl, p + HP) + m * W2 + o] = zz[m].y;
-      }
-      __builtin_amdgcn_sched_barrier(0);
-    }
-    __syncthreads();
+    fft.r1(tid);
+    fft.r2(tid);
+    fft.c1(tid);
+    fft.template c2<true, true>(tid, op);
+    fft.template edges<true, true>(tid, op);
+    fft.i1_packed(tid);
+    fft.i2(tid);
+    fft.i3(tid);
+    fft.i4(tid);
 
     // ---------- STORE y_t = y * z_gate, and LOAD u_{t+1} into the same slots
     // (in chunks of CH vectors to bound the registers in flight)
@@ -619,13 +175,13 @@ gated_scan_pow2(const ScanArgs a) {
 #pragma unroll
         for (int i = 0; i < CH; ++i) {
           const unsigned f = (c + i) * NT + tid;
-          const float4 yv = v4_load(f);
+          const float4 yv = fft.v4_load(f);
           const float4 gv = act4(IO::to_f4(ldg[i]), a.z_act);
           dst[f] = IO::from_f4(make_float4(yv.x * gv.x, yv.y * gv.y, yv.z * gv.z, yv.w * gv.w));
         }
         if (t + 1 < T) {
 #pragma unroll
-          for (int i = 0; i < CH; ++i) v4_store((c + i) * NT + tid, act4(IO::to_f4(ldu[i]), a.u_act));
+          for (int i = 0; i < CH; ++i) fft.v4_store((c + i) * NT + tid, act4(IO::to_f4(ldu[i]), a.u_act));
         }
         __builtin_amdgcn_sched_barrier(0);
       }

@@ -1,0 +1,641 @@
+// GatedDeltaNetCSSM (the `gdn` cell, src/models/cssm.py:4685-5141) on gfx950.
+//
+// Large planes cannot keep a (batch, head)'s state on one CU: at 128x128 and
+// d_k = 4 the 4x4 complex state of every half-spectrum bin is 1.06 MB, against
+// 512 KB of VGPRs and 160 KB of LDS per CU.  The spectral core therefore runs
+// as three stream-ordered kernels:
+//   rfft2_planes     q, k, v planes -> half spectra + per-plane sum |X|^2
+//                    (the spectral L2 norms, :4890-4897)
+//   gdn_scan_bins    per (b, head, bin): key-vector norm (:4899-4906), the
+//                    delta-rule recurrence with the 4x4 state in VGPRs over
+//                    all T (:4911-4991), readout o = S q (:4998-5000)
+//   irfft2_planes    o spectra -> o planes (:5025, C2R rule)
+// plus the prologue kernels (channels-last frame mean for ctx, the gate
+// vectors, the qkv depthwise conv, the causal short conv + SiLU + input gates).
+// The forward / inverse transforms are the LDS passes of fft_plane.h.
+#include <hip/hip_runtime.h>
+#include <math.h>
+#include <stdint.h>
+
+#include <initializer_list>
+
+#include "fft_plane.h"
+#include "launch.h"
+
+namespace cssm {
+
+namespace {
+
+__device__ __forceinline__ float ld_f(const float* p, size_t i) { return p[i]; }
+__device__ __forceinline__ float ld_f(const uint16_t* p, size_t i) { return bf16_to_f32(p[i]); }
+__device__ __forceinline__ void st_f(float* p, size_t i, float v) { p[i] = v; }
+__device__ __forceinline__ void st_f(uint16_t* p, size_t i, float v) { p[i] = uint16_t(f32_to_bf16(v)); }
+
+__device__ __forceinline__ float sigmoid_f(float x) { return 1.0f / (1.0f + expf(-x)); }
+
+// to_goom's floor (goom.py:161-174): |z| < 1e-7 -> 1e-7 + 0j
+__device__ __forceinline__ float2 goom_floor2(float2 z) {
+  return (z.x * z.x + z.y * z.y < 1e-14f) ? make_float2(1e-7f, 0.0f) : z;
+}
+
+}  // namespace
+
+// ---------------------------------------------------------------------------
+// Batched 2-D real FFTs of power-of-two planes.
+// ---------------------------------------------------------------------------
+
+// forward policy: bins -> HBM spectrum (undoing the pass's factor 2), |X|^2
+// summed per plane into LDS
+template <class G>
+struct SpecStoreOp {
+  static constexpr int H = G::H, WH = G::WH, WF = G::WF, H1 = G::H1, H2 = G::H2;
+  float2* out;      // (NP, H, WF) of this workgroup
+  float* psum;      // LDS (NP)
+  int nvalid;       // planes of the group that exist (the last group may be partial)
+
+  __device__ __forceinline__ void bins(int, int, int pl, int k, int v, float2 (&sp)[G::H2]) const {
+    if (pl >= nvalid) return;
+    float s = 0.0f;
+#pragma unroll
+    for (int q = 0; q < H2; ++q) {
+      const float2 x = make_float2(0.5f * sp[q].x, 0.5f * sp[q].y);
+      out[size_t(pl * H + k + H1 * q) * WF + v] = x;
+      s = fmaf(x.x, x.x, fmaf(x.y, x.y, s));
+    }
+    if (psum) atomicAdd(&psum[pl], s);
+  }
+  __device__ __forceinline__ void edge(int, int pl, int uA, int uB, int, float2 (&v4)[4]) const {
+    if (pl >= nvalid) return;
+    const int idx[4] = {uA * WF, uA * WF + WH, uB * WF, uB * WF + WH};
+    float s = 0.0f;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const float2 x = make_float2(0.5f * v4[i].x, 0.5f * v4[i].y);
+      out[size_t(pl * H) * WF + idx[i]] = x;
+      s = fmaf(x.x, x.x, fmaf(x.y, x.y, s));
+    }
+    if (psum) atomicAdd(&psum[pl], s);
+  }
+};
+
+// inverse policy: bins <- HBM spectrum / (H W)
+template <class G>
+struct SpecLoadOp {
+  static constexpr int H = G::H, WH = G::WH, WF = G::WF, H1 = G::H1, H2 = G::H2;
+  const float2* in;   // (NP, H, WF) of this workgroup
+  float scale;        // 1 / (H W)
+  int nvalid;         // planes of the group that exist; the others transform zeros
+
+  __device__ __forceinline__ void bins(int, int, int pl, int k, int v, float2 (&sp)[G::H2]) const {
+    const bool ok = pl < nvalid;
+#pragma unroll
+    for (int q = 0; q < H2; ++q) {
+      const float2 x = ok ? in[size_t(pl * H + k + H1 * q) * WF + v] : make_float2(0.f, 0.f);
+      sp[q] = make_float2(x.x * scale, x.y * scale);
+    }
+  }
+  __device__ __forceinline__ void edge(int, int pl, int uA, int uB, int, float2 (&v4)[4]) const {
+    const bool ok = pl < nvalid;
+    const int idx[4] = {uA * WF, uA * WF + WH, uB * WF, uB * WF + WH};
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const float2 x = ok ? in[size_t(pl * H) * WF + idx[i]] : make_float2(0.f, 0.f);
+      v4[i] = make_float2(x.x * scale, x.y * scale);
+    }
+  }
+};
+
+// rfft2 of NP planes per workgroup: x (P, H, W) real -> spec (P, H, WF), norms (P) = sum |X|^2 or skipped.
+// The last group may hold fewer than NP planes: the missing ones are neither read nor written.
+template <int LH, int LW, int NP, int PPT, class IO>
+__global__ void __launch_bounds__((NP << (LH + LW)) / PPT)
+rfft2_planes(const void* __restrict__ x, long long P, float2* __restrict__ spec, float* __restrict__ norms) {
+  using G = Geom<LH, LW, NP, PPT>;
+  constexpr int H = G::H, W = G::W, WF = G::WF, NT = G::NT;
+  using V4 = typename IO::V4;
+  using TE = typename IO::T;
+  __shared__ __attribute__((aligned(16))) float smem[G::LDS_FLOATS];
+  __shared__ float psum[NP];
+  const PlaneFft<G> fft(smem);
+  const unsigned tid = threadIdx.x;
+  const size_t p0 = size_t(blockIdx.x) * NP;
+  const int nvalid = int(P - (long long)p0 < NP ? P - (long long)p0 : NP);
+  const unsigned nv4 = unsigned(nvalid) * (H * W / 4);
+  fft.init_twiddles(tid);
+  for (int i = tid; i < NP; i += NT) psum[i] = 0.0f;
+  {
+    const V4* src = reinterpret_cast<const V4*>(static_cast<const TE*>(x) + p0 * H * W);
+    V4 ld[G::JLD];
+#pragma unroll
+    for (int i = 0; i < G::JLD; ++i) {
+      const unsigned f = i * NT + tid;
+      ld[i] = f < nv4 ? src[f] : V4{};
+    }
+#pragma unroll
+    for (int i = 0; i < G::JLD; ++i) fft.v4_store(i * NT + tid, IO::to_f4(ld[i]));
+  }
+  __syncthreads();
+  SpecStoreOp<G> op{spec + p0 * H * WF, norms ? psum : nullptr, nvalid};
+  fft.r1(tid);
+  fft.r2(tid);
+  fft.c1(tid);
+  fft.template c2<true, false>(tid, op);
+  fft.template edges<true, false>(tid, op);
+  if (norms) {
+    for (int i = tid; i < nvalid; i += NT) norms[p0 + i] = psum[i];
+  }
+}
+
+// irfft2 of NP planes per workgroup: spec (P, H, WF) -> y (P, H, W) real (numpy C2R rule);
+// a partial last group neither reads nor writes the missing planes
+template <int LH, int LW, int NP, int PPT, class IO>
+__global__ void __launch_bounds__((NP << (LH + LW)) / PPT)
+irfft2_planes(const float2* __restrict__ spec, long long P, void* __restrict__ y) {
+  using G = Geom<LH, LW, NP, PPT>;
+  constexpr int H = G::H, W = G::W, WF = G::WF, NT = G::NT;
+  using V4 = typename IO::V4;
+  using TE = typename IO::T;
+  __shared__ __attribute__((aligned(16))) float smem[G::LDS_FLOATS];
+  const PlaneFft<G> fft(smem);
+  const unsigned tid = threadIdx.x;
+  const size_t p0 = size_t(blockIdx.x) * NP;
+  const int nvalid = int(P - (long long)p0 < NP ? P - (long long)p0 : NP);
+  const unsigned nv4 = unsigned(nvalid) * (H * W / 4);
+  fft.init_twiddles(tid);
+  __syncthreads();
+  SpecLoadOp<G> op{spec + p0 * H * WF, 1.0f / float(H * W), nvalid};
+  fft.template c2<false, true>(tid, op);
+  fft.template edges<false, true>(tid, op);
+  fft.i1_packed(tid);
+  fft.i2(tid);
+  fft.i3(tid);
+  fft.i4(tid);
+  V4* dst = reinterpret_cast<V4*>(static_cast<TE*>(y) + p0 * H * W);
+#pragma unroll
+  for (int i = 0; i < G::JLD; ++i) {
+    const unsigned f = i * NT + tid;
+    if (f < nv4) dst[f] = IO::from_f4(fft.v4_load(f));
+  }
+}
+
+namespace {
+
+// plane group of the table (largest first): the largest that still gives >= 512 workgroups, else the smallest
+int pick_group(long long P, std::initializer_list<int> nps) {
+  int best = 0;
+  for (int np : nps) {
+    best = np;
+    if ((P + np - 1) / np >= 512) return np;
+  }
+  return best;
+}
+
+template <int LH, int NP, int PPT, class IO>
+hipError_t run_fwd(const void* x, long long P, float2* spec, float* norms, hipStream_t s) {
+  using G = Geom<LH, LH, NP, PPT>;
+  hipLaunchKernelGGL((rfft2_planes<LH, LH, NP, PPT, IO>), dim3(unsigned((P + NP - 1) / NP)), dim3(G::NT), 0, s, x, P,
+                     spec, norms);
+  return hipGetLastError();
+}
+
+template <int LH, int NP, int PPT, class IO>
+hipError_t run_inv(const float2* spec, long long P, void* y, hipStream_t s) {
+  using G = Geom<LH, LH, NP, PPT>;
+  hipLaunchKernelGGL((irfft2_planes<LH, LH, NP, PPT, IO>), dim3(unsigned((P + NP - 1) / NP)), dim3(G::NT), 0, s, spec,
+                     P, y);
+  return hipGetLastError();
+}
+
+// the plane groups of the fused gated scan, per plane size
+#define CSSM_FFT_TABLE(CASE)                                                        \
+  if (H == 128) {                                                                   \
+    const int np = pick_group(P, {1});                                              \
+    CASE(7, 1, 64)                                                                  \
+  } else if (H == 64) {                                                             \
+    const int np = pick_group(P, {4, 2, 1});                                        \
+    CASE(6, 4, 64) CASE(6, 2, 64) CASE(6, 1, 64)                                    \
+  } else if (H == 32) {                                                             \
+    const int np = pick_group(P, {8, 4, 2});                                        \
+    CASE(5, 8, 32) CASE(5, 4, 32) CASE(5, 2, 32)                                    \
+  } else if (H == 16) {                                                             \
+    const int np = pick_group(P, {16, 8});                                          \
+    CASE(4, 16, 32) CASE(4, 8, 32)                                                  \
+  } else if (H == 8) {                                                              \
+    const int np = pick_group(P, {32});                                             \
+    CASE(3, 32, 32)                                                                 \
+  } else if (H == 4) {                                                              \
+    const int np = pick_group(P, {128});                                            \
+    CASE(2, 128, 32)                                                                \
+  }
+
+template <class IO>
+hipError_t dispatch_fwd(const void* x, long long P, int H, float2* spec, float* norms, hipStream_t s) {
+#define CSSM_FWD_CASE(LH, NP_, PPT_) \
+  if (np == NP_) return run_fwd<LH, NP_, PPT_, IO>(x, P, spec, norms, s);
+  CSSM_FFT_TABLE(CSSM_FWD_CASE)
+#undef CSSM_FWD_CASE
+  return hipErrorInvalidValue;
+}
+
+template <class IO>
+hipError_t dispatch_inv(const float2* spec, long long P, int H, void* y, hipStream_t s) {
+#define CSSM_INV_CASE(LH, NP_, PPT_) \
+  if (np == NP_) return run_inv<LH, NP_, PPT_, IO>(spec, P, y, s);
+  CSSM_FFT_TABLE(CSSM_INV_CASE)
+#undef CSSM_INV_CASE
+  return hipErrorInvalidValue;
+}
+
+}  // namespace
+
+// any plane count: a partial last group is masked
+int fft_planes_min_group(int H, int W) { return gated_scan_min_group(H, W) ? 1 : 0; }
+
+hipError_t launch_rfft2(const void* x, int dtype, long long P, int H, int W, float2* spec, float* norms,
+                        hipStream_t s) {
+  if (H != W) return hipErrorInvalidValue;
+  return dtype == 0 ? dispatch_fwd<IoF32>(x, P, H, spec, norms, s) : dispatch_fwd<IoBF16>(x, P, H, spec, norms, s);
+}
+
+hipError_t launch_irfft2(const float2* spec, long long P, int H, int W, void* y, int dtype, hipStream_t s) {
+  if (H != W) return hipErrorInvalidValue;
+  return dtype == 0 ? dispatch_inv<IoF32>(spec, P, H, y, s) : dispatch_inv<IoBF16>(spec, P, H, y, s);
+}
+
+// ---------------------------------------------------------------------------
+// Delta-rule recurrence per (b, head, bin), all T steps, state in VGPRs.
+//   q_a, k_a, v_i   spectra of channels head*DK + a of the q / k / v blocks
+//   spectral norm:  x <- x / sqrt(sum_bins |x|^2 + 1e-6)        (q and k, :4890-4897)
+//   key norm:       k <- k / sqrt(sum_a |k_a|^2 + 1e-6)          (:4899-4906)
+//   M[a][b] = floor(alpha W_hat (delta_ab - beta k_a conj k_b))  (:4911-4925)
+//   D[i][a] = floor(beta v_i conj k_a)                           (:4927-4929)
+//   s_i     = M s_i + D[i]                                       (:4945-4958, math.py:384-411;
+//             the log-space general matrix scan evaluates this linear recurrence,
+//             operations.py:314-390, with to_goom's floors on M and D)
+//   o_i     = sum_a s_i[a] q_a                                   (:4998-5000)
+// ---------------------------------------------------------------------------
+struct GdnBinArgs {
+  const float2* spec;   // (B, T, 3C, H, WF)
+  const float* norms;   // (B, T, 3C) sum |X|^2, or nullptr (no spectral L2 norm)
+  const float2* ab;     // (alpha, beta) at (b T + t) ab_frame + head ab_head + bin ab_bin
+  long long ab_frame;
+  int ab_head, ab_bin;
+  const float2* what;   // (n_h, H, WF)
+  float2* ohat;         // (B, T, C, H, WF)
+  int T, C, HWF;
+};
+
+template <int DK>
+__global__ void __launch_bounds__(256) gdn_scan_bins(const GdnBinArgs a) {
+  const int bin = blockIdx.x * blockDim.x + threadIdx.x;
+  if (bin >= a.HWF) return;
+  const int head = blockIdx.y, b = blockIdx.z;
+  const int C = a.C, HWF = a.HWF;
+  const float2 wh = a.what[size_t(head) * HWF + bin];
+  float2 s[DK][DK];   // s[i][a]
+#pragma unroll
+  for (int i = 0; i < DK; ++i)
+#pragma unroll
+    for (int j = 0; j < DK; ++j) s[i][j] = make_float2(0.f, 0.f);
+
+  for (int t = 0; t < a.T; ++t) {
+    const size_t fr = size_t(b) * a.T + t;
+    const size_t ch0 = fr * 3 * C + size_t(head) * DK;   // q block; k at + C, v at + 2C
+    float2 q[DK], k[DK], v[DK];
+#pragma unroll
+    for (int j = 0; j < DK; ++j) {
+      q[j] = a.spec[(ch0 + j) * HWF + bin];
+      k[j] = a.spec[(ch0 + C + j) * HWF + bin];
+      v[j] = a.spec[(ch0 + 2 * C + j) * HWF + bin];
+    }
+    if (a.norms) {
+#pragma unroll
+      for (int j = 0; j < DK; ++j) {
+        const float nq = 1.0f / sqrtf(a.norms[ch0 + j] + 1e-6f);
+        const float nk = 1.0f / sqrtf(a.norms[ch0 + C + j] + 1e-6f);
+        q[j] = cscale(q[j], nq);
+        k[j] = cscale(k[j], nk);
+      }
+    }
+    float kk = 0.0f;
+#pragma unroll
+    for (int j = 0; j < DK; ++j) kk = fmaf(k[j].x, k[j].x, fmaf(k[j].y, k[j].y, kk));
+    const float kn = 1.0f / sqrtf(kk + 1e-6f);
+#pragma unroll
+    for (int j = 0; j < DK; ++j) k[j] = cscale(k[j], kn);
+
+    const float2 g = a.ab[fr * a.ab_frame + size_t(head) * a.ab_head + size_t(bin) * a.ab_bin];
+    const float alpha = g.x, beta = g.y;
+    const float2 aw = cscale(wh, alpha);
+    float2 M[DK][DK];
+#pragma unroll
+    for (int r = 0; r < DK; ++r)
+#pragma unroll
+      for (int c = 0; c < DK; ++c) {
+        // alpha W (delta_rc - beta k_r conj k_c)
+        const float2 kk_rc = cmulc(k[r], k[c]);
+        float2 m = make_float2(-beta * kk_rc.x, -beta * kk_rc.y);
+        if (r == c) m.x += 1.0f;
+        M[r][c] = goom_floor2(cmul(aw, m));
+      }
+#pragma unroll
+    for (int i = 0; i < DK; ++i) {
+      float2 sn[DK];
+#pragma unroll
+      for (int r = 0; r < DK; ++r) {
+        float2 acc = goom_floor2(cscale(cmulc(v[i], k[r]), beta));
+#pragma unroll
+        for (int c = 0; c < DK; ++c) {
+          acc.x = fmaf(M[r][c].x, s[i][c].x, fmaf(-M[r][c].y, s[i][c].y, acc.x));
+          acc.y = fmaf(M[r][c].x, s[i][c].y, fmaf(M[r][c].y, s[i][c].x, acc.y));
+        }
+        sn[r] = acc;
+      }
+      float2 o = make_float2(0.f, 0.f);
+#pragma unroll
+      for (int r = 0; r < DK; ++r) {
+        s[i][r] = sn[r];
+        o.x = fmaf(sn[r].x, q[r].x, fmaf(-sn[r].y, q[r].y, o.x));
+        o.y = fmaf(sn[r].x, q[r].y, fmaf(sn[r].y, q[r].x, o.y));
+      }
+      a.ohat[(fr * C + size_t(head) * DK + i) * HWF + bin] = o;
+    }
+  }
+}
+
+hipError_t launch_gdn_scan_bins(const float2* spec, const float* norms, const float2* ab, long long ab_frame,
+                                int ab_head, int ab_bin, const float2* what, int B, int T, int C, int H, int W,
+                                int dk, float2* ohat, hipStream_t s) {
+  GdnBinArgs a;
+  a.spec = spec;
+  a.norms = norms;
+  a.ab = ab;
+  a.ab_frame = ab_frame;
+  a.ab_head = ab_head;
+  a.ab_bin = ab_bin;
+  a.what = what;
+  a.ohat = ohat;
+  a.T = T;
+  a.C = C;
+  a.HWF = H * (W / 2 + 1);
+  const dim3 grid(unsigned((a.HWF + 255) / 256), unsigned(C / dk), unsigned(B));
+  switch (dk) {
+    case 1: hipLaunchKernelGGL(gdn_scan_bins<1>, grid, dim3(256), 0, s, a); break;
+    case 2: hipLaunchKernelGGL(gdn_scan_bins<2>, grid, dim3(256), 0, s, a); break;
+    case 3: hipLaunchKernelGGL(gdn_scan_bins<3>, grid, dim3(256), 0, s, a); break;
+    case 4: hipLaunchKernelGGL(gdn_scan_bins<4>, grid, dim3(256), 0, s, a); break;
+    default: return hipErrorInvalidValue;
+  }
+  return hipGetLastError();
+}
+
+// ---------------------------------------------------------------------------
+// ctx = mean over (H, W) of channels-last x (F, HW, C) -> (F, C)   (:4785)
+// ---------------------------------------------------------------------------
+template <class TI>
+__global__ void __launch_bounds__(256) frame_mean_cl(const TI* __restrict__ x, int HW, int C, float* __restrict__ out) {
+  __shared__ float red[256];
+  const int f = blockIdx.x;
+  const TI* xf = x + size_t(f) * HW * C;
+  for (int c0 = 0; c0 < C; c0 += 256) {
+    const int cw = min(256, C - c0);
+    const int rows = 256 / cw;          // pixels summed in parallel
+    const int r = threadIdx.x / cw, c = threadIdx.x % cw;
+    float acc = 0.0f;
+    if (r < rows) {
+      for (int p = r; p < HW; p += rows) acc += ld_f(xf, size_t(p) * C + c0 + c);
+    }
+    red[threadIdx.x] = acc;
+    __syncthreads();
+    if (threadIdx.x < cw) {
+      float sum = 0.0f;
+      for (int i = 0; i < rows; ++i) sum += red[i * cw + threadIdx.x];
+      out[size_t(f) * C + c0 + threadIdx.x] = sum / float(HW);
+    }
+    __syncthreads();
+  }
+}
+
+hipError_t launch_frame_mean(const void* x, int dtype, int F, int HW, int C, float* out, hipStream_t s) {
+  if (dtype == 0)
+    hipLaunchKernelGGL(frame_mean_cl<float>, dim3(F), dim3(256), 0, s, static_cast<const float*>(x), HW, C, out);
+  else
+    hipLaunchKernelGGL(frame_mean_cl<uint16_t>, dim3(F), dim3(256), 0, s, static_cast<const uint16_t*>(x), HW, C,
+                       out);
+  return hipGetLastError();
+}
+
+// ---------------------------------------------------------------------------
+// Gate vectors of GatedDeltaNetCSSM from ctx (:4785-4869), one block per (b, t):
+//   ctx_t = ctx + E[t]  (temporal: 1 = sinusoid table with rope_base, :353-383;
+//                        2 = learned table (T, C); 0 = none)
+//   alpha = 0.1 + 0.89 sigmoid(g_alpha), beta = sigmoid(g_beta)   (spectral, per bin / head)
+//   B_k, B_v = sigmoid(g)                                          (spatial, per pixel)
+// gate kinds: factored  g[u, v] = (ctx kh + bh)[u] + (ctx kw + bw)[v]
+//             dense     g = ctx kd + bd          (n outputs)
+//             channel   g = ctx kd + bd          (n_h outputs; spectral only)
+//             scalar    g = ctx kd + bd          (1 output)
+// ab (B T, n_ab) float2 (alpha, beta); bkv (B T, n_kv) float2 (B_k, B_v).
+// ---------------------------------------------------------------------------
+__device__ float dot_col(const float* ctx, const float* k, int C, int n, int col) {
+  float acc = 0.0f;
+  for (int c = 0; c < C; ++c) acc = fmaf(ctx[c], k[size_t(c) * n + col], acc);
+  return acc;
+}
+
+__global__ void __launch_bounds__(256)
+gdn_gates_kernel(const float* __restrict__ ctx_in, int T, int C, int H, int W, int nh, GdnGateWeights w,
+                 int temporal, float rope_base, const float* __restrict__ ttable, float2* __restrict__ ab,
+                 float2* __restrict__ bkv) {
+  extern __shared__ float sm[];
+  const int bt = blockIdx.x, t = bt % T;
+  const int WF = W / 2 + 1;
+  float* cx = sm;                 // C
+  float* rows = sm + C;           // 4 x H
+  float* cols = rows + 4 * H;     // 4 x max(W, WF)
+  const int CW = W > WF ? W : WF;
+  for (int c = threadIdx.x; c < C; c += blockDim.x) {
+    float v = ctx_in[size_t(bt) * C + c];
+    if (temporal == 1) {
+      // E[t, 2j] = sin(t / base^(2j / C)), E[t, 2j + 1] = cos(.)
+      const int j2 = c & ~1;
+      const double th = double(t) / pow(double(rope_base), double(j2) / double(C));
+      v += float((c & 1) ? cos(th) : sin(th));
+    } else if (temporal == 2) {
+      v += ttable[size_t(t) * C + c];
+    }
+    cx[c] = v;
+  }
+  __syncthreads();
+  // gate g in {0 alpha, 1 beta, 2 B_k, 3 B_v}; spectral gates span (H, WF), spatial (H, W)
+  for (int g = 0; g < 4; ++g) {
+    if (!w.kd[g]) continue;
+    if (w.kind == 1) {
+      const int nc = g < 2 ? WF : W;
+      for (int i = threadIdx.x; i < H + nc; i += blockDim.x) {
+        if (i < H) rows[g * H + i] = dot_col(cx, w.kd[g], C, H, i) + w.bd[g][i];
+        else cols[g * CW + i - H] = dot_col(cx, w.kw[g], C, nc, i - H) + w.bw[g][i - H];
+      }
+    }
+  }
+  __syncthreads();
+  auto spectral = [&](int g, int i) -> float {       // raw gate at output i
+    if (w.kind == 1) return rows[g * H + i / WF] + cols[g * CW + i % WF];
+    const int n = w.kind == 0 ? H * WF : (w.kind == 2 ? nh : 1);
+    return dot_col(cx, w.kd[g], C, n, i) + w.bd[g][i];
+  };
+  auto spatial = [&](int g, int i) -> float {
+    if (w.kind == 1) return rows[g * H + i / W] + cols[g * CW + i % W];
+    const int n = w.kind == 0 ? H * W : 1;
+    return dot_col(cx, w.kd[g], C, n, i) + w.bd[g][i];
+  };
+  const int n_ab = w.kind == 2 ? nh : (w.kind == 3 ? 1 : H * WF);
+  for (int i = threadIdx.x; i < n_ab; i += blockDim.x) {
+    const float al = 0.1f + 0.89f * sigmoid_f(spectral(0, i));
+    const float be = sigmoid_f(spectral(1, i));
+    ab[size_t(bt) * n_ab + i] = make_float2(al, be);
+  }
+  if (bkv && w.kd[2] && w.kind != 2) {
+    const int n_kv = w.kind == 3 ? 1 : H * W;
+    for (int i = threadIdx.x; i < n_kv; i += blockDim.x)
+      bkv[size_t(bt) * n_kv + i] = make_float2(sigmoid_f(spatial(2, i)), sigmoid_f(spatial(3, i)));
+  }
+}
+
+hipError_t launch_gdn_gates(const float* ctx, int B, int T, int C, int H, int W, int nh, const GdnGateWeights& w,
+                            int temporal, float rope_base, const float* ttable, float2* ab, float2* bkv,
+                            hipStream_t s) {
+  const int WF = W / 2 + 1;
+  const size_t sm = sizeof(float) * (size_t(C) + 4 * size_t(H) + 4 * size_t(W > WF ? W : WF));
+  if (sm > 64 * 1024) return hipErrorInvalidValue;
+  hipLaunchKernelGGL(gdn_gates_kernel, dim3(unsigned(B * T)), dim3(256), sm, s, ctx, T, C, H, W, nh, w, temporal,
+                     rope_base, ttable, ab, bkv);
+  return hipGetLastError();
+}
+
+// ---------------------------------------------------------------------------
+// Depthwise k x k SAME convolution on channels-last frames (qkv_dw, :4744-4750):
+//   y[f, h, w, c] = b[c] + sum_{i, j} k[i, j, 0, c] x[f, h + i - lo, w + j - lo, c],
+//   lo = (k - 1) // 2 (Flax 'SAME'), zeros outside the frame.
+// ---------------------------------------------------------------------------
+template <class TI, class TO>
+__global__ void __launch_bounds__(256)
+dwconv_cl(const TI* __restrict__ x, int H, int W, int C, int ks, const float* __restrict__ kw,
+          const float* __restrict__ bias, TO* __restrict__ y, long long total) {
+  const long long i = (long long)blockIdx.x * blockDim.x + threadIdx.x;
+  if (i >= total) return;
+  const int c = int(i % C);
+  const long long pix = i / C;
+  const int w = int(pix % W), h = int((pix / W) % H);
+  const long long f = pix / (size_t(H) * W);
+  const int lo = (ks - 1) / 2;
+  const TI* xf = x + size_t(f) * H * W * C;
+  float acc = bias[c];
+  for (int a = 0; a < ks; ++a) {
+    const int hh = h + a - lo;
+    if (hh < 0 || hh >= H) continue;
+    for (int b2 = 0; b2 < ks; ++b2) {
+      const int ww = w + b2 - lo;
+      if (ww < 0 || ww >= W) continue;
+      acc = fmaf(ld_f(xf, (size_t(hh) * W + ww) * C + c), kw[(a * ks + b2) * C + c], acc);
+    }
+  }
+  st_f(y, size_t(i), acc);
+}
+
+hipError_t launch_depthwise_conv(const void* x, int dtype, int F, int H, int W, int C, int ks, const float* kw,
+                                 const float* bias, void* y, int out_dtype, hipStream_t s) {
+  const long long total = (long long)F * H * W * C;
+  const unsigned blocks = unsigned((total + 255) / 256);
+  const dim3 g(blocks), b(256);
+  if (dtype == 0 && out_dtype == 0)
+    hipLaunchKernelGGL((dwconv_cl<float, float>), g, b, 0, s, static_cast<const float*>(x), H, W, C, ks, kw, bias,
+                       static_cast<float*>(y), total);
+  else if (dtype == 0)
+    hipLaunchKernelGGL((dwconv_cl<float, uint16_t>), g, b, 0, s, static_cast<const float*>(x), H, W, C, ks, kw, bias,
+                       static_cast<uint16_t*>(y), total);
+  else if (out_dtype == 0)
+    hipLaunchKernelGGL((dwconv_cl<uint16_t, float>), g, b, 0, s, static_cast<const uint16_t*>(x), H, W, C, ks, kw,
+                       bias, static_cast<float*>(y), total);
+  else
+    hipLaunchKernelGGL((dwconv_cl<uint16_t, uint16_t>), g, b, 0, s, static_cast<const uint16_t*>(x), H, W, C, ks, kw,
+                       bias, static_cast<uint16_t*>(y), total);
+  return hipGetLastError();
+}
+
+// ---------------------------------------------------------------------------
+// In place on plane-major qkv (B, T, 3C, HW): causal depthwise conv over T
+// (kernel (kt, 1, C) per block, left zero padding) + bias + SiLU (:4763-4780),
+// then the input gates on the k and v blocks (:4844-4848):
+//   gate_mode 0: none; 1: per pixel, gates (B T, HW) float2 (B_k, B_v);
+//   2: per frame, gates (B T) float2; 3: per channel and pixel, gates
+//   plane-major (B T, 2C, HW) float (B_k channels then B_v channels).
+// kt = 0 skips the convolution and the SiLU (the reference applies SiLU only
+// inside the short convolution).  One thread per (b, channel, pixel), T loop
+// inside with the last kt - 1 inputs in registers.
+// ---------------------------------------------------------------------------
+constexpr int kMaxShortConv = 8;
+
+template <class T>
+__global__ void __launch_bounds__(256)
+gdn_qkv_post(T* __restrict__ qkv, int Tn, int C, int HW, int kt, GdnShortConv sc, int gate_mode,
+             const void* __restrict__ gates, long long total) {
+  const long long i = (long long)blockIdx.x * blockDim.x + threadIdx.x;
+  if (i >= total) return;
+  const int p = int(i % HW);
+  const int c3 = int((i / HW) % (3 * C));
+  const int b = int(i / (size_t(HW) * 3 * C));
+  const int blk = c3 / C, c = c3 % C;
+  const float* wt = sc.w[blk];
+  const float bt = kt > 0 ? sc.b[blk][c] : 0.0f;
+  float hist[kMaxShortConv];
+#pragma unroll
+  for (int j = 0; j < kMaxShortConv; ++j) hist[j] = 0.0f;
+  for (int t = 0; t < Tn; ++t) {
+    const size_t fr = size_t(b) * Tn + t;
+    const size_t idx = (fr * 3 * C + c3) * HW + p;
+    float v = ld_f(qkv, idx);
+    if (kt > 0) {
+      // hist[j] = x_{t - kt + 1 + j} for j < kt - 1; the new input is j = kt - 1
+      float o = fmaf(wt[(kt - 1) * C + c], v, bt);
+#pragma unroll
+      for (int j = 0; j < kMaxShortConv - 1; ++j)
+        if (j < kt - 1) o = fmaf(wt[j * C + c], hist[j], o);
+#pragma unroll
+      for (int j = 0; j < kMaxShortConv - 2; ++j)
+        if (j < kt - 2) hist[j] = hist[j + 1];
+      if (kt >= 2) hist[kt - 2] = v;
+      v = o / (1.0f + expf(-o));
+    }
+    if (blk > 0 && gate_mode != 0) {
+      float g;
+      if (gate_mode == 1) {
+        const float2 gg = static_cast<const float2*>(gates)[fr * HW + p];
+        g = blk == 1 ? gg.x : gg.y;
+      } else if (gate_mode == 2) {
+        const float2 gg = static_cast<const float2*>(gates)[fr];
+        g = blk == 1 ? gg.x : gg.y;
+      } else {
+        g = static_cast<const float*>(gates)[(fr * 2 * C + size_t(blk - 1) * C + c) * HW + p];
+      }
+      v *= g;
+    }
+    st_f(qkv, idx, v);
+  }
+}
+
+hipError_t launch_gdn_qkv_post(void* qkv, int dtype, int B, int T, int C, int HW, int kt, const GdnShortConv& sc,
+                               int gate_mode, const void* gates, hipStream_t s) {
+  if (kt > kMaxShortConv) return hipErrorInvalidValue;
+  const long long total = (long long)B * 3 * C * HW;
+  const unsigned blocks = unsigned((total + 255) / 256);
+  if (dtype == 0)
+    hipLaunchKernelGGL(gdn_qkv_post<float>, dim3(blocks), dim3(256), 0, s, static_cast<float*>(qkv), T, C, HW, kt, sc,
+                       gate_mode, gates, total);
+  else
+    hipLaunchKernelGGL(gdn_qkv_post<uint16_t>, dim3(blocks), dim3(256), 0, s, static_cast<uint16_t*>(qkv), T, C, HW,
+                       kt, sc, gate_mode, gates, total);
+  return hipGetLastError();
+}
+
+}  // namespace cssm

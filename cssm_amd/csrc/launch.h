@@ -35,11 +35,52 @@ hipError_t launch_proj_in(const void* X, int in_dtype, int M, int K, int N, cons
                           hipStream_t s);
 hipError_t launch_proj_out(const void* Y, int in_dtype, int M, int K, int N, const float* W, const float* b, int HW,
                            void* out, int out_dtype, hipStream_t s);
+// single plane-major output (NH = N) or a split at channel NH; act 0 / 1 SiLU / 2 sigmoid
+hipError_t launch_proj_planes(const void* X, int in_dtype, int M, int K, int N, const float* W, const float* b,
+                              int HW, void* out_lo, void* out_hi, int out_dtype, int act_lo, int act_hi,
+                              float* partial, int NH, hipStream_t s);
+// output projection of plane-major Y with the per-pixel channel norm and gate G fused in front
+hipError_t launch_proj_out_norm_gate(const void* Y, const void* G, int in_dtype, int M, int K, int N, int norm,
+                                     const float* nscale, const float* nshift, const float* W, const float* b, int HW,
+                                     void* out, int out_dtype, hipStream_t s);
 hipError_t launch_ctx_reduce(const float* partial, int F, int tiles_per_frame, int C, float inv_hw, float* ctx,
                              hipStream_t s);
 
 hipError_t launch_short_conv(const void* x, int in_dtype, int B, int T, int C, int H, int W, int ks, const float* ws,
                              const float* bs, int kt, const float* wt, const float* bt, void* u, int out_dtype,
                              float* ctx, hipStream_t s);
+
+// ---- GatedDeltaNetCSSM
+// gate weights: index 0 alpha, 1 beta, 2 B_k, 3 B_v; kind 0 dense, 1 factored, 2 channel, 3 scalar.
+// kd/bd: dense / channel / scalar kernel and bias, or the factored row (_h) pair; kw/bw: factored column (_w).
+// kd[g] == nullptr skips gate g.
+struct GdnGateWeights {
+  int kind;
+  const float* kd[4];
+  const float* bd[4];
+  const float* kw[4];
+  const float* bw[4];
+};
+// causal short convolutions of the q / k / v blocks: kernel (kt, 1, C), bias (C)
+struct GdnShortConv {
+  const float* w[3];
+  const float* b[3];
+};
+
+hipError_t launch_rfft2(const void* x, int dtype, long long P, int H, int W, float2* spec, float* norms,
+                        hipStream_t s);
+hipError_t launch_irfft2(const float2* spec, long long P, int H, int W, void* y, int dtype, hipStream_t s);
+int fft_planes_min_group(int H, int W);
+hipError_t launch_gdn_scan_bins(const float2* spec, const float* norms, const float2* ab, long long ab_frame,
+                                int ab_head, int ab_bin, const float2* what, int B, int T, int C, int H, int W,
+                                int dk, float2* ohat, hipStream_t s);
+hipError_t launch_frame_mean(const void* x, int dtype, int F, int HW, int C, float* out, hipStream_t s);
+hipError_t launch_gdn_gates(const float* ctx, int B, int T, int C, int H, int W, int nh, const GdnGateWeights& w,
+                            int temporal, float rope_base, const float* ttable, float2* ab, float2* bkv,
+                            hipStream_t s);
+hipError_t launch_depthwise_conv(const void* x, int dtype, int F, int H, int W, int C, int ks, const float* kw,
+                                 const float* bias, void* y, int out_dtype, hipStream_t s);
+hipError_t launch_gdn_qkv_post(void* qkv, int dtype, int B, int T, int C, int HW, int kt, const GdnShortConv& sc,
+                               int gate_mode, const void* gates, hipStream_t s);
 
 }  // namespace cssm

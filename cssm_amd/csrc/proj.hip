@@ -30,6 +30,12 @@ __device__ __forceinline__ void st_el(uint16_t* p, size_t i, float v) {
   }
 }
 __device__ __forceinline__ float silu_acc(float x) { return x / (1.0f + expf(-x)); }
+// epilogue activation: 0 identity, 1 SiLU, 2 sigmoid
+__device__ __forceinline__ float act_acc(float x, int act) {
+  if (act == 1) return silu_acc(x);
+  if (act == 2) return 1.0f / (1.0f + expf(-x));
+  return x;
+}
 // 4 consecutive elements at a 4-element-aligned index
 __device__ __forceinline__ float4 ld4(const float* p, size_t i) { return *reinterpret_cast<const float4*>(p + i); }
 __device__ __forceinline__ float4 ld4(const uint16_t* p, size_t i) {
@@ -58,8 +64,9 @@ struct ProjTile {
 };
 
 // ---------------------------------------------------------------------------
-// proj_in: out_lo[f][c][p] = act_lo(sum_k X[f*HW+p][k] W[k][c] + b[c]),   c < N/2
-//          out_hi[f][c][p] = act_hi(... c + N/2 ...)
+// proj_in: out_lo[f][c][p] = act_lo(sum_k X[f*HW+p][k] W[k][c] + b[c]),   c < NH
+//          out_hi[f][c][p] = act_hi(... c + NH ...),                      NH <= c < N
+// (NH = N/2 for the in_proj split; NH = N writes one plane-major tensor)
 // partial (optional): partial[tile][c] = sum over the tile's rows of out_lo
 // (requires HW % TM == 0 so a tile lies in one frame).
 // ---------------------------------------------------------------------------
@@ -67,14 +74,14 @@ template <int TM, int TN, int WMW, int WNW, class TI, class TO>
 __global__ void __launch_bounds__(64 * WMW * WNW)
 proj_in_kernel(const TI* __restrict__ X, int M, int K, int N, const float* __restrict__ Wt,
                const float* __restrict__ bias, int HW, TO* __restrict__ out_lo, TO* __restrict__ out_hi,
-               int act_lo, int act_hi, float* __restrict__ partial) {
+               int act_lo, int act_hi, float* __restrict__ partial, int NH) {
   using P = ProjTile<TM, TN, WMW, WNW>;
   __shared__ float As[TM * P::AP];
   __shared__ float Bs[P::KC * P::BP];
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int wm = wave / WNW, wn = wave % WNW;
   const int m0 = blockIdx.x * TM, n0 = blockIdx.y * TN;
-  const int NH = N / 2;
+  const int NL = N - NH;   // channels of out_hi
 
   floatx4 acc[P::MT][P::NTL];
 #pragma unroll
@@ -122,6 +129,7 @@ proj_in_kernel(const TI* __restrict__ X, int M, int K, int N, const float* __res
     const float bv = nok ? bias[gn] : 0.0f;
     const bool lo = gn < NH;
     const int c = lo ? gn : gn - NH;
+    const int NC = lo ? NH : NL;
     TO* dst = lo ? out_lo : out_hi;
     const int act = lo ? act_lo : act_hi;
     float csum = 0.0f;
@@ -130,13 +138,10 @@ proj_in_kernel(const TI* __restrict__ X, int M, int K, int N, const float* __res
       const int gm0 = m0 + (wm * P::MT + i) * 16 + (lane >> 4) * 4;
       float v[4];
 #pragma unroll
-      for (int r = 0; r < 4; ++r) {
-        v[r] = acc[i][j][r] + bv;
-        if (act == 1) v[r] = silu_acc(v[r]);
-      }
+      for (int r = 0; r < 4; ++r) v[r] = act_acc(acc[i][j][r] + bv, act);
       if (nok && vec && gm0 + 3 < M) {
         const int f = gm0 / HW, p = gm0 % HW;
-        st4(dst, (size_t(f) * NH + c) * HW + p, v);
+        st4(dst, (size_t(f) * NC + c) * HW + p, v);
         csum += (v[0] + v[1]) + (v[2] + v[3]);
       } else if (nok) {
 #pragma unroll
@@ -144,7 +149,7 @@ proj_in_kernel(const TI* __restrict__ X, int M, int K, int N, const float* __res
           const int gm = gm0 + r;
           if (gm < M) {
             const int f = gm / HW, p = gm % HW;
-            st_el(dst, (size_t(f) * NH + c) * HW + p, v[r]);
+            st_el(dst, (size_t(f) * NC + c) * HW + p, v[r]);
             csum += v[r];
           }
         }
@@ -245,18 +250,33 @@ __global__ void ctx_reduce_kernel(const float* __restrict__ partial, int F, int 
 // the MFMAs run on the current one.  Four waves split the 128 columns (32
 // each) and keep all 128 rows, so every per-channel reduction stays in-wave.
 //   PLANE_A = false: A is channels-last (M, K) rows; true: A is plane-major
-//   (F, K, HW) (the scan output).  OUT_SPLIT = true: plane-major split output
-//   with SiLU / channel sums (proj_in); false: channels-last (M, N) (proj_out).
+//   (F, K, HW) (the scan output).  OUT_SPLIT = true: plane-major output,
+//   channels [0, NH) to out_lo and [NH, N) to out_hi, each with its
+//   activation, plus channel sums of out_lo (proj_in; NH = N writes a single
+//   tensor); false: channels-last (M, N) (proj_out).
+//   NORM (PLANE_A only): before the product, each pixel's K-vector is
+//   normalised across channels (norm 1: RMSNorm x rsqrt(mean x^2 + 1e-6) s_k;
+//   2: LayerNorm (x - mean) rsqrt(var + 1e-6) s_k + b_k; 0: none) and
+//   multiplied by the matching pixel of the plane-major gate G -- the GDN
+//   output path, cssm.py:5026-5031 and :5126, feeding output_proj :5141.
 // ---------------------------------------------------------------------------
-template <int KMAX, bool PLANE_A, bool OUT_SPLIT, int WN, class TI, class TO>
+struct NormGate {
+  const void* G;        // plane-major (F, K, HW) gate, same dtype as A
+  const float* scale;   // (K) or nullptr
+  const float* shift;   // (K) or nullptr (LayerNorm bias)
+  int kind;             // 0 none, 1 rms, 2 layer
+};
+
+template <int KMAX, bool PLANE_A, bool OUT_SPLIT, int WN, class TI, class TO, bool NORM = false>
 __global__ void __launch_bounds__(256, 2)
 proj_persist_kernel(const TI* __restrict__ A, int M, int K, int N, const float* __restrict__ Wt,
                     const float* __restrict__ bias, int HW, TO* __restrict__ out_lo, TO* __restrict__ out_hi,
-                    int act_lo, int act_hi, float* __restrict__ partial) {
+                    int act_lo, int act_hi, float* __restrict__ partial, int NH, NormGate ng) {
   // WN waves along the TN = 32 WN columns, WM = 4 / WN along the TM = 128 rows;
   // a wave owns (128 / WM) rows x 32 columns = MI x 2 MFMA tiles
   constexpr int TM = 128, TN = 32 * WN, NT = 256, WM = 4 / WN, MI = TM / WM / 16;
   static_assert(!OUT_SPLIT || WM == 1, "channel sums of proj_in need whole row tiles per wave");
+  static_assert(!NORM || (PLANE_A && !OUT_SPLIT), "the norm / gate prologue is for plane-major A");
   constexpr int AP = PLANE_A ? (TM + 16) : (KMAX + 2);   // pitch: rows of A (row-major) or k-rows (plane)
   constexpr int BP = TN + 16;
   constexpr int A_FLOATS = PLANE_A ? KMAX * AP : TM * AP;
@@ -265,11 +285,13 @@ proj_persist_kernel(const TI* __restrict__ A, int M, int K, int N, const float* 
   constexpr int PF = TM * KMAX / 4 / NT;                 // float4 of A prefetched per thread
   __shared__ __attribute__((aligned(16))) float As[AS_FLOATS];
   __shared__ float Bs[KMAX * BP];
+  __shared__ float rowsc[NORM ? 2 * TM : 1];             // per-pixel (scale, mean) of the norm
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int wm = wave / WN, wn = wave % WN;
   const int n0 = blockIdx.y * TN;
-  const int NH = N / 2;
+  const int NL = N - NH;
   const int tiles = (M + TM - 1) / TM;
+  const TI* __restrict__ Gp = static_cast<const TI*>(ng.G);
 
   for (int i = tid; i < KMAX * TN; i += NT) {
     const int kk = i / TN, c = i % TN;
@@ -277,7 +299,7 @@ proj_persist_kernel(const TI* __restrict__ A, int M, int K, int N, const float* 
     Bs[kk * BP + c] = (kk < K && gn < N) ? Wt[size_t(kk) * N + gn] : 0.0f;
   }
   // A prefetch: float4 f of the tile -> (row, k4) or (k, row4)
-  auto fetch = [&](int tile, float4* pf) {
+  auto fetch = [&](const TI* src, int tile, float4* pf) {
     const int m0 = tile * TM;
 #pragma unroll
     for (int i = 0; i < PF; ++i) {
@@ -286,13 +308,13 @@ proj_persist_kernel(const TI* __restrict__ A, int M, int K, int N, const float* 
       if (!PLANE_A) {
         const int r = f / (KMAX / 4), k4 = (f % (KMAX / 4)) * 4;
         const int gm = m0 + r;
-        if (gm < M && k4 < K) v = ld4(A, size_t(gm) * K + k4);
+        if (gm < M && k4 < K) v = ld4(src, size_t(gm) * K + k4);
       } else {
         const int kk = f / (TM / 4), r4 = (f % (TM / 4)) * 4;
         const int gm = m0 + r4;
         if (kk < K && gm < M) {
           const int fr = gm / HW, p = gm % HW;
-          v = ld4(A, (size_t(fr) * K + kk) * HW + p);
+          v = ld4(src, (size_t(fr) * K + kk) * HW + p);
         }
       }
       pf[i] = v;
@@ -312,16 +334,66 @@ proj_persist_kernel(const TI* __restrict__ A, int M, int K, int N, const float* 
       }
     }
   };
+  // NORM: per-pixel statistics over the K channels of the staged tile, then
+  // A[k][r] <- norm(A)[k][r] * G[k][r] in place (G from the prefetch registers)
+  auto norm_gate = [&](const float4* pg) {
+    if (tid < TM) {
+      float s1 = 0.f, s2 = 0.f;
+      for (int kk = 0; kk < K; ++kk) {
+        const float v = As[kk * AP + tid];
+        s1 += v;
+        s2 = fmaf(v, v, s2);
+      }
+      const float inv_k = 1.0f / float(K);
+      float mean = 0.f, sc = 1.f;
+      if (ng.kind == 1) {
+        sc = rsqrtf(s2 * inv_k + 1e-6f);
+      } else if (ng.kind == 2) {
+        mean = s1 * inv_k;
+        sc = rsqrtf(fmaxf(s2 * inv_k - mean * mean, 0.f) + 1e-6f);
+      }
+      rowsc[2 * tid] = sc;
+      rowsc[2 * tid + 1] = mean;
+    }
+    __syncthreads();
+#pragma unroll
+    for (int i = 0; i < PF; ++i) {
+      const int f = i * NT + tid;
+      const int kk = f / (TM / 4), r4 = (f % (TM / 4)) * 4;
+      if (kk >= K) continue;
+      float4 v = *reinterpret_cast<const float4*>(&As[kk * AP + r4]);
+      const float sk = ng.scale ? ng.scale[kk] : 1.f, bk = ng.shift ? ng.shift[kk] : 0.f;
+      float* e = &v.x;
+      const float* g = &pg[i].x;
+#pragma unroll
+      for (int q = 0; q < 4; ++q) {
+        const float sc = rowsc[2 * (r4 + q)], mu = rowsc[2 * (r4 + q) + 1];
+        e[q] = (ng.kind == 0 ? e[q] : fmaf((e[q] - mu) * sc, sk, bk)) * g[q];
+      }
+      *reinterpret_cast<float4*>(&As[kk * AP + r4]) = v;
+    }
+  };
 
   float4 pf[PF];
+  float4 pg[NORM ? PF : 1];
   int tile = blockIdx.x;
-  if (tile < tiles) fetch(tile, pf);
+  if (tile < tiles) {
+    fetch(A, tile, pf);
+    if (NORM) fetch(Gp, tile, pg);
+  }
   for (; tile < tiles; tile += gridDim.x) {
     __syncthreads();            // previous tile is done with As (and Bs is staged)
     stash(pf);
     __syncthreads();
+    if constexpr (NORM) {
+      norm_gate(pg);
+      __syncthreads();
+    }
     const int next = tile + gridDim.x;
-    if (next < tiles) fetch(next, pf);
+    if (next < tiles) {
+      fetch(A, next, pf);
+      if (NORM) fetch(Gp, next, pg);
+    }
 
     floatx4 acc[MI][2];
 #pragma unroll
@@ -354,6 +426,7 @@ proj_persist_kernel(const TI* __restrict__ A, int M, int K, int N, const float* 
         const float bv = nok ? bias[gn] : 0.0f;
         const bool lo = gn < NH;
         const int c = lo ? gn : gn - NH;
+        const int NC = lo ? NH : NL;
         TO* dst = lo ? out_lo : out_hi;
         const int act = lo ? act_lo : act_hi;
         float csum = 0.0f;
@@ -365,10 +438,11 @@ proj_persist_kernel(const TI* __restrict__ A, int M, int K, int N, const float* 
           for (int r = 0; r < 4; ++r) {
             v[r] = acc[i][j][r] + bv;
             if (act == 1) v[r] = v[r] * __builtin_amdgcn_rcpf(1.0f + __expf(-v[r]));
+            else if (act == 2) v[r] = __builtin_amdgcn_rcpf(1.0f + __expf(-v[r]));
           }
           if (nok && gm0 + 3 < M && (HW % 4) == 0) {
             const int fr = gm0 / HW, p = gm0 % HW;
-            st4(dst, (size_t(fr) * NH + c) * HW + p, v);
+            st4(dst, (size_t(fr) * NC + c) * HW + p, v);
             csum += (v[0] + v[1]) + (v[2] + v[3]);
           } else if (nok) {
 #pragma unroll
@@ -376,7 +450,7 @@ proj_persist_kernel(const TI* __restrict__ A, int M, int K, int N, const float* 
               const int gm = gm0 + r;
               if (gm < M) {
                 const int fr = gm / HW, p = gm % HW;
-                st_el(dst, (size_t(fr) * NH + c) * HW + p, v[r]);
+                st_el(dst, (size_t(fr) * NC + c) * HW + p, v[r]);
                 csum += v[r];
               }
             }
@@ -438,60 +512,72 @@ int proj_in_tile_rows(int K) { return K <= 128 ? kPersistTM : kProjTM; }
 
 template <class TI, class TO>
 static void launch_in(const void* X, int M, int K, int N, const float* W, const float* b, int HW, void* lo, void* hi,
-                      int act_lo, int act_hi, float* partial, hipStream_t s) {
+                      int act_lo, int act_hi, float* partial, int NH, hipStream_t s) {
   const dim3 grid((M + kProjTM - 1) / kProjTM, (N + 127) / 128);
   hipLaunchKernelGGL((proj_in_kernel<kProjTM, 128, 1, 4, TI, TO>), grid, dim3(256), 0, s, static_cast<const TI*>(X), M,
-                     K, N, W, b, HW, static_cast<TO*>(lo), static_cast<TO*>(hi), act_lo, act_hi, partial);
+                     K, N, W, b, HW, static_cast<TO*>(lo), static_cast<TO*>(hi), act_lo, act_hi, partial, NH);
 }
 
-template <int KMAX, bool PLANE_A, bool OUT_SPLIT, class TI, class TO>
+template <int KMAX, bool PLANE_A, bool OUT_SPLIT, bool NORM, class TI, class TO>
 static void launch_persist(const void* A, int M, int K, int N, const float* W, const float* b, int HW, void* lo,
-                           void* hi, int act_lo, int act_hi, float* partial, hipStream_t s) {
+                           void* hi, int act_lo, int act_hi, float* partial, int NH, const NormGate& ng,
+                           hipStream_t s) {
   const int tiles = (M + kPersistTM - 1) / kPersistTM;
   // narrow outputs (N <= 64) split the rows between wave pairs instead of idling half the waves
   if constexpr (!OUT_SPLIT) {
     if (N <= 64) {
       const dim3 grid(unsigned(persistent_grid(tiles)), unsigned((N + 63) / 64));
-      hipLaunchKernelGGL((proj_persist_kernel<KMAX, PLANE_A, OUT_SPLIT, 2, TI, TO>), grid, dim3(256), 0, s,
+      hipLaunchKernelGGL((proj_persist_kernel<KMAX, PLANE_A, OUT_SPLIT, 2, TI, TO, NORM>), grid, dim3(256), 0, s,
                          static_cast<const TI*>(A), M, K, N, W, b, HW, static_cast<TO*>(lo), static_cast<TO*>(hi),
-                         act_lo, act_hi, partial);
+                         act_lo, act_hi, partial, NH, ng);
       return;
     }
   }
   const dim3 grid(unsigned(persistent_grid(tiles)), unsigned((N + 127) / 128));
-  hipLaunchKernelGGL((proj_persist_kernel<KMAX, PLANE_A, OUT_SPLIT, 4, TI, TO>), grid, dim3(256), 0, s,
+  hipLaunchKernelGGL((proj_persist_kernel<KMAX, PLANE_A, OUT_SPLIT, 4, TI, TO, NORM>), grid, dim3(256), 0, s,
                      static_cast<const TI*>(A), M, K, N, W, b, HW, static_cast<TO*>(lo), static_cast<TO*>(hi),
-                     act_lo, act_hi, partial);
+                     act_lo, act_hi, partial, NH, ng);
 }
 
-template <bool PLANE_A, bool OUT_SPLIT, class TI, class TO>
+template <bool PLANE_A, bool OUT_SPLIT, bool NORM, class TI, class TO>
 static bool try_persist(const void* A, int M, int K, int N, const float* W, const float* b, int HW, void* lo,
-                        void* hi, int act_lo, int act_hi, float* partial, hipStream_t s) {
+                        void* hi, int act_lo, int act_hi, float* partial, int NH, const NormGate& ng, hipStream_t s) {
   if (K % 4 != 0 || K > 128) return false;
-  if (K <= 64) launch_persist<64, PLANE_A, OUT_SPLIT, TI, TO>(A, M, K, N, W, b, HW, lo, hi, act_lo, act_hi, partial, s);
-  else launch_persist<128, PLANE_A, OUT_SPLIT, TI, TO>(A, M, K, N, W, b, HW, lo, hi, act_lo, act_hi, partial, s);
+  if (K <= 64)
+    launch_persist<64, PLANE_A, OUT_SPLIT, NORM, TI, TO>(A, M, K, N, W, b, HW, lo, hi, act_lo, act_hi, partial, NH, ng, s);
+  else
+    launch_persist<128, PLANE_A, OUT_SPLIT, NORM, TI, TO>(A, M, K, N, W, b, HW, lo, hi, act_lo, act_hi, partial, NH, ng, s);
   return true;
+}
+
+// plane-major output(s) from channels-last X: channels [0, NH) -> lo, [NH, N) -> hi
+hipError_t launch_proj_planes(const void* X, int in_dtype, int M, int K, int N, const float* W, const float* b,
+                              int HW, void* out_lo, void* out_hi, int out_dtype, int act_lo, int act_hi,
+                              float* partial, int NH, hipStream_t s) {
+  const NormGate ng{nullptr, nullptr, nullptr, 0};
+  if (K <= 128 && K % 4 == 0) {
+    if (in_dtype == 0 && out_dtype == 0)
+      try_persist<false, true, false, float, float>(X, M, K, N, W, b, HW, out_lo, out_hi, act_lo, act_hi, partial, NH, ng, s);
+    else if (in_dtype == 0)
+      try_persist<false, true, false, float, uint16_t>(X, M, K, N, W, b, HW, out_lo, out_hi, act_lo, act_hi, partial, NH, ng, s);
+    else if (out_dtype == 0)
+      try_persist<false, true, false, uint16_t, float>(X, M, K, N, W, b, HW, out_lo, out_hi, act_lo, act_hi, partial, NH, ng, s);
+    else
+      try_persist<false, true, false, uint16_t, uint16_t>(X, M, K, N, W, b, HW, out_lo, out_hi, act_lo, act_hi, partial, NH, ng, s);
+    return hipGetLastError();
+  }
+  if (in_dtype == 0 && out_dtype == 0) launch_in<float, float>(X, M, K, N, W, b, HW, out_lo, out_hi, act_lo, act_hi, partial, NH, s);
+  else if (in_dtype == 0) launch_in<float, uint16_t>(X, M, K, N, W, b, HW, out_lo, out_hi, act_lo, act_hi, partial, NH, s);
+  else if (out_dtype == 0) launch_in<uint16_t, float>(X, M, K, N, W, b, HW, out_lo, out_hi, act_lo, act_hi, partial, NH, s);
+  else launch_in<uint16_t, uint16_t>(X, M, K, N, W, b, HW, out_lo, out_hi, act_lo, act_hi, partial, NH, s);
+  return hipGetLastError();
 }
 
 hipError_t launch_proj_in(const void* X, int in_dtype, int M, int K, int N, const float* W, const float* b, int HW,
                           void* out_lo, void* out_hi, int out_dtype, int act_lo, int act_hi, float* partial,
                           hipStream_t s) {
-  if (K <= 128 && K % 4 == 0) {
-    if (in_dtype == 0 && out_dtype == 0)
-      try_persist<false, true, float, float>(X, M, K, N, W, b, HW, out_lo, out_hi, act_lo, act_hi, partial, s);
-    else if (in_dtype == 0)
-      try_persist<false, true, float, uint16_t>(X, M, K, N, W, b, HW, out_lo, out_hi, act_lo, act_hi, partial, s);
-    else if (out_dtype == 0)
-      try_persist<false, true, uint16_t, float>(X, M, K, N, W, b, HW, out_lo, out_hi, act_lo, act_hi, partial, s);
-    else
-      try_persist<false, true, uint16_t, uint16_t>(X, M, K, N, W, b, HW, out_lo, out_hi, act_lo, act_hi, partial, s);
-    return hipGetLastError();
-  }
-  if (in_dtype == 0 && out_dtype == 0) launch_in<float, float>(X, M, K, N, W, b, HW, out_lo, out_hi, act_lo, act_hi, partial, s);
-  else if (in_dtype == 0) launch_in<float, uint16_t>(X, M, K, N, W, b, HW, out_lo, out_hi, act_lo, act_hi, partial, s);
-  else if (out_dtype == 0) launch_in<uint16_t, float>(X, M, K, N, W, b, HW, out_lo, out_hi, act_lo, act_hi, partial, s);
-  else launch_in<uint16_t, uint16_t>(X, M, K, N, W, b, HW, out_lo, out_hi, act_lo, act_hi, partial, s);
-  return hipGetLastError();
+  return launch_proj_planes(X, in_dtype, M, K, N, W, b, HW, out_lo, out_hi, out_dtype, act_lo, act_hi, partial,
+                            N / 2, s);
 }
 
 template <class TI, class TO>
@@ -510,21 +596,40 @@ static void launch_out(const void* Y, int M, int K, int N, const float* W, const
 
 hipError_t launch_proj_out(const void* Y, int in_dtype, int M, int K, int N, const float* W, const float* b, int HW,
                            void* out, int out_dtype, hipStream_t s) {
+  const NormGate ng{nullptr, nullptr, nullptr, 0};
   if (K <= 128 && K % 4 == 0 && HW % 4 == 0) {
     if (in_dtype == 0 && out_dtype == 0)
-      try_persist<true, false, float, float>(Y, M, K, N, W, b, HW, out, nullptr, 0, 0, nullptr, s);
+      try_persist<true, false, false, float, float>(Y, M, K, N, W, b, HW, out, nullptr, 0, 0, nullptr, N, ng, s);
     else if (in_dtype == 0)
-      try_persist<true, false, float, uint16_t>(Y, M, K, N, W, b, HW, out, nullptr, 0, 0, nullptr, s);
+      try_persist<true, false, false, float, uint16_t>(Y, M, K, N, W, b, HW, out, nullptr, 0, 0, nullptr, N, ng, s);
     else if (out_dtype == 0)
-      try_persist<true, false, uint16_t, float>(Y, M, K, N, W, b, HW, out, nullptr, 0, 0, nullptr, s);
+      try_persist<true, false, false, uint16_t, float>(Y, M, K, N, W, b, HW, out, nullptr, 0, 0, nullptr, N, ng, s);
     else
-      try_persist<true, false, uint16_t, uint16_t>(Y, M, K, N, W, b, HW, out, nullptr, 0, 0, nullptr, s);
+      try_persist<true, false, false, uint16_t, uint16_t>(Y, M, K, N, W, b, HW, out, nullptr, 0, 0, nullptr, N, ng, s);
     return hipGetLastError();
   }
   if (in_dtype == 0 && out_dtype == 0) launch_out<float, float>(Y, M, K, N, W, b, HW, out, s);
   else if (in_dtype == 0) launch_out<float, uint16_t>(Y, M, K, N, W, b, HW, out, s);
   else if (out_dtype == 0) launch_out<uint16_t, float>(Y, M, K, N, W, b, HW, out, s);
   else launch_out<uint16_t, uint16_t>(Y, M, K, N, W, b, HW, out, s);
+  return hipGetLastError();
+}
+
+// output projection with the per-pixel channel norm and the gate fused in front
+// (persistent kernel only: K <= 128, K % 4 == 0, HW % 4 == 0; else invalid value)
+hipError_t launch_proj_out_norm_gate(const void* Y, const void* G, int in_dtype, int M, int K, int N, int norm,
+                                     const float* nscale, const float* nshift, const float* W, const float* b, int HW,
+                                     void* out, int out_dtype, hipStream_t s) {
+  if (!(K <= 128 && K % 4 == 0 && HW % 4 == 0)) return hipErrorInvalidValue;
+  const NormGate ng{G, nscale, nshift, norm};
+  if (in_dtype == 0 && out_dtype == 0)
+    try_persist<true, false, true, float, float>(Y, M, K, N, W, b, HW, out, nullptr, 0, 0, nullptr, N, ng, s);
+  else if (in_dtype == 0)
+    try_persist<true, false, true, float, uint16_t>(Y, M, K, N, W, b, HW, out, nullptr, 0, 0, nullptr, N, ng, s);
+  else if (out_dtype == 0)
+    try_persist<true, false, true, uint16_t, float>(Y, M, K, N, W, b, HW, out, nullptr, 0, 0, nullptr, N, ng, s);
+  else
+    try_persist<true, false, true, uint16_t, uint16_t>(Y, M, K, N, W, b, HW, out, nullptr, 0, 0, nullptr, N, ng, s);
   return hipGetLastError();
 }
 

@@ -5,6 +5,7 @@ stream.  Nothing here computes on the CPU and there is no fallback path.
 """
 from __future__ import annotations
 
+import ctypes
 from typing import Dict, Optional
 
 import torch
@@ -207,3 +208,205 @@ def short_conv(x: torch.Tensor, spatial: Optional[Dict[str, torch.Tensor]],
     _lib.call("cssm_short_conv", x.data_ptr(), _DTYPES[x.dtype], B, T, C, H, W, ks, ws, bs, kt, wt, bt,
               u.data_ptr(), _DTYPES[od], ctx.data_ptr() if ctx is not None else None, _stream())
     return u, ctx
+
+
+# ----------------------------------------------------------------- GDN cell
+
+_GDN_GATE_TYPES = {"dense": _lib.GDN_GATE_DENSE, "factored": _lib.GDN_GATE_FACTORED,
+                   "channel": _lib.GDN_GATE_CHANNEL, "scalar": _lib.GDN_GATE_SCALAR}
+_ACTS = {"identity": _lib.ACT_IDENTITY, "silu": _lib.ACT_SILU, "sigmoid": _lib.ACT_SIGMOID}
+_NORMS = {"none": _lib.NORM_NONE, "rms": _lib.NORM_RMS, "layer": _lib.NORM_LAYER}
+
+
+def proj_planes(x: torch.Tensor, kernel: torch.Tensor, bias: torch.Tensor, frames: int, hw: int,
+                act: str = "identity", out_dtype: Optional[torch.dtype] = None) -> torch.Tensor:
+    """Dense(N) of channels-last rows into one plane-major (frames, N, hw) tensor
+    (qkv_proj / gate_proj / channel input gates, cssm.py:4753-4859)."""
+    _dev(x, "x")
+    if x.dtype not in _DTYPES:
+        raise ValueError(f"unsupported dtype {x.dtype}")
+    K = x.shape[-1]
+    if x.numel() != frames * hw * K:
+        raise ValueError("x does not hold frames * hw rows")
+    _dev(kernel, "kernel", torch.float32)
+    _dev(bias, "bias", torch.float32)
+    Kk, N = kernel.shape
+    if Kk != K or bias.shape != (N,):
+        raise ValueError(f"kernel {tuple(kernel.shape)} / bias {tuple(bias.shape)} do not match K={K}")
+    od = out_dtype or x.dtype
+    out = torch.empty((frames, N, hw), dtype=od, device=x.device)
+    _lib.call("cssm_proj_planes", x.data_ptr(), _DTYPES[x.dtype], frames, hw, K, N, kernel.data_ptr(),
+              bias.data_ptr(), out.data_ptr(), _DTYPES[od], _ACTS[act], _stream())
+    return out
+
+
+def frame_mean(x: torch.Tensor) -> torch.Tensor:
+    """(B, T, H, W, C) channels-last -> (B, T, C) spatial mean (cssm.py:4785)."""
+    _dev(x, "x")
+    if x.dtype not in _DTYPES:
+        raise ValueError(f"unsupported dtype {x.dtype}")
+    *lead, H, W, C = x.shape
+    F = int(torch.tensor(lead).prod()) if lead else 1
+    out = torch.empty((*lead, C), dtype=torch.float32, device=x.device)
+    _lib.call("cssm_frame_mean", x.data_ptr(), _DTYPES[x.dtype], F, H * W, C, out.data_ptr(), _stream())
+    return out
+
+
+def depthwise_conv(x: torch.Tensor, kernel: torch.Tensor, bias: torch.Tensor,
+                   out_dtype: Optional[torch.dtype] = None) -> torch.Tensor:
+    """Depthwise ks x ks SAME conv of channels-last (..., H, W, C) frames (qkv_dw, cssm.py:4744-4750)."""
+    _dev(x, "x")
+    *lead, H, W, C = x.shape
+    F = 1
+    for d in lead:
+        F *= d
+    _dev(kernel, "kernel", torch.float32)
+    _dev(bias, "bias", torch.float32)
+    ks = kernel.shape[0]
+    if tuple(kernel.shape) != (ks, ks, 1, C) or bias.shape != (C,):
+        raise ValueError(f"depthwise kernel {tuple(kernel.shape)} does not match C={C}")
+    od = out_dtype or x.dtype
+    out = torch.empty(x.shape, dtype=od, device=x.device)
+    _lib.call("cssm_depthwise_conv", x.data_ptr(), _DTYPES[x.dtype], F, H, W, C, ks, kernel.data_ptr(),
+              bias.data_ptr(), out.data_ptr(), _DTYPES[od], _stream())
+    return out
+
+
+def gdn_gate_params_struct(p: Dict, gate_type: str, input_gates: bool) -> _lib.GdnGateParams:
+    """cssm_gdn_gate_params from the Flax-named parameter dict (alpha, beta, B_k, B_v)."""
+    s = _lib.GdnGateParams()
+    s.gate_type = _GDN_GATE_TYPES[gate_type]
+    names = ["alpha", "beta"] + (["B_k", "B_v"] if input_gates and gate_type != "channel" else [])
+    for i, name in enumerate(names):
+        if gate_type == "factored":
+            ph, pw = p[f"{name}_h"], p[f"{name}_w"]
+            s.kernel[i] = _dev(ph["kernel"], f"{name}_h.kernel", torch.float32).data_ptr()
+            s.bias[i] = _dev(ph["bias"], f"{name}_h.bias", torch.float32).data_ptr()
+            s.kernel_w[i] = _dev(pw["kernel"], f"{name}_w.kernel", torch.float32).data_ptr()
+            s.bias_w[i] = _dev(pw["bias"], f"{name}_w.bias", torch.float32).data_ptr()
+        else:
+            s.kernel[i] = _dev(p[name]["kernel"], f"{name}.kernel", torch.float32).data_ptr()
+            s.bias[i] = _dev(p[name]["bias"], f"{name}.bias", torch.float32).data_ptr()
+    return s
+
+
+def gdn_gates(ctx: torch.Tensor, params: Dict, H: int, W: int, delta_key_dim: int, gate_type: str,
+              input_gates: bool, temporal: str = "sinusoid", rope_base: float = 10000.0,
+              temporal_table: Optional[torch.Tensor] = None):
+    """(ab, bkv): alpha/beta pairs (B, T, n_ab, 2) and B_k/B_v pairs (B, T, n_kv, 2) or None
+    (cssm.py:4785-4869).  temporal in {'none', 'sinusoid', 'learned'}."""
+    _dev(ctx, "ctx", torch.float32)
+    B, T, C = ctx.shape
+    Wf = W // 2 + 1
+    n_ab = {"dense": H * Wf, "factored": H * Wf, "channel": C // delta_key_dim, "scalar": 1}[gate_type]
+    ab = torch.empty((B, T, n_ab, 2), dtype=torch.float32, device=ctx.device)
+    bkv = None
+    if input_gates and gate_type != "channel":
+        n_kv = 1 if gate_type == "scalar" else H * W
+        bkv = torch.empty((B, T, n_kv, 2), dtype=torch.float32, device=ctx.device)
+    s = gdn_gate_params_struct(params, gate_type, input_gates)
+    tmode = {"none": 0, "sinusoid": 1, "learned": 2}[temporal]
+    tt = None
+    if tmode == 2:
+        tt = _dev(temporal_table, "temporal_table", torch.float32).data_ptr()
+    _lib.call("cssm_gdn_gates", ctx.data_ptr(), B, T, C, H, W, delta_key_dim, s, tmode, float(rope_base), tt,
+              ab.data_ptr(), bkv.data_ptr() if bkv is not None else None, _stream())
+    return ab, bkv
+
+
+def gdn_qkv_post(qkv: torch.Tensor, convs, gate_mode: int = 0, gates: Optional[torch.Tensor] = None) -> torch.Tensor:
+    """In place on plane-major qkv (B, T, 3C, H, W): causal short conv + SiLU (convs = [q, k, v]
+    dicts or None) and the input gates on k, v (cssm.py:4763-4848)."""
+    _dev(qkv, "qkv")
+    B, T, C3, H, W = qkv.shape
+    C = C3 // 3
+    kt = 0
+    kern = bias = None
+    if convs is not None:
+        kt = convs[0]["kernel"].shape[0]
+        ks = [_dev(c["kernel"], "short_conv.kernel", torch.float32) for c in convs]
+        bs = [_dev(c["bias"], "short_conv.bias", torch.float32) for c in convs]
+        kern = (ctypes.c_void_p * 3)(*[k.data_ptr() for k in ks])
+        bias = (ctypes.c_void_p * 3)(*[b.data_ptr() for b in bs])
+    gp = None
+    if gate_mode:
+        _dev(gates, "gates", torch.float32)
+        gp = gates.data_ptr()
+    _lib.call("cssm_gdn_qkv_post", qkv.data_ptr(), _DTYPES[qkv.dtype], B, T, C, H, W, kt, kern, bias, gate_mode,
+              gp, _stream())
+    return qkv
+
+
+def rfft2(x: torch.Tensor, want_norms: bool = False):
+    """Batched rfft2 of (..., H, W) real planes -> (spec (..., H, W//2+1) complex64, norms (...) or None)."""
+    _dev(x, "x")
+    *lead, H, W = x.shape
+    P = 1
+    for d in lead:
+        P *= d
+    spec = torch.empty((*lead, H, W // 2 + 1), dtype=torch.complex64, device=x.device)
+    norms = torch.empty(tuple(lead), dtype=torch.float32, device=x.device) if want_norms else None
+    _lib.call("cssm_rfft2", x.data_ptr(), _DTYPES[x.dtype], P, H, W, spec.data_ptr(),
+              norms.data_ptr() if norms is not None else None, _stream())
+    return spec, norms
+
+
+def irfft2(spec: torch.Tensor, W: int, out_dtype: torch.dtype = torch.float32) -> torch.Tensor:
+    """Batched irfft2(s=(H, W)) of (..., H, W//2+1) complex64 spectra -> (..., H, W) real."""
+    _dev(spec, "spec", torch.complex64)
+    *lead, H, Wf = spec.shape
+    if Wf != W // 2 + 1:
+        raise ValueError(f"spectrum width {Wf} does not match W={W}")
+    P = 1
+    for d in lead:
+        P *= d
+    y = torch.empty((*lead, H, W), dtype=out_dtype, device=spec.device)
+    _lib.call("cssm_irfft2", spec.data_ptr(), P, H, W, y.data_ptr(), _DTYPES[out_dtype], _stream())
+    return y
+
+
+def fft_supported(H: int, W: int) -> bool:
+    return bool(_lib.load().cssm_fft_min_group(H, W))
+
+
+def gdn_scan_bins(spec: torch.Tensor, norms: Optional[torch.Tensor], ab: torch.Tensor, gate_type: str,
+                  what: torch.Tensor, delta_key_dim: int) -> torch.Tensor:
+    """Delta-rule recurrence over T per (b, head, bin) (cssm.py:4890-5000).
+
+    spec (B, T, 3C, H, Wf) complex64, norms (B, T, 3C) or None, ab from :func:`gdn_gates`,
+    what (n_h, H, Wf) complex64.  Returns ohat (B, T, C, H, Wf) complex64."""
+    _dev(spec, "spec", torch.complex64)
+    B, T, C3, H, Wf = spec.shape
+    C = C3 // 3
+    W = 2 * (Wf - 1)
+    _dev(ab, "ab", torch.float32)
+    _dev(what, "what", torch.complex64)
+    if norms is not None:
+        _dev(norms, "norms", torch.float32)
+    n_ab = ab.shape[2]
+    strides = {"dense": (n_ab, 0, 1), "factored": (n_ab, 0, 1), "channel": (n_ab, 1, 0), "scalar": (1, 0, 0)}
+    fs, hs, bs = strides[gate_type]
+    ohat = torch.empty((B, T, C, H, Wf), dtype=torch.complex64, device=spec.device)
+    _lib.call("cssm_gdn_scan_bins", spec.data_ptr(), norms.data_ptr() if norms is not None else None,
+              ab.data_ptr(), fs, hs, bs, what.data_ptr(), B, T, C, H, W, delta_key_dim, ohat.data_ptr(), _stream())
+    return ohat
+
+
+def gdn_proj_out(o: torch.Tensor, gate: torch.Tensor, norm: str, norm_scale: Optional[torch.Tensor],
+                 norm_bias: Optional[torch.Tensor], kernel: torch.Tensor, bias: torch.Tensor,
+                 out_dtype: Optional[torch.dtype] = None) -> torch.Tensor:
+    """out = (norm(o) * gate) W + b from plane-major (F, K, hw) o and gate to channels-last (F * hw, N)
+    (cssm.py:5026-5141)."""
+    _dev(o, "o")
+    _dev(gate, "gate", o.dtype)
+    F, K, hw = o.shape
+    _dev(kernel, "kernel", torch.float32)
+    _dev(bias, "bias", torch.float32)
+    N = kernel.shape[1]
+    od = out_dtype or o.dtype
+    out = torch.empty((F * hw, N), dtype=od, device=o.device)
+    ns = _dev(norm_scale, "norm_scale", torch.float32).data_ptr() if norm_scale is not None else None
+    nb = _dev(norm_bias, "norm_bias", torch.float32).data_ptr() if norm_bias is not None else None
+    _lib.call("cssm_gdn_proj_out", o.data_ptr(), gate.data_ptr(), _DTYPES[o.dtype], F, hw, K, N, _NORMS[norm], ns, nb,
+              kernel.data_ptr(), bias.data_ptr(), out.data_ptr(), _DTYPES[od], _stream())
+    return out

@@ -193,6 +193,142 @@ int cssm_short_conv(const void* x, int in_dtype, int B, int T, int C, int H, int
                     const float* ws, const float* bs, int kt, const float* wt, const float* bt,
                     void* u, int out_dtype, float* ctx, void* stream);
 
+/*
+ * Dense projection of channels-last rows into ONE plane-major tensor.
+ * Replaces the GDN projections qkv_proj (cssm.py:4753-4758, N = 3C: q, k, v
+ * blocks), gate_proj + SiLU / sigmoid (:4853-4859, N = C) and the per-pixel
+ * 1x1-conv input gates of gate_type 'channel' (:4800-4806, N = 2C, sigmoid).
+ *   x      (F * HW, K) channels-last of in_dtype
+ *   kernel (K, N) float32, bias (N)
+ *   out    (F, N, HW) plane-major of out_dtype; act 0 identity, 1 SiLU, 2 sigmoid
+ */
+int cssm_proj_planes(const void* x, int in_dtype, int F, int HW, int K, int N, const float* kernel,
+                     const float* bias, void* out, int out_dtype, int act, void* stream);
+
+/*
+ * Spatial mean of channels-last frames: out[f, c] = mean_p x[f, p, c].
+ * Replaces cssm.py:4785 (ctx = gate_input.mean(axis=(2, 3)) of the GDN cell).
+ *   x (F, HW, C) of dtype; out (F, C) float32
+ */
+int cssm_frame_mean(const void* x, int dtype, int F, int HW, int C, float* out, void* stream);
+
+/*
+ * Depthwise ks x ks SAME convolution of channels-last frames with bias.
+ * Replaces qkv_dw (cssm.py:4744-4750; Flax 'SAME' pads (ks-1)//2 before).
+ *   x (F, H, W, C) of dtype, out (F, H, W, C) of out_dtype; kernel (ks, ks, 1, C) [qkv_dw/kernel], bias (C)
+ */
+int cssm_depthwise_conv(const void* x, int dtype, int F, int H, int W, int C, int ks, const float* kernel,
+                        const float* bias, void* out, int out_dtype, void* stream);
+
+/* gate_type of GatedDeltaNetCSSM (cssm.py:4798-4842) */
+typedef enum cssm_gdn_gate_type {
+  CSSM_GDN_GATE_DENSE = 0,
+  CSSM_GDN_GATE_FACTORED = 1,
+  CSSM_GDN_GATE_CHANNEL = 2,
+  CSSM_GDN_GATE_SCALAR = 3
+} cssm_gdn_gate_type;
+
+/*
+ * Gate weights of GatedDeltaNetCSSM.  Index 0 = alpha, 1 = beta (spectral
+ * gates), 2 = B_k, 3 = B_v (spatial input gates; kernel[2] = NULL skips them).
+ *   dense    kernel[i] (C, n) [<name>/kernel], bias[i] (n): n = H*Wf (spectral), H*W (spatial)
+ *   factored kernel[i] (C, H) [<name>_h/kernel], bias[i] (H); kernel_w[i] (C, Wf or W) [<name>_w/kernel],
+ *            bias_w[i]; gate = sigmoid(row[u] + col[v])
+ *   channel  alpha / beta: kernel (C, n_h), bias (n_h); B_k / B_v are per-pixel 1x1 convolutions of x,
+ *            computed with cssm_proj_planes (act = sigmoid), so kernel[2] must be NULL here
+ *   scalar   kernel (C, 1), bias (1)
+ */
+typedef struct cssm_gdn_gate_params {
+  int gate_type; /* cssm_gdn_gate_type */
+  const float* kernel[4];
+  const float* bias[4];
+  const float* kernel_w[4];
+  const float* bias_w[4];
+} cssm_gdn_gate_params;
+
+/*
+ * Gates of GatedDeltaNetCSSM from ctx.  Replaces cssm.py:4785-4869: the
+ * temporal context encoding (apply_temporal_rope_to_context :353-383, or the
+ * learned table), _gate (:4798-4842) for B_k / B_v (:4844-4848) and alpha /
+ * beta (:4864-4865): alpha = 0.1 + 0.89 sigmoid(g), beta = sigmoid(g).
+ *   ctx       (B, T, C) float32 (cssm_frame_mean of the layer input)
+ *   temporal  0 none (position_independent_gates), 1 sinusoid table E[t] with rope_base,
+ *             2 learned table temporal_table (T, C) [temporal_embed]
+ *   ab        (B, T, n_ab, 2) float32 out (alpha, beta): n_ab = H*Wf (dense, factored), n_h (channel), 1 (scalar)
+ *   bkv       (B, T, n_kv, 2) float32 out (B_k, B_v): n_kv = H*W (dense, factored), 1 (scalar); may be NULL
+ */
+int cssm_gdn_gates(const float* ctx, int B, int T, int C, int H, int W, int delta_key_dim,
+                   const cssm_gdn_gate_params* params, int temporal, float rope_base,
+                   const float* temporal_table, float* ab, float* bkv, void* stream);
+
+/*
+ * In place on the plane-major q, k, v blocks qkv (B, T, 3C, H, W): causal
+ * depthwise short convolution over T + bias + SiLU (cssm.py:4763-4780; kt = 0
+ * skips both), then the input gates on k and v (:4844-4848).
+ *   conv_kernel[3] (kt, 1, C) [short_conv_q/k/v/kernel], conv_bias[3] (C); kt <= 8
+ *   gate_mode 0 none; 1 gates (B, T, H*W, 2) per pixel; 2 gates (B, T, 2) per frame;
+ *             3 gates (B, T, 2C, H, W) per channel and pixel (B_k then B_v)
+ */
+int cssm_gdn_qkv_post(void* qkv, int dtype, int B, int T, int C, int H, int W, int kt,
+                      const float* const* conv_kernel, const float* const* conv_bias, int gate_mode,
+                      const void* gates, void* stream);
+
+/*
+ * Batched 2-D real FFT (numpy / XLA rfft2 convention) of P planes, with the
+ * optional per-plane sum of |X|^2 over the half spectrum (the spectral L2 norm
+ * of cssm.py:4890-4897).  Replaces the rfft2 calls of cssm.py:4880-4888.
+ *   x (P, H, W) of dtype; spec (P, H, Wf) complex64 out; norms (P) float32 out or NULL
+ * Supported planes: H = W in {4, ..., 128} (powers of two), any P.  x 16-byte
+ * (f32) / 8-byte (bf16) aligned, spec 8.
+ */
+int cssm_rfft2(const void* x, int dtype, long long P, int H, int W, float* spec, float* norms, void* stream);
+
+/*
+ * Batched inverse 2-D real FFT (numpy / XLA irfft2, s = (H, W): only the
+ * Hermitian part of the v = 0 and v = W/2 columns survives).  Replaces
+ * cssm.py:5025.  spec (P, H, Wf) complex64; y (P, H, W) of dtype out.
+ */
+int cssm_irfft2(const float* spec, long long P, int H, int W, void* y, int dtype, void* stream);
+
+/* 1 if cssm_rfft2 / cssm_irfft2 have a kernel for (H, W) planes, else 0. */
+int cssm_fft_min_group(int H, int W);
+
+/*
+ * Delta-rule recurrence of GatedDeltaNetCSSM per (batch, head, frequency bin)
+ * with the d_k x d_k complex state held in registers over all T.  Replaces
+ * cssm.py:4890-5000: spectral / key-vector L2 norms, M_t and Delta_t (with
+ * to_goom's floors on every entry), the log-space matrix scan
+ * (math.py:384-411, operations.py:314-390 -- exactly the linear recurrence
+ * s_t = M_t s_{t-1} + Delta_t) and the readout o = S q.
+ *   spec   (B, T, 3C, H, Wf) complex64: rfft2 of the q, k, v blocks
+ *   norms  (B, T, 3C) from cssm_rfft2, or NULL when use_spectral_l2_norm is off
+ *   ab     (alpha, beta) pairs: pair of (b, t, head, bin) at
+ *          ((b T + t) ab_frame + head ab_head + bin ab_bin); dense / factored:
+ *          (H*Wf, 0, 1), channel: (n_h, 1, 0), scalar: (1, 0, 0)
+ *   what   (n_h, H, Wf) complex64 (cssm_spectral_kernel, goom_floor = 0)
+ *   ohat   (B, T, C, H, Wf) complex64 out; output channel head*d_k + i
+ * delta_key_dim in {1, 2, 3, 4}, C a multiple of it.
+ */
+int cssm_gdn_scan_bins(const float* spec, const float* norms, const float* ab, long long ab_frame,
+                       int ab_head, int ab_bin, const float* what, int B, int T, int C, int H, int W,
+                       int delta_key_dim, float* ohat, void* stream);
+
+/* output_norm of GatedDeltaNetCSSM */
+typedef enum cssm_norm { CSSM_NORM_NONE = 0, CSSM_NORM_RMS = 1, CSSM_NORM_LAYER = 2 } cssm_norm;
+
+/*
+ * GDN output path: per-pixel channel norm, times the gate, then the output
+ * projection.  Replaces cssm.py:5026-5031 (RMSNorm _rms_norm :49-52, or
+ * LayerNorm), :5126 (x gate_val) and :5141 (output_proj).
+ *   o, gate  (F, K, HW) plane-major of in_dtype (irfft2 output; SiLU'd gate_proj)
+ *   norm     cssm_norm; norm_scale (K) [rms_scale or output_layernorm/scale], norm_bias (K) or NULL
+ *   kernel (K, N) [output_proj/kernel], bias (N); out (F * HW, N) channels-last of out_dtype
+ * K <= 128 and K % 4 == 0, HW % 4 == 0.
+ */
+int cssm_gdn_proj_out(const void* o, const void* gate, int in_dtype, int F, int HW, int K, int N, int norm,
+                      const float* norm_scale, const float* norm_bias, const float* kernel, const float* bias,
+                      void* out, int out_dtype, void* stream);
+
 /* 1 if cssm_gated_scan_fwd has a kernel for (H, W), else 0. */
 int cssm_gated_scan_supported(int H, int W);
 

@@ -1,0 +1,314 @@
+"""GPU parity of the GatedDeltaNetCSSM (`gdn`) kernels and layer against the
+float64 oracle (oracle/cssm_oracle.py) and numpy, all through the C ABI.
+
+Bar: max|y_gpu - y_ref| / RMS(y_ref) <= 1e-4 with
+fp32 I/O, <= 5e-3 with bf16 I/O.
+"""
+import numpy as np
+import pytest
+
+from oracle import cssm_oracle as O
+from tests.gpu_util import bf16_excess_err, print_case, rel_err, to_np
+
+torch = pytest.importorskip("torch")
+pytestmark = pytest.mark.gpu
+
+TOL_F32 = 1e-4
+TOL_BF16 = 5e-3
+
+
+@pytest.fixture(scope="module")
+def mods():
+    if not torch.cuda.is_available():
+        pytest.skip("no GPU")
+    from cssm_amd import cells, spectral
+    return cells, spectral
+
+
+def _dev(a, dtype=torch.float32):
+    return torch.from_numpy(np.ascontiguousarray(a)).to("cuda", dtype)
+
+
+def _tree(p):
+    if isinstance(p, dict):
+        return {k: _tree(v) for k, v in p.items()}
+    return _dev(p)
+
+
+# ------------------------------------------------------- batched transforms
+
+@pytest.mark.parametrize("P,H", [(6, 128), (8, 64), (12, 32), (16, 16), (64, 8), (128, 4)])
+@pytest.mark.parametrize("dt", ["f32", "bf16"])
+def test_rfft2_and_norms_match_numpy(mods, P, H, dt):
+    _, S = mods
+    print_case(test="rfft2", P=P, H=H, dtype=dt)
+    rng = np.random.default_rng(P * H)
+    x = rng.standard_normal((P, H, H))
+    xd = _dev(x, torch.float32 if dt == "f32" else torch.bfloat16)
+    spec, norms = S.rfft2(xd, want_norms=True)
+    xr = to_np(xd)                                   # the (rounded) input the kernel saw
+    ref = np.fft.rfft2(xr)
+    got = spec.cpu().numpy().astype(np.complex128)
+    assert np.max(np.abs(got - ref)) / np.sqrt(np.mean(np.abs(ref) ** 2)) < 2e-6
+    assert rel_err(to_np(norms), np.sum(np.abs(ref) ** 2, axis=(1, 2))) < 2e-6
+
+
+@pytest.mark.parametrize("P,H", [(6, 128), (8, 64), (12, 32), (16, 16), (64, 8), (128, 4)])
+def test_irfft2_c2r_rule_matches_numpy(mods, P, H):
+    _, S = mods
+    print_case(test="irfft2", P=P, H=H)
+    rng = np.random.default_rng(H)
+    Wf = H // 2 + 1
+    # arbitrary (non-Hermitian) spectra: only the C2R-surviving part may reach y
+    X = rng.standard_normal((P, H, Wf)) + 1j * rng.standard_normal((P, H, Wf))
+    y = S.irfft2(_dev(X, torch.complex64), H)
+    ref = np.fft.irfft2(X.astype(np.complex64).astype(np.complex128), s=(H, H))
+    assert rel_err(to_np(y), ref) < 2e-6
+
+
+def test_rfft2_irfft2_round_trip_full_c3_plane_count(mods):
+    """Size-independent check at the C3 plane shape: irfft2(rfft2(x)) = x."""
+    _, S = mods
+    print_case(test="fft_round_trip", P=384, H=128)
+    x = torch.randn((384, 128, 128), device="cuda", generator=torch.Generator(device="cuda").manual_seed(5))
+    spec, _ = S.rfft2(x)
+    y = S.irfft2(spec, 128)
+    assert float((y - x).abs().max()) / float(x.pow(2).mean().sqrt()) < 2e-6
+
+
+# ------------------------------------------------------------ prologue ops
+
+@pytest.mark.parametrize("act", ["identity", "silu", "sigmoid"])
+def test_proj_planes(mods, act):
+    _, S = mods
+    print_case(test="proj_planes", act=act)
+    rng = np.random.default_rng(3)
+    F, HW, K, N = 3, 1024, 64, 192
+    x = rng.standard_normal((F * HW, K))
+    Wt = rng.standard_normal((K, N)) / 8
+    b = rng.standard_normal(N) * 0.1
+    out = S.proj_planes(_dev(x), _dev(Wt), _dev(b), F, HW, act=act)
+    ref = (x @ Wt + b).reshape(F, HW, N).transpose(0, 2, 1)
+    ref = {"identity": ref, "silu": O.silu(ref), "sigmoid": O.sigmoid(ref)}[act]
+    assert rel_err(to_np(out), ref) < 1e-5
+
+
+def test_frame_mean_and_depthwise_conv(mods):
+    _, S = mods
+    print_case(test="frame_mean_dwconv")
+    rng = np.random.default_rng(4)
+    x = rng.standard_normal((2, 3, 16, 12, 20))
+    m = S.frame_mean(_dev(x))
+    assert rel_err(to_np(m), x.mean(axis=(2, 3))) < 1e-6
+    for ks in (5, 3, 4):
+        p = {"kernel": rng.standard_normal((ks, ks, 1, 20)) / ks, "bias": rng.standard_normal(20) * 0.1}
+        y = S.depthwise_conv(_dev(x), _dev(p["kernel"]), _dev(p["bias"]))
+        ref = O.depthwise_conv2d_same(x.reshape(6, 16, 12, 20), p).reshape(x.shape)
+        assert rel_err(to_np(y), ref) < 1e-6, ks
+
+
+@pytest.mark.parametrize("gate_type", ["factored", "dense", "channel", "scalar"])
+def test_gdn_gates_match_oracle(mods, gate_type):
+    _, S = mods
+    print_case(test="gdn_gates", gate_type=gate_type)
+    rng = np.random.default_rng(5)
+    B, T, H, W, C, dk = 2, 3, 16, 16, 8, 2
+    cfg = O.GDNConfig(channels=C, delta_key_dim=dk, gate_type=gate_type)
+    p = O.init_params(O.gdn_param_shapes(cfg, H, W), rng)
+    ctx = rng.standard_normal((B, T, C))
+    ab, bkv = S.gdn_gates(_dev(ctx), _tree(p), H, W, dk, gate_type, True)
+    ctx_t = ctx + O.temporal_context_encoding(T, C)[None]
+    Wf = W // 2 + 1
+    al = O.gdn_gate("alpha", p, cfg, ctx_t, None, H, W, bounded=True)
+    be = O.gdn_gate("beta", p, cfg, ctx_t, None, H, W)
+    ab_np = to_np(ab)
+    n = ab_np.shape[2]
+    assert rel_err(ab_np[..., 0], np.asarray(al).reshape(B, T, n)) < 1e-5
+    assert rel_err(ab_np[..., 1], np.asarray(be).reshape(B, T, n)) < 1e-5
+    if gate_type != "channel":
+        bk = O.gdn_gate("B_k", p, cfg, ctx_t, None, H, W, spatial=True)
+        bv = O.gdn_gate("B_v", p, cfg, ctx_t, None, H, W, spatial=True)
+        m = bkv.shape[2]
+        assert rel_err(to_np(bkv)[..., 0], np.asarray(bk).reshape(B, T, m)) < 1e-5
+        assert rel_err(to_np(bkv)[..., 1], np.asarray(bv).reshape(B, T, m)) < 1e-5
+    assert n == {"factored": H * Wf, "dense": H * Wf, "channel": C // dk, "scalar": 1}[gate_type]
+
+
+@pytest.mark.parametrize("kt", [4, 0, 2])
+def test_gdn_qkv_post_matches_oracle(mods, kt):
+    _, S = mods
+    print_case(test="gdn_qkv_post", kt=kt)
+    rng = np.random.default_rng(6)
+    B, T, C, H, W = 2, 5, 6, 8, 8
+    qkv = rng.standard_normal((B, T, 3 * C, H, W))
+    convs = [{"kernel": rng.standard_normal((kt, 1, C)) / 2, "bias": rng.standard_normal(C) * 0.1}
+             for _ in range(3)] if kt else None
+    gates = 1.0 / (1.0 + np.exp(-rng.standard_normal((B, T, H * W, 2))))
+    got = S.gdn_qkv_post(_dev(qkv), [_tree(c) for c in convs] if convs else None, 1, _dev(gates))
+    cl = qkv.reshape(B, T, 3, C, H, W).transpose(0, 1, 4, 5, 2, 3)       # (B, T, H, W, 3, C)
+    outs = []
+    for i in range(3):
+        z = cl[..., i, :]
+        if convs:
+            z = O.silu(O.causal_conv_t(z, convs[i]))
+        if i > 0:
+            z = z * gates[..., i - 1].reshape(B, T, H, W, 1)
+        outs.append(z)
+    ref = np.stack(outs, axis=4).transpose(0, 1, 4, 5, 2, 3).reshape(qkv.shape)
+    assert rel_err(to_np(got), ref) < 1e-5
+
+
+# --------------------------------------------------------- spectral core
+
+CORE_CASES = [
+    # name, (B, T, H, W, C), d_k, gate_type, spectral l2 norm
+    ("factored_dk4_32", (2, 6, 32, 32, 16), 4, "factored", True),
+    ("channel_dk2_16", (2, 5, 16, 16, 8), 2, "channel", True),
+    ("dense_dk3_16", (1, 4, 16, 16, 12), 3, "dense", False),
+    ("scalar_dk1_8", (2, 3, 8, 8, 4), 1, "scalar", True),
+    ("factored_dk4_128", (1, 3, 128, 128, 8), 4, "factored", True),
+]
+
+
+@pytest.mark.parametrize("name,shape,dk,gate_type,l2", CORE_CASES, ids=[c[0] for c in CORE_CASES])
+def test_gdn_spectral_core_matches_oracle(mods, name, shape, dk, gate_type, l2):
+    """rfft2 -> gdn_scan_bins -> irfft2 against the oracle's materialised-M GOOM scan."""
+    _, S = mods
+    print_case(test="gdn_core", case=name)
+    rng = np.random.default_rng(11)
+    B, T, H, W, C = shape
+    nh, Wf = C // dk, W // 2 + 1
+    cfg = O.GDNConfig(channels=C, delta_key_dim=dk, gate_type=gate_type, use_spectral_l2_norm=l2)
+    q, k, v = (rng.standard_normal(shape) for _ in range(3))
+    n_ab = {"factored": H * Wf, "dense": H * Wf, "channel": nh, "scalar": 1}[gate_type]
+    alpha = 0.1 + 0.89 / (1.0 + np.exp(-rng.standard_normal((B, T, n_ab))))
+    beta = 1.0 / (1.0 + np.exp(-rng.standard_normal((B, T, n_ab))))
+    kern = rng.standard_normal((nh, 11, 11)) * 0.2
+    what = O.spectral_kernel(kern, H, W, 0.999)
+    shp = (B, T, nh, 1, 1) if gate_type == "channel" else ((B, T, 1, 1, 1) if gate_type == "scalar"
+                                                           else (B, T, 1, H, Wf))
+    ref = O.gdn_core(q, k, v, alpha.reshape(shp), beta.reshape(shp), what, cfg, scan="linear")
+    planes = np.concatenate([z.transpose(0, 1, 4, 2, 3) for z in (q, k, v)], axis=2)     # (B, T, 3C, H, W)
+    spec, norms = S.rfft2(_dev(planes), want_norms=l2)
+    ab = _dev(np.stack([alpha, beta], axis=-1))
+    ohat = S.gdn_scan_bins(spec, norms, ab, gate_type, _dev(what, torch.complex64), dk)
+    o = S.irfft2(ohat, W)
+    assert rel_err(to_np(o), ref) <= TOL_F32
+
+
+def test_gdn_proj_out_norm_gate(mods):
+    _, S = mods
+    print_case(test="gdn_proj_out")
+    rng = np.random.default_rng(12)
+    F, C, HW, N = 3, 64, 1024, 64
+    o = rng.standard_normal((F, C, HW))
+    g = rng.standard_normal((F, C, HW))
+    Wt = rng.standard_normal((C, N)) / 8
+    b = rng.standard_normal(N) * 0.1
+    sc = 1.0 + 0.1 * rng.standard_normal(C)
+    sh = 0.1 * rng.standard_normal(C)
+    ocl = o.transpose(0, 2, 1)
+    gcl = g.transpose(0, 2, 1)
+    for norm, ref_n in (("rms", O.rms_norm(ocl, sc)), ("layer", O.layer_norm(ocl, sc, sh)), ("none", ocl)):
+        out = S.gdn_proj_out(_dev(o), _dev(g), norm, _dev(sc) if norm != "none" else None,
+                             _dev(sh) if norm == "layer" else None, _dev(Wt), _dev(b))
+        ref = (ref_n * gcl).reshape(F * HW, C) @ Wt + b
+        assert rel_err(to_np(out), ref) < 1e-5, norm
+
+
+# ------------------------------------------------------------------- layer
+
+LAYER_CASES = [
+    # name, (B, T, H, W, C), cfg kwargs
+    ("c3_shape_small", (1, 3, 128, 128, 8),
+     dict(delta_key_dim=4, gate_type="factored", qkv_conv_size=5, kernel_size=11)),
+    ("c4_shape_small", (2, 8, 32, 32, 16),
+     dict(delta_key_dim=4, gate_type="factored", kernel_size=11)),
+    ("channel_dk2_layer_norm", (2, 4, 16, 16, 8),
+     dict(delta_key_dim=2, gate_type="channel", output_norm="layer", output_gate_act="sigmoid")),
+    ("dense_dk3_no_input_gates", (1, 5, 16, 16, 12),
+     dict(delta_key_dim=3, gate_type="dense", use_input_gates=False, short_conv_size=0, qkv_conv_size=3)),
+    ("scalar_no_norm_no_l2", (2, 3, 8, 8, 8),
+     dict(delta_key_dim=2, gate_type="scalar", output_norm="none", use_spectral_l2_norm=False,
+          no_spectral_clamp=True, position_independent_gates=True)),
+]
+
+
+def _layer(kw, shape, seed):
+    rng = np.random.default_rng(seed)
+    B, T, H, W, C = shape
+    okw = {k: v for k, v in kw.items() if k != "position_independent_gates"}
+    cfg = O.GDNConfig(channels=C, **okw)
+    p = O.init_params(O.gdn_param_shapes(cfg, H, W), rng, spectral_init="xavier")
+    x = rng.standard_normal(shape)
+    return cfg, p, x
+
+
+@pytest.mark.parametrize("name,shape,kw", LAYER_CASES, ids=[c[0] for c in LAYER_CASES])
+def test_gdn_layer_matches_oracle(mods, name, shape, kw):
+    cells, _ = mods
+    print_case(test="gdn_layer", case=name)
+    cfg, p, x = _layer(kw, shape, 21)
+    if kw.get("position_independent_gates"):
+        # no temporal encoding of ctx: compare against the oracle with the table cancelled
+        T, C = shape[1], shape[4]
+        enc = O.temporal_context_encoding(T, C)
+        orig = O.temporal_context_encoding
+        O.temporal_context_encoding = lambda T_, C_, base=10000.0: np.zeros((T_, C_))
+        try:
+            ref = O.gdn_forward(p, x, cfg)
+        finally:
+            O.temporal_context_encoding = orig
+        assert enc.shape == (T, C)
+    else:
+        ref = O.gdn_forward(p, x, cfg)
+    cell = cells.GatedDeltaNetCSSM(channels=shape[4], **kw)
+    y = cell.apply(cells.GatedDeltaNetCSSM.load_params(p), _dev(x))
+    torch.cuda.synchronize()
+    assert tuple(y.shape) == shape
+    assert rel_err(to_np(y), ref) <= TOL_F32
+
+
+def test_gdn_layer_bf16_io(mods):
+    """C4-shaped (video, 32x32, d_k = 4) with bf16 I/O: sparse dots + N(0, 0.01) background."""
+    cells, _ = mods
+    print_case(test="gdn_layer_bf16")
+    kw = dict(delta_key_dim=4, gate_type="factored", kernel_size=11)
+    shape = (2, 8, 32, 32, 16)
+    cfg, p, _ = _layer(kw, shape, 22)
+    rng = np.random.default_rng(23)
+    x = rng.standard_normal(shape) * 0.01
+    x[rng.random(shape[:4]) < 0.02] = 1.0
+    xb = _dev(x, torch.bfloat16)
+    y = cells.GatedDeltaNetCSSM(channels=16, **kw).apply(cells.GatedDeltaNetCSSM.load_params(p), xb)
+    assert y.dtype == torch.bfloat16
+    ref = O.gdn_forward(p, to_np(xb), cfg)
+    assert np.sqrt(np.mean((to_np(y) - ref) ** 2)) <= TOL_BF16 * np.sqrt(np.mean(ref ** 2))
+    assert bf16_excess_err(to_np(y), ref) <= 2 * TOL_BF16
+
+
+def test_gdn_layer_is_causal_in_time(mods):
+    cells, _ = mods
+    print_case(test="gdn_layer_causal")
+    kw = dict(delta_key_dim=2, gate_type="factored")
+    cfg, p, x = _layer(kw, (1, 6, 16, 16, 8), 24)
+    cell = cells.GatedDeltaNetCSSM(channels=8, **kw)
+    v = cells.GatedDeltaNetCSSM.load_params(p)
+    y1 = to_np(cell.apply(v, _dev(x)))
+    x2 = x.copy()
+    x2[:, 4:] += 1.0
+    y2 = to_np(cell.apply(v, _dev(x2)))
+    assert np.array_equal(y1[:, :4], y2[:, :4])
+    assert not np.allclose(y1[:, 4:], y2[:, 4:])
+
+
+def test_gdn_layer_rejects_unsupported(mods):
+    cells, _ = mods
+    with pytest.raises(NotImplementedError):
+        cells.GatedDeltaNetCSSM(channels=8, rope_mode="spatial")
+    with pytest.raises(NotImplementedError):
+        cells.GatedDeltaNetCSSM(channels=8, int_attention_mode="spectral")
+    cell = cells.GatedDeltaNetCSSM(channels=8, delta_key_dim=2)
+    v = cell.init(0, (1, 2, 12, 12, 8))
+    with pytest.raises(NotImplementedError):
+        cell.apply(v, torch.zeros((1, 2, 12, 12, 8), device="cuda"))
