@@ -1,21 +1,29 @@
 #!/usr/bin/env python3
-"""Benchmark of the fused spectral-SSM layer (GatedCSSM) on one MI355X.
+"""Benchmark of the fused spectral-SSM layer (GatedCSSM / GatedDeltaNetCSSM) on one MI355X.
 
-Workload ("C2"): gated cell, fp32, batch 128 of one
-128x128x64 image repeated over T = 8 frames (materialised; the kernels do not
-see the repetition), x ~ N(0, 1), kernel_size 11, factored B/C/Delta gates,
-softplus Delta, no short convolutions, random-init weights (synthetic data).
+Default workload ("C2"): gated cell, fp32, batch 128
+of one 128x128x64 image repeated over T = 8 frames (materialised; the kernels
+do not see the repetition), x ~ N(0, 1), kernel_size 11, factored B/C/Delta
+gates, softplus Delta, no short convolutions, random-init weights with
+N(0, 0.1^2) biases (synthetic data).  ``--workload`` selects the other
+BASELINE configs (c1, c3, c4, c5); they are measured the same way.
 
-A step is one full layer forward, x -> out (in_proj GEMM with the plane-major
-split + SiLU + spatial-mean epilogue -> gate planes -> fused rfft2 / scan /
-irfft2 / x SiLU(z) kernel -> out_proj GEMM), with x already in HBM.
-value = frames/s = B * T / step time.  The roofline entry is for the fused
-scan kernel (the dominant kernel), timed with HIP events on its stream inside
-the timed steps; its algorithmic bytes per launch are
-B*T*(3*H*W*C*4 + 3*(H+W/2+1)*4) + C*H*(W/2+1)*8 (read u and z, write y, read
-the factored gate vectors and K_hat once).  cpu_baseline times the float64
-numpy restatement (oracle/) of the same layer on a bounded slice of the
-batch, on one host thread.
+A step is one full layer forward with x already in HBM:
+  gated: in_proj GEMM (plane-major split + SiLU + spatial-mean epilogue) ->
+         gate planes -> fused rfft2 / scan / irfft2 / x SiLU(z) kernel -> out_proj GEMM
+  gdn:   frame mean + gates -> [qkv depthwise conv] -> qkv_proj -> short conv + SiLU +
+         input gates -> gate_proj -> rfft2 -> per-bin delta-rule scan -> irfft2 ->
+         RMSNorm x gate + output_proj
+value = frames/s = B * T / step time (whole layer).
+
+roofline: the dominant kernel, timed with HIP events on its stream over the
+timed steps.  gated: the fused scan, algorithmic bytes per launch
+B*T*(3*H*W*C*s + 3*(H+W/2+1)*4) + C*H*(W/2+1)*8 (read u and z, write y, read the
+factored gate vectors, K_hat once).  gdn: the spectral core (rfft2 + scan +
+irfft2 launches together), B*T*(4*H*W*C*s + 2*(H+W/2+1)*4) + n_h*H*(W/2+1)*8
+(read q, k, v, write o, gates, W_hat once).  s = bytes per I/O element.
+cpu_baseline times the float64 numpy restatement (oracle/) of the same layer
+on a bounded slice of the batch, on one host thread.
 """
 from __future__ import annotations
 
@@ -30,9 +38,19 @@ ROOT = os.path.dirname(os.path.abspath(__file__))
 if ROOT not in sys.path:
     sys.path.insert(0, ROOT)
 
-WORKLOAD = dict(name="C2 gated 128x128 T=8", B=128, T=8, H=128, W=128, C=64, kernel_size=11,
-                gate_type="factored", gate_activation="softplus")
 HBM_PEAK_GBS = 8000.0
+METRIC = "frames/sec per fused spectral-SSM layer (1 GPU) + % HBM roofline"
+
+WORKLOADS = {
+    "c1": dict(cell="gated", name="C1 gated 1x1 T=1 32x32 expand 2", B=8, T=1, H=32, W=32, C=64, expand=2,
+               kernel_size=1, gate_type="factored", io="f32", data="normal"),
+    "c2": dict(cell="gated", name="C2 gated 128x128 T=8", B=128, T=8, H=128, W=128, C=64, expand=1, kernel_size=11,
+               gate_type="factored", io="f32", data="repeat"),
+    "c3": dict(cell="gdn", name="C3 GDN d_k=4 128x128 T=8", B=128, T=8, H=128, W=128, C=64, dk=4, kernel_size=11,
+               qkv_conv_size=5, gate_type="factored", io="f32", data="normal"),
+    "c4": dict(cell="gdn", name="C4 GDN video d_k=4 32x32 T=32 bf16", B=128, T=32, H=32, W=32, C=64, dk=4,
+               kernel_size=11, qkv_conv_size=1, gate_type="factored", io="bf16", data="dots"),
+}
 
 
 def parse():
@@ -40,24 +58,36 @@ def parse():
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=10)
     ap.add_argument("--warmup", type=int, default=3)
-    ap.add_argument("--batch", type=int, default=WORKLOAD["B"], help="override B (parity/debug runs only)")
+    ap.add_argument("--workload", default="c2", choices=sorted(WORKLOADS))
+    ap.add_argument("--batch", type=int, default=0, help="override B (parity/debug runs only)")
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--cpu-seconds", type=float, default=12.0, help="target CPU baseline wall time")
-    ap.add_argument("--traffic", default=os.path.join(ROOT, "profiles", "gated_scan_c2_traffic.txt"),
-                    help="rocprofv3 FETCH/WRITE summary giving HBM bytes per scan launch")
+    ap.add_argument("--traffic", default=None,
+                    help="rocprofv3 FETCH/WRITE summary giving HBM bytes per dominant-kernel launch "
+                         "(default profiles/<kernel>_<workload>_traffic.txt)")
     ap.add_argument("--copy-calibration", type=int, default=0, metavar="BYTES",
-                    help="first run one device-to-device copy of BYTES (a known-size kernel that scales "
+                    help="first run one streaming kernel over BYTES (a known-size kernel that scales "
                          "rocprofv3 FETCH_SIZE / WRITE_SIZE counters); not timed")
     return ap.parse_args()
 
 
-def scan_algorithmic_bytes(B, T, H, W, C):
+def io_bytes(w):
+    return 2 if w["io"] == "bf16" else 4
+
+
+def algorithmic_bytes(w, B):
+    T, H, W = w["T"], w["H"], w["W"]
     Wf = W // 2 + 1
-    return B * T * (3 * H * W * C * 4 + 3 * (H + Wf) * 4) + C * H * Wf * 8
+    s = io_bytes(w)
+    if w["cell"] == "gated":
+        C = w["C"] * w["expand"]
+        return B * T * (3 * H * W * C * s + 3 * (H + Wf) * 4) + C * H * Wf * 8
+    C, nh = w["C"], w["C"] // w["dk"]
+    return B * T * (4 * H * W * C * s + 2 * (H + Wf) * 4) + nh * H * Wf * 8
 
 
 def read_traffic(path):
-    """HBM bytes per scan launch from the committed rocprofv3 summary, or None."""
+    """HBM bytes per dominant-kernel launch from a committed rocprofv3 summary, or None."""
     try:
         with open(path) as f:
             for line in f:
@@ -68,8 +98,122 @@ def read_traffic(path):
     return None
 
 
-def cpu_baseline(seconds):
-    """float64 numpy restatement of the layer (oracle/), one image (T frames) at a time."""
+# ----------------------------------------------------------------- inputs
+
+def make_input(w, B, torch, dev):
+    T, H, W, C = w["T"], w["H"], w["W"], w["C"]
+    gen = torch.Generator(device=dev).manual_seed(0)
+    dt = torch.bfloat16 if w["io"] == "bf16" else torch.float32
+    if w["data"] == "repeat":
+        img = torch.randn((B, 1, H, W, C), generator=gen, device=dev)
+        return img.expand(B, T, H, W, C).contiguous().to(dt)
+    if w["data"] == "dots":
+        # ~2 % of pixels set to 1.0 along random-walk dot tracks, N(0, 0.01^2) background
+        x = torch.randn((B, T, H, W, C), generator=gen, device=dev) * 0.01
+        ndots = max(1, int(0.02 * H * W))
+        pos = torch.randint(0, H * W, (B, ndots), generator=gen, device=dev)
+        steps = torch.tensor([1, -1, W, -W, 0], device=dev)
+        for t in range(T):
+            mask = torch.zeros((B, H * W), dtype=torch.bool, device=dev)
+            mask.scatter_(1, pos, True)
+            x[:, t] = torch.where(mask.view(B, H, W, 1), torch.ones((), device=dev), x[:, t])
+            mv = steps[torch.randint(0, 5, (B, ndots), generator=gen, device=dev)]
+            pos = (pos + mv) % (H * W)
+        return x.to(dt)
+    return torch.randn((B, T, H, W, C), generator=gen, device=dev).to(dt)
+
+
+def make_cell(w, cells):
+    if w["cell"] == "gated":
+        return cells.GatedCSSM(channels=w["C"], expand=w["expand"], kernel_size=w["kernel_size"],
+                               gate_type=w["gate_type"], short_conv_size=0, short_conv_spatial_size=0)
+    return cells.GatedDeltaNetCSSM(channels=w["C"], delta_key_dim=w["dk"], kernel_size=w["kernel_size"],
+                                   gate_type=w["gate_type"], qkv_conv_size=w["qkv_conv_size"])
+
+
+def randomise_biases(variables, torch, dev):
+    gen = torch.Generator(device=dev).manual_seed(1)
+    for sub in variables["params"].values():     # non-zero biases exercise the bias paths
+        if isinstance(sub, dict) and "bias" in sub:
+            sub["bias"].normal_(0.0, 0.1, generator=gen)
+
+
+# ------------------------------------------------------ instrumented steps
+
+class Marks:
+    """HIP events on torch's current stream (the stream every kernel is launched on)."""
+
+    def __init__(self, torch, record):
+        self.torch, self.record, self.seq = torch, record, []
+
+    def __call__(self, name):
+        if self.record:
+            ev = self.torch.cuda.Event(enable_timing=True)
+            ev.record()
+            self.seq.append((name, ev))
+
+    def spans(self):
+        return [(self.seq[i + 1][0], self.seq[i][1], self.seq[i + 1][1]) for i in range(len(self.seq) - 1)]
+
+
+def gated_step(cell, variables, x, w, S, mark):
+    """The calls GatedCSSM.apply makes (short convolutions off), with a mark after each kernel."""
+    p = variables["params"]
+    B, T, H, W, _ = x.shape
+    Ci, F, HW = cell.channels * cell.expand, B * T, H * W
+    mark("start")
+    u, z, ctx = S.proj_in(x, p["in_proj"]["kernel"], p["in_proj"]["bias"], F, HW, silu_lo=True, silu_hi=True,
+                          want_ctx=True)
+    mark("in_proj")
+    gates = S.gated_gates(ctx.view(B, T, Ci), p, H, W, cell.gate_type, cell.gate_activation, c_scale=1.0 / HW)
+    khat = cell.spectral_kernel(p, H, W)
+    mark("gates")
+    y = S.gated_scan(u.view(B, T, Ci, H, W), z.view(B, T, Ci, H, W), gates, khat)
+    mark("scan")
+    out = S.proj_out(y.view(F, Ci, HW), p["out_proj"]["kernel"], p["out_proj"]["bias"])
+    mark("out_proj")
+    return out.view(B, T, H, W, cell.channels)
+
+
+def gdn_step(cell, variables, x, w, S, mark):
+    """The calls GatedDeltaNetCSSM.apply makes (factored gates, input gates, short conv, RMSNorm)."""
+    import torch
+    p = variables["params"]
+    B, T, H, W, C = x.shape
+    F, HW, f32 = B * T, H * W, torch.float32
+    mark("start")
+    what = cell.spectral_kernel(p, H, W)
+    ctx = S.frame_mean(x)
+    ab, bkv = S.gdn_gates(ctx, p, H, W, cell.delta_key_dim, cell.gate_type, True, "sinusoid", cell.rope_base)
+    mark("gates")
+    if cell.qkv_conv_size > 1:
+        xq = S.depthwise_conv(x, p["qkv_dw"]["kernel"], p["qkv_dw"]["bias"], out_dtype=f32)
+        mark("qkv_dw")
+    else:
+        xq = x
+    qkv = S.proj_planes(xq, p["qkv_proj"]["kernel"], p["qkv_proj"]["bias"], F, HW, out_dtype=f32)
+    qkv = qkv.view(B, T, 3 * C, H, W)
+    mark("qkv_proj")
+    S.gdn_qkv_post(qkv, [p["short_conv_q"], p["short_conv_k"], p["short_conv_v"]], 1, bkv)
+    mark("qkv_post")
+    gv = S.proj_planes(x, p["gate_proj"]["kernel"], p["gate_proj"]["bias"], F, HW, act="silu", out_dtype=f32)
+    mark("gate_proj")
+    spec, norms = S.rfft2(qkv, want_norms=True)
+    mark("rfft2")
+    ohat = S.gdn_scan_bins(spec, norms, ab, cell.gate_type, what, cell.delta_key_dim)
+    mark("scan_bins")
+    o = S.irfft2(ohat, W, out_dtype=f32)
+    mark("irfft2")
+    out = S.gdn_proj_out(o.view(F, C, HW), gv, "rms", p["rms_scale"], None, p["output_proj"]["kernel"],
+                         p["output_proj"]["bias"], out_dtype=x.dtype)
+    mark("proj_out")
+    return out.view(B, T, H, W, C)
+
+
+# ----------------------------------------------------------- CPU baseline
+
+def cpu_baseline(w, seconds):
+    """float64 numpy restatement of the layer (oracle/), one batch element (T frames) at a time."""
     import numpy as np
     from oracle import cssm_oracle as O
     try:
@@ -77,33 +221,44 @@ def cpu_baseline(seconds):
         limiter = threadpool_limits(limits=1)
     except Exception:          # threadpoolctl absent: numpy's FFT is single-threaded anyway
         limiter = None
-    w = WORKLOAD
-    cfg = O.GatedConfig(channels=w["C"], kernel_size=w["kernel_size"], gate_type=w["gate_type"],
-                        gate_activation=w["gate_activation"], short_conv_size=0, short_conv_spatial_size=0)
     rng = np.random.default_rng(1)
-    p = O.init_params(O.gated_param_shapes(cfg, w["C"], w["H"], w["W"]), rng)
-    img = rng.standard_normal((1, 1, w["H"], w["W"], w["C"]))
-    x = np.repeat(img, w["T"], axis=1)
+    T, H, W, C = w["T"], w["H"], w["W"], w["C"]
+    if w["cell"] == "gated":
+        cfg = O.GatedConfig(channels=C, expand=w["expand"], kernel_size=w["kernel_size"], gate_type=w["gate_type"],
+                            short_conv_size=0, short_conv_spatial_size=0)
+        p = O.init_params(O.gated_param_shapes(cfg, C, H, W), rng)
+        run = lambda x: O.gated_forward(p, x, cfg)                                   # noqa: E731
+    else:
+        cfg = O.GDNConfig(channels=C, delta_key_dim=w["dk"], kernel_size=w["kernel_size"], gate_type=w["gate_type"],
+                          qkv_conv_size=w["qkv_conv_size"])
+        p = O.init_params(O.gdn_param_shapes(cfg, H, W), rng, spectral_init="xavier")
+        run = lambda x: O.gdn_forward(p, x, cfg, scan="rank1")                       # noqa: E731
+    if w["data"] == "repeat":
+        x = np.repeat(rng.standard_normal((1, 1, H, W, C)), T, axis=1)
+    else:
+        x = rng.standard_normal((1, T, H, W, C))
     frames, t0 = 0, time.perf_counter()
     while True:
-        O.gated_forward(p, x, cfg)
-        frames += w["T"]
+        run(x)
+        frames += T
         el = time.perf_counter() - t0
         if el >= seconds:
             break
-    if limiter is not None:
-        limiter.unregister() if hasattr(limiter, "unregister") else None
+    if limiter is not None and hasattr(limiter, "unregister"):
+        limiter.unregister()
     return dict(value=frames / el, unit="frames/s", cores=1, kind="port",
-                sample=f"{frames // w['T']} image(s) x T={w['T']} (of B={w['B']}), full C={w['C']} at "
-                       f"{w['H']}x{w['W']}, float64 numpy oracle, {el:.1f} s, "
-                       f"{platform.processor() or platform.machine()} x{os.cpu_count()} logical cpus")
+                sample=f"{frames // T} batch element(s) x T={T} (of B={w['B']}), full C={C} at {H}x{W}, "
+                       f"float64 numpy oracle, {el:.1f} s, {platform.processor() or platform.machine()} "
+                       f"x{os.cpu_count()} logical cpus")
 
+
+# ------------------------------------------------------------------- main
 
 def main():
     args = parse()
     if args.gpus != 1:
         print(f"bench.py measures one GPU: this build has no multi-GPU path (asked for --gpus {args.gpus}); "
-              "the layer shards over batch with no exchange, see DESIGN.md", file=sys.stderr)
+              "the layer shards over batch with no exchange (DESIGN.md, sharding)", file=sys.stderr)
         sys.exit(2)
     import torch
     if not torch.cuda.is_available():
@@ -111,8 +266,9 @@ def main():
         sys.exit(1)
     from cssm_amd import cells, spectral as S
 
-    w = dict(WORKLOAD)
-    B, T, H, W, C = args.batch, w["T"], w["H"], w["W"], w["C"]
+    w = dict(WORKLOADS[args.workload])
+    B = args.batch or w["B"]
+    T, H, W = w["T"], w["H"], w["W"]
     dev = "cuda"
     if args.copy_calibration > 0:
         # a streaming kernel of known traffic (read n*4 B, write n*4 B): torch's neg, which
@@ -125,65 +281,42 @@ def main():
         torch.cuda.synchronize()
         del src, dst
     torch.manual_seed(0)
-    gen = torch.Generator(device=dev).manual_seed(0)
-    img = torch.randn((B, 1, H, W, C), generator=gen, device=dev)
-    x = img.expand(B, T, H, W, C).contiguous()
-    del img
-    cell = cells.GatedCSSM(channels=C, kernel_size=w["kernel_size"], gate_type=w["gate_type"],
-                           gate_activation=w["gate_activation"], short_conv_size=0, short_conv_spatial_size=0)
+    x = make_input(w, B, torch, dev)
+    cell = make_cell(w, cells)
     variables = cell.init(1, x.shape)
-    for name, sub in variables["params"].items():       # non-zero biases exercise the bias paths
-        if isinstance(sub, dict) and "bias" in sub:
-            sub["bias"].normal_(0.0, 0.1, generator=gen)
-
-    # instrumented step: the same calls GatedCSSM.apply makes, with events around each kernel
-    p = variables["params"]
-    F, HW = B * T, H * W
-    ev = {k: [] for k in ("in_proj", "gates", "scan", "out_proj")}
-
-    def step(record):
-        marks = []
-        if record:
-            marks = [torch.cuda.Event(enable_timing=True) for _ in range(5)]
-            marks[0].record()
-        u, z, ctx = S.proj_in(x, p["in_proj"]["kernel"], p["in_proj"]["bias"], F, HW, silu_lo=True,
-                              silu_hi=True, want_ctx=True)
-        if record:
-            marks[1].record()
-        gates = S.gated_gates(ctx.view(B, T, C), p, H, W, w["gate_type"], w["gate_activation"], c_scale=1.0 / HW)
-        khat = cell.spectral_kernel(p, H, W)
-        if record:
-            marks[2].record()
-        y = S.gated_scan(u.view(B, T, C, H, W), z.view(B, T, C, H, W), gates, khat)
-        if record:
-            marks[3].record()
-        out = S.proj_out(y.view(F, C, HW), p["out_proj"]["kernel"], p["out_proj"]["bias"])
-        if record:
-            marks[4].record()
-            for i, k in enumerate(("in_proj", "gates", "scan", "out_proj")):
-                ev[k].append((marks[i], marks[i + 1]))
-        return out
+    randomise_biases(variables, torch, dev)
+    step = gated_step if w["cell"] == "gated" else gdn_step
+    core = ("scan",) if w["cell"] == "gated" else ("rfft2", "scan_bins", "irfft2")
 
     for _ in range(args.warmup):
-        step(False)
+        step(cell, variables, x, w, S, Marks(torch, False))
     torch.cuda.synchronize()
+    marks = []
     t0 = time.perf_counter()
     for _ in range(args.steps):
-        step(True)
+        m = Marks(torch, True)
+        step(cell, variables, x, w, S, m)
+        marks.append(m)
     torch.cuda.synchronize()
     el = time.perf_counter() - t0
     ms_step = el * 1e3 / args.steps
     # the instrumented step must equal the module's forward bit for bit
-    if not torch.equal(step(False).view(B, T, H, W, C), cell.apply(variables, x)):
-        print("instrumented step differs from GatedCSSM.apply", file=sys.stderr)
+    if not torch.equal(step(cell, variables, x, w, S, Marks(torch, False)), cell.apply(variables, x)):
+        print("instrumented step differs from the module's apply", file=sys.stderr)
         sys.exit(1)
-    kern_ms = {k: sum(a.elapsed_time(b) for a, b in v) / len(v) for k, v in ev.items()}
-    scan_ms = kern_ms["scan"]
-    alg = scan_algorithmic_bytes(B, T, H, W, C)
-    achieved = alg / (scan_ms * 1e-3) / 1e9
-    traffic = read_traffic(args.traffic) if B == WORKLOAD["B"] else None
+    kern_ms = {}
+    for m in marks:
+        for name, a, b in m.spans():
+            kern_ms[name] = kern_ms.get(name, 0.0) + a.elapsed_time(b) / len(marks)
+    core_ms = sum(kern_ms[k] for k in core)
+    alg = algorithmic_bytes(w, B)
+    achieved = alg / (core_ms * 1e-3) / 1e9
+    kname = "gated_scan" if w["cell"] == "gated" else "gdn_core"
+    tpath = args.traffic or os.path.join(ROOT, "profiles", f"{kname}_{args.workload}_traffic.txt")
+    traffic = read_traffic(tpath) if B == w["B"] else None
+    Ci = w["C"] * w.get("expand", 1)
     res = {
-        "metric": "frames/sec per fused spectral-SSM layer (1 GPU) + % HBM roofline",
+        "metric": METRIC,
         "value": B * T / (ms_step * 1e-3),
         "unit": "frames/s",
         "n_gpus": 1,
@@ -194,19 +327,24 @@ def main():
         "scaling": "weak",
         "vs_baseline": None,
         "dtype": "f32",
-        "data": "synthetic: one N(0,1) 128x128x64 image repeated over T=8 (materialised), random-init weights",
-        "config": {"workload": w["name"], "cell": "gated", "batch": B, "T": T, "H": H, "W": W, "channels": C,
-                   "kernel_size": w["kernel_size"], "gate_type": w["gate_type"], "short_convs": "0/0",
-                   "io": "f32", "step": "full layer forward x -> out_proj"},
+        "data": {"repeat": f"synthetic: one N(0,1) {H}x{W}x{w['C']} image repeated over T={T} (materialised)",
+                 "normal": f"synthetic: N(0,1) {H}x{W}x{w['C']} frames, T={T}",
+                 "dots": f"synthetic: 2% moving dots = 1.0 on N(0,0.01^2) background, {H}x{W}x{w['C']}, "
+                         f"T={T}"}[w["data"]] + ", random-init weights",
+        "config": {"workload": w["name"], "cell": w["cell"], "batch": B, "T": T, "H": H, "W": W,
+                   "channels": w["C"], "inner_channels": Ci, "kernel_size": w["kernel_size"],
+                   "gate_type": w["gate_type"], "io": w["io"], "step": "full layer forward x -> out"},
         "images_per_s": B / (ms_step * 1e-3),
         "kernel_ms": {k: round(v, 4) for k, v in kern_ms.items()},
-        "scan_frames_per_s": B * T / (scan_ms * 1e-3),
-        "roofline": {"kernel": "gated_scan_pow2<7,7,1,64,f32>", "bound": "hbm", "achieved": achieved,
+        "core_frames_per_s": B * T / (core_ms * 1e-3),
+        "roofline": {"kernel": kname, "launches": list(core), "bound": "hbm", "achieved": achieved,
                      "peak": HBM_PEAK_GBS, "unit": "GB/s", "frac": achieved / HBM_PEAK_GBS,
                      "algorithmic_bytes": alg, "traffic": traffic},
     }
+    if w["cell"] == "gdn":
+        res["config"].update(delta_key_dim=w["dk"], qkv_conv_size=w["qkv_conv_size"])
     if not args.no_cpu_baseline:
-        res["cpu_baseline"] = cpu_baseline(args.cpu_seconds)
+        res["cpu_baseline"] = cpu_baseline(w, args.cpu_seconds)
     print(json.dumps(res), flush=True)
 
 

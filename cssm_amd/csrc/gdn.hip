@@ -44,37 +44,46 @@ __device__ __forceinline__ float2 goom_floor2(float2 z) {
 // Batched 2-D real FFTs of power-of-two planes.
 // ---------------------------------------------------------------------------
 
-// forward policy: bins -> HBM spectrum (undoing the pass's factor 2), |X|^2
-// summed per plane into LDS
+// forward policy: bins -> HBM spectrum (undoing the pass's factor 2).  The
+// sum of |X|^2 per plane is reduced deterministically: every C2 unit pair and
+// every edge job leaves its partial in a fixed LDS slot (slot = job index,
+// whose plane is job / (units per plane)), summed in a fixed order afterwards.
 template <class G>
 struct SpecStoreOp {
-  static constexpr int H = G::H, WH = G::WH, WF = G::WF, H1 = G::H1, H2 = G::H2;
+  static constexpr int H = G::H, WH = G::WH, WF = G::WF, H1 = G::H1, H2 = G::H2, NT = G::NT;
   float2* out;      // (NP, H, WF) of this workgroup
-  float* psum;      // LDS (NP)
+  float* part_c2;   // LDS (NC2) or nullptr: partial sums of the C2 jobs
+  float* part_e;    // LDS (NE) or nullptr: partial sums of the edge jobs
   int nvalid;       // planes of the group that exist (the last group may be partial)
+  unsigned tid;
 
-  __device__ __forceinline__ void bins(int, int, int pl, int k, int v, float2 (&sp)[G::H2]) const {
-    if (pl >= nvalid) return;
+  __device__ __forceinline__ void bins(int j, int a2, int pl, int k, int v, float2 (&sp)[G::H2]) const {
     float s = 0.0f;
+    if (pl < nvalid) {
 #pragma unroll
-    for (int q = 0; q < H2; ++q) {
-      const float2 x = make_float2(0.5f * sp[q].x, 0.5f * sp[q].y);
-      out[size_t(pl * H + k + H1 * q) * WF + v] = x;
-      s = fmaf(x.x, x.x, fmaf(x.y, x.y, s));
+      for (int q = 0; q < H2; ++q) {
+        const float2 x = make_float2(0.5f * sp[q].x, 0.5f * sp[q].y);
+        out[size_t(pl * H + k + H1 * q) * WF + v] = x;
+        s = fmaf(x.x, x.x, fmaf(x.y, x.y, s));
+      }
     }
-    if (psum) atomicAdd(&psum[pl], s);
+    if (part_c2) {
+      float& slot = part_c2[j * NT + tid];
+      slot = a2 ? slot + s : s;
+    }
   }
-  __device__ __forceinline__ void edge(int, int pl, int uA, int uB, int, float2 (&v4)[4]) const {
-    if (pl >= nvalid) return;
-    const int idx[4] = {uA * WF, uA * WF + WH, uB * WF, uB * WF + WH};
+  __device__ __forceinline__ void edge(int j, int pl, int uA, int uB, int, float2 (&v4)[4]) const {
     float s = 0.0f;
+    if (pl < nvalid) {
+      const int idx[4] = {uA * WF, uA * WF + WH, uB * WF, uB * WF + WH};
 #pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      const float2 x = make_float2(0.5f * v4[i].x, 0.5f * v4[i].y);
-      out[size_t(pl * H) * WF + idx[i]] = x;
-      s = fmaf(x.x, x.x, fmaf(x.y, x.y, s));
+      for (int i = 0; i < 4; ++i) {
+        const float2 x = make_float2(0.5f * v4[i].x, 0.5f * v4[i].y);
+        out[size_t(pl * H) * WF + idx[i]] = x;
+        s = fmaf(x.x, x.x, fmaf(x.y, x.y, s));
+      }
     }
-    if (psum) atomicAdd(&psum[pl], s);
+    if (part_e) part_e[j * NT + tid] = s;
   }
 };
 
@@ -114,15 +123,16 @@ rfft2_planes(const void* __restrict__ x, long long P, float2* __restrict__ spec,
   constexpr int H = G::H, W = G::W, WF = G::WF, NT = G::NT;
   using V4 = typename IO::V4;
   using TE = typename IO::T;
+  constexpr int UC2 = G::NC2 / NP, UE = G::NE / NP;     // C2 / edge jobs per plane
+  constexpr int GR = NT / NP > 0 ? NT / NP : 1;          // reducing threads per plane
   __shared__ __attribute__((aligned(16))) float smem[G::LDS_FLOATS];
-  __shared__ float psum[NP];
+  __shared__ float part_c2[G::NC2], part_e[G::NE], red[NT];
   const PlaneFft<G> fft(smem);
   const unsigned tid = threadIdx.x;
   const size_t p0 = size_t(blockIdx.x) * NP;
   const int nvalid = int(P - (long long)p0 < NP ? P - (long long)p0 : NP);
   const unsigned nv4 = unsigned(nvalid) * (H * W / 4);
   fft.init_twiddles(tid);
-  for (int i = tid; i < NP; i += NT) psum[i] = 0.0f;
   {
     const V4* src = reinterpret_cast<const V4*>(static_cast<const TE*>(x) + p0 * H * W);
     V4 ld[G::JLD];
@@ -135,14 +145,33 @@ rfft2_planes(const void* __restrict__ x, long long P, float2* __restrict__ spec,
     for (int i = 0; i < G::JLD; ++i) fft.v4_store(i * NT + tid, IO::to_f4(ld[i]));
   }
   __syncthreads();
-  SpecStoreOp<G> op{spec + p0 * H * WF, norms ? psum : nullptr, nvalid};
+  SpecStoreOp<G> op{spec + p0 * H * WF, norms ? part_c2 : nullptr, norms ? part_e : nullptr, nvalid, tid};
+  // C2 jobs on the packed DC / Nyquist column (v = 0) never reach the policy: their slots stay 0
+#pragma unroll
+  for (int j = 0; j < G::JC2; ++j) part_c2[j * NT + tid] = 0.0f;
   fft.r1(tid);
   fft.r2(tid);
   fft.c1(tid);
   fft.template c2<true, false>(tid, op);
   fft.template edges<true, false>(tid, op);
   if (norms) {
-    for (int i = tid; i < nvalid; i += NT) norms[p0 + i] = psum[i];
+    // plane pl: GR threads each sum a fixed stride of its UC2 + UE slots, then one sums those in order
+    for (int pl0 = 0; pl0 < NP; pl0 += NT / GR) {
+      const int pl = pl0 + int(tid) / GR, r = int(tid) % GR;
+      float acc = 0.0f;
+      if (pl < NP) {
+        for (int i = r; i < UC2; i += GR) acc += part_c2[pl * UC2 + i];
+        for (int i = r; i < UE; i += GR) acc += part_e[pl * UE + i];
+      }
+      red[tid] = acc;
+      __syncthreads();
+      if (r == 0 && pl < nvalid) {
+        float sum = 0.0f;
+        for (int i = 0; i < GR; ++i) sum += red[tid + i];
+        norms[p0 + pl] = sum;
+      }
+      __syncthreads();
+    }
   }
 }
 

@@ -312,3 +312,15 @@ def test_gdn_layer_rejects_unsupported(mods):
     v = cell.init(0, (1, 2, 12, 12, 8))
     with pytest.raises(NotImplementedError):
         cell.apply(v, torch.zeros((1, 2, 12, 12, 8), device="cuda"))
+
+
+def test_gdn_layer_is_deterministic(mods):
+    """Two calls on the same input give bit-identical outputs (no order-dependent reductions)."""
+    cells, _ = mods
+    print_case(test="gdn_layer_deterministic")
+    kw = dict(delta_key_dim=4, gate_type="factored", qkv_conv_size=5)
+    cfg, p, x = _layer(kw, (2, 3, 128, 128, 16), 25)
+    cell = cells.GatedDeltaNetCSSM(channels=16, **kw)
+    v = cells.GatedDeltaNetCSSM.load_params(p)
+    xd = _dev(x)
+    assert torch.equal(cell.apply(v, xd), cell.apply(v, xd))
