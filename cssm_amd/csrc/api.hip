@@ -307,7 +307,10 @@ int cssm_gdn_qkv_post(void* qkv, int dtype, int B, int T, int C, int H, int W, i
       sc.b[i] = conv_bias[i];
     }
   }
-  if (gate_mode == 1 && !aligned(gates, 8)) return fail(CSSM_ERR_ALIGN, "cssm_gdn_qkv_post: gates must be 8-byte aligned");
+  if ((H * W) % 4) return fail(CSSM_ERR_UNSUPPORTED, "cssm_gdn_qkv_post: H*W=%d must be a multiple of 4", H * W);
+  if (!aligned(qkv, dtype == CSSM_F32 ? 16 : 8) || (gate_mode == 1 && !aligned(gates, 8)) ||
+      (gate_mode == 3 && !aligned(gates, 16)))
+    return fail(CSSM_ERR_ALIGN, "cssm_gdn_qkv_post: misaligned qkv / gates");
   return hip_status(cssm::launch_gdn_qkv_post(qkv, dtype, B, T, C, H * W, kt, sc, gate_mode, gates,
                                               static_cast<hipStream_t>(stream)),
                     "cssm_gdn_qkv_post");

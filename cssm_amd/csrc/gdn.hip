@@ -28,6 +28,12 @@ namespace {
 
 __device__ __forceinline__ float ld_f(const float* p, size_t i) { return p[i]; }
 __device__ __forceinline__ float ld_f(const uint16_t* p, size_t i) { return bf16_to_f32(p[i]); }
+__device__ __forceinline__ float4 ld4v(const float* p, size_t i) { return *reinterpret_cast<const float4*>(p + i); }
+__device__ __forceinline__ float4 ld4v(const uint16_t* p, size_t i) {
+  const uint2 v = *reinterpret_cast<const uint2*>(p + i);
+  return make_float4(bf16_to_f32(v.x & 0xffffu), bf16_to_f32(v.x >> 16), bf16_to_f32(v.y & 0xffffu),
+                     bf16_to_f32(v.y >> 16));
+}
 __device__ __forceinline__ void st_f(float* p, size_t i, float v) { p[i] = v; }
 __device__ __forceinline__ void st_f(uint16_t* p, size_t i, float v) { p[i] = uint16_t(f32_to_bf16(v)); }
 
@@ -423,23 +429,47 @@ hipError_t launch_gdn_scan_bins(const float2* spec, const float* norms, const fl
 // ---------------------------------------------------------------------------
 template <class TI>
 __global__ void __launch_bounds__(256) frame_mean_cl(const TI* __restrict__ x, int HW, int C, float* __restrict__ out) {
-  __shared__ float red[256];
+  __shared__ float4 red[256];
   const int f = blockIdx.x;
   const TI* xf = x + size_t(f) * HW * C;
-  for (int c0 = 0; c0 < C; c0 += 256) {
-    const int cw = min(256, C - c0);
-    const int rows = 256 / cw;          // pixels summed in parallel
-    const int r = threadIdx.x / cw, c = threadIdx.x % cw;
-    float acc = 0.0f;
+  const int cv = (C % 4 == 0) ? 4 : 1;
+  for (int c0 = 0; c0 < C; c0 += 256 * cv) {
+    const int cw = min(256, (C - c0) / cv);          // channel groups of this chunk
+    const int rows = 256 / cw;                        // pixels summed in parallel
+    const int r = threadIdx.x / cw, c = c0 + (threadIdx.x % cw) * cv;
+    float4 acc = make_float4(0.f, 0.f, 0.f, 0.f);
     if (r < rows) {
-      for (int p = r; p < HW; p += rows) acc += ld_f(xf, size_t(p) * C + c0 + c);
+      int p = r;
+      if (cv == 4) {
+        // 4 independent loads in flight per iteration
+        for (; p + 3 * rows < HW; p += 4 * rows) {
+          float4 v[4];
+#pragma unroll
+          for (int u = 0; u < 4; ++u) v[u] = ld4v(xf, size_t(p + u * rows) * C + c);
+#pragma unroll
+          for (int u = 0; u < 4; ++u) {
+            acc.x += v[u].x; acc.y += v[u].y; acc.z += v[u].z; acc.w += v[u].w;
+          }
+        }
+        for (; p < HW; p += rows) {
+          const float4 v = ld4v(xf, size_t(p) * C + c);
+          acc.x += v.x; acc.y += v.y; acc.z += v.z; acc.w += v.w;
+        }
+      } else {
+        for (; p < HW; p += rows) acc.x += ld_f(xf, size_t(p) * C + c);
+      }
     }
     red[threadIdx.x] = acc;
     __syncthreads();
     if (threadIdx.x < cw) {
-      float sum = 0.0f;
-      for (int i = 0; i < rows; ++i) sum += red[i * cw + threadIdx.x];
-      out[size_t(f) * C + c0 + threadIdx.x] = sum / float(HW);
+      float4 sum = make_float4(0.f, 0.f, 0.f, 0.f);
+      for (int i = 0; i < rows; ++i) {
+        const float4 v = red[i * cw + threadIdx.x];
+        sum.x += v.x; sum.y += v.y; sum.z += v.z; sum.w += v.w;
+      }
+      const float inv = 1.0f / float(HW);
+      const float e[4] = {sum.x, sum.y, sum.z, sum.w};
+      for (int k = 0; k < cv; ++k) out[size_t(f) * C + c0 + threadIdx.x * cv + k] = e[k] * inv;
     }
     __syncthreads();
   }
@@ -551,30 +581,47 @@ template <class TI, class TO>
 __global__ void __launch_bounds__(256)
 dwconv_cl(const TI* __restrict__ x, int H, int W, int C, int ks, const float* __restrict__ kw,
           const float* __restrict__ bias, TO* __restrict__ y, long long total) {
+  // one thread per (pixel, 4 consecutive channels) when C % 4 == 0, else per (pixel, channel)
+  const int cv = (C % 4 == 0) ? 4 : 1;
   const long long i = (long long)blockIdx.x * blockDim.x + threadIdx.x;
   if (i >= total) return;
-  const int c = int(i % C);
-  const long long pix = i / C;
+  const int CG = C / cv;
+  const int c0 = int(i % CG) * cv;
+  const long long pix = i / CG;
   const int w = int(pix % W), h = int((pix / W) % H);
   const long long f = pix / (size_t(H) * W);
   const int lo = (ks - 1) / 2;
   const TI* xf = x + size_t(f) * H * W * C;
-  float acc = bias[c];
+  float acc[4];
+#pragma unroll
+  for (int e = 0; e < 4; ++e) acc[e] = e < cv ? bias[c0 + e] : 0.0f;
   for (int a = 0; a < ks; ++a) {
     const int hh = h + a - lo;
     if (hh < 0 || hh >= H) continue;
     for (int b2 = 0; b2 < ks; ++b2) {
       const int ww = w + b2 - lo;
       if (ww < 0 || ww >= W) continue;
-      acc = fmaf(ld_f(xf, (size_t(hh) * W + ww) * C + c), kw[(a * ks + b2) * C + c], acc);
+      const size_t xi = (size_t(hh) * W + ww) * C + c0;
+      const float* kt = kw + (a * ks + b2) * C + c0;
+      if (cv == 4) {
+        const float4 xv = ld4v(xf, xi);
+        const float4 kv = *reinterpret_cast<const float4*>(kt);
+        acc[0] = fmaf(xv.x, kv.x, acc[0]);
+        acc[1] = fmaf(xv.y, kv.y, acc[1]);
+        acc[2] = fmaf(xv.z, kv.z, acc[2]);
+        acc[3] = fmaf(xv.w, kv.w, acc[3]);
+      } else {
+        acc[0] = fmaf(ld_f(xf, xi), kt[0], acc[0]);
+      }
     }
   }
-  st_f(y, size_t(i), acc);
+  const size_t o = size_t(pix) * C + c0;
+  for (int e = 0; e < cv; ++e) st_f(y, o + e, acc[e]);
 }
 
 hipError_t launch_depthwise_conv(const void* x, int dtype, int F, int H, int W, int C, int ks, const float* kw,
                                  const float* bias, void* y, int out_dtype, hipStream_t s) {
-  const long long total = (long long)F * H * W * C;
+  const long long total = (long long)F * H * W * (C % 4 == 0 ? C / 4 : C);
   const unsigned blocks = unsigned((total + 255) / 256);
   const dim3 g(blocks), b(256);
   if (dtype == 0 && out_dtype == 0)
@@ -605,66 +652,88 @@ hipError_t launch_depthwise_conv(const void* x, int dtype, int F, int H, int W, 
 // ---------------------------------------------------------------------------
 constexpr int kMaxShortConv = 8;
 
-template <class T>
+template <int KT, class T>
 __global__ void __launch_bounds__(256)
-gdn_qkv_post(T* __restrict__ qkv, int Tn, int C, int HW, int kt, GdnShortConv sc, int gate_mode,
-             const void* __restrict__ gates, long long total) {
+gdn_qkv_post(T* __restrict__ qkv, int Tn, int C, int HW, GdnShortConv sc, int gate_mode, const void* __restrict__ gates,
+             long long total) {
+  // one thread per (b, channel, 4 pixels); HW % 4 == 0 (checked by the launcher)
   const long long i = (long long)blockIdx.x * blockDim.x + threadIdx.x;
   if (i >= total) return;
-  const int p = int(i % HW);
-  const int c3 = int((i / HW) % (3 * C));
-  const int b = int(i / (size_t(HW) * 3 * C));
+  const int HW4 = HW / 4;
+  const int p = int(i % HW4) * 4;
+  const int c3 = int((i / HW4) % (3 * C));
+  const int b = int(i / (size_t(HW4) * 3 * C));
   const int blk = c3 / C, c = c3 % C;
-  const float* wt = sc.w[blk];
-  const float bt = kt > 0 ? sc.b[blk][c] : 0.0f;
-  float hist[kMaxShortConv];
+  float w[KT > 0 ? KT : 1];
 #pragma unroll
-  for (int j = 0; j < kMaxShortConv; ++j) hist[j] = 0.0f;
+  for (int j = 0; j < KT; ++j) w[j] = sc.w[blk][j * C + c];
+  const float bt = KT > 0 ? sc.b[blk][c] : 0.0f;
+  float4 hist[KT > 1 ? KT - 1 : 1];   // x_{t-KT+1} .. x_{t-1}
+#pragma unroll
+  for (int j = 0; j < (KT > 1 ? KT - 1 : 1); ++j) hist[j] = make_float4(0.f, 0.f, 0.f, 0.f);
   for (int t = 0; t < Tn; ++t) {
     const size_t fr = size_t(b) * Tn + t;
     const size_t idx = (fr * 3 * C + c3) * HW + p;
-    float v = ld_f(qkv, idx);
-    if (kt > 0) {
-      // hist[j] = x_{t - kt + 1 + j} for j < kt - 1; the new input is j = kt - 1
-      float o = fmaf(wt[(kt - 1) * C + c], v, bt);
+    float4 v = ld4v(qkv, idx);
+    if (KT > 0) {
+      float o[4] = {bt, bt, bt, bt};
+      const float vin[4] = {v.x, v.y, v.z, v.w};
 #pragma unroll
-      for (int j = 0; j < kMaxShortConv - 1; ++j)
-        if (j < kt - 1) o = fmaf(wt[j * C + c], hist[j], o);
+      for (int e = 0; e < 4; ++e) o[e] = fmaf(w[KT - 1], vin[e], o[e]);
 #pragma unroll
-      for (int j = 0; j < kMaxShortConv - 2; ++j)
-        if (j < kt - 2) hist[j] = hist[j + 1];
-      if (kt >= 2) hist[kt - 2] = v;
-      v = o / (1.0f + expf(-o));
+      for (int j = 0; j < KT - 1; ++j) {
+        const float hv[4] = {hist[j].x, hist[j].y, hist[j].z, hist[j].w};
+#pragma unroll
+        for (int e = 0; e < 4; ++e) o[e] = fmaf(w[j], hv[e], o[e]);
+      }
+#pragma unroll
+      for (int j = 0; j + 1 < KT - 1; ++j) hist[j] = hist[j + 1];
+      if (KT > 1) hist[KT > 1 ? KT - 2 : 0] = v;
+#pragma unroll
+      for (int e = 0; e < 4; ++e) o[e] = o[e] / (1.0f + expf(-o[e]));
+      v = make_float4(o[0], o[1], o[2], o[3]);
     }
     if (blk > 0 && gate_mode != 0) {
-      float g;
+      float4 g;
       if (gate_mode == 1) {
-        const float2 gg = static_cast<const float2*>(gates)[fr * HW + p];
-        g = blk == 1 ? gg.x : gg.y;
+        const float2* gp = static_cast<const float2*>(gates) + fr * HW + p;
+        g = blk == 1 ? make_float4(gp[0].x, gp[1].x, gp[2].x, gp[3].x) : make_float4(gp[0].y, gp[1].y, gp[2].y, gp[3].y);
       } else if (gate_mode == 2) {
         const float2 gg = static_cast<const float2*>(gates)[fr];
-        g = blk == 1 ? gg.x : gg.y;
+        const float gs = blk == 1 ? gg.x : gg.y;
+        g = make_float4(gs, gs, gs, gs);
       } else {
-        g = static_cast<const float*>(gates)[(fr * 2 * C + size_t(blk - 1) * C + c) * HW + p];
+        g = *reinterpret_cast<const float4*>(static_cast<const float*>(gates) +
+                                             (fr * 2 * C + size_t(blk - 1) * C + c) * HW + p);
       }
-      v *= g;
+      v = make_float4(v.x * g.x, v.y * g.y, v.z * g.z, v.w * g.w);
     }
-    st_f(qkv, idx, v);
+    const float vo[4] = {v.x, v.y, v.z, v.w};
+#pragma unroll
+    for (int e = 0; e < 4; ++e) st_f(qkv, idx + e, vo[e]);
   }
+}
+
+template <class T>
+static hipError_t run_qkv_post(T* qkv, int B, int Tn, int C, int HW, int kt, const GdnShortConv& sc, int gate_mode,
+                               const void* gates, hipStream_t s) {
+  const long long total = (long long)B * 3 * C * (HW / 4);
+  const dim3 g(unsigned((total + 255) / 256)), b(256);
+  switch (kt) {
+#define CSSM_KT(K) \
+  case K: hipLaunchKernelGGL((gdn_qkv_post<K, T>), g, b, 0, s, qkv, Tn, C, HW, sc, gate_mode, gates, total); break;
+    CSSM_KT(0) CSSM_KT(1) CSSM_KT(2) CSSM_KT(3) CSSM_KT(4) CSSM_KT(5) CSSM_KT(6) CSSM_KT(7) CSSM_KT(8)
+#undef CSSM_KT
+    default: return hipErrorInvalidValue;
+  }
+  return hipGetLastError();
 }
 
 hipError_t launch_gdn_qkv_post(void* qkv, int dtype, int B, int T, int C, int HW, int kt, const GdnShortConv& sc,
                                int gate_mode, const void* gates, hipStream_t s) {
-  if (kt > kMaxShortConv) return hipErrorInvalidValue;
-  const long long total = (long long)B * 3 * C * HW;
-  const unsigned blocks = unsigned((total + 255) / 256);
-  if (dtype == 0)
-    hipLaunchKernelGGL(gdn_qkv_post<float>, dim3(blocks), dim3(256), 0, s, static_cast<float*>(qkv), T, C, HW, kt, sc,
-                       gate_mode, gates, total);
-  else
-    hipLaunchKernelGGL(gdn_qkv_post<uint16_t>, dim3(blocks), dim3(256), 0, s, static_cast<uint16_t*>(qkv), T, C, HW,
-                       kt, sc, gate_mode, gates, total);
-  return hipGetLastError();
+  if (kt > kMaxShortConv || HW % 4) return hipErrorInvalidValue;
+  if (dtype == 0) return run_qkv_post(static_cast<float*>(qkv), B, T, C, HW, kt, sc, gate_mode, gates, s);
+  return run_qkv_post(static_cast<uint16_t*>(qkv), B, T, C, HW, kt, sc, gate_mode, gates, s);
 }
 
 }  // namespace cssm
