@@ -28,6 +28,8 @@ namespace cssm {
 struct IoF32 {
   using T = float;
   using V4 = float4;
+  static __device__ __forceinline__ float to_f(const float v) { return v; }
+  static __device__ __forceinline__ float from_f(const float v) { return v; }
   static __device__ __forceinline__ float4 to_f4(const float4 v) { return v; }
   static __device__ __forceinline__ float4 from_f4(const float4 v) { return v; }
 };
@@ -45,6 +47,8 @@ __device__ __forceinline__ uint32_t f32_to_bf16(float f) {
 struct IoBF16 {
   using T = uint16_t;
   using V4 = uint2;   // 4 x bf16
+  static __device__ __forceinline__ float to_f(const uint16_t v) { return bf16_to_f32(v); }
+  static __device__ __forceinline__ uint16_t from_f(const float v) { return uint16_t(f32_to_bf16(v)); }
   static __device__ __forceinline__ float4 to_f4(const uint2 v) {
     return make_float4(bf16_to_f32(v.x & 0xffffu), bf16_to_f32(v.x >> 16),
                        bf16_to_f32(v.y & 0xffffu), bf16_to_f32(v.y >> 16));

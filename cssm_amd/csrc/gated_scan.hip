@@ -190,6 +190,173 @@ gated_scan_pow2(const ScanArgs a) {
   }
 }
 
+
+// ---------------------------------------------------------------------------
+// Small planes of any size up to 16 x 16 (the CSSM-SHViT stage shapes 14 x 14
+// and 7 x 7 are not powers of two): direct DFTs through LDS.
+//
+// A workgroup owns NP consecutive planes of the flattened (b, c) index (the
+// last group may be partial; a group may span two batch elements) for all T
+// steps.  Per step:
+//   rows   R[pl][h][v] = sum_w x[h][w] e^{-2 pi i v w / W}            (v < Wf)
+//   cols   X[pl][u][v] = sum_h R[h][v] e^{-2 pi i u h / H}   (each thread owns
+//          fixed bins, so the state h of its bins stays in registers)
+//   scan   h = floor(K_hat) e^{-Delta} h + (Delta + 1e-8) floor(X B);  S = C h / (H W)
+//   icols  Z[pl][h][v] = sum_u S[u][v] e^{+2 pi i u h / H}
+//   C2R    y[h][w] = Re Z[h][0] + 2 sum_{0 < v < W/2} Re(Z[h][v] e^{2 pi i v w / W})
+//                    + [W even] (-1)^w Re Z[h][W/2]                 (numpy irfft2)
+//   store  y * z_gate
+// Twiddles come from double-precision tables in LDS.
+// ---------------------------------------------------------------------------
+__device__ __forceinline__ float2 scan_bin_plain(float2& h, float2 U, float4 g, float2 kh) {
+  float2 V = make_float2(U.x * g.y, U.y * g.y);
+  if (V.x * V.x + V.y * V.y < g.z * g.z) V = make_float2(g.z, 0.0f);
+  const float2 A = make_float2(kh.x * g.x, kh.y * g.x);
+  const float2 hn = make_float2(fmaf(A.x, h.x, fmaf(-A.y, h.y, V.x)), fmaf(A.x, h.y, fmaf(A.y, h.x, V.y)));
+  h = hn;
+  return make_float2(hn.x * g.w, hn.y * g.w);
+}
+
+constexpr int cx_gcd(int a, int b) { return b == 0 ? a : cx_gcd(b, a % b); }
+
+template <int H, int W>
+struct SmallGeom {
+  static constexpr int WF = W / 2 + 1, HW = H * W, NT = 256;
+  // the smallest group with whole bins per thread, at most 64 planes (LDS)
+  static constexpr int NP0 = NT / cx_gcd(NT, H * WF);
+  static constexpr int NP = NP0 < 64 ? NP0 : 64;
+  static constexpr int NB = NP * H * WF, JB = (NB + NT - 1) / NT;   // bins per group / per thread
+  static constexpr int NX = NP * HW;                                // samples per group
+  static_assert(NX * 4 + 2 * NB * 8 + (WF * W + H * H) * 8 + NP * 12 <= 160 * 1024, "small-plane group exceeds LDS");
+};
+
+template <int H, int W, class IO>
+__global__ void __launch_bounds__(256) gated_scan_small(const ScanArgs a, long long P) {
+  using G = SmallGeom<H, W>;
+  constexpr int WF = G::WF, HW = G::HW, NT = G::NT, NP = G::NP, JB = G::JB;
+  using TE = typename IO::T;
+  __shared__ float xs[G::NX];            // input / output planes
+  __shared__ float2 rs[G::NB];           // row spectra, then the inverse column output
+  __shared__ float2 ss[G::NB];           // readout spectra
+  __shared__ float2 twW[WF * W];         // e^{-2 pi i v w / W}
+  __shared__ float2 twH[H * H];          // e^{-2 pi i u h / H}
+  __shared__ long long base_u[NP];       // element offset of plane pl at t = 0: (b T C + c) HW
+  __shared__ int gate_b[NP];             // batch index of plane pl (-1: beyond P)
+
+  const int T = a.T, C = a.C;
+  const int tid = threadIdx.x;
+  const long long p0 = (long long)blockIdx.x * NP;
+  for (int i = tid; i < WF * W; i += NT) {
+    double sn, cs;
+    sincospi(2.0 * double((i / W) * (i % W) % W) / double(W), &sn, &cs);
+    twW[i] = make_float2(float(cs), float(-sn));
+  }
+  for (int i = tid; i < H * H; i += NT) {
+    double sn, cs;
+    sincospi(2.0 * double((i / H) * (i % H) % H) / double(H), &sn, &cs);
+    twH[i] = make_float2(float(cs), float(-sn));
+  }
+  for (int i = tid; i < NP; i += NT) {
+    const long long pp = p0 + i;
+    const int b = int(pp / C), c = int(pp % C);
+    gate_b[i] = pp < P ? b : -1;
+    base_u[i] = pp < P ? ((long long)b * T * C + c) * HW : 0;
+  }
+  const TE* __restrict__ up = static_cast<const TE*>(a.u);
+  const TE* __restrict__ zp = static_cast<const TE*>(a.z);
+  TE* __restrict__ yp = static_cast<TE*>(a.y);
+  const size_t tstride = size_t(C) * HW;   // one time step
+
+  float2 h[JB];
+#pragma unroll
+  for (int j = 0; j < JB; ++j) h[j] = make_float2(0.f, 0.f);
+  __syncthreads();
+
+  for (int t = 0; t < T; ++t) {
+    // load u_t (act) into xs
+    for (int e = tid; e < G::NX; e += NT) {
+      const int pl = e / HW, px = e % HW;
+      float v = 0.0f;
+      if (gate_b[pl] >= 0) {
+        v = IO::to_f(up[size_t(base_u[pl]) + t * tstride + px]);
+        if (a.u_act == 1) v = silu_f(v);
+      }
+      xs[e] = v;
+    }
+    __syncthreads();
+    // rows: R[pl][h][v]
+    for (int o = tid; o < G::NB; o += NT) {
+      const int pl = o / (H * WF), r = o % (H * WF), hh = r / WF, v = r % WF;
+      const float* xr = xs + pl * HW + hh * W;
+      float re = 0.f, im = 0.f;
+#pragma unroll
+      for (int w = 0; w < W; ++w) {
+        const float2 tw = twW[v * W + w];
+        re = fmaf(xr[w], tw.x, re);
+        im = fmaf(xr[w], tw.y, im);
+      }
+      rs[o] = make_float2(re, im);
+    }
+    __syncthreads();
+    // columns + recurrence for the thread's bins (pl, u, v) = j NT + tid
+#pragma unroll
+    for (int j = 0; j < JB; ++j) {
+      const int o = j * NT + tid;
+      if (JB * NT != G::NB && o >= G::NB) continue;
+      const int pl = o / (H * WF), r = o % (H * WF), u = r / WF, v = r % WF;
+      float2 X = make_float2(0.f, 0.f);
+#pragma unroll
+      for (int hh = 0; hh < H; ++hh) {
+        const float2 R = rs[pl * H * WF + hh * WF + v], tw = twH[u * H + hh];
+        X.x = fmaf(R.x, tw.x, fmaf(-R.y, tw.y, X.x));
+        X.y = fmaf(R.x, tw.y, fmaf(R.y, tw.x, X.y));
+      }
+      float2 Sv = make_float2(0.f, 0.f);
+      const int b = gate_b[pl];
+      if (b >= 0) {
+        const int c = int((p0 + pl) % C);
+        const float4 g = a.gates[(size_t(b) * T + t) * (H * WF) + r];
+        const float2 kh = a.khat[size_t(c) * (H * WF) + r];
+        Sv = scan_bin_plain(h[j], X, g, kh);
+      }
+      ss[o] = Sv;
+    }
+    __syncthreads();
+    // inverse columns: Z[pl][h][v] = sum_u S[u][v] conj(tw[u h])
+    for (int o = tid; o < G::NB; o += NT) {
+      const int pl = o / (H * WF), r = o % (H * WF), hh = r / WF, v = r % WF;
+      float2 Z = make_float2(0.f, 0.f);
+#pragma unroll
+      for (int u = 0; u < H; ++u) {
+        const float2 Sv = ss[pl * H * WF + u * WF + v], tw = twH[u * H + hh];
+        Z.x = fmaf(Sv.x, tw.x, fmaf(Sv.y, tw.y, Z.x));
+        Z.y = fmaf(Sv.y, tw.x, fmaf(-Sv.x, tw.y, Z.y));
+      }
+      rs[o] = Z;
+    }
+    __syncthreads();
+    // C2R rows, x z_gate, store y_t
+    for (int e = tid; e < G::NX; e += NT) {
+      const int pl = e / HW, px = e % HW, hh = px / W, w = px % W;
+      if (gate_b[pl] < 0) continue;
+      const float2* zr = rs + pl * H * WF + hh * WF;
+      float y = zr[0].x;
+#pragma unroll
+      for (int v = 1; v < WF; ++v) {
+        // Re(Z e^{+2 pi i v w / W}) = Z.x cos + ... with tw = e^{-...}: Re(Z conj(tw))
+        const float2 tw = twW[v * W + w];
+        const float re = fmaf(zr[v].x, tw.x, zr[v].y * tw.y);
+        y = (W % 2 == 0 && v == W / 2) ? y + re : fmaf(2.0f, re, y);
+      }
+      const size_t gi = size_t(base_u[pl]) + t * tstride + px;
+      float zg = IO::to_f(zp[gi]);
+      if (a.z_act == 1) zg = silu_f(zg);
+      yp[gi] = IO::from_f(y * zg);
+    }
+    __syncthreads();
+  }
+}
+
 // ----------------------------------------------------------------- launchers
 
 template <int LH, int LW, int NP, int PPT, class IO>
@@ -204,8 +371,32 @@ static hipError_t run_scan(const ScanArgs& a, int B, hipStream_t s) {
 // divides C (one batch element per workgroup).  The largest group that still
 // gives >= 512 workgroups wins; small planes need large groups to fill a
 // workgroup with whole waves.
+template <int H, class IO>
+static hipError_t run_small(const ScanArgs& a, int B, hipStream_t s) {
+  using G = SmallGeom<H, H>;
+  const long long P = (long long)B * a.C;
+  hipLaunchKernelGGL((gated_scan_small<H, H, IO>), dim3(unsigned((P + G::NP - 1) / G::NP)), dim3(G::NT), 0, s, a, P);
+  return hipGetLastError();
+}
+
 template <class IO>
 static hipError_t dispatch_scan(const ScanArgs& a, int B, int H, int W, hipStream_t s) {
+  if (H == W && (H & (H - 1)) != 0) {
+    switch (H) {
+      case 3: return run_small<3, IO>(a, B, s);
+      case 5: return run_small<5, IO>(a, B, s);
+      case 6: return run_small<6, IO>(a, B, s);
+      case 7: return run_small<7, IO>(a, B, s);
+      case 9: return run_small<9, IO>(a, B, s);
+      case 10: return run_small<10, IO>(a, B, s);
+      case 11: return run_small<11, IO>(a, B, s);
+      case 12: return run_small<12, IO>(a, B, s);
+      case 13: return run_small<13, IO>(a, B, s);
+      case 14: return run_small<14, IO>(a, B, s);
+      case 15: return run_small<15, IO>(a, B, s);
+      default: return hipErrorInvalidValue;
+    }
+  }
   const int C = a.C;
   auto pick = [&](std::initializer_list<int> nps) -> int {
     int best = 0;
@@ -233,20 +424,27 @@ static hipError_t dispatch_scan(const ScanArgs& a, int B, int H, int W, hipStrea
   } else if (H == 8 && W == 8) {
     const int np = pick({32});
     CSSM_SCAN_CASE(3, 32, 32)
+    return run_small<8, IO>(a, B, s);        // C not a multiple of 32: direct DFTs
   } else if (H == 4 && W == 4) {
     const int np = pick({128});
     CSSM_SCAN_CASE(2, 128, 32)
+    return run_small<4, IO>(a, B, s);        // C not a multiple of 128: direct DFTs
   }
 #undef CSSM_SCAN_CASE
   return hipErrorInvalidValue;
 }
 
 bool gated_scan_has_kernel(int H, int W) {
-  return H == W && (H == 4 || H == 8 || H == 16 || H == 32 || H == 64 || H == 128);
+  if (H != W) return false;
+  if (H == 4 || H == 8 || H == 16 || H == 32 || H == 64 || H == 128) return true;
+  return H >= 3 && H <= 15;   // direct-DFT small-plane kernel
 }
 
 int gated_scan_min_group(int H, int W) {
   if (H != W) return 0;
+  if (H >= 3 && H <= 15 && H != 16) {
+    if ((H & (H - 1)) != 0 || H == 4 || H == 8) return 1;   // direct-DFT kernel: any C
+  }
   switch (H) {
     case 128: return 1;
     case 64: return 1;

@@ -283,8 +283,10 @@ hipError_t dispatch_inv(const float2* spec, long long P, int H, void* y, hipStre
 
 }  // namespace
 
-// any plane count: a partial last group is masked
-int fft_planes_min_group(int H, int W) { return gated_scan_min_group(H, W) ? 1 : 0; }
+// power-of-two planes 4..128, any plane count (a partial last group is masked)
+int fft_planes_min_group(int H, int W) {
+  return (H == W && H >= 4 && H <= 128 && (H & (H - 1)) == 0) ? 1 : 0;
+}
 
 hipError_t launch_rfft2(const void* x, int dtype, long long P, int H, int W, float2* spec, float* norms,
                         hipStream_t s) {

@@ -136,9 +136,11 @@ int cssm_gated_gates(const float* ctx, int B, int T, int C, int H, int W,
  *             (the irfft2 normalisation folded into C); dense and factored
  *             gate_type both arrive in this per-bin form.
  *   khat      from cssm_spectral_kernel with goom_floor = 1, C channels
- * Supported planes: H = W in {4, 8, 16, 32, 64, 128}, with C a multiple of
- * cssm_gated_scan_min_group(H, W).  u, z, y must be 16-byte aligned (f32) or
- * 8-byte aligned (bf16); gates 16; khat 8.
+ * Supported planes: H = W in {4, 8, 16, 32, 64, 128} (in-register FFT passes
+ * through LDS; C a multiple of cssm_gated_scan_min_group(H, W)) and any
+ * H = W in 3..15 (direct DFTs, any C) -- the CSSM-SHViT stage shapes 14 x 14
+ * and 7 x 7.  u, z, y must be 16-byte aligned (f32) or 8-byte aligned (bf16);
+ * gates 16; khat 8.
  */
 int cssm_gated_scan_fwd(const void* u, const void* z, void* y, int dtype, int B, int T, int C,
                         int H, int W, const float* gates, const float* khat, int u_act,

@@ -41,14 +41,14 @@ def test_abi_version_and_errors_without_gpu():
     assert b"non-null" in lib.cssm_last_error()
     buf = ctypes.create_string_buffer(64)
     p = ctypes.addressof(buf)
-    st = lib.cssm_gated_scan_fwd(p, p, p, 0, 1, 1, 32, 12, 12, p, p, 0, 0, None)
+    st = lib.cssm_gated_scan_fwd(p, p, p, 0, 1, 1, 32, 24, 24, p, p, 0, 0, None)
     assert st == -3 and b"no fused kernel" in lib.cssm_last_error()
     st = lib.cssm_gated_scan_fwd(p, p, p, 7, 1, 1, 32, 8, 8, p, p, 0, 0, None)
     assert st == -4
     st = lib.cssm_gated_scan_fwd(p + 4, p, p, 0, 1, 1, 32, 8, 8, p, p, 0, 0, None)
     assert st == -5
-    st = lib.cssm_gated_scan_fwd(p, p, p, 0, 1, 1, 8, 8, 8, p, p, 0, 0, None)
-    assert st == -3 and b"multiple of 32" in lib.cssm_last_error()
+    st = lib.cssm_gated_scan_fwd(p, p, p, 0, 1, 1, 4, 16, 16, p, p, 0, 0, None)
+    assert st == -3 and b"multiple of 8" in lib.cssm_last_error()
     st = lib.cssm_gated_scan_fwd(p, p, p, 0, 1, 1, 32, 8, 8, p, p, 2, 0, None)
     assert st == -4
     st = lib.cssm_spectral_kernel(p, 1, 11, 8, 16, 0.9, 1, 1, p, None)

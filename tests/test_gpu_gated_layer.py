@@ -90,6 +90,18 @@ LAYER_CASES = [
           short_conv_spatial_size=0)),
     ("dense_64_k15_crop", (2, 2, 64, 64, 8),
      dict(channels=8, kernel_size=15, gate_type="dense", short_conv_size=2, short_conv_spatial_size=0)),
+    # CSSM-SHViT-shaped stage layers (configs C5): T = 1, K = 1, expand 2
+    ("c5_stage1_14", (4, 1, 14, 14, 32),
+     dict(channels=32, expand=2, kernel_size=1, gate_type="factored", short_conv_size=0,
+          short_conv_spatial_size=0)),
+    ("c5_stage2_7", (4, 1, 7, 7, 56),
+     dict(channels=56, expand=2, kernel_size=1, gate_type="factored", short_conv_size=0,
+          short_conv_spatial_size=0)),
+    ("c5_stage3_4", (4, 1, 4, 4, 80),
+     dict(channels=80, expand=2, kernel_size=1, gate_type="factored", short_conv_size=0,
+          short_conv_spatial_size=0)),
+    ("small_7_T3_convs", (2, 3, 7, 7, 12),
+     dict(channels=12, kernel_size=11, gate_type="dense", short_conv_size=3, short_conv_spatial_size=3)),
 ]
 
 

@@ -111,6 +111,10 @@ SCAN_CASES = [
     # (B, T, C, H, W)
     (2, 1, 128, 4, 4), (1, 3, 128, 4, 4), (2, 3, 32, 8, 8), (2, 4, 16, 16, 16), (1, 3, 8, 32, 32),
     (2, 5, 8, 32, 32), (1, 3, 4, 64, 64), (2, 2, 2, 64, 64), (1, 3, 2, 128, 128), (2, 8, 1, 128, 128),
+    # direct-DFT small planes (CSSM-SHViT stage shapes and odd sizes); groups span batch
+    # elements and the last group is partial
+    (3, 2, 20, 14, 14), (2, 3, 40, 7, 7), (1, 1, 8, 12, 12), (2, 2, 5, 5, 5), (1, 3, 33, 15, 15),
+    (2, 2, 3, 9, 9), (1, 2, 70, 6, 6), (2, 1, 4, 3, 3),
 ]
 
 
@@ -129,13 +133,13 @@ def test_gated_scan_matches_oracle(S, B, T, C, H, W):
     assert rel_err(to_np(y), ref) <= TOL_F32
 
 
-@pytest.mark.parametrize("H", [8, 32, 128])
+@pytest.mark.parametrize("H", [8, 32, 128, 14])
 def test_gated_scan_goom_floor_zero_inputs(S, H):
     """Exact zeros (a zero frame, a zero B row) take to_goom's 1e-7 floor."""
     print_case(test="gated_scan_floor", H=H)
     rng = np.random.default_rng(5)
     B, T, W = 1, 4, H
-    C = {8: 32, 32: 8, 128: 2}[H]
+    C = {8: 32, 32: 8, 128: 2, 14: 4}[H]
     xm = rng.standard_normal((B, T, C, H, W))
     xm[:, 0] = 0.0
     zg = rng.standard_normal((B, T, C, H, W))
@@ -149,7 +153,8 @@ def test_gated_scan_goom_floor_zero_inputs(S, H):
     assert rel_err(y0, ref[:, 0]) <= TOL_F32
 
 
-@pytest.mark.parametrize("B,T,C,H,W", [(2, 4, 8, 32, 32), (1, 3, 2, 128, 128), (2, 2, 16, 16, 16)])
+@pytest.mark.parametrize("B,T,C,H,W", [(2, 4, 8, 32, 32), (1, 3, 2, 128, 128), (2, 2, 16, 16, 16),
+                                       (2, 1, 48, 14, 14), (2, 2, 24, 7, 7)])
 def test_gated_scan_bf16_io(S, B, T, C, H, W):
     print_case(test="gated_scan_bf16", B=B, T=T, C=C, H=H, W=W)
     rng = np.random.default_rng(99)
@@ -196,8 +201,8 @@ def test_gated_scan_c2_full_size_sampled(S):
 def test_gated_scan_rejects_bad_input(S):
     from cssm_amd._lib import CssmError
     print_case(test="gated_scan_errors")
-    u = torch.zeros((1, 1, 1, 12, 12), device="cuda")
-    gates = torch.zeros((1, 1, 12, 7, 4), device="cuda")
-    kh = torch.zeros((1, 12, 7), dtype=torch.complex64, device="cuda")
+    u = torch.zeros((1, 1, 1, 24, 24), device="cuda")
+    gates = torch.zeros((1, 1, 24, 13, 4), device="cuda")
+    kh = torch.zeros((1, 24, 13), dtype=torch.complex64, device="cuda")
     with pytest.raises(CssmError, match="no fused kernel"):
         S.gated_scan(u, u, gates, kh)
