@@ -50,6 +50,10 @@ WORKLOADS = {
                qkv_conv_size=5, gate_type="factored", io="f32", data="normal"),
     "c4": dict(cell="gdn", name="C4 GDN video d_k=4 32x32 T=32 bf16", B=128, T=32, H=32, W=32, C=64, dk=4,
                kernel_size=11, qkv_conv_size=1, gate_type="factored", io="bf16", data="dots"),
+    # CSSM-SHViT-S1-shaped stack: (H, C, layers) per stage, each layer GatedCSSM with expand 2
+    "c5": dict(cell="stack", name="C5 gated CSSM-SHViT-shaped stack (11 layers) T=1 bf16", B=512, T=1,
+               stages=((14, 128, 2), (7, 224, 4), (4, 320, 5)), H=14, W=14, C=128, expand=2, kernel_size=1,
+               gate_type="factored", io="bf16", data="normal"),
 }
 
 
@@ -76,6 +80,8 @@ def io_bytes(w):
 
 
 def algorithmic_bytes(w, B):
+    if w["cell"] == "stack":
+        return sum(n * algorithmic_bytes(dict(w, cell="gated", H=h, W=h, C=c), B) for h, c, n in w["stages"])
     T, H, W = w["T"], w["H"], w["W"]
     Wf = W // 2 + 1
     s = io_bytes(w)
@@ -124,6 +130,8 @@ def make_input(w, B, torch, dev):
 
 
 def make_cell(w, cells):
+    if w["cell"] == "stack":
+        return [[make_cell(dict(w, cell="gated", H=h, W=h, C=c), cells) for _ in range(n)] for h, c, n in w["stages"]]
     if w["cell"] == "gated":
         return cells.GatedCSSM(channels=w["C"], expand=w["expand"], kernel_size=w["kernel_size"],
                                gate_type=w["gate_type"], short_conv_size=0, short_conv_spatial_size=0)
@@ -156,23 +164,37 @@ class Marks:
         return [(self.seq[i + 1][0], self.seq[i][1], self.seq[i + 1][1]) for i in range(len(self.seq) - 1)]
 
 
-def gated_step(cell, variables, x, w, S, mark):
+def gated_step(cell, variables, x, w, S, mark, start=True):
     """The calls GatedCSSM.apply makes (short convolutions off), with a mark after each kernel."""
+    import torch
     p = variables["params"]
     B, T, H, W, _ = x.shape
     Ci, F, HW = cell.channels * cell.expand, B * T, H * W
-    mark("start")
+    if start:
+        mark("start")
     u, z, ctx = S.proj_in(x, p["in_proj"]["kernel"], p["in_proj"]["bias"], F, HW, silu_lo=True, silu_hi=True,
-                          want_ctx=True)
+                          want_ctx=True, out_dtype=torch.float32)
     mark("in_proj")
     gates = S.gated_gates(ctx.view(B, T, Ci), p, H, W, cell.gate_type, cell.gate_activation, c_scale=1.0 / HW)
     khat = cell.spectral_kernel(p, H, W)
     mark("gates")
     y = S.gated_scan(u.view(B, T, Ci, H, W), z.view(B, T, Ci, H, W), gates, khat)
     mark("scan")
-    out = S.proj_out(y.view(F, Ci, HW), p["out_proj"]["kernel"], p["out_proj"]["bias"])
+    out = S.proj_out(y.view(F, Ci, HW), p["out_proj"]["kernel"], p["out_proj"]["bias"], out_dtype=x.dtype)
     mark("out_proj")
     return out.view(B, T, H, W, cell.channels)
+
+
+def stack_step(cells_, variables, xs, w, S, mark):
+    """Every stage's layers back to back (stage inputs are synthetic: the reference's downsampling
+    between stages is outside the layer); returns the last stage's output."""
+    mark("start")
+    out = None
+    for stage, (layer_cells, layer_vars, x) in enumerate(zip(cells_, variables, xs)):
+        for cell, v in zip(layer_cells, layer_vars):
+            x = gated_step(cell, v, x, w, S, mark, start=False)
+        out = x
+    return out
 
 
 def gdn_step(cell, variables, x, w, S, mark):
@@ -223,6 +245,31 @@ def cpu_baseline(w, seconds):
         limiter = None
     rng = np.random.default_rng(1)
     T, H, W, C = w["T"], w["H"], w["W"], w["C"]
+    if w["cell"] == "stack":
+        layers = []
+        for h, c, n in w["stages"]:
+            cfg = O.GatedConfig(channels=c, expand=w["expand"], kernel_size=w["kernel_size"],
+                                gate_type=w["gate_type"], short_conv_size=0, short_conv_spatial_size=0)
+            layers += [(O.init_params(O.gated_param_shapes(cfg, c, h, h), rng), cfg, h, c) for _ in range(n)]
+        xs = {(h, c): rng.standard_normal((1, T, h, h, c)) for _, _, h, c in layers}
+
+        def run(_):
+            for p_, cfg_, h_, c_ in layers:
+                O.gated_forward(p_, xs[(h_, c_)], cfg_)
+        x = None
+        frames, t0 = 0, time.perf_counter()
+        while True:
+            run(x)
+            frames += T
+            el = time.perf_counter() - t0
+            if el >= seconds:
+                break
+        if limiter is not None and hasattr(limiter, "unregister"):
+            limiter.unregister()
+        return dict(value=frames / el, unit="frames/s", cores=1, kind="port",
+                    sample=f"{frames // T} batch element(s) (of B={w['B']}) through all "
+                           f"{len(layers)} layers, float64 numpy oracle, {el:.1f} s, "
+                           f"{platform.processor() or platform.machine()} x{os.cpu_count()} logical cpus")
     if w["cell"] == "gated":
         cfg = O.GatedConfig(channels=C, expand=w["expand"], kernel_size=w["kernel_size"], gate_type=w["gate_type"],
                             short_conv_size=0, short_conv_spatial_size=0)
@@ -281,12 +328,19 @@ def main():
         torch.cuda.synchronize()
         del src, dst
     torch.manual_seed(0)
-    x = make_input(w, B, torch, dev)
     cell = make_cell(w, cells)
-    variables = cell.init(1, x.shape)
-    randomise_biases(variables, torch, dev)
-    step = gated_step if w["cell"] == "gated" else gdn_step
-    core = ("scan",) if w["cell"] == "gated" else ("rfft2", "scan_bins", "irfft2")
+    if w["cell"] == "stack":
+        x = [make_input(dict(w, H=h, W=h, C=c), B, torch, dev) for h, c, _ in w["stages"]]
+        variables = [[cl.init(1 + i, xs.shape) for i, cl in enumerate(layer)] for layer, xs in zip(cell, x)]
+        for layer in variables:
+            for v in layer:
+                randomise_biases(v, torch, dev)
+    else:
+        x = make_input(w, B, torch, dev)
+        variables = cell.init(1, x.shape)
+        randomise_biases(variables, torch, dev)
+    step = {"gated": gated_step, "gdn": gdn_step, "stack": stack_step}[w["cell"]]
+    core = ("scan",) if w["cell"] in ("gated", "stack") else ("rfft2", "scan_bins", "irfft2")
 
     for _ in range(args.warmup):
         step(cell, variables, x, w, S, Marks(torch, False))
@@ -301,7 +355,15 @@ def main():
     el = time.perf_counter() - t0
     ms_step = el * 1e3 / args.steps
     # the instrumented step must equal the module's forward bit for bit
-    if not torch.equal(step(cell, variables, x, w, S, Marks(torch, False)), cell.apply(variables, x)):
+    if w["cell"] == "stack":
+        ref = None
+        for layer_cells, layer_vars, xs in zip(cell, variables, x):
+            for cl, v in zip(layer_cells, layer_vars):
+                xs = cl.apply(v, xs)
+            ref = xs
+    else:
+        ref = cell.apply(variables, x)
+    if not torch.equal(step(cell, variables, x, w, S, Marks(torch, False)), ref):
         print("instrumented step differs from the module's apply", file=sys.stderr)
         sys.exit(1)
     kern_ms = {}
@@ -311,7 +373,7 @@ def main():
     core_ms = sum(kern_ms[k] for k in core)
     alg = algorithmic_bytes(w, B)
     achieved = alg / (core_ms * 1e-3) / 1e9
-    kname = "gated_scan" if w["cell"] == "gated" else "gdn_core"
+    kname = "gdn_core" if w["cell"] == "gdn" else "gated_scan"
     tpath = args.traffic or os.path.join(ROOT, "profiles", f"{kname}_{args.workload}_traffic.txt")
     traffic = read_traffic(tpath) if B == w["B"] else None
     Ci = w["C"] * w.get("expand", 1)
@@ -343,6 +405,11 @@ def main():
     }
     if w["cell"] == "gdn":
         res["config"].update(delta_key_dim=w["dk"], qkv_conv_size=w["qkv_conv_size"])
+    if w["cell"] == "stack":
+        res["config"].update(stages=[{"H": h, "W": h, "channels": c, "inner_channels": c * w["expand"], "layers": n}
+                                     for h, c, n in w["stages"]], layers=sum(n for _, _, n in w["stages"]))
+        for k in ("H", "W", "channels", "inner_channels"):
+            res["config"].pop(k)
     if not args.no_cpu_baseline:
         res["cpu_baseline"] = cpu_baseline(w, args.cpu_seconds)
     print(json.dumps(res), flush=True)

@@ -152,11 +152,14 @@ class GatedCSSM:
         if Ci % g:
             raise NotImplementedError(f"{Ci} inner channels is not a multiple of {g} for {H}x{W} planes")
         x = x.contiguous()
+        # intermediates stay float32 whatever the I/O dtype (the reference computes with fp32
+        # params); only x is read and the output written in the I/O dtype
+        f32 = torch.float32
         has_conv = self.short_conv_spatial_size > 0 or self.short_conv_size > 0
         # in_proj straight into plane-major x_main and z; SiLU(z) (cssm.py:581) fused here,
         # SiLU(x_main) and ctx too unless the short convolutions come first
         xm, z, ctx = S.proj_in(x, p["in_proj"]["kernel"], p["in_proj"]["bias"], F, HW,
-                               silu_lo=not has_conv, silu_hi=True, want_ctx=not has_conv)
+                               silu_lo=not has_conv, silu_hi=True, want_ctx=not has_conv, out_dtype=f32)
         xm = xm.view(B, T, Ci, H, W)
         z = z.view(B, T, Ci, H, W)
         if has_conv:
@@ -169,7 +172,7 @@ class GatedCSSM:
         gates = S.gated_gates(ctx, p, H, W, self.gate_type, self.gate_activation, c_scale=1.0 / HW)
         khat = self.spectral_kernel(p, H, W)
         y = S.gated_scan(u, z, gates, khat)
-        out = S.proj_out(y.view(F, Ci, HW), p["out_proj"]["kernel"], p["out_proj"]["bias"])
+        out = S.proj_out(y.view(F, Ci, HW), p["out_proj"]["kernel"], p["out_proj"]["bias"], out_dtype=x.dtype)
         return out.view(B, T, H, W, self.channels)
 
     __call__ = apply

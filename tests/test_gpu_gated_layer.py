@@ -137,8 +137,8 @@ def test_gated_layer_bf16_io(mods):
     y = cells.GatedCSSM(**kw).apply(cells.GatedCSSM.load_params(p), xb)
     assert y.dtype == torch.bfloat16
     ref = O.gated_forward(p, to_np(xb), cfg)
-    # internal planes are stored in bf16 too, so allow the documented bf16 bar on top of rounding
-    assert bf16_excess_err(to_np(y), ref) <= 2 * TOL_BF16
+    # intermediates are fp32: beyond the output's own bf16 rounding the error is at the fp32 level
+    assert bf16_excess_err(to_np(y), ref) <= TOL_BF16
     assert np.sqrt(np.mean((to_np(y) - ref) ** 2)) <= TOL_BF16 * np.sqrt(np.mean(ref ** 2))
 
 
