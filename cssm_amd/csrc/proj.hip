@@ -16,6 +16,16 @@
 namespace cssm {
 
 typedef float floatx4 __attribute__((ext_vector_type(4)));
+typedef __bf16 bf16x4 __attribute__((ext_vector_type(4)));
+typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
+
+// fp32 -> three bf16 parts x1 + x2 + x3 = x to ~2^-27 relative (each rounds to nearest even)
+__device__ __forceinline__ void split3_bf16(float x, __bf16& x1, __bf16& x2, __bf16& x3) {
+  x1 = (__bf16)x;
+  const float r = x - (float)x1;
+  x2 = (__bf16)r;
+  x3 = (__bf16)(r - (float)x2);
+}
 
 __device__ __forceinline__ float ld_el(const float* p, size_t i) { return p[i]; }
 __device__ __forceinline__ float ld_el(const uint16_t* p, size_t i) { return __uint_as_float(uint32_t(p[i]) << 16); }
@@ -254,6 +264,15 @@ __global__ void ctx_reduce_kernel(const float* __restrict__ partial, int F, int 
 //   channels [0, NH) to out_lo and [NH, N) to out_hi, each with its
 //   activation, plus channel sums of out_lo (proj_in; NH = N writes a single
 //   tensor); false: channels-last (M, N) (proj_out).
+//   SPLIT: the product runs on bf16 MFMA (v_mfma_f32_16x16x32_bf16) with both
+//   operands split into three bf16 parts (A = A1 + A2 + A3, |A2| <= 2^-9 |A|,
+//   |A3| <= 2^-18 |A|) and the six products down to order 2^-18 kept:
+//   A1 B1 + A1 B2 + A2 B1 + A1 B3 + A2 B2 + A3 B1, fp32 accumulation.  The
+//   dropped terms are O(2^-27): fp32-level results at ~2.7x the fp32 MFMA
+//   rate (the fp32 path is MFMA-bound at K = 64).  A is split once when it is
+//   staged in LDS (three bf16 planes, k contiguous per row); the weight
+//   fragments of the wave's 32 columns are split once per launch and stay in
+//   VGPRs.
 //   NORM (PLANE_A only): before the product, each pixel's K-vector is
 //   normalised across channels (norm 1: RMSNorm x rsqrt(mean x^2 + 1e-6) s_k;
 //   2: LayerNorm (x - mean) rsqrt(var + 1e-6) s_k + b_k; 0: none) and
@@ -267,7 +286,7 @@ struct NormGate {
   int kind;             // 0 none, 1 rms, 2 layer
 };
 
-template <int KMAX, bool PLANE_A, bool OUT_SPLIT, int WN, class TI, class TO, bool NORM = false>
+template <int KMAX, bool PLANE_A, bool OUT_SPLIT, int WN, class TI, class TO, bool NORM = false, bool SPLIT = false>
 __global__ void __launch_bounds__(256, 2)
 proj_persist_kernel(const TI* __restrict__ A, int M, int K, int N, const float* __restrict__ Wt,
                     const float* __restrict__ bias, int HW, TO* __restrict__ out_lo, TO* __restrict__ out_hi,
@@ -277,14 +296,22 @@ proj_persist_kernel(const TI* __restrict__ A, int M, int K, int N, const float* 
   constexpr int TM = 128, TN = 32 * WN, NT = 256, WM = 4 / WN, MI = TM / WM / 16;
   static_assert(!OUT_SPLIT || WM == 1, "channel sums of proj_in need whole row tiles per wave");
   static_assert(!NORM || (PLANE_A && !OUT_SPLIT), "the norm / gate prologue is for plane-major A");
+  static_assert(!(NORM && SPLIT), "the norm / gate prologue runs on the fp32 path");
+  static_assert(!SPLIT || KMAX % 32 == 0, "bf16 MFMA k-blocks of 32");
   constexpr int AP = PLANE_A ? (TM + 16) : (KMAX + 2);   // pitch: rows of A (row-major) or k-rows (plane)
   constexpr int BP = TN + 16;
-  constexpr int A_FLOATS = PLANE_A ? KMAX * AP : TM * AP;
+  constexpr int KP = KMAX + 8;                            // SPLIT: bf16 pitch of the k-contiguous rows
+  constexpr int KB = KMAX / 32;                           // SPLIT: bf16 MFMA k-blocks
+  constexpr int A_FLOATS = SPLIT ? 3 * TM * KP / 2 : (PLANE_A ? KMAX * AP : TM * AP);   // SPLIT: 3 bf16 planes
   constexpr int OP = TN + 4;                              // output staging pitch (channels-last out)
   constexpr int AS_FLOATS = (!OUT_SPLIT && TM * OP > A_FLOATS) ? TM * OP : A_FLOATS;  // staging reuses As
   constexpr int PF = TM * KMAX / 4 / NT;                 // float4 of A prefetched per thread
   __shared__ __attribute__((aligned(16))) float As[AS_FLOATS];
-  __shared__ float Bs[KMAX * BP];
+  __shared__ __attribute__((aligned(16))) float Bs[SPLIT ? 1 : KMAX * BP];
+  // SPLIT views: the three A planes [TM][KP] as bf16
+  __bf16* const A1 = reinterpret_cast<__bf16*>(As);
+  __bf16* const A2 = A1 + TM * KP;
+  __bf16* const A3 = A2 + TM * KP;
   __shared__ float rowsc[NORM ? 2 * TM : 1];             // per-pixel (scale, mean) of the norm
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int wm = wave / WN, wn = wave % WN;
@@ -293,19 +320,48 @@ proj_persist_kernel(const TI* __restrict__ A, int M, int K, int N, const float* 
   const int tiles = (M + TM - 1) / TM;
   const TI* __restrict__ Gp = static_cast<const TI*>(ng.G);
 
-  for (int i = tid; i < KMAX * TN; i += NT) {
-    const int kk = i / TN, c = i % TN;
-    const int gn = n0 + c;
-    Bs[kk * BP + c] = (kk < K && gn < N) ? Wt[size_t(kk) * N + gn] : 0.0f;
+  // SPLIT: lane l's B fragments, column wn 32 + 16 j + l % 16, k = 32 kb + 8 (l / 16) + e
+  bf16x8 b1[SPLIT ? 2 : 1][SPLIT ? KB : 1], b2[SPLIT ? 2 : 1][SPLIT ? KB : 1], b3[SPLIT ? 2 : 1][SPLIT ? KB : 1];
+  if constexpr (SPLIT) {
+#pragma unroll
+    for (int j = 0; j < 2; ++j) {
+      const int gn = n0 + wn * 32 + j * 16 + (lane & 15);
+#pragma unroll
+      for (int kb = 0; kb < KB; ++kb)
+#pragma unroll
+        for (int e = 0; e < 8; ++e) {
+          const int kk = kb * 32 + (lane >> 4) * 8 + e;
+          const float w = (kk < K && gn < N) ? Wt[size_t(kk) * N + gn] : 0.0f;
+          __bf16 x1, x2, x3;
+          split3_bf16(w, x1, x2, x3);
+          b1[j][kb][e] = x1;
+          b2[j][kb][e] = x2;
+          b3[j][kb][e] = x3;
+        }
+    }
+  } else {
+    for (int i = tid; i < KMAX * TN; i += NT) {
+      const int kk = i / TN, c = i % TN;
+      const int gn = n0 + c;
+      Bs[kk * BP + c] = (kk < K && gn < N) ? Wt[size_t(kk) * N + gn] : 0.0f;
+    }
   }
-  // A prefetch: float4 f of the tile -> (row, k4) or (k, row4)
+  // A prefetch: float4 f of the tile -> (row, k4) or (k, row4); SPLIT with
+  // plane-major A: thread t holds KMAX/8 consecutive k of the 4 rows 4 (t % 32)
   auto fetch = [&](const TI* src, int tile, float4* pf) {
     const int m0 = tile * TM;
 #pragma unroll
     for (int i = 0; i < PF; ++i) {
       const int f = i * NT + tid;
       float4 v = make_float4(0.f, 0.f, 0.f, 0.f);
-      if (!PLANE_A) {
+      if (SPLIT && PLANE_A) {
+        const int kk = (tid / (TM / 4)) * (KMAX / 8) + i, r4 = (tid % (TM / 4)) * 4;
+        const int gm = m0 + r4;
+        if (kk < K && gm < M) {
+          const int fr = gm / HW, p = gm % HW;
+          v = ld4(src, (size_t(fr) * K + kk) * HW + p);
+        }
+      } else if (!PLANE_A) {
         const int r = f / (KMAX / 4), k4 = (f % (KMAX / 4)) * 4;
         const int gm = m0 + r;
         if (gm < M && k4 < K) v = ld4(src, size_t(gm) * K + k4);
@@ -321,6 +377,55 @@ proj_persist_kernel(const TI* __restrict__ A, int M, int K, int N, const float* 
     }
   };
   auto stash = [&](const float4* pf) {
+    if constexpr (SPLIT && PLANE_A) {
+      // 4 rows x KMAX/8 consecutive k -> per row, runs of 8 bf16 of each part (16 B stores)
+      const int k0 = (tid / (TM / 4)) * (KMAX / 8), r4 = (tid % (TM / 4)) * 4;
+#pragma unroll
+      for (int q = 0; q < 4; ++q) {
+#pragma unroll
+        for (int c8 = 0; c8 < KMAX / 64; ++c8) {
+          bf16x8 v1, v2, v3;
+#pragma unroll
+          for (int e = 0; e < 8; ++e) {
+            const float4 v = pf[c8 * 8 + e];
+            const float x = q == 0 ? v.x : (q == 1 ? v.y : (q == 2 ? v.z : v.w));
+            __bf16 x1, x2, x3;
+            split3_bf16(x, x1, x2, x3);
+            v1[e] = x1;
+            v2[e] = x2;
+            v3[e] = x3;
+          }
+          const int o = (r4 + q) * KP + k0 + c8 * 8;
+          *reinterpret_cast<bf16x8*>(&A1[o]) = v1;
+          *reinterpret_cast<bf16x8*>(&A2[o]) = v2;
+          *reinterpret_cast<bf16x8*>(&A3[o]) = v3;
+        }
+      }
+      return;
+    }
+    if constexpr (SPLIT) {
+      // row r, 4 consecutive k -> runs of 4 bf16 of each part (8 B stores)
+#pragma unroll
+      for (int i = 0; i < PF; ++i) {
+        const int f = i * NT + tid;
+        const int r = f / (KMAX / 4), k4 = (f % (KMAX / 4)) * 4;
+        const float x[4] = {pf[i].x, pf[i].y, pf[i].z, pf[i].w};
+        bf16x4 v1, v2, v3;
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+          __bf16 x1, x2, x3;
+          split3_bf16(x[e], x1, x2, x3);
+          v1[e] = x1;
+          v2[e] = x2;
+          v3[e] = x3;
+        }
+        const int o = r * KP + k4;
+        *reinterpret_cast<bf16x4*>(&A1[o]) = v1;
+        *reinterpret_cast<bf16x4*>(&A2[o]) = v2;
+        *reinterpret_cast<bf16x4*>(&A3[o]) = v3;
+      }
+      return;
+    }
 #pragma unroll
     for (int i = 0; i < PF; ++i) {
       const int f = i * NT + tid;
@@ -398,7 +503,32 @@ proj_persist_kernel(const TI* __restrict__ A, int M, int K, int N, const float* 
     floatx4 acc[MI][2];
 #pragma unroll
     for (int i = 0; i < MI; ++i) acc[i][0] = acc[i][1] = floatx4{0.f, 0.f, 0.f, 0.f};
-    const int kend = (K + 3) / 4 * 4;
+    if constexpr (SPLIT) {
+      // lane l: A rows l % 16 and B columns l % 16, k = 32 kb + 8 (l / 16) + 0..7
+#pragma unroll
+      for (int kb = 0; kb < KB; ++kb) {
+        if (kb * 32 >= K) break;
+        const int koff = kb * 32 + (lane >> 4) * 8;
+#pragma unroll
+        for (int i = 0; i < MI; ++i) {
+          const int o = ((wm * MI + i) * 16 + (lane & 15)) * KP + koff;
+          const bf16x8 a1 = *reinterpret_cast<const bf16x8*>(&A1[o]);
+          const bf16x8 a2 = *reinterpret_cast<const bf16x8*>(&A2[o]);
+          const bf16x8 a3 = *reinterpret_cast<const bf16x8*>(&A3[o]);
+#pragma unroll
+          for (int j = 0; j < 2; ++j) {
+            floatx4 c = acc[i][j];
+            c = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a3, b1[j][kb], c, 0, 0, 0);   // small terms first
+            c = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a2, b2[j][kb], c, 0, 0, 0);
+            c = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a1, b3[j][kb], c, 0, 0, 0);
+            c = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a2, b1[j][kb], c, 0, 0, 0);
+            c = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a1, b2[j][kb], c, 0, 0, 0);
+            acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a1, b1[j][kb], c, 0, 0, 0);
+          }
+        }
+      }
+    }
+    const int kend = SPLIT ? 0 : (K + 3) / 4 * 4;
     for (int kk = 0; kk < kend; kk += 4) {
       const int ka = kk + (lane >> 4);
       float a[MI], b[2];
@@ -518,7 +648,8 @@ static void launch_in(const void* X, int M, int K, int N, const float* W, const 
                      K, N, W, b, HW, static_cast<TO*>(lo), static_cast<TO*>(hi), act_lo, act_hi, partial, NH);
 }
 
-template <int KMAX, bool PLANE_A, bool OUT_SPLIT, bool NORM, class TI, class TO>
+// bf16x3 MFMA for every persistent projection except the norm / gate prologue (fp32)
+template <int KMAX, bool PLANE_A, bool OUT_SPLIT, bool NORM, class TI, class TO, bool SPLIT = !NORM>
 static void launch_persist(const void* A, int M, int K, int N, const float* W, const float* b, int HW, void* lo,
                            void* hi, int act_lo, int act_hi, float* partial, int NH, const NormGate& ng,
                            hipStream_t s) {
@@ -527,14 +658,14 @@ static void launch_persist(const void* A, int M, int K, int N, const float* W, c
   if constexpr (!OUT_SPLIT) {
     if (N <= 64) {
       const dim3 grid(unsigned(persistent_grid(tiles)), unsigned((N + 63) / 64));
-      hipLaunchKernelGGL((proj_persist_kernel<KMAX, PLANE_A, OUT_SPLIT, 2, TI, TO, NORM>), grid, dim3(256), 0, s,
+      hipLaunchKernelGGL((proj_persist_kernel<KMAX, PLANE_A, OUT_SPLIT, 2, TI, TO, NORM, SPLIT>), grid, dim3(256), 0, s,
                          static_cast<const TI*>(A), M, K, N, W, b, HW, static_cast<TO*>(lo), static_cast<TO*>(hi),
                          act_lo, act_hi, partial, NH, ng);
       return;
     }
   }
   const dim3 grid(unsigned(persistent_grid(tiles)), unsigned((N + 127) / 128));
-  hipLaunchKernelGGL((proj_persist_kernel<KMAX, PLANE_A, OUT_SPLIT, 4, TI, TO, NORM>), grid, dim3(256), 0, s,
+  hipLaunchKernelGGL((proj_persist_kernel<KMAX, PLANE_A, OUT_SPLIT, 4, TI, TO, NORM, SPLIT>), grid, dim3(256), 0, s,
                      static_cast<const TI*>(A), M, K, N, W, b, HW, static_cast<TO*>(lo), static_cast<TO*>(hi),
                      act_lo, act_hi, partial, NH, ng);
 }
