@@ -621,8 +621,97 @@ dwconv_cl(const TI* __restrict__ x, int H, int W, int C, int ks, const float* __
   for (int e = 0; e < cv; ++e) st_f(y, o + e, acc[e]);
 }
 
+// Register-blocked variant for ks in {3, 5, 7}: a thread computes 2 rows x 4
+// columns x 4 channels, so each input float4 it loads feeds up to 2 KS outputs
+// (6-9 loads per output instead of KS^2).  Needs C % 4 == 0, W % 4 == 0, H % 2 == 0.
+template <int KS, class TI, class TO>
+__global__ void __launch_bounds__(256)
+dwconv_cl_blocked(const TI* __restrict__ x, int H, int W, int C, const float* __restrict__ kw,
+                  const float* __restrict__ bias, TO* __restrict__ y, long long total) {
+  constexpr int LO = (KS - 1) / 2, RH = 2, RW = 4, NCOL = RW + KS - 1;
+  const long long i = (long long)blockIdx.x * blockDim.x + threadIdx.x;
+  if (i >= total) return;
+  const int CG = C / 4, WG = W / RW, HG = H / RH;
+  const int c0 = int(i % CG) * 4;
+  const long long t1 = i / CG;
+  const int w0 = int(t1 % WG) * RW;
+  const long long t2 = t1 / WG;
+  const int h0 = int(t2 % HG) * RH;
+  const long long f = t2 / HG;
+  const TI* xf = x + size_t(f) * H * W * C;
+  float4 acc[RH][RW];
+  const float4 bv = *reinterpret_cast<const float4*>(bias + c0);
+#pragma unroll
+  for (int r = 0; r < RH; ++r)
+#pragma unroll
+    for (int q = 0; q < RW; ++q) acc[r][q] = bv;
+#pragma unroll
+  for (int ih = 0; ih < RH + KS - 1; ++ih) {          // input rows h0 - LO .. h0 + RH - 1 + (KS - 1 - LO)
+    const int hh = h0 - LO + ih;
+    if (hh < 0 || hh >= H) continue;
+    float4 xin[NCOL];
+#pragma unroll
+    for (int ic = 0; ic < NCOL; ++ic) {
+      const int ww = w0 - LO + ic;
+      xin[ic] = (ww >= 0 && ww < W) ? ld4v(xf, (size_t(hh) * W + ww) * C + c0) : make_float4(0.f, 0.f, 0.f, 0.f);
+    }
+#pragma unroll
+    for (int r = 0; r < RH; ++r) {
+      const int a = ih - r;                               // tap row of output row h0 + r
+      if (a < 0 || a >= KS) continue;
+#pragma unroll
+      for (int b2 = 0; b2 < KS; ++b2) {
+        const float4 kv = *reinterpret_cast<const float4*>(kw + (a * KS + b2) * C + c0);
+#pragma unroll
+        for (int q = 0; q < RW; ++q) {
+          const float4 xv = xin[q + b2];
+          acc[r][q].x = fmaf(xv.x, kv.x, acc[r][q].x);
+          acc[r][q].y = fmaf(xv.y, kv.y, acc[r][q].y);
+          acc[r][q].z = fmaf(xv.z, kv.z, acc[r][q].z);
+          acc[r][q].w = fmaf(xv.w, kv.w, acc[r][q].w);
+        }
+      }
+    }
+  }
+#pragma unroll
+  for (int r = 0; r < RH; ++r)
+#pragma unroll
+    for (int q = 0; q < RW; ++q) {
+      const size_t o = ((size_t(f) * H + h0 + r) * W + w0 + q) * C + c0;
+      const float e[4] = {acc[r][q].x, acc[r][q].y, acc[r][q].z, acc[r][q].w};
+#pragma unroll
+      for (int k = 0; k < 4; ++k) st_f(y, o + k, e[k]);
+    }
+}
+
+template <int KS, class TI, class TO>
+static hipError_t run_dwconv_blocked(const void* x, int F, int H, int W, int C, const float* kw, const float* bias,
+                                     void* y, hipStream_t s) {
+  const long long total = (long long)F * (H / 2) * (W / 4) * (C / 4);
+  hipLaunchKernelGGL((dwconv_cl_blocked<KS, TI, TO>), dim3(unsigned((total + 255) / 256)), dim3(256), 0, s,
+                     static_cast<const TI*>(x), H, W, C, kw, bias, static_cast<TO*>(y), total);
+  return hipGetLastError();
+}
+
+template <class TI, class TO>
+static bool try_dwconv_blocked(const void* x, int F, int H, int W, int C, int ks, const float* kw, const float* bias,
+                               void* y, hipStream_t s, hipError_t& e) {
+  if (C % 4 || W % 4 || H % 2) return false;
+  switch (ks) {
+    case 3: e = run_dwconv_blocked<3, TI, TO>(x, F, H, W, C, kw, bias, y, s); return true;
+    case 5: e = run_dwconv_blocked<5, TI, TO>(x, F, H, W, C, kw, bias, y, s); return true;
+    case 7: e = run_dwconv_blocked<7, TI, TO>(x, F, H, W, C, kw, bias, y, s); return true;
+    default: return false;
+  }
+}
+
 hipError_t launch_depthwise_conv(const void* x, int dtype, int F, int H, int W, int C, int ks, const float* kw,
                                  const float* bias, void* y, int out_dtype, hipStream_t s) {
+  hipError_t e = hipSuccess;
+  if (dtype == 0 && out_dtype == 0 && try_dwconv_blocked<float, float>(x, F, H, W, C, ks, kw, bias, y, s, e)) return e;
+  if (dtype == 0 && out_dtype == 1 && try_dwconv_blocked<float, uint16_t>(x, F, H, W, C, ks, kw, bias, y, s, e)) return e;
+  if (dtype == 1 && out_dtype == 0 && try_dwconv_blocked<uint16_t, float>(x, F, H, W, C, ks, kw, bias, y, s, e)) return e;
+  if (dtype == 1 && out_dtype == 1 && try_dwconv_blocked<uint16_t, uint16_t>(x, F, H, W, C, ks, kw, bias, y, s, e)) return e;
   const long long total = (long long)F * H * W * (C % 4 == 0 ? C / 4 : C);
   const unsigned blocks = unsigned((total + 255) / 256);
   const dim3 g(blocks), b(256);

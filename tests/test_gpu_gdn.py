@@ -93,18 +93,25 @@ def test_proj_planes(mods, act):
     assert rel_err(to_np(out), ref) < 1e-5
 
 
-def test_frame_mean_and_depthwise_conv(mods):
+@pytest.mark.parametrize("shape", [(2, 3, 16, 12, 20), (1, 2, 7, 8, 12), (1, 2, 32, 32, 64)])
+def test_frame_mean_and_depthwise_conv(mods, shape):
+    """Register-blocked (ks 3/5/7, even H, W % 4, C % 4) and general depthwise convs, f32 and bf16 in."""
     _, S = mods
-    print_case(test="frame_mean_dwconv")
+    print_case(test="frame_mean_dwconv", shape=shape)
     rng = np.random.default_rng(4)
-    x = rng.standard_normal((2, 3, 16, 12, 20))
+    B, T, H, W, C = shape
+    x = rng.standard_normal(shape)
     m = S.frame_mean(_dev(x))
     assert rel_err(to_np(m), x.mean(axis=(2, 3))) < 1e-6
-    for ks in (5, 3, 4):
-        p = {"kernel": rng.standard_normal((ks, ks, 1, 20)) / ks, "bias": rng.standard_normal(20) * 0.1}
+    for ks in (5, 3, 4, 7):
+        p = {"kernel": rng.standard_normal((ks, ks, 1, C)) / ks, "bias": rng.standard_normal(C) * 0.1}
         y = S.depthwise_conv(_dev(x), _dev(p["kernel"]), _dev(p["bias"]))
-        ref = O.depthwise_conv2d_same(x.reshape(6, 16, 12, 20), p).reshape(x.shape)
-        assert rel_err(to_np(y), ref) < 1e-6, ks
+        ref = O.depthwise_conv2d_same(x.reshape(B * T, H, W, C), p).reshape(x.shape)
+        assert rel_err(to_np(y), ref) < 5e-6, ks            # fp32 sums of up to 49 taps
+        xb = _dev(x, torch.bfloat16)
+        yb = S.depthwise_conv(xb, _dev(p["kernel"]), _dev(p["bias"]), out_dtype=torch.float32)
+        refb = O.depthwise_conv2d_same(to_np(xb).reshape(B * T, H, W, C), p).reshape(x.shape)
+        assert rel_err(to_np(yb), refb) < 5e-6, ks
 
 
 @pytest.mark.parametrize("gate_type", ["factored", "dense", "channel", "scalar"])
