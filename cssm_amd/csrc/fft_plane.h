@@ -89,7 +89,6 @@ struct Geom {
   static constexpr int NC1 = NP * WH * H2, NC2 = NP * WH * (H1 / 2);
   static constexpr int JR1 = NR1 / NT, JR2 = NR2 / NT, JC1 = NC1 / NT, JC2 = NC2 / NT;
   static constexpr int NE = NP * HP;
-  static constexpr int JE = (NE + NT - 1) / NT;
   static constexpr int NV4 = NP * H * W / 4;
   static constexpr int JLD = NV4 / NT;
 
@@ -101,7 +100,7 @@ struct Geom {
   static constexpr int RS = W + 4;
   static constexpr int SZ_BUF = (NP * H * RS + 3) / 4 * 4;
   static constexpr int SZ_EDGE = 2 * NP * H;
-  static constexpr int TR1 = W1 + 1, TC1 = H1, TI1 = H2, TI3 = W2 + 1;   // table row lengths
+  static constexpr int TR1 = W1 + 1, TC1 = H1 + 1, TI1 = H2, TI3 = W2 + 1;   // table row lengths (padded)
   static constexpr int N_R1 = W2 * TR1, N_C1 = H2 * TC1, N_I1 = H1 * TI1, N_I3 = W1 * TI3;
   static constexpr int SZ_TW = 2 * (N_R1 + N_C1 + N_I1 + N_I3);
   static constexpr int OFF_EDGE = SZ_BUF, OFF_TW = OFF_EDGE + SZ_EDGE;
@@ -137,16 +136,63 @@ struct Geom {
   }
   // 4-vector c4 of row r: contiguous unless the block is split by the swap
   static constexpr bool V4_SPLIT = (HALF == 2);
-  // R1/I4 job jb -> (pl, p, s): s fastest; consecutive row groups of one wave
-  // are two rows apart so the row stride's bank shift (4) becomes 8
+  // ---- wave ownership.  Wave w owns RPW consecutive row pairs (pl, p) /
+  // (pl, p + H/2) and CPW consecutive packed columns (pl, v): every pass that
+  // only touches its owner's rows (load, R1, R2, I3, I4, store) or columns
+  // (C1, C2, edge, I1, I2) needs no workgroup barrier between passes; only
+  // the two transposes (R2 -> C1, I2 -> I3) synchronise the workgroup.
+  static constexpr int NW = NT / 64;
+  static constexpr int NRP = NP * HP, RPW = NRP / NW;
+  static constexpr int NCOL = NP * WH, CPW = NCOL / NW;
+  static_assert(NRP % NW == 0 && NCOL % NW == 0, "rows / columns must split evenly over the waves");
+  static_assert((RPW * W2) % 64 == 0 && (RPW * (W1 / 2)) % 64 == 0 && (CPW * H2) % 64 == 0 &&
+                    (CPW * (H1 / 2)) % 64 == 0 && (RPW * (W / 2)) % 64 == 0,
+                "every wave-local pass must fill whole waves");
+  static_assert(CPW >= WH ? CPW % WH == 0 : WH % CPW == 0, "packed columns must not straddle waves");
+  // the packed DC / Nyquist column of plane pl belongs to the wave owning column (pl, 0)
+  static constexpr int PPWE = CPW >= WH ? CPW / WH : 1;        // such planes per owning wave
+  static constexpr int NEW = PPWE * HP, NI1 = PPWE * (H1 / 2);  // edge / I1 jobs of an owning wave
+  static constexpr int JE = (NEW + 63) / 64, JI1 = (NI1 + 63) / 64;
+  static __device__ __forceinline__ bool owns_edge(int w) { return (w * CPW) % WH == 0; }
+  static __device__ __forceinline__ int edge_plane0(int w) { return (w * CPW) / WH; }
+
+  // R1/I4 job j of lane l in wave w -> (pl, p, s): s fastest; the row groups
+  // of one instruction are two rows apart, so the row stride's bank shift (4)
+  // becomes 8
   static constexpr int RG = 64 / W2;
-  static constexpr bool R1_STRIDE2 = (RG >= 2) && (HP % (2 * RG) == 0);
-  static __device__ __forceinline__ void r1_job(unsigned jb, int& pl, int& p, int& s) {
-    s = int(jb % W2);
-    const unsigned t1 = jb / W2;
-    pl = int(t1 / HP);
-    const unsigned tp = t1 % HP;
-    p = int(R1_STRIDE2 ? ((tp % RG) * 2 + (tp / RG) % 2 + 2 * RG * (tp / (2 * RG))) : tp);
+  static constexpr bool R1_STRIDE2 = (RG >= 2) && (RPW % (2 * RG) == 0);
+  static __device__ __forceinline__ void r1_job(int w, int j, int l, int& pl, int& p, int& s) {
+    s = l % W2;
+    const int g = j * RG + l / W2;
+    const int rp = R1_STRIDE2 ? ((g % RG) * 2 + (g / RG) % 2 + 2 * RG * (g / (2 * RG))) : g;
+    const int RP = w * RPW + rp;
+    pl = RP / HP;
+    p = RP % HP;
+  }
+  // R2/I3 job -> (pl, p, jj): jj (block pair) fastest
+  static __device__ __forceinline__ void r2_job(int w, int j, int l, int& pl, int& p, int& jj) {
+    const int q = j * 64 + l;
+    jj = q % (W1 / 2);
+    const int RP = w * RPW + q / (W1 / 2);
+    pl = RP / HP;
+    p = RP % HP;
+  }
+  // C1/I2 job -> (pl, v, s); C2 job -> (pl, v, pair): column fastest
+  static __device__ __forceinline__ void col_job(int w, int j, int l, int& pl, int& v, int& r) {
+    const int q = j * 64 + l;
+    const int COL = w * CPW + q % CPW;
+    r = q / CPW;
+    pl = COL / WH;
+    v = COL % WH;
+  }
+  // 4-vector i of lane l in wave w (load / store phase) -> LDS / global vector index
+  // of the group: consecutive lanes along a row, the two rows of an owned pair alternating
+  static __device__ __forceinline__ unsigned v4_slot(int w, int i, int l) {
+    const int q = i * 64 + l;
+    const int c4 = q % (W / 4), rs = q / (W / 4);
+    const int RP = w * RPW + rs / 2;
+    const int pl = RP / HP, r = RP % HP + (rs % 2) * HP;
+    return unsigned((pl * H + r) * (W / 4) + c4);
   }
 };
 
@@ -173,12 +219,21 @@ struct Buf {
 };
 
 
+// LDS exchange within one wave: the wave's LDS operations execute in order, so
+// a compiler / memory fence at wavefront scope is all a wave-local pass needs
+__device__ __forceinline__ void wave_sync() {
+  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+  __builtin_amdgcn_wave_barrier();
+  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+}
+
 // ---------------------------------------------------------------------------
 // The passes of the 2-D real FFT of NP planes held in LDS, in the order a
 // round trip runs them:
 //   load -> R1 -> R2 -> C1 -> C2 (+ per-bin op, + I1) -> edge (+ op)
 //        -> I1 packed column -> I2 -> I3 -> I4 -> store
-// Each pass ends with a workgroup barrier.  The forward row pass skips the 1/2
+// R2 and I2 end with a workgroup barrier (the transposes); every other pass is
+// wave-local (wave_sync).  Passes take the thread's wave w and lane l.  The forward row pass skips the 1/2
 // of the packed-row separation, so every bin a policy sees in the forward
 // direction is 2U (the edge unpack keeps its 1/2 and inherits the factor from
 // the doubled DC/Nyquist column).  The inverse passes take Y / (H W) for
@@ -257,11 +312,11 @@ struct PlaneFft {
   }
 
   // ---------------------------------------------- R1: DFT-W1 over m, twiddle
-  __device__ __forceinline__ void r1(unsigned tid) const {
+  __device__ __forceinline__ void r1(int w, int l) const {
 #pragma unroll
     for (int j = 0; j < G::JR1; ++j) {
       int pl, p, s;
-      G::r1_job(j * NT + tid, pl, p, s);
+      G::r1_job(w, j, l, pl, p, s);
       float2 zz[W1];
 #pragma unroll
       for (int m = 0; m < W1; ++m) {
@@ -278,15 +333,15 @@ struct PlaneFft {
       }
       __builtin_amdgcn_sched_barrier(0);
     }
-    __syncthreads();
+    wave_sync();
   }
 
   // ----------------- R2: DFT-W2 over s, separate packed row pairs (x2 scale)
-  __device__ __forceinline__ void r2(unsigned tid) const {
+  __device__ __forceinline__ void r2(int w, int l) const {
 #pragma unroll
     for (int j = 0; j < G::JR2; ++j) {
-      const unsigned jb = j * NT + tid;
-      const int jj = int(jb % (W1 / 2)), p = int((jb / (W1 / 2)) % HP), pl = int(jb / (HP * (W1 / 2)));
+      int pl, p, jj;
+      G::r2_job(w, j, l, pl, p, jj);
       int kA, kB;
       pair_units<W1>(jj, kA, kB);
       float2 za[W2], zb[W2];
@@ -328,11 +383,11 @@ struct PlaneFft {
   }
 
   // ------------------------------------------ C1: DFT-H1 over m, twiddle
-  __device__ __forceinline__ void c1(unsigned tid) const {
+  __device__ __forceinline__ void c1(int w, int l) const {
 #pragma unroll
     for (int j = 0; j < G::JC1; ++j) {
-      const unsigned jb = j * NT + tid;
-      const int v = int(jb % WH), s = int((jb / WH) % H2), pl = int(jb / (WH * H2));
+      int pl, v, s;
+      G::col_job(w, j, l, pl, v, s);
       const int col = G::p_col(v);
       float2 zz[H1];
 #pragma unroll
@@ -343,7 +398,7 @@ struct PlaneFft {
         cplx(G::row_off(pl, s + H2 * k) + col) = k ? cmul(zz[k], twC1[s * G::TC1 + k]) : zz[0];
       __builtin_amdgcn_sched_barrier(0);
     }
-    __syncthreads();
+    wave_sync();
   }
 
   // ------ C2: DFT-H2 over s -> spectrum; op.bins; inverse DFT-H2 (I1)
@@ -352,13 +407,13 @@ struct PlaneFft {
   // Nyquist column (v = 0) goes to the edge buffer (FWD) and is left to the
   // edge pass and i1_packed.
   template <bool FWD, bool INV, class Op>
-  __device__ __forceinline__ void c2(unsigned tid, Op& op) const {
+  __device__ __forceinline__ void c2(int w, int l, Op& op) const {
 #pragma unroll
     for (int j = 0; j < G::JC2; ++j) {
-      const unsigned jb = j * NT + tid;
-      const int v = int(jb % WH), pl = int(jb / (WH * (H1 / 2)));
+      int pl, v, pair;
+      G::col_job(w, j, l, pl, v, pair);
       int kA, kB;
-      pair_units<H1>(int((jb / WH) % (H1 / 2)), kA, kB);
+      pair_units<H1>(pair, kA, kB);
       const int col = G::p_col(v);
 #pragma unroll
       for (int a2 = 0; a2 < 2; ++a2) {
@@ -386,17 +441,18 @@ struct PlaneFft {
         __builtin_amdgcn_sched_barrier(0);
       }
     }
-    __syncthreads();
+    wave_sync();
   }
 
   // ------------------- edge pass: DC and Nyquist columns (unpack, op, repack)
   template <bool FWD, bool INV, class Op>
-  __device__ __forceinline__ void edges(unsigned tid, Op& op) const {
+  __device__ __forceinline__ void edges(int w, int l, Op& op) const {
+    if (!G::owns_edge(w)) return;
 #pragma unroll
     for (int j = 0; j < G::JE; ++j) {
-      const unsigned jb = j * NT + tid;
-      if (jb < unsigned(G::NE)) {
-        const int e = int(jb % HP), pl = int(jb / HP);
+      const int q = j * 64 + l;
+      if (q < G::NEW) {
+        const int e = q % HP, pl = G::edge_plane0(w) + q / HP;
         const int uA = e, uB = (e == 0) ? HP : H - e;
         float2 v4[4];
         if (FWD) {
@@ -430,18 +486,19 @@ struct PlaneFft {
         }
       }
     }
-    __syncthreads();
+    wave_sync();
   }
 
   // ---------------- I1 for the packed column: inverse DFT-H2, conj twiddle
-  __device__ __forceinline__ void i1_packed(unsigned tid) const {
+  __device__ __forceinline__ void i1_packed(int w, int l) const {
+    if (!G::owns_edge(w)) return;
 #pragma unroll
-    for (int j = 0; j < G::JC2; ++j) {
-      const unsigned jb = j * NT + tid;
-      const int v = int(jb % WH), pl = int(jb / (WH * (H1 / 2)));
-      if (v == 0) {
+    for (int j = 0; j < G::JI1; ++j) {
+      const int q = j * 64 + l;
+      if (q < G::NI1) {
+        const int pl = G::edge_plane0(w) + q / (H1 / 2);
         int kA, kB;
-        pair_units<H1>(int((jb / WH) % (H1 / 2)), kA, kB);
+        pair_units<H1>(q % (H1 / 2), kA, kB);
         float2 sa[H2], sb[H2];
 #pragma unroll
         for (int q = 0; q < H2; ++q) {
@@ -458,15 +515,15 @@ struct PlaneFft {
         }
       }
     }
-    __syncthreads();
+    wave_sync();
   }
 
   // ----------------------------- I2: inverse DFT-H1 over k -> rows (P slots)
-  __device__ __forceinline__ void i2(unsigned tid) const {
+  __device__ __forceinline__ void i2(int w, int l) const {
 #pragma unroll
     for (int j = 0; j < G::JC1; ++j) {
-      const unsigned jb = j * NT + tid;
-      const int v = int(jb % WH), s = int((jb / WH) % H2), pl = int(jb / (WH * H2));
+      int pl, v, s;
+      G::col_job(w, j, l, pl, v, s);
       const int col = G::p_col(v);
       float2 zz[H1];
 #pragma unroll
@@ -480,11 +537,11 @@ struct PlaneFft {
   }
 
   // ------------- I3: build packed Hermitian row pair, inverse DFT-W2, twiddle
-  __device__ __forceinline__ void i3(unsigned tid) const {
+  __device__ __forceinline__ void i3(int w, int l) const {
 #pragma unroll
     for (int j = 0; j < G::JR2; ++j) {
-      const unsigned jb = j * NT + tid;
-      const int jj = int(jb % (W1 / 2)), p = int((jb / (W1 / 2)) % HP), pl = int(jb / (HP * (W1 / 2)));
+      int pl, p, jj;
+      G::r2_job(w, j, l, pl, p, jj);
       int kA, kB;
       pair_units<W1>(jj, kA, kB);
       float2 za[W2], zb[W2];
@@ -524,15 +581,15 @@ struct PlaneFft {
       }
       __builtin_amdgcn_sched_barrier(0);
     }
-    __syncthreads();
+    wave_sync();
   }
 
   // ------------------------ I4: inverse DFT-W1 over k -> real rows p, p+H/2
-  __device__ __forceinline__ void i4(unsigned tid) const {
+  __device__ __forceinline__ void i4(int w, int l) const {
 #pragma unroll
     for (int j = 0; j < G::JR1; ++j) {
       int pl, p, s;
-      G::r1_job(j * NT + tid, pl, p, s);
+      G::r1_job(w, j, l, pl, p, s);
       float2 zz[W1];
 #pragma unroll
       for (int k = 0; k < W1; ++k) {
@@ -548,7 +605,7 @@ struct PlaneFft {
       }
       __builtin_amdgcn_sched_barrier(0);
     }
-    __syncthreads();
+    wave_sync();
   }
 };
 

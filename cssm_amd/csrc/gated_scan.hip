@@ -113,6 +113,7 @@ gated_scan_pow2(const ScanArgs a) {
   TE* __restrict__ yp = static_cast<TE*>(a.y);
 
   fft.init_twiddles(threadIdx.x);
+  const int wv = __builtin_amdgcn_readfirstlane(int(threadIdx.x) / 64), ln = int(threadIdx.x) % 64;
 
   float2 h[G::JC2][2][H2];
   float2 hE[G::JE][4];
@@ -125,36 +126,36 @@ gated_scan_pow2(const ScanArgs a) {
 #pragma unroll
     for (int k = 0; k < 4; ++k) hE[j][k] = make_float2(0.f, 0.f);
 
-  // u_0 into the plane buffer
+  // u_0 into the plane buffer (each wave loads the rows it owns)
+  __syncthreads();   // twiddle tables
   {
-    const unsigned tid = threadIdx.x;
     const V4* src = reinterpret_cast<const V4*>(up + group_elems(0));
     V4 ld[G::JLD];
 #pragma unroll
-    for (int i = 0; i < G::JLD; ++i) ld[i] = src[i * NT + tid];
+    for (int i = 0; i < G::JLD; ++i) ld[i] = src[G::v4_slot(wv, i, ln)];
 #pragma unroll
-    for (int i = 0; i < G::JLD; ++i) fft.v4_store(i * NT + tid, act4(IO::to_f4(ld[i]), a.u_act));
+    for (int i = 0; i < G::JLD; ++i) fft.v4_store(G::v4_slot(wv, i, ln), act4(IO::to_f4(ld[i]), a.u_act));
   }
-  __syncthreads();
+  wave_sync();
 
   for (int t = 0; t < T; ++t) {
     // Re-derive the thread index inside the loop so the compiler rebuilds the
     // (cheap, base + constant) LDS addresses per step instead of hoisting
     // hundreds of them into registers for the whole scan.
-    unsigned tid = threadIdx.x;
-    asm volatile("" : "+v"(tid));
+    int lane = ln;
+    asm volatile("" : "+v"(lane));
     GatedScanOp<G> op{h, hE, Buf(a.gates + (size_t(b) * T + t) * size_t(H) * WF, unsigned(H * WF * sizeof(float4))),
                       Buf(a.khat + size_t(c0) * H * WF, unsigned(NP * H * WF * sizeof(float2)))};
 
-    fft.r1(tid);
-    fft.r2(tid);
-    fft.c1(tid);
-    fft.template c2<true, true>(tid, op);
-    fft.template edges<true, true>(tid, op);
-    fft.i1_packed(tid);
-    fft.i2(tid);
-    fft.i3(tid);
-    fft.i4(tid);
+    fft.r1(wv, lane);
+    fft.r2(wv, lane);
+    fft.c1(wv, lane);
+    fft.template c2<true, true>(wv, lane, op);
+    fft.template edges<true, true>(wv, lane, op);
+    fft.i1_packed(wv, lane);
+    fft.i2(wv, lane);
+    fft.i3(wv, lane);
+    fft.i4(wv, lane);
 
     // ---------- STORE y_t = y * z_gate, and LOAD u_{t+1} into the same slots
     // (in chunks of CH vectors to bound the registers in flight)
@@ -167,26 +168,26 @@ gated_scan_pow2(const ScanArgs a) {
       for (int c = 0; c < G::JLD; c += CH) {
         V4 ldg[CH], ldu[CH];
 #pragma unroll
-        for (int i = 0; i < CH; ++i) ldg[i] = zsrc[(c + i) * NT + tid];
+        for (int i = 0; i < CH; ++i) ldg[i] = zsrc[G::v4_slot(wv, c + i, lane)];
         if (t + 1 < T) {
 #pragma unroll
-          for (int i = 0; i < CH; ++i) ldu[i] = usrc[(c + i) * NT + tid];
+          for (int i = 0; i < CH; ++i) ldu[i] = usrc[G::v4_slot(wv, c + i, lane)];
         }
 #pragma unroll
         for (int i = 0; i < CH; ++i) {
-          const unsigned f = (c + i) * NT + tid;
+          const unsigned f = G::v4_slot(wv, c + i, lane);
           const float4 yv = fft.v4_load(f);
           const float4 gv = act4(IO::to_f4(ldg[i]), a.z_act);
           dst[f] = IO::from_f4(make_float4(yv.x * gv.x, yv.y * gv.y, yv.z * gv.z, yv.w * gv.w));
         }
         if (t + 1 < T) {
 #pragma unroll
-          for (int i = 0; i < CH; ++i) fft.v4_store((c + i) * NT + tid, act4(IO::to_f4(ldu[i]), a.u_act));
+          for (int i = 0; i < CH; ++i) fft.v4_store(G::v4_slot(wv, c + i, lane), act4(IO::to_f4(ldu[i]), a.u_act));
         }
         __builtin_amdgcn_sched_barrier(0);
       }
     }
-    __syncthreads();
+    wave_sync();
   }
 }
 

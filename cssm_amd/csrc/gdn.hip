@@ -52,18 +52,17 @@ __device__ __forceinline__ float2 goom_floor2(float2 z) {
 
 // forward policy: bins -> HBM spectrum (undoing the pass's factor 2).  The
 // sum of |X|^2 per plane is reduced deterministically: every C2 unit pair and
-// every edge job leaves its partial in a fixed LDS slot (slot = job index,
-// whose plane is job / (units per plane)), summed in a fixed order afterwards.
+// every edge job leaves its partial in a fixed LDS slot, (pl WH + v) H1/2 + pair
+// and pl H/2 + e, summed per plane in a fixed order afterwards.
 template <class G>
 struct SpecStoreOp {
-  static constexpr int H = G::H, WH = G::WH, WF = G::WF, H1 = G::H1, H2 = G::H2, NT = G::NT;
+  static constexpr int H = G::H, WH = G::WH, WF = G::WF, H1 = G::H1, H2 = G::H2, HP = G::HP;
   float2* out;      // (NP, H, WF) of this workgroup
   float* part_c2;   // LDS (NC2) or nullptr: partial sums of the C2 jobs
   float* part_e;    // LDS (NE) or nullptr: partial sums of the edge jobs
   int nvalid;       // planes of the group that exist (the last group may be partial)
-  unsigned tid;
 
-  __device__ __forceinline__ void bins(int j, int a2, int pl, int k, int v, float2 (&sp)[G::H2]) const {
+  __device__ __forceinline__ void bins(int, int a2, int pl, int k, int v, float2 (&sp)[G::H2]) const {
     float s = 0.0f;
     if (pl < nvalid) {
 #pragma unroll
@@ -74,11 +73,13 @@ struct SpecStoreOp {
       }
     }
     if (part_c2) {
-      float& slot = part_c2[j * NT + tid];
+      // unit a2 = 0 is kA = pair, a2 = 1 is kB = -pair mod H1 (H1/2 for pair 0)
+      const int pair = a2 == 0 ? k : (k == H1 / 2 ? 0 : H1 - k);
+      float& slot = part_c2[(pl * WH + v) * (H1 / 2) + pair];
       slot = a2 ? slot + s : s;
     }
   }
-  __device__ __forceinline__ void edge(int j, int pl, int uA, int uB, int, float2 (&v4)[4]) const {
+  __device__ __forceinline__ void edge(int, int pl, int uA, int uB, int e, float2 (&v4)[4]) const {
     float s = 0.0f;
     if (pl < nvalid) {
       const int idx[4] = {uA * WF, uA * WF + WH, uB * WF, uB * WF + WH};
@@ -89,7 +90,7 @@ struct SpecStoreOp {
         s = fmaf(x.x, x.x, fmaf(x.y, x.y, s));
       }
     }
-    if (part_e) part_e[j * NT + tid] = s;
+    if (part_e) part_e[pl * HP + e] = s;
   }
 };
 
@@ -135,31 +136,33 @@ rfft2_planes(const void* __restrict__ x, long long P, float2* __restrict__ spec,
   __shared__ float part_c2[G::NC2], part_e[G::NE], red[NT];
   const PlaneFft<G> fft(smem);
   const unsigned tid = threadIdx.x;
+  const int w = __builtin_amdgcn_readfirstlane(int(tid) / 64), l = int(tid) % 64;
   const size_t p0 = size_t(blockIdx.x) * NP;
   const int nvalid = int(P - (long long)p0 < NP ? P - (long long)p0 : NP);
   const unsigned nv4 = unsigned(nvalid) * (H * W / 4);
   fft.init_twiddles(tid);
+  // C2 jobs on the packed DC / Nyquist column (v = 0) never reach the policy: their slots stay 0
+  for (int i = tid; i < G::NC2; i += NT) part_c2[i] = 0.0f;
+  __syncthreads();
   {
     const V4* src = reinterpret_cast<const V4*>(static_cast<const TE*>(x) + p0 * H * W);
     V4 ld[G::JLD];
 #pragma unroll
     for (int i = 0; i < G::JLD; ++i) {
-      const unsigned f = i * NT + tid;
+      const unsigned f = G::v4_slot(w, i, l);
       ld[i] = f < nv4 ? src[f] : V4{};
     }
 #pragma unroll
-    for (int i = 0; i < G::JLD; ++i) fft.v4_store(i * NT + tid, IO::to_f4(ld[i]));
+    for (int i = 0; i < G::JLD; ++i) fft.v4_store(G::v4_slot(w, i, l), IO::to_f4(ld[i]));
   }
+  wave_sync();
+  SpecStoreOp<G> op{spec + p0 * H * WF, norms ? part_c2 : nullptr, norms ? part_e : nullptr, nvalid};
+  fft.r1(w, l);
+  fft.r2(w, l);
+  fft.c1(w, l);
+  fft.template c2<true, false>(w, l, op);
+  fft.template edges<true, false>(w, l, op);
   __syncthreads();
-  SpecStoreOp<G> op{spec + p0 * H * WF, norms ? part_c2 : nullptr, norms ? part_e : nullptr, nvalid, tid};
-  // C2 jobs on the packed DC / Nyquist column (v = 0) never reach the policy: their slots stay 0
-#pragma unroll
-  for (int j = 0; j < G::JC2; ++j) part_c2[j * NT + tid] = 0.0f;
-  fft.r1(tid);
-  fft.r2(tid);
-  fft.c1(tid);
-  fft.template c2<true, false>(tid, op);
-  fft.template edges<true, false>(tid, op);
   if (norms) {
     // plane pl: GR threads each sum a fixed stride of its UC2 + UE slots, then one sums those in order
     for (int pl0 = 0; pl0 < NP; pl0 += NT / GR) {
@@ -193,22 +196,23 @@ irfft2_planes(const float2* __restrict__ spec, long long P, void* __restrict__ y
   __shared__ __attribute__((aligned(16))) float smem[G::LDS_FLOATS];
   const PlaneFft<G> fft(smem);
   const unsigned tid = threadIdx.x;
+  const int w = __builtin_amdgcn_readfirstlane(int(tid) / 64), l = int(tid) % 64;
   const size_t p0 = size_t(blockIdx.x) * NP;
   const int nvalid = int(P - (long long)p0 < NP ? P - (long long)p0 : NP);
   const unsigned nv4 = unsigned(nvalid) * (H * W / 4);
   fft.init_twiddles(tid);
   __syncthreads();
   SpecLoadOp<G> op{spec + p0 * H * WF, 1.0f / float(H * W), nvalid};
-  fft.template c2<false, true>(tid, op);
-  fft.template edges<false, true>(tid, op);
-  fft.i1_packed(tid);
-  fft.i2(tid);
-  fft.i3(tid);
-  fft.i4(tid);
+  fft.template c2<false, true>(w, l, op);
+  fft.template edges<false, true>(w, l, op);
+  fft.i1_packed(w, l);
+  fft.i2(w, l);
+  fft.i3(w, l);
+  fft.i4(w, l);
   V4* dst = reinterpret_cast<V4*>(static_cast<TE*>(y) + p0 * H * W);
 #pragma unroll
   for (int i = 0; i < G::JLD; ++i) {
-    const unsigned f = i * NT + tid;
+    const unsigned f = G::v4_slot(w, i, l);
     if (f < nv4) dst[f] = IO::from_f4(fft.v4_load(f));
   }
 }
