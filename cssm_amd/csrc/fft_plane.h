@@ -185,14 +185,41 @@ struct Geom {
     pl = COL / WH;
     v = COL % WH;
   }
-  // 4-vector i of lane l in wave w (load / store phase) -> LDS / global vector index
-  // of the group: consecutive lanes along a row, the two rows of an owned pair alternating
-  static __device__ __forceinline__ unsigned v4_slot(int w, int i, int l) {
-    const int q = i * 64 + l;
-    const int c4 = q % (W / 4), rs = q / (W / 4);
-    const int RP = w * RPW + rs / 2;
-    const int pl = RP / HP, r = RP % HP + (rs % 2) * HP;
-    return unsigned((pl * H + r) * (W / 4) + c4);
+  // ---- load / store phase.  Lane l's 4-vector i (i < JLD) of wave w is column
+  // c4 = l % (W/4) of group row v4_row(w, i, m) (row = pl * H + r): consecutive
+  // lanes run along a row and the two rows of an owned pair alternate, so the
+  // column is fixed per lane and the row advances by RK per i within a plane.
+  static constexpr int C4N = W / 4, RK = 128 / W;
+  static_assert(W <= 128 && 64 % C4N == 0, "load / store mapping needs W <= 128");
+  struct V4Lane {
+    int c4, rp, hh;   // column, row-pair offset, upper row of the pair
+  };
+  static __device__ __forceinline__ V4Lane v4_lane(int l) {
+    return V4Lane{l % C4N, (l / C4N) / 2, (l / C4N) % 2};
+  }
+  // V4_LINEAR: a wave's row pairs lie in one plane, so row(i) = row(0) + RK i
+  static constexpr bool V4_LINEAR = RPW <= HP && HP % RPW == 0;
+  static __device__ __forceinline__ int v4_row(int w, int i, const V4Lane& m) {
+    const int RP = w * RPW + i * RK + m.rp;
+    const int pl = V4_LINEAR ? (w * RPW) / HP : RP / HP;
+    return RP + (pl + m.hh) * HP;   // pl * H + RP % HP + hh * HP
+  }
+  // 4-vector index within the group (planes of H rows of W/4 vectors)
+  static __device__ __forceinline__ unsigned v4_index(int row, const V4Lane& m) {
+    return unsigned(row * C4N + m.c4);
+  }
+  // global byte offset of 4-vector i as a per-lane part and a uniform part
+  // (the uniform part is the row step when V4_LINEAR; planes of H rows of W/4
+  // vectors of VB bytes)
+  template <int VB>
+  static __device__ __forceinline__ void v4_goff(int w, int i, const V4Lane& m, unsigned& voff, int& soff) {
+    if (V4_LINEAR) {
+      voff = unsigned((v4_row(w, 0, m) * C4N + m.c4) * VB);
+      soff = i * RK * C4N * VB;
+    } else {
+      voff = unsigned((v4_row(w, i, m) * C4N + m.c4) * VB);
+      soff = 0;
+    }
   }
 };
 
@@ -215,6 +242,21 @@ struct Buf {
   }
   __device__ __forceinline__ float2 ld2(unsigned off) const {
     return __builtin_bit_cast(float2, __builtin_amdgcn_raw_buffer_load_b64(r, int(off), 0, 0));
+  }
+  // I/O vectors (float4 or 4 x bf16): byte offset voff (per lane) + soff (uniform)
+  __device__ __forceinline__ void ld(float4& v, unsigned voff, int soff) const {
+    v = __builtin_bit_cast(float4, __builtin_amdgcn_raw_buffer_load_b128(r, int(voff), soff, 0));
+  }
+  __device__ __forceinline__ void ld(uint2& v, unsigned voff, int soff) const {
+    v = __builtin_bit_cast(uint2, __builtin_amdgcn_raw_buffer_load_b64(r, int(voff), soff, 0));
+  }
+  __device__ __forceinline__ void st(const float4& v, unsigned voff, int soff) const {
+    typedef unsigned u32x4 __attribute__((__vector_size__(16)));
+    __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(u32x4, v), r, int(voff), soff, 0);
+  }
+  __device__ __forceinline__ void st(const uint2& v, unsigned voff, int soff) const {
+    typedef unsigned u32x2 __attribute__((__vector_size__(8)));
+    __builtin_amdgcn_raw_buffer_store_b64(__builtin_bit_cast(u32x2, v), r, int(voff), soff, 0);
   }
 };
 
@@ -285,30 +327,33 @@ struct PlaneFft {
     for (int i = tid; i < G::N_I3; i += NT) twI3[i] = cconj(tw((i % G::TI3) * (i / G::TI3), W));
   }
 
-  // LDS slot of 4-vector f of the group (row-major over planes and rows)
-  __device__ __forceinline__ void v4_store(unsigned f, float4 v) const {
-    const int pl = int(f / (H * W / 4)), rem = int(f % (H * W / 4));
-    const int r = rem / (W / 4), w = 4 * (rem % (W / 4));
-    const int blk = w / W2, pos = w % W2;
-    if (G::V4_SPLIT && blk >= W1 / 2) {
-      cplx(G::row_off(pl, r) + blk * W2 + (pos ^ 2)) = make_float2(v.x, v.y);
-      cplx(G::row_off(pl, r) + blk * W2 + pos) = make_float2(v.z, v.w);
+  // LDS offsets of 4-vector column c4 within a row: the two float2 halves sit
+  // at a and b (b = a + 2 unless the half-swap of an upper block splits them)
+  struct V4Col {
+    int a, b;
+  };
+  static __device__ __forceinline__ V4Col v4_col(int c4) {
+    const int w = 4 * c4, blk = w / W2, pos = w % W2;
+    if (G::V4_SPLIT && blk >= W1 / 2) return V4Col{blk * W2 + (pos ^ 2), blk * W2 + pos};
+    const int o = blk * W2 + (blk >= W1 / 2 ? (pos ^ G::HALF) : pos);
+    return V4Col{o, o + 2};
+  }
+  __device__ __forceinline__ void v4_put(int row, const V4Col& c, float4 v) const {
+    float* r = buf + row * G::RS;
+    if (G::V4_SPLIT) {
+      *reinterpret_cast<float2*>(r + c.a) = make_float2(v.x, v.y);
+      *reinterpret_cast<float2*>(r + c.b) = make_float2(v.z, v.w);
     } else {
-      const int o = blk >= W1 / 2 ? (pos ^ G::HALF) : pos;
-      *reinterpret_cast<float4*>(buf + G::row_off(pl, r) + blk * W2 + o) = v;
+      *reinterpret_cast<float4*>(r + c.a) = v;
     }
   }
-  __device__ __forceinline__ float4 v4_load(unsigned f) const {
-    const int pl = int(f / (H * W / 4)), rem = int(f % (H * W / 4));
-    const int r = rem / (W / 4), w = 4 * (rem % (W / 4));
-    const int blk = w / W2, pos = w % W2;
-    if (G::V4_SPLIT && blk >= W1 / 2) {
-      const float2 lo = cplx(G::row_off(pl, r) + blk * W2 + (pos ^ 2));
-      const float2 hi = cplx(G::row_off(pl, r) + blk * W2 + pos);
+  __device__ __forceinline__ float4 v4_get(int row, const V4Col& c) const {
+    const float* r = buf + row * G::RS;
+    if (G::V4_SPLIT) {
+      const float2 lo = *reinterpret_cast<const float2*>(r + c.a), hi = *reinterpret_cast<const float2*>(r + c.b);
       return make_float4(lo.x, lo.y, hi.x, hi.y);
     }
-    const int o = blk >= W1 / 2 ? (pos ^ G::HALF) : pos;
-    return *reinterpret_cast<const float4*>(buf + G::row_off(pl, r) + blk * W2 + o);
+    return *reinterpret_cast<const float4*>(r + c.a);
   }
 
   // ---------------------------------------------- R1: DFT-W1 over m, twiddle

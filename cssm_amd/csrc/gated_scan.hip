@@ -127,14 +127,23 @@ gated_scan_pow2(const ScanArgs a) {
     for (int k = 0; k < 4; ++k) hE[j][k] = make_float2(0.f, 0.f);
 
   // u_0 into the plane buffer (each wave loads the rows it owns)
+  constexpr int VB = int(sizeof(V4));
+  constexpr unsigned GROUP_BYTES = unsigned(NP * H * W * sizeof(TE));
   __syncthreads();   // twiddle tables
   {
-    const V4* src = reinterpret_cast<const V4*>(up + group_elems(0));
+    const auto m = G::v4_lane(ln);
+    const auto col = PlaneFft<G>::v4_col(m.c4);
+    const Buf ub(up + group_elems(0), GROUP_BYTES);
     V4 ld[G::JLD];
 #pragma unroll
-    for (int i = 0; i < G::JLD; ++i) ld[i] = src[G::v4_slot(wv, i, ln)];
+    for (int i = 0; i < G::JLD; ++i) {
+      unsigned vo;
+      int so;
+      G::template v4_goff<VB>(wv, i, m, vo, so);
+      ub.ld(ld[i], vo, so);
+    }
 #pragma unroll
-    for (int i = 0; i < G::JLD; ++i) fft.v4_store(G::v4_slot(wv, i, ln), act4(IO::to_f4(ld[i]), a.u_act));
+    for (int i = 0; i < G::JLD; ++i) fft.v4_put(G::v4_row(wv, i, m), col, act4(IO::to_f4(ld[i]), a.u_act));
   }
   wave_sync();
 
@@ -161,28 +170,35 @@ gated_scan_pow2(const ScanArgs a) {
     // (in chunks of CH vectors to bound the registers in flight)
     {
       constexpr int CH = G::JLD < 8 ? G::JLD : 8;
-      const V4* zsrc = reinterpret_cast<const V4*>(zp + group_elems(t));
-      const V4* usrc = reinterpret_cast<const V4*>(up + group_elems(t + 1 < T ? t + 1 : t));
-      V4* dst = reinterpret_cast<V4*>(yp + group_elems(t));
+      const auto m = G::v4_lane(lane);
+      const auto col = PlaneFft<G>::v4_col(m.c4);
+      const Buf zb(zp + group_elems(t), GROUP_BYTES);
+      const Buf ub(up + group_elems(t + 1 < T ? t + 1 : t), GROUP_BYTES);
+      const Buf yb(yp + group_elems(t), GROUP_BYTES);
 #pragma unroll
       for (int c = 0; c < G::JLD; c += CH) {
         V4 ldg[CH], ldu[CH];
 #pragma unroll
-        for (int i = 0; i < CH; ++i) ldg[i] = zsrc[G::v4_slot(wv, c + i, lane)];
-        if (t + 1 < T) {
-#pragma unroll
-          for (int i = 0; i < CH; ++i) ldu[i] = usrc[G::v4_slot(wv, c + i, lane)];
+        for (int i = 0; i < CH; ++i) {
+          unsigned vo;
+          int so;
+          G::template v4_goff<VB>(wv, c + i, m, vo, so);
+          zb.ld(ldg[i], vo, so);
+          if (t + 1 < T) ub.ld(ldu[i], vo, so);
         }
 #pragma unroll
         for (int i = 0; i < CH; ++i) {
-          const unsigned f = G::v4_slot(wv, c + i, lane);
-          const float4 yv = fft.v4_load(f);
+          unsigned vo;
+          int so;
+          G::template v4_goff<VB>(wv, c + i, m, vo, so);
+          const float4 yv = fft.v4_get(G::v4_row(wv, c + i, m), col);
           const float4 gv = act4(IO::to_f4(ldg[i]), a.z_act);
-          dst[f] = IO::from_f4(make_float4(yv.x * gv.x, yv.y * gv.y, yv.z * gv.z, yv.w * gv.w));
+          yb.st(IO::from_f4(make_float4(yv.x * gv.x, yv.y * gv.y, yv.z * gv.z, yv.w * gv.w)), vo, so);
         }
         if (t + 1 < T) {
 #pragma unroll
-          for (int i = 0; i < CH; ++i) fft.v4_store(G::v4_slot(wv, c + i, lane), act4(IO::to_f4(ldu[i]), a.u_act));
+          for (int i = 0; i < CH; ++i)
+            fft.v4_put(G::v4_row(wv, c + i, m), col, act4(IO::to_f4(ldu[i]), a.u_act));
         }
         __builtin_amdgcn_sched_barrier(0);
       }

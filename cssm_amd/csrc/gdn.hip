@@ -146,14 +146,16 @@ rfft2_planes(const void* __restrict__ x, long long P, float2* __restrict__ spec,
   __syncthreads();
   {
     const V4* src = reinterpret_cast<const V4*>(static_cast<const TE*>(x) + p0 * H * W);
+    const auto m = G::v4_lane(l);
+    const auto col = PlaneFft<G>::v4_col(m.c4);
     V4 ld[G::JLD];
 #pragma unroll
     for (int i = 0; i < G::JLD; ++i) {
-      const unsigned f = G::v4_slot(w, i, l);
+      const unsigned f = G::v4_index(G::v4_row(w, i, m), m);
       ld[i] = f < nv4 ? src[f] : V4{};
     }
 #pragma unroll
-    for (int i = 0; i < G::JLD; ++i) fft.v4_store(G::v4_slot(w, i, l), IO::to_f4(ld[i]));
+    for (int i = 0; i < G::JLD; ++i) fft.v4_put(G::v4_row(w, i, m), col, IO::to_f4(ld[i]));
   }
   wave_sync();
   SpecStoreOp<G> op{spec + p0 * H * WF, norms ? part_c2 : nullptr, norms ? part_e : nullptr, nvalid};
@@ -210,10 +212,13 @@ irfft2_planes(const float2* __restrict__ spec, long long P, void* __restrict__ y
   fft.i3(w, l);
   fft.i4(w, l);
   V4* dst = reinterpret_cast<V4*>(static_cast<TE*>(y) + p0 * H * W);
+  const auto m = G::v4_lane(l);
+  const auto col = PlaneFft<G>::v4_col(m.c4);
 #pragma unroll
   for (int i = 0; i < G::JLD; ++i) {
-    const unsigned f = G::v4_slot(w, i, l);
-    if (f < nv4) dst[f] = IO::from_f4(fft.v4_load(f));
+    const int row = G::v4_row(w, i, m);
+    const unsigned f = G::v4_index(row, m);
+    if (f < nv4) dst[f] = IO::from_f4(fft.v4_get(row, col));
   }
 }
 
