@@ -156,15 +156,18 @@ struct Geom {
   static __device__ __forceinline__ bool owns_edge(int w) { return (w * CPW) % WH == 0; }
   static __device__ __forceinline__ int edge_plane0(int w) { return (w * CPW) / WH; }
 
-  // R1/I4 job j of lane l in wave w -> (pl, p, s): s fastest; the row groups
-  // of one instruction are two rows apart, so the row stride's bank shift (4)
-  // becomes 8
+  // R1/I4 job j of lane l in wave w -> (pl, p, s): s fastest.  LDS serves 32
+  // lanes of 4-byte accesses per cycle from 32 banks and a row shifts the banks
+  // by 4 (RS = W + 4), so with W2 = 8 the RG/2 rows of a half-wave are taken two
+  // apart (even rows in lanes 0-31, odd rows in lanes 32-63 of each block of RG
+  // row pairs): RG/2 rows x W2 lanes then hit each bank once.  With W2 = 4
+  // consecutive rows already do.
   static constexpr int RG = 64 / W2;
-  static constexpr bool R1_STRIDE2 = (RG >= 2) && (RPW % (2 * RG) == 0);
+  static constexpr bool R1_STRIDE2 = (W2 == 8) && (RPW % RG == 0);
   static __device__ __forceinline__ void r1_job(int w, int j, int l, int& pl, int& p, int& s) {
     s = l % W2;
     const int g = j * RG + l / W2;
-    const int rp = R1_STRIDE2 ? ((g % RG) * 2 + (g / RG) % 2 + 2 * RG * (g / (2 * RG))) : g;
+    const int rp = R1_STRIDE2 ? (2 * (g % (RG / 2)) + (g / (RG / 2)) % 2 + RG * (g / RG)) : g;
     const int RP = w * RPW + rp;
     pl = RP / HP;
     p = RP % HP;

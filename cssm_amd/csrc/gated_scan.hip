@@ -57,40 +57,51 @@ struct ScanArgs {
 };
 
 
-// C2 / edge policy of the fused scan: the state of the thread's bins lives in
-// registers for the whole launch (h: C2 units, hE: DC / Nyquist bins).
+// C2 / edge policy of the fused scan: the state of the thread's C2 bins lives
+// in registers for the whole launch (h); the DC / Nyquist bins, which only the
+// waves owning a packed column touch, keep theirs in LDS (hE).
 template <class G>
 struct GatedScanOp {
   static constexpr int H = G::H, WH = G::WH, WF = G::WF, H1 = G::H1, H2 = G::H2;
   float2 (&h)[G::JC2][2][G::H2];
-  float2 (&hE)[G::JE][4];
+  float2* hE;   // LDS: state of the DC / Nyquist bins, 4 per edge job (pl, e)
   Buf gbuf;   // gates of (b, t): (H, WF) float4
   Buf kbuf;   // K_hat of the group's planes: (NP, H, WF) float2
 
   // gates of (b, t) and the spectral kernel of this plane at bins (k + H1 q, v)
   __device__ __forceinline__ void bins(int j, int a2, int pl, int k, int v, float2 (&sp)[G::H2]) const {
     const unsigned gi = unsigned(k * WF + v), ki = unsigned(pl * H * WF) + gi;
-    float4 gq[H2];
-    float2 kq[H2];
+    // gates in batches of QB bins (fewer registers in flight at 4 waves / SIMD)
+    constexpr int QB = G::NT >= 512 ? 4 : H2;
 #pragma unroll
-    for (int q = 0; q < H2; ++q) {
-      gq[q] = gbuf.ld4((gi + q * H1 * WF) * 16u);
-      kq[q] = kbuf.ld2((ki + q * H1 * WF) * 8u);
+    for (int q0 = 0; q0 < H2; q0 += QB) {
+      float4 gq[QB];
+      float2 kq[QB];
+#pragma unroll
+      for (int q = 0; q < QB; ++q) {
+        gq[q] = gbuf.ld4((gi + (q0 + q) * H1 * WF) * 16u);
+        kq[q] = kbuf.ld2((ki + (q0 + q) * H1 * WF) * 8u);
+      }
+#pragma unroll
+      for (int q = 0; q < QB; ++q) sp[q0 + q] = scan_bin(h[j][a2][q0 + q], sp[q0 + q], gq[q], kq[q]);
     }
-#pragma unroll
-    for (int q = 0; q < H2; ++q) sp[q] = scan_bin(h[j][a2][q], sp[q], gq[q], kq[q]);
   }
 
   __device__ __forceinline__ void edge(int j, int pl, int uA, int uB, int, float2 (&v4)[4]) const {
     const unsigned kp = unsigned(pl * H * WF);
     const unsigned bi[4] = {unsigned(uA * WF), unsigned(uA * WF + WH), unsigned(uB * WF), unsigned(uB * WF + WH)};
 #pragma unroll
-    for (int i = 0; i < 4; ++i) v4[i] = scan_bin(hE[j][i], v4[i], gbuf.ld4(bi[i] * 16u), kbuf.ld2((kp + bi[i]) * 8u));
+    for (int i = 0; i < 4; ++i) {
+      float2& hs = hE[(pl * G::HP + uA) * 4 + i];
+      float2 hv = hs;
+      v4[i] = scan_bin(hv, v4[i], gbuf.ld4(bi[i] * 16u), kbuf.ld2((kp + bi[i]) * 8u));
+      hs = hv;
+    }
   }
 };
 
 template <int LH, int LW, int NP, int PPT, class IO>
-__global__ void __launch_bounds__((NP << (LH + LW)) / PPT, PPT >= 64 ? 2 : 1)
+__global__ void __launch_bounds__((NP << (LH + LW)) / PPT, PPT >= 64 ? 2 : ((NP << (LH + LW)) / PPT >= 512 ? 4 : 1))
 gated_scan_pow2(const ScanArgs a) {
   using G = Geom<LH, LW, NP, PPT>;
   static_assert(G::NT == (NP << (LH + LW)) / PPT, "launch bound");
@@ -115,16 +126,15 @@ gated_scan_pow2(const ScanArgs a) {
   fft.init_twiddles(threadIdx.x);
   const int wv = __builtin_amdgcn_readfirstlane(int(threadIdx.x) / 64), ln = int(threadIdx.x) % 64;
 
+  // state: the C2 bins of this thread in VGPRs, the DC / Nyquist bins (touched
+  // only by the waves owning a packed column) in LDS
+  __shared__ float2 hE[NP * G::HP * 4];
   float2 h[G::JC2][2][H2];
-  float2 hE[G::JE][4];
 #pragma unroll
   for (int j = 0; j < G::JC2; ++j)
 #pragma unroll
     for (int q = 0; q < H2; ++q) h[j][0][q] = h[j][1][q] = make_float2(0.f, 0.f);
-#pragma unroll
-  for (int j = 0; j < G::JE; ++j)
-#pragma unroll
-    for (int k = 0; k < 4; ++k) hE[j][k] = make_float2(0.f, 0.f);
+  for (int i = threadIdx.x; i < NP * G::HP * 4; i += NT) hE[i] = make_float2(0.f, 0.f);
 
   // u_0 into the plane buffer (each wave loads the rows it owns)
   constexpr int VB = int(sizeof(V4));
@@ -169,7 +179,7 @@ gated_scan_pow2(const ScanArgs a) {
     // ---------- STORE y_t = y * z_gate, and LOAD u_{t+1} into the same slots
     // (in chunks of CH vectors to bound the registers in flight)
     {
-      constexpr int CH = G::JLD < 8 ? G::JLD : 8;
+      constexpr int CH = NT >= 512 ? 4 : (G::JLD < 8 ? G::JLD : 8);
       const auto m = G::v4_lane(lane);
       const auto col = PlaneFft<G>::v4_col(m.c4);
       const Buf zb(zp + group_elems(t), GROUP_BYTES);
@@ -428,7 +438,7 @@ static hipError_t dispatch_scan(const ScanArgs& a, int B, int H, int W, hipStrea
   if (np == NP_) return run_scan<LH, LH, NP_, PPT_, IO>(a, B, s);
   if (H == 128 && W == 128) {
     const int np = pick({1});
-    CSSM_SCAN_CASE(7, 1, 64)
+    CSSM_SCAN_CASE(7, 1, 32)
   } else if (H == 64 && W == 64) {
     const int np = pick({4, 2, 1});
     CSSM_SCAN_CASE(6, 4, 64) CSSM_SCAN_CASE(6, 2, 64) CSSM_SCAN_CASE(6, 1, 64)
