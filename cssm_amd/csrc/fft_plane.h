@@ -246,20 +246,24 @@ struct Buf {
   __device__ __forceinline__ float2 ld2(unsigned off) const {
     return __builtin_bit_cast(float2, __builtin_amdgcn_raw_buffer_load_b64(r, int(off), 0, 0));
   }
-  // I/O vectors (float4 or 4 x bf16): byte offset voff (per lane) + soff (uniform)
+  // Streamed I/O vectors (float4 or 4 x bf16; each touched once): byte offset
+  // voff (per lane) + soff (uniform), non-temporal cache policy so the planes
+  // passing through do not evict what the workgroups re-read from L2 every
+  // step (per-bin gates, spectral kernel)
+  static constexpr int kStream = 2;   // cache-policy operand: NT
   __device__ __forceinline__ void ld(float4& v, unsigned voff, int soff) const {
-    v = __builtin_bit_cast(float4, __builtin_amdgcn_raw_buffer_load_b128(r, int(voff), soff, 0));
+    v = __builtin_bit_cast(float4, __builtin_amdgcn_raw_buffer_load_b128(r, int(voff), soff, kStream));
   }
   __device__ __forceinline__ void ld(uint2& v, unsigned voff, int soff) const {
-    v = __builtin_bit_cast(uint2, __builtin_amdgcn_raw_buffer_load_b64(r, int(voff), soff, 0));
+    v = __builtin_bit_cast(uint2, __builtin_amdgcn_raw_buffer_load_b64(r, int(voff), soff, kStream));
   }
   __device__ __forceinline__ void st(const float4& v, unsigned voff, int soff) const {
     typedef unsigned u32x4 __attribute__((__vector_size__(16)));
-    __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(u32x4, v), r, int(voff), soff, 0);
+    __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(u32x4, v), r, int(voff), soff, kStream);
   }
   __device__ __forceinline__ void st(const uint2& v, unsigned voff, int soff) const {
     typedef unsigned u32x2 __attribute__((__vector_size__(8)));
-    __builtin_amdgcn_raw_buffer_store_b64(__builtin_bit_cast(u32x2, v), r, int(voff), soff, 0);
+    __builtin_amdgcn_raw_buffer_store_b64(__builtin_bit_cast(u32x2, v), r, int(voff), soff, kStream);
   }
 };
 

@@ -251,10 +251,11 @@ hipError_t run_inv(const float2* spec, long long P, void* y, hipStream_t s) {
 }
 
 // the plane groups of the fused gated scan, per plane size
-#define CSSM_FFT_TABLE(CASE)                                                        \
+// (PPT128: samples per thread at 128 x 128; 64 = 256 threads, 32 = 512 threads)
+#define CSSM_FFT_TABLE(CASE, PPT128)                                                \
   if (H == 128) {                                                                   \
     const int np = pick_group(P, {1});                                              \
-    CASE(7, 1, 64)                                                                  \
+    CASE(7, 1, PPT128)                                                              \
   } else if (H == 64) {                                                             \
     const int np = pick_group(P, {4, 2, 1});                                        \
     CASE(6, 4, 64) CASE(6, 2, 64) CASE(6, 1, 64)                                    \
@@ -276,7 +277,7 @@ template <class IO>
 hipError_t dispatch_fwd(const void* x, long long P, int H, float2* spec, float* norms, hipStream_t s) {
 #define CSSM_FWD_CASE(LH, NP_, PPT_) \
   if (np == NP_) return run_fwd<LH, NP_, PPT_, IO>(x, P, spec, norms, s);
-  CSSM_FFT_TABLE(CSSM_FWD_CASE)
+  CSSM_FFT_TABLE(CSSM_FWD_CASE, 64)
 #undef CSSM_FWD_CASE
   return hipErrorInvalidValue;
 }
@@ -285,7 +286,7 @@ template <class IO>
 hipError_t dispatch_inv(const float2* spec, long long P, int H, void* y, hipStream_t s) {
 #define CSSM_INV_CASE(LH, NP_, PPT_) \
   if (np == NP_) return run_inv<LH, NP_, PPT_, IO>(spec, P, y, s);
-  CSSM_FFT_TABLE(CSSM_INV_CASE)
+  CSSM_FFT_TABLE(CSSM_INV_CASE, 32)
 #undef CSSM_INV_CASE
   return hipErrorInvalidValue;
 }
