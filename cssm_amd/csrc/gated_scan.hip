@@ -163,6 +163,7 @@ gated_scan_pow2(const ScanArgs a) {
     // hundreds of them into registers for the whole scan.
     int lane = ln;
     asm volatile("" : "+v"(lane));
+    __builtin_assume(lane >= 0 && lane < 64);   // keeps the index arithmetic unsigned and 24-bit
     GatedScanOp<G> op{h, hE, Buf(a.gates + (size_t(b) * T + t) * size_t(H) * WF, unsigned(H * WF * sizeof(float4))),
                       Buf(a.khat + size_t(c0) * H * WF, unsigned(NP * H * WF * sizeof(float2)))};
 
@@ -174,27 +175,47 @@ gated_scan_pow2(const ScanArgs a) {
     fft.i1_packed(wv, lane);
     fft.i2(wv, lane);
     fft.i3(wv, lane);
+    // z_t of the first chunk of this wave's rows is issued before the last
+    // inverse pass, so those loads are in flight while it runs
+    constexpr int CH = NT >= 512 ? 4 : (G::JLD < 8 ? G::JLD : 8);
+    const auto m = G::v4_lane(lane);
+    const Buf zb(zp + group_elems(t), GROUP_BYTES);
+    V4 ldg[CH];
+#pragma unroll
+    for (int i = 0; i < CH; ++i) {
+      unsigned vo;
+      int so;
+      G::template v4_goff<VB>(wv, i, m, vo, so);
+      zb.ld(ldg[i], vo, so);
+    }
     fft.i4(wv, lane);
 
     // ---------- STORE y_t = y * z_gate, and LOAD u_{t+1} into the same slots
     // (in chunks of CH vectors to bound the registers in flight)
     {
-      constexpr int CH = NT >= 512 ? 4 : (G::JLD < 8 ? G::JLD : 8);
-      const auto m = G::v4_lane(lane);
       const auto col = PlaneFft<G>::v4_col(m.c4);
-      const Buf zb(zp + group_elems(t), GROUP_BYTES);
       const Buf ub(up + group_elems(t + 1 < T ? t + 1 : t), GROUP_BYTES);
       const Buf yb(yp + group_elems(t), GROUP_BYTES);
 #pragma unroll
       for (int c = 0; c < G::JLD; c += CH) {
-        V4 ldg[CH], ldu[CH];
+        V4 ldu[CH];
+        if (c > 0) {
 #pragma unroll
-        for (int i = 0; i < CH; ++i) {
-          unsigned vo;
-          int so;
-          G::template v4_goff<VB>(wv, c + i, m, vo, so);
-          zb.ld(ldg[i], vo, so);
-          if (t + 1 < T) ub.ld(ldu[i], vo, so);
+          for (int i = 0; i < CH; ++i) {
+            unsigned vo;
+            int so;
+            G::template v4_goff<VB>(wv, c + i, m, vo, so);
+            zb.ld(ldg[i], vo, so);
+          }
+        }
+        if (t + 1 < T) {
+#pragma unroll
+          for (int i = 0; i < CH; ++i) {
+            unsigned vo;
+            int so;
+            G::template v4_goff<VB>(wv, c + i, m, vo, so);
+            ub.ld(ldu[i], vo, so);
+          }
         }
 #pragma unroll
         for (int i = 0; i < CH; ++i) {
