@@ -117,19 +117,49 @@ __global__ void gated_gates_kernel(const float* __restrict__ ctx, int C, int H, 
   __syncthreads();
   const int nbin = H * WF;
   if (factored) {
+    // the 3 (H + WF) row / column dot products over C; small planes (few
+    // products, long C) split each over P threads and sum the parts in LDS
     const int nv = 3 * (H + WF);
-    for (int idx = threadIdx.x; idx < nv; idx += blockDim.x) {
-      const int g = idx / (H + WF), r = idx % (H + WF);
-      float acc;
-      if (r < H) {
-        acc = gw.bd[g][r];
-        for (int c = 0; c < C; ++c) acc = fmaf(cx[c], gw.kd[g][size_t(c) * H + r], acc);
-      } else {
-        const int v = r - H;
-        acc = gw.bw[g][v];
-        for (int c = 0; c < C; ++c) acc = fmaf(cx[c], gw.kw[g][size_t(c) * WF + v], acc);
+    const int P = nv >= int(blockDim.x) ? 1 : int(blockDim.x) / nv;
+    if (P == 1) {
+      for (int idx = threadIdx.x; idx < nv; idx += blockDim.x) {
+        const int g = idx / (H + WF), r = idx % (H + WF);
+        float acc;
+        if (r < H) {
+          acc = gw.bd[g][r];
+#pragma unroll 8
+          for (int c = 0; c < C; ++c) acc = fmaf(cx[c], gw.kd[g][size_t(c) * H + r], acc);
+        } else {
+          const int v = r - H;
+          acc = gw.bw[g][v];
+#pragma unroll 8
+          for (int c = 0; c < C; ++c) acc = fmaf(cx[c], gw.kw[g][size_t(c) * WF + v], acc);
+        }
+        fac[idx] = acc;
       }
-      fac[idx] = acc;
+    } else {
+      float* part = fac + nv;   // P * nv partial sums
+      for (int q = threadIdx.x; q < nv * P; q += blockDim.x) {
+        const int idx = q % nv, pc = q / nv;
+        const int g = idx / (H + WF), r = idx % (H + WF);
+        float acc = 0.0f;
+        // (loads unrolled so several are in flight: the weights come from L2)
+        if (r < H) {
+#pragma unroll 8
+          for (int c = pc; c < C; c += P) acc = fmaf(cx[c], gw.kd[g][size_t(c) * H + r], acc);
+        } else {
+#pragma unroll 8
+          for (int c = pc; c < C; c += P) acc = fmaf(cx[c], gw.kw[g][size_t(c) * WF + (r - H)], acc);
+        }
+        part[pc * nv + idx] = acc;
+      }
+      __syncthreads();
+      for (int idx = threadIdx.x; idx < nv; idx += blockDim.x) {
+        const int g = idx / (H + WF), r = idx % (H + WF);
+        float acc = r < H ? gw.bd[g][r] : gw.bw[g][r - H];
+        for (int pc = 0; pc < P; ++pc) acc += part[pc * nv + idx];
+        fac[idx] = acc;
+      }
     }
     __syncthreads();
     for (int o = threadIdx.x; o < nbin; o += blockDim.x) {
@@ -145,6 +175,7 @@ __global__ void gated_gates_kernel(const float* __restrict__ ctx, int C, int H, 
       for (int g = 0; g < 3; ++g) {
         float acc = gw.bd[g][o];
         const float* kk = gw.kd[g] + o;
+#pragma unroll 8
         for (int c = 0; c < C; ++c) acc = fmaf(cx[c], kk[size_t(c) * nbin], acc);
         gr[g] = acc;
       }
@@ -156,7 +187,8 @@ __global__ void gated_gates_kernel(const float* __restrict__ ctx, int C, int H, 
 
 // ---------------------------------------------------------------------------
 // mean over (H, W) of each plane of a plane-major tensor (cssm.py:536),
-// optionally after SiLU.  One block per plane; bf16 or f32 input.
+// optionally after SiLU; bf16 or f32 input.  Planes of up to 1024 samples
+// share a 256-thread block (16-64 lanes each); larger ones get a block each.
 // ---------------------------------------------------------------------------
 template <class TIN>
 __device__ __forceinline__ float load_as_f32(const TIN* p, size_t i);
@@ -168,24 +200,33 @@ __device__ __forceinline__ float load_as_f32<uint16_t>(const uint16_t* p, size_t
 }
 
 template <class TIN>
-__global__ void plane_mean_kernel(const TIN* __restrict__ x, int HW, int act, float* __restrict__ out) {
-  __shared__ float red[32];
-  const size_t base = size_t(blockIdx.x) * HW;
+__global__ void plane_mean_kernel(const TIN* __restrict__ x, long long nplanes, int HW, int L, int act,
+                                  float* __restrict__ out) {
+  // L lanes per plane (a power of two <= 64 dividing the wave, or the whole
+  // 256-thread block when L == 256): small planes share a block
+  __shared__ float red[4];
+  const int per = int(blockDim.x) / L;
+  const int sub = int(threadIdx.x) / L, li = int(threadIdx.x) % L;
+  const long long plane = (long long)blockIdx.x * per + sub;
   float acc = 0.0f;
-  for (int i = threadIdx.x; i < HW; i += blockDim.x) {
-    float v = load_as_f32<TIN>(x, base + i);
-    if (act == 1) v = v / (1.0f + expf(-v));
-    acc += v;
+  if (plane < nplanes) {
+    const size_t base = size_t(plane) * HW;
+    for (int i = li; i < HW; i += L) {
+      float v = load_as_f32<TIN>(x, base + i);
+      if (act == 1) v = v / (1.0f + expf(-v));
+      acc += v;
+    }
   }
-  for (int off = 32; off > 0; off >>= 1) acc += __shfl_down(acc, off, 64);
+  const int width = L < 64 ? L : 64;
+  for (int off = width / 2; off > 0; off >>= 1) acc += __shfl_xor(acc, off, 64);
+  if (L <= 64) {
+    if (li == 0 && plane < nplanes) out[plane] = acc / float(HW);
+    return;
+  }
   const int lane = threadIdx.x & 63, wid = threadIdx.x >> 6;
   if (lane == 0) red[wid] = acc;
   __syncthreads();
-  if (threadIdx.x == 0) {
-    float s = 0.0f;
-    for (int w = 0; w < int(blockDim.x >> 6); ++w) s += red[w];
-    out[blockIdx.x] = s / float(HW);
-  }
+  if (threadIdx.x == 0 && plane < nplanes) out[plane] = ((red[0] + red[1]) + (red[2] + red[3])) / float(HW);
 }
 
 // ----------------------------------------------------------------- launchers
@@ -204,19 +245,26 @@ hipError_t launch_spectral_kernel(const float* k, int C, int K, int H, int W, fl
 hipError_t launch_plane_mean(const void* x, int dtype, long long nplanes, int HW, int act, float* out,
                              hipStream_t s) {
   if (nplanes <= 0) return hipSuccess;
+  // lanes per plane: about 4 elements per lane, 16 .. 64 lanes, or the whole block for large planes
+  int L = 16;
+  while (L < 64 && L * 4 < HW) L *= 2;
+  if (HW > 64 * 16) L = 256;
+  const long long blocks = (nplanes + 256 / L - 1) / (256 / L);
   if (dtype == 0)
-    hipLaunchKernelGGL(plane_mean_kernel<float>, dim3(unsigned(nplanes)), dim3(256), 0, s,
-                       static_cast<const float*>(x), HW, act, out);
+    hipLaunchKernelGGL(plane_mean_kernel<float>, dim3(unsigned(blocks)), dim3(256), 0, s,
+                       static_cast<const float*>(x), nplanes, HW, L, act, out);
   else
-    hipLaunchKernelGGL(plane_mean_kernel<uint16_t>, dim3(unsigned(nplanes)), dim3(256), 0, s,
-                       static_cast<const uint16_t*>(x), HW, act, out);
+    hipLaunchKernelGGL(plane_mean_kernel<uint16_t>, dim3(unsigned(blocks)), dim3(256), 0, s,
+                       static_cast<const uint16_t*>(x), nplanes, HW, L, act, out);
   return hipGetLastError();
 }
 
 hipError_t launch_gated_gates(const float* ctx, int BT, int C, int H, int W, int factored, int act,
                               const GateWeights& w, float c_scale, float4* gates, hipStream_t s) {
   const int WF = W / 2 + 1;
-  const size_t shm = (size_t(C) + 3 * size_t(H + WF)) * sizeof(float);
+  const int nv = 3 * (H + WF);
+  const int P = nv >= 256 ? 1 : 256 / nv;   // partial sums per factored product (see the kernel)
+  const size_t shm = (size_t(C) + size_t(nv) * (1 + P)) * sizeof(float);
   if (shm > 64 * 1024) return hipErrorInvalidValue;
   hipLaunchKernelGGL(gated_gates_kernel, dim3(BT), dim3(256), shm, s, ctx, C, H, W, factored, act, w,
                      c_scale, gates);

@@ -174,74 +174,6 @@ proj_in_kernel(const TI* __restrict__ X, int M, int K, int N, const float* __res
   }
 }
 
-// ---------------------------------------------------------------------------
-// proj_out: out[f*HW + p][n] = sum_k Y[f][k][p] W[k][n] + b[n]
-// ---------------------------------------------------------------------------
-template <int TM, int TN, int WMW, int WNW, class TI, class TO>
-__global__ void __launch_bounds__(64 * WMW * WNW)
-proj_out_kernel(const TI* __restrict__ Y, int M, int K, int N, const float* __restrict__ Wt,
-                const float* __restrict__ bias, int HW, TO* __restrict__ out) {
-  using P = ProjTile<TM, TN, WMW, WNW>;
-  __shared__ float As[TM * P::AP];
-  __shared__ float Bs[P::KC * P::BP];
-  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-  const int wm = wave / WNW, wn = wave % WNW;
-  const int m0 = blockIdx.x * TM, n0 = blockIdx.y * TN;
-
-  floatx4 acc[P::MT][P::NTL];
-#pragma unroll
-  for (int i = 0; i < P::MT; ++i)
-#pragma unroll
-    for (int j = 0; j < P::NTL; ++j) acc[i][j] = floatx4{0.f, 0.f, 0.f, 0.f};
-
-  for (int k0 = 0; k0 < K; k0 += P::KC) {
-    // A tile from plane-major Y: consecutive threads walk the pixels of one channel
-    for (int i = tid; i < TM * P::KC; i += P::NT) {
-      const int kk = i / TM, r = i % TM;
-      const int gm = m0 + r, gk = k0 + kk;
-      float v = 0.0f;
-      if (gm < M && gk < K) {
-        const int f = gm / HW, p = gm % HW;
-        v = ld_el(Y, (size_t(f) * K + gk) * HW + p);
-      }
-      As[r * P::AP + kk] = v;
-    }
-    for (int i = tid; i < P::KC * TN; i += P::NT) {
-      const int kk = i / TN, c = i % TN;
-      const int gk = k0 + kk, gn = n0 + c;
-      Bs[kk * P::BP + c] = (gk < K && gn < N) ? Wt[size_t(gk) * N + gn] : 0.0f;
-    }
-    __syncthreads();
-#pragma unroll
-    for (int kk = 0; kk < P::KC; kk += 4) {
-      float a[P::MT], b[P::NTL];
-#pragma unroll
-      for (int i = 0; i < P::MT; ++i)
-        a[i] = As[((wm * P::MT + i) * 16 + (lane & 15)) * P::AP + kk + (lane >> 4)];
-#pragma unroll
-      for (int j = 0; j < P::NTL; ++j) b[j] = Bs[(kk + (lane >> 4)) * P::BP + (wn * P::NTL + j) * 16 + (lane & 15)];
-#pragma unroll
-      for (int i = 0; i < P::MT; ++i)
-#pragma unroll
-        for (int j = 0; j < P::NTL; ++j) acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x4f32(a[i], b[j], acc[i][j], 0, 0, 0);
-    }
-    __syncthreads();
-  }
-#pragma unroll
-  for (int j = 0; j < P::NTL; ++j) {
-    const int gn = n0 + (wn * P::NTL + j) * 16 + (lane & 15);
-    if (gn >= N) continue;
-    const float bv = bias[gn];
-#pragma unroll
-    for (int i = 0; i < P::MT; ++i)
-#pragma unroll
-      for (int r = 0; r < 4; ++r) {
-        const int gm = m0 + (wm * P::MT + i) * 16 + (lane >> 4) * 4 + r;
-        if (gm < M) st_el(out, size_t(gm) * N + gn, acc[i][j][r] + bv);
-      }
-  }
-}
-
 // ctx[f][c] = sum_t partial[f * tiles_per_frame + t][c] / HW
 __global__ void ctx_reduce_kernel(const float* __restrict__ partial, int F, int tiles_per_frame, int C, float inv_hw,
                                   float* __restrict__ ctx) {
@@ -624,6 +556,208 @@ proj_persist_kernel(const TI* __restrict__ A, int M, int K, int N, const float* 
   }
 }
 
+// ---------------------------------------------------------------------------
+// K-chunked projection for K beyond the persistent kernel's register-resident
+// weights (the CSSM-SHViT stages: K = 128 .. 640), on bf16 MFMA with both
+// operands split three ways and the same six products as the persistent
+// kernel (fp32-level results).  One 128 x 128 output tile per workgroup; K
+// advances in chunks of 32: the next chunk's A and B are loaded into registers
+// while the MFMAs run on the current one, then split into three bf16 planes in
+// LDS, A as [row][k] and B as [column][k] (k contiguous, the MFMA operand
+// order).  Four waves split the 128 columns (32 each) and keep all 128 rows,
+// as in the persistent kernel, so the proj_in channel sums stay in-wave.
+//   PLANE_A = false: A is channels-last (M, K), K % 4 == 0; true: plane-major (F, K, HW).
+//   OUT_SPLIT = true: plane-major output(s) as proj_in; false: channels-last (M, N).
+// ---------------------------------------------------------------------------
+template <bool PLANE_A, bool OUT_SPLIT, class TI, class TO>
+__global__ void __launch_bounds__(256, 2)
+proj_kc_kernel(const TI* __restrict__ A, int M, int K, int N, const float* __restrict__ Wt,
+               const float* __restrict__ bias, int HW, TO* __restrict__ out_lo, TO* __restrict__ out_hi,
+               int act_lo, int act_hi, float* __restrict__ partial, int NH) {
+  constexpr int TM = 128, TN = 128, NT = 256, KC = 32, KP = KC + 8, MI = TM / 16;
+  constexpr int OP = TN + 4;   // channels-last staging pitch (floats), 64 rows at a time
+  constexpr int AB = TM * KP;  // bf16 per plane (TM == TN)
+  __shared__ __attribute__((aligned(16))) __bf16 lds[6 * AB];   // A1 A2 A3 B1 B2 B3
+  static_assert(64 * OP * 4 <= 6 * AB * 2, "staging of half an output tile fits the operand planes");
+  __bf16* const Ap = lds;
+  __bf16* const Bp = lds + 3 * AB;
+  const int tid = threadIdx.x, lane = tid & 63, wn = tid >> 6;
+  const int m0 = blockIdx.x * TM, n0 = blockIdx.y * TN;
+  const int NL = N - NH;
+
+  // this thread's loads per chunk: 4 groups of 4 consecutive k
+  //   A channels-last: float4 f = i * 256 + tid -> row f / 8, k 4 (f % 8)
+  //   A plane-major / B: row (or column) tid % 128, k groups 2 i + tid / 128
+  const int rr = tid & 127, kq = tid >> 7;
+  int a_frame = 0, a_pix = 0;
+  const bool a_row_ok = m0 + rr < M;
+  if (PLANE_A && a_row_ok) {
+    a_frame = (m0 + rr) / HW;
+    a_pix = (m0 + rr) % HW;
+  }
+  const bool b_col_ok = n0 + rr < N;
+  float4 pa[4], pb[4];
+  auto fetch = [&](int k0) {
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      if constexpr (!PLANE_A) {
+        const int f = i * NT + tid, r = f >> 3, k = k0 + (f & 7) * 4;
+        pa[i] = (m0 + r < M && k < K) ? ld4(A, size_t(m0 + r) * K + k) : make_float4(0.f, 0.f, 0.f, 0.f);
+      } else {
+        const int k = k0 + (2 * i + kq) * 4;
+        float v[4];
+#pragma unroll
+        for (int e = 0; e < 4; ++e)
+          v[e] = (a_row_ok && k + e < K) ? ld_el(A, (size_t(a_frame) * K + k + e) * HW + a_pix) : 0.0f;
+        pa[i] = make_float4(v[0], v[1], v[2], v[3]);
+      }
+      const int k = k0 + (2 * i + kq) * 4;
+      float w[4];
+#pragma unroll
+      for (int e = 0; e < 4; ++e) w[e] = (b_col_ok && k + e < K) ? Wt[size_t(k + e) * N + n0 + rr] : 0.0f;
+      pb[i] = make_float4(w[0], w[1], w[2], w[3]);
+    }
+  };
+  auto put3 = [&](__bf16* planes, int off, float4 v) {
+    const float x[4] = {v.x, v.y, v.z, v.w};
+    bf16x4 v1, v2, v3;
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      __bf16 x1, x2, x3;
+      split3_bf16(x[e], x1, x2, x3);
+      v1[e] = x1;
+      v2[e] = x2;
+      v3[e] = x3;
+    }
+    *reinterpret_cast<bf16x4*>(planes + off) = v1;
+    *reinterpret_cast<bf16x4*>(planes + AB + off) = v2;
+    *reinterpret_cast<bf16x4*>(planes + 2 * AB + off) = v3;
+  };
+  auto stash = [&]() {
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      if constexpr (!PLANE_A) {
+        const int f = i * NT + tid;
+        put3(Ap, (f >> 3) * KP + (f & 7) * 4, pa[i]);
+      } else {
+        put3(Ap, rr * KP + (2 * i + kq) * 4, pa[i]);
+      }
+      put3(Bp, rr * KP + (2 * i + kq) * 4, pb[i]);
+    }
+  };
+
+  floatx4 acc[MI][2];
+#pragma unroll
+  for (int i = 0; i < MI; ++i) acc[i][0] = acc[i][1] = floatx4{0.f, 0.f, 0.f, 0.f};
+  fetch(0);
+  for (int k0 = 0; k0 < K; k0 += KC) {
+    __syncthreads();   // the previous chunk's MFMAs are done with the planes
+    stash();
+    __syncthreads();
+    if (k0 + KC < K) fetch(k0 + KC);
+    // lane l: A rows l % 16 and B columns l % 16, k = 8 (l / 16) + 0..7
+    const int ko = (lane >> 4) * 8;
+    bf16x8 b1[2], b2[2], b3[2];
+#pragma unroll
+    for (int j = 0; j < 2; ++j) {
+      const int o = (wn * 32 + j * 16 + (lane & 15)) * KP + ko;
+      b1[j] = *reinterpret_cast<const bf16x8*>(Bp + o);
+      b2[j] = *reinterpret_cast<const bf16x8*>(Bp + AB + o);
+      b3[j] = *reinterpret_cast<const bf16x8*>(Bp + 2 * AB + o);
+    }
+#pragma unroll
+    for (int i = 0; i < MI; ++i) {
+      const int o = (i * 16 + (lane & 15)) * KP + ko;
+      const bf16x8 a1 = *reinterpret_cast<const bf16x8*>(Ap + o);
+      const bf16x8 a2 = *reinterpret_cast<const bf16x8*>(Ap + AB + o);
+      const bf16x8 a3 = *reinterpret_cast<const bf16x8*>(Ap + 2 * AB + o);
+#pragma unroll
+      for (int j = 0; j < 2; ++j) {
+        floatx4 c = acc[i][j];
+        c = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a3, b1[j], c, 0, 0, 0);   // small terms first
+        c = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a2, b2[j], c, 0, 0, 0);
+        c = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a1, b3[j], c, 0, 0, 0);
+        c = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a2, b1[j], c, 0, 0, 0);
+        c = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a1, b2[j], c, 0, 0, 0);
+        acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a1, b1[j], c, 0, 0, 0);
+      }
+    }
+  }
+
+  // epilogue: lane holds rows 16 i + 4 (lane / 16) + r of column lane % 16 of n-tile j
+  if constexpr (OUT_SPLIT) {
+#pragma unroll
+    for (int j = 0; j < 2; ++j) {
+      const int gn = n0 + wn * 32 + j * 16 + (lane & 15);
+      const bool nok = gn < N;
+      const float bv = nok ? bias[gn] : 0.0f;
+      const bool lo = gn < NH;
+      const int c = lo ? gn : gn - NH;
+      const int NC = lo ? NH : NL;
+      TO* dst = lo ? out_lo : out_hi;
+      const int act = lo ? act_lo : act_hi;
+      float csum = 0.0f;
+#pragma unroll
+      for (int i = 0; i < MI; ++i) {
+        const int gm0 = m0 + i * 16 + (lane >> 4) * 4;
+        float v[4];
+#pragma unroll
+        for (int r = 0; r < 4; ++r) v[r] = act_acc(acc[i][j][r] + bv, act);
+        if (nok && gm0 + 3 < M && (HW % 4) == 0) {
+          const int fr = gm0 / HW, p = gm0 % HW;
+          st4(dst, (size_t(fr) * NC + c) * HW + p, v);
+          csum += (v[0] + v[1]) + (v[2] + v[3]);
+        } else if (nok) {
+#pragma unroll
+          for (int r = 0; r < 4; ++r) {
+            const int gm = gm0 + r;
+            if (gm < M) {
+              const int fr = gm / HW, p = gm % HW;
+              st_el(dst, (size_t(fr) * NC + c) * HW + p, v[r]);
+              csum += v[r];
+            }
+          }
+        }
+      }
+      if (partial != nullptr && lo) {
+        csum += __shfl_xor(csum, 16, 64);
+        csum += __shfl_xor(csum, 32, 64);
+        if (lane < 16 && nok) partial[size_t(blockIdx.x) * NH + c] = csum;
+      }
+    }
+  } else {
+    // channels-last: stage 64 rows at a time in LDS, then whole-row stores of 4 columns per lane
+    float* st = reinterpret_cast<float*>(lds);
+#pragma unroll
+    for (int h = 0; h < 2; ++h) {
+      __syncthreads();
+#pragma unroll
+      for (int j = 0; j < 2; ++j) {
+        const int cl = wn * 32 + j * 16 + (lane & 15);
+        const float bv = n0 + cl < N ? bias[n0 + cl] : 0.0f;
+#pragma unroll
+        for (int i = 0; i < MI / 2; ++i)
+#pragma unroll
+          for (int r = 0; r < 4; ++r) st[(i * 16 + (lane >> 4) * 4 + r) * OP + cl] = acc[h * (MI / 2) + i][j][r] + bv;
+      }
+      __syncthreads();
+      for (int f = tid; f < 64 * (TN / 4); f += NT) {
+        const int r = f / (TN / 4), c4 = (f % (TN / 4)) * 4;
+        const int gm = m0 + h * 64 + r, gn = n0 + c4;
+        if (gm >= M) continue;
+        const float* src = &st[r * OP + c4];
+        if (gn + 3 < N && (N % 4) == 0) {
+          const float v[4] = {src[0], src[1], src[2], src[3]};
+          st4(out_lo, size_t(gm) * N + gn, v);
+        } else {
+          for (int e = 0; e < 4; ++e)
+            if (gn + e < N) st_el(out_lo, size_t(gm) * N + gn + e, src[e]);
+        }
+      }
+    }
+  }
+}
+
 // ----------------------------------------------------------------- launchers
 
 constexpr int kProjTM = 64;      // row tile of the general kernels
@@ -638,7 +772,20 @@ static int persistent_grid(int tiles) {
   return tiles < g ? tiles : g;
 }
 
-int proj_in_tile_rows(int K) { return K <= 128 ? kPersistTM : kProjTM; }
+// K <= kPersistMaxK: persistent kernel (weights in registers); larger K with K % 4 == 0
+// (or any K for plane-major A): K-chunked kernel; otherwise the fp32 tiled kernels
+constexpr int kPersistMaxK = 64;
+constexpr int kKcTM = 128;   // row tile of the K-chunked kernel
+
+int proj_in_tile_rows(int K) { return K % 4 == 0 ? kPersistTM : kProjTM; }
+
+template <bool PLANE_A, bool OUT_SPLIT, class TI, class TO>
+static void launch_kc(const void* A, int M, int K, int N, const float* W, const float* b, int HW, void* lo, void* hi,
+                      int act_lo, int act_hi, float* partial, int NH, hipStream_t s) {
+  const dim3 grid(unsigned((M + kKcTM - 1) / kKcTM), unsigned((N + 127) / 128));
+  hipLaunchKernelGGL((proj_kc_kernel<PLANE_A, OUT_SPLIT, TI, TO>), grid, dim3(256), 0, s, static_cast<const TI*>(A), M,
+                     K, N, W, b, HW, static_cast<TO*>(lo), static_cast<TO*>(hi), act_lo, act_hi, partial, NH);
+}
 
 template <class TI, class TO>
 static void launch_in(const void* X, int M, int K, int N, const float* W, const float* b, int HW, void* lo, void* hi,
@@ -686,7 +833,18 @@ hipError_t launch_proj_planes(const void* X, int in_dtype, int M, int K, int N, 
                               int HW, void* out_lo, void* out_hi, int out_dtype, int act_lo, int act_hi,
                               float* partial, int NH, hipStream_t s) {
   const NormGate ng{nullptr, nullptr, nullptr, 0};
-  if (K <= 128 && K % 4 == 0) {
+  if (K > kPersistMaxK && K % 4 == 0) {
+    if (in_dtype == 0 && out_dtype == 0)
+      launch_kc<false, true, float, float>(X, M, K, N, W, b, HW, out_lo, out_hi, act_lo, act_hi, partial, NH, s);
+    else if (in_dtype == 0)
+      launch_kc<false, true, float, uint16_t>(X, M, K, N, W, b, HW, out_lo, out_hi, act_lo, act_hi, partial, NH, s);
+    else if (out_dtype == 0)
+      launch_kc<false, true, uint16_t, float>(X, M, K, N, W, b, HW, out_lo, out_hi, act_lo, act_hi, partial, NH, s);
+    else
+      launch_kc<false, true, uint16_t, uint16_t>(X, M, K, N, W, b, HW, out_lo, out_hi, act_lo, act_hi, partial, NH, s);
+    return hipGetLastError();
+  }
+  if (K <= kPersistMaxK && K % 4 == 0) {
     if (in_dtype == 0 && out_dtype == 0)
       try_persist<false, true, false, float, float>(X, M, K, N, W, b, HW, out_lo, out_hi, act_lo, act_hi, partial, NH, ng, s);
     else if (in_dtype == 0)
@@ -711,24 +869,21 @@ hipError_t launch_proj_in(const void* X, int in_dtype, int M, int K, int N, cons
                             N / 2, s);
 }
 
-template <class TI, class TO>
-static void launch_out(const void* Y, int M, int K, int N, const float* W, const float* b, int HW, void* out,
-                       hipStream_t s) {
-  if (N <= 64) {
-    const dim3 grid((M + kProjTM - 1) / kProjTM, (N + 63) / 64);
-    hipLaunchKernelGGL((proj_out_kernel<kProjTM, 64, 2, 2, TI, TO>), grid, dim3(256), 0, s, static_cast<const TI*>(Y), M,
-                       K, N, W, b, HW, static_cast<TO*>(out));
-  } else {
-    const dim3 grid((M + kProjTM - 1) / kProjTM, (N + 127) / 128);
-    hipLaunchKernelGGL((proj_out_kernel<kProjTM, 128, 1, 4, TI, TO>), grid, dim3(256), 0, s, static_cast<const TI*>(Y),
-                       M, K, N, W, b, HW, static_cast<TO*>(out));
-  }
-}
-
 hipError_t launch_proj_out(const void* Y, int in_dtype, int M, int K, int N, const float* W, const float* b, int HW,
                            void* out, int out_dtype, hipStream_t s) {
   const NormGate ng{nullptr, nullptr, nullptr, 0};
-  if (K <= 128 && K % 4 == 0 && HW % 4 == 0) {
+  if (K > kPersistMaxK || K % 4 != 0 || HW % 4 != 0) {
+    if (in_dtype == 0 && out_dtype == 0)
+      launch_kc<true, false, float, float>(Y, M, K, N, W, b, HW, out, nullptr, 0, 0, nullptr, N, s);
+    else if (in_dtype == 0)
+      launch_kc<true, false, float, uint16_t>(Y, M, K, N, W, b, HW, out, nullptr, 0, 0, nullptr, N, s);
+    else if (out_dtype == 0)
+      launch_kc<true, false, uint16_t, float>(Y, M, K, N, W, b, HW, out, nullptr, 0, 0, nullptr, N, s);
+    else
+      launch_kc<true, false, uint16_t, uint16_t>(Y, M, K, N, W, b, HW, out, nullptr, 0, 0, nullptr, N, s);
+    return hipGetLastError();
+  }
+  {
     if (in_dtype == 0 && out_dtype == 0)
       try_persist<true, false, false, float, float>(Y, M, K, N, W, b, HW, out, nullptr, 0, 0, nullptr, N, ng, s);
     else if (in_dtype == 0)
@@ -739,11 +894,6 @@ hipError_t launch_proj_out(const void* Y, int in_dtype, int M, int K, int N, con
       try_persist<true, false, false, uint16_t, uint16_t>(Y, M, K, N, W, b, HW, out, nullptr, 0, 0, nullptr, N, ng, s);
     return hipGetLastError();
   }
-  if (in_dtype == 0 && out_dtype == 0) launch_out<float, float>(Y, M, K, N, W, b, HW, out, s);
-  else if (in_dtype == 0) launch_out<float, uint16_t>(Y, M, K, N, W, b, HW, out, s);
-  else if (out_dtype == 0) launch_out<uint16_t, float>(Y, M, K, N, W, b, HW, out, s);
-  else launch_out<uint16_t, uint16_t>(Y, M, K, N, W, b, HW, out, s);
-  return hipGetLastError();
 }
 
 // output projection with the per-pixel channel norm and the gate fused in front

@@ -25,8 +25,12 @@ def _dev(a, dtype=torch.float32):
     return torch.from_numpy(np.ascontiguousarray(a)).to("cuda", dtype)
 
 
+# K <= 64: persistent kernel; K > 64 with K % 4 == 0: K-chunked kernel (HW % 128 == 0 fuses ctx);
+# K % 4 != 0: fp32 tiled kernel.  N not a multiple of 128 / 4 and odd HW exercise the edges.
 @pytest.mark.parametrize("F,HW,K,N,silu", [(4, 1024, 64, 256, True), (3, 16384, 64, 128, False),
-                                           (5, 196, 40, 72, True), (2, 49, 130, 10, False)])
+                                           (5, 196, 40, 72, True), (2, 49, 130, 10, False),
+                                           (2, 1024, 128, 512, True), (3, 196, 224, 896, True),
+                                           (2, 16, 320, 1280, False), (1, 49, 448, 90, True)])
 def test_proj_in_plane_major_and_ctx(mods, F, HW, K, N, silu):
     _, S = mods
     print_case(test="proj_in", F=F, HW=HW, K=K, N=N)
@@ -43,7 +47,8 @@ def test_proj_in_plane_major_and_ctx(mods, F, HW, K, N, silu):
     assert rel_err(to_np(ctx), ref_lo.mean(axis=2)) < 1e-5
 
 
-@pytest.mark.parametrize("F,HW,K,N", [(4, 1024, 64, 64), (2, 16384, 128, 64), (3, 196, 96, 150)])
+@pytest.mark.parametrize("F,HW,K,N", [(4, 1024, 64, 64), (2, 16384, 128, 64), (3, 196, 96, 150),
+                                      (3, 49, 448, 224), (2, 16, 640, 320), (2, 196, 256, 128), (5, 49, 36, 30)])
 def test_proj_out_channels_last(mods, F, HW, K, N):
     _, S = mods
     print_case(test="proj_out", F=F, HW=HW, K=K, N=N)

@@ -72,11 +72,14 @@ def test_spectral_kernel_goom_floor(S):
 
 # ------------------------------------------------------------------ plane mean
 
+# plane sizes on both sides of the lanes-per-plane switch points (16, 32, 64 lanes, whole block);
+# 2 * 3 * 5 = 30 planes leave a partial last block for every size
+@pytest.mark.parametrize("hw", [(4, 4), (7, 7), (14, 14), (16, 16), (32, 32), (40, 40)])
 @pytest.mark.parametrize("silu", [False, True])
-def test_plane_mean(S, silu):
-    print_case(test="plane_mean", silu=silu)
+def test_plane_mean(S, silu, hw):
+    print_case(test="plane_mean", silu=silu, hw=hw)
     rng = np.random.default_rng(3)
-    x = rng.standard_normal((2, 3, 5, 32, 32))
+    x = rng.standard_normal((2, 3, 5) + hw)
     got = to_np(S.plane_mean(_dev(x), silu=silu))
     ref = (O.silu(x) if silu else x).mean(axis=(-2, -1))
     assert np.max(np.abs(got - ref)) < 1e-6
@@ -86,10 +89,12 @@ def test_plane_mean(S, silu):
 
 @pytest.mark.parametrize("gate_type", ["dense", "factored"])
 @pytest.mark.parametrize("act", ["softplus", "sigmoid", "exp"])
-def test_gated_gates_match_oracle(S, gate_type, act):
-    print_case(test="gated_gates", gate_type=gate_type, act=act)
+@pytest.mark.parametrize("shape", [(16, 16), (448, 7), (640, 4), (96, 14)])
+def test_gated_gates_match_oracle(S, gate_type, act, shape):
+    print_case(test="gated_gates", gate_type=gate_type, act=act, shape=shape)
     rng = np.random.default_rng(11)
-    B, T, C, H, W = 2, 3, 16, 16, 16
+    C, H = shape
+    B, T, W = 2, 3, H
     cfg = O.GatedConfig(channels=C, gate_type=gate_type, gate_activation=act, short_conv_size=0,
                         short_conv_spatial_size=0, kernel_size=3)
     p = O.init_params(O.gated_param_shapes(cfg, C, H, W), rng)
