@@ -558,14 +558,16 @@ proj_persist_kernel(const TI* __restrict__ A, int M, int K, int N, const float* 
 
 // ---------------------------------------------------------------------------
 // K-chunked projection for K beyond the persistent kernel's register-resident
-// weights (the CSSM-SHViT stages: K = 128 .. 640), on bf16 MFMA with both
-// operands split three ways and the same six products as the persistent
-// kernel (fp32-level results).  One 128 x 128 output tile per workgroup; K
-// advances in chunks of 32: the next chunk's A and B are loaded into registers
-// while the MFMAs run on the current one, then split into three bf16 planes in
-// LDS, A as [row][k] and B as [column][k] (k contiguous, the MFMA operand
-// order).  Four waves split the 128 columns (32 each) and keep all 128 rows,
-// as in the persistent kernel, so the proj_in channel sums stay in-wave.
+// weights (the CSSM-SHViT stages: K = 128 .. 640), on bf16 MFMA with the
+// operands split into bf16 parts (x = x1 + x2 + x3): fp32 A takes the same six
+// products as the persistent kernel; bf16 A is exactly its first part, so
+// three products (A1 B1 + A1 B2 + A1 B3) give the same fp32-level result.  One
+// 128 x 128 output tile per workgroup; K advances in chunks of 32: the next
+// chunk's A and B are loaded into registers while the MFMAs run on the current
+// one, then split into bf16 planes in LDS, A as [row][k] and B as [column][k]
+// (k contiguous, the MFMA operand order).  Four waves split the 128 columns
+// (32 each) and keep all 128 rows, as in the persistent kernel, so the proj_in
+// channel sums stay in-wave.
 //   PLANE_A = false: A is channels-last (M, K), K % 4 == 0; true: plane-major (F, K, HW).
 //   OUT_SPLIT = true: plane-major output(s) as proj_in; false: channels-last (M, N).
 // ---------------------------------------------------------------------------
@@ -575,74 +577,89 @@ proj_kc_kernel(const TI* __restrict__ A, int M, int K, int N, const float* __res
                const float* __restrict__ bias, int HW, TO* __restrict__ out_lo, TO* __restrict__ out_hi,
                int act_lo, int act_hi, float* __restrict__ partial, int NH) {
   constexpr int TM = 128, TN = 128, NT = 256, KC = 32, KP = KC + 8, MI = TM / 16;
-  constexpr int OP = TN + 4;   // channels-last staging pitch (floats), 64 rows at a time
-  constexpr int AB = TM * KP;  // bf16 per plane (TM == TN)
-  __shared__ __attribute__((aligned(16))) __bf16 lds[6 * AB];   // A1 A2 A3 B1 B2 B3
-  static_assert(64 * OP * 4 <= 6 * AB * 2, "staging of half an output tile fits the operand planes");
+  constexpr bool A1_ONLY = sizeof(TI) == 2;      // bf16 A: one nonzero part
+  constexpr int APL = A1_ONLY ? 1 : 3;           // A planes
+  constexpr int OP = TN + 4;                     // channels-last staging pitch (floats), 64 rows at a time
+  constexpr int AB = TM * KP;                    // bf16 per plane (TM == TN)
+  __shared__ __attribute__((aligned(16))) __bf16 lds[(APL + 3) * AB];   // A planes, then B1 B2 B3
+  static_assert(OUT_SPLIT || 64 * OP * 4 <= (APL + 3) * AB * 2, "staging of half an output tile fits the planes");
   __bf16* const Ap = lds;
-  __bf16* const Bp = lds + 3 * AB;
+  __bf16* const Bp = lds + APL * AB;
   const int tid = threadIdx.x, lane = tid & 63, wn = tid >> 6;
   const int m0 = blockIdx.x * TM, n0 = blockIdx.y * TN;
   const int NL = N - NH;
 
-  // this thread's loads per chunk: 4 groups of 4 consecutive k
-  //   A channels-last: float4 f = i * 256 + tid -> row f / 8, k 4 (f % 8)
-  //   A plane-major / B: row (or column) tid % 128, k groups 2 i + tid / 128
+  // this thread's loads per chunk: 4 groups i of 4 consecutive k
+  //   A channels-last: rows (tid / 8) + 32 i, k 4 (tid % 8)
+  //   A plane-major and B: row / column tid % 128, k groups 2 i + tid / 128
   const int rr = tid & 127, kq = tid >> 7;
-  int a_frame = 0, a_pix = 0;
-  const bool a_row_ok = m0 + rr < M;
-  if (PLANE_A && a_row_ok) {
-    a_frame = (m0 + rr) / HW;
-    a_pix = (m0 + rr) % HW;
+  const int ar = tid >> 3, ak = (tid & 7) * 4;
+  const TI* a_ptr;
+  bool a_ok[4];
+  if constexpr (!PLANE_A) {
+    a_ptr = A + size_t(m0 + ar) * K + ak;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) a_ok[i] = m0 + ar + 32 * i < M;
+  } else {
+    const int gm = m0 + rr < M ? m0 + rr : 0;
+    a_ptr = A + (size_t(gm / HW) * K + 4 * kq) * HW + gm % HW;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) a_ok[i] = m0 + rr < M;
   }
-  const bool b_col_ok = n0 + rr < N;
+  const bool b_ok = n0 + rr < N;
+  const float* b_ptr = Wt + size_t(4 * kq) * N + (b_ok ? n0 + rr : 0);
   float4 pa[4], pb[4];
   auto fetch = [&](int k0) {
+    const bool full = k0 + KC <= K;
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
       if constexpr (!PLANE_A) {
-        const int f = i * NT + tid, r = f >> 3, k = k0 + (f & 7) * 4;
-        pa[i] = (m0 + r < M && k < K) ? ld4(A, size_t(m0 + r) * K + k) : make_float4(0.f, 0.f, 0.f, 0.f);
+        const bool ok = a_ok[i] && (full || k0 + ak < K);
+        pa[i] = ok ? ld4(a_ptr + size_t(32 * i) * K, k0) : make_float4(0.f, 0.f, 0.f, 0.f);
       } else {
-        const int k = k0 + (2 * i + kq) * 4;
         float v[4];
 #pragma unroll
-        for (int e = 0; e < 4; ++e)
-          v[e] = (a_row_ok && k + e < K) ? ld_el(A, (size_t(a_frame) * K + k + e) * HW + a_pix) : 0.0f;
+        for (int e = 0; e < 4; ++e) {
+          const int k = k0 + 8 * i + e;   // relative to this thread's 4 kq
+          v[e] = (a_ok[i] && (full || k + 4 * kq < K)) ? ld_el(a_ptr, size_t(k) * HW) : 0.0f;
+        }
         pa[i] = make_float4(v[0], v[1], v[2], v[3]);
       }
-      const int k = k0 + (2 * i + kq) * 4;
       float w[4];
 #pragma unroll
-      for (int e = 0; e < 4; ++e) w[e] = (b_col_ok && k + e < K) ? Wt[size_t(k + e) * N + n0 + rr] : 0.0f;
+      for (int e = 0; e < 4; ++e) {
+        const int k = k0 + 8 * i + e;
+        w[e] = (b_ok && (full || k + 4 * kq < K)) ? b_ptr[size_t(k) * N] : 0.0f;
+      }
       pb[i] = make_float4(w[0], w[1], w[2], w[3]);
     }
   };
-  auto put3 = [&](__bf16* planes, int off, float4 v) {
+  auto put = [&](__bf16* planes, int np, int off, float4 v) {
     const float x[4] = {v.x, v.y, v.z, v.w};
     bf16x4 v1, v2, v3;
 #pragma unroll
     for (int e = 0; e < 4; ++e) {
       __bf16 x1, x2, x3;
-      split3_bf16(x[e], x1, x2, x3);
+      if (np == 1) {
+        x1 = (__bf16)x[e];   // exact for bf16 inputs
+      } else {
+        split3_bf16(x[e], x1, x2, x3);
+        v2[e] = x2;
+        v3[e] = x3;
+      }
       v1[e] = x1;
-      v2[e] = x2;
-      v3[e] = x3;
     }
     *reinterpret_cast<bf16x4*>(planes + off) = v1;
-    *reinterpret_cast<bf16x4*>(planes + AB + off) = v2;
-    *reinterpret_cast<bf16x4*>(planes + 2 * AB + off) = v3;
+    if (np == 3) {
+      *reinterpret_cast<bf16x4*>(planes + AB + off) = v2;
+      *reinterpret_cast<bf16x4*>(planes + 2 * AB + off) = v3;
+    }
   };
   auto stash = [&]() {
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
-      if constexpr (!PLANE_A) {
-        const int f = i * NT + tid;
-        put3(Ap, (f >> 3) * KP + (f & 7) * 4, pa[i]);
-      } else {
-        put3(Ap, rr * KP + (2 * i + kq) * 4, pa[i]);
-      }
-      put3(Bp, rr * KP + (2 * i + kq) * 4, pb[i]);
+      put(Ap, APL, PLANE_A ? rr * KP + (2 * i + kq) * 4 : (ar + 32 * i) * KP + ak, pa[i]);
+      put(Bp, 3, rr * KP + (2 * i + kq) * 4, pb[i]);
     }
   };
 
@@ -669,23 +686,36 @@ proj_kc_kernel(const TI* __restrict__ A, int M, int K, int N, const float* __res
     for (int i = 0; i < MI; ++i) {
       const int o = (i * 16 + (lane & 15)) * KP + ko;
       const bf16x8 a1 = *reinterpret_cast<const bf16x8*>(Ap + o);
-      const bf16x8 a2 = *reinterpret_cast<const bf16x8*>(Ap + AB + o);
-      const bf16x8 a3 = *reinterpret_cast<const bf16x8*>(Ap + 2 * AB + o);
+      if constexpr (A1_ONLY) {
 #pragma unroll
-      for (int j = 0; j < 2; ++j) {
-        floatx4 c = acc[i][j];
-        c = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a3, b1[j], c, 0, 0, 0);   // small terms first
-        c = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a2, b2[j], c, 0, 0, 0);
-        c = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a1, b3[j], c, 0, 0, 0);
-        c = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a2, b1[j], c, 0, 0, 0);
-        c = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a1, b2[j], c, 0, 0, 0);
-        acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a1, b1[j], c, 0, 0, 0);
+        for (int j = 0; j < 2; ++j) {
+          floatx4 c = acc[i][j];
+          c = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a1, b3[j], c, 0, 0, 0);   // small terms first
+          c = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a1, b2[j], c, 0, 0, 0);
+          acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a1, b1[j], c, 0, 0, 0);
+        }
+      } else {
+        const bf16x8 a2 = *reinterpret_cast<const bf16x8*>(Ap + AB + o);
+        const bf16x8 a3 = *reinterpret_cast<const bf16x8*>(Ap + 2 * AB + o);
+#pragma unroll
+        for (int j = 0; j < 2; ++j) {
+          floatx4 c = acc[i][j];
+          c = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a3, b1[j], c, 0, 0, 0);   // small terms first
+          c = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a2, b2[j], c, 0, 0, 0);
+          c = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a1, b3[j], c, 0, 0, 0);
+          c = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a2, b1[j], c, 0, 0, 0);
+          c = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a1, b2[j], c, 0, 0, 0);
+          acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a1, b1[j], c, 0, 0, 0);
+        }
       }
     }
   }
 
   // epilogue: lane holds rows 16 i + 4 (lane / 16) + r of column lane % 16 of n-tile j
   if constexpr (OUT_SPLIT) {
+    // frame / pixel of this lane's first row, advanced by 16 rows per i
+    const int gmb = m0 + (lane >> 4) * 4;
+    const int fr0 = gmb / HW, p0 = gmb % HW;
 #pragma unroll
     for (int j = 0; j < 2; ++j) {
       const int gn = n0 + wn * 32 + j * 16 + (lane & 15);
@@ -697,26 +727,38 @@ proj_kc_kernel(const TI* __restrict__ A, int M, int K, int N, const float* __res
       TO* dst = lo ? out_lo : out_hi;
       const int act = lo ? act_lo : act_hi;
       float csum = 0.0f;
+      int fr = fr0, p = p0;
 #pragma unroll
       for (int i = 0; i < MI; ++i) {
-        const int gm0 = m0 + i * 16 + (lane >> 4) * 4;
+        const int gm0 = gmb + i * 16;
         float v[4];
 #pragma unroll
-        for (int r = 0; r < 4; ++r) v[r] = act_acc(acc[i][j][r] + bv, act);
+        for (int r = 0; r < 4; ++r) {
+          v[r] = acc[i][j][r] + bv;
+          if (act == 1) v[r] = v[r] * __builtin_amdgcn_rcpf(1.0f + __expf(-v[r]));
+          else if (act == 2) v[r] = __builtin_amdgcn_rcpf(1.0f + __expf(-v[r]));
+        }
         if (nok && gm0 + 3 < M && (HW % 4) == 0) {
-          const int fr = gm0 / HW, p = gm0 % HW;
-          st4(dst, (size_t(fr) * NC + c) * HW + p, v);
+          st4(dst, size_t(fr * NC + c) * HW + p, v);
           csum += (v[0] + v[1]) + (v[2] + v[3]);
         } else if (nok) {
+          int f2 = fr, p2 = p;
 #pragma unroll
           for (int r = 0; r < 4; ++r) {
-            const int gm = gm0 + r;
-            if (gm < M) {
-              const int fr = gm / HW, p = gm % HW;
-              st_el(dst, (size_t(fr) * NC + c) * HW + p, v[r]);
+            if (gm0 + r < M) {
+              st_el(dst, size_t(f2 * NC + c) * HW + p2, v[r]);
               csum += v[r];
             }
+            if (++p2 == HW) {
+              p2 = 0;
+              ++f2;
+            }
           }
+        }
+        p += 16;
+        while (p >= HW) {
+          p -= HW;
+          ++fr;
         }
       }
       if (partial != nullptr && lo) {
