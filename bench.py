@@ -213,11 +213,9 @@ def gdn_step(cell, variables, x, w, S, mark):
         mark("qkv_dw")
     else:
         xq = x
-    qkv = S.proj_planes(xq, p["qkv_proj"]["kernel"], p["qkv_proj"]["bias"], F, HW, out_dtype=f32)
-    qkv = qkv.view(B, T, 3 * C, H, W)
-    mark("qkv_proj")
-    S.gdn_qkv_post(qkv, [p["short_conv_q"], p["short_conv_k"], p["short_conv_v"]], 1, bkv)
-    mark("qkv_post")
+    qkv = S.gdn_qkv_proj(xq, p["qkv_proj"]["kernel"], p["qkv_proj"]["bias"], B, T, H, W,
+                         [p["short_conv_q"], p["short_conv_k"], p["short_conv_v"]], 1, bkv, out_dtype=f32)
+    mark("qkv_proj")   # with the short conv, SiLU and input gates (one kernel when T in {1, 2, 4, 8})
     gv = S.proj_planes(x, p["gate_proj"]["kernel"], p["gate_proj"]["bias"], F, HW, act="silu", out_dtype=f32)
     mark("gate_proj")
     spec, norms = S.rfft2(qkv, want_norms=True)

@@ -85,6 +85,8 @@ SIGNATURES = {
     "cssm_gdn_gates": (_I, [_P, _I, _I, _I, _I, _I, _I, ctypes.POINTER(GdnGateParams), _I, ctypes.c_float, _P,
                             _P, _P, _P]),
     "cssm_gdn_qkv_post": (_I, [_P, _I, _I, _I, _I, _I, _I, _I, _P, _P, _I, _P, _P]),
+    "cssm_gdn_qkv_proj": (_I, [_P, _I, _I, _I, _I, _I, _I, _I, _P, _P, _I, _P, _P, _I, _P, _P, _I, _P]),
+    "cssm_gdn_qkv_fused": (_I, [_I, _I, _I, _I]),
     "cssm_rfft2": (_I, [_P, _I, _LL, _I, _I, _P, _P, _P]),
     "cssm_irfft2": (_I, [_P, _LL, _I, _I, _P, _I, _P]),
     "cssm_fft_min_group": (_I, [_I, _I]),

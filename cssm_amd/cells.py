@@ -383,9 +383,6 @@ class GatedDeltaNetCSSM:
         # q, k, v in plane-major blocks (B, T, 3C, H, W)
         xq = (S.depthwise_conv(x, p["qkv_dw"]["kernel"], p["qkv_dw"]["bias"], out_dtype=f32)
               if self.qkv_conv_size > 1 else x)
-        qkv = S.proj_planes(xq, p["qkv_proj"]["kernel"], p["qkv_proj"]["bias"], F, HW,
-                            out_dtype=f32).view(B, T, 3 * C, H, W)
-        del xq
         gate_mode, gates = 0, None
         if self.use_input_gates:
             if self.gate_type == "channel":
@@ -396,8 +393,10 @@ class GatedDeltaNetCSSM:
         convs = None
         if self.short_conv_size > 0:
             convs = [p["short_conv_q"], p["short_conv_k"], p["short_conv_v"]]
-        S.gdn_qkv_post(qkv, convs, gate_mode, gates)
-        del gates
+        # qkv_proj with the short conv, SiLU and input gates in its epilogue
+        qkv = S.gdn_qkv_proj(xq, p["qkv_proj"]["kernel"], p["qkv_proj"]["bias"], B, T, H, W, convs, gate_mode, gates,
+                             out_dtype=f32)
+        del xq, gates
         gv = S.proj_planes(x, p["gate_proj"]["kernel"], p["gate_proj"]["bias"], F, HW,
                            act="silu" if self.output_gate_act == "silu" else "sigmoid", out_dtype=f32)
         # spectral core: rfft2 -> delta-rule recurrence -> irfft2

@@ -316,6 +316,37 @@ int cssm_gdn_qkv_post(void* qkv, int dtype, int B, int T, int C, int H, int W, i
                     "cssm_gdn_qkv_post");
 }
 
+int cssm_gdn_qkv_proj(const void* x, int in_dtype, int B, int T, int H, int W, int K, int C, const float* kernel,
+                      const float* bias, int kt, const float* const* conv_kernel, const float* const* conv_bias,
+                      int gate_mode, const void* gates, void* qkv, int out_dtype, void* stream) {
+  if (!x || !kernel || !bias || !qkv) return fail(CSSM_ERR_NULL, "cssm_gdn_qkv_proj: x, kernel, bias and qkv must be non-null");
+  if (B <= 0 || T <= 0 || H <= 0 || W <= 0 || K <= 0 || C <= 0 || kt < 0 || kt > 8)
+    return fail(CSSM_ERR_SHAPE, "cssm_gdn_qkv_proj: B=%d T=%d H=%d W=%d K=%d C=%d kt=%d (kt <= 8)", B, T, H, W, K, C, kt);
+  if ((long long)B * T * H * W > 0x7fffffffLL) return fail(CSSM_ERR_SHAPE, "cssm_gdn_qkv_proj: B*T*H*W exceeds 2^31");
+  if (!dtype_ok(in_dtype) || !dtype_ok(out_dtype))
+    return fail(CSSM_ERR_ARG, "cssm_gdn_qkv_proj: dtypes %d/%d", in_dtype, out_dtype);
+  if (gate_mode < 0 || gate_mode > 3) return fail(CSSM_ERR_ARG, "cssm_gdn_qkv_proj: gate_mode=%d", gate_mode);
+  if (gate_mode != 0 && !gates) return fail(CSSM_ERR_NULL, "cssm_gdn_qkv_proj: gates must be non-null");
+  cssm::GdnShortConv sc{};
+  if (kt > 0) {
+    if (!conv_kernel || !conv_bias) return fail(CSSM_ERR_NULL, "cssm_gdn_qkv_proj: short-conv weights missing");
+    for (int i = 0; i < 3; ++i) {
+      if (!conv_kernel[i] || !conv_bias[i]) return fail(CSSM_ERR_NULL, "cssm_gdn_qkv_proj: short-conv %d missing", i);
+      sc.w[i] = conv_kernel[i];
+      sc.b[i] = conv_bias[i];
+    }
+  }
+  if ((H * W) % 4) return fail(CSSM_ERR_UNSUPPORTED, "cssm_gdn_qkv_proj: H*W=%d must be a multiple of 4", H * W);
+  if (!aligned(qkv, out_dtype == CSSM_F32 ? 16 : 8) || (gate_mode == 1 && !aligned(gates, 8)) ||
+      (gate_mode == 3 && !aligned(gates, 16)))
+    return fail(CSSM_ERR_ALIGN, "cssm_gdn_qkv_proj: misaligned qkv / gates");
+  return hip_status(cssm::launch_gdn_qkv_proj(x, in_dtype, B, T, H * W, K, C, kernel, bias, kt, sc, gate_mode, gates,
+                                              qkv, out_dtype, static_cast<hipStream_t>(stream)),
+                    "cssm_gdn_qkv_proj");
+}
+
+int cssm_gdn_qkv_fused(int T, int H, int W, int K) { return cssm::gdn_qkv_fused_supported(T, H * W, K) ? 1 : 0; }
+
 int cssm_fft_min_group(int H, int W) { return cssm::fft_planes_min_group(H, W); }
 
 int cssm_rfft2(const void* x, int dtype, long long P, int H, int W, float* spec, float* norms, void* stream) {

@@ -791,7 +791,7 @@ gdn_qkv_post(T* __restrict__ qkv, int Tn, int C, int HW, GdnShortConv sc, int ga
       for (int j = 0; j + 1 < KT - 1; ++j) hist[j] = hist[j + 1];
       if (KT > 1) hist[KT > 1 ? KT - 2 : 0] = v;
 #pragma unroll
-      for (int e = 0; e < 4; ++e) o[e] = o[e] / (1.0f + expf(-o[e]));
+      for (int e = 0; e < 4; ++e) o[e] = o[e] * __builtin_amdgcn_rcpf(1.0f + __expf(-o[e]));
       v = make_float4(o[0], o[1], o[2], o[3]);
     }
     if (blk > 0 && gate_mode != 0) {

@@ -218,11 +218,25 @@ struct NormGate {
   int kind;             // 0 none, 1 rms, 2 layer
 };
 
-template <int KMAX, bool PLANE_A, bool OUT_SPLIT, int WN, class TI, class TO, bool NORM = false, bool SPLIT = false>
+// GDN qkv epilogue (TT > 0): the causal short convolution over T, SiLU and the
+// input gates of cssm.py:4763-4780 / :4844-4848, in the operation order of
+// gdn_qkv_post, on a tile of 128 / TT pixels x all TT frames of one batch
+// element (tile row r = t * (128 / TT) + pixel), so each lane holds the frames
+// of its pixels.  Output (B, TT, N = 3C, HW) plane-major.
+struct QkvPost {
+  const float* w[3];     // (kt, C) per q / k / v block
+  const float* b[3];     // (C)
+  int kt;                // 0: no convolution and no SiLU
+  int gate_mode;         // as cssm_gdn_qkv_post (0 none, 1 per pixel, 2 per frame, 3 per channel and pixel)
+  const void* gates;
+};
+
+template <int KMAX, bool PLANE_A, bool OUT_SPLIT, int WN, class TI, class TO, bool NORM = false, bool SPLIT = false,
+          int TT = 0>
 __global__ void __launch_bounds__(256, 2)
 proj_persist_kernel(const TI* __restrict__ A, int M, int K, int N, const float* __restrict__ Wt,
                     const float* __restrict__ bias, int HW, TO* __restrict__ out_lo, TO* __restrict__ out_hi,
-                    int act_lo, int act_hi, float* __restrict__ partial, int NH, NormGate ng) {
+                    int act_lo, int act_hi, float* __restrict__ partial, int NH, NormGate ng, QkvPost qp) {
   // WN waves along the TN = 32 WN columns, WM = 4 / WN along the TM = 128 rows;
   // a wave owns (128 / WM) rows x 32 columns = MI x 2 MFMA tiles
   constexpr int TM = 128, TN = 32 * WN, NT = 256, WM = 4 / WN, MI = TM / WM / 16;
@@ -245,12 +259,24 @@ proj_persist_kernel(const TI* __restrict__ A, int M, int K, int N, const float* 
   __bf16* const A2 = A1 + TM * KP;
   __bf16* const A3 = A2 + TM * KP;
   __shared__ float rowsc[NORM ? 2 * TM : 1];             // per-pixel (scale, mean) of the norm
+  __shared__ float2 gsh[TT > 0 ? TM : 1];                 // qkv epilogue: the tile's input gates
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int wm = wave / WN, wn = wave % WN;
   const int n0 = blockIdx.y * TN;
   const int NL = N - NH;
   const int tiles = (M + TM - 1) / TM;
   const TI* __restrict__ Gp = static_cast<const TI*>(ng.G);
+  static_assert(TT == 0 || (SPLIT && !PLANE_A && OUT_SPLIT && TM % (16 * TT) == 0), "qkv epilogue: frames x pixels tiles");
+  constexpr int TP = TT > 0 ? TM / TT : TM;   // pixels per tile (TT > 0)
+  // global row of row r of tile `tile`
+  auto grow = [&](int tile, int r) -> int {
+    if constexpr (TT == 0) {
+      return tile * TM + r;
+    } else {
+      const int tpf = HW / TP, bb = tile / tpf, pb = tile % tpf;
+      return (bb * TT + r / TP) * HW + pb * TP + r % TP;
+    }
+  };
 
   // SPLIT: lane l's B fragments, column wn 32 + 16 j + l % 16, k = 32 kb + 8 (l / 16) + e
   bf16x8 b1[SPLIT ? 2 : 1][SPLIT ? KB : 1], b2[SPLIT ? 2 : 1][SPLIT ? KB : 1], b3[SPLIT ? 2 : 1][SPLIT ? KB : 1];
@@ -295,8 +321,8 @@ proj_persist_kernel(const TI* __restrict__ A, int M, int K, int N, const float* 
         }
       } else if (!PLANE_A) {
         const int r = f / (KMAX / 4), k4 = (f % (KMAX / 4)) * 4;
-        const int gm = m0 + r;
-        if (gm < M && k4 < K) v = ld4(src, size_t(gm) * K + k4);
+        const int gm = TT > 0 ? grow(tile, r) : m0 + r;
+        if ((TT > 0 || gm < M) && k4 < K) v = ld4(src, size_t(gm) * K + k4);
       } else {
         const int kk = f / (TM / 4), r4 = (f % (TM / 4)) * 4;
         const int gm = m0 + r4;
@@ -413,12 +439,20 @@ proj_persist_kernel(const TI* __restrict__ A, int M, int K, int N, const float* 
 
   float4 pf[PF];
   float4 pg[NORM ? PF : 1];
-  int tile = blockIdx.x;
+  // k-th tile of this workgroup.  The qkv epilogue (TT > 0) writes half cache
+  // lines (16 pixels of a plane) per tile; the workgroup takes tiles in
+  // adjacent pairs so both halves of each line pass through the same L2.
+  auto tile_of = [&](int k) -> int {
+    if constexpr (TT > 0) return 2 * (int(blockIdx.x) + (k >> 1) * int(gridDim.x)) + (k & 1);
+    else return int(blockIdx.x) + k * int(gridDim.x);
+  };
+  int kt_ = 0;
+  int tile = tile_of(0);
   if (tile < tiles) {
     fetch(A, tile, pf);
     if (NORM) fetch(Gp, tile, pg);
   }
-  for (; tile < tiles; tile += gridDim.x) {
+  for (; tile < tiles; tile = tile_of(++kt_)) {
     __syncthreads();            // previous tile is done with As (and Bs is staged)
     stash(pf);
     __syncthreads();
@@ -426,7 +460,7 @@ proj_persist_kernel(const TI* __restrict__ A, int M, int K, int N, const float* 
       norm_gate(pg);
       __syncthreads();
     }
-    const int next = tile + gridDim.x;
+    const int next = tile_of(kt_ + 1);
     if (next < tiles) {
       fetch(A, next, pf);
       if (NORM) fetch(Gp, next, pg);
@@ -479,7 +513,69 @@ proj_persist_kernel(const TI* __restrict__ A, int M, int K, int N, const float* 
 
     // epilogue: lane holds rows 16 i + 4 (lane / 16) + r of column lane % 16 of n-tile j
     const int m0 = tile * TM;
-    if (OUT_SPLIT) {
+    if constexpr (TT > 0) {
+      // GDN qkv: lane rows 16 i + 4 (lane / 16) + r are pixel pb TP + (16 i) % TP + 4 (lane / 16) + r of
+      // frame t = 16 i / TP; frame t - d of the same pixels is row tile i - d IPF of the same lane
+      constexpr int IPF = TP / 16;
+      const int tpf = HW / TP, bb = tile / tpf, pb = tile % tpf;
+      const int C = N / 3;
+      // per-pixel / per-frame input gates of the tile (TT frames x TP pixels x (B_k, B_v)) through LDS
+      if (qp.gate_mode == 1 || qp.gate_mode == 2) {
+        for (int e = tid; e < TT * TP; e += NT) {
+          const int t = e / TP, p = e % TP;
+          const size_t fr = size_t(bb) * TT + t;
+          gsh[e] = qp.gate_mode == 1 ? static_cast<const float2*>(qp.gates)[fr * HW + pb * TP + p]
+                                     : static_cast<const float2*>(qp.gates)[fr];
+        }
+        __syncthreads();
+      }
+#pragma unroll
+      for (int j = 0; j < 2; ++j) {
+        const int gn = n0 + wn * 32 + j * 16 + (lane & 15);
+        if (gn >= N) continue;
+        const float bv = bias[gn];
+        const int blk = gn / C, c = gn % C;
+        // wd[d]: tap on frame t - d (d < kt); wd[0] = kernel[kt - 1]
+        float wd[8];
+#pragma unroll
+        for (int d = 0; d < 8; ++d) wd[d] = d < qp.kt ? qp.w[blk][(qp.kt - 1 - d) * C + c] : 0.0f;
+        const float bt = qp.kt > 0 ? qp.b[blk][c] : 0.0f;
+#pragma unroll
+        for (int i = 0; i < MI; ++i) {
+          const int t = i / IPF;
+          const int px = pb * TP + (i % IPF) * 16 + (lane >> 4) * 4;
+          const size_t fr = size_t(bb) * TT + t;
+          float v[4];
+#pragma unroll
+          for (int r = 0; r < 4; ++r) {
+            float x = acc[i][j][r] + bv;
+            if (qp.kt > 0) {
+              float o = fmaf(wd[0], x, bt);
+#pragma unroll
+              for (int d = 7; d >= 1; --d)
+                if (d < qp.kt && i >= d * IPF) o = fmaf(wd[d], acc[i - d * IPF][j][r] + bv, o);
+              x = o * __builtin_amdgcn_rcpf(1.0f + __expf(-o));   // SiLU as gdn_qkv_post computes it
+            }
+            v[r] = x;
+          }
+          if (blk > 0 && qp.gate_mode != 0) {
+            float g[4];
+            if (qp.gate_mode != 3) {
+              const float2* gp = gsh + t * TP + (i % IPF) * 16 + (lane >> 4) * 4;
+#pragma unroll
+              for (int r = 0; r < 4; ++r) g[r] = blk == 1 ? gp[r].x : gp[r].y;
+            } else {
+              const float4 gg = *reinterpret_cast<const float4*>(static_cast<const float*>(qp.gates) +
+                                                                 (fr * 2 * C + size_t(blk - 1) * C + c) * HW + px);
+              g[0] = gg.x; g[1] = gg.y; g[2] = gg.z; g[3] = gg.w;
+            }
+#pragma unroll
+            for (int r = 0; r < 4; ++r) v[r] *= g[r];
+          }
+          st4(out_lo, (fr * N + gn) * HW + px, v);
+        }
+      }
+    } else if (OUT_SPLIT) {
       // 4 consecutive pixels of one channel per lane and MFMA tile: 16 B stores
 #pragma unroll
       for (int j = 0; j < 2; ++j) {
@@ -849,14 +945,14 @@ static void launch_persist(const void* A, int M, int K, int N, const float* W, c
       const dim3 grid(unsigned(persistent_grid(tiles)), unsigned((N + 63) / 64));
       hipLaunchKernelGGL((proj_persist_kernel<KMAX, PLANE_A, OUT_SPLIT, 2, TI, TO, NORM, SPLIT>), grid, dim3(256), 0, s,
                          static_cast<const TI*>(A), M, K, N, W, b, HW, static_cast<TO*>(lo), static_cast<TO*>(hi),
-                         act_lo, act_hi, partial, NH, ng);
+                         act_lo, act_hi, partial, NH, ng, QkvPost{});
       return;
     }
   }
   const dim3 grid(unsigned(persistent_grid(tiles)), unsigned((N + 127) / 128));
   hipLaunchKernelGGL((proj_persist_kernel<KMAX, PLANE_A, OUT_SPLIT, 4, TI, TO, NORM, SPLIT>), grid, dim3(256), 0, s,
                      static_cast<const TI*>(A), M, K, N, W, b, HW, static_cast<TO*>(lo), static_cast<TO*>(hi),
-                     act_lo, act_hi, partial, NH, ng);
+                     act_lo, act_hi, partial, NH, ng, QkvPost{});
 }
 
 template <bool PLANE_A, bool OUT_SPLIT, bool NORM, class TI, class TO>
@@ -909,6 +1005,54 @@ hipError_t launch_proj_in(const void* X, int in_dtype, int M, int K, int N, cons
                           hipStream_t s) {
   return launch_proj_planes(X, in_dtype, M, K, N, W, b, HW, out_lo, out_hi, out_dtype, act_lo, act_hi, partial,
                             N / 2, s);
+}
+
+// GDN qkv projection with the short convolution, SiLU and input gates fused
+// into the epilogue (persistent kernel, tiles of 128 / T pixels x T frames);
+// returns false when the shape has no fused variant (the caller then runs
+// launch_proj_planes + launch_gdn_qkv_post, which compute the same values)
+template <int TT, class TI, class TO>
+static void launch_qkv_fused(const void* X, int M, int K, int N, const float* W, const float* b, int HW, void* out,
+                             const QkvPost& qp, hipStream_t s) {
+  const int tiles = M / kPersistTM;
+  const NormGate ng{nullptr, nullptr, nullptr, 0};
+  const dim3 grid(unsigned(persistent_grid((tiles + 1) / 2)), unsigned((N + 127) / 128));   // tiles in pairs
+  hipLaunchKernelGGL((proj_persist_kernel<64, false, true, 4, TI, TO, false, true, TT>), grid, dim3(256), 0, s,
+                     static_cast<const TI*>(X), M, K, N, W, b, HW, static_cast<TO*>(out), static_cast<TO*>(out), 0, 0,
+                     nullptr, N, ng, qp);
+}
+
+template <class TI, class TO>
+static bool qkv_fused_t(const void* X, int T, int M, int K, int N, const float* W, const float* b, int HW, void* out,
+                        const QkvPost& qp, hipStream_t s) {
+  switch (T) {
+    case 1: launch_qkv_fused<1, TI, TO>(X, M, K, N, W, b, HW, out, qp, s); return true;
+    case 2: launch_qkv_fused<2, TI, TO>(X, M, K, N, W, b, HW, out, qp, s); return true;
+    case 4: launch_qkv_fused<4, TI, TO>(X, M, K, N, W, b, HW, out, qp, s); return true;
+    case 8: launch_qkv_fused<8, TI, TO>(X, M, K, N, W, b, HW, out, qp, s); return true;
+    default: return false;
+  }
+}
+
+bool gdn_qkv_fused_supported(int T, int HW, int K) {
+  return (T == 1 || T == 2 || T == 4 || T == 8) && K <= kPersistMaxK && K % 4 == 0 && HW % (kPersistTM / T) == 0;
+}
+
+hipError_t launch_gdn_qkv_proj(const void* X, int in_dtype, int B, int T, int HW, int K, int C, const float* W,
+                               const float* b, int kt, const GdnShortConv& sc, int gate_mode, const void* gates,
+                               void* out, int out_dtype, hipStream_t s) {
+  const int M = B * T * HW, N = 3 * C;
+  if (gdn_qkv_fused_supported(T, HW, K) && kt <= 8) {
+    QkvPost qp{{sc.w[0], sc.w[1], sc.w[2]}, {sc.b[0], sc.b[1], sc.b[2]}, kt, gate_mode, gates};
+    if (in_dtype == 0 && out_dtype == 0) qkv_fused_t<float, float>(X, T, M, K, N, W, b, HW, out, qp, s);
+    else if (in_dtype == 0) qkv_fused_t<float, uint16_t>(X, T, M, K, N, W, b, HW, out, qp, s);
+    else if (out_dtype == 0) qkv_fused_t<uint16_t, float>(X, T, M, K, N, W, b, HW, out, qp, s);
+    else qkv_fused_t<uint16_t, uint16_t>(X, T, M, K, N, W, b, HW, out, qp, s);
+    return hipGetLastError();
+  }
+  hipError_t e = launch_proj_planes(X, in_dtype, M, K, N, W, b, HW, out, nullptr, out_dtype, 0, 0, nullptr, N, s);
+  if (e != hipSuccess) return e;
+  return launch_gdn_qkv_post(out, out_dtype, B, T, C, HW, kt, sc, gate_mode, gates, s);
 }
 
 hipError_t launch_proj_out(const void* Y, int in_dtype, int M, int K, int N, const float* W, const float* b, int HW,

@@ -337,6 +337,47 @@ def gdn_qkv_post(qkv: torch.Tensor, convs, gate_mode: int = 0, gates: Optional[t
     return qkv
 
 
+def gdn_qkv_proj(x: torch.Tensor, kernel: torch.Tensor, bias: torch.Tensor, B: int, T: int, H: int, W: int,
+                 convs, gate_mode: int = 0, gates: Optional[torch.Tensor] = None,
+                 out_dtype: Optional[torch.dtype] = None) -> torch.Tensor:
+    """qkv_proj of channels-last x (B, T, H, W, K) with the causal short conv + SiLU (convs = [q, k, v]
+    dicts or None) and the input gates on k, v fused in (cssm.py:4753-4848) -> (B, T, 3C, H, W)."""
+    _dev(x, "x")
+    if x.dtype not in _DTYPES:
+        raise ValueError(f"unsupported dtype {x.dtype}")
+    K = x.shape[-1]
+    if x.numel() != B * T * H * W * K:
+        raise ValueError("x does not hold B * T * H * W rows")
+    _dev(kernel, "kernel", torch.float32)
+    _dev(bias, "bias", torch.float32)
+    Kk, N = kernel.shape
+    if Kk != K or bias.shape != (N,) or N % 3:
+        raise ValueError(f"kernel {tuple(kernel.shape)} / bias {tuple(bias.shape)} do not match K={K}, N=3C")
+    C = N // 3
+    kt = 0
+    kern = cb = None
+    if convs is not None:
+        kt = convs[0]["kernel"].shape[0]
+        ks = [_dev(c["kernel"], "short_conv.kernel", torch.float32) for c in convs]
+        bs = [_dev(c["bias"], "short_conv.bias", torch.float32) for c in convs]
+        kern = (ctypes.c_void_p * 3)(*[k.data_ptr() for k in ks])
+        cb = (ctypes.c_void_p * 3)(*[b.data_ptr() for b in bs])
+    gp = None
+    if gate_mode:
+        _dev(gates, "gates", torch.float32)
+        gp = gates.data_ptr()
+    od = out_dtype or x.dtype
+    out = torch.empty((B, T, N, H, W), dtype=od, device=x.device)
+    _lib.call("cssm_gdn_qkv_proj", x.data_ptr(), _DTYPES[x.dtype], B, T, H, W, K, C, kernel.data_ptr(),
+              bias.data_ptr(), kt, kern, cb, gate_mode, gp, out.data_ptr(), _DTYPES[od], _stream())
+    return out
+
+
+def gdn_qkv_fused(T: int, H: int, W: int, K: int) -> bool:
+    """True when gdn_qkv_proj runs as one fused kernel for this shape."""
+    return bool(_lib.load().cssm_gdn_qkv_fused(T, H, W, K))
+
+
 def rfft2(x: torch.Tensor, want_norms: bool = False):
     """Batched rfft2 of (..., H, W) real planes -> (spec (..., H, W//2+1) complex64, norms (...) or None)."""
     _dev(x, "x")

@@ -276,6 +276,29 @@ int cssm_gdn_qkv_post(void* qkv, int dtype, int B, int T, int C, int H, int W, i
                       const void* gates, void* stream);
 
 /*
+ * qkv projection of GatedDeltaNetCSSM with the causal short convolution, SiLU
+ * and input gates of cssm_gdn_qkv_post fused into the GEMM's epilogue:
+ *   qkv = post(proj(x)),  proj = cssm_proj_planes with N = 3C (identity act).
+ * Replaces cssm.py:4753-4758 (qkv_proj), :4763-4780 and :4844-4848 in one pass
+ * over qkv instead of three.  Fused when cssm_gdn_qkv_fused(T, H, W, K) (tiles
+ * of 128 / T pixels x all T frames: T in {1, 2, 4, 8}, K <= 64, H*W a multiple
+ * of 128 / T); otherwise it runs the two calls it replaces, with the same
+ * results (fp32 qkv; a bf16 qkv then holds the projection in bf16 before the
+ * convolution, where the fused path keeps it in fp32).
+ *   x      (B, T, H*W, K) channels-last of in_dtype
+ *   kernel (K, 3C) [qkv_proj/kernel], bias (3C) [qkv_proj/bias]
+ *   kt, conv_kernel, conv_bias, gate_mode, gates: as cssm_gdn_qkv_post
+ *   qkv    (B, T, 3C, H, W) plane-major of out_dtype out
+ */
+int cssm_gdn_qkv_proj(const void* x, int in_dtype, int B, int T, int H, int W, int K, int C,
+                      const float* kernel, const float* bias, int kt, const float* const* conv_kernel,
+                      const float* const* conv_bias, int gate_mode, const void* gates, void* qkv,
+                      int out_dtype, void* stream);
+
+/* 1 if cssm_gdn_qkv_proj runs fused for (T, H, W, K), else 0 (it then runs two kernels). */
+int cssm_gdn_qkv_fused(int T, int H, int W, int K);
+
+/*
  * Batched 2-D real FFT (numpy / XLA rfft2 convention) of P planes, with the
  * optional per-plane sum of |X|^2 over the half spectrum (the spectral L2 norm
  * of cssm.py:4890-4897).  Replaces the rfft2 calls of cssm.py:4880-4888.

@@ -165,6 +165,65 @@ def test_gdn_qkv_post_matches_oracle(mods, kt):
     assert rel_err(to_np(got), ref) < 1e-5
 
 
+# (B, T, H, W, K, C): T in {1, 2, 4, 8} with H*W a multiple of 128 / T runs fused (one kernel), the rest
+# (T = 3, 16; H*W = 64 at T = 1) through proj_planes + qkv_post
+QKV_CASES = [(2, 8, 16, 16, 64, 16), (1, 4, 8, 8, 32, 8), (3, 2, 8, 8, 64, 12), (2, 1, 16, 8, 48, 8),
+             (2, 3, 8, 8, 64, 16), (1, 16, 8, 8, 32, 8), (2, 1, 8, 8, 64, 8)]
+
+
+@pytest.mark.parametrize("shape", QKV_CASES)
+@pytest.mark.parametrize("kt,gate_mode", [(4, 1), (0, 1), (3, 2), (4, 3), (2, 0)])
+def test_gdn_qkv_proj_matches_two_step(mods, shape, kt, gate_mode):
+    """The fused qkv projection equals proj_planes followed by qkv_post (fp32: bit for bit), and the oracle."""
+    _, S = mods
+    B, T, H, W, K, C = shape
+    print_case(test="gdn_qkv_proj", shape=shape, kt=kt, gate_mode=gate_mode,
+               fused=S.gdn_qkv_fused(T, H, W, K))
+    rng = np.random.default_rng(9)
+    x = rng.standard_normal((B, T, H, W, K))
+    Wt = rng.standard_normal((K, 3 * C)) / np.sqrt(K)
+    b = rng.standard_normal(3 * C) * 0.1
+    convs = [{"kernel": rng.standard_normal((kt, 1, C)) / 2, "bias": rng.standard_normal(C) * 0.1}
+             for _ in range(3)] if kt else None
+    gates = None
+    if gate_mode == 1:
+        gates = 1.0 / (1.0 + np.exp(-rng.standard_normal((B, T, H * W, 2))))
+    elif gate_mode == 2:
+        gates = 1.0 / (1.0 + np.exp(-rng.standard_normal((B, T, 2))))
+    elif gate_mode == 3:
+        gates = 1.0 / (1.0 + np.exp(-rng.standard_normal((B, T, 2 * C, H, W))))
+    dc = [_tree(c) for c in convs] if convs else None
+    dg = _dev(gates) if gates is not None else None
+    got = S.gdn_qkv_proj(_dev(x), _dev(Wt), _dev(b), B, T, H, W, dc, gate_mode, dg, out_dtype=torch.float32)
+    two = S.proj_planes(_dev(x), _dev(Wt), _dev(b), B * T, H * W, out_dtype=torch.float32).view(B, T, 3 * C, H, W)
+    S.gdn_qkv_post(two, dc, gate_mode, dg)
+    assert torch.equal(got, two)
+    # oracle: x @ W + b, causal conv over T + SiLU per block, gates on k and v
+    def oracle(xx):
+        cl = (xx.reshape(-1, K) @ Wt + b).reshape(B, T, H, W, 3, C)
+        outs = []
+        for i in range(3):
+            z = cl[..., i, :]
+            if convs:
+                z = O.silu(O.causal_conv_t(z, convs[i]))
+            if i > 0 and gate_mode == 1:
+                z = z * gates[..., i - 1].reshape(B, T, H, W, 1)
+            elif i > 0 and gate_mode == 2:
+                z = z * gates[..., i - 1].reshape(B, T, 1, 1, 1)
+            elif i > 0 and gate_mode == 3:
+                z = z * gates[:, :, (i - 1) * C:i * C].transpose(0, 1, 3, 4, 2)
+            outs.append(z)
+        return np.stack(outs, axis=4).transpose(0, 1, 4, 5, 2, 3).reshape(B, T, 3 * C, H, W)
+    assert rel_err(to_np(got), oracle(x)) < 1e-5
+    # bf16 in / bf16 out against the oracle of the bf16-rounded input: the fused path keeps the
+    # projection in fp32 before the conv, so only the final store rounds; the two-step path stores the
+    # projection in bf16 first (a second rounding, inside the conv)
+    xb = _dev(x, torch.bfloat16)
+    gb = S.gdn_qkv_proj(xb, _dev(Wt), _dev(b), B, T, H, W, dc, gate_mode, dg, out_dtype=torch.bfloat16)
+    bar = 5e-3 if S.gdn_qkv_fused(T, H, W, K) else 2e-2
+    assert bf16_excess_err(to_np(gb.float()), oracle(to_np(xb.float()))) < bar
+
+
 # --------------------------------------------------------- spectral core
 
 CORE_CASES = [
