@@ -345,7 +345,9 @@ int cssm_gdn_qkv_proj(const void* x, int in_dtype, int B, int T, int H, int W, i
                     "cssm_gdn_qkv_proj");
 }
 
-int cssm_gdn_qkv_fused(int T, int H, int W, int K) { return cssm::gdn_qkv_fused_supported(T, H * W, K) ? 1 : 0; }
+int cssm_gdn_qkv_fused(int T, int H, int W, int K, int kt) {
+  return cssm::gdn_qkv_fused_supported(T, H * W, K, kt) ? 1 : 0;
+}
 
 int cssm_fft_min_group(int H, int W) { return cssm::fft_planes_min_group(H, W); }
 

@@ -220,19 +220,22 @@ struct NormGate {
 
 // GDN qkv epilogue (TT > 0): the causal short convolution over T, SiLU and the
 // input gates of cssm.py:4763-4780 / :4844-4848, in the operation order of
-// gdn_qkv_post, on a tile of 128 / TT pixels x all TT frames of one batch
-// element (tile row r = t * (128 / TT) + pixel), so each lane holds the frames
-// of its pixels.  Output (B, TT, N = 3C, HW) plane-major.
+// gdn_qkv_post, on tiles of 128 / TT pixels x TT consecutive frames of one
+// batch element (tile row r = t * (128 / TT) + pixel), so each lane holds the
+// frames of its pixels.  T > TT (TT = 8) runs as T / 8 chunks of the same
+// pixels, in order on one workgroup, the last 3 frames of each chunk kept in
+// LDS for the next (kt <= 4).  Output (B, T, N = 3C, HW) plane-major.
 struct QkvPost {
   const float* w[3];     // (kt, C) per q / k / v block
   const float* b[3];     // (C)
   int kt;                // 0: no convolution and no SiLU
   int gate_mode;         // as cssm_gdn_qkv_post (0 none, 1 per pixel, 2 per frame, 3 per channel and pixel)
   const void* gates;
+  int T;                 // frames per batch element (a multiple of TT)
 };
 
 template <int KMAX, bool PLANE_A, bool OUT_SPLIT, int WN, class TI, class TO, bool NORM = false, bool SPLIT = false,
-          int TT = 0>
+          int TT = 0, bool CARRY = false>
 __global__ void __launch_bounds__(256, 2)
 proj_persist_kernel(const TI* __restrict__ A, int M, int K, int N, const float* __restrict__ Wt,
                     const float* __restrict__ bias, int HW, TO* __restrict__ out_lo, TO* __restrict__ out_hi,
@@ -260,6 +263,8 @@ proj_persist_kernel(const TI* __restrict__ A, int M, int K, int N, const float* 
   __bf16* const A3 = A2 + TM * KP;
   __shared__ float rowsc[NORM ? 2 * TM : 1];             // per-pixel (scale, mean) of the norm
   __shared__ float2 gsh[TT > 0 ? TM : 1];                 // qkv epilogue: the tile's input gates
+  constexpr int KH = 3;                                   // qkv epilogue: frames carried to the next chunk
+  __shared__ float hsh[CARRY ? KH * TN * (TM / 8) : 1];   // their projections, [frame][column][pixel]
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int wm = wave / WN, wn = wave % WN;
   const int n0 = blockIdx.y * TN;
@@ -269,12 +274,15 @@ proj_persist_kernel(const TI* __restrict__ A, int M, int K, int N, const float* 
   static_assert(TT == 0 || (SPLIT && !PLANE_A && OUT_SPLIT && TM % (16 * TT) == 0), "qkv epilogue: frames x pixels tiles");
   constexpr int TP = TT > 0 ? TM / TT : TM;   // pixels per tile (TT > 0)
   // global row of row r of tile `tile`
+  // TT > 0: tile = (b * HW / TP + pixel block) * nch + chunk
+  static_assert(!CARRY || TT == 8, "chunks of 8 frames carry frames");
+  const int nch = CARRY ? qp.T / TT : 1;
   auto grow = [&](int tile, int r) -> int {
     if constexpr (TT == 0) {
       return tile * TM + r;
     } else {
-      const int tpf = HW / TP, bb = tile / tpf, pb = tile % tpf;
-      return (bb * TT + r / TP) * HW + pb * TP + r % TP;
+      const int ch = tile % nch, q = tile / nch, tpf = HW / TP, bb = q / tpf, pb = q % tpf;
+      return (bb * (CARRY ? qp.T : TT) + ch * TT + r / TP) * HW + pb * TP + r % TP;
     }
   };
 
@@ -440,11 +448,16 @@ proj_persist_kernel(const TI* __restrict__ A, int M, int K, int N, const float* 
   float4 pf[PF];
   float4 pg[NORM ? PF : 1];
   // k-th tile of this workgroup.  The qkv epilogue (TT > 0) writes half cache
-  // lines (16 pixels of a plane) per tile; the workgroup takes tiles in
-  // adjacent pairs so both halves of each line pass through the same L2.
+  // lines (16 pixels of a plane) per tile; the workgroup takes its pixel blocks
+  // in adjacent pairs so both halves of each line pass through the same L2, and
+  // the chunks of a pixel block in order (they carry frames to each other).
   auto tile_of = [&](int k) -> int {
-    if constexpr (TT > 0) return 2 * (int(blockIdx.x) + (k >> 1) * int(gridDim.x)) + (k & 1);
-    else return int(blockIdx.x) + k * int(gridDim.x);
+    if constexpr (TT > 0) {
+      const int ch = k % nch, pbk = k / nch;
+      return (2 * (int(blockIdx.x) + (pbk >> 1) * int(gridDim.x)) + (pbk & 1)) * nch + ch;
+    } else {
+      return int(blockIdx.x) + k * int(gridDim.x);
+    }
   };
   int kt_ = 0;
   int tile = tile_of(0);
@@ -517,13 +530,14 @@ proj_persist_kernel(const TI* __restrict__ A, int M, int K, int N, const float* 
       // GDN qkv: lane rows 16 i + 4 (lane / 16) + r are pixel pb TP + (16 i) % TP + 4 (lane / 16) + r of
       // frame t = 16 i / TP; frame t - d of the same pixels is row tile i - d IPF of the same lane
       constexpr int IPF = TP / 16;
-      const int tpf = HW / TP, bb = tile / tpf, pb = tile % tpf;
+      const int ch = tile % nch, tq = tile / nch, tpf = HW / TP, bb = tq / tpf, pb = tq % tpf;
+      const size_t fr0 = size_t(bb) * (CARRY ? qp.T : TT) + size_t(ch) * TT;   // first frame of the tile
       const int C = N / 3;
       // per-pixel / per-frame input gates of the tile (TT frames x TP pixels x (B_k, B_v)) through LDS
       if (qp.gate_mode == 1 || qp.gate_mode == 2) {
         for (int e = tid; e < TT * TP; e += NT) {
           const int t = e / TP, p = e % TP;
-          const size_t fr = size_t(bb) * TT + t;
+          const size_t fr = fr0 + t;
           gsh[e] = qp.gate_mode == 1 ? static_cast<const float2*>(qp.gates)[fr * HW + pb * TP + p]
                                      : static_cast<const float2*>(qp.gates)[fr];
         }
@@ -531,7 +545,7 @@ proj_persist_kernel(const TI* __restrict__ A, int M, int K, int N, const float* 
       }
 #pragma unroll
       for (int j = 0; j < 2; ++j) {
-        const int gn = n0 + wn * 32 + j * 16 + (lane & 15);
+        const int cl = wn * 32 + j * 16 + (lane & 15), gn = n0 + cl;
         if (gn >= N) continue;
         const float bv = bias[gn];
         const int blk = gn / C, c = gn % C;
@@ -543,8 +557,8 @@ proj_persist_kernel(const TI* __restrict__ A, int M, int K, int N, const float* 
 #pragma unroll
         for (int i = 0; i < MI; ++i) {
           const int t = i / IPF;
-          const int px = pb * TP + (i % IPF) * 16 + (lane >> 4) * 4;
-          const size_t fr = size_t(bb) * TT + t;
+          const int pl = (i % IPF) * 16 + (lane >> 4) * 4, px = pb * TP + pl;   // pixel in tile / in plane
+          const size_t fr = fr0 + t;
           float v[4];
 #pragma unroll
           for (int r = 0; r < 4; ++r) {
@@ -552,8 +566,15 @@ proj_persist_kernel(const TI* __restrict__ A, int M, int K, int N, const float* 
             if (qp.kt > 0) {
               float o = fmaf(wd[0], x, bt);
 #pragma unroll
-              for (int d = 7; d >= 1; --d)
-                if (d < qp.kt && i >= d * IPF) o = fmaf(wd[d], acc[i - d * IPF][j][r] + bv, o);
+              for (int d = 7; d >= 1; --d) {
+                if (d >= qp.kt) continue;
+                if (i >= d * IPF) {
+                  o = fmaf(wd[d], acc[i - d * IPF][j][r] + bv, o);
+                } else if (CARRY && ch > 0 && d - t <= KH) {
+                  // frame t - d < 0 of this chunk: frame TT + t - d of the previous chunk
+                  o = fmaf(wd[d], hsh[((KH - (d - t)) * TN + cl) * TP + pl + r], o);
+                }   // else before the first frame: the zero left padding adds nothing
+              }
               x = o * __builtin_amdgcn_rcpf(1.0f + __expf(-o));   // SiLU as gdn_qkv_post computes it
             }
             v[r] = x;
@@ -573,6 +594,17 @@ proj_persist_kernel(const TI* __restrict__ A, int M, int K, int N, const float* 
             for (int r = 0; r < 4; ++r) v[r] *= g[r];
           }
           st4(out_lo, (fr * N + gn) * HW + px, v);
+        }
+        if constexpr (CARRY) {
+          // this chunk's last KH frames for the next chunk of the same pixels (each lane its own slots)
+          if (ch + 1 < nch) {
+#pragma unroll
+            for (int i = (TT - KH) * IPF; i < MI; ++i) {
+              const int pl = (i % IPF) * 16 + (lane >> 4) * 4;
+#pragma unroll
+              for (int r = 0; r < 4; ++r) hsh[((i / IPF - (TT - KH)) * TN + cl) * TP + pl + r] = acc[i][j][r] + bv;
+            }
+          }
         }
       }
     } else if (OUT_SPLIT) {
@@ -1011,13 +1043,15 @@ hipError_t launch_proj_in(const void* X, int in_dtype, int M, int K, int N, cons
 // into the epilogue (persistent kernel, tiles of 128 / T pixels x T frames);
 // returns false when the shape has no fused variant (the caller then runs
 // launch_proj_planes + launch_gdn_qkv_post, which compute the same values)
-template <int TT, class TI, class TO>
+template <int TT, bool CARRY, class TI, class TO>
 static void launch_qkv_fused(const void* X, int M, int K, int N, const float* W, const float* b, int HW, void* out,
                              const QkvPost& qp, hipStream_t s) {
   const int tiles = M / kPersistTM;
   const NormGate ng{nullptr, nullptr, nullptr, 0};
-  const dim3 grid(unsigned(persistent_grid((tiles + 1) / 2)), unsigned((N + 127) / 128));   // tiles in pairs
-  hipLaunchKernelGGL((proj_persist_kernel<64, false, true, 4, TI, TO, false, true, TT>), grid, dim3(256), 0, s,
+  const int nch = CARRY ? qp.T / TT : 1;
+  // pixel blocks in pairs, each with its nch chunks
+  const dim3 grid(unsigned(persistent_grid((tiles / nch + 1) / 2)), unsigned((N + 127) / 128));
+  hipLaunchKernelGGL((proj_persist_kernel<64, false, true, 4, TI, TO, false, true, TT, CARRY>), grid, dim3(256), 0, s,
                      static_cast<const TI*>(X), M, K, N, W, b, HW, static_cast<TO*>(out), static_cast<TO*>(out), 0, 0,
                      nullptr, N, ng, qp);
 }
@@ -1026,24 +1060,30 @@ template <class TI, class TO>
 static bool qkv_fused_t(const void* X, int T, int M, int K, int N, const float* W, const float* b, int HW, void* out,
                         const QkvPost& qp, hipStream_t s) {
   switch (T) {
-    case 1: launch_qkv_fused<1, TI, TO>(X, M, K, N, W, b, HW, out, qp, s); return true;
-    case 2: launch_qkv_fused<2, TI, TO>(X, M, K, N, W, b, HW, out, qp, s); return true;
-    case 4: launch_qkv_fused<4, TI, TO>(X, M, K, N, W, b, HW, out, qp, s); return true;
-    case 8: launch_qkv_fused<8, TI, TO>(X, M, K, N, W, b, HW, out, qp, s); return true;
-    default: return false;
+    case 1: launch_qkv_fused<1, false, TI, TO>(X, M, K, N, W, b, HW, out, qp, s); return true;
+    case 2: launch_qkv_fused<2, false, TI, TO>(X, M, K, N, W, b, HW, out, qp, s); return true;
+    case 4: launch_qkv_fused<4, false, TI, TO>(X, M, K, N, W, b, HW, out, qp, s); return true;
+    case 8: launch_qkv_fused<8, false, TI, TO>(X, M, K, N, W, b, HW, out, qp, s); return true;
+    default:
+      if (T % 8 != 0) return false;
+      launch_qkv_fused<8, true, TI, TO>(X, M, K, N, W, b, HW, out, qp, s);
+      return true;
   }
 }
 
-bool gdn_qkv_fused_supported(int T, int HW, int K) {
-  return (T == 1 || T == 2 || T == 4 || T == 8) && K <= kPersistMaxK && K % 4 == 0 && HW % (kPersistTM / T) == 0;
+// T in {1, 2, 4, 8} (one chunk), or a multiple of 8 with kt <= 4 (chunks of 8 frames carrying 3)
+bool gdn_qkv_fused_supported(int T, int HW, int K, int kt) {
+  const bool t_ok = T == 1 || T == 2 || T == 4 || T == 8 || (T % 8 == 0 && kt <= 4);
+  const int tp = kPersistTM / (T < 8 ? T : 8);
+  return t_ok && K <= kPersistMaxK && K % 4 == 0 && HW % tp == 0;
 }
 
 hipError_t launch_gdn_qkv_proj(const void* X, int in_dtype, int B, int T, int HW, int K, int C, const float* W,
                                const float* b, int kt, const GdnShortConv& sc, int gate_mode, const void* gates,
                                void* out, int out_dtype, hipStream_t s) {
   const int M = B * T * HW, N = 3 * C;
-  if (gdn_qkv_fused_supported(T, HW, K) && kt <= 8) {
-    QkvPost qp{{sc.w[0], sc.w[1], sc.w[2]}, {sc.b[0], sc.b[1], sc.b[2]}, kt, gate_mode, gates};
+  if (gdn_qkv_fused_supported(T, HW, K, kt) && kt <= 8) {
+    QkvPost qp{{sc.w[0], sc.w[1], sc.w[2]}, {sc.b[0], sc.b[1], sc.b[2]}, kt, gate_mode, gates, T};
     if (in_dtype == 0 && out_dtype == 0) qkv_fused_t<float, float>(X, T, M, K, N, W, b, HW, out, qp, s);
     else if (in_dtype == 0) qkv_fused_t<float, uint16_t>(X, T, M, K, N, W, b, HW, out, qp, s);
     else if (out_dtype == 0) qkv_fused_t<uint16_t, float>(X, T, M, K, N, W, b, HW, out, qp, s);

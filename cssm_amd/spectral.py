@@ -373,9 +373,9 @@ def gdn_qkv_proj(x: torch.Tensor, kernel: torch.Tensor, bias: torch.Tensor, B: i
     return out
 
 
-def gdn_qkv_fused(T: int, H: int, W: int, K: int) -> bool:
-    """True when gdn_qkv_proj runs as one fused kernel for this shape."""
-    return bool(_lib.load().cssm_gdn_qkv_fused(T, H, W, K))
+def gdn_qkv_fused(T: int, H: int, W: int, K: int, kt: int) -> bool:
+    """True when gdn_qkv_proj runs as one fused kernel for this shape and short-conv length."""
+    return bool(_lib.load().cssm_gdn_qkv_fused(T, H, W, K, kt))
 
 
 def rfft2(x: torch.Tensor, want_norms: bool = False):

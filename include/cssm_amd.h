@@ -280,9 +280,10 @@ int cssm_gdn_qkv_post(void* qkv, int dtype, int B, int T, int C, int H, int W, i
  * and input gates of cssm_gdn_qkv_post fused into the GEMM's epilogue:
  *   qkv = post(proj(x)),  proj = cssm_proj_planes with N = 3C (identity act).
  * Replaces cssm.py:4753-4758 (qkv_proj), :4763-4780 and :4844-4848 in one pass
- * over qkv instead of three.  Fused when cssm_gdn_qkv_fused(T, H, W, K) (tiles
- * of 128 / T pixels x all T frames: T in {1, 2, 4, 8}, K <= 64, H*W a multiple
- * of 128 / T); otherwise it runs the two calls it replaces, with the same
+ * over qkv instead of three.  Fused when cssm_gdn_qkv_fused(T, H, W, K, kt):
+ * tiles of 128 / T' pixels x T' frames, T' = min(T, 8), T in {1, 2, 4, 8} or a
+ * multiple of 8 with kt <= 4 (chunks of 8 frames carry 3 to the next), K <= 64,
+ * H*W a multiple of 128 / T'; otherwise it runs the two calls it replaces, with the same
  * results (fp32 qkv; a bf16 qkv then holds the projection in bf16 before the
  * convolution, where the fused path keeps it in fp32).
  *   x      (B, T, H*W, K) channels-last of in_dtype
@@ -295,8 +296,8 @@ int cssm_gdn_qkv_proj(const void* x, int in_dtype, int B, int T, int H, int W, i
                       const float* const* conv_bias, int gate_mode, const void* gates, void* qkv,
                       int out_dtype, void* stream);
 
-/* 1 if cssm_gdn_qkv_proj runs fused for (T, H, W, K), else 0 (it then runs two kernels). */
-int cssm_gdn_qkv_fused(int T, int H, int W, int K);
+/* 1 if cssm_gdn_qkv_proj runs fused for (T, H, W, K, kt), else 0 (it then runs two kernels). */
+int cssm_gdn_qkv_fused(int T, int H, int W, int K, int kt);
 
 /*
  * Batched 2-D real FFT (numpy / XLA rfft2 convention) of P planes, with the
