@@ -175,7 +175,8 @@ def gated_step(cell, variables, x, w, S, mark, start=True):
     u, z, ctx = S.proj_in(x, p["in_proj"]["kernel"], p["in_proj"]["bias"], F, HW, silu_lo=True, silu_hi=True,
                           want_ctx=True, out_dtype=torch.float32)
     mark("in_proj")
-    gates = S.gated_gates(ctx.view(B, T, Ci), p, H, W, cell.gate_type, cell.gate_activation, c_scale=1.0 / HW)
+    gates = S.gated_gates(ctx.view(B, T, Ci), p, H, W, cell.gate_type, cell.gate_activation,
+                          c_scale=S.scan_c_scale(H, W))
     khat = cell.spectral_kernel(p, H, W)
     mark("gates")
     y = S.gated_scan(u.view(B, T, Ci, H, W), z.view(B, T, Ci, H, W), gates, khat)

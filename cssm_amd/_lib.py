@@ -57,7 +57,7 @@ SIGNATURES = {
     "cssm_last_error": (ctypes.c_char_p, []),
     "cssm_spectral_kernel": (ctypes.c_int, [ctypes.c_void_p, ctypes.c_int, ctypes.c_int, ctypes.c_int,
                                             ctypes.c_int, ctypes.c_float, ctypes.c_int, ctypes.c_int,
-                                            ctypes.c_void_p, ctypes.c_void_p]),
+                                            ctypes.c_int, ctypes.c_void_p, ctypes.c_void_p]),
     "cssm_plane_mean": (ctypes.c_int, [ctypes.c_void_p, ctypes.c_int, ctypes.c_longlong, ctypes.c_int,
                                        ctypes.c_int, ctypes.c_int, ctypes.c_void_p, ctypes.c_void_p]),
     "cssm_gated_gates": (ctypes.c_int, [ctypes.c_void_p, ctypes.c_int, ctypes.c_int, ctypes.c_int,
@@ -94,6 +94,7 @@ SIGNATURES = {
     "cssm_gdn_proj_out": (_I, [_P, _P, _I, _I, _I, _I, _I, _I, _P, _P, _P, _P, _P, _I, _P]),
     "cssm_gated_scan_supported": (ctypes.c_int, [ctypes.c_int, ctypes.c_int]),
     "cssm_gated_scan_min_group": (ctypes.c_int, [ctypes.c_int, ctypes.c_int]),
+    "cssm_gated_scan_col_order": (ctypes.c_int, [ctypes.c_int, ctypes.c_int, ctypes.POINTER(ctypes.c_int)]),
 }
 
 _lock = threading.Lock()

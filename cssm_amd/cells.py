@@ -136,7 +136,7 @@ class GatedCSSM:
         key = (k.data_ptr(), k._version, H, W, self.spectral_rho)
         kh = self._khat_cache.get(key)
         if kh is None:
-            kh = S.spectral_kernel(k, H, W, self.spectral_rho, squash=True, goom_floor=True)
+            kh = S.spectral_kernel(k, H, W, self.spectral_rho, squash=True, goom_floor=True, scan_order=True)
             self._khat_cache = {key: kh}
         return kh
 
@@ -169,7 +169,7 @@ class GatedCSSM:
         else:
             u = xm
         ctx = ctx.view(B, T, Ci)
-        gates = S.gated_gates(ctx, p, H, W, self.gate_type, self.gate_activation, c_scale=1.0 / HW)
+        gates = S.gated_gates(ctx, p, H, W, self.gate_type, self.gate_activation, c_scale=S.scan_c_scale(H, W))
         khat = self.spectral_kernel(p, H, W)
         y = S.gated_scan(u, z, gates, khat)
         out = S.proj_out(y.view(F, Ci, HW), p["out_proj"]["kernel"], p["out_proj"]["bias"], out_dtype=x.dtype)

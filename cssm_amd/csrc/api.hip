@@ -56,7 +56,7 @@ const char* cssm_strerror(int status) {
 const char* cssm_last_error(void) { return g_last_error; }
 
 int cssm_spectral_kernel(const float* k, int C, int K, int H, int W, float rho, int squash,
-                         int goom_floor, float* khat, void* stream) {
+                         int goom_floor, int scan_order, float* khat, void* stream) {
   if (!k || !khat) return fail(CSSM_ERR_NULL, "cssm_spectral_kernel: k and khat must be non-null");
   if (C <= 0 || K <= 0 || H <= 0 || W <= 0)
     return fail(CSSM_ERR_SHAPE, "cssm_spectral_kernel: C=%d K=%d H=%d W=%d must be positive", C, K, H, W);
@@ -65,7 +65,7 @@ int cssm_spectral_kernel(const float* k, int C, int K, int H, int W, float rho, 
                 "cssm_spectral_kernel: K=%d lies between H=%d and W=%d (reference pad/crop undefined)", K,
                 H, W);
   if (!aligned(khat, 8)) return fail(CSSM_ERR_ALIGN, "cssm_spectral_kernel: khat must be 8-byte aligned");
-  const hipError_t e = cssm::launch_spectral_kernel(k, C, K, H, W, rho, squash, goom_floor,
+  const hipError_t e = cssm::launch_spectral_kernel(k, C, K, H, W, rho, squash, goom_floor, scan_order ? 1 : 0,
                                                     reinterpret_cast<float2*>(khat),
                                                     static_cast<hipStream_t>(stream));
   if (e == hipErrorInvalidValue)
@@ -116,6 +116,13 @@ int cssm_gated_gates(const float* ctx, int B, int T, int C, int H, int W, const 
 int cssm_gated_scan_supported(int H, int W) { return cssm::gated_scan_has_kernel(H, W) ? 1 : 0; }
 
 int cssm_gated_scan_min_group(int H, int W) { return cssm::gated_scan_min_group(H, W); }
+
+int cssm_gated_scan_col_order(int H, int W, int* cols) {
+  if (!cols) return fail(CSSM_ERR_NULL, "cssm_gated_scan_col_order: cols must be non-null");
+  if (H <= 0 || W <= 0) return fail(CSSM_ERR_SHAPE, "cssm_gated_scan_col_order: H=%d W=%d", H, W);
+  for (int p = 0; p < W / 2 + 1; ++p) cols[p] = cssm::scan_col(H, W, p);
+  return CSSM_OK;
+}
 
 int cssm_gated_scan_fwd(const void* u, const void* z, void* y, int dtype, int B, int T, int C, int H, int W,
                         const float* gates, const float* khat, int u_act, int z_act, void* stream) {

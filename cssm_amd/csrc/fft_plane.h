@@ -20,6 +20,7 @@
 #include <stdint.h>
 
 #include "fft_reg.h"
+#include "launch.h"
 
 namespace cssm {
 
@@ -77,8 +78,9 @@ constexpr int fft_radix1(int n) { return n >= 128 ? 16 : (n >= 32 ? 8 : (n >= 8 
 // LH, LW: log2 of the plane; NP planes per workgroup; PPT real samples per
 // thread per plane load (64 for large planes: a 128x128 plane is one 256-thread
 // workgroup, two of which share a CU so one's barriers and memory waits hide
-// behind the other's arithmetic).
-template <int LH, int LW, int NP, int PPT>
+// behind the other's arithmetic).  SO: the column passes walk the packed
+// columns in scan_col order (per-bin planes stored in that order).
+template <int LH, int LW, int NP, int PPT, bool SO = false>
 struct Geom {
   static constexpr int H = 1 << LH, W = 1 << LW;
   static constexpr int HP = H / 2, WH = W / 2, WF = WH + 1;
@@ -180,13 +182,16 @@ struct Geom {
     pl = RP / HP;
     p = RP % HP;
   }
-  // C1/I2 job -> (pl, v, s); C2 job -> (pl, v, pair): column fastest
-  static __device__ __forceinline__ void col_job(int w, int j, int l, int& pl, int& v, int& r) {
+  // C1/I2 job -> (pl, v, s); C2 job -> (pl, v, pair): column fastest.  The
+  // wave's columns are positions n = COL % W/2 of the per-bin planes, holding
+  // column v = scan_col(n) under SO (else v = n).
+  static __device__ __forceinline__ void col_job(int w, int j, int l, int& pl, int& v, int& r, int& n) {
     const int q = j * 64 + l;
     const int COL = w * CPW + q % CPW;
     r = q / CPW;
     pl = COL / WH;
-    v = COL % WH;
+    n = COL % WH;
+    v = SO ? scan_col(H, W, n) : n;
   }
   // ---- load / store phase.  Lane l's 4-vector i (i < JLD) of wave w is column
   // c4 = l % (W/4) of group row v4_row(w, i, m) (row = pl * H + r): consecutive
@@ -246,6 +251,14 @@ struct Buf {
   __device__ __forceinline__ float2 ld2(unsigned off) const {
     return __builtin_bit_cast(float2, __builtin_amdgcn_raw_buffer_load_b64(r, int(off), 0, 0));
   }
+  // per-lane byte offset voff plus a uniform soff (kept in an SGPR, so a
+  // constant stride costs no VALU address arithmetic)
+  __device__ __forceinline__ float4 ld4(unsigned voff, int soff) const {
+    return __builtin_bit_cast(float4, __builtin_amdgcn_raw_buffer_load_b128(r, int(voff), soff, 0));
+  }
+  __device__ __forceinline__ float2 ld2(unsigned voff, int soff) const {
+    return __builtin_bit_cast(float2, __builtin_amdgcn_raw_buffer_load_b64(r, int(voff), soff, 0));
+  }
   // Streamed I/O vectors (float4 or 4 x bf16; each touched once): byte offset
   // voff (per lane) + soff (uniform), non-temporal cache policy so the planes
   // passing through do not evict what the workgroups re-read from L2 every
@@ -290,10 +303,12 @@ __device__ __forceinline__ void wave_sync() {
 // of the v = 0 and v = W/2 columns survives).
 //
 // Policies (Op):
-//   op.bins(j, a2, pl, k, v, sp)  C2: sp[q] is bin (u = k + H1 q, v) of plane
-//        pl, 0 < v < W/2; on entry the forward value (when FWD), on exit the
-//        inverse input (when INV).  (j, a2) name the thread's unit slot, fixed
-//        for the whole launch, so per-bin state can live in registers.
+//   op.bins(j, a2, pl, k, n, sp)  C2: sp[q] is bin (u = k + H1 q, v) of plane
+//        pl, 0 < v < W/2, where n is the column's position in the per-bin
+//        planes (v = scan_col(n) under SO, else n); on entry the forward value
+//        (when FWD), on exit the inverse input (when INV).  (j, a2) name the
+//        thread's unit slot, fixed for the whole launch, so per-bin state can
+//        live in registers.
 //   op.edge(j, pl, uA, uB, e, v4) the DC / Nyquist bins of rows uA and uB
 //        (uB = -uA mod H; e = uA): v4 = {(uA, 0), (uA, W/2), (uB, 0), (uB, W/2)};
 //        forward value on entry (FWD), inverse input on exit (INV).
@@ -438,8 +453,8 @@ struct PlaneFft {
   __device__ __forceinline__ void c1(int w, int l) const {
 #pragma unroll
     for (int j = 0; j < G::JC1; ++j) {
-      int pl, v, s;
-      G::col_job(w, j, l, pl, v, s);
+      int pl, v, s, n;
+      G::col_job(w, j, l, pl, v, s, n);
       const int col = G::p_col(v);
       float2 zz[H1];
 #pragma unroll
@@ -462,8 +477,8 @@ struct PlaneFft {
   __device__ __forceinline__ void c2(int w, int l, Op& op) const {
 #pragma unroll
     for (int j = 0; j < G::JC2; ++j) {
-      int pl, v, pair;
-      G::col_job(w, j, l, pl, v, pair);
+      int pl, v, pair, n;
+      G::col_job(w, j, l, pl, v, pair, n);
       int kA, kB;
       pair_units<H1>(pair, kA, kB);
       const int col = G::p_col(v);
@@ -482,7 +497,7 @@ struct PlaneFft {
             for (int q = 0; q < H2; ++q) edge[pl * H + k + H1 * q] = sp[q];
           }
         } else {
-          op.bins(j, a2, pl, k, v, sp);
+          op.bins(j, a2, pl, k, n, sp);
           if (INV) {
             Dft<H2, true>::run(sp);
 #pragma unroll
@@ -574,8 +589,8 @@ struct PlaneFft {
   __device__ __forceinline__ void i2(int w, int l) const {
 #pragma unroll
     for (int j = 0; j < G::JC1; ++j) {
-      int pl, v, s;
-      G::col_job(w, j, l, pl, v, s);
+      int pl, v, s, n;
+      G::col_job(w, j, l, pl, v, s, n);
       const int col = G::p_col(v);
       float2 zz[H1];
 #pragma unroll

@@ -29,30 +29,29 @@ namespace cssm {
 
 // The forward row pass skips the 1/2 of the packed-row separation, so the
 // spectrum the recurrence sees is U' = 2U for every bin (the edge unpack keeps
-// its 1/2 and inherits the factor from the doubled DC/Nyquist column).  The
-// state is then h' = 2h; the GOOM floor is applied at the doubled scale and
-// C is halved, so y is unchanged.
+// its 1/2 and inherits the factor from the doubled DC/Nyquist column; the
+// small-plane kernel doubles its input on load to match).  The state is then
+// h' = 2h: the gate planes carry the floor term at that scale and C / 2
+// (c_scale = 1 / (2 H W)), so y is unchanged.
 //
 // gate g = (E, DB, VF, GC): E = exp(-Delta), DB = (Delta + 1e-8) B,
-// VF = (Delta + 1e-8) 1e-7 (the input term when |U B| < 1e-7), GC = C c_scale.
-// |DB U| < VF  <=>  |U B| < 1e-7 since Delta + 1e-8 > 0.
+// VF = 2e-7 (Delta + 1e-8) (the input term when |U B| < 1e-7), GC = C c_scale.
+// |DB U'| < VF  <=>  |U B| < 1e-7 since Delta + 1e-8 > 0.
 __device__ __forceinline__ float2 scan_bin(float2& h, float2 U, float4 g, float2 kh) {
   float2 V = make_float2(U.x * g.y, U.y * g.y);
-  const float vf = g.z + g.z;
-  if (V.x * V.x + V.y * V.y < vf * vf) V = make_float2(vf, 0.0f);
+  if (V.x * V.x + V.y * V.y < g.z * g.z) V = make_float2(g.z, 0.0f);
   const float2 A = make_float2(kh.x * g.x, kh.y * g.x);
   const float2 hn = make_float2(fmaf(A.x, h.x, fmaf(-A.y, h.y, V.x)), fmaf(A.x, h.y, fmaf(A.y, h.x, V.y)));
   h = hn;
-  const float gc = 0.5f * g.w;
-  return make_float2(hn.x * gc, hn.y * gc);
+  return make_float2(hn.x * g.w, hn.y * g.w);
 }
 
 struct ScanArgs {
   const void* u;
   const void* z;
   void* y;
-  const float4* gates;   // (B, T, H, WF) per-bin (E, DB, VF, GC)
-  const float2* khat;    // (C, H, WF), GOOM-floored
+  const float4* gates;   // (B, T, H, WF) per-bin (E, DB, VF, GC), columns in scan_col order
+  const float2* khat;    // (C, H, WF), GOOM-floored, columns in scan_col order
   int T, C, u_act, z_act;
 };
 
@@ -68,9 +67,10 @@ struct GatedScanOp {
   Buf gbuf;   // gates of (b, t): (H, WF) float4
   Buf kbuf;   // K_hat of the group's planes: (NP, H, WF) float2
 
-  // gates of (b, t) and the spectral kernel of this plane at bins (k + H1 q, v)
-  __device__ __forceinline__ void bins(int j, int a2, int pl, int k, int v, float2 (&sp)[G::H2]) const {
-    const unsigned gi = unsigned(k * WF + v), ki = unsigned(pl * H * WF) + gi;
+  // gates of (b, t) and the spectral kernel of this plane at bins (k + H1 q,
+  // column at position n)
+  __device__ __forceinline__ void bins(int j, int a2, int pl, int k, int n, float2 (&sp)[G::H2]) const {
+    const unsigned gi = unsigned(k * WF + n), ki = unsigned(pl * H * WF) + gi;
     // gates in batches of QB bins (fewer registers in flight at 4 waves / SIMD)
     constexpr int QB = G::NT >= 512 ? 4 : H2;
 #pragma unroll
@@ -79,8 +79,8 @@ struct GatedScanOp {
       float2 kq[QB];
 #pragma unroll
       for (int q = 0; q < QB; ++q) {
-        gq[q] = gbuf.ld4((gi + (q0 + q) * H1 * WF) * 16u);
-        kq[q] = kbuf.ld2((ki + (q0 + q) * H1 * WF) * 8u);
+        gq[q] = gbuf.ld4(gi * 16u, (q0 + q) * H1 * WF * 16);
+        kq[q] = kbuf.ld2(ki * 8u, (q0 + q) * H1 * WF * 8);
       }
 #pragma unroll
       for (int q = 0; q < QB; ++q) sp[q0 + q] = scan_bin(h[j][a2][q0 + q], sp[q0 + q], gq[q], kq[q]);
@@ -103,7 +103,7 @@ struct GatedScanOp {
 template <int LH, int LW, int NP, int PPT, class IO>
 __global__ void __launch_bounds__((NP << (LH + LW)) / PPT, PPT >= 64 ? 2 : ((NP << (LH + LW)) / PPT >= 512 ? 4 : 1))
 gated_scan_pow2(const ScanArgs a) {
-  using G = Geom<LH, LW, NP, PPT>;
+  using G = Geom<LH, LW, NP, PPT, true>;
   static_assert(G::NT == (NP << (LH + LW)) / PPT, "launch bound");
   constexpr int H = G::H, WF = G::WF, W = G::W, H2 = G::H2, NT = G::NT;
   using V4 = typename IO::V4;
@@ -250,21 +250,13 @@ gated_scan_pow2(const ScanArgs a) {
 //   cols   X[pl][u][v] = sum_h R[h][v] e^{-2 pi i u h / H}   (each thread owns
 //          fixed bins, so the state h of its bins stays in registers)
 //   scan   h = floor(K_hat) e^{-Delta} h + (Delta + 1e-8) floor(X B);  S = C h / (H W)
+//          (evaluated on 2X and 2h with the gate planes' doubled floor term and C / (2 H W))
 //   icols  Z[pl][h][v] = sum_u S[u][v] e^{+2 pi i u h / H}
 //   C2R    y[h][w] = Re Z[h][0] + 2 sum_{0 < v < W/2} Re(Z[h][v] e^{2 pi i v w / W})
 //                    + [W even] (-1)^w Re Z[h][W/2]                 (numpy irfft2)
 //   store  y * z_gate
 // Twiddles come from double-precision tables in LDS.
 // ---------------------------------------------------------------------------
-__device__ __forceinline__ float2 scan_bin_plain(float2& h, float2 U, float4 g, float2 kh) {
-  float2 V = make_float2(U.x * g.y, U.y * g.y);
-  if (V.x * V.x + V.y * V.y < g.z * g.z) V = make_float2(g.z, 0.0f);
-  const float2 A = make_float2(kh.x * g.x, kh.y * g.x);
-  const float2 hn = make_float2(fmaf(A.x, h.x, fmaf(-A.y, h.y, V.x)), fmaf(A.x, h.y, fmaf(A.y, h.x, V.y)));
-  h = hn;
-  return make_float2(hn.x * g.w, hn.y * g.w);
-}
-
 constexpr int cx_gcd(int a, int b) { return b == 0 ? a : cx_gcd(b, a % b); }
 
 template <int H, int W>
@@ -281,6 +273,7 @@ struct SmallGeom {
 template <int H, int W, class IO>
 __global__ void __launch_bounds__(256) gated_scan_small(const ScanArgs a, long long P) {
   using G = SmallGeom<H, W>;
+  static_assert(H < 128 && W < 128, "per-bin planes of these sizes are in natural column order");
   constexpr int WF = G::WF, HW = G::HW, NT = G::NT, NP = G::NP, JB = G::JB;
   using TE = typename IO::T;
   __shared__ float xs[G::NX];            // input / output planes
@@ -329,7 +322,7 @@ __global__ void __launch_bounds__(256) gated_scan_small(const ScanArgs a, long l
         v = IO::to_f(up[size_t(base_u[pl]) + t * tstride + px]);
         if (a.u_act == 1) v = silu_f(v);
       }
-      xs[e] = v;
+      xs[e] = 2.0f * v;   // the recurrence runs on 2U, as in the power-of-two kernel
     }
     __syncthreads();
     // rows: R[pl][h][v]
@@ -365,7 +358,7 @@ __global__ void __launch_bounds__(256) gated_scan_small(const ScanArgs a, long l
         const int c = int((p0 + pl) % C);
         const float4 g = a.gates[(size_t(b) * T + t) * (H * WF) + r];
         const float2 kh = a.khat[size_t(c) * (H * WF) + r];
-        Sv = scan_bin_plain(h[j], X, g, kh);
+        Sv = scan_bin(h[j], X, g, kh);
       }
       ss[o] = Sv;
     }
@@ -409,7 +402,7 @@ __global__ void __launch_bounds__(256) gated_scan_small(const ScanArgs a, long l
 
 template <int LH, int LW, int NP, int PPT, class IO>
 static hipError_t run_scan(const ScanArgs& a, int B, hipStream_t s) {
-  using G = Geom<LH, LW, NP, PPT>;
+  using G = Geom<LH, LW, NP, PPT, true>;
   const long long blocks = (long long)B * a.C / NP;
   hipLaunchKernelGGL((gated_scan_pow2<LH, LW, NP, PPT, IO>), dim3(unsigned(blocks)), dim3(G::NT), 0, s, a);
   return hipGetLastError();

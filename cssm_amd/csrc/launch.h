@@ -6,6 +6,20 @@
 
 namespace cssm {
 
+// Column order of the per-bin planes the gated scan reads (gates, K_hat):
+// position p of a row holds frequency column scan_col(H, W, p).  At 128 x 128
+// the 64 packed columns are interleaved so that the eight columns a wave owns
+// in the column passes lie in four row blocks at two pair positions (spread
+// over the LDS banks) while its per-bin loads still cover whole 128-byte
+// lines: positions 8 g .. 8 g + 7 map to blocks 4 (g % 4) + 0..3 at pairs
+// 2 (g / 4) + {0, 1}.  The Nyquist column stays last; every other plane size
+// keeps the natural order.
+__host__ __device__ inline int scan_col(int H, int W, int p) {
+  if (H != 128 || W != 128 || p >= 64) return p;
+  const int qc = p % 8, g = p / 8;
+  return 4 * (g % 4) + qc % 4 + 16 * (2 * (g / 4) + qc / 4);
+}
+
 struct GateWeights {
   const float* kd[3];
   const float* bd[3];
@@ -14,7 +28,7 @@ struct GateWeights {
 };
 
 hipError_t launch_spectral_kernel(const float* k, int C, int K, int H, int W, float rho, int squash,
-                                  int goom_floor, float2* khat, hipStream_t s);
+                                  int goom_floor, int scan_order, float2* khat, hipStream_t s);
 hipError_t launch_plane_mean(const void* x, int dtype, long long nplanes, int HW, int act, float* out,
                              hipStream_t s);
 hipError_t launch_gated_gates(const float* ctx, int BT, int C, int H, int W, int factored, int act,

@@ -21,7 +21,7 @@ namespace cssm {
 // out: (C, H, W/2+1) complex, optionally GOOM-floored (|x| < 1e-7 -> 1e-7+0j).
 // ---------------------------------------------------------------------------
 __global__ void spectral_kernel_prep(const float* __restrict__ k, int K, int H, int W, float rho,
-                                     int squash, int goom_floor, float2* __restrict__ out) {
+                                     int squash, int goom_floor, int scan_order, float2* __restrict__ out) {
   extern __shared__ double sm_d[];   // rows x WF complex (re, im)
   const int c = blockIdx.x;
   const int WF = W / 2 + 1;
@@ -53,9 +53,10 @@ __global__ void spectral_kernel_prep(const float* __restrict__ k, int K, int H, 
     sm_d[2 * idx + 1] = im;
   }
   __syncthreads();
-  // stage 2: F[u][v] = sum_i R[i][v] e^{-2 pi i u (i') / H}
+  // stage 2: F[u][v] = sum_i R[i][v] e^{-2 pi i u (i') / H}, at position
+  // (u, p) of the output with v = scan_col(p) in the scan's column order
   for (int idx = threadIdx.x; idx < H * WF; idx += blockDim.x) {
-    const int u = idx / WF, v = idx % WF;
+    const int u = idx / WF, v = scan_order ? scan_col(H, W, idx % WF) : idx % WF;
     double re = 0.0, im = 0.0;
     for (int i = 0; i < nr; ++i) {
       const int ip = i + oh;
@@ -85,9 +86,11 @@ __global__ void spectral_kernel_prep(const float* __restrict__ k, int K, int H, 
 // ---------------------------------------------------------------------------
 // Gates (cssm.py:536-556, _compute_gate :432-441, GOOM shifts :559-567).
 // One block per (b, t).  Output per bin (u, v) of the (H, W/2+1) half
-// spectrum, float4 = (exp(-Delta), (Delta + 1e-8) B, (Delta + 1e-8) 1e-7, C * c_scale):
-// the decay, the input gain, the input term that replaces (Delta + 1e-8) U B
-// when |U B| < 1e-7 (the to_goom floor), and the readout gain; where
+// spectrum, at position (u, p) with v = scan_col(H, W, p) (the scan's column
+// order), float4 = (exp(-Delta), (Delta + 1e-8) B, 2e-7 (Delta + 1e-8), C * c_scale):
+// the decay, the input gain, the input term that replaces (Delta + 1e-8) 2 U B
+// when |U B| < 1e-7 (the to_goom floor, at the doubled spectrum 2 U the scan's
+// forward transform produces), and the readout gain; where
 //   Delta = act(G_delta), act in {softplus, 2*sigmoid, exp(clip(-4, 2))}
 //   dense:    G_x[u, v] = ctx . kernel[:, u*WF + v] + bias[u*WF + v]
 //   factored: G_x[u, v] = (ctx . kh[:, u] + bh[u]) * (ctx . kw[:, v] + bw[v])
@@ -163,24 +166,25 @@ __global__ void gated_gates_kernel(const float* __restrict__ ctx, int C, int H, 
     }
     __syncthreads();
     for (int o = threadIdx.x; o < nbin; o += blockDim.x) {
-      const int u = o / WF, v = o % WF;
+      const int u = o / WF, v = scan_col(H, W, o % WF);
       float gr[3];
       for (int g = 0; g < 3; ++g) gr[g] = fac[g * (H + WF) + u] * fac[g * (H + WF) + H + v];
       const float d = gate_act(gr[0], act), dd = d + 1e-8f;
-      out[size_t(bt) * nbin + o] = make_float4(expf(-d), dd * gr[1], dd * 1e-7f, gr[2] * c_scale);
+      out[size_t(bt) * nbin + o] = make_float4(expf(-d), dd * gr[1], dd * 2e-7f, gr[2] * c_scale);
     }
   } else {
     for (int o = threadIdx.x; o < nbin; o += blockDim.x) {
+      const int bin = (o / WF) * WF + scan_col(H, W, o % WF);
       float gr[3];
       for (int g = 0; g < 3; ++g) {
-        float acc = gw.bd[g][o];
-        const float* kk = gw.kd[g] + o;
+        float acc = gw.bd[g][bin];
+        const float* kk = gw.kd[g] + bin;
 #pragma unroll 8
         for (int c = 0; c < C; ++c) acc = fmaf(cx[c], kk[size_t(c) * nbin], acc);
         gr[g] = acc;
       }
       const float d = gate_act(gr[0], act), dd = d + 1e-8f;
-      out[size_t(bt) * nbin + o] = make_float4(expf(-d), dd * gr[1], dd * 1e-7f, gr[2] * c_scale);
+      out[size_t(bt) * nbin + o] = make_float4(expf(-d), dd * gr[1], dd * 2e-7f, gr[2] * c_scale);
     }
   }
 }
@@ -232,13 +236,13 @@ __global__ void plane_mean_kernel(const TIN* __restrict__ x, long long nplanes, 
 // ----------------------------------------------------------------- launchers
 
 hipError_t launch_spectral_kernel(const float* k, int C, int K, int H, int W, float rho, int squash,
-                                  int goom_floor, float2* khat, hipStream_t s) {
+                                  int goom_floor, int scan_order, float2* khat, hipStream_t s) {
   const int WF = W / 2 + 1;
   const int rows = (K > H || K > W) ? H : K;
   const size_t shm = size_t(rows) * WF * 2 * sizeof(double);
   if (shm > 64 * 1024) return hipErrorInvalidValue;
   hipLaunchKernelGGL(spectral_kernel_prep, dim3(C), dim3(256), shm, s, k, K, H, W, rho, squash,
-                     goom_floor, khat);
+                     goom_floor, scan_order, khat);
   return hipGetLastError();
 }
 

@@ -6,7 +6,7 @@ stream.  Nothing here computes on the CPU and there is no fallback path.
 from __future__ import annotations
 
 import ctypes
-from typing import Dict, Optional
+from typing import Dict, List, Optional
 
 import torch
 
@@ -31,16 +31,35 @@ def _dev(t: torch.Tensor, name: str, dtype=None) -> torch.Tensor:
 
 
 def spectral_kernel(k: torch.Tensor, H: int, W: int, rho: float = 0.999, squash: bool = True,
-                    goom_floor: bool = True) -> torch.Tensor:
-    """K_hat (C, H, W//2+1) complex64 from k (C, K, K) (cssm.py:505-529, 4711-4716)."""
+                    goom_floor: bool = True, scan_order: bool = False) -> torch.Tensor:
+    """K_hat (C, H, W//2+1) complex64 from k (C, K, K) (cssm.py:505-529, 4711-4716).
+
+    ``scan_order`` stores the columns in :func:`scan_col_order` (what
+    :func:`gated_scan` reads); otherwise in natural order.
+    """
     _dev(k, "k", torch.float32)
     C, K, K2 = k.shape
     if K != K2:
         raise ValueError("spectral kernel must be square (C, K, K)")
     out = torch.empty((C, H, W // 2 + 1), dtype=torch.complex64, device=k.device)
     _lib.call("cssm_spectral_kernel", k.data_ptr(), C, K, H, W, float(rho), int(squash),
-              int(goom_floor), out.data_ptr(), _stream())
+              int(goom_floor), int(scan_order), out.data_ptr(), _stream())
     return out
+
+
+def scan_col_order(H: int, W: int) -> List[int]:
+    """Column order of the per-bin planes :func:`gated_scan` reads (gates, K_hat):
+    entry p is the frequency column stored at position p of a row (the identity
+    except at 128 x 128)."""
+    cols = (ctypes.c_int * (W // 2 + 1))()
+    _lib.call("cssm_gated_scan_col_order", H, W, cols)
+    return list(cols)
+
+
+def scan_c_scale(H: int, W: int) -> float:
+    """The c_scale :func:`gated_gates` takes for :func:`gated_scan`: the irfft2
+    normalisation and the 1/2 of the scan's doubled spectrum, folded into C."""
+    return 0.5 / (H * W)
 
 
 def plane_mean(x: torch.Tensor, silu: bool = False) -> torch.Tensor:
@@ -78,8 +97,9 @@ def gate_params_struct(gp: Dict[str, Dict[str, torch.Tensor]], gate_type: str,
 def gated_gates(ctx: torch.Tensor, params: Dict, H: int, W: int, gate_type: str = "dense",
                 activation: str = "softplus", c_scale: float = 1.0,
                 out: Optional[torch.Tensor] = None) -> torch.Tensor:
-    """(B, T, H, Wf, 4) = [exp(-Delta), (Delta + 1e-8) B, (Delta + 1e-8) 1e-7, C * c_scale]
-    (cssm.py:536-567)."""
+    """(B, T, H, Wf, 4) = [exp(-Delta), (Delta + 1e-8) B, 2e-7 (Delta + 1e-8), C * c_scale]
+    per bin (cssm.py:536-567), columns in :func:`scan_col_order`: the gate planes
+    :func:`gated_scan` reads with ``c_scale = scan_c_scale(H, W)``."""
     _dev(ctx, "ctx", torch.float32)
     B, T, C = ctx.shape
     if out is None:
@@ -97,8 +117,8 @@ def gated_scan(u: torch.Tensor, z: torch.Tensor, gates: torch.Tensor, khat: torc
     """Fused rfft2 -> recurrence -> irfft2 -> x z for plane-major (B, T, C, H, W) u, z.
 
     ``gates`` are the per-bin planes (B, T, H, Wf, 4) from :func:`gated_gates`
-    made with ``c_scale = 1/(H*W)``; ``khat`` comes from
-    :func:`spectral_kernel` with ``goom_floor=True``.
+    made with ``c_scale = scan_c_scale(H, W)``; ``khat`` comes from
+    :func:`spectral_kernel` with ``goom_floor=True, scan_order=True``.
     """
     _dev(u, "u")
     _dev(z, "z", u.dtype)

@@ -29,7 +29,7 @@
 extern "C" {
 #endif
 
-#define CSSM_ABI_VERSION 1
+#define CSSM_ABI_VERSION 2
 
 typedef enum cssm_status {
   CSSM_OK = 0,
@@ -91,12 +91,14 @@ const char* cssm_last_error(void);
  *   squash      1 = apply rho/(1+|F|) (0 = GDN no_spectral_clamp, cssm.py:4715)
  *   goom_floor  1 = replace |K_hat| < 1e-7 by 1e-7+0j (to_goom floor, goom.py:161-174),
  *               which is what the scan consumes.
+ *   scan_order  1 = columns in the order of cssm_gated_scan_col_order (what
+ *               cssm_gated_scan_fwd reads), 0 = natural order.
  * Pad rule: K <= H, W zero-pads with (H-K)//2 before; K >= H and K >= W
  * centre-crops from (K-H)//2.  K between H and W is rejected (the reference
  * produces mismatched shapes there).
  */
 int cssm_spectral_kernel(const float* k, int C, int K, int H, int W, float rho, int squash,
-                         int goom_floor, float* khat, void* stream);
+                         int goom_floor, int scan_order, float* khat, void* stream);
 
 /*
  * Spatial mean of every H x W plane: out[i] = mean(act(x[i, :, :])).
@@ -111,12 +113,16 @@ int cssm_plane_mean(const void* x, int dtype, long long nplanes, int H, int W, i
  * Replaces cssm.py:538-556 (_make_gate for delta_proj, B_proj, C_proj and
  * _compute_gate) and the Delta terms of cssm.py:559-567.
  *   ctx   (B, T, C) float32
- *   gates (B, T, H, Wf, 4) float32 out, per bin:
- *         [exp(-Delta), (Delta + 1e-8) B, (Delta + 1e-8) 1e-7, C * c_scale]
- *         = decay, input gain, the input term that replaces (Delta + 1e-8) U B
- *         when |U B| < 1e-7 (the to_goom floor), readout gain.
- * c_scale = 1 gives the reference values; cssm_gated_scan_fwd expects
- * c_scale = 1 / (H * W) (the irfft2 normalisation folded into C).
+ *   gates (B, T, H, Wf, 4) float32 out: the per-bin planes cssm_gated_scan_fwd
+ *         reads.  Position p of row u holds bin (u, v = cols[p]) of
+ *         cssm_gated_scan_col_order, as
+ *         [exp(-Delta), (Delta + 1e-8) B, 2e-7 (Delta + 1e-8), C * c_scale]
+ *         = decay, input gain, the input term that replaces (Delta + 1e-8) 2 U B
+ *         when |U B| < 1e-7 (the to_goom floor; the scan's forward transform
+ *         yields 2 U, so the floor term is doubled), readout gain.
+ * c_scale = 1 gives the reference C; cssm_gated_scan_fwd expects
+ * c_scale = 1 / (2 H W) (the irfft2 normalisation and the 1/2 of the doubled
+ * spectrum folded into C).
  */
 int cssm_gated_gates(const float* ctx, int B, int T, int C, int H, int W,
                      const cssm_gate_params* params, float c_scale, float* gates, void* stream);
@@ -132,10 +138,12 @@ int cssm_gated_gates(const float* ctx, int B, int T, int C, int H, int W,
  *   u, z, y   (B, T, C, H, W) plane-major of dtype; u = x_main after the short
  *             convolutions, z = the gate branch; u_act / z_act select SiLU on
  *             load (the reference applies SiLU to both, cssm.py:502, :581).
- *   gates     (B, T, H, Wf, 4) from cssm_gated_gates with c_scale = 1/(H*W)
- *             (the irfft2 normalisation folded into C); dense and factored
- *             gate_type both arrive in this per-bin form.
- *   khat      from cssm_spectral_kernel with goom_floor = 1, C channels
+ *   gates     (B, T, H, Wf, 4) from cssm_gated_gates with c_scale = 1/(2 H W)
+ *             (the irfft2 normalisation and the 1/2 of the doubled spectrum
+ *             folded into C); dense and factored gate_type both arrive in this
+ *             per-bin form, columns in the order of cssm_gated_scan_col_order.
+ *   khat      from cssm_spectral_kernel with goom_floor = 1 and scan_order = 1,
+ *             C channels
  * Supported planes: H = W in {4, 8, 16, 32, 64, 128} (in-register FFT passes
  * through LDS; C a multiple of cssm_gated_scan_min_group(H, W)) and any
  * H = W in 3..15 (direct DFTs, any C) -- the CSSM-SHViT stage shapes 14 x 14
@@ -360,6 +368,16 @@ int cssm_gated_scan_supported(int H, int W);
 
 /* Channel-count granule of the fused scan for (H, W): C must be a multiple (0 = unsupported). */
 int cssm_gated_scan_min_group(int H, int W);
+
+/*
+ * Column order of the per-bin planes cssm_gated_scan_fwd reads (gates, khat):
+ * cols[p] (p < W/2 + 1) = the frequency column stored at position p of a row.
+ * The identity except at 128 x 128, where the 64 packed columns are
+ * interleaved (each wave's column passes then spread over the LDS banks while
+ * its per-bin loads still cover whole cache lines); the Nyquist column stays
+ * last.  No counterpart in the reference (the layout is this library's own).
+ */
+int cssm_gated_scan_col_order(int H, int W, int* cols);
 
 #ifdef __cplusplus
 }
