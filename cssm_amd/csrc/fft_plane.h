@@ -19,6 +19,8 @@
 #include <hip/hip_runtime.h>
 #include <stdint.h>
 
+#include <type_traits>
+
 #include "fft_reg.h"
 #include "launch.h"
 
@@ -559,6 +561,10 @@ struct PlaneFft {
   // ---------------- I1 for the packed column: inverse DFT-H2, conj twiddle
   __device__ __forceinline__ void i1_packed(int w, int l) const {
     if (!G::owns_edge(w)) return;
+    if constexpr (H2 == 8) {
+      i1_packed_quads(w, l);
+      return;
+    }
 #pragma unroll
     for (int j = 0; j < G::JI1; ++j) {
       const int q = j * 64 + l;
@@ -580,6 +586,59 @@ struct PlaneFft {
           cplx(G::row_off(pl, s + H2 * kA) + col) = s ? cmul(sa[s], twI1[kA * G::TI1 + s]) : sa[0];
           cplx(G::row_off(pl, s + H2 * kB) + col) = s ? cmul(sb[s], twI1[kB * G::TI1 + s]) : sb[0];
         }
+      }
+    }
+    wave_sync();
+  }
+
+  // I1 of the packed column for H2 = 8 on four lanes per unit k, so a wave
+  // runs 16 units at once instead of one pair of units per lane.  Lane c of a
+  // quad takes q = c and c + 4 of X[k + H1 q]: a radix-2 step gives
+  // a_c = x_c + x_{c+4} (even outputs) and b_c = (x_c - x_{c+4}) e^{2 pi i c / 8}
+  // (odd outputs); the two inverse 4-point DFTs over c run across the quad
+  // (pairs c ^ 2, then c ^ 1, exchanged by DPP), after which lane c holds
+  // outputs s = 2 m and 2 m + 1 with m the 2-bit reversal of c.
+  __device__ __forceinline__ void i1_packed_quads(int w, int l) const {
+    static_assert(H2 == 8, "quad I1 needs H2 = 8");
+    constexpr int NJ = G::PPWE * H1 * 4, J = (NJ + 63) / 64;
+    constexpr float R = 0.70710678118654752f;
+    // x + sgn * (the value of lane l ^ d in the quad), d = 2 (ctrl 0x4e) or 1 (0xb1)
+    auto xch = [](float2 v, auto ctrl) -> float2 {
+      constexpr int C = decltype(ctrl)::value;
+      return make_float2(__int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(v.x), C, 0xf, 0xf, false)),
+                         __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(v.y), C, 0xf, 0xf, false)));
+    };
+#pragma unroll
+    for (int j = 0; j < J; ++j) {
+      const int q = j * 64 + l;
+      if (NJ % 64 == 0 || q < NJ) {
+        const int c = q & 3, k = (q >> 2) % H1, pl = G::edge_plane0(w) + (q >> 2) / H1;
+        const float2 x0 = edge[pl * H + k + H1 * c], x1 = edge[pl * H + k + H1 * (c + 4)];
+        float2 a = cadd(x0, x1), b = csub(x0, x1);
+        {  // b *= e^{2 pi i c / 8}
+          const float cs = c == 0 ? 1.0f : (c == 1 ? R : (c == 2 ? 0.0f : -R));
+          const float sn = c == 0 ? 0.0f : (c == 2 ? 1.0f : R);
+          b = make_float2(b.x * cs - b.y * sn, b.x * sn + b.y * cs);
+        }
+        // stage over c ^ 2: c < 2 keeps v_c + v_{c+2}; c >= 2 takes (v_{c-2} - v_c) e^{2 pi i (c-2) / 4}
+        const float sA = c < 2 ? 1.0f : -1.0f;
+        float2 pa = xch(a, std::integral_constant<int, 0x4e>()), pb = xch(b, std::integral_constant<int, 0x4e>());
+        a = make_float2(fmaf(sA, a.x, pa.x), fmaf(sA, a.y, pa.y));
+        b = make_float2(fmaf(sA, b.x, pb.x), fmaf(sA, b.y, pb.y));
+        if (c == 3) {   // x i
+          a = make_float2(-a.y, a.x);
+          b = make_float2(-b.y, b.x);
+        }
+        // stage over c ^ 1: even c keeps v_c + v_{c+1}, odd c takes v_{c-1} - v_c
+        const float sB = (c & 1) ? -1.0f : 1.0f;
+        pa = xch(a, std::integral_constant<int, 0xb1>());
+        pb = xch(b, std::integral_constant<int, 0xb1>());
+        a = make_float2(fmaf(sB, a.x, pa.x), fmaf(sB, a.y, pa.y));
+        b = make_float2(fmaf(sB, b.x, pb.x), fmaf(sB, b.y, pb.y));
+        const int s0 = 2 * (((c & 1) << 1) | (c >> 1));
+        const int col = G::p_col(0);
+        cplx(G::row_off(pl, s0 + H2 * k) + col) = s0 ? cmul(a, twI1[k * G::TI1 + s0]) : a;
+        cplx(G::row_off(pl, s0 + 1 + H2 * k) + col) = cmul(b, twI1[k * G::TI1 + s0 + 1]);
       }
     }
     wave_sync();
