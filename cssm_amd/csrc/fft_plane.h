@@ -310,7 +310,9 @@ __device__ __forceinline__ void wave_sync() {
 //        planes (v = scan_col(n) under SO, else n); on entry the forward value
 //        (when FWD), on exit the inverse input (when INV).  (j, a2) name the
 //        thread's unit slot, fixed for the whole launch, so per-bin state can
-//        live in registers.
+//        live in registers.  Op::kPackedColumnToo: also call it for the packed
+//        DC / Nyquist column (v = 0; the values are discarded), which saves the
+//        divergent branch where the op's side effects allow it.
 //   op.edge(j, pl, uA, uB, e, v4) the DC / Nyquist bins of rows uA and uB
 //        (uB = -uA mod H; e = uA): v4 = {(uA, 0), (uA, W/2), (uB, 0), (uB, W/2)};
 //        forward value on entry (FWD), inverse input on exit (INV).
@@ -493,7 +495,21 @@ struct PlaneFft {
           for (int s = 0; s < H2; ++s) sp[s] = cplx(G::row_off(pl, s + H2 * k) + col);
           Dft<H2, false>::run(sp);
         }
-        if (v == 0) {
+        if constexpr (Op::kPackedColumnToo) {
+          // the packed column's lanes run the per-bin work as well (no divergent
+          // branch); what they write back is replaced by i1_packed
+          if (FWD && v == 0) {
+#pragma unroll
+            for (int q = 0; q < H2; ++q) edge[pl * H + k + H1 * q] = sp[q];
+          }
+          op.bins(j, a2, pl, k, n, sp);
+          if (INV) {
+            Dft<H2, true>::run(sp);
+#pragma unroll
+            for (int s = 0; s < H2; ++s)
+              cplx(G::row_off(pl, s + H2 * k) + col) = s ? cmul(sp[s], twI1[k * G::TI1 + s]) : sp[0];
+          }
+        } else if (v == 0) {
           if (FWD) {
 #pragma unroll
             for (int q = 0; q < H2; ++q) edge[pl * H + k + H1 * q] = sp[q];

@@ -62,6 +62,9 @@ struct ScanArgs {
 template <class G>
 struct GatedScanOp {
   static constexpr int H = G::H, WH = G::WH, WF = G::WF, H1 = G::H1, H2 = G::H2;
+  // the packed column's lanes may run bins(): their state slots serve no
+  // other bin and their results are overwritten by the packed-column I1
+  static constexpr bool kPackedColumnToo = true;
   float2 (&h)[G::JC2][2][G::H2];
   float2* hE;   // LDS: state of the DC / Nyquist bins, 4 per edge job (pl, e)
   Buf gbuf;   // gates of (b, t): (H, WF) float4

@@ -56,6 +56,7 @@ __device__ __forceinline__ float2 goom_floor2(float2 z) {
 // and pl H/2 + e, summed per plane in a fixed order afterwards.
 template <class G>
 struct SpecStoreOp {
+  static constexpr bool kPackedColumnToo = false;   // bins() writes HBM: only real columns
   static constexpr int H = G::H, WH = G::WH, WF = G::WF, H1 = G::H1, H2 = G::H2, HP = G::HP;
   float2* out;      // (NP, H, WF) of this workgroup
   float* part_c2;   // LDS (NC2) or nullptr: partial sums of the C2 jobs
@@ -97,6 +98,7 @@ struct SpecStoreOp {
 // inverse policy: bins <- HBM spectrum / (H W)
 template <class G>
 struct SpecLoadOp {
+  static constexpr bool kPackedColumnToo = false;   // bins() writes HBM: only real columns
   static constexpr int H = G::H, WH = G::WH, WF = G::WF, H1 = G::H1, H2 = G::H2;
   const float2* in;   // (NP, H, WF) of this workgroup
   float scale;        // 1 / (H W)
