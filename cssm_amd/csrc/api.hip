@@ -417,3 +417,52 @@ int cssm_gdn_proj_out(const void* o, const void* gate, int in_dtype, int F, int 
 }
 
 }  // extern "C"
+
+// ---------------------------------------------------------------- CSSMSHViTBlock wiring
+
+int cssm_block_norm_stats(const void* x, int dtype, int B, int T, int H, int W, int C, int mode, float eps,
+                          float* stats, void* stream) {
+  if (!x || !stats) return fail(CSSM_ERR_NULL, "cssm_block_norm_stats: x and stats must be non-null");
+  if (B <= 0 || T <= 0 || H <= 0 || W <= 0 || C <= 0)
+    return fail(CSSM_ERR_SHAPE, "cssm_block_norm_stats: B=%d T=%d H=%d W=%d C=%d", B, T, H, W, C);
+  if (!dtype_ok(dtype)) return fail(CSSM_ERR_ARG, "cssm_block_norm_stats: dtype=%d", dtype);
+  if (mode < 0 || mode > 2) return fail(CSSM_ERR_ARG, "cssm_block_norm_stats: mode=%d", mode);
+  if (!(eps >= 0.0f)) return fail(CSSM_ERR_ARG, "cssm_block_norm_stats: eps must be >= 0");
+  if (!aligned(stats, 8)) return fail(CSSM_ERR_ALIGN, "cssm_block_norm_stats: stats must be 8-byte aligned");
+  return hip_status(cssm::launch_block_norm_stats(x, dtype, B, T, H, W, C, mode, eps, stats,
+                                                  static_cast<hipStream_t>(stream)),
+                    "cssm_block_norm_stats");
+}
+
+int cssm_block_norm_posconv(const void* x, int dtype, int B, int T_in, int T_out, int H, int W, int C, int mode,
+                            const float* stats, const float* scale, const float* bias, const float* pos_kernel,
+                            const float* pos_bias, void* out, void* stream) {
+  if (!x || !stats || !scale || !bias || !out)
+    return fail(CSSM_ERR_NULL, "cssm_block_norm_posconv: x, stats, scale, bias and out must be non-null");
+  if ((pos_kernel == nullptr) != (pos_bias == nullptr))
+    return fail(CSSM_ERR_NULL, "cssm_block_norm_posconv: pos_kernel and pos_bias come together");
+  if (B <= 0 || T_in <= 0 || T_out <= 0 || H <= 0 || W <= 0 || C <= 0 || (T_in != 1 && T_in != T_out))
+    return fail(CSSM_ERR_SHAPE, "cssm_block_norm_posconv: B=%d T_in=%d T_out=%d H=%d W=%d C=%d", B, T_in, T_out, H,
+                W, C);
+  if (!dtype_ok(dtype)) return fail(CSSM_ERR_ARG, "cssm_block_norm_posconv: dtype=%d", dtype);
+  if (mode < 0 || mode > 2) return fail(CSSM_ERR_ARG, "cssm_block_norm_posconv: mode=%d", mode);
+  if (x == out) return fail(CSSM_ERR_ARG, "cssm_block_norm_posconv: out must not alias x");
+  if (!aligned(stats, 8)) return fail(CSSM_ERR_ALIGN, "cssm_block_norm_posconv: stats must be 8-byte aligned");
+  return hip_status(cssm::launch_block_norm_posconv(x, dtype, B, T_in, T_out, H, W, C, mode, stats, scale, bias,
+                                                    pos_kernel, pos_bias, out, static_cast<hipStream_t>(stream)),
+                    "cssm_block_norm_posconv");
+}
+
+int cssm_block_residual(const void* res, int T_res, const void* y, int T_y, int dtype, int B, int T_out, int H,
+                        int W, int C, int act, void* out, void* stream) {
+  if (!res || !y || !out) return fail(CSSM_ERR_NULL, "cssm_block_residual: res, y and out must be non-null");
+  if (B <= 0 || T_res <= 0 || T_y <= 0 || T_out <= 0 || H <= 0 || W <= 0 || C <= 0 ||
+      (T_out != 1 && (T_res != T_out || T_y != T_out)))
+    return fail(CSSM_ERR_SHAPE, "cssm_block_residual: B=%d T_res=%d T_y=%d T_out=%d H=%d W=%d C=%d", B, T_res, T_y,
+                T_out, H, W, C);
+  if (!dtype_ok(dtype)) return fail(CSSM_ERR_ARG, "cssm_block_residual: dtype=%d", dtype);
+  if (act < 0 || act > 2) return fail(CSSM_ERR_ARG, "cssm_block_residual: act=%d", act);
+  return hip_status(cssm::launch_block_residual(res, T_res, y, T_y, dtype, B, T_out, H, W, C, act, out,
+                                                static_cast<hipStream_t>(stream)),
+                    "cssm_block_residual");
+}

@@ -102,4 +102,15 @@ hipError_t launch_gdn_qkv_proj(const void* X, int in_dtype, int B, int T, int HW
                                void* out, int out_dtype, hipStream_t s);
 bool gdn_qkv_fused_supported(int T, int HW, int K, int kt);
 
+// ---- CSSMSHViTBlock wiring (block.hip)
+// norm1 statistics: mode 0 global_layer (per b), 1 temporal_layer (per b, pixel), 2 layer (per b, t, pixel);
+// stats (groups, 2) = (mean, rsqrt(var + eps))
+hipError_t launch_block_norm_stats(const void* x, int dtype, int B, int T, int H, int W, int C, int mode, float eps,
+                                   float* stats, hipStream_t s);
+hipError_t launch_block_norm_posconv(const void* x, int dtype, int B, int T_in, int T_out, int H, int W, int C,
+                                     int mode, const float* stats, const float* scale, const float* bias,
+                                     const float* pk, const float* pb, void* out, hipStream_t s);
+hipError_t launch_block_residual(const void* res, int T_res, const void* y, int T_y, int dtype, int B, int T_out,
+                                 int H, int W, int C, int act, void* out, hipStream_t s);
+
 }  // namespace cssm

@@ -471,3 +471,61 @@ def gdn_proj_out(o: torch.Tensor, gate: torch.Tensor, norm: str, norm_scale: Opt
     _lib.call("cssm_gdn_proj_out", o.data_ptr(), gate.data_ptr(), _DTYPES[o.dtype], F, hw, K, N, _NORMS[norm], ns, nb,
               kernel.data_ptr(), bias.data_ptr(), out.data_ptr(), _DTYPES[od], _stream())
     return out
+
+
+# --------------------------------------------------------- CSSMSHViTBlock wiring
+
+BLOCK_NORMS = {"global_layer": 0, "temporal_layer": 1, "layer": 2}
+OUTPUT_ACTS = {"none": 0, "gelu": 1, "silu": 2}
+
+
+def block_norm_stats(x: torch.Tensor, block_norm: str, eps: float = 1e-6) -> torch.Tensor:
+    """norm1 statistics (mean, rstd) per group of channels-last (B, T, H, W, C) x
+    (cssm_shvit.py:106-114): one group per b ('global_layer'), per (b, h, w)
+    ('temporal_layer') or per (b, t, h, w) ('layer')."""
+    _dev(x, "x")
+    if x.dtype not in _DTYPES:
+        raise ValueError(f"unsupported dtype {x.dtype}")
+    B, T, H, W, C = x.shape
+    mode = BLOCK_NORMS[block_norm]
+    groups = B if mode == 0 else (B * H * W if mode == 1 else B * T * H * W)
+    stats = torch.empty((groups, 2), dtype=torch.float32, device=x.device)
+    _lib.call("cssm_block_norm_stats", x.data_ptr(), _DTYPES[x.dtype], B, T, H, W, C, mode, float(eps),
+              stats.data_ptr(), _stream())
+    return stats
+
+
+def block_norm_posconv(x: torch.Tensor, stats: torch.Tensor, block_norm: str, scale: torch.Tensor,
+                       bias: torch.Tensor, pos_kernel: Optional[torch.Tensor], pos_bias: Optional[torch.Tensor],
+                       T_out: int) -> torch.Tensor:
+    """(B, T_out, H, W, C) = norm1(x) + pos_conv(norm1(x)) (cssm_shvit.py:104-145);
+    x with T = T_out frames or one image frame repeated to T_out."""
+    _dev(x, "x")
+    B, T_in, H, W, C = x.shape
+    _dev(stats, "stats", torch.float32)
+    _dev(scale, "scale", torch.float32)
+    _dev(bias, "bias", torch.float32)
+    pk = pb = 0
+    if pos_kernel is not None:
+        if tuple(pos_kernel.shape) != (3, 3, 1, C):
+            raise ValueError(f"pos_conv kernel shape {tuple(pos_kernel.shape)} != {(3, 3, 1, C)}")
+        pk = _dev(pos_kernel, "pos_kernel", torch.float32).data_ptr()
+        pb = _dev(pos_bias, "pos_bias", torch.float32).data_ptr()
+    out = torch.empty((B, T_out, H, W, C), dtype=x.dtype, device=x.device)
+    _lib.call("cssm_block_norm_posconv", x.data_ptr(), _DTYPES[x.dtype], B, T_in, T_out, H, W, C,
+              BLOCK_NORMS[block_norm], stats.data_ptr(), scale.data_ptr(), bias.data_ptr(), pk or None, pb or None,
+              out.data_ptr(), _stream())
+    return out
+
+
+def block_residual(res: torch.Tensor, y: torch.Tensor, T_out: int, output_act: str = "none") -> torch.Tensor:
+    """res + act(y) (cssm_shvit.py:211-228): the last frame of each when T_out = 1,
+    frame by frame otherwise; (B, T_out, H, W, C)."""
+    _dev(res, "res")
+    _dev(y, "y", res.dtype)
+    B, T_res, H, W, C = res.shape
+    T_y = y.shape[1]
+    out = torch.empty((B, T_out, H, W, C), dtype=res.dtype, device=res.device)
+    _lib.call("cssm_block_residual", res.data_ptr(), T_res, y.data_ptr(), T_y, _DTYPES[res.dtype], B, T_out, H, W,
+              C, OUTPUT_ACTS[output_act], out.data_ptr(), _stream())
+    return out

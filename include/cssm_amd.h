@@ -379,6 +379,41 @@ int cssm_gated_scan_min_group(int H, int W);
  */
 int cssm_gated_scan_col_order(int H, int W, int* cols);
 
+/*
+ * CSSMSHViTBlock wiring around the cell, the token-mixer half of the block
+ * (cssm_shvit.py:86-229): norm1 -> pos_conv -> cell -> frame selection ->
+ * output activation -> residual.  Tensors are channels-last (B, T, H, W, C) of
+ * dtype (CSSM_F32 / CSSM_BF16); an image is T = 1.
+ *
+ * norm1 statistics (flax LayerNorm, epsilon eps, variance E[x^2] - E[x]^2,
+ * sums in double).  mode 0 global_layer: one group per b over T, H, W, C
+ * (:106-108); 1 temporal_layer: per (b, h, w) over T, C (:109-111); 2 layer: per
+ * (b, t, h, w) over C (:112-114).  stats (groups, 2) float32 = (mean, rstd).
+ */
+int cssm_block_norm_stats(const void* x, int dtype, int B, int T, int H, int W, int C, int mode, float eps,
+                          float* stats, void* stream);
+
+/*
+ * out (B, T_out, H, W, C) = xn + pos_conv(xn), xn = (x - mean) rstd scale + bias
+ * per norm1 group (stats from cssm_block_norm_stats with the same mode),
+ * pos_conv = the depthwise 3 x 3 'SAME' convolution with bias
+ * (cssm_shvit.py:122-145; kernel (3, 3, 1, C) HWIO, zero padding of xn).
+ * pos_kernel = pos_bias = NULL: out = xn (use_pos_conv = False).  T_in = T_out,
+ * or T_in = 1 with the image repeated to T_out frames (:99-101).
+ */
+int cssm_block_norm_posconv(const void* x, int dtype, int B, int T_in, int T_out, int H, int W, int C, int mode,
+                            const float* stats, const float* scale, const float* bias, const float* pos_kernel,
+                            const float* pos_bias, void* out, void* stream);
+
+/*
+ * out = res + act(y) (cssm_shvit.py:211-228): T_out = 1 takes the last frame
+ * of res (T_res frames) and of y (T_y frames), T_out > 1 frame by frame
+ * (keep_time; T_res = T_y = T_out).  act 0 none, 1 gelu (tanh form, as
+ * jax.nn.gelu), 2 silu (output_act).  out (B, T_out, H, W, C).
+ */
+int cssm_block_residual(const void* res, int T_res, const void* y, int T_y, int dtype, int B, int T_out, int H,
+                        int W, int C, int act, void* out, void* stream);
+
 #ifdef __cplusplus
 }
 #endif

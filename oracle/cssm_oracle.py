@@ -613,6 +613,55 @@ def gdn_forward(params, x, cfg: GDNConfig, scan='linear', return_intermediates=F
     return res
 
 
+# ---------------------------------------------------------------------------
+# CSSMSHViTBlock wiring (cssm_shvit.py:86-229), the token-mixer half
+# ---------------------------------------------------------------------------
+
+BLOCK_NORM_AXES = {'global_layer': (1, 2, 3, 4), 'temporal_layer': (1, 4), 'layer': (4,)}
+
+
+def block_norm1(x5, scale, bias, block_norm='global_layer', eps=1e-6):
+    """norm1 of CSSMSHViTBlock (cssm_shvit.py:104-114): flax LayerNorm with
+    reduction axes (1, 2, 3, 4) ('global_layer'), (1, 4) ('temporal_layer') or
+    the channel axis ('layer', per frame), feature axis -1 (per-channel scale and
+    bias), epsilon 1e-6 and flax's fast variance E[x^2] - E[x]^2."""
+    axes = BLOCK_NORM_AXES[block_norm]
+    mu = np.mean(x5, axis=axes, keepdims=True)
+    var = np.maximum(np.mean(x5 * x5, axis=axes, keepdims=True) - mu * mu, 0.0)
+    return (x5 - mu) / np.sqrt(var + eps) * scale + bias
+
+
+def gelu_tanh(x):
+    """jax.nn.gelu with its default approximate=True (the tanh form)."""
+    return 0.5 * x * (1.0 + np.tanh(math.sqrt(2.0 / math.pi) * (x + 0.044715 * x ** 3)))
+
+
+def shvit_block_mixer(params, x, cell_forward, num_timesteps=8, block_norm='global_layer',
+                      use_pos_conv=True, output_act='none'):
+    """CSSMSHViTBlock.__call__ up to the token-mixer residual (cssm_shvit.py:86-228).
+
+    x (B, H, W, C) image -> repeated to (B, T, H, W, C) (:99-101), or (B, T, H, W, C)
+    video; residual = that 5-D input (:104); norm1 (:106-114); pos_conv: depthwise
+    3 x 3 'SAME' per frame, added (:132-145); the cell (:185) by ``cell_forward(p, x5)``;
+    the last frame for an image, every frame for video (keep_time, :191-213);
+    output_act (:215-218); + the matching residual (:220-228).
+    """
+    is_image = x.ndim == 4
+    x5 = np.repeat(x[:, None], num_timesteps, axis=1) if is_image else x
+    residual = x5
+    h = block_norm1(x5, params['norm1']['scale'], params['norm1']['bias'], block_norm)
+    if use_pos_conv:
+        B, T, H, W, C = h.shape
+        h = h + depthwise_conv2d_same(h.reshape(B * T, H, W, C), params['pos_conv']).reshape(h.shape)
+    y = cell_forward(params['cssm'], h)
+    y = y[:, -1] if is_image else y
+    if output_act == 'gelu':
+        y = gelu_tanh(y)
+    elif output_act == 'silu':
+        y = silu(y)
+    return (residual[:, -1] if is_image else residual) + y
+
+
 def gdn_param_shapes(cfg: GDNConfig, H, W) -> Dict[str, object]:
     """Parameter tree of GatedDeltaNetCSSM's slow path (Flax names)."""
     C = cfg.channels

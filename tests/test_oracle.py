@@ -320,3 +320,84 @@ def test_goom_log_add_exp_is_exact_addition(rng):
     b = rng.standard_normal(50) + 1j * rng.standard_normal(50)
     r = O.from_goom(O.log_add_exp(O.to_goom(a), O.to_goom(b)))
     assert np.allclose(r, a + b, rtol=1e-12, atol=1e-12)
+
+
+# ------------------------------------------------------------ CSSMSHViT block
+
+@pytest.mark.parametrize("mode", ["global_layer", "temporal_layer", "layer"])
+def test_block_norm1_normalises_its_groups(mode, rng):
+    """Within each of the reference's reduction groups norm1 is one affine map
+    x -> (x - mean) / sqrt(var + eps) (unit scale, zero bias); the input's scale
+    and offset vary per pixel and frame, so any other grouping breaks that.  A
+    per-channel scale / bias then maps through channel-wise."""
+    shape = (2, 3, 4, 5, 6)
+    x = (rng.uniform(0.5, 3.0, shape[:4] + (1,)) * rng.standard_normal(shape)
+         + rng.uniform(-2.0, 2.0, shape[:4] + (1,)))
+    y = O.block_norm1(x, np.ones(6), np.zeros(6), mode)
+    axes = O.BLOCK_NORM_AXES[mode]
+    keep = [a for a in range(5) if a not in axes]
+    xg = np.transpose(x, keep + list(axes)).reshape(int(np.prod([shape[a] for a in keep])), -1)
+    yg = np.transpose(y, keep + list(axes)).reshape(xg.shape)
+    for xv, yv in zip(xg, yg):
+        expect = (xv - xv.mean()) / np.sqrt(xv.var() + 1e-6)
+        assert np.max(np.abs(yv - expect)) < 1e-12
+    s, b = rng.standard_normal(6), rng.standard_normal(6)
+    assert np.allclose(O.block_norm1(x, s, b, mode), y * s + b, atol=1e-12)
+    for other in O.BLOCK_NORM_AXES:
+        if other != mode:
+            yo = np.transpose(O.block_norm1(x, np.ones(6), np.zeros(6), other), keep + list(axes)).reshape(xg.shape)
+            assert max(np.max(np.abs(yv - (xv - xv.mean()) / np.sqrt(xv.var() + 1e-6)))
+                       for xv, yv in zip(xg, yo)) > 1e-3
+
+
+def test_block_global_norm_of_a_repeated_image_is_the_image_norm(rng):
+    img = rng.standard_normal((2, 5, 5, 4))
+    x5 = np.repeat(img[:, None], 3, axis=1)
+    y = O.block_norm1(x5, np.ones(4), np.zeros(4), "global_layer")
+    mu = img.mean(axis=(1, 2, 3), keepdims=True)
+    sd = np.sqrt(img.var(axis=(1, 2, 3), keepdims=True) + 1e-6)
+    assert np.allclose(y[:, 1], (img - mu) / sd, atol=1e-12)
+
+
+def test_depthwise_conv_same_is_a_cross_correlation(rng):
+    """An impulse at (h0, w0) lands tap (i, j) at (h0 + 1 - i, w0 + 1 - j): lax's
+    SAME convolution correlates (no kernel flip), per channel, with bias."""
+    k = rng.standard_normal((3, 3, 1, 2))
+    bias = rng.standard_normal(2)
+    x = np.zeros((1, 6, 7, 2))
+    x[0, 3, 2, 1] = 1.0
+    y = O.depthwise_conv2d_same(x, {"kernel": k, "bias": bias})
+    assert np.allclose(y[0, :, :, 0], bias[0])
+    for i in range(3):
+        for j in range(3):
+            assert abs(y[0, 3 + 1 - i, 2 + 1 - j, 1] - (k[i, j, 0, 1] + bias[1])) < 1e-15
+
+
+def test_gelu_tanh_form():
+    x = np.linspace(-6, 6, 101)
+    erf_gelu = np.array([0.5 * v * (1 + math.erf(v / math.sqrt(2))) for v in x])
+    g = O.gelu_tanh(x)
+    assert np.max(np.abs(g - erf_gelu)) < 1e-3 and np.max(np.abs(g - erf_gelu)) > 1e-5   # the tanh form, not erf
+    assert g[50] == 0.0 and abs(g[-1] - 6.0) < 1e-6
+
+
+@pytest.mark.parametrize("image", [True, False])
+def test_shvit_block_wiring_closed_forms(image, rng):
+    """With a cell that returns zeros the block returns its input (last frame for
+    an image); with the identity cell it returns input + norm1 + pos_conv of the
+    last (image) or every (video) frame; the activation acts on the cell output."""
+    B, T, H, W, C = 2, 3, 5, 4, 3
+    x = rng.standard_normal((B, H, W, C) if image else (B, T, H, W, C))
+    p = {"norm1": {"scale": rng.standard_normal(C), "bias": rng.standard_normal(C)},
+         "pos_conv": {"kernel": rng.standard_normal((3, 3, 1, C)), "bias": rng.standard_normal(C)},
+         "cssm": {}}
+    out0 = O.shvit_block_mixer(p, x, lambda q, h: np.zeros_like(h), num_timesteps=T)
+    assert np.array_equal(out0, x)
+    x5 = np.repeat(x[:, None], T, axis=1) if image else x
+    h = O.block_norm1(x5, p["norm1"]["scale"], p["norm1"]["bias"])
+    h = h + O.depthwise_conv2d_same(h.reshape(-1, H, W, C), p["pos_conv"]).reshape(h.shape)
+    outi = O.shvit_block_mixer(p, x, lambda q, hh: hh, num_timesteps=T)
+    assert np.allclose(outi, x + (h[:, -1] if image else h), atol=1e-12)
+    outs = O.shvit_block_mixer(p, x, lambda q, hh: hh, num_timesteps=T, output_act="silu", use_pos_conv=False)
+    hn = O.block_norm1(x5, p["norm1"]["scale"], p["norm1"]["bias"])
+    assert np.allclose(outs, x + O.silu(hn[:, -1] if image else hn), atol=1e-12)
