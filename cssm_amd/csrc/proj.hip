@@ -243,7 +243,9 @@ proj_persist_kernel(const TI* __restrict__ A, int M, int K, int N, const float* 
   // WN waves along the TN = 32 WN columns, WM = 4 / WN along the TM = 128 rows;
   // a wave owns (128 / WM) rows x 32 columns = MI x 2 MFMA tiles
   constexpr int TM = 128, TN = 32 * WN, NT = 256, WM = 4 / WN, MI = TM / WM / 16;
-  static_assert(!OUT_SPLIT || WM == 1, "channel sums of proj_in need whole row tiles per wave");
+  // plane-major outputs with WM > 1 (narrow N) come without channel sums (partial == nullptr, host-checked):
+  // the sums need whole row tiles per wave
+  static_assert(!OUT_SPLIT || WM == 1 || TT == 0, "the qkv epilogue needs whole row tiles per wave");
   static_assert(!NORM || (PLANE_A && !OUT_SPLIT), "the norm / gate prologue is for plane-major A");
   static_assert(!(NORM && SPLIT), "the norm / gate prologue runs on the fp32 path");
   static_assert(!SPLIT || KMAX % 32 == 0, "bf16 MFMA k-blocks of 32");
@@ -646,7 +648,7 @@ proj_persist_kernel(const TI* __restrict__ A, int M, int K, int N, const float* 
             }
           }
         }
-        if (partial != nullptr && lo) {
+        if (WM == 1 && partial != nullptr && lo) {
           csum += __shfl_xor(csum, 16, 64);
           csum += __shfl_xor(csum, 32, 64);
           if (lane < 16 && nok) partial[size_t(tile) * NH + c] = csum;
@@ -972,8 +974,9 @@ static void launch_persist(const void* A, int M, int K, int N, const float* W, c
                            hipStream_t s) {
   const int tiles = (M + kPersistTM - 1) / kPersistTM;
   // narrow outputs (N <= 64) split the rows between wave pairs instead of idling half the waves
-  if constexpr (!OUT_SPLIT) {
-    if (N <= 64) {
+  // (plane-major outputs only without the channel sums, which need whole row tiles per wave)
+  {
+    if (N <= 64 && (!OUT_SPLIT || partial == nullptr)) {
       const dim3 grid(unsigned(persistent_grid(tiles)), unsigned((N + 63) / 64));
       hipLaunchKernelGGL((proj_persist_kernel<KMAX, PLANE_A, OUT_SPLIT, 2, TI, TO, NORM, SPLIT>), grid, dim3(256), 0, s,
                          static_cast<const TI*>(A), M, K, N, W, b, HW, static_cast<TO*>(lo), static_cast<TO*>(hi),
@@ -991,11 +994,16 @@ template <bool PLANE_A, bool OUT_SPLIT, bool NORM, class TI, class TO>
 static bool try_persist(const void* A, int M, int K, int N, const float* W, const float* b, int HW, void* lo,
                         void* hi, int act_lo, int act_hi, float* partial, int NH, const NormGate& ng, hipStream_t s) {
   if (K % 4 != 0 || K > 128) return false;
-  if (K <= 64)
+  if (K <= 64) {
     launch_persist<64, PLANE_A, OUT_SPLIT, NORM, TI, TO>(A, M, K, N, W, b, HW, lo, hi, act_lo, act_hi, partial, NH, ng, s);
-  else
+    return true;
+  }
+  // 64 < K <= 128 only for the norm / gate prologue (the other projections take the K-chunked kernel there)
+  if constexpr (NORM) {
     launch_persist<128, PLANE_A, OUT_SPLIT, NORM, TI, TO>(A, M, K, N, W, b, HW, lo, hi, act_lo, act_hi, partial, NH, ng, s);
-  return true;
+    return true;
+  }
+  return false;
 }
 
 // plane-major output(s) from channels-last X: channels [0, NH) -> lo, [NH, N) -> hi
