@@ -244,62 +244,133 @@ gated_scan_pow2(const ScanArgs a) {
 
 // ---------------------------------------------------------------------------
 // Small planes of any size up to 16 x 16 (the CSSM-SHViT stage shapes 14 x 14
-// and 7 x 7 are not powers of two): direct DFTs through LDS.
+// and 7 x 7 are not powers of two): direct DFTs with compile-time twiddles.
 //
 // A workgroup owns NP consecutive planes of the flattened (b, c) index (the
 // last group may be partial; a group may span two batch elements) for all T
 // steps.  Per step:
-//   rows   R[pl][h][v] = sum_w x[h][w] e^{-2 pi i v w / W}            (v < Wf)
-//   cols   X[pl][u][v] = sum_h R[h][v] e^{-2 pi i u h / H}   (each thread owns
-//          fixed bins, so the state h of its bins stays in registers)
+//   rows   R[pl][h][v] = sum_w x[h][w] e^{-2 pi i v w / W}   (v < Wf; one thread
+//          per row computes all Wf bins, the row read once from LDS)
+//   cols   X[pl][u][v] = sum_h R[h][v] e^{-2 pi i u h / H}   (one thread per
+//          column (pl, v), fixed for the launch, so the state of its H bins
+//          stays in registers)
 //   scan   h = floor(K_hat) e^{-Delta} h + (Delta + 1e-8) floor(X B);  S = C h / (H W)
 //          (evaluated on 2X and 2h with the gate planes' doubled floor term and C / (2 H W))
 //   icols  Z[pl][h][v] = sum_u S[u][v] e^{+2 pi i u h / H}
 //   C2R    y[h][w] = Re Z[h][0] + 2 sum_{0 < v < W/2} Re(Z[h][v] e^{2 pi i v w / W})
 //                    + [W even] (-1)^w Re Z[h][W/2]                 (numpy irfft2)
 //   store  y * z_gate
-// Twiddles come from double-precision tables in LDS.
+// Every DFT unrolls over both indices with the twiddles as immediates (exact
+// to float from a double-precision series); the trivial ones (1, -1, +-i)
+// fold into adds and swaps.
 // ---------------------------------------------------------------------------
-constexpr int cx_gcd(int a, int b) { return b == 0 ? a : cx_gcd(b, a % b); }
-
 template <int H, int W>
 struct SmallGeom {
-  static constexpr int WF = W / 2 + 1, HW = H * W, NT = 256;
-  // the smallest group with whole bins per thread, at most 64 planes (LDS)
-  static constexpr int NP0 = NT / cx_gcd(NT, H * WF);
-  static constexpr int NP = NP0 < 64 ? NP0 : 64;
-  static constexpr int NB = NP * H * WF, JB = (NB + NT - 1) / NT;   // bins per group / per thread
-  static constexpr int NX = NP * HW;                                // samples per group
-  static_assert(NX * 4 + 2 * NB * 8 + (WF * W + H * H) * 8 + NP * 12 <= 160 * 1024, "small-plane group exceeds LDS");
+  // 128-thread groups from 8 x 8 up: more, smaller groups per CU overlap one
+  // group's loads and stores with another's DFTs (one step per group at T = 1)
+  static constexpr int WF = W / 2 + 1, HW = H * W, NT = WF >= 5 ? 128 : 256;
+  static constexpr int NP = NT / WF;               // planes per group: one column per thread
+  static constexpr int NCJ = NP * WF, NRJ = NP * H; // column / row jobs per group
+  // spectra in LDS at pl PS + h RSP + v (complex units): an odd row stride
+  // spreads the row passes' lanes (consecutive rows) over the banks, and a
+  // plane stride of WF mod 32 puts the column pass's planes (WF lanes each) on
+  // disjoint bank windows
+  static constexpr int RSP = WF | 1;
+  static constexpr int PS = H * RSP + ((WF - H * RSP) % 32 + 32) % 32;
+  static_assert(NP * HW * 4 + NP * PS * 8 + NP * 12 <= 64 * 1024, "small-plane group exceeds LDS");
 };
 
+// cos / sin (2 pi J / N) as compile-time constants; mac_c / mac_s add
+// v cos or v sin to acc, skipping zero factors and folding +-1
+template <int N, int J, bool SIN>
+constexpr double trig() {
+  constexpr double x = 2.0 * kPi * double(((J % N) + N) % N) / double(N);
+  return SIN ? cx_sin(x) : cx_cos(x);
+}
+template <int N, int J, bool SIN>
+__device__ __forceinline__ void mac_t(float& acc, float v) {
+  constexpr double d = trig<N, J, SIN>();
+  if constexpr (d > -1e-12 && d < 1e-12) {
+  } else if constexpr (d > 1.0 - 1e-12) {
+    acc += v;
+  } else if constexpr (d < -1.0 + 1e-12) {
+    acc -= v;
+  } else {
+    acc = fmaf(v, float(d), acc);
+  }
+}
+template <int N, int J, bool SIN>
+__device__ __forceinline__ void mac_t(float2& acc, float2 v) {
+  mac_t<N, J, SIN>(acc.x, v.x);
+  mac_t<N, J, SIN>(acc.y, v.y);
+}
+
+// Complex N-point DFT (forward e^{-i}, INV: e^{+i}; any N) by the symmetry of
+// the twiddles: with a_n = x_n + x_{N-n}, b_n = x_n - x_{N-n} (0 < n < N/2),
+//   X[k], X[N-k] = A_k -+ i B_k (forward; +- for INV),
+//   A_k = x_0 [+ (-1)^k x_{N/2}] + sum_n a_n cos(2 pi n k / N),  B_k = sum_n b_n sin(2 pi n k / N)
+// which takes about a quarter of the direct form's multiply-adds.
+template <int N, bool INV>
+__device__ __forceinline__ void dft_sym(const float2 (&x)[N], float2 (&X)[N]) {
+  constexpr int M = (N - 1) / 2;
+  constexpr bool EVEN = (N % 2) == 0;
+  float2 a[M + 1], b[M + 1];
+  static_for<1, M + 1>([&](auto Nn) {
+    constexpr int n = decltype(Nn)::value;
+    a[n] = cadd(x[n], x[N - n]);
+    b[n] = csub(x[n], x[N - n]);
+  });
+  static_for<0, M + 1>([&](auto K) {
+    constexpr int k = decltype(K)::value;
+    float2 A = x[0], B = make_float2(0.f, 0.f);
+    if constexpr (EVEN) {
+      if constexpr (k % 2 == 0) A = cadd(A, x[N / 2]);
+      else A = csub(A, x[N / 2]);
+    }
+    static_for<1, M + 1>([&](auto Nn) {
+      constexpr int n = decltype(Nn)::value;
+      mac_t<N, n * k, false>(A, a[n]);
+      if constexpr (k > 0) mac_t<N, n * k, true>(B, b[n]);
+    });
+    if constexpr (k == 0) {
+      X[0] = A;
+    } else {
+      // -i B (forward) or +i B (inverse) for X[k]; the opposite for X[N - k]
+      const float2 iB = INV ? make_float2(-B.y, B.x) : make_float2(B.y, -B.x);
+      X[k] = cadd(A, iB);
+      X[N - k] = csub(A, iB);
+    }
+  });
+  if constexpr (EVEN) {
+    float2 A = x[0];
+    if constexpr ((N / 2) % 2 == 0) A = cadd(A, x[N / 2]);
+    else A = csub(A, x[N / 2]);
+    static_for<1, M + 1>([&](auto Nn) {
+      constexpr int n = decltype(Nn)::value;
+      if constexpr (n % 2 == 0) A = cadd(A, a[n]);
+      else A = csub(A, a[n]);
+    });
+    X[N / 2] = A;
+  }
+}
+
 template <int H, int W, class IO>
-__global__ void __launch_bounds__(256) gated_scan_small(const ScanArgs a, long long P) {
+__global__ void __launch_bounds__((SmallGeom<H, W>::NT), (512 / SmallGeom<H, W>::NT))
+gated_scan_small(const ScanArgs a, long long P) {
   using G = SmallGeom<H, W>;
+  constexpr int WF = G::WF, HW = G::HW, NT = G::NT, NP = G::NP;
+  constexpr int NE = (NP * HW + NT - 1) / NT;   // plane elements per thread
+  constexpr int LB = NE;                         // all of a thread's loads in flight at once
   static_assert(H < 128 && W < 128, "per-bin planes of these sizes are in natural column order");
-  constexpr int WF = G::WF, HW = G::HW, NT = G::NT, NP = G::NP, JB = G::JB;
   using TE = typename IO::T;
-  __shared__ float xs[G::NX];            // input / output planes
-  __shared__ float2 rs[G::NB];           // row spectra, then the inverse column output
-  __shared__ float2 ss[G::NB];           // readout spectra
-  __shared__ float2 twW[WF * W];         // e^{-2 pi i v w / W}
-  __shared__ float2 twH[H * H];          // e^{-2 pi i u h / H}
+  __shared__ float xs[NP * HW];          // u_t, then y_t
+  __shared__ float2 rs[NP * G::PS];      // row spectra, then the inverse column output
   __shared__ long long base_u[NP];       // element offset of plane pl at t = 0: (b T C + c) HW
   __shared__ int gate_b[NP];             // batch index of plane pl (-1: beyond P)
 
   const int T = a.T, C = a.C;
   const int tid = threadIdx.x;
   const long long p0 = (long long)blockIdx.x * NP;
-  for (int i = tid; i < WF * W; i += NT) {
-    double sn, cs;
-    sincospi(2.0 * double((i / W) * (i % W) % W) / double(W), &sn, &cs);
-    twW[i] = make_float2(float(cs), float(-sn));
-  }
-  for (int i = tid; i < H * H; i += NT) {
-    double sn, cs;
-    sincospi(2.0 * double((i / H) * (i % H) % H) / double(H), &sn, &cs);
-    twH[i] = make_float2(float(cs), float(-sn));
-  }
   for (int i = tid; i < NP; i += NT) {
     const long long pp = p0 + i;
     const int b = int(pp / C), c = int(pp % C);
@@ -311,91 +382,160 @@ __global__ void __launch_bounds__(256) gated_scan_small(const ScanArgs a, long l
   TE* __restrict__ yp = static_cast<TE*>(a.y);
   const size_t tstride = size_t(C) * HW;   // one time step
 
-  float2 h[JB];
+  // this thread's column (pl, v) and the state of its H bins
+  const int cpl = tid / WF, cv = tid % WF;
+  const bool has_col = tid < G::NCJ;
+  float2 st[H];
 #pragma unroll
-  for (int j = 0; j < JB; ++j) h[j] = make_float2(0.f, 0.f);
+  for (int u = 0; u < H; ++u) st[u] = make_float2(0.f, 0.f);
   __syncthreads();
+  // all planes of the group in one batch element: one contiguous run per step
+  const bool contig = gate_b[0] >= 0 && gate_b[NP - 1] == gate_b[0];
 
   for (int t = 0; t < T; ++t) {
-    // load u_t (act) into xs
-    for (int e = tid; e < G::NX; e += NT) {
-      const int pl = e / HW, px = e % HW;
-      float v = 0.0f;
-      if (gate_b[pl] >= 0) {
-        v = IO::to_f(up[size_t(base_u[pl]) + t * tstride + px]);
-        if (a.u_act == 1) v = silu_f(v);
+    // the element offsets of the load / store loops are rebuilt every step
+    // (cheap) instead of being hoisted into registers for the whole launch
+    int tl = tid;
+    asm volatile("" : "+v"(tl));
+    // load u_t (act), doubled: the recurrence runs on 2U as in the power-of-two
+    // kernel; the thread's loads go out in batches of LB before they are used.
+    // A group inside one batch element is one contiguous run of planes.
+    const long long base0 = base_u[0] + (long long)t * tstride;
+#pragma unroll
+    for (int k0 = 0; k0 < NE; k0 += LB) {
+      float v[LB];
+#pragma unroll
+      for (int k = 0; k < LB; ++k) {
+        const int e = (k0 + k) * NT + tl;
+        v[k] = 0.0f;
+        if (k0 + k < NE && e < NP * HW) {
+          if (contig) {
+            v[k] = IO::to_f(up[size_t(base0 + e)]);
+          } else {
+            const int pl = e / HW, px = e % HW;
+            if (gate_b[pl] >= 0) v[k] = IO::to_f(up[size_t(base_u[pl]) + t * tstride + px]);
+          }
+        }
       }
-      xs[e] = 2.0f * v;   // the recurrence runs on 2U, as in the power-of-two kernel
+#pragma unroll
+      for (int k = 0; k < LB; ++k) {
+        const int e = (k0 + k) * NT + tl;
+        if (k0 + k < NE && e < NP * HW) xs[e] = 2.0f * (a.u_act == 1 ? silu_f(v[k]) : v[k]);
+      }
     }
     __syncthreads();
-    // rows: R[pl][h][v]
-    for (int o = tid; o < G::NB; o += NT) {
-      const int pl = o / (H * WF), r = o % (H * WF), hh = r / WF, v = r % WF;
-      const float* xr = xs + pl * HW + hh * W;
-      float re = 0.f, im = 0.f;
+    // rows: one thread per (pl, h), all Wf bins
+    for (int j = tid; j < G::NRJ; j += NT) {
+      const float* xr = xs + j * W;          // row h of plane pl: j = pl H + h
+      float x[W];
 #pragma unroll
-      for (int w = 0; w < W; ++w) {
-        const float2 tw = twW[v * W + w];
-        re = fmaf(xr[w], tw.x, re);
-        im = fmaf(xr[w], tw.y, im);
-      }
-      rs[o] = make_float2(re, im);
+      for (int w = 0; w < W; ++w) x[w] = xr[w];
+      float2* rr = rs + (j / H) * G::PS + (j % H) * G::RSP;
+      // real input: R[v] = x_0 [+ (-1)^v x_{W/2}] + sum_w (x_w + x_{W-w}) cos - i (x_w - x_{W-w}) sin
+      constexpr int MW = (W - 1) / 2;
+      float ap[MW + 1], bm[MW + 1];
+      static_for<1, MW + 1>([&](auto Wi) {
+        constexpr int w = decltype(Wi)::value;
+        ap[w] = x[w] + x[W - w];
+        bm[w] = x[w] - x[W - w];
+      });
+      static_for<0, WF>([&](auto V) {
+        constexpr int v = decltype(V)::value;
+        float re = x[0], im = 0.f;
+        if constexpr (W % 2 == 0) re += (v % 2 == 0) ? x[W / 2] : -x[W / 2];
+        static_for<1, MW + 1>([&](auto Wi) {
+          constexpr int w = decltype(Wi)::value;
+          mac_t<W, v * w, false>(re, ap[w]);
+          mac_t<W, v * w, true>(im, bm[w]);
+        });
+        rr[v] = make_float2(re, -im);
+      });
     }
     __syncthreads();
-    // columns + recurrence for the thread's bins (pl, u, v) = j NT + tid
+    // columns: forward DFT over h, the recurrence on the H bins, inverse DFT over u
+    if (has_col) {
+      const int b = gate_b[cpl];
+      float2 r[H];
 #pragma unroll
-    for (int j = 0; j < JB; ++j) {
-      const int o = j * NT + tid;
-      if (JB * NT != G::NB && o >= G::NB) continue;
-      const int pl = o / (H * WF), r = o % (H * WF), u = r / WF, v = r % WF;
-      float2 X = make_float2(0.f, 0.f);
-#pragma unroll
-      for (int hh = 0; hh < H; ++hh) {
-        const float2 R = rs[pl * H * WF + hh * WF + v], tw = twH[u * H + hh];
-        X.x = fmaf(R.x, tw.x, fmaf(-R.y, tw.y, X.x));
-        X.y = fmaf(R.x, tw.y, fmaf(R.y, tw.x, X.y));
-      }
-      float2 Sv = make_float2(0.f, 0.f);
-      const int b = gate_b[pl];
+      for (int h = 0; h < H; ++h) r[h] = rs[cpl * G::PS + h * G::RSP + cv];
+      float2 sv[H];
+      dft_sym<H, false>(r, sv);
       if (b >= 0) {
-        const int c = int((p0 + pl) % C);
-        const float4 g = a.gates[(size_t(b) * T + t) * (H * WF) + r];
-        const float2 kh = a.khat[size_t(c) * (H * WF) + r];
-        Sv = scan_bin(h[j], X, g, kh);
-      }
-      ss[o] = Sv;
-    }
-    __syncthreads();
-    // inverse columns: Z[pl][h][v] = sum_u S[u][v] conj(tw[u h])
-    for (int o = tid; o < G::NB; o += NT) {
-      const int pl = o / (H * WF), r = o % (H * WF), hh = r / WF, v = r % WF;
-      float2 Z = make_float2(0.f, 0.f);
+        const int c = int((p0 + cpl) % C);
+        const float4* gq = a.gates + (size_t(b) * T + t) * (H * WF) + cv;
+        const float2* kq = a.khat + size_t(c) * (H * WF) + cv;
 #pragma unroll
-      for (int u = 0; u < H; ++u) {
-        const float2 Sv = ss[pl * H * WF + u * WF + v], tw = twH[u * H + hh];
-        Z.x = fmaf(Sv.x, tw.x, fmaf(Sv.y, tw.y, Z.x));
-        Z.y = fmaf(Sv.y, tw.x, fmaf(-Sv.x, tw.y, Z.y));
+        for (int u = 0; u < H; ++u) sv[u] = scan_bin(st[u], sv[u], gq[u * WF], kq[u * WF]);
+      } else {
+#pragma unroll
+        for (int u = 0; u < H; ++u) sv[u] = make_float2(0.f, 0.f);
       }
-      rs[o] = Z;
+      dft_sym<H, true>(sv, r);
+#pragma unroll
+      for (int h = 0; h < H; ++h) rs[cpl * G::PS + h * G::RSP + cv] = r[h];
     }
     __syncthreads();
-    // C2R rows, x z_gate, store y_t
-    for (int e = tid; e < G::NX; e += NT) {
-      const int pl = e / HW, px = e % HW, hh = px / W, w = px % W;
-      if (gate_b[pl] < 0) continue;
-      const float2* zr = rs + pl * H * WF + hh * WF;
-      float y = zr[0].x;
+    // C2R rows into xs
+    for (int j = tid; j < G::NRJ; j += NT) {
+      float2 z[WF];
+      const float2* zr = rs + (j / H) * G::PS + (j % H) * G::RSP;
+#pragma unroll
+      for (int v = 0; v < WF; ++v) z[v] = zr[v];
+      float* yr = xs + j * W;
+      // Re(Z_v e^{+2 pi i v w / W}) = Z.x cos - Z.y sin, each bin counted twice but
+      // the Nyquist bin of an even W: with P_w = sum Z.x cos and Q_w = sum Z.y sin
+      // (weights folded in), y[w] = P_w - Q_w and y[W - w] = P_w + Q_w
+      float zx[WF], zy[WF];
+      zx[0] = z[0].x;
+      zy[0] = 0.f;
 #pragma unroll
       for (int v = 1; v < WF; ++v) {
-        // Re(Z e^{+2 pi i v w / W}) = Z.x cos + ... with tw = e^{-...}: Re(Z conj(tw))
-        const float2 tw = twW[v * W + w];
-        const float re = fmaf(zr[v].x, tw.x, zr[v].y * tw.y);
-        y = (W % 2 == 0 && v == W / 2) ? y + re : fmaf(2.0f, re, y);
+        const float c = (W % 2 == 0 && v == W / 2) ? 1.0f : 2.0f;
+        zx[v] = c * z[v].x;
+        zy[v] = c * z[v].y;
       }
-      const size_t gi = size_t(base_u[pl]) + t * tstride + px;
-      float zg = IO::to_f(zp[gi]);
-      if (a.z_act == 1) zg = silu_f(zg);
-      yp[gi] = IO::from_f(y * zg);
+      static_for<0, W / 2 + 1>([&](auto Wi) {
+        constexpr int w = decltype(Wi)::value;
+        float P = zx[0], Q = 0.f;
+        static_for<1, WF>([&](auto V) {
+          constexpr int v = decltype(V)::value;
+          mac_t<W, v * w, false>(P, zx[v]);
+          mac_t<W, v * w, true>(Q, zy[v]);
+        });
+        yr[w] = P - Q;
+        if constexpr (w > 0 && W - w != w) yr[W - w] = P + Q;
+      });
+    }
+    __syncthreads();
+    // x z_gate, store y_t (z loads in batches, as for u)
+#pragma unroll
+    for (int k0 = 0; k0 < NE; k0 += LB) {
+      float zg[LB];
+#pragma unroll
+      for (int k = 0; k < LB; ++k) {
+        const int e = (k0 + k) * NT + tl;
+        zg[k] = 0.0f;
+        if (k0 + k < NE && e < NP * HW) {
+          if (contig) {
+            zg[k] = IO::to_f(zp[size_t(base0 + e)]);
+          } else {
+            const int pl = e / HW, px = e % HW;
+            if (gate_b[pl] >= 0) zg[k] = IO::to_f(zp[size_t(base_u[pl]) + t * tstride + px]);
+          }
+        }
+      }
+#pragma unroll
+      for (int k = 0; k < LB; ++k) {
+        const int e = (k0 + k) * NT + tl;
+        if (k0 + k >= NE || e >= NP * HW) continue;
+        const float g = a.z_act == 1 ? silu_f(zg[k]) : zg[k];
+        if (contig) {
+          yp[size_t(base0 + e)] = IO::from_f(xs[e] * g);
+        } else {
+          const int pl = e / HW, px = e % HW;
+          if (gate_b[pl] >= 0) yp[size_t(base_u[pl]) + t * tstride + px] = IO::from_f(xs[e] * g);
+        }
+      }
     }
     __syncthreads();
   }
