@@ -610,9 +610,7 @@ static hipError_t dispatch_scan(const ScanArgs& a, int B, int H, int W, hipStrea
     CSSM_SCAN_CASE(3, 32, 32)
     return run_small<8, IO>(a, B, s);        // C not a multiple of 32: direct DFTs
   } else if (H == 4 && W == 4) {
-    const int np = pick({128});
-    CSSM_SCAN_CASE(2, 128, 32)
-    return run_small<4, IO>(a, B, s);        // C not a multiple of 128: direct DFTs
+    return run_small<4, IO>(a, B, s);        // direct DFTs beat 128-plane FFT groups here
   }
 #undef CSSM_SCAN_CASE
   return hipErrorInvalidValue;
