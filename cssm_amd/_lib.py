@@ -10,6 +10,7 @@ import os
 import threading
 
 LIB_PATH = os.path.join(os.path.dirname(os.path.abspath(__file__)), "libcssm_hip.so")
+ABI_VERSION = 2   # CSSM_ABI_VERSION of the include/cssm_amd.h these bindings follow
 
 CSSM_OK = 0
 F32, BF16 = 0, 1
@@ -125,6 +126,10 @@ def load() -> ctypes.CDLL:
             if not os.path.exists(LIB_PATH):
                 raise RuntimeError(f"{LIB_PATH} is missing: build it with `python -m cssm_amd.build`")
             lib = ctypes.CDLL(LIB_PATH)
+            got = lib.cssm_abi_version()
+            if got != ABI_VERSION:
+                raise RuntimeError(f"{LIB_PATH} has ABI version {got}, these bindings expect {ABI_VERSION}: "
+                                   "rebuild it with `python -m cssm_amd.build`")
             for name, (res, args) in SIGNATURES.items():
                 fn = getattr(lib, name)
                 fn.restype = res

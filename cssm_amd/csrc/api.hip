@@ -155,9 +155,9 @@ int cssm_gated_scan_fwd(const void* u, const void* z, void* y, int dtype, int B,
 
 size_t cssm_proj_in_workspace_size(int F, int HW, int K, int N) {
   if (F <= 0 || HW <= 0 || K <= 0 || N <= 0) return 0;
-  const int tm = cssm::proj_in_tile_rows(K);
-  if (HW % tm != 0) return 0;
-  return size_t(F) * (HW / tm) * (N / 2) * sizeof(float);
+  const int tm = cssm::proj_in_tile_rows(K), slots = cssm::proj_in_ctx_slots(K, HW);
+  const size_t tiles = (size_t(F) * HW + tm - 1) / tm;
+  return tiles * slots * (N / 2) * sizeof(float);
 }
 
 int cssm_proj_in(const void* x, int in_dtype, int F, int HW, int K, int N, const float* kernel, const float* bias,
@@ -176,8 +176,8 @@ int cssm_proj_in(const void* x, int in_dtype, int F, int HW, int K, int N, const
     return fail(CSSM_ERR_ALIGN, "cssm_proj_in: f32 outputs must be 16-byte aligned");
   const hipStream_t s = static_cast<hipStream_t>(stream);
   const int M = F * HW;
-  const int tm = cssm::proj_in_tile_rows(K);
-  const bool fused_ctx = ctx != nullptr && (HW % tm) == 0;
+  const int tm = cssm::proj_in_tile_rows(K), slots = cssm::proj_in_ctx_slots(K, HW);
+  const bool fused_ctx = ctx != nullptr && slots > 0;
   float* partial = nullptr;
   if (fused_ctx) {
     const size_t need = cssm_proj_in_workspace_size(F, HW, K, N);
@@ -189,7 +189,7 @@ int cssm_proj_in(const void* x, int in_dtype, int F, int HW, int K, int N, const
                                       act_hi, partial, s);
   if (e != hipSuccess) return hip_status(e, "cssm_proj_in");
   if (ctx != nullptr) {
-    e = fused_ctx ? cssm::launch_ctx_reduce(partial, F, HW / tm, N / 2, 1.0f / float(HW), ctx, s)
+    e = fused_ctx ? cssm::launch_ctx_reduce(partial, F, HW, tm, slots, N / 2, ctx, s)
                   : cssm::launch_plane_mean(out_lo, out_dtype, (long long)F * (N / 2), HW, 0, ctx, s);
   }
   return hip_status(e, "cssm_proj_in");

@@ -44,6 +44,7 @@ hipError_t launch_gated_scan(const void* u, const void* z, void* y, int dtype, i
 // projection GEMMs (fp32 MFMA)
 // rows per proj_in tile (the channel partial sums come one per tile)
 int proj_in_tile_rows(int K);
+int proj_in_ctx_slots(int K, int HW);
 hipError_t launch_proj_in(const void* X, int in_dtype, int M, int K, int N, const float* W, const float* b, int HW,
                           void* out_lo, void* out_hi, int out_dtype, int act_lo, int act_hi, float* partial,
                           hipStream_t s);
@@ -57,7 +58,7 @@ hipError_t launch_proj_planes(const void* X, int in_dtype, int M, int K, int N, 
 hipError_t launch_proj_out_norm_gate(const void* Y, const void* G, int in_dtype, int M, int K, int N, int norm,
                                      const float* nscale, const float* nshift, const float* W, const float* b, int HW,
                                      void* out, int out_dtype, hipStream_t s);
-hipError_t launch_ctx_reduce(const float* partial, int F, int tiles_per_frame, int C, float inv_hw, float* ctx,
+hipError_t launch_ctx_reduce(const float* partial, int F, int HW, int tile_rows, int slots, int C, float* ctx,
                              hipStream_t s);
 
 hipError_t launch_short_conv(const void* x, int in_dtype, int B, int T, int C, int H, int W, int ks, const float* ws,

@@ -11,6 +11,8 @@
 #include <hip/hip_runtime.h>
 #include <stdint.h>
 
+#include <type_traits>
+
 #include "launch.h"
 
 namespace cssm {
@@ -45,6 +47,10 @@ __device__ __forceinline__ float act_acc(float x, int act) {
   if (act == 1) return silu_acc(x);
   if (act == 2) return 1.0f / (1.0f + expf(-x));
   return x;
+}
+// buffer resource over [p, p + bytes): raw buffer loads beyond it return 0
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t make_rsrc(const void* p, unsigned bytes) {
+  return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(p), 0, int(bytes), 0x00020000);
 }
 // 4 consecutive elements at a 4-element-aligned index
 __device__ __forceinline__ float4 ld4(const float* p, size_t i) { return *reinterpret_cast<const float4*>(p + i); }
@@ -174,15 +180,20 @@ proj_in_kernel(const TI* __restrict__ X, int M, int K, int N, const float* __res
   }
 }
 
-// ctx[f][c] = sum_t partial[f * tiles_per_frame + t][c] / HW
-__global__ void ctx_reduce_kernel(const float* __restrict__ partial, int F, int tiles_per_frame, int C, float inv_hw,
+// ctx[f][c] = sum over the row tiles t of TM rows that overlap frame f of
+// partial[t][f - first frame of t][c], in tile order, / HW
+__global__ void ctx_reduce_kernel(const float* __restrict__ partial, int F, int HW, int TM, int slots, int C,
                                   float* __restrict__ ctx) {
   const int i = blockIdx.x * blockDim.x + threadIdx.x;
   if (i >= F * C) return;
   const int f = i / C, c = i % C;
+  const long long r0 = (long long)f * HW, r1 = r0 + HW - 1;
   float s = 0.0f;
-  for (int t = 0; t < tiles_per_frame; ++t) s += partial[(size_t(f) * tiles_per_frame + t) * C + c];
-  ctx[i] = s * inv_hw;
+  for (long long t = r0 / TM; t <= r1 / TM; ++t) {
+    const int slot = int(f - (t * TM) / HW);
+    s += partial[(size_t(t) * slots + slot) * C + c];
+  }
+  ctx[i] = s * (1.0f / float(HW));
 }
 
 // ---------------------------------------------------------------------------
@@ -692,12 +703,16 @@ proj_persist_kernel(const TI* __restrict__ A, int M, int K, int N, const float* 
 // operands split into bf16 parts (x = x1 + x2 + x3): fp32 A takes the same six
 // products as the persistent kernel; bf16 A is exactly its first part, so
 // three products (A1 B1 + A1 B2 + A1 B3) give the same fp32-level result.  One
-// 128 x 128 output tile per workgroup; K advances in chunks of 32: the next
-// chunk's A and B are loaded into registers while the MFMAs run on the current
-// one, then split into bf16 planes in LDS, A as [row][k] and B as [column][k]
-// (k contiguous, the MFMA operand order).  Four waves split the 128 columns
-// (32 each) and keep all 128 rows, as in the persistent kernel, so the proj_in
-// channel sums stay in-wave.
+// 128 x 128 output tile per workgroup; four waves split the 128 columns (32
+// each) and keep all 128 rows, as in the persistent kernel, so the proj_in
+// channel sums stay in-wave.  K advances in chunks of 32 with one barrier per
+// chunk and two chunks' loads in flight:
+//   A   global -> registers two chunks ahead, then split into bf16 planes in
+//       one of two LDS stages ([row][k], k contiguous: the MFMA operand order)
+//       while the MFMAs read the other stage;
+//   B   each wave loads its own 32 columns straight into registers (two
+//       chunks ahead) and splits them there: the fragments never pass through
+//       LDS and no other wave reads them.
 //   PLANE_A = false: A is channels-last (M, K), K % 4 == 0; true: plane-major (F, K, HW).
 //   OUT_SPLIT = true: plane-major output(s) as proj_in; false: channels-last (M, N).
 // ---------------------------------------------------------------------------
@@ -705,139 +720,202 @@ template <bool PLANE_A, bool OUT_SPLIT, class TI, class TO>
 __global__ void __launch_bounds__(256, 2)
 proj_kc_kernel(const TI* __restrict__ A, int M, int K, int N, const float* __restrict__ Wt,
                const float* __restrict__ bias, int HW, TO* __restrict__ out_lo, TO* __restrict__ out_hi,
-               int act_lo, int act_hi, float* __restrict__ partial, int NH) {
+               int act_lo, int act_hi, float* __restrict__ partial, int NH, int slots) {
   constexpr int TM = 128, TN = 128, NT = 256, KC = 32, KP = KC + 8, MI = TM / 16;
   constexpr bool A1_ONLY = sizeof(TI) == 2;      // bf16 A: one nonzero part
   constexpr int APL = A1_ONLY ? 1 : 3;           // A planes
   constexpr int OP = TN + 4;                     // channels-last staging pitch (floats), 64 rows at a time
-  constexpr int AB = TM * KP;                    // bf16 per plane (TM == TN)
-  __shared__ __attribute__((aligned(16))) __bf16 lds[(APL + 3) * AB];   // A planes, then B1 B2 B3
-  static_assert(OUT_SPLIT || 64 * OP * 4 <= (APL + 3) * AB * 2, "staging of half an output tile fits the planes");
-  __bf16* const Ap = lds;
-  __bf16* const Bp = lds + APL * AB;
+  constexpr int AB = TM * KP;                    // bf16 per plane
+  constexpr int STG = APL * AB;                  // bf16 per pipeline stage
+  constexpr int LDS_N = (!OUT_SPLIT && 64 * OP * 2 > 2 * STG) ? 64 * OP * 2 : 2 * STG;
+  __shared__ __attribute__((aligned(16))) __bf16 lds[LDS_N];   // two A stages; the output staging reuses them
   const int tid = threadIdx.x, lane = tid & 63, wn = tid >> 6;
-  const int m0 = blockIdx.x * TM, n0 = blockIdx.y * TN;
+  // XCD-aware tile order: workgroup ids go round-robin over the 8 XCDs, so the
+  // tiles are dealt to the XCDs in 8 contiguous runs, column tile fastest: the
+  // column tiles of one row tile run on the same XCD and share its A rows in L2
+  int rt, ct;
+  {
+    const int total = int(gridDim.x), ctiles = (N + TN - 1) / TN;
+    const int x = int(blockIdx.x) % 8, li = int(blockIdx.x) / 8, q = total / 8, r = total % 8;
+    const int t = x * q + (x < r ? x : r) + li;
+    rt = t / ctiles;
+    ct = t % ctiles;
+  }
+  const int m0 = rt * TM, n0 = ct * TN;
   const int NL = N - NH;
 
-  // this thread's loads per chunk: 4 groups i of 4 consecutive k
-  //   A channels-last: rows (tid / 8) + 32 i, k 4 (tid % 8)
-  //   A plane-major and B: row / column tid % 128, k groups 2 i + tid / 128
+  // this thread's A loads per chunk: 4 groups i of 4 consecutive k
+  //   channels-last: rows (tid / 8) + 32 i, k 4 (tid % 8)
+  //   plane-major:   row tid % 128, k groups 2 i + tid / 128
+  // All loads are buffer loads with a per-lane byte offset and a uniform
+  // (SGPR) one, so the unrolled chunk offsets cost no VGPRs across the loop.
   const int rr = tid & 127, kq = tid >> 7;
   const int ar = tid >> 3, ak = (tid & 7) * 4;
-  const TI* a_ptr;
+  constexpr int EA = sizeof(TI);
+  __amdgpu_buffer_rsrc_t ra;   // A rows of this tile
+  unsigned a_off;
   bool a_ok[4];
   if constexpr (!PLANE_A) {
-    a_ptr = A + size_t(m0 + ar) * K + ak;
+    const int rows = M - m0 < TM ? M - m0 : TM;
+    ra = make_rsrc(A + size_t(m0) * K, unsigned(rows) * unsigned(K) * EA);
+    a_off = unsigned(ar * K + ak) * EA;
 #pragma unroll
     for (int i = 0; i < 4; ++i) a_ok[i] = m0 + ar + 32 * i < M;
   } else {
-    const int gm = m0 + rr < M ? m0 + rr : 0;
-    a_ptr = A + (size_t(gm / HW) * K + 4 * kq) * HW + gm % HW;
+    const int last = (M - m0 < TM ? M : m0 + TM) - 1;
+    const int fr0 = m0 / HW, nfr = last / HW - fr0 + 1;
+    ra = make_rsrc(A + size_t(fr0) * K * HW, unsigned(nfr) * unsigned(K) * unsigned(HW) * EA);
+    const int gm = m0 + rr < M ? m0 + rr : m0;
+    a_off = unsigned(((gm / HW - fr0) * K + 4 * kq) * HW + gm % HW) * EA;
 #pragma unroll
     for (int i = 0; i < 4; ++i) a_ok[i] = m0 + rr < M;
   }
-  const bool b_ok = n0 + rr < N;
-  const float* b_ptr = Wt + size_t(4 * kq) * N + (b_ok ? n0 + rr : 0);
-  float4 pa[4], pb[4];
-  auto fetch = [&](int k0) {
+  // this lane's B fragments: columns wn 32 + 16 j + lane % 16, k = chunk + 8 (lane / 16) + e
+  const int kl = (lane >> 4) * 8;
+  const __amdgpu_buffer_rsrc_t rb = make_rsrc(Wt, unsigned(K) * unsigned(N) * 4u);
+  unsigned b_off[2];
+  bool b_ok[2];
+#pragma unroll
+  for (int j = 0; j < 2; ++j) {
+    const int gn = n0 + wn * 32 + j * 16 + (lane & 15);
+    b_ok[j] = gn < N;
+    b_off[j] = unsigned(kl * N + (b_ok[j] ? gn : 0)) * 4u;
+  }
+  // register sets s = 0, 1: chunk j's loads land in set j % 2, its A in LDS stage j % 2.
+  // Raw A: the bf16 bits themselves for channels-last bf16 A (they are the one bf16 part), else floats.
+  constexpr bool RAW16 = A1_ONLY && !PLANE_A;
+  using RawA = typename std::conditional<RAW16, uint2, float4>::type;
+  RawA pa[2][4];
+  float pw[2][2][8];
+  // A lane whose element lies outside the tensor (rows beyond M, k beyond K)
+  // loads at byte offset kOut instead: beyond every resource range, so the
+  // buffer load returns 0 without touching memory.
+  constexpr unsigned kOut = 0x80000000u;
+  auto fetch = [&](int k0, int s) {
     const bool full = k0 + KC <= K;
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
       if constexpr (!PLANE_A) {
-        const bool ok = a_ok[i] && (full || k0 + ak < K);
-        pa[i] = ok ? ld4(a_ptr + size_t(32 * i) * K, k0) : make_float4(0.f, 0.f, 0.f, 0.f);
+        const unsigned vo = (a_ok[i] && (full || k0 + ak < K)) ? a_off : kOut;
+        const int so = (32 * i * K + k0) * EA;
+        if constexpr (RAW16)
+          pa[s][i] = __builtin_bit_cast(uint2, __builtin_amdgcn_raw_buffer_load_b64(ra, int(vo), so, 0));
+        else
+          pa[s][i] = __builtin_bit_cast(float4, __builtin_amdgcn_raw_buffer_load_b128(ra, int(vo), so, 0));
       } else {
         float v[4];
 #pragma unroll
         for (int e = 0; e < 4; ++e) {
           const int k = k0 + 8 * i + e;   // relative to this thread's 4 kq
-          v[e] = (a_ok[i] && (full || k + 4 * kq < K)) ? ld_el(a_ptr, size_t(k) * HW) : 0.0f;
+          const unsigned vo = (a_ok[i] && (full || k + 4 * kq < K)) ? a_off : kOut;
+          const int so = k * HW * EA;
+          if constexpr (EA == 2)
+            v[e] = __uint_as_float(unsigned(__builtin_amdgcn_raw_buffer_load_b16(ra, int(vo), so, 0)) << 16);
+          else
+            v[e] = __uint_as_float(__builtin_amdgcn_raw_buffer_load_b32(ra, int(vo), so, 0));
         }
-        pa[i] = make_float4(v[0], v[1], v[2], v[3]);
+        pa[s][i] = make_float4(v[0], v[1], v[2], v[3]);
       }
-      float w[4];
+    }
 #pragma unroll
-      for (int e = 0; e < 4; ++e) {
-        const int k = k0 + 8 * i + e;
-        w[e] = (b_ok && (full || k + 4 * kq < K)) ? b_ptr[size_t(k) * N] : 0.0f;
-      }
-      pb[i] = make_float4(w[0], w[1], w[2], w[3]);
-    }
-  };
-  auto put = [&](__bf16* planes, int np, int off, float4 v) {
-    const float x[4] = {v.x, v.y, v.z, v.w};
-    bf16x4 v1, v2, v3;
+    for (int j = 0; j < 2; ++j)
 #pragma unroll
-    for (int e = 0; e < 4; ++e) {
-      __bf16 x1, x2, x3;
-      if (np == 1) {
-        x1 = (__bf16)x[e];   // exact for bf16 inputs
-      } else {
-        split3_bf16(x[e], x1, x2, x3);
-        v2[e] = x2;
-        v3[e] = x3;
+      for (int e = 0; e < 8; ++e) {
+        const unsigned vo = (b_ok[j] && (full || k0 + kl + e < K)) ? b_off[j] : kOut;
+        pw[s][j][e] = __uint_as_float(__builtin_amdgcn_raw_buffer_load_b32(rb, int(vo), (k0 + e) * N * 4, 0));
       }
-      v1[e] = x1;
-    }
-    *reinterpret_cast<bf16x4*>(planes + off) = v1;
-    if (np == 3) {
-      *reinterpret_cast<bf16x4*>(planes + AB + off) = v2;
-      *reinterpret_cast<bf16x4*>(planes + 2 * AB + off) = v3;
-    }
   };
-  auto stash = [&]() {
+  // A of register set s -> the bf16 planes of LDS stage s
+  auto stash = [&](int s) {
+    __bf16* const planes = lds + s * STG;
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
-      put(Ap, APL, PLANE_A ? rr * KP + (2 * i + kq) * 4 : (ar + 32 * i) * KP + ak, pa[i]);
-      put(Bp, 3, rr * KP + (2 * i + kq) * 4, pb[i]);
+      const int off = PLANE_A ? rr * KP + (2 * i + kq) * 4 : (ar + 32 * i) * KP + ak;
+      if constexpr (RAW16) {
+        *reinterpret_cast<uint2*>(planes + off) = pa[s][i];
+      } else {
+        const float4 p = pa[s][i];
+        const float x[4] = {p.x, p.y, p.z, p.w};
+        bf16x4 v1, v2, v3;
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+          __bf16 x1, x2 = __bf16(0.0f), x3 = __bf16(0.0f);
+          if constexpr (A1_ONLY) x1 = (__bf16)x[e];   // exact for bf16 inputs
+          else split3_bf16(x[e], x1, x2, x3);
+          v1[e] = x1;
+          v2[e] = x2;
+          v3[e] = x3;
+        }
+        *reinterpret_cast<bf16x4*>(planes + off) = v1;
+        if constexpr (!A1_ONLY) {
+          *reinterpret_cast<bf16x4*>(planes + AB + off) = v2;
+          *reinterpret_cast<bf16x4*>(planes + 2 * AB + off) = v3;
+        }
+      }
     }
+  };
+  bf16x8 b1[2], b2[2], b3[2];
+  auto split_b = [&](int s) {
+#pragma unroll
+    for (int j = 0; j < 2; ++j)
+#pragma unroll
+      for (int e = 0; e < 8; ++e) {
+        __bf16 x1, x2, x3;
+        split3_bf16(pw[s][j][e], x1, x2, x3);
+        b1[j][e] = x1;
+        b2[j][e] = x2;
+        b3[j][e] = x3;
+      }
   };
 
   floatx4 acc[MI][2];
 #pragma unroll
   for (int i = 0; i < MI; ++i) acc[i][0] = acc[i][1] = floatx4{0.f, 0.f, 0.f, 0.f};
-  fetch(0);
-  for (int k0 = 0; k0 < K; k0 += KC) {
-    __syncthreads();   // the previous chunk's MFMAs are done with the planes
-    stash();
-    __syncthreads();
-    if (k0 + KC < K) fetch(k0 + KC);
-    // lane l: A rows l % 16 and B columns l % 16, k = 8 (l / 16) + 0..7
-    const int ko = (lane >> 4) * 8;
-    bf16x8 b1[2], b2[2], b3[2];
+  // two chunks in flight: chunk j is loaded at the start of step j - 2 and
+  // staged at the end of step j - 1, so its loads have two steps to land
+  fetch(0, 0);
+  if (KC < K) fetch(KC, 1);
+  stash(0);
+  for (int k0 = 0; k0 < K; k0 += 2 * KC) {
 #pragma unroll
-    for (int j = 0; j < 2; ++j) {
-      const int o = (wn * 32 + j * 16 + (lane & 15)) * KP + ko;
-      b1[j] = *reinterpret_cast<const bf16x8*>(Bp + o);
-      b2[j] = *reinterpret_cast<const bf16x8*>(Bp + AB + o);
-      b3[j] = *reinterpret_cast<const bf16x8*>(Bp + 2 * AB + o);
-    }
+    for (int s = 0; s < 2; ++s) {
+      const int kc = k0 + s * KC;
+      if (kc >= K) break;
+      // stage s holds chunk kc; every wave is done with stage s ^ 1 (chunk kc - KC)
+      __syncthreads();
+      split_b(s);
+      if (kc + 2 * KC < K) fetch(kc + 2 * KC, s);
+      const __bf16* const Ap = lds + s * STG;
+      // lane l: A rows l % 16 and B columns l % 16, k = 8 (l / 16) + 0..7
 #pragma unroll
-    for (int i = 0; i < MI; ++i) {
-      const int o = (i * 16 + (lane & 15)) * KP + ko;
-      const bf16x8 a1 = *reinterpret_cast<const bf16x8*>(Ap + o);
-      if constexpr (A1_ONLY) {
+      for (int i = 0; i < MI; ++i) {
+        const int o = (i * 16 + (lane & 15)) * KP + kl;
+        const bf16x8 a1 = *reinterpret_cast<const bf16x8*>(Ap + o);
+        if constexpr (A1_ONLY) {
 #pragma unroll
-        for (int j = 0; j < 2; ++j) {
-          floatx4 c = acc[i][j];
-          c = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a1, b3[j], c, 0, 0, 0);   // small terms first
-          c = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a1, b2[j], c, 0, 0, 0);
-          acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a1, b1[j], c, 0, 0, 0);
-        }
-      } else {
-        const bf16x8 a2 = *reinterpret_cast<const bf16x8*>(Ap + AB + o);
-        const bf16x8 a3 = *reinterpret_cast<const bf16x8*>(Ap + 2 * AB + o);
+          for (int j = 0; j < 2; ++j) {
+            floatx4 c = acc[i][j];
+            c = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a1, b3[j], c, 0, 0, 0);   // small terms first
+            c = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a1, b2[j], c, 0, 0, 0);
+            acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a1, b1[j], c, 0, 0, 0);
+          }
+        } else {
+          const bf16x8 a2 = *reinterpret_cast<const bf16x8*>(Ap + AB + o);
+          const bf16x8 a3 = *reinterpret_cast<const bf16x8*>(Ap + 2 * AB + o);
 #pragma unroll
-        for (int j = 0; j < 2; ++j) {
-          floatx4 c = acc[i][j];
-          c = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a3, b1[j], c, 0, 0, 0);   // small terms first
-          c = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a2, b2[j], c, 0, 0, 0);
-          c = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a1, b3[j], c, 0, 0, 0);
-          c = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a2, b1[j], c, 0, 0, 0);
-          c = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a1, b2[j], c, 0, 0, 0);
-          acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a1, b1[j], c, 0, 0, 0);
+          for (int j = 0; j < 2; ++j) {
+            floatx4 c = acc[i][j];
+            c = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a3, b1[j], c, 0, 0, 0);   // small terms first
+            c = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a2, b2[j], c, 0, 0, 0);
+            c = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a1, b3[j], c, 0, 0, 0);
+            c = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a2, b1[j], c, 0, 0, 0);
+            c = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a1, b2[j], c, 0, 0, 0);
+            acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a1, b1[j], c, 0, 0, 0);
+          }
         }
       }
+      // the next chunk's A into the other stage
+      if (kc + KC < K) stash(s ^ 1);
     }
   }
 
@@ -846,6 +924,19 @@ proj_kc_kernel(const TI* __restrict__ A, int M, int K, int N, const float* __res
     // frame / pixel of this lane's first row, advanced by 16 rows per i
     const int gmb = m0 + (lane >> 4) * 4;
     const int fr0 = gmb / HW, p0 = gmb % HW;
+    // channel sums per (tile, frame): the tile's rows m0 .. m0 + 127 cover
+    // frames tf0 .. tf0 + slots - 1; frame tf0 + q goes to slot q of the tile.
+    // With HW >= 16 (host-checked) a 16-row block i spans frames fa, fa + 1
+    // (fa = frame of row m0 + 16 i, uniform); each lane keeps its sums of the
+    // current frame rf (run) and of rf + 1 (nxt) and the wave writes a slot
+    // when the blocks leave its frame, so every slot is written once.
+    const int tf0 = m0 / HW;
+    const int last_row = (M - m0 < TM ? M : m0 + TM) - 1;
+    auto flush = [&](float x, int slot, int c, bool on) {
+      x += __shfl_xor(x, 16, 64);
+      x += __shfl_xor(x, 32, 64);
+      if (on && lane < 16) partial[(size_t(rt) * slots + slot) * NH + c] = x;
+    };
 #pragma unroll
     for (int j = 0; j < 2; ++j) {
       const int gn = n0 + wn * 32 + j * 16 + (lane & 15);
@@ -856,7 +947,9 @@ proj_kc_kernel(const TI* __restrict__ A, int M, int K, int N, const float* __res
       const int NC = lo ? NH : NL;
       TO* dst = lo ? out_lo : out_hi;
       const int act = lo ? act_lo : act_hi;
-      float csum = 0.0f;
+      const bool sums = partial != nullptr;
+      float run = 0.0f, nxt = 0.0f;
+      int rf = tf0, fa = tf0, pa_ = m0 % HW;   // uniform: frame / pixel of row m0 + 16 i
       int fr = fr0, p = p0;
 #pragma unroll
       for (int i = 0; i < MI; ++i) {
@@ -868,21 +961,34 @@ proj_kc_kernel(const TI* __restrict__ A, int M, int K, int N, const float* __res
           if (act == 1) v[r] = v[r] * __builtin_amdgcn_rcpf(1.0f + __expf(-v[r]));
           else if (act == 2) v[r] = __builtin_amdgcn_rcpf(1.0f + __expf(-v[r]));
         }
+        if (sums && fa != rf) {   // fa == rf + 1
+          flush(run, rf - tf0, c, nok && lo);
+          run = nxt;
+          nxt = 0.0f;
+          rf = fa;
+        }
         if (nok && gm0 + 3 < M && (HW % 4) == 0) {
           st4(dst, size_t(fr * NC + c) * HW + p, v);
-          csum += (v[0] + v[1]) + (v[2] + v[3]);
         } else if (nok) {
           int f2 = fr, p2 = p;
 #pragma unroll
           for (int r = 0; r < 4; ++r) {
-            if (gm0 + r < M) {
-              st_el(dst, size_t(f2 * NC + c) * HW + p2, v[r]);
-              csum += v[r];
-            }
+            if (gm0 + r < M) st_el(dst, size_t(f2 * NC + c) * HW + p2, v[r]);
             if (++p2 == HW) {
               p2 = 0;
               ++f2;
             }
+          }
+        }
+        if (sums) {
+          // value r is row gm0 + r: frame fr, or fr + 1 once p + r passes HW; rows beyond M add nothing
+#pragma unroll
+          for (int r = 0; r < 4; ++r) {
+            const bool in = gm0 + r < M;
+            const bool second = (fr + (p + r >= HW ? 1 : 0)) != rf;
+            const float x = in ? v[r] : 0.0f;
+            if (second) nxt += x;
+            else run += x;
           }
         }
         p += 16;
@@ -890,11 +996,15 @@ proj_kc_kernel(const TI* __restrict__ A, int M, int K, int N, const float* __res
           p -= HW;
           ++fr;
         }
+        pa_ += 16;
+        while (pa_ >= HW) {
+          pa_ -= HW;
+          ++fa;
+        }
       }
-      if (partial != nullptr && lo) {
-        csum += __shfl_xor(csum, 16, 64);
-        csum += __shfl_xor(csum, 32, 64);
-        if (lane < 16 && nok) partial[size_t(blockIdx.x) * NH + c] = csum;
+      if (sums) {
+        flush(run, rf - tf0, c, nok && lo);
+        if (last_row / HW > rf) flush(nxt, rf + 1 - tf0, c, nok && lo);
       }
     }
   } else {
@@ -951,12 +1061,23 @@ constexpr int kKcTM = 128;   // row tile of the K-chunked kernel
 
 int proj_in_tile_rows(int K) { return K % 4 == 0 ? kPersistTM : kProjTM; }
 
+// channel-sum slots per row tile (partial sums of ctx): 1 when every tile
+// lies in one frame; the K-chunked kernel also sums tiles spanning frames,
+// one slot per frame (needs HW >= 16); 0: no fused sums for this shape
+int proj_in_ctx_slots(int K, int HW) {
+  const int tm = proj_in_tile_rows(K);
+  if (HW % tm == 0) return 1;
+  if (K > kPersistMaxK && K % 4 == 0 && HW >= 16) return (kKcTM - 2) / HW + 2;
+  return 0;
+}
+
 template <bool PLANE_A, bool OUT_SPLIT, class TI, class TO>
 static void launch_kc(const void* A, int M, int K, int N, const float* W, const float* b, int HW, void* lo, void* hi,
                       int act_lo, int act_hi, float* partial, int NH, hipStream_t s) {
-  const dim3 grid(unsigned((M + kKcTM - 1) / kKcTM), unsigned((N + 127) / 128));
+  const dim3 grid(unsigned((M + kKcTM - 1) / kKcTM) * unsigned((N + 127) / 128));
+  const int slots = partial ? proj_in_ctx_slots(K, HW) : 0;
   hipLaunchKernelGGL((proj_kc_kernel<PLANE_A, OUT_SPLIT, TI, TO>), grid, dim3(256), 0, s, static_cast<const TI*>(A), M,
-                     K, N, W, b, HW, static_cast<TO*>(lo), static_cast<TO*>(hi), act_lo, act_hi, partial, NH);
+                     K, N, W, b, HW, static_cast<TO*>(lo), static_cast<TO*>(hi), act_lo, act_hi, partial, NH, slots);
 }
 
 template <class TI, class TO>
@@ -1148,10 +1269,10 @@ hipError_t launch_proj_out_norm_gate(const void* Y, const void* G, int in_dtype,
   return hipGetLastError();
 }
 
-hipError_t launch_ctx_reduce(const float* partial, int F, int tiles_per_frame, int C, float inv_hw, float* ctx,
+hipError_t launch_ctx_reduce(const float* partial, int F, int HW, int tile_rows, int slots, int C, float* ctx,
                              hipStream_t s) {
   const int n = F * C;
-  hipLaunchKernelGGL(ctx_reduce_kernel, dim3((n + 255) / 256), dim3(256), 0, s, partial, F, tiles_per_frame, C, inv_hw,
+  hipLaunchKernelGGL(ctx_reduce_kernel, dim3((n + 255) / 256), dim3(256), 0, s, partial, F, HW, tile_rows, slots, C,
                      ctx);
   return hipGetLastError();
 }

@@ -25,12 +25,14 @@ def _dev(a, dtype=torch.float32):
     return torch.from_numpy(np.ascontiguousarray(a)).to("cuda", dtype)
 
 
-# K <= 64: persistent kernel; K > 64 with K % 4 == 0: K-chunked kernel (HW % 128 == 0 fuses ctx);
-# K % 4 != 0: fp32 tiled kernel.  N not a multiple of 128 / 4 and odd HW exercise the edges.
+# K <= 64: persistent kernel; K > 64 with K % 4 == 0: K-chunked kernel (ctx fused as per-frame sums of
+# each row tile for HW >= 16, including tiles that span 2-9 frames); K % 4 != 0: fp32 tiled kernel.
+# N not a multiple of 128 / 4, odd HW and HW < 16 (ctx from the output planes) exercise the edges.
 @pytest.mark.parametrize("F,HW,K,N,silu", [(4, 1024, 64, 256, True), (3, 16384, 64, 128, False),
                                            (5, 196, 40, 72, True), (2, 49, 130, 10, False),
                                            (2, 1024, 128, 512, True), (3, 196, 224, 896, True),
-                                           (2, 16, 320, 1280, False), (1, 49, 448, 90, True)])
+                                           (2, 16, 320, 1280, False), (1, 49, 448, 90, True),
+                                           (5, 100, 200, 64, True), (3, 8, 96, 64, False)])
 def test_proj_in_plane_major_and_ctx(mods, F, HW, K, N, silu):
     _, S = mods
     print_case(test="proj_in", F=F, HW=HW, K=K, N=N)
