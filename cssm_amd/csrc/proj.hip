@@ -716,18 +716,22 @@ proj_persist_kernel(const TI* __restrict__ A, int M, int K, int N, const float* 
 //   PLANE_A = false: A is channels-last (M, K), K % 4 == 0; true: plane-major (F, K, HW).
 //   OUT_SPLIT = true: plane-major output(s) as proj_in; false: channels-last (M, N).
 // ---------------------------------------------------------------------------
-template <bool PLANE_A, bool OUT_SPLIT, class TI, class TO>
-__global__ void __launch_bounds__(256, 2)
+template <bool PLANE_A, bool OUT_SPLIT, class TI, class TO, int TM_>
+__global__ void __launch_bounds__(256, (sizeof(TI) == 2 && !PLANE_A) ? 3 : 2)
 proj_kc_kernel(const TI* __restrict__ A, int M, int K, int N, const float* __restrict__ Wt,
                const float* __restrict__ bias, int HW, TO* __restrict__ out_lo, TO* __restrict__ out_hi,
                int act_lo, int act_hi, float* __restrict__ partial, int NH, int slots) {
-  constexpr int TM = 128, TN = 128, NT = 256, KC = 32, KP = KC + 8, MI = TM / 16;
+  constexpr int TM = TM_, TN = 128, NT = 256, KC = 32, KP = KC + 8, MI = TM / 16;
+  static_assert(TM == 64 || TM == 128, "row tiles of 64 or 128");
+  constexpr int NI = TM / 32, NKQ = 256 / TM;   // A load groups per thread; plane-major k groups
   constexpr bool A1_ONLY = sizeof(TI) == 2;      // bf16 A: one nonzero part
   constexpr int APL = A1_ONLY ? 1 : 3;           // A planes
   constexpr int OP = TN + 4;                     // channels-last staging pitch (floats), 64 rows at a time
   constexpr int AB = TM * KP;                    // bf16 per plane
   constexpr int STG = APL * AB;                  // bf16 per pipeline stage
-  constexpr int LDS_N = (!OUT_SPLIT && 64 * OP * 2 > 2 * STG) ? 64 * OP * 2 : 2 * STG;
+  constexpr int SPC = TM + 4;                    // plane-major staging pitch (floats): [16 columns][SPC] per wave
+  constexpr int OUT_N = OUT_SPLIT ? 4 * 16 * SPC * 2 : 64 * OP * 2;   // output staging, in bf16 units
+  constexpr int LDS_N = OUT_N > 2 * STG ? OUT_N : 2 * STG;
   __shared__ __attribute__((aligned(16))) __bf16 lds[LDS_N];   // two A stages; the output staging reuses them
   const int tid = threadIdx.x, lane = tid & 63, wn = tid >> 6;
   // XCD-aware tile order: workgroup ids go round-robin over the 8 XCDs, so the
@@ -744,23 +748,23 @@ proj_kc_kernel(const TI* __restrict__ A, int M, int K, int N, const float* __res
   const int m0 = rt * TM, n0 = ct * TN;
   const int NL = N - NH;
 
-  // this thread's A loads per chunk: 4 groups i of 4 consecutive k
+  // this thread's A loads per chunk: NI groups i of 4 consecutive k
   //   channels-last: rows (tid / 8) + 32 i, k 4 (tid % 8)
-  //   plane-major:   row tid % 128, k groups 2 i + tid / 128
+  //   plane-major:   row tid % TM, k groups NKQ i + tid / TM
   // All loads are buffer loads with a per-lane byte offset and a uniform
   // (SGPR) one, so the unrolled chunk offsets cost no VGPRs across the loop.
-  const int rr = tid & 127, kq = tid >> 7;
+  const int rr = tid % TM, kq = tid / TM;
   const int ar = tid >> 3, ak = (tid & 7) * 4;
   constexpr int EA = sizeof(TI);
   __amdgpu_buffer_rsrc_t ra;   // A rows of this tile
   unsigned a_off;
-  bool a_ok[4];
+  bool a_ok[NI];
   if constexpr (!PLANE_A) {
     const int rows = M - m0 < TM ? M - m0 : TM;
     ra = make_rsrc(A + size_t(m0) * K, unsigned(rows) * unsigned(K) * EA);
     a_off = unsigned(ar * K + ak) * EA;
 #pragma unroll
-    for (int i = 0; i < 4; ++i) a_ok[i] = m0 + ar + 32 * i < M;
+    for (int i = 0; i < NI; ++i) a_ok[i] = m0 + ar + 32 * i < M;
   } else {
     const int last = (M - m0 < TM ? M : m0 + TM) - 1;
     const int fr0 = m0 / HW, nfr = last / HW - fr0 + 1;
@@ -768,7 +772,7 @@ proj_kc_kernel(const TI* __restrict__ A, int M, int K, int N, const float* __res
     const int gm = m0 + rr < M ? m0 + rr : m0;
     a_off = unsigned(((gm / HW - fr0) * K + 4 * kq) * HW + gm % HW) * EA;
 #pragma unroll
-    for (int i = 0; i < 4; ++i) a_ok[i] = m0 + rr < M;
+    for (int i = 0; i < NI; ++i) a_ok[i] = m0 + rr < M;
   }
   // this lane's B fragments: columns wn 32 + 16 j + lane % 16, k = chunk + 8 (lane / 16) + e
   const int kl = (lane >> 4) * 8;
@@ -785,7 +789,7 @@ proj_kc_kernel(const TI* __restrict__ A, int M, int K, int N, const float* __res
   // Raw A: the bf16 bits themselves for channels-last bf16 A (they are the one bf16 part), else floats.
   constexpr bool RAW16 = A1_ONLY && !PLANE_A;
   using RawA = typename std::conditional<RAW16, uint2, float4>::type;
-  RawA pa[2][4];
+  RawA pa[2][NI];
   float pw[2][2][8];
   // A lane whose element lies outside the tensor (rows beyond M, k beyond K)
   // loads at byte offset kOut instead: beyond every resource range, so the
@@ -794,7 +798,7 @@ proj_kc_kernel(const TI* __restrict__ A, int M, int K, int N, const float* __res
   auto fetch = [&](int k0, int s) {
     const bool full = k0 + KC <= K;
 #pragma unroll
-    for (int i = 0; i < 4; ++i) {
+    for (int i = 0; i < NI; ++i) {
       if constexpr (!PLANE_A) {
         const unsigned vo = (a_ok[i] && (full || k0 + ak < K)) ? a_off : kOut;
         const int so = (32 * i * K + k0) * EA;
@@ -806,7 +810,7 @@ proj_kc_kernel(const TI* __restrict__ A, int M, int K, int N, const float* __res
         float v[4];
 #pragma unroll
         for (int e = 0; e < 4; ++e) {
-          const int k = k0 + 8 * i + e;   // relative to this thread's 4 kq
+          const int k = k0 + 4 * NKQ * i + e;   // relative to this thread's 4 kq
           const unsigned vo = (a_ok[i] && (full || k + 4 * kq < K)) ? a_off : kOut;
           const int so = k * HW * EA;
           if constexpr (EA == 2)
@@ -829,8 +833,8 @@ proj_kc_kernel(const TI* __restrict__ A, int M, int K, int N, const float* __res
   auto stash = [&](int s) {
     __bf16* const planes = lds + s * STG;
 #pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      const int off = PLANE_A ? rr * KP + (2 * i + kq) * 4 : (ar + 32 * i) * KP + ak;
+    for (int i = 0; i < NI; ++i) {
+      const int off = PLANE_A ? rr * KP + (NKQ * i + kq) * 4 : (ar + 32 * i) * KP + ak;
       if constexpr (RAW16) {
         *reinterpret_cast<uint2*>(planes + off) = pa[s][i];
       } else {
@@ -921,106 +925,137 @@ proj_kc_kernel(const TI* __restrict__ A, int M, int K, int N, const float* __res
 
   // epilogue: lane holds rows 16 i + 4 (lane / 16) + r of column lane % 16 of n-tile j
   if constexpr (OUT_SPLIT) {
-    // frame / pixel of this lane's first row, advanced by 16 rows per i
-    const int gmb = m0 + (lane >> 4) * 4;
-    const int fr0 = gmb / HW, p0 = gmb % HW;
-    // channel sums per (tile, frame): the tile's rows m0 .. m0 + 127 cover
-    // frames tf0 .. tf0 + slots - 1; frame tf0 + q goes to slot q of the tile.
-    // With HW >= 16 (host-checked) a 16-row block i spans frames fa, fa + 1
-    // (fa = frame of row m0 + 16 i, uniform); each lane keeps its sums of the
-    // current frame rf (run) and of rf + 1 (nxt) and the wave writes a slot
-    // when the blocks leave its frame, so every slot is written once.
-    const int tf0 = m0 / HW;
-    const int last_row = (M - m0 < TM ? M : m0 + TM) - 1;
-    auto flush = [&](float x, int slot, int c, bool on) {
-      x += __shfl_xor(x, 16, 64);
-      x += __shfl_xor(x, 32, 64);
-      if (on && lane < 16) partial[(size_t(rt) * slots + slot) * NH + c] = x;
-    };
+    // 1) bias and activation in place; the activation is one wave-uniform
+    //    branch when both halves use the same one
 #pragma unroll
     for (int j = 0; j < 2; ++j) {
       const int gn = n0 + wn * 32 + j * 16 + (lane & 15);
-      const bool nok = gn < N;
-      const float bv = nok ? bias[gn] : 0.0f;
-      const bool lo = gn < NH;
-      const int c = lo ? gn : gn - NH;
-      const int NC = lo ? NH : NL;
-      TO* dst = lo ? out_lo : out_hi;
-      const int act = lo ? act_lo : act_hi;
-      const bool sums = partial != nullptr;
-      float run = 0.0f, nxt = 0.0f;
-      int rf = tf0, fa = tf0, pa_ = m0 % HW;   // uniform: frame / pixel of row m0 + 16 i
-      int fr = fr0, p = p0;
+      const float bv = gn < N ? bias[gn] : 0.0f;
+      const int act = gn < NH ? act_lo : act_hi;
+      if (act_lo == act_hi && act_lo == 0) {
 #pragma unroll
-      for (int i = 0; i < MI; ++i) {
-        const int gm0 = gmb + i * 16;
-        float v[4];
+        for (int i = 0; i < MI; ++i)
 #pragma unroll
-        for (int r = 0; r < 4; ++r) {
-          v[r] = acc[i][j][r] + bv;
-          if (act == 1) v[r] = v[r] * __builtin_amdgcn_rcpf(1.0f + __expf(-v[r]));
-          else if (act == 2) v[r] = __builtin_amdgcn_rcpf(1.0f + __expf(-v[r]));
-        }
-        if (sums && fa != rf) {   // fa == rf + 1
-          flush(run, rf - tf0, c, nok && lo);
-          run = nxt;
-          nxt = 0.0f;
-          rf = fa;
-        }
-        if (nok && gm0 + 3 < M && (HW % 4) == 0) {
-          st4(dst, size_t(fr * NC + c) * HW + p, v);
-        } else if (nok) {
-          int f2 = fr, p2 = p;
+          for (int r = 0; r < 4; ++r) acc[i][j][r] += bv;
+      } else {
+#pragma unroll
+        for (int i = 0; i < MI; ++i)
 #pragma unroll
           for (int r = 0; r < 4; ++r) {
-            if (gm0 + r < M) st_el(dst, size_t(f2 * NC + c) * HW + p2, v[r]);
+            const float v = acc[i][j][r] + bv;
+            const float sg = __builtin_amdgcn_rcpf(1.0f + __expf(-v));
+            acc[i][j][r] = act == 1 ? v * sg : (act == 2 ? sg : v);
+          }
+      }
+    }
+    // 2) channel sums per (tile, frame): the tile's rows m0 .. m0 + 127 cover
+    //    frames tf0 .. tf0 + slots - 1; frame tf0 + q goes to slot q of the
+    //    tile.  With HW >= 16 (host-checked) a 16-row block i spans frames fa,
+    //    fa + 1 (fa = frame of row m0 + 16 i, uniform); each lane keeps its
+    //    sums of the current frame rf (run) and of rf + 1 (nxt) and the wave
+    //    writes a slot when the blocks leave its frame, so every slot is
+    //    written once.
+    if (partial != nullptr) {
+      const int gmb = m0 + (lane >> 4) * 4;
+      const int tf0 = m0 / HW;
+      const int last_row = (M - m0 < TM ? M : m0 + TM) - 1;
+      auto flush = [&](float x, int slot, int c, bool on) {
+        x += __shfl_xor(x, 16, 64);
+        x += __shfl_xor(x, 32, 64);
+        if (on && lane < 16) partial[(size_t(rt) * slots + slot) * NH + c] = x;
+      };
+#pragma unroll
+      for (int j = 0; j < 2; ++j) {
+        const int gn = n0 + wn * 32 + j * 16 + (lane & 15);
+        const bool on = gn < N && gn < NH;
+        float run = 0.0f, nxt = 0.0f;
+        int rf = tf0, fa = tf0, pa_ = m0 % HW;   // uniform: frame / pixel of row m0 + 16 i
+        int fr = gmb / HW, p = gmb % HW;          // this lane's row gmb + 16 i
+#pragma unroll
+        for (int i = 0; i < MI; ++i) {
+          if (fa != rf) {   // fa == rf + 1
+            flush(run, rf - tf0, gn, on);
+            run = nxt;
+            nxt = 0.0f;
+            rf = fa;
+          }
+          // value r is row gmb + 16 i + r: frame fr, or fr + 1 once p + r passes HW; rows beyond M add nothing
+#pragma unroll
+          for (int r = 0; r < 4; ++r) {
+            const float x = gmb + i * 16 + r < M ? acc[i][j][r] : 0.0f;
+            if (fr + (p + r >= HW ? 1 : 0) != rf) nxt += x;
+            else run += x;
+          }
+          p += 16;
+          while (p >= HW) {
+            p -= HW;
+            ++fr;
+          }
+          pa_ += 16;
+          while (pa_ >= HW) {
+            pa_ -= HW;
+            ++fa;
+          }
+        }
+        flush(run, rf - tf0, gn, on);
+        if (last_row / HW > rf) flush(nxt, rf + 1 - tf0, gn, on);
+      }
+    }
+    // 3) stores through LDS, one n-tile j (16 columns) per wave at a time:
+    //    the wave writes its values as [column][row], then LPC lanes store
+    //    one column's TM rows, 4 consecutive rows per lane, so a store
+    //    instruction covers 64 / LPC runs of consecutive pixels
+    __syncthreads();   // every wave is done reading the A stages
+    float* const stg = reinterpret_cast<float*>(lds) + wn * (16 * SPC);
+    constexpr int LPC = TM / 4, CPI = 64 / LPC;   // lanes per column, columns per store
+    const int q = lane % LPC, half = lane / LPC;
+    const int row0 = m0 + 4 * q;                  // this lane's 4 rows
+    const int rfr = row0 / HW, rpx = row0 % HW;   // frame / pixel of row0
+#pragma unroll
+    for (int j = 0; j < 2; ++j) {
+#pragma unroll
+      for (int i = 0; i < MI; ++i)
+        *reinterpret_cast<floatx4*>(&stg[(lane & 15) * SPC + i * 16 + (lane >> 4) * 4]) = acc[i][j];
+      // same-wave LDS writes and reads execute in order
+#pragma unroll
+      for (int cp = 0; cp < 16 / CPI; ++cp) {
+        const int cl = CPI * cp + half;
+        const int gn = n0 + wn * 32 + j * 16 + cl;
+        const floatx4 v4 = *reinterpret_cast<const floatx4*>(&stg[cl * SPC + 4 * q]);
+        if (gn >= N || row0 >= M) continue;
+        const bool lo = gn < NH;
+        const int c = lo ? gn : gn - NH, NC = lo ? NH : NL;
+        TO* dst = lo ? out_lo : out_hi;
+        const float v[4] = {v4[0], v4[1], v4[2], v4[3]};
+        if ((HW % 4) == 0 && row0 + 3 < M) {
+          st4(dst, size_t(rfr * NC + c) * HW + rpx, v);
+        } else {
+          int f2 = rfr, p2 = rpx;
+#pragma unroll
+          for (int r = 0; r < 4; ++r) {
+            if (row0 + r < M) st_el(dst, size_t(f2 * NC + c) * HW + p2, v[r]);
             if (++p2 == HW) {
               p2 = 0;
               ++f2;
             }
           }
         }
-        if (sums) {
-          // value r is row gm0 + r: frame fr, or fr + 1 once p + r passes HW; rows beyond M add nothing
-#pragma unroll
-          for (int r = 0; r < 4; ++r) {
-            const bool in = gm0 + r < M;
-            const bool second = (fr + (p + r >= HW ? 1 : 0)) != rf;
-            const float x = in ? v[r] : 0.0f;
-            if (second) nxt += x;
-            else run += x;
-          }
-        }
-        p += 16;
-        while (p >= HW) {
-          p -= HW;
-          ++fr;
-        }
-        pa_ += 16;
-        while (pa_ >= HW) {
-          pa_ -= HW;
-          ++fa;
-        }
-      }
-      if (sums) {
-        flush(run, rf - tf0, c, nok && lo);
-        if (last_row / HW > rf) flush(nxt, rf + 1 - tf0, c, nok && lo);
       }
     }
   } else {
     // channels-last: stage 64 rows at a time in LDS, then whole-row stores of 4 columns per lane
     float* st = reinterpret_cast<float*>(lds);
 #pragma unroll
-    for (int h = 0; h < 2; ++h) {
+    for (int h = 0; h < TM / 64; ++h) {
       __syncthreads();
 #pragma unroll
       for (int j = 0; j < 2; ++j) {
         const int cl = wn * 32 + j * 16 + (lane & 15);
         const float bv = n0 + cl < N ? bias[n0 + cl] : 0.0f;
 #pragma unroll
-        for (int i = 0; i < MI / 2; ++i)
+        for (int i = 0; i < 4; ++i)
 #pragma unroll
-          for (int r = 0; r < 4; ++r) st[(i * 16 + (lane >> 4) * 4 + r) * OP + cl] = acc[h * (MI / 2) + i][j][r] + bv;
+          for (int r = 0; r < 4; ++r) st[(i * 16 + (lane >> 4) * 4 + r) * OP + cl] = acc[h * 4 + i][j][r] + bv;
       }
       __syncthreads();
       for (int f = tid; f < 64 * (TN / 4); f += NT) {
@@ -1045,12 +1080,16 @@ proj_kc_kernel(const TI* __restrict__ A, int M, int K, int N, const float* __res
 constexpr int kProjTM = 64;      // row tile of the general kernels
 constexpr int kPersistTM = 128;  // row tile of the persistent small-K kernels
 
-static int persistent_grid(int tiles) {
+static int cu_count() {
   int dev = 0, cus = 256;
   if (hipGetDevice(&dev) == hipSuccess) {
-    hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev);
+    if (hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess) cus = 256;
   }
-  const int g = 2 * cus;   // two workgroups per CU
+  return cus;
+}
+
+static int persistent_grid(int tiles) {
+  const int g = 2 * cu_count();   // two workgroups per CU
   return tiles < g ? tiles : g;
 }
 
@@ -1071,13 +1110,28 @@ int proj_in_ctx_slots(int K, int HW) {
   return 0;
 }
 
+template <bool PLANE_A, bool OUT_SPLIT, class TI, class TO, int TM>
+static void launch_kc_tm(const void* A, int M, int K, int N, const float* W, const float* b, int HW, void* lo,
+                         void* hi, int act_lo, int act_hi, float* partial, int NH, hipStream_t s) {
+  const dim3 grid(unsigned((M + TM - 1) / TM) * unsigned((N + 127) / 128));
+  const int slots = partial ? proj_in_ctx_slots(K, HW) : 0;
+  hipLaunchKernelGGL((proj_kc_kernel<PLANE_A, OUT_SPLIT, TI, TO, TM>), grid, dim3(256), 0, s, static_cast<const TI*>(A),
+                     M, K, N, W, b, HW, static_cast<TO*>(lo), static_cast<TO*>(hi), act_lo, act_hi, partial, NH, slots);
+}
+
+// 128-row tiles; channels-last outputs (proj_out, narrow N) whose 128-row
+// tiles would leave CUs idle take 64-row tiles (twice the workgroups)
 template <bool PLANE_A, bool OUT_SPLIT, class TI, class TO>
 static void launch_kc(const void* A, int M, int K, int N, const float* W, const float* b, int HW, void* lo, void* hi,
                       int act_lo, int act_hi, float* partial, int NH, hipStream_t s) {
-  const dim3 grid(unsigned((M + kKcTM - 1) / kKcTM) * unsigned((N + 127) / 128));
-  const int slots = partial ? proj_in_ctx_slots(K, HW) : 0;
-  hipLaunchKernelGGL((proj_kc_kernel<PLANE_A, OUT_SPLIT, TI, TO>), grid, dim3(256), 0, s, static_cast<const TI*>(A), M,
-                     K, N, W, b, HW, static_cast<TO*>(lo), static_cast<TO*>(hi), act_lo, act_hi, partial, NH, slots);
+  if constexpr (!OUT_SPLIT) {
+    const long long tiles = (long long)((M + kKcTM - 1) / kKcTM) * ((N + 127) / 128);
+    if (tiles < cu_count()) {
+      launch_kc_tm<PLANE_A, OUT_SPLIT, TI, TO, 64>(A, M, K, N, W, b, HW, lo, hi, act_lo, act_hi, partial, NH, s);
+      return;
+    }
+  }
+  launch_kc_tm<PLANE_A, OUT_SPLIT, TI, TO, kKcTM>(A, M, K, N, W, b, HW, lo, hi, act_lo, act_hi, partial, NH, s);
 }
 
 template <class TI, class TO>
