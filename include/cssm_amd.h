@@ -166,7 +166,8 @@ int cssm_gated_scan_fwd(const void* u, const void* z, void* y, int dtype, int B,
  *   out_lo   (F, N/2, HW) plane-major of out_dtype: output channels [0, N/2)
  *   out_hi   (F, N/2, HW): output channels [N/2, N) (N must be even)
  *   act_lo, act_hi  cssm_load_act applied to each half
- *   ctx      (F, N/2) float32 out = mean over HW of the stored out_lo, or NULL
+ *   ctx      (F, N/2) float32 out = mean over HW of out_lo, or NULL (summed in fp32; with a
+ *            bf16 out_lo the sums may be taken before or after its rounding)
  *   workspace  device scratch of cssm_proj_in_workspace_size(F, HW, K, N) bytes
  *              (used only when ctx is requested)
  */
