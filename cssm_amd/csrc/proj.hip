@@ -1111,27 +1111,31 @@ int proj_in_ctx_slots(int K, int HW) {
 }
 
 template <bool PLANE_A, bool OUT_SPLIT, class TI, class TO, int TM>
-static void launch_kc_tm(const void* A, int M, int K, int N, const float* W, const float* b, int HW, void* lo,
-                         void* hi, int act_lo, int act_hi, float* partial, int NH, hipStream_t s) {
+static hipError_t launch_kc_tm(const void* A, int M, int K, int N, const float* W, const float* b, int HW, void* lo,
+                               void* hi, int act_lo, int act_hi, float* partial, int NH, hipStream_t s) {
+  // the kernel's buffer resources (one row tile of A, all of W) must stay below 2^31 bytes, the
+  // offset its out-of-range lanes load at
+  const long long a_bytes = PLANE_A ? (long long)((TM - 2) / HW + 2) * K * HW * (long long)sizeof(TI)
+                                    : (long long)TM * K * (long long)sizeof(TI);
+  if (a_bytes >= (1LL << 31) || (long long)K * N * 4 >= (1LL << 31)) return hipErrorInvalidValue;
   const dim3 grid(unsigned((M + TM - 1) / TM) * unsigned((N + 127) / 128));
   const int slots = partial ? proj_in_ctx_slots(K, HW) : 0;
   hipLaunchKernelGGL((proj_kc_kernel<PLANE_A, OUT_SPLIT, TI, TO, TM>), grid, dim3(256), 0, s, static_cast<const TI*>(A),
                      M, K, N, W, b, HW, static_cast<TO*>(lo), static_cast<TO*>(hi), act_lo, act_hi, partial, NH, slots);
+  return hipGetLastError();
 }
 
 // 128-row tiles; channels-last outputs (proj_out, narrow N) whose 128-row
 // tiles would leave CUs idle take 64-row tiles (twice the workgroups)
 template <bool PLANE_A, bool OUT_SPLIT, class TI, class TO>
-static void launch_kc(const void* A, int M, int K, int N, const float* W, const float* b, int HW, void* lo, void* hi,
-                      int act_lo, int act_hi, float* partial, int NH, hipStream_t s) {
+static hipError_t launch_kc(const void* A, int M, int K, int N, const float* W, const float* b, int HW, void* lo,
+                            void* hi, int act_lo, int act_hi, float* partial, int NH, hipStream_t s) {
   if constexpr (!OUT_SPLIT) {
     const long long tiles = (long long)((M + kKcTM - 1) / kKcTM) * ((N + 127) / 128);
-    if (tiles < cu_count()) {
-      launch_kc_tm<PLANE_A, OUT_SPLIT, TI, TO, 64>(A, M, K, N, W, b, HW, lo, hi, act_lo, act_hi, partial, NH, s);
-      return;
-    }
+    if (tiles < cu_count())
+      return launch_kc_tm<PLANE_A, OUT_SPLIT, TI, TO, 64>(A, M, K, N, W, b, HW, lo, hi, act_lo, act_hi, partial, NH, s);
   }
-  launch_kc_tm<PLANE_A, OUT_SPLIT, TI, TO, kKcTM>(A, M, K, N, W, b, HW, lo, hi, act_lo, act_hi, partial, NH, s);
+  return launch_kc_tm<PLANE_A, OUT_SPLIT, TI, TO, kKcTM>(A, M, K, N, W, b, HW, lo, hi, act_lo, act_hi, partial, NH, s);
 }
 
 template <class TI, class TO>
@@ -1188,14 +1192,15 @@ hipError_t launch_proj_planes(const void* X, int in_dtype, int M, int K, int N, 
   const NormGate ng{nullptr, nullptr, nullptr, 0};
   if (K > kPersistMaxK && K % 4 == 0) {
     if (in_dtype == 0 && out_dtype == 0)
-      launch_kc<false, true, float, float>(X, M, K, N, W, b, HW, out_lo, out_hi, act_lo, act_hi, partial, NH, s);
-    else if (in_dtype == 0)
-      launch_kc<false, true, float, uint16_t>(X, M, K, N, W, b, HW, out_lo, out_hi, act_lo, act_hi, partial, NH, s);
-    else if (out_dtype == 0)
-      launch_kc<false, true, uint16_t, float>(X, M, K, N, W, b, HW, out_lo, out_hi, act_lo, act_hi, partial, NH, s);
-    else
-      launch_kc<false, true, uint16_t, uint16_t>(X, M, K, N, W, b, HW, out_lo, out_hi, act_lo, act_hi, partial, NH, s);
-    return hipGetLastError();
+      return launch_kc<false, true, float, float>(X, M, K, N, W, b, HW, out_lo, out_hi, act_lo, act_hi, partial, NH, s);
+    if (in_dtype == 0)
+      return launch_kc<false, true, float, uint16_t>(X, M, K, N, W, b, HW, out_lo, out_hi, act_lo, act_hi, partial, NH,
+                                                     s);
+    if (out_dtype == 0)
+      return launch_kc<false, true, uint16_t, float>(X, M, K, N, W, b, HW, out_lo, out_hi, act_lo, act_hi, partial, NH,
+                                                     s);
+    return launch_kc<false, true, uint16_t, uint16_t>(X, M, K, N, W, b, HW, out_lo, out_hi, act_lo, act_hi, partial,
+                                                      NH, s);
   }
   if (K <= kPersistMaxK && K % 4 == 0) {
     if (in_dtype == 0 && out_dtype == 0)
@@ -1283,14 +1288,12 @@ hipError_t launch_proj_out(const void* Y, int in_dtype, int M, int K, int N, con
   const NormGate ng{nullptr, nullptr, nullptr, 0};
   if (K > kPersistMaxK || K % 4 != 0 || HW % 4 != 0) {
     if (in_dtype == 0 && out_dtype == 0)
-      launch_kc<true, false, float, float>(Y, M, K, N, W, b, HW, out, nullptr, 0, 0, nullptr, N, s);
-    else if (in_dtype == 0)
-      launch_kc<true, false, float, uint16_t>(Y, M, K, N, W, b, HW, out, nullptr, 0, 0, nullptr, N, s);
-    else if (out_dtype == 0)
-      launch_kc<true, false, uint16_t, float>(Y, M, K, N, W, b, HW, out, nullptr, 0, 0, nullptr, N, s);
-    else
-      launch_kc<true, false, uint16_t, uint16_t>(Y, M, K, N, W, b, HW, out, nullptr, 0, 0, nullptr, N, s);
-    return hipGetLastError();
+      return launch_kc<true, false, float, float>(Y, M, K, N, W, b, HW, out, nullptr, 0, 0, nullptr, N, s);
+    if (in_dtype == 0)
+      return launch_kc<true, false, float, uint16_t>(Y, M, K, N, W, b, HW, out, nullptr, 0, 0, nullptr, N, s);
+    if (out_dtype == 0)
+      return launch_kc<true, false, uint16_t, float>(Y, M, K, N, W, b, HW, out, nullptr, 0, 0, nullptr, N, s);
+    return launch_kc<true, false, uint16_t, uint16_t>(Y, M, K, N, W, b, HW, out, nullptr, 0, 0, nullptr, N, s);
   }
   {
     if (in_dtype == 0 && out_dtype == 0)
