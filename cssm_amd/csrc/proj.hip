@@ -621,7 +621,11 @@ proj_persist_kernel(const TI* __restrict__ A, int M, int K, int N, const float* 
         }
       }
     } else if (OUT_SPLIT) {
-      // 4 consecutive pixels of one channel per lane and MFMA tile: 16 B stores
+      // 4 consecutive pixels of one channel per lane and MFMA tile: 16 B stores.
+      // Frame / pixel of the lane's first row: one division per tile, then
+      // advanced by 16 rows per i.
+      const int gmb = m0 + wm * MI * 16 + (lane >> 4) * 4;
+      const int fr_b = gmb / HW, p_b = gmb % HW;
 #pragma unroll
       for (int j = 0; j < 2; ++j) {
         const int gn = n0 + wn * 32 + j * 16 + (lane & 15);
@@ -632,31 +636,49 @@ proj_persist_kernel(const TI* __restrict__ A, int M, int K, int N, const float* 
         const int NC = lo ? NH : NL;
         TO* dst = lo ? out_lo : out_hi;
         const int act = lo ? act_lo : act_hi;
+        // bias and activation: one wave-uniform branch when both halves use the same activation
+        if (act_lo == act_hi && act_lo == 0) {
+#pragma unroll
+          for (int i = 0; i < MI; ++i)
+#pragma unroll
+            for (int r = 0; r < 4; ++r) acc[i][j][r] += bv;
+        } else {
+#pragma unroll
+          for (int i = 0; i < MI; ++i)
+#pragma unroll
+            for (int r = 0; r < 4; ++r) {
+              const float v = acc[i][j][r] + bv;
+              const float sg = __builtin_amdgcn_rcpf(1.0f + __expf(-v));
+              acc[i][j][r] = act == 1 ? v * sg : (act == 2 ? sg : v);
+            }
+        }
         float csum = 0.0f;
+        int fr = fr_b, p = p_b;
 #pragma unroll
         for (int i = 0; i < MI; ++i) {
-          const int gm0 = m0 + (wm * MI + i) * 16 + (lane >> 4) * 4;
-          float v[4];
-#pragma unroll
-          for (int r = 0; r < 4; ++r) {
-            v[r] = acc[i][j][r] + bv;
-            if (act == 1) v[r] = v[r] * __builtin_amdgcn_rcpf(1.0f + __expf(-v[r]));
-            else if (act == 2) v[r] = __builtin_amdgcn_rcpf(1.0f + __expf(-v[r]));
-          }
+          const int gm0 = gmb + i * 16;
+          const float v[4] = {acc[i][j][0], acc[i][j][1], acc[i][j][2], acc[i][j][3]};
           if (nok && gm0 + 3 < M && (HW % 4) == 0) {
-            const int fr = gm0 / HW, p = gm0 % HW;
             st4(dst, (size_t(fr) * NC + c) * HW + p, v);
             csum += (v[0] + v[1]) + (v[2] + v[3]);
           } else if (nok) {
+            int f2 = fr, p2 = p;
 #pragma unroll
             for (int r = 0; r < 4; ++r) {
-              const int gm = gm0 + r;
-              if (gm < M) {
-                const int fr = gm / HW, p = gm % HW;
-                st_el(dst, (size_t(fr) * NC + c) * HW + p, v[r]);
+              if (gm0 + r < M) {
+                st_el(dst, (size_t(f2) * NC + c) * HW + p2, v[r]);
                 csum += v[r];
               }
+              if (++p2 == HW) {
+                p2 = 0;
+                ++f2;
+              }
             }
+          }
+          p += 16;
+          while (p >= HW) {
+            p -= HW;
+            ++fr;
           }
         }
         if (WM == 1 && partial != nullptr && lo) {
