@@ -35,6 +35,12 @@ __device__ __forceinline__ float4 ld4v(const uint16_t* p, size_t i) {
                      bf16_to_f32(v.y >> 16));
 }
 __device__ __forceinline__ void st_f(float* p, size_t i, float v) { p[i] = v; }
+// 4 consecutive elements at a 4-element-aligned index
+__device__ __forceinline__ void st4v(float* p, size_t i, float4 v) { *reinterpret_cast<float4*>(p + i) = v; }
+__device__ __forceinline__ void st4v(uint16_t* p, size_t i, float4 v) {
+  const uint2 u = make_uint2(f32_to_bf16(v.x) | (f32_to_bf16(v.y) << 16), f32_to_bf16(v.z) | (f32_to_bf16(v.w) << 16));
+  *reinterpret_cast<uint2*>(p + i) = u;
+}
 __device__ __forceinline__ void st_f(uint16_t* p, size_t i, float v) { p[i] = uint16_t(f32_to_bf16(v)); }
 
 __device__ __forceinline__ float sigmoid_f(float x) { return 1.0f / (1.0f + expf(-x)); }
@@ -639,18 +645,18 @@ dwconv_cl(const TI* __restrict__ x, int H, int W, int C, int ks, const float* __
 template <int KS, class TI, class TO>
 __global__ void __launch_bounds__(256)
 dwconv_cl_blocked(const TI* __restrict__ x, int H, int W, int C, const float* __restrict__ kw,
-                  const float* __restrict__ bias, TO* __restrict__ y, long long total) {
+                  const float* __restrict__ bias, TO* __restrict__ y, int per_frame) {
   constexpr int LO = (KS - 1) / 2, RH = 2, RW = 4, NCOL = RW + KS - 1;
-  const long long i = (long long)blockIdx.x * blockDim.x + threadIdx.x;
-  if (i >= total) return;
-  const int CG = C / 4, WG = W / RW, HG = H / RH;
-  const int c0 = int(i % CG) * 4;
-  const long long t1 = i / CG;
-  const int w0 = int(t1 % WG) * RW;
-  const long long t2 = t1 / WG;
-  const int h0 = int(t2 % HG) * RH;
-  const long long f = t2 / HG;
-  const TI* xf = x + size_t(f) * H * W * C;
+  // frame blockIdx.y; (row pair, column quad, channel quad) from 32-bit index arithmetic
+  const int i = int(blockIdx.x) * int(blockDim.x) + int(threadIdx.x);
+  if (i >= per_frame) return;
+  const int CG = C / 4, WG = W / RW;
+  const int c0 = (i % CG) * 4;
+  const int t1 = i / CG;
+  const int w0 = (t1 % WG) * RW;
+  const int h0 = (t1 / WG) * RH;
+  const size_t f = blockIdx.y;
+  const TI* xf = x + f * H * W * C;
   float4 acc[RH][RW];
   const float4 bv = *reinterpret_cast<const float4*>(bias + c0);
 #pragma unroll
@@ -685,30 +691,31 @@ dwconv_cl_blocked(const TI* __restrict__ x, int H, int W, int C, const float* __
       }
     }
   }
+  // 4 consecutive channels per store: one 16-byte (f32) or 8-byte (bf16) store
 #pragma unroll
   for (int r = 0; r < RH; ++r)
 #pragma unroll
-    for (int q = 0; q < RW; ++q) {
-      const size_t o = ((size_t(f) * H + h0 + r) * W + w0 + q) * C + c0;
-      const float e[4] = {acc[r][q].x, acc[r][q].y, acc[r][q].z, acc[r][q].w};
-#pragma unroll
-      for (int k = 0; k < 4; ++k) st_f(y, o + k, e[k]);
-    }
+    for (int q = 0; q < RW; ++q) st4v(y, ((f * H + h0 + r) * W + w0 + q) * C + c0, acc[r][q]);
 }
 
 template <int KS, class TI, class TO>
 static hipError_t run_dwconv_blocked(const void* x, int F, int H, int W, int C, const float* kw, const float* bias,
                                      void* y, hipStream_t s) {
-  const long long total = (long long)F * (H / 2) * (W / 4) * (C / 4);
-  hipLaunchKernelGGL((dwconv_cl_blocked<KS, TI, TO>), dim3(unsigned((total + 255) / 256)), dim3(256), 0, s,
-                     static_cast<const TI*>(x), H, W, C, kw, bias, static_cast<TO*>(y), total);
+  const int per_frame = (H / 2) * (W / 4) * (C / 4);
+  hipLaunchKernelGGL((dwconv_cl_blocked<KS, TI, TO>), dim3(unsigned((per_frame + 255) / 256), unsigned(F)), dim3(256),
+                     0, s, static_cast<const TI*>(x), H, W, C, kw, bias, static_cast<TO*>(y), per_frame);
   return hipGetLastError();
 }
 
 template <class TI, class TO>
 static bool try_dwconv_blocked(const void* x, int F, int H, int W, int C, int ks, const float* kw, const float* bias,
                                void* y, hipStream_t s, hipError_t& e) {
-  if (C % 4 || W % 4 || H % 2) return false;
+  // float4 loads / stores of 4 channels: 16-byte aligned f32 (8-byte bf16) tensors; one frame's
+  // work items must fit 32-bit indices and the frames the grid's y dimension
+  const size_t ax = sizeof(TI) * 4, ay = sizeof(TO) * 4;
+  if (C % 4 || W % 4 || H % 2 || reinterpret_cast<uintptr_t>(x) % ax || reinterpret_cast<uintptr_t>(y) % ay ||
+      (long long)H * W * C >= (1LL << 31) || F > 65535)
+    return false;
   switch (ks) {
     case 3: e = run_dwconv_blocked<3, TI, TO>(x, F, H, W, C, kw, bias, y, s); return true;
     case 5: e = run_dwconv_blocked<5, TI, TO>(x, F, H, W, C, kw, bias, y, s); return true;

@@ -112,6 +112,10 @@ def test_frame_mean_and_depthwise_conv(mods, shape):
         yb = S.depthwise_conv(xb, _dev(p["kernel"]), _dev(p["bias"]), out_dtype=torch.float32)
         refb = O.depthwise_conv2d_same(to_np(xb).reshape(B * T, H, W, C), p).reshape(x.shape)
         assert rel_err(to_np(yb), refb) < 5e-6, ks
+        # bf16 out: the fp32 result rounded once to nearest even
+        ybb = S.depthwise_conv(xb, _dev(p["kernel"]), _dev(p["bias"]), out_dtype=torch.bfloat16)
+        assert ybb.dtype == torch.bfloat16
+        assert bf16_excess_err(to_np(ybb), refb) < 2e-5, ks
 
 
 @pytest.mark.parametrize("gate_type", ["factored", "dense", "channel", "scalar"])
