@@ -304,7 +304,7 @@ def main():
     args = parse()
     if args.gpus != 1:
         print(f"bench.py measures one GPU: this build has no multi-GPU path (asked for --gpus {args.gpus}); "
-              "the layer shards over batch with no exchange (DESIGN.md, sharding)", file=sys.stderr)
+              "the layer shards over batch with no exchange between GPUs", file=sys.stderr)
         sys.exit(2)
     import torch
     if not torch.cuda.is_available():

@@ -22,7 +22,8 @@ ARCH = os.environ.get("CSSM_OFFLOAD_ARCH", "gfx950")
 
 HIPCC_FLAGS = [
     "-O3", "-std=c++17", "-fPIC", f"--offload-arch={ARCH}",
-    # packed FP32 VALU ops are disabled on this target
+    # packed FP32 VALU ops (v_pk_*_f32) are disabled: their results have been unreliable on this
+    # device pool; hipcc's host pass warns that it does not know the feature (harmless)
     "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",
     "-munsafe-fp-atomics", "-Wall", "-Wno-unused-function",
     "-I", os.path.join(ROOT, "include"),
