@@ -109,7 +109,7 @@ __device__ __forceinline__ float gate_act(float x, int act) {
   return softplus_f(x);
 }
 
-__global__ void gated_gates_kernel(const float* __restrict__ ctx, int C, int H, int W, int factored,
+__global__ void __launch_bounds__(1024) gated_gates_kernel(const float* __restrict__ ctx, int C, int H, int W, int factored,
                                    int act, GateWeights gw, float c_scale, float4* __restrict__ out) {
   extern __shared__ float sm_f[];
   const int WF = W / 2 + 1;
@@ -267,10 +267,13 @@ hipError_t launch_gated_gates(const float* ctx, int BT, int C, int H, int W, int
                               const GateWeights& w, float c_scale, float4* gates, hipStream_t s) {
   const int WF = W / 2 + 1;
   const int nv = 3 * (H + WF);
-  const int P = nv >= 256 ? 1 : 256 / nv;   // partial sums per factored product (see the kernel)
+  // 1024 threads per frame: the factored products split over P = 1024 / nv threads each, which
+  // keeps each thread's chain of dependent loads + FMAs at C / P (latency, not arithmetic, bounds it)
+  constexpr int NT = 1024;
+  const int P = nv >= NT ? 1 : NT / nv;   // partial sums per factored product (see the kernel)
   const size_t shm = (size_t(C) + size_t(nv) * (1 + P)) * sizeof(float);
   if (shm > 64 * 1024) return hipErrorInvalidValue;
-  hipLaunchKernelGGL(gated_gates_kernel, dim3(BT), dim3(256), shm, s, ctx, C, H, W, factored, act, w,
+  hipLaunchKernelGGL(gated_gates_kernel, dim3(BT), dim3(NT), shm, s, ctx, C, H, W, factored, act, w,
                      c_scale, gates);
   return hipGetLastError();
 }
