@@ -522,17 +522,18 @@ __device__ float dot_col(const float* ctx, const float* k, int C, int n, int col
   return acc;
 }
 
-__global__ void __launch_bounds__(256)
+__global__ void __launch_bounds__(1024)
 gdn_gates_kernel(const float* __restrict__ ctx_in, int T, int C, int H, int W, int nh, GdnGateWeights w,
                  int temporal, float rope_base, const float* __restrict__ ttable, float2* __restrict__ ab,
                  float2* __restrict__ bkv) {
   extern __shared__ float sm[];
   const int bt = blockIdx.x, t = bt % T;
   const int WF = W / 2 + 1;
+  const int CW = W > WF ? W : WF;
   float* cx = sm;                 // C
   float* rows = sm + C;           // 4 x H
   float* cols = rows + 4 * H;     // 4 x max(W, WF)
-  const int CW = W > WF ? W : WF;
+  float* part = cols + 4 * CW;    // factored: P partial sums of each of the 4 (H + CW) products
   for (int c = threadIdx.x; c < C; c += blockDim.x) {
     float v = ctx_in[size_t(bt) * C + c];
     if (temporal == 1) {
@@ -546,15 +547,34 @@ gdn_gates_kernel(const float* __restrict__ ctx_in, int T, int C, int H, int W, i
     cx[c] = v;
   }
   __syncthreads();
-  // gate g in {0 alpha, 1 beta, 2 B_k, 3 B_v}; spectral gates span (H, WF), spatial (H, W)
-  for (int g = 0; g < 4; ++g) {
-    if (!w.kd[g]) continue;
-    if (w.kind == 1) {
+  // gate g in {0 alpha, 1 beta, 2 B_k, 3 B_v}; spectral gates span (H, WF), spatial (H, W).
+  // Factored: the row / column products of all four gates at once, product q = g (H + CW) + i,
+  // each split over P threads (channel stride P) whose partials are summed in order.
+  if (w.kind == 1) {
+    const int NV = 4 * (H + CW);
+    const int P = NV >= int(blockDim.x) ? 1 : int(blockDim.x) / NV;
+    for (int e = threadIdx.x; e < NV * P; e += blockDim.x) {
+      const int q = e % NV, pc = e / NV;
+      const int g = q / (H + CW), i = q % (H + CW);
       const int nc = g < 2 ? WF : W;
-      for (int i = threadIdx.x; i < H + nc; i += blockDim.x) {
-        if (i < H) rows[g * H + i] = dot_col(cx, w.kd[g], C, H, i) + w.bd[g][i];
-        else cols[g * CW + i - H] = dot_col(cx, w.kw[g], C, nc, i - H) + w.bw[g][i - H];
+      float acc = 0.0f;
+      if (w.kd[g] && (i < H || i - H < nc)) {
+        const float* k = i < H ? w.kd[g] + i : w.kw[g] + (i - H);
+        const int n = i < H ? H : nc;
+#pragma unroll 4
+        for (int c = pc; c < C; c += P) acc = fmaf(cx[c], k[size_t(c) * n], acc);
       }
+      part[pc * NV + q] = acc;
+    }
+    __syncthreads();
+    for (int q = threadIdx.x; q < NV; q += blockDim.x) {
+      const int g = q / (H + CW), i = q % (H + CW);
+      const int nc = g < 2 ? WF : W;
+      if (!w.kd[g] || (i >= H && i - H >= nc)) continue;
+      float acc = i < H ? w.bd[g][i] : w.bw[g][i - H];
+      for (int pc = 0; pc < P; ++pc) acc += part[pc * NV + q];
+      if (i < H) rows[g * H + i] = acc;
+      else cols[g * CW + i - H] = acc;
     }
   }
   __syncthreads();
@@ -584,10 +604,12 @@ gdn_gates_kernel(const float* __restrict__ ctx_in, int T, int C, int H, int W, i
 hipError_t launch_gdn_gates(const float* ctx, int B, int T, int C, int H, int W, int nh, const GdnGateWeights& w,
                             int temporal, float rope_base, const float* ttable, float2* ab, float2* bkv,
                             hipStream_t s) {
-  const int WF = W / 2 + 1;
-  const size_t sm = sizeof(float) * (size_t(C) + 4 * size_t(H) + 4 * size_t(W > WF ? W : WF));
+  const int WF = W / 2 + 1, CW = W > WF ? W : WF;
+  constexpr int NT = 1024;
+  const int NV = 4 * (H + CW), P = w.kind == 1 ? (NV >= NT ? 1 : NT / NV) : 0;
+  const size_t sm = sizeof(float) * (size_t(C) + 4 * size_t(H) + 4 * size_t(CW) + size_t(P) * NV);
   if (sm > 64 * 1024) return hipErrorInvalidValue;
-  hipLaunchKernelGGL(gdn_gates_kernel, dim3(unsigned(B * T)), dim3(256), sm, s, ctx, T, C, H, W, nh, w, temporal,
+  hipLaunchKernelGGL(gdn_gates_kernel, dim3(unsigned(B * T)), dim3(NT), sm, s, ctx, T, C, H, W, nh, w, temporal,
                      rope_base, ttable, ab, bkv);
   return hipGetLastError();
 }
