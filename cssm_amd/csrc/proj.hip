@@ -264,7 +264,10 @@ proj_persist_kernel(const TI* __restrict__ A, int M, int K, int N, const float* 
   constexpr int BP = TN + 16;
   constexpr int KP = KMAX + 8;                            // SPLIT: bf16 pitch of the k-contiguous rows
   constexpr int KB = KMAX / 32;                           // SPLIT: bf16 MFMA k-blocks
-  constexpr int A_FLOATS = SPLIT ? 3 * TM * KP / 2 : (PLANE_A ? KMAX * AP : TM * AP);   // SPLIT: 3 bf16 planes
+  // SPLIT with bf16 A: A is exactly its first bf16 part, so one plane and three products
+  constexpr bool A1_ONLY = SPLIT && sizeof(TI) == 2;
+  constexpr int APL = A1_ONLY ? 1 : 3;
+  constexpr int A_FLOATS = SPLIT ? APL * TM * KP / 2 : (PLANE_A ? KMAX * AP : TM * AP);   // SPLIT: APL bf16 planes
   constexpr int OP = TN + 4;                              // output staging pitch (channels-last out)
   constexpr int AS_FLOATS = (!OUT_SPLIT && TM * OP > A_FLOATS) ? TM * OP : A_FLOATS;  // staging reuses As
   constexpr int PF = TM * KMAX / 4 / NT;                 // float4 of A prefetched per thread
@@ -272,7 +275,7 @@ proj_persist_kernel(const TI* __restrict__ A, int M, int K, int N, const float* 
   __shared__ __attribute__((aligned(16))) float Bs[SPLIT ? 1 : KMAX * BP];
   // SPLIT views: the three A planes [TM][KP] as bf16
   __bf16* const A1 = reinterpret_cast<__bf16*>(As);
-  __bf16* const A2 = A1 + TM * KP;
+  __bf16* const A2 = A1 + TM * KP;   // (SPLIT, fp32 A only)
   __bf16* const A3 = A2 + TM * KP;
   __shared__ float rowsc[NORM ? 2 * TM : 1];             // per-pixel (scale, mean) of the norm
   __shared__ float2 gsh[TT > 0 ? TM : 1];                 // qkv epilogue: the tile's input gates
@@ -368,16 +371,19 @@ proj_persist_kernel(const TI* __restrict__ A, int M, int K, int N, const float* 
           for (int e = 0; e < 8; ++e) {
             const float4 v = pf[c8 * 8 + e];
             const float x = q == 0 ? v.x : (q == 1 ? v.y : (q == 2 ? v.z : v.w));
-            __bf16 x1, x2, x3;
-            split3_bf16(x, x1, x2, x3);
+            __bf16 x1, x2 = __bf16(0.0f), x3 = __bf16(0.0f);
+            if constexpr (A1_ONLY) x1 = (__bf16)x;   // exact for bf16 inputs
+            else split3_bf16(x, x1, x2, x3);
             v1[e] = x1;
             v2[e] = x2;
             v3[e] = x3;
           }
           const int o = (r4 + q) * KP + k0 + c8 * 8;
           *reinterpret_cast<bf16x8*>(&A1[o]) = v1;
-          *reinterpret_cast<bf16x8*>(&A2[o]) = v2;
-          *reinterpret_cast<bf16x8*>(&A3[o]) = v3;
+          if constexpr (!A1_ONLY) {
+            *reinterpret_cast<bf16x8*>(&A2[o]) = v2;
+            *reinterpret_cast<bf16x8*>(&A3[o]) = v3;
+          }
         }
       }
       return;
@@ -392,16 +398,19 @@ proj_persist_kernel(const TI* __restrict__ A, int M, int K, int N, const float* 
         bf16x4 v1, v2, v3;
 #pragma unroll
         for (int e = 0; e < 4; ++e) {
-          __bf16 x1, x2, x3;
-          split3_bf16(x[e], x1, x2, x3);
+          __bf16 x1, x2 = __bf16(0.0f), x3 = __bf16(0.0f);
+          if constexpr (A1_ONLY) x1 = (__bf16)x[e];   // exact for bf16 inputs
+          else split3_bf16(x[e], x1, x2, x3);
           v1[e] = x1;
           v2[e] = x2;
           v3[e] = x3;
         }
         const int o = r * KP + k4;
         *reinterpret_cast<bf16x4*>(&A1[o]) = v1;
-        *reinterpret_cast<bf16x4*>(&A2[o]) = v2;
-        *reinterpret_cast<bf16x4*>(&A3[o]) = v3;
+        if constexpr (!A1_ONLY) {
+          *reinterpret_cast<bf16x4*>(&A2[o]) = v2;
+          *reinterpret_cast<bf16x4*>(&A3[o]) = v3;
+        }
       }
       return;
     }
@@ -505,17 +514,28 @@ proj_persist_kernel(const TI* __restrict__ A, int M, int K, int N, const float* 
         for (int i = 0; i < MI; ++i) {
           const int o = ((wm * MI + i) * 16 + (lane & 15)) * KP + koff;
           const bf16x8 a1 = *reinterpret_cast<const bf16x8*>(&A1[o]);
-          const bf16x8 a2 = *reinterpret_cast<const bf16x8*>(&A2[o]);
-          const bf16x8 a3 = *reinterpret_cast<const bf16x8*>(&A3[o]);
+          if constexpr (A1_ONLY) {
+            // the three products with A's one nonzero part, in the six-product order
 #pragma unroll
-          for (int j = 0; j < 2; ++j) {
-            floatx4 c = acc[i][j];
-            c = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a3, b1[j][kb], c, 0, 0, 0);   // small terms first
-            c = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a2, b2[j][kb], c, 0, 0, 0);
-            c = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a1, b3[j][kb], c, 0, 0, 0);
-            c = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a2, b1[j][kb], c, 0, 0, 0);
-            c = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a1, b2[j][kb], c, 0, 0, 0);
-            acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a1, b1[j][kb], c, 0, 0, 0);
+            for (int j = 0; j < 2; ++j) {
+              floatx4 c = acc[i][j];
+              c = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a1, b3[j][kb], c, 0, 0, 0);
+              c = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a1, b2[j][kb], c, 0, 0, 0);
+              acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a1, b1[j][kb], c, 0, 0, 0);
+            }
+          } else {
+            const bf16x8 a2 = *reinterpret_cast<const bf16x8*>(&A2[o]);
+            const bf16x8 a3 = *reinterpret_cast<const bf16x8*>(&A3[o]);
+#pragma unroll
+            for (int j = 0; j < 2; ++j) {
+              floatx4 c = acc[i][j];
+              c = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a3, b1[j][kb], c, 0, 0, 0);   // small terms first
+              c = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a2, b2[j][kb], c, 0, 0, 0);
+              c = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a1, b3[j][kb], c, 0, 0, 0);
+              c = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a2, b1[j][kb], c, 0, 0, 0);
+              c = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a1, b2[j][kb], c, 0, 0, 0);
+              acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a1, b1[j][kb], c, 0, 0, 0);
+            }
           }
         }
       }
