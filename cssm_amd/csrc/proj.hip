@@ -48,6 +48,12 @@ __device__ __forceinline__ float act_acc(float x, int act) {
   if (act == 2) return 1.0f / (1.0f + expf(-x));
   return x;
 }
+// orders one wave's LDS accesses across its lanes (the region is private to the wave)
+__device__ __forceinline__ void wave_fence() {
+  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+  __builtin_amdgcn_wave_barrier();
+  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+}
 // buffer resource over [p, p + bytes): raw buffer loads beyond it return 0
 __device__ __forceinline__ __amdgpu_buffer_rsrc_t make_rsrc(const void* p, unsigned bytes) {
   return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(p), 0, int(bytes), 0x00020000);
@@ -1055,10 +1061,11 @@ proj_kc_kernel(const TI* __restrict__ A, int M, int K, int N, const float* __res
     const int rfr = row0 / HW, rpx = row0 % HW;   // frame / pixel of row0
 #pragma unroll
     for (int j = 0; j < 2; ++j) {
+      if (j > 0) wave_fence();   // every lane has read n-tile j - 1 before it is overwritten
 #pragma unroll
       for (int i = 0; i < MI; ++i)
         *reinterpret_cast<floatx4*>(&stg[(lane & 15) * SPC + i * 16 + (lane >> 4) * 4]) = acc[i][j];
-      // same-wave LDS writes and reads execute in order
+      wave_fence();              // the wave's writes are visible to its other lanes
 #pragma unroll
       for (int cp = 0; cp < 16 / CPI; ++cp) {
         const int cl = CPI * cp + half;
