@@ -6,7 +6,8 @@ of one 128x128x64 image repeated over T = 8 frames (materialised; the kernels
 do not see the repetition), x ~ N(0, 1), kernel_size 11, factored B/C/Delta
 gates, softplus Delta, no short convolutions, random-init weights with
 N(0, 0.1^2) biases (synthetic data).  ``--workload`` selects the other
-BASELINE configs (c1, c3, c4, c5); they are measured the same way.
+BASELINE configs as the headline; by default the others (c1, c3, c4, c5) are
+measured in the same run, each the same way, and reported under "configs".
 
 A step is one full layer forward with x already in HBM:
   gated: in_proj GEMM (plane-major split + SiLU + spatial-mean epilogue) ->
@@ -22,8 +23,10 @@ B*T*(3*H*W*C*s + 3*(H+W/2+1)*4) + C*H*(W/2+1)*8 (read u and z, write y, read the
 factored gate vectors, K_hat once).  gdn: the spectral core (rfft2 + scan +
 irfft2 launches together), B*T*(4*H*W*C*s + 2*(H+W/2+1)*4) + n_h*H*(W/2+1)*8
 (read q, k, v, write o, gates, W_hat once).  s = bytes per I/O element.
-cpu_baseline times the float64 numpy restatement (oracle/) of the same layer
-on a bounded slice of the batch, on one host thread.
+cpu_baseline times the float32 torch-CPU restatement (oracle/cssm_cpu_fp32.py)
+of the same layer on a batch slice, on the process's host-core share (warmup 5,
+median of up to 20 calls for the headline; warmup 1 and a shorter budget for
+the other configs).
 """
 from __future__ import annotations
 
@@ -60,12 +63,17 @@ WORKLOADS = {
 def parse():
     ap = argparse.ArgumentParser(description=__doc__.split("\n\n")[0])
     ap.add_argument("--gpus", type=int, default=1)
-    ap.add_argument("--steps", type=int, default=10)
-    ap.add_argument("--warmup", type=int, default=3)
+    ap.add_argument("--steps", type=int, default=50)
+    ap.add_argument("--warmup", type=int, default=5)
     ap.add_argument("--workload", default="c2", choices=sorted(WORKLOADS))
     ap.add_argument("--batch", type=int, default=0, help="override B (parity/debug runs only)")
+    ap.add_argument("--configs", default="c1,c3,c4,c5",
+                    help="other BASELINE configs measured in the same run and reported under 'configs' "
+                         "(comma-separated; 'none' for the headline workload only)")
+    ap.add_argument("--config-steps", type=int, default=20, help="timed steps of each extra config")
     ap.add_argument("--no-cpu-baseline", action="store_true")
-    ap.add_argument("--cpu-seconds", type=float, default=12.0, help="target CPU baseline wall time")
+    ap.add_argument("--cpu-seconds", type=float, default=20.0,
+                    help="time budget of the headline CPU baseline (a quarter of it for each extra config)")
     ap.add_argument("--traffic", default=None,
                     help="rocprofv3 FETCH/WRITE summary giving HBM bytes per dominant-kernel launch "
                          "(default profiles/<kernel>_<workload>_traffic.txt)")
@@ -233,99 +241,110 @@ def gdn_step(cell, variables, x, w, S, mark):
 
 # ----------------------------------------------------------- CPU baseline
 
-def cpu_baseline(w, seconds):
-    """float64 numpy restatement of the layer (oracle/), one batch element (T frames) at a time."""
-    import numpy as np
-    from oracle import cssm_oracle as O
+CPU_SLICE = {"c1": 8, "c2": 2, "c3": 2, "c4": 8, "c5": 16}   # batch elements the CPU baseline runs
+
+
+def cpu_threads():
+    """Host threads for the CPU baseline: the process's CPU share (OMP_NUM_THREADS when set,
+    which the GPU boxes set to the one-GPU share, else the affinity mask)."""
     try:
-        from threadpoolctl import threadpool_limits
-        limiter = threadpool_limits(limits=1)
-    except Exception:          # threadpoolctl absent: numpy's FFT is single-threaded anyway
-        limiter = None
+        n = len(os.sched_getaffinity(0))
+    except AttributeError:
+        n = os.cpu_count() or 1
+    env = os.environ.get("OMP_NUM_THREADS", "")
+    return max(1, min(n, int(env))) if env.isdigit() and int(env) > 0 else n
+
+
+def cpu_model():
+    try:
+        with open("/proc/cpuinfo") as f:
+            for line in f:
+                if line.startswith("model name"):
+                    return line.split(":", 1)[1].strip()
+    except OSError:
+        pass
+    return platform.processor() or platform.machine()
+
+
+def cpu_baseline(w, budget_s, warmup, max_repeats):
+    """The float32 torch-CPU restatement of the layer (oracle/cssm_cpu_fp32.py) on the host's
+    cores: one batch slice of the workload, `warmup` untimed calls, then timed calls until
+    `max_repeats` or the time budget (at least 3); the median call gives frames/s."""
+    import numpy as np
+    import torch
+    from oracle import cssm_oracle as O
+    from oracle import cssm_cpu_fp32 as P
+    n = cpu_threads()
+    prev = torch.get_num_threads()
+    torch.set_num_threads(n)
     rng = np.random.default_rng(1)
-    T, H, W, C = w["T"], w["H"], w["W"], w["C"]
+    gen = torch.Generator().manual_seed(0)
+    Bs = min(CPU_SLICE.get(w["key"], 2), w["B"])
+    T = w["T"]
     if w["cell"] == "stack":
         layers = []
-        for h, c, n in w["stages"]:
+        for h, c, nl in w["stages"]:
             cfg = O.GatedConfig(channels=c, expand=w["expand"], kernel_size=w["kernel_size"],
                                 gate_type=w["gate_type"], short_conv_size=0, short_conv_spatial_size=0)
-            layers += [(O.init_params(O.gated_param_shapes(cfg, c, h, h), rng), cfg, h, c) for _ in range(n)]
-        xs = {(h, c): rng.standard_normal((1, T, h, h, c)) for _, _, h, c in layers}
+            for _ in range(nl):
+                prm = O.init_params(O.gated_param_shapes(cfg, c, h, h), rng)
+                layers.append((P.GatedCPU(prm, c, expand=w["expand"], kernel_size=w["kernel_size"],
+                                          gate_type=w["gate_type"]), h, c))
+        xs = {(h, c): torch.randn((Bs, T, h, h, c), generator=gen) for _, h, c in layers}
 
-        def run(_):
-            for p_, cfg_, h_, c_ in layers:
-                O.gated_forward(p_, xs[(h_, c_)], cfg_)
-        x = None
-        frames, t0 = 0, time.perf_counter()
-        while True:
-            run(x)
-            frames += T
-            el = time.perf_counter() - t0
-            if el >= seconds:
-                break
-        if limiter is not None and hasattr(limiter, "unregister"):
-            limiter.unregister()
-        return dict(value=frames / el, unit="frames/s", cores=1, kind="port",
-                    sample=f"{frames // T} batch element(s) (of B={w['B']}) through all "
-                           f"{len(layers)} layers, float64 numpy oracle, {el:.1f} s, "
-                           f"{platform.processor() or platform.machine()} x{os.cpu_count()} logical cpus")
-    if w["cell"] == "gated":
-        cfg = O.GatedConfig(channels=C, expand=w["expand"], kernel_size=w["kernel_size"], gate_type=w["gate_type"],
-                            short_conv_size=0, short_conv_spatial_size=0)
-        p = O.init_params(O.gated_param_shapes(cfg, C, H, W), rng)
-        run = lambda x: O.gated_forward(p, x, cfg)                                   # noqa: E731
+        def run():
+            for cell, h, c in layers:
+                cell(xs[(h, c)])
+        what = f"{len(layers)} layers"
     else:
-        cfg = O.GDNConfig(channels=C, delta_key_dim=w["dk"], kernel_size=w["kernel_size"], gate_type=w["gate_type"],
-                          qkv_conv_size=w["qkv_conv_size"])
-        p = O.init_params(O.gdn_param_shapes(cfg, H, W), rng, spectral_init="xavier")
-        run = lambda x: O.gdn_forward(p, x, cfg, scan="rank1")                       # noqa: E731
-    if w["data"] == "repeat":
-        x = np.repeat(rng.standard_normal((1, 1, H, W, C)), T, axis=1)
-    else:
-        x = rng.standard_normal((1, T, H, W, C))
-    frames, t0 = 0, time.perf_counter()
-    while True:
-        run(x)
-        frames += T
-        el = time.perf_counter() - t0
-        if el >= seconds:
-            break
-    if limiter is not None and hasattr(limiter, "unregister"):
-        limiter.unregister()
-    return dict(value=frames / el, unit="frames/s", cores=1, kind="port",
-                sample=f"{frames // T} batch element(s) x T={T} (of B={w['B']}), full C={C} at {H}x{W}, "
-                       f"float64 numpy oracle, {el:.1f} s, {platform.processor() or platform.machine()} "
-                       f"x{os.cpu_count()} logical cpus")
+        H, W, C = w["H"], w["W"], w["C"]
+        if w["cell"] == "gated":
+            cfg = O.GatedConfig(channels=C, expand=w["expand"], kernel_size=w["kernel_size"],
+                                gate_type=w["gate_type"], short_conv_size=0, short_conv_spatial_size=0)
+            cell = P.GatedCPU(O.init_params(O.gated_param_shapes(cfg, C, H, W), rng), C, expand=w["expand"],
+                              kernel_size=w["kernel_size"], gate_type=w["gate_type"])
+        else:
+            cfg = O.GDNConfig(channels=C, delta_key_dim=w["dk"], kernel_size=w["kernel_size"],
+                              gate_type=w["gate_type"], qkv_conv_size=w["qkv_conv_size"])
+            cell = P.GdnCPU(O.init_params(O.gdn_param_shapes(cfg, H, W), rng, spectral_init="xavier"), C, w["dk"],
+                            qkv_conv_size=w["qkv_conv_size"])
+        if w["data"] == "repeat":
+            x = torch.randn((Bs, 1, H, W, C), generator=gen).expand(Bs, T, H, W, C).contiguous()
+        else:
+            x = torch.randn((Bs, T, H, W, C), generator=gen)
+        if w["io"] == "bf16":
+            x = x.bfloat16().float()
+
+        def run():
+            cell(x)
+        what = f"{H}x{W}x{C}"
+    times = []
+    with torch.inference_mode():
+        for _ in range(warmup):
+            run()
+        t_all = time.perf_counter()
+        while len(times) < max_repeats and (len(times) < 3 or time.perf_counter() - t_all < budget_s):
+            t0 = time.perf_counter()
+            run()
+            times.append(time.perf_counter() - t0)
+    torch.set_num_threads(prev)
+    med = sorted(times)[len(times) // 2]
+    return dict(value=Bs * T / med, unit="frames/s", cores=n, kind="port",
+                sample=f"float32 torch-CPU restatement of the layer (oracle/cssm_cpu_fp32.py), batch slice "
+                       f"B'={Bs} of B={w['B']} (T={T}, {what}), warmup {warmup}, median of {len(times)} timed "
+                       f"calls ({med * 1e3:.1f} ms per call), {n} threads on {cpu_model()} "
+                       f"(os.cpu_count()={os.cpu_count()})")
 
 
 # ------------------------------------------------------------------- main
 
-def main():
-    args = parse()
-    if args.gpus != 1:
-        print(f"bench.py measures one GPU: this build has no multi-GPU path (asked for --gpus {args.gpus}); "
-              "the layer shards over batch with no exchange between GPUs", file=sys.stderr)
-        sys.exit(2)
-    import torch
-    if not torch.cuda.is_available():
-        print("bench.py needs a GPU", file=sys.stderr)
-        sys.exit(1)
-    from cssm_amd import cells, spectral as S
-
-    w = dict(WORKLOADS[args.workload])
+def run_workload(key, args, torch, cells, S, headline):
+    """One workload on the GPU: warmup, `steps` timed layer forwards, per-kernel HIP-event times;
+    returns the result dict (the bench line's keys for the headline, a compact record otherwise)."""
+    w = dict(WORKLOADS[key], key=key)
     B = args.batch or w["B"]
     T, H, W = w["T"], w["H"], w["W"]
     dev = "cuda"
-    if args.copy_calibration > 0:
-        # a streaming kernel of known traffic (read n*4 B, write n*4 B): torch's neg, which
-        # nothing else in this run launches, so its dispatch is easy to find in the counters
-        n = args.copy_calibration // 4
-        src = torch.ones(n, dtype=torch.float32, device=dev)
-        dst = torch.empty_like(src)
-        torch.cuda.synchronize()
-        torch.neg(src, out=dst)
-        torch.cuda.synchronize()
-        del src, dst
     torch.manual_seed(0)
     cell = make_cell(w, cells)
     if w["cell"] == "stack":
@@ -340,19 +359,20 @@ def main():
         randomise_biases(variables, torch, dev)
     step = {"gated": gated_step, "gdn": gdn_step, "stack": stack_step}[w["cell"]]
     core = ("scan",) if w["cell"] in ("gated", "stack") else ("rfft2", "scan_bins", "irfft2")
+    steps = args.steps if headline else max(1, args.config_steps)
 
     for _ in range(args.warmup):
         step(cell, variables, x, w, S, Marks(torch, False))
     torch.cuda.synchronize()
     marks = []
     t0 = time.perf_counter()
-    for _ in range(args.steps):
+    for _ in range(steps):
         m = Marks(torch, True)
         step(cell, variables, x, w, S, m)
         marks.append(m)
     torch.cuda.synchronize()
     el = time.perf_counter() - t0
-    ms_step = el * 1e3 / args.steps
+    ms_step = el * 1e3 / steps
     # the instrumented step must equal the module's forward bit for bit
     if w["cell"] == "stack":
         ref = None
@@ -363,8 +383,7 @@ def main():
     else:
         ref = cell.apply(variables, x)
     if not torch.equal(step(cell, variables, x, w, S, Marks(torch, False)), ref):
-        print("instrumented step differs from the module's apply", file=sys.stderr)
-        sys.exit(1)
+        raise RuntimeError(f"{key}: instrumented step differs from the module's apply")
     kern_ms = {}
     for m in marks:
         for name, a, b in m.spans():
@@ -373,44 +392,96 @@ def main():
     alg = algorithmic_bytes(w, B)
     achieved = alg / (core_ms * 1e-3) / 1e9
     kname = "gdn_core" if w["cell"] == "gdn" else "gated_scan"
-    tpath = args.traffic or os.path.join(ROOT, "profiles", f"{kname}_{args.workload}_traffic.txt")
+    tpath = args.traffic if (headline and args.traffic) else \
+        os.path.join(ROOT, "profiles", f"{kname}_{key}_traffic.txt")
     traffic = read_traffic(tpath) if B == w["B"] else None
     Ci = w["C"] * w.get("expand", 1)
+    del x, variables, ref, cell, marks
+    torch.cuda.empty_cache()
+    data = {"repeat": f"synthetic: one N(0,1) {H}x{W}x{w['C']} image repeated over T={T} (materialised)",
+            "normal": f"synthetic: N(0,1) {H}x{W}x{w['C']} frames, T={T}",
+            "dots": f"synthetic: 2% moving dots = 1.0 on N(0,0.01^2) background, {H}x{W}x{w['C']}, "
+                    f"T={T}"}[w["data"]] + ", random-init weights"
+    config = {"workload": w["name"], "cell": w["cell"], "batch": B, "T": T, "H": H, "W": W,
+              "channels": w["C"], "inner_channels": Ci, "kernel_size": w["kernel_size"],
+              "gate_type": w["gate_type"], "io": w["io"], "step": "full layer forward x -> out"}
+    if w["cell"] == "gdn":
+        config.update(delta_key_dim=w["dk"], qkv_conv_size=w["qkv_conv_size"])
+    if w["cell"] == "stack":
+        config.update(stages=[{"H": h, "W": h, "channels": c, "inner_channels": c * w["expand"], "layers": n}
+                              for h, c, n in w["stages"]], layers=sum(n for _, _, n in w["stages"]))
+        for k in ("H", "W", "channels", "inner_channels"):
+            config.pop(k)
+    roof = {"kernel": kname, "launches": list(core), "bound": "hbm", "achieved": achieved,
+            "peak": HBM_PEAK_GBS, "unit": "GB/s", "frac": achieved / HBM_PEAK_GBS,
+            "algorithmic_bytes": alg, "traffic": traffic}
     res = {
         "metric": METRIC,
         "value": B * T / (ms_step * 1e-3),
         "unit": "frames/s",
         "n_gpus": 1,
-        "steps": args.steps,
+        "steps": steps,
         "warmup": args.warmup,
         "ms_per_step": ms_step,
         "higher_is_better": True,
         "scaling": "weak",
         "vs_baseline": None,
+        # the arithmetic runs in float32 (FFT passes, recurrence, split-bf16 MFMA products at
+        # float32 level) whatever the I/O dtype; io_dtype is what x and the output are stored in
         "dtype": "f32",
-        "data": {"repeat": f"synthetic: one N(0,1) {H}x{W}x{w['C']} image repeated over T={T} (materialised)",
-                 "normal": f"synthetic: N(0,1) {H}x{W}x{w['C']} frames, T={T}",
-                 "dots": f"synthetic: 2% moving dots = 1.0 on N(0,0.01^2) background, {H}x{W}x{w['C']}, "
-                         f"T={T}"}[w["data"]] + ", random-init weights",
-        "config": {"workload": w["name"], "cell": w["cell"], "batch": B, "T": T, "H": H, "W": W,
-                   "channels": w["C"], "inner_channels": Ci, "kernel_size": w["kernel_size"],
-                   "gate_type": w["gate_type"], "io": w["io"], "step": "full layer forward x -> out"},
+        "io_dtype": w["io"],
+        "data": data,
+        "config": config,
         "images_per_s": B / (ms_step * 1e-3),
         "kernel_ms": {k: round(v, 4) for k, v in kern_ms.items()},
+        "core_ms": round(core_ms, 4),
         "core_frames_per_s": B * T / (core_ms * 1e-3),
-        "roofline": {"kernel": kname, "launches": list(core), "bound": "hbm", "achieved": achieved,
-                     "peak": HBM_PEAK_GBS, "unit": "GB/s", "frac": achieved / HBM_PEAK_GBS,
-                     "algorithmic_bytes": alg, "traffic": traffic},
+        "roofline": roof,
     }
-    if w["cell"] == "gdn":
-        res["config"].update(delta_key_dim=w["dk"], qkv_conv_size=w["qkv_conv_size"])
-    if w["cell"] == "stack":
-        res["config"].update(stages=[{"H": h, "W": h, "channels": c, "inner_channels": c * w["expand"], "layers": n}
-                                     for h, c, n in w["stages"]], layers=sum(n for _, _, n in w["stages"]))
-        for k in ("H", "W", "channels", "inner_channels"):
-            res["config"].pop(k)
     if not args.no_cpu_baseline:
-        res["cpu_baseline"] = cpu_baseline(w, args.cpu_seconds)
+        if headline:
+            res["cpu_baseline"] = cpu_baseline(w, budget_s=args.cpu_seconds, warmup=5, max_repeats=20)
+        else:
+            res["cpu_baseline"] = cpu_baseline(w, budget_s=args.cpu_seconds / 4, warmup=1, max_repeats=20)
+    if not headline:
+        for k in ("metric", "n_gpus", "higher_is_better", "scaling", "vs_baseline", "warmup"):
+            res.pop(k)
+    return res
+
+
+def main():
+    args = parse()
+    if args.gpus != 1:
+        print(f"bench.py measures one GPU: this build has no multi-GPU path (asked for --gpus {args.gpus}); "
+              "the layer shards over batch with no exchange between GPUs", file=sys.stderr)
+        sys.exit(2)
+    import torch
+    if not torch.cuda.is_available():
+        print("bench.py needs a GPU", file=sys.stderr)
+        sys.exit(1)
+    from cssm_amd import cells, spectral as S
+
+    if args.copy_calibration > 0:
+        # a streaming kernel of known traffic (read n*4 B, write n*4 B): torch's neg, which
+        # nothing else in this run launches, so its dispatch is easy to find in the counters
+        n = args.copy_calibration // 4
+        src = torch.ones(n, dtype=torch.float32, device="cuda")
+        dst = torch.empty_like(src)
+        torch.cuda.synchronize()
+        torch.neg(src, out=dst)
+        torch.cuda.synchronize()
+        del src, dst
+    extra = [] if args.configs in ("", "none") else [k for k in args.configs.split(",") if k != args.workload]
+    for k in extra:
+        if k not in WORKLOADS:
+            print(f"unknown workload {k!r} in --configs (have {sorted(WORKLOADS)})", file=sys.stderr)
+            sys.exit(2)
+    res = run_workload(args.workload, args, torch, cells, S, headline=True)
+    if extra:
+        res["configs"] = {}
+        for k in extra:
+            print(f"bench: workload {k}", file=sys.stderr, flush=True)
+            res["configs"][k] = run_workload(k, args, torch, cells, S, headline=False)
     print(json.dumps(res), flush=True)
 
 

@@ -35,6 +35,31 @@ def _lecun_normal(shape, fan_in, gen, device):
     return t
 
 
+class _DerivedCache:
+    """Buffers derived from parameter tensors (K_hat, W_hat, concatenated gate weights).
+
+    An entry is reused only while its source tensors are the same objects at the
+    same in-place version: a new parameter tree (a reloaded checkpoint, fresh
+    weights) never hits an entry made from an earlier one, even when the
+    allocator hands the new tensors the old addresses.  One entry per slot.
+    """
+
+    def __init__(self):
+        self._slots: Dict[str, Any] = {}
+
+    def get(self, slot: str, sources, extra, make):
+        hit = self._slots.get(slot)
+        if hit is not None:
+            srcs, vers, ex, val = hit
+            if (ex == extra and len(srcs) == len(sources)
+                    and all(a is b for a, b in zip(srcs, sources))
+                    and vers == tuple(t._version for t in sources)):
+                return val
+        val = make()
+        self._slots[slot] = (tuple(sources), tuple(t._version for t in sources), extra, val)
+        return val
+
+
 def tree_to_device(tree, device="cuda"):
     """Nested dict of numpy arrays / tensors -> float32 contiguous device tensors."""
     if isinstance(tree, dict):
@@ -83,7 +108,7 @@ class GatedCSSM:
         self.gate_type = gate_type
         self.expand = expand
         self.name = name
-        self._khat_cache: Dict[Any, torch.Tensor] = {}
+        self._cache = _DerivedCache()
 
     # ------------------------------------------------------------- parameters
     def param_shapes(self, c_in: int, H: int, W: int) -> Dict[str, Any]:
@@ -131,14 +156,11 @@ class GatedCSSM:
 
     # ---------------------------------------------------------------- forward
     def spectral_kernel(self, p: Dict[str, Any], H: int, W: int) -> torch.Tensor:
-        """Floored K_hat for (H, W); cached per kernel tensor version."""
+        """Floored K_hat for (H, W); recomputed when the kernel tensor or its version changes."""
         k = p["kernel"]
-        key = (k.data_ptr(), k._version, H, W, self.spectral_rho)
-        kh = self._khat_cache.get(key)
-        if kh is None:
-            kh = S.spectral_kernel(k, H, W, self.spectral_rho, squash=True, goom_floor=True, scan_order=True)
-            self._khat_cache = {key: kh}
-        return kh
+        return self._cache.get("khat", (k,), (H, W, self.spectral_rho),
+                               lambda: S.spectral_kernel(k, H, W, self.spectral_rho, squash=True, goom_floor=True,
+                                                         scan_order=True))
 
     def apply(self, variables: Params, x: torch.Tensor, injected_qkv_spatial=None) -> torch.Tensor:
         """y = GatedCSSM(x); x (B, T, H, W, C) float32 or bfloat16 on the GPU, y same dtype."""
@@ -264,7 +286,7 @@ class GatedDeltaNetCSSM:
         self.dtype = dtype
         self.param_dtype = param_dtype
         self.name = name
-        self._cache: Dict[Any, Any] = {}
+        self._cache = _DerivedCache()
 
     # ------------------------------------------------------------- parameters
     def param_shapes(self, H: int, W: int) -> Dict[str, Any]:
@@ -338,28 +360,20 @@ class GatedDeltaNetCSSM:
 
     # ---------------------------------------------------------------- forward
     def spectral_kernel(self, p: Dict[str, Any], H: int, W: int) -> torch.Tensor:
-        """W_hat (n_h, H, Wf) (cssm.py:4711-4734); cached per kernel tensor version."""
+        """W_hat (n_h, H, Wf) (cssm.py:4711-4734); recomputed when the kernel tensor or its version changes."""
         k = p["kernel"]
-        key = ("what", k.data_ptr(), k._version, H, W, self.spectral_rho)
-        kh = self._cache.get(key)
-        if kh is None:
-            kh = S.spectral_kernel(k, H, W, self.spectral_rho, squash=not self.no_spectral_clamp, goom_floor=False)
-            self._cache = {k_: v for k_, v in self._cache.items() if k_[0] != "what"}
-            self._cache[key] = kh
-        return kh
+        return self._cache.get("what", (k,), (H, W, self.spectral_rho, self.no_spectral_clamp),
+                               lambda: S.spectral_kernel(k, H, W, self.spectral_rho,
+                                                         squash=not self.no_spectral_clamp, goom_floor=False))
 
     def _channel_input_gate_weights(self, p):
-        """B_k | B_v 1x1-conv kernels concatenated to one (C, 2C) Dense (cached)."""
+        """B_k | B_v 1x1-conv kernels concatenated to one (C, 2C) Dense (recomputed when a source changes)."""
         kk, kv = p["B_k"]["kernel"], p["B_v"]["kernel"]
-        key = ("bkv", kk.data_ptr(), kk._version, kv.data_ptr(), kv._version)
-        w = self._cache.get(key)
-        if w is None:
-            C = self.channels
-            w = (torch.cat([kk.reshape(C, C), kv.reshape(C, C)], dim=1).contiguous(),
-                 torch.cat([p["B_k"]["bias"], p["B_v"]["bias"]]).contiguous())
-            self._cache = {k_: v for k_, v in self._cache.items() if k_[0] != "bkv"}
-            self._cache[key] = w
-        return w
+        bk, bv = p["B_k"]["bias"], p["B_v"]["bias"]
+        C = self.channels
+        return self._cache.get("bkv", (kk, kv, bk, bv), None,
+                               lambda: (torch.cat([kk.reshape(C, C), kv.reshape(C, C)], dim=1).contiguous(),
+                                        torch.cat([bk, bv]).contiguous()))
 
     def apply(self, variables: Params, x: torch.Tensor, injected_qkv_spatial=None) -> torch.Tensor:
         """y = GatedDeltaNetCSSM(x); x (B, T, H, W, C) float32 or bfloat16 on the GPU, y same dtype."""

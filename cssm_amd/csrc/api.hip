@@ -34,6 +34,10 @@ int hip_status(hipError_t e, const char* what) {
 
 bool aligned(const void* p, size_t a) { return (reinterpret_cast<uintptr_t>(p) % a) == 0; }
 
+// alignment of the 4-element vector loads / stores the projection kernels make:
+// 16 bytes for float32, 8 for bfloat16
+size_t vec_align(int dtype) { return dtype == CSSM_F32 ? 16 : 8; }
+
 }  // namespace
 
 extern "C" {
@@ -172,6 +176,8 @@ int cssm_proj_in(const void* x, int in_dtype, int F, int HW, int K, int N, const
     return fail(CSSM_ERR_ARG, "cssm_proj_in: dtypes %d/%d", in_dtype, out_dtype);
   if ((act_lo != CSSM_LOAD_IDENTITY && act_lo != CSSM_LOAD_SILU) || (act_hi != CSSM_LOAD_IDENTITY && act_hi != CSSM_LOAD_SILU))
     return fail(CSSM_ERR_ARG, "cssm_proj_in: act_lo=%d act_hi=%d", act_lo, act_hi);
+  if (!aligned(x, vec_align(in_dtype)))
+    return fail(CSSM_ERR_ALIGN, "cssm_proj_in: x must be %zu-byte aligned", vec_align(in_dtype));
   if (out_dtype == CSSM_F32 && (!aligned(out_lo, 16) || !aligned(out_hi, 16)))
     return fail(CSSM_ERR_ALIGN, "cssm_proj_in: f32 outputs must be 16-byte aligned");
   const hipStream_t s = static_cast<hipStream_t>(stream);
@@ -203,6 +209,9 @@ int cssm_proj_out(const void* y, int in_dtype, int F, int HW, int K, int N, cons
   if ((long long)F * HW > 0x7fffffffLL) return fail(CSSM_ERR_SHAPE, "cssm_proj_out: F*HW exceeds 2^31");
   if ((in_dtype != CSSM_F32 && in_dtype != CSSM_BF16) || (out_dtype != CSSM_F32 && out_dtype != CSSM_BF16))
     return fail(CSSM_ERR_ARG, "cssm_proj_out: dtypes %d/%d", in_dtype, out_dtype);
+  if (!aligned(y, vec_align(in_dtype)) || (out_dtype == CSSM_F32 && !aligned(out, 16)))
+    return fail(CSSM_ERR_ALIGN, "cssm_proj_out: y must be %zu-byte aligned, a f32 out 16-byte aligned",
+                vec_align(in_dtype));
   return hip_status(cssm::launch_proj_out(y, in_dtype, F * HW, K, N, kernel, bias, HW, out, out_dtype,
                                           static_cast<hipStream_t>(stream)),
                     "cssm_proj_out");
@@ -238,6 +247,8 @@ int cssm_proj_planes(const void* x, int in_dtype, int F, int HW, int K, int N, c
   if ((long long)F * HW > 0x7fffffffLL) return fail(CSSM_ERR_SHAPE, "cssm_proj_planes: F*HW exceeds 2^31");
   if (!dtype_ok(in_dtype) || !dtype_ok(out_dtype)) return fail(CSSM_ERR_ARG, "cssm_proj_planes: dtypes %d/%d", in_dtype, out_dtype);
   if (act < 0 || act > 2) return fail(CSSM_ERR_ARG, "cssm_proj_planes: act=%d", act);
+  if (!aligned(x, vec_align(in_dtype)))
+    return fail(CSSM_ERR_ALIGN, "cssm_proj_planes: x must be %zu-byte aligned", vec_align(in_dtype));
   if (out_dtype == CSSM_F32 && !aligned(out, 16)) return fail(CSSM_ERR_ALIGN, "cssm_proj_planes: f32 out must be 16-byte aligned");
   return hip_status(cssm::launch_proj_planes(x, in_dtype, F * HW, K, N, kernel, bias, HW, out, out, out_dtype, act, act,
                                              nullptr, N, static_cast<hipStream_t>(stream)),
@@ -344,9 +355,9 @@ int cssm_gdn_qkv_proj(const void* x, int in_dtype, int B, int T, int H, int W, i
     }
   }
   if ((H * W) % 4) return fail(CSSM_ERR_UNSUPPORTED, "cssm_gdn_qkv_proj: H*W=%d must be a multiple of 4", H * W);
-  if (!aligned(qkv, out_dtype == CSSM_F32 ? 16 : 8) || (gate_mode == 1 && !aligned(gates, 8)) ||
-      (gate_mode == 3 && !aligned(gates, 16)))
-    return fail(CSSM_ERR_ALIGN, "cssm_gdn_qkv_proj: misaligned qkv / gates");
+  if (!aligned(x, vec_align(in_dtype)) || !aligned(qkv, vec_align(out_dtype)) ||
+      (gate_mode == 1 && !aligned(gates, 8)) || (gate_mode == 3 && !aligned(gates, 16)))
+    return fail(CSSM_ERR_ALIGN, "cssm_gdn_qkv_proj: misaligned x / qkv / gates");
   return hip_status(cssm::launch_gdn_qkv_proj(x, in_dtype, B, T, H * W, K, C, kernel, bias, kt, sc, gate_mode, gates,
                                               qkv, out_dtype, static_cast<hipStream_t>(stream)),
                     "cssm_gdn_qkv_proj");
@@ -410,7 +421,8 @@ int cssm_gdn_proj_out(const void* o, const void* gate, int in_dtype, int F, int 
   if (!dtype_ok(in_dtype) || !dtype_ok(out_dtype)) return fail(CSSM_ERR_ARG, "cssm_gdn_proj_out: dtypes %d/%d", in_dtype, out_dtype);
   if (norm < CSSM_NORM_NONE || norm > CSSM_NORM_LAYER) return fail(CSSM_ERR_ARG, "cssm_gdn_proj_out: norm=%d", norm);
   const size_t va = in_dtype == CSSM_F32 ? 16 : 8;
-  if (!aligned(o, va) || !aligned(gate, va)) return fail(CSSM_ERR_ALIGN, "cssm_gdn_proj_out: misaligned o / gate");
+  if (!aligned(o, va) || !aligned(gate, va) || (out_dtype == CSSM_F32 && !aligned(out, 16)))
+    return fail(CSSM_ERR_ALIGN, "cssm_gdn_proj_out: misaligned o / gate / out");
   return hip_status(cssm::launch_proj_out_norm_gate(o, gate, in_dtype, F * HW, K, N, norm, norm_scale, norm_bias, kernel,
                                                     bias, HW, out, out_dtype, static_cast<hipStream_t>(stream)),
                     "cssm_gdn_proj_out");

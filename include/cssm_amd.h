@@ -170,6 +170,8 @@ int cssm_gated_scan_fwd(const void* u, const void* z, void* y, int dtype, int B,
  *            bf16 out_lo the sums may be taken before or after its rounding)
  *   workspace  device scratch of cssm_proj_in_workspace_size(F, HW, K, N) bytes
  *              (used only when ctx is requested)
+ * x must be 16-byte aligned (f32) or 8-byte aligned (bf16), f32 outputs 16-byte
+ * aligned (CSSM_ERR_ALIGN otherwise).
  */
 int cssm_proj_in(const void* x, int in_dtype, int F, int HW, int K, int N, const float* kernel,
                  const float* bias, void* out_lo, void* out_hi, int out_dtype, int act_lo, int act_hi,
@@ -185,6 +187,7 @@ size_t cssm_proj_in_workspace_size(int F, int HW, int K, int N);
  *   y       (F, K, HW) plane-major of in_dtype
  *   kernel  (K, N) float32, bias (N)
  *   out     (F * HW, N) channels-last of out_dtype
+ * y must be 16-byte aligned (f32) or 8-byte aligned (bf16), a f32 out 16-byte aligned.
  */
 int cssm_proj_out(const void* y, int in_dtype, int F, int HW, int K, int N, const float* kernel,
                   const float* bias, void* out, int out_dtype, void* stream);
@@ -212,6 +215,7 @@ int cssm_short_conv(const void* x, int in_dtype, int B, int T, int C, int H, int
  *   x      (F * HW, K) channels-last of in_dtype
  *   kernel (K, N) float32, bias (N)
  *   out    (F, N, HW) plane-major of out_dtype; act 0 identity, 1 SiLU, 2 sigmoid
+ * x must be 16-byte aligned (f32) or 8-byte aligned (bf16), a f32 out 16-byte aligned.
  */
 int cssm_proj_planes(const void* x, int in_dtype, int F, int HW, int K, int N, const float* kernel,
                      const float* bias, void* out, int out_dtype, int act, void* stream);
@@ -299,6 +303,7 @@ int cssm_gdn_qkv_post(void* qkv, int dtype, int B, int T, int C, int H, int W, i
  *   kernel (K, 3C) [qkv_proj/kernel], bias (3C) [qkv_proj/bias]
  *   kt, conv_kernel, conv_bias, gate_mode, gates: as cssm_gdn_qkv_post
  *   qkv    (B, T, 3C, H, W) plane-major of out_dtype out
+ * x and qkv must be 16-byte aligned (f32) or 8-byte aligned (bf16); gates 8 (mode 1) or 16 (mode 3).
  */
 int cssm_gdn_qkv_proj(const void* x, int in_dtype, int B, int T, int H, int W, int K, int C,
                       const float* kernel, const float* bias, int kt, const float* const* conv_kernel,
@@ -358,7 +363,8 @@ typedef enum cssm_norm { CSSM_NORM_NONE = 0, CSSM_NORM_RMS = 1, CSSM_NORM_LAYER 
  *   o, gate  (F, K, HW) plane-major of in_dtype (irfft2 output; SiLU'd gate_proj)
  *   norm     cssm_norm; norm_scale (K) [rms_scale or output_layernorm/scale], norm_bias (K) or NULL
  *   kernel (K, N) [output_proj/kernel], bias (N); out (F * HW, N) channels-last of out_dtype
- * K <= 128 and K % 4 == 0, HW % 4 == 0.
+ * K <= 128 and K % 4 == 0, HW % 4 == 0.  o and gate 16-byte aligned (f32) or 8-byte
+ * aligned (bf16), a f32 out 16-byte aligned.
  */
 int cssm_gdn_proj_out(const void* o, const void* gate, int in_dtype, int F, int HW, int K, int N, int norm,
                       const float* norm_scale, const float* norm_bias, const float* kernel, const float* bias,

@@ -1,0 +1,234 @@
+"""float32 torch-CPU restatement of the CSSM layer: the reported CPU baseline.
+
+TEST INFRASTRUCTURE ONLY.  ``bench.py``'s ``cpu_baseline`` leg times this
+module on the host's cores (torch's intra-op threads), and ``tests/`` pins it
+against the float64 oracle (``oracle/cssm_oracle.py``).  The product path
+(``cssm_amd``) never imports it; it is never the thing measured on the GPU.
+
+It follows the reference's op order with torch CPU kernels in float32 /
+complex64, which is how the reference's JAX CPU path runs (the reference
+itself cannot run here: JAX/Flax are absent):
+
+  gated (cssm.py:476-585): in_proj -> [short convs] -> SiLU -> rfft2 -> ctx ->
+      factored / dense Delta, B, C gates -> GOOM floors -> sequential complex
+      recurrence over T -> x C -> irfft2 -> x SiLU(z) -> out_proj.
+  gdn (cssm.py:4685-5141): [qkv_dw] -> qkv_proj -> causal short conv + SiLU ->
+      input gates -> gate_proj -> rfft2 -> spectral / key norms -> delta rule
+      per (head, bin) over T -> readout -> irfft2 -> RMSNorm -> x gate ->
+      output_proj.
+
+The recurrence is the exact linear form of the reference's log-space scan
+(GOOM log_add_exp is exact addition), evaluated sequentially over T.
+"""
+from __future__ import annotations
+
+import math
+
+import torch
+import torch.nn.functional as Fn
+
+
+def _t(a):
+    return torch.as_tensor(a, dtype=torch.float32)
+
+
+def params_to_torch(tree):
+    """Nested dict of numpy arrays -> float32 CPU tensors."""
+    if isinstance(tree, dict):
+        return {k: params_to_torch(v) for k, v in tree.items()}
+    return _t(tree).contiguous()
+
+
+def _dense(x, p):
+    return torch.addmm(p["bias"], x.reshape(-1, x.shape[-1]), p["kernel"]).reshape(*x.shape[:-1], -1)
+
+
+def _floor(z):
+    """to_goom's floor (goom.py:161-174): |z| < 1e-7 -> 1e-7 + 0j."""
+    r = torch.view_as_real(z)
+    small = (r[..., 0] * r[..., 0] + r[..., 1] * r[..., 1]) < 1e-14
+    return torch.where(small, torch.full_like(z, 1e-7), z)
+
+
+def _planes_in(x, p):
+    """Dense over the channels of channels-last frames (F, H, W, K), written plane-major
+    (F, N, H, W) by one batched matmul: W^T (N, K) @ x^T (K, HW) per frame."""
+    F, H, W, K = x.shape
+    y = torch.matmul(p["kernel"].t(), x.reshape(F, H * W, K).transpose(1, 2))
+    return (y + p["bias"][None, :, None]).reshape(F, -1, H, W)
+
+
+def _planes_out(y, p):
+    """Dense over the channels of plane-major frames (F, C, H, W) -> channels-last (F, H, W, N)."""
+    F, C, H, W = y.shape
+    return (torch.matmul(y.reshape(F, C, H * W).transpose(1, 2), p["kernel"]) + p["bias"]).reshape(F, H, W, -1)
+
+
+def _pad_kernel(k, H, W):
+    """cssm.py:510-526: zero-pad with (H-K)//2 before, centre-crop when K > H."""
+    K = k.shape[-1]
+    if K > H or K > W:
+        sh, sw = (K - H) // 2, (K - W) // 2
+        return k[:, sh:sh + H, sw:sw + W]
+    ph, pw = (H - K) // 2, (W - K) // 2
+    return Fn.pad(k, (pw, W - K - pw, ph, H - K - ph))
+
+
+def spectral_kernel(k, H, W, rho, squash=True):
+    F = torch.fft.rfft2(_pad_kernel(k, H, W))
+    return F * rho / (1.0 + F.abs()) if squash else F
+
+
+def _gate_act(x, kind):
+    """cssm.py:432-441."""
+    if kind == "sigmoid":
+        return torch.sigmoid(x) * 2.0
+    if kind == "exp":
+        return torch.exp(x.clamp(-4.0, 2.0))
+    return Fn.softplus(x)
+
+
+def _dwconv_same(x, p):
+    """Depthwise k x k SAME conv with bias on (N, H, W, C) (flax Conv, HWIO kernel)."""
+    k = p["kernel"].shape[0]
+    C = x.shape[-1]
+    w = p["kernel"].permute(3, 2, 0, 1).contiguous()          # (C, 1, k, k)
+    lo, hi = (k - 1) // 2, k // 2
+    xp = Fn.pad(x.permute(0, 3, 1, 2), (lo, hi, lo, hi))
+    return (Fn.conv2d(xp, w, groups=C) + p["bias"][None, :, None, None]).permute(0, 2, 3, 1)
+
+
+def _causal_t(x5, p):
+    """cssm.py:494-500 on plane-major (B, T, C, H, W): left pad k-1 frames, VALID
+    depthwise conv over T, bias per channel."""
+    k = p["kernel"].shape[0]
+    T = x5.shape[1]
+    w = p["kernel"][:, 0, :, None, None]                   # (k, C, 1, 1)
+    out = p["bias"][:, None, None].expand_as(x5).clone()
+    for t in range(T):
+        for j in range(k):
+            s = t - (k - 1) + j
+            if s >= 0:
+                out[:, t] += x5[:, s] * w[j]
+    return out
+
+
+def _dwconv_planes(x, p):
+    """Depthwise k x k SAME conv with bias on plane-major (N, C, H, W)."""
+    k = p["kernel"].shape[0]
+    C = x.shape[1]
+    w = p["kernel"].permute(3, 2, 0, 1).contiguous()          # (C, 1, k, k)
+    lo, hi = (k - 1) // 2, k // 2
+    return Fn.conv2d(Fn.pad(x, (lo, hi, lo, hi)), w, groups=C) + p["bias"][None, :, None, None]
+
+
+class GatedCPU:
+    """GatedCSSM forward (cssm.py:476-585) in float32 on the CPU."""
+
+    def __init__(self, params, channels, expand=1, kernel_size=11, spectral_rho=0.999, gate_type="factored",
+                 gate_activation="softplus", short_conv_size=0, short_conv_spatial_size=0):
+        self.p = params_to_torch(params)
+        self.Ci = channels * expand
+        self.rho = spectral_rho
+        self.gate_type = gate_type
+        self.act = gate_activation
+        self.kt, self.ks = short_conv_size, short_conv_spatial_size
+        self._khat = {}
+
+    def __call__(self, x):
+        p, Ci = self.p, self.Ci
+        B, T, H, W, _ = x.shape
+        Wf = W // 2 + 1
+        xz = _planes_in(x.reshape(B * T, H, W, -1), p["in_proj"])      # (F, 2C, H, W)
+        xm, z = xz[:, :Ci], xz[:, Ci:]
+        if self.ks > 0:
+            xm = _dwconv_planes(xm, p["short_conv_spatial"])
+        xm = xm.reshape(B, T, Ci, H, W)
+        if self.kt > 0:
+            xm = _causal_t(xm, p["short_conv_temporal"])
+        xm = Fn.silu(xm)
+        if (H, W) not in self._khat:
+            self._khat[(H, W)] = _floor(spectral_kernel(p["kernel"], H, W, self.rho))
+        kh = self._khat[(H, W)]
+        U = torch.fft.rfft2(xm)                                         # (B, T, C, H, Wf)
+        ctx = xm.mean(dim=(3, 4))
+
+        def make(name):
+            if self.gate_type == "factored":
+                return _dense(ctx, p[name + "_h"])[..., :, None] * _dense(ctx, p[name + "_w"])[..., None, :]
+            return _dense(ctx, p[name]).reshape(B, T, H, Wf)
+        d = _gate_act(make("delta_proj"), self.act)[:, :, None]
+        gB, gC = make("B_proj")[:, :, None], make("C_proj")[:, :, None]
+        h = torch.zeros_like(U[:, 0])
+        Y = torch.empty_like(U)
+        for t in range(T):
+            h = kh * torch.exp(-d[:, t]) * h + (d[:, t] + 1e-8) * _floor(U[:, t] * gB[:, t])
+            Y[:, t] = h * gC[:, t]
+        y = torch.fft.irfft2(Y, s=(H, W)).reshape(B * T, Ci, H, W) * Fn.silu(z)
+        return _planes_out(y, p["out_proj"]).reshape(B, T, H, W, -1)
+
+
+class GdnCPU:
+    """GatedDeltaNetCSSM slow-path forward (cssm.py:4685-5141) in float32 on the CPU,
+    factored gates, sinusoid temporal context, RMS output norm, SiLU output gate."""
+
+    def __init__(self, params, channels, delta_key_dim=4, spectral_rho=0.999, qkv_conv_size=1, short_conv_size=4,
+                 use_input_gates=True, rope_base=10000.0):
+        self.p = params_to_torch(params)
+        self.C, self.dk = channels, delta_key_dim
+        self.rho = spectral_rho
+        self.q = qkv_conv_size
+        self.kt = short_conv_size
+        self.input_gates = use_input_gates
+        self.base = rope_base
+        self._what = {}
+
+    def __call__(self, x):
+        p, C, dk = self.p, self.C, self.dk
+        B, T, H, W, _ = x.shape
+        nh, Wf = C // dk, W // 2 + 1
+        if (H, W) not in self._what:
+            self._what[(H, W)] = spectral_kernel(p["kernel"], H, W, self.rho)
+        what = self._what[(H, W)]
+        xf = x.reshape(B * T, H, W, C)
+        xq = _dwconv_same(xf, p["qkv_dw"]) if self.q > 1 else xf
+        qkv = _planes_in(xq, p["qkv_proj"]).reshape(B, T, 3 * C, H, W)
+        q, k, v = qkv[:, :, :C], qkv[:, :, C:2 * C], qkv[:, :, 2 * C:]
+        if self.kt > 0:
+            q = Fn.silu(_causal_t(q, p["short_conv_q"]))
+            k = Fn.silu(_causal_t(k, p["short_conv_k"]))
+            v = Fn.silu(_causal_t(v, p["short_conv_v"]))
+        ctx = x.mean(dim=(2, 3))
+        inv = 1.0 / (self.base ** (torch.arange(0, C, 2, dtype=torch.float32) / C))
+        th = torch.arange(T, dtype=torch.float32)[:, None] * inv[None]
+        ctx = ctx + torch.stack([torch.sin(th), torch.cos(th)], -1).reshape(T, C)[None]
+
+        def fgate(name):
+            return torch.sigmoid(_dense(ctx, p[name + "_h"])[..., :, None] + _dense(ctx, p[name + "_w"])[..., None, :])
+        if self.input_gates:
+            k = k * fgate("B_k")[:, :, None]
+            v = v * fgate("B_v")[:, :, None]
+        gv = Fn.silu(_planes_in(xf, p["gate_proj"]))                  # (F, C, H, W)
+        al = (0.1 + 0.89 * fgate("alpha"))[:, :, None]                 # (B, T, 1, H, Wf)
+        be = fgate("beta")[:, :, None]
+
+        def spec(z):                                                   # (B, T, nh, dk, H, Wf)
+            return torch.fft.rfft2(z).reshape(B, T, nh, dk, H, Wf)
+
+        def l2(z):
+            return z / torch.sqrt((z.abs() ** 2).sum(dim=(4, 5), keepdim=True) + 1e-6)
+        qs, ks, vs = l2(spec(q)), l2(spec(k)), spec(v)
+        ks = ks / torch.sqrt((ks.abs() ** 2).sum(dim=3, keepdim=True) + 1e-6)
+        s = torch.zeros((B, nh, dk, dk, H, Wf), dtype=torch.complex64)     # s[b, n, i, a, u, v]
+        O = torch.empty((B, T, nh, dk, H, Wf), dtype=torch.complex64)
+        for t in range(T):
+            kk = ks[:, t]
+            a_t = al[:, t][:, :, None, None] * what[None, :, None, None]
+            b_t = be[:, t][:, :, None, None]
+            khs = torch.einsum("bnauv,bniauv->bniuv", kk.conj(), s)
+            s = a_t * (s - b_t * kk[:, :, None] * khs[:, :, :, None])
+            s = s + b_t * vs[:, t][:, :, :, None] * kk.conj()[:, :, None]
+            O[:, t] = torch.einsum("bniauv,bnauv->bniuv", s, qs[:, t])
+        o = torch.fft.irfft2(O.reshape(B * T, C, H, W // 2 + 1), s=(H, W))   # (F, C, H, W)
+        o = o * torch.rsqrt((o ** 2).mean(1, keepdim=True) + 1e-6) * p["rms_scale"][None, :, None, None]
+        return _planes_out(o * gv, p["output_proj"]).reshape(B, T, H, W, C)

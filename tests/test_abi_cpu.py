@@ -75,3 +75,29 @@ def test_scan_col_order(H):
         pairs = sorted({v // 16 for v in grp})
         assert blocks == list(range(blocks[0], blocks[0] + 4)) and len(pairs) == 2
         assert len({(v % 16, v // 16) for v in grp}) == 8
+
+
+def test_projection_entry_points_reject_misaligned_pointers():
+    """Every pointer a projection kernel reads or writes with 4-element vectors is
+    checked before any GPU work: an offset pointer returns CSSM_ERR_ALIGN (-5)."""
+    from cssm_amd import _lib
+    lib = _lib.load()
+    buf = ctypes.create_string_buffer(4096)
+    p = (ctypes.addressof(buf) + 255) // 256 * 256
+    F, HW, K, N = 2, 16, 8, 8
+    f32, bf16 = _lib.F32, _lib.BF16
+    # proj_in: x (f32 16 B, bf16 8 B)
+    assert lib.cssm_proj_in(p + 4, f32, F, HW, K, N, p, p, p, p, f32, 0, 0, None, None, 0, None) == -5
+    assert lib.cssm_proj_in(p + 4, bf16, F, HW, K, N, p, p, p, p, f32, 0, 0, None, None, 0, None) == -5
+    assert b"x must be" in lib.cssm_last_error()
+    # proj_out: y and a f32 out
+    assert lib.cssm_proj_out(p + 8, f32, F, HW, K, N, p, p, p, f32, None) == -5
+    assert lib.cssm_proj_out(p, f32, F, HW, K, N, p, p, p + 4, f32, None) == -5
+    assert lib.cssm_proj_out(p + 2, bf16, F, HW, K, N, p, p, p, bf16, None) == -5
+    # proj_planes: x
+    assert lib.cssm_proj_planes(p + 4, f32, F, HW, K, N, p, p, p, f32, 0, None) == -5
+    # gdn_qkv_proj: x
+    assert lib.cssm_gdn_qkv_proj(p + 4, f32, 1, 2, 4, 4, K, 4, p, p, 0, None, None, 0, None, p, f32, None) == -5
+    assert b"x / qkv" in lib.cssm_last_error()
+    # gdn_proj_out: out
+    assert lib.cssm_gdn_proj_out(p, p, f32, F, HW, K, N, 0, None, None, p, p, p + 4, f32, None) == -5

@@ -49,6 +49,57 @@ def test_proj_in_plane_major_and_ctx(mods, F, HW, K, N, silu):
     assert rel_err(to_np(ctx), ref_lo.mean(axis=2)) < 1e-5
 
 
+# bf16 A (the bf16-I/O projections): the persistent kernel (K <= 64) stages one bf16 plane and the
+# K-chunked kernel (K > 64) loads raw bf16; both take three split products instead of six.  The
+# exact product of the bf16-rounded input is the reference, at the fp32 bar.
+@pytest.mark.parametrize("F,HW,K,N", [(4, 1024, 64, 256), (3, 196, 40, 72), (2, 1024, 128, 512),
+                                      (3, 196, 224, 896), (2, 16, 320, 1280)])
+def test_proj_in_bf16_input(mods, F, HW, K, N):
+    _, S = mods
+    print_case(test="proj_in_bf16", F=F, HW=HW, K=K, N=N)
+    rng = np.random.default_rng(10)
+    xb = _dev(rng.standard_normal((F * HW, K)), torch.bfloat16)
+    x = to_np(xb)
+    Wt = rng.standard_normal((K, N)) / np.sqrt(K)
+    b = rng.standard_normal(N) * 0.1
+    lo, hi, ctx = S.proj_in(xb, _dev(Wt), _dev(b), F, HW, silu_lo=True, silu_hi=False, want_ctx=True,
+                            out_dtype=torch.float32)
+    ref = (x @ Wt + b).reshape(F, HW, N).transpose(0, 2, 1)
+    ref_lo = O.silu(ref[:, : N // 2])
+    assert rel_err(to_np(lo), ref_lo) < 1e-5
+    assert rel_err(to_np(hi), ref[:, N // 2:]) < 1e-5
+    assert rel_err(to_np(ctx), ref_lo.mean(axis=2)) < 1e-5
+
+
+@pytest.mark.parametrize("F,HW,K,N", [(4, 1024, 64, 64), (2, 196, 256, 128), (2, 16, 640, 320), (3, 49, 448, 224)])
+def test_proj_out_bf16_input(mods, F, HW, K, N):
+    """Plane-major bf16 A into the output projection (persistent and K-chunked kernels)."""
+    _, S = mods
+    print_case(test="proj_out_bf16", F=F, HW=HW, K=K, N=N)
+    rng = np.random.default_rng(11)
+    yb = _dev(rng.standard_normal((F, K, HW)), torch.bfloat16)
+    y = to_np(yb)
+    Wt = rng.standard_normal((K, N)) / np.sqrt(K)
+    b = rng.standard_normal(N) * 0.1
+    out = S.proj_out(yb, _dev(Wt), _dev(b), out_dtype=torch.float32)
+    ref = y.transpose(0, 2, 1).reshape(F * HW, K) @ Wt + b
+    assert rel_err(to_np(out), ref) < 1e-5
+
+
+@pytest.mark.parametrize("F,HW,K,N", [(4, 1024, 64, 192), (2, 256, 64, 64), (3, 196, 256, 128)])
+def test_proj_planes_bf16_input(mods, F, HW, K, N):
+    _, S = mods
+    print_case(test="proj_planes_bf16", F=F, HW=HW, K=K, N=N)
+    rng = np.random.default_rng(12)
+    xb = _dev(rng.standard_normal((F * HW, K)), torch.bfloat16)
+    x = to_np(xb)
+    Wt = rng.standard_normal((K, N)) / np.sqrt(K)
+    b = rng.standard_normal(N) * 0.1
+    out = S.proj_planes(xb, _dev(Wt), _dev(b), F, HW, act="identity", out_dtype=torch.float32)
+    ref = (x @ Wt + b).reshape(F, HW, N).transpose(0, 2, 1)
+    assert rel_err(to_np(out), ref) < 1e-5
+
+
 @pytest.mark.parametrize("F,HW,K,N", [(4, 1024, 64, 64), (2, 16384, 128, 64), (3, 196, 96, 150),
                                       (3, 49, 448, 224), (2, 16, 640, 320), (2, 196, 256, 128), (5, 49, 36, 30)])
 def test_proj_out_channels_last(mods, F, HW, K, N):
@@ -147,6 +198,21 @@ def test_gated_layer_bf16_io(mods):
     # intermediates are fp32: beyond the output's own bf16 rounding the error is at the fp32 level
     assert bf16_excess_err(to_np(y), ref) <= TOL_BF16
     assert np.sqrt(np.mean((to_np(y) - ref) ** 2)) <= TOL_BF16 * np.sqrt(np.mean(ref ** 2))
+
+
+def test_gated_layer_two_parameter_trees(mods):
+    """One cell applied to two parameter trees of the same shape in turn (e.g. a reloaded
+    checkpoint): each output follows its own weights, whatever addresses the allocator reuses."""
+    cells, _ = mods
+    print_case(test="gated_layer_two_trees")
+    kw = dict(channels=8, kernel_size=5, gate_type="factored", short_conv_size=0, short_conv_spatial_size=0)
+    cell = cells.GatedCSSM(**kw)
+    for seed in (51, 52, 51):
+        cfg, p, x = _layer_inputs((1, 2, 16, 16, 8), kw, seed)
+        v = cells.GatedCSSM.load_params(p)
+        y = cell.apply(v, _dev(x))
+        del v
+        assert rel_err(to_np(y), O.gated_forward(p, x, cfg)) <= TOL_F32, seed
 
 
 def test_gated_layer_is_causal_in_time(mods):

@@ -359,6 +359,72 @@ def test_gdn_layer_bf16_io(mods):
     assert bf16_excess_err(to_np(y), ref) <= TOL_BF16
 
 
+def test_gdn_layer_c3_time_length_fused_qkv_128(mods):
+    """C3's own frame count (T = 8) at 128 x 128 with the 5 x 5 qkv depthwise conv: the fused
+    T = 8 qkv projection (short conv + SiLU + input gates in the GEMM epilogue) runs in the layer."""
+    cells, S = mods
+    print_case(test="gdn_layer_c3_T8_128")
+    kw = dict(delta_key_dim=4, gate_type="factored", qkv_conv_size=5, kernel_size=11)
+    shape = (1, 8, 128, 128, 8)
+    assert S.gdn_qkv_fused(8, 128, 128, 8, 4)
+    cfg, p, x = _layer(kw, shape, 26)
+    ref = O.gdn_forward(p, x, cfg)
+    y = cells.GatedDeltaNetCSSM(channels=8, **kw).apply(cells.GatedDeltaNetCSSM.load_params(p), _dev(x))
+    assert rel_err(to_np(y), ref) <= TOL_F32
+
+
+def _moving_dots(rng, shape):
+    """~2 % of pixels = 1.0 on random-walk tracks over N(0, 0.01^2) background (the C4 input)."""
+    B, T, H, W, C = shape
+    x = rng.standard_normal(shape) * 0.01
+    pos = rng.integers(0, H * W, (B, max(1, int(0.02 * H * W))))
+    steps = np.array([1, -1, W, -W, 0])
+    for t in range(T):
+        for b in range(B):
+            x[b, t].reshape(H * W, C)[pos[b]] = 1.0
+        pos = (pos + steps[rng.integers(0, 5, pos.shape)]) % (H * W)
+    return x
+
+
+def test_gdn_layer_c4_shape_bf16_chunk_carry(mods):
+    """C4's frame shape at full width (T = 32, 32 x 32, C = 64, d_k = 4, bf16 I/O) on moving dots:
+    the fused qkv projection walks the frames in chunks of 8 and carries the short conv's last
+    3 frames between chunks, inside the layer."""
+    cells, S = mods
+    print_case(test="gdn_layer_c4_T32_bf16")
+    kw = dict(delta_key_dim=4, gate_type="factored", kernel_size=11, short_conv_size=4)
+    shape = (1, 32, 32, 32, 64)
+    assert S.gdn_qkv_fused(32, 32, 32, 64, 4)
+    cfg, p, _ = _layer(kw, shape, 27)
+    x = _moving_dots(np.random.default_rng(28), shape)
+    xb = _dev(x, torch.bfloat16)
+    y = cells.GatedDeltaNetCSSM(channels=64, **kw).apply(cells.GatedDeltaNetCSSM.load_params(p), xb)
+    assert y.dtype == torch.bfloat16
+    ref = O.gdn_forward(p, to_np(xb), cfg)
+    assert bf16_excess_err(to_np(y), ref) <= TOL_BF16
+    # the same layer in fp32 I/O holds the fp32 bar (the carry is exact)
+    y32 = cells.GatedDeltaNetCSSM(channels=64, **kw).apply(cells.GatedDeltaNetCSSM.load_params(p),
+                                                           _dev(to_np(xb)))
+    assert rel_err(to_np(y32), ref) <= TOL_F32
+
+
+def test_gdn_layer_two_parameter_trees(mods):
+    """One cell applied to two parameter trees of the same shape in turn: each output follows its
+    own weights (the derived W_hat and input-gate buffers are not reused across trees)."""
+    cells, _ = mods
+    print_case(test="gdn_layer_two_trees")
+    for gate_type in ("factored", "channel"):
+        kw = dict(delta_key_dim=2, gate_type=gate_type)
+        shape = (1, 3, 16, 16, 8)
+        cell = cells.GatedDeltaNetCSSM(channels=8, **kw)
+        for seed in (31, 32, 31):
+            cfg, p, x = _layer(kw, shape, seed)
+            v = cells.GatedDeltaNetCSSM.load_params(p)
+            y = cell.apply(v, _dev(x))
+            del v
+            assert rel_err(to_np(y), O.gdn_forward(p, x, cfg)) <= TOL_F32, (gate_type, seed)
+
+
 def test_gdn_layer_is_causal_in_time(mods):
     cells, _ = mods
     print_case(test="gdn_layer_causal")
