@@ -6,6 +6,8 @@
 #include <stdio.h>
 #include <string.h>
 
+#include <mutex>
+
 #include "../../include/cssm_amd.h"
 #include "launch.h"
 
@@ -478,3 +480,61 @@ int cssm_block_residual(const void* res, int T_res, const void* y, int T_y, int 
                                                 static_cast<hipStream_t>(stream)),
                     "cssm_block_residual");
 }
+
+// ---------------------------------------------------------------- input projection without allocation
+
+// Device scratch of cssm_proj_in_noalloc: the ctx partial sums (one float per
+// (row tile, frame slot, channel)), CSSM_PROJ_IN_SCRATCH_BYTES per device,
+// held until the process ends.  Host code never passes this name to a kernel:
+// its device address comes from hipGetSymbolAddress, once per device.
+static __device__ __align__(256) float scratch[CSSM_PROJ_IN_SCRATCH_BYTES / sizeof(float)];
+
+namespace {
+
+constexpr int kMaxDevices = 64;
+std::mutex g_scratch_mu;
+void* g_scratch_ptr[kMaxDevices] = {};
+
+// device address of `scratch` on the current device (looked up on the first call per device)
+int scratch_for_current_device(void** out, const char* what) {
+  int dev = -1;
+  hipError_t e = hipGetDevice(&dev);
+  if (e != hipSuccess) return hip_status(e, what);
+  if (dev < 0 || dev >= kMaxDevices) return fail(CSSM_ERR_UNSUPPORTED, "%s: device ordinal %d", what, dev);
+  std::lock_guard<std::mutex> lock(g_scratch_mu);
+  if (g_scratch_ptr[dev] == nullptr) {
+    void* p = nullptr;
+    e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+    if (e != hipSuccess) return hip_status(e, what);
+    if (p == nullptr) return fail(CSSM_ERR_HIP, "%s: no device address for the scratch array", what);
+    g_scratch_ptr[dev] = p;
+  }
+  *out = g_scratch_ptr[dev];
+  return CSSM_OK;
+}
+
+}  // namespace
+
+extern "C" {
+
+int cssm_proj_in_noalloc(const void* x, int in_dtype, int F, int HW, int K, int N, const float* kernel,
+                         const float* bias, void* out_lo, void* out_hi, int out_dtype, int act_lo, int act_hi,
+                         float* ctx, void* stream) {
+  if (ctx != nullptr && F > 0 && HW > 0 && K > 0 && N > 0) {
+    const size_t need = cssm_proj_in_workspace_size(F, HW, K, N);
+    if (need > CSSM_PROJ_IN_SCRATCH_BYTES)
+      return fail(CSSM_ERR_UNSUPPORTED,
+                  "cssm_proj_in_noalloc: ctx of F=%d HW=%d K=%d N=%d needs %zu bytes of scratch, the static scratch "
+                  "holds %zu (use cssm_proj_in with a workspace)",
+                  F, HW, K, N, need, (size_t)CSSM_PROJ_IN_SCRATCH_BYTES);
+  }
+  void* ws = nullptr;
+  if (ctx != nullptr) {
+    const int st = scratch_for_current_device(&ws, "cssm_proj_in_noalloc");
+    if (st != CSSM_OK) return st;
+  }
+  return cssm_proj_in(x, in_dtype, F, HW, K, N, kernel, bias, out_lo, out_hi, out_dtype, act_lo, act_hi, ctx, ws,
+                      ws ? (size_t)CSSM_PROJ_IN_SCRATCH_BYTES : 0, stream);
+}
+
+}  // extern "C"

@@ -180,6 +180,29 @@ int cssm_proj_in(const void* x, int in_dtype, int F, int HW, int K, int N, const
 /* Bytes of device workspace cssm_proj_in needs to produce ctx. */
 size_t cssm_proj_in_workspace_size(int F, int HW, int K, int N);
 
+/* Size of the static device scratch of cssm_proj_in_noalloc (64 MiB per device). */
+#define CSSM_PROJ_IN_SCRATCH_BYTES (64u << 20)
+
+/*
+ * cssm_proj_in without a workspace argument: the same kernels and results, with
+ * the ctx partial sums in a static device array of CSSM_PROJ_IN_SCRATCH_BYTES
+ * (one per device, held until the process ends).  No counterpart in the
+ * reference: it is for callers that cannot allocate device memory (code under
+ * HIP graph capture, tight serving loops, hosts that forbid allocation).  It
+ * calls no allocating routine.
+ *   Arguments as cssm_proj_in.  ctx is rejected with CSSM_ERR_UNSUPPORTED when
+ *   cssm_proj_in_workspace_size(F, HW, K, N) exceeds the scratch (C2's
+ *   F = 1024 frames of 128 x 128 at K = 64, N = 128 need 32 MiB).
+ *   The first call on a device, with that device current, looks up the array's
+ *   device address; stream must belong to the current device.
+ * Every call on one device shares its scratch: calls that overlap on one GPU
+ * (different streams, or host threads) race and must be serialised by the
+ * caller.  Each call writes every partial sum it reads, so nothing needs clearing.
+ */
+int cssm_proj_in_noalloc(const void* x, int in_dtype, int F, int HW, int K, int N, const float* kernel,
+                         const float* bias, void* out_lo, void* out_hi, int out_dtype, int act_lo, int act_hi,
+                         float* ctx, void* stream);
+
 /*
  * Output projection from plane-major planes back to channels-last.
  * Replaces cssm.py:584 (out_proj = Dense(C) on the channels-last transpose
