@@ -15,10 +15,11 @@ A step is one full layer forward with x already in HBM:
   gdn:   frame mean + gates -> [qkv depthwise conv] -> qkv_proj -> short conv + SiLU +
          input gates -> gate_proj -> rfft2 -> per-bin delta-rule scan -> irfft2 ->
          RMSNorm x gate + output_proj
-value = frames/s = B * T / step time (whole layer).
+value = frames/s = B * T / step time (whole layer), from K timed steps.
 
-roofline: the dominant kernel, timed with HIP events on its stream over the
-timed steps.  gated: the fused scan, algorithmic bytes per launch
+roofline: the dominant kernel, timed with HIP events on its stream over a
+second run of K steps with an event after every kernel (recording events costs
+the launch-bound stack workload idle GPU time, so value comes from the first).  gated: the fused scan, algorithmic bytes per launch
 B*T*(3*H*W*C*s + 3*(H+W/2+1)*4) + C*H*(W/2+1)*8 (read u and z, write y, read the
 factored gate vectors, K_hat once).  gdn: the spectral core (rfft2 + scan +
 irfft2 launches together), B*T*(4*H*W*C*s + 2*(H+W/2+1)*4) + n_h*H*(W/2+1)*8
@@ -157,14 +158,20 @@ def randomise_biases(variables, torch, dev):
 # ------------------------------------------------------ instrumented steps
 
 class Marks:
-    """HIP events on torch's current stream (the stream every kernel is launched on)."""
+    """HIP events on torch's current stream (the stream every kernel is launched on).
 
-    def __init__(self, torch, record):
-        self.torch, self.record, self.seq = torch, record, []
+    ``pool`` holds events created before the timed region, so the timed steps only
+    record them (creating an event costs far more host time than recording one, and
+    would show up as GPU idle time in the launch-bound workloads)."""
+
+    def __init__(self, torch, record, pool=None):
+        self.torch, self.record, self.seq, self.pool = torch, record, [], pool
+        self.count = 0
 
     def __call__(self, name):
+        self.count += 1
         if self.record:
-            ev = self.torch.cuda.Event(enable_timing=True)
+            ev = self.pool.pop() if self.pool else self.torch.cuda.Event(enable_timing=True)
             ev.record()
             self.seq.append((name, ev))
 
@@ -361,18 +368,32 @@ def run_workload(key, args, torch, cells, S, headline):
     core = ("scan",) if w["cell"] in ("gated", "stack") else ("rfft2", "scan_bins", "irfft2")
     steps = args.steps if headline else max(1, args.config_steps)
 
-    for _ in range(args.warmup):
+    per_step = 0
+    for _ in range(max(1, args.warmup)):
+        m = Marks(torch, False)
+        step(cell, variables, x, w, S, m)
+        per_step = m.count
+    # timed region 1: the layer as a caller runs it (value, ms_per_step)
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for _ in range(steps):
         step(cell, variables, x, w, S, Marks(torch, False))
+    torch.cuda.synchronize()
+    el = time.perf_counter() - t0
+    ms_step = el * 1e3 / steps
+    # timed region 2: the same steps with a HIP event recorded after every kernel on the stream
+    # they run on (per-kernel times, the dominant kernel's roofline).  Recording an event costs
+    # the launch-bound workloads (C5: 45 per step) idle GPU time, so value comes from region 1.
+    pool = [torch.cuda.Event(enable_timing=True) for _ in range(steps * per_step)]
     torch.cuda.synchronize()
     marks = []
     t0 = time.perf_counter()
     for _ in range(steps):
-        m = Marks(torch, True)
+        m = Marks(torch, True, pool)
         step(cell, variables, x, w, S, m)
         marks.append(m)
     torch.cuda.synchronize()
-    el = time.perf_counter() - t0
-    ms_step = el * 1e3 / steps
+    ms_step_marked = (time.perf_counter() - t0) * 1e3 / steps
     # the instrumented step must equal the module's forward bit for bit
     if w["cell"] == "stack":
         ref = None
@@ -423,6 +444,7 @@ def run_workload(key, args, torch, cells, S, headline):
         "steps": steps,
         "warmup": args.warmup,
         "ms_per_step": ms_step,
+        "ms_per_step_with_kernel_events": round(ms_step_marked, 4),
         "higher_is_better": True,
         "scaling": "weak",
         "vs_baseline": None,
@@ -438,11 +460,6 @@ def run_workload(key, args, torch, cells, S, headline):
         "core_frames_per_s": B * T / (core_ms * 1e-3),
         "roofline": roof,
     }
-    if not args.no_cpu_baseline:
-        if headline:
-            res["cpu_baseline"] = cpu_baseline(w, budget_s=args.cpu_seconds, warmup=5, max_repeats=20)
-        else:
-            res["cpu_baseline"] = cpu_baseline(w, budget_s=args.cpu_seconds / 4, warmup=1, max_repeats=20)
     if not headline:
         for k in ("metric", "n_gpus", "higher_is_better", "scaling", "vs_baseline", "warmup"):
             res.pop(k)
@@ -482,6 +499,15 @@ def main():
         for k in extra:
             print(f"bench: workload {k}", file=sys.stderr, flush=True)
             res["configs"][k] = run_workload(k, args, torch, cells, S, headline=False)
+    # the CPU baselines run after every GPU measurement, so the host's thread pool never
+    # competes with the launch thread of a timed GPU loop
+    if not args.no_cpu_baseline:
+        print("bench: cpu baselines", file=sys.stderr, flush=True)
+        res["cpu_baseline"] = cpu_baseline(dict(WORKLOADS[args.workload], key=args.workload),
+                                           budget_s=args.cpu_seconds, warmup=5, max_repeats=20)
+        for k in extra:
+            res["configs"][k]["cpu_baseline"] = cpu_baseline(dict(WORKLOADS[k], key=k), budget_s=args.cpu_seconds / 4,
+                                                             warmup=1, max_repeats=20)
     print(json.dumps(res), flush=True)
 
 
