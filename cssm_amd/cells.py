@@ -162,8 +162,11 @@ class GatedCSSM:
                                lambda: S.spectral_kernel(k, H, W, self.spectral_rho, squash=True, goom_floor=True,
                                                          scan_order=True))
 
-    def apply(self, variables: Params, x: torch.Tensor, injected_qkv_spatial=None) -> torch.Tensor:
-        """y = GatedCSSM(x); x (B, T, H, W, C) float32 or bfloat16 on the GPU, y same dtype."""
+    def apply(self, variables: Params, x: torch.Tensor, injected_qkv_spatial=None,
+              out_dtype: Optional[torch.dtype] = None) -> torch.Tensor:
+        """y = GatedCSSM(x); x (B, T, H, W, C) float32 or bfloat16 on the GPU, y of x's dtype
+        (or ``out_dtype``: float32 is what the reference cell returns for bf16 input, since it
+        computes with float32 parameters)."""
         p = variables["params"]
         B, T, H, W, c_in = x.shape
         Ci = self.channels * self.expand
@@ -194,7 +197,8 @@ class GatedCSSM:
         gates = S.gated_gates(ctx, p, H, W, self.gate_type, self.gate_activation, c_scale=S.scan_c_scale(H, W))
         khat = self.spectral_kernel(p, H, W)
         y = S.gated_scan(u, z, gates, khat)
-        out = S.proj_out(y.view(F, Ci, HW), p["out_proj"]["kernel"], p["out_proj"]["bias"], out_dtype=x.dtype)
+        out = S.proj_out(y.view(F, Ci, HW), p["out_proj"]["kernel"], p["out_proj"]["bias"],
+                         out_dtype=out_dtype or x.dtype)
         return out.view(B, T, H, W, self.channels)
 
     __call__ = apply
@@ -375,8 +379,10 @@ class GatedDeltaNetCSSM:
                                lambda: (torch.cat([kk.reshape(C, C), kv.reshape(C, C)], dim=1).contiguous(),
                                         torch.cat([bk, bv]).contiguous()))
 
-    def apply(self, variables: Params, x: torch.Tensor, injected_qkv_spatial=None) -> torch.Tensor:
-        """y = GatedDeltaNetCSSM(x); x (B, T, H, W, C) float32 or bfloat16 on the GPU, y same dtype."""
+    def apply(self, variables: Params, x: torch.Tensor, injected_qkv_spatial=None,
+              out_dtype: Optional[torch.dtype] = None) -> torch.Tensor:
+        """y = GatedDeltaNetCSSM(x); x (B, T, H, W, C) float32 or bfloat16 on the GPU, y of x's dtype
+        (or ``out_dtype``)."""
         p = variables["params"]
         B, T, H, W, C = x.shape
         if C != self.channels:
@@ -427,7 +433,7 @@ class GatedDeltaNetCSSM:
         else:
             ns = nb = None
         out = S.gdn_proj_out(o.view(F, C, HW), gv, self.output_norm, ns, nb, p["output_proj"]["kernel"],
-                             p["output_proj"]["bias"], out_dtype=x.dtype)
+                             p["output_proj"]["bias"], out_dtype=out_dtype or x.dtype)
         return out.view(B, T, H, W, C)
 
     __call__ = apply

@@ -636,8 +636,47 @@ def gelu_tanh(x):
     return 0.5 * x * (1.0 + np.tanh(math.sqrt(2.0 / math.pi) * (x + 0.044715 * x ** 3)))
 
 
+def timestep_gate_pool(params, residual, y):
+    """timestep_gate (cssm_shvit.py:195-210): softmax pooling of the cell's T frames with
+    logits from [mean of the first input frame, mean of frame t] through gate_fc1 -> gelu
+    -> gate_fc2, plus a prior of 4 on the last frame.  residual, y (B, T, H, W, C)."""
+    T = y.shape[1]
+    q = residual[:, 0].mean(axis=(1, 2))                                  # (B, C)
+    k = y.mean(axis=(2, 3))                                               # (B, T, C)
+    gate_in = np.concatenate([np.broadcast_to(q[:, None], k.shape), k], axis=-1)
+    h = gelu_tanh(dense(gate_in, params['gate_fc1']))
+    logits = dense(h, params['gate_fc2'])[..., 0]
+    prior = np.zeros(T)
+    prior[-1] = 4.0
+    z = logits + prior
+    w = np.exp(z - z.max(axis=-1, keepdims=True))
+    w = w / w.sum(axis=-1, keepdims=True)
+    return np.einsum('bt,bthwc->bhwc', w, y)
+
+
+def shvit_mlp_half(params, x, use_dwconv=True):
+    """The block's second half (cssm_shvit.py:231-266, Mlp shvit.py:156-182): x + fc2(h'),
+    h = gelu(fc1(LayerNorm_norm2(x))), h' = h + dwconv(h) (depthwise 3 x 3 'SAME')."""
+    shp = x.shape
+    x4 = x.reshape(-1, *shp[-3:])                                          # frames as batch (:241-244)
+    h = flax_layer_norm(x4, params['norm2'])
+    h = gelu_tanh(dense(h, params['mlp']['fc1']))
+    if use_dwconv:
+        h = h + depthwise_conv2d_same(h, params['mlp']['dwconv']['dwconv'])
+    h = dense(h, params['mlp']['fc2'])
+    return x + h.reshape(shp)
+
+
+def shvit_block(params, x, cell_forward, num_timesteps=8, block_norm='global_layer', use_pos_conv=True,
+                output_act='none', timestep_gate=False, use_dwconv=True):
+    """CSSMSHViTBlock.__call__ (cssm_shvit.py:65-266): the token mixer, then norm2 -> Mlp -> residual."""
+    x = shvit_block_mixer(params, x, cell_forward, num_timesteps, block_norm, use_pos_conv, output_act,
+                          timestep_gate)
+    return shvit_mlp_half(params, x, use_dwconv)
+
+
 def shvit_block_mixer(params, x, cell_forward, num_timesteps=8, block_norm='global_layer',
-                      use_pos_conv=True, output_act='none'):
+                      use_pos_conv=True, output_act='none', timestep_gate=False):
     """CSSMSHViTBlock.__call__ up to the token-mixer residual (cssm_shvit.py:86-228).
 
     x (B, H, W, C) image -> repeated to (B, T, H, W, C) (:99-101), or (B, T, H, W, C)
@@ -654,7 +693,11 @@ def shvit_block_mixer(params, x, cell_forward, num_timesteps=8, block_norm='glob
         B, T, H, W, C = h.shape
         h = h + depthwise_conv2d_same(h.reshape(B * T, H, W, C), params['pos_conv']).reshape(h.shape)
     y = cell_forward(params['cssm'], h)
-    y = y[:, -1] if is_image else y
+    if timestep_gate:                                                     # :195-210
+        y = timestep_gate_pool(params, x5, y)
+        is_image = True                                                   # T collapsed (:191)
+    else:
+        y = y[:, -1] if is_image else y
     if output_act == 'gelu':
         y = gelu_tanh(y)
     elif output_act == 'silu':
@@ -769,3 +812,229 @@ def init_params(shapes, rng: np.random.Generator, bias_std=0.1, spectral_std=Non
         else:
             out[name] = rng.standard_normal(v) * 0.1
     return out
+
+
+# ---------------------------------------------------------------------------
+# SimpleCSSM caller (simple_cssm.py:63-558): stem -> cells with residual ->
+# readout, for the cells of this path (gated / gdn / gdn_d2 / gdn_d3) and the
+# position embeddings that add no RoPE ('none', 'learnable')
+# ---------------------------------------------------------------------------
+
+@dataclass
+class SimpleConfig:
+    """SimpleCSSM attributes that shape the computation around the cells."""
+    num_classes: int = 2
+    embed_dim: int = 32
+    depth: int = 1
+    cssm_type: str = 'gated'
+    kernel_size: int = 15
+    frame_readout: str = 'last'
+    norm_type: str = 'layer'
+    stem_norm: str = ''
+    body_norm: str = ''
+    pos_embed: str = 'none'
+    act_type: str = 'softplus'
+    pool_type: str = 'mean'
+    seq_len: int = 8
+    n_register_tokens: int = 0
+    stem_mode: str = 'default'
+    stem_layers: int = 2
+    stem_norm_order: str = 'post'
+    readout_norm: str = 'pre'
+    inter_mlp_ratio: float = 0.0
+    gate_type: str = 'dense'
+    short_conv_size: int = 4
+    short_conv_spatial_size: int = 3
+    delta_key_dim: int = 2
+    output_norm: str = 'rms'
+    use_input_gates: bool = True
+    output_gate_act: str = 'silu'
+    use_spectral_l2_norm: bool = True
+    qkv_conv_size: int = 1
+    no_spectral_clamp: bool = False
+
+
+def simple_cell_config(cfg: SimpleConfig):
+    """The cell config SimpleCSSM builds for block i (simple_cssm.py:325-443)."""
+    if cfg.cssm_type == 'gated':
+        return GatedConfig(channels=cfg.embed_dim, kernel_size=cfg.kernel_size, gate_type=cfg.gate_type,
+                           short_conv_size=cfg.short_conv_size,
+                           short_conv_spatial_size=cfg.short_conv_spatial_size)
+    dk = {'gdn_d2': 2, 'gdn_d3': 3}.get(cfg.cssm_type, cfg.delta_key_dim)
+    return GDNConfig(channels=cfg.embed_dim, delta_key_dim=dk, kernel_size=cfg.kernel_size, gate_type=cfg.gate_type,
+                     short_conv_size=cfg.short_conv_size, output_norm=cfg.output_norm,
+                     use_input_gates=cfg.use_input_gates, output_gate_act=cfg.output_gate_act,
+                     use_spectral_l2_norm=cfg.use_spectral_l2_norm, qkv_conv_size=cfg.qkv_conv_size,
+                     no_spectral_clamp=cfg.no_spectral_clamp)
+
+
+def _act(x, kind):
+    """SimpleCSSM._get_act (simple_cssm.py:155-164): softplus / gelu (tanh form) / relu."""
+    if kind == 'gelu':
+        return gelu_tanh(x)
+    if kind == 'relu':
+        return np.maximum(x, 0.0)
+    return softplus(x)
+
+
+def flax_layer_norm(x, p, axes=(-1,), eps=1e-6):
+    """flax LayerNorm: stats over `axes` with the fast variance E[x^2] - E[x]^2 (clipped at 0),
+    per-channel scale and bias on the last axis."""
+    mu = np.mean(x, axis=axes, keepdims=True)
+    var = np.maximum(np.mean(x * x, axis=axes, keepdims=True) - mu * mu, 0.0)
+    return (x - mu) / np.sqrt(var + eps) * p['scale'] + p['bias']
+
+
+def simple_norm(x, kind, p, stats=None, training=False):
+    """_apply_norm (simple_cssm.py:192-235)."""
+    if kind == 'batch':
+        # flax BatchNorm (epsilon 1e-5): running statistics in inference, batch statistics otherwise
+        if training:
+            axes = tuple(range(x.ndim - 1))
+            mu = np.mean(x, axis=axes)
+            var = np.maximum(np.mean(x * x, axis=axes) - mu * mu, 0.0)
+        else:
+            mu, var = stats['mean'], stats['var']
+        return (x - mu) / np.sqrt(var + 1e-5) * p['scale'] + p['bias']
+    if kind == 'instance':
+        # GroupNorm(num_groups=C): one group per channel, stats over every non-batch axis but C
+        return flax_layer_norm(x, p, axes=tuple(range(1, x.ndim - 1)) or (-1,))
+    if x.ndim == 5 and kind == 'temporal_layer':
+        return flax_layer_norm(x, p, axes=(1, 4))
+    if x.ndim == 5 and kind == 'global_layer':
+        return flax_layer_norm(x, p, axes=(1, 2, 3, 4))
+    if x.ndim == 5 and kind == 'global_instance':
+        return flax_layer_norm(x, p, axes=(1, 2, 3))
+    return flax_layer_norm(x, p)
+
+
+def conv2d_same(x, p):
+    """flax Conv with 'SAME' padding, stride 1, bias: (N, H, W, Cin) -> (N, H, W, Cout)."""
+    return full_conv2d_same(x, p)
+
+
+def max_pool_2x2_same(x):
+    """nn.max_pool(window (2, 2), strides (2, 2), 'SAME') on (N, H, W, C): odd sizes pad
+    the far edge with -inf."""
+    N, H, W, C = x.shape
+    Ho, Wo = (H + 1) // 2, (W + 1) // 2
+    xp = np.full((N, 2 * Ho, 2 * Wo, C), -np.inf)
+    xp[:, :H, :W] = x
+    return xp.reshape(N, Ho, 2, Wo, 2, C).max(axis=(2, 4))
+
+
+def simple_param_shapes(cfg: SimpleConfig, x_shape):
+    """SimpleCSSM parameter tree (Flax names) and batch_stats for input (B, [T,] H, W, C_in)."""
+    H, W, cin = x_shape[-3], x_shape[-2], x_shape[-1]
+    D = cfg.embed_dim
+    stem_norm = cfg.stem_norm or cfg.norm_type
+    body_norm = cfg.body_norm or cfg.norm_type
+    p: Dict[str, object] = {}
+    bs: Dict[str, object] = {}
+
+    def norm(name, c, kind):
+        p[name] = {'scale': (c,), 'bias': (c,)}
+        if kind == 'batch':
+            bs[name] = {'mean': (c,), 'var': (c,)}
+    if cfg.stem_mode == 'pathtracker':
+        p['conv1'] = {'kernel': (1, 1, cin, D), 'bias': (D,)}
+        norm('norm1', cin if cfg.stem_norm_order == 'pre' else D, stem_norm)
+    else:
+        c = cin
+        for i in range(cfg.stem_layers):
+            norm(f'norm{i + 1}', c if cfg.stem_norm_order == 'pre' else D, stem_norm)
+            p[f'conv{i + 1}'] = {'kernel': (3, 3, c, D), 'bias': (D,)}
+            c = D
+            H, W = (H + 1) // 2, (W + 1) // 2
+    if cfg.pos_embed == 'learnable':
+        p['pos_embed'] = (1, 1, H, W, D)
+    if cfg.n_register_tokens > 0:
+        p['register_tokens'] = (1, cfg.n_register_tokens, H, W, D)
+    ccfg = simple_cell_config(cfg)
+    for i in range(cfg.depth):
+        p[f'cssm_{i}'] = (gated_param_shapes(ccfg, D, H, W) if cfg.cssm_type == 'gated'
+                          else gdn_param_shapes(ccfg, H, W))
+        if cfg.depth > 1 and i < cfg.depth - 1:
+            norm(f'body_norm_{i}', D, body_norm)
+            if cfg.inter_mlp_ratio > 0:
+                hid = int(D * cfg.inter_mlp_ratio)
+                p[f'mlp_{i}_up'] = {'kernel': (D, hid), 'bias': (hid,)}
+                p[f'mlp_{i}_down'] = {'kernel': (hid, D), 'bias': (D,)}
+    norm('norm_pre', D, body_norm)
+    norm('norm_post', D, body_norm)
+    p['head'] = {'kernel': (D, cfg.num_classes), 'bias': (cfg.num_classes,)}
+    return p, bs
+
+
+def simple_cssm_forward(params, x, cfg: SimpleConfig, batch_stats=None, training=False,
+                        return_features=False, return_spatial=False, injected_post_cssm=None):
+    """SimpleCSSM.__call__ (simple_cssm.py:166-558) for the cells of this path."""
+    if cfg.pos_embed not in ('none', 'learnable'):
+        raise NotImplementedError('RoPE position embeddings are outside the restated path')
+    act = lambda v: _act(v, cfg.act_type)                      # noqa: E731
+    stem_norm = cfg.stem_norm or cfg.norm_type
+    body_norm = cfg.body_norm or cfg.norm_type
+    bs = batch_stats or {}
+
+    def norm(v, kind, name):
+        return simple_norm(v, kind, params[name], bs.get(name), training)
+    x = np.asarray(x, dtype=np.float64)
+    if x.ndim == 4:                                                         # :239-240
+        x = np.repeat(x[:, None], cfg.seq_len, axis=1)
+    B, T, H, W, C = x.shape
+    x = x.reshape(B * T, H, W, C)                                           # :245
+
+    def norm_act(v, name):                                                  # :247-255
+        if cfg.stem_norm_order == 'pre':
+            return act(norm(v, stem_norm, name))
+        return norm(act(v), stem_norm, name)
+    if cfg.stem_mode == 'pathtracker':                                      # :257-264
+        if cfg.stem_norm_order == 'pre':
+            x = conv2d_same(norm_act(x, 'norm1'), params['conv1'])
+        else:
+            x = norm_act(conv2d_same(x, params['conv1']), 'norm1')
+    else:                                                                   # :266-274
+        for i in range(cfg.stem_layers):
+            if cfg.stem_norm_order == 'pre':
+                x = conv2d_same(norm_act(x, f'norm{i + 1}'), params[f'conv{i + 1}'])
+            else:
+                x = norm_act(conv2d_same(x, params[f'conv{i + 1}']), f'norm{i + 1}')
+            x = max_pool_2x2_same(x)
+    _, Hn, Wn, D = x.shape
+    x = x.reshape(B, T, Hn, Wn, D)                                          # :277-278
+    if cfg.pos_embed == 'learnable':                                        # :281-285
+        x = x + params['pos_embed']
+    nreg = cfg.n_register_tokens
+    if nreg > 0:                                                            # :302-306
+        reg = np.broadcast_to(params['register_tokens'], (B, nreg, Hn, Wn, D))
+        x = np.concatenate([reg, x], axis=1)
+    ccfg = simple_cell_config(cfg)
+    for i in range(cfg.depth):                                              # :319-496
+        cp = params[f'cssm_{i}']
+        y = gated_forward(cp, x, ccfg) if cfg.cssm_type == 'gated' else gdn_forward(cp, x, ccfg)
+        x = x + y                                                           # :482
+        if cfg.depth > 1 and i < cfg.depth - 1:                             # :486-496
+            x = act(norm(x, body_norm, f'body_norm_{i}'))
+            if cfg.inter_mlp_ratio > 0:
+                h = act(dense(x, params[f'mlp_{i}_up']))
+                x = x + dense(h, params[f'mlp_{i}_down'])
+    if injected_post_cssm is not None:                                      # :500-501
+        x = np.asarray(injected_post_cssm, dtype=np.float64)
+    if return_features:                                                     # :502-503
+        return x
+    if nreg > 0:                                                            # :507-508
+        x = x[:, nreg:]
+    if return_spatial:                                                      # :510-521
+        x = act(norm(x, body_norm, 'norm_pre')) if cfg.readout_norm == 'pre' else \
+            norm(act(x), body_norm, 'norm_pre')
+        return dense(x, params['head'])
+    if cfg.frame_readout == 'last':                                         # :524-527
+        x = x[:, -1]
+    if cfg.readout_norm == 'pre':                                           # :530-535
+        x = act(norm(x, body_norm, 'norm_pre'))
+    else:
+        x = norm(act(x), body_norm, 'norm_pre')
+    axes = (1, 2) if cfg.frame_readout == 'last' else (1, 2, 3)             # :538-549
+    x = x.max(axis=axes) if cfg.pool_type == 'max' else x.mean(axis=axes)
+    x = norm(x, body_norm, 'norm_post')                                     # :552
+    return dense(x, params['head'])                                         # :555

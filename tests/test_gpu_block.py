@@ -136,7 +136,7 @@ def test_block_matches_oracle(mods, name, kw, shape, T):
     x = rng.standard_normal(shape)
     ref = O.shvit_block_mixer(p, x, fwd, num_timesteps=T or shape[1], **bk)
     blk = blocks.CSSMSHViTBlock(dim=C, num_timesteps=T or shape[1], **kw)
-    got = blk.apply(blocks.CSSMSHViTBlock.load_params(p), _dev(x))
+    got = blk.token_mixer(blocks.CSSMSHViTBlock.load_params(p), _dev(x))
     torch.cuda.synchronize()
     assert tuple(got.shape) == shape
     assert rel_err(to_np(got), ref) <= TOL_F32
@@ -151,7 +151,7 @@ def test_block_bf16_io(mods):
     shape = (4, 14, 14, 32)
     p, fwd, bk = _oracle_block(kw, 32, 14, 14, rng)
     xb = _dev(rng.standard_normal(shape), torch.bfloat16)
-    got = blocks.CSSMSHViTBlock(dim=32, num_timesteps=1, **kw).apply(blocks.CSSMSHViTBlock.load_params(p), xb)
+    got = blocks.CSSMSHViTBlock(dim=32, num_timesteps=1, **kw).token_mixer(blocks.CSSMSHViTBlock.load_params(p), xb)
     assert got.dtype == torch.bfloat16
     ref = O.shvit_block_mixer(p, to_np(xb), fwd, num_timesteps=1, **bk)
     assert bf16_excess_err(to_np(got), ref) <= TOL_BF16
@@ -160,6 +160,68 @@ def test_block_bf16_io(mods):
 def test_block_rejects_what_is_not_built(mods):
     blocks, _ = mods
     with pytest.raises(NotImplementedError):
-        blocks.CSSMSHViTBlock(dim=16, timestep_gate=True)
-    with pytest.raises(NotImplementedError):
         blocks.CSSMSHViTBlock(dim=16, cssm_type="gdn", static_image_fast_path=True)
+
+
+def _full_block_params(p, rng, C, mlp_ratio, timestep_gate, use_dwconv):
+    """norm2 / mlp (and gate_fc1 / gate_fc2) added to a token-mixer parameter tree."""
+    hid = int(C * mlp_ratio)
+    p = dict(p)
+    p["norm2"] = {"scale": 1.0 + 0.2 * rng.standard_normal(C), "bias": 0.2 * rng.standard_normal(C)}
+    p["mlp"] = {"fc1": {"kernel": rng.standard_normal((C, hid)) / np.sqrt(C), "bias": 0.1 * rng.standard_normal(hid)},
+                "fc2": {"kernel": rng.standard_normal((hid, C)) / np.sqrt(hid), "bias": 0.1 * rng.standard_normal(C)}}
+    if use_dwconv:
+        p["mlp"]["dwconv"] = {"dwconv": {"kernel": rng.standard_normal((3, 3, 1, hid)) / 3,
+                                         "bias": 0.1 * rng.standard_normal(hid)}}
+    if timestep_gate:
+        hg = max(C // 4, 8)
+        p["gate_fc1"] = {"kernel": rng.standard_normal((2 * C, hg)) / np.sqrt(2 * C), "bias": 0.1 * rng.standard_normal(hg)}
+        p["gate_fc2"] = {"kernel": rng.standard_normal((hg, 1)) / np.sqrt(hg), "bias": 0.1 * rng.standard_normal(1)}
+    return p
+
+
+FULL_CASES = [
+    # name, block kwargs (incl. cssm_type), shape, num_timesteps, timestep_gate, use_dwconv, mlp_ratio
+    ("gated_image_mlp", dict(cssm_type="gated", kernel_size=5), (2, 14, 14, 16), 3, False, True, 4.0),
+    ("gated_image_timestep_gate", dict(cssm_type="gated", kernel_size=3, output_act="gelu"), (2, 8, 8, 16), 4,
+     True, True, 2.0),
+    ("gdn_video_keep_time_mlp", dict(cssm_type="gdn", delta_key_dim=2, kernel_size=3, block_norm="temporal_layer"),
+     (1, 3, 8, 8, 16), None, False, True, 4.0),
+    ("gdn_video_timestep_gate_no_dwconv", dict(cssm_type="gdn", delta_key_dim=4, kernel_size=3, block_norm="layer"),
+     (2, 3, 8, 8, 16), None, True, False, 3.0),
+]
+
+
+@pytest.mark.parametrize("name,kw,shape,T,tg,dw,ratio", FULL_CASES, ids=[c[0] for c in FULL_CASES])
+def test_full_block_matches_oracle(mods, name, kw, shape, T, tg, dw, ratio):
+    """The whole block (cssm_shvit.py:65-266): token mixer, optional timestep-gate pooling,
+    then norm2 -> Mlp (fc1 -> gelu -> + dwconv -> fc2) -> residual."""
+    blocks, _ = mods
+    print_case(test="shvit_full_block", case=name)
+    rng = np.random.default_rng(33)
+    H, W, C = shape[-3:]
+    p, fwd, bk = _oracle_block(kw, C, H, W, rng)
+    p = _full_block_params(p, rng, C, ratio, tg, dw)
+    x = rng.standard_normal(shape)
+    ref = O.shvit_block(p, x, fwd, num_timesteps=T or shape[1], timestep_gate=tg, use_dwconv=dw, **bk)
+    blk = blocks.CSSMSHViTBlock(dim=C, num_timesteps=T or shape[1], timestep_gate=tg, use_dwconv=dw, mlp_ratio=ratio,
+                                **kw)
+    assert blk.param_shapes(H, W).keys() == p.keys()
+    got = blk.apply(blocks.CSSMSHViTBlock.load_params(p), _dev(x))
+    torch.cuda.synchronize()
+    assert tuple(got.shape) == ref.shape
+    assert rel_err(to_np(got), ref) <= TOL_F32
+
+
+def test_full_block_bf16_io(mods):
+    blocks, _ = mods
+    print_case(test="shvit_full_block_bf16")
+    rng = np.random.default_rng(34)
+    kw = dict(cssm_type="gated", kernel_size=1, short_conv_size=0, short_conv_spatial_size=0)
+    p, fwd, bk = _oracle_block(kw, 32, 7, 7, rng)
+    p = _full_block_params(p, rng, 32, 4.0, False, True)
+    xb = _dev(rng.standard_normal((4, 7, 7, 32)), torch.bfloat16)
+    got = blocks.CSSMSHViTBlock(dim=32, num_timesteps=1, **kw).apply(blocks.CSSMSHViTBlock.load_params(p), xb)
+    assert got.dtype == torch.bfloat16
+    ref = O.shvit_block(p, to_np(xb), fwd, num_timesteps=1, **bk)
+    assert bf16_excess_err(to_np(got), ref) <= TOL_BF16

@@ -401,3 +401,59 @@ def test_shvit_block_wiring_closed_forms(image, rng):
     outs = O.shvit_block_mixer(p, x, lambda q, hh: hh, num_timesteps=T, output_act="silu", use_pos_conv=False)
     hn = O.block_norm1(x5, p["norm1"]["scale"], p["norm1"]["bias"])
     assert np.allclose(outs, x + O.silu(hn[:, -1] if image else hn), atol=1e-12)
+
+
+# ------------------------------------------------------ CSSM-SHViT block, second half
+
+def test_timestep_gate_prior_closed_form(rng):
+    """With gate_fc2 zeroed the logits are 0 and the weights are softmax(prior):
+    e^4 / (T - 1 + e^4) on the last frame, 1 / (T - 1 + e^4) on the others (cssm_shvit.py:205-209)."""
+    B, T, H, W, C = 2, 4, 3, 3, 8
+    p = {"gate_fc1": {"kernel": rng.standard_normal((2 * C, 8)), "bias": rng.standard_normal(8)},
+         "gate_fc2": {"kernel": np.zeros((8, 1)), "bias": np.zeros(1)}}
+    y = np.stack([np.full((B, H, W, C), float(t + 1)) for t in range(T)], axis=1)
+    got = O.timestep_gate_pool(p, rng.standard_normal((B, T, H, W, C)), y)
+    z = T - 1 + math.exp(4.0)
+    expect = (sum(range(1, T)) + T * math.exp(4.0)) / z
+    assert np.allclose(got, expect, rtol=1e-14, atol=0)
+
+
+def test_timestep_gate_logits_use_first_input_frame_and_frame_means(rng):
+    """A gate that reads only the query half (the first input frame's mean) weighs every frame the
+    same as the prior does; one that reads frame t's mean moves weight toward the larger mean."""
+    B, T, H, W, C = 1, 3, 2, 2, 8
+    y = np.stack([np.full((B, H, W, C), v) for v in (0.0, 5.0, 0.0)], axis=1)
+    res = rng.standard_normal((B, T, H, W, C))
+    w1 = np.zeros((2 * C, 8))
+    w1[C:, 0] = 1.0                                   # reads the frame means only
+    p = {"gate_fc1": {"kernel": w1, "bias": np.zeros(8)},
+         "gate_fc2": {"kernel": np.eye(8)[:, :1] * 10.0, "bias": np.zeros(1)}}
+    got = O.timestep_gate_pool(p, res, y)
+    assert got.mean() > 4.9                           # frame 1 (mean 5) takes almost all the weight
+    w1 = np.zeros((2 * C, 8))
+    w1[:C, 0] = 1.0                                   # reads the query only: equal logits
+    p["gate_fc1"]["kernel"] = w1
+    got = O.timestep_gate_pool(p, res, y)
+    z = 2 + math.exp(4.0)
+    assert np.allclose(got, 5.0 / z, rtol=1e-12)
+
+
+def test_mlp_half_closed_forms(rng):
+    """fc2 zeroed: the block returns its input (the residual); dwconv with only a centre tap a
+    and fc1 / fc2 identities: x + (1 + a) gelu(LN(x)) + bias (h + dwconv(h), shvit.py:173-176)."""
+    B, H, W, C = 2, 4, 5, 6
+    x = rng.standard_normal((B, H, W, C))
+    n2 = {"scale": np.ones(C), "bias": np.zeros(C)}
+    dwk = np.zeros((3, 3, 1, C))
+    dwk[1, 1, 0, :] = 0.5
+    p = {"norm2": n2, "mlp": {"fc1": {"kernel": np.eye(C), "bias": np.zeros(C)},
+                               "fc2": {"kernel": np.zeros((C, C)), "bias": np.zeros(C)},
+                               "dwconv": {"dwconv": {"kernel": dwk, "bias": np.full(C, 0.25)}}}}
+    assert np.array_equal(O.shvit_mlp_half(p, x), x)
+    p["mlp"]["fc2"]["kernel"] = np.eye(C)
+    mu = x.mean(-1, keepdims=True)
+    ln = (x - mu) / np.sqrt(x.var(-1, keepdims=True) + 1e-6)
+    assert np.allclose(O.shvit_mlp_half(p, x), x + 1.5 * O.gelu_tanh(ln) + 0.25, rtol=1e-12, atol=1e-12)
+    # video: every frame through the same MLP
+    xv = rng.standard_normal((B, 3, H, W, C))
+    assert np.allclose(O.shvit_mlp_half(p, xv)[:, 1], O.shvit_mlp_half(p, xv[:, 1]), rtol=0, atol=1e-14)
