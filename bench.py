@@ -234,12 +234,16 @@ def gdn_step(cell, variables, x, w, S, mark):
     mark("qkv_proj")   # with the short conv, SiLU and input gates (one kernel when T in {1, 2, 4, 8})
     gv = S.proj_planes(x, p["gate_proj"]["kernel"], p["gate_proj"]["bias"], F, HW, act="silu", out_dtype=f32)
     mark("gate_proj")
-    spec, norms = S.rfft2(qkv, want_norms=True)
-    mark("rfft2")
-    ohat = S.gdn_scan_bins(spec, norms, ab, cell.gate_type, what, cell.delta_key_dim)
-    mark("scan_bins")
-    o = S.irfft2(ohat, W, out_dtype=f32)
-    mark("irfft2")
+    if S.gdn_core_fused_supported(H, W, cell.delta_key_dim):
+        o = S.gdn_core_fused(qkv, True, ab, cell.gate_type, what, cell.delta_key_dim)
+        mark("core_fused")   # rfft2 -> norms -> delta rule -> irfft2 in one kernel
+    else:
+        spec, norms = S.rfft2(qkv, want_norms=True)
+        mark("rfft2")
+        ohat = S.gdn_scan_bins(spec, norms, ab, cell.gate_type, what, cell.delta_key_dim)
+        mark("scan_bins")
+        o = S.irfft2(ohat, W, out_dtype=f32)
+        mark("irfft2")
     out = S.gdn_proj_out(o.view(F, C, HW), gv, "rms", p["rms_scale"], None, p["output_proj"]["kernel"],
                          p["output_proj"]["bias"], out_dtype=x.dtype)
     mark("proj_out")
@@ -365,7 +369,8 @@ def run_workload(key, args, torch, cells, S, headline):
         variables = cell.init(1, x.shape)
         randomise_biases(variables, torch, dev)
     step = {"gated": gated_step, "gdn": gdn_step, "stack": stack_step}[w["cell"]]
-    core = ("scan",) if w["cell"] in ("gated", "stack") else ("rfft2", "scan_bins", "irfft2")
+    core = ("scan",) if w["cell"] in ("gated", "stack") else (
+        ("core_fused",) if S.gdn_core_fused_supported(H, W, w["dk"]) else ("rfft2", "scan_bins", "irfft2"))
     steps = args.steps if headline else max(1, args.config_steps)
 
     per_step = 0

@@ -94,6 +94,8 @@ SIGNATURES = {
     "cssm_fft_min_group": (_I, [_I, _I]),
     "cssm_gdn_scan_bins": (_I, [_P, _P, _P, _LL, _I, _I, _P, _I, _I, _I, _I, _I, _I, _P, _P]),
     "cssm_gdn_proj_out": (_I, [_P, _P, _I, _I, _I, _I, _I, _I, _P, _P, _P, _P, _P, _I, _P]),
+    "cssm_gdn_core_fused": (_I, [_P, _I, _P, _LL, _I, _I, _P, _I, _I, _I, _I, _I, _I, _P, _P]),
+    "cssm_gdn_core_fused_supported": (_I, [_I, _I, _I]),
     "cssm_gated_scan_supported": (ctypes.c_int, [ctypes.c_int, ctypes.c_int]),
     "cssm_gated_scan_min_group": (ctypes.c_int, [ctypes.c_int, ctypes.c_int]),
     "cssm_gated_scan_col_order": (ctypes.c_int, [ctypes.c_int, ctypes.c_int, ctypes.POINTER(ctypes.c_int)]),

@@ -419,13 +419,18 @@ class GatedDeltaNetCSSM:
         del xq, gates
         gv = S.proj_planes(x, p["gate_proj"]["kernel"], p["gate_proj"]["bias"], F, HW,
                            act="silu" if self.output_gate_act == "silu" else "sigmoid", out_dtype=f32)
-        # spectral core: rfft2 -> delta-rule recurrence -> irfft2
-        spec, norms = S.rfft2(qkv, want_norms=self.use_spectral_l2_norm)
-        del qkv
-        ohat = S.gdn_scan_bins(spec, norms, ab, self.gate_type, what, dk)
-        del spec
-        o = S.irfft2(ohat, W, out_dtype=f32)
-        del ohat
+        # spectral core: rfft2 -> delta-rule recurrence -> irfft2, in one kernel where a workgroup
+        # holds a head's state (32 x 32, d_k = 4), else through spectra in HBM
+        if S.gdn_core_fused_supported(H, W, dk):
+            o = S.gdn_core_fused(qkv, self.use_spectral_l2_norm, ab, self.gate_type, what, dk)
+            del qkv
+        else:
+            spec, norms = S.rfft2(qkv, want_norms=self.use_spectral_l2_norm)
+            del qkv
+            ohat = S.gdn_scan_bins(spec, norms, ab, self.gate_type, what, dk)
+            del spec
+            o = S.irfft2(ohat, W, out_dtype=f32)
+            del ohat
         if self.output_norm == "rms":
             ns, nb = p["rms_scale"], None
         elif self.output_norm == "layer":

@@ -412,6 +412,31 @@ int cssm_gdn_scan_bins(const float* spec, const float* norms, const float* ab, l
                     "cssm_gdn_scan_bins");
 }
 
+int cssm_gdn_core_fused_supported(int H, int W, int delta_key_dim) {
+  return cssm::gdn_core_fused_supported(H, W, delta_key_dim) ? 1 : 0;
+}
+
+int cssm_gdn_core_fused(const float* qkv, int use_l2, const float* ab, long long ab_frame, int ab_head, int ab_bin,
+                        const float* what, int B, int T, int C, int H, int W, int delta_key_dim, float* o,
+                        void* stream) {
+  if (!qkv || !ab || !what || !o) return fail(CSSM_ERR_NULL, "cssm_gdn_core_fused: null argument");
+  if (B <= 0 || T <= 0 || C <= 0 || H <= 0 || W <= 0 || delta_key_dim < 1 || delta_key_dim > 4 ||
+      C % delta_key_dim || ab_frame < 0 || ab_head < 0 || ab_bin < 0)
+    return fail(CSSM_ERR_SHAPE, "cssm_gdn_core_fused: B=%d T=%d C=%d H=%d W=%d d_k=%d", B, T, C, H, W,
+                delta_key_dim);
+  if (!cssm::gdn_core_fused_supported(H, W, delta_key_dim))
+    return fail(CSSM_ERR_UNSUPPORTED, "cssm_gdn_core_fused: no fused core for %dx%d planes at d_k=%d", H, W,
+                delta_key_dim);
+  if (use_l2 != 0 && use_l2 != 1) return fail(CSSM_ERR_ARG, "cssm_gdn_core_fused: use_l2=%d", use_l2);
+  if ((long long)B * T * 3 * C * H * W >= (1LL << 40)) return fail(CSSM_ERR_SHAPE, "cssm_gdn_core_fused: too large");
+  if (!aligned(qkv, 16) || !aligned(o, 16) || !aligned(ab, 8) || !aligned(what, 8))
+    return fail(CSSM_ERR_ALIGN, "cssm_gdn_core_fused: qkv and o must be 16-byte aligned, ab and what 8");
+  return hip_status(cssm::launch_gdn_core_fused(qkv, use_l2, reinterpret_cast<const float2*>(ab), ab_frame, ab_head,
+                                                ab_bin, reinterpret_cast<const float2*>(what), B, T, C, H, W,
+                                                delta_key_dim, o, static_cast<hipStream_t>(stream)),
+                    "cssm_gdn_core_fused");
+}
+
 int cssm_gdn_proj_out(const void* o, const void* gate, int in_dtype, int F, int HW, int K, int N, int norm,
                       const float* norm_scale, const float* norm_bias, const float* kernel, const float* bias, void* out,
                       int out_dtype, void* stream) {

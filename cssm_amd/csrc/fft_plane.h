@@ -337,6 +337,12 @@ struct PlaneFft {
         twI1(twC1 + G::N_C1),
         twI3(twI1 + G::N_I1) {}
 
+  // a view of planes laid out by another geometry of the same plane size (same
+  // row stride and twiddle tables): the caller supplies the plane buffer, the
+  // packed-column scratch and the twiddle tables
+  __device__ __forceinline__ PlaneFft(float* b, float2* e, float2* tw)
+      : buf(b), edge(e), twR1(tw), twC1(twR1 + G::N_R1), twI1(twC1 + G::N_C1), twI3(twI1 + G::N_I1) {}
+
   __device__ __forceinline__ float2& cplx(int off) const { return *reinterpret_cast<float2*>(buf + off); }
 
   // twiddles w_N^m = exp(-2 pi i m / N) from double precision; call once

@@ -340,6 +340,55 @@ struct GdnBinArgs {
   int T, C, HWF;
 };
 
+// One step of the recurrence for one bin: key-vector norm, M and D with the
+// floors, s_i <- M s_i + D[i], o_i = sum_a s_i[a] q_a.  q and k arrive with the
+// spectral norms already applied; k is normalised here.
+template <int DK>
+__device__ __forceinline__ void gdn_bin_step(float2 (&s)[DK][DK], const float2 (&q)[DK], float2 (&k)[DK],
+                                             const float2 (&v)[DK], float2 wh, float alpha, float beta,
+                                             float2 (&o)[DK]) {
+  float kk = 0.0f;
+#pragma unroll
+  for (int j = 0; j < DK; ++j) kk = fmaf(k[j].x, k[j].x, fmaf(k[j].y, k[j].y, kk));
+  const float kn = 1.0f / sqrtf(kk + 1e-6f);
+#pragma unroll
+  for (int j = 0; j < DK; ++j) k[j] = cscale(k[j], kn);
+  const float2 aw = cscale(wh, alpha);
+  float2 M[DK][DK];
+#pragma unroll
+  for (int r = 0; r < DK; ++r)
+#pragma unroll
+    for (int c = 0; c < DK; ++c) {
+      // alpha W (delta_rc - beta k_r conj k_c)
+      const float2 kk_rc = cmulc(k[r], k[c]);
+      float2 m = make_float2(-beta * kk_rc.x, -beta * kk_rc.y);
+      if (r == c) m.x += 1.0f;
+      M[r][c] = goom_floor2(cmul(aw, m));
+    }
+#pragma unroll
+  for (int i = 0; i < DK; ++i) {
+    float2 sn[DK];
+#pragma unroll
+    for (int r = 0; r < DK; ++r) {
+      float2 acc = goom_floor2(cscale(cmulc(v[i], k[r]), beta));
+#pragma unroll
+      for (int c = 0; c < DK; ++c) {
+        acc.x = fmaf(M[r][c].x, s[i][c].x, fmaf(-M[r][c].y, s[i][c].y, acc.x));
+        acc.y = fmaf(M[r][c].x, s[i][c].y, fmaf(M[r][c].y, s[i][c].x, acc.y));
+      }
+      sn[r] = acc;
+    }
+    float2 oi = make_float2(0.f, 0.f);
+#pragma unroll
+    for (int r = 0; r < DK; ++r) {
+      s[i][r] = sn[r];
+      oi.x = fmaf(sn[r].x, q[r].x, fmaf(-sn[r].y, q[r].y, oi.x));
+      oi.y = fmaf(sn[r].x, q[r].y, fmaf(sn[r].y, q[r].x, oi.y));
+    }
+    o[i] = oi;
+  }
+}
+
 template <int DK>
 __global__ void __launch_bounds__(256) gdn_scan_bins(const GdnBinArgs a) {
   const int bin = blockIdx.x * blockDim.x + threadIdx.x;
@@ -372,50 +421,307 @@ __global__ void __launch_bounds__(256) gdn_scan_bins(const GdnBinArgs a) {
         k[j] = cscale(k[j], nk);
       }
     }
-    float kk = 0.0f;
-#pragma unroll
-    for (int j = 0; j < DK; ++j) kk = fmaf(k[j].x, k[j].x, fmaf(k[j].y, k[j].y, kk));
-    const float kn = 1.0f / sqrtf(kk + 1e-6f);
-#pragma unroll
-    for (int j = 0; j < DK; ++j) k[j] = cscale(k[j], kn);
-
     const float2 g = a.ab[fr * a.ab_frame + size_t(head) * a.ab_head + size_t(bin) * a.ab_bin];
-    const float alpha = g.x, beta = g.y;
-    const float2 aw = cscale(wh, alpha);
-    float2 M[DK][DK];
+    float2 o[DK];
+    gdn_bin_step<DK>(s, q, k, v, wh, g.x, g.y, o);
+#pragma unroll
+    for (int i = 0; i < DK; ++i) a.ohat[(fr * C + size_t(head) * DK + i) * HWF + bin] = o[i];
+  }
+}
+
+// ---------------------------------------------------------------------------
+// Fused spectral core for 32 x 32 planes and d_k = 4 (the video-shaped
+// config): one workgroup per (b, head) runs all T steps, so the 4 x 4 complex
+// state of the head's 32 x 17 bins (70 KB) stays in VGPRs, and each step reads
+// q, k, v and writes o once, with no spectra in HBM.  Per step:
+//   load     the head's 12 q / k / v planes (issued a step ahead) -> LDS
+//   forward  2-D real FFT of the 12 planes (fft_plane.h passes); the spectrum
+//            stays in LDS: interior bin k + H1 q of unit k in the slot (row
+//            q + H2 k) the column pass read it from, the DC / Nyquist columns
+//            in esp
+//   norms    per-plane sums of |X|^2 (spectral L2 norms of q and k), reduced
+//            per wave and across the four waves in a fixed order
+//   bins     per bin (thread-owned, state in VGPRs): gdn_bin_step, o / (H W)
+//            written over the q slots of the bin
+//   inverse  2-D real FFT of the 4 o planes -> HBM
+// The forward passes see every bin doubled (the packed-row separation skips
+// its 1/2); the bins are halved on reading.
+// ---------------------------------------------------------------------------
+namespace {
+constexpr int kFusedDK = 4;
+using FusedFwdG = Geom<5, 5, 3 * kFusedDK, 48>;   // the 12 q, k, v planes, 256 threads
+using FusedInvG = Geom<5, 5, kFusedDK, 16>;       // the 4 o planes in the same buffer, 256 threads
+static_assert(FusedFwdG::NT == 256 && FusedInvG::NT == 256, "one thread count for both plane groups");
+static_assert(FusedFwdG::RS == FusedInvG::RS, "one row stride for both plane groups");
+}  // namespace
+
+// forward policy: the spectrum stays in LDS (interior bins in the slots the
+// column pass read, DC / Nyquist bins of plane pl, row u in esp[(pl H + u) 2 + (0 | 1)])
+template <class G>
+struct SpecKeepOp {
+  static constexpr bool kPackedColumnToo = false;
+  static constexpr int H = G::H, H2 = G::H2;
+  float* buf;
+  float2* esp;
+  __device__ __forceinline__ void bins(int, int, int pl, int k, int v, float2 (&sp)[G::H2]) const {
+    const int col = G::p_col(v);
+#pragma unroll
+    for (int q = 0; q < H2; ++q) *reinterpret_cast<float2*>(buf + G::row_off(pl, q + H2 * k) + col) = sp[q];
+  }
+  __device__ __forceinline__ void edge(int, int pl, int uA, int uB, int, float2 (&v4)[4]) const {
+    esp[(pl * H + uA) * 2] = v4[0];
+    esp[(pl * H + uA) * 2 + 1] = v4[1];
+    esp[(pl * H + uB) * 2] = v4[2];
+    esp[(pl * H + uB) * 2 + 1] = v4[3];
+  }
+};
+
+// inverse policy: the bins from the same places
+template <class G>
+struct SpecFromLdsOp {
+  static constexpr bool kPackedColumnToo = false;
+  static constexpr int H = G::H, H2 = G::H2;
+  const float* buf;
+  const float2* esp;
+  __device__ __forceinline__ void bins(int, int, int pl, int k, int v, float2 (&sp)[G::H2]) const {
+    const int col = G::p_col(v);
+#pragma unroll
+    for (int q = 0; q < H2; ++q) sp[q] = *reinterpret_cast<const float2*>(buf + G::row_off(pl, q + H2 * k) + col);
+  }
+  __device__ __forceinline__ void edge(int, int pl, int uA, int uB, int, float2 (&v4)[4]) const {
+    v4[0] = esp[(pl * H + uA) * 2];
+    v4[1] = esp[(pl * H + uA) * 2 + 1];
+    v4[2] = esp[(pl * H + uB) * 2];
+    v4[3] = esp[(pl * H + uB) * 2 + 1];
+  }
+};
+
+struct GdnFusedArgs {
+  const float* qkv;      // (B, T, 3C, H, W) float32
+  const float2* ab;      // (alpha, beta) at (b T + t) ab_frame + head ab_head + bin ab_bin
+  long long ab_frame;
+  int ab_head, ab_bin;
+  const float2* what;    // (n_h, H, WF)
+  float* o;              // (B, T, C, H, W) float32
+  int T, C, use_l2;
+};
+
+__global__ void __launch_bounds__(256, 2) gdn_core_fused32(const GdnFusedArgs a) {
+  using GF = FusedFwdG;
+  using GI = FusedInvG;
+  constexpr int H = GF::H, W = GF::W, WF = GF::WF, WH = GF::WH, HW = H * W, DK = kFusedDK, NP = 3 * DK;
+  // bins i = tid + NT j: j < BPT in registers, the NX = NB - BPT NT rest (tid < NX) with their state in LDS
+  constexpr int NT = GF::NT, NB = H * WF, NINT = H * (WH - 1), BPT = NB / NT, NX = NB - BPT * NT, BT = BPT + 1;
+  constexpr int NW = NT / 64, JL = GI::JLD;
+  static_assert(NX > 0 && NX <= 64, "the bins beyond BPT per thread fill at most one wave");
+  __shared__ __attribute__((aligned(16))) float smem[GF::LDS_FLOATS];
+  __shared__ float2 esp[NP * H * 2];
+  __shared__ float2 sx[NX * DK * DK];
+  __shared__ float red[NW * 2 * DK];
+  const PlaneFft<GF> fwd(smem);
+  const PlaneFft<GI> inv(smem, reinterpret_cast<float2*>(smem + GF::OFF_EDGE),
+                         reinterpret_cast<float2*>(smem + GF::OFF_TW));
+  const int tid = int(threadIdx.x);
+  const int w = __builtin_amdgcn_readfirstlane(tid / 64), l = tid % 64;
+  const int head = blockIdx.x, b = blockIdx.y;
+  const int T = a.T, C = a.C;
+  fwd.init_twiddles(tid);
+
+  // this thread's bins i = tid + NT j: interior (u, v) = (i / 15, 1 + i % 15) first (consecutive
+  // threads along a row), then the DC / Nyquist bins (u, 0 | W / 2) = ((i - NINT) / 2, ...)
+  auto bin_uv = [](int i, int& u, int& v) {
+    if (i < NINT) {
+      u = i / (WH - 1);
+      v = 1 + i % (WH - 1);
+    } else {
+      const int e = i - NINT;
+      u = e >> 1;
+      v = (e & 1) ? WH : 0;
+    }
+  };
+  float2 s[BPT][DK][DK];
+#pragma unroll
+  for (int j = 0; j < BPT; ++j)
 #pragma unroll
     for (int r = 0; r < DK; ++r)
 #pragma unroll
-      for (int c = 0; c < DK; ++c) {
-        // alpha W (delta_rc - beta k_r conj k_c)
-        const float2 kk_rc = cmulc(k[r], k[c]);
-        float2 m = make_float2(-beta * kk_rc.x, -beta * kk_rc.y);
-        if (r == c) m.x += 1.0f;
-        M[r][c] = goom_floor2(cmul(aw, m));
+      for (int c = 0; c < DK; ++c) s[j][r][c] = make_float2(0.f, 0.f);
+  for (int i = tid; i < NX * DK * DK; i += NT) sx[i] = make_float2(0.f, 0.f);
+  // LDS place of bin (u, v) of plane pl
+  auto bin_ptr = [&](int pl, int u, int v) -> float2* {
+    if (v == 0 || v == WH) return &esp[(pl * H + u) * 2 + (v ? 1 : 0)];
+    return reinterpret_cast<float2*>(smem + GF::row_off(pl, u / GF::H1 + GF::H2 * (u % GF::H1)) + GF::p_col(v));
+  };
+
+  // q, k, v planes of (b, t): three runs of DK contiguous planes, each loaded
+  // with the 4-plane group's mapping (wave w, its rows)
+  constexpr unsigned GB = unsigned(DK * HW * sizeof(float));
+  float4 pf[3][JL];
+  auto issue = [&](int t, int lane) {
+    const auto m = GI::v4_lane(lane);
+#pragma unroll
+    for (int g = 0; g < 3; ++g) {
+      const Buf src(a.qkv + ((size_t(b) * T + t) * 3 * C + size_t(g) * C + size_t(head) * DK) * HW, GB);
+#pragma unroll
+      for (int i = 0; i < JL; ++i) {
+        unsigned vo;
+        int so;
+        GI::template v4_goff<16>(w, i, m, vo, so);
+        src.ld(pf[g][i], vo, so);
       }
+    }
+  };
+  issue(0, l);
+
+  for (int t = 0; t < T; ++t) {
+    // Re-derive the thread index inside the loop so the compiler rebuilds the (cheap) LDS and
+    // bin addresses per step instead of holding them in registers for the whole scan
+    int tl = tid;
+    asm volatile("" : "+v"(tl));
+    __builtin_assume(tl >= 0 && tl < NT);
+    const int lane = tl % 64;
+    int bu[BT], bv[BT];
+    bool bok[BT];
 #pragma unroll
-    for (int i = 0; i < DK; ++i) {
-      float2 sn[DK];
+    for (int j = 0; j < BT; ++j) {
+      const int i = tl + NT * j;
+      bok[j] = i < NB;
+      bin_uv(bok[j] ? i : 0, bu[j], bv[j]);
+    }
+    __syncthreads();   // the previous step's inverse and stores are done with the buffer
+    {
+      const auto m = GI::v4_lane(lane);
+      const auto vcol = PlaneFft<GI>::v4_col(m.c4);
 #pragma unroll
-      for (int r = 0; r < DK; ++r) {
-        float2 acc = goom_floor2(cscale(cmulc(v[i], k[r]), beta));
+      for (int g = 0; g < 3; ++g)
 #pragma unroll
-        for (int c = 0; c < DK; ++c) {
-          acc.x = fmaf(M[r][c].x, s[i][c].x, fmaf(-M[r][c].y, s[i][c].y, acc.x));
-          acc.y = fmaf(M[r][c].x, s[i][c].y, fmaf(M[r][c].y, s[i][c].x, acc.y));
+        for (int i = 0; i < JL; ++i) inv.v4_put(GI::v4_row(w, i, m) + g * DK * H, vcol, pf[g][i]);
+    }
+    if (t + 1 < T) issue(t + 1, lane);
+    const size_t fr = size_t(b) * T + t;
+    float2 gab[BT], wh[BT];
+#pragma unroll
+    for (int j = 0; j < BT; ++j) {
+      const int bin = bu[j] * WF + bv[j];
+      gab[j] = bok[j] ? a.ab[fr * a.ab_frame + size_t(head) * a.ab_head + size_t(bin) * a.ab_bin]
+                      : make_float2(0.f, 0.f);
+      wh[j] = bok[j] ? a.what[size_t(head) * H * WF + bin] : make_float2(0.f, 0.f);
+    }
+    __syncthreads();
+
+    fwd.r1(w, lane);
+    fwd.r2(w, lane);
+    fwd.c1(w, lane);
+    const SpecKeepOp<GF> keep{smem, esp};
+    fwd.template c2<true, false>(w, lane, keep);
+    fwd.template edges<true, false>(w, lane, keep);
+    __syncthreads();
+
+    // spectral L2 norms of the q and k planes (the bins are 2 X here)
+    float nrm[2 * DK];
+#pragma unroll
+    for (int p = 0; p < 2 * DK; ++p) nrm[p] = 1.0f;
+    if (a.use_l2) {
+      float acc[2 * DK];
+#pragma unroll
+      for (int p = 0; p < 2 * DK; ++p) acc[p] = 0.0f;
+#pragma unroll
+      for (int j = 0; j < BT; ++j) {
+        if (!bok[j]) continue;
+#pragma unroll
+        for (int p = 0; p < 2 * DK; ++p) {
+          const float2 x = *bin_ptr(p, bu[j], bv[j]);
+          acc[p] = fmaf(x.x, x.x, fmaf(x.y, x.y, acc[p]));
         }
-        sn[r] = acc;
       }
-      float2 o = make_float2(0.f, 0.f);
 #pragma unroll
-      for (int r = 0; r < DK; ++r) {
-        s[i][r] = sn[r];
-        o.x = fmaf(sn[r].x, q[r].x, fmaf(-sn[r].y, q[r].y, o.x));
-        o.y = fmaf(sn[r].x, q[r].y, fmaf(sn[r].y, q[r].x, o.y));
+      for (int p = 0; p < 2 * DK; ++p) {
+        float x = acc[p];
+#pragma unroll
+        for (int d = 32; d >= 1; d >>= 1) x += __shfl_xor(x, d, 64);
+        if (lane == 0) red[w * 2 * DK + p] = x;
       }
-      a.ohat[(fr * C + size_t(head) * DK + i) * HWF + bin] = o;
+      __syncthreads();
+#pragma unroll
+      for (int p = 0; p < 2 * DK; ++p) {
+        float sum = 0.0f;
+#pragma unroll
+        for (int ww = 0; ww < NW; ++ww) sum += red[ww * 2 * DK + p];
+        nrm[p] = 1.0f / sqrtf(0.25f * sum + 1e-6f);
+      }
+    }
+
+    // the recurrence of each of this thread's bins; o / (H W) over its q slots
+    auto bin_step = [&](int j, float2 (&st)[DK][DK]) {
+      float2 q[DK], k[DK], v[DK], o[DK];
+#pragma unroll
+      for (int c = 0; c < DK; ++c) {
+        q[c] = cscale(*bin_ptr(c, bu[j], bv[j]), 0.5f * nrm[c]);
+        k[c] = cscale(*bin_ptr(DK + c, bu[j], bv[j]), 0.5f * nrm[DK + c]);
+        v[c] = cscale(*bin_ptr(2 * DK + c, bu[j], bv[j]), 0.5f);
+      }
+      gdn_bin_step<DK>(st, q, k, v, wh[j], gab[j].x, gab[j].y, o);
+#pragma unroll
+      for (int c = 0; c < DK; ++c) *bin_ptr(c, bu[j], bv[j]) = cscale(o[c], 1.0f / float(HW));
+    };
+#pragma unroll
+    for (int j = 0; j < BPT; ++j) bin_step(j, s[j]);
+    if (bok[BPT]) {
+      float2 st[DK][DK];
+#pragma unroll
+      for (int r = 0; r < DK; ++r)
+#pragma unroll
+        for (int c = 0; c < DK; ++c) st[r][c] = sx[(tl * DK + r) * DK + c];
+      bin_step(BPT, st);
+#pragma unroll
+      for (int r = 0; r < DK; ++r)
+#pragma unroll
+        for (int c = 0; c < DK; ++c) sx[(tl * DK + r) * DK + c] = st[r][c];
+    }
+    __syncthreads();
+
+    const SpecFromLdsOp<GI> from{smem, esp};
+    inv.template c2<false, true>(w, lane, from);
+    inv.template edges<false, true>(w, lane, from);
+    inv.i1_packed(w, lane);
+    inv.i2(w, lane);
+    inv.i3(w, lane);
+    inv.i4(w, lane);
+    {
+      const auto m = GI::v4_lane(lane);
+      const auto vcol = PlaneFft<GI>::v4_col(m.c4);
+      const Buf dst(a.o + (fr * C + size_t(head) * DK) * HW, GB);
+#pragma unroll
+      for (int i = 0; i < JL; ++i) {
+        unsigned vo;
+        int so;
+        GI::template v4_goff<16>(w, i, m, vo, so);
+        dst.st(inv.v4_get(GI::v4_row(w, i, m), vcol), vo, so);
+      }
     }
   }
+}
+
+// fused core: 32 x 32 planes, d_k = 4, float32 qkv / o
+bool gdn_core_fused_supported(int H, int W, int dk) { return H == 32 && W == 32 && dk == kFusedDK; }
+
+hipError_t launch_gdn_core_fused(const float* qkv, int use_l2, const float2* ab, long long ab_frame, int ab_head,
+                                 int ab_bin, const float2* what, int B, int T, int C, int H, int W, int dk, float* o,
+                                 hipStream_t s) {
+  if (!gdn_core_fused_supported(H, W, dk) || C % dk) return hipErrorInvalidValue;
+  GdnFusedArgs a;
+  a.qkv = qkv;
+  a.ab = ab;
+  a.ab_frame = ab_frame;
+  a.ab_head = ab_head;
+  a.ab_bin = ab_bin;
+  a.what = what;
+  a.o = o;
+  a.T = T;
+  a.C = C;
+  a.use_l2 = use_l2;
+  hipLaunchKernelGGL(gdn_core_fused32, dim3(unsigned(C / dk), unsigned(B)), dim3(256), 0, s, a);
+  return hipGetLastError();
 }
 
 hipError_t launch_gdn_scan_bins(const float2* spec, const float* norms, const float2* ab, long long ab_frame,

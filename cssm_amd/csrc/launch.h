@@ -89,6 +89,11 @@ int fft_planes_min_group(int H, int W);
 hipError_t launch_gdn_scan_bins(const float2* spec, const float* norms, const float2* ab, long long ab_frame,
                                 int ab_head, int ab_bin, const float2* what, int B, int T, int C, int H, int W,
                                 int dk, float2* ohat, hipStream_t s);
+// the GDN spectral core in one kernel (32 x 32 planes, d_k = 4): rfft2 -> norms -> delta rule -> irfft2
+bool gdn_core_fused_supported(int H, int W, int dk);
+hipError_t launch_gdn_core_fused(const float* qkv, int use_l2, const float2* ab, long long ab_frame, int ab_head,
+                                 int ab_bin, const float2* what, int B, int T, int C, int H, int W, int dk, float* o,
+                                 hipStream_t s);
 hipError_t launch_frame_mean(const void* x, int dtype, int F, int HW, int C, float* out, hipStream_t s);
 hipError_t launch_gdn_gates(const float* ctx, int B, int T, int C, int H, int W, int nh, const GdnGateWeights& w,
                             int temporal, float rope_base, const float* ttable, float2* ab, float2* bkv,

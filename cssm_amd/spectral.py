@@ -453,6 +453,30 @@ def gdn_scan_bins(spec: torch.Tensor, norms: Optional[torch.Tensor], ab: torch.T
     return ohat
 
 
+def gdn_core_fused_supported(H: int, W: int, delta_key_dim: int) -> bool:
+    return bool(_lib.load().cssm_gdn_core_fused_supported(H, W, delta_key_dim))
+
+
+def gdn_core_fused(qkv: torch.Tensor, use_l2: bool, ab: torch.Tensor, gate_type: str, what: torch.Tensor,
+                   delta_key_dim: int) -> torch.Tensor:
+    """The GDN spectral core in one kernel (cssm.py:4875-5025): plane-major float32 qkv
+    (B, T, 3C, H, W) -> o (B, T, C, H, W) float32, the irfft2 of the readout; the same as
+    :func:`rfft2` + :func:`gdn_scan_bins` + :func:`irfft2` where
+    :func:`gdn_core_fused_supported` holds."""
+    _dev(qkv, "qkv", torch.float32)
+    B, T, C3, H, W = qkv.shape
+    C = C3 // 3
+    _dev(ab, "ab", torch.float32)
+    _dev(what, "what", torch.complex64)
+    n_ab = ab.shape[2]
+    strides = {"dense": (n_ab, 0, 1), "factored": (n_ab, 0, 1), "channel": (n_ab, 1, 0), "scalar": (1, 0, 0)}
+    fs, hs, bs = strides[gate_type]
+    o = torch.empty((B, T, C, H, W), dtype=torch.float32, device=qkv.device)
+    _lib.call("cssm_gdn_core_fused", qkv.data_ptr(), int(bool(use_l2)), ab.data_ptr(), fs, hs, bs, what.data_ptr(),
+              B, T, C, H, W, delta_key_dim, o.data_ptr(), _stream())
+    return o
+
+
 def gdn_proj_out(o: torch.Tensor, gate: torch.Tensor, norm: str, norm_scale: Optional[torch.Tensor],
                  norm_bias: Optional[torch.Tensor], kernel: torch.Tensor, bias: torch.Tensor,
                  out_dtype: Optional[torch.dtype] = None) -> torch.Tensor:

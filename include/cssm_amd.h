@@ -376,6 +376,27 @@ int cssm_gdn_scan_bins(const float* spec, const float* norms, const float* ab, l
                        int ab_head, int ab_bin, const float* what, int B, int T, int C, int H, int W,
                        int delta_key_dim, float* ohat, void* stream);
 
+/*
+ * The GDN spectral core as one kernel where a workgroup can hold a (batch,
+ * head)'s state for all T (32 x 32 planes, delta_key_dim 4: the video-shaped
+ * config): per step it reads the head's q, k, v planes once, runs their rfft2,
+ * the spectral / key-vector norms, the delta rule and the readout S q, and
+ * writes the irfft2 of o once; no spectrum reaches HBM.  Replaces cssm.py:4875-5025,
+ * computing what cssm_rfft2 + cssm_gdn_scan_bins + cssm_irfft2 compute (the
+ * per-plane norm sums add in another order).
+ *   qkv    (B, T, 3C, H, W) float32 plane-major (the cssm_gdn_qkv_proj output)
+ *   use_l2 1 = spectral L2 norms of q and k (use_spectral_l2_norm), 0 = none
+ *   ab, ab_frame, ab_head, ab_bin, what: as cssm_gdn_scan_bins
+ *   o      (B, T, C, H, W) float32 out: the irfft2 of the readout, channel head*d_k + i
+ * qkv and o 16-byte aligned, ab and what 8.
+ */
+int cssm_gdn_core_fused(const float* qkv, int use_l2, const float* ab, long long ab_frame, int ab_head, int ab_bin,
+                        const float* what, int B, int T, int C, int H, int W, int delta_key_dim, float* o,
+                        void* stream);
+
+/* 1 if cssm_gdn_core_fused has a kernel for (H, W, delta_key_dim), else 0. */
+int cssm_gdn_core_fused_supported(int H, int W, int delta_key_dim);
+
 /* output_norm of GatedDeltaNetCSSM */
 typedef enum cssm_norm { CSSM_NORM_NONE = 0, CSSM_NORM_RMS = 1, CSSM_NORM_LAYER = 2 } cssm_norm;
 

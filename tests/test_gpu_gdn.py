@@ -268,6 +268,50 @@ def test_gdn_spectral_core_matches_oracle(mods, name, shape, dk, gate_type, l2):
     assert rel_err(to_np(o), ref) <= TOL_F32
 
 
+FUSED_CASES = [
+    # name, (B, T, H, W, C), gate_type, spectral l2 norm   (the fused core: 32 x 32, d_k = 4)
+    ("factored_l2", (2, 7, 32, 32, 16), "factored", True),
+    ("dense_no_l2", (1, 4, 32, 32, 8), "dense", False),
+    ("channel_l2", (2, 3, 32, 32, 12), "channel", True),
+    ("scalar_l2_T1", (3, 1, 32, 32, 8), "scalar", True),
+    ("c4_heads_T32", (1, 32, 32, 32, 64), "factored", True),
+]
+
+
+@pytest.mark.parametrize("name,shape,gate_type,l2", FUSED_CASES, ids=[c[0] for c in FUSED_CASES])
+def test_gdn_core_fused_matches_oracle_and_three_kernels(mods, name, shape, gate_type, l2):
+    """The one-kernel core (per (b, head), state in VGPRs over T) against the oracle's
+    materialised-M GOOM scan at the fp32 bar, and against rfft2 -> gdn_scan_bins -> irfft2
+    (the same FFT passes; only the per-plane norm sums add in another order)."""
+    _, S = mods
+    print_case(test="gdn_core_fused", case=name)
+    rng = np.random.default_rng(12)
+    B, T, H, W, C = shape
+    dk = 4
+    assert S.gdn_core_fused_supported(H, W, dk)
+    nh, Wf = C // dk, W // 2 + 1
+    cfg = O.GDNConfig(channels=C, delta_key_dim=dk, gate_type=gate_type, use_spectral_l2_norm=l2)
+    q, k, v = (rng.standard_normal(shape) for _ in range(3))
+    n_ab = {"factored": H * Wf, "dense": H * Wf, "channel": nh, "scalar": 1}[gate_type]
+    alpha = 0.1 + 0.89 / (1.0 + np.exp(-rng.standard_normal((B, T, n_ab))))
+    beta = 1.0 / (1.0 + np.exp(-rng.standard_normal((B, T, n_ab))))
+    what = O.spectral_kernel(rng.standard_normal((nh, 11, 11)) * 0.2, H, W, 0.999)
+    shp = (B, T, nh, 1, 1) if gate_type == "channel" else ((B, T, 1, 1, 1) if gate_type == "scalar"
+                                                           else (B, T, 1, H, Wf))
+    ref = O.gdn_core(q, k, v, alpha.reshape(shp), beta.reshape(shp), what, cfg, scan="linear")
+    planes = _dev(np.concatenate([z.transpose(0, 1, 4, 2, 3) for z in (q, k, v)], axis=2))
+    ab = _dev(np.stack([alpha, beta], axis=-1))
+    wd = _dev(what, torch.complex64)
+    o = S.gdn_core_fused(planes, l2, ab, gate_type, wd, dk)
+    spec, norms = S.rfft2(planes, want_norms=l2)
+    o3 = S.irfft2(S.gdn_scan_bins(spec, norms, ab, gate_type, wd, dk), W)
+    torch.cuda.synchronize()
+    assert rel_err(to_np(o), ref) <= TOL_F32
+    assert rel_err(to_np(o), to_np(o3)) <= 1e-5
+    # deterministic: the norm sums add in a fixed order
+    assert torch.equal(o, S.gdn_core_fused(planes, l2, ab, gate_type, wd, dk))
+
+
 def test_gdn_proj_out_norm_gate(mods):
     _, S = mods
     print_case(test="gdn_proj_out")
