@@ -233,6 +233,15 @@ struct Geom {
   }
 };
 
+// Policies may define `static constexpr bool kPrefetch = true` and
+// `prefetch(pl, k, n)`: called at the start of each column-pass unit, before
+// its column DFT, so loads the policy's bins() will need are in flight while
+// the DFT runs.
+template <class Op, class = void>
+struct op_prefetches : std::false_type {};
+template <class Op>
+struct op_prefetches<Op, std::void_t<decltype(Op::kPrefetch)>> : std::bool_constant<Op::kPrefetch> {};
+
 // pair-unit decode: pair jj of radix N1 -> units (kA, kB) with kB = -kA mod N1
 // (jj = 0 groups the two self-paired units 0 and N1/2)
 template <int N1>
@@ -496,6 +505,7 @@ struct PlaneFft {
       for (int a2 = 0; a2 < 2; ++a2) {
         const int k = a2 ? kB : kA;
         float2 sp[H2];
+        if constexpr (op_prefetches<Op>::value) op.prefetch(pl, k, n);
         if (FWD) {
 #pragma unroll
           for (int s = 0; s < H2; ++s) sp[s] = cplx(G::row_off(pl, s + H2 * k) + col);

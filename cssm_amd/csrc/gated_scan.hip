@@ -65,25 +65,43 @@ struct GatedScanOp {
   // the packed column's lanes may run bins(): their state slots serve no
   // other bin and their results are overwritten by the packed-column I1
   static constexpr bool kPackedColumnToo = true;
+  // gates in batches of QB bins (fewer registers in flight at 4 waves / SIMD); the
+  // first batch of a unit is issued before its column DFT (prefetch)
+  static constexpr bool kPrefetch = true;
+  static constexpr int QB = G::NT >= 512 ? 4 : G::H2;
   float2 (&h)[G::JC2][2][G::H2];
   float2* hE;   // LDS: state of the DC / Nyquist bins, 4 per edge job (pl, e)
   Buf gbuf;   // gates of (b, t): (H, WF) float4
   Buf kbuf;   // K_hat of the group's planes: (NP, H, WF) float2
+  float4 pg[QB];   // the unit's first gate batch, in flight during its column DFT
+  float2 pk[QB];
+
+  __device__ __forceinline__ void prefetch(int pl, int k, int n) {
+    const unsigned gi = unsigned(k * WF + n), ki = unsigned(pl * H * WF) + gi;
+#pragma unroll
+    for (int q = 0; q < QB; ++q) {
+      pg[q] = gbuf.ld4(gi * 16u, q * H1 * WF * 16);
+      pk[q] = kbuf.ld2(ki * 8u, q * H1 * WF * 8);
+    }
+  }
 
   // gates of (b, t) and the spectral kernel of this plane at bins (k + H1 q,
   // column at position n)
   __device__ __forceinline__ void bins(int j, int a2, int pl, int k, int n, float2 (&sp)[G::H2]) const {
     const unsigned gi = unsigned(k * WF + n), ki = unsigned(pl * H * WF) + gi;
-    // gates in batches of QB bins (fewer registers in flight at 4 waves / SIMD)
-    constexpr int QB = G::NT >= 512 ? 4 : H2;
 #pragma unroll
     for (int q0 = 0; q0 < H2; q0 += QB) {
       float4 gq[QB];
       float2 kq[QB];
 #pragma unroll
       for (int q = 0; q < QB; ++q) {
-        gq[q] = gbuf.ld4(gi * 16u, (q0 + q) * H1 * WF * 16);
-        kq[q] = kbuf.ld2(ki * 8u, (q0 + q) * H1 * WF * 8);
+        if (q0 == 0) {
+          gq[q] = pg[q];
+          kq[q] = pk[q];
+        } else {
+          gq[q] = gbuf.ld4(gi * 16u, (q0 + q) * H1 * WF * 16);
+          kq[q] = kbuf.ld2(ki * 8u, (q0 + q) * H1 * WF * 8);
+        }
       }
 #pragma unroll
       for (int q = 0; q < QB; ++q) sp[q0 + q] = scan_bin(h[j][a2][q0 + q], sp[q0 + q], gq[q], kq[q]);
