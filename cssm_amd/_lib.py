@@ -72,6 +72,7 @@ SIGNATURES = {
                                     ctypes.c_int, ctypes.c_void_p, ctypes.c_void_p, ctypes.c_void_p,
                                     ctypes.c_void_p, ctypes.c_int, ctypes.c_int, ctypes.c_int, ctypes.c_void_p,
                                     ctypes.c_void_p, ctypes.c_size_t, ctypes.c_void_p]),
+    "cssm_gated_scan_bwd": (_I, [_P, _P, _P, _P, _I, _I, _I, _I, _I, ctypes.c_float, _P, _P, _P, _P, _P]),
     "cssm_proj_in_workspace_size": (ctypes.c_size_t, [ctypes.c_int, ctypes.c_int, ctypes.c_int, ctypes.c_int]),
     "cssm_proj_in_noalloc": (_I, [_P, _I, _I, _I, _I, _I, _P, _P, _P, _P, _I, _I, _I, _P, _P]),
     "cssm_proj_out": (ctypes.c_int, [ctypes.c_void_p, ctypes.c_int, ctypes.c_int, ctypes.c_int, ctypes.c_int,

@@ -159,6 +159,27 @@ int cssm_gated_scan_fwd(const void* u, const void* z, void* y, int dtype, int B,
   return hip_status(e, "cssm_gated_scan_fwd");
 }
 
+int cssm_gated_scan_bwd(const float* uspec, const float* dspec, const float* gates, const float* khat, int B, int T,
+                        int C, int H, int W, float c_scale, float* yspec, float* sdu, float* dgates, float* dkhat,
+                        void* stream) {
+  if (!uspec || !dspec || !gates || !khat || !yspec || !sdu || !dgates || !dkhat)
+    return fail(CSSM_ERR_NULL, "cssm_gated_scan_bwd: null argument");
+  if (B <= 0 || T <= 0 || C <= 0 || H <= 0 || W <= 0 || W % 2 || !(c_scale > 0.0f))
+    return fail(CSSM_ERR_SHAPE, "cssm_gated_scan_bwd: B=%d T=%d C=%d H=%d W=%d c_scale=%g", B, T, C, H, W,
+                double(c_scale));
+  if (T > 32) return fail(CSSM_ERR_UNSUPPORTED, "cssm_gated_scan_bwd: T=%d (the reverse pass holds T <= 32 states)", T);
+  if (!aligned(gates, 16) || !aligned(dgates, 16) || !aligned(uspec, 8) || !aligned(dspec, 8) || !aligned(khat, 8) ||
+      !aligned(yspec, 8) || !aligned(sdu, 8) || !aligned(dkhat, 8))
+    return fail(CSSM_ERR_ALIGN, "cssm_gated_scan_bwd: gates 16-byte aligned, complex tensors 8");
+  return hip_status(cssm::launch_gated_scan_bwd_bins(
+                        reinterpret_cast<const float2*>(uspec), reinterpret_cast<const float2*>(dspec),
+                        reinterpret_cast<const float4*>(gates), reinterpret_cast<const float2*>(khat), B, T, C, H, W,
+                        c_scale, reinterpret_cast<float2*>(yspec), reinterpret_cast<float2*>(sdu),
+                        reinterpret_cast<float4*>(dgates), reinterpret_cast<float2*>(dkhat),
+                        static_cast<hipStream_t>(stream)),
+                    "cssm_gated_scan_bwd");
+}
+
 size_t cssm_proj_in_workspace_size(int F, int HW, int K, int N) {
   if (F <= 0 || HW <= 0 || K <= 0 || N <= 0) return 0;
   const int tm = cssm::proj_in_tile_rows(K), slots = cssm::proj_in_ctx_slots(K, HW);

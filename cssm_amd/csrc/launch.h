@@ -89,6 +89,10 @@ int fft_planes_min_group(int H, int W);
 hipError_t launch_gdn_scan_bins(const float2* spec, const float* norms, const float2* ab, long long ab_frame,
                                 int ab_head, int ab_bin, const float2* what, int B, int T, int C, int H, int W,
                                 int dk, float2* ohat, hipStream_t s);
+// backward of the gated scan: the spectral-domain reverse recurrence per (b, bin), T <= 32
+hipError_t launch_gated_scan_bwd_bins(const float2* uspec, const float2* dspec, const float4* gates,
+                                      const float2* khat, int B, int T, int C, int H, int W, float c_scale,
+                                      float2* yspec, float2* sdu, float4* dgates, float2* dkhat, hipStream_t s);
 // the GDN spectral core in one kernel (32 x 32 planes, d_k = 4): rfft2 -> norms -> delta rule -> irfft2
 bool gdn_core_fused_supported(int H, int W, int dk);
 hipError_t launch_gdn_core_fused(const float* qkv, int use_l2, const float2* ab, long long ab_frame, int ab_head,

@@ -142,6 +142,33 @@ def gated_scan(u: torch.Tensor, z: torch.Tensor, gates: torch.Tensor, khat: torc
     return out
 
 
+def gated_scan_backward(u: torch.Tensor, z: torch.Tensor, gates: torch.Tensor, khat: torch.Tensor,
+                        dy: torch.Tensor, c_scale: float):
+    """Vector-Jacobian product of :func:`gated_scan` (identity load activations) for the
+    cotangent dy of its output: returns (du, dz, dgates, dkhat) with the shapes and column
+    orders of (u, z, gates, khat).  Batched rfft2 of u and of dy * z, the per-bin reverse
+    recurrence (cssm_gated_scan_bwd), then batched irfft2 of the bin gradients and of C h."""
+    for t, n in ((u, "u"), (z, "z"), (dy, "dy")):
+        _dev(t, n, torch.float32)
+    B, T, C, H, W = u.shape
+    Wf = W // 2 + 1
+    _dev(gates, "gates", torch.float32)
+    _dev(khat, "khat", torch.complex64)
+    uspec, _ = rfft2(u)
+    dspec, _ = rfft2(dy * z)
+    yspec = torch.empty_like(uspec)
+    sdu = torch.empty_like(uspec)
+    dgates = torch.empty_like(gates)
+    dkh = torch.empty((B, C, H, Wf), dtype=torch.complex64, device=u.device)
+    _lib.call("cssm_gated_scan_bwd", uspec.data_ptr(), dspec.data_ptr(), gates.data_ptr(), khat.data_ptr(),
+              B, T, C, H, W, float(c_scale), yspec.data_ptr(), sdu.data_ptr(), dgates.data_ptr(), dkh.data_ptr(),
+              _stream())
+    del dspec, uspec
+    dz = dy * irfft2(yspec, W)
+    du = irfft2(sdu, W)
+    return du, dz, dgates, dkh.sum(dim=0)
+
+
 def gated_scan_supported(H: int, W: int) -> bool:
     return bool(_lib.load().cssm_gated_scan_supported(H, W))
 

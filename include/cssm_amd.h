@@ -155,6 +155,28 @@ int cssm_gated_scan_fwd(const void* u, const void* z, void* y, int dtype, int B,
                         int z_act, void* stream);
 
 /*
+ * Backward of cssm_gated_scan_fwd (with u_act = z_act = identity): the
+ * spectral-domain reverse recurrence.  Replaces the gradient jax.value_and_grad
+ * takes through cssm.py:531-581 (main.py:283; the log-space scan's custom VJPs,
+ * goom.py:47-137) -- the reverse scan over conj(A) of the linear recurrence.
+ * The caller runs the transforms' adjoints as batched FFTs around it:
+ *   uspec = cssm_rfft2(u), dspec = cssm_rfft2(dy) with dy = dL/dy * z (the
+ *   gradient at irfft2's output), and afterwards y_pre = cssm_irfft2(yspec)
+ *   (so dL/dz = dL/dy * y_pre) and dL/du = cssm_irfft2(sdu).
+ *   uspec, dspec     (B, T, C, H, Wf) complex64, natural column order
+ *   gates, khat      exactly as cssm_gated_scan_fwd read them (scan column order)
+ *   c_scale          the c_scale the gate planes were made with (1 / (2 H W))
+ *   yspec  (B, T, C, H, Wf) out: C h_t                  (natural order)
+ *   sdu    (B, T, C, H, Wf) out: dL/dU_t H W / c_v      (natural order; c_v = 2 inside 0 < v < W/2)
+ *   dgates (B, T, H, Wf, 4) out: dL/d(gate planes), summed over channels (scan order)
+ *   dkhat  (B, C, H, Wf)    out: dL/dkhat per batch element (sum over B; scan order)
+ * T <= 32; W even.
+ */
+int cssm_gated_scan_bwd(const float* uspec, const float* dspec, const float* gates, const float* khat, int B, int T,
+                        int C, int H, int W, float c_scale, float* yspec, float* sdu, float* dgates, float* dkhat,
+                        void* stream);
+
+/*
  * Input projection with the layout change to plane-major fused in.
  * Replaces cssm.py:480-484 (in_proj = Dense(2C) on channels-last x, split
  * into x_main and z), with the SiLU of cssm.py:502 / :581 optionally applied

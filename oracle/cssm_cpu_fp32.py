@@ -1,9 +1,11 @@
-"""float32 torch-CPU restatement of the CSSM layer: the reported CPU baseline.
+"""torch-CPU restatement of the CSSM layer: the reported CPU baseline (float32)
+and the gradient reference of the training path (float64).
 
 TEST INFRASTRUCTURE ONLY.  ``bench.py``'s ``cpu_baseline`` leg times this
 module on the host's cores (torch's intra-op threads), and ``tests/`` pins it
-against the float64 oracle (``oracle/cssm_oracle.py``).  The product path
-(``cssm_amd``) never imports it; it is never the thing measured on the GPU.
+against the float64 oracle (``oracle/cssm_oracle.py``) and, for gradients,
+against central finite differences.  The product path (``cssm_amd``) never
+imports it; it is never the thing measured on the GPU.
 
 It follows the reference's op order with torch CPU kernels in float32 /
 complex64, which is how the reference's JAX CPU path runs (the reference
@@ -28,15 +30,12 @@ import torch
 import torch.nn.functional as Fn
 
 
-def _t(a):
-    return torch.as_tensor(a, dtype=torch.float32)
-
-
-def params_to_torch(tree):
-    """Nested dict of numpy arrays -> float32 CPU tensors."""
+def params_to_torch(tree, dtype=torch.float32, requires_grad=False):
+    """Nested dict of numpy arrays -> CPU tensors of dtype (leaf tensors when requires_grad)."""
     if isinstance(tree, dict):
-        return {k: params_to_torch(v) for k, v in tree.items()}
-    return _t(tree).contiguous()
+        return {k: params_to_torch(v, dtype, requires_grad) for k, v in tree.items()}
+    t = torch.as_tensor(tree, dtype=dtype).clone().contiguous()
+    return t.requires_grad_(requires_grad)
 
 
 def _dense(x, p):
@@ -48,6 +47,30 @@ def _floor(z):
     r = torch.view_as_real(z)
     small = (r[..., 0] * r[..., 0] + r[..., 1] * r[..., 1]) < 1e-14
     return torch.where(small, torch.full_like(z, 1e-7), z)
+
+
+def scan_core(u, z, gates, khat, c_scale, cols):
+    """The contract of the fused scan kernel (cssm_gated_scan_fwd with identity load
+    activations): u, z (B, T, C, H, W); gates (B, T, H, Wf, 4) = [exp(-Delta),
+    (Delta + 1e-8) B, 2 VF, C c_scale] and floored khat (C, H, Wf), both with column p
+    holding frequency column cols[p].  Returns irfft2(C h_t) * z with
+    h_t = khat e^{-Delta_t} h_{t-1} + (V_t := (Delta + 1e-8) B U_t, or VF where |U_t B| < 1e-7)."""
+    inv = torch.argsort(torch.as_tensor(cols))
+    g = gates.index_select(3, inv)
+    kh = khat.index_select(2, inv)
+    B, T, C, H, W = u.shape
+    U = torch.fft.rfft2(u)
+    h = torch.zeros_like(U[:, 0])
+    Y = []
+    for t in range(T):
+        E, DB, VF2, GC = (g[:, t, None, ..., i] for i in range(4))
+        P = U[:, t] * DB
+        r = torch.view_as_real(P)
+        small = (r[..., 0] ** 2 + r[..., 1] ** 2) < (0.5 * VF2) ** 2
+        V = torch.where(small, (0.5 * VF2).to(P.dtype), P)
+        h = kh * E * h + V
+        Y.append(h * (GC / c_scale))
+    return torch.fft.irfft2(torch.stack(Y, 1), s=(H, W)) * z
 
 
 def _planes_in(x, p):
@@ -126,8 +149,9 @@ class GatedCPU:
     """GatedCSSM forward (cssm.py:476-585) in float32 on the CPU."""
 
     def __init__(self, params, channels, expand=1, kernel_size=11, spectral_rho=0.999, gate_type="factored",
-                 gate_activation="softplus", short_conv_size=0, short_conv_spatial_size=0):
-        self.p = params_to_torch(params)
+                 gate_activation="softplus", short_conv_size=0, short_conv_spatial_size=0, dtype=torch.float32,
+                 requires_grad=False):
+        self.p = params_to_torch(params, dtype, requires_grad)
         self.Ci = channels * expand
         self.rho = spectral_rho
         self.gate_type = gate_type
@@ -147,7 +171,7 @@ class GatedCPU:
         if self.kt > 0:
             xm = _causal_t(xm, p["short_conv_temporal"])
         xm = Fn.silu(xm)
-        if (H, W) not in self._khat:
+        if (H, W) not in self._khat or p["kernel"].requires_grad:
             self._khat[(H, W)] = _floor(spectral_kernel(p["kernel"], H, W, self.rho))
         kh = self._khat[(H, W)]
         U = torch.fft.rfft2(xm)                                         # (B, T, C, H, Wf)

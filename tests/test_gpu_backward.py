@@ -1,0 +1,121 @@
+"""GPU parity of the training path: the HIP scan VJP (batched FFTs around the reverse
+recurrence cssm_gated_scan_bwd) and the whole gated layer's gradients (x and every
+parameter) against float64 torch autograd of the restatement in oracle/cssm_cpu_fp32.py,
+which tests/test_grad_reference.py pins to finite differences and to the numpy oracle.
+Bar: max|g_gpu - g_ref| / RMS(g_ref) <= 1e-4 per gradient tensor (fp32 arithmetic)."""
+import numpy as np
+import pytest
+
+from oracle import cssm_oracle as O
+from tests.gpu_util import print_case, rel_err
+
+torch = pytest.importorskip("torch")
+pytestmark = pytest.mark.gpu
+from oracle import cssm_cpu_fp32 as P  # noqa: E402
+
+TOL = 1e-4
+F64 = torch.float64
+
+
+@pytest.fixture(scope="module")
+def mods():
+    if not torch.cuda.is_available():
+        pytest.skip("no GPU")
+    from cssm_amd import cells, spectral, training
+    return cells, spectral, training
+
+
+def _np(t):
+    t = t.detach().cpu()
+    return t.numpy() if not t.is_complex() else t.numpy().astype(np.complex128)
+
+
+SCAN_CASES = [(2, 4, 8, 16, 16), (1, 3, 8, 128, 128), (3, 1, 16, 32, 32), (1, 9, 8, 8, 8)]
+
+
+@pytest.mark.parametrize("shape", SCAN_CASES, ids=[f"{s[3]}x{s[4]}_T{s[1]}" for s in SCAN_CASES])
+def test_scan_vjp_matches_float64_reference(mods, shape):
+    _, S, _ = mods
+    print_case(test="scan_vjp", shape=shape)
+    rng = np.random.default_rng(40)
+    B, T, C, H, W = shape
+    Wf = W // 2 + 1
+    cols = np.array(S.scan_col_order(H, W))
+    cs = S.scan_c_scale(H, W)
+    u, z = rng.standard_normal(shape), rng.standard_normal(shape)
+    delta = O.softplus(rng.standard_normal((B, T, H, Wf)))
+    gB, gC = rng.standard_normal((B, T, H, Wf)), rng.standard_normal((B, T, H, Wf))
+    gates = np.stack([np.exp(-delta), (delta + 1e-8) * gB, 2e-7 * (delta + 1e-8), gC * cs], -1)[:, :, :, cols]
+    kh = O.goom_floor(0.95 * rng.random((C, H, Wf)) * np.exp(2j * np.pi * rng.random((C, H, Wf))))[:, :, cols]
+    dy = rng.standard_normal(shape)
+    ts = [torch.from_numpy(a).requires_grad_(True) for a in (u, z, gates, kh)]
+    ref_y = P.scan_core(*ts, cs, cols)
+    refs = torch.autograd.grad(ref_y, ts, torch.from_numpy(dy))
+    dev = [torch.from_numpy(np.ascontiguousarray(a)).to("cuda", torch.float32 if a.dtype != np.complex128
+                                                         else torch.complex64) for a in (u, z, gates, kh, dy)]
+    y = S.gated_scan(*dev[:4])
+    got = S.gated_scan_backward(*dev[:4], dev[4], cs)
+    torch.cuda.synchronize()
+    assert rel_err(_np(y), ref_y.detach().numpy()) <= TOL
+    for name, g, r in zip(("du", "dz", "dgates", "dkhat"), got, refs):
+        gn, rn = _np(g), r.numpy()
+        assert gn.shape == rn.shape, name
+        if np.iscomplexobj(rn):
+            gn, rn = np.stack([gn.real, gn.imag]), np.stack([rn.real, rn.imag])
+        assert rel_err(gn, rn) <= TOL, name
+
+
+LAYER_CASES = [
+    ("factored_16", (2, 3, 16, 16, 8), dict(channels=8, kernel_size=5, gate_type="factored", short_conv_size=0,
+                                            short_conv_spatial_size=0)),
+    ("dense_convs_sigmoid_8", (1, 4, 8, 8, 8), dict(channels=8, kernel_size=3, gate_type="dense", short_conv_size=3,
+                                                    short_conv_spatial_size=3, gate_activation="sigmoid")),
+    ("c1_expand2_T1_k1", (4, 1, 32, 32, 16), dict(channels=16, expand=2, kernel_size=1, gate_type="factored",
+                                                  short_conv_size=0, short_conv_spatial_size=0)),
+    ("factored_128_exp", (1, 2, 128, 128, 4), dict(channels=4, kernel_size=11, gate_type="factored",
+                                                   gate_activation="exp", short_conv_size=2,
+                                                   short_conv_spatial_size=0)),
+]
+
+
+def _leaves(tree, prefix=""):
+    if isinstance(tree, dict):
+        out = []
+        for k, v in tree.items():
+            out += _leaves(v, f"{prefix}/{k}")
+        return out
+    return [(prefix, tree)]
+
+
+@pytest.mark.parametrize("name,shape,kw", LAYER_CASES, ids=[c[0] for c in LAYER_CASES])
+def test_layer_gradients_match_float64_reference(mods, name, shape, kw):
+    cells, _, training = mods
+    print_case(test="layer_grad", case=name)
+    rng = np.random.default_rng(41)
+    cfg = O.GatedConfig(**kw)
+    p = O.init_params(O.gated_param_shapes(cfg, shape[-1], shape[2], shape[3]), rng)
+    x = rng.standard_normal(shape)
+    ref_m = P.GatedCPU(p, dtype=F64, requires_grad=True, **kw)
+    xr = torch.from_numpy(x).requires_grad_(True)
+    out_r = ref_m(xr)
+    w = rng.standard_normal(tuple(out_r.shape))
+    ref_leaves = [("x", xr)] + _leaves(ref_m.p)
+    refs = torch.autograd.grad((out_r * torch.from_numpy(w)).sum(), [t for _, t in ref_leaves])
+
+    cell = cells.GatedCSSM(**kw)
+    v = cells.GatedCSSM.load_params(p)
+    leaves = _leaves(v["params"])
+    for _, t in leaves:
+        t.requires_grad_(True)
+    xd = torch.from_numpy(x).to("cuda", torch.float32).requires_grad_(True)
+    out = training.gated_train_apply(cell, v, xd)
+    with torch.no_grad():
+        assert rel_err(_np(out), out_r.detach().numpy()) <= TOL
+        assert rel_err(_np(out), _np(cell.apply(v, xd.detach()))) <= 1e-5
+    grads = torch.autograd.grad((out * torch.from_numpy(w).to("cuda", torch.float32)).sum(),
+                                [xd] + [t for _, t in leaves])
+    torch.cuda.synchronize()
+    names = ["x"] + [n for n, _ in leaves]
+    assert names == [n for n, _ in ref_leaves]
+    for n, g, r in zip(names, grads, refs):
+        assert rel_err(_np(g), r.numpy()) <= TOL, n

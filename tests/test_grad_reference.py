@@ -1,0 +1,124 @@
+"""The float64 gradient reference of the training path (oracle/cssm_cpu_fp32.py at
+float64): its forward equals the numpy oracle, and its autograd gradient equals central
+finite differences along random directions, for the whole gated layer and for the scan
+kernel's own contract (gate planes and K_hat in scan column order).  CPU only."""
+import numpy as np
+import pytest
+
+from oracle import cssm_oracle as O
+
+torch = pytest.importorskip("torch")
+from oracle import cssm_cpu_fp32 as P  # noqa: E402
+
+F64 = torch.float64
+LAYERS = [
+    dict(channels=4, expand=1, kernel_size=5, gate_type="factored", short_conv_size=0, short_conv_spatial_size=0),
+    dict(channels=4, expand=1, kernel_size=3, gate_type="dense", short_conv_size=3, short_conv_spatial_size=3,
+         gate_activation="sigmoid"),
+    dict(channels=3, expand=2, kernel_size=1, gate_type="factored", short_conv_size=0, short_conv_spatial_size=0,
+         gate_activation="exp"),
+]
+
+
+def _layer(kw, shape, seed):
+    rng = np.random.default_rng(seed)
+    cfg = O.GatedConfig(**kw)
+    p = O.init_params(O.gated_param_shapes(cfg, shape[-1], shape[2], shape[3]), rng)
+    x = rng.standard_normal(shape)
+    return cfg, p, x
+
+
+def _leaves(tree):
+    if isinstance(tree, dict):
+        out = []
+        for v in tree.values():
+            out += _leaves(v)
+        return out
+    return [tree]
+
+
+@pytest.mark.parametrize("kw", LAYERS)
+def test_float64_layer_forward_equals_oracle(kw):
+    cfg, p, x = _layer(kw, (2, 3, 8, 8, kw["channels"]), 0)
+    got = P.GatedCPU(p, dtype=F64, **kw)(torch.from_numpy(x)).numpy()
+    ref = O.gated_forward(p, x, cfg)
+    assert np.max(np.abs(got - ref)) <= 1e-11 * np.sqrt(np.mean(ref ** 2))
+
+
+@pytest.mark.parametrize("kw", LAYERS)
+def test_float64_layer_gradient_equals_finite_differences(kw):
+    """<grad L, v> against (L(theta + e v) - L(theta - e v)) / 2e, L = <out, w>, over x and
+    every parameter at once, along three random directions."""
+    cfg, p, x = _layer(kw, (1, 3, 8, 8, kw["channels"]), 1)
+    rng = np.random.default_rng(2)
+    m = P.GatedCPU(p, dtype=F64, requires_grad=True, **kw)
+    xt = torch.from_numpy(x).requires_grad_(True)
+    leaves = [xt] + _leaves(m.p)
+    out = m(xt)
+    w = torch.from_numpy(rng.standard_normal(out.shape))
+    grads = torch.autograd.grad((out * w).sum(), leaves)
+    for _ in range(3):
+        vs = [torch.from_numpy(rng.standard_normal(t.shape)) for t in leaves]
+        analytic = sum(float((g * v).sum()) for g, v in zip(grads, vs))
+        eps = 1e-6
+
+        def loss(sign):
+            with torch.no_grad():
+                for t, v in zip(leaves, vs):
+                    t.add_(sign * eps * v)
+                val = float((m(xt) * w).sum())
+                for t, v in zip(leaves, vs):
+                    t.sub_(sign * eps * v)
+            return val
+        fd = (loss(1.0) - loss(-1.0)) / (2 * eps)
+        assert abs(fd - analytic) <= 1e-6 * max(1.0, abs(analytic)), (fd, analytic)
+
+
+def _core_inputs(rng, B, T, C, H, W):
+    Wf = W // 2 + 1
+    u = rng.standard_normal((B, T, C, H, W))
+    z = rng.standard_normal((B, T, C, H, W))
+    delta = O.softplus(rng.standard_normal((B, T, H, Wf)))
+    gB, gC = rng.standard_normal((B, T, H, Wf)), rng.standard_normal((B, T, H, Wf))
+    kh = O.goom_floor(0.9 * np.exp(2j * np.pi * rng.random((C, H, Wf))) * rng.random((C, H, Wf)))
+    return u, z, delta, gB, gC, kh
+
+
+def test_scan_core_contract_equals_oracle():
+    """The kernel-contract restatement (gate planes with the folded GOOM terms, a permuted
+    column order) reproduces the oracle's gated_core."""
+    rng = np.random.default_rng(3)
+    B, T, C, H, W = 2, 4, 3, 8, 8
+    u, z, delta, gB, gC, kh = _core_inputs(rng, B, T, C, H, W)
+    ref = O.gated_core(u, z, kh, delta, gB, gC)
+    cols = np.array([0, 3, 1, 4, 2])                  # any permutation of the Wf columns
+    cs = 0.5 / (H * W)
+    gates = np.stack([np.exp(-delta), (delta + 1e-8) * gB, 2e-7 * (delta + 1e-8), gC * cs], -1)[:, :, :, cols]
+    got = P.scan_core(torch.from_numpy(u), torch.from_numpy(z), torch.from_numpy(gates),
+                      torch.from_numpy(kh[:, :, cols]), cs, cols).numpy()
+    assert np.max(np.abs(got - ref)) <= 1e-12 * np.sqrt(np.mean(ref ** 2))
+
+
+def test_scan_core_gradient_equals_finite_differences():
+    rng = np.random.default_rng(4)
+    B, T, C, H, W = 1, 3, 2, 8, 8
+    u, z, delta, gB, gC, kh = _core_inputs(rng, B, T, C, H, W)
+    cols = np.arange(W // 2 + 1)
+    cs = 0.5 / (H * W)
+    gates = np.stack([np.exp(-delta), (delta + 1e-8) * gB, 2e-7 * (delta + 1e-8), gC * cs], -1)
+    ts = [torch.from_numpy(a).requires_grad_(True) for a in (u, z, gates, kh)]
+    out = P.scan_core(*ts, cs, cols)
+    w = torch.from_numpy(rng.standard_normal(out.shape))
+    grads = torch.autograd.grad((out * w).sum(), ts)
+    for _ in range(3):
+        vs = [torch.from_numpy(rng.standard_normal(t.shape) + (1j * rng.standard_normal(t.shape) if t.is_complex()
+                                                               else 0)) for t in ts]
+        analytic = sum(float((g.conj() * v).real.sum()) if g.is_complex() else float((g * v).sum())
+                       for g, v in zip(grads, vs))
+        eps = 1e-6
+
+        def loss(sign):
+            with torch.no_grad():
+                return float((P.scan_core(*[t + sign * eps * v for t, v in zip(ts, vs)], cs, cols) * w).sum())
+        fd = (loss(1.0) - loss(-1.0)) / (2 * eps)
+        assert abs(fd - analytic) <= 1e-6 * max(1.0, abs(analytic)), (fd, analytic)
