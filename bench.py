@@ -18,8 +18,9 @@ A step is one full layer forward with x already in HBM:
 value = frames/s = B * T / step time (whole layer), from K timed steps.
 
 roofline: the dominant kernel, timed with HIP events on its stream over a
-second run of K steps with an event after every kernel (recording events costs
-the launch-bound stack workload idle GPU time, so value comes from the first).  gated: the fused scan, algorithmic bytes per launch
+second run of K steps with an event after every kernel, each step queued behind
+a bounded spin kernel so that the spans hold GPU time only (value comes from the
+first run, which records nothing).  gated: the fused scan, algorithmic bytes per launch
 B*T*(3*H*W*C*s + 3*(H+W/2+1)*4) + C*H*(W/2+1)*8 (read u and z, write y, read the
 factored gate vectors, K_hat once).  gdn: the spectral core (rfft2 + scan +
 irfft2 launches together), B*T*(4*H*W*C*s + 2*(H+W/2+1)*4) + n_h*H*(W/2+1)*8
@@ -387,18 +388,27 @@ def run_workload(key, args, torch, cells, S, headline):
     el = time.perf_counter() - t0
     ms_step = el * 1e3 / steps
     # timed region 2: the same steps with a HIP event recorded after every kernel on the stream
-    # they run on (per-kernel times, the dominant kernel's roofline).  Recording an event costs
-    # the launch-bound workloads (C5: 45 per step) idle GPU time, so value comes from region 1.
-    pool = [torch.cuda.Event(enable_timing=True) for _ in range(steps * per_step)]
+    # they run on (per-kernel times, the dominant kernel's roofline).  Each step is queued behind
+    # a bounded spin kernel (torch.cuda._sleep) long enough for the host to enqueue the whole
+    # step first, so no span contains GPU idle time spent waiting for the host (event records
+    # cost the launch-bound workloads -- C5: 55 per step -- more host time than the GPU needs).
+    pool = [torch.cuda.Event(enable_timing=True) for _ in range(steps * per_step + 2)]
+    e0, e1 = pool.pop(), pool.pop()
+    cal = 1_000_000
+    e0.record()
+    torch.cuda._sleep(cal)
+    e1.record()
+    torch.cuda.synchronize()
+    cycles_per_ms = cal / max(e0.elapsed_time(e1), 1e-3)
+    head = int(cycles_per_ms * (2.0 * ms_step + 1.0))
     torch.cuda.synchronize()
     marks = []
-    t0 = time.perf_counter()
     for _ in range(steps):
+        torch.cuda._sleep(head)
         m = Marks(torch, True, pool)
         step(cell, variables, x, w, S, m)
         marks.append(m)
     torch.cuda.synchronize()
-    ms_step_marked = (time.perf_counter() - t0) * 1e3 / steps
     # the instrumented step must equal the module's forward bit for bit
     if w["cell"] == "stack":
         ref = None
@@ -449,7 +459,8 @@ def run_workload(key, args, torch, cells, S, headline):
         "steps": steps,
         "warmup": args.warmup,
         "ms_per_step": ms_step,
-        "ms_per_step_with_kernel_events": round(ms_step_marked, 4),
+        # sum of the per-kernel spans of one step: GPU time of the step's kernels back to back
+        "ms_kernel_sum": round(sum(kern_ms.values()), 4),
         "higher_is_better": True,
         "scaling": "weak",
         "vs_baseline": None,
