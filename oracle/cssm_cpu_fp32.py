@@ -171,9 +171,14 @@ class GatedCPU:
         if self.kt > 0:
             xm = _causal_t(xm, p["short_conv_temporal"])
         xm = Fn.silu(xm)
-        if (H, W) not in self._khat or p["kernel"].requires_grad:
-            self._khat[(H, W)] = _floor(spectral_kernel(p["kernel"], H, W, self.rho))
-        kh = self._khat[(H, W)]
+        # K_hat is reused only for the same kernel tensor object when no derivative flows through it
+        # (a perturbed, differentiated or forward-mode dual kernel is recomputed)
+        kern = p["kernel"]
+        hit = self._khat.get((H, W))
+        if hit is None or hit[0] is not kern or kern.requires_grad:
+            hit = (kern, _floor(spectral_kernel(kern, H, W, self.rho)))
+            self._khat[(H, W)] = hit
+        kh = hit[1]
         U = torch.fft.rfft2(xm)                                         # (B, T, C, H, Wf)
         ctx = xm.mean(dim=(3, 4))
 

@@ -2,7 +2,9 @@
 recurrence cssm_gated_scan_bwd) and the whole gated layer's gradients (x and every
 parameter) against float64 torch autograd of the restatement in oracle/cssm_cpu_fp32.py,
 which tests/test_grad_reference.py pins to finite differences and to the numpy oracle.
-Bar: max|g_gpu - g_ref| / RMS(g_ref) <= 1e-4 per gradient tensor (fp32 arithmetic)."""
+Bar: max|g_gpu - g_ref| / RMS(g_ref) <= 1e-4 per gradient tensor (fp32 arithmetic); the
+adjoint identity <v, J^T w> = <J v, w> against float64 forward-mode AD holds to 1e-4 of
+sum |grad| |v| (the fp32 dot product's own error bound)."""
 import numpy as np
 import pytest
 
@@ -119,3 +121,50 @@ def test_layer_gradients_match_float64_reference(mods, name, shape, kw):
     assert names == [n for n, _ in ref_leaves]
     for n, g, r in zip(names, grads, refs):
         assert rel_err(_np(g), r.numpy()) <= TOL, n
+
+
+def _dot(a, b):
+    return float((a.conj() * b).real.sum()) if a.is_complex() else float((a * b).sum())
+
+
+@pytest.mark.parametrize("name,shape,kw", LAYER_CASES[:2], ids=[c[0] for c in LAYER_CASES[:2]])
+def test_layer_vjp_adjoint_to_float64_jvp(mods, name, shape, kw):
+    """<v, J^T w> from the HIP backward equals <J v, w> from float64 forward-mode AD of the
+    restatement (a derivative computed without any reverse pass), over x and every parameter."""
+    cells, _, training = mods
+    print_case(test="layer_adjoint", case=name)
+    rng = np.random.default_rng(42)
+    cfg = O.GatedConfig(**kw)
+    p = O.init_params(O.gated_param_shapes(cfg, shape[-1], shape[2], shape[3]), rng)
+    x = rng.standard_normal(shape)
+    m = P.GatedCPU(p, dtype=F64, **kw)
+    slots = []
+
+    def collect(tree):
+        for k, v in tree.items():
+            collect(v) if isinstance(v, dict) else slots.append((tree, k))
+    collect(m.p)
+    prim = [torch.from_numpy(x)] + [d[k] for d, k in slots]
+    tang = [torch.from_numpy(rng.standard_normal(tuple(t.shape))) for t in prim]
+
+    def f(xx, *leaves):
+        for (d, k), t in zip(slots, leaves):
+            d[k] = t
+        return m(xx)
+    y, jv = torch.func.jvp(f, tuple(prim), tuple(tang))
+    w = torch.from_numpy(rng.standard_normal(tuple(y.shape)))
+    lhs = _dot(jv, w)
+
+    cell = cells.GatedCSSM(**kw)
+    v = cells.GatedCSSM.load_params(p)
+    leaves = _leaves(v["params"])
+    assert [n for n, _ in leaves] == [n for n, _ in _leaves(m.p)]        # tangents pair with gradients
+    for _, t in leaves:
+        t.requires_grad_(True)
+    xd = torch.from_numpy(x).to("cuda", torch.float32).requires_grad_(True)
+    out = training.gated_train_apply(cell, v, xd)
+    grads = torch.autograd.grad((out * w.to("cuda", torch.float32)).sum(), [xd] + [t for _, t in leaves])
+    torch.cuda.synchronize()
+    rhs = sum(_dot(g.double().cpu(), t) for g, t in zip(grads, tang))
+    scale = sum(float(g.double().cpu().norm() * t.norm()) for g, t in zip(grads, tang))
+    assert abs(lhs - rhs) <= 1e-4 * scale, (lhs, rhs, scale)

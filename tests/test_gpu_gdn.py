@@ -67,13 +67,20 @@ def test_irfft2_c2r_rule_matches_numpy(mods, P, H):
 
 
 def test_rfft2_irfft2_round_trip_full_c3_plane_count(mods):
-    """Size-independent check at the C3 plane shape: irfft2(rfft2(x)) = x."""
+    """Size-independent check at C3's full plane count (B*T*3C = 128*8*192 = 196,608 planes of
+    128x128, the q/k/v planes one C3 layer transforms): irfft2(rfft2(x)) = x.  ~39 GB resident."""
     _, S = mods
-    print_case(test="fft_round_trip", P=384, H=128)
-    x = torch.randn((384, 128, 128), device="cuda", generator=torch.Generator(device="cuda").manual_seed(5))
+    P = 128 * 8 * 3 * 64
+    print_case(test="fft_round_trip", P=P, H=128)
+    x = torch.randn((P, 128, 128), device="cuda", generator=torch.Generator(device="cuda").manual_seed(5))
+    rms = float(x.pow(2).mean().sqrt())
     spec, _ = S.rfft2(x)
     y = S.irfft2(spec, 128)
-    assert float((y - x).abs().max()) / float(x.pow(2).mean().sqrt()) < 2e-6
+    del spec
+    err = float(y.sub_(x).abs_().max())
+    del x, y
+    torch.cuda.empty_cache()
+    assert err / rms < 2e-6
 
 
 # ------------------------------------------------------------ prologue ops

@@ -122,3 +122,56 @@ def test_scan_core_gradient_equals_finite_differences():
                 return float((P.scan_core(*[t + sign * eps * v for t, v in zip(ts, vs)], cs, cols) * w).sum())
         fd = (loss(1.0) - loss(-1.0)) / (2 * eps)
         assert abs(fd - analytic) <= 1e-6 * max(1.0, abs(analytic)), (fd, analytic)
+
+
+def _slots(tree):
+    """(dict, key) of every leaf, in the order _leaves lists them."""
+    out = []
+    for k, v in tree.items():
+        out += _slots(v) if isinstance(v, dict) else [(tree, k)]
+    return out
+
+
+def _dot(a, b):
+    return float((a.conj() * b).real.sum()) if a.is_complex() else float((a * b).sum())
+
+
+def test_scan_core_adjoint_identity():
+    """<J v, w> (forward mode, torch.func.jvp) = <v, J^T w> (reverse mode) for the scan contract."""
+    rng = np.random.default_rng(6)
+    B, T, C, H, W = 2, 4, 3, 8, 8
+    u, z, delta, gB, gC, kh = _core_inputs(rng, B, T, C, H, W)
+    cols = np.array([0, 3, 1, 4, 2])
+    cs = 0.5 / (H * W)
+    gates = np.stack([np.exp(-delta), (delta + 1e-8) * gB, 2e-7 * (delta + 1e-8), gC * cs], -1)[:, :, :, cols]
+    prim = [torch.from_numpy(a) for a in (u, z, gates, kh[:, :, cols])]
+    tang = [torch.from_numpy(rng.standard_normal(t.shape) + (1j * rng.standard_normal(t.shape) if t.is_complex()
+                                                            else 0)) for t in prim]
+    y, jv = torch.func.jvp(lambda *a: P.scan_core(*a, cs, cols), tuple(prim), tuple(tang))
+    w = torch.from_numpy(rng.standard_normal(tuple(y.shape)))
+    ts = [t.clone().requires_grad_(True) for t in prim]
+    g = torch.autograd.grad((P.scan_core(*ts, cs, cols) * w).sum(), ts)
+    lhs, rhs = _dot(jv, w), sum(_dot(a, b) for a, b in zip(g, tang))
+    assert abs(lhs - rhs) <= 1e-12 * abs(lhs)
+
+
+@pytest.mark.parametrize("kw", LAYERS)
+def test_float64_layer_adjoint_identity(kw):
+    """<J v, w> = <v, J^T w> for the whole layer over x and every parameter at once."""
+    cfg, p, x = _layer(kw, (2, 3, 8, 8, kw["channels"]), 7)
+    rng = np.random.default_rng(8)
+    m = P.GatedCPU(p, dtype=F64, **kw)
+    slots = _slots(m.p)
+    prim = [torch.from_numpy(x)] + [d[k] for d, k in slots]
+    tang = [torch.from_numpy(rng.standard_normal(tuple(t.shape))) for t in prim]
+
+    def f(xx, *leaves):
+        for (d, k), t in zip(slots, leaves):
+            d[k] = t
+        return m(xx)
+    y, jv = torch.func.jvp(f, tuple(prim), tuple(tang))
+    w = torch.from_numpy(rng.standard_normal(tuple(y.shape)))
+    ts = [t.detach().clone().requires_grad_(True) for t in prim]
+    g = torch.autograd.grad((f(*ts) * w).sum(), ts)
+    lhs, rhs = _dot(jv, w), sum(_dot(a, b) for a, b in zip(g, tang))
+    assert abs(lhs - rhs) <= 1e-11 * abs(lhs), (lhs, rhs)
