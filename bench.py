@@ -393,6 +393,9 @@ def run_workload(key, args, torch, cells, S, headline):
     # step first, so no span contains GPU idle time spent waiting for the host (event records
     # cost the launch-bound workloads -- C5: 55 per step -- more host time than the GPU needs).
     pool = [torch.cuda.Event(enable_timing=True) for _ in range(steps * per_step + 2)]
+    for ev in pool:             # an event's first record sets it up on the host: done here, untimed
+        ev.record()
+    torch.cuda.synchronize()
     e0, e1 = pool.pop(), pool.pop()
     cal = 1_000_000
     e0.record()

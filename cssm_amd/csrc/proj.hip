@@ -475,6 +475,20 @@ proj_persist_kernel(const TI* __restrict__ A, int M, int K, int N, const float* 
 
   float4 pf[PF];
   float4 pg[NORM ? PF : 1];
+  // qkv epilogue: a tile's per-pixel / per-frame input gates (TT frames x TP pixels) are
+  // loaded with its A rows and written to gsh by the stash, behind the barrier that follows it
+  const bool tile_gates = TT > 0 && (qp.gate_mode == 1 || qp.gate_mode == 2);
+  float2 gpf = make_float2(0.f, 0.f);
+  auto fetch_gates = [&](int tl) {
+    if constexpr (TT > 0) {
+      if (tile_gates && tid < TT * TP) {
+        const int ch = tl % nch, tq = tl / nch, tpf = HW / TP, bb = tq / tpf, pb = tq % tpf;
+        const size_t fr = size_t(bb) * (CARRY ? qp.T : TT) + size_t(ch) * TT + tid / TP;
+        gpf = qp.gate_mode == 1 ? static_cast<const float2*>(qp.gates)[fr * HW + pb * TP + tid % TP]
+                                : static_cast<const float2*>(qp.gates)[fr];
+      }
+    }
+  };
   // k-th tile of this workgroup.  The qkv epilogue (TT > 0) writes half cache
   // lines (16 pixels of a plane) per tile; the workgroup takes its pixel blocks
   // in adjacent pairs so both halves of each line pass through the same L2, and
@@ -491,11 +505,15 @@ proj_persist_kernel(const TI* __restrict__ A, int M, int K, int N, const float* 
   int tile = tile_of(0);
   if (tile < tiles) {
     fetch(A, tile, pf);
+    fetch_gates(tile);
     if (NORM) fetch(Gp, tile, pg);
   }
   for (; tile < tiles; tile = tile_of(++kt_)) {
-    __syncthreads();            // previous tile is done with As (and Bs is staged)
+    __syncthreads();            // previous tile is done with As, gsh (and Bs is staged)
     stash(pf);
+    if constexpr (TT > 0) {
+      if (tile_gates && tid < TT * TP) gsh[tid] = gpf;
+    }
     __syncthreads();
     if constexpr (NORM) {
       norm_gate(pg);
@@ -504,6 +522,7 @@ proj_persist_kernel(const TI* __restrict__ A, int M, int K, int N, const float* 
     const int next = tile_of(kt_ + 1);
     if (next < tiles) {
       fetch(A, next, pf);
+      fetch_gates(next);
       if (NORM) fetch(Gp, next, pg);
     }
 
@@ -572,16 +591,7 @@ proj_persist_kernel(const TI* __restrict__ A, int M, int K, int N, const float* 
       const int ch = tile % nch, tq = tile / nch, tpf = HW / TP, bb = tq / tpf, pb = tq % tpf;
       const size_t fr0 = size_t(bb) * (CARRY ? qp.T : TT) + size_t(ch) * TT;   // first frame of the tile
       const int C = N / 3;
-      // per-pixel / per-frame input gates of the tile (TT frames x TP pixels x (B_k, B_v)) through LDS
-      if (qp.gate_mode == 1 || qp.gate_mode == 2) {
-        for (int e = tid; e < TT * TP; e += NT) {
-          const int t = e / TP, p = e % TP;
-          const size_t fr = fr0 + t;
-          gsh[e] = qp.gate_mode == 1 ? static_cast<const float2*>(qp.gates)[fr * HW + pb * TP + p]
-                                     : static_cast<const float2*>(qp.gates)[fr];
-        }
-        __syncthreads();
-      }
+      // the tile's input gates (TT frames x TP pixels x (B_k, B_v)) are in gsh (staged with A)
 #pragma unroll
       for (int j = 0; j < 2; ++j) {
         const int cl = wn * 32 + j * 16 + (lane & 15), gn = n0 + cl;
