@@ -542,7 +542,8 @@ def gdn_core(q_in, k_in, v_in, alpha, beta, W_hat, cfg: GDNConfig, scan='linear'
     scan='linear': materialises M_t and Delta_t with the GOOM floors and runs the
     complex linear recurrence s_t = M_t s_{t-1} + Delta_t[i,:] (exact algebra of the
     log-space scan); scan='rank1': the same recurrence in rank-1 form without
-    materialising M (no floors on M entries), as the HIP kernel evaluates it.
+    materialising M and with no floors on M or Delta entries -- equal to 'linear'
+    wherever no entry reaches the floor.
     """
     B, T, H, W, C = q_in.shape
     dk = cfg.delta_key_dim

@@ -285,6 +285,46 @@ FUSED_CASES = [
 ]
 
 
+@pytest.mark.parametrize("H", [32, 16])
+def test_gdn_core_floored_heads(mods, H):
+    """Heads whose keys or values vanish drive the per-bin step onto its materialised-M path
+    (to_goom's floor takes entries of M and Delta); checked per head against the oracle, so a
+    floored head's small output is not hidden by the others' RMS.  Head 0: k = 0 (every
+    off-diagonal M entry and all of Delta floored); head 1: k with one nonzero component;
+    head 2: v = 0 (Delta floored); head 3: unconstrained.  H = 32 runs the fused core, H = 16
+    the three-kernel core."""
+    _, S = mods
+    print_case(test="gdn_core_floored_heads", H=H)
+    rng = np.random.default_rng(31)
+    B, T, W, C, dk = 1, 4, H, 16, 4
+    shape = (B, T, H, W, C)
+    nh, Wf = C // dk, W // 2 + 1
+    cfg = O.GDNConfig(channels=C, delta_key_dim=dk, gate_type="factored", use_spectral_l2_norm=True)
+    q, k, v = (rng.standard_normal(shape) for _ in range(3))
+    k[..., 0:4] = 0.0
+    k[..., 5:8] = 0.0
+    v[..., 8:12] = 0.0
+    alpha = 0.1 + 0.89 / (1.0 + np.exp(-rng.standard_normal((B, T, H * Wf))))
+    beta = 1.0 / (1.0 + np.exp(-rng.standard_normal((B, T, H * Wf))))
+    what = O.spectral_kernel(rng.standard_normal((nh, 11, 11)) * 0.2, H, W, 0.999)
+    shp = (B, T, 1, H, Wf)
+    ref = O.gdn_core(q, k, v, alpha.reshape(shp), beta.reshape(shp), what, cfg, scan="linear")
+    planes = _dev(np.concatenate([z.transpose(0, 1, 4, 2, 3) for z in (q, k, v)], axis=2))
+    ab = _dev(np.stack([alpha, beta], axis=-1))
+    wd = _dev(what, torch.complex64)
+    if S.gdn_core_fused_supported(H, W, dk):
+        o = S.gdn_core_fused(planes, True, ab, "factored", wd, dk)
+    else:
+        spec, norms = S.rfft2(planes, want_norms=True)
+        o = S.irfft2(S.gdn_scan_bins(spec, norms, ab, "factored", wd, dk), W)
+    torch.cuda.synchronize()
+    got, refp = to_np(o), ref                                 # (B, T, C, H, W)
+    for h in range(nh):
+        sl = slice(h * dk, (h + 1) * dk)
+        assert np.sqrt(np.mean(refp[:, :, sl] ** 2)) > 0, h
+        assert rel_err(got[:, :, sl], refp[:, :, sl]) <= TOL_F32, h
+
+
 @pytest.mark.parametrize("name,shape,gate_type,l2", FUSED_CASES, ids=[c[0] for c in FUSED_CASES])
 def test_gdn_core_fused_matches_oracle_and_three_kernels(mods, name, shape, gate_type, l2):
     """The one-kernel core (per (b, head), state in VGPRs over T) against the oracle's
