@@ -239,9 +239,11 @@ struct NormGate {
 // input gates of cssm.py:4763-4780 / :4844-4848, in the operation order of
 // gdn_qkv_post, on tiles of 128 / TT pixels x TT consecutive frames of one
 // batch element (tile row r = t * (128 / TT) + pixel), so each lane holds the
-// frames of its pixels.  T > TT (TT = 8) runs as T / 8 chunks of the same
-// pixels, in order on one workgroup, the last 3 frames of each chunk kept in
-// LDS for the next (kt <= 4).  Output (B, T, N = 3C, HW) plane-major.
+// frames of its pixels.  The taps on frames t .. t - 3 are applied (kt <= 4,
+// or T <= 4 where earlier taps only meet the zero padding).  T > TT (TT = 8)
+// runs as T / 8 chunks of the same pixels, in order on one workgroup, the last
+// 3 frames of each chunk kept in LDS for the next.  Output (B, T, N = 3C, HW)
+// plane-major.
 struct QkvPost {
   const float* w[3];     // (kt, C) per q / k / v block
   const float* b[3];     // (C)
@@ -287,6 +289,11 @@ proj_persist_kernel(const TI* __restrict__ A, int M, int K, int N, const float* 
   __shared__ float2 gsh[TT > 0 ? TM : 1];                 // qkv epilogue: the tile's input gates
   constexpr int KH = 3;                                   // qkv epilogue: frames carried to the next chunk
   __shared__ float hsh[CARRY ? KH * TN * (TM / 8) : 1];   // their projections, [frame][column][pixel]
+  // qkv epilogue of the one-chunk tiles (T <= 8): per column of the block, the conv taps on frames
+  // t, t-1, .., t-KH (zero beyond kt), the projection bias and the conv bias, staged once per
+  // workgroup: [column][8].  The chunked tiles read them per tile (measured faster there).
+  constexpr bool QCW_LDS = TT > 0 && !CARRY;
+  __shared__ __attribute__((aligned(16))) float qcw[QCW_LDS ? TN * 8 : 1];
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int wm = wave / WN, wn = wave % WN;
   const int n0 = blockIdx.y * TN;
@@ -332,6 +339,19 @@ proj_persist_kernel(const TI* __restrict__ A, int M, int K, int N, const float* 
       const int kk = i / TN, c = i % TN;
       const int gn = n0 + c;
       Bs[kk * BP + c] = (kk < K && gn < N) ? Wt[size_t(kk) * N + gn] : 0.0f;
+    }
+  }
+  if constexpr (QCW_LDS) {
+    for (int cl = tid; cl < TN; cl += NT) {
+      const int gn = n0 + cl, C = N / 3;
+      float* e = &qcw[cl * 8];
+      if (gn < N) {
+        const int blk = gn / C, c = gn % C;
+#pragma unroll
+        for (int d = 0; d <= KH; ++d) e[d] = d < qp.kt ? qp.w[blk][(qp.kt - 1 - d) * C + c] : 0.0f;
+        e[4] = bias[gn];
+        e[5] = qp.kt > 0 ? qp.b[blk][c] : 0.0f;
+      }
     }
   }
   // A prefetch: float4 f of the tile -> (row, k4) or (k, row4); SPLIT with
@@ -596,13 +616,36 @@ proj_persist_kernel(const TI* __restrict__ A, int M, int K, int N, const float* 
       for (int j = 0; j < 2; ++j) {
         const int cl = wn * 32 + j * 16 + (lane & 15), gn = n0 + cl;
         if (gn >= N) continue;
-        const float bv = bias[gn];
         const int blk = gn / C, c = gn % C;
-        // wd[d]: tap on frame t - d (d < kt); wd[0] = kernel[kt - 1]
-        float wd[8];
+        // wd[d]: tap on frame t - d.  One-chunk tiles: taps on frames t .. t - KH (zero beyond kt,
+        // so those products add nothing) with the projection bias folded into the accumulators
+        // once; chunked tiles: up to 8 taps, the ones beyond kt skipped, the bias added per use.
+        constexpr int NTAP = CARRY ? 8 : KH + 1;
+        float wd[NTAP], bv, bt;
+        if constexpr (QCW_LDS) {
+          const float4 w4 = *reinterpret_cast<const float4*>(&qcw[cl * 8]);
+          const float2 bb2 = *reinterpret_cast<const float2*>(&qcw[cl * 8 + 4]);
+          wd[0] = w4.x;
+          wd[1] = w4.y;
+          wd[2] = w4.z;
+          wd[3] = w4.w;
+          bv = bb2.x;
+          bt = bb2.y;
 #pragma unroll
-        for (int d = 0; d < 8; ++d) wd[d] = d < qp.kt ? qp.w[blk][(qp.kt - 1 - d) * C + c] : 0.0f;
-        const float bt = qp.kt > 0 ? qp.b[blk][c] : 0.0f;
+          for (int i = 0; i < MI; ++i)
+#pragma unroll
+            for (int r = 0; r < 4; ++r) acc[i][j][r] += bv;
+        } else {
+#pragma unroll
+          for (int d = 0; d < NTAP; ++d) wd[d] = d < qp.kt ? qp.w[blk][(qp.kt - 1 - d) * C + c] : 0.0f;
+          bv = bias[gn];
+          bt = qp.kt > 0 ? qp.b[blk][c] : 0.0f;
+        }
+        // the projection of frame i of this tile with its bias
+        auto xb = [&](int i, int r) -> float {
+          if constexpr (QCW_LDS) return acc[i][j][r];
+          else return acc[i][j][r] + bv;
+        };
 #pragma unroll
         for (int i = 0; i < MI; ++i) {
           const int t = i / IPF;
@@ -611,14 +654,14 @@ proj_persist_kernel(const TI* __restrict__ A, int M, int K, int N, const float* 
           float v[4];
 #pragma unroll
           for (int r = 0; r < 4; ++r) {
-            float x = acc[i][j][r] + bv;
+            float x = xb(i, r);
             if (qp.kt > 0) {
               float o = fmaf(wd[0], x, bt);
 #pragma unroll
-              for (int d = 7; d >= 1; --d) {
-                if (d >= qp.kt) continue;
+              for (int d = NTAP - 1; d >= 1; --d) {
+                if (!QCW_LDS && d >= qp.kt) continue;
                 if (i >= d * IPF) {
-                  o = fmaf(wd[d], acc[i - d * IPF][j][r] + bv, o);
+                  o = fmaf(wd[d], xb(i - d * IPF, r), o);
                 } else if (CARRY && ch > 0 && d - t <= KH) {
                   // frame t - d < 0 of this chunk: frame TT + t - d of the previous chunk
                   o = fmaf(wd[d], hsh[((KH - (d - t)) * TN + cl) * TP + pl + r], o);
@@ -651,7 +694,7 @@ proj_persist_kernel(const TI* __restrict__ A, int M, int K, int N, const float* 
             for (int i = (TT - KH) * IPF; i < MI; ++i) {
               const int pl = (i % IPF) * 16 + (lane >> 4) * 4;
 #pragma unroll
-              for (int r = 0; r < 4; ++r) hsh[((i / IPF - (TT - KH)) * TN + cl) * TP + pl + r] = acc[i][j][r] + bv;
+              for (int r = 0; r < 4; ++r) hsh[((i / IPF - (TT - KH)) * TN + cl) * TP + pl + r] = xb(i, r);
             }
           }
         }
@@ -1318,9 +1361,11 @@ static bool qkv_fused_t(const void* X, int T, int M, int K, int N, const float* 
   }
 }
 
-// T in {1, 2, 4, 8} (one chunk), or a multiple of 8 with kt <= 4 (chunks of 8 frames carrying 3)
+// T in {1, 2, 4} (one chunk; taps beyond the third earlier frame only meet the zero padding),
+// or a multiple of 8 with kt <= 4 (the epilogue applies the taps on frames t .. t - 3; chunks of
+// 8 frames carry 3)
 bool gdn_qkv_fused_supported(int T, int HW, int K, int kt) {
-  const bool t_ok = T == 1 || T == 2 || T == 4 || T == 8 || (T % 8 == 0 && kt <= 4);
+  const bool t_ok = T == 1 || T == 2 || T == 4 || (T % 8 == 0 && kt <= 4);
   const int tp = kPersistTM / (T < 8 ? T : 8);
   return t_ok && K <= kPersistMaxK && K % 4 == 0 && HW % tp == 0;
 }

@@ -339,7 +339,7 @@ int cssm_gdn_qkv_post(void* qkv, int dtype, int B, int T, int C, int H, int W, i
  *   qkv = post(proj(x)),  proj = cssm_proj_planes with N = 3C (identity act).
  * Replaces cssm.py:4753-4758 (qkv_proj), :4763-4780 and :4844-4848 in one pass
  * over qkv instead of three.  Fused when cssm_gdn_qkv_fused(T, H, W, K, kt):
- * tiles of 128 / T' pixels x T' frames, T' = min(T, 8), T in {1, 2, 4, 8} or a
+ * tiles of 128 / T' pixels x T' frames, T' = min(T, 8), T in {1, 2, 4} or a
  * multiple of 8 with kt <= 4 (chunks of 8 frames carry 3 to the next), K <= 64,
  * H*W a multiple of 128 / T'; otherwise it runs the two calls it replaces, with the same
  * results (fp32 qkv; a bf16 qkv then holds the projection in bf16 before the

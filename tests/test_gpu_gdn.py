@@ -176,9 +176,9 @@ def test_gdn_qkv_post_matches_oracle(mods, kt):
     assert rel_err(to_np(got), ref) < 1e-5
 
 
-# (B, T, H, W, K, C): T in {1, 2, 4, 8} with H*W a multiple of 128 / T runs fused (one kernel), and so
+# (B, T, H, W, K, C): T in {1, 2, 4} with H*W a multiple of 128 / T runs fused (one kernel), and so
 # does T a multiple of 8 (chunks of 8 frames carrying 3) for kt <= 4; the rest (T = 3; H*W = 64 at
-# T = 1; kt = 6 at T = 16) through proj_planes + qkv_post
+# T = 1; kt = 6 at T = 8 or 16) through proj_planes + qkv_post
 QKV_CASES = [(2, 8, 16, 16, 64, 16), (1, 4, 8, 8, 32, 8), (3, 2, 8, 8, 64, 12), (2, 1, 16, 8, 48, 8),
              (2, 3, 8, 8, 64, 16), (1, 16, 8, 8, 32, 8), (2, 1, 8, 8, 64, 8), (1, 32, 8, 8, 64, 8),
              (2, 24, 4, 4, 32, 8)]
