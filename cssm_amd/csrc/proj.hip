@@ -289,10 +289,11 @@ proj_persist_kernel(const TI* __restrict__ A, int M, int K, int N, const float* 
   __shared__ float2 gsh[TT > 0 ? TM : 1];                 // qkv epilogue: the tile's input gates
   constexpr int KH = 3;                                   // qkv epilogue: frames carried to the next chunk
   __shared__ float hsh[CARRY ? KH * TN * (TM / 8) : 1];   // their projections, [frame][column][pixel]
-  // qkv epilogue of the one-chunk tiles (T <= 8): per column of the block, the conv taps on frames
-  // t, t-1, .., t-KH (zero beyond kt), the projection bias and the conv bias, staged once per
-  // workgroup: [column][8].  The chunked tiles read them per tile (measured faster there).
-  constexpr bool QCW_LDS = TT > 0 && !CARRY;
+  // qkv epilogue: per column of the block, the conv taps on frames t, t-1, .., t-KH (zero beyond
+  // kt), the projection bias and the conv bias, staged once per workgroup: [column][8].  Not for
+  // fp32 A with the frame carry, whose LDS would then exceed two workgroups per CU: it reads them
+  // per tile.
+  constexpr bool QCW_LDS = TT > 0 && !(CARRY && !A1_ONLY);
   __shared__ __attribute__((aligned(16))) float qcw[QCW_LDS ? TN * 8 : 1];
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int wm = wave / WN, wn = wave % WN;
@@ -372,7 +373,16 @@ proj_persist_kernel(const TI* __restrict__ A, int M, int K, int N, const float* 
       } else if (!PLANE_A) {
         const int r = f / (KMAX / 4), k4 = (f % (KMAX / 4)) * 4;
         const int gm = TT > 0 ? grow(tile, r) : m0 + r;
-        if ((TT > 0 || gm < M) && k4 < K) v = ld4(src, size_t(gm) * K + k4);
+        if ((TT > 0 || gm < M) && k4 < K) {
+          if constexpr (A1_ONLY) {
+            // the raw bf16 bits (they are A's one bf16 part): no conversion here, so nothing waits
+            // for the load before the stash copies them
+            const uint2 raw = *reinterpret_cast<const uint2*>(src + size_t(gm) * K + k4);
+            v = make_float4(__uint_as_float(raw.x), __uint_as_float(raw.y), 0.f, 0.f);
+          } else {
+            v = ld4(src, size_t(gm) * K + k4);
+          }
+        }
       } else {
         const int kk = f / (TM / 4), r4 = (f % (TM / 4)) * 4;
         const int gm = m0 + r4;
@@ -420,6 +430,11 @@ proj_persist_kernel(const TI* __restrict__ A, int M, int K, int N, const float* 
       for (int i = 0; i < PF; ++i) {
         const int f = i * NT + tid;
         const int r = f / (KMAX / 4), k4 = (f % (KMAX / 4)) * 4;
+        if constexpr (A1_ONLY) {
+          // bf16 A: the fetched raw bits are the one part
+          *reinterpret_cast<uint2*>(&A1[r * KP + k4]) = make_uint2(__float_as_uint(pf[i].x), __float_as_uint(pf[i].y));
+          continue;
+        }
         const float x[4] = {pf[i].x, pf[i].y, pf[i].z, pf[i].w};
         bf16x4 v1, v2, v3;
 #pragma unroll
@@ -617,10 +632,10 @@ proj_persist_kernel(const TI* __restrict__ A, int M, int K, int N, const float* 
         const int cl = wn * 32 + j * 16 + (lane & 15), gn = n0 + cl;
         if (gn >= N) continue;
         const int blk = gn / C, c = gn % C;
-        // wd[d]: tap on frame t - d.  One-chunk tiles: taps on frames t .. t - KH (zero beyond kt,
-        // so those products add nothing) with the projection bias folded into the accumulators
-        // once; chunked tiles: up to 8 taps, the ones beyond kt skipped, the bias added per use.
-        constexpr int NTAP = CARRY ? 8 : KH + 1;
+        // wd[d]: tap on frame t - d.  From LDS: taps on frames t .. t - KH (zero beyond kt, so those
+        // products add nothing) with the projection bias folded into the accumulators once; read
+        // per tile: up to 8 taps, the ones beyond kt skipped, the bias added per use.
+        constexpr int NTAP = QCW_LDS ? KH + 1 : 8;
         float wd[NTAP], bv, bt;
         if constexpr (QCW_LDS) {
           const float4 w4 = *reinterpret_cast<const float4*>(&qcw[cl * 8]);
