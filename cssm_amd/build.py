@@ -17,7 +17,7 @@ ROOT = os.path.dirname(PKG_DIR)
 CSRC = os.path.join(PKG_DIR, "csrc")
 BUILD_DIR = os.path.join(PKG_DIR, "_build")
 LIB_PATH = os.path.join(PKG_DIR, "libcssm_hip.so")
-SOURCES = ["api.hip", "prep.hip", "gated_scan.hip", "gated_bwd.hip", "proj.hip", "shortconv.hip", "gdn.hip", "block.hip"]
+SOURCES = ["api.hip", "prep.hip", "gated_scan.hip", "gated_bwd.hip", "proj.hip", "shortconv.hip", "gdn.hip", "gdn_bwd.hip", "block.hip"]
 ARCH = os.environ.get("CSSM_OFFLOAD_ARCH", "gfx950")
 
 HIPCC_FLAGS = [

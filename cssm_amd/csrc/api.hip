@@ -433,6 +433,50 @@ int cssm_gdn_scan_bins(const float* spec, const float* norms, const float* ab, l
                     "cssm_gdn_scan_bins");
 }
 
+static int gdn_train_check(const char* fn, int B, int T, int C, int H, int W, int dk, long long ab_frame, int ab_head,
+                           int ab_bin) {
+  if (B <= 0 || T <= 0 || C <= 0 || H <= 0 || W <= 0 || dk < 1 || dk > 4 || C % dk)
+    return fail(CSSM_ERR_SHAPE, "%s: B=%d T=%d C=%d H=%d W=%d d_k=%d (1..4, divides C)", fn, B, T, C, H, W, dk);
+  if (ab_frame < 0 || ab_head < 0 || ab_bin < 0) return fail(CSSM_ERR_ARG, "%s: negative gate stride", fn);
+  if (B > 65535 || C / dk > 65535) return fail(CSSM_ERR_SHAPE, "%s: grid too large", fn);
+  return CSSM_OK;
+}
+
+int cssm_gdn_scan_bins_train(const float* spec, const float* ab, long long ab_frame, int ab_head, int ab_bin,
+                             const float* what, int B, int T, int C, int H, int W, int dk, float* ohat, float* states,
+                             void* stream) {
+  if (!spec || !ab || !what || !ohat || !states)
+    return fail(CSSM_ERR_NULL, "cssm_gdn_scan_bins_train: spec, ab, what, ohat and states must be non-null");
+  if (int e = gdn_train_check("cssm_gdn_scan_bins_train", B, T, C, H, W, dk, ab_frame, ab_head, ab_bin)) return e;
+  if (!aligned(spec, 8) || !aligned(ab, 8) || !aligned(what, 8) || !aligned(ohat, 8) || !aligned(states, 8))
+    return fail(CSSM_ERR_ALIGN, "cssm_gdn_scan_bins_train: complex tensors must be 8-byte aligned");
+  return hip_status(cssm::launch_gdn_scan_bins_train(
+                        reinterpret_cast<const float2*>(spec), reinterpret_cast<const float2*>(ab), ab_frame, ab_head,
+                        ab_bin, reinterpret_cast<const float2*>(what), B, T, C, H, W, dk,
+                        reinterpret_cast<float2*>(ohat), reinterpret_cast<float2*>(states), nullptr, nullptr, nullptr,
+                        nullptr, false, static_cast<hipStream_t>(stream)),
+                    "cssm_gdn_scan_bins_train");
+}
+
+int cssm_gdn_scan_bins_bwd(const float* spec, const float* ab, long long ab_frame, int ab_head, int ab_bin,
+                           const float* what, const float* states, const float* dohat, int B, int T, int C, int H,
+                           int W, int dk, float* dspec, float* dab, float* dwhat, void* stream) {
+  if (!spec || !ab || !what || !states || !dohat || !dspec || !dab || !dwhat)
+    return fail(CSSM_ERR_NULL, "cssm_gdn_scan_bins_bwd: null argument");
+  if (int e = gdn_train_check("cssm_gdn_scan_bins_bwd", B, T, C, H, W, dk, ab_frame, ab_head, ab_bin)) return e;
+  if (!aligned(spec, 8) || !aligned(ab, 8) || !aligned(what, 8) || !aligned(states, 8) || !aligned(dohat, 8) ||
+      !aligned(dspec, 8) || !aligned(dab, 8) || !aligned(dwhat, 8))
+    return fail(CSSM_ERR_ALIGN, "cssm_gdn_scan_bins_bwd: complex tensors must be 8-byte aligned");
+  return hip_status(cssm::launch_gdn_scan_bins_train(
+                        reinterpret_cast<const float2*>(spec), reinterpret_cast<const float2*>(ab), ab_frame, ab_head,
+                        ab_bin, reinterpret_cast<const float2*>(what), B, T, C, H, W, dk, nullptr,
+                        const_cast<float2*>(reinterpret_cast<const float2*>(states)),
+                        reinterpret_cast<const float2*>(dohat), reinterpret_cast<float2*>(dspec),
+                        reinterpret_cast<float2*>(dab), reinterpret_cast<float2*>(dwhat), true,
+                        static_cast<hipStream_t>(stream)),
+                    "cssm_gdn_scan_bins_bwd");
+}
+
 int cssm_gdn_core_fused_supported(int H, int W, int delta_key_dim) {
   return cssm::gdn_core_fused_supported(H, W, delta_key_dim) ? 1 : 0;
 }

@@ -89,6 +89,12 @@ int fft_planes_min_group(int H, int W);
 hipError_t launch_gdn_scan_bins(const float2* spec, const float* norms, const float2* ab, long long ab_frame,
                                 int ab_head, int ab_bin, const float2* what, int B, int T, int C, int H, int W,
                                 int dk, float2* ohat, hipStream_t s);
+// training: forward with the state entering every step saved (backward = false), or the reverse
+// pass from those states (backward = true); gdn_bwd.hip
+hipError_t launch_gdn_scan_bins_train(const float2* spec, const float2* ab, long long ab_frame, int ab_head,
+                                      int ab_bin, const float2* what, int B, int T, int C, int H, int W, int dk,
+                                      float2* ohat, float2* states, const float2* dohat, float2* dspec,
+                                      float2* dab, float2* dwhat, bool backward, hipStream_t s);
 // backward of the gated scan: the spectral-domain reverse recurrence per (b, bin), T <= 32
 hipError_t launch_gated_scan_bwd_bins(const float2* uspec, const float2* dspec, const float4* gates,
                                       const float2* khat, int B, int T, int C, int H, int W, float c_scale,

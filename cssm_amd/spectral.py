@@ -480,6 +480,55 @@ def gdn_scan_bins(spec: torch.Tensor, norms: Optional[torch.Tensor], ab: torch.T
     return ohat
 
 
+def _ab_strides(ab: torch.Tensor, gate_type: str):
+    n_ab = ab.shape[2]
+    return {"dense": (n_ab, 0, 1), "factored": (n_ab, 0, 1), "channel": (n_ab, 1, 0), "scalar": (1, 0, 0)}[gate_type]
+
+
+def gdn_scan_bins_train(spec: torch.Tensor, ab: torch.Tensor, gate_type: str, what: torch.Tensor,
+                        delta_key_dim: int):
+    """Training forward of the delta rule (cssm.py:4898-5000): spec (B, T, 3C, H, Wf) complex64 with
+    q and k already scaled by the spectral L2 norms.  Returns (ohat (B, T, C, H, Wf), states
+    (B, T, C / d_k, d_k, d_k, H*Wf): the state entering every step, for
+    :func:`gdn_scan_bins_backward`)."""
+    _dev(spec, "spec", torch.complex64)
+    _dev(ab, "ab", torch.float32)
+    _dev(what, "what", torch.complex64)
+    B, T, C3, H, Wf = spec.shape
+    C, dk = C3 // 3, delta_key_dim
+    W = 2 * (Wf - 1)
+    fs, hs, bs = _ab_strides(ab, gate_type)
+    ohat = torch.empty((B, T, C, H, Wf), dtype=torch.complex64, device=spec.device)
+    states = torch.empty((B, T, C // dk, dk, dk, H * Wf), dtype=torch.complex64, device=spec.device)
+    _lib.call("cssm_gdn_scan_bins_train", spec.data_ptr(), ab.data_ptr(), fs, hs, bs, what.data_ptr(), B, T, C, H,
+              W, dk, ohat.data_ptr(), states.data_ptr(), _stream())
+    return ohat, states
+
+
+def gdn_scan_bins_backward(spec: torch.Tensor, ab: torch.Tensor, gate_type: str, what: torch.Tensor,
+                           states: torch.Tensor, dohat: torch.Tensor, delta_key_dim: int):
+    """Reverse pass of :func:`gdn_scan_bins_train` (gradients as dL/dRe + i dL/dIm).  Returns
+    (dspec (B, T, 3C, H, Wf) complex64, dab (B, T, C / d_k, H*Wf, 2) float32 per (head, bin) --
+    summed by the caller over what the gate type shares --, dwhat (B, C / d_k, H, Wf) complex64 per
+    batch element)."""
+    for t, n in ((spec, "spec"), (what, "what"), (states, "states"), (dohat, "dohat")):
+        _dev(t, n, torch.complex64)
+    _dev(ab, "ab", torch.float32)
+    B, T, C3, H, Wf = spec.shape
+    C, dk = C3 // 3, delta_key_dim
+    W = 2 * (Wf - 1)
+    if tuple(dohat.shape) != (B, T, C, H, Wf) or tuple(states.shape) != (B, T, C // dk, dk, dk, H * Wf):
+        raise ValueError("dohat / states shapes do not match spec")
+    fs, hs, bs = _ab_strides(ab, gate_type)
+    dspec = torch.empty_like(spec)
+    dab = torch.empty((B, T, C // dk, H * Wf, 2), dtype=torch.float32, device=spec.device)
+    dwhat = torch.empty((B, C // dk, H, Wf), dtype=torch.complex64, device=spec.device)
+    _lib.call("cssm_gdn_scan_bins_bwd", spec.data_ptr(), ab.data_ptr(), fs, hs, bs, what.data_ptr(),
+              states.data_ptr(), dohat.data_ptr(), B, T, C, H, W, dk, dspec.data_ptr(), dab.data_ptr(),
+              dwhat.data_ptr(), _stream())
+    return dspec, dab, dwhat
+
+
 def gdn_core_fused_supported(H: int, W: int, delta_key_dim: int) -> bool:
     return bool(_lib.load().cssm_gdn_core_fused_supported(H, W, delta_key_dim))
 

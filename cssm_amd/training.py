@@ -133,3 +133,182 @@ def gated_train_apply(cell, params: Dict[str, Any], x: torch.Tensor) -> torch.Te
     out = torch.addmm(p["out_proj"]["bias"], y.view(F, Ci, HW).transpose(1, 2).reshape(-1, Ci),
                       p["out_proj"]["kernel"])
     return out.view(B, T, H, W, cell.channels)
+
+
+# ----------------------------------------------------------------------------- GDN cell
+#
+# GatedDeltaNetCSSM trains the same way: torch differentiates the prologue (qkv_dw, qkv_proj, short
+# conv, SiLU, input gates, gate_proj), the gates alpha / beta from ctx, W_hat, the spectral L2 norms
+# and the output path (norm x gate, output_proj); the batched transforms run on the HIP FFT kernels
+# with their adjoints, and the delta rule runs forward in cssm_gdn_scan_bins_train (which keeps the
+# state entering every step) and backward in cssm_gdn_scan_bins_bwd.
+
+def _c2r_weights(W: int, device) -> torch.Tensor:
+    """c_v of the C2R rule: 2 for 0 < v < W/2, 1 at v = 0 and v = W/2."""
+    c = torch.full((W // 2 + 1,), 2.0, device=device)
+    c[0] = 1.0
+    c[-1] = 1.0
+    return c
+
+
+class _Rfft2Fn(torch.autograd.Function):
+    """spec = rfft2(x) over the last two axes (float32 planes -> complex64), on the HIP kernels.
+    Adjoint: dx = H W irfft2(dspec / c_v)."""
+
+    @staticmethod
+    def forward(ctx, x):
+        ctx.hw = tuple(x.shape[-2:])
+        spec, _ = S.rfft2(x.contiguous())
+        return spec
+
+    @staticmethod
+    def backward(ctx, dspec):
+        H, W = ctx.hw
+        w = 1.0 / _c2r_weights(W, dspec.device)
+        return S.irfft2((dspec * w).contiguous(), W) * float(H * W)
+
+
+class _Irfft2Fn(torch.autograd.Function):
+    """y = irfft2(spec, s=(H, W)) over the last two axes, on the HIP kernels.
+    Adjoint: dspec = rfft2(dy) c_v / (H W)."""
+
+    @staticmethod
+    def forward(ctx, spec, W):
+        ctx.W = W
+        return S.irfft2(spec.contiguous(), W)
+
+    @staticmethod
+    def backward(ctx, dy):
+        H, W = dy.shape[-2], ctx.W
+        d, _ = S.rfft2(dy.contiguous())
+        return d * (_c2r_weights(W, dy.device) / float(H * W)), None
+
+
+class _GdnBinsFn(torch.autograd.Function):
+    """ohat = delta-rule recurrence of the (norm-scaled) spectra, cssm.py:4898-5000."""
+
+    @staticmethod
+    def forward(ctx, spec, ab, what, gate_type, dk):
+        ohat, states = S.gdn_scan_bins_train(spec, ab, gate_type, what, dk)
+        ctx.save_for_backward(spec, ab, what, states)
+        ctx.gate_type, ctx.dk = gate_type, dk
+        return ohat
+
+    @staticmethod
+    def backward(ctx, dohat):
+        spec, ab, what, states = ctx.saved_tensors
+        dspec, dab, dwhat = S.gdn_scan_bins_backward(spec, ab, ctx.gate_type, what, states, dohat.contiguous(),
+                                                     ctx.dk)
+        if ctx.gate_type in ("dense", "factored"):      # one (alpha, beta) per bin, shared by the heads
+            dab = dab.sum(dim=2)
+        elif ctx.gate_type == "channel":                # one per head, shared by the bins
+            dab = dab.sum(dim=3)
+        else:                                           # one per frame
+            dab = dab.sum(dim=(2, 3)).unsqueeze(2)
+        return dspec, dab, dwhat.sum(dim=0), None, None
+
+
+def what_planes(k: torch.Tensor, H: int, W: int, rho: float, squash: bool) -> torch.Tensor:
+    """W_hat (n_h, H, Wf) = rho F / (1 + |F|) (or F), F = rfft2 of the padded / cropped kernel,
+    differentiably (cssm.py:4711-4716; no floor for the GDN cell)."""
+    K = k.shape[-1]
+    if K > H or K > W:
+        sh, sw = (K - H) // 2, (K - W) // 2
+        kp = k[:, sh:sh + H, sw:sw + W]
+    else:
+        ph, pw = (H - K) // 2, (W - K) // 2
+        kp = Fn.pad(k, (pw, W - K - pw, ph, H - K - ph))
+    F = torch.fft.rfft2(kp)
+    return (F * rho / (1.0 + F.abs())) if squash else F
+
+
+def _temporal_encoding(T: int, C: int, base: float, device) -> torch.Tensor:
+    """E[t, 2j] = sin(t / base^(2j / C)), E[t, 2j + 1] = cos(.) (cssm.py:353-383), in float64."""
+    inv = 1.0 / (base ** (torch.arange(0, C, 2, dtype=torch.float64, device=device) / C))
+    th = torch.arange(T, dtype=torch.float64, device=device)[:, None] * inv[None]
+    return torch.stack([torch.sin(th), torch.cos(th)], -1).reshape(T, C).float()
+
+
+def _gdn_gate(p, name, gate_type, ctx, x, H, W, nh, bounded=False, spatial=False):
+    """_gate (cssm.py:4798-4842).  Spatial gates come back broadcastable against plane-major
+    (B, T, C, H, W); the others as the (B, T, n_ab) alpha / beta planes the bins kernel reads."""
+    B, T, C = ctx.shape
+    Wf = W // 2 + 1
+
+    def dense(z, q):
+        return z @ q["kernel"] + q["bias"]
+    if gate_type == "channel":
+        if spatial:
+            q = p[name]
+            g = torch.sigmoid(x @ q["kernel"].reshape(C, C) + q["bias"])     # (B, T, H, W, C)
+            return g.permute(0, 1, 4, 2, 3)
+        raw = torch.sigmoid(dense(ctx, p[name]))                             # (B, T, n_h)
+    elif gate_type == "factored":
+        raw = torch.sigmoid(dense(ctx, p[f"{name}_h"])[..., :, None] + dense(ctx, p[f"{name}_w"])[..., None, :])
+        if spatial:
+            return raw[:, :, None]                                           # (B, T, 1, H, W)
+        raw = raw.reshape(B, T, H * Wf)
+    elif gate_type == "scalar":
+        raw = torch.sigmoid(dense(ctx, p[name]))                             # (B, T, 1)
+        if spatial:
+            return raw[..., None, None]
+    else:
+        raw = torch.sigmoid(dense(ctx, p[name]))
+        if spatial:
+            return raw.view(B, T, 1, H, W)
+    return 0.1 + 0.89 * raw if bounded else raw
+
+
+def gdn_train_apply(cell, params: Dict[str, Any], x: torch.Tensor) -> torch.Tensor:
+    """GatedDeltaNetCSSM forward with autograd (x (B, T, H, W, C) float32 on the GPU; params the
+    cell's tree of float32 device tensors).  Same results as ``cell.apply`` up to float32 rounding."""
+    p = params["params"] if "params" in params else params
+    B, T, H, W, C = x.shape
+    dk = cell.delta_key_dim
+    nh, F, HW = C // dk, B * T, H * W
+    if not S.fft_supported(H, W):
+        raise NotImplementedError(f"no spectral transform kernel for {H}x{W} planes")
+    x = x.float()
+    what = what_planes(p["kernel"], H, W, cell.spectral_rho, not cell.no_spectral_clamp).contiguous()
+    ctx = x.mean(dim=(2, 3))
+    if not cell.position_independent_gates:
+        ctx = ctx + _temporal_encoding(T, C, cell.rope_base, x.device)[None]
+    xq = x.reshape(F, H, W, C)
+    if cell.qkv_conv_size > 1:
+        q = p["qkv_dw"]
+        ks = q["kernel"].shape[0]
+        lo, hi = (ks - 1) // 2, ks // 2
+        w = q["kernel"].permute(3, 2, 0, 1)                                  # (C, 1, k, k)
+        xq = (Fn.conv2d(Fn.pad(xq.permute(0, 3, 1, 2), (lo, hi, lo, hi)), w, groups=C)
+              + q["bias"][None, :, None, None]).permute(0, 2, 3, 1)
+    qkv = torch.addmm(p["qkv_proj"]["bias"], xq.reshape(-1, C), p["qkv_proj"]["kernel"])
+    qkv = qkv.view(F, HW, 3 * C).transpose(1, 2).reshape(B, T, 3 * C, H, W)   # plane-major
+    q, k, v = qkv[:, :, :C], qkv[:, :, C:2 * C], qkv[:, :, 2 * C:]
+    if cell.short_conv_size > 0:
+        q = Fn.silu(_causal_t(q, p["short_conv_q"]))
+        k = Fn.silu(_causal_t(k, p["short_conv_k"]))
+        v = Fn.silu(_causal_t(v, p["short_conv_v"]))
+    if cell.use_input_gates:
+        k = k * _gdn_gate(p, "B_k", cell.gate_type, ctx, x, H, W, nh, spatial=True)
+        v = v * _gdn_gate(p, "B_v", cell.gate_type, ctx, x, H, W, nh, spatial=True)
+    gv = torch.addmm(p["gate_proj"]["bias"], x.reshape(-1, C), p["gate_proj"]["kernel"])
+    gv = Fn.silu(gv) if cell.output_gate_act == "silu" else torch.sigmoid(gv)
+    alpha = _gdn_gate(p, "alpha", cell.gate_type, ctx, x, H, W, nh, bounded=True)
+    beta = _gdn_gate(p, "beta", cell.gate_type, ctx, x, H, W, nh)
+    ab = torch.stack([alpha, beta], dim=-1).contiguous()                    # (B, T, n_ab, 2)
+    spec = _Rfft2Fn.apply(torch.cat([q, k, v], dim=2))                       # (B, T, 3C, H, Wf)
+    if cell.use_spectral_l2_norm:
+        qk = spec[:, :, :2 * C]
+        qk = qk * torch.rsqrt((qk.real ** 2 + qk.imag ** 2).sum(dim=(3, 4), keepdim=True) + 1e-6)
+        spec = torch.cat([qk, spec[:, :, 2 * C:]], dim=2)
+    ohat = _GdnBinsFn.apply(spec.contiguous(), ab, what, cell.gate_type, dk)
+    o = _Irfft2Fn.apply(ohat, W)                                             # (B, T, C, H, W)
+    o = o.reshape(F, C, HW).transpose(1, 2)                                  # (F, HW, C)
+    if cell.output_norm == "rms":
+        o = o * torch.rsqrt((o * o).mean(dim=-1, keepdim=True) + 1e-6) * p["rms_scale"]
+    elif cell.output_norm == "layer":
+        mu = o.mean(dim=-1, keepdim=True)
+        var = ((o - mu) ** 2).mean(dim=-1, keepdim=True)
+        o = (o - mu) * torch.rsqrt(var + 1e-6) * p["output_layernorm"]["scale"] + p["output_layernorm"]["bias"]
+    out = torch.addmm(p["output_proj"]["bias"], (o * gv.view(F, HW, C)).reshape(-1, C), p["output_proj"]["kernel"])
+    return out.view(B, T, H, W, C)

@@ -399,6 +399,37 @@ int cssm_gdn_scan_bins(const float* spec, const float* norms, const float* ab, l
                        int delta_key_dim, float* ohat, void* stream);
 
 /*
+ * Training forward of the delta-rule recurrence: cssm_gdn_scan_bins with the
+ * spectral L2 norms left to the caller (spec holds q and k already scaled by
+ * them, and v), plus the state entering every step, which the reverse pass
+ * reads.  The reference takes its gradients with jax.value_and_grad through the
+ * log-space scan (main.py:283; GOOM VJPs goom.py:47-137); this pair replaces
+ * that span's forward and backward (cssm.py:4898-5000).
+ *   spec, ab, ab_frame, ab_head, ab_bin, what: as cssm_gdn_scan_bins
+ *   ohat    (B, T, C, H, Wf) complex64 out
+ *   states  (B, T, C / d_k, d_k, d_k, H*Wf) complex64 out: s_{t-1} of step t
+ */
+int cssm_gdn_scan_bins_train(const float* spec, const float* ab, long long ab_frame, int ab_head, int ab_bin,
+                             const float* what, int B, int T, int C, int H, int W, int delta_key_dim, float* ohat,
+                             float* states, void* stream);
+
+/*
+ * Reverse pass of cssm_gdn_scan_bins_train: the reverse recurrence over T per
+ * (batch, head, bin) through the key-vector norm, M = alpha W (I - beta k k^H)
+ * and Delta = beta v k^H (no gradient through an entry to_goom's floor took),
+ * with gradients written as dL/dRe + i dL/dIm.
+ *   spec, ab, strides, what, states: as the forward call
+ *   dohat  (B, T, C, H, Wf) complex64: dL/d ohat
+ *   dspec  (B, T, 3C, H, Wf) complex64 out: dL/d spec (q and k as scaled in spec)
+ *   dab    (B, T, C / d_k, H*Wf) (dalpha, dbeta) out per (b, t, head, bin): the caller
+ *          sums them over what a gate type shares (heads, bins)
+ *   dwhat  (B, C / d_k, H*Wf) complex64 out: dL/d W_hat per batch element (sum over B)
+ */
+int cssm_gdn_scan_bins_bwd(const float* spec, const float* ab, long long ab_frame, int ab_head, int ab_bin,
+                           const float* what, const float* states, const float* dohat, int B, int T, int C, int H,
+                           int W, int delta_key_dim, float* dspec, float* dab, float* dwhat, void* stream);
+
+/*
  * The GDN spectral core as one kernel where a workgroup can hold a (batch,
  * head)'s state for all T (32 x 32 planes, delta_key_dim 4: the video-shaped
  * config): per step it reads the head's q, k, v planes once, runs their rfft2,

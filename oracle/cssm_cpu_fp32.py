@@ -261,3 +261,130 @@ class GdnCPU:
         o = torch.fft.irfft2(O.reshape(B * T, C, H, W // 2 + 1), s=(H, W))   # (F, C, H, W)
         o = o * torch.rsqrt((o ** 2).mean(1, keepdim=True) + 1e-6) * p["rms_scale"][None, :, None, None]
         return _planes_out(o * gv, p["output_proj"]).reshape(B, T, H, W, C)
+
+
+class GdnRef:
+    """GatedDeltaNetCSSM slow-path forward (cssm.py:4685-5141) in torch on the CPU, float64 by
+    default, with autograd through every parameter and the input: the gradient reference of the
+    training path.  Every gate type, the rms / layer / no output norm, the qkv depthwise conv, the
+    short conv and the input gates; M = alpha W (I - beta k k^H) and Delta = beta v k^H are
+    materialised per step with to_goom's floor applied entry by entry through torch.where, so a
+    floored entry passes no gradient to its inputs (cssm.py:4911-4937, goom.py:161-174).
+    ``cfg`` is the oracle's GDNConfig (rope_mode 'none': the sinusoid context table)."""
+
+    def __init__(self, params, cfg, dtype=torch.float64, requires_grad=True):
+        self.p = params_to_torch(params, dtype, requires_grad)
+        self.cfg = cfg
+        self.dtype = dtype
+
+    def _gate(self, name, ctx, x, H, W, nh, bounded=False, spatial=False):
+        p, gt = self.p, self.cfg.gate_type
+        B, T, C = ctx.shape
+        Wf = W // 2 + 1
+        if gt == "channel":
+            if spatial:
+                q = p[name]
+                k2 = q["kernel"].reshape(C, C)
+                return torch.sigmoid(x @ k2 + q["bias"])                     # (B, T, H, W, C)
+            raw = torch.sigmoid(_dense(ctx, p[name])).reshape(B, T, nh, 1, 1)
+        elif gt == "factored":
+            raw = torch.sigmoid(_dense(ctx, p[f"{name}_h"])[..., :, None] + _dense(ctx, p[f"{name}_w"])[..., None, :])
+            if spatial:
+                return raw[..., None]                                        # (B, T, H, W, 1)
+            raw = raw.reshape(B, T, 1, H, Wf)
+        elif gt == "scalar":
+            raw = torch.sigmoid(_dense(ctx, p[name])).reshape(B, T, 1, 1, 1)
+            if spatial:
+                return raw
+        else:
+            raw = torch.sigmoid(_dense(ctx, p[name]))
+            if spatial:
+                return raw.reshape(B, T, H, W, 1)
+            raw = raw.reshape(B, T, 1, H, Wf)
+        return 0.1 + 0.89 * raw if bounded else raw
+
+    def __call__(self, x):
+        p, cfg, dt = self.p, self.cfg, self.dtype
+        B, T, H, W, C = x.shape
+        dk = cfg.delta_key_dim
+        nh, Wf = C // dk, W // 2 + 1
+        what = spectral_kernel(p["kernel"], H, W, cfg.spectral_rho, squash=not cfg.no_spectral_clamp)
+        xf = x.reshape(B * T, H, W, C)
+        xq = _dwconv_same(xf, p["qkv_dw"]) if cfg.qkv_conv_size > 1 else xf
+        qkv = _dense(xq, p["qkv_proj"]).reshape(B, T, H, W, 3 * C)
+        q, k, v = qkv[..., :C], qkv[..., C:2 * C], qkv[..., 2 * C:]
+        if cfg.short_conv_size > 0:
+            def conv(z, name):                                               # channels-last -> plane-major and back
+                zp = z.permute(0, 1, 4, 2, 3)
+                return Fn.silu(_causal_t(zp, p[name])).permute(0, 1, 3, 4, 2)
+            q, k, v = conv(q, "short_conv_q"), conv(k, "short_conv_k"), conv(v, "short_conv_v")
+        inv = 1.0 / (cfg.rope_base ** (torch.arange(0, C, 2, dtype=torch.float64) / C))
+        th = torch.arange(T, dtype=torch.float64)[:, None] * inv[None]
+        ctx = x.mean(dim=(2, 3)) + torch.stack([torch.sin(th), torch.cos(th)], -1).reshape(T, C).to(dt)[None]
+        if cfg.use_input_gates:
+            k = k * self._gate("B_k", ctx, x, H, W, nh, spatial=True)
+            v = v * self._gate("B_v", ctx, x, H, W, nh, spatial=True)
+        gv = _dense(x, p["gate_proj"])
+        gv = Fn.silu(gv) if cfg.output_gate_act == "silu" else torch.sigmoid(gv)
+        al = self._gate("alpha", ctx, x, H, W, nh, bounded=True).expand(B, T, nh, H, Wf)
+        be = self._gate("beta", ctx, x, H, W, nh).expand(B, T, nh, H, Wf)
+
+        def spec(z):                                                         # (B, T, nh, dk, H, Wf)
+            return torch.fft.rfft2(z.permute(0, 1, 4, 2, 3)).reshape(B, T, nh, dk, H, Wf)
+
+        def l2(z):
+            if not cfg.use_spectral_l2_norm:
+                return z
+            return z / torch.sqrt((z.real ** 2 + z.imag ** 2).sum(dim=(4, 5), keepdim=True) + 1e-6)
+        qs, ks, vs = l2(spec(q)), l2(spec(k)), spec(v)
+        ks = ks / torch.sqrt((ks.real ** 2 + ks.imag ** 2).sum(dim=3, keepdim=True) + 1e-6)
+        eye = torch.eye(dk, dtype=dt)[None, None, :, :, None, None]
+        s = torch.zeros((B, nh, dk, dk, H, Wf), dtype=qs.dtype)              # s[b, n, i, r, u, v]
+        outs = []
+        for t in range(T):
+            kk = ks[:, t]                                                    # (B, nh, dk, H, Wf)
+            aw = al[:, t][:, :, None, None] * what[None, :, None, None]      # (B, nh, 1, 1, H, Wf)
+            b_t = be[:, t][:, :, None, None]
+            M = _floor(aw * (eye - b_t * kk[:, :, :, None] * kk.conj()[:, :, None, :]))   # M[b, n, r, c]
+            D = _floor(b_t * vs[:, t][:, :, :, None] * kk.conj()[:, :, None, :])          # D[b, n, i, r]
+            s = torch.einsum("bnrcuv,bnicuv->bniruv", M, s) + D
+            outs.append(torch.einsum("bniruv,bnruv->bniuv", s, qs[:, t]))
+        O = torch.stack(outs, dim=1)                                         # (B, T, nh, dk, H, Wf)
+        o = torch.fft.irfft2(O.reshape(B, T, C, H, Wf), s=(H, W)).permute(0, 1, 3, 4, 2)   # (B, T, H, W, C)
+        if cfg.output_norm == "rms":
+            o = o * torch.rsqrt((o * o).mean(dim=-1, keepdim=True) + 1e-6) * p["rms_scale"]
+        elif cfg.output_norm == "layer":
+            mu = o.mean(dim=-1, keepdim=True)
+            var = ((o - mu) ** 2).mean(dim=-1, keepdim=True)
+            o = (o - mu) * torch.rsqrt(var + 1e-6) * p["output_layernorm"]["scale"] + p["output_layernorm"]["bias"]
+        return _dense(o * gv, p["output_proj"])
+
+
+def gdn_bins_core(spec, ab, what, gate_type, dk):
+    """The contract of cssm_gdn_scan_bins_train (cssm.py:4898-5000): spec (B, T, 3C, H, Wf) with q
+    and k already scaled by the spectral L2 norms, ab (B, T, n_ab, 2) (alpha, beta) laid out per
+    gate type, what (n_h, H, Wf).  Per-bin key norm, floored M and Delta (torch.where), s_t = M
+    s_{t-1} + Delta, o_t = s_t q.  Returns ohat (B, T, C, H, Wf)."""
+    B, T, C3, H, Wf = spec.shape
+    C = C3 // 3
+    nh = C // dk
+    q = spec[:, :, :C].reshape(B, T, nh, dk, H, Wf)
+    k = spec[:, :, C:2 * C].reshape(B, T, nh, dk, H, Wf)
+    v = spec[:, :, 2 * C:].reshape(B, T, nh, dk, H, Wf)
+    k = k / torch.sqrt((k.real ** 2 + k.imag ** 2).sum(dim=3, keepdim=True) + 1e-6)
+    shp = {"dense": (B, T, 1, H, Wf), "factored": (B, T, 1, H, Wf), "channel": (B, T, nh, 1, 1),
+           "scalar": (B, T, 1, 1, 1)}[gate_type]
+    al = ab[..., 0].reshape(shp).expand(B, T, nh, H, Wf)
+    be = ab[..., 1].reshape(shp).expand(B, T, nh, H, Wf)
+    eye = torch.eye(dk, dtype=ab.dtype)[None, None, :, :, None, None]
+    s = torch.zeros((B, nh, dk, dk, H, Wf), dtype=spec.dtype)
+    outs = []
+    for t in range(T):
+        kk = k[:, t]
+        aw = al[:, t][:, :, None, None] * what[None, :, None, None]
+        b_t = be[:, t][:, :, None, None]
+        M = _floor(aw * (eye - b_t * kk[:, :, :, None] * kk.conj()[:, :, None, :]))
+        D = _floor(b_t * v[:, t][:, :, :, None] * kk.conj()[:, :, None, :])
+        s = torch.einsum("bnrcuv,bnicuv->bniruv", M, s) + D
+        outs.append(torch.einsum("bniruv,bnruv->bniuv", s, q[:, t]))
+    return torch.stack(outs, dim=1).reshape(B, T, C, H, Wf)

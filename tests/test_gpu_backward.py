@@ -168,3 +168,99 @@ def test_layer_vjp_adjoint_to_float64_jvp(mods, name, shape, kw):
     rhs = sum(_dot(g.double().cpu(), t) for g, t in zip(grads, tang))
     scale = sum(float(g.double().cpu().norm() * t.norm()) for g, t in zip(grads, tang))
     assert abs(lhs - rhs) <= 1e-4 * scale, (lhs, rhs, scale)
+
+
+# ------------------------------------------------------------------------- GDN cell
+
+BINS_CASES = [("factored", 4, 16, False), ("dense", 2, 8, False), ("channel", 4, 8, False), ("scalar", 1, 8, False),
+              ("factored_floored", 4, 16, True)]
+
+
+@pytest.mark.parametrize("name,dk,H,floored", BINS_CASES, ids=[c[0] for c in BINS_CASES])
+def test_gdn_bins_vjp_matches_float64_reference(mods, name, dk, H, floored):
+    """cssm_gdn_scan_bins_train / _bwd through the autograd Function (its per-gate-type sums of
+    the (alpha, beta) gradients included) against float64 autograd of the kernel contract.  The
+    floored case zeroes the keys of head 0 and the values of head 2, so to_goom's floor takes
+    entries of M and Delta there, which must pass no gradient."""
+    _, S, training = mods
+    print_case(test="gdn_bins_vjp", case=name)
+    gt = name.split("_")[0]
+    rng = np.random.default_rng(43)
+    B, T, C, W = 2, 5, 16, H
+    nh, Wf = C // dk, W // 2 + 1
+    spec = rng.standard_normal((B, T, 3 * C, H, Wf)) + 1j * rng.standard_normal((B, T, 3 * C, H, Wf))
+    spec[:, :, :C] *= 0.05
+    spec[:, :, C:2 * C] *= 0.05
+    if floored:
+        spec[:, :, C:C + dk] = 0.0
+        spec[:, :, 2 * C + 2 * dk:2 * C + 3 * dk] = 0.0
+    n_ab = {"factored": H * Wf, "dense": H * Wf, "channel": nh, "scalar": 1}[gt]
+    alpha = 0.1 + 0.89 / (1.0 + np.exp(-rng.standard_normal((B, T, n_ab))))
+    beta = 1.0 / (1.0 + np.exp(-rng.standard_normal((B, T, n_ab))))
+    ab = np.stack([alpha, beta], -1)
+    what = O.spectral_kernel(rng.standard_normal((nh, 5, 5)) * 0.2, H, W, 0.999)
+    dohat = rng.standard_normal((B, T, C, H, Wf)) + 1j * rng.standard_normal((B, T, C, H, Wf))
+    ts = [torch.from_numpy(a).requires_grad_(True) for a in (spec, ab, what)]
+    ref = P.gdn_bins_core(ts[0], ts[1], ts[2], gt, dk)
+    refs = torch.autograd.grad(ref, ts, torch.from_numpy(dohat))
+    dev = [torch.from_numpy(spec).to("cuda", torch.complex64).requires_grad_(True),
+           torch.from_numpy(ab).to("cuda", torch.float32).requires_grad_(True),
+           torch.from_numpy(what).to("cuda", torch.complex64).requires_grad_(True)]
+    out = training._GdnBinsFn.apply(dev[0], dev[1], dev[2], gt, dk)
+    got = torch.autograd.grad(out, dev, torch.from_numpy(dohat).to("cuda", torch.complex64))
+    torch.cuda.synchronize()
+    assert rel_err(_ri(out), _ri(ref)) <= TOL
+    for n, g, r in zip(("dspec", "dab", "dwhat"), got, refs):
+        assert g.shape == r.shape, n
+        assert rel_err(_ri(g), _ri(r)) <= TOL, n
+
+
+def _ri(t):
+    """Real and imaginary parts stacked (float64 numpy) for the parity metric."""
+    a = t.detach().cpu().numpy()
+    return np.stack([a.real, a.imag]).astype(np.float64) if np.iscomplexobj(a) else a.astype(np.float64)
+
+
+GDN_LAYER_CASES = [
+    ("factored_rms_16", (1, 3, 16, 16, 8), dict(gate_type="factored", output_norm="rms", delta_key_dim=4)),
+    ("dense_layer_qkvdw_8", (2, 2, 8, 8, 8), dict(gate_type="dense", output_norm="layer", delta_key_dim=2,
+                                                  qkv_conv_size=3)),
+    ("channel_none_noconv_16", (1, 4, 16, 16, 8), dict(gate_type="channel", output_norm="none", delta_key_dim=4,
+                                                       short_conv_size=0)),
+    ("scalar_nol2_32", (1, 2, 32, 32, 4), dict(gate_type="scalar", output_norm="rms", delta_key_dim=2,
+                                               use_input_gates=False, use_spectral_l2_norm=False)),
+]
+
+
+@pytest.mark.parametrize("name,shape,kw", GDN_LAYER_CASES, ids=[c[0] for c in GDN_LAYER_CASES])
+def test_gdn_layer_gradients_match_float64_reference(mods, name, shape, kw):
+    cells, _, training = mods
+    print_case(test="gdn_layer_grad", case=name)
+    rng = np.random.default_rng(44)
+    cfg = O.GDNConfig(channels=shape[-1], kernel_size=5, **kw)
+    p = O.init_params(O.gdn_param_shapes(cfg, shape[2], shape[3]), rng)
+    x = rng.standard_normal(shape)
+    ref_m = P.GdnRef(p, cfg)
+    xr = torch.from_numpy(x).requires_grad_(True)
+    out_r = ref_m(xr)
+    w = rng.standard_normal(tuple(out_r.shape))
+    ref_leaves = [("x", xr)] + _leaves(ref_m.p)
+    refs = torch.autograd.grad((out_r * torch.from_numpy(w)).sum(), [t for _, t in ref_leaves])
+
+    cell = cells.GatedDeltaNetCSSM(channels=shape[-1], kernel_size=5, **kw)
+    v = cells.GatedDeltaNetCSSM.load_params(p)
+    leaves = _leaves(v["params"])
+    for _, t in leaves:
+        t.requires_grad_(True)
+    xd = torch.from_numpy(x).to("cuda", torch.float32).requires_grad_(True)
+    out = training.gdn_train_apply(cell, v, xd)
+    with torch.no_grad():
+        assert rel_err(_np(out), out_r.detach().numpy()) <= TOL
+        assert rel_err(_np(out), _np(cell.apply(v, xd.detach()))) <= 2e-5
+    grads = torch.autograd.grad((out * torch.from_numpy(w).to("cuda", torch.float32)).sum(),
+                                [xd] + [t for _, t in leaves])
+    torch.cuda.synchronize()
+    names = ["x"] + [n for n, _ in leaves]
+    assert names == [n for n, _ in ref_leaves]
+    for n, g, r in zip(names, grads, refs):
+        assert rel_err(_np(g), r.numpy()) <= TOL, n

@@ -175,3 +175,98 @@ def test_float64_layer_adjoint_identity(kw):
     g = torch.autograd.grad((f(*ts) * w).sum(), ts)
     lhs, rhs = _dot(jv, w), sum(_dot(a, b) for a, b in zip(g, tang))
     assert abs(lhs - rhs) <= 1e-11 * abs(lhs), (lhs, rhs)
+
+
+# ------------------------------------------------------------------------- GDN cell
+
+GDN_CFGS = [
+    dict(gate_type="factored", output_norm="rms", delta_key_dim=4),
+    dict(gate_type="dense", output_norm="layer", delta_key_dim=2, qkv_conv_size=3),
+    dict(gate_type="channel", output_norm="none", delta_key_dim=4, short_conv_size=0),
+    dict(gate_type="scalar", output_norm="rms", delta_key_dim=2, use_input_gates=False, use_spectral_l2_norm=False),
+]
+
+
+def _gdn(kw, shape, seed):
+    rng = np.random.default_rng(seed)
+    cfg = O.GDNConfig(channels=shape[-1], kernel_size=5, **kw)
+    p = O.init_params(O.gdn_param_shapes(cfg, shape[2], shape[3]), rng)
+    return cfg, p, rng.standard_normal(shape)
+
+
+@pytest.mark.parametrize("kw", GDN_CFGS, ids=[c["gate_type"] for c in GDN_CFGS])
+def test_gdn_float64_forward_equals_oracle(kw):
+    cfg, p, x = _gdn(kw, (2, 3, 8, 8, 8), 10)
+    ref = O.gdn_forward(p, x, cfg)
+    got = P.GdnRef(p, cfg, requires_grad=False)(torch.from_numpy(x)).numpy()
+    assert np.max(np.abs(got - ref)) <= 1e-11 * np.sqrt(np.mean(ref ** 2))
+
+
+@pytest.mark.parametrize("kw", GDN_CFGS, ids=[c["gate_type"] for c in GDN_CFGS])
+def test_gdn_float64_gradient_equals_finite_differences(kw):
+    cfg, p, x = _gdn(kw, (1, 3, 8, 8, 8), 11)
+    rng = np.random.default_rng(12)
+    m = P.GdnRef(p, cfg)
+    xt = torch.from_numpy(x).requires_grad_(True)
+    leaves = [xt] + _leaves(m.p)
+    out = m(xt)
+    w = torch.from_numpy(rng.standard_normal(tuple(out.shape)))
+    grads = torch.autograd.grad((out * w).sum(), leaves)
+    for _ in range(2):
+        vs = [torch.from_numpy(rng.standard_normal(tuple(t.shape))) for t in leaves]
+        analytic = sum(float((g * v).sum()) for g, v in zip(grads, vs))
+        eps = 1e-6
+
+        def loss(sign):
+            with torch.no_grad():
+                for t, v in zip(leaves, vs):
+                    t.add_(sign * eps * v)
+                val = float((m(xt) * w).sum())
+                for t, v in zip(leaves, vs):
+                    t.sub_(sign * eps * v)
+            return val
+        fd = (loss(1.0) - loss(-1.0)) / (2 * eps)
+        assert abs(fd - analytic) <= 1e-6 * max(1.0, abs(analytic)), (fd, analytic)
+
+
+def test_gdn_bins_contract_equals_oracle_core():
+    """gdn_bins_core (the training kernels' contract: norms applied by the caller) reproduces the
+    oracle's gdn_core once the spectral norms and the irfft2 are put around it."""
+    rng = np.random.default_rng(13)
+    B, T, H, W, C, dk = 2, 3, 8, 8, 8, 4
+    nh, Wf = C // dk, W // 2 + 1
+    cfg = O.GDNConfig(channels=C, delta_key_dim=dk, gate_type="factored")
+    q, k, v = (rng.standard_normal((B, T, H, W, C)) for _ in range(3))
+    alpha = 0.1 + 0.89 / (1.0 + np.exp(-rng.standard_normal((B, T, H * Wf))))
+    beta = 1.0 / (1.0 + np.exp(-rng.standard_normal((B, T, H * Wf))))
+    what = O.spectral_kernel(rng.standard_normal((nh, 5, 5)) * 0.2, H, W, 0.999)
+    ref = O.gdn_core(q, k, v, alpha.reshape(B, T, 1, H, Wf), beta.reshape(B, T, 1, H, Wf), what, cfg)
+    spec = torch.fft.rfft2(torch.from_numpy(np.concatenate([z.transpose(0, 1, 4, 2, 3) for z in (q, k, v)], 2)))
+    qk = spec[:, :, :2 * C]
+    qk = qk / torch.sqrt((qk.abs() ** 2).sum(dim=(3, 4), keepdim=True) + 1e-6)
+    spec = torch.cat([qk, spec[:, :, 2 * C:]], 2)
+    ab = torch.from_numpy(np.stack([alpha, beta], -1))
+    ohat = P.gdn_bins_core(spec, ab, torch.from_numpy(what), "factored", dk)
+    got = torch.fft.irfft2(ohat, s=(H, W)).numpy()
+    assert np.max(np.abs(got - ref)) <= 1e-12 * np.sqrt(np.mean(ref ** 2))
+
+
+def test_gdn_float64_adjoint_identity():
+    """<J v, w> (forward mode) = <v, J^T w> (reverse mode) for the GDN layer over x and every parameter."""
+    cfg, p, x = _gdn(GDN_CFGS[0], (1, 2, 8, 8, 8), 14)
+    rng = np.random.default_rng(15)
+    m = P.GdnRef(p, cfg, requires_grad=False)
+    slots = _slots(m.p)
+    prim = [torch.from_numpy(x)] + [d[k] for d, k in slots]
+    tang = [torch.from_numpy(rng.standard_normal(tuple(t.shape))) for t in prim]
+
+    def f(xx, *leaves):
+        for (d, k), t in zip(slots, leaves):
+            d[k] = t
+        return m(xx)
+    y, jv = torch.func.jvp(f, tuple(prim), tuple(tang))
+    w = torch.from_numpy(rng.standard_normal(tuple(y.shape)))
+    ts = [t.detach().clone().requires_grad_(True) for t in prim]
+    g = torch.autograd.grad((f(*ts) * w).sum(), ts)
+    lhs, rhs = _dot(jv, w), sum(_dot(a, b) for a, b in zip(g, tang))
+    assert abs(lhs - rhs) <= 1e-11 * abs(lhs), (lhs, rhs)
