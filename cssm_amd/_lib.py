@@ -94,6 +94,8 @@ SIGNATURES = {
     "cssm_irfft2": (_I, [_P, _LL, _I, _I, _P, _I, _P]),
     "cssm_fft_min_group": (_I, [_I, _I]),
     "cssm_gdn_scan_bins": (_I, [_P, _P, _P, _LL, _I, _I, _P, _I, _I, _I, _I, _I, _I, _P, _P]),
+    "cssm_depthwise_conv_wgrad": (_I, [_P, _P, _I, _I, _I, _I, _I, _P, _I, _P]),
+    "cssm_depthwise_conv_wgrad_supported": (_I, [_I, _I, _I]),
     "cssm_gdn_scan_bins_train": (_I, [_P, _P, _LL, _I, _I, _P, _I, _I, _I, _I, _I, _I, _P, _P, _P]),
     "cssm_gdn_scan_bins_bwd": (_I, [_P, _P, _LL, _I, _I, _P, _P, _P, _I, _I, _I, _I, _I, _I, _P, _P, _P, _P]),
     "cssm_gdn_proj_out": (_I, [_P, _P, _I, _I, _I, _I, _I, _I, _P, _P, _P, _P, _P, _I, _P]),

@@ -477,6 +477,22 @@ int cssm_gdn_scan_bins_bwd(const float* spec, const float* ab, long long ab_fram
                     "cssm_gdn_scan_bins_bwd");
 }
 
+int cssm_depthwise_conv_wgrad_supported(int W, int C, int ks) { return cssm::dwconv_wgrad_supported(W, C, ks) ? 1 : 0; }
+
+int cssm_depthwise_conv_wgrad(const float* x, const float* dy, int F, int H, int W, int C, int ks, float* partial,
+                              int blocks, void* stream) {
+  if (!x || !dy || !partial) return fail(CSSM_ERR_NULL, "cssm_depthwise_conv_wgrad: null argument");
+  if (F <= 0 || H <= 0 || W <= 0 || C <= 0 || blocks <= 0 || blocks > 65535)
+    return fail(CSSM_ERR_SHAPE, "cssm_depthwise_conv_wgrad: F=%d H=%d W=%d C=%d blocks=%d", F, H, W, C, blocks);
+  if (!cssm::dwconv_wgrad_supported(W, C, ks))
+    return fail(CSSM_ERR_UNSUPPORTED, "cssm_depthwise_conv_wgrad: ks=%d C=%d W=%d (ks 3/5/7, C/4 dividing 64, W %% 8 == 0)",
+                ks, C, W);
+  if (!aligned(x, 16) || !aligned(dy, 16) || !aligned(partial, 16))
+    return fail(CSSM_ERR_ALIGN, "cssm_depthwise_conv_wgrad: tensors must be 16-byte aligned");
+  return hip_status(cssm::launch_dwconv_wgrad(x, dy, F, H, W, C, ks, partial, blocks, static_cast<hipStream_t>(stream)),
+                    "cssm_depthwise_conv_wgrad");
+}
+
 int cssm_gdn_core_fused_supported(int H, int W, int delta_key_dim) {
   return cssm::gdn_core_fused_supported(H, W, delta_key_dim) ? 1 : 0;
 }

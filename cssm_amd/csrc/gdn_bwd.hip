@@ -250,4 +250,107 @@ hipError_t launch_gdn_scan_bins_train(const float2* spec, const float2* ab, long
   return hipGetLastError();
 }
 
+// ---------------------------------------------------------------------------
+// Weight gradient of the depthwise KS x KS SAME convolution of channels-last
+// frames (qkv_dw, cssm.py:4744-4750): dW[a][b][c] = sum over frames and pixels
+// of x[h + a - lo][w + b - lo][c] dy[h][w][c] (zero outside the frame).  A thread
+// owns 4 channels and strips of 8 pixels of a row: it loads the strip's dy and,
+// per tap row, the 8 + KS - 1 inputs it needs once, and keeps all KS^2 taps'
+// sums in registers.  Block partials (KS^2, C) are reduced in a fixed order
+// (lane shuffles, then across waves through LDS); the caller sums the blocks.
+namespace {
+template <int KS>
+__global__ void __launch_bounds__(256) dwconv_wgrad_cl(const float* __restrict__ x, const float* __restrict__ dy,
+                                                        int F, int H, int W, int C, float* __restrict__ partial) {
+  constexpr int LO = (KS - 1) / 2, RW = 8, NCOL = RW + KS - 1;
+  const int CQ = C / 4, SPB = 256 / CQ;                     // channel quads; strips per block pass
+  const int tid = int(threadIdx.x), cq = tid % CQ, sl = tid / CQ;
+  const int c0 = cq * 4, WS = W / RW;
+  const long long strips = (long long)F * H * WS;
+  float4 acc[KS][KS];
+#pragma unroll
+  for (int a = 0; a < KS; ++a)
+#pragma unroll
+    for (int b = 0; b < KS; ++b) acc[a][b] = make_float4(0.f, 0.f, 0.f, 0.f);
+  for (long long s = (long long)blockIdx.x * SPB + sl; s < strips; s += (long long)gridDim.x * SPB) {
+    const int ws = int(s % WS);
+    const long long fh = s / WS;
+    const int h = int(fh % H);
+    const long long f = fh / H;
+    const int w0 = ws * RW;
+    const float* xf = x + f * H * W * C;
+    float4 g[RW];
+#pragma unroll
+    for (int q = 0; q < RW; ++q)
+      g[q] = *reinterpret_cast<const float4*>(dy + ((f * H + h) * W + w0 + q) * C + c0);
+#pragma unroll
+    for (int a = 0; a < KS; ++a) {
+      const int hh = h + a - LO;
+      if (hh < 0 || hh >= H) continue;
+      float4 xin[NCOL];
+#pragma unroll
+      for (int ic = 0; ic < NCOL; ++ic) {
+        const int ww = w0 - LO + ic;
+        xin[ic] = (ww >= 0 && ww < W) ? *reinterpret_cast<const float4*>(xf + (size_t(hh) * W + ww) * C + c0)
+                                      : make_float4(0.f, 0.f, 0.f, 0.f);
+      }
+#pragma unroll
+      for (int b = 0; b < KS; ++b)
+#pragma unroll
+        for (int q = 0; q < RW; ++q) {
+          acc[a][b].x = fmaf(xin[q + b].x, g[q].x, acc[a][b].x);
+          acc[a][b].y = fmaf(xin[q + b].y, g[q].y, acc[a][b].y);
+          acc[a][b].z = fmaf(xin[q + b].z, g[q].z, acc[a][b].z);
+          acc[a][b].w = fmaf(xin[q + b].w, g[q].w, acc[a][b].w);
+        }
+    }
+  }
+  // threads of one channel quad: lanes l, l + CQ, ... of a wave, then the waves
+  __shared__ float4 red[4][64];
+  const int lane = tid & 63, wave = tid >> 6;
+#pragma unroll
+  for (int a = 0; a < KS; ++a)
+#pragma unroll
+    for (int b = 0; b < KS; ++b) {
+      float4 v = acc[a][b];
+      for (int d = 32; d >= CQ; d >>= 1) {
+        v.x += __shfl_xor(v.x, d, 64);
+        v.y += __shfl_xor(v.y, d, 64);
+        v.z += __shfl_xor(v.z, d, 64);
+        v.w += __shfl_xor(v.w, d, 64);
+      }
+      if (lane < CQ) red[wave][lane] = v;      // CQ <= 64 here: every quad in every wave
+      __syncthreads();
+      if (tid < CQ) {
+        float4 t = red[0][tid];
+        for (int ww = 1; ww < 4; ++ww) {
+          t.x += red[ww][tid].x;
+          t.y += red[ww][tid].y;
+          t.z += red[ww][tid].z;
+          t.w += red[ww][tid].w;
+        }
+        *reinterpret_cast<float4*>(partial + (size_t(blockIdx.x) * KS * KS + a * KS + b) * C + tid * 4) = t;
+      }
+      __syncthreads();
+    }
+}
+}  // namespace
+
+bool dwconv_wgrad_supported(int W, int C, int ks) {
+  const int cq = C / 4;
+  return (ks == 3 || ks == 5 || ks == 7) && C % 4 == 0 && cq >= 1 && cq <= 64 && 64 % cq == 0 && W % 8 == 0;
+}
+
+hipError_t launch_dwconv_wgrad(const float* x, const float* dy, int F, int H, int W, int C, int ks, float* partial,
+                               int blocks, hipStream_t s) {
+  if (!dwconv_wgrad_supported(W, C, ks) || blocks <= 0) return hipErrorInvalidValue;
+  switch (ks) {
+    case 3: hipLaunchKernelGGL(dwconv_wgrad_cl<3>, dim3(unsigned(blocks)), dim3(256), 0, s, x, dy, F, H, W, C, partial); break;
+    case 5: hipLaunchKernelGGL(dwconv_wgrad_cl<5>, dim3(unsigned(blocks)), dim3(256), 0, s, x, dy, F, H, W, C, partial); break;
+    case 7: hipLaunchKernelGGL(dwconv_wgrad_cl<7>, dim3(unsigned(blocks)), dim3(256), 0, s, x, dy, F, H, W, C, partial); break;
+    default: return hipErrorInvalidValue;
+  }
+  return hipGetLastError();
+}
+
 }  // namespace cssm

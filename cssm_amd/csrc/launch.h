@@ -89,6 +89,11 @@ int fft_planes_min_group(int H, int W);
 hipError_t launch_gdn_scan_bins(const float2* spec, const float* norms, const float2* ab, long long ab_frame,
                                 int ab_head, int ab_bin, const float2* what, int B, int T, int C, int H, int W,
                                 int dk, float2* ohat, hipStream_t s);
+// weight gradient of the depthwise SAME conv of channels-last frames: per-block partial sums
+// (blocks, ks*ks, C) for the caller to add; gdn_bwd.hip
+bool dwconv_wgrad_supported(int W, int C, int ks);
+hipError_t launch_dwconv_wgrad(const float* x, const float* dy, int F, int H, int W, int C, int ks, float* partial,
+                               int blocks, hipStream_t s);
 // training: forward with the state entering every step saved (backward = false), or the reverse
 // pass from those states (backward = true); gdn_bwd.hip
 hipError_t launch_gdn_scan_bins_train(const float2* spec, const float2* ab, long long ab_frame, int ab_head,

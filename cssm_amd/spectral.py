@@ -480,6 +480,26 @@ def gdn_scan_bins(spec: torch.Tensor, norms: Optional[torch.Tensor], ab: torch.T
     return ohat
 
 
+def depthwise_conv_wgrad_supported(W: int, C: int, ks: int) -> bool:
+    return bool(_lib.load().cssm_depthwise_conv_wgrad_supported(W, C, ks))
+
+
+def depthwise_conv_wgrad(x: torch.Tensor, dy: torch.Tensor, ks: int, blocks: int = 1024) -> torch.Tensor:
+    """dL/d kernel (ks, ks, 1, C) of :func:`depthwise_conv` for its input x and output gradient dy,
+    both float32 channels-last (..., H, W, C): block partial sums on the GPU, added here."""
+    _dev(x, "x", torch.float32)
+    _dev(dy, "dy", torch.float32)
+    *lead, H, W, C = x.shape
+    F = 1
+    for d in lead:
+        F *= d
+    blocks = max(1, min(blocks, (F * H * (W // 8) + 63) // 64))
+    partial = torch.empty((blocks, ks, ks, C), dtype=torch.float32, device=x.device)
+    _lib.call("cssm_depthwise_conv_wgrad", x.data_ptr(), dy.data_ptr(), F, H, W, C, ks, partial.data_ptr(), blocks,
+              _stream())
+    return partial.sum(dim=0).unsqueeze(2)
+
+
 def _ab_strides(ab: torch.Tensor, gate_type: str):
     n_ab = ab.shape[2]
     return {"dense": (n_ab, 0, 1), "factored": (n_ab, 0, 1), "channel": (n_ab, 1, 0), "scalar": (1, 0, 0)}[gate_type]

@@ -42,6 +42,81 @@ class _ScanFn(torch.autograd.Function):
         return du, dz, dgates, dkhat, None
 
 
+class _ProjPlanesFn(torch.autograd.Function):
+    """Dense over channels-last rows x (F HW, K) into plane-major (F, N, HW) on the HIP projection
+    kernel.  Adjoint: dx = dy W^T back to channels-last (the plane-major -> channels-last kernel with
+    W^T), dW = sum_f (dy_f x_f)^T (one batched GEMM over frames), db = sum of dy."""
+
+    @staticmethod
+    def forward(ctx, x2, kernel, bias, frames, hw):
+        ctx.save_for_backward(x2, kernel)
+        ctx.frames, ctx.hw = frames, hw
+        return S.proj_planes(x2, kernel, bias, frames, hw, out_dtype=torch.float32)
+
+    @staticmethod
+    def backward(ctx, dy):
+        x2, kernel = ctx.saved_tensors
+        dy = dy.contiguous()
+        K, N = kernel.shape
+        dx = S.proj_out(dy, kernel.t().contiguous(), kernel.new_zeros(K), out_dtype=torch.float32)
+        dw = torch.bmm(dy, x2.view(ctx.frames, ctx.hw, K)).sum(dim=0).t()
+        return dx, dw, dy.sum(dim=(0, 2)), None, None
+
+
+class _ProjOutFn(torch.autograd.Function):
+    """Dense over plane-major y (F, K, HW) into channels-last (F HW, N) on the HIP projection kernel.
+    Adjoint: dy = dout W^T back to plane-major (the channels-last -> plane-major kernel with W^T),
+    dW = sum_f y_f dout_f (one batched GEMM over frames), db = sum of dout."""
+
+    @staticmethod
+    def forward(ctx, y, kernel, bias):
+        ctx.save_for_backward(y, kernel)
+        return S.proj_out(y, kernel, bias, out_dtype=torch.float32)
+
+    @staticmethod
+    def backward(ctx, dout):
+        y, kernel = ctx.saved_tensors
+        dout = dout.contiguous()
+        F, K, hw = y.shape
+        N = kernel.shape[1]
+        dy = S.proj_planes(dout, kernel.t().contiguous(), kernel.new_zeros(K), F, hw, out_dtype=torch.float32)
+        dw = torch.bmm(y, dout.view(F, hw, N)).sum(dim=0)
+        return dy, dw, dout.sum(dim=0)
+
+
+class _DwConvFn(torch.autograd.Function):
+    """Depthwise ks x ks SAME conv with bias of channels-last (F, H, W, C) frames on the HIP kernel.
+    Adjoints: dx = the same conv of dy with the taps flipped (odd ks: the padding is symmetric),
+    dW from the weight-gradient kernel, db = sum of dy."""
+
+    @staticmethod
+    def forward(ctx, x, kernel, bias):
+        ctx.save_for_backward(x, kernel)
+        return S.depthwise_conv(x, kernel, bias, out_dtype=torch.float32)
+
+    @staticmethod
+    def backward(ctx, dy):
+        x, kernel = ctx.saved_tensors
+        dy = dy.contiguous()
+        C = x.shape[-1]
+        dx = S.depthwise_conv(dy, kernel.flip(0, 1).contiguous(), kernel.new_zeros(C), out_dtype=torch.float32)
+        dw = S.depthwise_conv_wgrad(x, dy, kernel.shape[0])
+        return dx, dw, dy.sum(dim=(0, 1, 2))
+
+
+def _dwconv_cl(x4, q):
+    """Depthwise SAME conv of channels-last (F, H, W, C) frames: the HIP kernels where they apply
+    (odd ks in 3..7, C / 4 dividing 64, W % 8 == 0), else torch's conv."""
+    ks = q["kernel"].shape[0]
+    F, H, W, C = x4.shape
+    if ks % 2 == 1 and S.depthwise_conv_wgrad_supported(W, C, ks):
+        return _DwConvFn.apply(x4.contiguous(), q["kernel"], q["bias"])
+    lo, hi = (ks - 1) // 2, ks // 2
+    w = q["kernel"].permute(3, 2, 0, 1)                                      # (C, 1, k, k)
+    return (Fn.conv2d(Fn.pad(x4.permute(0, 3, 1, 2), (lo, hi, lo, hi)), w, groups=C)
+            + q["bias"][None, :, None, None]).permute(0, 2, 3, 1)
+
+
 def _col_index(H: int, W: int, device) -> torch.Tensor:
     return torch.tensor(S.scan_col_order(H, W), dtype=torch.long, device=device)
 
@@ -112,8 +187,8 @@ def gated_train_apply(cell, params: Dict[str, Any], x: torch.Tensor) -> torch.Te
     F, HW = B * T, H * W
     if not S.gated_scan_supported(H, W):
         raise NotImplementedError(f"no fused scan kernel for {H}x{W} planes")
-    xz = torch.addmm(p["in_proj"]["bias"], x.reshape(-1, cin).float(), p["in_proj"]["kernel"])
-    xz = xz.view(F, HW, 2 * Ci).transpose(1, 2)                          # plane-major (F, 2C, HW)
+    xz = _ProjPlanesFn.apply(x.reshape(-1, cin).float().contiguous(), p["in_proj"]["kernel"], p["in_proj"]["bias"],
+                             F, HW)                                        # plane-major (F, 2C, HW)
     xm, z = xz[:, :Ci].reshape(B, T, Ci, H, W), xz[:, Ci:].reshape(B, T, Ci, H, W)
     if cell.short_conv_spatial_size > 0:
         sp = p["short_conv_spatial"]
@@ -130,8 +205,7 @@ def gated_train_apply(cell, params: Dict[str, Any], x: torch.Tensor) -> torch.Te
     gates = gate_planes(u.mean(dim=(3, 4)), p, H, W, cell.gate_type, cell.gate_activation, c_scale)
     khat = khat_planes(p["kernel"], H, W, cell.spectral_rho)
     y = _ScanFn.apply(u, zg, gates, khat, c_scale)                           # (B, T, C, H, W)
-    out = torch.addmm(p["out_proj"]["bias"], y.view(F, Ci, HW).transpose(1, 2).reshape(-1, Ci),
-                      p["out_proj"]["kernel"])
+    out = _ProjOutFn.apply(y.view(F, Ci, HW), p["out_proj"]["kernel"], p["out_proj"]["bias"])
     return out.view(B, T, H, W, cell.channels)
 
 
@@ -275,14 +349,9 @@ def gdn_train_apply(cell, params: Dict[str, Any], x: torch.Tensor) -> torch.Tens
         ctx = ctx + _temporal_encoding(T, C, cell.rope_base, x.device)[None]
     xq = x.reshape(F, H, W, C)
     if cell.qkv_conv_size > 1:
-        q = p["qkv_dw"]
-        ks = q["kernel"].shape[0]
-        lo, hi = (ks - 1) // 2, ks // 2
-        w = q["kernel"].permute(3, 2, 0, 1)                                  # (C, 1, k, k)
-        xq = (Fn.conv2d(Fn.pad(xq.permute(0, 3, 1, 2), (lo, hi, lo, hi)), w, groups=C)
-              + q["bias"][None, :, None, None]).permute(0, 2, 3, 1)
-    qkv = torch.addmm(p["qkv_proj"]["bias"], xq.reshape(-1, C), p["qkv_proj"]["kernel"])
-    qkv = qkv.view(F, HW, 3 * C).transpose(1, 2).reshape(B, T, 3 * C, H, W)   # plane-major
+        xq = _dwconv_cl(xq, p["qkv_dw"])
+    qkv = _ProjPlanesFn.apply(xq.reshape(-1, C).contiguous(), p["qkv_proj"]["kernel"], p["qkv_proj"]["bias"], F,
+                              HW).view(B, T, 3 * C, H, W)                 # plane-major
     q, k, v = qkv[:, :, :C], qkv[:, :, C:2 * C], qkv[:, :, 2 * C:]
     if cell.short_conv_size > 0:
         q = Fn.silu(_causal_t(q, p["short_conv_q"]))
@@ -291,8 +360,8 @@ def gdn_train_apply(cell, params: Dict[str, Any], x: torch.Tensor) -> torch.Tens
     if cell.use_input_gates:
         k = k * _gdn_gate(p, "B_k", cell.gate_type, ctx, x, H, W, nh, spatial=True)
         v = v * _gdn_gate(p, "B_v", cell.gate_type, ctx, x, H, W, nh, spatial=True)
-    gv = torch.addmm(p["gate_proj"]["bias"], x.reshape(-1, C), p["gate_proj"]["kernel"])
-    gv = Fn.silu(gv) if cell.output_gate_act == "silu" else torch.sigmoid(gv)
+    gv = _ProjPlanesFn.apply(x.reshape(-1, C).contiguous(), p["gate_proj"]["kernel"], p["gate_proj"]["bias"], F, HW)
+    gv = Fn.silu(gv) if cell.output_gate_act == "silu" else torch.sigmoid(gv)   # plane-major (F, C, HW)
     alpha = _gdn_gate(p, "alpha", cell.gate_type, ctx, x, H, W, nh, bounded=True)
     beta = _gdn_gate(p, "beta", cell.gate_type, ctx, x, H, W, nh)
     ab = torch.stack([alpha, beta], dim=-1).contiguous()                    # (B, T, n_ab, 2)
@@ -302,13 +371,14 @@ def gdn_train_apply(cell, params: Dict[str, Any], x: torch.Tensor) -> torch.Tens
         qk = qk * torch.rsqrt((qk.real ** 2 + qk.imag ** 2).sum(dim=(3, 4), keepdim=True) + 1e-6)
         spec = torch.cat([qk, spec[:, :, 2 * C:]], dim=2)
     ohat = _GdnBinsFn.apply(spec.contiguous(), ab, what, cell.gate_type, dk)
-    o = _Irfft2Fn.apply(ohat, W)                                             # (B, T, C, H, W)
-    o = o.reshape(F, C, HW).transpose(1, 2)                                  # (F, HW, C)
+    o = _Irfft2Fn.apply(ohat, W).view(F, C, HW)                              # plane-major
+    # per-pixel norm over the channels (dim 1 of the plane-major frames)
     if cell.output_norm == "rms":
-        o = o * torch.rsqrt((o * o).mean(dim=-1, keepdim=True) + 1e-6) * p["rms_scale"]
+        o = o * torch.rsqrt((o * o).mean(dim=1, keepdim=True) + 1e-6) * p["rms_scale"][None, :, None]
     elif cell.output_norm == "layer":
-        mu = o.mean(dim=-1, keepdim=True)
-        var = ((o - mu) ** 2).mean(dim=-1, keepdim=True)
-        o = (o - mu) * torch.rsqrt(var + 1e-6) * p["output_layernorm"]["scale"] + p["output_layernorm"]["bias"]
-    out = torch.addmm(p["output_proj"]["bias"], (o * gv.view(F, HW, C)).reshape(-1, C), p["output_proj"]["kernel"])
+        mu = o.mean(dim=1, keepdim=True)
+        var = ((o - mu) ** 2).mean(dim=1, keepdim=True)
+        o = ((o - mu) * torch.rsqrt(var + 1e-6) * p["output_layernorm"]["scale"][None, :, None]
+             + p["output_layernorm"]["bias"][None, :, None])
+    out = _ProjOutFn.apply((o * gv).contiguous(), p["output_proj"]["kernel"], p["output_proj"]["bias"])
     return out.view(B, T, H, W, C)

@@ -399,6 +399,22 @@ int cssm_gdn_scan_bins(const float* spec, const float* norms, const float* ab, l
                        int delta_key_dim, float* ohat, void* stream);
 
 /*
+ * Weight gradient of the depthwise ks x ks SAME convolution cssm_depthwise_conv
+ * computes (qkv_dw, cssm.py:4744-4750; the reference takes it through
+ * jax.value_and_grad, main.py:283): dW[a][b][c] = sum over frames and pixels of
+ * x[h + a - (ks-1)/2][w + b - (ks-1)/2][c] dy[h][w][c], zero outside the frame.
+ *   x, dy    (F, H, W, C) float32 channels-last
+ *   partial  (blocks, ks, ks, C) float32 out: per-block partial sums (add them over blocks)
+ * ks in {3, 5, 7}, C / 4 dividing 64, W a multiple of 8 (cssm_depthwise_conv_wgrad_supported);
+ * 16-byte aligned tensors; blocks <= 65535.
+ */
+int cssm_depthwise_conv_wgrad(const float* x, const float* dy, int F, int H, int W, int C, int ks, float* partial,
+                              int blocks, void* stream);
+
+/* 1 if cssm_depthwise_conv_wgrad has a kernel for (W, C, ks), else 0. */
+int cssm_depthwise_conv_wgrad_supported(int W, int C, int ks);
+
+/*
  * Training forward of the delta-rule recurrence: cssm_gdn_scan_bins with the
  * spectral L2 norms left to the caller (spec holds q and k already scaled by
  * them, and v), plus the state entering every step, which the reverse pass

@@ -264,3 +264,31 @@ def test_gdn_layer_gradients_match_float64_reference(mods, name, shape, kw):
     assert names == [n for n, _ in ref_leaves]
     for n, g, r in zip(names, grads, refs):
         assert rel_err(_np(g), r.numpy()) <= TOL, n
+
+
+DW_CASES = [(3, (2, 16, 16, 8)), (5, (3, 8, 24, 16)), (7, (1, 12, 16, 64)), (5, (4, 32, 32, 4))]
+
+
+@pytest.mark.parametrize("ks,shape", DW_CASES, ids=[f"k{c[0]}_{c[1][1]}x{c[1][2]}_C{c[1][3]}" for c in DW_CASES])
+def test_depthwise_conv_vjp_matches_float64(mods, ks, shape):
+    """The training path's depthwise SAME conv (HIP forward, flipped-tap data gradient, the
+    weight-gradient kernel) against float64 autograd of torch's grouped conv."""
+    _, S, training = mods
+    print_case(test="dwconv_vjp", ks=ks, shape=shape)
+    rng = np.random.default_rng(45)
+    F, H, W, C = shape
+    assert S.depthwise_conv_wgrad_supported(W, C, ks)
+    x, k, b = rng.standard_normal(shape), rng.standard_normal((ks, ks, 1, C)) / ks, rng.standard_normal(C)
+    dy = rng.standard_normal(shape)
+    ts = [torch.from_numpy(a).requires_grad_(True) for a in (x, k, b)]
+    lo, hi = (ks - 1) // 2, ks // 2
+    ref = (torch.nn.functional.conv2d(torch.nn.functional.pad(ts[0].permute(0, 3, 1, 2), (lo, hi, lo, hi)),
+                                      ts[1].permute(3, 2, 0, 1), groups=C) + ts[2][None, :, None, None]).permute(0, 2, 3, 1)
+    refs = torch.autograd.grad(ref, ts, torch.from_numpy(dy))
+    dev = [torch.from_numpy(a).to("cuda", torch.float32).requires_grad_(True) for a in (x, k, b)]
+    out = training._DwConvFn.apply(*dev)
+    got = torch.autograd.grad(out, dev, torch.from_numpy(dy).to("cuda", torch.float32))
+    torch.cuda.synchronize()
+    assert rel_err(_np(out), ref.detach().numpy()) <= 1e-5
+    for n, g, r in zip(("dx", "dkernel", "dbias"), got, refs):
+        assert rel_err(_np(g), r.numpy()) <= TOL, n
