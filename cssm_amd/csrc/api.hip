@@ -348,7 +348,6 @@ int cssm_gdn_qkv_post(void* qkv, int dtype, int B, int T, int C, int H, int W, i
       sc.b[i] = conv_bias[i];
     }
   }
-  if ((H * W) % 4) return fail(CSSM_ERR_UNSUPPORTED, "cssm_gdn_qkv_post: H*W=%d must be a multiple of 4", H * W);
   if (!aligned(qkv, dtype == CSSM_F32 ? 16 : 8) || (gate_mode == 1 && !aligned(gates, 8)) ||
       (gate_mode == 3 && !aligned(gates, 16)))
     return fail(CSSM_ERR_ALIGN, "cssm_gdn_qkv_post: misaligned qkv / gates");
@@ -377,7 +376,6 @@ int cssm_gdn_qkv_proj(const void* x, int in_dtype, int B, int T, int H, int W, i
       sc.b[i] = conv_bias[i];
     }
   }
-  if ((H * W) % 4) return fail(CSSM_ERR_UNSUPPORTED, "cssm_gdn_qkv_proj: H*W=%d must be a multiple of 4", H * W);
   if (!aligned(x, vec_align(in_dtype)) || !aligned(qkv, vec_align(out_dtype)) ||
       (gate_mode == 1 && !aligned(gates, 8)) || (gate_mode == 3 && !aligned(gates, 16)))
     return fail(CSSM_ERR_ALIGN, "cssm_gdn_qkv_proj: misaligned x / qkv / gates");
@@ -523,8 +521,8 @@ int cssm_gdn_proj_out(const void* o, const void* gate, int in_dtype, int F, int 
                       int out_dtype, void* stream) {
   if (!o || !gate || !kernel || !bias || !out) return fail(CSSM_ERR_NULL, "cssm_gdn_proj_out: null argument");
   if (F <= 0 || HW <= 0 || K <= 0 || N <= 0) return fail(CSSM_ERR_SHAPE, "cssm_gdn_proj_out: F=%d HW=%d K=%d N=%d", F, HW, K, N);
-  if (K > 128 || K % 4 || HW % 4)
-    return fail(CSSM_ERR_UNSUPPORTED, "cssm_gdn_proj_out: needs K <= 128, K %% 4 == 0, HW %% 4 == 0 (K=%d HW=%d)", K, HW);
+  if (K > 128 || K % 4)
+    return fail(CSSM_ERR_UNSUPPORTED, "cssm_gdn_proj_out: needs K <= 128, K %% 4 == 0 (K=%d)", K);
   if ((long long)F * HW > 0x7fffffffLL) return fail(CSSM_ERR_SHAPE, "cssm_gdn_proj_out: F*HW exceeds 2^31");
   if (!dtype_ok(in_dtype) || !dtype_ok(out_dtype)) return fail(CSSM_ERR_ARG, "cssm_gdn_proj_out: dtypes %d/%d", in_dtype, out_dtype);
   if (norm < CSSM_NORM_NONE || norm > CSSM_NORM_LAYER) return fail(CSSM_ERR_ARG, "cssm_gdn_proj_out: norm=%d", norm);

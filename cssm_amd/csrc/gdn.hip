@@ -19,6 +19,7 @@
 
 #include <initializer_list>
 
+#include "dft_small.h"
 #include "fft_plane.h"
 #include "gdn_step.h"
 #include "launch.h"
@@ -298,18 +299,136 @@ hipError_t dispatch_inv(const float2* spec, long long P, int H, void* y, hipStre
 }  // namespace
 
 // power-of-two planes 4..128, any plane count (a partial last group is masked)
+// ---------------------------------------------------------------------------
+// Batched 2-D real FFTs of small planes that are not powers of two (H = W in
+// 3..15: the 14 x 14 and 7 x 7 CSSM-SHViT stages) by direct DFTs with
+// compile-time twiddles (dft_small.h): rows R2C, then one thread per column
+// (plane, v) for the column DFT; the inverse runs the column DFTs first, then
+// numpy's C2R rule per row.  A workgroup transforms NP consecutive planes.
+template <int H, class IO>
+__global__ void __launch_bounds__((SmallGeom<H, H>::NT))
+rfft2_small(const void* xv, long long P, float2* __restrict__ spec, float* __restrict__ norms) {
+  using G = SmallGeom<H, H>;
+  constexpr int W = H, WF = G::WF, HW = G::HW, NT = G::NT, NP = G::NP;
+  __shared__ float xs[NP * HW];
+  __shared__ float2 rs[NP * G::PS];
+  __shared__ float cn[NP * WF];                      // per column sum |X|^2
+  const typename IO::T* __restrict__ x = static_cast<const typename IO::T*>(xv);
+  const int tid = int(threadIdx.x);
+  const long long p0 = (long long)blockIdx.x * NP;
+  const int np = int(P - p0 < NP ? P - p0 : NP);
+  for (int e = tid; e < np * HW; e += NT) xs[e] = IO::to_f(x[size_t(p0) * HW + e]);
+  __syncthreads();
+  for (int j = tid; j < np * H; j += NT) small_row_r2c<W>(xs + j * W, rs + (j / H) * G::PS + (j % H) * G::RSP);
+  __syncthreads();
+  const int cpl = tid / WF, cv = tid % WF;
+  if (tid < G::NCJ && cpl < np) {
+    float2 r[H], X[H];
+#pragma unroll
+    for (int h = 0; h < H; ++h) r[h] = rs[cpl * G::PS + h * G::RSP + cv];
+    dft_sym<H, false>(r, X);
+    float2* out = spec + size_t(p0 + cpl) * (H * WF) + cv;
+    float acc = 0.0f;
+#pragma unroll
+    for (int u = 0; u < H; ++u) {
+      out[u * WF] = X[u];
+      acc = fmaf(X[u].x, X[u].x, fmaf(X[u].y, X[u].y, acc));
+    }
+    cn[cpl * WF + cv] = acc;
+  }
+  if (norms) {
+    __syncthreads();
+    if (tid < np) {
+      float sum = 0.0f;
+#pragma unroll
+      for (int v = 0; v < WF; ++v) sum += cn[tid * WF + v];
+      norms[p0 + tid] = sum;
+    }
+  }
+}
+
+template <int H, class IO>
+__global__ void __launch_bounds__((SmallGeom<H, H>::NT))
+irfft2_small(const float2* __restrict__ spec, long long P, void* yv) {
+  using G = SmallGeom<H, H>;
+  constexpr int W = H, WF = G::WF, HW = G::HW, NT = G::NT, NP = G::NP;
+  __shared__ float xs[NP * HW];
+  __shared__ float2 rs[NP * G::PS];
+  typename IO::T* __restrict__ y = static_cast<typename IO::T*>(yv);
+  const int tid = int(threadIdx.x);
+  const long long p0 = (long long)blockIdx.x * NP;
+  const int np = int(P - p0 < NP ? P - p0 : NP);
+  for (int e = tid; e < np * H * WF; e += NT) {
+    const int pl = e / (H * WF), r = e % (H * WF);
+    rs[pl * G::PS + (r / WF) * G::RSP + r % WF] = spec[size_t(p0) * (H * WF) + e];
+  }
+  __syncthreads();
+  const int cpl = tid / WF, cv = tid % WF;
+  if (tid < G::NCJ && cpl < np) {
+    float2 r[H], Z[H];
+#pragma unroll
+    for (int u = 0; u < H; ++u) r[u] = rs[cpl * G::PS + u * G::RSP + cv];
+    dft_sym<H, true>(r, Z);
+    constexpr float inv = 1.0f / float(HW);
+#pragma unroll
+    for (int h = 0; h < H; ++h) rs[cpl * G::PS + h * G::RSP + cv] = cscale(Z[h], inv);
+  }
+  __syncthreads();
+  for (int j = tid; j < np * H; j += NT) small_row_c2r<W>(rs + (j / H) * G::PS + (j % H) * G::RSP, xs + j * W);
+  __syncthreads();
+  for (int e = tid; e < np * HW; e += NT) y[size_t(p0) * HW + e] = IO::from_f(xs[e]);
+}
+
+template <class IO>
+static hipError_t small_fwd(const void* x, long long P, int H, float2* spec, float* norms, hipStream_t s) {
+#define CSSM_SMALL_FWD(N)                                                                                  \
+  case N:                                                                                                  \
+    hipLaunchKernelGGL((rfft2_small<N, IO>), dim3(unsigned((P + SmallGeom<N, N>::NP - 1) / SmallGeom<N, N>::NP)), \
+                       dim3(SmallGeom<N, N>::NT), 0, s, x, P, spec, norms);                                \
+    break;
+  switch (H) {
+    CSSM_SMALL_FWD(3) CSSM_SMALL_FWD(5) CSSM_SMALL_FWD(6) CSSM_SMALL_FWD(7) CSSM_SMALL_FWD(9) CSSM_SMALL_FWD(10)
+    CSSM_SMALL_FWD(11) CSSM_SMALL_FWD(12) CSSM_SMALL_FWD(13) CSSM_SMALL_FWD(14) CSSM_SMALL_FWD(15)
+    default: return hipErrorInvalidValue;
+  }
+#undef CSSM_SMALL_FWD
+  return hipGetLastError();
+}
+
+template <class IO>
+static hipError_t small_inv(const float2* spec, long long P, int H, void* y, hipStream_t s) {
+#define CSSM_SMALL_INV(N)                                                                                  \
+  case N:                                                                                                  \
+    hipLaunchKernelGGL((irfft2_small<N, IO>), dim3(unsigned((P + SmallGeom<N, N>::NP - 1) / SmallGeom<N, N>::NP)), \
+                       dim3(SmallGeom<N, N>::NT), 0, s, spec, P, y);                                       \
+    break;
+  switch (H) {
+    CSSM_SMALL_INV(3) CSSM_SMALL_INV(5) CSSM_SMALL_INV(6) CSSM_SMALL_INV(7) CSSM_SMALL_INV(9) CSSM_SMALL_INV(10)
+    CSSM_SMALL_INV(11) CSSM_SMALL_INV(12) CSSM_SMALL_INV(13) CSSM_SMALL_INV(14) CSSM_SMALL_INV(15)
+    default: return hipErrorInvalidValue;
+  }
+#undef CSSM_SMALL_INV
+  return hipGetLastError();
+}
+
+static bool small_plane(int H, int W) { return H == W && H >= 3 && H <= 15 && (H & (H - 1)) != 0; }
+
 int fft_planes_min_group(int H, int W) {
-  return (H == W && H >= 4 && H <= 128 && (H & (H - 1)) == 0) ? 1 : 0;
+  return ((H == W && H >= 4 && H <= 128 && (H & (H - 1)) == 0) || small_plane(H, W)) ? 1 : 0;
 }
 
 hipError_t launch_rfft2(const void* x, int dtype, long long P, int H, int W, float2* spec, float* norms,
                         hipStream_t s) {
   if (H != W) return hipErrorInvalidValue;
+  if (small_plane(H, W))
+    return dtype == 0 ? small_fwd<IoF32>(x, P, H, spec, norms, s) : small_fwd<IoBF16>(x, P, H, spec, norms, s);
   return dtype == 0 ? dispatch_fwd<IoF32>(x, P, H, spec, norms, s) : dispatch_fwd<IoBF16>(x, P, H, spec, norms, s);
 }
 
 hipError_t launch_irfft2(const float2* spec, long long P, int H, int W, void* y, int dtype, hipStream_t s) {
   if (H != W) return hipErrorInvalidValue;
+  if (small_plane(H, W))
+    return dtype == 0 ? small_inv<IoF32>(spec, P, H, y, s) : small_inv<IoBF16>(spec, P, H, y, s);
   return dtype == 0 ? dispatch_inv<IoF32>(spec, P, H, y, s) : dispatch_inv<IoBF16>(spec, P, H, y, s);
 }
 
@@ -1037,76 +1156,89 @@ hipError_t launch_depthwise_conv(const void* x, int dtype, int F, int H, int W, 
 // ---------------------------------------------------------------------------
 constexpr int kMaxShortConv = 8;
 
-template <int KT, class T>
+template <int KT, class T, int PX>
 __global__ void __launch_bounds__(256)
 gdn_qkv_post(T* __restrict__ qkv, int Tn, int C, int HW, GdnShortConv sc, int gate_mode, const void* __restrict__ gates,
              long long total) {
-  // one thread per (b, channel, 4 pixels); HW % 4 == 0 (checked by the launcher)
+  // one thread per (b, channel, PX pixels): PX = 4 (vector loads) when HW % 4 == 0, else 1
   const long long i = (long long)blockIdx.x * blockDim.x + threadIdx.x;
   if (i >= total) return;
-  const int HW4 = HW / 4;
-  const int p = int(i % HW4) * 4;
-  const int c3 = int((i / HW4) % (3 * C));
-  const int b = int(i / (size_t(HW4) * 3 * C));
+  const int HWq = HW / PX;
+  const int p = int(i % HWq) * PX;
+  const int c3 = int((i / HWq) % (3 * C));
+  const int b = int(i / (size_t(HWq) * 3 * C));
   const int blk = c3 / C, c = c3 % C;
   float w[KT > 0 ? KT : 1];
 #pragma unroll
   for (int j = 0; j < KT; ++j) w[j] = sc.w[blk][j * C + c];
   const float bt = KT > 0 ? sc.b[blk][c] : 0.0f;
-  float4 hist[KT > 1 ? KT - 1 : 1];   // x_{t-KT+1} .. x_{t-1}
+  float hist[KT > 1 ? KT - 1 : 1][PX];   // x_{t-KT+1} .. x_{t-1}
 #pragma unroll
-  for (int j = 0; j < (KT > 1 ? KT - 1 : 1); ++j) hist[j] = make_float4(0.f, 0.f, 0.f, 0.f);
+  for (int j = 0; j < (KT > 1 ? KT - 1 : 1); ++j)
+#pragma unroll
+    for (int e = 0; e < PX; ++e) hist[j][e] = 0.0f;
   for (int t = 0; t < Tn; ++t) {
     const size_t fr = size_t(b) * Tn + t;
     const size_t idx = (fr * 3 * C + c3) * HW + p;
-    float4 v = ld4v(qkv, idx);
+    float v[PX];
+    if constexpr (PX == 4) {
+      const float4 q = ld4v(qkv, idx);
+      v[0] = q.x;
+      v[1] = q.y;
+      v[2] = q.z;
+      v[3] = q.w;
+    } else {
+      v[0] = ld_f(qkv, idx);
+    }
     if (KT > 0) {
-      float o[4] = {bt, bt, bt, bt};
-      const float vin[4] = {v.x, v.y, v.z, v.w};
+      float o[PX];
 #pragma unroll
-      for (int e = 0; e < 4; ++e) o[e] = fmaf(w[KT - 1], vin[e], o[e]);
+      for (int e = 0; e < PX; ++e) o[e] = fmaf(w[KT > 0 ? KT - 1 : 0], v[e], bt);
 #pragma unroll
-      for (int j = 0; j < KT - 1; ++j) {
-        const float hv[4] = {hist[j].x, hist[j].y, hist[j].z, hist[j].w};
+      for (int j = 0; j < KT - 1; ++j)
 #pragma unroll
-        for (int e = 0; e < 4; ++e) o[e] = fmaf(w[j], hv[e], o[e]);
-      }
+        for (int e = 0; e < PX; ++e) o[e] = fmaf(w[j], hist[j][e], o[e]);
 #pragma unroll
-      for (int j = 0; j + 1 < KT - 1; ++j) hist[j] = hist[j + 1];
-      if (KT > 1) hist[KT > 1 ? KT - 2 : 0] = v;
+      for (int j = 0; j + 1 < KT - 1; ++j)
 #pragma unroll
-      for (int e = 0; e < 4; ++e) o[e] = o[e] * __builtin_amdgcn_rcpf(1.0f + __expf(-o[e]));
-      v = make_float4(o[0], o[1], o[2], o[3]);
+        for (int e = 0; e < PX; ++e) hist[j][e] = hist[j + 1][e];
+      if (KT > 1)
+#pragma unroll
+        for (int e = 0; e < PX; ++e) hist[KT > 1 ? KT - 2 : 0][e] = v[e];
+#pragma unroll
+      for (int e = 0; e < PX; ++e) v[e] = o[e] * __builtin_amdgcn_rcpf(1.0f + __expf(-o[e]));
     }
     if (blk > 0 && gate_mode != 0) {
-      float4 g;
+      float g[PX];
       if (gate_mode == 1) {
         const float2* gp = static_cast<const float2*>(gates) + fr * HW + p;
-        g = blk == 1 ? make_float4(gp[0].x, gp[1].x, gp[2].x, gp[3].x) : make_float4(gp[0].y, gp[1].y, gp[2].y, gp[3].y);
+#pragma unroll
+        for (int e = 0; e < PX; ++e) g[e] = blk == 1 ? gp[e].x : gp[e].y;
       } else if (gate_mode == 2) {
         const float2 gg = static_cast<const float2*>(gates)[fr];
-        const float gs = blk == 1 ? gg.x : gg.y;
-        g = make_float4(gs, gs, gs, gs);
-      } else {
-        g = *reinterpret_cast<const float4*>(static_cast<const float*>(gates) +
-                                             (fr * 2 * C + size_t(blk - 1) * C + c) * HW + p);
-      }
-      v = make_float4(v.x * g.x, v.y * g.y, v.z * g.z, v.w * g.w);
-    }
-    const float vo[4] = {v.x, v.y, v.z, v.w};
 #pragma unroll
-    for (int e = 0; e < 4; ++e) st_f(qkv, idx + e, vo[e]);
+        for (int e = 0; e < PX; ++e) g[e] = blk == 1 ? gg.x : gg.y;
+      } else {
+        const float* gq = static_cast<const float*>(gates) + (fr * 2 * C + size_t(blk - 1) * C + c) * HW + p;
+#pragma unroll
+        for (int e = 0; e < PX; ++e) g[e] = gq[e];
+      }
+#pragma unroll
+      for (int e = 0; e < PX; ++e) v[e] *= g[e];
+    }
+#pragma unroll
+    for (int e = 0; e < PX; ++e) st_f(qkv, idx + e, v[e]);
   }
 }
 
-template <class T>
+template <class T, int PX>
 static hipError_t run_qkv_post(T* qkv, int B, int Tn, int C, int HW, int kt, const GdnShortConv& sc, int gate_mode,
                                const void* gates, hipStream_t s) {
-  const long long total = (long long)B * 3 * C * (HW / 4);
+  const long long total = (long long)B * 3 * C * (HW / PX);
   const dim3 g(unsigned((total + 255) / 256)), b(256);
   switch (kt) {
 #define CSSM_KT(K) \
-  case K: hipLaunchKernelGGL((gdn_qkv_post<K, T>), g, b, 0, s, qkv, Tn, C, HW, sc, gate_mode, gates, total); break;
+  case K: hipLaunchKernelGGL((gdn_qkv_post<K, T, PX>), g, b, 0, s, qkv, Tn, C, HW, sc, gate_mode, gates, total); break;
     CSSM_KT(0) CSSM_KT(1) CSSM_KT(2) CSSM_KT(3) CSSM_KT(4) CSSM_KT(5) CSSM_KT(6) CSSM_KT(7) CSSM_KT(8)
 #undef CSSM_KT
     default: return hipErrorInvalidValue;
@@ -1116,9 +1248,13 @@ static hipError_t run_qkv_post(T* qkv, int B, int Tn, int C, int HW, int kt, con
 
 hipError_t launch_gdn_qkv_post(void* qkv, int dtype, int B, int T, int C, int HW, int kt, const GdnShortConv& sc,
                                int gate_mode, const void* gates, hipStream_t s) {
-  if (kt > kMaxShortConv || HW % 4) return hipErrorInvalidValue;
-  if (dtype == 0) return run_qkv_post(static_cast<float*>(qkv), B, T, C, HW, kt, sc, gate_mode, gates, s);
-  return run_qkv_post(static_cast<uint16_t*>(qkv), B, T, C, HW, kt, sc, gate_mode, gates, s);
+  if (kt > kMaxShortConv) return hipErrorInvalidValue;
+  const bool v4 = HW % 4 == 0;
+  if (dtype == 0)
+    return v4 ? run_qkv_post<float, 4>(static_cast<float*>(qkv), B, T, C, HW, kt, sc, gate_mode, gates, s)
+              : run_qkv_post<float, 1>(static_cast<float*>(qkv), B, T, C, HW, kt, sc, gate_mode, gates, s);
+  return v4 ? run_qkv_post<uint16_t, 4>(static_cast<uint16_t*>(qkv), B, T, C, HW, kt, sc, gate_mode, gates, s)
+            : run_qkv_post<uint16_t, 1>(static_cast<uint16_t*>(qkv), B, T, C, HW, kt, sc, gate_mode, gates, s);
 }
 
 }  // namespace cssm

@@ -386,7 +386,18 @@ proj_persist_kernel(const TI* __restrict__ A, int M, int K, int N, const float* 
       } else {
         const int kk = f / (TM / 4), r4 = (f % (TM / 4)) * 4;
         const int gm = m0 + r4;
-        if (kk < K && gm < M) {
+        if (NORM && HW % 4 != 0) {
+          // planes of HW % 4 != 0 pixels (7 x 7, 14 x 14): the 4 rows may straddle two frames and
+          // are not 16-byte aligned, so each is read on its own (the norm / gate prologue only;
+          // the plain projections route such planes to the K-chunked kernel)
+          float e[4];
+#pragma unroll
+          for (int q = 0; q < 4; ++q) {
+            const int g = gm + q;
+            e[q] = (kk < K && g < M) ? ld_el(src, (size_t(g / HW) * K + kk) * HW + g % HW) : 0.0f;
+          }
+          v = make_float4(e[0], e[1], e[2], e[3]);
+        } else if (kk < K && gm < M) {
           const int fr = gm / HW, p = gm % HW;
           v = ld4(src, (size_t(fr) * K + kk) * HW + p);
         }
@@ -1432,7 +1443,7 @@ hipError_t launch_proj_out(const void* Y, int in_dtype, int M, int K, int N, con
 hipError_t launch_proj_out_norm_gate(const void* Y, const void* G, int in_dtype, int M, int K, int N, int norm,
                                      const float* nscale, const float* nshift, const float* W, const float* b, int HW,
                                      void* out, int out_dtype, hipStream_t s) {
-  if (!(K <= 128 && K % 4 == 0 && HW % 4 == 0)) return hipErrorInvalidValue;
+  if (!(K <= 128 && K % 4 == 0)) return hipErrorInvalidValue;
   const NormGate ng{G, nscale, nshift, norm};
   if (in_dtype == 0 && out_dtype == 0)
     try_persist<true, false, true, float, float>(Y, M, K, N, W, b, HW, out, nullptr, 0, 0, nullptr, N, ng, s);

@@ -363,8 +363,9 @@ int cssm_gdn_qkv_fused(int T, int H, int W, int K, int kt);
  * optional per-plane sum of |X|^2 over the half spectrum (the spectral L2 norm
  * of cssm.py:4890-4897).  Replaces the rfft2 calls of cssm.py:4880-4888.
  *   x (P, H, W) of dtype; spec (P, H, Wf) complex64 out; norms (P) float32 out or NULL
- * Supported planes: H = W in {4, ..., 128} (powers of two), any P.  x 16-byte
- * (f32) / 8-byte (bf16) aligned, spec 8.
+ * Supported planes: H = W in {4, ..., 128} (powers of two: in-register radix
+ * passes) or in 3..15 (direct DFTs: the 14 x 14 / 7 x 7 CSSM-SHViT stages), any
+ * P.  x 16-byte (f32) / 8-byte (bf16) aligned, spec 8.
  */
 int cssm_rfft2(const void* x, int dtype, long long P, int H, int W, float* spec, float* norms, void* stream);
 
@@ -476,8 +477,8 @@ typedef enum cssm_norm { CSSM_NORM_NONE = 0, CSSM_NORM_RMS = 1, CSSM_NORM_LAYER 
  *   o, gate  (F, K, HW) plane-major of in_dtype (irfft2 output; SiLU'd gate_proj)
  *   norm     cssm_norm; norm_scale (K) [rms_scale or output_layernorm/scale], norm_bias (K) or NULL
  *   kernel (K, N) [output_proj/kernel], bias (N); out (F * HW, N) channels-last of out_dtype
- * K <= 128 and K % 4 == 0, HW % 4 == 0.  o and gate 16-byte aligned (f32) or 8-byte
- * aligned (bf16), a f32 out 16-byte aligned.
+ * K <= 128 and K % 4 == 0; any HW (HW % 4 != 0 reads the planes element-wise).  o and
+ * gate 16-byte aligned (f32) or 8-byte aligned (bf16), a f32 out 16-byte aligned.
  */
 int cssm_gdn_proj_out(const void* o, const void* gate, int in_dtype, int F, int HW, int K, int N, int norm,
                       const float* norm_scale, const float* norm_bias, const float* kernel, const float* bias,

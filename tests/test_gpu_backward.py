@@ -229,6 +229,8 @@ GDN_LAYER_CASES = [
                                                        short_conv_size=0)),
     ("scalar_nol2_32", (1, 2, 32, 32, 4), dict(gate_type="scalar", output_norm="rms", delta_key_dim=2,
                                                use_input_gates=False, use_spectral_l2_norm=False)),
+    ("factored_14x14_small_planes", (2, 3, 14, 14, 8), dict(gate_type="factored", output_norm="rms",
+                                                           delta_key_dim=4, qkv_conv_size=3)),
 ]
 
 

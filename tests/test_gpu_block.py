@@ -104,6 +104,9 @@ BLOCK_CASES = [
     ("gdn_image_global", dict(cssm_type="gdn", delta_key_dim=2, kernel_size=5), (2, 8, 8, 16), 2),
     ("gdn_video_layer", dict(cssm_type="gdn", delta_key_dim=4, kernel_size=3, block_norm="layer"),
      (1, 3, 8, 8, 16), None),
+    # the CSSM-SHViT stage shapes with the gdn cell (cssm_shvit_s1(cssm_type='gdn')): small-plane transforms
+    ("gdn_image_14x14", dict(cssm_type="gdn", delta_key_dim=4, kernel_size=5), (2, 14, 14, 16), 3),
+    ("gdn_image_7x7_T1", dict(cssm_type="gdn", delta_key_dim=2, kernel_size=3), (3, 7, 7, 8), 1),
 ]
 
 

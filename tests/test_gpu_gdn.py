@@ -37,7 +37,13 @@ def _tree(p):
 
 # ------------------------------------------------------- batched transforms
 
-@pytest.mark.parametrize("P,H", [(6, 128), (8, 64), (12, 32), (16, 16), (64, 8), (128, 4)])
+# powers of two 4..128 run the LDS radix passes; the other sizes 3..15 the direct small-plane DFTs
+# (P not a multiple of a group's planes: the last group is partial)
+FFT_SIZES = [(6, 128), (8, 64), (12, 32), (16, 16), (64, 8), (128, 4),
+             (40, 14), (67, 7), (30, 3), (21, 5), (17, 15), (9, 12), (33, 6)]
+
+
+@pytest.mark.parametrize("P,H", FFT_SIZES)
 @pytest.mark.parametrize("dt", ["f32", "bf16"])
 def test_rfft2_and_norms_match_numpy(mods, P, H, dt):
     _, S = mods
@@ -53,7 +59,7 @@ def test_rfft2_and_norms_match_numpy(mods, P, H, dt):
     assert rel_err(to_np(norms), np.sum(np.abs(ref) ** 2, axis=(1, 2))) < 2e-6
 
 
-@pytest.mark.parametrize("P,H", [(6, 128), (8, 64), (12, 32), (16, 16), (64, 8), (128, 4)])
+@pytest.mark.parametrize("P,H", FFT_SIZES)
 def test_irfft2_c2r_rule_matches_numpy(mods, P, H):
     _, S = mods
     print_case(test="irfft2", P=P, H=H)
@@ -394,6 +400,11 @@ LAYER_CASES = [
     ("scalar_no_norm_no_l2", (2, 3, 8, 8, 8),
      dict(delta_key_dim=2, gate_type="scalar", output_norm="none", use_spectral_l2_norm=False,
           no_spectral_clamp=True, position_independent_gates=True)),
+    # CSSM-SHViT stage planes (not powers of two)
+    ("shvit_14_factored_qkvdw", (2, 3, 14, 14, 16),
+     dict(delta_key_dim=4, gate_type="factored", qkv_conv_size=3, kernel_size=5)),
+    ("shvit_7_channel", (3, 2, 7, 7, 8), dict(delta_key_dim=2, gate_type="channel", kernel_size=3)),
+    ("small_12_dense_T1", (2, 1, 12, 12, 8), dict(delta_key_dim=4, gate_type="dense", kernel_size=5)),
 ]
 
 
@@ -538,9 +549,9 @@ def test_gdn_layer_rejects_unsupported(mods):
     with pytest.raises(NotImplementedError):
         cells.GatedDeltaNetCSSM(channels=8, int_attention_mode="spectral")
     cell = cells.GatedDeltaNetCSSM(channels=8, delta_key_dim=2)
-    v = cell.init(0, (1, 2, 12, 12, 8))
+    v = cell.init(0, (1, 2, 20, 20, 8))                   # neither a power of two nor <= 15
     with pytest.raises(NotImplementedError):
-        cell.apply(v, torch.zeros((1, 2, 12, 12, 8), device="cuda"))
+        cell.apply(v, torch.zeros((1, 2, 20, 20, 8), device="cuda"))
 
 
 def test_gdn_layer_is_deterministic(mods):
