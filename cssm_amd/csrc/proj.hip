@@ -1365,8 +1365,14 @@ static void launch_qkv_fused(const void* X, int M, int K, int N, const float* W,
   const int tiles = M / kPersistTM;
   const NormGate ng{nullptr, nullptr, nullptr, 0};
   const int nch = CARRY ? qp.T / TT : 1;
-  // pixel blocks in pairs, each with its nch chunks
-  const dim3 grid(unsigned(persistent_grid((tiles / nch + 1) / 2)), unsigned((N + 127) / 128));
+  // pixel blocks in pairs, each with its nch chunks.  The column blocks (3C = 192: two) of one
+  // sequence of pixel blocks are resident together: the grid is sized so that every workgroup
+  // fits at once, and ids x and x + gridDim.x land on the same XCD, so the second block's A
+  // rows come from L2 (C3: 7.17 -> 6.59 ms against one grid of column block 0 before block 1)
+  const int cb = (N + 127) / 128;
+  const int slots = (2 * cu_count()) / cb > 0 ? (2 * cu_count()) / cb : 1;
+  const int pbs = (tiles / nch + 1) / 2;
+  const dim3 grid(unsigned(pbs < slots ? pbs : slots), unsigned(cb));
   hipLaunchKernelGGL((proj_persist_kernel<64, false, true, 4, TI, TO, false, true, TT, CARRY>), grid, dim3(256), 0, s,
                      static_cast<const TI*>(X), M, K, N, W, b, HW, static_cast<TO*>(out), static_cast<TO*>(out), 0, 0,
                      nullptr, N, ng, qp);

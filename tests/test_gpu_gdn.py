@@ -106,9 +106,12 @@ def test_proj_planes(mods, act):
     assert rel_err(to_np(out), ref) < 1e-5
 
 
-@pytest.mark.parametrize("shape", [(2, 3, 16, 12, 20), (1, 2, 7, 8, 12), (1, 2, 32, 32, 64)])
+@pytest.mark.parametrize("shape", [(2, 3, 16, 12, 20), (1, 2, 7, 8, 12), (1, 2, 32, 32, 64), (1, 2, 14, 8, 16),
+                                   (1, 1, 8, 8, 336)])
 def test_frame_mean_and_depthwise_conv(mods, shape):
-    """Register-blocked (ks 3/5/7, even H, W % 4, C % 4) and general depthwise convs, f32 and bf16 in."""
+    """Register-blocked (ks 3/5/7, even H, W % 4, C % 4: 8 rows per thread when H % 8 == 0, else 2;
+    taps from LDS when C ks^2 <= 8192, as at C = 336 for ks 3 but not 5 / 7) and general depthwise
+    convs, f32 and bf16 in."""
     _, S = mods
     print_case(test="frame_mean_dwconv", shape=shape)
     rng = np.random.default_rng(4)
