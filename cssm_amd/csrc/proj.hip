@@ -254,7 +254,7 @@ struct QkvPost {
 };
 
 template <int KMAX, bool PLANE_A, bool OUT_SPLIT, int WN, class TI, class TO, bool NORM = false, bool SPLIT = false,
-          int TT = 0, bool CARRY = false>
+          int TT = 0, bool CARRY = false, bool PX1 = false>
 __global__ void __launch_bounds__(256, 2)
 proj_persist_kernel(const TI* __restrict__ A, int M, int K, int N, const float* __restrict__ Wt,
                     const float* __restrict__ bias, int HW, TO* __restrict__ out_lo, TO* __restrict__ out_hi,
@@ -266,6 +266,7 @@ proj_persist_kernel(const TI* __restrict__ A, int M, int K, int N, const float* 
   // the sums need whole row tiles per wave
   static_assert(!OUT_SPLIT || WM == 1 || TT == 0, "the qkv epilogue needs whole row tiles per wave");
   static_assert(!NORM || (PLANE_A && !OUT_SPLIT), "the norm / gate prologue is for plane-major A");
+  static_assert(!PX1 || NORM, "element-wise plane rows only for the norm / gate prologue");
   static_assert(!(NORM && SPLIT), "the norm / gate prologue runs on the fp32 path");
   static_assert(!SPLIT || KMAX % 32 == 0, "bf16 MFMA k-blocks of 32");
   constexpr int AP = PLANE_A ? (TM + 16) : (KMAX + 2);   // pitch: rows of A (row-major) or k-rows (plane)
@@ -386,10 +387,11 @@ proj_persist_kernel(const TI* __restrict__ A, int M, int K, int N, const float* 
       } else {
         const int kk = f / (TM / 4), r4 = (f % (TM / 4)) * 4;
         const int gm = m0 + r4;
-        if (NORM && HW % 4 != 0) {
-          // planes of HW % 4 != 0 pixels (7 x 7, 14 x 14): the 4 rows may straddle two frames and
-          // are not 16-byte aligned, so each is read on its own (the norm / gate prologue only;
-          // the plain projections route such planes to the K-chunked kernel)
+        if constexpr (PX1) {
+          // PX1, planes of HW % 4 != 0 pixels (7 x 7, 14 x 14): the 4 rows may straddle two frames
+          // and are not 16-byte aligned, so each is read on its own (the norm / gate prologue
+          // only; the plain projections route such planes to the K-chunked kernel).  A separate
+          // instantiation: a runtime branch here slowed the HW % 4 == 0 kernel's loads by 1.6x
           float e[4];
 #pragma unroll
           for (int q = 0; q < 4; ++q) {
@@ -397,9 +399,11 @@ proj_persist_kernel(const TI* __restrict__ A, int M, int K, int N, const float* 
             e[q] = (kk < K && g < M) ? ld_el(src, (size_t(g / HW) * K + kk) * HW + g % HW) : 0.0f;
           }
           v = make_float4(e[0], e[1], e[2], e[3]);
-        } else if (kk < K && gm < M) {
-          const int fr = gm / HW, p = gm % HW;
-          v = ld4(src, (size_t(fr) * K + kk) * HW + p);
+        } else {
+          if (kk < K && gm < M) {
+            const int fr = gm / HW, p = gm % HW;
+            v = ld4(src, (size_t(fr) * K + kk) * HW + p);
+          }
         }
       }
       pf[i] = v;
@@ -1275,7 +1279,7 @@ static void launch_in(const void* X, int M, int K, int N, const float* W, const 
 }
 
 // bf16x3 MFMA for every persistent projection except the norm / gate prologue (fp32)
-template <int KMAX, bool PLANE_A, bool OUT_SPLIT, bool NORM, class TI, class TO, bool SPLIT = !NORM>
+template <int KMAX, bool PLANE_A, bool OUT_SPLIT, bool NORM, class TI, class TO, bool PX1 = false, bool SPLIT = !NORM>
 static void launch_persist(const void* A, int M, int K, int N, const float* W, const float* b, int HW, void* lo,
                            void* hi, int act_lo, int act_hi, float* partial, int NH, const NormGate& ng,
                            hipStream_t s) {
@@ -1285,29 +1289,29 @@ static void launch_persist(const void* A, int M, int K, int N, const float* W, c
   {
     if (N <= 64 && (!OUT_SPLIT || partial == nullptr)) {
       const dim3 grid(unsigned(persistent_grid(tiles)), unsigned((N + 63) / 64));
-      hipLaunchKernelGGL((proj_persist_kernel<KMAX, PLANE_A, OUT_SPLIT, 2, TI, TO, NORM, SPLIT>), grid, dim3(256), 0, s,
+      hipLaunchKernelGGL((proj_persist_kernel<KMAX, PLANE_A, OUT_SPLIT, 2, TI, TO, NORM, SPLIT, 0, false, PX1>), grid, dim3(256), 0, s,
                          static_cast<const TI*>(A), M, K, N, W, b, HW, static_cast<TO*>(lo), static_cast<TO*>(hi),
                          act_lo, act_hi, partial, NH, ng, QkvPost{});
       return;
     }
   }
   const dim3 grid(unsigned(persistent_grid(tiles)), unsigned((N + 127) / 128));
-  hipLaunchKernelGGL((proj_persist_kernel<KMAX, PLANE_A, OUT_SPLIT, 4, TI, TO, NORM, SPLIT>), grid, dim3(256), 0, s,
+  hipLaunchKernelGGL((proj_persist_kernel<KMAX, PLANE_A, OUT_SPLIT, 4, TI, TO, NORM, SPLIT, 0, false, PX1>), grid, dim3(256), 0, s,
                      static_cast<const TI*>(A), M, K, N, W, b, HW, static_cast<TO*>(lo), static_cast<TO*>(hi),
                      act_lo, act_hi, partial, NH, ng, QkvPost{});
 }
 
-template <bool PLANE_A, bool OUT_SPLIT, bool NORM, class TI, class TO>
+template <bool PLANE_A, bool OUT_SPLIT, bool NORM, class TI, class TO, bool PX1 = false>
 static bool try_persist(const void* A, int M, int K, int N, const float* W, const float* b, int HW, void* lo,
                         void* hi, int act_lo, int act_hi, float* partial, int NH, const NormGate& ng, hipStream_t s) {
   if (K % 4 != 0 || K > 128) return false;
   if (K <= 64) {
-    launch_persist<64, PLANE_A, OUT_SPLIT, NORM, TI, TO>(A, M, K, N, W, b, HW, lo, hi, act_lo, act_hi, partial, NH, ng, s);
+    launch_persist<64, PLANE_A, OUT_SPLIT, NORM, TI, TO, PX1>(A, M, K, N, W, b, HW, lo, hi, act_lo, act_hi, partial, NH, ng, s);
     return true;
   }
   // 64 < K <= 128 only for the norm / gate prologue (the other projections take the K-chunked kernel there)
   if constexpr (NORM) {
-    launch_persist<128, PLANE_A, OUT_SPLIT, NORM, TI, TO>(A, M, K, N, W, b, HW, lo, hi, act_lo, act_hi, partial, NH, ng, s);
+    launch_persist<128, PLANE_A, OUT_SPLIT, NORM, TI, TO, PX1>(A, M, K, N, W, b, HW, lo, hi, act_lo, act_hi, partial, NH, ng, s);
     return true;
   }
   return false;
@@ -1451,14 +1455,26 @@ hipError_t launch_proj_out_norm_gate(const void* Y, const void* G, int in_dtype,
                                      void* out, int out_dtype, hipStream_t s) {
   if (!(K <= 128 && K % 4 == 0)) return hipErrorInvalidValue;
   const NormGate ng{G, nscale, nshift, norm};
-  if (in_dtype == 0 && out_dtype == 0)
-    try_persist<true, false, true, float, float>(Y, M, K, N, W, b, HW, out, nullptr, 0, 0, nullptr, N, ng, s);
-  else if (in_dtype == 0)
-    try_persist<true, false, true, float, uint16_t>(Y, M, K, N, W, b, HW, out, nullptr, 0, 0, nullptr, N, ng, s);
-  else if (out_dtype == 0)
-    try_persist<true, false, true, uint16_t, float>(Y, M, K, N, W, b, HW, out, nullptr, 0, 0, nullptr, N, ng, s);
-  else
-    try_persist<true, false, true, uint16_t, uint16_t>(Y, M, K, N, W, b, HW, out, nullptr, 0, 0, nullptr, N, ng, s);
+  if (HW % 4 == 0) {
+    if (in_dtype == 0 && out_dtype == 0)
+      try_persist<true, false, true, float, float>(Y, M, K, N, W, b, HW, out, nullptr, 0, 0, nullptr, N, ng, s);
+    else if (in_dtype == 0)
+      try_persist<true, false, true, float, uint16_t>(Y, M, K, N, W, b, HW, out, nullptr, 0, 0, nullptr, N, ng, s);
+    else if (out_dtype == 0)
+      try_persist<true, false, true, uint16_t, float>(Y, M, K, N, W, b, HW, out, nullptr, 0, 0, nullptr, N, ng, s);
+    else
+      try_persist<true, false, true, uint16_t, uint16_t>(Y, M, K, N, W, b, HW, out, nullptr, 0, 0, nullptr, N, ng, s);
+  } else {
+    if (in_dtype == 0 && out_dtype == 0)
+      try_persist<true, false, true, float, float, true>(Y, M, K, N, W, b, HW, out, nullptr, 0, 0, nullptr, N, ng, s);
+    else if (in_dtype == 0)
+      try_persist<true, false, true, float, uint16_t, true>(Y, M, K, N, W, b, HW, out, nullptr, 0, 0, nullptr, N, ng, s);
+    else if (out_dtype == 0)
+      try_persist<true, false, true, uint16_t, float, true>(Y, M, K, N, W, b, HW, out, nullptr, 0, 0, nullptr, N, ng, s);
+    else
+      try_persist<true, false, true, uint16_t, uint16_t, true>(Y, M, K, N, W, b, HW, out, nullptr, 0, 0, nullptr, N, ng,
+                                                               s);
+  }
   return hipGetLastError();
 }
 
