@@ -300,6 +300,23 @@ __device__ __forceinline__ void wave_sync() {
   __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
 }
 
+// Sum of x over the 64 lanes of the wave, the same value in every lane, with no
+// LDS round trip: quad swaps (lane ^ 1, lane ^ 2) and the half-row / row
+// mirrors of DPP (sums of 4, 8, 16 lanes), then the four row sums read out of
+// lanes 0, 16, 32, 48.  The order of the additions is fixed.
+template <int CTRL>
+__device__ __forceinline__ float dpp_f(float v) {
+  return __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(v), CTRL, 0xf, 0xf, false));
+}
+__device__ __forceinline__ float wave_sum(float x) {
+  x += dpp_f<0xb1>(x);    // quad_perm [1, 0, 3, 2]
+  x += dpp_f<0x4e>(x);    // quad_perm [2, 3, 0, 1]
+  x += dpp_f<0x141>(x);   // row_half_mirror
+  x += dpp_f<0x140>(x);   // row_mirror
+  auto rl = [](float v, int l) { return __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), l)); };
+  return (rl(x, 0) + rl(x, 16)) + (rl(x, 32) + rl(x, 48));
+}
+
 // ---------------------------------------------------------------------------
 // The passes of the 2-D real FFT of NP planes held in LDS, in the order a
 // round trip runs them:

@@ -700,12 +700,12 @@ __global__ void __launch_bounds__(256, 2) gdn_core_fused32(const GdnFusedArgs a)
           acc[p] = fmaf(x.x, x.x, fmaf(x.y, x.y, acc[p]));
         }
       }
+      // wave sums by DPP and lane reads (a shuffle tree through LDS made this phase ~18 % of a step)
 #pragma unroll
       for (int p = 0; p < 2 * DK; ++p) {
-        float x = acc[p];
-#pragma unroll
-        for (int d = 32; d >= 1; d >>= 1) x += __shfl_xor(x, d, 64);
+        const float x = wave_sum(acc[p]);
         if (lane == 0) red[w * 2 * DK + p] = x;
+        __builtin_amdgcn_sched_barrier(0);
       }
       __syncthreads();
 #pragma unroll
