@@ -130,6 +130,15 @@ int cssm_gated_scan_col_order(int H, int W, int* cols) {
   return CSSM_OK;
 }
 
+int cssm_gated_scan_khat_order(int H, int W, int* idx) {
+  if (!idx) return fail(CSSM_ERR_NULL, "cssm_gated_scan_khat_order: idx must be non-null");
+  if (H <= 0 || W <= 0) return fail(CSSM_ERR_SHAPE, "cssm_gated_scan_khat_order: H=%d W=%d", H, W);
+  const int WF = W / 2 + 1;
+  for (int u = 0; u < H; ++u)
+    for (int p = 0; p < WF; ++p) idx[cssm::khat_pos(H, W, u, p)] = u * WF + cssm::scan_col(H, W, p);
+  return CSSM_OK;
+}
+
 int cssm_gated_scan_fwd(const void* u, const void* z, void* y, int dtype, int B, int T, int C, int H, int W,
                         const float* gates, const float* khat, int u_act, int z_act, void* stream) {
   if (!u || !z || !y || !gates || !khat)

@@ -32,11 +32,11 @@ struct GatedBwdArgs {
   const float2* uspec;    // (B, T, C, H, WF) rfft2(u), natural column order
   const float2* dspec;    // (B, T, C, H, WF) rfft2(dy), natural order (dy = dL/dy_pre, y_pre = y / z)
   const float4* gates;    // (B, T, H, WF) (E, DB, VF2, GCs), scan column order
-  const float2* khat;     // (C, H, WF) floored K_hat, scan column order
+  const float2* khat;     // (C, H, WF) floored K_hat, scan layout (khat_pos)
   float2* yspec;          // (B, T, C, H, WF) out: Y_t = C h_t (irfft2 -> y_pre), natural order
   float2* sdu;            // (B, T, C, H, WF) out: dU_t H W / c_v (irfft2 -> du), natural order
   float4* dgates;         // (B, T, H, WF) out: (dE, dDB, dVF2, dGCs) summed over channels, scan order
-  float2* dkhat;          // (B, C, H, WF) out: sum over t of E_t dA_t per batch element, scan order
+  float2* dkhat;          // (B, C, H, WF) out: sum over t of E_t dA_t per batch element, khat's layout
   int T, C, H, W;
   float c_scale;          // the GCs = C c_scale of the gate planes
 };
@@ -49,6 +49,7 @@ __global__ void __launch_bounds__(256) gated_scan_bwd_bins(const GatedBwdArgs a)
   const int b = blockIdx.y, T = a.T, C = a.C;
   const int u = i / WF, p = i % WF, v = scan_col(H, W, p);
   const int nat = u * WF + v;                       // spectra: natural column order
+  const int kpos = khat_pos(H, W, u, p);            // K_hat and its gradient: the scan's slot
   const float cv = (v == 0 || 2 * v == W) ? 1.0f : 2.0f;
   const float dscale = cv / float(H * W), uscale = float(H * W) / cv, inv_cs = 1.0f / a.c_scale;
 
@@ -59,7 +60,7 @@ __global__ void __launch_bounds__(256) gated_scan_bwd_bins(const GatedBwdArgs a)
     gs[t] = make_float4(0.f, 0.f, 0.f, 0.f);
   }
   for (int c = 0; c < C; ++c) {
-    const float2 kf = a.khat[size_t(c) * HWF + i];
+    const float2 kf = a.khat[size_t(c) * HWF + kpos];
     float2 h[MAXT], U[MAXT];
     float2 hp = make_float2(0.f, 0.f);
 #pragma unroll
@@ -102,7 +103,7 @@ __global__ void __launch_bounds__(256) gated_scan_bwd_bins(const GatedBwdArgs a)
       const float2 A = cscale(kf, g[tt].x);
       carry = cmulc(gt, A);                              // conj(A_t) g_t
     }
-    a.dkhat[(size_t(b) * C + c) * HWF + i] = dkf;
+    a.dkhat[(size_t(b) * C + c) * HWF + kpos] = dkf;
   }
 #pragma unroll
   for (int t = 0; t < MAXT; ++t)

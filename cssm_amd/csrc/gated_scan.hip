@@ -52,7 +52,7 @@ struct ScanArgs {
   const void* z;
   void* y;
   const float4* gates;   // (B, T, H, WF) per-bin (E, DB, VF, GC), columns in scan_col order
-  const float2* khat;    // (C, H, WF), GOOM-floored, columns in scan_col order
+  const float2* khat;    // (C, H, WF), GOOM-floored, scan layout (columns in scan_col order, slots khat_pos)
   int T, C, u_act, z_act;
 };
 
@@ -76,24 +76,44 @@ struct GatedScanOp {
   Buf kbuf;   // K_hat of the group's planes: (NP, H, WF) float2
   float4 pg[QB];   // the unit's first gate batch, in flight during its column DFT
   float2 pk[QB];
+  // 128 x 128: K_hat's rows u and u + 16 share slot pairs (khat_pos), so bins q, q + 1 of a unit
+  // (rows k + 16 q, k + 16 (q + 1), q even) come in one 16-byte load over whole cache lines
+  static constexpr bool KPAIR = G::H == 128 && G::W == 128;
+  static_assert(!KPAIR || (QB % 2 == 0 && H1 == 16), "paired K_hat rows need even batches of rows 16 apart");
+
+  // K_hat of bins q0 .. q0 + QB - 1 of unit k at column position n of plane pl
+  __device__ __forceinline__ void khat_batch(int pl, int k, int n, int q0, float2 (&kq)[QB]) const {
+    if constexpr (KPAIR) {
+      const unsigned kp = unsigned(pl * H * WF * 8) + unsigned(k * WF + n) * 16u;
+#pragma unroll
+      for (int p = 0; p < QB / 2; ++p) {
+        const float4 v = kbuf.ld4(kp, (q0 / 2 + p) * H1 * WF * 16);
+        kq[2 * p] = make_float2(v.x, v.y);
+        kq[2 * p + 1] = make_float2(v.z, v.w);
+      }
+    } else {
+      const unsigned ki = unsigned(pl * H * WF) + unsigned(k * WF + n);
+#pragma unroll
+      for (int q = 0; q < QB; ++q) kq[q] = kbuf.ld2(ki * 8u, (q0 + q) * H1 * WF * 8);
+    }
+  }
 
   __device__ __forceinline__ void prefetch(int pl, int k, int n) {
-    const unsigned gi = unsigned(k * WF + n), ki = unsigned(pl * H * WF) + gi;
+    const unsigned gi = unsigned(k * WF + n);
 #pragma unroll
-    for (int q = 0; q < QB; ++q) {
-      pg[q] = gbuf.ld4(gi * 16u, q * H1 * WF * 16);
-      pk[q] = kbuf.ld2(ki * 8u, q * H1 * WF * 8);
-    }
+    for (int q = 0; q < QB; ++q) pg[q] = gbuf.ld4(gi * 16u, q * H1 * WF * 16);
+    khat_batch(pl, k, n, 0, pk);
   }
 
   // gates of (b, t) and the spectral kernel of this plane at bins (k + H1 q,
   // column at position n)
   __device__ __forceinline__ void bins(int j, int a2, int pl, int k, int n, float2 (&sp)[G::H2]) const {
-    const unsigned gi = unsigned(k * WF + n), ki = unsigned(pl * H * WF) + gi;
+    const unsigned gi = unsigned(k * WF + n);
 #pragma unroll
     for (int q0 = 0; q0 < H2; q0 += QB) {
       float4 gq[QB];
       float2 kq[QB];
+      if (q0 != 0) khat_batch(pl, k, n, q0, kq);
 #pragma unroll
       for (int q = 0; q < QB; ++q) {
         if (q0 == 0) {
@@ -101,7 +121,6 @@ struct GatedScanOp {
           kq[q] = pk[q];
         } else {
           gq[q] = gbuf.ld4(gi * 16u, (q0 + q) * H1 * WF * 16);
-          kq[q] = kbuf.ld2(ki * 8u, (q0 + q) * H1 * WF * 8);
         }
       }
 #pragma unroll
@@ -112,11 +131,13 @@ struct GatedScanOp {
   __device__ __forceinline__ void edge(int j, int pl, int uA, int uB, int, float2 (&v4)[4]) const {
     const unsigned kp = unsigned(pl * H * WF);
     const unsigned bi[4] = {unsigned(uA * WF), unsigned(uA * WF + WH), unsigned(uB * WF), unsigned(uB * WF + WH)};
+    const unsigned ks[4] = {unsigned(khat_pos(H, G::W, uA, 0)), unsigned(khat_pos(H, G::W, uA, WH)),
+                            unsigned(khat_pos(H, G::W, uB, 0)), unsigned(khat_pos(H, G::W, uB, WH))};
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
       float2& hs = hE[(pl * G::HP + uA) * 4 + i];
       float2 hv = hs;
-      v4[i] = scan_bin(hv, v4[i], gbuf.ld4(bi[i] * 16u), kbuf.ld2((kp + bi[i]) * 8u));
+      v4[i] = scan_bin(hv, v4[i], gbuf.ld4(bi[i] * 16u), kbuf.ld2((kp + ks[i]) * 8u));
       hs = hv;
     }
   }

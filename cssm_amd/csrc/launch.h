@@ -20,6 +20,18 @@ __host__ __device__ inline int scan_col(int H, int W, int p) {
   return 4 * (g % 4) + qc % 4 + 16 * (2 * (g / 4) + qc / 4);
 }
 
+// Slot (in float2 units, within one channel's H x (W/2+1) plane) of K_hat's
+// bin at row u, column position p of the scan layout.  At 128 x 128 the rows u
+// and u + 16 with (u / 16) even share each column's 16-byte slot pairs, so a
+// column-pass lane, whose bins are rows k + 16 q, reads the bins of q and q + 1
+// with one 16-byte load over whole cache lines; every other plane size keeps
+// row-major order (u (W/2+1) + p).
+__host__ __device__ inline int khat_pos(int H, int W, int u, int p) {
+  const int WF = W / 2 + 1;
+  if (H != 128 || W != 128) return u * WF + p;
+  return ((u % 16 + 16 * (u / 32)) * WF + p) * 2 + (u / 16) % 2;
+}
+
 struct GateWeights {
   const float* kd[3];
   const float* bd[3];

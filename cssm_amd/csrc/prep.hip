@@ -54,7 +54,8 @@ __global__ void spectral_kernel_prep(const float* __restrict__ k, int K, int H, 
   }
   __syncthreads();
   // stage 2: F[u][v] = sum_i R[i][v] e^{-2 pi i u (i') / H}, at position
-  // (u, p) of the output with v = scan_col(p) in the scan's column order
+  // (u, p) of the output with v = scan_col(p) in the scan's column order, in
+  // the scan's slot khat_pos(u, p)
   for (int idx = threadIdx.x; idx < H * WF; idx += blockDim.x) {
     const int u = idx / WF, v = scan_order ? scan_col(H, W, idx % WF) : idx % WF;
     double re = 0.0, im = 0.0;
@@ -79,7 +80,7 @@ __global__ void spectral_kernel_prep(const float* __restrict__ k, int K, int H, 
       const float m2 = o.x * o.x + o.y * o.y;
       if (m2 < 1e-14f) o = make_float2(1e-7f, 0.0f);
     }
-    out[size_t(c) * H * WF + idx] = o;
+    out[size_t(c) * H * WF + (scan_order ? khat_pos(H, W, u, idx % WF) : idx)] = o;
   }
 }
 

@@ -34,8 +34,9 @@ def spectral_kernel(k: torch.Tensor, H: int, W: int, rho: float = 0.999, squash:
                     goom_floor: bool = True, scan_order: bool = False) -> torch.Tensor:
     """K_hat (C, H, W//2+1) complex64 from k (C, K, K) (cssm.py:505-529, 4711-4716).
 
-    ``scan_order`` stores the columns in :func:`scan_col_order` (what
-    :func:`gated_scan` reads); otherwise in natural order.
+    ``scan_order`` stores the bins in the scan layout :func:`gated_scan` reads (the
+    slots of :func:`scan_khat_order`: columns in :func:`scan_col_order`, at 128 x 128
+    also rows paired); otherwise in natural order.
     """
     _dev(k, "k", torch.float32)
     C, K, K2 = k.shape
@@ -54,6 +55,17 @@ def scan_col_order(H: int, W: int) -> List[int]:
     cols = (ctypes.c_int * (W // 2 + 1))()
     _lib.call("cssm_gated_scan_col_order", H, W, cols)
     return list(cols)
+
+
+def scan_khat_order(H: int, W: int) -> List[int]:
+    """Slots of K_hat in the scan layout (:func:`spectral_kernel` with ``scan_order``):
+    entry s is the natural index u (W//2+1) + v of the bin stored in complex slot s of
+    a channel's plane, so ``natural.view(C, -1)[:, order]`` is the scan layout.  Columns
+    follow :func:`scan_col_order`; rows are row-major except at 128 x 128, where rows u
+    and u + 16 alternate within each column's slot pairs."""
+    idx = (ctypes.c_int * (H * (W // 2 + 1)))()
+    _lib.call("cssm_gated_scan_khat_order", H, W, idx)
+    return list(idx)
 
 
 def scan_c_scale(H: int, W: int) -> float:

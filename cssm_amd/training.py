@@ -121,6 +121,10 @@ def _col_index(H: int, W: int, device) -> torch.Tensor:
     return torch.tensor(S.scan_col_order(H, W), dtype=torch.long, device=device)
 
 
+def _khat_index(H: int, W: int, device) -> torch.Tensor:
+    return torch.tensor(S.scan_khat_order(H, W), dtype=torch.long, device=device)
+
+
 def gate_planes(ctx: torch.Tensor, p: Dict[str, Any], H: int, W: int, gate_type: str, activation: str,
                 c_scale: float) -> torch.Tensor:
     """The per-bin planes cssm_gated_gates writes, differentiably: (B, T, H, Wf, 4) =
@@ -150,7 +154,7 @@ def gate_planes(ctx: torch.Tensor, p: Dict[str, Any], H: int, W: int, gate_type:
 def khat_planes(k: torch.Tensor, H: int, W: int, rho: float) -> torch.Tensor:
     """The floored K_hat cssm_spectral_kernel(goom_floor=1, scan_order=1) writes, differentiably:
     rho F / (1 + |F|) with F = rfft2(pad / crop of k) (cssm.py:505-529), |K| < 1e-7 -> 1e-7 + 0j,
-    columns in scan order."""
+    in the scan layout (:func:`cssm_amd.spectral.scan_khat_order`)."""
     K = k.shape[-1]
     if K > H or K > W:
         sh, sw = (K - H) // 2, (K - W) // 2
@@ -161,7 +165,8 @@ def khat_planes(k: torch.Tensor, H: int, W: int, rho: float) -> torch.Tensor:
     F = torch.fft.rfft2(kp)
     kh = F * rho / (1.0 + F.abs())
     kh = torch.where(kh.abs() < 1e-7, torch.full_like(kh, 1e-7), kh)
-    return kh.index_select(2, _col_index(H, W, k.device)).contiguous()
+    C = kh.shape[0]
+    return kh.reshape(C, -1).index_select(1, _khat_index(H, W, k.device)).view(C, H, W // 2 + 1)
 
 
 def _causal_t(x5, p):

@@ -91,8 +91,10 @@ const char* cssm_last_error(void);
  *   squash      1 = apply rho/(1+|F|) (0 = GDN no_spectral_clamp, cssm.py:4715)
  *   goom_floor  1 = replace |K_hat| < 1e-7 by 1e-7+0j (to_goom floor, goom.py:161-174),
  *               which is what the scan consumes.
- *   scan_order  1 = columns in the order of cssm_gated_scan_col_order (what
- *               cssm_gated_scan_fwd reads), 0 = natural order.
+ *   scan_order  1 = the scan layout cssm_gated_scan_fwd reads: columns in the
+ *               order of cssm_gated_scan_col_order, each channel's bins in the
+ *               slots of cssm_gated_scan_khat_order (row-major except at
+ *               128 x 128); 0 = natural (C, H, Wf) order.
  * Pad rule: K <= H, W zero-pads with (H-K)//2 before; K >= H and K >= W
  * centre-crops from (K-H)//2.  K between H and W is rejected (the reference
  * produces mismatched shapes there).
@@ -164,12 +166,12 @@ int cssm_gated_scan_fwd(const void* u, const void* z, void* y, int dtype, int B,
  *   gradient at irfft2's output), and afterwards y_pre = cssm_irfft2(yspec)
  *   (so dL/dz = dL/dy * y_pre) and dL/du = cssm_irfft2(sdu).
  *   uspec, dspec     (B, T, C, H, Wf) complex64, natural column order
- *   gates, khat      exactly as cssm_gated_scan_fwd read them (scan column order)
+ *   gates, khat      exactly as cssm_gated_scan_fwd read them (scan layout)
  *   c_scale          the c_scale the gate planes were made with (1 / (2 H W))
  *   yspec  (B, T, C, H, Wf) out: C h_t                  (natural order)
  *   sdu    (B, T, C, H, Wf) out: dL/dU_t H W / c_v      (natural order; c_v = 2 inside 0 < v < W/2)
  *   dgates (B, T, H, Wf, 4) out: dL/d(gate planes), summed over channels (scan order)
- *   dkhat  (B, C, H, Wf)    out: dL/dkhat per batch element (sum over B; scan order)
+ *   dkhat  (B, C, H, Wf)    out: dL/dkhat per batch element (sum over B; khat's scan layout)
  * T <= 32; W even.
  */
 int cssm_gated_scan_bwd(const float* uspec, const float* dspec, const float* gates, const float* khat, int B, int T,
@@ -499,6 +501,18 @@ int cssm_gated_scan_min_group(int H, int W);
  * last.  No counterpart in the reference (the layout is this library's own).
  */
 int cssm_gated_scan_col_order(int H, int W, int* cols);
+
+/*
+ * Slots of K_hat in the scan layout cssm_spectral_kernel(scan_order = 1) writes
+ * and cssm_gated_scan_fwd / _bwd read: idx[s] (s < H (W/2 + 1)) = the natural
+ * index u (W/2 + 1) + v of the bin stored in complex slot s of a channel's
+ * plane.  Columns follow cssm_gated_scan_col_order; rows are row-major except at
+ * 128 x 128, where rows u and u + 16 ((u / 16) even) alternate within each
+ * column's slot pairs, so a column-pass lane loads two of its bins (rows k + 16 q
+ * and k + 16 (q + 1)) with one 16-byte load over whole cache lines.  No
+ * counterpart in the reference (the layout is this library's own).
+ */
+int cssm_gated_scan_khat_order(int H, int W, int* idx);
 
 /*
  * CSSMSHViTBlock wiring around the cell, the token-mixer half of the block

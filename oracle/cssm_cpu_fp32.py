@@ -49,15 +49,22 @@ def _floor(z):
     return torch.where(small, torch.full_like(z, 1e-7), z)
 
 
-def scan_core(u, z, gates, khat, c_scale, cols):
+def scan_core(u, z, gates, khat, c_scale, cols, korder=None):
     """The contract of the fused scan kernel (cssm_gated_scan_fwd with identity load
     activations): u, z (B, T, C, H, W); gates (B, T, H, Wf, 4) = [exp(-Delta),
-    (Delta + 1e-8) B, 2 VF, C c_scale] and floored khat (C, H, Wf), both with column p
-    holding frequency column cols[p].  Returns irfft2(C h_t) * z with
+    (Delta + 1e-8) B, 2 VF, C c_scale] with column p holding frequency column cols[p];
+    floored khat (C, H, Wf) in the scan layout: complex slot s of a channel's plane holds
+    natural bin korder[s] (cssm_gated_scan_khat_order; korder None: columns permuted by
+    cols, rows in order).  Returns irfft2(C h_t) * z with
     h_t = khat e^{-Delta_t} h_{t-1} + (V_t := (Delta + 1e-8) B U_t, or VF where |U_t B| < 1e-7)."""
     inv = torch.argsort(torch.as_tensor(cols))
     g = gates.index_select(3, inv)
-    kh = khat.index_select(2, inv)
+    if korder is None:
+        kh = khat.index_select(2, inv)
+    else:
+        Cc, Hh, Wfh = khat.shape
+        kinv = torch.argsort(torch.as_tensor(korder))
+        kh = khat.reshape(Cc, -1).index_select(1, kinv).view(Cc, Hh, Wfh)
     B, T, C, H, W = u.shape
     U = torch.fft.rfft2(u)
     h = torch.zeros_like(U[:, 0])

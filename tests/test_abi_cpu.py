@@ -56,6 +56,27 @@ def test_abi_version_and_errors_without_gpu():
 
 
 @pytest.mark.parametrize("H", [4, 8, 14, 32, 64, 128])
+def test_scan_khat_order(H):
+    """K_hat's slots in the scan layout (host-side, no GPU): a permutation of the H (W/2 + 1)
+    bins whose columns follow scan_col_order; row-major except at 128 x 128, where slot
+    pair (2 s, 2 s + 1) holds rows u and u + 16 of one column for u in the even blocks of
+    16 rows -- the two bins a column-pass lane takes with one 16-byte load."""
+    from cssm_amd import spectral
+    Wf = H // 2 + 1
+    order = spectral.scan_khat_order(H, H)
+    cols = spectral.scan_col_order(H, H)
+    assert sorted(order) == list(range(H * Wf))
+    if H != 128:
+        assert order == [u * Wf + cols[p] for u in range(H) for p in range(Wf)]
+        return
+    for s in range(0, H * Wf, 2):
+        (ua, va), (ub, vb) = divmod(order[s], Wf), divmod(order[s + 1], Wf)
+        assert va == vb and ub == ua + 16 and (ua // 16) % 2 == 0
+        pr, p = divmod(s // 2, Wf)
+        assert va == cols[p] and ua == pr % 16 + 32 * (pr // 16)
+
+
+@pytest.mark.parametrize("H", [4, 8, 14, 32, 64, 128])
 def test_scan_col_order(H):
     """The per-bin planes' column order (host-side, no GPU): a permutation of the
     W/2 + 1 columns that keeps DC and Nyquist in place; at 128 x 128 each group of

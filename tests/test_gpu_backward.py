@@ -48,10 +48,12 @@ def test_scan_vjp_matches_float64_reference(mods, shape):
     delta = O.softplus(rng.standard_normal((B, T, H, Wf)))
     gB, gC = rng.standard_normal((B, T, H, Wf)), rng.standard_normal((B, T, H, Wf))
     gates = np.stack([np.exp(-delta), (delta + 1e-8) * gB, 2e-7 * (delta + 1e-8), gC * cs], -1)[:, :, :, cols]
-    kh = O.goom_floor(0.95 * rng.random((C, H, Wf)) * np.exp(2j * np.pi * rng.random((C, H, Wf))))[:, :, cols]
+    korder = np.array(S.scan_khat_order(H, W))
+    kh = O.goom_floor(0.95 * rng.random((C, H, Wf)) * np.exp(2j * np.pi * rng.random((C, H, Wf))))
+    kh = kh.reshape(C, -1)[:, korder].reshape(C, H, Wf)                       # the scan layout
     dy = rng.standard_normal(shape)
     ts = [torch.from_numpy(a).requires_grad_(True) for a in (u, z, gates, kh)]
-    ref_y = P.scan_core(*ts, cs, cols)
+    ref_y = P.scan_core(*ts, cs, cols, korder)
     refs = torch.autograd.grad(ref_y, ts, torch.from_numpy(dy))
     dev = [torch.from_numpy(np.ascontiguousarray(a)).to("cuda", torch.float32 if a.dtype != np.complex128
                                                          else torch.complex64) for a in (u, z, gates, kh, dy)]

@@ -53,9 +53,15 @@ def _pack_gates(delta, gB, gC, H, W):
     return _dev(g[:, :, :, _scan_cols(H, W), :])
 
 
+def _scan_korder(H, W):
+    from cssm_amd import spectral
+    return np.asarray(spectral.scan_khat_order(H, W))
+
+
 def _scan_khat(khat, H, W):
-    """Floored K_hat (C, H, Wf) in the scan's column order."""
-    return _dev(khat[:, :, _scan_cols(H, W)], torch.complex64)
+    """Floored K_hat (C, H, Wf) in the scan layout (slot s holds natural bin korder[s])."""
+    C = khat.shape[0]
+    return _dev(khat.reshape(C, -1)[:, _scan_korder(H, W)].reshape(khat.shape), torch.complex64)
 
 
 # ------------------------------------------------------------- spectral kernel
@@ -84,12 +90,17 @@ def test_spectral_kernel_goom_floor(S):
 
 @pytest.mark.parametrize("H", [128, 32])
 def test_spectral_kernel_scan_order(S, H):
-    """scan_order = 1 stores the same values with the columns in the scan's order."""
+    """scan_order = 1 stores the same values in the scan layout: columns in the scan's
+    order, and at 128 x 128 rows u and u + 16 paired within each column's slots."""
     print_case(test="spectral_kernel_scan_order", H=H)
     k = np.random.default_rng(8).standard_normal((3, 11, 11)) * 0.3
     nat = S.spectral_kernel(_dev(k), H, H, goom_floor=True)
     so = S.spectral_kernel(_dev(k), H, H, goom_floor=True, scan_order=True)
-    assert torch.equal(so, nat[:, :, torch.as_tensor(_scan_cols(H, H), device="cuda")])
+    ko = torch.as_tensor(_scan_korder(H, H), device="cuda")
+    assert torch.equal(so.reshape(3, -1), nat.reshape(3, -1)[:, ko])
+    if H == 128:
+        # slot pair (2 s, 2 s + 1) of column position p holds rows u, u + 16 of one column
+        assert torch.equal(so.reshape(3, -1)[:, 1], nat[:, 16, int(_scan_cols(H, H)[0])])
 
 
 # ------------------------------------------------------------------ plane mean
