@@ -10,7 +10,7 @@ import os
 import threading
 
 LIB_PATH = os.path.join(os.path.dirname(os.path.abspath(__file__)), "libcssm_hip.so")
-ABI_VERSION = 2   # CSSM_ABI_VERSION of the include/cssm_amd.h these bindings follow
+ABI_VERSION = 3   # CSSM_ABI_VERSION of the include/cssm_amd.h these bindings follow
 
 CSSM_OK = 0
 F32, BF16 = 0, 1

@@ -29,7 +29,9 @@
 extern "C" {
 #endif
 
-#define CSSM_ABI_VERSION 2
+/* 3: K_hat's scan layout (cssm_spectral_kernel scan_order = 1) pairs rows at 128 x 128
+ *    (cssm_gated_scan_khat_order). */
+#define CSSM_ABI_VERSION 3
 
 typedef enum cssm_status {
   CSSM_OK = 0,
