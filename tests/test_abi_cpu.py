@@ -33,7 +33,7 @@ def test_library_exports_every_declared_symbol():
 def test_abi_version_and_errors_without_gpu():
     from cssm_amd import _lib
     lib = _lib.load()
-    assert lib.cssm_abi_version() == 2
+    assert lib.cssm_abi_version() == _lib.ABI_VERSION == 3
     assert lib.cssm_strerror(-1) == b"null pointer argument"
     # argument validation happens before any GPU work
     st = lib.cssm_gated_scan_fwd(None, None, None, 0, 1, 1, 1, 8, 8, None, None, 0, 0, None)
