@@ -576,10 +576,12 @@ __global__ void __launch_bounds__(256, 2) gdn_core_fused32(const GdnFusedArgs a)
   using GF = FusedFwdG;
   using GI = FusedInvG;
   constexpr int H = GF::H, W = GF::W, WF = GF::WF, WH = GF::WH, HW = H * W, DK = kFusedDK, NP = 3 * DK;
-  // bins i = tid + NT j: j < BPT in registers, the NX = NB - BPT NT rest (tid < NX) with their state in LDS
+  // bins i = tid + NT j: j < BPT in registers; the NX = NB - BPT NT rest with their state in LDS, one
+  // state row per lane: lane l < DK XW of wave w takes row l % DK of bin BPT NT + XW w + l / DK, so every
+  // wave adds a fraction of a step instead of one wave adding a whole one
   constexpr int NT = GF::NT, NB = H * WF, NINT = H * (WH - 1), BPT = NB / NT, NX = NB - BPT * NT, BT = BPT + 1;
-  constexpr int NW = NT / 64, JL = GI::JLD;
-  static_assert(NX > 0 && NX <= 64, "the bins beyond BPT per thread fill at most one wave");
+  constexpr int NW = NT / 64, JL = GI::JLD, XW = NX / NW;
+  static_assert(NX % NW == 0 && XW * DK <= 64, "the bins beyond BPT per thread split evenly over the waves' lanes");
   __shared__ __attribute__((aligned(16))) float smem[GF::LDS_FLOATS];
   __shared__ float2 esp[NP * H * 2];
   __shared__ float2 sx[NX * DK * DK];
@@ -648,10 +650,12 @@ __global__ void __launch_bounds__(256, 2) gdn_core_fused32(const GdnFusedArgs a)
     const int lane = tl % 64;
     int bu[BT], bv[BT];
     bool bok[BT];
+    // slot BPT: the extra bin whose state row this lane updates
+    const int xl = tl % 64, xbin = XW * (tl / 64) + xl / DK, xrow = xl % DK;
 #pragma unroll
     for (int j = 0; j < BT; ++j) {
-      const int i = tl + NT * j;
-      bok[j] = i < NB;
+      const int i = j < BPT ? tl + NT * j : BPT * NT + xbin;
+      bok[j] = j < BPT ? i < NB : xl < XW * DK;
       bin_uv(bok[j] ? i : 0, bu[j], bv[j]);
     }
     __syncthreads();   // the previous step's inverse and stores are done with the buffer
@@ -693,7 +697,7 @@ __global__ void __launch_bounds__(256, 2) gdn_core_fused32(const GdnFusedArgs a)
       for (int p = 0; p < 2 * DK; ++p) acc[p] = 0.0f;
 #pragma unroll
       for (int j = 0; j < BT; ++j) {
-        if (!bok[j]) continue;
+        if (!bok[j] || (j == BPT && xrow != 0)) continue;   // an extra bin once, on its row-0 lane
 #pragma unroll
         for (int p = 0; p < 2 * DK; ++p) {
           const float2 x = *bin_ptr(p, bu[j], bv[j]);
@@ -733,16 +737,24 @@ __global__ void __launch_bounds__(256, 2) gdn_core_fused32(const GdnFusedArgs a)
 #pragma unroll
     for (int j = 0; j < BPT; ++j) bin_step(j, s[j]);
     if (bok[BPT]) {
-      float2 st[DK][DK];
+      // row xrow of extra bin xbin (the bin's DK lanes are adjacent in one wave, so all of them have
+      // read q, k, v before any writes its o row over q)
+      float2 q[DK], k[DK], v[DK], si[DK];
 #pragma unroll
-      for (int r = 0; r < DK; ++r)
+      for (int c = 0; c < DK; ++c) {
+        q[c] = cscale(*bin_ptr(c, bu[BPT], bv[BPT]), 0.5f * nrm[c]);
+        k[c] = cscale(*bin_ptr(DK + c, bu[BPT], bv[BPT]), 0.5f * nrm[DK + c]);
+        v[c] = cscale(*bin_ptr(2 * DK + c, bu[BPT], bv[BPT]), 0.5f);
+        si[c] = sx[(xbin * DK + xrow) * DK + c];
+      }
+      const GdnBinPre<DK> pre = gdn_bin_prep<DK>(k, v, wh[BPT], gab[BPT].x, gab[BPT].y);
+      float2 vr = v[0];   // v[xrow] by selects (a lane-varying index would place v in memory)
 #pragma unroll
-        for (int c = 0; c < DK; ++c) st[r][c] = sx[(tl * DK + r) * DK + c];
-      bin_step(BPT, st);
+      for (int c = 1; c < DK; ++c) vr = xrow == c ? v[c] : vr;
+      const float2 oi = gdn_bin_row<DK>(si, vr, q, k, pre, gab[BPT].y);
 #pragma unroll
-      for (int r = 0; r < DK; ++r)
-#pragma unroll
-        for (int c = 0; c < DK; ++c) sx[(tl * DK + r) * DK + c] = st[r][c];
+      for (int c = 0; c < DK; ++c) sx[(xbin * DK + xrow) * DK + c] = si[c];
+      *bin_ptr(xrow, bu[BPT], bv[BPT]) = cscale(oi, 1.0f / float(HW));
     }
     __syncthreads();
 
