@@ -832,8 +832,9 @@ proj_persist_kernel(const TI* __restrict__ A, int M, int K, int N, const float* 
 // K-chunked projection for K beyond the persistent kernel's register-resident
 // weights (the CSSM-SHViT stages: K = 128 .. 640), on bf16 MFMA with the
 // operands split into bf16 parts (x = x1 + x2 + x3): fp32 A takes the same six
-// products as the persistent kernel; bf16 A is exactly its first part, so
-// three products (A1 B1 + A1 B2 + A1 B3) give the same fp32-level result.  One
+// products as the persistent kernel (three, down to order 2^-16, when the output
+// is bf16); bf16 A is exactly its first part, so three products
+// (A1 B1 + A1 B2 + A1 B3) give the same fp32-level result.  One
 // 128 x 128 output tile per workgroup; four waves split the 128 columns (32
 // each) and keep all 128 rows, as in the persistent kernel, so the proj_in
 // channel sums stay in-wave.  K advances in chunks of 32 with one barrier per
@@ -856,7 +857,10 @@ proj_kc_kernel(const TI* __restrict__ A, int M, int K, int N, const float* __res
   static_assert(TM == 64 || TM == 128, "row tiles of 64 or 128");
   constexpr int NI = TM / 32, NKQ = 256 / TM;   // A load groups per thread; plane-major k groups
   constexpr bool A1_ONLY = sizeof(TI) == 2;      // bf16 A: one nonzero part
-  constexpr int APL = A1_ONLY ? 1 : 3;           // A planes
+  // fp32 A with a bf16 output: the three products down to order 2^-16 (A1 B1 + A1 B2 + A2 B1) are far
+  // inside the output's own rounding (2^-9), so A3 and the order-2^-16 products are dropped
+  constexpr bool SIX = !A1_ONLY && sizeof(TO) == 4;
+  constexpr int APL = A1_ONLY ? 1 : (SIX ? 3 : 2);   // A planes
   constexpr int OP = TN + 4;                     // channels-last staging pitch (floats), 64 rows at a time
   constexpr int AB = TM * KP;                    // bf16 per plane
   constexpr int STG = APL * AB;                  // bf16 per pipeline stage
@@ -982,10 +986,8 @@ proj_kc_kernel(const TI* __restrict__ A, int M, int K, int N, const float* __res
           v3[e] = x3;
         }
         *reinterpret_cast<bf16x4*>(planes + off) = v1;
-        if constexpr (!A1_ONLY) {
-          *reinterpret_cast<bf16x4*>(planes + AB + off) = v2;
-          *reinterpret_cast<bf16x4*>(planes + 2 * AB + off) = v3;
-        }
+        if constexpr (APL >= 2) *reinterpret_cast<bf16x4*>(planes + AB + off) = v2;
+        if constexpr (APL == 3) *reinterpret_cast<bf16x4*>(planes + 2 * AB + off) = v3;
       }
     }
   };
@@ -1036,16 +1038,26 @@ proj_kc_kernel(const TI* __restrict__ A, int M, int K, int N, const float* __res
           }
         } else {
           const bf16x8 a2 = *reinterpret_cast<const bf16x8*>(Ap + AB + o);
-          const bf16x8 a3 = *reinterpret_cast<const bf16x8*>(Ap + 2 * AB + o);
+          if constexpr (SIX) {
+            const bf16x8 a3 = *reinterpret_cast<const bf16x8*>(Ap + 2 * AB + o);
 #pragma unroll
-          for (int j = 0; j < 2; ++j) {
-            floatx4 c = acc[i][j];
-            c = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a3, b1[j], c, 0, 0, 0);   // small terms first
-            c = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a2, b2[j], c, 0, 0, 0);
-            c = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a1, b3[j], c, 0, 0, 0);
-            c = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a2, b1[j], c, 0, 0, 0);
-            c = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a1, b2[j], c, 0, 0, 0);
-            acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a1, b1[j], c, 0, 0, 0);
+            for (int j = 0; j < 2; ++j) {
+              floatx4 c = acc[i][j];
+              c = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a3, b1[j], c, 0, 0, 0);   // small terms first
+              c = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a2, b2[j], c, 0, 0, 0);
+              c = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a1, b3[j], c, 0, 0, 0);
+              c = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a2, b1[j], c, 0, 0, 0);
+              c = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a1, b2[j], c, 0, 0, 0);
+              acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a1, b1[j], c, 0, 0, 0);
+            }
+          } else {
+#pragma unroll
+            for (int j = 0; j < 2; ++j) {
+              floatx4 c = acc[i][j];
+              c = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a2, b1[j], c, 0, 0, 0);   // small terms first
+              c = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a1, b2[j], c, 0, 0, 0);
+              acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a1, b1[j], c, 0, 0, 0);
+            }
           }
         }
       }

@@ -114,6 +114,23 @@ def test_proj_out_channels_last(mods, F, HW, K, N):
     assert rel_err(to_np(out), ref) < 1e-5
 
 
+@pytest.mark.parametrize("F,HW,K,N", [(3, 49, 448, 224), (2, 16, 640, 320), (2, 196, 256, 128)])
+def test_proj_out_bf16_output(mods, F, HW, K, N):
+    """fp32 plane-major A with a bf16 channels-last output (the CSSM-SHViT stages' out_proj): the
+    K-chunked kernel keeps the split products down to order 2^-16, so beyond the output's own
+    rounding the error stays at that level."""
+    _, S = mods
+    print_case(test="proj_out_bf16_out", F=F, HW=HW, K=K, N=N)
+    rng = np.random.default_rng(11)
+    y = rng.standard_normal((F, K, HW))
+    Wt = rng.standard_normal((K, N)) / np.sqrt(K)
+    b = rng.standard_normal(N) * 0.1
+    out = S.proj_out(_dev(y), _dev(Wt), _dev(b), out_dtype=torch.bfloat16)
+    assert out.dtype == torch.bfloat16
+    ref = y.transpose(0, 2, 1).reshape(F * HW, K) @ Wt + b
+    assert bf16_excess_err(to_np(out), ref) < 1e-4
+
+
 @pytest.mark.parametrize("ks,kt", [(3, 4), (3, 0), (0, 4), (5, 2)])
 def test_short_conv_matches_oracle(mods, ks, kt):
     _, S = mods
