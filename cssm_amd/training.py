@@ -42,6 +42,30 @@ class _ScanFn(torch.autograd.Function):
         return du, dz, dgates, dkhat, None
 
 
+class _SplitSiluFn(torch.autograd.Function):
+    """(SiLU(xz[:, :n]), SiLU(xz[:, n:])) of plane-major (F, 2n, HW).  The backward writes both halves'
+    SiLU gradients straight into one (F, 2n, HW) tensor, where two slice gradients would each be a
+    zero-filled full tensor to add (six passes over xz instead of two)."""
+
+    @staticmethod
+    def forward(ctx, xz, n):
+        ctx.save_for_backward(xz)
+        ctx.n = n
+        return Fn.silu(xz[:, :n]), Fn.silu(xz[:, n:])
+
+    @staticmethod
+    def backward(ctx, du, dz):
+        (xz,) = ctx.saved_tensors
+        n = ctx.n
+        dxz = torch.empty_like(xz)
+        for g, part in ((du, slice(None, n)), (dz, slice(n, None))):
+            if g is None:
+                dxz[:, part].zero_()
+            else:
+                torch.ops.aten.silu_backward.grad_input(g, xz[:, part], grad_input=dxz[:, part])
+        return dxz, None
+
+
 class _ProjPlanesFn(torch.autograd.Function):
     """Dense over channels-last rows x (F HW, K) into plane-major (F, N, HW) on the HIP projection
     kernel.  Adjoint: dx = dy W^T back to channels-last (the plane-major -> channels-last kernel with
@@ -194,6 +218,11 @@ def gated_train_apply(cell, params: Dict[str, Any], x: torch.Tensor) -> torch.Te
         raise NotImplementedError(f"no fused scan kernel for {H}x{W} planes")
     xz = _ProjPlanesFn.apply(x.reshape(-1, cin).float().contiguous(), p["in_proj"]["kernel"], p["in_proj"]["bias"],
                              F, HW)                                        # plane-major (F, 2C, HW)
+    c_scale = S.scan_c_scale(H, W)
+    if cell.short_conv_spatial_size == 0 and cell.short_conv_size == 0:
+        u, zg = _SplitSiluFn.apply(xz, Ci)
+        u, zg = u.view(B, T, Ci, H, W), zg.view(B, T, Ci, H, W)
+        return _gated_core(cell, p, u, zg, B, T, H, W, Ci, c_scale)
     xm, z = xz[:, :Ci].reshape(B, T, Ci, H, W), xz[:, Ci:].reshape(B, T, Ci, H, W)
     if cell.short_conv_spatial_size > 0:
         sp = p["short_conv_spatial"]
@@ -206,11 +235,15 @@ def gated_train_apply(cell, params: Dict[str, Any], x: torch.Tensor) -> torch.Te
         xm = _causal_t(xm, p["short_conv_temporal"])
     u = Fn.silu(xm).contiguous()
     zg = Fn.silu(z).contiguous()
-    c_scale = S.scan_c_scale(H, W)
+    return _gated_core(cell, p, u, zg, B, T, H, W, Ci, c_scale)
+
+
+def _gated_core(cell, p, u, zg, B, T, H, W, Ci, c_scale):
+    """Gates from ctx, K_hat, the fused scan and out_proj, from u = SiLU(x_m) and SiLU(z)."""
     gates = gate_planes(u.mean(dim=(3, 4)), p, H, W, cell.gate_type, cell.gate_activation, c_scale)
     khat = khat_planes(p["kernel"], H, W, cell.spectral_rho)
     y = _ScanFn.apply(u, zg, gates, khat, c_scale)                           # (B, T, C, H, W)
-    out = _ProjOutFn.apply(y.view(F, Ci, HW), p["out_proj"]["kernel"], p["out_proj"]["bias"])
+    out = _ProjOutFn.apply(y.view(B * T, Ci, H * W), p["out_proj"]["kernel"], p["out_proj"]["bias"])
     return out.view(B, T, H, W, cell.channels)
 
 
