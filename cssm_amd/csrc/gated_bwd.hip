@@ -59,22 +59,56 @@ __global__ void __launch_bounds__(256) gated_scan_bwd_bins(const GatedBwdArgs a)
     g[t] = t < T ? a.gates[(size_t(b) * T + t) * HWF + i] : make_float4(0.f, 0.f, 0.f, 0.f);
     gs[t] = make_float4(0.f, 0.f, 0.f, 0.f);
   }
+  // the spectra do not alias the outputs, and channel c + 1's U and dY are loaded while channel c
+  // computes and stores (without that, each channel's loads waited behind its own stores)
+  const float2* __restrict__ us = a.uspec;
+  const float2* __restrict__ dsp = a.dspec;
+  const float2* __restrict__ kh = a.khat;
+  float2* __restrict__ ys = a.yspec;
+  float2* __restrict__ sd = a.sdu;
+  auto fetch = [&](int c, float2& kn, float2 (&Uo)[MAXT], float2 (&Do)[MAXT]) {
+    kn = kh[size_t(c) * HWF + kpos];
+#pragma unroll
+    for (int t = 0; t < MAXT; ++t) {
+      if (t >= T) break;
+      const size_t s = ((size_t(b) * T + t) * C + c) * HWF + nat;
+      Uo[t] = us[s];
+      Do[t] = dsp[s];
+    }
+  };
+  // one channel ahead for T <= 8; at T <= 32 a second set of U and dY would exceed the register file,
+  // so each channel's loads are issued at its top (still ahead of its stores)
+  constexpr bool AHEAD = MAXT <= 8;
+  float2 kn;
+  float2 Un[AHEAD ? MAXT : 1], Dn[AHEAD ? MAXT : 1];
+  if constexpr (AHEAD) fetch(0, kn, Un, Dn);
   for (int c = 0; c < C; ++c) {
-    const float2 kf = a.khat[size_t(c) * HWF + kpos];
-    float2 h[MAXT], U[MAXT];
+    float2 h[MAXT], U[MAXT], D[MAXT];
+    if constexpr (AHEAD) {
+#pragma unroll
+      for (int t = 0; t < MAXT; ++t) {
+        U[t] = Un[t];
+        D[t] = Dn[t];
+      }
+    } else {
+      fetch(c, kn, U, D);
+    }
+    const float2 kf = kn;
+    if constexpr (AHEAD) {
+      if (c + 1 < C) fetch(c + 1, kn, Un, Dn);
+    }
     float2 hp = make_float2(0.f, 0.f);
 #pragma unroll
     for (int t = 0; t < MAXT; ++t) {
       if (t >= T) break;
       const size_t s = ((size_t(b) * T + t) * C + c) * HWF + nat;
-      U[t] = a.uspec[s];
       const float2 A = cscale(kf, g[t].x);
       const float2 P = cscale(U[t], g[t].y);
       const float vf = 0.5f * g[t].z;
       const float2 V = (P.x * P.x + P.y * P.y < vf * vf) ? make_float2(vf, 0.f) : P;
       hp = cadd(cmul(A, hp), V);
       h[t] = hp;
-      a.yspec[s] = cscale(hp, g[t].w * inv_cs);
+      ys[s] = cscale(hp, g[t].w * inv_cs);
     }
     float2 carry = make_float2(0.f, 0.f);             // conj(A_{t+1}) g_{t+1}
     float2 dkf = make_float2(0.f, 0.f);
@@ -82,7 +116,7 @@ __global__ void __launch_bounds__(256) gated_scan_bwd_bins(const GatedBwdArgs a)
     for (int tt = MAXT - 1; tt >= 0; --tt) {
       if (tt >= T) continue;
       const size_t s = ((size_t(b) * T + tt) * C + c) * HWF + nat;
-      const float2 dY = cscale(a.dspec[s], dscale);
+      const float2 dY = cscale(D[tt], dscale);
       const float Ct = g[tt].w * inv_cs;
       const float2 gt = cadd(cscale(dY, Ct), carry);
       gs[tt].w += (h[tt].x * dY.x + h[tt].y * dY.y) * inv_cs;
@@ -99,7 +133,7 @@ __global__ void __launch_bounds__(256) gated_scan_bwd_bins(const GatedBwdArgs a)
         gs[tt].y += U[tt].x * gt.x + U[tt].y * gt.y;     // Re(conj(U) g)
         dU = cscale(gt, g[tt].y);
       }
-      a.sdu[s] = cscale(dU, uscale);
+      sd[s] = cscale(dU, uscale);
       const float2 A = cscale(kf, g[tt].x);
       carry = cmulc(gt, A);                              // conj(A_t) g_t
     }
