@@ -26,6 +26,10 @@ B*T*(3*H*W*C*s + 3*(H+W/2+1)*4) + C*H*(W/2+1)*8 (read u and z, write y, read the
 factored gate vectors, K_hat once).  gdn: the spectral core (rfft2 + scan +
 irfft2 launches together), B*T*(4*H*W*C*s + 2*(H+W/2+1)*4) + n_h*H*(W/2+1)*8
 (read q, k, v, write o, gates, W_hat once).  s = bytes per I/O element.
+training (``--train``, default c2): the same workload's training step, forward +
+backward (loss = mean(out^2); gradients of x and every parameter), frames/s of
+the whole step with its forward / backward split, and the roofline of the
+reverse recurrence cssm_gated_scan_bwd on its algorithmic bytes.
 cpu_baseline times the float32 torch-CPU restatement (oracle/cssm_cpu_fp32.py)
 of the same layer on a batch slice, on the process's host-core share (warmup 5,
 median of up to 20 calls for the headline; warmup 1 and a shorter budget for
@@ -74,6 +78,9 @@ def parse():
                     help="other BASELINE configs measured in the same run and reported under 'configs' "
                          "(comma-separated; 'none' for the headline workload only)")
     ap.add_argument("--config-steps", type=int, default=20, help="timed steps of each extra config")
+    ap.add_argument("--train", default="c2",
+                    help="workload whose training step (forward + backward) is also measured, reported under "
+                         "'training' ('none' to skip)")
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--cpu-seconds", type=float, default=20.0,
                     help="time budget of the headline CPU baseline (a quarter of it for each extra config)")
@@ -349,6 +356,109 @@ def cpu_baseline(w, budget_s, warmup, max_repeats):
                        f"(os.cpu_count()={os.cpu_count()})")
 
 
+# ------------------------------------------------------------------ training
+
+def run_training(key, args, torch, cells, S):
+    """The layer's training step on the GPU (training.gated_train_apply / gdn_train_apply): forward,
+    loss = mean(out^2), gradients of x and every parameter.  value = frames/s of the whole step;
+    the roofline line prices the gated cell's reverse recurrence (cssm_gated_scan_bwd) on its
+    algorithmic bytes, timed with HIP events around direct calls on the stream the step uses."""
+    from cssm_amd import training, _lib
+    w = dict(WORKLOADS[key], key=key)
+    if w["cell"] not in ("gated", "gdn"):
+        raise ValueError(f"no training step for {key}")
+    B = args.batch or w["B"]
+    T, H, W = w["T"], w["H"], w["W"]
+    cell = make_cell(w, cells)
+    x = make_input(w, B, torch, "cuda").float()
+    variables = cell.init(1, x.shape)
+    randomise_biases(variables, torch, "cuda")
+
+    def leaves(t):
+        out = []
+        for v in t.values():
+            out += leaves(v) if isinstance(v, dict) else [v]
+        return out
+    ps = leaves(variables["params"])
+    for t in ps:
+        t.requires_grad_(True)
+    xr = x.clone().requires_grad_(True)
+    fn = training.gated_train_apply if w["cell"] == "gated" else training.gdn_train_apply
+    ev = [torch.cuda.Event(enable_timing=True) for _ in range(3)]
+
+    def step(timed):
+        if timed:
+            ev[0].record()
+        out = fn(cell, variables, xr)
+        loss = out.float().pow(2).mean()
+        if timed:
+            ev[1].record()
+        grads = torch.autograd.grad(loss, [xr] + ps)
+        if timed:
+            ev[2].record()
+        return grads
+    for _ in range(2):
+        step(False)
+    steps = max(1, min(args.config_steps, 10))
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for _ in range(steps):
+        step(False)
+    torch.cuda.synchronize()
+    ms_step = (time.perf_counter() - t0) * 1e3 / steps
+    fwd = bwd = 0.0
+    for _ in range(steps):
+        step(True)
+        torch.cuda.synchronize()
+        fwd += ev[0].elapsed_time(ev[1]) / steps
+        bwd += ev[1].elapsed_time(ev[2]) / steps
+    res = {"value": B * T / (ms_step * 1e-3), "unit": "frames/s", "steps": steps, "ms_per_step": ms_step,
+           "ms_forward": fwd, "ms_backward": bwd, "dtype": "f32",
+           "config": {"workload": w["name"], "cell": w["cell"], "batch": B, "T": T, "H": H, "W": W,
+                      "channels": w["C"], "step": "forward + backward: loss = mean(out^2), gradients of x and "
+                                                  "every parameter"},
+           "data": "synthetic, as the forward line of the same workload; random-init weights"}
+    if w["cell"] == "gated":
+        # the reverse recurrence alone, on spectra of the step's shape and the cell's gate planes / K_hat
+        C = w["C"] * w["expand"]
+        Wf = W // 2 + 1
+        p = variables["params"]
+        g = torch.Generator(device="cuda").manual_seed(3)
+        with torch.no_grad():
+            cs = S.scan_c_scale(H, W)
+            ctx = torch.randn((B, T, C), generator=g, device="cuda") * 0.1
+            gates = training.gate_planes(ctx, p, H, W, cell.gate_type, cell.gate_activation, cs).contiguous()
+            khat = training.khat_planes(p["kernel"], H, W, cell.spectral_rho).contiguous()
+            uspec = torch.randn((B, T, C, H, Wf), dtype=torch.complex64, generator=g, device="cuda")
+            dspec = torch.randn_like(uspec)
+            outs = [torch.empty_like(uspec), torch.empty_like(uspec), torch.empty_like(gates),
+                    torch.empty((B, C, H, Wf), dtype=torch.complex64, device="cuda")]
+            st = torch.cuda.current_stream().cuda_stream
+
+            def bwd_bins():
+                _lib.call("cssm_gated_scan_bwd", uspec.data_ptr(), dspec.data_ptr(), gates.data_ptr(),
+                          khat.data_ptr(), B, T, C, H, W, float(cs), *[o.data_ptr() for o in outs], st)
+            bwd_bins()
+            reps = 5
+            ev[0].record()
+            for _ in range(reps):
+                bwd_bins()
+            ev[1].record()
+            torch.cuda.synchronize()
+            k_ms = ev[0].elapsed_time(ev[1]) / reps
+        spec = B * T * C * H * Wf * 8
+        alg = 4 * spec + 2 * B * T * H * Wf * 16 + C * H * Wf * 8 + B * C * H * Wf * 8
+        res["roofline"] = {"kernel": "gated_scan_bwd_bins", "bound": "hbm", "ms": k_ms,
+                           "achieved": alg / (k_ms * 1e-3) / 1e9, "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                           "frac": alg / (k_ms * 1e-3) / 1e9 / HBM_PEAK_GBS, "algorithmic_bytes": alg,
+                           "bytes": "U and dY spectra read, C h and dU spectra written, gate planes read and "
+                                    "their gradient written, K_hat read and its per-batch gradient written"}
+        del uspec, dspec, outs
+    del x, xr, variables, ps
+    torch.cuda.empty_cache()
+    return res
+
+
 # ------------------------------------------------------------------- main
 
 def run_workload(key, args, torch, cells, S, headline):
@@ -537,6 +647,9 @@ def main():
         for k in extra:
             print(f"bench: workload {k}", file=sys.stderr, flush=True)
             res["configs"][k] = run_workload(k, args, torch, cells, S, headline=False)
+    if args.train not in ("", "none"):
+        print(f"bench: training step {args.train}", file=sys.stderr, flush=True)
+        res["training"] = run_training(args.train, args, torch, cells, S)
     # the CPU baselines run after every GPU measurement, so the host's thread pool never
     # competes with the launch thread of a timed GPU loop
     if not args.no_cpu_baseline:
