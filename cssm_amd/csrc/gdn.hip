@@ -1006,9 +1006,10 @@ hipError_t launch_gdn_gates(const float* ctx, int B, int T, int C, int H, int W,
 template <class TI, class TO>
 __global__ void __launch_bounds__(256)
 dwconv_cl(const TI* __restrict__ x, int H, int W, int C, int ks, const float* __restrict__ kw,
-          const float* __restrict__ bias, TO* __restrict__ y, long long total) {
-  // one thread per (pixel, 4 consecutive channels) when C % 4 == 0, else per (pixel, channel)
-  const int cv = (C % 4 == 0) ? 4 : 1;
+          const float* __restrict__ bias, TO* __restrict__ y, long long total, int vec) {
+  // one thread per (pixel, 4 consecutive channels) when vec (C % 4 == 0 and x, y and the taps
+  // aligned for 4-channel vectors, host-checked), else per (pixel, channel)
+  const int cv = vec ? 4 : 1;
   const long long i = (long long)blockIdx.x * blockDim.x + threadIdx.x;
   if (i >= total) return;
   const int CG = C / cv;
@@ -1138,10 +1139,12 @@ static hipError_t run_dwconv_rows(const void* x, int F, int H, int W, int C, con
 template <class TI, class TO>
 static bool try_dwconv_blocked(const void* x, int F, int H, int W, int C, int ks, const float* kw, const float* bias,
                                void* y, hipStream_t s, hipError_t& e) {
-  // float4 loads / stores of 4 channels: 16-byte aligned f32 (8-byte bf16) tensors; one frame's
-  // work items must fit 32-bit indices and the frames the grid's y dimension
+  // float4 loads / stores of 4 channels: 16-byte aligned f32 (8-byte bf16) tensors and 16-byte
+  // aligned taps and bias; one frame's work items must fit 32-bit indices and the frames the
+  // grid's y dimension (otherwise the general kernel runs)
   const size_t ax = sizeof(TI) * 4, ay = sizeof(TO) * 4;
   if (C % 4 || W % 4 || H % 2 || reinterpret_cast<uintptr_t>(x) % ax || reinterpret_cast<uintptr_t>(y) % ay ||
+      reinterpret_cast<uintptr_t>(kw) % 16 || reinterpret_cast<uintptr_t>(bias) % 16 ||
       (long long)H * W * C >= (1LL << 31) || F > 65535)
     return false;
   switch (ks) {
@@ -1159,21 +1162,24 @@ hipError_t launch_depthwise_conv(const void* x, int dtype, int F, int H, int W, 
   if (dtype == 0 && out_dtype == 1 && try_dwconv_blocked<float, uint16_t>(x, F, H, W, C, ks, kw, bias, y, s, e)) return e;
   if (dtype == 1 && out_dtype == 0 && try_dwconv_blocked<uint16_t, float>(x, F, H, W, C, ks, kw, bias, y, s, e)) return e;
   if (dtype == 1 && out_dtype == 1 && try_dwconv_blocked<uint16_t, uint16_t>(x, F, H, W, C, ks, kw, bias, y, s, e)) return e;
-  const long long total = (long long)F * H * W * (C % 4 == 0 ? C / 4 : C);
+  const size_t ax = (dtype == 0 ? 4 : 2) * 4, ay = (out_dtype == 0 ? 4 : 2) * 4;
+  const int vec = C % 4 == 0 && reinterpret_cast<uintptr_t>(x) % ax == 0 && reinterpret_cast<uintptr_t>(y) % ay == 0 &&
+                  reinterpret_cast<uintptr_t>(kw) % 16 == 0;
+  const long long total = (long long)F * H * W * (vec ? C / 4 : C);
   const unsigned blocks = unsigned((total + 255) / 256);
   const dim3 g(blocks), b(256);
   if (dtype == 0 && out_dtype == 0)
     hipLaunchKernelGGL((dwconv_cl<float, float>), g, b, 0, s, static_cast<const float*>(x), H, W, C, ks, kw, bias,
-                       static_cast<float*>(y), total);
+                       static_cast<float*>(y), total, vec);
   else if (dtype == 0)
     hipLaunchKernelGGL((dwconv_cl<float, uint16_t>), g, b, 0, s, static_cast<const float*>(x), H, W, C, ks, kw, bias,
-                       static_cast<uint16_t*>(y), total);
+                       static_cast<uint16_t*>(y), total, vec);
   else if (out_dtype == 0)
     hipLaunchKernelGGL((dwconv_cl<uint16_t, float>), g, b, 0, s, static_cast<const uint16_t*>(x), H, W, C, ks, kw,
-                       bias, static_cast<float*>(y), total);
+                       bias, static_cast<float*>(y), total, vec);
   else
     hipLaunchKernelGGL((dwconv_cl<uint16_t, uint16_t>), g, b, 0, s, static_cast<const uint16_t*>(x), H, W, C, ks, kw,
-                       bias, static_cast<uint16_t*>(y), total);
+                       bias, static_cast<uint16_t*>(y), total, vec);
   return hipGetLastError();
 }
 

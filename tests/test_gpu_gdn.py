@@ -132,6 +132,14 @@ def test_frame_mean_and_depthwise_conv(mods, shape):
         ybb = S.depthwise_conv(xb, _dev(p["kernel"]), _dev(p["bias"]), out_dtype=torch.bfloat16)
         assert ybb.dtype == torch.bfloat16
         assert bf16_excess_err(to_np(ybb), refb) < 2e-5, ks
+        # taps and bias 4 bytes off a 16-byte boundary: the per-channel kernel, same values
+        kbuf = torch.zeros(ks * ks * C + C + 2, device="cuda")
+        kbuf[1:1 + ks * ks * C] = _dev(p["kernel"]).flatten()
+        kbuf[2 + ks * ks * C:] = _dev(p["bias"])
+        kmis, bmis = kbuf[1:1 + ks * ks * C].view(ks, ks, 1, C), kbuf[2 + ks * ks * C:]
+        assert kmis.data_ptr() % 16 != 0
+        ym = S.depthwise_conv(_dev(x), kmis, bmis)
+        assert rel_err(to_np(ym), ref) < 5e-6, ks
 
 
 @pytest.mark.parametrize("gate_type", ["factored", "dense", "channel", "scalar"])
