@@ -187,19 +187,49 @@ proj_in_kernel(const TI* __restrict__ X, int M, int K, int N, const float* __res
 }
 
 // ctx[f][c] = sum over the row tiles t of TM rows that overlap frame f of
-// partial[t][f - first frame of t][c], in tile order, / HW
-__global__ void ctx_reduce_kernel(const float* __restrict__ partial, int F, int HW, int TM, int slots, int C,
-                                  float* __restrict__ ctx) {
-  const int i = blockIdx.x * blockDim.x + threadIdx.x;
-  if (i >= F * C) return;
-  const int f = i / C, c = i % C;
+// partial[t][f - first frame of t][c], / HW.  One block per frame: with C <= 128
+// the 256 threads split the frame's tiles into G = 256 / C strided groups (each
+// summed in tile order, loads unrolled so several are in flight), and the group
+// sums add in group order; wider C loops over channels with one group.  The
+// order is fixed, so ctx is deterministic.
+__global__ void __launch_bounds__(256) ctx_reduce_kernel(const float* __restrict__ partial, int F, int HW, int TM,
+                                                         int slots, int C, float* __restrict__ ctx) {
+  __shared__ float red[256];
+  const int f = blockIdx.x, tid = threadIdx.x;
   const long long r0 = (long long)f * HW, r1 = r0 + HW - 1;
-  float s = 0.0f;
-  for (long long t = r0 / TM; t <= r1 / TM; ++t) {
-    const int slot = int(f - (t * TM) / HW);
-    s += partial[(size_t(t) * slots + slot) * C + c];
+  const long long t0 = r0 / TM, t1 = r1 / TM;
+  const int G = C <= 128 ? 256 / C : 1;
+  const int g = tid / C;   // (C <= 128: tid < G C covers every thread of the block)
+  auto sum_tiles = [&](int c, int gi) {
+    float s = 0.0f;
+    long long t = t0 + gi;
+    for (; t + 3 * G <= t1; t += 4 * G) {
+      float v[4];
+#pragma unroll
+      for (int u = 0; u < 4; ++u) {
+        const long long tt = t + u * G;
+        v[u] = partial[(size_t(tt) * slots + int(f - (tt * TM) / HW)) * C + c];
+      }
+      s += v[0];
+      s += v[1];
+      s += v[2];
+      s += v[3];
+    }
+    for (; t <= t1; t += G) s += partial[(size_t(t) * slots + int(f - (t * TM) / HW)) * C + c];
+    return s;
+  };
+  if (G > 1) {
+    const int c = tid % C;
+    red[tid] = g < G ? sum_tiles(c, g) : 0.0f;
+    __syncthreads();
+    if (tid < C) {
+      float s = 0.0f;
+      for (int q = 0; q < G; ++q) s += red[q * C + tid];
+      ctx[size_t(f) * C + tid] = s * (1.0f / float(HW));
+    }
+  } else {
+    for (int c = tid; c < C; c += 256) ctx[size_t(f) * C + c] = sum_tiles(c, 0) * (1.0f / float(HW));
   }
-  ctx[i] = s * (1.0f / float(HW));
 }
 
 // ---------------------------------------------------------------------------
@@ -1492,9 +1522,7 @@ hipError_t launch_proj_out_norm_gate(const void* Y, const void* G, int in_dtype,
 
 hipError_t launch_ctx_reduce(const float* partial, int F, int HW, int tile_rows, int slots, int C, float* ctx,
                              hipStream_t s) {
-  const int n = F * C;
-  hipLaunchKernelGGL(ctx_reduce_kernel, dim3((n + 255) / 256), dim3(256), 0, s, partial, F, HW, tile_rows, slots, C,
-                     ctx);
+  hipLaunchKernelGGL(ctx_reduce_kernel, dim3(unsigned(F)), dim3(256), 0, s, partial, F, HW, tile_rows, slots, C, ctx);
   return hipGetLastError();
 }
 
