@@ -233,16 +233,20 @@ def gdn_step(cell, variables, x, w, S, mark):
     ctx = S.frame_mean(x)
     ab, bkv = S.gdn_gates(ctx, p, H, W, cell.delta_key_dim, cell.gate_type, True, "sinusoid", cell.rope_base)
     mark("gates")
+    convs = [p["short_conv_q"], p["short_conv_k"], p["short_conv_v"]]
     if cell.qkv_conv_size > 1:
         xq = S.depthwise_conv(x, p["qkv_dw"]["kernel"], p["qkv_dw"]["bias"], out_dtype=f32)
         mark("qkv_dw")
+        qkv = S.gdn_qkv_proj(xq, p["qkv_proj"]["kernel"], p["qkv_proj"]["bias"], B, T, H, W, convs, 1, bkv,
+                             out_dtype=f32)
+        mark("qkv_proj")   # with the short conv, SiLU and input gates (one kernel when T in {1, 2, 4, 8})
+        gv = S.proj_planes(x, p["gate_proj"]["kernel"], p["gate_proj"]["bias"], F, HW, act="silu", out_dtype=f32)
+        mark("gate_proj")
     else:
-        xq = x
-    qkv = S.gdn_qkv_proj(xq, p["qkv_proj"]["kernel"], p["qkv_proj"]["bias"], B, T, H, W,
-                         [p["short_conv_q"], p["short_conv_k"], p["short_conv_v"]], 1, bkv, out_dtype=f32)
-    mark("qkv_proj")   # with the short conv, SiLU and input gates (one kernel when T in {1, 2, 4, 8})
-    gv = S.proj_planes(x, p["gate_proj"]["kernel"], p["gate_proj"]["bias"], F, HW, act="silu", out_dtype=f32)
-    mark("gate_proj")
+        # both projections read x: gate_proj's columns ride in the fused qkv launch
+        qkv, gv = S.gdn_qkv_gate_proj(x, p["qkv_proj"]["kernel"], p["qkv_proj"]["bias"], B, T, H, W, convs, 1, bkv,
+                                      p["gate_proj"]["kernel"], p["gate_proj"]["bias"], "silu", out_dtype=f32)
+        mark("qkv_gate_proj")
     if S.gdn_core_fused_supported(H, W, cell.delta_key_dim):
         o = S.gdn_core_fused(qkv, True, ab, cell.gate_type, what, cell.delta_key_dim)
         mark("core_fused")   # rfft2 -> norms -> delta rule -> irfft2 in one kernel

@@ -89,6 +89,8 @@ SIGNATURES = {
                             _P, _P, _P]),
     "cssm_gdn_qkv_post": (_I, [_P, _I, _I, _I, _I, _I, _I, _I, _P, _P, _I, _P, _P]),
     "cssm_gdn_qkv_proj": (_I, [_P, _I, _I, _I, _I, _I, _I, _I, _P, _P, _I, _P, _P, _I, _P, _P, _I, _P]),
+    "cssm_gdn_qkv_gate_proj": (_I, [_P, _I, _I, _I, _I, _I, _I, _I, _P, _P, _I, _P, _P, _I, _P, _P, _P, _I, _P, _P,
+                                    _I, _P]),
     "cssm_gdn_qkv_fused": (_I, [_I, _I, _I, _I, _I]),
     "cssm_rfft2": (_I, [_P, _I, _LL, _I, _I, _P, _P, _P]),
     "cssm_irfft2": (_I, [_P, _LL, _I, _I, _P, _I, _P]),

@@ -413,12 +413,18 @@ class GatedDeltaNetCSSM:
         convs = None
         if self.short_conv_size > 0:
             convs = [p["short_conv_q"], p["short_conv_k"], p["short_conv_v"]]
-        # qkv_proj with the short conv, SiLU and input gates in its epilogue
-        qkv = S.gdn_qkv_proj(xq, p["qkv_proj"]["kernel"], p["qkv_proj"]["bias"], B, T, H, W, convs, gate_mode, gates,
-                             out_dtype=f32)
+        # qkv_proj with the short conv, SiLU and input gates in its epilogue; without the qkv conv both
+        # projections read x, and gate_proj rides in the same call
+        gact = "silu" if self.output_gate_act == "silu" else "sigmoid"
+        if xq is x:
+            qkv, gv = S.gdn_qkv_gate_proj(x, p["qkv_proj"]["kernel"], p["qkv_proj"]["bias"], B, T, H, W, convs,
+                                          gate_mode, gates, p["gate_proj"]["kernel"], p["gate_proj"]["bias"], gact,
+                                          out_dtype=f32)
+        else:
+            qkv = S.gdn_qkv_proj(xq, p["qkv_proj"]["kernel"], p["qkv_proj"]["bias"], B, T, H, W, convs, gate_mode,
+                                 gates, out_dtype=f32)
+            gv = S.proj_planes(x, p["gate_proj"]["kernel"], p["gate_proj"]["bias"], F, HW, act=gact, out_dtype=f32)
         del xq, gates
-        gv = S.proj_planes(x, p["gate_proj"]["kernel"], p["gate_proj"]["bias"], F, HW,
-                           act="silu" if self.output_gate_act == "silu" else "sigmoid", out_dtype=f32)
         # spectral core: rfft2 -> delta-rule recurrence -> irfft2, in one kernel where a workgroup
         # holds a head's state (32 x 32, d_k = 4), else through spectra in HBM
         if S.gdn_core_fused_supported(H, W, dk):

@@ -365,32 +365,54 @@ int cssm_gdn_qkv_post(void* qkv, int dtype, int B, int T, int C, int H, int W, i
                     "cssm_gdn_qkv_post");
 }
 
-int cssm_gdn_qkv_proj(const void* x, int in_dtype, int B, int T, int H, int W, int K, int C, const float* kernel,
-                      const float* bias, int kt, const float* const* conv_kernel, const float* const* conv_bias,
-                      int gate_mode, const void* gates, void* qkv, int out_dtype, void* stream) {
-  if (!x || !kernel || !bias || !qkv) return fail(CSSM_ERR_NULL, "cssm_gdn_qkv_proj: x, kernel, bias and qkv must be non-null");
+// shared by the qkv projection and its gate_proj variant (wg != nullptr)
+static int gdn_qkv_proj_impl(const char* fn, const void* x, int in_dtype, int B, int T, int H, int W, int K, int C,
+                             const float* kernel, const float* bias, int kt, const float* const* conv_kernel,
+                             const float* const* conv_bias, int gate_mode, const void* gates, void* qkv,
+                             int out_dtype, void* stream, const float* wg, const float* bg, int gact, void* gv) {
+  if (!x || !kernel || !bias || !qkv) return fail(CSSM_ERR_NULL, "%s: x, kernel, bias and qkv must be non-null", fn);
   if (B <= 0 || T <= 0 || H <= 0 || W <= 0 || K <= 0 || C <= 0 || kt < 0 || kt > 8)
-    return fail(CSSM_ERR_SHAPE, "cssm_gdn_qkv_proj: B=%d T=%d H=%d W=%d K=%d C=%d kt=%d (kt <= 8)", B, T, H, W, K, C, kt);
-  if ((long long)B * T * H * W > 0x7fffffffLL) return fail(CSSM_ERR_SHAPE, "cssm_gdn_qkv_proj: B*T*H*W exceeds 2^31");
-  if (!dtype_ok(in_dtype) || !dtype_ok(out_dtype))
-    return fail(CSSM_ERR_ARG, "cssm_gdn_qkv_proj: dtypes %d/%d", in_dtype, out_dtype);
-  if (gate_mode < 0 || gate_mode > 3) return fail(CSSM_ERR_ARG, "cssm_gdn_qkv_proj: gate_mode=%d", gate_mode);
-  if (gate_mode != 0 && !gates) return fail(CSSM_ERR_NULL, "cssm_gdn_qkv_proj: gates must be non-null");
+    return fail(CSSM_ERR_SHAPE, "%s: B=%d T=%d H=%d W=%d K=%d C=%d kt=%d (kt <= 8)", fn, B, T, H, W, K, C, kt);
+  if ((long long)B * T * H * W > 0x7fffffffLL) return fail(CSSM_ERR_SHAPE, "%s: B*T*H*W exceeds 2^31", fn);
+  if (!dtype_ok(in_dtype) || !dtype_ok(out_dtype)) return fail(CSSM_ERR_ARG, "%s: dtypes %d/%d", fn, in_dtype, out_dtype);
+  if (gate_mode < 0 || gate_mode > 3) return fail(CSSM_ERR_ARG, "%s: gate_mode=%d", fn, gate_mode);
+  if (gate_mode != 0 && !gates) return fail(CSSM_ERR_NULL, "%s: gates must be non-null", fn);
   cssm::GdnShortConv sc{};
   if (kt > 0) {
-    if (!conv_kernel || !conv_bias) return fail(CSSM_ERR_NULL, "cssm_gdn_qkv_proj: short-conv weights missing");
+    if (!conv_kernel || !conv_bias) return fail(CSSM_ERR_NULL, "%s: short-conv weights missing", fn);
     for (int i = 0; i < 3; ++i) {
-      if (!conv_kernel[i] || !conv_bias[i]) return fail(CSSM_ERR_NULL, "cssm_gdn_qkv_proj: short-conv %d missing", i);
+      if (!conv_kernel[i] || !conv_bias[i]) return fail(CSSM_ERR_NULL, "%s: short-conv %d missing", fn, i);
       sc.w[i] = conv_kernel[i];
       sc.b[i] = conv_bias[i];
     }
   }
   if (!aligned(x, vec_align(in_dtype)) || !aligned(qkv, vec_align(out_dtype)) ||
       (gate_mode == 1 && !aligned(gates, 8)) || (gate_mode == 3 && !aligned(gates, 16)))
-    return fail(CSSM_ERR_ALIGN, "cssm_gdn_qkv_proj: misaligned x / qkv / gates");
+    return fail(CSSM_ERR_ALIGN, "%s: misaligned x / qkv / gates", fn);
+  if (wg) {
+    if (!bg || !gv) return fail(CSSM_ERR_NULL, "%s: gate_bias and gv must be non-null", fn);
+    if (gact != 1 && gact != 2) return fail(CSSM_ERR_ARG, "%s: gate_act=%d (1 SiLU, 2 sigmoid)", fn, gact);
+    if (!aligned(gv, vec_align(out_dtype))) return fail(CSSM_ERR_ALIGN, "%s: misaligned gv", fn);
+  }
   return hip_status(cssm::launch_gdn_qkv_proj(x, in_dtype, B, T, H * W, K, C, kernel, bias, kt, sc, gate_mode, gates,
-                                              qkv, out_dtype, static_cast<hipStream_t>(stream)),
-                    "cssm_gdn_qkv_proj");
+                                              qkv, out_dtype, static_cast<hipStream_t>(stream), wg, bg, gact, gv),
+                    fn);
+}
+
+int cssm_gdn_qkv_proj(const void* x, int in_dtype, int B, int T, int H, int W, int K, int C, const float* kernel,
+                      const float* bias, int kt, const float* const* conv_kernel, const float* const* conv_bias,
+                      int gate_mode, const void* gates, void* qkv, int out_dtype, void* stream) {
+  return gdn_qkv_proj_impl("cssm_gdn_qkv_proj", x, in_dtype, B, T, H, W, K, C, kernel, bias, kt, conv_kernel,
+                           conv_bias, gate_mode, gates, qkv, out_dtype, stream, nullptr, nullptr, 0, nullptr);
+}
+
+int cssm_gdn_qkv_gate_proj(const void* x, int in_dtype, int B, int T, int H, int W, int K, int C, const float* kernel,
+                           const float* bias, int kt, const float* const* conv_kernel, const float* const* conv_bias,
+                           int gate_mode, const void* gates, const float* gate_kernel, const float* gate_bias,
+                           int gate_act, void* qkv, void* gv, int out_dtype, void* stream) {
+  if (!gate_kernel) return fail(CSSM_ERR_NULL, "cssm_gdn_qkv_gate_proj: gate_kernel must be non-null");
+  return gdn_qkv_proj_impl("cssm_gdn_qkv_gate_proj", x, in_dtype, B, T, H, W, K, C, kernel, bias, kt, conv_kernel,
+                           conv_bias, gate_mode, gates, qkv, out_dtype, stream, gate_kernel, gate_bias, gate_act, gv);
 }
 
 int cssm_gdn_qkv_fused(int T, int H, int W, int K, int kt) {

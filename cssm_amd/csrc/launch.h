@@ -129,10 +129,13 @@ hipError_t launch_depthwise_conv(const void* x, int dtype, int F, int H, int W, 
                                  const float* bias, void* y, int out_dtype, hipStream_t s);
 hipError_t launch_gdn_qkv_post(void* qkv, int dtype, int B, int T, int C, int HW, int kt, const GdnShortConv& sc,
                                int gate_mode, const void* gates, hipStream_t s);
-// qkv_proj + short conv + SiLU + input gates: one fused launch when gdn_qkv_fused_supported(T, HW, K, kt), else the two
+// qkv_proj + short conv + SiLU + input gates: one fused launch when gdn_qkv_fused_supported(T, HW, K, kt), else the two.
+// With wg != nullptr also gate_proj of the same rows (wg (K, C), bg (C), act gact) into gv (B, T, C, HW): fused as
+// C more columns of the same launch, else one more projection.
 hipError_t launch_gdn_qkv_proj(const void* X, int in_dtype, int B, int T, int HW, int K, int C, const float* W,
                                const float* b, int kt, const GdnShortConv& sc, int gate_mode, const void* gates,
-                               void* out, int out_dtype, hipStream_t s);
+                               void* out, int out_dtype, hipStream_t s, const float* wg = nullptr,
+                               const float* bg = nullptr, int gact = 0, void* gv = nullptr);
 bool gdn_qkv_fused_supported(int T, int HW, int K, int kt);
 
 // ---- CSSMSHViTBlock wiring (block.hip)

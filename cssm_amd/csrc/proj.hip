@@ -71,6 +71,25 @@ __device__ __forceinline__ void st4(float* p, size_t i, const float* v) {
 __device__ __forceinline__ void st4(uint16_t* p, size_t i, const float* v) {
   for (int r = 0; r < 4; ++r) st_el(p, i + r, v[r]);
 }
+// bf16 bits of v with st_el's rounding
+__device__ __forceinline__ uint32_t bf16_bits(float v) {
+  uint32_t x = __float_as_uint(v);
+  if ((x & 0x7f800000u) == 0x7f800000u) return (x >> 16) | ((x & 0x007fffffu) ? 0x40u : 0u);
+  x += 0x7fffu + ((x >> 16) & 1u);
+  return x >> 16;
+}
+// 4 consecutive elements at byte offset off of a buffer resource; an offset past the
+// resource's range drops the store
+__device__ __forceinline__ void bst4(__amdgpu_buffer_rsrc_t r, unsigned off, const float* v, float*) {
+  typedef unsigned u4 __attribute__((ext_vector_type(4)));
+  const u4 w = {__float_as_uint(v[0]), __float_as_uint(v[1]), __float_as_uint(v[2]), __float_as_uint(v[3])};
+  __builtin_amdgcn_raw_buffer_store_b128(w, r, off, 0, 0);
+}
+__device__ __forceinline__ void bst4(__amdgpu_buffer_rsrc_t r, unsigned off, const float* v, uint16_t*) {
+  typedef unsigned u2 __attribute__((ext_vector_type(2)));
+  const u2 w = {bf16_bits(v[0]) | (bf16_bits(v[1]) << 16), bf16_bits(v[2]) | (bf16_bits(v[3]) << 16)};
+  __builtin_amdgcn_raw_buffer_store_b64(w, r, off, 0, 0);
+}
 
 // Block tile TM rows x TN output channels, K staged through LDS in chunks of
 // KC.  Wave layout WMW x WNW waves, each owning (TM / WMW) x (TN / WNW)
@@ -281,6 +300,14 @@ struct QkvPost {
   int gate_mode;         // as cssm_gdn_qkv_post (0 none, 1 per pixel, 2 per frame, 3 per channel and pixel)
   const void* gates;
   int T;                 // frames per batch element (a multiple of TT)
+  // gate_proj on the same rows (ng = C, else 0): kernel columns N .. N + C - 1 are
+  // x wg + bg with SiLU (gact 1) or sigmoid (gact 2), no convolution and no input
+  // gate, written plane-major to gv (B, T, C, HW) in the output dtype
+  const float* wg;       // (K, C)
+  const float* bg;       // (C)
+  int ng;
+  int gact;
+  void* gv;
 };
 
 template <int KMAX, bool PLANE_A, bool OUT_SPLIT, int WN, class TI, class TO, bool NORM = false, bool SPLIT = false,
@@ -358,7 +385,11 @@ proj_persist_kernel(const TI* __restrict__ A, int M, int K, int N, const float* 
 #pragma unroll
         for (int e = 0; e < 8; ++e) {
           const int kk = kb * 32 + (lane >> 4) * 8 + e;
-          const float w = (kk < K && gn < N) ? Wt[size_t(kk) * N + gn] : 0.0f;
+          float w = 0.0f;
+          if (kk < K) {
+            if (gn < N) w = Wt[size_t(kk) * N + gn];
+            else if (TT > 0 && gn < N + qp.ng) w = qp.wg[size_t(kk) * qp.ng + (gn - N)];
+          }
           __bf16 x1, x2, x3;
           split3_bf16(w, x1, x2, x3);
           b1[j][kb][e] = x1;
@@ -383,6 +414,11 @@ proj_persist_kernel(const TI* __restrict__ A, int M, int K, int N, const float* 
         for (int d = 0; d <= KH; ++d) e[d] = d < qp.kt ? qp.w[blk][(qp.kt - 1 - d) * C + c] : 0.0f;
         e[4] = bias[gn];
         e[5] = qp.kt > 0 ? qp.b[blk][c] : 0.0f;
+      } else if (gn < N + qp.ng) {
+#pragma unroll
+        for (int d = 0; d <= KH; ++d) e[d] = 0.0f;
+        e[4] = qp.bg[gn - N];
+        e[5] = 0.0f;
       }
     }
   }
@@ -675,8 +711,9 @@ proj_persist_kernel(const TI* __restrict__ A, int M, int K, int N, const float* 
 #pragma unroll
       for (int j = 0; j < 2; ++j) {
         const int cl = wn * 32 + j * 16 + (lane & 15), gn = n0 + cl;
-        if (gn >= N) continue;
+        if (gn >= N + qp.ng) continue;
         const int blk = gn / C, c = gn % C;
+        const bool gcol = gn >= N;   // a gate_proj column: bias and activation only
         // wd[d]: tap on frame t - d.  From LDS: taps on frames t .. t - KH (zero beyond kt, so those
         // products add nothing) with the projection bias folded into the accumulators once; read
         // per tile: up to 8 taps, the ones beyond kt skipped, the bias added per use.
@@ -697,9 +734,9 @@ proj_persist_kernel(const TI* __restrict__ A, int M, int K, int N, const float* 
             for (int r = 0; r < 4; ++r) acc[i][j][r] += bv;
         } else {
 #pragma unroll
-          for (int d = 0; d < NTAP; ++d) wd[d] = d < qp.kt ? qp.w[blk][(qp.kt - 1 - d) * C + c] : 0.0f;
-          bv = bias[gn];
-          bt = qp.kt > 0 ? qp.b[blk][c] : 0.0f;
+          for (int d = 0; d < NTAP; ++d) wd[d] = (!gcol && d < qp.kt) ? qp.w[blk][(qp.kt - 1 - d) * C + c] : 0.0f;
+          bv = gcol ? qp.bg[gn - N] : bias[gn];
+          bt = (!gcol && qp.kt > 0) ? qp.b[blk][c] : 0.0f;
         }
         // the projection of frame i of this tile with its bias
         auto xb = [&](int i, int r) -> float {
@@ -715,7 +752,10 @@ proj_persist_kernel(const TI* __restrict__ A, int M, int K, int N, const float* 
 #pragma unroll
           for (int r = 0; r < 4; ++r) {
             float x = xb(i, r);
-            if (qp.kt > 0) {
+            if (gcol) {
+              const float sg = __builtin_amdgcn_rcpf(1.0f + __expf(-x));   // as the plain projection's epilogue
+              x = qp.gact == 1 ? x * sg : sg;
+            } else if (qp.kt > 0) {
               float o = fmaf(wd[0], x, bt);
 #pragma unroll
               for (int d = NTAP - 1; d >= 1; --d) {
@@ -731,7 +771,7 @@ proj_persist_kernel(const TI* __restrict__ A, int M, int K, int N, const float* 
             }
             v[r] = x;
           }
-          if (blk > 0 && qp.gate_mode != 0) {
+          if (!gcol && blk > 0 && qp.gate_mode != 0) {
             float g[4];
             if (qp.gate_mode != 3) {
               const float2* gp = gsh + t * TP + (i % IPF) * 16 + (lane >> 4) * 4;
@@ -745,7 +785,8 @@ proj_persist_kernel(const TI* __restrict__ A, int M, int K, int N, const float* 
 #pragma unroll
             for (int r = 0; r < 4; ++r) v[r] *= g[r];
           }
-          st4(out_lo, (fr * N + gn) * HW + px, v);
+          if (gcol) st4(static_cast<TO*>(qp.gv), (fr * qp.ng + (gn - N)) * HW + px, v);
+          else st4(out_lo, (fr * N + gn) * HW + px, v);
         }
         if constexpr (CARRY) {
           // this chunk's last KH frames for the next chunk of the same pixels (each lane its own slots)
@@ -1401,6 +1442,289 @@ hipError_t launch_proj_in(const void* X, int in_dtype, int M, int K, int N, cons
                             N / 2, s);
 }
 
+// ---------------------------------------------------------------------------
+// GDN qkv projection, frame-sequential: qkv_proj + causal short conv + SiLU +
+// input gates (+ gate_proj columns), computing what the tiled epilogue of
+// proj_persist_kernel (TT > 0) computes, operation for operation.  A tile is
+// 64 consecutive pixels of ONE frame x 128 output columns; a workgroup walks
+// the T frames of one (batch element, pixel block) in order, and each lane
+// keeps the pre-conv projections of its 32 elements on the three previous
+// frames in registers (the taps on frames t-1 .. t-3: kt <= 4, or T <= 4 where
+// earlier taps only meet the zero padding).  A wave owns all 64 rows of its 32
+// columns, so its four stores per column write 256 contiguous bytes of one
+// plane; the tiles of 16 pixels x 8 frames wrote 64-byte runs into eight
+// frames' planes at once, and that write pattern, not the arithmetic, bounded
+// them (same loads and stores with no MFMA or epilogue math: same time).
+// ---------------------------------------------------------------------------
+constexpr int kFseqTM = 64;
+template <class TI, class TO>
+__global__ void __launch_bounds__(256, 2)
+qkv_fseq_kernel(const TI* __restrict__ A, int T, int HW, int K, int N, const float* __restrict__ Wt,
+                const float* __restrict__ bias, int nseq, TO* __restrict__ out, QkvPost qp) {
+  constexpr int TM = kFseqTM, TN = 128, NT = 256, MI = TM / 16, KMAX = 64, KB = KMAX / 32, KP = KMAX + 8;
+  constexpr bool A1_ONLY = sizeof(TI) == 2;      // bf16 A is exactly its first bf16 part
+  constexpr int APL = A1_ONLY ? 1 : 3;
+  constexpr int PF = TM * KMAX / 4 / NT;         // groups of 4 consecutive k per thread and tile
+  constexpr int KH = 3;                          // earlier frames the conv reads
+  constexpr unsigned kDrop = 0x80000000u;        // a buffer offset past every resource's range
+  __shared__ __attribute__((aligned(16))) __bf16 Asm[APL * TM * KP];
+  __shared__ __attribute__((aligned(16))) float qcw[TN * 8];
+  __shared__ float2 gsh[TM];
+  __bf16* const A1 = Asm;
+  __bf16* const A2 = A1 + (APL > 1 ? TM * KP : 0);
+  __bf16* const A3 = A2 + (APL > 1 ? TM * KP : 0);
+  const int tid = threadIdx.x, lane = tid & 63, wn = tid >> 6;
+  const int n0 = blockIdx.y * TN, C = N / 3, NG = N + qp.ng;
+  const int tpf = HW / TM;                       // pixel blocks per frame
+
+  // B fragments: lane l holds column wn 32 + 16 j + l % 16, k = 32 kb + 8 (l / 16) + e, in three bf16 parts
+  bf16x8 b1[2][KB], b2[2][KB], b3[2][KB];
+#pragma unroll
+  for (int j = 0; j < 2; ++j) {
+    const int gn = n0 + wn * 32 + j * 16 + (lane & 15);
+#pragma unroll
+    for (int kb = 0; kb < KB; ++kb)
+#pragma unroll
+      for (int e = 0; e < 8; ++e) {
+        const int kk = kb * 32 + (lane >> 4) * 8 + e;
+        float w = 0.0f;
+        if (kk < K) {
+          if (gn < N) w = Wt[size_t(kk) * N + gn];
+          else if (gn < NG) w = qp.wg[size_t(kk) * qp.ng + (gn - N)];
+        }
+        __bf16 x1, x2, x3;
+        split3_bf16(w, x1, x2, x3);
+        b1[j][kb][e] = x1;
+        b2[j][kb][e] = x2;
+        b3[j][kb][e] = x3;
+      }
+  }
+  // per column: taps on frames t, t-1, t-2, t-3 (zero beyond kt), projection bias, conv bias;
+  // gate_proj columns: no taps, their bias
+  for (int cl = tid; cl < TN; cl += NT) {
+    const int gn = n0 + cl;
+    float* e = &qcw[cl * 8];
+#pragma unroll
+    for (int d = 0; d < 8; ++d) e[d] = 0.0f;
+    if (gn < N) {
+      const int blk = gn / C, c = gn % C;
+#pragma unroll
+      for (int d = 0; d <= KH; ++d) e[d] = d < qp.kt ? qp.w[blk][(qp.kt - 1 - d) * C + c] : 0.0f;
+      e[4] = bias[gn];
+      e[5] = qp.kt > 0 ? qp.b[blk][c] : 0.0f;
+    } else if (gn < NG) {
+      e[4] = qp.bg[gn - N];
+    }
+  }
+  // per lane and column tile j: the store offset within a frame's planes of qkv (eo) or gv (eg),
+  // kDrop where the column is not in that output; block 0 q, 1 k, 2 v, 3 gate_proj; the column's
+  // channel among the 2C per-channel input-gate planes
+  unsigned eo[2], eg[2];
+  int eblk[2], egch[2];
+#pragma unroll
+  for (int j = 0; j < 2; ++j) {
+    const int gn = n0 + wn * 32 + j * 16 + (lane & 15);
+    const unsigned l4 = unsigned(lane >> 4) * 4u;
+    const bool live = gn < NG, gcol = gn >= N;
+    const int blk = live ? (gcol ? 3 : gn / C) : 0;
+    eblk[j] = blk;
+    egch[j] = (blk == 1 || blk == 2) ? gn - C : 0;
+    eo[j] = (live && !gcol) ? (unsigned(gn) * unsigned(HW) + l4) * sizeof(TO) : kDrop;
+    eg[j] = (live && gcol) ? (unsigned(gn - N) * unsigned(HW) + l4) * sizeof(TO) : kDrop;
+  }
+
+  // A rows of tile (seq, t): pixels pb TM .. pb TM + TM - 1 of frame b T + t, channels-last
+  float4 pf[PF];
+  float2 gpf = make_float2(0.f, 0.f);
+  const bool tile_gates = qp.gate_mode == 1 || qp.gate_mode == 2;
+  auto fetch = [&](int seq, int t) {
+    const int b = seq / tpf, pb = seq % tpf;
+    const size_t fr = size_t(b) * T + t, row0 = fr * HW + size_t(pb) * TM;
+#pragma unroll
+    for (int i = 0; i < PF; ++i) {
+      const int f = i * NT + tid;
+      const int r = f / (KMAX / 4), k4 = (f % (KMAX / 4)) * 4;
+      float4 v = make_float4(0.f, 0.f, 0.f, 0.f);
+      if (k4 < K) {
+        if constexpr (A1_ONLY) {
+          const uint2 raw = *reinterpret_cast<const uint2*>(A + (row0 + r) * K + k4);
+          v = make_float4(__uint_as_float(raw.x), __uint_as_float(raw.y), 0.f, 0.f);
+        } else {
+          v = ld4(A, (row0 + r) * K + k4);
+        }
+      }
+      pf[i] = v;
+    }
+    if (tile_gates && tid < TM)
+      gpf = qp.gate_mode == 1 ? static_cast<const float2*>(qp.gates)[fr * HW + size_t(pb) * TM + tid]
+                              : static_cast<const float2*>(qp.gates)[fr];
+  };
+  auto stash = [&]() {
+#pragma unroll
+    for (int i = 0; i < PF; ++i) {
+      const int f = i * NT + tid;
+      const int r = f / (KMAX / 4), k4 = (f % (KMAX / 4)) * 4;
+      const int o = r * KP + k4;
+      if constexpr (A1_ONLY) {
+        *reinterpret_cast<uint2*>(&A1[o]) = make_uint2(__float_as_uint(pf[i].x), __float_as_uint(pf[i].y));
+      } else {
+        const float x[4] = {pf[i].x, pf[i].y, pf[i].z, pf[i].w};
+        bf16x4 v1, v2, v3;
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+          __bf16 x1, x2, x3;
+          split3_bf16(x[e], x1, x2, x3);
+          v1[e] = x1;
+          v2[e] = x2;
+          v3[e] = x3;
+        }
+        *reinterpret_cast<bf16x4*>(&A1[o]) = v1;
+        *reinterpret_cast<bf16x4*>(&A2[o]) = v2;
+        *reinterpret_cast<bf16x4*>(&A3[o]) = v3;
+      }
+    }
+    if (tile_gates && tid < TM) gsh[tid] = gpf;
+  };
+
+  // pre-conv projections (with bias) of the lane's elements on frames t-1, t-2, t-3
+  floatx4 h1[MI][2], h2[MI][2], h3[MI][2];
+  int seq = blockIdx.x, t = 0;
+  if (seq < nseq) fetch(seq, 0);
+  while (seq < nseq) {
+    __syncthreads();            // the previous tile is done with Asm and gsh (and qcw is staged)
+    stash();
+    __syncthreads();
+    int nt = t + 1, ns = seq;
+    if (nt == T) {
+      nt = 0;
+      ns += gridDim.x;
+    }
+    if (ns < nseq) fetch(ns, nt);
+    if (t == 0) {
+#pragma unroll
+      for (int i = 0; i < MI; ++i)
+#pragma unroll
+        for (int j = 0; j < 2; ++j) h1[i][j] = h2[i][j] = h3[i][j] = floatx4{0.f, 0.f, 0.f, 0.f};
+    }
+
+    floatx4 acc[MI][2];
+#pragma unroll
+    for (int i = 0; i < MI; ++i) acc[i][0] = acc[i][1] = floatx4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int kb = 0; kb < KB; ++kb) {
+      if (kb * 32 >= K) break;
+      const int koff = kb * 32 + (lane >> 4) * 8;
+#pragma unroll
+      for (int i = 0; i < MI; ++i) {
+        const int o = (i * 16 + (lane & 15)) * KP + koff;
+        const bf16x8 a1 = *reinterpret_cast<const bf16x8*>(&A1[o]);
+        if constexpr (A1_ONLY) {
+#pragma unroll
+          for (int j = 0; j < 2; ++j) {
+            floatx4 c = acc[i][j];
+            c = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a1, b3[j][kb], c, 0, 0, 0);
+            c = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a1, b2[j][kb], c, 0, 0, 0);
+            acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a1, b1[j][kb], c, 0, 0, 0);
+          }
+        } else {
+          const bf16x8 a2 = *reinterpret_cast<const bf16x8*>(&A2[o]);
+          const bf16x8 a3 = *reinterpret_cast<const bf16x8*>(&A3[o]);
+#pragma unroll
+          for (int j = 0; j < 2; ++j) {
+            floatx4 c = acc[i][j];
+            c = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a3, b1[j][kb], c, 0, 0, 0);   // small terms first
+            c = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a2, b2[j][kb], c, 0, 0, 0);
+            c = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a1, b3[j][kb], c, 0, 0, 0);
+            c = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a2, b1[j][kb], c, 0, 0, 0);
+            c = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a1, b2[j][kb], c, 0, 0, 0);
+            acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a1, b1[j][kb], c, 0, 0, 0);
+          }
+        }
+      }
+    }
+
+    // epilogue: lane holds pixels 16 i + 4 (lane / 16) + r of column lane % 16 of column tile j
+    const int b = seq / tpf, pb = seq % tpf;
+    const size_t fr = size_t(b) * T + t;
+    const __amdgpu_buffer_rsrc_t ro = make_rsrc(out + fr * N * HW, unsigned(N) * unsigned(HW) * sizeof(TO));
+    const __amdgpu_buffer_rsrc_t rg =
+        make_rsrc(static_cast<TO*>(qp.gv) + fr * qp.ng * HW, unsigned(qp.ng) * unsigned(HW) * sizeof(TO));
+    const unsigned pxo = unsigned(pb * TM) * sizeof(TO);
+#pragma unroll
+    for (int j = 0; j < 2; ++j) {
+      const int cl = wn * 32 + j * 16 + (lane & 15);
+      const int blk = eblk[j];
+      const float4 w4 = *reinterpret_cast<const float4*>(&qcw[cl * 8]);
+      const float2 bb2 = *reinterpret_cast<const float2*>(&qcw[cl * 8 + 4]);
+      const float bv = bb2.x, bt = bb2.y;
+      // every lane issues the same stores: a lane whose column is in neither output has both offsets
+      // at kDrop, and the gv store with no gate columns hits an empty range
+      auto store = [&](int i, const float* v) {
+        const unsigned po = pxo + unsigned(i * 16) * sizeof(TO);
+        bst4(ro, eo[j] + po, v, out);
+        bst4(rg, eg[j] + po, v, out);
+      };
+      if (blk == 3) {
+#pragma unroll
+        for (int i = 0; i < MI; ++i) {
+          float v[4];
+#pragma unroll
+          for (int r = 0; r < 4; ++r) {
+            const float x = acc[i][j][r] + bv;
+            const float sg = __builtin_amdgcn_rcpf(1.0f + __expf(-x));   // as the plain projection's epilogue
+            v[r] = qp.gact == 1 ? x * sg : sg;
+          }
+          store(i, v);
+        }
+      } else {
+        const bool gk = blk == 1, gated = blk != 0;
+#pragma unroll
+        for (int i = 0; i < MI; ++i) {
+          float v[4];
+#pragma unroll
+          for (int r = 0; r < 4; ++r) {
+            const float x = acc[i][j][r] + bv;
+            float y = x;
+            if (qp.kt > 0) {
+              // the tiled epilogue's order: tap 0 and the conv bias, then the taps on t-3, t-2, t-1
+              // (frames before the first are the zero padding, held as zeros)
+              float o = fmaf(w4.x, x, bt);
+              o = fmaf(w4.w, h3[i][j][r], o);
+              o = fmaf(w4.z, h2[i][j][r], o);
+              o = fmaf(w4.y, h1[i][j][r], o);
+              y = o * __builtin_amdgcn_rcpf(1.0f + __expf(-o));   // SiLU as gdn_qkv_post computes it
+            }
+            h3[i][j][r] = h2[i][j][r];
+            h2[i][j][r] = h1[i][j][r];
+            h1[i][j][r] = x;
+            v[r] = y;
+          }
+          if (tile_gates) {
+            const float2* gp = gsh + i * 16 + (lane >> 4) * 4;
+#pragma unroll
+            for (int r = 0; r < 4; ++r) {
+              float2 q = gp[r];   // loaded for every lane, then selected
+              asm volatile("" : "+v"(q.x), "+v"(q.y));
+              v[r] *= gated ? (gk ? q.x : q.y) : 1.0f;
+            }
+          } else if (qp.gate_mode == 3 && gated) {
+            const float4 gg = *reinterpret_cast<const float4*>(
+                static_cast<const float*>(qp.gates) + (fr * 2 * C + size_t(egch[j])) * HW + size_t(pb) * TM + i * 16 +
+                (lane >> 4) * 4);
+            v[0] *= gg.x;
+            v[1] *= gg.y;
+            v[2] *= gg.z;
+            v[3] *= gg.w;
+          }
+          store(i, v);
+        }
+      }
+    }
+    seq = ns;
+    t = nt;
+  }
+}
+
 // GDN qkv projection with the short convolution, SiLU and input gates fused
 // into the epilogue (persistent kernel, tiles of 128 / T pixels x T frames);
 // returns false when the shape has no fused variant (the caller then runs
@@ -1415,7 +1739,7 @@ static void launch_qkv_fused(const void* X, int M, int K, int N, const float* W,
   // sequence of pixel blocks are resident together: the grid is sized so that every workgroup
   // fits at once, and ids x and x + gridDim.x land on the same XCD, so the second block's A
   // rows come from L2 (C3: 7.17 -> 6.59 ms against one grid of column block 0 before block 1)
-  const int cb = (N + 127) / 128;
+  const int cb = (N + qp.ng + 127) / 128;
   const int slots = (2 * cu_count()) / cb > 0 ? (2 * cu_count()) / cb : 1;
   const int pbs = (tiles / nch + 1) / 2;
   const dim3 grid(unsigned(pbs < slots ? pbs : slots), unsigned(cb));
@@ -1428,8 +1752,6 @@ template <class TI, class TO>
 static bool qkv_fused_t(const void* X, int T, int M, int K, int N, const float* W, const float* b, int HW, void* out,
                         const QkvPost& qp, hipStream_t s) {
   switch (T) {
-    case 1: launch_qkv_fused<1, false, TI, TO>(X, M, K, N, W, b, HW, out, qp, s); return true;
-    case 2: launch_qkv_fused<2, false, TI, TO>(X, M, K, N, W, b, HW, out, qp, s); return true;
     case 4: launch_qkv_fused<4, false, TI, TO>(X, M, K, N, W, b, HW, out, qp, s); return true;
     case 8: launch_qkv_fused<8, false, TI, TO>(X, M, K, N, W, b, HW, out, qp, s); return true;
     default:
@@ -1439,21 +1761,55 @@ static bool qkv_fused_t(const void* X, int T, int M, int K, int N, const float* 
   }
 }
 
-// T in {1, 2, 4} (one chunk; taps beyond the third earlier frame only meet the zero padding),
-// or a multiple of 8 with kt <= 4 (the epilogue applies the taps on frames t .. t - 3; chunks of
-// 8 frames carry 3)
-bool gdn_qkv_fused_supported(int T, int HW, int K, int kt) {
-  const bool t_ok = T == 1 || T == 2 || T == 4 || (T % 8 == 0 && kt <= 4);
+// The frame-sequential kernel: any T with kt <= 4, or T <= 4 (the taps on frames before the third
+// earlier one only meet the zero padding); pixel blocks of 64
+static bool qkv_fseq_supported(int T, int HW, int K, int kt) {
+  return (kt <= 4 || T <= 4) && K <= kPersistMaxK && K % 4 == 0 && HW % kFseqTM == 0;
+}
+
+// The tiled kernel (where the frame-sequential one does not apply): T = 4 (one chunk; taps beyond
+// the third earlier frame only meet the zero padding), or a multiple of 8 with kt <= 4 (the epilogue
+// applies the taps on frames t .. t - 3; chunks of 8 frames carry 3); tiles of 128 / min(T, 8) pixels
+static bool qkv_tiled_supported(int T, int HW, int K, int kt) {
+  const bool t_ok = T == 4 || (T % 8 == 0 && kt <= 4);
   const int tp = kPersistTM / (T < 8 ? T : 8);
   return t_ok && K <= kPersistMaxK && K % 4 == 0 && HW % tp == 0;
 }
 
+bool gdn_qkv_fused_supported(int T, int HW, int K, int kt) {
+  return qkv_fseq_supported(T, HW, K, kt) || qkv_tiled_supported(T, HW, K, kt);
+}
+
+template <class TI, class TO>
+static void launch_qkv_fseq(const void* X, int B, int T, int HW, int K, int N, const float* W, const float* b,
+                            void* out, const QkvPost& qp, hipStream_t s) {
+  // (batch element, pixel block) sequences; the column blocks of one sequence are resident together
+  // (ids x and x + gridDim.x land on the same XCD), so the second block's A rows come from L2
+  const int nseq = B * (HW / kFseqTM);
+  const int cb = (N + qp.ng + 127) / 128;
+  const int slots = (2 * cu_count()) / cb > 0 ? (2 * cu_count()) / cb : 1;
+  const dim3 grid(unsigned(nseq < slots ? nseq : slots), unsigned(cb));
+  hipLaunchKernelGGL((qkv_fseq_kernel<TI, TO>), grid, dim3(256), 0, s, static_cast<const TI*>(X), T, HW, K, N, W, b,
+                     nseq, static_cast<TO*>(out), qp);
+}
+
 hipError_t launch_gdn_qkv_proj(const void* X, int in_dtype, int B, int T, int HW, int K, int C, const float* W,
                                const float* b, int kt, const GdnShortConv& sc, int gate_mode, const void* gates,
-                               void* out, int out_dtype, hipStream_t s) {
+                               void* out, int out_dtype, hipStream_t s, const float* wg, const float* bg, int gact,
+                               void* gv) {
   const int M = B * T * HW, N = 3 * C;
-  if (gdn_qkv_fused_supported(T, HW, K, kt) && kt <= 8) {
-    QkvPost qp{{sc.w[0], sc.w[1], sc.w[2]}, {sc.b[0], sc.b[1], sc.b[2]}, kt, gate_mode, gates, T};
+  const QkvPost qp{{sc.w[0], sc.w[1], sc.w[2]}, {sc.b[0], sc.b[1], sc.b[2]}, kt, gate_mode, gates, T,
+                   wg, bg, wg ? C : 0, gact, gv};
+  // the frame-sequential kernel stores through buffer resources over one frame's planes
+  const size_t esz = out_dtype == 0 ? 4 : 2;
+  if (qkv_fseq_supported(T, HW, K, kt) && kt <= 8 && size_t(N) * HW * esz < (size_t(1) << 31)) {
+    if (in_dtype == 0 && out_dtype == 0) launch_qkv_fseq<float, float>(X, B, T, HW, K, N, W, b, out, qp, s);
+    else if (in_dtype == 0) launch_qkv_fseq<float, uint16_t>(X, B, T, HW, K, N, W, b, out, qp, s);
+    else if (out_dtype == 0) launch_qkv_fseq<uint16_t, float>(X, B, T, HW, K, N, W, b, out, qp, s);
+    else launch_qkv_fseq<uint16_t, uint16_t>(X, B, T, HW, K, N, W, b, out, qp, s);
+    return hipGetLastError();
+  }
+  if (qkv_tiled_supported(T, HW, K, kt) && kt <= 8) {
     if (in_dtype == 0 && out_dtype == 0) qkv_fused_t<float, float>(X, T, M, K, N, W, b, HW, out, qp, s);
     else if (in_dtype == 0) qkv_fused_t<float, uint16_t>(X, T, M, K, N, W, b, HW, out, qp, s);
     else if (out_dtype == 0) qkv_fused_t<uint16_t, float>(X, T, M, K, N, W, b, HW, out, qp, s);
@@ -1462,6 +1818,10 @@ hipError_t launch_gdn_qkv_proj(const void* X, int in_dtype, int B, int T, int HW
   }
   hipError_t e = launch_proj_planes(X, in_dtype, M, K, N, W, b, HW, out, nullptr, out_dtype, 0, 0, nullptr, N, s);
   if (e != hipSuccess) return e;
+  if (wg) {
+    e = launch_proj_planes(X, in_dtype, M, K, C, wg, bg, HW, gv, gv, out_dtype, gact, gact, nullptr, C, s);
+    if (e != hipSuccess) return e;
+  }
   return launch_gdn_qkv_post(out, out_dtype, B, T, C, HW, kt, sc, gate_mode, gates, s);
 }
 

@@ -396,11 +396,7 @@ def gdn_qkv_post(qkv: torch.Tensor, convs, gate_mode: int = 0, gates: Optional[t
     return qkv
 
 
-def gdn_qkv_proj(x: torch.Tensor, kernel: torch.Tensor, bias: torch.Tensor, B: int, T: int, H: int, W: int,
-                 convs, gate_mode: int = 0, gates: Optional[torch.Tensor] = None,
-                 out_dtype: Optional[torch.dtype] = None) -> torch.Tensor:
-    """qkv_proj of channels-last x (B, T, H, W, K) with the causal short conv + SiLU (convs = [q, k, v]
-    dicts or None) and the input gates on k, v fused in (cssm.py:4753-4848) -> (B, T, 3C, H, W)."""
+def _qkv_args(x, kernel, bias, B, T, H, W, convs, gate_mode, gates):
     _dev(x, "x")
     if x.dtype not in _DTYPES:
         raise ValueError(f"unsupported dtype {x.dtype}")
@@ -412,7 +408,6 @@ def gdn_qkv_proj(x: torch.Tensor, kernel: torch.Tensor, bias: torch.Tensor, B: i
     Kk, N = kernel.shape
     if Kk != K or bias.shape != (N,) or N % 3:
         raise ValueError(f"kernel {tuple(kernel.shape)} / bias {tuple(bias.shape)} do not match K={K}, N=3C")
-    C = N // 3
     kt = 0
     kern = cb = None
     if convs is not None:
@@ -425,11 +420,43 @@ def gdn_qkv_proj(x: torch.Tensor, kernel: torch.Tensor, bias: torch.Tensor, B: i
     if gate_mode:
         _dev(gates, "gates", torch.float32)
         gp = gates.data_ptr()
+    return K, N // 3, kt, kern, cb, gp
+
+
+def gdn_qkv_proj(x: torch.Tensor, kernel: torch.Tensor, bias: torch.Tensor, B: int, T: int, H: int, W: int,
+                 convs, gate_mode: int = 0, gates: Optional[torch.Tensor] = None,
+                 out_dtype: Optional[torch.dtype] = None) -> torch.Tensor:
+    """qkv_proj of channels-last x (B, T, H, W, K) with the causal short conv + SiLU (convs = [q, k, v]
+    dicts or None) and the input gates on k, v fused in (cssm.py:4753-4848) -> (B, T, 3C, H, W)."""
+    K, C, kt, kern, cb, gp = _qkv_args(x, kernel, bias, B, T, H, W, convs, gate_mode, gates)
     od = out_dtype or x.dtype
-    out = torch.empty((B, T, N, H, W), dtype=od, device=x.device)
+    out = torch.empty((B, T, 3 * C, H, W), dtype=od, device=x.device)
     _lib.call("cssm_gdn_qkv_proj", x.data_ptr(), _DTYPES[x.dtype], B, T, H, W, K, C, kernel.data_ptr(),
               bias.data_ptr(), kt, kern, cb, gate_mode, gp, out.data_ptr(), _DTYPES[od], _stream())
     return out
+
+
+def gdn_qkv_gate_proj(x: torch.Tensor, kernel: torch.Tensor, bias: torch.Tensor, B: int, T: int, H: int, W: int,
+                      convs, gate_mode: int, gates: Optional[torch.Tensor], gate_kernel: torch.Tensor,
+                      gate_bias: torch.Tensor, gate_act: str = "silu",
+                      out_dtype: Optional[torch.dtype] = None):
+    """gdn_qkv_proj and gate_proj (act SiLU or sigmoid, cssm.py:4853-4859) of the same x in one call
+    -> (qkv (B, T, 3C, H, W), gv (B, T, C, H, W)); where the qkv projection runs fused the gate columns
+    ride in the same launch, so x is read once."""
+    K, C, kt, kern, cb, gp = _qkv_args(x, kernel, bias, B, T, H, W, convs, gate_mode, gates)
+    _dev(gate_kernel, "gate_kernel", torch.float32)
+    _dev(gate_bias, "gate_bias", torch.float32)
+    if tuple(gate_kernel.shape) != (K, C) or tuple(gate_bias.shape) != (C,):
+        raise ValueError(f"gate kernel {tuple(gate_kernel.shape)} / bias {tuple(gate_bias.shape)} are not ({K}, {C})")
+    if gate_act not in ("silu", "sigmoid"):
+        raise ValueError(f"gate_act {gate_act!r}")
+    od = out_dtype or x.dtype
+    out = torch.empty((B, T, 3 * C, H, W), dtype=od, device=x.device)
+    gv = torch.empty((B, T, C, H, W), dtype=od, device=x.device)
+    _lib.call("cssm_gdn_qkv_gate_proj", x.data_ptr(), _DTYPES[x.dtype], B, T, H, W, K, C, kernel.data_ptr(),
+              bias.data_ptr(), kt, kern, cb, gate_mode, gp, gate_kernel.data_ptr(), gate_bias.data_ptr(),
+              _ACTS[gate_act], out.data_ptr(), gv.data_ptr(), _DTYPES[od], _stream())
+    return out, gv
 
 
 def gdn_qkv_fused(T: int, H: int, W: int, K: int, kt: int) -> bool:

@@ -342,10 +342,13 @@ int cssm_gdn_qkv_post(void* qkv, int dtype, int B, int T, int C, int H, int W, i
  * and input gates of cssm_gdn_qkv_post fused into the GEMM's epilogue:
  *   qkv = post(proj(x)),  proj = cssm_proj_planes with N = 3C (identity act).
  * Replaces cssm.py:4753-4758 (qkv_proj), :4763-4780 and :4844-4848 in one pass
- * over qkv instead of three.  Fused when cssm_gdn_qkv_fused(T, H, W, K, kt):
- * tiles of 128 / T' pixels x T' frames, T' = min(T, 8), T in {1, 2, 4} or a
- * multiple of 8 with kt <= 4 (chunks of 8 frames carry 3 to the next), K <= 64,
- * H*W a multiple of 128 / T'; otherwise it runs the two calls it replaces, with the same
+ * over qkv instead of three.  Fused when cssm_gdn_qkv_fused(T, H, W, K, kt)
+ * (K <= 64, K % 4 == 0): any T with kt <= 4 or T <= 4 and H*W a multiple of 64
+ * (tiles of 64 pixels of one frame, a workgroup walking the frames in order with
+ * the three previous frames' projections in registers; 3C*H*W elements of
+ * out_dtype under 2^31 bytes); else T = 4, or a multiple of 8 with kt <= 4, and
+ * H*W a multiple of 128 / min(T, 8) (tiles of pixels x frames, chunks of 8 frames
+ * carrying 3); otherwise it runs the two calls it replaces, with the same
  * results (fp32 qkv; a bf16 qkv then holds the projection in bf16 before the
  * convolution, where the fused path keeps it in fp32).
  *   x      (B, T, H*W, K) channels-last of in_dtype
@@ -358,6 +361,24 @@ int cssm_gdn_qkv_proj(const void* x, int in_dtype, int B, int T, int H, int W, i
                       const float* kernel, const float* bias, int kt, const float* const* conv_kernel,
                       const float* const* conv_bias, int gate_mode, const void* gates, void* qkv,
                       int out_dtype, void* stream);
+
+/*
+ * cssm_gdn_qkv_proj and gate_proj of the same x in one call: besides qkv,
+ *   gv = act(x gate_kernel + gate_bias)   (cssm.py:4853-4859, act 1 SiLU, 2 sigmoid)
+ * where the layer has no qkv conv (qkv_conv_size <= 1, cssm.py:4740 / :4754),
+ * so both projections read the layer input x_flat.  When the qkv projection runs fused, the C
+ * gate columns are C more columns of the same launch (no conv, no input gate):
+ * x is read once; otherwise a second projection computes gv.  Results equal
+ * cssm_gdn_qkv_proj + cssm_proj_planes(act) on the same x.
+ *   gate_kernel (K, C) [gate_proj/kernel], gate_bias (C) [gate_proj/bias]
+ *   gv          (B, T, C, H, W) plane-major of out_dtype out, aligned as qkv
+ * Other arguments and requirements as cssm_gdn_qkv_proj.
+ */
+int cssm_gdn_qkv_gate_proj(const void* x, int in_dtype, int B, int T, int H, int W, int K, int C,
+                           const float* kernel, const float* bias, int kt, const float* const* conv_kernel,
+                           const float* const* conv_bias, int gate_mode, const void* gates,
+                           const float* gate_kernel, const float* gate_bias, int gate_act, void* qkv, void* gv,
+                           int out_dtype, void* stream);
 
 /* 1 if cssm_gdn_qkv_proj runs fused for (T, H, W, K, kt), else 0 (it then runs two kernels). */
 int cssm_gdn_qkv_fused(int T, int H, int W, int K, int kt);

@@ -120,5 +120,17 @@ def test_projection_entry_points_reject_misaligned_pointers():
     # gdn_qkv_proj: x
     assert lib.cssm_gdn_qkv_proj(p + 4, f32, 1, 2, 4, 4, K, 4, p, p, 0, None, None, 0, None, p, f32, None) == -5
     assert b"x / qkv" in lib.cssm_last_error()
+    # gdn_qkv_gate_proj: x, gv; a missing gate bias / output or an unknown act before any GPU work
+    assert lib.cssm_gdn_qkv_gate_proj(p + 4, f32, 1, 2, 4, 4, K, 4, p, p, 0, None, None, 0, None, p, p, 1, p, p,
+                                      f32, None) == -5
+    assert lib.cssm_gdn_qkv_gate_proj(p, f32, 1, 2, 4, 4, K, 4, p, p, 0, None, None, 0, None, p, p, 1, p, p + 4,
+                                      f32, None) == -5
+    assert b"gv" in lib.cssm_last_error()
+    assert lib.cssm_gdn_qkv_gate_proj(p, f32, 1, 2, 4, 4, K, 4, p, p, 0, None, None, 0, None, p, None, 1, p, p,
+                                      f32, None) == -1
+    assert lib.cssm_gdn_qkv_gate_proj(p, f32, 1, 2, 4, 4, K, 4, p, p, 0, None, None, 0, None, None, p, 1, p, p,
+                                      f32, None) == -1
+    assert lib.cssm_gdn_qkv_gate_proj(p, f32, 1, 2, 4, 4, K, 4, p, p, 0, None, None, 0, None, p, p, 0, p, p,
+                                      f32, None) == -4
     # gdn_proj_out: out
     assert lib.cssm_gdn_proj_out(p, p, f32, F, HW, K, N, 0, None, None, p, p, p + 4, f32, None) == -5

@@ -193,12 +193,14 @@ def test_gdn_qkv_post_matches_oracle(mods, kt):
     assert rel_err(to_np(got), ref) < 1e-5
 
 
-# (B, T, H, W, K, C): T in {1, 2, 4} with H*W a multiple of 128 / T runs fused (one kernel), and so
-# does T a multiple of 8 (chunks of 8 frames carrying 3) for kt <= 4; the rest (T = 3; H*W = 64 at
-# T = 1; kt = 6 at T = 8 or 16) through proj_planes + qkv_post
+# (B, T, H, W, K, C): with H*W a multiple of 64 and kt <= 4 (or T <= 4) one frame-sequential kernel
+# (any T); else T = 4 or a multiple of 8 (chunks of 8 frames carrying 3, kt <= 4) with H*W a
+# multiple of 128 / min(T, 8) the tiled kernel ((1, 4, 4, 8): T = 4; (1, 8, 4, 4): T = 8;
+# (2, 24, 4, 4): chunks); the rest (kt = 6 at T = 8 or 16; T = 3 at 4 x 4) through proj_planes +
+# qkv_post
 QKV_CASES = [(2, 8, 16, 16, 64, 16), (1, 4, 8, 8, 32, 8), (3, 2, 8, 8, 64, 12), (2, 1, 16, 8, 48, 8),
              (2, 3, 8, 8, 64, 16), (1, 16, 8, 8, 32, 8), (2, 1, 8, 8, 64, 8), (1, 32, 8, 8, 64, 8),
-             (2, 24, 4, 4, 32, 8)]
+             (2, 24, 4, 4, 32, 8), (1, 4, 4, 8, 32, 8), (1, 8, 4, 4, 32, 8), (2, 3, 4, 4, 32, 8)]
 
 
 @pytest.mark.parametrize("shape", QKV_CASES)
@@ -252,6 +254,56 @@ def test_gdn_qkv_proj_matches_two_step(mods, shape, kt, gate_mode):
     gb = S.gdn_qkv_proj(xb, _dev(Wt), _dev(b), B, T, H, W, dc, gate_mode, dg, out_dtype=torch.bfloat16)
     bar = 5e-3 if S.gdn_qkv_fused(T, H, W, K, kt) else 4e-2
     assert bf16_excess_err(to_np(gb.float()), oracle(to_np(xb.float()))) < bar
+
+
+@pytest.mark.parametrize("shape", [(2, 8, 16, 16, 64, 16), (1, 4, 8, 8, 32, 8), (2, 1, 16, 8, 48, 8),
+                                   (2, 3, 8, 8, 64, 16), (1, 32, 8, 8, 64, 8), (2, 2, 8, 8, 64, 40),
+                                   (1, 16, 8, 8, 64, 64)])
+@pytest.mark.parametrize("kt,gate_mode,gact", [(4, 1, "silu"), (0, 0, "sigmoid"), (3, 3, "silu"), (6, 2, "silu")])
+def test_gdn_qkv_gate_proj_matches_separate_calls(mods, shape, kt, gate_mode, gact):
+    """qkv and gate_proj in one call equal gdn_qkv_proj and proj_planes(act) on the same x (qkv bit for bit,
+    the gate columns to fp32 rounding) and the oracle act(x Wg + bg), fused (gate columns in the qkv
+    launch) and not (T = 3, kt = 6: a second projection); bf16 in / out against the oracle."""
+    _, S = mods
+    B, T, H, W, K, C = shape
+    fused = S.gdn_qkv_fused(T, H, W, K, kt)
+    print_case(test="gdn_qkv_gate_proj", shape=shape, kt=kt, gate_mode=gate_mode, gact=gact, fused=fused)
+    rng = np.random.default_rng(21)
+    x = rng.standard_normal((B, T, H, W, K))
+    Wt = rng.standard_normal((K, 3 * C)) / np.sqrt(K)
+    b = rng.standard_normal(3 * C) * 0.1
+    Wg = rng.standard_normal((K, C)) / np.sqrt(K)
+    bg = rng.standard_normal(C) * 0.1
+    convs = [{"kernel": rng.standard_normal((kt, 1, C)) / 2, "bias": rng.standard_normal(C) * 0.1}
+             for _ in range(3)] if kt else None
+    gates = None
+    if gate_mode == 1:
+        gates = 1.0 / (1.0 + np.exp(-rng.standard_normal((B, T, H * W, 2))))
+    elif gate_mode == 2:
+        gates = 1.0 / (1.0 + np.exp(-rng.standard_normal((B, T, 2))))
+    elif gate_mode == 3:
+        gates = 1.0 / (1.0 + np.exp(-rng.standard_normal((B, T, 2 * C, H, W))))
+    dc = [_tree(c) for c in convs] if convs else None
+    dg = _dev(gates) if gates is not None else None
+    qkv, gv = S.gdn_qkv_gate_proj(_dev(x), _dev(Wt), _dev(b), B, T, H, W, dc, gate_mode, dg, _dev(Wg), _dev(bg),
+                                  gact, out_dtype=torch.float32)
+    assert tuple(gv.shape) == (B, T, C, H, W)
+    ref_qkv = S.gdn_qkv_proj(_dev(x), _dev(Wt), _dev(b), B, T, H, W, dc, gate_mode, dg, out_dtype=torch.float32)
+    assert torch.equal(qkv, ref_qkv)
+    ref_gv = S.proj_planes(_dev(x), _dev(Wg), _dev(bg), B * T, H * W, act=gact, out_dtype=torch.float32)
+    assert rel_err(to_np(gv).reshape(B * T, C, H * W), to_np(ref_gv)) < 1e-6
+
+    def oracle_gv(xx):
+        z = xx.reshape(-1, K) @ Wg + bg
+        z = O.silu(z) if gact == "silu" else 1.0 / (1.0 + np.exp(-z))
+        return z.reshape(B, T, H, W, C).transpose(0, 1, 4, 2, 3)
+    assert rel_err(to_np(gv), oracle_gv(x)) < 1e-5
+    xb = _dev(x, torch.bfloat16)
+    qb, gb = S.gdn_qkv_gate_proj(xb, _dev(Wt), _dev(b), B, T, H, W, dc, gate_mode, dg, _dev(Wg), _dev(bg), gact,
+                                 out_dtype=torch.bfloat16)
+    assert torch.equal(qb, S.gdn_qkv_proj(xb, _dev(Wt), _dev(b), B, T, H, W, dc, gate_mode, dg,
+                                          out_dtype=torch.bfloat16))
+    assert bf16_excess_err(to_np(gb.float()), oracle_gv(to_np(xb.float()))) < 5e-3
 
 
 # --------------------------------------------------------- spectral core
