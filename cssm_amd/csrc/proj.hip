@@ -1457,24 +1457,27 @@ hipError_t launch_proj_in(const void* X, int in_dtype, int M, int K, int N, cons
 // them (same loads and stores with no MFMA or epilogue math: same time).
 // ---------------------------------------------------------------------------
 constexpr int kFseqTM = 64;
-template <class TI, class TO>
-__global__ void __launch_bounds__(256, 2)
+// CBW 128-column blocks per workgroup (4 waves each) share one staged A tile: A is read from HBM
+// once for all of them (separate workgroups per column block drift apart and miss in L2)
+template <int CBW, class TI, class TO>
+__global__ void __launch_bounds__(256 * CBW, 2 / CBW)
 qkv_fseq_kernel(const TI* __restrict__ A, int T, int HW, int K, int N, const float* __restrict__ Wt,
                 const float* __restrict__ bias, int nseq, TO* __restrict__ out, QkvPost qp) {
-  constexpr int TM = kFseqTM, TN = 128, NT = 256, MI = TM / 16, KMAX = 64, KB = KMAX / 32, KP = KMAX + 8;
+  constexpr int TM = kFseqTM, TN = 128, NT = 256 * CBW, MI = TM / 16, KMAX = 64, KB = KMAX / 32, KP = KMAX + 8;
   constexpr bool A1_ONLY = sizeof(TI) == 2;      // bf16 A is exactly its first bf16 part
   constexpr int APL = A1_ONLY ? 1 : 3;
   constexpr int PF = TM * KMAX / 4 / NT;         // groups of 4 consecutive k per thread and tile
   constexpr int KH = 3;                          // earlier frames the conv reads
   constexpr unsigned kDrop = 0x80000000u;        // a buffer offset past every resource's range
   __shared__ __attribute__((aligned(16))) __bf16 Asm[APL * TM * KP];
-  __shared__ __attribute__((aligned(16))) float qcw[TN * 8];
+  __shared__ __attribute__((aligned(16))) float qcw[CBW * TN * 8];
   __shared__ float2 gsh[TM];
   __bf16* const A1 = Asm;
   __bf16* const A2 = A1 + (APL > 1 ? TM * KP : 0);
   __bf16* const A3 = A2 + (APL > 1 ? TM * KP : 0);
-  const int tid = threadIdx.x, lane = tid & 63, wn = tid >> 6;
-  const int n0 = blockIdx.y * TN, C = N / 3, NG = N + qp.ng;
+  const int tid = threadIdx.x, lane = tid & 63, wn = (tid >> 6) & 3, cq = tid >> 8;
+  const int nb = blockIdx.y * CBW * TN;          // the workgroup's first column
+  const int n0 = nb + cq * TN, C = N / 3, NG = N + qp.ng;   // this wave's column block
   const int tpf = HW / TM;                       // pixel blocks per frame
 
   // B fragments: lane l holds column wn 32 + 16 j + l % 16, k = 32 kb + 8 (l / 16) + e, in three bf16 parts
@@ -1501,8 +1504,8 @@ qkv_fseq_kernel(const TI* __restrict__ A, int T, int HW, int K, int N, const flo
   }
   // per column: taps on frames t, t-1, t-2, t-3 (zero beyond kt), projection bias, conv bias;
   // gate_proj columns: no taps, their bias
-  for (int cl = tid; cl < TN; cl += NT) {
-    const int gn = n0 + cl;
+  for (int cl = tid; cl < CBW * TN; cl += NT) {
+    const int gn = nb + cl;
     float* e = &qcw[cl * 8];
 #pragma unroll
     for (int d = 0; d < 8; ++d) e[d] = 0.0f;
@@ -1652,7 +1655,7 @@ qkv_fseq_kernel(const TI* __restrict__ A, int T, int HW, int K, int N, const flo
     const unsigned pxo = unsigned(pb * TM) * sizeof(TO);
 #pragma unroll
     for (int j = 0; j < 2; ++j) {
-      const int cl = wn * 32 + j * 16 + (lane & 15);
+      const int cl = cq * TN + wn * 32 + j * 16 + (lane & 15);
       const int blk = eblk[j];
       const float4 w4 = *reinterpret_cast<const float4*>(&qcw[cl * 8]);
       const float2 bb2 = *reinterpret_cast<const float2*>(&qcw[cl * 8 + 4]);
@@ -1783,14 +1786,22 @@ bool gdn_qkv_fused_supported(int T, int HW, int K, int kt) {
 template <class TI, class TO>
 static void launch_qkv_fseq(const void* X, int B, int T, int HW, int K, int N, const float* W, const float* b,
                             void* out, const QkvPost& qp, hipStream_t s) {
-  // (batch element, pixel block) sequences; the column blocks of one sequence are resident together
-  // (ids x and x + gridDim.x land on the same XCD), so the second block's A rows come from L2
+  // (batch element, pixel block) sequences; column blocks of 128 in pairs per workgroup (one when
+  // a single block holds every column), two workgroups' worth of waves per CU
   const int nseq = B * (HW / kFseqTM);
   const int cb = (N + qp.ng + 127) / 128;
-  const int slots = (2 * cu_count()) / cb > 0 ? (2 * cu_count()) / cb : 1;
-  const dim3 grid(unsigned(nseq < slots ? nseq : slots), unsigned(cb));
-  hipLaunchKernelGGL((qkv_fseq_kernel<TI, TO>), grid, dim3(256), 0, s, static_cast<const TI*>(X), T, HW, K, N, W, b,
-                     nseq, static_cast<TO*>(out), qp);
+  if (cb == 1) {
+    const int slots = 2 * cu_count();
+    const dim3 grid(unsigned(nseq < slots ? nseq : slots), 1u);
+    hipLaunchKernelGGL((qkv_fseq_kernel<1, TI, TO>), grid, dim3(256), 0, s, static_cast<const TI*>(X), T, HW, K, N,
+                       W, b, nseq, static_cast<TO*>(out), qp);
+    return;
+  }
+  const int cy = (cb + 1) / 2;
+  const int slots = cu_count() / cy > 0 ? cu_count() / cy : 1;
+  const dim3 grid(unsigned(nseq < slots ? nseq : slots), unsigned(cy));
+  hipLaunchKernelGGL((qkv_fseq_kernel<2, TI, TO>), grid, dim3(512), 0, s, static_cast<const TI*>(X), T, HW, K, N, W,
+                     b, nseq, static_cast<TO*>(out), qp);
 }
 
 hipError_t launch_gdn_qkv_proj(const void* X, int in_dtype, int B, int T, int HW, int K, int C, const float* W,
