@@ -343,7 +343,8 @@ proj_persist_kernel(const TI* __restrict__ A, int M, int K, int N, const float* 
   __bf16* const A1 = reinterpret_cast<__bf16*>(As);
   __bf16* const A2 = A1 + TM * KP;   // (SPLIT, fp32 A only)
   __bf16* const A3 = A2 + TM * KP;
-  __shared__ float rowsc[NORM ? 2 * TM : 1];             // per-pixel (scale, mean) of the norm
+  __shared__ float rowsc[NORM ? 2 * NT : 1];             // per-pixel partial sums, then (scale, mean) of the norm
+  __shared__ float nss[NORM ? 2 * KMAX : 1];             // the norm's per-channel scale and shift
   __shared__ float2 gsh[TT > 0 ? TM : 1];                 // qkv epilogue: the tile's input gates
   constexpr int KH = 3;                                   // qkv epilogue: frames carried to the next chunk
   __shared__ float hsh[CARRY ? KH * TN * (TM / 8) : 1];   // their projections, [frame][column][pixel]
@@ -402,6 +403,12 @@ proj_persist_kernel(const TI* __restrict__ A, int M, int K, int N, const float* 
       const int kk = i / TN, c = i % TN;
       const int gn = n0 + c;
       Bs[kk * BP + c] = (kk < K && gn < N) ? Wt[size_t(kk) * N + gn] : 0.0f;
+    }
+  }
+  if constexpr (NORM) {
+    for (int kk = tid; kk < KMAX; kk += NT) {
+      nss[2 * kk] = (ng.scale && kk < K) ? ng.scale[kk] : 1.f;
+      nss[2 * kk + 1] = (ng.shift && kk < K) ? ng.shift[kk] : 0.f;
     }
   }
   if constexpr (QCW_LDS) {
@@ -552,12 +559,38 @@ proj_persist_kernel(const TI* __restrict__ A, int M, int K, int N, const float* 
   // NORM: per-pixel statistics over the K channels of the staged tile, then
   // A[k][r] <- norm(A)[k][r] * G[k][r] in place (G from the prefetch registers)
   auto norm_gate = [&](const float4* pg) {
+    // per-pixel sums over the K channels: NT / TM threads per pixel, each over its share of the
+    // channels with four independent partial sums (not one dependent chain of K loads)
+    {
+      static_assert(!NORM || NT % TM == 0, "whole threads per pixel");
+      constexpr int TPP = NORM ? NT / TM : 1;
+      const int px = tid % TM, part = tid / TM, kc = (K + TPP - 1) / TPP;
+      const int k0 = part * kc, k1 = k0 + kc < K ? k0 + kc : K;
+      float a1[4] = {0.f, 0.f, 0.f, 0.f}, a2[4] = {0.f, 0.f, 0.f, 0.f};
+      int kk = k0;
+      for (; kk + 4 <= k1; kk += 4) {
+#pragma unroll
+        for (int q = 0; q < 4; ++q) {
+          const float v = As[(kk + q) * AP + px];
+          a1[q] += v;
+          a2[q] = fmaf(v, v, a2[q]);
+        }
+      }
+      for (; kk < k1; ++kk) {
+        const float v = As[kk * AP + px];
+        a1[0] += v;
+        a2[0] = fmaf(v, v, a2[0]);
+      }
+      rowsc[2 * tid] = (a1[0] + a1[1]) + (a1[2] + a1[3]);
+      rowsc[2 * tid + 1] = (a2[0] + a2[1]) + (a2[2] + a2[3]);
+    }
+    __syncthreads();
     if (tid < TM) {
       float s1 = 0.f, s2 = 0.f;
-      for (int kk = 0; kk < K; ++kk) {
-        const float v = As[kk * AP + tid];
-        s1 += v;
-        s2 = fmaf(v, v, s2);
+#pragma unroll
+      for (int q = 0; q < (NORM ? NT / TM : 1); ++q) {
+        s1 += rowsc[2 * (tid + q * TM)];
+        s2 += rowsc[2 * (tid + q * TM) + 1];
       }
       const float inv_k = 1.0f / float(K);
       float mean = 0.f, sc = 1.f;
@@ -567,6 +600,7 @@ proj_persist_kernel(const TI* __restrict__ A, int M, int K, int N, const float* 
         mean = s1 * inv_k;
         sc = rsqrtf(fmaxf(s2 * inv_k - mean * mean, 0.f) + 1e-6f);
       }
+      // thread tid alone reads slot tid (its own) and slots tid + q TM (q >= 1, not written here)
       rowsc[2 * tid] = sc;
       rowsc[2 * tid + 1] = mean;
     }
@@ -577,7 +611,7 @@ proj_persist_kernel(const TI* __restrict__ A, int M, int K, int N, const float* 
       const int kk = f / (TM / 4), r4 = (f % (TM / 4)) * 4;
       if (kk >= K) continue;
       float4 v = *reinterpret_cast<const float4*>(&As[kk * AP + r4]);
-      const float sk = ng.scale ? ng.scale[kk] : 1.f, bk = ng.shift ? ng.shift[kk] : 0.f;
+      const float sk = nss[2 * kk], bk = nss[2 * kk + 1];
       float* e = &v.x;
       const float* g = &pg[i].x;
 #pragma unroll
