@@ -953,13 +953,18 @@ proj_persist_kernel(const TI* __restrict__ A, int M, int K, int N, const float* 
 //   PLANE_A = false: A is channels-last (M, K), K % 4 == 0; true: plane-major (F, K, HW).
 //   OUT_SPLIT = true: plane-major output(s) as proj_in; false: channels-last (M, N).
 // ---------------------------------------------------------------------------
-template <bool PLANE_A, bool OUT_SPLIT, class TI, class TO, int TM_>
+// PX4 (plane-major A, H*W % 4 == 0, host-checked): a thread loads 4 consecutive pixels of one
+// channel plane per 16-byte load (4 channels: 4 loads) instead of one element per load, and
+// transposes them in registers for the [row][k] LDS layout: a quarter of the A load
+// instructions, which otherwise fill the wave's outstanding-load counter and stall the issue
+template <bool PLANE_A, bool OUT_SPLIT, class TI, class TO, int TM_, bool PX4 = false>
 __global__ void __launch_bounds__(256, (sizeof(TI) == 2 && !PLANE_A) ? 3 : 2)
 proj_kc_kernel(const TI* __restrict__ A, int M, int K, int N, const float* __restrict__ Wt,
                const float* __restrict__ bias, int HW, TO* __restrict__ out_lo, TO* __restrict__ out_hi,
                int act_lo, int act_hi, float* __restrict__ partial, int NH, int slots) {
   constexpr int TM = TM_, TN = 128, NT = 256, KC = 32, KP = KC + 8, MI = TM / 16;
   static_assert(TM == 64 || TM == 128, "row tiles of 64 or 128");
+  static_assert(!PX4 || PLANE_A, "4-pixel loads are for plane-major A");
   constexpr int NI = TM / 32, NKQ = 256 / TM;   // A load groups per thread; plane-major k groups
   constexpr bool A1_ONLY = sizeof(TI) == 2;      // bf16 A: one nonzero part
   // fp32 A with a bf16 output: the three products down to order 2^-16 (A1 B1 + A1 B2 + A2 B1) are far
@@ -1009,10 +1014,20 @@ proj_kc_kernel(const TI* __restrict__ A, int M, int K, int N, const float* __res
     const int last = (M - m0 < TM ? M : m0 + TM) - 1;
     const int fr0 = m0 / HW, nfr = last / HW - fr0 + 1;
     ra = make_rsrc(A + size_t(fr0) * K * HW, unsigned(nfr) * unsigned(K) * unsigned(HW) * EA);
-    const int gm = m0 + rr < M ? m0 + rr : m0;
-    a_off = unsigned(((gm / HW - fr0) * K + 4 * kq) * HW + gm % HW) * EA;
+    if constexpr (PX4) {
+      // item (4-row group rg, 4-channel group kg) of thread tid < 2 TM; a group of 4 rows lies in one
+      // frame (H*W and m0 are multiples of 4)
+      const int rg = tid % (TM / 4), kg = tid / (TM / 4);
+      const int gm = m0 + 4 * rg < M ? m0 + 4 * rg : m0;
+      a_off = unsigned(((gm / HW - fr0) * K + 4 * kg) * HW + gm % HW) * EA;
 #pragma unroll
-    for (int i = 0; i < NI; ++i) a_ok[i] = m0 + rr < M;
+      for (int i = 0; i < NI; ++i) a_ok[i] = tid < 2 * TM && m0 + 4 * rg < M;
+    } else {
+      const int gm = m0 + rr < M ? m0 + rr : m0;
+      a_off = unsigned(((gm / HW - fr0) * K + 4 * kq) * HW + gm % HW) * EA;
+#pragma unroll
+      for (int i = 0; i < NI; ++i) a_ok[i] = m0 + rr < M;
+    }
   }
   // this lane's B fragments: columns wn 32 + 16 j + lane % 16, k = chunk + 8 (lane / 16) + e
   const int kl = (lane >> 4) * 8;
@@ -1029,29 +1044,56 @@ proj_kc_kernel(const TI* __restrict__ A, int M, int K, int N, const float* __res
   // Raw A: the bf16 bits themselves for channels-last bf16 A (they are the one bf16 part), else floats.
   constexpr bool RAW16 = A1_ONLY && !PLANE_A;
   using RawA = typename std::conditional<RAW16, uint2, float4>::type;
-  RawA pa[2][NI];
+  constexpr int NA = PX4 ? 4 : NI;               // A registers per set (PX4: one per channel of the item)
+  RawA pa[2][NA];
   float pw[2][2][8];
   // A lane whose element lies outside the tensor (rows beyond M, k beyond K)
   // loads at byte offset kOut instead: beyond every resource range, so the
   // buffer load returns 0 without touching memory.
   constexpr unsigned kOut = 0x80000000u;
+  // Offsets are selected without branches: a lane's base offset is kOut where its row or column is
+  // outside the tensor, and a channel at or beyond K ORs kOut in (past every resource's range: the
+  // buffer load returns 0 without touching memory).  A select that the compiler turned into a
+  // branch around the load made it wait for every load in flight.
+  unsigned a_base[NI], b_base[2];
+#pragma unroll
+  for (int i = 0; i < NI; ++i) a_base[i] = a_ok[i] ? a_off : kOut;
+#pragma unroll
+  for (int j = 0; j < 2; ++j) b_base[j] = b_ok[j] ? b_off[j] : kOut;
+  auto past_k = [&](int k) -> unsigned { return k < K ? 0u : kOut; };
   auto fetch = [&](int k0, int s) {
-    const bool full = k0 + KC <= K;
 #pragma unroll
     for (int i = 0; i < NI; ++i) {
       if constexpr (!PLANE_A) {
-        const unsigned vo = (a_ok[i] && (full || k0 + ak < K)) ? a_off : kOut;
+        const unsigned vo = a_base[i] | past_k(k0 + ak);
         const int so = (32 * i * K + k0) * EA;
         if constexpr (RAW16)
           pa[s][i] = __builtin_bit_cast(uint2, __builtin_amdgcn_raw_buffer_load_b64(ra, int(vo), so, 0));
         else
           pa[s][i] = __builtin_bit_cast(float4, __builtin_amdgcn_raw_buffer_load_b128(ra, int(vo), so, 0));
+      } else if constexpr (PX4) {
+        // channel k0 + 4 kg + q of the item's 4 rows
+        if (i == 0) {
+          const int kg = tid / (TM / 4);
+#pragma unroll
+          for (int q = 0; q < 4; ++q) {
+            const unsigned vo = a_base[0] | past_k(k0 + 4 * kg + q);
+            const int so = (k0 + q) * HW * EA;
+            if constexpr (EA == 2) {
+              const uint2 raw = __builtin_bit_cast(uint2, __builtin_amdgcn_raw_buffer_load_b64(ra, int(vo), so, 0));
+              pa[s][q] = make_float4(__uint_as_float(raw.x << 16), __uint_as_float(raw.x & 0xffff0000u),
+                                     __uint_as_float(raw.y << 16), __uint_as_float(raw.y & 0xffff0000u));
+            } else {
+              pa[s][q] = __builtin_bit_cast(float4, __builtin_amdgcn_raw_buffer_load_b128(ra, int(vo), so, 0));
+            }
+          }
+        }
       } else {
         float v[4];
 #pragma unroll
         for (int e = 0; e < 4; ++e) {
           const int k = k0 + 4 * NKQ * i + e;   // relative to this thread's 4 kq
-          const unsigned vo = (a_ok[i] && (full || k + 4 * kq < K)) ? a_off : kOut;
+          const unsigned vo = a_base[i] | past_k(k + 4 * kq);
           const int so = k * HW * EA;
           if constexpr (EA == 2)
             v[e] = __uint_as_float(unsigned(__builtin_amdgcn_raw_buffer_load_b16(ra, int(vo), so, 0)) << 16);
@@ -1065,13 +1107,37 @@ proj_kc_kernel(const TI* __restrict__ A, int M, int K, int N, const float* __res
     for (int j = 0; j < 2; ++j)
 #pragma unroll
       for (int e = 0; e < 8; ++e) {
-        const unsigned vo = (b_ok[j] && (full || k0 + kl + e < K)) ? b_off[j] : kOut;
+        const unsigned vo = b_base[j] | past_k(k0 + kl + e);
         pw[s][j][e] = __uint_as_float(__builtin_amdgcn_raw_buffer_load_b32(rb, int(vo), (k0 + e) * N * 4, 0));
       }
   };
   // A of register set s -> the bf16 planes of LDS stage s
   auto stash = [&](int s) {
     __bf16* const planes = lds + s * STG;
+    if constexpr (PX4) {
+      if (tid < 2 * TM) {
+        const int rg = tid % (TM / 4), kg = tid / (TM / 4);
+#pragma unroll
+        for (int q = 0; q < 4; ++q) {   // row 4 rg + q: its 4 channels from the 4 loads
+          const float x[4] = {(&pa[s][0].x)[q], (&pa[s][1].x)[q], (&pa[s][2].x)[q], (&pa[s][3].x)[q]};
+          bf16x4 v1, v2, v3;
+#pragma unroll
+          for (int e = 0; e < 4; ++e) {
+            __bf16 x1, x2 = __bf16(0.0f), x3 = __bf16(0.0f);
+            if constexpr (A1_ONLY) x1 = (__bf16)x[e];   // exact for bf16 inputs
+            else split3_bf16(x[e], x1, x2, x3);
+            v1[e] = x1;
+            v2[e] = x2;
+            v3[e] = x3;
+          }
+          const int off = (4 * rg + q) * KP + 4 * kg;
+          *reinterpret_cast<bf16x4*>(planes + off) = v1;
+          if constexpr (APL >= 2) *reinterpret_cast<bf16x4*>(planes + AB + off) = v2;
+          if constexpr (APL == 3) *reinterpret_cast<bf16x4*>(planes + 2 * AB + off) = v3;
+        }
+      }
+      return;
+    }
 #pragma unroll
     for (int i = 0; i < NI; ++i) {
       const int off = PLANE_A ? rr * KP + (NKQ * i + kq) * 4 : (ar + 32 * i) * KP + ak;
@@ -1126,7 +1192,9 @@ proj_kc_kernel(const TI* __restrict__ A, int M, int K, int N, const float* __res
       // stage s holds chunk kc; every wave is done with stage s ^ 1 (chunk kc - KC)
       __syncthreads();
       split_b(s);
-      if (kc + 2 * KC < K) fetch(kc + 2 * KC, s);
+      // unconditional: a chunk past K loads zeros (every lane's offset is past its resource), and a
+      // conditional refill made the compiler wait for all loads in flight to merge the register sets
+      fetch(kc + 2 * KC, s);
       const __bf16* const Ap = lds + s * STG;
       // lane l: A rows l % 16 and B columns l % 16, k = 8 (l / 16) + 0..7
 #pragma unroll
@@ -1369,6 +1437,14 @@ static hipError_t launch_kc_tm(const void* A, int M, int K, int N, const float* 
   if (a_bytes >= (1LL << 31) || (long long)K * N * 4 >= (1LL << 31)) return hipErrorInvalidValue;
   const dim3 grid(unsigned((M + TM - 1) / TM) * unsigned((N + 127) / 128));
   const int slots = partial ? proj_in_ctx_slots(K, HW) : 0;
+  if constexpr (PLANE_A) {
+    if (HW % 4 == 0) {
+      hipLaunchKernelGGL((proj_kc_kernel<PLANE_A, OUT_SPLIT, TI, TO, TM, true>), grid, dim3(256), 0, s,
+                         static_cast<const TI*>(A), M, K, N, W, b, HW, static_cast<TO*>(lo), static_cast<TO*>(hi),
+                         act_lo, act_hi, partial, NH, slots);
+      return hipGetLastError();
+    }
+  }
   hipLaunchKernelGGL((proj_kc_kernel<PLANE_A, OUT_SPLIT, TI, TO, TM>), grid, dim3(256), 0, s, static_cast<const TI*>(A),
                      M, K, N, W, b, HW, static_cast<TO*>(lo), static_cast<TO*>(hi), act_lo, act_hi, partial, NH, slots);
   return hipGetLastError();
