@@ -1338,21 +1338,26 @@ proj_kc_kernel(const TI* __restrict__ A, int M, int K, int N, const float* __res
       for (int cp = 0; cp < 16 / CPI; ++cp) {
         const int cl = CPI * cp + half;
         const int gn = n0 + wn * 32 + j * 16 + cl;
-        const floatx4 v4 = *reinterpret_cast<const floatx4*>(&stg[cl * SPC + 4 * q]);
-        if (gn >= N || row0 >= M) continue;
+        if (gn >= N) continue;
         const bool lo = gn < NH;
         const int c = lo ? gn : gn - NH, NC = lo ? NH : NL;
         TO* dst = lo ? out_lo : out_hi;
-        const float v[4] = {v4[0], v4[1], v4[2], v4[3]};
-        if ((HW % 4) == 0 && row0 + 3 < M) {
+        // one way for the whole tile (uniform), so every row is stored by exactly one lane
+        if ((HW % 4) == 0 && m0 + TM <= M) {
+          const floatx4 v4 = *reinterpret_cast<const floatx4*>(&stg[cl * SPC + 4 * q]);
+          const float v[4] = {v4[0], v4[1], v4[2], v4[3]};
           st4(dst, size_t(rfr * NC + c) * HW + rpx, v);
         } else {
-          int f2 = rfr, p2 = rpx;
+          // element stores: lane q takes rows q, q + TM/4, q + TM/2, q + 3TM/4 of the column, so one
+          // store instruction writes TM/4 consecutive rows (pixels) instead of every fourth one
+          int f2 = (m0 + q) / HW, p2 = (m0 + q) % HW;
 #pragma unroll
           for (int r = 0; r < 4; ++r) {
-            if (row0 + r < M) st_el(dst, size_t(f2 * NC + c) * HW + p2, v[r]);
-            if (++p2 == HW) {
-              p2 = 0;
+            const int row = m0 + q + r * (TM / 4);
+            if (row < M) st_el(dst, size_t(f2 * NC + c) * HW + p2, stg[cl * SPC + q + r * (TM / 4)]);
+            p2 += TM / 4;
+            while (p2 >= HW) {
+              p2 -= HW;
               ++f2;
             }
           }

@@ -100,8 +100,11 @@ def test_proj_planes_bf16_input(mods, F, HW, K, N):
     assert rel_err(to_np(out), ref) < 1e-5
 
 
+# K-chunked kernel (K > 64): 4-pixel loads of plane-major A where H*W % 4 == 0 (K = 70: channels past K
+# within a chunk), element loads for H*W = 49
 @pytest.mark.parametrize("F,HW,K,N", [(4, 1024, 64, 64), (2, 16384, 128, 64), (3, 196, 96, 150),
-                                      (3, 49, 448, 224), (2, 16, 640, 320), (2, 196, 256, 128), (5, 49, 36, 30)])
+                                      (3, 49, 448, 224), (2, 16, 640, 320), (2, 196, 256, 128), (5, 49, 36, 30),
+                                      (3, 16, 70, 40)])
 def test_proj_out_channels_last(mods, F, HW, K, N):
     _, S = mods
     print_case(test="proj_out", F=F, HW=HW, K=K, N=N)
