@@ -239,7 +239,7 @@ def gdn_step(cell, variables, x, w, S, mark):
         mark("qkv_dw")
         qkv = S.gdn_qkv_proj(xq, p["qkv_proj"]["kernel"], p["qkv_proj"]["bias"], B, T, H, W, convs, 1, bkv,
                              out_dtype=f32)
-        mark("qkv_proj")   # with the short conv, SiLU and input gates (one kernel when T in {1, 2, 4, 8})
+        mark("qkv_proj")   # with the short conv, SiLU and input gates (one kernel where cssm_gdn_qkv_fused says so)
         gv = S.proj_planes(x, p["gate_proj"]["kernel"], p["gate_proj"]["bias"], F, HW, act="silu", out_dtype=f32)
         mark("gate_proj")
     else:
