@@ -8,6 +8,9 @@ gates, softplus Delta, no short convolutions, random-init weights with
 N(0, 0.1^2) biases (synthetic data).  ``--workload`` selects the other
 BASELINE configs as the headline; by default the others (c1, c3, c4, c5) are
 measured in the same run, each the same way, and reported under "configs".
+The launch-bound ones (c1, c5) also carry "graph": the same step captured once
+in a HIP graph and replayed (checked bit for bit against the eager step); their
+value and ms_per_step stay the eager caller's.
 
 A step is one full layer forward with x already in HBM:
   gated: in_proj GEMM (plane-major split + SiLU + spatial-mean epilogue) ->
@@ -465,6 +468,41 @@ def run_training(key, args, torch, cells, S):
 
 # ------------------------------------------------------------------- main
 
+# configurations whose eager step is launch-bound: also timed replaying one captured HIP graph
+GRAPH_WORKLOADS = ("c1", "c5")
+
+
+def graph_replay_ms(step, cell, variables, x, w, S, torch, steps):
+    """ms per step of the same layer step captured once in a HIP graph (torch.cuda.graph) and
+    replayed `steps` times: the same kernels on the same resident x and weights, one graph launch
+    per step instead of one host round trip per kernel.  Its output must equal the eager step's
+    bit for bit."""
+    side = torch.cuda.Stream()
+    side.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(side):
+        for _ in range(2):
+            step(cell, variables, x, w, S, Marks(torch, False))
+    torch.cuda.current_stream().wait_stream(side)
+    torch.cuda.synchronize()
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
+        out = step(cell, variables, x, w, S, Marks(torch, False))
+    for _ in range(3):
+        graph.replay()
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for _ in range(steps):
+        graph.replay()
+    torch.cuda.synchronize()
+    ms = (time.perf_counter() - t0) * 1e3 / steps
+    ref = step(cell, variables, x, w, S, Marks(torch, False))
+    torch.cuda.synchronize()
+    if not torch.equal(out, ref):
+        raise RuntimeError(f"{w['key']}: graph replay differs from the eager step")
+    del graph, out, ref
+    return ms
+
+
 def run_workload(key, args, torch, cells, S, headline):
     """One workload on the GPU: warmup, `steps` timed layer forwards, per-kernel HIP-event times;
     returns the result dict (the bench line's keys for the headline, a compact record otherwise)."""
@@ -502,6 +540,7 @@ def run_workload(key, args, torch, cells, S, headline):
     torch.cuda.synchronize()
     el = time.perf_counter() - t0
     ms_step = el * 1e3 / steps
+    graph_ms = graph_replay_ms(step, cell, variables, x, w, S, torch, steps) if key in GRAPH_WORKLOADS else None
     # timed region 2: the same steps with a HIP event recorded after every kernel on the stream
     # they run on (per-kernel times, the dominant kernel's roofline).  Where recording the
     # events makes the host slower than the GPU (the launch-bound C5 stack: 55 per step), each
@@ -612,6 +651,9 @@ def run_workload(key, args, torch, cells, S, headline):
         "core_frames_per_s": B * T / (core_ms * 1e-3),
         "roofline": roof,
     }
+    if graph_ms is not None:
+        # the same step replayed from one captured HIP graph (value and ms_per_step stay the eager ones)
+        res["graph"] = {"ms_per_step": round(graph_ms, 5), "frames_per_s": B * T / (graph_ms * 1e-3)}
     if not headline:
         for k in ("metric", "n_gpus", "higher_is_better", "scaling", "vs_baseline", "warmup"):
             res.pop(k)

@@ -553,8 +553,8 @@ def _moving_dots(rng, shape):
 
 def test_gdn_layer_c4_shape_bf16_chunk_carry(mods):
     """C4's frame shape at full width (T = 32, 32 x 32, C = 64, d_k = 4, bf16 I/O) on moving dots:
-    the fused qkv projection walks the frames in chunks of 8 and carries the short conv's last
-    3 frames between chunks, inside the layer."""
+    the frame-sequential qkv projection walks the 32 frames carrying the short conv's three
+    previous frames in registers, with gate_proj's columns in the same launch, inside the layer."""
     cells, S = mods
     print_case(test="gdn_layer_c4_T32_bf16")
     kw = dict(delta_key_dim=4, gate_type="factored", kernel_size=11, short_conv_size=4)
