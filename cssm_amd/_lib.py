@@ -132,6 +132,9 @@ class CssmError(RuntimeError):
 def load() -> ctypes.CDLL:
     """Load (once) and return the HIP library; raises if it is not built."""
     global _lib
+    lib = _lib
+    if lib is not None:         # loaded: no lock on the per-call path
+        return lib
     with _lock:
         if _lib is None:
             if not os.path.exists(LIB_PATH):

@@ -16,7 +16,14 @@ _DTYPES = {torch.float32: _lib.F32, torch.bfloat16: _lib.BF16}
 _GATE_ACTS = {"softplus": _lib.ACT_SOFTPLUS, "sigmoid": _lib.ACT_SIGMOID2, "exp": _lib.ACT_EXP}
 
 
+# the current stream's raw handle without building a torch.cuda.Stream object per call (the
+# per-kernel host cost that small batches pay); torch.cuda.current_stream() where torch lacks it
+_raw_stream = getattr(torch._C, "_cuda_getCurrentRawStream", None)
+
+
 def _stream() -> int:
+    if _raw_stream is not None:
+        return _raw_stream(torch.cuda.current_device())
     return torch.cuda.current_stream().cuda_stream
 
 

@@ -67,3 +67,14 @@ def test_cell_forward_replays_from_a_graph(cells, name, kw, shape, dtype):
         graph.replay()
         torch.cuda.synchronize()
         assert torch.equal(static_y, ref), f"{name}: replay {i} differs from the eager forward"
+
+
+def test_entry_points_enqueue_on_the_current_stream(cells):
+    """The raw stream handle the bindings pass is torch's current stream, on a side stream too
+    (what graph capture and multi-stream callers rely on)."""
+    from cssm_amd import spectral as S
+    assert S._stream() == torch.cuda.current_stream().cuda_stream
+    side = torch.cuda.Stream()
+    with torch.cuda.stream(side):
+        assert S._stream() == side.cuda_stream
+    assert S._stream() == torch.cuda.current_stream().cuda_stream
