@@ -284,11 +284,12 @@ struct NormGate {
   int kind;             // 0 none, 1 rms, 2 layer
 };
 
-// GDN qkv epilogue (TT > 0): the causal short convolution over T, SiLU and the
-// input gates of cssm.py:4763-4780 / :4844-4848, in the operation order of
-// gdn_qkv_post, on tiles of 128 / TT pixels x TT consecutive frames of one
-// batch element (tile row r = t * (128 / TT) + pixel), so each lane holds the
-// frames of its pixels.  The taps on frames t .. t - 3 are applied (kt <= 4,
+// GDN qkv epilogue (TT > 0; the tiled kernel, for the shapes the frame-sequential
+// qkv_fseq_kernel does not take: H*W not a multiple of 64): the causal short
+// convolution over T, SiLU and the input gates of cssm.py:4763-4780 / :4844-4848,
+// in the operation order of gdn_qkv_post, on tiles of 128 / TT pixels x TT
+// consecutive frames of one batch element (tile row r = t * (128 / TT) + pixel),
+// so each lane holds the frames of its pixels (TT = 4 or 8).  The taps on frames t .. t - 3 are applied (kt <= 4,
 // or T <= 4 where earlier taps only meet the zero padding).  T > TT (TT = 8)
 // runs as T / 8 chunks of the same pixels, in order on one workgroup, the last
 // 3 frames of each chunk kept in LDS for the next.  Output (B, T, N = 3C, HW)
@@ -1843,9 +1844,9 @@ qkv_fseq_kernel(const TI* __restrict__ A, int T, int HW, int K, int N, const flo
   }
 }
 
-// GDN qkv projection with the short convolution, SiLU and input gates fused
-// into the epilogue (persistent kernel, tiles of 128 / T pixels x T frames);
-// returns false when the shape has no fused variant (the caller then runs
+// The tiled GDN qkv projection (persistent kernel, tiles of 128 / T' pixels x
+// T' = min(T, 8) frames, the short conv, SiLU and input gates in its epilogue);
+// returns false when the shape has no tiled variant (the caller then runs
 // launch_proj_planes + launch_gdn_qkv_post, which compute the same values)
 template <int TT, bool CARRY, class TI, class TO>
 static void launch_qkv_fused(const void* X, int M, int K, int N, const float* W, const float* b, int HW, void* out,
