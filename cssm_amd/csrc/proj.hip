@@ -1705,11 +1705,16 @@ qkv_fseq_kernel(const TI* __restrict__ A, int T, int HW, int K, int N, const flo
     if (tile_gates && tid < TM) gsh[tid] = gpf;
   };
 
-  // pre-conv projections (with bias) of the lane's elements on frames t-1, t-2, t-3
-  floatx4 h1[MI][2], h2[MI][2], h3[MI][2];
+  // pre-conv projections (with bias) of the lane's elements on the three previous frames, in
+  // three slots whose roles rotate with the tile step's phase P (a compile-time constant):
+  // frame t-1 in slot (P+2)%3, t-2 in (P+1)%3, t-3 in P, which the current frame then takes;
+  // the loop runs the phases in turn, so no register moves shift the history
+  floatx4 hs[3][MI][2];
   int seq = blockIdx.x, t = 0;
   if (seq < nseq) fetch(seq, 0);
-  while (seq < nseq) {
+  auto tile_step = [&](auto phase) -> bool {
+    constexpr int P = decltype(phase)::value;
+    if (seq >= nseq) return false;
     __syncthreads();            // the previous tile is done with Asm and gsh (and qcw is staged)
     stash();
     __syncthreads();
@@ -1721,9 +1726,11 @@ qkv_fseq_kernel(const TI* __restrict__ A, int T, int HW, int K, int N, const flo
     if (ns < nseq) fetch(ns, nt);
     if (t == 0) {
 #pragma unroll
-      for (int i = 0; i < MI; ++i)
+      for (int q = 0; q < 3; ++q)
 #pragma unroll
-        for (int j = 0; j < 2; ++j) h1[i][j] = h2[i][j] = h3[i][j] = floatx4{0.f, 0.f, 0.f, 0.f};
+        for (int i = 0; i < MI; ++i)
+#pragma unroll
+          for (int j = 0; j < 2; ++j) hs[q][i][j] = floatx4{0.f, 0.f, 0.f, 0.f};
     }
 
     floatx4 acc[MI][2];
@@ -1796,7 +1803,9 @@ qkv_fseq_kernel(const TI* __restrict__ A, int T, int HW, int K, int N, const flo
           store(i, v);
         }
       } else {
-        const bool gk = blk == 1, gated = blk != 0;
+        const bool gated = blk != 0;
+        // the lane's input gate: component 0 (B_k) of a k column, 1 (B_v) of a v column
+        const float* const gcomp = reinterpret_cast<const float*>(gsh) + (blk == 1 ? 0 : 1);
 #pragma unroll
         for (int i = 0; i < MI; ++i) {
           float v[4];
@@ -1808,23 +1817,21 @@ qkv_fseq_kernel(const TI* __restrict__ A, int T, int HW, int K, int N, const flo
               // the tiled epilogue's order: tap 0 and the conv bias, then the taps on t-3, t-2, t-1
               // (frames before the first are the zero padding, held as zeros)
               float o = fmaf(w4.x, x, bt);
-              o = fmaf(w4.w, h3[i][j][r], o);
-              o = fmaf(w4.z, h2[i][j][r], o);
-              o = fmaf(w4.y, h1[i][j][r], o);
+              o = fmaf(w4.w, hs[P][i][j][r], o);
+              o = fmaf(w4.z, hs[(P + 1) % 3][i][j][r], o);
+              o = fmaf(w4.y, hs[(P + 2) % 3][i][j][r], o);
               y = o * __builtin_amdgcn_rcpf(1.0f + __expf(-o));   // SiLU as gdn_qkv_post computes it
             }
-            h3[i][j][r] = h2[i][j][r];
-            h2[i][j][r] = h1[i][j][r];
-            h1[i][j][r] = x;
+            hs[P][i][j][r] = x;   // frame t becomes the next phase's t-1
             v[r] = y;
           }
           if (tile_gates) {
-            const float2* gp = gsh + i * 16 + (lane >> 4) * 4;
+            const float* gp = gcomp + 2 * (i * 16 + (lane >> 4) * 4);
 #pragma unroll
             for (int r = 0; r < 4; ++r) {
-              float2 q = gp[r];   // loaded for every lane, then selected
-              asm volatile("" : "+v"(q.x), "+v"(q.y));
-              v[r] *= gated ? (gk ? q.x : q.y) : 1.0f;
+              float g = gp[2 * r];   // loaded for every lane, then selected
+              asm volatile("" : "+v"(g));
+              v[r] *= gated ? g : 1.0f;
             }
           } else if (qp.gate_mode == 3 && gated) {
             const float4 gg = *reinterpret_cast<const float4*>(
@@ -1841,6 +1848,10 @@ qkv_fseq_kernel(const TI* __restrict__ A, int T, int HW, int K, int N, const flo
     }
     seq = ns;
     t = nt;
+    return true;
+  };
+  while (tile_step(std::integral_constant<int, 0>{}) && tile_step(std::integral_constant<int, 1>{}) &&
+         tile_step(std::integral_constant<int, 2>{})) {
   }
 }
 
