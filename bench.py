@@ -233,13 +233,19 @@ def gdn_step(cell, variables, x, w, S, mark):
     F, HW, f32 = B * T, H * W, torch.float32
     mark("start")
     what = cell.spectral_kernel(p, H, W)
-    ctx = S.frame_mean(x)
+    fused = (S.depthwise_conv_mean(x, p["qkv_dw"]["kernel"], p["qkv_dw"]["bias"], out_dtype=f32)
+             if cell.qkv_conv_size > 1 else None)
+    if fused is not None:
+        xq, ctx = fused
+        mark("qkv_dw_mean")   # the qkv depthwise conv with the context mean in the same pass over x
+    else:
+        ctx = S.frame_mean(x)
+        xq = (S.depthwise_conv(x, p["qkv_dw"]["kernel"], p["qkv_dw"]["bias"], out_dtype=f32)
+              if cell.qkv_conv_size > 1 else x)
     ab, bkv = S.gdn_gates(ctx, p, H, W, cell.delta_key_dim, cell.gate_type, True, "sinusoid", cell.rope_base)
     mark("gates")
     convs = [p["short_conv_q"], p["short_conv_k"], p["short_conv_v"]]
     if cell.qkv_conv_size > 1:
-        xq = S.depthwise_conv(x, p["qkv_dw"]["kernel"], p["qkv_dw"]["bias"], out_dtype=f32)
-        mark("qkv_dw")
         qkv = S.gdn_qkv_proj(xq, p["qkv_proj"]["kernel"], p["qkv_proj"]["bias"], B, T, H, W, convs, 1, bkv,
                              out_dtype=f32)
         mark("qkv_proj")   # with the short conv, SiLU and input gates (one kernel where cssm_gdn_qkv_fused says so)

@@ -85,6 +85,8 @@ SIGNATURES = {
     "cssm_proj_planes": (_I, [_P, _I, _I, _I, _I, _I, _P, _P, _P, _I, _I, _P]),
     "cssm_frame_mean": (_I, [_P, _I, _I, _I, _I, _P, _P]),
     "cssm_depthwise_conv": (_I, [_P, _I, _I, _I, _I, _I, _I, _P, _P, _P, _I, _P]),
+    "cssm_depthwise_conv_mean_workspace": (_LL, [_I, _I, _I, _I, _I]),
+    "cssm_depthwise_conv_mean": (_I, [_P, _I, _I, _I, _I, _I, _I, _P, _P, _P, _I, _P, _P, _P]),
     "cssm_gdn_gates": (_I, [_P, _I, _I, _I, _I, _I, _I, ctypes.POINTER(GdnGateParams), _I, ctypes.c_float, _P,
                             _P, _P, _P]),
     "cssm_gdn_qkv_post": (_I, [_P, _I, _I, _I, _I, _I, _I, _I, _P, _P, _I, _P, _P]),

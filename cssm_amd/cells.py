@@ -396,13 +396,19 @@ class GatedDeltaNetCSSM:
         # precision); only x is read and the output written in the I/O dtype
         f32 = torch.float32
         what = self.spectral_kernel(p, H, W)
-        # gates from the spatial mean of the layer input (+ temporal encoding)
-        ctx = S.frame_mean(x)
+        # gates from the spatial mean of the layer input (+ temporal encoding); with the qkv conv,
+        # the mean comes out of the conv's pass over x where the fused form applies
+        fused = (S.depthwise_conv_mean(x, p["qkv_dw"]["kernel"], p["qkv_dw"]["bias"], out_dtype=f32)
+                 if self.qkv_conv_size > 1 else None)
+        if fused is not None:
+            xq, ctx = fused
+        else:
+            ctx = S.frame_mean(x)
+            xq = (S.depthwise_conv(x, p["qkv_dw"]["kernel"], p["qkv_dw"]["bias"], out_dtype=f32)
+                  if self.qkv_conv_size > 1 else x)
         temporal = "none" if self.position_independent_gates else "sinusoid"
         ab, bkv = S.gdn_gates(ctx, p, H, W, dk, self.gate_type, self.use_input_gates, temporal, self.rope_base)
         # q, k, v in plane-major blocks (B, T, 3C, H, W)
-        xq = (S.depthwise_conv(x, p["qkv_dw"]["kernel"], p["qkv_dw"]["bias"], out_dtype=f32)
-              if self.qkv_conv_size > 1 else x)
         gate_mode, gates = 0, None
         if self.use_input_gates:
             if self.gate_type == "channel":

@@ -307,6 +307,30 @@ int cssm_depthwise_conv(const void* x, int dtype, int F, int H, int W, int C, in
                     "cssm_depthwise_conv");
 }
 
+long long cssm_depthwise_conv_mean_workspace(int F, int H, int W, int C, int ks) {
+  if (F <= 0 || H <= 0 || W <= 0 || C <= 0) return 0;
+  return (long long)cssm::depthwise_conv_mean_blocks(F, H, W, C, ks) * F * C;
+}
+
+int cssm_depthwise_conv_mean(const void* x, int dtype, int F, int H, int W, int C, int ks, const float* kernel,
+                             const float* bias, void* out, int out_dtype, float* workspace, float* ctx, void* stream) {
+  if (!x || !kernel || !bias || !out || !workspace || !ctx)
+    return fail(CSSM_ERR_NULL, "cssm_depthwise_conv_mean: null argument");
+  if (F <= 0 || H <= 0 || W <= 0 || C <= 0 || ks <= 0 || ks > 31)
+    return fail(CSSM_ERR_SHAPE, "cssm_depthwise_conv_mean: F=%d H=%d W=%d C=%d ks=%d", F, H, W, C, ks);
+  if (!dtype_ok(dtype) || !dtype_ok(out_dtype))
+    return fail(CSSM_ERR_ARG, "cssm_depthwise_conv_mean: dtypes %d/%d", dtype, out_dtype);
+  if (x == out) return fail(CSSM_ERR_ARG, "cssm_depthwise_conv_mean: out must not alias x");
+  if (!cssm::depthwise_conv_mean_blocks(F, H, W, C, ks))
+    return fail(CSSM_ERR_UNSUPPORTED, "cssm_depthwise_conv_mean: no fused form for H=%d W=%d C=%d ks=%d", H, W, C, ks);
+  if (!aligned(x, vec_align(dtype)) || !aligned(out, vec_align(out_dtype)) || !aligned(kernel, 16) ||
+      !aligned(bias, 16) || !aligned(workspace, 16))
+    return fail(CSSM_ERR_ALIGN, "cssm_depthwise_conv_mean: misaligned x / out / kernel / bias / workspace");
+  return hip_status(cssm::launch_depthwise_conv_mean(x, dtype, F, H, W, C, ks, kernel, bias, out, out_dtype, workspace,
+                                                     ctx, static_cast<hipStream_t>(stream)),
+                    "cssm_depthwise_conv_mean");
+}
+
 int cssm_gdn_gates(const float* ctx, int B, int T, int C, int H, int W, int dk, const cssm_gdn_gate_params* p,
                    int temporal, float rope_base, const float* temporal_table, float* ab, float* bkv, void* stream) {
   if (!ctx || !p || !ab) return fail(CSSM_ERR_NULL, "cssm_gdn_gates: ctx, params and ab must be non-null");

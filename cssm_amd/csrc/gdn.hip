@@ -1053,12 +1053,17 @@ dwconv_cl(const TI* __restrict__ x, int H, int W, int C, int ks, const float* __
 // 2.9 -> 2.0 ms with 8 rows).  Needs C % 4 == 0, W % 4 == 0, H % RH == 0.  The
 // sum per output runs over the taps in the same order for every RH.
 constexpr int kDwMaxLdsTaps = 8192;   // floats
-template <int KS, int RH, bool LDSW, class TI, class TO>
+// SUM: also the frame's per-channel sums of x (the GDN context's spatial mean, cssm.py:4785): each
+// thread adds the inputs at its own output pixels (the centre taps, so every pixel once), the block
+// adds its threads' sums in a fixed order into part[(frame, block), C]; needs every block full
+// (per_frame % 256 == 0) and C / 4 dividing 256 (host-checked).
+template <int KS, int RH, bool LDSW, class TI, class TO, bool SUM = false>
 __global__ void __launch_bounds__(256)
 dwconv_cl_blocked(const TI* __restrict__ x, int H, int W, int C, const float* __restrict__ kw,
-                  const float* __restrict__ bias, TO* __restrict__ y, int per_frame) {
+                  const float* __restrict__ bias, TO* __restrict__ y, int per_frame, float* __restrict__ part) {
   constexpr int LO = (KS - 1) / 2, RW = 4, NCOL = RW + KS - 1;
   extern __shared__ float4 kws[];   // LDSW: (KS, KS, C / 4) taps
+  __shared__ float4 red[SUM ? 256 : 1];
   const int CG = C / 4, WG = W / RW;
   if constexpr (LDSW) {
     for (int j = int(threadIdx.x); j < KS * KS * CG; j += int(blockDim.x))
@@ -1075,6 +1080,7 @@ dwconv_cl_blocked(const TI* __restrict__ x, int H, int W, int C, const float* __
   const size_t f = blockIdx.y;
   const TI* xf = x + f * H * W * C;
   float4 acc[RH][RW];
+  float4 cs = make_float4(0.f, 0.f, 0.f, 0.f);   // SUM: this thread's pixels, its 4 channels
   const float4 bv = *reinterpret_cast<const float4*>(bias + c0);
 #pragma unroll
   for (int r = 0; r < RH; ++r)
@@ -1089,6 +1095,17 @@ dwconv_cl_blocked(const TI* __restrict__ x, int H, int W, int C, const float* __
     for (int ic = 0; ic < NCOL; ++ic) {
       const int ww = w0 - LO + ic;
       xin[ic] = (ww >= 0 && ww < W) ? ld4v(xf, (size_t(hh) * W + ww) * C + c0) : make_float4(0.f, 0.f, 0.f, 0.f);
+    }
+    if constexpr (SUM) {
+      if (ih >= LO && ih < LO + RH) {   // an output row of this thread: its RW centre inputs
+#pragma unroll
+        for (int q = 0; q < RW; ++q) {
+          cs.x += xin[LO + q].x;
+          cs.y += xin[LO + q].y;
+          cs.z += xin[LO + q].z;
+          cs.w += xin[LO + q].w;
+        }
+      }
     }
 #pragma unroll
     for (int r = 0; r < RH; ++r) {
@@ -1114,31 +1131,66 @@ dwconv_cl_blocked(const TI* __restrict__ x, int H, int W, int C, const float* __
   for (int r = 0; r < RH; ++r)
 #pragma unroll
     for (int q = 0; q < RW; ++q) st4v(y, ((f * H + h0 + r) * W + w0 + q) * C + c0, acc[r][q]);
+  if constexpr (SUM) {
+    // every thread of the block is here (no block is partial); thread t holds channel quad t % CG
+    red[threadIdx.x] = cs;
+    __syncthreads();
+    if (int(threadIdx.x) < CG) {
+      float4 sum = red[threadIdx.x];
+      for (int k = 1; k < 256 / CG; ++k) {
+        const float4 v = red[threadIdx.x + k * CG];
+        sum.x += v.x;
+        sum.y += v.y;
+        sum.z += v.z;
+        sum.w += v.w;
+      }
+      *reinterpret_cast<float4*>(part + (f * gridDim.x + blockIdx.x) * C + 4 * threadIdx.x) = sum;
+    }
+  }
+}
+
+// ctx[f, c] = (sum of the frame's block partials, in block order) / HW
+__global__ void __launch_bounds__(256) dw_mean_reduce(const float* __restrict__ part, int nblk, int C, float inv,
+                                                      float* __restrict__ ctx) {
+  const size_t f = blockIdx.x;
+  for (int c = int(threadIdx.x); c < C; c += int(blockDim.x)) {
+    float sum = 0.f;
+    for (int b = 0; b < nblk; ++b) sum += part[(f * nblk + b) * C + c];
+    ctx[f * C + c] = sum * inv;
+  }
 }
 
 template <int KS, int RH, bool LDSW, class TI, class TO>
 static hipError_t run_dwconv_blocked(const void* x, int F, int H, int W, int C, const float* kw, const float* bias,
-                                     void* y, hipStream_t s) {
+                                     void* y, float* part, hipStream_t s) {
   const int per_frame = (H / RH) * (W / 4) * (C / 4);
   const size_t shm = LDSW ? size_t(KS) * KS * C * sizeof(float) : 0;
-  hipLaunchKernelGGL((dwconv_cl_blocked<KS, RH, LDSW, TI, TO>), dim3(unsigned((per_frame + 255) / 256), unsigned(F)),
-                     dim3(256), shm, s, static_cast<const TI*>(x), H, W, C, kw, bias, static_cast<TO*>(y), per_frame);
+  const dim3 grid(unsigned((per_frame + 255) / 256), unsigned(F));
+  if (part)
+    hipLaunchKernelGGL((dwconv_cl_blocked<KS, RH, LDSW, TI, TO, true>), grid, dim3(256), shm, s,
+                       static_cast<const TI*>(x), H, W, C, kw, bias, static_cast<TO*>(y), per_frame, part);
+  else
+    hipLaunchKernelGGL((dwconv_cl_blocked<KS, RH, LDSW, TI, TO>), grid, dim3(256), shm, s, static_cast<const TI*>(x),
+                       H, W, C, kw, bias, static_cast<TO*>(y), per_frame, part);
   return hipGetLastError();
 }
 
+// rows per thread of the blocked kernel: 8 when the taps fit LDS and H % 8 == 0, else 2
+static int dwconv_rows(int H, int C, int ks) { return (C * ks * ks <= kDwMaxLdsTaps && H % 8 == 0) ? 8 : 2; }
+
 template <int KS, class TI, class TO>
 static hipError_t run_dwconv_rows(const void* x, int F, int H, int W, int C, const float* kw, const float* bias,
-                                  void* y, hipStream_t s) {
+                                  void* y, float* part, hipStream_t s) {
   if (C * KS * KS <= kDwMaxLdsTaps) {
-    if (H % 8 == 0) return run_dwconv_blocked<KS, 8, true, TI, TO>(x, F, H, W, C, kw, bias, y, s);
-    return run_dwconv_blocked<KS, 2, true, TI, TO>(x, F, H, W, C, kw, bias, y, s);
+    if (dwconv_rows(H, C, KS) == 8) return run_dwconv_blocked<KS, 8, true, TI, TO>(x, F, H, W, C, kw, bias, y, part, s);
+    return run_dwconv_blocked<KS, 2, true, TI, TO>(x, F, H, W, C, kw, bias, y, part, s);
   }
-  return run_dwconv_blocked<KS, 2, false, TI, TO>(x, F, H, W, C, kw, bias, y, s);
+  return run_dwconv_blocked<KS, 2, false, TI, TO>(x, F, H, W, C, kw, bias, y, part, s);
 }
 
 template <class TI, class TO>
 static bool try_dwconv_blocked(const void* x, int F, int H, int W, int C, int ks, const float* kw, const float* bias,
-                               void* y, hipStream_t s, hipError_t& e) {
+                               void* y, hipStream_t s, hipError_t& e, float* part = nullptr) {
   // float4 loads / stores of 4 channels: 16-byte aligned f32 (8-byte bf16) tensors and 16-byte
   // aligned taps and bias; one frame's work items must fit 32-bit indices and the frames the
   // grid's y dimension (otherwise the general kernel runs)
@@ -1148,9 +1200,9 @@ static bool try_dwconv_blocked(const void* x, int F, int H, int W, int C, int ks
       (long long)H * W * C >= (1LL << 31) || F > 65535)
     return false;
   switch (ks) {
-    case 3: e = run_dwconv_rows<3, TI, TO>(x, F, H, W, C, kw, bias, y, s); return true;
-    case 5: e = run_dwconv_rows<5, TI, TO>(x, F, H, W, C, kw, bias, y, s); return true;
-    case 7: e = run_dwconv_rows<7, TI, TO>(x, F, H, W, C, kw, bias, y, s); return true;
+    case 3: e = run_dwconv_rows<3, TI, TO>(x, F, H, W, C, kw, bias, y, part, s); return true;
+    case 5: e = run_dwconv_rows<5, TI, TO>(x, F, H, W, C, kw, bias, y, part, s); return true;
+    case 7: e = run_dwconv_rows<7, TI, TO>(x, F, H, W, C, kw, bias, y, part, s); return true;
     default: return false;
   }
 }
@@ -1180,6 +1232,34 @@ hipError_t launch_depthwise_conv(const void* x, int dtype, int F, int H, int W, 
   else
     hipLaunchKernelGGL((dwconv_cl<uint16_t, uint16_t>), g, b, 0, s, static_cast<const uint16_t*>(x), H, W, C, ks, kw,
                        bias, static_cast<uint16_t*>(y), total, vec);
+  return hipGetLastError();
+}
+
+// blocks per frame of the depthwise conv with the fused frame mean, 0 where it has no fused form (the
+// blocked kernel with every block full and C / 4 dividing 256)
+int depthwise_conv_mean_blocks(int F, int H, int W, int C, int ks) {
+  if (C % 4 || W % 4 || H % 2 || (ks != 3 && ks != 5 && ks != 7) || (long long)H * W * C >= (1LL << 31) || F > 65535)
+    return 0;
+  const int CG = C / 4;
+  if (256 % CG) return 0;
+  const int per_frame = (H / dwconv_rows(H, C, ks)) * (W / 4) * CG;
+  return per_frame % 256 ? 0 : per_frame / 256;
+}
+
+hipError_t launch_depthwise_conv_mean(const void* x, int dtype, int F, int H, int W, int C, int ks, const float* kw,
+                                      const float* bias, void* y, int out_dtype, float* part, float* ctx,
+                                      hipStream_t s) {
+  const int nblk = depthwise_conv_mean_blocks(F, H, W, C, ks);
+  if (!nblk) return hipErrorInvalidValue;
+  hipError_t e = hipSuccess;
+  bool ran = false;
+  if (dtype == 0 && out_dtype == 0) ran = try_dwconv_blocked<float, float>(x, F, H, W, C, ks, kw, bias, y, s, e, part);
+  else if (dtype == 0) ran = try_dwconv_blocked<float, uint16_t>(x, F, H, W, C, ks, kw, bias, y, s, e, part);
+  else if (out_dtype == 0) ran = try_dwconv_blocked<uint16_t, float>(x, F, H, W, C, ks, kw, bias, y, s, e, part);
+  else ran = try_dwconv_blocked<uint16_t, uint16_t>(x, F, H, W, C, ks, kw, bias, y, s, e, part);
+  if (!ran) return hipErrorInvalidValue;   // alignment: the caller checks it first
+  if (e != hipSuccess) return e;
+  hipLaunchKernelGGL(dw_mean_reduce, dim3(unsigned(F)), dim3(256), 0, s, part, nblk, C, 1.0f / float(H * W), ctx);
   return hipGetLastError();
 }
 

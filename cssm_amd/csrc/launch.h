@@ -127,6 +127,12 @@ hipError_t launch_gdn_gates(const float* ctx, int B, int T, int C, int H, int W,
                             hipStream_t s);
 hipError_t launch_depthwise_conv(const void* x, int dtype, int F, int H, int W, int C, int ks, const float* kw,
                                  const float* bias, void* y, int out_dtype, hipStream_t s);
+// the depthwise conv and the per-(frame, channel) mean of x in one pass (the blocked kernel's centre
+// taps): part (F, blocks, C) workspace, ctx (F, C); blocks = depthwise_conv_mean_blocks(...) > 0
+int depthwise_conv_mean_blocks(int F, int H, int W, int C, int ks);
+hipError_t launch_depthwise_conv_mean(const void* x, int dtype, int F, int H, int W, int C, int ks, const float* kw,
+                                      const float* bias, void* y, int out_dtype, float* part, float* ctx,
+                                      hipStream_t s);
 hipError_t launch_gdn_qkv_post(void* qkv, int dtype, int B, int T, int C, int HW, int kt, const GdnShortConv& sc,
                                int gate_mode, const void* gates, hipStream_t s);
 // qkv_proj + short conv + SiLU + input gates: one fused launch when gdn_qkv_fused_supported(T, HW, K, kt), else the two.

@@ -338,6 +338,33 @@ def depthwise_conv(x: torch.Tensor, kernel: torch.Tensor, bias: torch.Tensor,
     return out
 
 
+def depthwise_conv_mean(x: torch.Tensor, kernel: torch.Tensor, bias: torch.Tensor,
+                        out_dtype: Optional[torch.dtype] = None):
+    """depthwise_conv and frame_mean of the same x in one pass -> (y, ctx (..., C) float32), or None
+    where the fused form does not apply (the caller then runs the two calls): qkv_dw and the GDN
+    context mean (cssm.py:4744-4750, :4785) both read the layer input."""
+    _dev(x, "x")
+    *lead, H, W, C = x.shape
+    F = 1
+    for d in lead:
+        F *= d
+    _dev(kernel, "kernel", torch.float32)
+    _dev(bias, "bias", torch.float32)
+    ks = kernel.shape[0]
+    if tuple(kernel.shape) != (ks, ks, 1, C) or bias.shape != (C,):
+        raise ValueError(f"depthwise kernel {tuple(kernel.shape)} does not match C={C}")
+    n = _lib.load().cssm_depthwise_conv_mean_workspace(F, H, W, C, ks)
+    if n <= 0 or kernel.data_ptr() % 16 or bias.data_ptr() % 16:
+        return None
+    od = out_dtype or x.dtype
+    out = torch.empty(x.shape, dtype=od, device=x.device)
+    ws = torch.empty(n, dtype=torch.float32, device=x.device)
+    ctx = torch.empty((*lead, C), dtype=torch.float32, device=x.device)
+    _lib.call("cssm_depthwise_conv_mean", x.data_ptr(), _DTYPES[x.dtype], F, H, W, C, ks, kernel.data_ptr(),
+              bias.data_ptr(), out.data_ptr(), _DTYPES[od], ws.data_ptr(), ctx.data_ptr(), _stream())
+    return out, ctx
+
+
 def gdn_gate_params_struct(p: Dict, gate_type: str, input_gates: bool) -> _lib.GdnGateParams:
     """cssm_gdn_gate_params from the Flax-named parameter dict (alpha, beta, B_k, B_v)."""
     s = _lib.GdnGateParams()

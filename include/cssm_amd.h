@@ -284,6 +284,23 @@ int cssm_frame_mean(const void* x, int dtype, int F, int HW, int C, float* out, 
 int cssm_depthwise_conv(const void* x, int dtype, int F, int H, int W, int C, int ks, const float* kernel,
                         const float* bias, void* out, int out_dtype, void* stream);
 
+/*
+ * cssm_depthwise_conv and cssm_frame_mean of the same x in one pass, where the
+ * GDN cell has a qkv conv (cssm.py:4744-4750 and the context mean :4785 both
+ * read the layer input): the conv's threads also add x at their own output
+ * pixels, each block sums its threads in a fixed order into the workspace, and
+ * a second small kernel adds a frame's blocks in order and divides by H*W
+ * (the same sums as cssm_frame_mean up to the order of the additions).
+ *   workspace  cssm_depthwise_conv_mean_workspace(F, H, W, C, ks) floats, 16-byte aligned
+ *   ctx        (F, C) float32 out
+ * Other arguments as cssm_depthwise_conv; kernel and bias 16-byte aligned.  Returns
+ * CSSM_ERR_UNSUPPORTED where the workspace query returns 0 (the caller then runs the two calls).
+ */
+long long cssm_depthwise_conv_mean_workspace(int F, int H, int W, int C, int ks);
+int cssm_depthwise_conv_mean(const void* x, int dtype, int F, int H, int W, int C, int ks, const float* kernel,
+                             const float* bias, void* out, int out_dtype, float* workspace, float* ctx,
+                             void* stream);
+
 /* gate_type of GatedDeltaNetCSSM (cssm.py:4798-4842) */
 typedef enum cssm_gdn_gate_type {
   CSSM_GDN_GATE_DENSE = 0,

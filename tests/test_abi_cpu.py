@@ -134,3 +134,25 @@ def test_projection_entry_points_reject_misaligned_pointers():
                                       f32, None) == -4
     # gdn_proj_out: out
     assert lib.cssm_gdn_proj_out(p, p, f32, F, HW, K, N, 0, None, None, p, p, p + 4, f32, None) == -5
+
+
+def test_depthwise_conv_mean_workspace_and_errors():
+    """The fused conv + frame-mean form: its workspace query (blocks per frame x F x C floats, 0 where
+    the blocked conv has partial blocks or C / 4 does not divide 256) and its argument errors, all
+    before any GPU work."""
+    from cssm_amd import _lib
+    lib = _lib.load()
+    # 128 x 128 x 64, ks 5: 8-row blocks, (128/8)(128/4)(64/4) = 8192 threads per frame = 32 blocks
+    assert lib.cssm_depthwise_conv_mean_workspace(3, 128, 128, 64, 5) == 32 * 3 * 64
+    # 32 x 32 x 32, ks 3: 4 * 8 * 8 = 256 threads = 1 block
+    assert lib.cssm_depthwise_conv_mean_workspace(2, 32, 32, 32, 3) == 1 * 2 * 32
+    assert lib.cssm_depthwise_conv_mean_workspace(2, 16, 16, 64, 5) == 0     # 128 threads: a partial block
+    assert lib.cssm_depthwise_conv_mean_workspace(2, 32, 32, 36, 3) == 0     # C / 4 = 9 does not divide 256
+    assert lib.cssm_depthwise_conv_mean_workspace(2, 32, 32, 32, 9) == 0     # no blocked kernel for 9 x 9
+    buf = ctypes.create_string_buffer(4096)
+    p = (ctypes.addressof(buf) + 255) // 256 * 256
+    f32 = _lib.F32
+    assert lib.cssm_depthwise_conv_mean(p, f32, 2, 32, 32, 32, 3, p, p, p + 1024, f32, None, p, None) == -1
+    assert lib.cssm_depthwise_conv_mean(p, f32, 2, 16, 16, 64, 5, p, p, p + 1024, f32, p, p, None) == -3
+    assert b"no fused form" in lib.cssm_last_error()
+    assert lib.cssm_depthwise_conv_mean(p + 4, f32, 2, 32, 32, 32, 3, p, p, p + 1024, f32, p, p, None) == -5

@@ -306,6 +306,39 @@ def test_gdn_qkv_gate_proj_matches_separate_calls(mods, shape, kt, gate_mode, ga
     assert bf16_excess_err(to_np(gb.float()), oracle_gv(to_np(xb.float()))) < 5e-3
 
 
+@pytest.mark.parametrize("shape,ks,dt", [((1, 2, 32, 32, 64), 5, torch.float32), ((2, 1, 32, 32, 32), 3, torch.float32),
+                                         ((1, 3, 32, 16, 64), 7, torch.bfloat16), ((1, 1, 128, 128, 64), 5, torch.float32)])
+def test_depthwise_conv_mean_matches_separate_calls(mods, shape, ks, dt):
+    """The conv with the frame mean fused in: its conv output equals depthwise_conv bit for bit, its
+    mean frame_mean's to rounding and numpy's.  The two fp32 means add H*W terms in different orders
+    (up to 16384 here), so they agree to ~1e-6 of the means, not bit for bit: the inputs carry a mean
+    of 0.5 so the comparison is not dominated by cancellation, and the bar is 1e-5."""
+    _, S = mods
+    print_case(test="dwconv_mean", shape=shape, ks=ks, dtype=str(dt))
+    rng = np.random.default_rng(31)
+    C = shape[-1]
+    x = _dev(rng.standard_normal(shape) + 0.5, dt)
+    kw = _dev(rng.standard_normal((ks, ks, 1, C)) / ks)
+    b = _dev(rng.standard_normal(C) * 0.1)
+    r = S.depthwise_conv_mean(x, kw, b, out_dtype=torch.float32)
+    assert r is not None
+    y, ctx = r
+    assert torch.equal(y, S.depthwise_conv(x, kw, b, out_dtype=torch.float32))
+    ref = S.frame_mean(x)
+    assert ctx.shape == ref.shape
+    assert rel_err(to_np(ctx), to_np(ref)) < 1e-5
+    xn = to_np(x.float()).astype(np.float64)
+    assert rel_err(to_np(ctx), xn.mean(axis=(2, 3))) < 1e-5
+
+
+def test_depthwise_conv_mean_unsupported_shape(mods):
+    """Where the blocked conv would leave a partial block the fused form declines (None): the cell
+    then runs the conv and frame_mean."""
+    _, S = mods
+    x = _dev(np.zeros((1, 1, 16, 16, 64)))
+    assert S.depthwise_conv_mean(x, _dev(np.zeros((5, 5, 1, 64))), _dev(np.zeros(64))) is None
+
+
 # --------------------------------------------------------- spectral core
 
 CORE_CASES = [
