@@ -80,7 +80,7 @@ def parse():
     ap.add_argument("--configs", default="c1,c3,c4,c5",
                     help="other BASELINE configs measured in the same run and reported under 'configs' "
                          "(comma-separated; 'none' for the headline workload only)")
-    ap.add_argument("--config-steps", type=int, default=20, help="timed steps of each extra config")
+    ap.add_argument("--config-steps", type=int, default=20, help="timed steps of each extra config (at least ~30 ms of them, at most 300)")
     ap.add_argument("--train", default="c2",
                     help="workload whose training step (forward + backward) is also measured, reported under "
                          "'training' ('none' to skip)")
@@ -538,6 +538,15 @@ def run_workload(key, args, torch, cells, S, headline):
         m = Marks(torch, False)
         step(cell, variables, x, w, S, m)
         per_step = m.count
+    if not headline:
+        # tiny steps (C1: ~50 us): enough of them for ~30 ms of timed work, not a host-jittered 1 ms
+        torch.cuda.synchronize()
+        t0 = time.perf_counter()
+        for _ in range(3):
+            step(cell, variables, x, w, S, Marks(torch, False))
+        torch.cuda.synchronize()
+        est_ms = (time.perf_counter() - t0) * 1e3 / 3
+        steps = max(steps, min(300, int(30.0 / max(est_ms, 1e-3))))
     # timed region 1: the layer as a caller runs it (value, ms_per_step)
     torch.cuda.synchronize()
     t0 = time.perf_counter()
