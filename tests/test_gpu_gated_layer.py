@@ -32,7 +32,8 @@ def _dev(a, dtype=torch.float32):
                                            (5, 196, 40, 72, True), (2, 49, 130, 10, False),
                                            (2, 1024, 128, 512, True), (3, 196, 224, 896, True),
                                            (2, 16, 320, 1280, False), (1, 49, 448, 90, True),
-                                           (5, 100, 200, 64, True), (3, 8, 96, 64, False)])
+                                           (5, 100, 200, 64, True), (3, 8, 96, 64, False),
+                                           (3, 49, 96, 200, True)])
 def test_proj_in_plane_major_and_ctx(mods, F, HW, K, N, silu):
     _, S = mods
     print_case(test="proj_in", F=F, HW=HW, K=K, N=N)
