@@ -1595,12 +1595,22 @@ qkv_fseq_kernel(const TI* __restrict__ A, int T, int HW, int K, int N, const flo
   const int nb = blockIdx.y * CBW * TN;          // the workgroup's first column
   const int n0 = nb + cq * TN, C = N / 3, NG = N + qp.ng;   // this wave's column block
   const int tpf = HW / TM;                       // pixel blocks per frame
+  // column offset (within the workgroup's CBW * 128 columns) of this lane's column in its column tile j.
+  // With gate columns filling a 256-column workgroup (3C + C = 256) the 16-column tiles are dealt so
+  // that waves w and w + 4 together hold three qkv tiles and one gate tile: waves 0-3 take qkv tiles
+  // 2w, 2w + 1, waves 4-7 qkv tile 8 + (w - 4) and gate tile 12 + (w - 4)
+  const bool deal = CBW == 2 && qp.ng > 0 && N + qp.ng == 256;
+  auto jcol = [&](int j) -> int {
+    const int w = cq * 4 + wn;
+    const int jt = !deal ? w * 2 + j : (w < 4 ? 2 * w + j : (j == 0 ? 8 + (w - 4) : 12 + (w - 4)));
+    return jt * 16 + (lane & 15);
+  };
 
   // B fragments: lane l holds column wn 32 + 16 j + l % 16, k = 32 kb + 8 (l / 16) + e, in three bf16 parts
   bf16x8 b1[2][KB], b2[2][KB], b3[2][KB];
 #pragma unroll
   for (int j = 0; j < 2; ++j) {
-    const int gn = n0 + wn * 32 + j * 16 + (lane & 15);
+    const int gn = nb + jcol(j);
 #pragma unroll
     for (int kb = 0; kb < KB; ++kb)
 #pragma unroll
@@ -1642,7 +1652,7 @@ qkv_fseq_kernel(const TI* __restrict__ A, int T, int HW, int K, int N, const flo
   int eblk[2], egch[2];
 #pragma unroll
   for (int j = 0; j < 2; ++j) {
-    const int gn = n0 + wn * 32 + j * 16 + (lane & 15);
+    const int gn = nb + jcol(j);
     const unsigned l4 = unsigned(lane >> 4) * 4u;
     const bool live = gn < NG, gcol = gn >= N;
     const int blk = live ? (gcol ? 3 : gn / C) : 0;
@@ -1778,7 +1788,7 @@ qkv_fseq_kernel(const TI* __restrict__ A, int T, int HW, int K, int N, const flo
     const unsigned pxo = unsigned(pb * TM) * sizeof(TO);
 #pragma unroll
     for (int j = 0; j < 2; ++j) {
-      const int cl = cq * TN + wn * 32 + j * 16 + (lane & 15);
+      const int cl = jcol(j);
       const int blk = eblk[j];
       const float4 w4 = *reinterpret_cast<const float4*>(&qcw[cl * 8]);
       const float2 bb2 = *reinterpret_cast<const float2*>(&qcw[cl * 8 + 4]);
