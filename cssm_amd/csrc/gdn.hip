@@ -667,7 +667,6 @@ __global__ void __launch_bounds__(256, 2) gdn_core_fused32(const GdnFusedArgs a)
 #pragma unroll
         for (int i = 0; i < JL; ++i) inv.v4_put(GI::v4_row(w, i, m) + g * DK * H, vcol, pf[g][i]);
     }
-    if (t + 1 < T) issue(t + 1, lane);
     const size_t fr = size_t(b) * T + t;
     float2 gab[BT], wh[BT];
 #pragma unroll
@@ -677,6 +676,9 @@ __global__ void __launch_bounds__(256, 2) gdn_core_fused32(const GdnFusedArgs a)
                       : make_float2(0.f, 0.f);
       wh[j] = bok[j] ? a.what[size_t(head) * H * WF + bin] : make_float2(0.f, 0.f);
     }
+    // the next step's planes after this step's gates: loads retire in issue order, so the bin
+    // steps' wait for the gates does not also wait for the next planes
+    if (t + 1 < T) issue(t + 1, lane);
     __syncthreads();
 
     fwd.r1(w, lane);
