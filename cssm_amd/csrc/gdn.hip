@@ -908,19 +908,25 @@ __device__ float dot_col(const float* ctx, const float* k, int C, int n, int col
   return acc;
 }
 
+// FB frames per block (factored gates, host-chosen): each weight is loaded once and applied to the
+// FB frames' contexts (the per-frame sums keep their order, so the result does not depend on FB)
+constexpr int kGatesMaxFB = 4;
 __global__ void __launch_bounds__(1024)
 gdn_gates_kernel(const float* __restrict__ ctx_in, int T, int C, int H, int W, int nh, GdnGateWeights w,
                  int temporal, float rope_base, const float* __restrict__ ttable, float2* __restrict__ ab,
-                 float2* __restrict__ bkv) {
+                 float2* __restrict__ bkv, int FB) {
   extern __shared__ float sm[];
-  const int bt = blockIdx.x, t = bt % T;
+  const int f0 = int(blockIdx.x) * FB;   // first (b, t) frame of the block
   const int WF = W / 2 + 1;
   const int CW = W > WF ? W : WF;
-  float* cx = sm;                 // C
-  float* rows = sm + C;           // 4 x H
-  float* cols = rows + 4 * H;     // 4 x max(W, WF)
-  float* part = cols + 4 * CW;    // factored: P partial sums of each of the 4 (H + CW) products
-  for (int c = threadIdx.x; c < C; c += blockDim.x) {
+  const int NV = 4 * (H + CW);
+  const int P = w.kind == 1 ? (NV >= int(blockDim.x) ? 1 : int(blockDim.x) / NV) : 0;
+  float* cx = sm;                      // FB x C
+  float* rows = cx + FB * C;           // FB x 4 x H
+  float* cols = rows + FB * 4 * H;     // FB x 4 x max(W, WF)
+  float* part = cols + FB * 4 * CW;    // factored: FB x P partial sums of each of the 4 (H + CW) products
+  for (int e = threadIdx.x; e < FB * C; e += blockDim.x) {
+    const int fl = e / C, c = e % C, bt = f0 + fl, t = bt % T;
     float v = ctx_in[size_t(bt) * C + c];
     if (temporal == 1) {
       // E[t, 2j] = sin(t / base^(2j / C)), E[t, 2j + 1] = cos(.)
@@ -930,60 +936,69 @@ gdn_gates_kernel(const float* __restrict__ ctx_in, int T, int C, int H, int W, i
     } else if (temporal == 2) {
       v += ttable[size_t(t) * C + c];
     }
-    cx[c] = v;
+    cx[e] = v;
   }
   __syncthreads();
   // gate g in {0 alpha, 1 beta, 2 B_k, 3 B_v}; spectral gates span (H, WF), spatial (H, W).
   // Factored: the row / column products of all four gates at once, product q = g (H + CW) + i,
   // each split over P threads (channel stride P) whose partials are summed in order.
   if (w.kind == 1) {
-    const int NV = 4 * (H + CW);
-    const int P = NV >= int(blockDim.x) ? 1 : int(blockDim.x) / NV;
     for (int e = threadIdx.x; e < NV * P; e += blockDim.x) {
       const int q = e % NV, pc = e / NV;
       const int g = q / (H + CW), i = q % (H + CW);
       const int nc = g < 2 ? WF : W;
-      float acc = 0.0f;
+      float acc[kGatesMaxFB] = {0.0f, 0.0f, 0.0f, 0.0f};
       if (w.kd[g] && (i < H || i - H < nc)) {
         const float* k = i < H ? w.kd[g] + i : w.kw[g] + (i - H);
         const int n = i < H ? H : nc;
 #pragma unroll 4
-        for (int c = pc; c < C; c += P) acc = fmaf(cx[c], k[size_t(c) * n], acc);
+        for (int c = pc; c < C; c += P) {
+          const float kv = k[size_t(c) * n];
+#pragma unroll
+          for (int fl = 0; fl < kGatesMaxFB; ++fl)
+            if (fl < FB) acc[fl] = fmaf(cx[fl * C + c], kv, acc[fl]);
+        }
       }
-      part[pc * NV + q] = acc;
+#pragma unroll
+      for (int fl = 0; fl < kGatesMaxFB; ++fl)
+        if (fl < FB) part[(fl * P + pc) * NV + q] = acc[fl];
     }
     __syncthreads();
-    for (int q = threadIdx.x; q < NV; q += blockDim.x) {
+    for (int e = threadIdx.x; e < FB * NV; e += blockDim.x) {
+      const int fl = e / NV, q = e % NV;
       const int g = q / (H + CW), i = q % (H + CW);
       const int nc = g < 2 ? WF : W;
       if (!w.kd[g] || (i >= H && i - H >= nc)) continue;
       float acc = i < H ? w.bd[g][i] : w.bw[g][i - H];
-      for (int pc = 0; pc < P; ++pc) acc += part[pc * NV + q];
-      if (i < H) rows[g * H + i] = acc;
-      else cols[g * CW + i - H] = acc;
+      for (int pc = 0; pc < P; ++pc) acc += part[(fl * P + pc) * NV + q];
+      if (i < H) rows[(fl * 4 + g) * H + i] = acc;
+      else cols[(fl * 4 + g) * CW + i - H] = acc;
     }
   }
   __syncthreads();
-  auto spectral = [&](int g, int i) -> float {       // raw gate at output i
-    if (w.kind == 1) return rows[g * H + i / WF] + cols[g * CW + i % WF];
+  auto spectral = [&](int fl, int g, int i) -> float {       // raw gate at output i of frame fl
+    if (w.kind == 1) return rows[(fl * 4 + g) * H + i / WF] + cols[(fl * 4 + g) * CW + i % WF];
     const int n = w.kind == 0 ? H * WF : (w.kind == 2 ? nh : 1);
-    return dot_col(cx, w.kd[g], C, n, i) + w.bd[g][i];
+    return dot_col(cx + fl * C, w.kd[g], C, n, i) + w.bd[g][i];
   };
-  auto spatial = [&](int g, int i) -> float {
-    if (w.kind == 1) return rows[g * H + i / W] + cols[g * CW + i % W];
+  auto spatial = [&](int fl, int g, int i) -> float {
+    if (w.kind == 1) return rows[(fl * 4 + g) * H + i / W] + cols[(fl * 4 + g) * CW + i % W];
     const int n = w.kind == 0 ? H * W : 1;
-    return dot_col(cx, w.kd[g], C, n, i) + w.bd[g][i];
+    return dot_col(cx + fl * C, w.kd[g], C, n, i) + w.bd[g][i];
   };
   const int n_ab = w.kind == 2 ? nh : (w.kind == 3 ? 1 : H * WF);
-  for (int i = threadIdx.x; i < n_ab; i += blockDim.x) {
-    const float al = 0.1f + 0.89f * sigmoid_f(spectral(0, i));
-    const float be = sigmoid_f(spectral(1, i));
-    ab[size_t(bt) * n_ab + i] = make_float2(al, be);
+  for (int e = threadIdx.x; e < FB * n_ab; e += blockDim.x) {
+    const int fl = e / n_ab, i = e % n_ab;
+    const float al = 0.1f + 0.89f * sigmoid_f(spectral(fl, 0, i));
+    const float be = sigmoid_f(spectral(fl, 1, i));
+    ab[size_t(f0 + fl) * n_ab + i] = make_float2(al, be);
   }
   if (bkv && w.kd[2] && w.kind != 2) {
     const int n_kv = w.kind == 3 ? 1 : H * W;
-    for (int i = threadIdx.x; i < n_kv; i += blockDim.x)
-      bkv[size_t(bt) * n_kv + i] = make_float2(sigmoid_f(spatial(2, i)), sigmoid_f(spatial(3, i)));
+    for (int e = threadIdx.x; e < FB * n_kv; e += blockDim.x) {
+      const int fl = e / n_kv, i = e % n_kv;
+      bkv[size_t(f0 + fl) * n_kv + i] = make_float2(sigmoid_f(spatial(fl, 2, i)), sigmoid_f(spatial(fl, 3, i)));
+    }
   }
 }
 
@@ -993,10 +1008,18 @@ hipError_t launch_gdn_gates(const float* ctx, int B, int T, int C, int H, int W,
   const int WF = W / 2 + 1, CW = W > WF ? W : WF;
   constexpr int NT = 1024;
   const int NV = 4 * (H + CW), P = w.kind == 1 ? (NV >= NT ? 1 : NT / NV) : 0;
-  const size_t sm = sizeof(float) * (size_t(C) + 4 * size_t(H) + 4 * size_t(CW) + size_t(P) * NV);
-  if (sm > 64 * 1024) return hipErrorInvalidValue;
-  hipLaunchKernelGGL(gdn_gates_kernel, dim3(unsigned(B * T)), dim3(NT), sm, s, ctx, T, C, H, W, nh, w, temporal,
-                     rope_base, ttable, ab, bkv);
+  const size_t per_frame = size_t(C) + 4 * size_t(H) + 4 * size_t(CW) + size_t(P) * NV;   // floats
+  if (sizeof(float) * per_frame > 64 * 1024) return hipErrorInvalidValue;
+  // factored gates: frames per block where they divide B T and fit the 64 KB
+  int fb = 1;
+  if (w.kind == 1)
+    for (int c = kGatesMaxFB; c > 1; c /= 2)
+      if ((B * T) % c == 0 && sizeof(float) * per_frame * c <= 64 * 1024) {
+        fb = c;
+        break;
+      }
+  hipLaunchKernelGGL(gdn_gates_kernel, dim3(unsigned(B * T / fb)), dim3(NT), sizeof(float) * per_frame * fb, s, ctx,
+                     T, C, H, W, nh, w, temporal, rope_base, ttable, ab, bkv, fb);
   return hipGetLastError();
 }
 

@@ -142,12 +142,14 @@ def test_frame_mean_and_depthwise_conv(mods, shape):
         assert rel_err(to_np(ym), ref) < 5e-6, ks
 
 
+# (B, T): the factored gates run 4, 2 or 1 frames per block as B T divides (6 -> 2, 8 -> 4, 5 -> 1)
+@pytest.mark.parametrize("bt", [(2, 3), (2, 4), (1, 5)])
 @pytest.mark.parametrize("gate_type", ["factored", "dense", "channel", "scalar"])
-def test_gdn_gates_match_oracle(mods, gate_type):
+def test_gdn_gates_match_oracle(mods, gate_type, bt):
     _, S = mods
-    print_case(test="gdn_gates", gate_type=gate_type)
+    print_case(test="gdn_gates", gate_type=gate_type, bt=bt)
     rng = np.random.default_rng(5)
-    B, T, H, W, C, dk = 2, 3, 16, 16, 8, 2
+    (B, T), H, W, C, dk = bt, 16, 16, 8, 2
     cfg = O.GDNConfig(channels=C, delta_key_dim=dk, gate_type=gate_type)
     p = O.init_params(O.gdn_param_shapes(cfg, H, W), rng)
     ctx = rng.standard_normal((B, T, C))
