@@ -173,7 +173,7 @@ int cssm_gated_scan_bwd(const float* uspec, const float* dspec, const float* gat
                         void* stream) {
   if (!uspec || !dspec || !gates || !khat || !yspec || !sdu || !dgates || !dkhat)
     return fail(CSSM_ERR_NULL, "cssm_gated_scan_bwd: null argument");
-  if (B <= 0 || T <= 0 || C <= 0 || H <= 0 || W <= 0 || W % 2 || !(c_scale > 0.0f))
+  if (B <= 0 || T <= 0 || C <= 0 || H <= 0 || W <= 0 || !(c_scale > 0.0f))
     return fail(CSSM_ERR_SHAPE, "cssm_gated_scan_bwd: B=%d T=%d C=%d H=%d W=%d c_scale=%g", B, T, C, H, W,
                 double(c_scale));
   if (T > 32) return fail(CSSM_ERR_UNSUPPORTED, "cssm_gated_scan_bwd: T=%d (the reverse pass holds T <= 32 states)", T);

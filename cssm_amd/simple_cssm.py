@@ -215,7 +215,11 @@ class SimpleCSSM:
                 mu, var = bs[name]["mean"], bs[name]["var"]
             return (x - mu) * torch.rsqrt(var + 1e-5) * q["scale"] + q["bias"]
         if kind == "instance":
-            axes = tuple(range(1, x.dim() - 1)) or (-1,)
+            # GroupNorm(num_groups=C) reduces over axes 1..ndim-2 and the size-1 within-group axis;
+            # on a pooled (B, C) vector each group is one element (mean = x, var = 0): the bias
+            axes = tuple(range(1, x.dim() - 1))
+            if not axes:
+                return (x - x) * (1.0 / math.sqrt(1e-6)) * q["scale"] + q["bias"]
             mu = x.mean(dim=axes, keepdim=True)
             var = torch.clamp((x * x).mean(dim=axes, keepdim=True) - mu * mu, min=0.0)
             return (x - mu) * torch.rsqrt(var + 1e-6) * q["scale"] + q["bias"]

@@ -256,10 +256,12 @@ def _gated_core(cell, p, u, zg, B, T, H, W, Ci, c_scale):
 # state entering every step) and backward in cssm_gdn_scan_bins_bwd.
 
 def _c2r_weights(W: int, device) -> torch.Tensor:
-    """c_v of the C2R rule: 2 for 0 < v < W/2, 1 at v = 0 and v = W/2."""
+    """c_v of the C2R rule: 1 at v = 0 and (W even) at the Nyquist column v = W/2, else 2.
+    For odd W the last column v = (W - 1)/2 is an interior bin and keeps weight 2."""
     c = torch.full((W // 2 + 1,), 2.0, device=device)
     c[0] = 1.0
-    c[-1] = 1.0
+    if W % 2 == 0:
+        c[-1] = 1.0
     return c
 
 

@@ -171,10 +171,11 @@ int cssm_gated_scan_fwd(const void* u, const void* z, void* y, int dtype, int B,
  *   gates, khat      exactly as cssm_gated_scan_fwd read them (scan layout)
  *   c_scale          the c_scale the gate planes were made with (1 / (2 H W))
  *   yspec  (B, T, C, H, Wf) out: C h_t                  (natural order)
- *   sdu    (B, T, C, H, Wf) out: dL/dU_t H W / c_v      (natural order; c_v = 2 inside 0 < v < W/2)
+ *   sdu    (B, T, C, H, Wf) out: dL/dU_t H W / c_v      (natural order; c_v = 1 at v = 0 and at
+ *          v = W/2 for even W, else 2)
  *   dgates (B, T, H, Wf, 4) out: dL/d(gate planes), summed over channels (scan order)
  *   dkhat  (B, C, H, Wf)    out: dL/dkhat per batch element (sum over B; khat's scan layout)
- * T <= 32; W even.
+ * T <= 32; any H, W (odd W has no Nyquist column).
  */
 int cssm_gated_scan_bwd(const float* uspec, const float* dspec, const float* gates, const float* khat, int B, int T,
                         int C, int H, int W, float c_scale, float* yspec, float* sdu, float* dgates, float* dkhat,

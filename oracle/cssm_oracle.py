@@ -414,6 +414,7 @@ class GDNConfig:
     gate_type: str = 'channel'
     use_goom: bool = True
     use_log: bool = True
+    scan_mode: str = 'associative'
     short_conv_size: int = 4
     output_norm: str = 'rms'
     use_input_gates: bool = True
@@ -535,15 +536,62 @@ def gdn_spectral_norms(q_spec, k_spec, cfg: GDNConfig):
     return spec_norm(q_spec), k
 
 
+def gdn_scan_variant(cfg: GDNConfig):
+    """Which evaluation of the delta-rule scan the slow path takes (cssm.py:4939-4991):
+    'linear'  scan_mode='pallas' at d_k=2 (pallas_matrix_2x2_scan) or use_log=False (the direct
+              complex scan): the recurrence on M and Delta as they are, no floors;
+    'goom'    use_log and use_goom: to_goom on every M / Delta entry (|x| < 1e-7 -> 1e-7 + 0j);
+    'log_eps' use_log without use_goom: log(|x| + 1e-8) + i angle(x) on every entry
+              (cssm.py:4697-4699), exp afterwards.
+    The log-space combine (log_matmul / log_add_exp, operations.py:17-61, 314-390) evaluates the
+    linear recurrence on those entries (to_goom of an intermediate sum binds only at a relative
+    cancellation below 1e-7 of its largest term)."""
+    if cfg.scan_mode == 'pallas' and cfg.delta_key_dim == 2:
+        return 'linear'
+    if not cfg.use_log:
+        return 'linear'
+    return 'goom' if cfg.use_goom else 'log_eps'
+
+
+def gdn_scan_entries(z, variant):
+    """M / Delta entries as the chosen scan sees them after its log map and exp (cssm.py:4693-4701,
+    4945-4958): 'goom' to_goom's floor; 'log_eps' exp(log(|z| + 1e-8) + i angle(z)); 'linear'
+    unchanged.  A zero entry under 'log_eps' becomes 1e-8 + 0j here: the reference's angle is
+    atan2(Im, Re), which gives 0 or +-pi for the signed zeros its FFT and complex products happen
+    to leave, so its value there is +-1e-8 depending on sign bits the algorithm does not fix."""
+    if variant == 'goom':
+        return goom_floor(z)
+    if variant == 'log_eps':
+        z = np.asarray(z)
+        mapped = np.exp(np.log(np.abs(z) + 1e-8) + 1j * np.angle(z))
+        return np.where(z == 0, 1e-8 + 0j, mapped)
+    if variant == 'linear':
+        return z
+    raise ValueError(variant)
+
+
+def gdn_matrix_scan(M, D):
+    """s_t = M_t s_{t-1} + Delta_t[i, :], s_{-1} = 0 (math.py:384-411 in linear algebra).
+    M (B,T,nh,H,Wf,dk,dk) [row a, column b]; D (B,T,nh,dv,H,Wf,dk); returns S like D."""
+    B, T, nh, dv, H, Wf, dk = D.shape
+    s = np.zeros((B, nh, dv, H, Wf, dk), dtype=np.complex128)
+    S = np.empty((B, T, nh, dv, H, Wf, dk), dtype=np.complex128)
+    for t in range(T):
+        s = np.einsum('znuvab,zniuvb->zniuva', M[:, t], s) + D[:, t]
+        S[:, t] = s
+    return S
+
+
 def gdn_core(q_in, k_in, v_in, alpha, beta, W_hat, cfg: GDNConfig, scan='linear'):
     """rfft2 -> norms -> delta-rule matrix scan -> readout -> irfft2 (cssm.py:4875-5025).
 
     q_in/k_in/v_in: (B,T,H,W,C) channels-last; returns o_spatial (B,T,C,H,W).
-    scan='linear': materialises M_t and Delta_t with the GOOM floors and runs the
+    scan='linear': materialises M_t and Delta_t, maps every entry as the configured scan
+    sees it (gdn_scan_variant: to_goom's floors, log(|x| + 1e-8), or nothing) and runs the
     complex linear recurrence s_t = M_t s_{t-1} + Delta_t[i,:] (exact algebra of the
     log-space scan); scan='rank1': the same recurrence in rank-1 form without
-    materialising M and with no floors on M or Delta entries -- equal to 'linear'
-    wherever no entry reaches the floor.
+    materialising M and with no map on M or Delta entries -- equal to 'linear'
+    wherever no floor binds.
     """
     B, T, H, W, C = q_in.shape
     dk = cfg.delta_key_dim
@@ -566,16 +614,11 @@ def gdn_core(q_in, k_in, v_in, alpha, beta, W_hat, cfg: GDNConfig, scan='linear'
         M = a_bc * Wh * (I - b_bc * k_outer)                                   # cssm.py:4925
         vk = v_spec[..., :, None, :, :] * np.conj(k_n[..., None, :, :, :])    # (B,T,nh,dv,dk,H,Wf)
         D = b_bc * vk                                                          # cssm.py:4927-4929
-        if cfg.use_log and cfg.use_goom:
-            M = goom_floor(M)                                                  # to_goom floors
-            D = goom_floor(D)
-        Mt = np.moveaxis(M, (3, 4), (5, 6))     # (B,T,nh,H,Wf,dk,dk)
-        Dt = np.moveaxis(D, (4,), (6,))         # (B,T,nh,dv,H,Wf,dk)
-        s = np.zeros((B, nh, dv, H, Wf, dk), dtype=np.complex128)
-        S = np.empty((B, T, nh, dv, H, Wf, dk), dtype=np.complex128)
-        for t in range(T):                      # s_t = M_t s_{t-1} + Delta_t[i,:] (math.py:384-411)
-            s = np.einsum('znuvab,zniuvb->zniuva', Mt[:, t], s) + Dt[:, t]
-            S[:, t] = s
+        variant = gdn_scan_variant(cfg)                                        # cssm.py:4939-4991
+        M = gdn_scan_entries(M, variant)
+        D = gdn_scan_entries(D, variant)
+        S = gdn_matrix_scan(np.moveaxis(M, (3, 4), (5, 6)),   # (B,T,nh,H,Wf,dk,dk)
+                            np.moveaxis(D, (4,), (6,)))       # (B,T,nh,dv,H,Wf,dk)
     else:
         s = np.zeros((B, nh, dv, dk, H, Wf), dtype=np.complex128)   # s[..., i, a, u, v]
         S = np.empty((B, T, nh, dv, H, Wf, dk), dtype=np.complex128)
@@ -899,7 +942,13 @@ def simple_norm(x, kind, p, stats=None, training=False):
         return (x - mu) / np.sqrt(var + 1e-5) * p['scale'] + p['bias']
     if kind == 'instance':
         # GroupNorm(num_groups=C): one group per channel, stats over every non-batch axis but C
-        return flax_layer_norm(x, p, axes=tuple(range(1, x.ndim - 1)) or (-1,))
+        # (flax GroupNorm reduces over axes 1..ndim-2 and the size-1 within-group axis).  A pooled
+        # (B, C) vector leaves only the within-group axis: each group is one element, mean = x and
+        # var = 0, so the output is the bias.
+        axes = tuple(range(1, x.ndim - 1))
+        if not axes:
+            return (x - x) / np.sqrt(0.0 + 1e-6) * p['scale'] + p['bias']
+        return flax_layer_norm(x, p, axes=axes)
     if x.ndim == 5 and kind == 'temporal_layer':
         return flax_layer_norm(x, p, axes=(1, 4))
     if x.ndim == 5 and kind == 'global_layer':

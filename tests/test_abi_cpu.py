@@ -156,3 +156,17 @@ def test_depthwise_conv_mean_workspace_and_errors():
     assert lib.cssm_depthwise_conv_mean(p, f32, 2, 16, 16, 64, 5, p, p, p + 1024, f32, p, p, None) == -3
     assert b"no fused form" in lib.cssm_last_error()
     assert lib.cssm_depthwise_conv_mean(p + 4, f32, 2, 32, 32, 32, 3, p, p, p + 1024, f32, p, p, None) == -5
+
+
+def test_noalloc_refuses_sizes_beyond_its_scratch():
+    """cssm_proj_in_noalloc checks the ctx partial sums against its static scratch before any
+    device lookup or launch, so a request beyond it fails on the host (pointers never read)."""
+    from cssm_amd import _lib
+    lib = _lib.load()
+    F, HW, K, N = 4096, 16384, 64, 128
+    need = int(lib.cssm_proj_in_workspace_size(F, HW, K, N))
+    assert need > (64 << 20)
+    buf = ctypes.create_string_buffer(64)
+    p = ctypes.addressof(buf)
+    st = lib.cssm_proj_in_noalloc(p, _lib.F32, F, HW, K, N, p, p, p, p, _lib.F32, 0, 0, ctypes.c_void_p(p), None)
+    assert st == -3 and b"scratch" in lib.cssm_last_error()

@@ -32,7 +32,7 @@ def _np(t):
     return t.numpy() if not t.is_complex() else t.numpy().astype(np.complex128)
 
 
-SCAN_CASES = [(2, 4, 8, 16, 16), (1, 3, 8, 128, 128), (3, 1, 16, 32, 32), (1, 9, 8, 8, 8)]
+SCAN_CASES = [(2, 4, 8, 16, 16), (1, 3, 8, 128, 128), (3, 1, 16, 32, 32), (1, 9, 8, 8, 8), (2, 3, 8, 7, 7)]
 
 
 @pytest.mark.parametrize("shape", SCAN_CASES, ids=[f"{s[3]}x{s[4]}_T{s[1]}" for s in SCAN_CASES])
@@ -79,6 +79,9 @@ LAYER_CASES = [
     ("factored_128_exp", (1, 2, 128, 128, 4), dict(channels=4, kernel_size=11, gate_type="factored",
                                                    gate_activation="exp", short_conv_size=2,
                                                    short_conv_spatial_size=0)),
+    # odd planes: the last column is an interior bin (no Nyquist column), weight 2 in the C2R rule
+    ("factored_7x7_odd", (2, 2, 7, 7, 8), dict(channels=8, kernel_size=3, gate_type="factored", short_conv_size=0,
+                                               short_conv_spatial_size=0)),
 ]
 
 
@@ -233,6 +236,8 @@ GDN_LAYER_CASES = [
                                                use_input_gates=False, use_spectral_l2_norm=False)),
     ("factored_14x14_small_planes", (2, 3, 14, 14, 8), dict(gate_type="factored", output_norm="rms",
                                                            delta_key_dim=4, qkv_conv_size=3)),
+    # odd planes (the 7 x 7 SHViT stage): the transforms' adjoints weight the last column 2
+    ("factored_7x7_odd_planes", (2, 3, 7, 7, 8), dict(gate_type="factored", output_norm="rms", delta_key_dim=4)),
 ]
 
 

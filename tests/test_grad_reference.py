@@ -270,3 +270,26 @@ def test_gdn_float64_adjoint_identity():
     g = torch.autograd.grad((f(*ts) * w).sum(), ts)
     lhs, rhs = _dot(jv, w), sum(_dot(a, b) for a, b in zip(g, tang))
     assert abs(lhs - rhs) <= 1e-11 * abs(lhs), (lhs, rhs)
+
+
+@pytest.mark.parametrize("H,W", [(8, 8), (7, 7), (6, 5)])
+def test_c2r_weights_give_the_transform_adjoints(H, W):
+    """The training path's FFT adjoints (rfft2: dx = H W irfft2(dspec / c_v); irfft2:
+    dspec = rfft2(dy) c_v / (H W)) with c_v from training._c2r_weights equal float64 autograd
+    of torch.fft on the CPU.  c_v = 1 at v = 0 and at the Nyquist column of even W, else 2: for
+    odd W the last column is an interior bin, and weighting it 1 fails here."""
+    from cssm_amd import training
+    rng = np.random.default_rng(9)
+    c = training._c2r_weights(W, "cpu").double()
+    Wf = W // 2 + 1
+    assert c.shape == (Wf,)
+    spec = torch.from_numpy(rng.standard_normal((2, H, Wf)) + 1j * rng.standard_normal((2, H, Wf)))
+    spec.requires_grad_(True)
+    dy = torch.from_numpy(rng.standard_normal((2, H, W)))
+    (g_spec,) = torch.autograd.grad(torch.fft.irfft2(spec, s=(H, W)), spec, dy)
+    assert torch.allclose(g_spec, torch.fft.rfft2(dy) * c / (H * W), atol=1e-12)
+    x = torch.from_numpy(rng.standard_normal((2, H, W))).requires_grad_(True)
+    dspec = torch.from_numpy(rng.standard_normal((2, H, Wf)) + 1j * rng.standard_normal((2, H, Wf)))
+    (g_x,) = torch.autograd.grad(torch.fft.rfft2(x), x, dspec)
+    # torch's complex gradient convention is conj-linear; dL/dRe + i dL/dIm of a real loss
+    assert torch.allclose(g_x, torch.fft.irfft2(dspec / c, s=(H, W)) * (H * W), atol=1e-10)

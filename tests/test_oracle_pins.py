@@ -399,3 +399,371 @@ def test_layer_norm_pin_catches(mutant, monkeypatch):
     monkeypatch.setattr(O, "layer_norm", mutant)
     with pytest.raises(AssertionError):
         pin_layer_norm()
+
+
+# ================================================================ layer wiring
+#
+# The pins below fix how each layer wires its pieces together (which half of in_proj is the
+# state input, where ctx is taken, which qkv slice is which, which stream each input gate
+# scales, what gate_proj and ctx read), each through an identity of the reference's wiring:
+#   gated   cssm.py:480-484 (x_main = xz[..., :C], z = xz[..., C:]), :502 (SiLU), :536 (ctx =
+#           mean of the activated x_main), :581 (y * SiLU(z)), :584 (out_proj)
+#   GDN     cssm.py:4740-4758 (qkv_dw -> qkv_proj; q, k, v = slices 0, 1, 2), :4785-4786 (ctx from
+#           the layer input x), :4844-4848 (B_k scales k_in, B_v scales v_in), :4853-4855
+#           (gate_proj reads x_flat), :5026-5041 (norm, x gate, output_proj)
+# Each mutant re-runs the layer with exactly one wiring mistake.
+
+
+def _gated_forward_mistake(mistake):
+    """O.gated_forward with one wiring mistake: 'swap_split' (x_main and z exchanged),
+    'ctx_pre_silu' (ctx from x_main before the SiLU), 'ctx_from_x' (ctx from the layer input)."""
+    def fwd(params, x, cfg, scan="linear", return_intermediates=False):
+        x = np.asarray(x, dtype=np.float64)
+        B, T, H, W, Cin = x.shape
+        Ci = cfg.channels * cfg.expand
+        xz = O.dense(x, params["in_proj"])
+        x_main, z = xz[..., :Ci], xz[..., Ci:]
+        if mistake == "swap_split":
+            x_main, z = z, x_main
+        if cfg.short_conv_spatial_size > 0:
+            x_main = O.depthwise_conv2d_same(x_main.reshape(B * T, H, W, Ci),
+                                             params["short_conv_spatial"]).reshape(B, T, H, W, Ci)
+        if cfg.short_conv_size > 0:
+            x_main = O.causal_conv_t(x_main, params["short_conv_temporal"])
+        pre = x_main
+        x_main = O.silu(x_main)
+        khat = O.spectral_kernel(params["kernel"], H, W, cfg.spectral_rho)
+        ctx = {"ctx_pre_silu": pre, "ctx_from_x": x}.get(mistake, x_main).mean(axis=(2, 3))
+        delta, gB, gC = O.gated_gates(ctx, params, cfg, H, W)
+        y = O.gated_core(x_main.transpose(0, 1, 4, 2, 3), O.silu(z).transpose(0, 1, 4, 2, 3), khat, delta,
+                         gB, gC, scan=scan)
+        return O.dense(y.transpose(0, 1, 3, 4, 2), params["out_proj"])
+    return fwd
+
+
+def pin_gated_split_order():
+    """With the z half of in_proj zeroed, SiLU(z) = 0 and y * SiLU(z) = 0, so the layer returns
+    out_proj's bias exactly (short convs on, so a swapped split would feed their bias through)."""
+    rng = np.random.default_rng(21)
+    C, H, W = 4, 8, 8
+    cfg = O.GatedConfig(channels=C, kernel_size=3, gate_type="factored", short_conv_size=2,
+                        short_conv_spatial_size=3)
+    p = O.init_params(O.gated_param_shapes(cfg, C, H, W), rng)
+    p["in_proj"]["kernel"][:, C:] = 0.0
+    p["in_proj"]["bias"][C:] = 0.0
+    x = rng.standard_normal((2, 3, H, W, C))
+    out = O.gated_forward(p, x, cfg)
+    assert np.array_equal(out, np.broadcast_to(p["out_proj"]["bias"], out.shape)), "z half must gate the output"
+
+
+def _silu_twin(b=-0.5):
+    """a < -1.278 with SiLU(a) = SiLU(b): SiLU is not injective below its minimum."""
+    from scipy.optimize import brentq
+    return brentq(lambda a: float(O.silu(a) - O.silu(b)), -20.0, -1.2785, xtol=1e-15, rtol=1e-15)
+
+
+def pin_gated_ctx_source():
+    """ctx is the spatial mean of the activated x_main: two inputs whose x_main differ only by
+    swapping SiLU twins (SiLU(a) = SiLU(b), a != b) give the same SiLU(x_main) and z, hence the
+    same output, while any pre-SiLU mean (or the mean of x) differs between them by O(1)."""
+    rng = np.random.default_rng(22)
+    C, H, W = 3, 8, 8
+    cfg = O.GatedConfig(channels=C, kernel_size=3, gate_type="factored", short_conv_size=0,
+                        short_conv_spatial_size=0)
+    p = O.init_params(O.gated_param_shapes(cfg, C, H, W), rng)
+    p["in_proj"]["kernel"][:, :C] = np.eye(C)             # x_main = x exactly
+    p["in_proj"]["bias"][:C] = 0.0
+    p["in_proj"]["kernel"][0, C:] = 0.0                   # z does not read channel 0
+    for g in ("delta_proj", "B_proj", "C_proj"):          # gates strongly ctx-dependent
+        for s in ("_h", "_w"):
+            p[g + s]["kernel"] *= 8.0
+    a, b = _silu_twin(), -0.5
+    mask = rng.random((1, 2, H, W)) < 0.3
+    x1 = rng.standard_normal((1, 2, H, W, C))
+    x2 = x1.copy()
+    x1[..., 0] = np.where(mask, a, b)
+    x2[..., 0] = np.where(mask, b, a)
+    y1, y2 = O.gated_forward(p, x1, cfg), O.gated_forward(p, x2, cfg)
+    assert np.max(np.abs(y1 - y2)) <= 1e-10 * np.sqrt(np.mean(y1 ** 2)), "ctx must follow SiLU(x_main)"
+
+
+def test_gated_split_order():
+    pin_gated_split_order()
+
+
+def test_gated_ctx_source():
+    pin_gated_ctx_source()
+
+
+@pytest.mark.parametrize("mistake", ["swap_split"])
+def test_gated_split_pin_catches(mistake, monkeypatch):
+    monkeypatch.setattr(O, "gated_forward", _gated_forward_mistake(mistake))
+    with pytest.raises(AssertionError):
+        pin_gated_split_order()
+
+
+@pytest.mark.parametrize("mistake", ["ctx_pre_silu", "ctx_from_x"])
+def test_gated_ctx_pin_catches(mistake, monkeypatch):
+    monkeypatch.setattr(O, "gated_forward", _gated_forward_mistake(mistake))
+    with pytest.raises(AssertionError):
+        pin_gated_ctx_source()
+
+
+def _gdn_prologue_mistake(mistake):
+    """O.gdn_prologue with one wiring mistake: 'slices_kqv' / 'slices_vkq' / 'slices_qvk' (the
+    qkv_proj slices in another order), 'gates_swapped' (B_v on k, B_k on v), 'bk_on_q' / 'bv_on_q'
+    (an input gate on q instead of its stream), 'gate_proj_after_conv' (gate_proj reads the qkv_dw
+    output), 'ctx_after_conv' (ctx from the qkv_dw output)."""
+    def pro(params, x, cfg):
+        x = np.asarray(x, dtype=np.float64)
+        B, T, H, W, C = x.shape
+        W_hat = O.spectral_kernel(params["kernel"], H, W, cfg.spectral_rho, squash=not cfg.no_spectral_clamp)
+        x_flat = x.reshape(B * T, H, W, C)
+        xc = O.depthwise_conv2d_same(x_flat, params["qkv_dw"]) if cfg.qkv_conv_size > 1 else x_flat
+        qkv = O.dense(xc, params["qkv_proj"]).reshape(B, T, H, W, 3 * C)
+        sl = [qkv[..., :C], qkv[..., C:2 * C], qkv[..., 2 * C:]]
+        order = {"slices_kqv": (1, 0, 2), "slices_vkq": (2, 1, 0), "slices_qvk": (0, 2, 1)}.get(mistake, (0, 1, 2))
+        q_in, k_in, v_in = (sl[i] for i in order)
+        if cfg.short_conv_size > 0:
+            q_in = O.silu(O.causal_conv_t(q_in, params["short_conv_q"]))
+            k_in = O.silu(O.causal_conv_t(k_in, params["short_conv_k"]))
+            v_in = O.silu(O.causal_conv_t(v_in, params["short_conv_v"]))
+        ctx_src = xc.reshape(B, T, H, W, C) if mistake == "ctx_after_conv" else x
+        ctx = ctx_src.mean(axis=(2, 3)) + O.temporal_context_encoding(T, C, cfg.rope_base)[None]
+        if cfg.use_input_gates:
+            gk = O.gdn_gate("B_k", params, cfg, ctx, x, H, W, spatial=True)
+            gv_ = O.gdn_gate("B_v", params, cfg, ctx, x, H, W, spatial=True)
+            if mistake == "gates_swapped":
+                gk, gv_ = gv_, gk
+            if mistake == "bk_on_q":
+                q_in = q_in * gk
+            else:
+                k_in = k_in * gk
+            if mistake == "bv_on_q":
+                q_in = q_in * gv_
+            else:
+                v_in = v_in * gv_
+        g_src = xc if mistake == "gate_proj_after_conv" else x_flat
+        gv = O.dense(g_src, params["gate_proj"]).reshape(B, T, H, W, C)
+        gate_val = O.silu(gv) if cfg.output_gate_act == "silu" else O.sigmoid(gv)
+        alpha = O.gdn_gate("alpha", params, cfg, ctx, x, H, W, bounded=True)
+        beta = O.gdn_gate("beta", params, cfg, ctx, x, H, W)
+        return dict(q_in=q_in, k_in=k_in, v_in=v_in, gate_val=gate_val, alpha=alpha, beta=beta, W_hat=W_hat,
+                    ctx=ctx)
+    return pro
+
+
+def pin_gdn_slice_order():
+    """With the q columns of qkv_proj zeroed (no short conv): q_hat = 0, so o = S q = 0, the norm of
+    0 is 0 and the layer returns output_proj's bias exactly.  A k or v slice in q's place feeds
+    real values, and a zero k or v reaches the floored entries (1e-7), so any other order leaves
+    a non-zero o.  k and v are told apart by scaling (0-homogeneous in k, linear in v)."""
+    rng = np.random.default_rng(23)
+    C, H, W = 8, 6, 6
+    cfg = O.GDNConfig(channels=C, delta_key_dim=4, kernel_size=3, gate_type="factored", short_conv_size=0)
+    p = O.init_params(O.gdn_param_shapes(cfg, H, W), rng, spectral_init="xavier")
+    p["qkv_proj"]["kernel"][:, :C] = 0.0
+    p["qkv_proj"]["bias"][:C] = 0.0
+    x = rng.standard_normal((2, 3, H, W, C))
+    out = O.gdn_forward(p, x, cfg)
+    assert np.array_equal(out, np.broadcast_to(p["output_proj"]["bias"], out.shape)), "q is slice 0"
+    # k is normalised per bin and v enters s linearly: with no output norm and no short conv the
+    # output minus its bias is unchanged when the k columns are scaled and scales with the v columns
+    cfg = O.GDNConfig(channels=C, delta_key_dim=4, kernel_size=3, gate_type="factored", short_conv_size=0,
+                      output_norm="none")
+    p = O.init_params(O.gdn_param_shapes(cfg, H, W), rng, spectral_init="xavier")
+
+    def scaled(sl, lam):
+        q = {k: (dict(v) if isinstance(v, dict) else v) for k, v in p.items()}
+        kern, bias = p["qkv_proj"]["kernel"].copy(), p["qkv_proj"]["bias"].copy()
+        kern[:, sl * C:(sl + 1) * C] *= lam
+        bias[sl * C:(sl + 1) * C] *= lam
+        q["qkv_proj"] = {"kernel": kern, "bias": bias}
+        return O.gdn_forward(q, x, cfg) - p["output_proj"]["bias"]
+    r1 = scaled(1, 1.0)
+    assert np.max(np.abs(scaled(1, 3.0) - r1)) <= 1e-6 * np.max(np.abs(r1)), "k is slice 1 (normalised)"
+    assert np.max(np.abs(scaled(2, 3.0) - 3.0 * r1)) <= 1e-9 * np.max(np.abs(r1)), "v is slice 2 (linear)"
+
+
+def _gdn_gate_scaling_case(use_l2, bk, bv):
+    """T = 1, output_norm 'none', no short conv, factored input gates with zero kernels, so B_k and
+    B_v are the uniform sigmoid(bk) and sigmoid(bv); returns out - output_proj bias."""
+    rng = np.random.default_rng(24)
+    C, H, W = 8, 6, 6
+    cfg = O.GDNConfig(channels=C, delta_key_dim=4, kernel_size=3, gate_type="factored", short_conv_size=0,
+                      output_norm="none", use_spectral_l2_norm=use_l2)
+    p = O.init_params(O.gdn_param_shapes(cfg, H, W), rng, spectral_init="xavier")
+    for name, b in (("B_k", bk), ("B_v", bv)):
+        for s, n in (("_h", H), ("_w", W)):
+            p[name + s] = {"kernel": np.zeros((C, n)), "bias": np.full(n, b / 2.0)}
+    x = rng.standard_normal((1, 1, H, W, C))
+    return O.gdn_forward(p, x, cfg) - p["output_proj"]["bias"]
+
+
+def pin_gdn_input_gate_streams():
+    """B_k scales k, which the key-vector norm removes: with the spectral L2 norm off (so q keeps
+    its scale) the output cannot depend on B_k.  B_v scales v, on which o is linear: with the
+    spectral norm on (q and k both normalised) the output scales by B_v's ratio."""
+    r0 = _gdn_gate_scaling_case(False, 0.0, 0.0)
+    rk = _gdn_gate_scaling_case(False, 2.0, 0.0)
+    assert np.max(np.abs(rk - r0)) <= 1e-6 * np.max(np.abs(r0)), "B_k must scale only k"
+    r0 = _gdn_gate_scaling_case(True, 0.0, 0.0)
+    rv = _gdn_gate_scaling_case(True, 0.0, 2.0)
+    ratio = float(O.sigmoid(2.0) / O.sigmoid(0.0))
+    assert np.max(np.abs(rv - ratio * r0)) <= 1e-9 * np.max(np.abs(rv)), "B_v must scale v"
+
+
+def pin_gdn_gate_proj_and_ctx_inputs():
+    """qkv_dw = 2 delta with qkv_proj W gives the same q, k, v as qkv_dw = delta with qkv_proj 2W.
+    gate_proj and ctx read the layer input x (not the conv output), so both parameter sets give
+    the same output; reading the conv output would see 2x against x."""
+    rng = np.random.default_rng(25)
+    C, H, W = 8, 6, 6
+    cfg = O.GDNConfig(channels=C, delta_key_dim=4, kernel_size=3, gate_type="factored", qkv_conv_size=3)
+    p1 = O.init_params(O.gdn_param_shapes(cfg, H, W), rng, spectral_init="xavier")
+    for name in ("alpha", "beta", "B_k", "B_v"):                  # gates strongly ctx-dependent
+        for s in ("_h", "_w"):
+            p1[name + s]["kernel"] *= 6.0
+    p2 = {k: (dict(v) if isinstance(v, dict) else v) for k, v in p1.items()}
+    d = np.zeros((3, 3, 1, C))
+    d[1, 1] = 1.0
+    p1["qkv_dw"] = {"kernel": 2.0 * d, "bias": np.zeros(C)}
+    p2["qkv_dw"] = {"kernel": d, "bias": np.zeros(C)}
+    p2["qkv_proj"] = {"kernel": 2.0 * p1["qkv_proj"]["kernel"], "bias": p1["qkv_proj"]["bias"]}
+    x = rng.standard_normal((1, 3, H, W, C))
+    y1, y2 = O.gdn_forward(p1, x, cfg), O.gdn_forward(p2, x, cfg)
+    assert np.max(np.abs(y1 - y2)) <= 1e-12 * np.max(np.abs(y1)), "gate_proj / ctx must read x"
+
+
+def test_gdn_slice_order():
+    pin_gdn_slice_order()
+
+
+def test_gdn_input_gate_streams():
+    pin_gdn_input_gate_streams()
+
+
+def test_gdn_gate_proj_and_ctx_inputs():
+    pin_gdn_gate_proj_and_ctx_inputs()
+
+
+@pytest.mark.parametrize("mistake", ["slices_kqv", "slices_vkq", "slices_qvk"])
+def test_gdn_slice_pin_catches(mistake, monkeypatch):
+    monkeypatch.setattr(O, "gdn_prologue", _gdn_prologue_mistake(mistake))
+    with pytest.raises(AssertionError):
+        pin_gdn_slice_order()
+
+
+@pytest.mark.parametrize("mistake", ["gates_swapped", "bk_on_q", "bv_on_q"])
+def test_gdn_input_gate_pin_catches(mistake, monkeypatch):
+    monkeypatch.setattr(O, "gdn_prologue", _gdn_prologue_mistake(mistake))
+    with pytest.raises(AssertionError):
+        pin_gdn_input_gate_streams()
+
+
+@pytest.mark.parametrize("mistake", ["gate_proj_after_conv", "ctx_after_conv"])
+def test_gdn_gate_proj_ctx_pin_catches(mistake, monkeypatch):
+    monkeypatch.setattr(O, "gdn_prologue", _gdn_prologue_mistake(mistake))
+    with pytest.raises(AssertionError):
+        pin_gdn_gate_proj_and_ctx_inputs()
+
+
+def test_gdn_prologue_mistake_free_copy_agrees():
+    """The mutant harness with no mistake reproduces the oracle (so each mutant differs from the
+    oracle only by its mistake)."""
+    rng = np.random.default_rng(26)
+    cfg = O.GDNConfig(channels=8, delta_key_dim=4, kernel_size=3, gate_type="factored", qkv_conv_size=3)
+    p = O.init_params(O.gdn_param_shapes(cfg, 6, 6), rng, spectral_init="xavier")
+    x = rng.standard_normal((1, 3, 6, 6, 8))
+    a, b = O.gdn_prologue(p, x, cfg), _gdn_prologue_mistake(None)(p, x, cfg)
+    for k in ("q_in", "k_in", "v_in", "gate_val", "alpha", "beta", "W_hat", "ctx"):
+        assert np.allclose(a[k], b[k], rtol=0, atol=1e-13), k
+    cfgg = O.GatedConfig(channels=4, kernel_size=3, gate_type="factored", short_conv_size=2)
+    pg = O.init_params(O.gated_param_shapes(cfgg, 4, 8, 8), rng)
+    xg = rng.standard_normal((1, 3, 8, 8, 4))
+    assert np.allclose(O.gated_forward(pg, xg, cfgg), _gated_forward_mistake(None)(pg, xg, cfgg), rtol=0,
+                       atol=1e-13)
+
+
+# ------------------------------------------------------- GDN scan variants
+
+def pin_gdn_scan_variants():
+    """Which scan each configuration takes (cssm.py:4939-4991) and how each maps a zero, a tiny
+    negative, a tiny imaginary and an ordinary entry (to_goom: |x| < 1e-7 -> 1e-7 + 0j;
+    log(|x| + 1e-8) + i angle(x) then exp; the direct / pallas scans: unchanged).  Through the
+    layer core, a head with zero values at T = 1 has s = Delta' = c everywhere, so o_i = c sum_a q_a
+    with c = 1e-7, 1e-8 or 0 for the three scans."""
+    V = lambda **kw: O.gdn_scan_variant(O.GDNConfig(channels=8, **kw))
+    assert V(delta_key_dim=4) == "goom"
+    assert V(delta_key_dim=4, use_goom=False) == "log_eps"
+    assert V(delta_key_dim=4, use_log=False) == "linear"
+    assert V(delta_key_dim=4, use_log=False, use_goom=False) == "linear"
+    assert V(delta_key_dim=2, scan_mode="pallas") == "linear"
+    assert V(delta_key_dim=2, scan_mode="pallas", use_goom=False) == "linear"
+    assert V(delta_key_dim=4, scan_mode="pallas") == "goom"
+    assert V(delta_key_dim=3, scan_mode="pallas", use_goom=False) == "log_eps"
+    z = np.array([0.0, -3e-8, 5e-8j, 0.3 * np.exp(0.7j), -2.0])
+    want = {"goom": [1e-7, 1e-7, 1e-7, z[3], -2.0],
+            "log_eps": [1e-8, -4e-8, 6e-8j, (0.3 + 1e-8) * np.exp(0.7j), -(2.0 + 1e-8)],
+            "linear": list(z)}
+    for var, w in want.items():
+        got = O.gdn_scan_entries(z, var)
+        assert np.allclose(got, np.array(w, dtype=complex), rtol=1e-15, atol=1e-22), var
+    # through gdn_core: head 0 has v = 0 at T = 1
+    rng = np.random.default_rng(27)
+    B, T, H, W, C, dk = 1, 1, 6, 6, 8, 4
+    Wf = W // 2 + 1
+    q, k, v = (rng.standard_normal((B, T, H, W, C)) for _ in range(3))
+    v[..., :dk] = 0.0
+    alpha = 0.1 + 0.89 * O.sigmoid(rng.standard_normal((B, T, 1, H, Wf)))
+    beta = O.sigmoid(rng.standard_normal((B, T, 1, H, Wf)))
+    Wh = O.spectral_kernel(rng.standard_normal((C // dk, 3, 3)), H, W)
+    qs = np.fft.rfft2(q[0, 0, :, :, :dk].transpose(2, 0, 1))
+    qn = qs / np.sqrt(np.sum(np.abs(qs) ** 2, axis=(1, 2), keepdims=True) + 1e-6)
+    for kw, c in ((dict(), 1e-7), (dict(use_goom=False), 1e-8), (dict(use_log=False), 0.0)):
+        cfg = O.GDNConfig(channels=C, delta_key_dim=dk, kernel_size=3, gate_type="factored", **kw)
+        o = O.gdn_core(q, k, v, alpha, beta, Wh, cfg)
+        expect = np.fft.irfft2(np.broadcast_to(c * qn.sum(axis=0), (dk, H, Wf)), s=(H, W))
+        assert np.allclose(o[0, 0, :dk], expect, rtol=0, atol=1e-12 * max(c, 1e-30)), kw
+
+
+def _variant_goom_false_is_linear(cfg):
+    """Mistake (the earlier oracle): use_goom=False drops every floor instead of adding 1e-8."""
+    return "linear" if not cfg.use_goom else _orig_scan_variant(cfg)
+
+
+def _variant_pallas_ignored(cfg):
+    """Mistake: scan_mode='pallas' at d_k=2 still takes the log-space scan."""
+    return ("goom" if cfg.use_goom else "log_eps") if cfg.use_log else "linear"
+
+
+def _entries_log_eps_as_max(z, variant):
+    """Mistake: max(|x|, 1e-8) with the phase, instead of |x| + 1e-8."""
+    if variant == "log_eps":
+        return np.maximum(np.abs(z), 1e-8) * np.exp(1j * np.angle(z))
+    return _orig_scan_entries(z, variant)
+
+
+def _entries_log_eps_no_phase(z, variant):
+    """Mistake: the phase dropped (exp of the real log only)."""
+    if variant == "log_eps":
+        return (np.abs(z) + 1e-8).astype(complex)
+    return _orig_scan_entries(z, variant)
+
+
+_orig_scan_variant = O.gdn_scan_variant
+_orig_scan_entries = O.gdn_scan_entries
+
+
+def test_gdn_scan_variants():
+    pin_gdn_scan_variants()
+
+
+@pytest.mark.parametrize("name,mutant", [("gdn_scan_variant", _variant_goom_false_is_linear),
+                                         ("gdn_scan_variant", _variant_pallas_ignored),
+                                         ("gdn_scan_entries", _entries_log_eps_as_max),
+                                         ("gdn_scan_entries", _entries_log_eps_no_phase)])
+def test_gdn_scan_variant_pin_catches(name, mutant, monkeypatch):
+    monkeypatch.setattr(O, name, mutant)
+    with pytest.raises(AssertionError):
+        pin_gdn_scan_variants()

@@ -119,3 +119,24 @@ def test_oracle_readout_order_closed_form(order, expect):
         feat = np.broadcast_to(np.array([1.0, 2.0, 6.0]), (2, 3, 4, 4, 3)).copy()
         out = O.simple_cssm_forward(p, np.zeros((2, 3, 8, 8, 3)), cfg, injected_post_cssm=feat)
         assert np.allclose(out, np.broadcast_to(expect, (2, 3)), rtol=0, atol=1e-5)
+
+
+def test_instance_norm_on_pooled_vector_is_the_bias():
+    """nn.GroupNorm(num_groups=C) (simple_cssm.py:212-214) on a pooled (B, C) vector: flax reduces
+    over axes 1..ndim-2 (none here) and the size-1 within-group axis, so each group is one element
+    (mean = x, var = 0) and the output is the bias alone.  On (B, H, W, C) it normalises each
+    channel over H, W.  Both the oracle and the module's norm follow that."""
+    rng = np.random.default_rng(5)
+    C = 6
+    p = {"scale": rng.standard_normal(C) + 2.0, "bias": rng.standard_normal(C)}
+    x2 = rng.standard_normal((3, C)) * 4.0
+    assert np.array_equal(O.simple_norm(x2, "instance", p), np.broadcast_to(p["bias"], (3, C)))
+    x4 = rng.standard_normal((2, 5, 5, C))
+    mu = x4.mean(axis=(1, 2), keepdims=True)
+    sd = np.sqrt(x4.var(axis=(1, 2), keepdims=True) + 1e-6)
+    assert np.allclose(O.simple_norm(x4, "instance", p), (x4 - mu) / sd * p["scale"] + p["bias"], atol=1e-12)
+    m = SimpleCSSM(cssm_type="gated", embed_dim=C, pos_embed="none", body_norm="instance")
+    pt = {"n": {k: torch.from_numpy(v) for k, v in p.items()}}
+    for x in (x2, x4):
+        got = m._norm(torch.from_numpy(x), "instance", "n", pt, None, False).numpy()
+        assert np.allclose(got, O.simple_norm(x, "instance", p), rtol=0, atol=1e-12)
