@@ -257,12 +257,12 @@ def gdn_step(cell, variables, x, w, S, mark):
                                       p["gate_proj"]["kernel"], p["gate_proj"]["bias"], "silu", out_dtype=f32)
         mark("qkv_gate_proj")
     if S.gdn_core_fused_supported(H, W, cell.delta_key_dim):
-        o = S.gdn_core_fused(qkv, True, ab, cell.gate_type, what, cell.delta_key_dim)
+        o = S.gdn_core_fused(qkv, True, ab, cell.gate_type, what, cell.delta_key_dim, cell.scan_variant)
         mark("core_fused")   # rfft2 -> norms -> delta rule -> irfft2 in one kernel
     else:
         spec, norms = S.rfft2(qkv, want_norms=True)
         mark("rfft2")
-        ohat = S.gdn_scan_bins(spec, norms, ab, cell.gate_type, what, cell.delta_key_dim)
+        ohat = S.gdn_scan_bins(spec, norms, ab, cell.gate_type, what, cell.delta_key_dim, cell.scan_variant)
         mark("scan_bins")
         o = S.irfft2(ohat, W, out_dtype=f32)
         mark("irfft2")

@@ -216,9 +216,11 @@ class GatedDeltaNetCSSM:
     Not part of this build (NotImplementedError): rope_mode other than 'none',
     int_attention_mode, cross_freq_conv_size > 0, ssl_proj_dim > 0, the
     static-image fast path, bf16 / fp8 split-precision scans (use_complex32/16),
-    and a non-separable qkv conv.  scan_mode and use_goom / use_log select
-    numerically equivalent evaluations of the same recurrence; the kernels apply
-    to_goom's floors on every M / Delta entry.
+    and a non-separable qkv conv.  scan_mode and use_log / use_goom select how
+    the scan sees the entries of M and Delta, as in the reference
+    (cssm.py:4693-4701, 4939-4991): to_goom's 1e-7 floor (the default), none
+    (use_log=False, or scan_mode='pallas' at d_k = 2) or log(|x| + 1e-8)
+    (use_goom=False); see :func:`spectral.gdn_scan_variant`.
     """
 
     def __init__(self, channels: int, delta_key_dim: int = 2, kernel_size: int = 11, rope_mode: str = "none",
@@ -269,6 +271,7 @@ class GatedDeltaNetCSSM:
         self.use_complex32 = use_complex32
         self.use_complex16 = use_complex16
         self.scan_mode = scan_mode
+        self.scan_variant = S.gdn_scan_variant(use_log, use_goom, scan_mode, delta_key_dim)
         self.ssd_chunk_size = ssd_chunk_size
         self.learned_init = learned_init
         self.short_conv_size = short_conv_size
@@ -434,12 +437,12 @@ class GatedDeltaNetCSSM:
         # spectral core: rfft2 -> delta-rule recurrence -> irfft2, in one kernel where a workgroup
         # holds a head's state (32 x 32, d_k = 4), else through spectra in HBM
         if S.gdn_core_fused_supported(H, W, dk):
-            o = S.gdn_core_fused(qkv, self.use_spectral_l2_norm, ab, self.gate_type, what, dk)
+            o = S.gdn_core_fused(qkv, self.use_spectral_l2_norm, ab, self.gate_type, what, dk, self.scan_variant)
             del qkv
         else:
             spec, norms = S.rfft2(qkv, want_norms=self.use_spectral_l2_norm)
             del qkv
-            ohat = S.gdn_scan_bins(spec, norms, ab, self.gate_type, what, dk)
+            ohat = S.gdn_scan_bins(spec, norms, ab, self.gate_type, what, dk, self.scan_variant)
             del spec
             o = S.irfft2(ohat, W, out_dtype=f32)
             del ohat

@@ -469,10 +469,17 @@ int cssm_irfft2(const float* spec, long long P, int H, int W, void* y, int dtype
                     "cssm_irfft2");
 }
 
+static int gdn_variant_check(const char* fn, int scan_variant) {
+  if (scan_variant != CSSM_GDN_SCAN_GOOM && scan_variant != CSSM_GDN_SCAN_LINEAR && scan_variant != CSSM_GDN_SCAN_LOG_EPS)
+    return fail(CSSM_ERR_ARG, "%s: scan_variant=%d (0 goom, 1 linear, 2 log-eps)", fn, scan_variant);
+  return CSSM_OK;
+}
+
 int cssm_gdn_scan_bins(const float* spec, const float* norms, const float* ab, long long ab_frame, int ab_head,
-                       int ab_bin, const float* what, int B, int T, int C, int H, int W, int dk, float* ohat,
-                       void* stream) {
+                       int ab_bin, const float* what, int B, int T, int C, int H, int W, int dk, int scan_variant,
+                       float* ohat, void* stream) {
   if (!spec || !ab || !what || !ohat) return fail(CSSM_ERR_NULL, "cssm_gdn_scan_bins: spec, ab, what and ohat must be non-null");
+  if (int e = gdn_variant_check("cssm_gdn_scan_bins", scan_variant)) return e;
   if (B <= 0 || T <= 0 || C <= 0 || H <= 0 || W <= 0 || dk < 1 || dk > 4 || C % dk)
     return fail(CSSM_ERR_SHAPE, "cssm_gdn_scan_bins: B=%d T=%d C=%d H=%d W=%d d_k=%d (1..4, divides C)", B, T, C, H, W, dk);
   if (ab_frame < 0 || ab_head < 0 || ab_bin < 0) return fail(CSSM_ERR_ARG, "cssm_gdn_scan_bins: negative gate stride");
@@ -482,7 +489,8 @@ int cssm_gdn_scan_bins(const float* spec, const float* norms, const float* ab, l
   return hip_status(cssm::launch_gdn_scan_bins(reinterpret_cast<const float2*>(spec), norms,
                                                reinterpret_cast<const float2*>(ab), ab_frame, ab_head, ab_bin,
                                                reinterpret_cast<const float2*>(what), B, T, C, H, W, dk,
-                                               reinterpret_cast<float2*>(ohat), static_cast<hipStream_t>(stream)),
+                                               scan_variant, reinterpret_cast<float2*>(ohat),
+                                               static_cast<hipStream_t>(stream)),
                     "cssm_gdn_scan_bins");
 }
 
@@ -496,16 +504,17 @@ static int gdn_train_check(const char* fn, int B, int T, int C, int H, int W, in
 }
 
 int cssm_gdn_scan_bins_train(const float* spec, const float* ab, long long ab_frame, int ab_head, int ab_bin,
-                             const float* what, int B, int T, int C, int H, int W, int dk, float* ohat, float* states,
-                             void* stream) {
+                             const float* what, int B, int T, int C, int H, int W, int dk, int scan_variant,
+                             float* ohat, float* states, void* stream) {
   if (!spec || !ab || !what || !ohat || !states)
     return fail(CSSM_ERR_NULL, "cssm_gdn_scan_bins_train: spec, ab, what, ohat and states must be non-null");
   if (int e = gdn_train_check("cssm_gdn_scan_bins_train", B, T, C, H, W, dk, ab_frame, ab_head, ab_bin)) return e;
+  if (int e = gdn_variant_check("cssm_gdn_scan_bins_train", scan_variant)) return e;
   if (!aligned(spec, 8) || !aligned(ab, 8) || !aligned(what, 8) || !aligned(ohat, 8) || !aligned(states, 8))
     return fail(CSSM_ERR_ALIGN, "cssm_gdn_scan_bins_train: complex tensors must be 8-byte aligned");
   return hip_status(cssm::launch_gdn_scan_bins_train(
                         reinterpret_cast<const float2*>(spec), reinterpret_cast<const float2*>(ab), ab_frame, ab_head,
-                        ab_bin, reinterpret_cast<const float2*>(what), B, T, C, H, W, dk,
+                        ab_bin, reinterpret_cast<const float2*>(what), B, T, C, H, W, dk, scan_variant,
                         reinterpret_cast<float2*>(ohat), reinterpret_cast<float2*>(states), nullptr, nullptr, nullptr,
                         nullptr, false, static_cast<hipStream_t>(stream)),
                     "cssm_gdn_scan_bins_train");
@@ -513,16 +522,17 @@ int cssm_gdn_scan_bins_train(const float* spec, const float* ab, long long ab_fr
 
 int cssm_gdn_scan_bins_bwd(const float* spec, const float* ab, long long ab_frame, int ab_head, int ab_bin,
                            const float* what, const float* states, const float* dohat, int B, int T, int C, int H,
-                           int W, int dk, float* dspec, float* dab, float* dwhat, void* stream) {
+                           int W, int dk, int scan_variant, float* dspec, float* dab, float* dwhat, void* stream) {
   if (!spec || !ab || !what || !states || !dohat || !dspec || !dab || !dwhat)
     return fail(CSSM_ERR_NULL, "cssm_gdn_scan_bins_bwd: null argument");
   if (int e = gdn_train_check("cssm_gdn_scan_bins_bwd", B, T, C, H, W, dk, ab_frame, ab_head, ab_bin)) return e;
+  if (int e = gdn_variant_check("cssm_gdn_scan_bins_bwd", scan_variant)) return e;
   if (!aligned(spec, 8) || !aligned(ab, 8) || !aligned(what, 8) || !aligned(states, 8) || !aligned(dohat, 8) ||
       !aligned(dspec, 8) || !aligned(dab, 8) || !aligned(dwhat, 8))
     return fail(CSSM_ERR_ALIGN, "cssm_gdn_scan_bins_bwd: complex tensors must be 8-byte aligned");
   return hip_status(cssm::launch_gdn_scan_bins_train(
                         reinterpret_cast<const float2*>(spec), reinterpret_cast<const float2*>(ab), ab_frame, ab_head,
-                        ab_bin, reinterpret_cast<const float2*>(what), B, T, C, H, W, dk, nullptr,
+                        ab_bin, reinterpret_cast<const float2*>(what), B, T, C, H, W, dk, scan_variant, nullptr,
                         const_cast<float2*>(reinterpret_cast<const float2*>(states)),
                         reinterpret_cast<const float2*>(dohat), reinterpret_cast<float2*>(dspec),
                         reinterpret_cast<float2*>(dab), reinterpret_cast<float2*>(dwhat), true,
@@ -551,9 +561,10 @@ int cssm_gdn_core_fused_supported(int H, int W, int delta_key_dim) {
 }
 
 int cssm_gdn_core_fused(const float* qkv, int use_l2, const float* ab, long long ab_frame, int ab_head, int ab_bin,
-                        const float* what, int B, int T, int C, int H, int W, int delta_key_dim, float* o,
-                        void* stream) {
+                        const float* what, int B, int T, int C, int H, int W, int delta_key_dim, int scan_variant,
+                        float* o, void* stream) {
   if (!qkv || !ab || !what || !o) return fail(CSSM_ERR_NULL, "cssm_gdn_core_fused: null argument");
+  if (int e = gdn_variant_check("cssm_gdn_core_fused", scan_variant)) return e;
   if (B <= 0 || T <= 0 || C <= 0 || H <= 0 || W <= 0 || delta_key_dim < 1 || delta_key_dim > 4 ||
       C % delta_key_dim || ab_frame < 0 || ab_head < 0 || ab_bin < 0)
     return fail(CSSM_ERR_SHAPE, "cssm_gdn_core_fused: B=%d T=%d C=%d H=%d W=%d d_k=%d", B, T, C, H, W,
@@ -567,7 +578,7 @@ int cssm_gdn_core_fused(const float* qkv, int use_l2, const float* ab, long long
     return fail(CSSM_ERR_ALIGN, "cssm_gdn_core_fused: qkv and o must be 16-byte aligned, ab and what 8");
   return hip_status(cssm::launch_gdn_core_fused(qkv, use_l2, reinterpret_cast<const float2*>(ab), ab_frame, ab_head,
                                                 ab_bin, reinterpret_cast<const float2*>(what), B, T, C, H, W,
-                                                delta_key_dim, o, static_cast<hipStream_t>(stream)),
+                                                delta_key_dim, scan_variant, o, static_cast<hipStream_t>(stream)),
                     "cssm_gdn_core_fused");
 }
 

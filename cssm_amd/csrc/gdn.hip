@@ -453,6 +453,7 @@ struct GdnBinArgs {
   const float2* what;   // (n_h, H, WF)
   float2* ohat;         // (B, T, C, H, WF)
   int T, C, HWF;
+  int variant;          // kScanGoom / kScanLinear / kScanLogEps (gdn_step.h)
 };
 
 template <int DK>
@@ -489,7 +490,7 @@ __global__ void __launch_bounds__(256) gdn_scan_bins(const GdnBinArgs a) {
     }
     const float2 g = a.ab[fr * a.ab_frame + size_t(head) * a.ab_head + size_t(bin) * a.ab_bin];
     float2 o[DK];
-    gdn_bin_step<DK>(s, q, k, v, wh, g.x, g.y, o);
+    gdn_bin_step<DK>(s, q, k, v, wh, g.x, g.y, a.variant, o);
 #pragma unroll
     for (int i = 0; i < DK; ++i) a.ohat[(fr * C + size_t(head) * DK + i) * HWF + bin] = o[i];
   }
@@ -570,6 +571,7 @@ struct GdnFusedArgs {
   const float2* what;    // (n_h, H, WF)
   float* o;              // (B, T, C, H, W) float32
   int T, C, use_l2;
+  int variant;           // kScanGoom / kScanLinear / kScanLogEps (gdn_step.h)
 };
 
 __global__ void __launch_bounds__(256, 2) gdn_core_fused32(const GdnFusedArgs a) {
@@ -732,7 +734,7 @@ __global__ void __launch_bounds__(256, 2) gdn_core_fused32(const GdnFusedArgs a)
         k[c] = cscale(*bin_ptr(DK + c, bu[j], bv[j]), 0.5f * nrm[DK + c]);
         v[c] = cscale(*bin_ptr(2 * DK + c, bu[j], bv[j]), 0.5f);
       }
-      gdn_bin_step<DK>(st, q, k, v, wh[j], gab[j].x, gab[j].y, o);
+      gdn_bin_step<DK>(st, q, k, v, wh[j], gab[j].x, gab[j].y, a.variant, o);
 #pragma unroll
       for (int c = 0; c < DK; ++c) *bin_ptr(c, bu[j], bv[j]) = cscale(o[c], 1.0f / float(HW));
     };
@@ -749,11 +751,11 @@ __global__ void __launch_bounds__(256, 2) gdn_core_fused32(const GdnFusedArgs a)
         v[c] = cscale(*bin_ptr(2 * DK + c, bu[BPT], bv[BPT]), 0.5f);
         si[c] = sx[(xbin * DK + xrow) * DK + c];
       }
-      const GdnBinPre<DK> pre = gdn_bin_prep<DK>(k, v, wh[BPT], gab[BPT].x, gab[BPT].y);
+      const GdnBinPre<DK> pre = gdn_bin_prep<DK>(k, v, wh[BPT], gab[BPT].x, gab[BPT].y, a.variant);
       float2 vr = v[0];   // v[xrow] by selects (a lane-varying index would place v in memory)
 #pragma unroll
       for (int c = 1; c < DK; ++c) vr = xrow == c ? v[c] : vr;
-      const float2 oi = gdn_bin_row<DK>(si, vr, q, k, pre, gab[BPT].y);
+      const float2 oi = gdn_bin_row<DK>(si, vr, q, k, pre, gab[BPT].y, a.variant);
 #pragma unroll
       for (int c = 0; c < DK; ++c) sx[(xbin * DK + xrow) * DK + c] = si[c];
       *bin_ptr(xrow, bu[BPT], bv[BPT]) = cscale(oi, 1.0f / float(HW));
@@ -786,8 +788,8 @@ __global__ void __launch_bounds__(256, 2) gdn_core_fused32(const GdnFusedArgs a)
 bool gdn_core_fused_supported(int H, int W, int dk) { return H == 32 && W == 32 && dk == kFusedDK; }
 
 hipError_t launch_gdn_core_fused(const float* qkv, int use_l2, const float2* ab, long long ab_frame, int ab_head,
-                                 int ab_bin, const float2* what, int B, int T, int C, int H, int W, int dk, float* o,
-                                 hipStream_t s) {
+                                 int ab_bin, const float2* what, int B, int T, int C, int H, int W, int dk, int variant,
+                                 float* o, hipStream_t s) {
   if (!gdn_core_fused_supported(H, W, dk) || C % dk) return hipErrorInvalidValue;
   GdnFusedArgs a;
   a.qkv = qkv;
@@ -800,13 +802,14 @@ hipError_t launch_gdn_core_fused(const float* qkv, int use_l2, const float2* ab,
   a.T = T;
   a.C = C;
   a.use_l2 = use_l2;
+  a.variant = variant;
   hipLaunchKernelGGL(gdn_core_fused32, dim3(unsigned(C / dk), unsigned(B)), dim3(256), 0, s, a);
   return hipGetLastError();
 }
 
 hipError_t launch_gdn_scan_bins(const float2* spec, const float* norms, const float2* ab, long long ab_frame,
                                 int ab_head, int ab_bin, const float2* what, int B, int T, int C, int H, int W,
-                                int dk, float2* ohat, hipStream_t s) {
+                                int dk, int variant, float2* ohat, hipStream_t s) {
   GdnBinArgs a;
   a.spec = spec;
   a.norms = norms;
@@ -819,6 +822,7 @@ hipError_t launch_gdn_scan_bins(const float2* spec, const float* norms, const fl
   a.T = T;
   a.C = C;
   a.HWF = H * (W / 2 + 1);
+  a.variant = variant;
   const dim3 grid(unsigned((a.HWF + 255) / 256), unsigned(C / dk), unsigned(B));
   switch (dk) {
     case 1: hipLaunchKernelGGL(gdn_scan_bins<1>, grid, dim3(256), 0, s, a); break;

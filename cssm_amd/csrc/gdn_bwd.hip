@@ -18,7 +18,11 @@
 // and through M = aW m, m = delta - beta k'_r conj(k'_c), D = beta v_i conj(k'_r)
 // into aW, beta, k', v.  A floored entry is the constant 1e-7: it passes no
 // gradient to its inputs (the carry still uses the floored value, as the
-// forward did).  The key normalisation's backward is
+// forward did).  The other scan variants (gdn_step.h): the linear scan maps no
+// entry; the log-eps scan's map f(x) = x (1 + 1e-8 / |x|) stretches the
+// tangential part of the gradient, df^T g = g + (1e-8 / |x|) Re(conj(g) i u) i u
+// with u = x / |x| (its constant 1e-8 at x = 0 passes none).
+// The key normalisation's backward is
 //   dk = n dk' - n^3 k Re(sum_l dk'_l conj(k_l)),   n = (|k|^2 + 1e-6)^(-1/2).
 #include <hip/hip_runtime.h>
 #include <math.h>
@@ -42,6 +46,7 @@ struct GdnTrainArgs {
   float2* dab;           // (B, T, n_h, H WF) reverse out: (dalpha, dbeta) of each (head, bin)
   float2* dwhat;         // (B, n_h, H WF) reverse out: dW_hat summed over t, per batch element
   int T, C, HWF;
+  int variant;           // kScanGoom / kScanLinear / kScanLogEps (gdn_step.h)
 };
 
 template <int DK>
@@ -78,27 +83,50 @@ __global__ void __launch_bounds__(256) gdn_scan_bins_save(const GdnTrainArgs a) 
       for (int c = 0; c < DK; ++c) a.states[state_at<DK>(a, b, t, head, i, c, bin)] = s[i][c];
     const float2 g = a.ab[fr * a.ab_frame + size_t(head) * a.ab_head + size_t(bin) * a.ab_bin];
     float2 o[DK];
-    gdn_bin_step<DK>(s, q, k, v, wh, g.x, g.y, o);
+    gdn_bin_step<DK>(s, q, k, v, wh, g.x, g.y, a.variant, o);
 #pragma unroll
     for (int i = 0; i < DK; ++i) a.ohat[(fr * C + size_t(head) * DK + i) * HWF + bin] = o[i];
   }
 }
 
-// M[r][c] as the forward computes it (its materialised path), and whether the floor took it
-__device__ __forceinline__ float2 m_entry(float2 aw, float beta, float2 kr, float2 kc, bool diag, float2& m,
-                                          bool& floored) {
+// an entry x of M or Delta as the scan variant sees it, and whether that value is a constant
+// (to_goom's floor took x, or the log-eps map's 1e-8 at x = 0), which passes no gradient to x
+__device__ __forceinline__ float2 mapped_entry(float2 x, int variant, bool& frozen) {
+  const float r2 = x.x * x.x + x.y * x.y;
+  if (variant == kScanLinear) {
+    frozen = false;
+    return x;
+  }
+  if (variant == kScanLogEps) {
+    frozen = r2 == 0.0f;
+    return logeps_entry(x);
+  }
+  frozen = r2 < 1e-14f;
+  return frozen ? make_float2(1e-7f, 0.0f) : x;
+}
+
+// dL/dx from g = dL/d mapped_entry(x) where that value is not a constant
+__device__ __forceinline__ float2 entry_adjoint(float2 g, float2 x, int variant) {
+  if (variant != kScanLogEps) return g;
+  const float rinv = rsqrtf(fmaf(x.x, x.x, x.y * x.y));
+  const float2 iu = make_float2(-x.y * rinv, x.x * rinv);      // i x / |x|
+  const float f = 1e-8f * rinv * (g.x * iu.x + g.y * iu.y);    // (1e-8 / |x|) Re(conj(g) i u)
+  return make_float2(fmaf(f, iu.x, g.x), fmaf(f, iu.y, g.y));
+}
+
+// M[r][c] as the forward computes it (its materialised path): m = delta_rc - beta k_r conj(k_c), x = aW m
+__device__ __forceinline__ float2 m_entry(float2 aw, float beta, float2 kr, float2 kc, bool diag, int variant,
+                                          float2& m, float2& x, bool& frozen) {
   const float2 kk = cmulc(kr, kc);
   m = make_float2(-beta * kk.x, -beta * kk.y);
   if (diag) m.x += 1.0f;
-  const float2 x = cmul(aw, m);
-  floored = x.x * x.x + x.y * x.y < 1e-14f;
-  return floored ? make_float2(1e-7f, 0.0f) : x;
+  x = cmul(aw, m);
+  return mapped_entry(x, variant, frozen);
 }
 
-__device__ __forceinline__ float2 d_entry(float beta, float2 vi, float2 kr, bool& floored) {
-  const float2 x = cscale(cmulc(vi, kr), beta);
-  floored = x.x * x.x + x.y * x.y < 1e-14f;
-  return floored ? make_float2(1e-7f, 0.0f) : x;
+__device__ __forceinline__ float2 d_entry(float beta, float2 vi, float2 kr, int variant, float2& x, bool& frozen) {
+  x = cscale(cmulc(vi, kr), beta);
+  return mapped_entry(x, variant, frozen);
 }
 
 template <int DK>
@@ -106,7 +134,7 @@ __global__ void __launch_bounds__(256) gdn_scan_bins_bwd(const GdnTrainArgs a) {
   const int bin = blockIdx.x * blockDim.x + threadIdx.x;
   if (bin >= a.HWF) return;
   const int head = blockIdx.y, b = blockIdx.z;
-  const int C = a.C, HWF = a.HWF, nh = C / DK;
+  const int C = a.C, HWF = a.HWF, nh = C / DK, variant = a.variant;
   const float2 wh = a.what[size_t(head) * HWF + bin];
   float2 carry[DK][DK];
 #pragma unroll
@@ -150,12 +178,13 @@ __global__ void __launch_bounds__(256) gdn_scan_bins_bwd(const GdnTrainArgs a) {
 #pragma unroll
       for (int r = 0; r < DK; ++r) {
         bool fl;
-        float2 st = d_entry(beta, v[i], k[r], fl);
+        float2 xd;
+        float2 st = d_entry(beta, v[i], k[r], variant, xd, fl);
 #pragma unroll
         for (int c = 0; c < DK; ++c) {
-          float2 m;
+          float2 m, xm;
           bool fm;
-          const float2 M = m_entry(aw, beta, k[r], k[c], r == c, m, fm);
+          const float2 M = m_entry(aw, beta, k[r], k[c], r == c, variant, m, xm, fm);
           st = cadd(st, cmul(M, sp[i][c]));
         }
         dq[r] = cadd(dq[r], cmulc(dov[i], st));
@@ -176,9 +205,9 @@ __global__ void __launch_bounds__(256) gdn_scan_bins_bwd(const GdnTrainArgs a) {
     for (int r = 0; r < DK; ++r)
 #pragma unroll
       for (int c = 0; c < DK; ++c) {
-        float2 m;
+        float2 m, xm;
         bool fm;
-        const float2 M = m_entry(aw, beta, k[r], k[c], r == c, m, fm);
+        const float2 M = m_entry(aw, beta, k[r], k[c], r == c, variant, m, xm, fm);
         float2 dM = make_float2(0.f, 0.f);
 #pragma unroll
         for (int i = 0; i < DK; ++i) {
@@ -186,6 +215,7 @@ __global__ void __launch_bounds__(256) gdn_scan_bins_bwd(const GdnTrainArgs a) {
           dM = cadd(dM, cmulc(g[i][r], sp[i][c]));             // g conj(s_{t-1})
         }
         if (!fm) {
+          dM = entry_adjoint(dM, xm, variant);                 // dL/d(aW m)
           daw = cadd(daw, cmulc(dM, m));                       // dM conj(m)
           const float2 dm = cmulc(dM, aw);                     // dM conj(aW)
           // m = delta - beta k_r conj(k_c)
@@ -201,9 +231,10 @@ __global__ void __launch_bounds__(256) gdn_scan_bins_bwd(const GdnTrainArgs a) {
 #pragma unroll
       for (int r = 0; r < DK; ++r) {
         bool fl;
-        d_entry(beta, v[i], k[r], fl);
+        float2 xd;
+        d_entry(beta, v[i], k[r], variant, xd, fl);
         if (fl) continue;
-        const float2 dD = g[i][r];
+        const float2 dD = entry_adjoint(g[i][r], xd, variant);
         const float2 vk = cmulc(v[i], k[r]);
         dbeta += dD.x * vk.x + dD.y * vk.y;                    // Re(conj(dD) v_i conj(k_r))
         dv[i] = cadd(dv[i], cscale(cmul(dD, k[r]), beta));
@@ -231,10 +262,10 @@ __global__ void __launch_bounds__(256) gdn_scan_bins_bwd(const GdnTrainArgs a) {
 
 hipError_t launch_gdn_scan_bins_train(const float2* spec, const float2* ab, long long ab_frame, int ab_head,
                                       int ab_bin, const float2* what, int B, int T, int C, int H, int W, int dk,
-                                      float2* ohat, float2* states, const float2* dohat, float2* dspec,
+                                      int variant, float2* ohat, float2* states, const float2* dohat, float2* dspec,
                                       float2* dab, float2* dwhat, bool backward, hipStream_t s) {
   GdnTrainArgs a{spec, ab, ab_frame, ab_head, ab_bin, what, ohat, states, dohat, dspec, dab, dwhat, T, C,
-                 H * (W / 2 + 1)};
+                 H * (W / 2 + 1), variant};
   const dim3 grid(unsigned((a.HWF + 255) / 256), unsigned(C / dk), unsigned(B));
 #define CSSM_GDN_TRAIN(D)                                                                   \
   if (backward) hipLaunchKernelGGL(gdn_scan_bins_bwd<D>, grid, dim3(256), 0, s, a);         \

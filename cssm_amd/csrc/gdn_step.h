@@ -13,8 +13,29 @@ __device__ __forceinline__ float2 goom_floor2(float2 z) {
   return (z.x * z.x + z.y * z.y < 1e-14f) ? make_float2(1e-7f, 0.0f) : z;
 }
 
-// One step of the recurrence for one bin: key-vector norm, M and D with the
-// floors, s_i <- M s_i + D[i], o_i = sum_a s_i[a] q_a.  q and k arrive with the
+// How the slow path's matrix scan sees the entries of M and Delta (cssm.py:4693-4701, 4939-4991):
+//   kScanGoom    use_log and use_goom: to_goom's floor on every entry
+//   kScanLinear  use_log=False (direct complex scan), or scan_mode='pallas' at d_k = 2
+//                (pallas_matrix_2x2_scan): the entries as they are
+//   kScanLogEps  use_log without use_goom: exp(log(|z| + 1e-8) + i angle(z)) = (|z| + 1e-8) z / |z|,
+//                1e-8 at z = 0
+// Each scan evaluates the linear recurrence s_t = M_t s_{t-1} + Delta_t on those entries.
+enum : int { kScanGoom = 0, kScanLinear = 1, kScanLogEps = 2 };
+
+__device__ __forceinline__ float2 logeps_entry(float2 z) {
+  const float r2 = fmaf(z.x, z.x, z.y * z.y);
+  if (r2 == 0.0f) return make_float2(1e-8f, 0.0f);
+  const float f = 1.0f + 1e-8f * rsqrtf(r2);
+  return make_float2(z.x * f, z.y * f);
+}
+
+// the entry the scan sees (kScanGoom or kScanLogEps; kScanLinear never materialises M)
+__device__ __forceinline__ float2 scan_entry(float2 z, int variant) {
+  return variant == kScanLogEps ? logeps_entry(z) : goom_floor2(z);
+}
+
+// One step of the recurrence for one bin: key-vector norm, M and D as the
+// scan variant sees them, s_i <- M s_i + D[i], o_i = sum_a s_i[a] q_a.  q and k arrive with the
 // spectral norms already applied; k is normalised here.  The rows i of the state
 // update independently given k, v and the gates, so the step splits into a
 // per-bin preamble (gdn_bin_prep) and a per-row update (gdn_bin_row) that
@@ -22,13 +43,13 @@ __device__ __forceinline__ float2 goom_floor2(float2 z) {
 template <int DK>
 struct GdnBinPre {
   float2 aw;    // alpha W_hat
-  bool rank1;   // no entry of M or Delta meets to_goom's floor (rank-1 form of M s)
+  bool rank1;   // no entry of M or Delta is mapped (rank-1 form of M s)
 };
 
-// normalises k in place; aw and the floor test of the step
+// normalises k in place; aw and which form of the step the scan variant needs
 template <int DK>
 __device__ __forceinline__ GdnBinPre<DK> gdn_bin_prep(float2 (&k)[DK], const float2 (&v)[DK], float2 wh, float alpha,
-                                                      float beta) {
+                                                      float beta, int variant) {
   float kk = 0.0f;
 #pragma unroll
   for (int j = 0; j < DK; ++j) kk = fmaf(k[j].x, k[j].x, fmaf(k[j].y, k[j].y, kk));
@@ -61,13 +82,16 @@ __device__ __forceinline__ GdnBinPre<DK> gdn_bin_prep(float2 (&k)[DK], const flo
     for (int c = r + 1; c < DK; ++c) kpair = fminf(kpair, k2[r] * k2[c]);
   }
   pre.rank1 = aw2 * dmin > kLim && (DK == 1 || aw2 * b2 * kpair > kLim) && b2 * v2min * k2min > kLim;
+  // the linear scan maps no entry; the log-eps scan moves every entry, so it always materialises
+  if (variant != kScanGoom) pre.rank1 = variant == kScanLinear;
   return pre;
 }
 
 // row i of the state: s_i <- M s_i + Delta[i] (in place), returns o_i = sum_r s_ir q_r
 template <int DK>
 __device__ __forceinline__ float2 gdn_bin_row(float2 (&si)[DK], const float2 vi, const float2 (&q)[DK],
-                                              const float2 (&k)[DK], const GdnBinPre<DK>& pre, float beta) {
+                                              const float2 (&k)[DK], const GdnBinPre<DK>& pre, float beta,
+                                              int variant) {
   const float2 aw = pre.aw;
   if (pre.rank1) {
     float2 p = make_float2(0.f, 0.f);                 // sum_c conj(k_c) s_ic
@@ -95,14 +119,14 @@ __device__ __forceinline__ float2 gdn_bin_row(float2 (&si)[DK], const float2 vi,
   float2 sn[DK];
 #pragma unroll
   for (int r = 0; r < DK; ++r) {
-    float2 acc = goom_floor2(cscale(cmulc(vi, k[r]), beta));
+    float2 acc = scan_entry(cscale(cmulc(vi, k[r]), beta), variant);
 #pragma unroll
     for (int c = 0; c < DK; ++c) {
       // M_rc = alpha W (delta_rc - beta k_r conj k_c)
       const float2 kk_rc = cmulc(k[r], k[c]);
       float2 m = make_float2(-beta * kk_rc.x, -beta * kk_rc.y);
       if (r == c) m.x += 1.0f;
-      const float2 M = goom_floor2(cmul(aw, m));
+      const float2 M = scan_entry(cmul(aw, m), variant);
       acc.x = fmaf(M.x, si[c].x, fmaf(-M.y, si[c].y, acc.x));
       acc.y = fmaf(M.x, si[c].y, fmaf(M.y, si[c].x, acc.y));
     }
@@ -121,10 +145,10 @@ __device__ __forceinline__ float2 gdn_bin_row(float2 (&si)[DK], const float2 vi,
 template <int DK>
 __device__ __forceinline__ void gdn_bin_step(float2 (&s)[DK][DK], const float2 (&q)[DK], float2 (&k)[DK],
                                              const float2 (&v)[DK], float2 wh, float alpha, float beta,
-                                             float2 (&o)[DK]) {
-  const GdnBinPre<DK> pre = gdn_bin_prep<DK>(k, v, wh, alpha, beta);
+                                             int variant, float2 (&o)[DK]) {
+  const GdnBinPre<DK> pre = gdn_bin_prep<DK>(k, v, wh, alpha, beta, variant);
 #pragma unroll
-  for (int i = 0; i < DK; ++i) o[i] = gdn_bin_row<DK>(s[i], v[i], q, k, pre, beta);
+  for (int i = 0; i < DK; ++i) o[i] = gdn_bin_row<DK>(s[i], v[i], q, k, pre, beta, variant);
 }
 
 }  // namespace cssm

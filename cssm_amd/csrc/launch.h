@@ -100,7 +100,7 @@ hipError_t launch_irfft2(const float2* spec, long long P, int H, int W, void* y,
 int fft_planes_min_group(int H, int W);
 hipError_t launch_gdn_scan_bins(const float2* spec, const float* norms, const float2* ab, long long ab_frame,
                                 int ab_head, int ab_bin, const float2* what, int B, int T, int C, int H, int W,
-                                int dk, float2* ohat, hipStream_t s);
+                                int dk, int variant, float2* ohat, hipStream_t s);
 // weight gradient of the depthwise SAME conv of channels-last frames: per-block partial sums
 // (blocks, ks*ks, C) for the caller to add; gdn_bwd.hip
 bool dwconv_wgrad_supported(int W, int C, int ks);
@@ -110,7 +110,7 @@ hipError_t launch_dwconv_wgrad(const float* x, const float* dy, int F, int H, in
 // pass from those states (backward = true); gdn_bwd.hip
 hipError_t launch_gdn_scan_bins_train(const float2* spec, const float2* ab, long long ab_frame, int ab_head,
                                       int ab_bin, const float2* what, int B, int T, int C, int H, int W, int dk,
-                                      float2* ohat, float2* states, const float2* dohat, float2* dspec,
+                                      int variant, float2* ohat, float2* states, const float2* dohat, float2* dspec,
                                       float2* dab, float2* dwhat, bool backward, hipStream_t s);
 // backward of the gated scan: the spectral-domain reverse recurrence per (b, bin), T <= 32
 hipError_t launch_gated_scan_bwd_bins(const float2* uspec, const float2* dspec, const float4* gates,
@@ -119,8 +119,8 @@ hipError_t launch_gated_scan_bwd_bins(const float2* uspec, const float2* dspec, 
 // the GDN spectral core in one kernel (32 x 32 planes, d_k = 4): rfft2 -> norms -> delta rule -> irfft2
 bool gdn_core_fused_supported(int H, int W, int dk);
 hipError_t launch_gdn_core_fused(const float* qkv, int use_l2, const float2* ab, long long ab_frame, int ab_head,
-                                 int ab_bin, const float2* what, int B, int T, int C, int H, int W, int dk, float* o,
-                                 hipStream_t s);
+                                 int ab_bin, const float2* what, int B, int T, int C, int H, int W, int dk, int variant,
+                                 float* o, hipStream_t s);
 hipError_t launch_frame_mean(const void* x, int dtype, int F, int HW, int C, float* out, hipStream_t s);
 hipError_t launch_gdn_gates(const float* ctx, int B, int T, int C, int H, int W, int nh, const GdnGateWeights& w,
                             int temporal, float rope_base, const float* ttable, float2* ab, float2* bkv,

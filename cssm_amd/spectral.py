@@ -530,12 +530,35 @@ def fft_supported(H: int, W: int) -> bool:
     return bool(_lib.load().cssm_fft_min_group(H, W))
 
 
+# how the delta-rule scan sees the entries of M and Delta (cssm_gdn_scan_variant)
+GDN_SCAN_VARIANTS = {"goom": 0, "linear": 1, "log_eps": 2}
+
+
+def gdn_scan_variant(use_log: bool, use_goom: bool, scan_mode: str, delta_key_dim: int) -> str:
+    """The scan GatedDeltaNetCSSM's slow path runs for its flags (cssm.py:4939-4991): 'linear' for
+    scan_mode='pallas' at d_k = 2 (pallas_matrix_2x2_scan) and for use_log=False (the direct complex
+    scan), 'goom' for use_log with use_goom, 'log_eps' for use_log without it (log(|x| + 1e-8),
+    cssm.py:4693-4701)."""
+    if scan_mode == "pallas" and delta_key_dim == 2:
+        return "linear"
+    if not use_log:
+        return "linear"
+    return "goom" if use_goom else "log_eps"
+
+
+def _variant(scan_variant: str) -> int:
+    if scan_variant not in GDN_SCAN_VARIANTS:
+        raise ValueError(f"scan_variant {scan_variant!r}: one of {sorted(GDN_SCAN_VARIANTS)}")
+    return GDN_SCAN_VARIANTS[scan_variant]
+
+
 def gdn_scan_bins(spec: torch.Tensor, norms: Optional[torch.Tensor], ab: torch.Tensor, gate_type: str,
-                  what: torch.Tensor, delta_key_dim: int) -> torch.Tensor:
+                  what: torch.Tensor, delta_key_dim: int, scan_variant: str = "goom") -> torch.Tensor:
     """Delta-rule recurrence over T per (b, head, bin) (cssm.py:4890-5000).
 
     spec (B, T, 3C, H, Wf) complex64, norms (B, T, 3C) or None, ab from :func:`gdn_gates`,
-    what (n_h, H, Wf) complex64.  Returns ohat (B, T, C, H, Wf) complex64."""
+    what (n_h, H, Wf) complex64, scan_variant from :func:`gdn_scan_variant`.  Returns ohat
+    (B, T, C, H, Wf) complex64."""
     _dev(spec, "spec", torch.complex64)
     B, T, C3, H, Wf = spec.shape
     C = C3 // 3
@@ -549,7 +572,8 @@ def gdn_scan_bins(spec: torch.Tensor, norms: Optional[torch.Tensor], ab: torch.T
     fs, hs, bs = strides[gate_type]
     ohat = torch.empty((B, T, C, H, Wf), dtype=torch.complex64, device=spec.device)
     _lib.call("cssm_gdn_scan_bins", spec.data_ptr(), norms.data_ptr() if norms is not None else None,
-              ab.data_ptr(), fs, hs, bs, what.data_ptr(), B, T, C, H, W, delta_key_dim, ohat.data_ptr(), _stream())
+              ab.data_ptr(), fs, hs, bs, what.data_ptr(), B, T, C, H, W, delta_key_dim, _variant(scan_variant),
+              ohat.data_ptr(), _stream())
     return ohat
 
 
@@ -579,7 +603,7 @@ def _ab_strides(ab: torch.Tensor, gate_type: str):
 
 
 def gdn_scan_bins_train(spec: torch.Tensor, ab: torch.Tensor, gate_type: str, what: torch.Tensor,
-                        delta_key_dim: int):
+                        delta_key_dim: int, scan_variant: str = "goom"):
     """Training forward of the delta rule (cssm.py:4898-5000): spec (B, T, 3C, H, Wf) complex64 with
     q and k already scaled by the spectral L2 norms.  Returns (ohat (B, T, C, H, Wf), states
     (B, T, C / d_k, d_k, d_k, H*Wf): the state entering every step, for
@@ -594,12 +618,13 @@ def gdn_scan_bins_train(spec: torch.Tensor, ab: torch.Tensor, gate_type: str, wh
     ohat = torch.empty((B, T, C, H, Wf), dtype=torch.complex64, device=spec.device)
     states = torch.empty((B, T, C // dk, dk, dk, H * Wf), dtype=torch.complex64, device=spec.device)
     _lib.call("cssm_gdn_scan_bins_train", spec.data_ptr(), ab.data_ptr(), fs, hs, bs, what.data_ptr(), B, T, C, H,
-              W, dk, ohat.data_ptr(), states.data_ptr(), _stream())
+              W, dk, _variant(scan_variant), ohat.data_ptr(), states.data_ptr(), _stream())
     return ohat, states
 
 
 def gdn_scan_bins_backward(spec: torch.Tensor, ab: torch.Tensor, gate_type: str, what: torch.Tensor,
-                           states: torch.Tensor, dohat: torch.Tensor, delta_key_dim: int):
+                           states: torch.Tensor, dohat: torch.Tensor, delta_key_dim: int,
+                           scan_variant: str = "goom"):
     """Reverse pass of :func:`gdn_scan_bins_train` (gradients as dL/dRe + i dL/dIm).  Returns
     (dspec (B, T, 3C, H, Wf) complex64, dab (B, T, C / d_k, H*Wf, 2) float32 per (head, bin) --
     summed by the caller over what the gate type shares --, dwhat (B, C / d_k, H, Wf) complex64 per
@@ -617,8 +642,8 @@ def gdn_scan_bins_backward(spec: torch.Tensor, ab: torch.Tensor, gate_type: str,
     dab = torch.empty((B, T, C // dk, H * Wf, 2), dtype=torch.float32, device=spec.device)
     dwhat = torch.empty((B, C // dk, H, Wf), dtype=torch.complex64, device=spec.device)
     _lib.call("cssm_gdn_scan_bins_bwd", spec.data_ptr(), ab.data_ptr(), fs, hs, bs, what.data_ptr(),
-              states.data_ptr(), dohat.data_ptr(), B, T, C, H, W, dk, dspec.data_ptr(), dab.data_ptr(),
-              dwhat.data_ptr(), _stream())
+              states.data_ptr(), dohat.data_ptr(), B, T, C, H, W, dk, _variant(scan_variant), dspec.data_ptr(),
+              dab.data_ptr(), dwhat.data_ptr(), _stream())
     return dspec, dab, dwhat
 
 
@@ -627,7 +652,7 @@ def gdn_core_fused_supported(H: int, W: int, delta_key_dim: int) -> bool:
 
 
 def gdn_core_fused(qkv: torch.Tensor, use_l2: bool, ab: torch.Tensor, gate_type: str, what: torch.Tensor,
-                   delta_key_dim: int) -> torch.Tensor:
+                   delta_key_dim: int, scan_variant: str = "goom") -> torch.Tensor:
     """The GDN spectral core in one kernel (cssm.py:4875-5025): plane-major float32 qkv
     (B, T, 3C, H, W) -> o (B, T, C, H, W) float32, the irfft2 of the readout; the same as
     :func:`rfft2` + :func:`gdn_scan_bins` + :func:`irfft2` where
@@ -642,7 +667,7 @@ def gdn_core_fused(qkv: torch.Tensor, use_l2: bool, ab: torch.Tensor, gate_type:
     fs, hs, bs = strides[gate_type]
     o = torch.empty((B, T, C, H, W), dtype=torch.float32, device=qkv.device)
     _lib.call("cssm_gdn_core_fused", qkv.data_ptr(), int(bool(use_l2)), ab.data_ptr(), fs, hs, bs, what.data_ptr(),
-              B, T, C, H, W, delta_key_dim, o.data_ptr(), _stream())
+              B, T, C, H, W, delta_key_dim, _variant(scan_variant), o.data_ptr(), _stream())
     return o
 
 

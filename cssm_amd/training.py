@@ -302,24 +302,24 @@ class _GdnBinsFn(torch.autograd.Function):
     """ohat = delta-rule recurrence of the (norm-scaled) spectra, cssm.py:4898-5000."""
 
     @staticmethod
-    def forward(ctx, spec, ab, what, gate_type, dk):
-        ohat, states = S.gdn_scan_bins_train(spec, ab, gate_type, what, dk)
+    def forward(ctx, spec, ab, what, gate_type, dk, variant):
+        ohat, states = S.gdn_scan_bins_train(spec, ab, gate_type, what, dk, variant)
         ctx.save_for_backward(spec, ab, what, states)
-        ctx.gate_type, ctx.dk = gate_type, dk
+        ctx.gate_type, ctx.dk, ctx.variant = gate_type, dk, variant
         return ohat
 
     @staticmethod
     def backward(ctx, dohat):
         spec, ab, what, states = ctx.saved_tensors
         dspec, dab, dwhat = S.gdn_scan_bins_backward(spec, ab, ctx.gate_type, what, states, dohat.contiguous(),
-                                                     ctx.dk)
+                                                     ctx.dk, ctx.variant)
         if ctx.gate_type in ("dense", "factored"):      # one (alpha, beta) per bin, shared by the heads
             dab = dab.sum(dim=2)
         elif ctx.gate_type == "channel":                # one per head, shared by the bins
             dab = dab.sum(dim=3)
         else:                                           # one per frame
             dab = dab.sum(dim=(2, 3)).unsqueeze(2)
-        return dspec, dab, dwhat.sum(dim=0), None, None
+        return dspec, dab, dwhat.sum(dim=0), None, None, None
 
 
 def what_planes(k: torch.Tensor, H: int, W: int, rho: float, squash: bool) -> torch.Tensor:
@@ -410,7 +410,7 @@ def gdn_train_apply(cell, params: Dict[str, Any], x: torch.Tensor) -> torch.Tens
         qk = spec[:, :, :2 * C]
         qk = qk * torch.rsqrt((qk.real ** 2 + qk.imag ** 2).sum(dim=(3, 4), keepdim=True) + 1e-6)
         spec = torch.cat([qk, spec[:, :, 2 * C:]], dim=2)
-    ohat = _GdnBinsFn.apply(spec.contiguous(), ab, what, cell.gate_type, dk)
+    ohat = _GdnBinsFn.apply(spec.contiguous(), ab, what, cell.gate_type, dk, cell.scan_variant)
     o = _Irfft2Fn.apply(ohat, W).view(F, C, HW)                              # plane-major
     # per-pixel norm over the channels (dim 1 of the plane-major frames)
     if cell.output_norm == "rms":

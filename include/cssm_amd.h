@@ -31,7 +31,7 @@ extern "C" {
 
 /* 3: K_hat's scan layout (cssm_spectral_kernel scan_order = 1) pairs rows at 128 x 128
  *    (cssm_gated_scan_khat_order). */
-#define CSSM_ABI_VERSION 3
+#define CSSM_ABI_VERSION 4
 
 typedef enum cssm_status {
   CSSM_OK = 0,
@@ -423,11 +423,30 @@ int cssm_irfft2(const float* spec, long long P, int H, int W, void* y, int dtype
 int cssm_fft_min_group(int H, int W);
 
 /*
+ * How the GDN delta-rule scan sees the entries of M_t and Delta_t: the three
+ * evaluations GatedDeltaNetCSSM's slow path selects (cssm.py:4693-4701,
+ * 4939-4991), each the linear recurrence s_t = M_t s_{t-1} + Delta_t on the
+ * entries as mapped:
+ *   GOOM     use_log and use_goom (the default): to_goom's floor on every
+ *            entry, |x| < 1e-7 -> 1e-7 + 0j (goom.py:161-174)
+ *   LINEAR   use_log=False (the direct complex scan, cssm.py:4960-4991), or
+ *            scan_mode='pallas' at delta_key_dim 2 (pallas_matrix_2x2_scan,
+ *            cssm.py:4940-4944): no map
+ *   LOG_EPS  use_log without use_goom: exp(log(|x| + 1e-8) + i angle(x)),
+ *            i.e. (|x| + 1e-8) x / |x|, and 1e-8 + 0j at x = 0
+ */
+typedef enum cssm_gdn_scan_variant {
+  CSSM_GDN_SCAN_GOOM = 0,
+  CSSM_GDN_SCAN_LINEAR = 1,
+  CSSM_GDN_SCAN_LOG_EPS = 2
+} cssm_gdn_scan_variant;
+
+/*
  * Delta-rule recurrence of GatedDeltaNetCSSM per (batch, head, frequency bin)
  * with the d_k x d_k complex state held in registers over all T.  Replaces
- * cssm.py:4890-5000: spectral / key-vector L2 norms, M_t and Delta_t (with
- * to_goom's floors on every entry), the log-space matrix scan
- * (math.py:384-411, operations.py:314-390 -- exactly the linear recurrence
+ * cssm.py:4890-5000: spectral / key-vector L2 norms, M_t and Delta_t (their
+ * entries mapped as scan_variant says), the matrix scan (math.py:384-411,
+ * operations.py:314-390 -- exactly the linear recurrence
  * s_t = M_t s_{t-1} + Delta_t) and the readout o = S q.
  *   spec   (B, T, 3C, H, Wf) complex64: rfft2 of the q, k, v blocks
  *   norms  (B, T, 3C) from cssm_rfft2, or NULL when use_spectral_l2_norm is off
@@ -435,12 +454,13 @@ int cssm_fft_min_group(int H, int W);
  *          ((b T + t) ab_frame + head ab_head + bin ab_bin); dense / factored:
  *          (H*Wf, 0, 1), channel: (n_h, 1, 0), scalar: (1, 0, 0)
  *   what   (n_h, H, Wf) complex64 (cssm_spectral_kernel, goom_floor = 0)
+ *   scan_variant  cssm_gdn_scan_variant
  *   ohat   (B, T, C, H, Wf) complex64 out; output channel head*d_k + i
  * delta_key_dim in {1, 2, 3, 4}, C a multiple of it.
  */
 int cssm_gdn_scan_bins(const float* spec, const float* norms, const float* ab, long long ab_frame,
                        int ab_head, int ab_bin, const float* what, int B, int T, int C, int H, int W,
-                       int delta_key_dim, float* ohat, void* stream);
+                       int delta_key_dim, int scan_variant, float* ohat, void* stream);
 
 /*
  * Weight gradient of the depthwise ks x ks SAME convolution cssm_depthwise_conv
@@ -465,20 +485,21 @@ int cssm_depthwise_conv_wgrad_supported(int W, int C, int ks);
  * reads.  The reference takes its gradients with jax.value_and_grad through the
  * log-space scan (main.py:283; GOOM VJPs goom.py:47-137); this pair replaces
  * that span's forward and backward (cssm.py:4898-5000).
- *   spec, ab, ab_frame, ab_head, ab_bin, what: as cssm_gdn_scan_bins
+ *   spec, ab, ab_frame, ab_head, ab_bin, what, scan_variant: as cssm_gdn_scan_bins
  *   ohat    (B, T, C, H, Wf) complex64 out
  *   states  (B, T, C / d_k, d_k, d_k, H*Wf) complex64 out: s_{t-1} of step t
  */
 int cssm_gdn_scan_bins_train(const float* spec, const float* ab, long long ab_frame, int ab_head, int ab_bin,
-                             const float* what, int B, int T, int C, int H, int W, int delta_key_dim, float* ohat,
-                             float* states, void* stream);
+                             const float* what, int B, int T, int C, int H, int W, int delta_key_dim,
+                             int scan_variant, float* ohat, float* states, void* stream);
 
 /*
  * Reverse pass of cssm_gdn_scan_bins_train: the reverse recurrence over T per
  * (batch, head, bin) through the key-vector norm, M = alpha W (I - beta k k^H)
- * and Delta = beta v k^H (no gradient through an entry to_goom's floor took),
+ * and Delta = beta v k^H through the entry map of scan_variant (no gradient
+ * through an entry to_goom's floor took, or the LOG_EPS map's constant at 0),
  * with gradients written as dL/dRe + i dL/dIm.
- *   spec, ab, strides, what, states: as the forward call
+ *   spec, ab, strides, what, scan_variant, states: as the forward call
  *   dohat  (B, T, C, H, Wf) complex64: dL/d ohat
  *   dspec  (B, T, 3C, H, Wf) complex64 out: dL/d spec (q and k as scaled in spec)
  *   dab    (B, T, C / d_k, H*Wf) (dalpha, dbeta) out per (b, t, head, bin): the caller
@@ -487,7 +508,8 @@ int cssm_gdn_scan_bins_train(const float* spec, const float* ab, long long ab_fr
  */
 int cssm_gdn_scan_bins_bwd(const float* spec, const float* ab, long long ab_frame, int ab_head, int ab_bin,
                            const float* what, const float* states, const float* dohat, int B, int T, int C, int H,
-                           int W, int delta_key_dim, float* dspec, float* dab, float* dwhat, void* stream);
+                           int W, int delta_key_dim, int scan_variant, float* dspec, float* dab, float* dwhat,
+                           void* stream);
 
 /*
  * The GDN spectral core as one kernel where a workgroup can hold a (batch,
@@ -499,13 +521,13 @@ int cssm_gdn_scan_bins_bwd(const float* spec, const float* ab, long long ab_fram
  * per-plane norm sums add in another order).
  *   qkv    (B, T, 3C, H, W) float32 plane-major (the cssm_gdn_qkv_proj output)
  *   use_l2 1 = spectral L2 norms of q and k (use_spectral_l2_norm), 0 = none
- *   ab, ab_frame, ab_head, ab_bin, what: as cssm_gdn_scan_bins
+ *   ab, ab_frame, ab_head, ab_bin, what, scan_variant: as cssm_gdn_scan_bins
  *   o      (B, T, C, H, W) float32 out: the irfft2 of the readout, channel head*d_k + i
  * qkv and o 16-byte aligned, ab and what 8.
  */
 int cssm_gdn_core_fused(const float* qkv, int use_l2, const float* ab, long long ab_frame, int ab_head, int ab_bin,
-                        const float* what, int B, int T, int C, int H, int W, int delta_key_dim, float* o,
-                        void* stream);
+                        const float* what, int B, int T, int C, int H, int W, int delta_key_dim, int scan_variant,
+                        float* o, void* stream);
 
 /* 1 if cssm_gdn_core_fused has a kernel for (H, W, delta_key_dim), else 0. */
 int cssm_gdn_core_fused_supported(int H, int W, int delta_key_dim);

@@ -49,6 +49,24 @@ def _floor(z):
     return torch.where(small, torch.full_like(z, 1e-7), z)
 
 
+def _scan_entries(z, variant):
+    """M / Delta entries as the GDN scan variant sees them (cssm.py:4693-4701, 4939-4991; the
+    oracle's gdn_scan_entries): 'goom' to_goom's floor, 'linear' unchanged, 'log_eps'
+    exp(log(|z| + 1e-8) + i angle(z)) = (|z| + 1e-8) z / |z| and 1e-8 at z = 0, which passes no
+    gradient there."""
+    if variant == "goom":
+        return _floor(z)
+    if variant == "linear":
+        return z
+    if variant == "log_eps":
+        r = torch.view_as_real(z)
+        r2 = r[..., 0] * r[..., 0] + r[..., 1] * r[..., 1]
+        zero = r2 == 0
+        mag = torch.sqrt(torch.where(zero, torch.ones_like(r2), r2))
+        return torch.where(zero, torch.full_like(z, 1e-8), z * (1.0 + 1e-8 / mag))
+    raise ValueError(variant)
+
+
 def scan_core(u, z, gates, khat, c_scale, cols, korder=None):
     """The contract of the fused scan kernel (cssm_gated_scan_fwd with identity load
     activations): u, z (B, T, C, H, W); gates (B, T, H, Wf, 4) = [exp(-Delta),
@@ -276,7 +294,8 @@ class GdnRef:
     training path.  Every gate type, the rms / layer / no output norm, the qkv depthwise conv, the
     short conv and the input gates; M = alpha W (I - beta k k^H) and Delta = beta v k^H are
     materialised per step with to_goom's floor applied entry by entry through torch.where, so a
-    floored entry passes no gradient to its inputs (cssm.py:4911-4937, goom.py:161-174).
+    floored entry passes no gradient to its inputs (cssm.py:4911-4937, goom.py:161-174), or
+    mapped as the scan variant of cfg's use_log / use_goom / scan_mode says (_scan_entries).
     ``cfg`` is the oracle's GDNConfig (rope_mode 'none': the sinusoid context table)."""
 
     def __init__(self, params, cfg, dtype=torch.float64, requires_grad=True):
@@ -346,14 +365,15 @@ class GdnRef:
         qs, ks, vs = l2(spec(q)), l2(spec(k)), spec(v)
         ks = ks / torch.sqrt((ks.real ** 2 + ks.imag ** 2).sum(dim=3, keepdim=True) + 1e-6)
         eye = torch.eye(dk, dtype=dt)[None, None, :, :, None, None]
+        variant = _gdn_variant(cfg)
         s = torch.zeros((B, nh, dk, dk, H, Wf), dtype=qs.dtype)              # s[b, n, i, r, u, v]
         outs = []
         for t in range(T):
             kk = ks[:, t]                                                    # (B, nh, dk, H, Wf)
             aw = al[:, t][:, :, None, None] * what[None, :, None, None]      # (B, nh, 1, 1, H, Wf)
             b_t = be[:, t][:, :, None, None]
-            M = _floor(aw * (eye - b_t * kk[:, :, :, None] * kk.conj()[:, :, None, :]))   # M[b, n, r, c]
-            D = _floor(b_t * vs[:, t][:, :, :, None] * kk.conj()[:, :, None, :])          # D[b, n, i, r]
+            M = _scan_entries(aw * (eye - b_t * kk[:, :, :, None] * kk.conj()[:, :, None, :]), variant)
+            D = _scan_entries(b_t * vs[:, t][:, :, :, None] * kk.conj()[:, :, None, :], variant)   # D[b, n, i, r]
             s = torch.einsum("bnrcuv,bnicuv->bniruv", M, s) + D
             outs.append(torch.einsum("bniruv,bnruv->bniuv", s, qs[:, t]))
         O = torch.stack(outs, dim=1)                                         # (B, T, nh, dk, H, Wf)
@@ -367,11 +387,21 @@ class GdnRef:
         return _dense(o * gv, p["output_proj"])
 
 
-def gdn_bins_core(spec, ab, what, gate_type, dk):
+def _gdn_variant(cfg):
+    """The scan variant of a GDNConfig (cssm.py:4939-4991), as the oracle's gdn_scan_variant."""
+    if cfg.scan_mode == "pallas" and cfg.delta_key_dim == 2:
+        return "linear"
+    if not cfg.use_log:
+        return "linear"
+    return "goom" if cfg.use_goom else "log_eps"
+
+
+def gdn_bins_core(spec, ab, what, gate_type, dk, variant="goom"):
     """The contract of cssm_gdn_scan_bins_train (cssm.py:4898-5000): spec (B, T, 3C, H, Wf) with q
     and k already scaled by the spectral L2 norms, ab (B, T, n_ab, 2) (alpha, beta) laid out per
-    gate type, what (n_h, H, Wf).  Per-bin key norm, floored M and Delta (torch.where), s_t = M
-    s_{t-1} + Delta, o_t = s_t q.  Returns ohat (B, T, C, H, Wf)."""
+    gate type, what (n_h, H, Wf).  Per-bin key norm, M and Delta mapped as the scan variant says
+    (floored by default, torch.where), s_t = M s_{t-1} + Delta, o_t = s_t q.  Returns ohat
+    (B, T, C, H, Wf)."""
     B, T, C3, H, Wf = spec.shape
     C = C3 // 3
     nh = C // dk
@@ -390,8 +420,8 @@ def gdn_bins_core(spec, ab, what, gate_type, dk):
         kk = k[:, t]
         aw = al[:, t][:, :, None, None] * what[None, :, None, None]
         b_t = be[:, t][:, :, None, None]
-        M = _floor(aw * (eye - b_t * kk[:, :, :, None] * kk.conj()[:, :, None, :]))
-        D = _floor(b_t * v[:, t][:, :, :, None] * kk.conj()[:, :, None, :])
+        M = _scan_entries(aw * (eye - b_t * kk[:, :, :, None] * kk.conj()[:, :, None, :]), variant)
+        D = _scan_entries(b_t * v[:, t][:, :, :, None] * kk.conj()[:, :, None, :], variant)
         s = torch.einsum("bnrcuv,bnicuv->bniruv", M, s) + D
         outs.append(torch.einsum("bniruv,bnruv->bniuv", s, q[:, t]))
     return torch.stack(outs, dim=1).reshape(B, T, C, H, Wf)

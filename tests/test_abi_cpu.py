@@ -33,7 +33,7 @@ def test_library_exports_every_declared_symbol():
 def test_abi_version_and_errors_without_gpu():
     from cssm_amd import _lib
     lib = _lib.load()
-    assert lib.cssm_abi_version() == _lib.ABI_VERSION == 3
+    assert lib.cssm_abi_version() == _lib.ABI_VERSION == 4
     assert lib.cssm_strerror(-1) == b"null pointer argument"
     # argument validation happens before any GPU work
     st = lib.cssm_gated_scan_fwd(None, None, None, 0, 1, 1, 1, 8, 8, None, None, 0, 0, None)
@@ -53,6 +53,16 @@ def test_abi_version_and_errors_without_gpu():
     assert st == -4
     st = lib.cssm_spectral_kernel(p, 1, 11, 8, 16, 0.9, 1, 1, 0, p, None)
     assert st == -2
+    # the GDN scan variant (cssm_gdn_scan_variant) is checked before any device work
+    for v in (-1, 3):
+        st = lib.cssm_gdn_scan_bins(p, None, p, 1, 0, 1, p, 1, 2, 8, 8, 8, 4, v, p, None)
+        assert st == -4 and b"scan_variant" in lib.cssm_last_error()
+        st = lib.cssm_gdn_core_fused(p, 1, p, 1, 0, 1, p, 1, 2, 8, 32, 32, 4, v, p, None)
+        assert st == -4 and b"scan_variant" in lib.cssm_last_error()
+        st = lib.cssm_gdn_scan_bins_train(p, p, 1, 0, 1, p, 1, 2, 8, 8, 8, 4, v, p, p, None)
+        assert st == -4 and b"scan_variant" in lib.cssm_last_error()
+        st = lib.cssm_gdn_scan_bins_bwd(p, p, 1, 0, 1, p, p, p, 1, 2, 8, 8, 8, 4, v, p, p, p, None)
+        assert st == -4 and b"scan_variant" in lib.cssm_last_error()
 
 
 @pytest.mark.parametrize("H", [4, 8, 14, 32, 64, 128])

@@ -177,16 +177,19 @@ def test_layer_vjp_adjoint_to_float64_jvp(mods, name, shape, kw):
 
 # ------------------------------------------------------------------------- GDN cell
 
-BINS_CASES = [("factored", 4, 16, False), ("dense", 2, 8, False), ("channel", 4, 8, False), ("scalar", 1, 8, False),
-              ("factored_floored", 4, 16, True)]
+BINS_CASES = [("factored", 4, 16, False, "goom"), ("dense", 2, 8, False, "goom"), ("channel", 4, 8, False, "goom"),
+              ("scalar", 1, 8, False, "goom"), ("factored_floored", 4, 16, True, "goom"),
+              ("factored_zeros_linear", 4, 16, True, "linear"), ("dense_linear", 2, 8, False, "linear"),
+              ("factored_zeros_logeps", 4, 16, True, "log_eps"), ("channel_logeps", 2, 8, False, "log_eps")]
 
 
-@pytest.mark.parametrize("name,dk,H,floored", BINS_CASES, ids=[c[0] for c in BINS_CASES])
-def test_gdn_bins_vjp_matches_float64_reference(mods, name, dk, H, floored):
+@pytest.mark.parametrize("name,dk,H,floored,variant", BINS_CASES, ids=[c[0] for c in BINS_CASES])
+def test_gdn_bins_vjp_matches_float64_reference(mods, name, dk, H, floored, variant):
     """cssm_gdn_scan_bins_train / _bwd through the autograd Function (its per-gate-type sums of
-    the (alpha, beta) gradients included) against float64 autograd of the kernel contract.  The
-    floored case zeroes the keys of head 0 and the values of head 2, so to_goom's floor takes
-    entries of M and Delta there, which must pass no gradient."""
+    the (alpha, beta) gradients included) against float64 autograd of the kernel contract under
+    each scan variant.  The floored cases zero the keys of head 0 and the values of head 2, so
+    M and Delta hold exact zeros there: to_goom's floor and the log-eps map's 1e-8 take them
+    (a constant, which passes no gradient), the linear scan keeps them."""
     _, S, training = mods
     print_case(test="gdn_bins_vjp", case=name)
     gt = name.split("_")[0]
@@ -206,12 +209,12 @@ def test_gdn_bins_vjp_matches_float64_reference(mods, name, dk, H, floored):
     what = O.spectral_kernel(rng.standard_normal((nh, 5, 5)) * 0.2, H, W, 0.999)
     dohat = rng.standard_normal((B, T, C, H, Wf)) + 1j * rng.standard_normal((B, T, C, H, Wf))
     ts = [torch.from_numpy(a).requires_grad_(True) for a in (spec, ab, what)]
-    ref = P.gdn_bins_core(ts[0], ts[1], ts[2], gt, dk)
+    ref = P.gdn_bins_core(ts[0], ts[1], ts[2], gt, dk, variant)
     refs = torch.autograd.grad(ref, ts, torch.from_numpy(dohat))
     dev = [torch.from_numpy(spec).to("cuda", torch.complex64).requires_grad_(True),
            torch.from_numpy(ab).to("cuda", torch.float32).requires_grad_(True),
            torch.from_numpy(what).to("cuda", torch.complex64).requires_grad_(True)]
-    out = training._GdnBinsFn.apply(dev[0], dev[1], dev[2], gt, dk)
+    out = training._GdnBinsFn.apply(dev[0], dev[1], dev[2], gt, dk, variant)
     got = torch.autograd.grad(out, dev, torch.from_numpy(dohat).to("cuda", torch.complex64))
     torch.cuda.synchronize()
     assert rel_err(_ri(out), _ri(ref)) <= TOL
@@ -238,6 +241,11 @@ GDN_LAYER_CASES = [
                                                            delta_key_dim=4, qkv_conv_size=3)),
     # odd planes (the 7 x 7 SHViT stage): the transforms' adjoints weight the last column 2
     ("factored_7x7_odd_planes", (2, 3, 7, 7, 8), dict(gate_type="factored", output_norm="rms", delta_key_dim=4)),
+    # the scan variants of use_log=False (linear) and use_goom=False (log(|x| + 1e-8))
+    ("factored_linear_scan_16", (1, 3, 16, 16, 8), dict(gate_type="factored", output_norm="rms", delta_key_dim=4,
+                                                        use_log=False)),
+    ("channel_logeps_scan_8", (2, 2, 8, 8, 8), dict(gate_type="channel", output_norm="rms", delta_key_dim=2,
+                                                    use_goom=False)),
 ]
 
 

@@ -389,21 +389,30 @@ FUSED_CASES = [
 ]
 
 
+# the reference's flags for each scan variant (cssm.py:4939-4991)
+VARIANT_FLAGS = {"goom": dict(), "linear": dict(use_log=False), "log_eps": dict(use_goom=False)}
+
+
+@pytest.mark.parametrize("variant", ["goom", "linear", "log_eps"])
 @pytest.mark.parametrize("H", [32, 16])
-def test_gdn_core_floored_heads(mods, H):
-    """Heads whose keys or values vanish drive the per-bin step onto its materialised-M path
-    (to_goom's floor takes entries of M and Delta); checked per head against the oracle, so a
-    floored head's small output is not hidden by the others' RMS.  Head 0: k = 0 (every
-    off-diagonal M entry and all of Delta floored); head 1: k with one nonzero component;
-    head 2: v = 0 (Delta floored); head 3: unconstrained.  H = 32 runs the fused core, H = 16
-    the three-kernel core."""
+def test_gdn_core_floored_heads(mods, H, variant):
+    """Heads whose keys or values vanish put exact zeros into M and Delta, where the scan
+    variants differ: to_goom's floor makes them 1e-7 (the materialised-M path), the log-eps map
+    1e-8 (every entry moved), the linear scan leaves them 0 (rank-1 form throughout).  Checked per
+    head against the oracle, so a head's small output is not hidden by the others' RMS.  Head 0:
+    k = 0 (every off-diagonal M entry and all of Delta zero); head 1: k with one nonzero
+    component; head 2: v = 0 (Delta zero); head 3: unconstrained.  A head whose reference is
+    exactly zero (heads 0 and 2 of the linear scan) must come out exactly zero.  H = 32 runs the
+    fused core, H = 16 the three-kernel core."""
     _, S = mods
-    print_case(test="gdn_core_floored_heads", H=H)
+    print_case(test="gdn_core_floored_heads", H=H, variant=variant)
     rng = np.random.default_rng(31)
     B, T, W, C, dk = 1, 4, H, 16, 4
     shape = (B, T, H, W, C)
     nh, Wf = C // dk, W // 2 + 1
-    cfg = O.GDNConfig(channels=C, delta_key_dim=dk, gate_type="factored", use_spectral_l2_norm=True)
+    cfg = O.GDNConfig(channels=C, delta_key_dim=dk, gate_type="factored", use_spectral_l2_norm=True,
+                      **VARIANT_FLAGS[variant])
+    assert O.gdn_scan_variant(cfg) == variant == S.gdn_scan_variant(cfg.use_log, cfg.use_goom, cfg.scan_mode, dk)
     q, k, v = (rng.standard_normal(shape) for _ in range(3))
     k[..., 0:4] = 0.0
     k[..., 5:8] = 0.0
@@ -417,14 +426,18 @@ def test_gdn_core_floored_heads(mods, H):
     ab = _dev(np.stack([alpha, beta], axis=-1))
     wd = _dev(what, torch.complex64)
     if S.gdn_core_fused_supported(H, W, dk):
-        o = S.gdn_core_fused(planes, True, ab, "factored", wd, dk)
+        o = S.gdn_core_fused(planes, True, ab, "factored", wd, dk, variant)
     else:
         spec, norms = S.rfft2(planes, want_norms=True)
-        o = S.irfft2(S.gdn_scan_bins(spec, norms, ab, "factored", wd, dk), W)
+        o = S.irfft2(S.gdn_scan_bins(spec, norms, ab, "factored", wd, dk, variant), W)
     torch.cuda.synchronize()
     got, refp = to_np(o), ref                                 # (B, T, C, H, W)
+    zero_heads = {0, 2} if variant == "linear" else set()
     for h in range(nh):
         sl = slice(h * dk, (h + 1) * dk)
+        if h in zero_heads:
+            assert np.all(refp[:, :, sl] == 0) and np.all(got[:, :, sl] == 0), h
+            continue
         assert np.sqrt(np.mean(refp[:, :, sl] ** 2)) > 0, h
         assert rel_err(got[:, :, sl], refp[:, :, sl]) <= TOL_F32, h
 
@@ -539,6 +552,42 @@ def test_gdn_layer_matches_oracle(mods, name, shape, kw):
     torch.cuda.synchronize()
     assert tuple(y.shape) == shape
     assert rel_err(to_np(y), ref) <= TOL_F32
+
+
+ZERO_FRAME_CASES = [
+    # name, (B, T, H, W, C), cfg kwargs: the fused 32 x 32 core, the three-kernel core, a small plane
+    ("fused32", (2, 6, 32, 32, 16), dict(delta_key_dim=4, gate_type="factored", kernel_size=11)),
+    ("planes16_dk2", (2, 5, 16, 16, 8), dict(delta_key_dim=2, gate_type="channel", kernel_size=5)),
+    ("small14", (1, 4, 14, 14, 8), dict(delta_key_dim=4, gate_type="dense", kernel_size=5, short_conv_size=0)),
+]
+
+
+@pytest.mark.parametrize("variant", ["goom", "linear", "log_eps", "pallas_d2"])
+@pytest.mark.parametrize("name,shape,kw", ZERO_FRAME_CASES, ids=[c[0] for c in ZERO_FRAME_CASES])
+def test_gdn_layer_zero_masked_frames_per_scan_variant(mods, name, shape, kw, variant):
+    """The layer under each of the reference's scan flags (use_log=False, use_goom=False,
+    scan_mode='pallas') with its first frames zeroed as --variable_seq_len does
+    (main.py:1429-1438): those frames' q / k / v planes are constant (bias only), so every
+    non-DC bin of their spectra is zero up to the transform's rounding, the entries the scan
+    variants map differently.  Against the oracle under the same flags."""
+    cells, _ = mods
+    flags = dict(VARIANT_FLAGS.get(variant, {}))
+    kw = dict(kw)
+    if variant == "pallas_d2":
+        flags = dict(scan_mode="pallas")     # the linear 2 x 2 scan at d_k = 2, ignored otherwise
+    kw.update(flags)
+    print_case(test="gdn_layer_zero_frames", case=name, variant=variant)
+    cfg, p, x = _layer(kw, shape, 27)
+    x[:, :2] = 0.0
+    cell = cells.GatedDeltaNetCSSM(channels=shape[4], **kw)
+    expect = ("linear" if kw["delta_key_dim"] == 2 else "goom") if variant == "pallas_d2" else variant
+    assert cell.scan_variant == O.gdn_scan_variant(cfg) == expect
+    ref = O.gdn_forward(p, x, cfg)
+    y = cell.apply(cells.GatedDeltaNetCSSM.load_params(p), _dev(x))
+    torch.cuda.synchronize()
+    assert rel_err(to_np(y), ref) <= TOL_F32
+    # the masked frames alone, against their own RMS
+    assert rel_err(to_np(y[:, :2]), ref[:, :2]) <= TOL_F32
 
 
 def test_gdn_layer_bf16_io(mods):

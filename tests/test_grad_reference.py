@@ -184,7 +184,11 @@ GDN_CFGS = [
     dict(gate_type="dense", output_norm="layer", delta_key_dim=2, qkv_conv_size=3),
     dict(gate_type="channel", output_norm="none", delta_key_dim=4, short_conv_size=0),
     dict(gate_type="scalar", output_norm="rms", delta_key_dim=2, use_input_gates=False, use_spectral_l2_norm=False),
+    # the other scan variants: the linear scan (use_log=False) and log(|x| + 1e-8) (use_goom=False)
+    dict(gate_type="factored", output_norm="rms", delta_key_dim=2, use_log=False),
+    dict(gate_type="dense", output_norm="rms", delta_key_dim=4, use_goom=False),
 ]
+GDN_IDS = ["factored", "dense", "channel", "scalar", "factored_linear_scan", "dense_logeps_scan"]
 
 
 def _gdn(kw, shape, seed):
@@ -194,7 +198,7 @@ def _gdn(kw, shape, seed):
     return cfg, p, rng.standard_normal(shape)
 
 
-@pytest.mark.parametrize("kw", GDN_CFGS, ids=[c["gate_type"] for c in GDN_CFGS])
+@pytest.mark.parametrize("kw", GDN_CFGS, ids=GDN_IDS)
 def test_gdn_float64_forward_equals_oracle(kw):
     cfg, p, x = _gdn(kw, (2, 3, 8, 8, 8), 10)
     ref = O.gdn_forward(p, x, cfg)
@@ -202,7 +206,7 @@ def test_gdn_float64_forward_equals_oracle(kw):
     assert np.max(np.abs(got - ref)) <= 1e-11 * np.sqrt(np.mean(ref ** 2))
 
 
-@pytest.mark.parametrize("kw", GDN_CFGS, ids=[c["gate_type"] for c in GDN_CFGS])
+@pytest.mark.parametrize("kw", GDN_CFGS, ids=GDN_IDS)
 def test_gdn_float64_gradient_equals_finite_differences(kw):
     cfg, p, x = _gdn(kw, (1, 3, 8, 8, 8), 11)
     rng = np.random.default_rng(12)
@@ -249,6 +253,33 @@ def test_gdn_bins_contract_equals_oracle_core():
     ohat = P.gdn_bins_core(spec, ab, torch.from_numpy(what), "factored", dk)
     got = torch.fft.irfft2(ohat, s=(H, W)).numpy()
     assert np.max(np.abs(got - ref)) <= 1e-12 * np.sqrt(np.mean(ref ** 2))
+
+
+@pytest.mark.parametrize("variant", ["goom", "linear", "log_eps"])
+def test_gdn_scan_entry_maps_equal_oracle(variant):
+    """The torch references' entry map (and so the training path's gradient reference) is the
+    oracle's gdn_scan_entries, on random entries, exact zeros (both signs) and entries at the
+    floor's edge."""
+    rng = np.random.default_rng(16)
+    z = (rng.standard_normal(64) + 1j * rng.standard_normal(64)) * np.logspace(-10, 0, 64)
+    z = np.concatenate([z, [0.0, -0.0 + 0j, complex(0, -0.0), 9.9e-8, 1.01e-7]])
+    got = P._scan_entries(torch.from_numpy(z), variant).numpy()
+    ref = O.gdn_scan_entries(z, variant)
+    assert np.max(np.abs(got - ref)) <= 1e-15 * np.max(np.abs(ref)) + 1e-22
+
+
+def test_gdn_logeps_entry_gradient_is_the_tangential_stretch():
+    """d/dx of (|x| + 1e-8) x / |x|: identity along x, (1 + 1e-8 / |x|) across it (what the backward
+    kernel's entry adjoint applies); none through the constant at x = 0."""
+    x = torch.tensor([3e-8 + 4e-8j, 0.6 - 0.8j, 0j], dtype=torch.complex128, requires_grad=True)
+    for g in (1.0 + 0j, 1j):
+        y = P._scan_entries(x, "log_eps")
+        gr, = torch.autograd.grad(y, x, torch.full_like(y, g))
+        xv = x.detach().numpy()
+        u = xv[:2] / np.abs(xv[:2])
+        expect = g + (1e-8 / np.abs(xv[:2])) * np.real(np.conj(g) * 1j * u) * 1j * u
+        assert np.allclose(gr.numpy()[:2], expect, rtol=1e-12, atol=0)
+        assert gr.numpy()[2] == 0
 
 
 def test_gdn_float64_adjoint_identity():
