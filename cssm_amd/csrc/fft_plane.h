@@ -124,7 +124,8 @@ struct Geom {
   // R1/I4 (scalar, rows two apart within a wave), R2/I3 (whole blocks),
   // C1/C2/I1/I2 (one packed-spectrum slot per lane along a row), load/store.
   static constexpr int HALF = W2 >= 4 ? W2 / 2 : 0;
-  static __device__ __forceinline__ int row_off(int pl, int r) { return (pl * H + r) * RS; }
+  // (rows of a plane group stay far below 2^24, so the product is a full-rate 24-bit multiply)
+  static __device__ __forceinline__ int row_off(int pl, int r) { return int(__umul24(unsigned(pl * H + r), unsigned(RS))); }
   // block blk < W1/2 (lo: halves in place) or >= W1/2 (hi: halves swapped), position pos < W2
   static __device__ __forceinline__ int lo_off(int pl, int r, int blk, int pos) {
     return row_off(pl, r) + blk * W2 + pos;
@@ -397,7 +398,7 @@ struct PlaneFft {
     return V4Col{o, o + 2};
   }
   __device__ __forceinline__ void v4_put(int row, const V4Col& c, float4 v) const {
-    float* r = buf + row * G::RS;
+    float* r = buf + G::row_off(0, row);
     if (G::V4_SPLIT) {
       *reinterpret_cast<float2*>(r + c.a) = make_float2(v.x, v.y);
       *reinterpret_cast<float2*>(r + c.b) = make_float2(v.z, v.w);
@@ -406,7 +407,7 @@ struct PlaneFft {
     }
   }
   __device__ __forceinline__ float4 v4_get(int row, const V4Col& c) const {
-    const float* r = buf + row * G::RS;
+    const float* r = buf + G::row_off(0, row);
     if (G::V4_SPLIT) {
       const float2 lo = *reinterpret_cast<const float2*>(r + c.a), hi = *reinterpret_cast<const float2*>(r + c.b);
       return make_float4(lo.x, lo.y, hi.x, hi.y);

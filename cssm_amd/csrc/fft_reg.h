@@ -9,8 +9,8 @@
 //   forward  X[k] = sum_n x[n] exp(-2 pi i n k / N)   (INV = false)
 //   inverse  x[n] = sum_k X[k] exp(+2 pi i n k / N)   (INV = true, unnormalised)
 //
-// The functions are __host__ __device__ so the host-side unit test in
-// tests/ can check them against a brute-force DFT without a GPU.
+// The functions are __host__ __device__ so the host-side unit test
+// (tests/test_fft_reg_host.py) checks them against a brute-force DFT without a GPU.
 #pragma once
 
 #include <hip/hip_runtime.h>
@@ -116,40 +116,65 @@ struct Dft<4, INV> {
   }
 };
 
-// N = N1 * N2 with N1 = 4: index n = s + N2 m, k = k1 + N1 q.
-//   pass 1 (per s):  A_s[k1] = w_N^{s k1} * DFT_4{ x[s + N2 m] }[k1]
-//   pass 2 (per k1): X[k1 + 4 q] = DFT_N2{ A_s[k1] }[q]
+// Radix-2 butterfly with a compile-time twiddle w = w_N^J (the conjugate when
+// INV): x <- x + w y, y <- x - w y.  The trivial twiddles (1, -1, +-i) cost
+// four additions.  Otherwise w = c (1 + i t) with t = s / c (or w = s (t + i)
+// with t = c / s, whichever keeps |t| <= 1), so w y = c z with
+// z = (y.x - t y.y, y.y + t y.x): two FMAs for z and two for each output, six
+// in all instead of a complex multiply (4) plus the four additions (Linzer and
+// Feig's factoring of the twiddle into the butterfly, IBM J. Res. Dev. 1993).
+template <int N, int J, bool INV>
+CSSM_HD void bfly(float2& x, float2& y) {
+  constexpr int j = ((J % N) + N) % N;
+  const float2 a = x, b = y;
+  if constexpr (j == 0) {
+    x = cadd(a, b);
+    y = csub(a, b);
+  } else if constexpr (2 * j == N) {
+    x = csub(a, b);
+    y = cadd(a, b);
+  } else if constexpr (4 * j == N || 4 * j == 3 * N) {
+    const float2 wb = (4 * j == N) ? mul_quarter<INV>(b) : mul_quarter<!INV>(b);
+    x = cadd(a, wb);
+    y = csub(a, wb);
+  } else {
+    constexpr double cd = cx_cos(2.0 * kPi * double(j) / double(N));
+    constexpr double sd = (INV ? 1.0 : -1.0) * cx_sin(2.0 * kPi * double(j) / double(N));
+    constexpr bool CBIG = (cd < 0 ? -cd : cd) >= (sd < 0 ? -sd : sd);
+    constexpr float f = float(CBIG ? cd : sd);          // the factored-out component
+    constexpr float t = float(CBIG ? sd / cd : cd / sd);
+    float2 z;
+    if constexpr (CBIG) {   // w b = c (b.x - t b.y, b.y + t b.x)
+      z = make_float2(fmaf(-t, b.y, b.x), fmaf(t, b.x, b.y));
+    } else {                // w b = s (t b.x - b.y, t b.y + b.x)
+      z = make_float2(fmaf(t, b.x, -b.y), fmaf(t, b.y, b.x));
+    }
+    x = make_float2(fmaf(f, z.x, a.x), fmaf(f, z.y, a.y));
+    y = make_float2(fmaf(-f, z.x, a.x), fmaf(-f, z.y, a.y));
+  }
+}
+
+// N = 2 N2 (N a power of two, >= 8): decimation in time, X[k] = E[k] + w_N^k O[k],
+// X[k + N2] = E[k] - w_N^k O[k] with E, O the DFTs of the even and odd samples,
+// each pair one bfly (52 operations for N = 8, 148 for N = 16).
 template <int N, bool INV>
 struct Dft {
-  static_assert(N % 4 == 0 && N >= 8, "composite in-register DFT needs N = 4 * N2");
+  static_assert(N >= 8 && (N & (N - 1)) == 0, "composite in-register DFT needs a power of two >= 8");
   CSSM_HD static void run(float2* x) {
-    constexpr int N1 = 4, N2 = N / 4;
-    float2 a[N];
+    constexpr int N2 = N / 2;
+    float2 e[N2], o[N2];
     static_for<0, N2>([&](auto S) {
-      constexpr int s = decltype(S)::value;
-      float2 t[N1];
-      static_for<0, N1>([&](auto M) {
-        constexpr int m = decltype(M)::value;
-        t[m] = x[s + N2 * m];
-      });
-      Dft<N1, INV>::run(t);
-      static_for<0, N1>([&](auto K) {
-        constexpr int k = decltype(K)::value;
-        a[s * N1 + k] = twiddle<N, s * k, INV>(t[k]);
-      });
+      constexpr int n = decltype(S)::value;
+      e[n] = x[2 * n];
+      o[n] = x[2 * n + 1];
     });
-    static_for<0, N1>([&](auto K) {
-      constexpr int k1 = decltype(K)::value;
-      float2 t[N2];
-      static_for<0, N2>([&](auto S) {
-        constexpr int s = decltype(S)::value;
-        t[s] = a[s * N1 + k1];
-      });
-      Dft<N2, INV>::run(t);
-      static_for<0, N2>([&](auto Q) {
-        constexpr int q = decltype(Q)::value;
-        x[k1 + N1 * q] = t[q];
-      });
+    Dft<N2, INV>::run(e);
+    Dft<N2, INV>::run(o);
+    static_for<0, N2>([&](auto K) {
+      constexpr int k = decltype(K)::value;
+      bfly<N, k, INV>(e[k], o[k]);
+      x[k] = e[k];
+      x[k + N2] = o[k];
     });
   }
 };

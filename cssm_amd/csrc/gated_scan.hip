@@ -234,21 +234,26 @@ gated_scan_pow2(const ScanArgs a) {
     fft.i4(wv, lane);
 
     // ---------- STORE y_t = y * z_gate, and LOAD u_{t+1} into the same slots
-    // (in chunks of CH vectors to bound the registers in flight)
+    // (in chunks of CH vectors to bound the registers in flight).  With 4-vector
+    // chunks (512-thread groups) z runs one chunk ahead: z of chunk c + 1 is issued
+    // with u of chunk c, so a chunk's stores never wait for a load issued after the
+    // previous chunk's u arrived.
     {
+      constexpr bool ZAHEAD = NT >= 512;
       const auto col = PlaneFft<G>::v4_col(m.c4);
       const Buf ub(up + group_elems(t + 1 < T ? t + 1 : t), GROUP_BYTES);
       const Buf yb(yp + group_elems(t), GROUP_BYTES);
 #pragma unroll
       for (int c = 0; c < G::JLD; c += CH) {
-        V4 ldu[CH];
-        if (c > 0) {
+        V4 ldu[CH], ldn[CH];
+        const int cz = ZAHEAD ? c + CH : c;   // the chunk whose z is loaded now
+        if (ZAHEAD ? cz < G::JLD : c > 0) {
 #pragma unroll
           for (int i = 0; i < CH; ++i) {
             unsigned vo;
             int so;
-            G::template v4_goff<VB>(wv, c + i, m, vo, so);
-            zb.ld(ldg[i], vo, so);
+            G::template v4_goff<VB>(wv, cz + i, m, vo, so);
+            zb.ld(ZAHEAD ? ldn[i] : ldg[i], vo, so);
           }
         }
         if (t + 1 < T) {
@@ -273,6 +278,10 @@ gated_scan_pow2(const ScanArgs a) {
 #pragma unroll
           for (int i = 0; i < CH; ++i)
             fft.v4_put(G::v4_row(wv, c + i, m), col, act4(IO::to_f4(ldu[i]), a.u_act));
+        }
+        if (ZAHEAD && cz < G::JLD) {
+#pragma unroll
+          for (int i = 0; i < CH; ++i) ldg[i] = ldn[i];
         }
         __builtin_amdgcn_sched_barrier(0);
       }
