@@ -221,6 +221,34 @@ def test_gated_layer_bf16_io(mods):
     assert np.sqrt(np.mean((to_np(y) - ref) ** 2)) <= TOL_BF16 * np.sqrt(np.mean(ref ** 2))
 
 
+C5_STAGES = [("c5_14x14x128", (2, 1, 14, 14, 128)), ("c5_7x7x224", (2, 1, 7, 7, 224)),
+             ("c5_4x4x320", (2, 1, 4, 4, 320))]
+
+
+@pytest.mark.parametrize("name,shape", C5_STAGES, ids=[c[0] for c in C5_STAGES])
+def test_gated_layer_c5_stage_widths_bf16(mods, name, shape):
+    """One layer of each CSSM-SHViT stage at its own width (C5: 128 / 224 / 320 channels, expand 2,
+    T = 1, kernel_size 1, bf16 I/O): in_proj on the K-chunked kernel with its per-frame ctx
+    epilogue at K = 128 / 224 / 320, the small-plane scan at 14 x 14 / 7 x 7 and the 4 x 4
+    planes, out_proj at K = 256 / 448 / 640 with a bf16 output."""
+    cells, _ = mods
+    print_case(test="gated_layer_c5_width", case=name)
+    C = shape[-1]
+    kw = dict(channels=C, expand=2, kernel_size=1, gate_type="factored", short_conv_size=0,
+              short_conv_spatial_size=0)
+    cfg, p, x = _layer_inputs(shape, kw, 61)
+    xb = _dev(x, torch.bfloat16)
+    y = cells.GatedCSSM(**kw).apply(cells.GatedCSSM.load_params(p), xb)
+    torch.cuda.synchronize()
+    assert y.dtype == torch.bfloat16 and tuple(y.shape) == shape
+    ref = O.gated_forward(p, to_np(xb), cfg)
+    assert bf16_excess_err(to_np(y), ref) <= TOL_BF16
+    assert np.sqrt(np.mean((to_np(y) - ref) ** 2)) <= TOL_BF16 * np.sqrt(np.mean(ref ** 2))
+    # the same layer with float32 output holds the fp32 bar against the bf16-rounded input
+    yf = cells.GatedCSSM(**kw).apply(cells.GatedCSSM.load_params(p), xb, out_dtype=torch.float32)
+    assert rel_err(to_np(yf), ref) <= TOL_F32
+
+
 def test_gated_layer_two_parameter_trees(mods):
     """One cell applied to two parameter trees of the same shape in turn (e.g. a reloaded
     checkpoint): each output follows its own weights, whatever addresses the allocator reuses."""
