@@ -206,7 +206,8 @@ int cssm_proj_in(const void* x, int in_dtype, int F, int HW, int K, int N, const
   if ((long long)F * HW > 0x7fffffffLL) return fail(CSSM_ERR_SHAPE, "cssm_proj_in: F*HW exceeds 2^31");
   if ((in_dtype != CSSM_F32 && in_dtype != CSSM_BF16) || (out_dtype != CSSM_F32 && out_dtype != CSSM_BF16))
     return fail(CSSM_ERR_ARG, "cssm_proj_in: dtypes %d/%d", in_dtype, out_dtype);
-  if ((act_lo != CSSM_LOAD_IDENTITY && act_lo != CSSM_LOAD_SILU) || (act_hi != CSSM_LOAD_IDENTITY && act_hi != CSSM_LOAD_SILU))
+  if ((act_lo != CSSM_LOAD_IDENTITY && act_lo != CSSM_LOAD_SILU && act_lo != CSSM_PROJ_STORE_PRE_CTX_SILU) ||
+      (act_hi != CSSM_LOAD_IDENTITY && act_hi != CSSM_LOAD_SILU))
     return fail(CSSM_ERR_ARG, "cssm_proj_in: act_lo=%d act_hi=%d", act_lo, act_hi);
   if (!aligned(x, vec_align(in_dtype)))
     return fail(CSSM_ERR_ALIGN, "cssm_proj_in: x must be %zu-byte aligned", vec_align(in_dtype));
@@ -228,7 +229,8 @@ int cssm_proj_in(const void* x, int in_dtype, int F, int HW, int K, int N, const
   if (e != hipSuccess) return hip_status(e, "cssm_proj_in");
   if (ctx != nullptr) {
     e = fused_ctx ? cssm::launch_ctx_reduce(partial, F, HW, tm, slots, N / 2, ctx, s)
-                  : cssm::launch_plane_mean(out_lo, out_dtype, (long long)F * (N / 2), HW, 0, ctx, s);
+                  : cssm::launch_plane_mean(out_lo, out_dtype, (long long)F * (N / 2), HW,
+                                            act_lo == CSSM_PROJ_STORE_PRE_CTX_SILU ? 1 : 0, ctx, s);
   }
   return hip_status(e, "cssm_proj_in");
 }
@@ -467,6 +469,50 @@ int cssm_irfft2(const float* spec, long long P, int H, int W, void* y, int dtype
   return hip_status(cssm::launch_irfft2(reinterpret_cast<const float2*>(spec), P, H, W, y, dtype,
                                         static_cast<hipStream_t>(stream)),
                     "cssm_irfft2");
+}
+
+int cssm_fft_ex_supported(int H, int W) { return cssm::fft_ex_supported(H, W) ? 1 : 0; }
+
+static bool plane_set_ok(const float* p, int fs, int C) { return p == nullptr || (fs >= C && aligned(p, 16)); }
+
+int cssm_rfft2_ex(const float* x, int x_fs, int x_act, const float* a, int a_fs, int a_act, int C, long long P,
+                  int H, int W, float* spec, void* stream) {
+  if (!x || !spec) return fail(CSSM_ERR_NULL, "cssm_rfft2_ex: x and spec must be non-null");
+  if (P <= 0 || C <= 0 || P % C) return fail(CSSM_ERR_SHAPE, "cssm_rfft2_ex: P=%lld C=%d (P a multiple of C)", P, C);
+  if (!cssm::fft_ex_supported(H, W))
+    return fail(CSSM_ERR_UNSUPPORTED, "cssm_rfft2_ex: %dx%d planes (square powers of two 4..128)", H, W);
+  if ((x_act != CSSM_LOAD_IDENTITY && x_act != CSSM_LOAD_SILU) || (a_act != CSSM_LOAD_IDENTITY && a_act != CSSM_LOAD_SILU))
+    return fail(CSSM_ERR_ARG, "cssm_rfft2_ex: x_act=%d a_act=%d", x_act, a_act);
+  if (!plane_set_ok(x, x_fs, C) || !plane_set_ok(a, a_fs, C) || !aligned(spec, 8))
+    return fail(CSSM_ERR_ALIGN, "cssm_rfft2_ex: plane sets need fs >= C and 16-byte alignment, spec 8");
+  cssm::FftEx e{};
+  e.x = {x, x_fs};
+  e.a = {a, a_fs};
+  e.x_act = x_act;
+  e.a_act = a_act;
+  e.C = C;
+  return hip_status(cssm::launch_rfft2_ex(e, P, H, W, reinterpret_cast<float2*>(spec), static_cast<hipStream_t>(stream)),
+                    "cssm_rfft2_ex");
+}
+
+int cssm_irfft2_ex(const float* spec, long long P, int H, int W, int C, float* y, int y_fs, const float* add,
+                   const float* m, int m_fs, const float* d, int d_fs, void* stream) {
+  if (!spec || !y) return fail(CSSM_ERR_NULL, "cssm_irfft2_ex: spec and y must be non-null");
+  if (P <= 0 || C <= 0 || P % C) return fail(CSSM_ERR_SHAPE, "cssm_irfft2_ex: P=%lld C=%d (P a multiple of C)", P, C);
+  if (!cssm::fft_ex_supported(H, W))
+    return fail(CSSM_ERR_UNSUPPORTED, "cssm_irfft2_ex: %dx%d planes (square powers of two 4..128)", H, W);
+  if (!plane_set_ok(y, y_fs, C) || !plane_set_ok(m, m_fs, C) || !plane_set_ok(d, d_fs, C) || !aligned(spec, 8))
+    return fail(CSSM_ERR_ALIGN, "cssm_irfft2_ex: plane sets need fs >= C and 16-byte alignment, spec 8");
+  cssm::FftEx e{};
+  e.m = {m, m_fs};
+  e.d = {d, d_fs};
+  e.y = y;
+  e.y_fs = y_fs;
+  e.add = add;
+  e.C = C;
+  return hip_status(cssm::launch_irfft2_ex(reinterpret_cast<const float2*>(spec), P, H, W, e,
+                                           static_cast<hipStream_t>(stream)),
+                    "cssm_irfft2_ex");
 }
 
 static int gdn_variant_check(const char* fn, int scan_variant) {

@@ -433,6 +433,151 @@ hipError_t launch_irfft2(const float2* spec, long long P, int H, int W, void* y,
 }
 
 // ---------------------------------------------------------------------------
+// The transforms of the gated cell's training backward with the elementwise
+// work around them fused into their load / store phases, on float32 planes
+// addressed as a strided set: plane p = f C + c of a set (ptr, fs) starts at
+// ptr + (f fs + c) H W, so the halves of a plane-major (F, 2C, HW) tensor are
+// sets with fs = 2C.
+//   rfft2_ex   spec = rfft2(act_x(x) [* act_a(a)])        (act: identity or SiLU)
+//   irfft2_ex  y = (irfft2(spec) + add[p]) [* m] [* SiLU'(d)]
+// SiLU'(v) = s (1 + v (1 - s)), s = sigmoid(v).
+// ---------------------------------------------------------------------------
+__device__ __forceinline__ float silu1(float v) { return v * __builtin_amdgcn_rcpf(1.0f + __expf(-v)); }
+__device__ __forceinline__ float dsilu1(float v) {
+  const float s = __builtin_amdgcn_rcpf(1.0f + __expf(-v));
+  return s * fmaf(v, 1.0f - s, 1.0f);
+}
+
+template <int LH, int LW, int NP, int PPT>
+__global__ void __launch_bounds__((NP << (LH + LW)) / PPT)
+rfft2_planes_ex(const FftEx e, long long P, float2* __restrict__ spec) {
+  using G = Geom<LH, LW, NP, PPT>;
+  constexpr int H = G::H, W = G::W, WF = G::WF, NT = G::NT, V4P = H * W / 4;
+  __shared__ __attribute__((aligned(16))) float smem[G::LDS_FLOATS];
+  const PlaneFft<G> fft(smem);
+  const unsigned tid = threadIdx.x;
+  const int w = __builtin_amdgcn_readfirstlane(int(tid) / 64), l = int(tid) % 64;
+  const long long p0 = (long long)blockIdx.x * NP;
+  const int nvalid = int(P - p0 < NP ? P - p0 : NP);
+  fft.init_twiddles(tid);
+  __syncthreads();
+  {
+    const auto m = G::v4_lane(l);
+    const auto col = PlaneFft<G>::v4_col(m.c4);
+    float4 ld[G::JLD];
+#pragma unroll
+    for (int i = 0; i < G::JLD; ++i) {
+      const unsigned f = G::v4_index(G::v4_row(w, i, m), m);
+      const int pl = int(f / V4P), q = int(f % V4P);
+      float4 v = make_float4(0.f, 0.f, 0.f, 0.f);
+      if (pl < nvalid) {
+        v = *reinterpret_cast<const float4*>(e.x.p + e.x.off(p0 + pl, e.C, H * W) + 4 * q);
+        if (e.x_act) v = make_float4(silu1(v.x), silu1(v.y), silu1(v.z), silu1(v.w));
+        if (e.a.p) {
+          float4 u = *reinterpret_cast<const float4*>(e.a.p + e.a.off(p0 + pl, e.C, H * W) + 4 * q);
+          if (e.a_act) u = make_float4(silu1(u.x), silu1(u.y), silu1(u.z), silu1(u.w));
+          v = make_float4(v.x * u.x, v.y * u.y, v.z * u.z, v.w * u.w);
+        }
+      }
+      ld[i] = v;
+    }
+#pragma unroll
+    for (int i = 0; i < G::JLD; ++i) fft.v4_put(G::v4_row(w, i, m), col, ld[i]);
+  }
+  wave_sync();
+  SpecStoreOp<G> op{spec + p0 * H * WF, nullptr, nullptr, nvalid};
+  fft.r1(w, l);
+  fft.r2(w, l);
+  fft.c1(w, l);
+  fft.template c2<true, false>(w, l, op);
+  fft.template edges<true, false>(w, l, op);
+}
+
+template <int LH, int LW, int NP, int PPT>
+__global__ void __launch_bounds__((NP << (LH + LW)) / PPT)
+irfft2_planes_ex(const float2* __restrict__ spec, long long P, const FftEx e) {
+  using G = Geom<LH, LW, NP, PPT>;
+  constexpr int H = G::H, W = G::W, WF = G::WF, NT = G::NT, V4P = H * W / 4;
+  __shared__ __attribute__((aligned(16))) float smem[G::LDS_FLOATS];
+  const PlaneFft<G> fft(smem);
+  const unsigned tid = threadIdx.x;
+  const int w = __builtin_amdgcn_readfirstlane(int(tid) / 64), l = int(tid) % 64;
+  const long long p0 = (long long)blockIdx.x * NP;
+  const int nvalid = int(P - p0 < NP ? P - p0 : NP);
+  fft.init_twiddles(tid);
+  __syncthreads();
+  SpecLoadOp<G> op{spec + p0 * H * WF, 1.0f / float(H * W), nvalid};
+  fft.template c2<false, true>(w, l, op);
+  fft.template edges<false, true>(w, l, op);
+  fft.i1_packed(w, l);
+  fft.i2(w, l);
+  fft.i3(w, l);
+  fft.i4(w, l);
+  const auto m = G::v4_lane(l);
+  const auto col = PlaneFft<G>::v4_col(m.c4);
+  const PlaneSet ys{e.y, e.y_fs};
+#pragma unroll
+  for (int i = 0; i < G::JLD; ++i) {
+    const int row = G::v4_row(w, i, m);
+    const unsigned f = G::v4_index(row, m);
+    const int pl = int(f / V4P), q = int(f % V4P);
+    if (pl >= nvalid) continue;
+    const long long p = p0 + pl;
+    float4 v = fft.v4_get(row, col);
+    if (e.add) {
+      const float c = e.add[p];
+      v = make_float4(v.x + c, v.y + c, v.z + c, v.w + c);
+    }
+    if (e.m.p) {
+      const float4 u = *reinterpret_cast<const float4*>(e.m.p + e.m.off(p, e.C, H * W) + 4 * q);
+      v = make_float4(v.x * u.x, v.y * u.y, v.z * u.z, v.w * u.w);
+    }
+    if (e.d.p) {
+      const float4 u = *reinterpret_cast<const float4*>(e.d.p + e.d.off(p, e.C, H * W) + 4 * q);
+      v = make_float4(v.x * dsilu1(u.x), v.y * dsilu1(u.y), v.z * dsilu1(u.z), v.w * dsilu1(u.w));
+    }
+    *reinterpret_cast<float4*>(e.y + ys.off(p, e.C, H * W) + 4 * q) = v;
+  }
+}
+
+namespace {
+template <int LH, int NP, int PPT>
+hipError_t run_fwd_ex(const FftEx& e, long long P, float2* spec, hipStream_t s) {
+  using G = Geom<LH, LH, NP, PPT>;
+  hipLaunchKernelGGL((rfft2_planes_ex<LH, LH, NP, PPT>), dim3(unsigned((P + NP - 1) / NP)), dim3(G::NT), 0, s, e, P,
+                     spec);
+  return hipGetLastError();
+}
+template <int LH, int NP, int PPT>
+hipError_t run_inv_ex(const float2* spec, long long P, const FftEx& e, hipStream_t s) {
+  using G = Geom<LH, LH, NP, PPT>;
+  hipLaunchKernelGGL((irfft2_planes_ex<LH, LH, NP, PPT>), dim3(unsigned((P + NP - 1) / NP)), dim3(G::NT), 0, s,
+                     spec, P, e);
+  return hipGetLastError();
+}
+}  // namespace
+
+bool fft_ex_supported(int H, int W) { return H == W && H >= 4 && H <= 128 && (H & (H - 1)) == 0; }
+
+hipError_t launch_rfft2_ex(const FftEx& e, long long P, int H, int W, float2* spec, hipStream_t s) {
+  if (!fft_ex_supported(H, W)) return hipErrorInvalidValue;
+#define CSSM_FWD_EX_CASE(LH, NP_, PPT_) \
+  if (np == NP_) return run_fwd_ex<LH, NP_, PPT_>(e, P, spec, s);
+  CSSM_FFT_TABLE(CSSM_FWD_EX_CASE, 64)
+#undef CSSM_FWD_EX_CASE
+  return hipErrorInvalidValue;
+}
+
+hipError_t launch_irfft2_ex(const float2* spec, long long P, int H, int W, const FftEx& e, hipStream_t s) {
+  if (!fft_ex_supported(H, W)) return hipErrorInvalidValue;
+#define CSSM_INV_EX_CASE(LH, NP_, PPT_) \
+  if (np == NP_) return run_inv_ex<LH, NP_, PPT_>(spec, P, e, s);
+  CSSM_FFT_TABLE(CSSM_INV_EX_CASE, 32)
+#undef CSSM_INV_EX_CASE
+  return hipErrorInvalidValue;
+}
+
+// ---------------------------------------------------------------------------
 // Delta-rule recurrence per (b, head, bin), all T steps, state in VGPRs.
 //   q_a, k_a, v_i   spectra of channels head*DK + a of the q / k / v blocks
 //   spectral norm:  x <- x / sqrt(sum_bins |x|^2 + 1e-6)        (q and k, :4890-4897)

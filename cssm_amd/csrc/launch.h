@@ -97,6 +97,27 @@ struct GdnShortConv {
 hipError_t launch_rfft2(const void* x, int dtype, long long P, int H, int W, float2* spec, float* norms,
                         hipStream_t s);
 hipError_t launch_irfft2(const float2* spec, long long P, int H, int W, void* y, int dtype, hipStream_t s);
+// training-path transforms with fused load / store work on strided float32 plane sets (gdn.hip):
+// plane p = f C + c of a set (p, fs) starts at p + (f fs + c) H W
+struct PlaneSet {
+  const float* p;
+  int fs;
+  __device__ __forceinline__ size_t off(long long plane, int C, int HW) const {
+    return (size_t(plane / C) * size_t(fs) + size_t(plane % C)) * size_t(HW);
+  }
+};
+struct FftEx {
+  PlaneSet x, a;      // rfft2: input and optional factor (a.p null: none)
+  int x_act, a_act;   // cssm_load_act of each
+  PlaneSet m, d;      // irfft2: optional factor m and SiLU'-argument d
+  float* y;           // irfft2: output set (fs y_fs)
+  int y_fs;
+  const float* add;   // irfft2: per-plane addend, or null
+  int C;
+};
+bool fft_ex_supported(int H, int W);
+hipError_t launch_rfft2_ex(const FftEx& e, long long P, int H, int W, float2* spec, hipStream_t s);
+hipError_t launch_irfft2_ex(const float2* spec, long long P, int H, int W, const FftEx& e, hipStream_t s);
 int fft_planes_min_group(int H, int W);
 hipError_t launch_gdn_scan_bins(const float2* spec, const float* norms, const float2* ab, long long ab_frame,
                                 int ab_head, int ab_bin, const float2* what, int B, int T, int C, int H, int W,

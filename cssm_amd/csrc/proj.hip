@@ -869,20 +869,27 @@ proj_persist_kernel(const TI* __restrict__ A, int M, int K, int N, const float* 
         }
         float csum = 0.0f;
         int fr = fr_b, p = p_b;
+        // act 3 (proj_in's lower half for training): values stored as they are, channel sums of SiLU
+        const bool sum_silu = lo && act_lo == 3;
 #pragma unroll
         for (int i = 0; i < MI; ++i) {
           const int gm0 = gmb + i * 16;
           const float v[4] = {acc[i][j][0], acc[i][j][1], acc[i][j][2], acc[i][j][3]};
+          float sv[4] = {v[0], v[1], v[2], v[3]};
+          if (sum_silu) {
+#pragma unroll
+            for (int r = 0; r < 4; ++r) sv[r] = v[r] * __builtin_amdgcn_rcpf(1.0f + __expf(-v[r]));
+          }
           if (nok && gm0 + 3 < M && (HW % 4) == 0) {
             st4(dst, (size_t(fr) * NC + c) * HW + p, v);
-            csum += (v[0] + v[1]) + (v[2] + v[3]);
+            csum += (sv[0] + sv[1]) + (sv[2] + sv[3]);
           } else if (nok) {
             int f2 = fr, p2 = p;
 #pragma unroll
             for (int r = 0; r < 4; ++r) {
               if (gm0 + r < M) {
                 st_el(dst, (size_t(f2) * NC + c) * HW + p2, v[r]);
-                csum += v[r];
+                csum += sv[r];
               }
               if (++p2 == HW) {
                 p2 = 0;
@@ -1299,7 +1306,9 @@ proj_kc_kernel(const TI* __restrict__ A, int M, int K, int N, const float* __res
           // value r is row gmb + 16 i + r: frame fr, or fr + 1 once p + r passes HW; rows beyond M add nothing
 #pragma unroll
           for (int r = 0; r < 4; ++r) {
-            const float x = gmb + i * 16 + r < M ? acc[i][j][r] : 0.0f;
+            float x = gmb + i * 16 + r < M ? acc[i][j][r] : 0.0f;
+            // act 3: the stored lower half stays pre-activation, its channel sums are of SiLU
+            if (act_lo == 3) x = x * __builtin_amdgcn_rcpf(1.0f + __expf(-x));
             if (fr + (p + r >= HW ? 1 : 0) != rf) nxt += x;
             else run += x;
           }

@@ -179,13 +179,24 @@ def gated_scan_backward(u: torch.Tensor, z: torch.Tensor, gates: torch.Tensor, k
     sdu = torch.empty_like(uspec)
     dgates = torch.empty_like(gates)
     dkh = torch.empty((B, C, H, Wf), dtype=torch.complex64, device=u.device)
-    _lib.call("cssm_gated_scan_bwd", uspec.data_ptr(), dspec.data_ptr(), gates.data_ptr(), khat.data_ptr(),
-              B, T, C, H, W, float(c_scale), yspec.data_ptr(), sdu.data_ptr(), dgates.data_ptr(), dkh.data_ptr(),
-              _stream())
+    gated_scan_bwd_bins(uspec, dspec, gates, khat, B, T, C, H, W, c_scale, yspec, sdu, dgates, dkh)
     del dspec, uspec
     dz = dy * irfft2(yspec, W)
     du = irfft2(sdu, W)
     return du, dz, dgates, dkh.sum(dim=0)
+
+
+def gated_scan_bwd_bins(uspec, dspec, gates, khat, B: int, T: int, C: int, H: int, W: int, c_scale: float,
+                        yspec, sdu, dgates, dkh) -> None:
+    """The per-bin reverse recurrence of the gated scan (cssm_gated_scan_bwd) on contiguous spectra
+    (B, T, C, H, W//2+1) laid out as the batched transforms write them; outputs written in place."""
+    for t_, n in ((uspec, "uspec"), (dspec, "dspec"), (yspec, "yspec"), (sdu, "sdu"), (khat, "khat"), (dkh, "dkh")):
+        _dev(t_, n, torch.complex64)
+    _dev(gates, "gates", torch.float32)
+    _dev(dgates, "dgates", torch.float32)
+    _lib.call("cssm_gated_scan_bwd", uspec.data_ptr(), dspec.data_ptr(), gates.data_ptr(), khat.data_ptr(),
+              B, T, C, H, W, float(c_scale), yspec.data_ptr(), sdu.data_ptr(), dgates.data_ptr(), dkh.data_ptr(),
+              _stream())
 
 
 def gated_scan_supported(H: int, W: int) -> bool:
@@ -198,12 +209,16 @@ def gated_scan_min_group(H: int, W: int) -> int:
 
 def proj_in(x: torch.Tensor, kernel: torch.Tensor, bias: torch.Tensor, frames: int, hw: int,
             silu_lo: bool = False, silu_hi: bool = False, want_ctx: bool = False,
-            out_dtype: Optional[torch.dtype] = None):
+            out_dtype: Optional[torch.dtype] = None, ctx_of_silu: bool = False):
     """Dense(N) on channels-last rows with the plane-major split (cssm.py:480-484).
 
     x: (..., K) with frames * hw rows.  Returns (lo, hi, ctx): lo, hi are
     (frames, N/2, hw) plane-major; ctx (frames, N/2) = spatial mean of lo, or None.
+    ``ctx_of_silu``: lo is stored without activation and ctx is the mean of SiLU(lo)
+    (CSSM_PROJ_STORE_PRE_CTX_SILU; silu_lo must be False).
     """
+    if ctx_of_silu and silu_lo:
+        raise ValueError("ctx_of_silu stores lo without activation")
     _dev(x, "x")
     if x.dtype not in _DTYPES:
         raise ValueError(f"unsupported dtype {x.dtype}")
@@ -226,8 +241,8 @@ def proj_in(x: torch.Tensor, kernel: torch.Tensor, bias: torch.Tensor, frames: i
         if nbytes:
             ws = torch.empty(nbytes // 4, dtype=torch.float32, device=x.device)
     _lib.call("cssm_proj_in", x.data_ptr(), _DTYPES[x.dtype], frames, hw, K, N, kernel.data_ptr(),
-              bias.data_ptr(), lo.data_ptr(), hi.data_ptr(), _DTYPES[od], int(silu_lo), int(silu_hi),
-              ctx.data_ptr() if ctx is not None else None, ws.data_ptr() if ws is not None else None,
+              bias.data_ptr(), lo.data_ptr(), hi.data_ptr(), _DTYPES[od], 3 if ctx_of_silu else int(silu_lo),
+              int(silu_hi), ctx.data_ptr() if ctx is not None else None, ws.data_ptr() if ws is not None else None,
               nbytes, _stream())
     return lo, hi, ctx
 
@@ -528,6 +543,57 @@ def irfft2(spec: torch.Tensor, W: int, out_dtype: torch.dtype = torch.float32) -
 
 def fft_supported(H: int, W: int) -> bool:
     return bool(_lib.load().cssm_fft_min_group(H, W))
+
+
+def fft_ex_supported(H: int, W: int) -> bool:
+    return bool(_lib.load().cssm_fft_ex_supported(H, W))
+
+
+def _plane_set(t: Optional[torch.Tensor], C: int, HW: int, name: str):
+    """(pointer, frame stride in planes) of a float32 plane set viewed as (F, C, HW) inside a
+    contiguous (F, S, HW) tensor, S >= C (a channel slice of a plane-major tensor)."""
+    if t is None:
+        return None, C
+    if not isinstance(t, torch.Tensor) or t.device.type != "cuda" or t.dtype != torch.float32:
+        raise ValueError(f"{name} must be a float32 GPU tensor")
+    F = t.shape[0]
+    if t.dim() != 3 or t.shape[1] != C or t.shape[2] != HW or t.stride(2) != 1 or t.stride(1) != HW \
+            or t.stride(0) % HW or t.stride(0) // HW < C:
+        raise ValueError(f"{name}: a (F, {C}, {HW}) channel slice of a plane-major tensor is needed")
+    return t.data_ptr(), t.stride(0) // HW
+
+
+def rfft2_ex(x: torch.Tensor, H: int, W: int, x_silu: bool = False, a: Optional[torch.Tensor] = None,
+             a_silu: bool = False) -> torch.Tensor:
+    """spec = rfft2(act(x) * act(a)) of float32 plane sets x, a (F, C, H*W) (channel slices of
+    plane-major tensors allowed): (F, C, H, W//2+1) complex64 (cssm_rfft2_ex)."""
+    F, C, HW = x.shape
+    xp, xfs = _plane_set(x, C, HW, "x")
+    ap, afs = _plane_set(a, C, HW, "a")
+    spec = torch.empty((F, C, H, W // 2 + 1), dtype=torch.complex64, device=x.device)
+    _lib.call("cssm_rfft2_ex", xp, xfs, int(x_silu), ap, afs, int(a_silu), C, F * C, H, W, spec.data_ptr(),
+              _stream())
+    return spec
+
+
+def irfft2_ex(spec: torch.Tensor, W: int, y: torch.Tensor, add: Optional[torch.Tensor] = None,
+              m: Optional[torch.Tensor] = None, d: Optional[torch.Tensor] = None) -> torch.Tensor:
+    """y = (irfft2(spec) + add[p]) * m * SiLU'(d) into the float32 plane set y (F, C, H*W) (a
+    channel slice of a plane-major tensor allowed); add (F, C) or None, m / d plane sets or None
+    (cssm_irfft2_ex).  Returns y."""
+    _dev(spec, "spec", torch.complex64)
+    F, C, H, Wf = spec.shape
+    HW = H * W
+    yp, yfs = _plane_set(y, C, HW, "y")
+    mp, mfs = _plane_set(m, C, HW, "m")
+    dp, dfs = _plane_set(d, C, HW, "d")
+    if add is not None:
+        _dev(add, "add", torch.float32)
+        if tuple(add.shape) != (F, C) or not add.is_contiguous():
+            raise ValueError(f"add must be contiguous ({F}, {C})")
+    _lib.call("cssm_irfft2_ex", spec.data_ptr(), F * C, H, W, C, yp, yfs,
+              add.data_ptr() if add is not None else None, mp, mfs, dp, dfs, _stream())
+    return y
 
 
 # how the delta-rule scan sees the entries of M and Delta (cssm_gdn_scan_variant)

@@ -207,6 +207,84 @@ def _causal_t(x5, p):
     return sum(terms)
 
 
+def _gate_leaves(p: Dict[str, Any], gate_type: str):
+    """The gate projections' parameter tensors in a fixed order, and a function rebuilding the
+    dict gate_planes reads from such a list."""
+    names = []
+    for n in ("delta_proj", "B_proj", "C_proj"):
+        names += [f"{n}_h", f"{n}_w"] if gate_type == "factored" else [n]
+    leaves = [p[n][k] for n in names for k in ("kernel", "bias")]
+
+    def rebuild(ts):
+        return {n: {"kernel": ts[2 * i], "bias": ts[2 * i + 1]} for i, n in enumerate(names)}
+    return leaves, rebuild
+
+
+class _GatedInScanFn(torch.autograd.Function):
+    """in_proj -> SiLU -> ctx -> gates -> fused scan -> x SiLU(z) of the gated cell without short
+    convolutions (cssm.py:480-581 up to out_proj), as one autograd node whose backward runs on HIP
+    kernels end to end: in_proj stores the pre-activations and takes ctx as the mean of their
+    SiLU in the same pass (CSSM_PROJ_STORE_PRE_CTX_SILU); the scan applies both SiLUs on load.
+    Backward: rfft2 of SiLU(x_main) and of dy * SiLU(z) (cssm_rfft2_ex), the reverse recurrence
+    (cssm_gated_scan_bwd), the gate / K_hat construction differentiated by torch on its small
+    tensors, then cssm_irfft2_ex writes the two pre-activation gradients straight into one
+    plane-major (F, 2C, HW) tensor: dz = irfft2(Y) * dy * SiLU'(z) and
+    dx_main = (irfft2(dU) + dctx / HW) * SiLU'(x_main), the ctx term being the spatial mean's
+    gradient; in_proj's gradients follow from that tensor (dx on the projection kernel with W^T,
+    dW as one batched GEMM over frames)."""
+
+    @staticmethod
+    def forward(ctx, x2, w_in, b_in, kernel, meta, *gate_params):
+        B, T, H, W, Ci, gate_type, activation, rho, rebuild = meta
+        F, HW = B * T, H * W
+        xm, z, cx = S.proj_in(x2, w_in, b_in, F, HW, want_ctx=True, out_dtype=torch.float32, ctx_of_silu=True)
+        c_scale = S.scan_c_scale(H, W)
+        gates = gate_planes(cx.view(B, T, Ci), rebuild(list(gate_params)), H, W, gate_type, activation, c_scale)
+        khat = khat_planes(kernel, H, W, rho)
+        y = S.gated_scan(xm.view(B, T, Ci, H, W), z.view(B, T, Ci, H, W), gates.contiguous(), khat.contiguous(),
+                         u_silu=True, z_silu=True)
+        ctx.save_for_backward(x2, w_in, xm, z, cx, kernel, *gate_params)
+        ctx.meta = meta
+        return y
+
+    @staticmethod
+    def backward(ctx, dy):
+        x2, w_in, xm, z, cx, kernel, *gate_params = ctx.saved_tensors
+        B, T, H, W, Ci, gate_type, activation, rho, rebuild = ctx.meta
+        F, HW, Wf = B * T, H * W, W // 2 + 1
+        K = x2.shape[1]
+        dy = dy.contiguous().view(F, Ci, HW)
+        c_scale = S.scan_c_scale(H, W)
+        with torch.enable_grad():
+            cx_l = cx.detach().requires_grad_(True)
+            gp_l = [g.detach().requires_grad_(True) for g in gate_params]
+            k_l = kernel.detach().requires_grad_(True)
+            gates = gate_planes(cx_l.view(B, T, Ci), rebuild(gp_l), H, W, gate_type, activation, c_scale)
+            khat = khat_planes(k_l, H, W, rho)
+        gates_c, khat_c = gates.detach().contiguous(), khat.detach().contiguous()
+        uspec = S.rfft2_ex(xm, H, W, x_silu=True)
+        dspec = S.rfft2_ex(dy, H, W, a=z, a_silu=True)
+        yspec = torch.empty_like(uspec)
+        sdu = torch.empty_like(uspec)
+        dgates = torch.empty_like(gates_c)
+        dkh = torch.empty((B, Ci, H, Wf), dtype=torch.complex64, device=dy.device)
+        S.gated_scan_bwd_bins(uspec, dspec, gates_c, khat_c, B, T, Ci, H, W, c_scale, yspec, sdu, dgates, dkh)
+        del uspec, dspec
+        grads = torch.autograd.grad([gates, khat], [cx_l] + gp_l + [k_l], [dgates, dkh.sum(dim=0)],
+                                    allow_unused=True)
+        dcx = grads[0]
+        dxz = torch.empty((F, 2 * Ci, HW), dtype=torch.float32, device=dy.device)
+        S.irfft2_ex(yspec, W, dxz[:, Ci:], m=dy, d=z)
+        S.irfft2_ex(sdu, W, dxz[:, :Ci], add=(dcx.reshape(F, Ci) * (1.0 / HW)).contiguous(), d=xm)
+        del yspec, sdu
+        dx = S.proj_out(dxz, w_in.t().contiguous(), w_in.new_zeros(K), out_dtype=torch.float32)
+        dw = torch.bmm(dxz, x2.view(F, HW, K)).sum(dim=0).t()
+        db = dxz.sum(dim=(0, 2))
+        gp_grads = [g if g is not None else torch.zeros_like(p) for g, p in zip(grads[1:-1], gate_params)]
+        dk = grads[-1] if grads[-1] is not None else torch.zeros_like(kernel)
+        return (dx, dw, db, dk, None, *gp_grads)
+
+
 def gated_train_apply(cell, params: Dict[str, Any], x: torch.Tensor) -> torch.Tensor:
     """GatedCSSM forward with autograd (x (B, T, H, W, C) float32 on the GPU; params: the cell's
     tree of float32 device tensors).  Same results as ``cell.apply`` up to float32 rounding."""
@@ -216,10 +294,19 @@ def gated_train_apply(cell, params: Dict[str, Any], x: torch.Tensor) -> torch.Te
     F, HW = B * T, H * W
     if not S.gated_scan_supported(H, W):
         raise NotImplementedError(f"no fused scan kernel for {H}x{W} planes")
+    no_convs = cell.short_conv_spatial_size == 0 and cell.short_conv_size == 0
+    if no_convs and S.fft_ex_supported(H, W):
+        # in_proj through the scan as one node whose backward runs on the fused HIP transforms
+        gps, rebuild = _gate_leaves(p, cell.gate_type)
+        meta = (B, T, H, W, Ci, cell.gate_type, cell.gate_activation, cell.spectral_rho, rebuild)
+        y = _GatedInScanFn.apply(x.reshape(-1, cin).float().contiguous(), p["in_proj"]["kernel"],
+                                 p["in_proj"]["bias"], p["kernel"], meta, *gps)
+        out = _ProjOutFn.apply(y.view(B * T, Ci, H * W), p["out_proj"]["kernel"], p["out_proj"]["bias"])
+        return out.view(B, T, H, W, cell.channels)
     xz = _ProjPlanesFn.apply(x.reshape(-1, cin).float().contiguous(), p["in_proj"]["kernel"], p["in_proj"]["bias"],
                              F, HW)                                        # plane-major (F, 2C, HW)
     c_scale = S.scan_c_scale(H, W)
-    if cell.short_conv_spatial_size == 0 and cell.short_conv_size == 0:
+    if no_convs:
         u, zg = _SplitSiluFn.apply(xz, Ci)
         u, zg = u.view(B, T, Ci, H, W), zg.view(B, T, Ci, H, W)
         return _gated_core(cell, p, u, zg, B, T, H, W, Ci, c_scale)

@@ -58,6 +58,11 @@ typedef enum cssm_gate_act {
 /* elementwise activation applied when an input plane is loaded */
 typedef enum cssm_load_act { CSSM_LOAD_IDENTITY = 0, CSSM_LOAD_SILU = 1 } cssm_load_act;
 
+/* cssm_proj_in's act_lo only: store the lower half as it is (pre-activation), take ctx as the
+ * spatial mean of its SiLU -- what the training path needs, which keeps the pre-activations for
+ * the SiLU's backward and applies the SiLU when the scan loads them. */
+#define CSSM_PROJ_STORE_PRE_CTX_SILU 3
+
 /*
  * Gate projection weights of GatedCSSM (Flax parameter names in brackets).
  * Index 0 = delta_proj, 1 = B_proj, 2 = C_proj.
@@ -192,7 +197,8 @@ int cssm_gated_scan_bwd(const float* uspec, const float* dspec, const float* gat
  *   kernel   (K, N) float32 [in_proj/kernel], bias (N) [in_proj/bias]
  *   out_lo   (F, N/2, HW) plane-major of out_dtype: output channels [0, N/2)
  *   out_hi   (F, N/2, HW): output channels [N/2, N) (N must be even)
- *   act_lo, act_hi  cssm_load_act applied to each half
+ *   act_lo, act_hi  cssm_load_act applied to each half; act_lo may also be
+ *            CSSM_PROJ_STORE_PRE_CTX_SILU (out_lo stored without activation, ctx of its SiLU)
  *   ctx      (F, N/2) float32 out = mean over HW of out_lo, or NULL (summed in fp32; with a
  *            bf16 out_lo the sums may be taken before or after its rounding)
  *   workspace  device scratch of cssm_proj_in_workspace_size(F, HW, K, N) bytes
@@ -421,6 +427,29 @@ int cssm_irfft2(const float* spec, long long P, int H, int W, void* y, int dtype
 
 /* 1 if cssm_rfft2 / cssm_irfft2 have a kernel for (H, W) planes, else 0. */
 int cssm_fft_min_group(int H, int W);
+
+/*
+ * The transforms of the gated cell's training backward (the reference takes
+ * these gradients with jax.value_and_grad through cssm.py:502-581, main.py:283)
+ * with the elementwise work around them fused into their load and store
+ * phases.  float32 planes are addressed as strided sets: plane p = f*C + c of
+ * a set (ptr, fs) starts at ptr + (f*fs + c)*H*W, so the halves of a
+ * plane-major (F, 2C, H*W) tensor are sets with fs = 2C.  P planes, a
+ * multiple of C; H = W a power of two 4..128 (cssm_fft_ex_supported); sets
+ * 16-byte aligned with fs >= C; spec (P, H, W/2+1) complex64, 8-byte aligned.
+ *   cssm_rfft2_ex   spec = rfft2(x_act(x) * a_act(a)); a may be NULL (factor 1)
+ *                   (x_act, a_act: cssm_load_act)
+ *   cssm_irfft2_ex  y = (irfft2(spec) + add[p]) * m * SiLU'(d), each of add
+ *                   (P floats), m and d optional (NULL); SiLU'(v) = s (1 + v (1 - s)),
+ *                   s = sigmoid(v)
+ */
+int cssm_rfft2_ex(const float* x, int x_fs, int x_act, const float* a, int a_fs, int a_act, int C, long long P,
+                  int H, int W, float* spec, void* stream);
+int cssm_irfft2_ex(const float* spec, long long P, int H, int W, int C, float* y, int y_fs, const float* add,
+                   const float* m, int m_fs, const float* d, int d_fs, void* stream);
+
+/* 1 if cssm_rfft2_ex / cssm_irfft2_ex have a kernel for (H, W) planes, else 0. */
+int cssm_fft_ex_supported(int H, int W);
 
 /*
  * How the GDN delta-rule scan sees the entries of M_t and Delta_t: the three

@@ -82,7 +82,49 @@ LAYER_CASES = [
     # odd planes: the last column is an interior bin (no Nyquist column), weight 2 in the C2R rule
     ("factored_7x7_odd", (2, 2, 7, 7, 8), dict(channels=8, kernel_size=3, gate_type="factored", short_conv_size=0,
                                                short_conv_spatial_size=0)),
+    # no short convs on power-of-two planes: in_proj through the scan as one node with the fused
+    # transforms (cssm_rfft2_ex / cssm_irfft2_ex) in its backward
+    ("dense_128_fused_node", (1, 2, 128, 128, 4), dict(channels=4, kernel_size=11, gate_type="dense",
+                                                       short_conv_size=0, short_conv_spatial_size=0)),
+    ("factored_4x4_expand2_fused_node", (3, 2, 4, 4, 8), dict(channels=8, expand=2, kernel_size=1,
+                                                               gate_type="factored", gate_activation="sigmoid",
+                                                               short_conv_size=0, short_conv_spatial_size=0)),
 ]
+
+
+@pytest.mark.parametrize("H,F,C", [(128, 2, 3), (32, 3, 4), (8, 2, 8), (4, 3, 2)])
+def test_fused_training_transforms_match_torch(mods, H, F, C):
+    """cssm_rfft2_ex / cssm_irfft2_ex on the halves of a plane-major (F, 2C, HW) tensor (frame
+    stride 2C) against torch's FFTs of the same elementwise expressions."""
+    _, S, _ = mods
+    print_case(test="fft_ex", H=H, F=F, C=C)
+    rng = np.random.default_rng(46)
+    W, HW, Wf = H, H * H, H // 2 + 1
+    xz = torch.from_numpy(rng.standard_normal((F, 2 * C, HW))).to("cuda", torch.float32)
+    dy = torch.from_numpy(rng.standard_normal((F, C, HW))).to("cuda", torch.float32)
+    xm, z = xz[:, :C], xz[:, C:]
+    silu, sg = torch.nn.functional.silu, torch.sigmoid
+    d64 = lambda t: t.double().cpu()
+    ref_u = torch.fft.rfft2(silu(d64(xm)).view(F, C, H, W))
+    ref_d = torch.fft.rfft2((d64(dy) * silu(d64(z))).view(F, C, H, W))
+    got_u = S.rfft2_ex(xm, H, W, x_silu=True)
+    got_d = S.rfft2_ex(dy, H, W, a=z, a_silu=True)
+    torch.cuda.synchronize()
+    for g, r in ((got_u, ref_u), (got_d, ref_d)):
+        assert rel_err(torch.view_as_real(g).cpu().numpy(), torch.view_as_real(r).numpy()) <= 1e-5
+    spec = torch.from_numpy(rng.standard_normal((F, C, H, Wf)) + 1j * rng.standard_normal((F, C, H, Wf))).to(
+        "cuda", torch.complex64)
+    add = torch.from_numpy(rng.standard_normal((F, C))).to("cuda", torch.float32)
+    out = torch.full((F, 2 * C, HW), 7.0, device="cuda")
+    S.irfft2_ex(spec, W, out[:, C:], m=dy, d=z)
+    S.irfft2_ex(spec, W, out[:, :C], add=add, d=xm)
+    torch.cuda.synchronize()
+    base = torch.fft.irfft2(spec.cpu().to(torch.complex128), s=(H, W)).view(F, C, HW)
+    dsilu = lambda v: sg(v) * (1 + v * (1 - sg(v)))
+    ref_hi = base * d64(dy) * dsilu(d64(z))
+    ref_lo = (base + d64(add)[:, :, None]) * dsilu(d64(xm))
+    assert rel_err(out[:, C:].cpu().numpy(), ref_hi.numpy()) <= 1e-5
+    assert rel_err(out[:, :C].cpu().numpy(), ref_lo.numpy()) <= 1e-5
 
 
 def _leaves(tree, prefix=""):
