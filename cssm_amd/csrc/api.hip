@@ -495,9 +495,13 @@ int cssm_rfft2_ex(const float* x, int x_fs, int x_act, const float* a, int a_fs,
                     "cssm_rfft2_ex");
 }
 
+int cssm_irfft2_ex_sums_supported(long long P, int H, int W) { return cssm::irfft2_ex_sums_supported(P, H, W) ? 1 : 0; }
+
 int cssm_irfft2_ex(const float* spec, long long P, int H, int W, int C, float* y, int y_fs, const float* add,
-                   const float* m, int m_fs, const float* d, int d_fs, void* stream) {
+                   const float* m, int m_fs, const float* d, int d_fs, float* sums, void* stream) {
   if (!spec || !y) return fail(CSSM_ERR_NULL, "cssm_irfft2_ex: spec and y must be non-null");
+  if (sums && !cssm::irfft2_ex_sums_supported(P, H, W))
+    return fail(CSSM_ERR_UNSUPPORTED, "cssm_irfft2_ex: plane sums of %lld %dx%d planes", P, H, W);
   if (P <= 0 || C <= 0 || P % C) return fail(CSSM_ERR_SHAPE, "cssm_irfft2_ex: P=%lld C=%d (P a multiple of C)", P, C);
   if (!cssm::fft_ex_supported(H, W))
     return fail(CSSM_ERR_UNSUPPORTED, "cssm_irfft2_ex: %dx%d planes (square powers of two 4..128)", H, W);
@@ -509,6 +513,7 @@ int cssm_irfft2_ex(const float* spec, long long P, int H, int W, int C, float* y
   e.y = y;
   e.y_fs = y_fs;
   e.add = add;
+  e.sums = sums;
   e.C = C;
   return hip_status(cssm::launch_irfft2_ex(reinterpret_cast<const float2*>(spec), P, H, W, e,
                                            static_cast<hipStream_t>(stream)),

@@ -516,6 +516,7 @@ irfft2_planes_ex(const float2* __restrict__ spec, long long P, const FftEx e) {
   const auto m = G::v4_lane(l);
   const auto col = PlaneFft<G>::v4_col(m.c4);
   const PlaneSet ys{e.y, e.y_fs};
+  float psum = 0.0f;   // this lane's part of its wave's plane sum (e.sums)
 #pragma unroll
   for (int i = 0; i < G::JLD; ++i) {
     const int row = G::v4_row(w, i, m);
@@ -537,6 +538,22 @@ irfft2_planes_ex(const float2* __restrict__ spec, long long P, const FftEx e) {
       v = make_float4(v.x * dsilu1(u.x), v.y * dsilu1(u.y), v.z * dsilu1(u.z), v.w * dsilu1(u.w));
     }
     *reinterpret_cast<float4*>(e.y + ys.off(p, e.C, H * W) + 4 * q) = v;
+    psum += (v.x + v.y) + (v.z + v.w);
+  }
+  if constexpr (G::V4_LINEAR) {
+    if (e.sums) {
+      // each wave's rows lie in one plane: wave sums in a fixed order, then the plane's waves in order
+      __shared__ float wsum[G::NW];
+      const float s = wave_sum(psum);
+      if (l == 0) wsum[w] = s;
+      __syncthreads();
+      constexpr int WPP = G::HP / G::RPW;   // waves per plane
+      if (int(tid) < NP && int(tid) < nvalid) {
+        float acc = 0.0f;
+        for (int k = 0; k < WPP; ++k) acc += wsum[int(tid) * WPP + k];
+        e.sums[p0 + tid] = acc;
+      }
+    }
   }
 }
 
@@ -558,6 +575,15 @@ hipError_t run_inv_ex(const float2* spec, long long P, const FftEx& e, hipStream
 }  // namespace
 
 bool fft_ex_supported(int H, int W) { return H == W && H >= 4 && H <= 128 && (H & (H - 1)) == 0; }
+
+bool irfft2_ex_sums_supported(long long P, int H, int W) {
+  if (!fft_ex_supported(H, W) || P <= 0) return false;
+#define CSSM_SUMS_CASE(LH, NP_, PPT_) \
+  if (np == NP_) return Geom<LH, LH, NP_, PPT_>::V4_LINEAR;
+  CSSM_FFT_TABLE(CSSM_SUMS_CASE, 32)
+#undef CSSM_SUMS_CASE
+  return false;
+}
 
 hipError_t launch_rfft2_ex(const FftEx& e, long long P, int H, int W, float2* spec, hipStream_t s) {
   if (!fft_ex_supported(H, W)) return hipErrorInvalidValue;

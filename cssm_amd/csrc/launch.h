@@ -113,8 +113,10 @@ struct FftEx {
   float* y;           // irfft2: output set (fs y_fs)
   int y_fs;
   const float* add;   // irfft2: per-plane addend, or null
+  float* sums;        // irfft2: per-plane sums of y (P), or null (plane groups whose waves each hold one plane)
   int C;
 };
+bool irfft2_ex_sums_supported(long long P, int H, int W);
 bool fft_ex_supported(int H, int W);
 hipError_t launch_rfft2_ex(const FftEx& e, long long P, int H, int W, float2* spec, hipStream_t s);
 hipError_t launch_irfft2_ex(const float2* spec, long long P, int H, int W, const FftEx& e, hipStream_t s);

@@ -576,10 +576,16 @@ def rfft2_ex(x: torch.Tensor, H: int, W: int, x_silu: bool = False, a: Optional[
     return spec
 
 
+def irfft2_ex_sums_supported(P: int, H: int, W: int) -> bool:
+    return bool(_lib.load().cssm_irfft2_ex_sums_supported(P, H, W))
+
+
 def irfft2_ex(spec: torch.Tensor, W: int, y: torch.Tensor, add: Optional[torch.Tensor] = None,
-              m: Optional[torch.Tensor] = None, d: Optional[torch.Tensor] = None) -> torch.Tensor:
+              m: Optional[torch.Tensor] = None, d: Optional[torch.Tensor] = None,
+              sums: Optional[torch.Tensor] = None) -> torch.Tensor:
     """y = (irfft2(spec) + add[p]) * m * SiLU'(d) into the float32 plane set y (F, C, H*W) (a
-    channel slice of a plane-major tensor allowed); add (F, C) or None, m / d plane sets or None
+    channel slice of a plane-major tensor allowed); add (F, C) or None, m / d plane sets or None;
+    sums (F, C) float32 receives each plane's sum of y where :func:`irfft2_ex_sums_supported`
     (cssm_irfft2_ex).  Returns y."""
     _dev(spec, "spec", torch.complex64)
     F, C, H, Wf = spec.shape
@@ -591,8 +597,13 @@ def irfft2_ex(spec: torch.Tensor, W: int, y: torch.Tensor, add: Optional[torch.T
         _dev(add, "add", torch.float32)
         if tuple(add.shape) != (F, C) or not add.is_contiguous():
             raise ValueError(f"add must be contiguous ({F}, {C})")
+    if sums is not None:
+        _dev(sums, "sums", torch.float32)
+        if tuple(sums.shape) != (F, C):
+            raise ValueError(f"sums must be ({F}, {C})")
     _lib.call("cssm_irfft2_ex", spec.data_ptr(), F * C, H, W, C, yp, yfs,
-              add.data_ptr() if add is not None else None, mp, mfs, dp, dfs, _stream())
+              add.data_ptr() if add is not None else None, mp, mfs, dp, dfs,
+              sums.data_ptr() if sums is not None else None, _stream())
     return y
 
 

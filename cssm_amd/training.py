@@ -274,12 +274,16 @@ class _GatedInScanFn(torch.autograd.Function):
                                     allow_unused=True)
         dcx = grads[0]
         dxz = torch.empty((F, 2 * Ci, HW), dtype=torch.float32, device=dy.device)
-        S.irfft2_ex(yspec, W, dxz[:, Ci:], m=dy, d=z)
-        S.irfft2_ex(sdu, W, dxz[:, :Ci], add=(dcx.reshape(F, Ci) * (1.0 / HW)).contiguous(), d=xm)
+        # the bias gradient from the plane sums the inverse transforms take while storing
+        sums = (torch.empty((2, F, Ci), dtype=torch.float32, device=dy.device)
+                if S.irfft2_ex_sums_supported(F * Ci, H, W) else None)
+        S.irfft2_ex(yspec, W, dxz[:, Ci:], m=dy, d=z, sums=sums[1] if sums is not None else None)
+        S.irfft2_ex(sdu, W, dxz[:, :Ci], add=(dcx.reshape(F, Ci) * (1.0 / HW)).contiguous(), d=xm,
+                    sums=sums[0] if sums is not None else None)
         del yspec, sdu
         dx = S.proj_out(dxz, w_in.t().contiguous(), w_in.new_zeros(K), out_dtype=torch.float32)
         dw = torch.bmm(dxz, x2.view(F, HW, K)).sum(dim=0).t()
-        db = dxz.sum(dim=(0, 2))
+        db = sums.sum(dim=1).reshape(-1) if sums is not None else dxz.sum(dim=(0, 2))
         gp_grads = [g if g is not None else torch.zeros_like(p) for g, p in zip(grads[1:-1], gate_params)]
         dk = grads[-1] if grads[-1] is not None else torch.zeros_like(kernel)
         return (dx, dw, db, dk, None, *gp_grads)

@@ -441,12 +441,16 @@ int cssm_fft_min_group(int H, int W);
  *                   (x_act, a_act: cssm_load_act)
  *   cssm_irfft2_ex  y = (irfft2(spec) + add[p]) * m * SiLU'(d), each of add
  *                   (P floats), m and d optional (NULL); SiLU'(v) = s (1 + v (1 - s)),
- *                   s = sigmoid(v)
+ *                   s = sigmoid(v); sums (P floats, optional) receives each plane's sum of
+ *                   y, in a fixed order (where cssm_irfft2_ex_sums_supported(P, H, W))
  */
 int cssm_rfft2_ex(const float* x, int x_fs, int x_act, const float* a, int a_fs, int a_act, int C, long long P,
                   int H, int W, float* spec, void* stream);
 int cssm_irfft2_ex(const float* spec, long long P, int H, int W, int C, float* y, int y_fs, const float* add,
-                   const float* m, int m_fs, const float* d, int d_fs, void* stream);
+                   const float* m, int m_fs, const float* d, int d_fs, float* sums, void* stream);
+
+/* 1 if cssm_irfft2_ex can return plane sums for P planes of H x W, else 0. */
+int cssm_irfft2_ex_sums_supported(long long P, int H, int W);
 
 /* 1 if cssm_rfft2_ex / cssm_irfft2_ex have a kernel for (H, W) planes, else 0. */
 int cssm_fft_ex_supported(int H, int W);

@@ -92,7 +92,7 @@ LAYER_CASES = [
 ]
 
 
-@pytest.mark.parametrize("H,F,C", [(128, 2, 3), (32, 3, 4), (8, 2, 8), (4, 3, 2)])
+@pytest.mark.parametrize("H,F,C", [(128, 2, 3), (64, 2, 4), (32, 3, 4), (8, 2, 8), (4, 3, 2)])
 def test_fused_training_transforms_match_torch(mods, H, F, C):
     """cssm_rfft2_ex / cssm_irfft2_ex on the halves of a plane-major (F, 2C, HW) tensor (frame
     stride 2C) against torch's FFTs of the same elementwise expressions."""
@@ -116,9 +116,14 @@ def test_fused_training_transforms_match_torch(mods, H, F, C):
         "cuda", torch.complex64)
     add = torch.from_numpy(rng.standard_normal((F, C))).to("cuda", torch.float32)
     out = torch.full((F, 2 * C, HW), 7.0, device="cuda")
-    S.irfft2_ex(spec, W, out[:, C:], m=dy, d=z)
-    S.irfft2_ex(spec, W, out[:, :C], add=add, d=xm)
+    sums_ok = S.irfft2_ex_sums_supported(F * C, H, W)
+    sums = torch.full((2, F, C), 7.0, device="cuda") if sums_ok else None
+    S.irfft2_ex(spec, W, out[:, C:], m=dy, d=z, sums=sums[1] if sums_ok else None)
+    S.irfft2_ex(spec, W, out[:, :C], add=add, d=xm, sums=sums[0] if sums_ok else None)
     torch.cuda.synchronize()
+    if sums_ok:
+        ps = out.view(F, 2, C, HW).sum(dim=3).transpose(0, 1).double().cpu()
+        assert rel_err(sums.cpu().numpy(), ps.numpy()) <= 1e-5
     base = torch.fft.irfft2(spec.cpu().to(torch.complex128), s=(H, W)).view(F, C, HW)
     dsilu = lambda v: sg(v) * (1 + v * (1 - sg(v)))
     ref_hi = base * d64(dy) * dsilu(d64(z))
