@@ -109,6 +109,7 @@ SIGNATURES = {
     "cssm_irfft2_ex": (_I, [_P, _LL, _I, _I, _I, _P, _I, _P, _P, _I, _P, _I, _P, _P]),
     "cssm_irfft2_ex_sums_supported": (_I, [_LL, _I, _I]),
     "cssm_fft_ex_supported": (_I, [_I, _I]),
+    "cssm_im2col_same": (_I, [_P, _I, _I, _I, _I, _I, _I, _P, _P]),
     "cssm_gated_scan_supported": (ctypes.c_int, [ctypes.c_int, ctypes.c_int]),
     "cssm_gated_scan_min_group": (ctypes.c_int, [ctypes.c_int, ctypes.c_int]),
     "cssm_gated_scan_col_order": (ctypes.c_int, [ctypes.c_int, ctypes.c_int, ctypes.POINTER(ctypes.c_int)]),

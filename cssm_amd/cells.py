@@ -207,7 +207,8 @@ class GatedCSSM:
 class GatedDeltaNetCSSM:
     """GatedDeltaNetCSSM (cssm.py:4264-5141), slow path: the `gdn` cell.
 
-    x -> [qkv_dw] -> qkv_proj -> causal short conv + SiLU -> input gates B_k, B_v
+    x -> [qkv_dw] -> qkv_proj (a k x k full-channel conv when qkv_conv_separable is
+    False) -> causal short conv + SiLU -> input gates B_k, B_v
     -> rfft2 -> spectral / key L2 norms -> delta-rule recurrence over T with the
     d_k x d_k complex state per (head, bin) -> readout S q -> irfft2 -> RMSNorm
     -> x SiLU(gate_proj(x)) -> output_proj.  Gates alpha / beta / B_k / B_v come
@@ -215,8 +216,8 @@ class GatedDeltaNetCSSM:
 
     Not part of this build (NotImplementedError): rope_mode other than 'none',
     int_attention_mode, cross_freq_conv_size > 0, ssl_proj_dim > 0, the
-    static-image fast path, bf16 / fp8 split-precision scans (use_complex32/16),
-    and a non-separable qkv conv.  scan_mode and use_log / use_goom select how
+    static-image fast path and bf16 / fp8 split-precision scans
+    (use_complex32/16).  scan_mode and use_log / use_goom select how
     the scan sees the entries of M and Delta, as in the reference
     (cssm.py:4693-4701, 4939-4991): to_goom's 1e-7 floor (the default), none
     (use_log=False, or scan_mode='pallas' at d_k = 2) or log(|x| + 1e-8)
@@ -247,8 +248,6 @@ class GatedDeltaNetCSSM:
             unsupported.append("static_image_fast_path")
         if (use_complex32 or use_complex16) and not use_log:
             unsupported.append("split-precision scans (use_complex32/16)")
-        if qkv_conv_size > 1 and not qkv_conv_separable:
-            unsupported.append("non-separable qkv conv")
         if gate_type not in ("dense", "factored", "channel", "scalar"):
             unsupported.append(f"gate_type={gate_type!r}")
         if output_norm not in ("rms", "layer", "none"):
@@ -302,9 +301,11 @@ class GatedDeltaNetCSSM:
         nh, Wf = C // dk, W // 2 + 1
         s: Dict[str, Any] = {"kernel": (nh, self.kernel_size, self.kernel_size)}
         q = self.qkv_conv_size
-        if q > 1:
+        if q > 1 and self.qkv_conv_separable:
             s["qkv_dw"] = {"kernel": (q, q, 1, C), "bias": (C,)}
-        s["qkv_proj"] = {"kernel": (C, 3 * C), "bias": (3 * C,)}
+        # the full-channel conv is one (q, q, C, 3C) Conv under the same name (cssm.py:4750-4753)
+        s["qkv_proj"] = ({"kernel": (q, q, C, 3 * C), "bias": (3 * C,)} if q > 1 and not self.qkv_conv_separable
+                         else {"kernel": (C, 3 * C), "bias": (3 * C,)})
         if self.short_conv_size > 0:
             for n in ("q", "k", "v"):
                 s[f"short_conv_{n}"] = {"kernel": (self.short_conv_size, 1, C), "bias": (C,)}
@@ -401,14 +402,15 @@ class GatedDeltaNetCSSM:
         what = self.spectral_kernel(p, H, W)
         # gates from the spatial mean of the layer input (+ temporal encoding); with the qkv conv,
         # the mean comes out of the conv's pass over x where the fused form applies
+        full_conv = self.qkv_conv_size > 1 and not self.qkv_conv_separable
         fused = (S.depthwise_conv_mean(x, p["qkv_dw"]["kernel"], p["qkv_dw"]["bias"], out_dtype=f32)
-                 if self.qkv_conv_size > 1 else None)
+                 if self.qkv_conv_size > 1 and not full_conv else None)
         if fused is not None:
             xq, ctx = fused
         else:
             ctx = S.frame_mean(x)
             xq = (S.depthwise_conv(x, p["qkv_dw"]["kernel"], p["qkv_dw"]["bias"], out_dtype=f32)
-                  if self.qkv_conv_size > 1 else x)
+                  if self.qkv_conv_size > 1 and not full_conv else x)
         temporal = "none" if self.position_independent_gates else "sinusoid"
         ab, bkv = S.gdn_gates(ctx, p, H, W, dk, self.gate_type, self.use_input_gates, temporal, self.rope_base)
         # q, k, v in plane-major blocks (B, T, 3C, H, W)
@@ -425,7 +427,13 @@ class GatedDeltaNetCSSM:
         # qkv_proj with the short conv, SiLU and input gates in its epilogue; without the qkv conv both
         # projections read x, and gate_proj rides in the same call
         gact = "silu" if self.output_gate_act == "silu" else "sigmoid"
-        if xq is x:
+        if full_conv:
+            # k x k conv with full channel mixing (im2col rows through the projection GEMM), then the
+            # short conv, SiLU and input gates in place on its planes
+            qkv = S.conv_full_planes(x.view(F, H, W, C), p["qkv_proj"]["kernel"], p["qkv_proj"]["bias"])
+            qkv = S.gdn_qkv_post(qkv.view(B, T, 3 * C, H, W), convs, gate_mode, gates)
+            gv = S.proj_planes(x, p["gate_proj"]["kernel"], p["gate_proj"]["bias"], F, HW, act=gact, out_dtype=f32)
+        elif xq is x:
             qkv, gv = S.gdn_qkv_gate_proj(x, p["qkv_proj"]["kernel"], p["qkv_proj"]["bias"], B, T, H, W, convs,
                                           gate_mode, gates, p["gate_proj"]["kernel"], p["gate_proj"]["bias"], gact,
                                           out_dtype=f32)

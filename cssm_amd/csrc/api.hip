@@ -473,6 +473,18 @@ int cssm_irfft2(const float* spec, long long P, int H, int W, void* y, int dtype
 
 int cssm_fft_ex_supported(int H, int W) { return cssm::fft_ex_supported(H, W) ? 1 : 0; }
 
+int cssm_im2col_same(const void* x, int dtype, int F, int H, int W, int C, int ks, float* out, void* stream) {
+  if (!x || !out) return fail(CSSM_ERR_NULL, "cssm_im2col_same: x and out must be non-null");
+  if (F <= 0 || H <= 0 || W <= 0 || C <= 0 || ks < 1 || ks > 15)
+    return fail(CSSM_ERR_SHAPE, "cssm_im2col_same: F=%d H=%d W=%d C=%d ks=%d", F, H, W, C, ks);
+  if (dtype != CSSM_F32 && dtype != CSSM_BF16) return fail(CSSM_ERR_ARG, "cssm_im2col_same: dtype %d", dtype);
+  if (C % 4 == 0 && (!aligned(x, dtype == CSSM_F32 ? 16 : 8) || !aligned(out, 16)))
+    return fail(CSSM_ERR_ALIGN, "cssm_im2col_same: x and out must be vector-aligned for C %% 4 == 0");
+  return hip_status(cssm::launch_im2col_same(x, dtype, (long long)F * H * W, H, W, C, ks, out,
+                                             static_cast<hipStream_t>(stream)),
+                    "cssm_im2col_same");
+}
+
 static bool plane_set_ok(const float* p, int fs, int C) { return p == nullptr || (fs >= C && aligned(p, 16)); }
 
 int cssm_rfft2_ex(const float* x, int x_fs, int x_act, const float* a, int a_fs, int a_act, int C, long long P,

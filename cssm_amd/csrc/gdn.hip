@@ -574,6 +574,57 @@ hipError_t run_inv_ex(const float2* spec, long long P, const FftEx& e, hipStream
 }
 }  // namespace
 
+// ---------------------------------------------------------------------------
+// im2col of a SAME k x k convolution over channels-last frames (the full-channel
+// qkv conv, cssm.py:4751-4753): row p = (f, h, w) of the output holds, for tap
+// (a, b) and channel c, x[f][h + a - lo][w + b - lo][c] at column (a k + b) C + c,
+// zero outside the frame (lo = (k - 1) / 2, as SAME pads).  The conv is then the
+// projection kernel's GEMM of these rows with the (k k C, N) kernel.
+// One thread per (row, tap, 4 channels) when C % 4 == 0, else per channel.
+// ---------------------------------------------------------------------------
+template <class TI, int VEC>
+__global__ void __launch_bounds__(256) im2col_same_cl(const TI* __restrict__ x, long long rows, int H, int W, int C,
+                                                      int ks, float* __restrict__ out) {
+  const int CG = C / VEC, taps = ks * ks, lo = (ks - 1) / 2;
+  const long long n = rows * taps * CG;
+  for (long long i = (long long)blockIdx.x * blockDim.x + threadIdx.x; i < n; i += (long long)gridDim.x * blockDim.x) {
+    const int cg = int(i % CG);
+    const long long rt = i / CG;
+    const int tap = int(rt % taps);
+    const long long r = rt / taps;
+    const int w = int(r % W), h = int((r / W) % H);
+    const long long f = r / ((long long)H * W);
+    const int hh = h + tap / ks - lo, ww = w + tap % ks - lo;
+    float v[VEC];
+    if (hh >= 0 && hh < H && ww >= 0 && ww < W) {
+      const size_t src = ((size_t(f) * H + hh) * W + ww) * C + size_t(cg) * VEC;
+#pragma unroll
+      for (int e = 0; e < VEC; ++e) v[e] = ld_f(x, src + e);
+    } else {
+#pragma unroll
+      for (int e = 0; e < VEC; ++e) v[e] = 0.0f;
+    }
+    const size_t dst = size_t(r) * size_t(taps) * C + size_t(tap) * C + size_t(cg) * VEC;
+    if constexpr (VEC == 4) st4v(out, dst, make_float4(v[0], v[1], v[2], v[3]));
+    else out[dst] = v[0];
+  }
+}
+
+hipError_t launch_im2col_same(const void* x, int dtype, long long rows, int H, int W, int C, int ks, float* out,
+                              hipStream_t s) {
+  const bool v4 = C % 4 == 0;
+  const long long n = rows * ks * ks * (v4 ? C / 4 : C);
+  const unsigned blocks = unsigned(n / 256 + 1 < 65536 * 4 ? n / 256 + 1 : 65536 * 4);
+  if (dtype == 0) {
+    if (v4) hipLaunchKernelGGL((im2col_same_cl<float, 4>), dim3(blocks), dim3(256), 0, s, static_cast<const float*>(x), rows, H, W, C, ks, out);
+    else hipLaunchKernelGGL((im2col_same_cl<float, 1>), dim3(blocks), dim3(256), 0, s, static_cast<const float*>(x), rows, H, W, C, ks, out);
+  } else {
+    if (v4) hipLaunchKernelGGL((im2col_same_cl<uint16_t, 4>), dim3(blocks), dim3(256), 0, s, static_cast<const uint16_t*>(x), rows, H, W, C, ks, out);
+    else hipLaunchKernelGGL((im2col_same_cl<uint16_t, 1>), dim3(blocks), dim3(256), 0, s, static_cast<const uint16_t*>(x), rows, H, W, C, ks, out);
+  }
+  return hipGetLastError();
+}
+
 bool fft_ex_supported(int H, int W) { return H == W && H >= 4 && H <= 128 && (H & (H - 1)) == 0; }
 
 bool irfft2_ex_sums_supported(long long P, int H, int W) {

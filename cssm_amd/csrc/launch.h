@@ -117,6 +117,9 @@ struct FftEx {
   int C;
 };
 bool irfft2_ex_sums_supported(long long P, int H, int W);
+// im2col of a SAME ks x ks conv over channels-last frames: rows (F H W) x (ks ks C) float32 (gdn.hip)
+hipError_t launch_im2col_same(const void* x, int dtype, long long rows, int H, int W, int C, int ks, float* out,
+                              hipStream_t s);
 bool fft_ex_supported(int H, int W);
 hipError_t launch_rfft2_ex(const FftEx& e, long long P, int H, int W, float2* spec, hipStream_t s);
 hipError_t launch_irfft2_ex(const float2* spec, long long P, int H, int W, const FftEx& e, hipStream_t s);

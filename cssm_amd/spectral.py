@@ -545,6 +545,31 @@ def fft_supported(H: int, W: int) -> bool:
     return bool(_lib.load().cssm_fft_min_group(H, W))
 
 
+def conv_full_planes(x: torch.Tensor, kernel: torch.Tensor, bias: torch.Tensor,
+                     max_bytes: int = 1 << 29) -> torch.Tensor:
+    """SAME ks x ks conv with full channel mixing of channels-last x (F, H, W, C) into plane-major
+    (F, N, H*W) float32 (nn.Conv(N, (ks, ks), padding='SAME'), cssm.py:4751-4753): im2col rows of a
+    chunk of frames (cssm_im2col_same, at most ``max_bytes`` of them) times the kernel viewed as
+    (ks ks C, N) on the projection kernel (cssm_proj_planes)."""
+    _dev(x, "x")
+    F, H, W, C = x.shape
+    ks = kernel.shape[0]
+    if tuple(kernel.shape[:3]) != (ks, ks, C):
+        raise ValueError(f"kernel {tuple(kernel.shape)} does not match ({ks}, {ks}, {C}, N)")
+    N = kernel.shape[3]
+    wk = kernel.reshape(ks * ks * C, N).contiguous()
+    out = torch.empty((F, N, H * W), dtype=torch.float32, device=x.device)
+    K = ks * ks * C
+    fc = max(1, min(F, max_bytes // (H * W * K * 4)))
+    cols = torch.empty((fc * H * W, K), dtype=torch.float32, device=x.device)
+    for f0 in range(0, F, fc):
+        n = min(fc, F - f0)
+        xs = x[f0:f0 + n]
+        _lib.call("cssm_im2col_same", xs.data_ptr(), _DTYPES[x.dtype], n, H, W, C, ks, cols.data_ptr(), _stream())
+        out[f0:f0 + n] = proj_planes(cols[:n * H * W], wk, bias, n, H * W, out_dtype=torch.float32)
+    return out
+
+
 def fft_ex_supported(H: int, W: int) -> bool:
     return bool(_lib.load().cssm_fft_ex_supported(H, W))
 

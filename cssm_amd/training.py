@@ -479,10 +479,19 @@ def gdn_train_apply(cell, params: Dict[str, Any], x: torch.Tensor) -> torch.Tens
     if not cell.position_independent_gates:
         ctx = ctx + _temporal_encoding(T, C, cell.rope_base, x.device)[None]
     xq = x.reshape(F, H, W, C)
-    if cell.qkv_conv_size > 1:
-        xq = _dwconv_cl(xq, p["qkv_dw"])
-    qkv = _ProjPlanesFn.apply(xq.reshape(-1, C).contiguous(), p["qkv_proj"]["kernel"], p["qkv_proj"]["bias"], F,
-                              HW).view(B, T, 3 * C, H, W)                 # plane-major
+    ks = cell.qkv_conv_size
+    if ks > 1 and not cell.qkv_conv_separable:
+        # full-channel SAME conv (cssm.py:4750-4753), lo = (ks - 1) // 2 rows / columns of zeros before
+        # and ks // 2 after, as lax pads; torch's conv2d correlates like lax does
+        lo, hi = (ks - 1) // 2, ks // 2
+        xp = Fn.pad(xq.permute(0, 3, 1, 2), (lo, hi, lo, hi))
+        qkv = Fn.conv2d(xp, p["qkv_proj"]["kernel"].permute(3, 2, 0, 1), p["qkv_proj"]["bias"])
+        qkv = qkv.reshape(B, T, 3 * C, H, W)                                # plane-major
+    else:
+        if ks > 1:
+            xq = _dwconv_cl(xq, p["qkv_dw"])
+        qkv = _ProjPlanesFn.apply(xq.reshape(-1, C).contiguous(), p["qkv_proj"]["kernel"], p["qkv_proj"]["bias"],
+                                  F, HW).view(B, T, 3 * C, H, W)          # plane-major
     q, k, v = qkv[:, :, :C], qkv[:, :, C:2 * C], qkv[:, :, 2 * C:]
     if cell.short_conv_size > 0:
         q = Fn.silu(_causal_t(q, p["short_conv_q"]))

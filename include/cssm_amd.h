@@ -452,6 +452,18 @@ int cssm_irfft2_ex(const float* spec, long long P, int H, int W, int C, float* y
 /* 1 if cssm_irfft2_ex can return plane sums for P planes of H x W, else 0. */
 int cssm_irfft2_ex_sums_supported(long long P, int H, int W);
 
+/*
+ * im2col of a SAME ks x ks convolution over channels-last frames, for the
+ * full-channel qkv conv of GatedDeltaNetCSSM (qkv_conv_separable=False,
+ * cssm.py:4751-4753: nn.Conv(3C, (ks, ks), padding='SAME')), which is then
+ * cssm_proj_planes of these rows with the conv kernel viewed as (ks*ks*C, 3C).
+ *   x    (F, H, W, C) of dtype (cssm_dtype)
+ *   out  (F*H*W, ks*ks*C) float32: row (f, h, w), column (a*ks + b)*C + c holds
+ *        x[f][h + a - lo][w + b - lo][c], lo = (ks - 1) / 2, zero outside the frame
+ * ks in 1..15; with C % 4 == 0 x and out vector-aligned (16 bytes, 8 for bf16 x).
+ */
+int cssm_im2col_same(const void* x, int dtype, int F, int H, int W, int C, int ks, float* out, void* stream);
+
 /* 1 if cssm_rfft2_ex / cssm_irfft2_ex have a kernel for (H, W) planes, else 0. */
 int cssm_fft_ex_supported(int H, int W);
 

@@ -146,6 +146,16 @@ def _dwconv_same(x, p):
     return (Fn.conv2d(xp, w, groups=C) + p["bias"][None, :, None, None]).permute(0, 2, 3, 1)
 
 
+def _conv_same(x, p):
+    """k x k SAME conv with full channel mixing and bias on (N, H, W, C) (flax Conv, HWIO kernel
+    (k, k, C, N); the full qkv conv of cssm.py:4750-4753)."""
+    k = p["kernel"].shape[0]
+    w = p["kernel"].permute(3, 2, 0, 1).contiguous()          # (N, C, k, k)
+    lo, hi = (k - 1) // 2, k // 2
+    xp = Fn.pad(x.permute(0, 3, 1, 2), (lo, hi, lo, hi))
+    return (Fn.conv2d(xp, w) + p["bias"][None, :, None, None]).permute(0, 2, 3, 1)
+
+
 def _causal_t(x5, p):
     """cssm.py:494-500 on plane-major (B, T, C, H, W): left pad k-1 frames, VALID
     depthwise conv over T, bias per channel."""
@@ -336,8 +346,11 @@ class GdnRef:
         nh, Wf = C // dk, W // 2 + 1
         what = spectral_kernel(p["kernel"], H, W, cfg.spectral_rho, squash=not cfg.no_spectral_clamp)
         xf = x.reshape(B * T, H, W, C)
-        xq = _dwconv_same(xf, p["qkv_dw"]) if cfg.qkv_conv_size > 1 else xf
-        qkv = _dense(xq, p["qkv_proj"]).reshape(B, T, H, W, 3 * C)
+        if cfg.qkv_conv_size > 1 and not cfg.qkv_conv_separable:
+            qkv = _conv_same(xf, p["qkv_proj"]).reshape(B, T, H, W, 3 * C)
+        else:
+            xq = _dwconv_same(xf, p["qkv_dw"]) if cfg.qkv_conv_size > 1 else xf
+            qkv = _dense(xq, p["qkv_proj"]).reshape(B, T, H, W, 3 * C)
         q, k, v = qkv[..., :C], qkv[..., C:2 * C], qkv[..., 2 * C:]
         if cfg.short_conv_size > 0:
             def conv(z, name):                                               # channels-last -> plane-major and back

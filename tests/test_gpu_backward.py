@@ -293,6 +293,12 @@ GDN_LAYER_CASES = [
                                                         use_log=False)),
     ("channel_logeps_scan_8", (2, 2, 8, 8, 8), dict(gate_type="channel", output_norm="rms", delta_key_dim=2,
                                                     use_goom=False)),
+    # the k x k full-channel qkv conv (qkv_conv_separable=False), odd and even tap counts
+    ("factored_full_qkv_conv3_16", (1, 3, 16, 16, 8), dict(gate_type="factored", output_norm="rms",
+                                                          delta_key_dim=4, qkv_conv_size=3,
+                                                          qkv_conv_separable=False)),
+    ("channel_full_qkv_conv4_8", (2, 2, 8, 8, 8), dict(gate_type="channel", output_norm="rms", delta_key_dim=2,
+                                                       qkv_conv_size=4, qkv_conv_separable=False)),
 ]
 
 

@@ -333,6 +333,28 @@ def test_depthwise_conv_mean_matches_separate_calls(mods, shape, ks, dt):
     assert rel_err(to_np(ctx), xn.mean(axis=(2, 3))) < 1e-5
 
 
+FULL_CONV_CASES = [(3, (4, 16, 16, 8), 24), (4, (3, 14, 14, 6), 18), (5, (2, 8, 8, 16), 48), (1, (2, 8, 8, 4), 12)]
+
+
+@pytest.mark.parametrize("ks,shape,N", FULL_CONV_CASES,
+                         ids=[f"k{c[0]}_{c[1][1]}x{c[1][2]}_C{c[1][3]}_N{c[2]}" for c in FULL_CONV_CASES])
+def test_full_conv_planes_matches_oracle(mods, ks, shape, N):
+    """The full-channel SAME conv (im2col rows through the projection GEMM) against the oracle's
+    direct sum over taps, f32 and bf16 in, in one chunk of frames and in chunks of one frame."""
+    _, S = mods
+    print_case(test="full_conv_planes", ks=ks, shape=shape, N=N)
+    rng = np.random.default_rng(8)
+    F, H, W, C = shape
+    x = rng.standard_normal(shape)
+    p = {"kernel": rng.standard_normal((ks, ks, C, N)) / (ks * np.sqrt(C)), "bias": rng.standard_normal(N)}
+    for xd in (_dev(x), _dev(x, torch.bfloat16)):
+        ref = O.full_conv2d_same(to_np(xd).reshape(shape), p).reshape(F, H * W, N).transpose(0, 2, 1)
+        for mb in (1 << 29, H * W * ks * ks * C * 4):
+            y = S.conv_full_planes(xd, _dev(p["kernel"]), _dev(p["bias"]), max_bytes=mb)
+            assert tuple(y.shape) == (F, N, H * W)
+            assert rel_err(to_np(y), ref) < 5e-6, (xd.dtype, mb)
+
+
 def test_depthwise_conv_mean_unsupported_shape(mods):
     """Where the blocked conv would leave a partial block the fused form declines (None): the cell
     then runs the conv and frame_mean."""
@@ -516,6 +538,14 @@ LAYER_CASES = [
      dict(delta_key_dim=4, gate_type="factored", qkv_conv_size=3, kernel_size=5)),
     ("shvit_7_channel", (3, 2, 7, 7, 8), dict(delta_key_dim=2, gate_type="channel", kernel_size=3)),
     ("small_12_dense_T1", (2, 1, 12, 12, 8), dict(delta_key_dim=4, gate_type="dense", kernel_size=5)),
+    # the k x k full-channel qkv conv (qkv_conv_separable=False): the fused 32 x 32 core, an even tap
+    # count on 14 x 14 planes with d_k = 3, channel input gates
+    ("full_qkv_conv3_fused32", (1, 3, 32, 32, 16),
+     dict(delta_key_dim=4, gate_type="factored", qkv_conv_size=3, qkv_conv_separable=False)),
+    ("full_qkv_conv4_14_dk3", (2, 3, 14, 14, 12),
+     dict(delta_key_dim=3, gate_type="factored", qkv_conv_size=4, qkv_conv_separable=False, kernel_size=3)),
+    ("full_qkv_conv5_channel_16", (2, 2, 16, 16, 8),
+     dict(delta_key_dim=2, gate_type="channel", qkv_conv_size=5, qkv_conv_separable=False, kernel_size=5)),
 ]
 
 

@@ -187,8 +187,10 @@ GDN_CFGS = [
     # the other scan variants: the linear scan (use_log=False) and log(|x| + 1e-8) (use_goom=False)
     dict(gate_type="factored", output_norm="rms", delta_key_dim=2, use_log=False),
     dict(gate_type="dense", output_norm="rms", delta_key_dim=4, use_goom=False),
+    # the full-channel qkv conv (qkv_conv_separable=False), an even tap count (SAME pads 1 before, 2 after)
+    dict(gate_type="channel", output_norm="rms", delta_key_dim=2, qkv_conv_size=4, qkv_conv_separable=False),
 ]
-GDN_IDS = ["factored", "dense", "channel", "scalar", "factored_linear_scan", "dense_logeps_scan"]
+GDN_IDS = ["factored", "dense", "channel", "scalar", "factored_linear_scan", "dense_logeps_scan", "full_qkv_conv4"]
 
 
 def _gdn(kw, shape, seed):

@@ -373,6 +373,34 @@ def test_depthwise_conv_same_is_a_cross_correlation(rng):
             assert abs(y[0, 3 + 1 - i, 2 + 1 - j, 1] - (k[i, j, 0, 1] + bias[1])) < 1e-15
 
 
+@pytest.mark.parametrize("k", [3, 4])
+def test_full_conv_same_is_a_channel_mixing_cross_correlation(rng, k):
+    """An impulse in input channel c at (h0, w0) lands tap (i, j) at (h0 + lo - i, w0 + lo - j) of
+    every output channel o with weight kernel[i, j, c, o] (lax's SAME correlation, lo = (k - 1) // 2
+    before and k // 2 after, so an even k reaches one row further down than up); a kernel that is
+    diagonal in (c, o) is the depthwise conv."""
+    C, N = 3, 5
+    kern = rng.standard_normal((k, k, C, N))
+    bias = rng.standard_normal(N)
+    x = np.zeros((1, 7, 8, C))
+    x[0, 3, 4, 2] = 1.0
+    y = O.full_conv2d_same(x, {"kernel": kern, "bias": bias})
+    lo = (k - 1) // 2
+    hit = np.zeros((7, 8), bool)
+    for i in range(k):
+        for j in range(k):
+            assert np.allclose(y[0, 3 + lo - i, 4 + lo - j], kern[i, j, 2] + bias, atol=1e-14)
+            hit[3 + lo - i, 4 + lo - j] = True
+    assert np.allclose(y[0][~hit], bias, atol=1e-14)
+    dw = rng.standard_normal((k, k, 1, C))
+    xr = rng.standard_normal((2, 6, 5, C))
+    diag = np.zeros((k, k, C, C))
+    for c in range(C):
+        diag[:, :, c, c] = dw[:, :, 0, c]
+    assert np.allclose(O.full_conv2d_same(xr, {"kernel": diag}),
+                       O.depthwise_conv2d_same(xr, {"kernel": dw, "bias": np.zeros(C)}), atol=1e-12)
+
+
 def test_gelu_tanh_form():
     x = np.linspace(-6, 6, 101)
     erf_gelu = np.array([0.5 * v * (1 + math.erf(v / math.sqrt(2))) for v in x])
