@@ -806,10 +806,12 @@ __global__ void __launch_bounds__(256, 2) gdn_core_fused32(const GdnFusedArgs a)
   constexpr int NT = GF::NT, NB = H * WF, NINT = H * (WH - 1), BPT = NB / NT, NX = NB - BPT * NT, BT = BPT + 1;
   constexpr int NW = NT / 64, JL = GI::JLD, XW = NX / NW;
   static_assert(NX % NW == 0 && XW * DK <= 64, "the bins beyond BPT per thread split evenly over the waves' lanes");
+  static_assert(GI::V4_LINEAR && GI::RPW == GI::HP && NW == DK && GI::C4N == 8,
+                "the norms' sums assume wave w loads all of plane w of a group, 8 lanes to a row");
   __shared__ __attribute__((aligned(16))) float smem[GF::LDS_FLOATS];
   __shared__ float2 esp[NP * H * 2];
   __shared__ float2 sx[NX * DK * DK];
-  __shared__ float red[NW * 2 * DK];
+  __shared__ float red[2 * DK];
   const PlaneFft<GF> fwd(smem);
   const PlaneFft<GI> inv(smem, reinterpret_cast<float2*>(smem + GF::OFF_EDGE),
                          reinterpret_cast<float2*>(smem + GF::OFF_TW));
@@ -890,6 +892,32 @@ __global__ void __launch_bounds__(256, 2) gdn_core_fused32(const GdnFusedArgs a)
       for (int g = 0; g < 3; ++g)
 #pragma unroll
         for (int i = 0; i < JL; ++i) inv.v4_put(GI::v4_row(w, i, m) + g * DK * H, vcol, pf[g][i]);
+      // spectral L2 norms of the q and k planes by Parseval, from the planes as loaded: over the half
+      // spectrum sum |X|^2 = (H W sum x^2 + H sum_h (r_h^2 + a_h^2)) / 2, r_h and a_h the plain and
+      // alternating sums of row h (the columns v = 0 and v = W / 2 are the DFTs of those over h).
+      // Wave w holds all of plane w of each group; the 8 lanes of a row hold its 4-vectors.
+      if (a.use_l2) {
+#pragma unroll
+        for (int g = 0; g < 2; ++g) {
+          float e = 0.0f, rr = 0.0f;
+#pragma unroll
+          for (int i = 0; i < JL; ++i) {
+            const float4 v = pf[g][i];
+            e = fmaf(v.x, v.x, fmaf(v.y, v.y, fmaf(v.z, v.z, fmaf(v.w, v.w, e))));
+            float r = (v.x + v.y) + (v.z + v.w), al = (v.x - v.y) + (v.z - v.w);
+            r += dpp_f<0xb1>(r);    // quad_perm [1, 0, 3, 2]
+            al += dpp_f<0xb1>(al);
+            r += dpp_f<0x4e>(r);    // quad_perm [2, 3, 0, 1]
+            al += dpp_f<0x4e>(al);
+            r += dpp_f<0x141>(r);   // row_half_mirror: the 8 lanes of the row
+            al += dpp_f<0x141>(al);
+            rr = fmaf(r, r, fmaf(al, al, rr));
+          }
+          const float x = wave_sum(fmaf(float(HW), e, m.c4 == 0 ? float(H) * rr : 0.0f));
+          if (lane == 0) red[g * DK + w] = x;
+          __builtin_amdgcn_sched_barrier(0);
+        }
+      }
     }
     const size_t fr = size_t(b) * T + t;
     float2 gab[BT], wh[BT];
@@ -913,39 +941,10 @@ __global__ void __launch_bounds__(256, 2) gdn_core_fused32(const GdnFusedArgs a)
     fwd.template edges<true, false>(w, lane, keep);
     __syncthreads();
 
-    // spectral L2 norms of the q and k planes (the bins are 2 X here)
+    // 1 / sqrt(sum |X|^2 + 1e-6) from the sums the waves stored before the forward transform
     float nrm[2 * DK];
 #pragma unroll
-    for (int p = 0; p < 2 * DK; ++p) nrm[p] = 1.0f;
-    if (a.use_l2) {
-      float acc[2 * DK];
-#pragma unroll
-      for (int p = 0; p < 2 * DK; ++p) acc[p] = 0.0f;
-#pragma unroll
-      for (int j = 0; j < BT; ++j) {
-        if (!bok[j] || (j == BPT && xrow != 0)) continue;   // an extra bin once, on its row-0 lane
-#pragma unroll
-        for (int p = 0; p < 2 * DK; ++p) {
-          const float2 x = *bin_ptr(p, bu[j], bv[j]);
-          acc[p] = fmaf(x.x, x.x, fmaf(x.y, x.y, acc[p]));
-        }
-      }
-      // wave sums by DPP and lane reads (a shuffle tree through LDS made this phase ~18 % of a step)
-#pragma unroll
-      for (int p = 0; p < 2 * DK; ++p) {
-        const float x = wave_sum(acc[p]);
-        if (lane == 0) red[w * 2 * DK + p] = x;
-        __builtin_amdgcn_sched_barrier(0);
-      }
-      __syncthreads();
-#pragma unroll
-      for (int p = 0; p < 2 * DK; ++p) {
-        float sum = 0.0f;
-#pragma unroll
-        for (int ww = 0; ww < NW; ++ww) sum += red[ww * 2 * DK + p];
-        nrm[p] = 1.0f / sqrtf(0.25f * sum + 1e-6f);
-      }
-    }
+    for (int p = 0; p < 2 * DK; ++p) nrm[p] = a.use_l2 ? 1.0f / sqrtf(0.5f * red[p] + 1e-6f) : 1.0f;
 
     // the recurrence of each of this thread's bins; o / (H W) over its q slots
     auto bin_step = [&](int j, float2 (&st)[DK][DK]) {
