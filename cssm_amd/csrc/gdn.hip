@@ -126,8 +126,68 @@ struct SpecLoadOp {
   }
 };
 
-// rfft2 of NP planes per workgroup: x (P, H, W) real -> spec (P, H, WF), norms (P) = sum |X|^2 or skipped.
+// Which plane groups the transforms run persistently (a workgroup per resident slot looping over
+// groups, the next group's loads issued during the current one's passes): where a wave's rows lie in
+// one plane (V4_LINEAR).  Forward only for one plane per group (128 x 128): at 64 x 64 the
+// persistent forward measured slower than one group per workgroup.
+constexpr bool fwd_persistent(bool v4_linear, int np) { return v4_linear && np == 1; }
+constexpr bool inv_persistent(bool v4_linear) { return v4_linear; }
+
+// waves per SIMD the inverse kernels must keep: two 512-thread workgroups of 128 x 128 planes share
+// a CU (LDS), i.e. four waves per SIMD, which caps a wave at 128 VGPRs with the prefetched bins
+template <int LH, int PPT>
+constexpr int kInvWavesPerSimd = (LH == 7 && PPT == 32) ? 4 : 1;
+
+// inverse policy with the group's interior bins already in registers: SpecBins::fetch loads, for
+// the lane's C2 units (the job map the pass uses), every bin SpecLoadOp::bins would read, so a
+// persistent inverse issues the next group's loads while the current group's later passes run.
+// The DC / Nyquist columns (one wave's edge jobs) are read from HBM in the edge pass.
+template <class G>
+struct SpecBins {
+  static constexpr int H = G::H, WF = G::WF, H1 = G::H1, H2 = G::H2;
+  float2 c[G::JC2][2][H2];   // C2 unit (j, a2): its H2 bins
+  // group spectrum `in` of nv valid planes (the rest read as 0); lane l of wave w
+  __device__ __forceinline__ void fetch(const float2* in, int nv, int w, int l) {
+    const Buf src(in, unsigned(nv) * unsigned(H * WF * 8));
+#pragma unroll
+    for (int j = 0; j < G::JC2; ++j) {
+      int pl, v, pair, n;
+      G::col_job(w, j, l, pl, v, pair, n);
+      int kA, kB;
+      pair_units<H1>(pair, kA, kB);
+#pragma unroll
+      for (int a2 = 0; a2 < 2; ++a2) {
+        const int k = a2 ? kB : kA;
+        const unsigned vo = unsigned(((pl * H + k) * WF + n) * 8);
+#pragma unroll
+        for (int q = 0; q < H2; ++q) c[j][a2][q] = src.ld2(vo, q * H1 * WF * 8);
+      }
+    }
+  }
+};
+
+template <class G>
+struct SpecRegOp {
+  static constexpr bool kPackedColumnToo = false;
+  static constexpr int H2 = G::H2;
+  const SpecBins<G>& b;
+  SpecLoadOp<G> edges_from;   // the group's spectrum, for the edge pass
+  __device__ __forceinline__ void bins(int j, int a2, int, int, int, float2 (&sp)[G::H2]) const {
+    const float scale = edges_from.scale;
+#pragma unroll
+    for (int q = 0; q < H2; ++q) sp[q] = make_float2(b.c[j][a2][q].x * scale, b.c[j][a2][q].y * scale);
+  }
+  __device__ __forceinline__ void edge(int j, int pl, int uA, int uB, int e, float2 (&v4)[4]) const {
+    edges_from.edge(j, pl, uA, uB, e, v4);
+  }
+};
+
+// rfft2 of NP planes per group: x (P, H, W) real -> spec (P, H, WF), norms (P) = sum |X|^2 or skipped.
 // The last group may hold fewer than NP planes: the missing ones are neither read nor written.
+// Persistent: workgroup b transforms groups b, b + gridDim.x, ...  Where a wave's rows lie in one
+// plane (V4_LINEAR) it loads the next group's planes into registers while the current group's passes
+// run, so a CU's HBM reads do not stop for the transforms; each wave's loads are buffer loads off
+// its plane's base with one per-lane offset and uniform row steps.
 template <int LH, int LW, int NP, int PPT, class IO>
 __global__ void __launch_bounds__((NP << (LH + LW)) / PPT)
 rfft2_planes(const void* __restrict__ x, long long P, float2* __restrict__ spec, float* __restrict__ norms) {
@@ -142,88 +202,145 @@ rfft2_planes(const void* __restrict__ x, long long P, float2* __restrict__ spec,
   const PlaneFft<G> fft(smem);
   const unsigned tid = threadIdx.x;
   const int w = __builtin_amdgcn_readfirstlane(int(tid) / 64), l = int(tid) % 64;
-  const size_t p0 = size_t(blockIdx.x) * NP;
-  const int nvalid = int(P - (long long)p0 < NP ? P - (long long)p0 : NP);
-  const unsigned nv4 = unsigned(nvalid) * (H * W / 4);
+  const long long NG = (P + NP - 1) / NP;
   fft.init_twiddles(tid);
   // C2 jobs on the packed DC / Nyquist column (v = 0) never reach the policy: their slots stay 0
   for (int i = tid; i < G::NC2; i += NT) part_c2[i] = 0.0f;
   __syncthreads();
-  {
-    const V4* src = reinterpret_cast<const V4*>(static_cast<const TE*>(x) + p0 * H * W);
-    const auto m = G::v4_lane(l);
-    const auto col = PlaneFft<G>::v4_col(m.c4);
-    V4 ld[G::JLD];
+  const auto m = G::v4_lane(l);
+  const auto col = PlaneFft<G>::v4_col(m.c4);
+  constexpr bool PF = fwd_persistent(G::V4_LINEAR, NP);
+  V4 ld[G::JLD];
+  auto load = [&](long long g) {
+    const size_t q0 = size_t(g) * NP;
+    const int nv = int(P - (long long)q0 < NP ? P - (long long)q0 : NP);
+    if constexpr (PF) {
+      constexpr int VB = int(sizeof(V4));
+      const int pw = (w * G::RPW) / G::HP;   // this wave's plane in the group
+      const Buf src(static_cast<const TE*>(x) + (q0 + pw) * H * W, pw < nv ? unsigned(H * W * sizeof(TE)) : 0u);
+      const unsigned vo = unsigned(((G::v4_row(w, 0, m) - pw * H) * G::C4N + m.c4) * VB);
 #pragma unroll
-    for (int i = 0; i < G::JLD; ++i) {
-      const unsigned f = G::v4_index(G::v4_row(w, i, m), m);
-      ld[i] = f < nv4 ? src[f] : V4{};
+      for (int i = 0; i < G::JLD; ++i) src.ld(ld[i], vo, i * G::RK * G::C4N * VB);
+    } else {
+      const unsigned nv4 = unsigned(nv) * (H * W / 4);
+      const V4* src = reinterpret_cast<const V4*>(static_cast<const TE*>(x) + q0 * H * W);
+#pragma unroll
+      for (int i = 0; i < G::JLD; ++i) {
+        const unsigned f = G::v4_index(G::v4_row(w, i, m), m);
+        ld[i] = f < nv4 ? src[f] : V4{};
+      }
     }
+  };
+  auto group = [&](long long g) {
+    const size_t p0 = size_t(g) * NP;
+    const int nvalid = int(P - (long long)p0 < NP ? P - (long long)p0 : NP);
+    if (!PF) load(g);
 #pragma unroll
     for (int i = 0; i < G::JLD; ++i) fft.v4_put(G::v4_row(w, i, m), col, IO::to_f4(ld[i]));
-  }
-  wave_sync();
-  SpecStoreOp<G> op{spec + p0 * H * WF, norms ? part_c2 : nullptr, norms ? part_e : nullptr, nvalid};
-  fft.r1(w, l);
-  fft.r2(w, l);
-  fft.c1(w, l);
-  fft.template c2<true, false>(w, l, op);
-  fft.template edges<true, false>(w, l, op);
-  __syncthreads();
-  if (norms) {
-    // plane pl: GR threads each sum a fixed stride of its UC2 + UE slots, then one sums those in order
-    for (int pl0 = 0; pl0 < NP; pl0 += NT / GR) {
-      const int pl = pl0 + int(tid) / GR, r = int(tid) % GR;
-      float acc = 0.0f;
-      if (pl < NP) {
-        for (int i = r; i < UC2; i += GR) acc += part_c2[pl * UC2 + i];
-        for (int i = r; i < UE; i += GR) acc += part_e[pl * UE + i];
+    wave_sync();
+    if (PF && g + gridDim.x < NG) load(g + gridDim.x);
+    // the lane index re-derived per group, so the passes rebuild their (cheap) LDS addresses instead
+    // of the compiler holding every pass's addresses in registers across the loop
+    int ll = l;
+    asm volatile("" : "+v"(ll));
+    __builtin_assume(ll >= 0 && ll < 64);
+    SpecStoreOp<G> op{spec + p0 * H * WF, norms ? part_c2 : nullptr, norms ? part_e : nullptr, nvalid};
+    fft.r1(w, ll);
+    fft.r2(w, ll);
+    fft.c1(w, ll);
+    fft.template c2<true, false>(w, ll, op);
+    fft.template edges<true, false>(w, ll, op);
+    __syncthreads();   // the passes are done with the plane buffer (and the norms' slots are written)
+    if (norms) {
+      // plane pl: GR threads each sum a fixed stride of its UC2 + UE slots, then one sums those in order
+      for (int pl0 = 0; pl0 < NP; pl0 += NT / GR) {
+        const int pl = pl0 + int(tid) / GR, r = int(tid) % GR;
+        float acc = 0.0f;
+        if (pl < NP) {
+          for (int i = r; i < UC2; i += GR) acc += part_c2[pl * UC2 + i];
+          for (int i = r; i < UE; i += GR) acc += part_e[pl * UE + i];
+        }
+        red[tid] = acc;
+        __syncthreads();
+        if (r == 0 && pl < nvalid) {
+          float sum = 0.0f;
+          for (int i = 0; i < GR; ++i) sum += red[tid + i];
+          norms[p0 + pl] = sum;
+        }
+        __syncthreads();
       }
-      red[tid] = acc;
-      __syncthreads();
-      if (r == 0 && pl < nvalid) {
-        float sum = 0.0f;
-        for (int i = 0; i < GR; ++i) sum += red[tid + i];
-        norms[p0 + pl] = sum;
-      }
-      __syncthreads();
     }
+  };
+  if constexpr (PF) {
+    long long g = blockIdx.x;
+    if (g < NG) load(g);
+    for (; g < NG; g += gridDim.x) group(g);
+  } else {
+    group(blockIdx.x);
   }
 }
 
-// irfft2 of NP planes per workgroup: spec (P, H, WF) -> y (P, H, W) real (numpy C2R rule);
-// a partial last group neither reads nor writes the missing planes
+// irfft2 of NP planes per group: spec (P, H, WF) -> y (P, H, W) real (numpy C2R rule);
+// a partial last group neither reads nor writes the missing planes.
+// Persistent like rfft2_planes: with V4_LINEAR the next group's bins are loaded into registers
+// (SpecBins) as soon as the current group's C2 / edge passes have taken theirs, and land while
+// the remaining passes and the stores run.
 template <int LH, int LW, int NP, int PPT, class IO>
-__global__ void __launch_bounds__((NP << (LH + LW)) / PPT)
+__global__ void __launch_bounds__((NP << (LH + LW)) / PPT, (kInvWavesPerSimd<LH, PPT>))
 irfft2_planes(const float2* __restrict__ spec, long long P, void* __restrict__ y) {
   using G = Geom<LH, LW, NP, PPT>;
-  constexpr int H = G::H, W = G::W, WF = G::WF, NT = G::NT;
+  constexpr int H = G::H, W = G::W, WF = G::WF;
+  constexpr bool PF = inv_persistent(G::V4_LINEAR);
   using V4 = typename IO::V4;
   using TE = typename IO::T;
   __shared__ __attribute__((aligned(16))) float smem[G::LDS_FLOATS];
   const PlaneFft<G> fft(smem);
   const unsigned tid = threadIdx.x;
   const int w = __builtin_amdgcn_readfirstlane(int(tid) / 64), l = int(tid) % 64;
-  const size_t p0 = size_t(blockIdx.x) * NP;
-  const int nvalid = int(P - (long long)p0 < NP ? P - (long long)p0 : NP);
-  const unsigned nv4 = unsigned(nvalid) * (H * W / 4);
+  const long long NG = (P + NP - 1) / NP;
+  const float scale = 1.0f / float(H * W);
   fft.init_twiddles(tid);
   __syncthreads();
-  SpecLoadOp<G> op{spec + p0 * H * WF, 1.0f / float(H * W), nvalid};
-  fft.template c2<false, true>(w, l, op);
-  fft.template edges<false, true>(w, l, op);
-  fft.i1_packed(w, l);
-  fft.i2(w, l);
-  fft.i3(w, l);
-  fft.i4(w, l);
-  V4* dst = reinterpret_cast<V4*>(static_cast<TE*>(y) + p0 * H * W);
   const auto m = G::v4_lane(l);
   const auto col = PlaneFft<G>::v4_col(m.c4);
+  SpecBins<G> bins;
+  auto nvalid_of = [&](long long g) { return int(P - g * NP < NP ? P - g * NP : NP); };
+  auto group = [&](long long g) {
+    const size_t p0 = size_t(g) * NP;
+    const int nvalid = nvalid_of(g);
+    const unsigned nv4 = unsigned(nvalid) * (H * W / 4);
+    int ll = l;   // re-derived per group, as in rfft2_planes
+    asm volatile("" : "+v"(ll));
+    __builtin_assume(ll >= 0 && ll < 64);
+    if constexpr (PF) {
+      const SpecRegOp<G> op{bins, SpecLoadOp<G>{spec + p0 * H * WF, scale, nvalid}};
+      fft.template c2<false, true>(w, ll, op);
+      if (g + gridDim.x < NG) bins.fetch(spec + (g + gridDim.x) * NP * H * WF, nvalid_of(g + gridDim.x), w, l);
+      fft.template edges<false, true>(w, ll, op);
+    } else {
+      SpecLoadOp<G> op{spec + p0 * H * WF, scale, nvalid};
+      fft.template c2<false, true>(w, ll, op);
+      fft.template edges<false, true>(w, ll, op);
+    }
+    fft.i1_packed(w, ll);
+    fft.i2(w, ll);
+    fft.i3(w, ll);
+    fft.i4(w, ll);
+    V4* dst = reinterpret_cast<V4*>(static_cast<TE*>(y) + p0 * H * W);
 #pragma unroll
-  for (int i = 0; i < G::JLD; ++i) {
-    const int row = G::v4_row(w, i, m);
-    const unsigned f = G::v4_index(row, m);
-    if (f < nv4) dst[f] = IO::from_f4(fft.v4_get(row, col));
+    for (int i = 0; i < G::JLD; ++i) {
+      const int row = G::v4_row(w, i, m);
+      const unsigned f = G::v4_index(row, m);
+      if (f < nv4) dst[f] = IO::from_f4(fft.v4_get(row, col));
+    }
+    __syncthreads();   // the stores have read the plane buffer before the next group's C2 writes it
+  };
+  if constexpr (PF) {
+    long long g = blockIdx.x;
+    if (g < NG) bins.fetch(spec + g * NP * H * WF, nvalid_of(g), w, l);
+    for (; g < NG; g += gridDim.x) group(g);
+  } else {
+    group(blockIdx.x);
   }
 }
 
@@ -239,19 +356,36 @@ int pick_group(long long P, std::initializer_list<int> nps) {
   return best;
 }
 
+// workgroups of a persistent launch over `groups` units: what fits on the device at once
+unsigned resident_grid(const void* kernel, int nt, long long groups) {
+  int dev = 0, cus = 256, per_cu = 0;
+  if (hipGetDevice(&dev) != hipSuccess || hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) !=
+                                              hipSuccess)
+    cus = 256;
+  if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, kernel, nt, 0) != hipSuccess || per_cu < 1) per_cu = 1;
+  const long long cap = (long long)cus * per_cu;
+  return unsigned(groups < cap ? groups : cap);
+}
+
 template <int LH, int NP, int PPT, class IO>
 hipError_t run_fwd(const void* x, long long P, float2* spec, float* norms, hipStream_t s) {
   using G = Geom<LH, LH, NP, PPT>;
-  hipLaunchKernelGGL((rfft2_planes<LH, LH, NP, PPT, IO>), dim3(unsigned((P + NP - 1) / NP)), dim3(G::NT), 0, s, x, P,
-                     spec, norms);
+  const auto k = rfft2_planes<LH, LH, NP, PPT, IO>;
+  // persistent kernels: as many workgroups as fit at once; the others one per group
+  static const unsigned grid = fwd_persistent(G::V4_LINEAR, NP) ? resident_grid(reinterpret_cast<const void*>(k), G::NT, 1LL << 40) : ~0u;
+  const long long groups = (P + NP - 1) / NP;
+  hipLaunchKernelGGL(k, dim3(unsigned(groups < grid ? groups : grid)), dim3(G::NT), 0, s, x, P, spec, norms);
   return hipGetLastError();
 }
 
 template <int LH, int NP, int PPT, class IO>
 hipError_t run_inv(const float2* spec, long long P, void* y, hipStream_t s) {
   using G = Geom<LH, LH, NP, PPT>;
-  hipLaunchKernelGGL((irfft2_planes<LH, LH, NP, PPT, IO>), dim3(unsigned((P + NP - 1) / NP)), dim3(G::NT), 0, s, spec,
-                     P, y);
+  const auto k = irfft2_planes<LH, LH, NP, PPT, IO>;
+  // persistent kernels: as many workgroups as fit at once; the others one per group
+  static const unsigned grid = inv_persistent(G::V4_LINEAR) ? resident_grid(reinterpret_cast<const void*>(k), G::NT, 1LL << 40) : ~0u;
+  const long long groups = (P + NP - 1) / NP;
+  hipLaunchKernelGGL(k, dim3(unsigned(groups < grid ? groups : grid)), dim3(G::NT), 0, s, spec, P, y);
   return hipGetLastError();
 }
 
@@ -448,112 +582,208 @@ __device__ __forceinline__ float dsilu1(float v) {
   return s * fmaf(v, 1.0f - s, 1.0f);
 }
 
+// persistent like rfft2_planes (with V4_LINEAR the next group's x and a are in flight during the
+// current passes); the activations and product are applied as the samples go into LDS
 template <int LH, int LW, int NP, int PPT>
 __global__ void __launch_bounds__((NP << (LH + LW)) / PPT)
 rfft2_planes_ex(const FftEx e, long long P, float2* __restrict__ spec) {
   using G = Geom<LH, LW, NP, PPT>;
-  constexpr int H = G::H, W = G::W, WF = G::WF, NT = G::NT, V4P = H * W / 4;
+  constexpr int H = G::H, W = G::W, WF = G::WF, V4P = H * W / 4;
   __shared__ __attribute__((aligned(16))) float smem[G::LDS_FLOATS];
   const PlaneFft<G> fft(smem);
   const unsigned tid = threadIdx.x;
   const int w = __builtin_amdgcn_readfirstlane(int(tid) / 64), l = int(tid) % 64;
-  const long long p0 = (long long)blockIdx.x * NP;
-  const int nvalid = int(P - p0 < NP ? P - p0 : NP);
+  const long long NG = (P + NP - 1) / NP;
   fft.init_twiddles(tid);
   __syncthreads();
-  {
-    const auto m = G::v4_lane(l);
-    const auto col = PlaneFft<G>::v4_col(m.c4);
-    float4 ld[G::JLD];
+  const auto m = G::v4_lane(l);
+  const auto col = PlaneFft<G>::v4_col(m.c4);
+  constexpr bool PF = fwd_persistent(G::V4_LINEAR, NP);
+  float4 lx[G::JLD], la[G::JLD];
+  const bool two = e.a.p != nullptr;
+  auto load = [&](long long g) {
+    const long long q0 = g * NP;
+    const int nv = int(P - q0 < NP ? P - q0 : NP);
+    if constexpr (PF) {
+      const int pw = (w * G::RPW) / G::HP;   // this wave's plane in the group
+      const unsigned bytes = pw < nv ? unsigned(H * W * sizeof(float)) : 0u;
+      const long long pp = pw < nv ? q0 + pw : q0;
+      const Buf sx(e.x.p + e.x.off(pp, e.C, H * W), bytes);
+      const unsigned vo = unsigned(((G::v4_row(w, 0, m) - pw * H) * G::C4N + m.c4) * 16);
 #pragma unroll
-    for (int i = 0; i < G::JLD; ++i) {
-      const unsigned f = G::v4_index(G::v4_row(w, i, m), m);
-      const int pl = int(f / V4P), q = int(f % V4P);
-      float4 v = make_float4(0.f, 0.f, 0.f, 0.f);
-      if (pl < nvalid) {
-        v = *reinterpret_cast<const float4*>(e.x.p + e.x.off(p0 + pl, e.C, H * W) + 4 * q);
-        if (e.x_act) v = make_float4(silu1(v.x), silu1(v.y), silu1(v.z), silu1(v.w));
-        if (e.a.p) {
-          float4 u = *reinterpret_cast<const float4*>(e.a.p + e.a.off(p0 + pl, e.C, H * W) + 4 * q);
-          if (e.a_act) u = make_float4(silu1(u.x), silu1(u.y), silu1(u.z), silu1(u.w));
-          v = make_float4(v.x * u.x, v.y * u.y, v.z * u.z, v.w * u.w);
+      for (int i = 0; i < G::JLD; ++i) sx.ld(lx[i], vo, i * G::RK * G::C4N * 16);
+      if (two) {
+        const Buf sa(e.a.p + e.a.off(pp, e.C, H * W), bytes);
+#pragma unroll
+        for (int i = 0; i < G::JLD; ++i) sa.ld(la[i], vo, i * G::RK * G::C4N * 16);
+      }
+    } else {
+#pragma unroll
+      for (int i = 0; i < G::JLD; ++i) {
+        const unsigned f = G::v4_index(G::v4_row(w, i, m), m);
+        const int pl = int(f / V4P), q = int(f % V4P);
+        lx[i] = la[i] = make_float4(0.f, 0.f, 0.f, 0.f);
+        if (pl < nv) {
+          lx[i] = *reinterpret_cast<const float4*>(e.x.p + e.x.off(q0 + pl, e.C, H * W) + 4 * q);
+          if (two) la[i] = *reinterpret_cast<const float4*>(e.a.p + e.a.off(q0 + pl, e.C, H * W) + 4 * q);
         }
       }
-      ld[i] = v;
     }
+  };
+  auto group = [&](long long g) {
+    const long long p0 = g * NP;
+    const int nvalid = int(P - p0 < NP ? P - p0 : NP);
+    if (!PF) load(g);
 #pragma unroll
-    for (int i = 0; i < G::JLD; ++i) fft.v4_put(G::v4_row(w, i, m), col, ld[i]);
+    for (int i = 0; i < G::JLD; ++i) {
+      float4 v = lx[i];
+      if (e.x_act) v = make_float4(silu1(v.x), silu1(v.y), silu1(v.z), silu1(v.w));
+      if (two) {
+        float4 u = la[i];
+        if (e.a_act) u = make_float4(silu1(u.x), silu1(u.y), silu1(u.z), silu1(u.w));
+        v = make_float4(v.x * u.x, v.y * u.y, v.z * u.z, v.w * u.w);
+      }
+      fft.v4_put(G::v4_row(w, i, m), col, v);
+    }
+    wave_sync();
+    if (PF && g + gridDim.x < NG) load(g + gridDim.x);
+    int ll = l;   // re-derived per group, as in rfft2_planes
+    asm volatile("" : "+v"(ll));
+    __builtin_assume(ll >= 0 && ll < 64);
+    SpecStoreOp<G> op{spec + p0 * H * WF, nullptr, nullptr, nvalid};
+    fft.r1(w, ll);
+    fft.r2(w, ll);
+    fft.c1(w, ll);
+    fft.template c2<true, false>(w, ll, op);
+    fft.template edges<true, false>(w, ll, op);
+    __syncthreads();   // the passes are done with the plane buffer
+  };
+  if constexpr (PF) {
+    long long g = blockIdx.x;
+    if (g < NG) load(g);
+    for (; g < NG; g += gridDim.x) group(g);
+  } else {
+    group(blockIdx.x);
   }
-  wave_sync();
-  SpecStoreOp<G> op{spec + p0 * H * WF, nullptr, nullptr, nvalid};
-  fft.r1(w, l);
-  fft.r2(w, l);
-  fft.c1(w, l);
-  fft.template c2<true, false>(w, l, op);
-  fft.template edges<true, false>(w, l, op);
 }
 
+// persistent like irfft2_planes
 template <int LH, int LW, int NP, int PPT>
-__global__ void __launch_bounds__((NP << (LH + LW)) / PPT)
+__global__ void __launch_bounds__((NP << (LH + LW)) / PPT, (kInvWavesPerSimd<LH, PPT>))
 irfft2_planes_ex(const float2* __restrict__ spec, long long P, const FftEx e) {
   using G = Geom<LH, LW, NP, PPT>;
-  constexpr int H = G::H, W = G::W, WF = G::WF, NT = G::NT, V4P = H * W / 4;
+  constexpr int H = G::H, W = G::W, WF = G::WF, V4P = H * W / 4;
+  constexpr bool PF = inv_persistent(G::V4_LINEAR);
   __shared__ __attribute__((aligned(16))) float smem[G::LDS_FLOATS];
+  __shared__ float wsum[G::NW];
   const PlaneFft<G> fft(smem);
   const unsigned tid = threadIdx.x;
   const int w = __builtin_amdgcn_readfirstlane(int(tid) / 64), l = int(tid) % 64;
-  const long long p0 = (long long)blockIdx.x * NP;
-  const int nvalid = int(P - p0 < NP ? P - p0 : NP);
+  const long long NG = (P + NP - 1) / NP;
+  const float scale = 1.0f / float(H * W);
   fft.init_twiddles(tid);
   __syncthreads();
-  SpecLoadOp<G> op{spec + p0 * H * WF, 1.0f / float(H * W), nvalid};
-  fft.template c2<false, true>(w, l, op);
-  fft.template edges<false, true>(w, l, op);
-  fft.i1_packed(w, l);
-  fft.i2(w, l);
-  fft.i3(w, l);
-  fft.i4(w, l);
   const auto m = G::v4_lane(l);
   const auto col = PlaneFft<G>::v4_col(m.c4);
   const PlaneSet ys{e.y, e.y_fs};
-  float psum = 0.0f;   // this lane's part of its wave's plane sum (e.sums)
+  auto nvalid_of = [&](long long g) { return int(P - g * NP < NP ? P - g * NP : NP); };
+  auto group = [&](long long g) {
+    const long long p0 = g * NP;
+    const int nvalid = nvalid_of(g);
+    int ll = l;   // re-derived per group, as in rfft2_planes
+    asm volatile("" : "+v"(ll));
+    __builtin_assume(ll >= 0 && ll < 64);
+    {
+      SpecLoadOp<G> op{spec + p0 * H * WF, scale, nvalid};
+      fft.template c2<false, true>(w, ll, op);
+      fft.template edges<false, true>(w, ll, op);
+    }
+    fft.i1_packed(w, ll);
+    fft.i2(w, ll);
+    fft.i3(w, ll);
+    fft.i4(w, ll);
+    float psum = 0.0f;   // this lane's part of its wave's plane sum (e.sums)
+    if constexpr (PF) {
+      // the wave's rows lie in plane pw: buffer loads / stores off that plane's bases, one lane
+      // offset and uniform row steps; the m and d loads issued four vectors at a time
+      const int pw = (w * G::RPW) / G::HP;
+      if (pw < nvalid) {
+        const long long p = p0 + pw;
+        constexpr unsigned PB = unsigned(H * W * sizeof(float));
+        constexpr int STEP = G::RK * G::C4N * 16;
+        const int row0 = G::v4_row(w, 0, m);
+        const unsigned vo = unsigned(((row0 - pw * H) * G::C4N + m.c4) * 16);
+        const Buf bm(e.m.p ? e.m.p + e.m.off(p, e.C, H * W) : e.y, e.m.p ? PB : 0u);
+        const Buf bd(e.d.p ? e.d.p + e.d.off(p, e.C, H * W) : e.y, e.d.p ? PB : 0u);
+        const float c = e.add ? e.add[p] : 0.0f;
+        const Buf by(e.y + ys.off(p, e.C, H * W), PB);
+        constexpr int CH = G::JLD < 4 ? G::JLD : 4;
 #pragma unroll
-  for (int i = 0; i < G::JLD; ++i) {
-    const int row = G::v4_row(w, i, m);
-    const unsigned f = G::v4_index(row, m);
-    const int pl = int(f / V4P), q = int(f % V4P);
-    if (pl >= nvalid) continue;
-    const long long p = p0 + pl;
-    float4 v = fft.v4_get(row, col);
-    if (e.add) {
-      const float c = e.add[p];
-      v = make_float4(v.x + c, v.y + c, v.z + c, v.w + c);
+        for (int i0 = 0; i0 < G::JLD; i0 += CH) {
+          float4 mv[CH], dv[CH];
+#pragma unroll
+          for (int i = 0; i < CH; ++i) {
+            if (e.m.p) bm.ld(mv[i], vo, (i0 + i) * STEP);
+            if (e.d.p) bd.ld(dv[i], vo, (i0 + i) * STEP);
+          }
+#pragma unroll
+          for (int i = 0; i < CH; ++i) {
+            float4 v = fft.v4_get(row0 + (i0 + i) * G::RK, col);
+            v = make_float4(v.x + c, v.y + c, v.z + c, v.w + c);
+            if (e.m.p) v = make_float4(v.x * mv[i].x, v.y * mv[i].y, v.z * mv[i].z, v.w * mv[i].w);
+            if (e.d.p)
+              v = make_float4(v.x * dsilu1(dv[i].x), v.y * dsilu1(dv[i].y), v.z * dsilu1(dv[i].z),
+                              v.w * dsilu1(dv[i].w));
+            by.st(v, vo, (i0 + i) * STEP);
+            psum += (v.x + v.y) + (v.z + v.w);
+          }
+        }
+      }
+    } else {
+#pragma unroll
+    for (int i = 0; i < G::JLD; ++i) {
+      const int row = G::v4_row(w, i, m);
+      const unsigned f = G::v4_index(row, m);
+      const int pl = int(f / V4P), q = int(f % V4P);
+      if (pl >= nvalid) continue;
+      const long long p = p0 + pl;
+      float4 v = fft.v4_get(row, col);
+      if (e.add) {
+        const float c = e.add[p];
+        v = make_float4(v.x + c, v.y + c, v.z + c, v.w + c);
+      }
+      if (e.m.p) {
+        const float4 u = *reinterpret_cast<const float4*>(e.m.p + e.m.off(p, e.C, H * W) + 4 * q);
+        v = make_float4(v.x * u.x, v.y * u.y, v.z * u.z, v.w * u.w);
+      }
+      if (e.d.p) {
+        const float4 u = *reinterpret_cast<const float4*>(e.d.p + e.d.off(p, e.C, H * W) + 4 * q);
+        v = make_float4(v.x * dsilu1(u.x), v.y * dsilu1(u.y), v.z * dsilu1(u.z), v.w * dsilu1(u.w));
+      }
+      *reinterpret_cast<float4*>(e.y + ys.off(p, e.C, H * W) + 4 * q) = v;
+      psum += (v.x + v.y) + (v.z + v.w);
     }
-    if (e.m.p) {
-      const float4 u = *reinterpret_cast<const float4*>(e.m.p + e.m.off(p, e.C, H * W) + 4 * q);
-      v = make_float4(v.x * u.x, v.y * u.y, v.z * u.z, v.w * u.w);
     }
-    if (e.d.p) {
-      const float4 u = *reinterpret_cast<const float4*>(e.d.p + e.d.off(p, e.C, H * W) + 4 * q);
-      v = make_float4(v.x * dsilu1(u.x), v.y * dsilu1(u.y), v.z * dsilu1(u.z), v.w * dsilu1(u.w));
-    }
-    *reinterpret_cast<float4*>(e.y + ys.off(p, e.C, H * W) + 4 * q) = v;
-    psum += (v.x + v.y) + (v.z + v.w);
-  }
-  if constexpr (G::V4_LINEAR) {
-    if (e.sums) {
-      // each wave's rows lie in one plane: wave sums in a fixed order, then the plane's waves in order
-      __shared__ float wsum[G::NW];
-      const float s = wave_sum(psum);
-      if (l == 0) wsum[w] = s;
-      __syncthreads();
-      constexpr int WPP = G::HP / G::RPW;   // waves per plane
-      if (int(tid) < NP && int(tid) < nvalid) {
-        float acc = 0.0f;
-        for (int k = 0; k < WPP; ++k) acc += wsum[int(tid) * WPP + k];
-        e.sums[p0 + tid] = acc;
+    if constexpr (G::V4_LINEAR) {
+      if (e.sums) {
+        // each wave's rows lie in one plane: wave sums in a fixed order, then the plane's waves in order
+        const float s = wave_sum(psum);
+        if (l == 0) wsum[w] = s;
+        __syncthreads();
+        constexpr int WPP = G::HP / G::RPW;   // waves per plane
+        if (int(tid) < NP && int(tid) < nvalid) {
+          float acc = 0.0f;
+          for (int k = 0; k < WPP; ++k) acc += wsum[int(tid) * WPP + k];
+          e.sums[p0 + tid] = acc;
+        }
       }
     }
+    __syncthreads();   // the stores (and the sums) are done with LDS before the next group's C2
+  };
+  if constexpr (PF) {
+    for (long long g = blockIdx.x; g < NG; g += gridDim.x) group(g);
+  } else {
+    group(blockIdx.x);
   }
 }
 
@@ -561,15 +791,21 @@ namespace {
 template <int LH, int NP, int PPT>
 hipError_t run_fwd_ex(const FftEx& e, long long P, float2* spec, hipStream_t s) {
   using G = Geom<LH, LH, NP, PPT>;
-  hipLaunchKernelGGL((rfft2_planes_ex<LH, LH, NP, PPT>), dim3(unsigned((P + NP - 1) / NP)), dim3(G::NT), 0, s, e, P,
-                     spec);
+  const auto k = rfft2_planes_ex<LH, LH, NP, PPT>;
+  // persistent kernels: as many workgroups as fit at once; the others one per group
+  static const unsigned grid = fwd_persistent(G::V4_LINEAR, NP) ? resident_grid(reinterpret_cast<const void*>(k), G::NT, 1LL << 40) : ~0u;
+  const long long groups = (P + NP - 1) / NP;
+  hipLaunchKernelGGL(k, dim3(unsigned(groups < grid ? groups : grid)), dim3(G::NT), 0, s, e, P, spec);
   return hipGetLastError();
 }
 template <int LH, int NP, int PPT>
 hipError_t run_inv_ex(const float2* spec, long long P, const FftEx& e, hipStream_t s) {
   using G = Geom<LH, LH, NP, PPT>;
-  hipLaunchKernelGGL((irfft2_planes_ex<LH, LH, NP, PPT>), dim3(unsigned((P + NP - 1) / NP)), dim3(G::NT), 0, s,
-                     spec, P, e);
+  const auto k = irfft2_planes_ex<LH, LH, NP, PPT>;
+  // persistent kernels: as many workgroups as fit at once; the others one per group
+  static const unsigned grid = inv_persistent(G::V4_LINEAR) ? resident_grid(reinterpret_cast<const void*>(k), G::NT, 1LL << 40) : ~0u;
+  const long long groups = (P + NP - 1) / NP;
+  hipLaunchKernelGGL(k, dim3(unsigned(groups < grid ? groups : grid)), dim3(G::NT), 0, s, spec, P, e);
   return hipGetLastError();
 }
 }  // namespace

@@ -965,13 +965,18 @@ proj_persist_kernel(const TI* __restrict__ A, int M, int K, int N, const float* 
 // channel plane per 16-byte load (4 channels: 4 loads) instead of one element per load, and
 // transposes them in registers for the [row][k] LDS layout: a quarter of the A load
 // instructions, which otherwise fill the wave's outstanding-load counter and stall the issue
-template <bool PLANE_A, bool OUT_SPLIT, class TI, class TO, int TM_, bool PX4 = false>
+// TN_ = 64 (channels-last outputs with N <= 64): the four waves split the tile as two row halves
+// by two 32-column halves instead of four column quarters, so no wave runs on columns past N.
+template <bool PLANE_A, bool OUT_SPLIT, class TI, class TO, int TM_, bool PX4 = false, int TN_ = 128>
 __global__ void __launch_bounds__(256, (sizeof(TI) == 2 && !PLANE_A) ? 3 : 2)
 proj_kc_kernel(const TI* __restrict__ A, int M, int K, int N, const float* __restrict__ Wt,
                const float* __restrict__ bias, int HW, TO* __restrict__ out_lo, TO* __restrict__ out_hi,
                int act_lo, int act_hi, float* __restrict__ partial, int NH, int slots) {
-  constexpr int TM = TM_, TN = 128, NT = 256, KC = 32, KP = KC + 8, MI = TM / 16;
+  constexpr int TM = TM_, TN = TN_, NT = 256, KC = 32, KP = KC + 8;
   static_assert(TM == 64 || TM == 128, "row tiles of 64 or 128");
+  static_assert(TN == 128 || (TN == 64 && !OUT_SPLIT), "64-column tiles for channels-last outputs only");
+  // waves: WC across the tile's columns (32 each) by WR across its rows (RW each, MI blocks of 16)
+  constexpr int WC = TN / 32, WR = 4 / WC, RW = TM / WR, MI = RW / 16;
   static_assert(!PX4 || PLANE_A, "4-pixel loads are for plane-major A");
   constexpr int NI = TM / 32, NKQ = 256 / TM;   // A load groups per thread; plane-major k groups
   constexpr bool A1_ONLY = sizeof(TI) == 2;      // bf16 A: one nonzero part
@@ -986,7 +991,8 @@ proj_kc_kernel(const TI* __restrict__ A, int M, int K, int N, const float* __res
   constexpr int OUT_N = OUT_SPLIT ? 4 * 16 * SPC * 2 : 64 * OP * 2;   // output staging, in bf16 units
   constexpr int LDS_N = OUT_N > 2 * STG ? OUT_N : 2 * STG;
   __shared__ __attribute__((aligned(16))) __bf16 lds[LDS_N];   // two A stages; the output staging reuses them
-  const int tid = threadIdx.x, lane = tid & 63, wn = tid >> 6;
+  const int tid = threadIdx.x, lane = tid & 63, wv = tid >> 6;
+  const int wn = wv % WC, wr = wv / WC;   // column group, row group of this wave
   // XCD-aware tile order: workgroup ids go round-robin over the 8 XCDs, so the
   // tiles are dealt to the XCDs in 8 contiguous runs, column tile fastest: the
   // column tiles of one row tile run on the same XCD and share its A rows in L2
@@ -1207,7 +1213,7 @@ proj_kc_kernel(const TI* __restrict__ A, int M, int K, int N, const float* __res
       // lane l: A rows l % 16 and B columns l % 16, k = 8 (l / 16) + 0..7
 #pragma unroll
       for (int i = 0; i < MI; ++i) {
-        const int o = (i * 16 + (lane & 15)) * KP + kl;
+        const int o = (wr * RW + i * 16 + (lane & 15)) * KP + kl;
         const bf16x8 a1 = *reinterpret_cast<const bf16x8*>(Ap + o);
         if constexpr (A1_ONLY) {
 #pragma unroll
@@ -1375,7 +1381,8 @@ proj_kc_kernel(const TI* __restrict__ A, int M, int K, int N, const float* __res
       }
     }
   } else {
-    // channels-last: stage 64 rows at a time in LDS, then whole-row stores of 4 columns per lane
+    // channels-last: stage 64 rows at a time in LDS, then whole-row stores of 4 columns per lane;
+    // the waves whose row blocks fall in the 64 rows stage them
     float* st = reinterpret_cast<float*>(lds);
 #pragma unroll
     for (int h = 0; h < TM / 64; ++h) {
@@ -1385,9 +1392,12 @@ proj_kc_kernel(const TI* __restrict__ A, int M, int K, int N, const float* __res
         const int cl = wn * 32 + j * 16 + (lane & 15);
         const float bv = n0 + cl < N ? bias[n0 + cl] : 0.0f;
 #pragma unroll
-        for (int i = 0; i < 4; ++i)
+        for (int i = 0; i < MI; ++i) {
+          const int rb = wr * RW + i * 16 - h * 64;   // block's first row within these 64 (uniform)
+          if (rb < 0 || rb >= 64) continue;
 #pragma unroll
-          for (int r = 0; r < 4; ++r) st[(i * 16 + (lane >> 4) * 4 + r) * OP + cl] = acc[h * 4 + i][j][r] + bv;
+          for (int r = 0; r < 4; ++r) st[(rb + (lane >> 4) * 4 + r) * OP + cl] = acc[i][j][r] + bv;
+        }
       }
       __syncthreads();
       for (int f = tid; f < 64 * (TN / 4); f += NT) {
@@ -1442,7 +1452,7 @@ int proj_in_ctx_slots(int K, int HW) {
   return 0;
 }
 
-template <bool PLANE_A, bool OUT_SPLIT, class TI, class TO, int TM>
+template <bool PLANE_A, bool OUT_SPLIT, class TI, class TO, int TM, int TN = 128>
 static hipError_t launch_kc_tm(const void* A, int M, int K, int N, const float* W, const float* b, int HW, void* lo,
                                void* hi, int act_lo, int act_hi, float* partial, int NH, hipStream_t s) {
   // the kernel's buffer resources (one row tile of A, all of W) must stay below 2^31 bytes, the
@@ -1450,18 +1460,19 @@ static hipError_t launch_kc_tm(const void* A, int M, int K, int N, const float* 
   const long long a_bytes = PLANE_A ? (long long)((TM - 2) / HW + 2) * K * HW * (long long)sizeof(TI)
                                     : (long long)TM * K * (long long)sizeof(TI);
   if (a_bytes >= (1LL << 31) || (long long)K * N * 4 >= (1LL << 31)) return hipErrorInvalidValue;
-  const dim3 grid(unsigned((M + TM - 1) / TM) * unsigned((N + 127) / 128));
+  const dim3 grid(unsigned((M + TM - 1) / TM) * unsigned((N + TN - 1) / TN));
   const int slots = partial ? proj_in_ctx_slots(K, HW) : 0;
   if constexpr (PLANE_A) {
     if (HW % 4 == 0) {
-      hipLaunchKernelGGL((proj_kc_kernel<PLANE_A, OUT_SPLIT, TI, TO, TM, true>), grid, dim3(256), 0, s,
+      hipLaunchKernelGGL((proj_kc_kernel<PLANE_A, OUT_SPLIT, TI, TO, TM, true, TN>), grid, dim3(256), 0, s,
                          static_cast<const TI*>(A), M, K, N, W, b, HW, static_cast<TO*>(lo), static_cast<TO*>(hi),
                          act_lo, act_hi, partial, NH, slots);
       return hipGetLastError();
     }
   }
-  hipLaunchKernelGGL((proj_kc_kernel<PLANE_A, OUT_SPLIT, TI, TO, TM>), grid, dim3(256), 0, s, static_cast<const TI*>(A),
-                     M, K, N, W, b, HW, static_cast<TO*>(lo), static_cast<TO*>(hi), act_lo, act_hi, partial, NH, slots);
+  hipLaunchKernelGGL((proj_kc_kernel<PLANE_A, OUT_SPLIT, TI, TO, TM, false, TN>), grid, dim3(256), 0, s,
+                     static_cast<const TI*>(A), M, K, N, W, b, HW, static_cast<TO*>(lo), static_cast<TO*>(hi), act_lo,
+                     act_hi, partial, NH, slots);
   return hipGetLastError();
 }
 
@@ -1471,6 +1482,15 @@ template <bool PLANE_A, bool OUT_SPLIT, class TI, class TO>
 static hipError_t launch_kc(const void* A, int M, int K, int N, const float* W, const float* b, int HW, void* lo,
                             void* hi, int act_lo, int act_hi, float* partial, int NH, hipStream_t s) {
   if constexpr (!OUT_SPLIT) {
+    // narrow outputs: 64-column tiles (no wave on columns past N)
+    if (N <= 64) {
+      const long long tiles = (M + kKcTM - 1) / kKcTM;
+      if (tiles < cu_count())
+        return launch_kc_tm<PLANE_A, OUT_SPLIT, TI, TO, 64, 64>(A, M, K, N, W, b, HW, lo, hi, act_lo, act_hi, partial,
+                                                              NH, s);
+      return launch_kc_tm<PLANE_A, OUT_SPLIT, TI, TO, kKcTM, 64>(A, M, K, N, W, b, HW, lo, hi, act_lo, act_hi, partial,
+                                                                 NH, s);
+    }
     const long long tiles = (long long)((M + kKcTM - 1) / kKcTM) * ((N + 127) / 128);
     if (tiles < cu_count())
       return launch_kc_tm<PLANE_A, OUT_SPLIT, TI, TO, 64>(A, M, K, N, W, b, HW, lo, hi, act_lo, act_hi, partial, NH, s);

@@ -87,6 +87,31 @@ class _ProjPlanesFn(torch.autograd.Function):
         return dx, dw, dy.sum(dim=(0, 2)), None, None
 
 
+def _col_sums(x: torch.Tensor) -> torch.Tensor:
+    """Column sums of a contiguous float32 (M, N) tensor on the frame-mean kernel: the rows as M / R
+    'frames' of R rows (R the largest power of two <= 1024 dividing M, so the mean's 1 / R and the
+    rescale are exact), their means summed in a fixed order."""
+    M, N = x.shape
+    R = min(M & -M, 1024)
+    return S.frame_mean(x.view(M // R, R, 1, N)).sum(dim=0) * R
+
+
+class _PermuteIndex(torch.autograd.Function):
+    """x.index_select(dim, idx) for a permutation idx, with the gradient gathered back through the
+    inverse permutation (instead of index_select's scatter-add into a zeroed tensor)."""
+
+    @staticmethod
+    def forward(ctx, x, dim, idx, inv):
+        ctx.dim = dim
+        ctx.save_for_backward(inv)
+        return x.index_select(dim, idx)
+
+    @staticmethod
+    def backward(ctx, g):
+        (inv,) = ctx.saved_tensors
+        return g.index_select(ctx.dim, inv), None, None, None
+
+
 class _ProjOutFn(torch.autograd.Function):
     """Dense over plane-major y (F, K, HW) into channels-last (F HW, N) on the HIP projection kernel.
     Adjoint: dy = dout W^T back to plane-major (the channels-last -> plane-major kernel with W^T),
@@ -105,7 +130,7 @@ class _ProjOutFn(torch.autograd.Function):
         N = kernel.shape[1]
         dy = S.proj_planes(dout, kernel.t().contiguous(), kernel.new_zeros(K), F, hw, out_dtype=torch.float32)
         dw = torch.bmm(y, dout.view(F, hw, N)).sum(dim=0)
-        return dy, dw, dout.sum(dim=0)
+        return dy, dw, _col_sums(dout)
 
 
 class _DwConvFn(torch.autograd.Function):
@@ -125,7 +150,7 @@ class _DwConvFn(torch.autograd.Function):
         C = x.shape[-1]
         dx = S.depthwise_conv(dy, kernel.flip(0, 1).contiguous(), kernel.new_zeros(C), out_dtype=torch.float32)
         dw = S.depthwise_conv_wgrad(x, dy, kernel.shape[0])
-        return dx, dw, dy.sum(dim=(0, 1, 2))
+        return dx, dw, _col_sums(dy.view(-1, C))
 
 
 def _dwconv_cl(x4, q):
@@ -141,12 +166,19 @@ def _dwconv_cl(x4, q):
             + q["bias"][None, :, None, None]).permute(0, 2, 3, 1)
 
 
-def _col_index(H: int, W: int, device) -> torch.Tensor:
-    return torch.tensor(S.scan_col_order(H, W), dtype=torch.long, device=device)
+def _perm(order, device):
+    idx = torch.tensor(order, dtype=torch.long, device=device)
+    return idx, torch.argsort(idx)
 
 
-def _khat_index(H: int, W: int, device) -> torch.Tensor:
-    return torch.tensor(S.scan_khat_order(H, W), dtype=torch.long, device=device)
+def _col_index(H: int, W: int, device):
+    """(scan column order, its inverse) as index tensors."""
+    return _perm(S.scan_col_order(H, W), device)
+
+
+def _khat_index(H: int, W: int, device):
+    """(K_hat scan slot order, its inverse) as index tensors."""
+    return _perm(S.scan_khat_order(H, W), device)
 
 
 def gate_planes(ctx: torch.Tensor, p: Dict[str, Any], H: int, W: int, gate_type: str, activation: str,
@@ -172,7 +204,7 @@ def gate_planes(ctx: torch.Tensor, p: Dict[str, Any], H: int, W: int, gate_type:
         d = Fn.softplus(g)
     dd = d + 1e-8
     planes = torch.stack([torch.exp(-d), dd * make("B_proj"), dd * 2e-7, make("C_proj") * c_scale], dim=-1)
-    return planes.index_select(3, _col_index(H, W, ctx.device)).contiguous()
+    return _PermuteIndex.apply(planes, 3, *_col_index(H, W, ctx.device)).contiguous()
 
 
 def khat_planes(k: torch.Tensor, H: int, W: int, rho: float) -> torch.Tensor:
@@ -190,7 +222,7 @@ def khat_planes(k: torch.Tensor, H: int, W: int, rho: float) -> torch.Tensor:
     kh = F * rho / (1.0 + F.abs())
     kh = torch.where(kh.abs() < 1e-7, torch.full_like(kh, 1e-7), kh)
     C = kh.shape[0]
-    return kh.reshape(C, -1).index_select(1, _khat_index(H, W, k.device)).view(C, H, W // 2 + 1)
+    return _PermuteIndex.apply(kh.reshape(C, -1), 1, *_khat_index(H, W, k.device)).view(C, H, W // 2 + 1)
 
 
 def _causal_t(x5, p):

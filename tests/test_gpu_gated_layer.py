@@ -72,7 +72,8 @@ def test_proj_in_bf16_input(mods, F, HW, K, N):
     assert rel_err(to_np(ctx), ref_lo.mean(axis=2)) < 1e-5
 
 
-@pytest.mark.parametrize("F,HW,K,N", [(4, 1024, 64, 64), (2, 196, 256, 128), (2, 16, 640, 320), (3, 49, 448, 224)])
+@pytest.mark.parametrize("F,HW,K,N", [(4, 1024, 64, 64), (2, 196, 256, 128), (2, 16, 640, 320), (3, 49, 448, 224),
+                                      (2, 49, 128, 48)])
 def test_proj_out_bf16_input(mods, F, HW, K, N):
     """Plane-major bf16 A into the output projection (persistent and K-chunked kernels)."""
     _, S = mods
@@ -102,10 +103,12 @@ def test_proj_planes_bf16_input(mods, F, HW, K, N):
 
 
 # K-chunked kernel (K > 64): 4-pixel loads of plane-major A where H*W % 4 == 0 (K = 70: channels past K
-# within a chunk), element loads for H*W = 49
+# within a chunk), element loads for H*W = 49; N <= 64 takes 64-column tiles (waves split as two row
+# halves by two column halves), 64-row tiles when few tiles (M = 48, 147, 1372), 128-row ones with a
+# partial last tile (M = 137200)
 @pytest.mark.parametrize("F,HW,K,N", [(4, 1024, 64, 64), (2, 16384, 128, 64), (3, 196, 96, 150),
                                       (3, 49, 448, 224), (2, 16, 640, 320), (2, 196, 256, 128), (5, 49, 36, 30),
-                                      (3, 16, 70, 40)])
+                                      (3, 16, 70, 40), (3, 49, 100, 64), (7, 196, 130, 50), (700, 196, 96, 64)])
 def test_proj_out_channels_last(mods, F, HW, K, N):
     _, S = mods
     print_case(test="proj_out", F=F, HW=HW, K=K, N=N)

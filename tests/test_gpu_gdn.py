@@ -59,6 +59,21 @@ def test_rfft2_and_norms_match_numpy(mods, P, H, dt):
     assert rel_err(to_np(norms), np.sum(np.abs(ref) ** 2, axis=(1, 2))) < 2e-6
 
 
+@pytest.mark.parametrize("P,H", [(1100, 128), (2049, 64), (6403, 32)])
+def test_rfft2_more_groups_than_resident_workgroups(mods, P, H):
+    """The persistent forward transform with more plane groups than workgroups resident at once
+    (512 at 128 x 128 and 64 x 64 on 256 CUs, 768 at 32 x 32): later groups' planes are loaded
+    during earlier groups' passes (128, 64) or after them (32); partial last groups at 64 and 32."""
+    _, S = mods
+    print_case(test="rfft2_groups", P=P, H=H)
+    x = torch.randn((P, H, H), device="cuda", generator=torch.Generator(device="cuda").manual_seed(P))
+    spec, norms = S.rfft2(x, want_norms=True)
+    ref = np.fft.rfft2(to_np(x).astype(np.float64))
+    got = spec.cpu().numpy().astype(np.complex128)
+    assert np.max(np.abs(got - ref)) / np.sqrt(np.mean(np.abs(ref) ** 2)) < 2e-6
+    assert rel_err(to_np(norms), np.sum(np.abs(ref) ** 2, axis=(1, 2))) < 2e-6
+
+
 @pytest.mark.parametrize("P,H", FFT_SIZES)
 def test_irfft2_c2r_rule_matches_numpy(mods, P, H):
     _, S = mods
