@@ -59,19 +59,27 @@ def test_rfft2_and_norms_match_numpy(mods, P, H, dt):
     assert rel_err(to_np(norms), np.sum(np.abs(ref) ** 2, axis=(1, 2))) < 2e-6
 
 
-@pytest.mark.parametrize("P,H", [(1100, 128), (2049, 64), (6403, 32)])
-def test_rfft2_more_groups_than_resident_workgroups(mods, P, H):
-    """The persistent forward transform with more plane groups than workgroups resident at once
-    (512 at 128 x 128 and 64 x 64 on 256 CUs, 768 at 32 x 32): later groups' planes are loaded
-    during earlier groups' passes (128, 64) or after them (32); partial last groups at 64 and 32."""
+@pytest.mark.parametrize("P,H,dt", [(1100, 128, "f32"), (1100, 128, "bf16"), (2049, 64, "f32"), (6403, 32, "f32")])
+def test_rfft2_more_groups_than_resident_workgroups(mods, P, H, dt):
+    """The persistent forward transform (128 x 128) with more planes than workgroups resident at
+    once (512 on 256 CUs): later planes are loaded during earlier planes' passes; 64 and 32 run one
+    plane group per workgroup (partial last groups).  Then the inverse, persistent at 128 and 64,
+    over the same spectra."""
     _, S = mods
-    print_case(test="rfft2_groups", P=P, H=H)
+    print_case(test="rfft2_groups", P=P, H=H, dtype=dt)
     x = torch.randn((P, H, H), device="cuda", generator=torch.Generator(device="cuda").manual_seed(P))
+    x = x if dt == "f32" else x.to(torch.bfloat16)
     spec, norms = S.rfft2(x, want_norms=True)
     ref = np.fft.rfft2(to_np(x).astype(np.float64))
     got = spec.cpu().numpy().astype(np.complex128)
     assert np.max(np.abs(got - ref)) / np.sqrt(np.mean(np.abs(ref) ** 2)) < 2e-6
     assert rel_err(to_np(norms), np.sum(np.abs(ref) ** 2, axis=(1, 2))) < 2e-6
+    y = S.irfft2(spec, H)
+    yref = np.fft.irfft2(got, s=(H, H))
+    assert rel_err(to_np(y), yref) < 2e-6
+    if dt == "bf16":
+        yb = S.irfft2(spec, H, out_dtype=torch.bfloat16)   # the float result rounded once
+        assert bf16_excess_err(to_np(yb), yref) < 2e-5
 
 
 @pytest.mark.parametrize("P,H", FFT_SIZES)
