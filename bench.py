@@ -245,12 +245,17 @@ def gdn_step(cell, variables, x, w, S, mark):
     ab, bkv = S.gdn_gates(ctx, p, H, W, cell.delta_key_dim, cell.gate_type, True, "sinusoid", cell.rope_base)
     mark("gates")
     convs = [p["short_conv_q"], p["short_conv_k"], p["short_conv_v"]]
-    if cell.qkv_conv_size > 1:
+    # bf16 input: the output projection computes gate_proj from x itself (no gate planes in HBM)
+    xgate = x.dtype == torch.bfloat16 and S.gdn_proj_out_xgate_supported(C, C, HW)
+    gv = None
+    if cell.qkv_conv_size > 1 or xgate:
         qkv = S.gdn_qkv_proj(xq, p["qkv_proj"]["kernel"], p["qkv_proj"]["bias"], B, T, H, W, convs, 1, bkv,
                              out_dtype=f32)
         mark("qkv_proj")   # with the short conv, SiLU and input gates (one kernel where cssm_gdn_qkv_fused says so)
-        gv = S.proj_planes(x, p["gate_proj"]["kernel"], p["gate_proj"]["bias"], F, HW, act="silu", out_dtype=f32)
-        mark("gate_proj")
+        if not xgate:
+            gv = S.proj_planes(x, p["gate_proj"]["kernel"], p["gate_proj"]["bias"], F, HW, act="silu",
+                               out_dtype=f32)
+            mark("gate_proj")
     else:
         # both projections read x: gate_proj's columns ride in the fused qkv launch
         qkv, gv = S.gdn_qkv_gate_proj(x, p["qkv_proj"]["kernel"], p["qkv_proj"]["bias"], B, T, H, W, convs, 1, bkv,
@@ -266,9 +271,15 @@ def gdn_step(cell, variables, x, w, S, mark):
         mark("scan_bins")
         o = S.irfft2(ohat, W, out_dtype=f32)
         mark("irfft2")
-    out = S.gdn_proj_out(o.view(F, C, HW), gv, "rms", p["rms_scale"], None, p["output_proj"]["kernel"],
-                         p["output_proj"]["bias"], out_dtype=x.dtype)
-    mark("proj_out")
+    if xgate:
+        out = S.gdn_proj_out_xgate(o.view(F, C, HW), x, "rms", p["rms_scale"], None, p["gate_proj"]["kernel"],
+                                   p["gate_proj"]["bias"], "silu", p["output_proj"]["kernel"], p["output_proj"]["bias"],
+                                   out_dtype=x.dtype)
+        mark("proj_out_xgate")   # RMSNorm x SiLU(gate_proj(x)) computed in front of output_proj
+    else:
+        out = S.gdn_proj_out(o.view(F, C, HW), gv, "rms", p["rms_scale"], None, p["output_proj"]["kernel"],
+                             p["output_proj"]["bias"], out_dtype=x.dtype)
+        mark("proj_out")
     return out.view(B, T, H, W, C)
 
 

@@ -424,15 +424,23 @@ class GatedDeltaNetCSSM:
         convs = None
         if self.short_conv_size > 0:
             convs = [p["short_conv_q"], p["short_conv_k"], p["short_conv_v"]]
-        # qkv_proj with the short conv, SiLU and input gates in its epilogue; without the qkv conv both
-        # projections read x, and gate_proj rides in the same call
+        # qkv_proj with the short conv, SiLU and input gates in its epilogue.  gate_proj: with a bf16 layer
+        # input the output projection computes it from x (its planes never reach HBM); otherwise, without
+        # the qkv conv, as more columns of the qkv launch (x read once), else a projection of its own
         gact = "silu" if self.output_gate_act == "silu" else "sigmoid"
+        xgate = x.dtype == torch.bfloat16 and S.gdn_proj_out_xgate_supported(C, C, HW)
+        gv = None
         if full_conv:
             # k x k conv with full channel mixing (im2col rows through the projection GEMM), then the
             # short conv, SiLU and input gates in place on its planes
             qkv = S.conv_full_planes(x.view(F, H, W, C), p["qkv_proj"]["kernel"], p["qkv_proj"]["bias"])
             qkv = S.gdn_qkv_post(qkv.view(B, T, 3 * C, H, W), convs, gate_mode, gates)
-            gv = S.proj_planes(x, p["gate_proj"]["kernel"], p["gate_proj"]["bias"], F, HW, act=gact, out_dtype=f32)
+            if not xgate:
+                gv = S.proj_planes(x, p["gate_proj"]["kernel"], p["gate_proj"]["bias"], F, HW, act=gact,
+                                   out_dtype=f32)
+        elif xgate:
+            qkv = S.gdn_qkv_proj(xq, p["qkv_proj"]["kernel"], p["qkv_proj"]["bias"], B, T, H, W, convs, gate_mode,
+                                 gates, out_dtype=f32)
         elif xq is x:
             qkv, gv = S.gdn_qkv_gate_proj(x, p["qkv_proj"]["kernel"], p["qkv_proj"]["bias"], B, T, H, W, convs,
                                           gate_mode, gates, p["gate_proj"]["kernel"], p["gate_proj"]["bias"], gact,
@@ -460,8 +468,13 @@ class GatedDeltaNetCSSM:
             ns, nb = p["output_layernorm"]["scale"], p["output_layernorm"]["bias"]
         else:
             ns = nb = None
-        out = S.gdn_proj_out(o.view(F, C, HW), gv, self.output_norm, ns, nb, p["output_proj"]["kernel"],
-                             p["output_proj"]["bias"], out_dtype=out_dtype or x.dtype)
+        if xgate:
+            out = S.gdn_proj_out_xgate(o.view(F, C, HW), x, self.output_norm, ns, nb, p["gate_proj"]["kernel"],
+                                       p["gate_proj"]["bias"], gact, p["output_proj"]["kernel"],
+                                       p["output_proj"]["bias"], out_dtype=out_dtype or x.dtype)
+        else:
+            out = S.gdn_proj_out(o.view(F, C, HW), gv, self.output_norm, ns, nb, p["output_proj"]["kernel"],
+                                 p["output_proj"]["bias"], out_dtype=out_dtype or x.dtype)
         return out.view(B, T, H, W, C)
 
     __call__ = apply

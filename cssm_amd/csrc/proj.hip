@@ -276,12 +276,21 @@ __global__ void __launch_bounds__(256) ctx_reduce_kernel(const float* __restrict
 //   2: LayerNorm (x - mean) rsqrt(var + 1e-6) s_k + b_k; 0: none) and
 //   multiplied by the matching pixel of the plane-major gate G -- the GDN
 //   output path, cssm.py:5026-5031 and :5126, feeding output_proj :5141.
+//   XG (with NORM): the gate is not read but computed in the kernel from the
+//   layer input, G = act(X Wg + bg) (gate_proj, cssm.py:4853-4859), X the
+//   tile's channels-last bf16 rows staged in LDS next to A, on bf16 MFMA with
+//   Wg split into three bf16 parts (X is exactly its one part), then applied
+//   with the norm in the MFMA output layout.
 // ---------------------------------------------------------------------------
 struct NormGate {
   const void* G;        // plane-major (F, K, HW) gate, same dtype as A
   const float* scale;   // (K) or nullptr
   const float* shift;   // (K) or nullptr (LayerNorm bias)
   int kind;             // 0 none, 1 rms, 2 layer
+  const uint16_t* X;    // XG: channels-last (M, K) bf16 layer input
+  const float* wg;      // XG: (K, K) gate_proj kernel
+  const float* bg;      // XG: (K) its bias
+  int gact;             // XG: 1 SiLU, 2 sigmoid
 };
 
 // GDN qkv epilogue (TT > 0; the tiled kernel, for the shapes the frame-sequential
@@ -312,7 +321,7 @@ struct QkvPost {
 };
 
 template <int KMAX, bool PLANE_A, bool OUT_SPLIT, int WN, class TI, class TO, bool NORM = false, bool SPLIT = false,
-          int TT = 0, bool CARRY = false, bool PX1 = false>
+          int TT = 0, bool CARRY = false, bool PX1 = false, bool XG = false>
 __global__ void __launch_bounds__(256, 2)
 proj_persist_kernel(const TI* __restrict__ A, int M, int K, int N, const float* __restrict__ Wt,
                     const float* __restrict__ bias, int HW, TO* __restrict__ out_lo, TO* __restrict__ out_hi,
@@ -326,6 +335,7 @@ proj_persist_kernel(const TI* __restrict__ A, int M, int K, int N, const float* 
   static_assert(!NORM || (PLANE_A && !OUT_SPLIT), "the norm / gate prologue is for plane-major A");
   static_assert(!PX1 || NORM, "element-wise plane rows only for the norm / gate prologue");
   static_assert(!(NORM && SPLIT), "the norm / gate prologue runs on the fp32 path");
+  static_assert(!XG || (NORM && !PX1 && KMAX == 64 && WN == 2), "computed gate: K <= 64 channels, N <= 64 columns");
   static_assert(!SPLIT || KMAX % 32 == 0, "bf16 MFMA k-blocks of 32");
   constexpr int AP = PLANE_A ? (TM + 16) : (KMAX + 2);   // pitch: rows of A (row-major) or k-rows (plane)
   constexpr int BP = TN + 16;
@@ -346,6 +356,7 @@ proj_persist_kernel(const TI* __restrict__ A, int M, int K, int N, const float* 
   __bf16* const A3 = A2 + TM * KP;
   __shared__ float rowsc[NORM ? 2 * NT : 1];             // per-pixel partial sums, then (scale, mean) of the norm
   __shared__ float nss[NORM ? 2 * KMAX : 1];             // the norm's per-channel scale and shift
+  __shared__ __attribute__((aligned(16))) __bf16 Xs[XG ? TM * KP : 8];   // XG: the tile's X rows [row][k]
   __shared__ float2 gsh[TT > 0 ? TM : 1];                 // qkv epilogue: the tile's input gates
   constexpr int KH = 3;                                   // qkv epilogue: frames carried to the next chunk
   __shared__ float hsh[CARRY ? KH * TN * (TM / 8) : 1];   // their projections, [frame][column][pixel]
@@ -410,6 +421,29 @@ proj_persist_kernel(const TI* __restrict__ A, int M, int K, int N, const float* 
     for (int kk = tid; kk < KMAX; kk += NT) {
       nss[2 * kk] = (ng.scale && kk < K) ? ng.scale[kk] : 1.f;
       nss[2 * kk + 1] = (ng.shift && kk < K) ? ng.shift[kk] : 0.f;
+    }
+  }
+  // XG: lane l's gate_proj fragments, gate channel wn 32 + 16 j + l % 16, k = 32 kb + 8 (l / 16) + e, in three
+  // bf16 parts, and that channel's bias
+  bf16x8 g1[XG ? 2 : 1][XG ? KB : 1], g2[XG ? 2 : 1][XG ? KB : 1], g3[XG ? 2 : 1][XG ? KB : 1];
+  float gb[2] = {0.f, 0.f};
+  if constexpr (XG) {
+#pragma unroll
+    for (int j = 0; j < 2; ++j) {
+      const int gc = wn * 32 + j * 16 + (lane & 15);
+      gb[j] = gc < K ? ng.bg[gc] : 0.f;
+#pragma unroll
+      for (int kb = 0; kb < KB; ++kb)
+#pragma unroll
+        for (int e = 0; e < 8; ++e) {
+          const int kk = kb * 32 + (lane >> 4) * 8 + e;
+          const float w = (kk < K && gc < K) ? ng.wg[size_t(kk) * K + gc] : 0.0f;
+          __bf16 x1, x2, x3;
+          split3_bf16(w, x1, x2, x3);
+          g1[j][kb][e] = x1;
+          g2[j][kb][e] = x2;
+          g3[j][kb][e] = x3;
+        }
     }
   }
   if constexpr (QCW_LDS) {
@@ -606,26 +640,102 @@ proj_persist_kernel(const TI* __restrict__ A, int M, int K, int N, const float* 
       rowsc[2 * tid + 1] = mean;
     }
     __syncthreads();
+    if constexpr (!XG) {   // XG: the statistics only; xgate_norm applies them with the computed gate
 #pragma unroll
-    for (int i = 0; i < PF; ++i) {
-      const int f = i * NT + tid;
-      const int kk = f / (TM / 4), r4 = (f % (TM / 4)) * 4;
-      if (kk >= K) continue;
-      float4 v = *reinterpret_cast<const float4*>(&As[kk * AP + r4]);
-      const float sk = nss[2 * kk], bk = nss[2 * kk + 1];
-      float* e = &v.x;
-      const float* g = &pg[i].x;
+      for (int i = 0; i < PF; ++i) {
+        const int f = i * NT + tid;
+        const int kk = f / (TM / 4), r4 = (f % (TM / 4)) * 4;
+        if (kk >= K) continue;
+        float4 v = *reinterpret_cast<const float4*>(&As[kk * AP + r4]);
+        const float sk = nss[2 * kk], bk = nss[2 * kk + 1];
+        float* e = &v.x;
+        const float* g = &pg[i].x;
 #pragma unroll
-      for (int q = 0; q < 4; ++q) {
-        const float sc = rowsc[2 * (r4 + q)], mu = rowsc[2 * (r4 + q) + 1];
-        e[q] = (ng.kind == 0 ? e[q] : fmaf((e[q] - mu) * sc, sk, bk)) * g[q];
+        for (int q = 0; q < 4; ++q) {
+          const float sc = rowsc[2 * (r4 + q)], mu = rowsc[2 * (r4 + q) + 1];
+          e[q] = (ng.kind == 0 ? e[q] : fmaf((e[q] - mu) * sc, sk, bk)) * g[q];
+        }
+        *reinterpret_cast<float4*>(&As[kk * AP + r4]) = v;
       }
-      *reinterpret_cast<float4*>(&As[kk * AP + r4]) = v;
     }
   };
 
   float4 pf[PF];
-  float4 pg[NORM ? PF : 1];
+  float4 pg[(NORM && !XG) ? PF : 1];
+  // XG: the tile's X rows, 16-byte pieces c = i NT + tid: row c / (KMAX / 8), channels 8 (c % (KMAX / 8)) ..
+  constexpr int PX = XG ? TM * KMAX / 8 / NT : 1;
+  uint4 px[PX];
+  auto fetch_x = [&](int tile) {
+    if constexpr (XG) {
+      const int m0 = tile * TM;
+#pragma unroll
+      for (int i = 0; i < PX; ++i) {
+        const int c = i * NT + tid, r = c / (KMAX / 8), k8 = (c % (KMAX / 8)) * 8;
+        px[i] = (m0 + r < M && k8 < K) ? *reinterpret_cast<const uint4*>(ng.X + size_t(m0 + r) * K + k8)
+                                        : make_uint4(0u, 0u, 0u, 0u);
+      }
+    }
+  };
+  auto stash_x = [&]() {
+    if constexpr (XG) {
+#pragma unroll
+      for (int i = 0; i < PX; ++i) {
+        const int c = i * NT + tid, r = c / (KMAX / 8), k8 = (c % (KMAX / 8)) * 8;
+        *reinterpret_cast<uint4*>(&Xs[r * KP + k8]) = px[i];
+      }
+    }
+  };
+  // XG: x Wg for this wave's rows (wm MI + i) 16 + 4 (l / 16) + q and gate channels wn 32 + 16 j + l % 16
+  // (the MFMA output layout), issued before the norm's statistics so the MFMAs run under them; then
+  // A <- norm(A) * act(x Wg + bg) for exactly those elements
+  floatx4 ag[XG ? MI : 1][2];
+  auto xgate_mma = [&]() {
+    if constexpr (XG) {
+#pragma unroll
+      for (int i = 0; i < MI; ++i) ag[i][0] = ag[i][1] = floatx4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+      for (int kb = 0; kb < KB; ++kb) {
+        if (kb * 32 >= K) break;
+        const int koff = kb * 32 + (lane >> 4) * 8;
+#pragma unroll
+        for (int i = 0; i < MI; ++i) {
+          const bf16x8 a1 = *reinterpret_cast<const bf16x8*>(&Xs[((wm * MI + i) * 16 + (lane & 15)) * KP + koff]);
+#pragma unroll
+          for (int j = 0; j < 2; ++j) {
+            floatx4 c = ag[i][j];
+            c = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a1, g3[j][kb], c, 0, 0, 0);   // small terms first
+            c = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a1, g2[j][kb], c, 0, 0, 0);
+            ag[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a1, g1[j][kb], c, 0, 0, 0);
+          }
+        }
+      }
+    }
+  };
+  auto xgate_norm = [&]() {
+    if constexpr (XG) {
+#pragma unroll
+      for (int j = 0; j < 2; ++j) {
+        const int kk = wn * 32 + j * 16 + (lane & 15);
+        if (kk >= K) continue;
+        const float sk = nss[2 * kk], bk = nss[2 * kk + 1];
+#pragma unroll
+        for (int i = 0; i < MI; ++i) {
+          const int r0 = (wm * MI + i) * 16 + (lane >> 4) * 4;
+          float4 v = *reinterpret_cast<const float4*>(&As[kk * AP + r0]);
+          float* e = &v.x;
+#pragma unroll
+          for (int q = 0; q < 4; ++q) {
+            const float z = ag[i][j][q] + gb[j];
+            const float sg = __builtin_amdgcn_rcpf(1.0f + __expf(-z));
+            const float g = ng.gact == 1 ? z * sg : sg;
+            const float sc = rowsc[2 * (r0 + q)], mu = rowsc[2 * (r0 + q) + 1];
+            e[q] = (ng.kind == 0 ? e[q] : fmaf((e[q] - mu) * sc, sk, bk)) * g;
+          }
+          *reinterpret_cast<float4*>(&As[kk * AP + r0]) = v;
+        }
+      }
+    }
+  };
   // qkv epilogue: a tile's per-pixel / per-frame input gates (TT frames x TP pixels) are
   // loaded with its A rows and written to gsh by the stash, behind the barrier that follows it
   const bool tile_gates = TT > 0 && (qp.gate_mode == 1 || qp.gate_mode == 2);
@@ -657,24 +767,29 @@ proj_persist_kernel(const TI* __restrict__ A, int M, int K, int N, const float* 
   if (tile < tiles) {
     fetch(A, tile, pf);
     fetch_gates(tile);
-    if (NORM) fetch(Gp, tile, pg);
+    if constexpr (XG) fetch_x(tile);
+    else if (NORM) fetch(Gp, tile, pg);
   }
   for (; tile < tiles; tile = tile_of(++kt_)) {
-    __syncthreads();            // previous tile is done with As, gsh (and Bs is staged)
+    __syncthreads();            // previous tile is done with As, Xs, gsh (and Bs is staged)
     stash(pf);
+    stash_x();
     if constexpr (TT > 0) {
       if (tile_gates && tid < TT * TP) gsh[tid] = gpf;
     }
     __syncthreads();
     if constexpr (NORM) {
+      xgate_mma();
       norm_gate(pg);
+      xgate_norm();
       __syncthreads();
     }
     const int next = tile_of(kt_ + 1);
     if (next < tiles) {
       fetch(A, next, pf);
       fetch_gates(next);
-      if (NORM) fetch(Gp, next, pg);
+      if constexpr (XG) fetch_x(next);
+      else if (NORM) fetch(Gp, next, pg);
     }
 
     floatx4 acc[MI][2];
@@ -2054,6 +2169,37 @@ hipError_t launch_proj_out_norm_gate(const void* Y, const void* G, int in_dtype,
       try_persist<true, false, true, uint16_t, uint16_t, true>(Y, M, K, N, W, b, HW, out, nullptr, 0, 0, nullptr, N, ng,
                                                                s);
   }
+  return hipGetLastError();
+}
+
+// the same with the gate computed from the layer input X (bf16 channels-last (M, K)): gate_proj in the
+// kernel (K <= 64, K % 8 == 0, N <= 64, HW % 4 == 0; else invalid value)
+bool proj_out_xgate_supported(int K, int N, int HW) { return K <= 64 && K % 8 == 0 && N <= 64 && HW % 4 == 0; }
+
+template <class TI, class TO>
+static void launch_xgate(const void* Y, const uint16_t* X, int M, int K, int N, const NormGate& ng, const float* W,
+                         const float* b, int HW, void* out, hipStream_t s) {
+  const int tiles = (M + kPersistTM - 1) / kPersistTM;
+  const dim3 grid(unsigned(persistent_grid(tiles)), 1);
+  hipLaunchKernelGGL((proj_persist_kernel<64, true, false, 2, TI, TO, true, false, 0, false, false, true>), grid,
+                     dim3(256), 0, s, static_cast<const TI*>(Y), M, K, N, W, b, HW, static_cast<TO*>(out), nullptr, 0,
+                     0, nullptr, N, ng, QkvPost{});
+}
+
+hipError_t launch_proj_out_norm_xgate(const void* Y, int in_dtype, const uint16_t* X, int M, int K, int N, int norm,
+                                      const float* nscale, const float* nshift, const float* wg, const float* bg,
+                                      int gact, const float* W, const float* b, int HW, void* out, int out_dtype,
+                                      hipStream_t s) {
+  if (!proj_out_xgate_supported(K, N, HW)) return hipErrorInvalidValue;
+  NormGate ng{nullptr, nscale, nshift, norm};
+  ng.X = X;
+  ng.wg = wg;
+  ng.bg = bg;
+  ng.gact = gact;
+  if (in_dtype == 0 && out_dtype == 0) launch_xgate<float, float>(Y, X, M, K, N, ng, W, b, HW, out, s);
+  else if (in_dtype == 0) launch_xgate<float, uint16_t>(Y, X, M, K, N, ng, W, b, HW, out, s);
+  else if (out_dtype == 0) launch_xgate<uint16_t, float>(Y, X, M, K, N, ng, W, b, HW, out, s);
+  else launch_xgate<uint16_t, uint16_t>(Y, X, M, K, N, ng, W, b, HW, out, s);
   return hipGetLastError();
 }
 

@@ -793,6 +793,39 @@ def gdn_proj_out(o: torch.Tensor, gate: torch.Tensor, norm: str, norm_scale: Opt
     return out
 
 
+def gdn_proj_out_xgate_supported(K: int, N: int, hw: int) -> bool:
+    """True when :func:`gdn_proj_out_xgate` has a kernel for these widths and plane size."""
+    return bool(_lib.load().cssm_gdn_proj_out_xgate_supported(K, N, hw))
+
+
+def gdn_proj_out_xgate(o: torch.Tensor, x: torch.Tensor, norm: str, norm_scale: Optional[torch.Tensor],
+                       norm_bias: Optional[torch.Tensor], gate_kernel: torch.Tensor, gate_bias: torch.Tensor,
+                       gate_act: str, kernel: torch.Tensor, bias: torch.Tensor,
+                       out_dtype: Optional[torch.dtype] = None) -> torch.Tensor:
+    """:func:`gdn_proj_out` with the gate computed in the kernel from the bf16 layer input x (F hw rows of K
+    channels): gate = SiLU / sigmoid(x gate_kernel + gate_bias) (gate_proj, cssm.py:4853-4859)."""
+    _dev(o, "o")
+    _dev(x, "x", torch.bfloat16)
+    F, K, hw = o.shape
+    if x.numel() != F * hw * K:
+        raise ValueError("x does not hold F * hw rows of K channels")
+    for t, nm in ((gate_kernel, "gate_kernel"), (gate_bias, "gate_bias"), (kernel, "kernel"), (bias, "bias")):
+        _dev(t, nm, torch.float32)
+    if tuple(gate_kernel.shape) != (K, K) or tuple(gate_bias.shape) != (K,):
+        raise ValueError(f"gate kernel {tuple(gate_kernel.shape)} / bias {tuple(gate_bias.shape)} are not ({K}, {K})")
+    if gate_act not in ("silu", "sigmoid"):
+        raise ValueError(f"gate_act {gate_act!r}")
+    N = kernel.shape[1]
+    od = out_dtype or o.dtype
+    out = torch.empty((F * hw, N), dtype=od, device=o.device)
+    ns = _dev(norm_scale, "norm_scale", torch.float32).data_ptr() if norm_scale is not None else None
+    nb = _dev(norm_bias, "norm_bias", torch.float32).data_ptr() if norm_bias is not None else None
+    _lib.call("cssm_gdn_proj_out_xgate", o.data_ptr(), _DTYPES[o.dtype], x.data_ptr(), F, hw, K, N, _NORMS[norm], ns,
+              nb, gate_kernel.data_ptr(), gate_bias.data_ptr(), _ACTS[gate_act], kernel.data_ptr(), bias.data_ptr(),
+              out.data_ptr(), _DTYPES[od], _stream())
+    return out
+
+
 # --------------------------------------------------------- CSSMSHViTBlock wiring
 
 BLOCK_NORMS = {"global_layer": 0, "temporal_layer": 1, "layer": 2}

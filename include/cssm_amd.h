@@ -30,8 +30,10 @@ extern "C" {
 #endif
 
 /* 3: K_hat's scan layout (cssm_spectral_kernel scan_order = 1) pairs rows at 128 x 128
- *    (cssm_gated_scan_khat_order). */
-#define CSSM_ABI_VERSION 4
+ *    (cssm_gated_scan_khat_order).
+ * 4: scan_variant arguments of the GDN delta-rule entry points.
+ * 5: cssm_im2col_same, cssm_gdn_proj_out_xgate. */
+#define CSSM_ABI_VERSION 5
 
 typedef enum cssm_status {
   CSSM_OK = 0,
@@ -593,6 +595,22 @@ typedef enum cssm_norm { CSSM_NORM_NONE = 0, CSSM_NORM_RMS = 1, CSSM_NORM_LAYER 
 int cssm_gdn_proj_out(const void* o, const void* gate, int in_dtype, int F, int HW, int K, int N, int norm,
                       const float* norm_scale, const float* norm_bias, const float* kernel, const float* bias,
                       void* out, int out_dtype, void* stream);
+
+/*
+ * The same output path with the gate computed in the kernel from the layer
+ * input instead of read: gate = act(x gate_kernel + gate_bias) (gate_proj,
+ * cssm.py:4853-4859, act SiLU or sigmoid as output_gate_act), so gate_proj's
+ * planes never reach HBM.
+ *   x            (F * HW, K) channels-last bf16 layer input, 16-byte aligned
+ *   gate_kernel  (K, K) [gate_proj/kernel], gate_bias (K); gate_act 1 SiLU, 2 sigmoid
+ * Other arguments as cssm_gdn_proj_out.  K <= 64, K % 8 == 0, N <= 64 and HW % 4 == 0
+ * (cssm_gdn_proj_out_xgate_supported), else CSSM_ERR_UNSUPPORTED.
+ */
+int cssm_gdn_proj_out_xgate(const void* o, int in_dtype, const void* x, int F, int HW, int K, int N, int norm,
+                            const float* norm_scale, const float* norm_bias, const float* gate_kernel,
+                            const float* gate_bias, int gate_act, const float* kernel, const float* bias, void* out,
+                            int out_dtype, void* stream);
+int cssm_gdn_proj_out_xgate_supported(int K, int N, int HW);
 
 /* 1 if cssm_gated_scan_fwd has a kernel for (H, W), else 0. */
 int cssm_gated_scan_supported(int H, int W);

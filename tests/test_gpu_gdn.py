@@ -541,6 +541,56 @@ def test_gdn_proj_out_norm_gate(mods):
         assert rel_err(to_np(out), ref) < 1e-5, norm
 
 
+XGATE_CASES = [
+    # F, HW, K, N, norm, gate act, o dtype, out dtype: the C4 widths, narrower ones, a partial last
+    # row tile (F HW not a multiple of 128), LayerNorm and no norm, sigmoid, bf16 o and f32 out
+    (3, 1024, 64, 64, "rms", "silu", torch.float32, torch.bfloat16),
+    (5, 196, 64, 64, "layer", "sigmoid", torch.float32, torch.float32),
+    (2, 1024, 32, 48, "none", "silu", torch.bfloat16, torch.float32),
+    (7, 16, 16, 16, "rms", "sigmoid", torch.float32, torch.float32),
+    (3, 64, 40, 40, "layer", "silu", torch.bfloat16, torch.bfloat16),
+]
+
+
+@pytest.mark.parametrize("F,HW,K,N,norm,gact,odt,outdt", XGATE_CASES,
+                         ids=[f"F{c[0]}_HW{c[1]}_K{c[2]}_N{c[3]}_{c[4]}_{c[5]}" for c in XGATE_CASES])
+def test_gdn_proj_out_xgate_matches_gate_planes(mods, F, HW, K, N, norm, gact, odt, outdt):
+    """The output projection computing gate_proj from the bf16 layer input against the float64 reference
+    of norm(o) * act(x Wg + bg) then output_proj, and against the two-call path (the gate planes from a
+    projection, then cssm_gdn_proj_out)."""
+    _, S = mods
+    print_case(test="gdn_proj_out_xgate", F=F, HW=HW, K=K, N=N, norm=norm, gact=gact)
+    rng = np.random.default_rng(31)
+    o = _dev(rng.standard_normal((F, K, HW)), odt)
+    xb = _dev(rng.standard_normal((F * HW, K)), torch.bfloat16)
+    Wg = rng.standard_normal((K, K)) / np.sqrt(K)
+    bg = rng.standard_normal(K) * 0.1
+    Wt = rng.standard_normal((K, N)) / np.sqrt(K)
+    b = rng.standard_normal(N) * 0.1
+    sc = 1.0 + 0.1 * rng.standard_normal(K)
+    sh = 0.1 * rng.standard_normal(K)
+    ns = _dev(sc) if norm != "none" else None
+    nb = _dev(sh) if norm == "layer" else None
+    out = S.gdn_proj_out_xgate(o, xb, norm, ns, nb, _dev(Wg), _dev(bg), gact, _dev(Wt), _dev(b), out_dtype=outdt)
+    assert out.dtype == outdt and tuple(out.shape) == (F * HW, N)
+    ocl = to_np(o).transpose(0, 2, 1)
+    ref_n = {"rms": lambda: O.rms_norm(ocl, sc), "layer": lambda: O.layer_norm(ocl, sc, sh), "none": lambda: ocl}[norm]()
+    z = to_np(xb).reshape(F, HW, K) @ Wg + bg
+    g = z / (1.0 + np.exp(-z)) if gact == "silu" else 1.0 / (1.0 + np.exp(-z))
+    ref = (ref_n * g).reshape(F * HW, K) @ Wt + b
+    if outdt == torch.bfloat16:
+        assert bf16_excess_err(to_np(out), ref) < 2e-5
+    else:
+        assert rel_err(to_np(out), ref) < 1e-5
+    gv = S.proj_planes(xb, _dev(Wg), _dev(bg), F, HW, act=gact, out_dtype=odt)
+    two = S.gdn_proj_out(o, gv, norm, ns, nb, _dev(Wt), _dev(b), out_dtype=torch.float32)
+    if odt == torch.float32:   # with bf16 o the two-call path rounds the gate planes to bf16 as well
+        if outdt == torch.bfloat16:
+            assert bf16_excess_err(to_np(out), to_np(two)) < 2e-5
+        else:
+            assert rel_err(to_np(out), to_np(two)) < 1e-5
+
+
 # ------------------------------------------------------------------- layer
 
 LAYER_CASES = [
