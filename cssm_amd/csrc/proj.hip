@@ -276,6 +276,11 @@ __global__ void __launch_bounds__(256) ctx_reduce_kernel(const float* __restrict
 //   2: LayerNorm (x - mean) rsqrt(var + 1e-6) s_k + b_k; 0: none) and
 //   multiplied by the matching pixel of the plane-major gate G -- the GDN
 //   output path, cssm.py:5026-5031 and :5126, feeding output_proj :5141.
+//   At K <= 64 on whole 4-pixel runs the product is the split-bf16 one too
+//   (NSPLIT): the gate planes are prefetched in the MFMA output layout, the
+//   norm x gate is evaluated in that layout and written as three bf16 planes
+//   over the fp32 staging; elsewhere (K = 128, element-wise planes, XG) A is
+//   normalised in place and the product runs on fp32 MFMA.
 //   XG (with NORM): the gate is not read but computed in the kernel from the
 //   layer input, G = act(X Wg + bg) (gate_proj, cssm.py:4853-4859), X the
 //   tile's channels-last bf16 rows staged in LDS next to A, on bf16 MFMA with
@@ -334,8 +339,13 @@ proj_persist_kernel(const TI* __restrict__ A, int M, int K, int N, const float* 
   static_assert(!OUT_SPLIT || WM == 1 || TT == 0, "the qkv epilogue needs whole row tiles per wave");
   static_assert(!NORM || (PLANE_A && !OUT_SPLIT), "the norm / gate prologue is for plane-major A");
   static_assert(!PX1 || NORM, "element-wise plane rows only for the norm / gate prologue");
-  static_assert(!(NORM && SPLIT), "the norm / gate prologue runs on the fp32 path");
-  static_assert(!XG || (NORM && !PX1 && KMAX == 64 && WN == 2), "computed gate: K <= 64 channels, N <= 64 columns");
+  static_assert(!(NORM && SPLIT), "the norm / gate prologue splits A itself (NSPLIT), after the norm");
+  // NORM at K <= 64 on whole 4-pixel runs (NSPLIT): the product runs on bf16 MFMA as well; the normalised
+  // and gated A is split into three bf16 planes after the norm, over the fp32 staging (K = 128, and the
+  // element-wise planes, keep the fp32 MFMA product)
+  constexpr bool NSPLIT = NORM && KMAX == 64 && !PX1 && !XG;
+  constexpr bool MSPLIT = SPLIT || NSPLIT;   // the product on split-bf16 MFMA, weight fragments in VGPRs
+  static_assert(!XG || (NORM && KMAX == 64 && !PX1 && WN == 2), "computed gate: K <= 64 channels, N <= 64 columns");
   static_assert(!SPLIT || KMAX % 32 == 0, "bf16 MFMA k-blocks of 32");
   constexpr int AP = PLANE_A ? (TM + 16) : (KMAX + 2);   // pitch: rows of A (row-major) or k-rows (plane)
   constexpr int BP = TN + 16;
@@ -344,12 +354,13 @@ proj_persist_kernel(const TI* __restrict__ A, int M, int K, int N, const float* 
   // SPLIT with bf16 A: A is exactly its first bf16 part, so one plane and three products
   constexpr bool A1_ONLY = SPLIT && sizeof(TI) == 2;
   constexpr int APL = A1_ONLY ? 1 : 3;
-  constexpr int A_FLOATS = SPLIT ? APL * TM * KP / 2 : (PLANE_A ? KMAX * AP : TM * AP);   // SPLIT: APL bf16 planes
+  constexpr int A_STAGE = SPLIT ? APL * TM * KP / 2 : (PLANE_A ? KMAX * AP : TM * AP);   // SPLIT: APL bf16 planes
+  constexpr int A_FLOATS = (NSPLIT && 3 * TM * KP / 2 > A_STAGE) ? 3 * TM * KP / 2 : A_STAGE;   // NSPLIT: + 3 planes
   constexpr int OP = TN + 4;                              // output staging pitch (channels-last out)
   constexpr int AS_FLOATS = (!OUT_SPLIT && TM * OP > A_FLOATS) ? TM * OP : A_FLOATS;  // staging reuses As
   constexpr int PF = TM * KMAX / 4 / NT;                 // float4 of A prefetched per thread
   __shared__ __attribute__((aligned(16))) float As[AS_FLOATS];
-  __shared__ __attribute__((aligned(16))) float Bs[SPLIT ? 1 : KMAX * BP];
+  __shared__ __attribute__((aligned(16))) float Bs[MSPLIT ? 1 : KMAX * BP];
   // SPLIT views: the three A planes [TM][KP] as bf16
   __bf16* const A1 = reinterpret_cast<__bf16*>(As);
   __bf16* const A2 = A1 + TM * KP;   // (SPLIT, fp32 A only)
@@ -388,8 +399,8 @@ proj_persist_kernel(const TI* __restrict__ A, int M, int K, int N, const float* 
   };
 
   // SPLIT: lane l's B fragments, column wn 32 + 16 j + l % 16, k = 32 kb + 8 (l / 16) + e
-  bf16x8 b1[SPLIT ? 2 : 1][SPLIT ? KB : 1], b2[SPLIT ? 2 : 1][SPLIT ? KB : 1], b3[SPLIT ? 2 : 1][SPLIT ? KB : 1];
-  if constexpr (SPLIT) {
+  bf16x8 b1[MSPLIT ? 2 : 1][MSPLIT ? KB : 1], b2[MSPLIT ? 2 : 1][MSPLIT ? KB : 1], b3[MSPLIT ? 2 : 1][MSPLIT ? KB : 1];
+  if constexpr (MSPLIT) {
 #pragma unroll
     for (int j = 0; j < 2; ++j) {
       const int gn = n0 + wn * 32 + j * 16 + (lane & 15);
@@ -640,7 +651,7 @@ proj_persist_kernel(const TI* __restrict__ A, int M, int K, int N, const float* 
       rowsc[2 * tid + 1] = mean;
     }
     __syncthreads();
-    if constexpr (!XG) {   // XG: the statistics only; xgate_norm applies them with the computed gate
+    if constexpr (!NSPLIT && !XG) {   // NSPLIT / XG: the statistics only; norm_split / xgate_norm apply them
 #pragma unroll
       for (int i = 0; i < PF; ++i) {
         const int f = i * NT + tid;
@@ -661,7 +672,25 @@ proj_persist_kernel(const TI* __restrict__ A, int M, int K, int N, const float* 
   };
 
   float4 pf[PF];
-  float4 pg[(NORM && !XG) ? PF : 1];
+  float4 pg[(NORM && !NSPLIT && !XG) ? PF : 1];
+  // NSPLIT without XG: the gate planes in the MFMA output layout, 4 pixels of gate channel wn 32 + 16 j + l % 16
+  // at rows (wm MI + i) 16 + 4 (l / 16) + 0..3
+  float4 pgm[(NSPLIT && !XG) ? MI : 1][2];
+  auto fetch_gm = [&](int tile) {
+    if constexpr (NSPLIT && !XG) {
+      const int m0 = tile * TM;
+#pragma unroll
+      for (int j = 0; j < 2; ++j) {
+        const int kk = wn * 32 + j * 16 + (lane & 15);
+#pragma unroll
+        for (int i = 0; i < MI; ++i) {
+          const int gm = m0 + (wm * MI + i) * 16 + (lane >> 4) * 4;   // HW % 4 == 0: the 4 pixels share a frame
+          pgm[i][j] = (kk < K && gm < M) ? ld4(Gp, (size_t(gm / HW) * K + kk) * HW + gm % HW)
+                                         : make_float4(0.f, 0.f, 0.f, 0.f);
+        }
+      }
+    }
+  };
   // XG: the tile's X rows, 16-byte pieces c = i NT + tid: row c / (KMAX / 8), channels 8 (c % (KMAX / 8)) ..
   constexpr int PX = XG ? TM * KMAX / 8 / NT : 1;
   uint4 px[PX];
@@ -711,6 +740,7 @@ proj_persist_kernel(const TI* __restrict__ A, int M, int K, int N, const float* 
       }
     }
   };
+  // XG: A <- norm(A) * act(x Wg + bg) in place for exactly this wave's elements of the MFMA output layout
   auto xgate_norm = [&]() {
     if constexpr (XG) {
 #pragma unroll
@@ -732,6 +762,52 @@ proj_persist_kernel(const TI* __restrict__ A, int M, int K, int N, const float* 
             e[q] = (ng.kind == 0 ? e[q] : fmaf((e[q] - mu) * sc, sk, bk)) * g;
           }
           *reinterpret_cast<float4*>(&As[kk * AP + r0]) = v;
+        }
+      }
+    }
+  };
+  // NSPLIT: A <- norm(A) * gate for this wave's elements (rows (wm MI + i) 16 + 4 (l / 16) + q, channels
+  // wn 32 + 16 j + l % 16: the MFMA output layout; the gate from the planes prefetched in that layout),
+  // then, once every wave has read the fp32 staging, their three bf16 parts into the planes over it (zero for
+  // channels past K, which the k-blocks still read)
+  auto norm_split = [&]() {
+    if constexpr (NSPLIT) {
+      float4 nv[MI][2];
+#pragma unroll
+      for (int j = 0; j < 2; ++j) {
+        const int kk = wn * 32 + j * 16 + (lane & 15);
+        const int kc = kk < K ? kk : 0;
+        const float sk = nss[2 * kc], bk = nss[2 * kc + 1];
+#pragma unroll
+        for (int i = 0; i < MI; ++i) {
+          const int r0 = (wm * MI + i) * 16 + (lane >> 4) * 4;
+          float4 v = *reinterpret_cast<const float4*>(&As[kc * AP + r0]);
+          float* e = &v.x;
+#pragma unroll
+          for (int q = 0; q < 4; ++q) {
+            const float g = (&pgm[i][j].x)[q];
+            const float sc = rowsc[2 * (r0 + q)], mu = rowsc[2 * (r0 + q) + 1];
+            e[q] = kk < K ? (ng.kind == 0 ? e[q] : fmaf((e[q] - mu) * sc, sk, bk)) * g : 0.0f;
+          }
+          nv[i][j] = v;
+        }
+      }
+      __syncthreads();   // every wave has read the fp32 staging the planes overwrite
+#pragma unroll
+      for (int j = 0; j < 2; ++j) {
+        const int kk = wn * 32 + j * 16 + (lane & 15);
+#pragma unroll
+        for (int i = 0; i < MI; ++i) {
+          const int r0 = (wm * MI + i) * 16 + (lane >> 4) * 4;
+#pragma unroll
+          for (int q = 0; q < 4; ++q) {
+            __bf16 x1, x2, x3;
+            split3_bf16((&nv[i][j].x)[q], x1, x2, x3);
+            const int o = (r0 + q) * KP + kk;
+            A1[o] = x1;
+            A2[o] = x2;
+            A3[o] = x3;
+          }
         }
       }
     }
@@ -768,6 +844,7 @@ proj_persist_kernel(const TI* __restrict__ A, int M, int K, int N, const float* 
     fetch(A, tile, pf);
     fetch_gates(tile);
     if constexpr (XG) fetch_x(tile);
+    else if constexpr (NSPLIT) fetch_gm(tile);
     else if (NORM) fetch(Gp, tile, pg);
   }
   for (; tile < tiles; tile = tile_of(++kt_)) {
@@ -779,9 +856,10 @@ proj_persist_kernel(const TI* __restrict__ A, int M, int K, int N, const float* 
     }
     __syncthreads();
     if constexpr (NORM) {
-      xgate_mma();
-      norm_gate(pg);
-      xgate_norm();
+      xgate_mma();    // XG: x Wg, under the statistics
+      norm_gate(pg);  // the per-pixel statistics (without NSPLIT / XG also the norm x gate in place)
+      xgate_norm();   // XG: norm x computed gate in place
+      norm_split();   // NSPLIT: norm x gate into the bf16 planes
       __syncthreads();
     }
     const int next = tile_of(kt_ + 1);
@@ -789,13 +867,14 @@ proj_persist_kernel(const TI* __restrict__ A, int M, int K, int N, const float* 
       fetch(A, next, pf);
       fetch_gates(next);
       if constexpr (XG) fetch_x(next);
+      else if constexpr (NSPLIT) fetch_gm(next);
       else if (NORM) fetch(Gp, next, pg);
     }
 
     floatx4 acc[MI][2];
 #pragma unroll
     for (int i = 0; i < MI; ++i) acc[i][0] = acc[i][1] = floatx4{0.f, 0.f, 0.f, 0.f};
-    if constexpr (SPLIT) {
+    if constexpr (MSPLIT) {
       // lane l: A rows l % 16 and B columns l % 16, k = 32 kb + 8 (l / 16) + 0..7
 #pragma unroll
       for (int kb = 0; kb < KB; ++kb) {
@@ -831,7 +910,7 @@ proj_persist_kernel(const TI* __restrict__ A, int M, int K, int N, const float* 
         }
       }
     }
-    const int kend = SPLIT ? 0 : (K + 3) / 4 * 4;
+    const int kend = MSPLIT ? 0 : (K + 3) / 4 * 4;
     for (int kk = 0; kk < kend; kk += 4) {
       const int ka = kk + (lane >> 4);
       float a[MI], b[2];
