@@ -10,7 +10,7 @@ import os
 import threading
 
 LIB_PATH = os.path.join(os.path.dirname(os.path.abspath(__file__)), "libcssm_hip.so")
-ABI_VERSION = 5   # CSSM_ABI_VERSION of the include/cssm_amd.h these bindings follow
+ABI_VERSION = 6   # CSSM_ABI_VERSION of the include/cssm_amd.h these bindings follow
 
 CSSM_OK = 0
 F32, BF16 = 0, 1
@@ -64,6 +64,9 @@ SIGNATURES = {
     "cssm_gated_gates": (ctypes.c_int, [ctypes.c_void_p, ctypes.c_int, ctypes.c_int, ctypes.c_int,
                                         ctypes.c_int, ctypes.c_int, ctypes.POINTER(GateParams),
                                         ctypes.c_float, ctypes.c_void_p, ctypes.c_void_p]),
+    "cssm_gated_gates_bwd": (ctypes.c_int, [ctypes.c_void_p, ctypes.c_int, ctypes.c_int, ctypes.c_int,
+                                            ctypes.c_int, ctypes.c_int, ctypes.POINTER(GateParams),
+                                            ctypes.c_float, ctypes.c_void_p, ctypes.c_void_p, ctypes.c_void_p]),
     "cssm_gated_scan_fwd": (ctypes.c_int, [ctypes.c_void_p, ctypes.c_void_p, ctypes.c_void_p, ctypes.c_int,
                                            ctypes.c_int, ctypes.c_int, ctypes.c_int, ctypes.c_int,
                                            ctypes.c_int, ctypes.c_void_p, ctypes.c_void_p, ctypes.c_int,

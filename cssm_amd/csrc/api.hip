@@ -119,6 +119,36 @@ int cssm_gated_gates(const float* ctx, int B, int T, int C, int H, int W, const 
   return hip_status(e, "cssm_gated_gates");
 }
 
+int cssm_gated_gates_bwd(const float* ctx, int B, int T, int C, int H, int W, const cssm_gate_params* p,
+                         float c_scale, const float* dgates, float* out, void* stream) {
+  if (!ctx || !p || !dgates || !out)
+    return fail(CSSM_ERR_NULL, "cssm_gated_gates_bwd: ctx, params, dgates and out must be non-null");
+  if (B <= 0 || T <= 0 || C <= 0 || H <= 0 || W <= 0)
+    return fail(CSSM_ERR_SHAPE, "cssm_gated_gates_bwd: B=%d T=%d C=%d H=%d W=%d", B, T, C, H, W);
+  if (p->gate_type != CSSM_GATE_DENSE && p->gate_type != CSSM_GATE_FACTORED)
+    return fail(CSSM_ERR_ARG, "cssm_gated_gates_bwd: gate_type=%d", p->gate_type);
+  if (p->activation < CSSM_ACT_SOFTPLUS || p->activation > CSSM_ACT_EXP)
+    return fail(CSSM_ERR_ARG, "cssm_gated_gates_bwd: activation=%d", p->activation);
+  const bool fac = p->gate_type == CSSM_GATE_FACTORED;
+  cssm::GateWeights w;
+  for (int i = 0; i < 3; ++i) {
+    if (!p->kernel[i] || !p->bias[i] || (fac && (!p->kernel_w[i] || !p->bias_w[i])))
+      return fail(CSSM_ERR_NULL, "cssm_gated_gates_bwd: gate %d weights missing", i);
+    w.kd[i] = p->kernel[i];
+    w.bd[i] = p->bias[i];
+    w.kw[i] = fac ? p->kernel_w[i] : nullptr;
+    w.bw[i] = fac ? p->bias_w[i] : nullptr;
+  }
+  if (!aligned(dgates, 16)) return fail(CSSM_ERR_ALIGN, "cssm_gated_gates_bwd: dgates must be 16-byte aligned");
+  const hipError_t e = cssm::launch_gated_gates_bwd(ctx, B * T, C, H, W, fac ? 1 : 0, p->activation, w, c_scale,
+                                                    reinterpret_cast<const float4*>(dgates), out,
+                                                    static_cast<hipStream_t>(stream));
+  if (e == hipErrorInvalidValue)
+    return fail(CSSM_ERR_UNSUPPORTED, "cssm_gated_gates_bwd: C=%d with %dx%d planes exceeds the staging buffer",
+                C, H, W);
+  return hip_status(e, "cssm_gated_gates_bwd");
+}
+
 int cssm_gated_scan_supported(int H, int W) { return cssm::gated_scan_has_kernel(H, W) ? 1 : 0; }
 
 int cssm_gated_scan_min_group(int H, int W) { return cssm::gated_scan_min_group(H, W); }

@@ -45,6 +45,10 @@ hipError_t launch_plane_mean(const void* x, int dtype, long long nplanes, int HW
                              hipStream_t s);
 hipError_t launch_gated_gates(const float* ctx, int BT, int C, int H, int W, int factored, int act,
                               const GateWeights& w, float c_scale, float4* gates, hipStream_t s);
+// adjoint of launch_gated_gates: out = dG (BT, 3, H*WF) dense, or the factor gradients (BT, 3, H + WF)
+hipError_t launch_gated_gates_bwd(const float* ctx, int BT, int C, int H, int W, int factored, int act,
+                                  const GateWeights& w, float c_scale, const float4* dgates, float* out,
+                                  hipStream_t s);
 // fused scan: plane sizes with a kernel, and the smallest plane group (C must be a multiple)
 bool gated_scan_has_kernel(int H, int W);
 int gated_scan_min_group(int H, int W);

@@ -110,6 +110,57 @@ __device__ __forceinline__ float gate_act(float x, int act) {
   return softplus_f(x);
 }
 
+// The 3 (H + WF) factored row / column products of one frame, written to fac
+// (g * (H + WF) + r: rows r < H, columns H + v).  Small planes (few products,
+// long C) split each product over P threads and sum the parts in LDS (part:
+// P * nv floats past fac).  Ends with a barrier.
+__device__ __forceinline__ void gate_factors(const float* cx, int C, int H, int WF, const GateWeights& gw,
+                                             float* fac) {
+  const int nv = 3 * (H + WF);
+  const int P = nv >= int(blockDim.x) ? 1 : int(blockDim.x) / nv;
+  if (P == 1) {
+    for (int idx = threadIdx.x; idx < nv; idx += blockDim.x) {
+      const int g = idx / (H + WF), r = idx % (H + WF);
+      float acc;
+      if (r < H) {
+        acc = gw.bd[g][r];
+#pragma unroll 8
+        for (int c = 0; c < C; ++c) acc = fmaf(cx[c], gw.kd[g][size_t(c) * H + r], acc);
+      } else {
+        const int v = r - H;
+        acc = gw.bw[g][v];
+#pragma unroll 8
+        for (int c = 0; c < C; ++c) acc = fmaf(cx[c], gw.kw[g][size_t(c) * WF + v], acc);
+      }
+      fac[idx] = acc;
+    }
+  } else {
+    float* part = fac + nv;   // P * nv partial sums
+    for (int q = threadIdx.x; q < nv * P; q += blockDim.x) {
+      const int idx = q % nv, pc = q / nv;
+      const int g = idx / (H + WF), r = idx % (H + WF);
+      float acc = 0.0f;
+      // (loads unrolled so several are in flight: the weights come from L2)
+      if (r < H) {
+#pragma unroll 8
+        for (int c = pc; c < C; c += P) acc = fmaf(cx[c], gw.kd[g][size_t(c) * H + r], acc);
+      } else {
+#pragma unroll 8
+        for (int c = pc; c < C; c += P) acc = fmaf(cx[c], gw.kw[g][size_t(c) * WF + (r - H)], acc);
+      }
+      part[pc * nv + idx] = acc;
+    }
+    __syncthreads();
+    for (int idx = threadIdx.x; idx < nv; idx += blockDim.x) {
+      const int g = idx / (H + WF), r = idx % (H + WF);
+      float acc = r < H ? gw.bd[g][r] : gw.bw[g][r - H];
+      for (int pc = 0; pc < P; ++pc) acc += part[pc * nv + idx];
+      fac[idx] = acc;
+    }
+  }
+  __syncthreads();
+}
+
 __global__ void __launch_bounds__(1024) gated_gates_kernel(const float* __restrict__ ctx, int C, int H, int W, int factored,
                                    int act, GateWeights gw, float c_scale, float4* __restrict__ out) {
   extern __shared__ float sm_f[];
@@ -121,51 +172,7 @@ __global__ void __launch_bounds__(1024) gated_gates_kernel(const float* __restri
   __syncthreads();
   const int nbin = H * WF;
   if (factored) {
-    // the 3 (H + WF) row / column dot products over C; small planes (few
-    // products, long C) split each over P threads and sum the parts in LDS
-    const int nv = 3 * (H + WF);
-    const int P = nv >= int(blockDim.x) ? 1 : int(blockDim.x) / nv;
-    if (P == 1) {
-      for (int idx = threadIdx.x; idx < nv; idx += blockDim.x) {
-        const int g = idx / (H + WF), r = idx % (H + WF);
-        float acc;
-        if (r < H) {
-          acc = gw.bd[g][r];
-#pragma unroll 8
-          for (int c = 0; c < C; ++c) acc = fmaf(cx[c], gw.kd[g][size_t(c) * H + r], acc);
-        } else {
-          const int v = r - H;
-          acc = gw.bw[g][v];
-#pragma unroll 8
-          for (int c = 0; c < C; ++c) acc = fmaf(cx[c], gw.kw[g][size_t(c) * WF + v], acc);
-        }
-        fac[idx] = acc;
-      }
-    } else {
-      float* part = fac + nv;   // P * nv partial sums
-      for (int q = threadIdx.x; q < nv * P; q += blockDim.x) {
-        const int idx = q % nv, pc = q / nv;
-        const int g = idx / (H + WF), r = idx % (H + WF);
-        float acc = 0.0f;
-        // (loads unrolled so several are in flight: the weights come from L2)
-        if (r < H) {
-#pragma unroll 8
-          for (int c = pc; c < C; c += P) acc = fmaf(cx[c], gw.kd[g][size_t(c) * H + r], acc);
-        } else {
-#pragma unroll 8
-          for (int c = pc; c < C; c += P) acc = fmaf(cx[c], gw.kw[g][size_t(c) * WF + (r - H)], acc);
-        }
-        part[pc * nv + idx] = acc;
-      }
-      __syncthreads();
-      for (int idx = threadIdx.x; idx < nv; idx += blockDim.x) {
-        const int g = idx / (H + WF), r = idx % (H + WF);
-        float acc = r < H ? gw.bd[g][r] : gw.bw[g][r - H];
-        for (int pc = 0; pc < P; ++pc) acc += part[pc * nv + idx];
-        fac[idx] = acc;
-      }
-    }
-    __syncthreads();
+    gate_factors(cx, C, H, WF, gw, fac);
     for (int o = threadIdx.x; o < nbin; o += blockDim.x) {
       const int u = o / WF, v = scan_col(H, W, o % WF);
       float gr[3];
@@ -187,6 +194,118 @@ __global__ void __launch_bounds__(1024) gated_gates_kernel(const float* __restri
       const float d = gate_act(gr[0], act), dd = d + 1e-8f;
       out[size_t(bt) * nbin + o] = make_float4(expf(-d), dd * gr[1], dd * 2e-7f, gr[2] * c_scale);
     }
+  }
+}
+
+// ---------------------------------------------------------------------------
+// Adjoint of the gates (what autodiff of cssm.py:536-567 gives): from dP, the
+// gradient of one bin's float4 above, the gradients of the three gate
+// pre-activations G_delta, G_B, G_C at that bin:
+//   dDelta = -exp(-Delta) dP.x + G_B dP.y + 2e-7 dP.z
+//   dG_delta = dDelta act'(G_delta),  dG_B = (Delta + 1e-8) dP.y,  dG_C = c_scale dP.w
+// with act' = sigmoid (softplus), 2 s (1 - s) (2*sigmoid), exp on [-4, 2] and 0
+// outside (bounded exp; the clip passes the gradient at its bounds).
+// dense: out (BT, 3, H*WF) = dG in natural bin order (u * WF + v).
+// factored: out (BT, 3, H + WF) = the gradients of the row and column factors,
+//   d(ctx.kh + bh)[u] = sum_v dG[u, v] (ctx.kw + bw)[v] and its column twin,
+//   in the factors' layout; each sum runs in a fixed order (no atomics).
+// The weight, bias and ctx gradients are products of this with ctx / the
+// gate kernels over frames (plain GEMMs the caller runs).
+// ---------------------------------------------------------------------------
+__device__ __forceinline__ float gate_act_grad(float x, int act) {
+  if (act == 1) {
+    const float s = 1.0f / (1.0f + expf(-x));
+    return 2.0f * s * (1.0f - s);
+  }
+  if (act == 2) return (x >= -4.0f && x <= 2.0f) ? expf(x) : 0.0f;
+  return 1.0f / (1.0f + expf(-x));                            // softplus' = sigmoid
+}
+
+__device__ __forceinline__ void gate_bin_grad(const float4 dp, const float gr[3], int act, float c_scale,
+                                              float dg[3]) {
+  const float d = gate_act(gr[0], act);
+  const float dd = fmaf(-expf(-d), dp.x, fmaf(gr[1], dp.y, 2e-7f * dp.z));
+  dg[0] = dd * gate_act_grad(gr[0], act);
+  dg[1] = (d + 1e-8f) * dp.y;
+  dg[2] = c_scale * dp.w;
+}
+
+__global__ void __launch_bounds__(1024) gated_gates_bwd_kernel(const float* __restrict__ ctx, int C, int H, int W,
+                                                               int factored, int act, GateWeights gw, float c_scale,
+                                                               const float4* __restrict__ dgates,
+                                                               float* __restrict__ out) {
+  extern __shared__ float sm_f[];
+  const int WF = W / 2 + 1;
+  const int bt = blockIdx.x;
+  const int nbin = H * WF;
+  const float4* dp = dgates + size_t(bt) * nbin;
+  if (!factored) {
+    float* cx = sm_f;
+    for (int i = threadIdx.x; i < C; i += blockDim.x) cx[i] = ctx[size_t(bt) * C + i];
+    __syncthreads();
+    float* o3 = out + size_t(bt) * 3 * nbin;
+    for (int o = threadIdx.x; o < nbin; o += blockDim.x) {
+      const int bin = (o / WF) * WF + scan_col(H, W, o % WF);
+      float gr[3];
+      for (int g = 0; g < 3; ++g) {
+        float acc = gw.bd[g][bin];
+        const float* kk = gw.kd[g] + bin;
+#pragma unroll 8
+        for (int c = 0; c < C; ++c) acc = fmaf(cx[c], kk[size_t(c) * nbin], acc);
+        gr[g] = acc;
+      }
+      float dg[3];
+      gate_bin_grad(dp[o], gr, act, c_scale, dg);
+      for (int g = 0; g < 3; ++g) o3[size_t(g) * nbin + bin] = dg[g];
+    }
+    return;
+  }
+  const int nv = 3 * (H + WF);
+  const int P = nv >= int(blockDim.x) ? 1 : int(blockDim.x) / nv;
+  float* cx = sm_f;                                  // C
+  float* fac = cx + C;                               // nv factors (+ P * nv parts while they are built)
+  float* colp = fac + nv + size_t(P) * nv;           // S * WF * 3 column partial sums
+  for (int i = threadIdx.x; i < C; i += blockDim.x) cx[i] = ctx[size_t(bt) * C + i];
+  __syncthreads();
+  gate_factors(cx, C, H, WF, gw, fac);
+  float* o3 = out + size_t(bt) * nv;
+  // rows: wave w takes rows w, w + nwaves, ...; its lanes walk the row's positions
+  const int lane = threadIdx.x & 63, wv = threadIdx.x >> 6, nw = int(blockDim.x) >> 6;
+  for (int u = wv; u < H; u += nw) {
+    float acc[3] = {0.0f, 0.0f, 0.0f};
+    for (int pos = lane; pos < WF; pos += 64) {
+      const int v = scan_col(H, W, pos);
+      float gr[3], dg[3];
+      for (int g = 0; g < 3; ++g) gr[g] = fac[g * (H + WF) + u] * fac[g * (H + WF) + H + v];
+      gate_bin_grad(dp[u * WF + pos], gr, act, c_scale, dg);
+      for (int g = 0; g < 3; ++g) acc[g] = fmaf(dg[g], fac[g * (H + WF) + H + v], acc[g]);
+    }
+    for (int g = 0; g < 3; ++g)
+      for (int off = 32; off > 0; off >>= 1) acc[g] += __shfl_xor(acc[g], off, 64);
+    if (lane == 0)
+      for (int g = 0; g < 3; ++g) o3[g * (H + WF) + u] = acc[g];
+  }
+  // columns: thread (s, pos) sums rows s, s + S, ... of position pos; the S parts
+  // of each column then add up in order of s
+  const int S = int(blockDim.x) / WF;
+  if (int(threadIdx.x) < S * WF) {
+    const int pos = threadIdx.x % WF, s = threadIdx.x / WF;
+    const int v = scan_col(H, W, pos);
+    float acc[3] = {0.0f, 0.0f, 0.0f};
+    for (int u = s; u < H; u += S) {
+      float gr[3], dg[3];
+      for (int g = 0; g < 3; ++g) gr[g] = fac[g * (H + WF) + u] * fac[g * (H + WF) + H + v];
+      gate_bin_grad(dp[u * WF + pos], gr, act, c_scale, dg);
+      for (int g = 0; g < 3; ++g) acc[g] = fmaf(dg[g], fac[g * (H + WF) + u], acc[g]);
+    }
+    for (int g = 0; g < 3; ++g) colp[(size_t(s) * WF + v) * 3 + g] = acc[g];
+  }
+  __syncthreads();
+  for (int q = threadIdx.x; q < 3 * WF; q += blockDim.x) {
+    const int g = q / WF, v = q % WF;
+    float acc = 0.0f;
+    for (int s = 0; s < S; ++s) acc += colp[(size_t(s) * WF + v) * 3 + g];
+    o3[g * (H + WF) + H + v] = acc;
   }
 }
 
@@ -276,6 +395,23 @@ hipError_t launch_gated_gates(const float* ctx, int BT, int C, int H, int W, int
   if (shm > 64 * 1024) return hipErrorInvalidValue;
   hipLaunchKernelGGL(gated_gates_kernel, dim3(BT), dim3(NT), shm, s, ctx, C, H, W, factored, act, w,
                      c_scale, gates);
+  return hipGetLastError();
+}
+
+hipError_t launch_gated_gates_bwd(const float* ctx, int BT, int C, int H, int W, int factored, int act,
+                                  const GateWeights& w, float c_scale, const float4* dgates, float* out,
+                                  hipStream_t s) {
+  const int WF = W / 2 + 1;
+  const int nv = 3 * (H + WF);
+  constexpr int NT = 1024;
+  if (factored && WF > NT) return hipErrorInvalidValue;
+  const int P = nv >= NT ? 1 : NT / nv;
+  const int S = NT / WF;
+  const size_t shm = factored ? (size_t(C) + size_t(nv) * (1 + P) + size_t(S) * WF * 3) * sizeof(float)
+                              : size_t(C) * sizeof(float);
+  if (shm > 64 * 1024) return hipErrorInvalidValue;
+  hipLaunchKernelGGL(gated_gates_bwd_kernel, dim3(BT), dim3(NT), shm, s, ctx, C, H, W, factored, act, w,
+                     c_scale, dgates, out);
   return hipGetLastError();
 }
 

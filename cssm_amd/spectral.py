@@ -130,6 +130,27 @@ def gated_gates(ctx: torch.Tensor, params: Dict, H: int, W: int, gate_type: str 
     return out
 
 
+def gated_gates_backward(ctx: torch.Tensor, params: Dict, H: int, W: int, dgates: torch.Tensor,
+                         gate_type: str = "dense", activation: str = "softplus",
+                         c_scale: float = 1.0) -> torch.Tensor:
+    """Adjoint of :func:`gated_gates` (autodiff of cssm.py:536-567): from ``dgates``, the gradient
+    of the (B, T, H, Wf, 4) planes, the gradients of the gate pre-activations, float32
+    (B, T, 3, H * Wf) for dense gates (natural bin order) or (B, T, 3, H + Wf) for factored ones
+    (row factors, then column factors), for delta / B / C."""
+    _dev(ctx, "ctx", torch.float32)
+    _dev(dgates, "dgates", torch.float32)
+    B, T, C = ctx.shape
+    Wf = W // 2 + 1
+    if tuple(dgates.shape) != (B, T, H, Wf, 4):
+        raise ValueError(f"dgates {tuple(dgates.shape)} != {(B, T, H, Wf, 4)}")
+    n = H + Wf if gate_type == "factored" else H * Wf
+    out = torch.empty((B, T, 3, n), dtype=torch.float32, device=ctx.device)
+    s = gate_params_struct(params, gate_type, activation)
+    _lib.call("cssm_gated_gates_bwd", ctx.data_ptr(), B, T, C, H, W, s, float(c_scale), dgates.data_ptr(),
+              out.data_ptr(), _stream())
+    return out
+
+
 def gated_scan(u: torch.Tensor, z: torch.Tensor, gates: torch.Tensor, khat: torch.Tensor,
                u_silu: bool = False, z_silu: bool = False,
                out: Optional[torch.Tensor] = None) -> torch.Tensor:

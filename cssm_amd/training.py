@@ -258,7 +258,8 @@ class _GatedInScanFn(torch.autograd.Function):
     kernels end to end: in_proj stores the pre-activations and takes ctx as the mean of their
     SiLU in the same pass (CSSM_PROJ_STORE_PRE_CTX_SILU); the scan applies both SiLUs on load.
     Backward: rfft2 of SiLU(x_main) and of dy * SiLU(z) (cssm_rfft2_ex), the reverse recurrence
-    (cssm_gated_scan_bwd), the gate / K_hat construction differentiated by torch on its small
+    (cssm_gated_scan_bwd), the gates' adjoint (cssm_gated_gates_bwd) with the gate projections'
+    gradients as GEMMs over frames, K_hat's construction differentiated by torch on its small
     tensors, then cssm_irfft2_ex writes the two pre-activation gradients straight into one
     plane-major (F, 2C, HW) tensor: dz = irfft2(Y) * dy * SiLU'(z) and
     dx_main = (irfft2(dU) + dctx / HW) * SiLU'(x_main), the ctx term being the spatial mean's
@@ -271,10 +272,9 @@ class _GatedInScanFn(torch.autograd.Function):
         F, HW = B * T, H * W
         xm, z, cx = S.proj_in(x2, w_in, b_in, F, HW, want_ctx=True, out_dtype=torch.float32, ctx_of_silu=True)
         c_scale = S.scan_c_scale(H, W)
-        gates = gate_planes(cx.view(B, T, Ci), rebuild(list(gate_params)), H, W, gate_type, activation, c_scale)
-        khat = khat_planes(kernel, H, W, rho)
-        y = S.gated_scan(xm.view(B, T, Ci, H, W), z.view(B, T, Ci, H, W), gates.contiguous(), khat.contiguous(),
-                         u_silu=True, z_silu=True)
+        gates = S.gated_gates(cx.view(B, T, Ci), rebuild(list(gate_params)), H, W, gate_type, activation, c_scale)
+        khat = S.spectral_kernel(kernel, H, W, rho, goom_floor=True, scan_order=True)
+        y = S.gated_scan(xm.view(B, T, Ci, H, W), z.view(B, T, Ci, H, W), gates, khat, u_silu=True, z_silu=True)
         ctx.save_for_backward(x2, w_in, xm, z, cx, kernel, *gate_params)
         ctx.meta = meta
         return y
@@ -287,24 +287,35 @@ class _GatedInScanFn(torch.autograd.Function):
         K = x2.shape[1]
         dy = dy.contiguous().view(F, Ci, HW)
         c_scale = S.scan_c_scale(H, W)
+        gps = rebuild(list(gate_params))
+        cx3 = cx.view(B, T, Ci)
         with torch.enable_grad():
-            cx_l = cx.detach().requires_grad_(True)
-            gp_l = [g.detach().requires_grad_(True) for g in gate_params]
             k_l = kernel.detach().requires_grad_(True)
-            gates = gate_planes(cx_l.view(B, T, Ci), rebuild(gp_l), H, W, gate_type, activation, c_scale)
             khat = khat_planes(k_l, H, W, rho)
-        gates_c, khat_c = gates.detach().contiguous(), khat.detach().contiguous()
+        gates_c = S.gated_gates(cx3, gps, H, W, gate_type, activation, c_scale)
         uspec = S.rfft2_ex(xm, H, W, x_silu=True)
         dspec = S.rfft2_ex(dy, H, W, a=z, a_silu=True)
         yspec = torch.empty_like(uspec)
         sdu = torch.empty_like(uspec)
         dgates = torch.empty_like(gates_c)
         dkh = torch.empty((B, Ci, H, Wf), dtype=torch.complex64, device=dy.device)
-        S.gated_scan_bwd_bins(uspec, dspec, gates_c, khat_c, B, T, Ci, H, W, c_scale, yspec, sdu, dgates, dkh)
-        del uspec, dspec
-        grads = torch.autograd.grad([gates, khat], [cx_l] + gp_l + [k_l], [dgates, dkh.sum(dim=0)],
-                                    allow_unused=True)
-        dcx = grads[0]
+        S.gated_scan_bwd_bins(uspec, dspec, gates_c, khat.detach().contiguous(), B, T, Ci, H, W, c_scale, yspec,
+                              sdu, dgates, dkh)
+        del uspec, dspec, gates_c
+        (dk,) = torch.autograd.grad([khat], [k_l], [dkh.sum(dim=0)])
+        # the gate pre-activations' gradients (cssm_gated_gates_bwd), then the projections' as GEMMs
+        # over frames: every gate kernel side by side is one (Ci, 3 n) matrix, the layout of dfac
+        dfac = S.gated_gates_backward(cx3, gps, H, W, dgates, gate_type, activation, c_scale).view(F, -1)
+        del dgates
+        wcat = torch.cat(gate_params[0::2], dim=1)
+        dcx = dfac @ wcat.t()
+        dwcat = cx.view(F, Ci).t() @ dfac
+        dbcat = dfac.sum(dim=0)
+        gp_grads, off = [], 0
+        for kp in gate_params[0::2]:
+            n = kp.shape[1]
+            gp_grads += [dwcat[:, off:off + n], dbcat[off:off + n]]
+            off += n
         dxz = torch.empty((F, 2 * Ci, HW), dtype=torch.float32, device=dy.device)
         # the bias gradient from the plane sums the inverse transforms take while storing
         sums = (torch.empty((2, F, Ci), dtype=torch.float32, device=dy.device)
@@ -316,8 +327,6 @@ class _GatedInScanFn(torch.autograd.Function):
         dx = S.proj_out(dxz, w_in.t().contiguous(), w_in.new_zeros(K), out_dtype=torch.float32)
         dw = torch.bmm(dxz, x2.view(F, HW, K)).sum(dim=0).t()
         db = sums.sum(dim=1).reshape(-1) if sums is not None else dxz.sum(dim=(0, 2))
-        gp_grads = [g if g is not None else torch.zeros_like(p) for g, p in zip(grads[1:-1], gate_params)]
-        dk = grads[-1] if grads[-1] is not None else torch.zeros_like(kernel)
         return (dx, dw, db, dk, None, *gp_grads)
 
 

@@ -32,8 +32,9 @@ extern "C" {
 /* 3: K_hat's scan layout (cssm_spectral_kernel scan_order = 1) pairs rows at 128 x 128
  *    (cssm_gated_scan_khat_order).
  * 4: scan_variant arguments of the GDN delta-rule entry points.
- * 5: cssm_im2col_same, cssm_gdn_proj_out_xgate. */
-#define CSSM_ABI_VERSION 5
+ * 5: cssm_im2col_same, cssm_gdn_proj_out_xgate.
+ * 6: cssm_gated_gates_bwd. */
+#define CSSM_ABI_VERSION 6
 
 typedef enum cssm_status {
   CSSM_OK = 0,
@@ -137,6 +138,27 @@ int cssm_plane_mean(const void* x, int dtype, long long nplanes, int H, int W, i
  */
 int cssm_gated_gates(const float* ctx, int B, int T, int C, int H, int W,
                      const cssm_gate_params* params, float c_scale, float* gates, void* stream);
+
+/*
+ * Adjoint of cssm_gated_gates for training: what autodiff of cssm.py:536-567
+ * (the gate projections, the activation and the GOOM shifts) hands back for
+ * the gate pre-activations, given dgates (B, T, H, Wf, 4) float32, the
+ * gradient of the gates output (same layout).  Per bin, with Delta = act(G_delta):
+ *   dG_delta = (-exp(-Delta) dg0 + G_B dg1 + 2e-7 dg2) act'(G_delta)
+ *   dG_B = (Delta + 1e-8) dg1,  dG_C = c_scale dg3
+ * out, float32:
+ *   dense:    (B, T, 3, H * Wf), dG of delta / B / C at bin u * Wf + v
+ *             (natural column order);
+ *   factored: (B, T, 3, H + Wf), the gradients of the row factors
+ *             ctx . kernel + bias (first H) and the column factors
+ *             ctx . kernel_w + bias_w (last Wf), each a sum in a fixed order.
+ * The kernel, bias and ctx gradients are then GEMMs of out with ctx and the
+ * gate kernels over the B*T frames (no per-call state; deterministic).
+ * Same params and c_scale as the forward call.
+ */
+int cssm_gated_gates_bwd(const float* ctx, int B, int T, int C, int H, int W,
+                         const cssm_gate_params* params, float c_scale, const float* dgates, float* out,
+                         void* stream);
 
 /*
  * Fused spectral scan of GatedCSSM for one layer call:

@@ -33,7 +33,7 @@ def test_library_exports_every_declared_symbol():
 def test_abi_version_and_errors_without_gpu():
     from cssm_amd import _lib
     lib = _lib.load()
-    assert lib.cssm_abi_version() == _lib.ABI_VERSION == 5
+    assert lib.cssm_abi_version() == _lib.ABI_VERSION == 6
     assert lib.cssm_strerror(-1) == b"null pointer argument"
     # argument validation happens before any GPU work
     st = lib.cssm_gated_scan_fwd(None, None, None, 0, 1, 1, 1, 8, 8, None, None, 0, 0, None)
@@ -77,6 +77,23 @@ def test_abi_version_and_errors_without_gpu():
     assert st == -5
     st = lib.cssm_gdn_proj_out_xgate(p, 0, None, 2, 1024, 64, 64, 1, None, None, p, p, 1, p, p, p, 1, None)
     assert st == -1
+    # the gates' adjoint: pointers, gate type, weights and alignment checked before any GPU work
+    gp = _lib.GateParams()
+    gp.gate_type, gp.activation = _lib.GATE_FACTORED, _lib.ACT_SOFTPLUS
+    for i in range(3):
+        gp.kernel[i] = gp.bias[i] = gp.kernel_w[i] = gp.bias_w[i] = p
+    st = lib.cssm_gated_gates_bwd(p, 1, 1, 8, 8, 8, ctypes.byref(gp), 1.0, p, None, None)
+    assert st == -1 and b"non-null" in lib.cssm_last_error()
+    st = lib.cssm_gated_gates_bwd(p, 1, 1, 8, 8, 8, ctypes.byref(gp), 1.0, p + 4, p, None)
+    assert st == -5
+    st = lib.cssm_gated_gates_bwd(p, 1, 0, 8, 8, 8, ctypes.byref(gp), 1.0, p, p, None)
+    assert st == -2
+    gp.bias_w[1] = None
+    st = lib.cssm_gated_gates_bwd(p, 1, 1, 8, 8, 8, ctypes.byref(gp), 1.0, p, p, None)
+    assert st == -1 and b"gate 1" in lib.cssm_last_error()
+    gp.gate_type = 7
+    st = lib.cssm_gated_gates_bwd(p, 1, 1, 8, 8, 8, ctypes.byref(gp), 1.0, p, p, None)
+    assert st == -4 and b"gate_type" in lib.cssm_last_error()
 
 
 @pytest.mark.parametrize("H", [4, 8, 14, 32, 64, 128])

@@ -69,6 +69,60 @@ def test_scan_vjp_matches_float64_reference(mods, shape):
         assert rel_err(gn, rn) <= TOL, name
 
 
+# (gate_type, activation, B, T, C, H, W): C = 64 at 128 x 128 is the C2 layer's frame; small
+# planes split each factored product over many threads, 7 x 7 has no Nyquist column
+GATE_BWD_CASES = [("factored", "softplus", 2, 3, 64, 128, 128), ("factored", "sigmoid", 3, 2, 16, 8, 8),
+                  ("factored", "exp", 2, 2, 32, 32, 32), ("factored", "softplus", 1, 3, 8, 7, 7),
+                  ("dense", "exp", 2, 2, 8, 16, 16), ("dense", "softplus", 1, 3, 12, 7, 7),
+                  ("dense", "sigmoid", 1, 2, 4, 64, 64)]
+
+
+@pytest.mark.parametrize("gate_type,act,B,T,C,H,W", GATE_BWD_CASES,
+                         ids=[f"{c[0]}_{c[1]}_{c[5]}x{c[6]}" for c in GATE_BWD_CASES])
+def test_gated_gates_backward_matches_float64_autograd(mods, gate_type, act, B, T, C, H, W):
+    """cssm_gated_gates_bwd against float64 autograd of the gate construction (cssm.py:536-567,
+    restated by the oracle's _dense / _gate_act): the gradients of the row / column factors
+    (factored) or of the per-bin pre-activations (dense), given a random gradient of the planes."""
+    _, S, _ = mods
+    print_case(test="gates_bwd", gate_type=gate_type, act=act, shape=(B, T, C, H, W))
+    rng = np.random.default_rng(43)
+    Wf = W // 2 + 1
+    cols = np.array(S.scan_col_order(H, W))
+    cs = S.scan_c_scale(H, W)
+    ctx = rng.standard_normal((B, T, C))
+    names = ("delta_proj", "B_proj", "C_proj")
+    if gate_type == "factored":
+        parts = {f"{n}_{a}": (C, H if a == "h" else Wf) for n in names for a in ("h", "w")}
+    else:
+        parts = {n: (C, H * Wf) for n in names}
+    p = {k: {"kernel": rng.standard_normal(sh) / np.sqrt(C), "bias": 0.5 * rng.standard_normal(sh[1])}
+         for k, sh in parts.items()}
+    pt = {k: {kk: torch.from_numpy(vv) for kk, vv in v.items()} for k, v in p.items()}
+    ct = torch.from_numpy(ctx)
+    if gate_type == "factored":
+        leaves = [P._dense(ct, pt[f"{n}_{a}"]).requires_grad_(True) for n in names for a in ("h", "w")]
+        G = [leaves[2 * i][..., :, None] * leaves[2 * i + 1][..., None, :] for i in range(3)]
+    else:
+        leaves = [P._dense(ct, pt[n]).requires_grad_(True) for n in names]
+        G = [g.reshape(B, T, H, Wf) for g in leaves]
+    d = P._gate_act(G[0], act)
+    planes = torch.stack([torch.exp(-d), (d + 1e-8) * G[1], 2e-7 * (d + 1e-8), G[2] * cs], -1)
+    dp = rng.standard_normal((B, T, H, Wf, 4))
+    refs = torch.autograd.grad(planes, leaves, torch.from_numpy(dp))
+    ref = torch.cat([r.reshape(B, T, -1) for r in refs], dim=-1).numpy()
+
+    dev = {k: {kk: torch.from_numpy(vv).to("cuda", torch.float32) for kk, vv in v.items()} for k, v in p.items()}
+    cd = torch.from_numpy(ctx).to("cuda", torch.float32)
+    dgates = torch.from_numpy(np.ascontiguousarray(dp[:, :, :, cols])).to("cuda", torch.float32)
+    got = S.gated_gates_backward(cd, dev, H, W, dgates, gate_type, act, cs)
+    torch.cuda.synchronize()
+    assert got.shape == (B, T, 3, H + Wf if gate_type == "factored" else H * Wf)
+    assert rel_err(_np(got).reshape(B, T, -1), ref) <= TOL
+    # the forward of the same parameters, for the same planes
+    fwd = S.gated_gates(cd, dev, H, W, gate_type, act, cs)
+    assert rel_err(_np(fwd), planes.detach().numpy()[:, :, :, cols]) <= TOL
+
+
 LAYER_CASES = [
     ("factored_16", (2, 3, 16, 16, 8), dict(channels=8, kernel_size=5, gate_type="factored", short_conv_size=0,
                                             short_conv_spatial_size=0)),
@@ -89,6 +143,9 @@ LAYER_CASES = [
     ("factored_4x4_expand2_fused_node", (3, 2, 4, 4, 8), dict(channels=8, expand=2, kernel_size=1,
                                                                gate_type="factored", gate_activation="sigmoid",
                                                                short_conv_size=0, short_conv_spatial_size=0)),
+    ("factored_32_exp_fused_node", (2, 3, 32, 32, 8), dict(channels=8, kernel_size=7, gate_type="factored",
+                                                            gate_activation="exp", short_conv_size=0,
+                                                            short_conv_spatial_size=0)),
 ]
 
 
