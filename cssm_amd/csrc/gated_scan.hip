@@ -313,16 +313,23 @@ gated_scan_pow2(const ScanArgs a) {
 // to float from a double-precision series); the trivial ones (1, -1, +-i)
 // fold into adds and swaps.
 // ---------------------------------------------------------------------------
+// (at least 4 waves per SIMD below 8 x 8; from 8 x 8 up the column pass's registers would spill
+// under that bound, so the compiler may take up to 256)
 template <int H, int W, class IO>
-__global__ void __launch_bounds__((SmallGeom<H, W>::NT), (512 / SmallGeom<H, W>::NT))
+__global__ void __launch_bounds__((SmallGeom<H, W>::NT), (H >= 8 ? 2 : 512 / SmallGeom<H, W>::NT))
 gated_scan_small(const ScanArgs a, long long P) {
   using G = SmallGeom<H, W>;
   constexpr int WF = G::WF, HW = G::HW, NT = G::NT, NP = G::NP;
-  constexpr int NE = (NP * HW + NT - 1) / NT;   // plane elements per thread
-  constexpr int LB = NE;                         // all of a thread's loads in flight at once
+  constexpr int NE = (NP * HW + NT - 1) / NT;   // plane elements per thread (element path)
+  // vector path: a group inside one batch element is one contiguous run of NP H W elements;
+  // when its start is 4-element aligned it moves as NV 4-element vectors, NEV per thread
+  constexpr bool VEC_OK = (NP * HW) % 4 == 0;
+  constexpr int NV = NP * HW / 4, NEV = (NV + NT - 1) / NT;
+  constexpr bool GATES_EARLY = H < 8 && H != 4;
   static_assert(H < 128 && W < 128, "per-bin planes of these sizes are in natural column order");
   using TE = typename IO::T;
-  __shared__ float xs[NP * HW];          // u_t, then y_t
+  using V4 = typename IO::V4;
+  __shared__ __attribute__((aligned(16))) float xs[NP * HW];   // u_t, then y_t
   __shared__ float2 rs[NP * G::PS];      // row spectra, then the inverse column output
   __shared__ long long base_u[NP];       // element offset of plane pl at t = 0: (b T C + c) HW
   __shared__ int gate_b[NP];             // batch index of plane pl (-1: beyond P)
@@ -340,6 +347,9 @@ gated_scan_small(const ScanArgs a, long long P) {
   const TE* __restrict__ zp = static_cast<const TE*>(a.z);
   TE* __restrict__ yp = static_cast<TE*>(a.y);
   const size_t tstride = size_t(C) * HW;   // one time step
+  constexpr unsigned VA = unsigned(sizeof(V4)) - 1u;
+  const bool ptr_ok = ((reinterpret_cast<uintptr_t>(up) | reinterpret_cast<uintptr_t>(zp) |
+                        reinterpret_cast<uintptr_t>(yp)) & VA) == 0;
 
   // this thread's column (pl, v) and the state of its H bins
   const int cpl = tid / WF, cv = tid % WF;
@@ -350,24 +360,66 @@ gated_scan_small(const ScanArgs a, long long P) {
   __syncthreads();
   // all planes of the group in one batch element: one contiguous run per step
   const bool contig = gate_b[0] >= 0 && gate_b[NP - 1] == gate_b[0];
+  const int bcol = has_col ? gate_b[cpl] : -1;
+  const int ccol = int((p0 + (has_col ? cpl : 0)) % C);
 
   for (int t = 0; t < T; ++t) {
     // the element offsets of the load / store loops are rebuilt every step
     // (cheap) instead of being hoisted into registers for the whole launch
     int tl = tid;
     asm volatile("" : "+v"(tl));
-    // load u_t (act), doubled: the recurrence runs on 2U as in the power-of-two
-    // kernel; the thread's loads go out in batches of LB before they are used.
-    // A group inside one batch element is one contiguous run of planes.
     const long long base0 = base_u[0] + (long long)t * tstride;
+    const bool vec = VEC_OK && contig && ptr_ok && (base0 & 3) == 0;   // uniform over the group
+    // The step's global loads are issued before any of them is used: u_t (doubled, act
+    // applied: the recurrence runs on 2U as in the power-of-two kernel), on the vector path
+    // z_t (read when y_t is stored), and the gates and K_hat of this thread's column (read
+    // after its forward DFT) either here or after the row pass (GATES_EARLY: measured faster
+    // at 7 x 7, slower at 4 x 4 and 14 x 14), so one memory latency per step is exposed
+    // instead of three.
+    float4 gq[H];
+    float2 kq[H];
+    auto load_gates = [&]() {
+      if (bcol >= 0) {
+        const float4* gp = a.gates + (size_t(bcol) * T + t) * (H * WF) + cv;
+        const float2* kp = a.khat + size_t(ccol) * (H * WF) + cv;
 #pragma unroll
-    for (int k0 = 0; k0 < NE; k0 += LB) {
-      float v[LB];
+        for (int u = 0; u < H; ++u) {
+          gq[u] = gp[u * WF];
+          kq[u] = kp[u * WF];
+        }
+      }
+    };
+    if constexpr (GATES_EARLY) load_gates();
+    V4 zv[NEV];
+    if (vec) {
+      const V4* u4 = reinterpret_cast<const V4*>(up + base0);
+      const V4* z4 = reinterpret_cast<const V4*>(zp + base0);
+      V4 uv[NEV];
 #pragma unroll
-      for (int k = 0; k < LB; ++k) {
-        const int e = (k0 + k) * NT + tl;
+      for (int k = 0; k < NEV; ++k) {
+        const int e = k * NT + tl;
+        if (k * NT + NT <= NV || e < NV) uv[k] = u4[e];
+      }
+#pragma unroll
+      for (int k = 0; k < NEV; ++k) {
+        const int e = k * NT + tl;
+        if (k * NT + NT <= NV || e < NV) zv[k] = z4[e];
+      }
+#pragma unroll
+      for (int k = 0; k < NEV; ++k) {
+        const int e = k * NT + tl;
+        if (k * NT + NT <= NV || e < NV) {
+          const float4 f = act4(IO::to_f4(uv[k]), a.u_act);
+          *reinterpret_cast<float4*>(xs + 4 * e) = make_float4(2.0f * f.x, 2.0f * f.y, 2.0f * f.z, 2.0f * f.w);
+        }
+      }
+    } else {
+      float v[NE];
+#pragma unroll
+      for (int k = 0; k < NE; ++k) {
+        const int e = k * NT + tl;
         v[k] = 0.0f;
-        if (k0 + k < NE && e < NP * HW) {
+        if (e < NP * HW) {
           if (contig) {
             v[k] = IO::to_f(up[size_t(base0 + e)]);
           } else {
@@ -377,9 +429,9 @@ gated_scan_small(const ScanArgs a, long long P) {
         }
       }
 #pragma unroll
-      for (int k = 0; k < LB; ++k) {
-        const int e = (k0 + k) * NT + tl;
-        if (k0 + k < NE && e < NP * HW) xs[e] = 2.0f * (a.u_act == 1 ? silu_f(v[k]) : v[k]);
+      for (int k = 0; k < NE; ++k) {
+        const int e = k * NT + tl;
+        if (e < NP * HW) xs[e] = 2.0f * (a.u_act == 1 ? silu_f(v[k]) : v[k]);
       }
     }
     __syncthreads();
@@ -388,20 +440,17 @@ gated_scan_small(const ScanArgs a, long long P) {
       small_row_r2c<W>(xs + j * W, rs + (j / H) * G::PS + (j % H) * G::RSP);   // row h of plane pl: j = pl H + h
     }
     __syncthreads();
+    if constexpr (!GATES_EARLY) load_gates();
     // columns: forward DFT over h, the recurrence on the H bins, inverse DFT over u
     if (has_col) {
-      const int b = gate_b[cpl];
       float2 r[H];
 #pragma unroll
       for (int h = 0; h < H; ++h) r[h] = rs[cpl * G::PS + h * G::RSP + cv];
       float2 sv[H];
       dft_sym<H, false>(r, sv);
-      if (b >= 0) {
-        const int c = int((p0 + cpl) % C);
-        const float4* gq = a.gates + (size_t(b) * T + t) * (H * WF) + cv;
-        const float2* kq = a.khat + size_t(c) * (H * WF) + cv;
+      if (bcol >= 0) {
 #pragma unroll
-        for (int u = 0; u < H; ++u) sv[u] = scan_bin(st[u], sv[u], gq[u * WF], kq[u * WF]);
+        for (int u = 0; u < H; ++u) sv[u] = scan_bin(st[u], sv[u], gq[u], kq[u]);
       } else {
 #pragma unroll
         for (int u = 0; u < H; ++u) sv[u] = make_float2(0.f, 0.f);
@@ -416,15 +465,25 @@ gated_scan_small(const ScanArgs a, long long P) {
       small_row_c2r<W>(rs + (j / H) * G::PS + (j % H) * G::RSP, xs + j * W);
     }
     __syncthreads();
-    // x z_gate, store y_t (z loads in batches, as for u)
+    // x z_gate, store y_t
+    if (vec) {
+      V4* y4 = reinterpret_cast<V4*>(yp + base0);
 #pragma unroll
-    for (int k0 = 0; k0 < NE; k0 += LB) {
-      float zg[LB];
+      for (int k = 0; k < NEV; ++k) {
+        const int e = k * NT + tl;
+        if (k * NT + NT <= NV || e < NV) {
+          const float4 yv = *reinterpret_cast<const float4*>(xs + 4 * e);
+          const float4 g = act4(IO::to_f4(zv[k]), a.z_act);
+          y4[e] = IO::from_f4(make_float4(yv.x * g.x, yv.y * g.y, yv.z * g.z, yv.w * g.w));
+        }
+      }
+    } else {
+      float zg[NE];
 #pragma unroll
-      for (int k = 0; k < LB; ++k) {
-        const int e = (k0 + k) * NT + tl;
+      for (int k = 0; k < NE; ++k) {
+        const int e = k * NT + tl;
         zg[k] = 0.0f;
-        if (k0 + k < NE && e < NP * HW) {
+        if (e < NP * HW) {
           if (contig) {
             zg[k] = IO::to_f(zp[size_t(base0 + e)]);
           } else {
@@ -434,9 +493,9 @@ gated_scan_small(const ScanArgs a, long long P) {
         }
       }
 #pragma unroll
-      for (int k = 0; k < LB; ++k) {
-        const int e = (k0 + k) * NT + tl;
-        if (k0 + k >= NE || e >= NP * HW) continue;
+      for (int k = 0; k < NE; ++k) {
+        const int e = k * NT + tl;
+        if (e >= NP * HW) continue;
         const float g = a.z_act == 1 ? silu_f(zg[k]) : zg[k];
         if (contig) {
           yp[size_t(base0 + e)] = IO::from_f(xs[e] * g);

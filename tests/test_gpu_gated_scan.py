@@ -157,6 +157,11 @@ SCAN_CASES = [
     # elements and the last group is partial
     (3, 2, 20, 14, 14), (2, 3, 40, 7, 7), (1, 1, 8, 12, 12), (2, 2, 5, 5, 5), (1, 3, 33, 15, 15),
     (2, 2, 3, 9, 9), (1, 2, 70, 6, 6), (2, 1, 4, 3, 3),
+    # groups inside one batch element move as 4-element vectors when their start is aligned:
+    # every group at 7 x 7 / C = 128 over three steps; at 14 x 14 / C = 40 the groups alternate
+    # between one batch element and two; at 3 x 3 / C = 301 some groups lie in one batch
+    # element but start at an odd element (element path)
+    (2, 3, 128, 7, 7), (1, 2, 40, 14, 14), (2, 2, 301, 3, 3),
 ]
 
 
@@ -196,7 +201,8 @@ def test_gated_scan_goom_floor_zero_inputs(S, H):
 
 
 @pytest.mark.parametrize("B,T,C,H,W", [(2, 4, 8, 32, 32), (1, 3, 2, 128, 128), (2, 2, 16, 16, 16),
-                                       (2, 1, 48, 14, 14), (2, 2, 24, 7, 7)])
+                                       (2, 1, 48, 14, 14), (2, 2, 24, 7, 7), (2, 2, 128, 7, 7),
+                                       (1, 2, 170, 4, 4)])
 def test_gated_scan_bf16_io(S, B, T, C, H, W):
     print_case(test="gated_scan_bf16", B=B, T=T, C=C, H=H, W=W)
     rng = np.random.default_rng(99)
