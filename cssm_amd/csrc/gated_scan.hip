@@ -314,9 +314,11 @@ gated_scan_pow2(const ScanArgs a) {
 // fold into adds and swaps.
 // ---------------------------------------------------------------------------
 // (at least 4 waves per SIMD below 8 x 8; from 8 x 8 up the column pass's registers would spill
-// under that bound, so the compiler may take up to 256)
-template <int H, int W, class IO>
-__global__ void __launch_bounds__((SmallGeom<H, W>::NT), (H >= 8 ? 2 : 512 / SmallGeom<H, W>::NT))
+// under that bound, so the compiler may take up to 256, or 168 for 3 waves at T = 1 up to 14 x 14)
+// ONE (T = 1): the state enters at zero and is never read again, so h = V: no state registers,
+// no K_hat loads and no decay (A h = 0 exactly: A is finite), the same results as the general form.
+template <int H, int W, class IO, bool ONE>
+__global__ void __launch_bounds__((SmallGeom<H, W>::NT), (H >= 8 ? (ONE && H <= 14 ? 3 : 2) : 512 / SmallGeom<H, W>::NT))
 gated_scan_small(const ScanArgs a, long long P) {
   using G = SmallGeom<H, W>;
   constexpr int WF = G::WF, HW = G::HW, NT = G::NT, NP = G::NP;
@@ -354,9 +356,9 @@ gated_scan_small(const ScanArgs a, long long P) {
   // this thread's column (pl, v) and the state of its H bins
   const int cpl = tid / WF, cv = tid % WF;
   const bool has_col = tid < G::NCJ;
-  float2 st[H];
+  float2 st[ONE ? 1 : H];
 #pragma unroll
-  for (int u = 0; u < H; ++u) st[u] = make_float2(0.f, 0.f);
+  for (int u = 0; u < (ONE ? 1 : H); ++u) st[u] = make_float2(0.f, 0.f);
   __syncthreads();
   // all planes of the group in one batch element: one contiguous run per step
   const bool contig = gate_b[0] >= 0 && gate_b[NP - 1] == gate_b[0];
@@ -377,15 +379,21 @@ gated_scan_small(const ScanArgs a, long long P) {
     // at 7 x 7, slower at 4 x 4 and 14 x 14), so one memory latency per step is exposed
     // instead of three.
     float4 gq[H];
-    float2 kq[H];
+    float2 kq[ONE ? 1 : H];
     auto load_gates = [&]() {
       if (bcol >= 0) {
         const float4* gp = a.gates + (size_t(bcol) * T + t) * (H * WF) + cv;
         const float2* kp = a.khat + size_t(ccol) * (H * WF) + cv;
 #pragma unroll
         for (int u = 0; u < H; ++u) {
-          gq[u] = gp[u * WF];
-          kq[u] = kp[u * WF];
+          if constexpr (ONE) {
+            // the decay component is not read: the input gain, floor term and readout gain only
+            const float* g3 = reinterpret_cast<const float*>(gp + u * WF) + 1;
+            gq[u] = make_float4(0.0f, g3[0], g3[1], g3[2]);
+          } else {
+            gq[u] = gp[u * WF];
+            kq[u] = kp[u * WF];
+          }
         }
       }
     };
@@ -450,7 +458,15 @@ gated_scan_small(const ScanArgs a, long long P) {
       dft_sym<H, false>(r, sv);
       if (bcol >= 0) {
 #pragma unroll
-        for (int u = 0; u < H; ++u) sv[u] = scan_bin(st[u], sv[u], gq[u], kq[u]);
+        for (int u = 0; u < H; ++u) {
+          if constexpr (ONE) {
+            float2 V = make_float2(sv[u].x * gq[u].y, sv[u].y * gq[u].y);
+            if (V.x * V.x + V.y * V.y < gq[u].z * gq[u].z) V = make_float2(gq[u].z, 0.0f);
+            sv[u] = make_float2(V.x * gq[u].w, V.y * gq[u].w);
+          } else {
+            sv[u] = scan_bin(st[u], sv[u], gq[u], kq[u]);
+          }
+        }
       } else {
 #pragma unroll
         for (int u = 0; u < H; ++u) sv[u] = make_float2(0.f, 0.f);
@@ -527,7 +543,11 @@ template <int H, class IO>
 static hipError_t run_small(const ScanArgs& a, int B, hipStream_t s) {
   using G = SmallGeom<H, H>;
   const long long P = (long long)B * a.C;
-  hipLaunchKernelGGL((gated_scan_small<H, H, IO>), dim3(unsigned((P + G::NP - 1) / G::NP)), dim3(G::NT), 0, s, a, P);
+  const dim3 grid(unsigned((P + G::NP - 1) / G::NP));
+  if (a.T == 1)
+    hipLaunchKernelGGL((gated_scan_small<H, H, IO, true>), grid, dim3(G::NT), 0, s, a, P);
+  else
+    hipLaunchKernelGGL((gated_scan_small<H, H, IO, false>), grid, dim3(G::NT), 0, s, a, P);
   return hipGetLastError();
 }
 
