@@ -199,13 +199,12 @@ def gated_step(cell, variables, x, w, S, mark, start=True):
     Ci, F, HW = cell.channels * cell.expand, B * T, H * W
     if start:
         mark("start")
-    u, z, ctx = S.proj_in(x, p["in_proj"]["kernel"], p["in_proj"]["bias"], F, HW, silu_lo=True, silu_hi=True,
-                          want_ctx=True, out_dtype=torch.float32)
-    mark("in_proj")
-    gates = S.gated_gates(ctx.view(B, T, Ci), p, H, W, cell.gate_type, cell.gate_activation,
-                          c_scale=S.scan_c_scale(H, W))
+    # in_proj with the gates from its ctx (the gate kernel reduces the projection's channel sums)
+    u, z, _, gates = S.proj_in_gates(x, p["in_proj"]["kernel"], p["in_proj"]["bias"], B, T, H, W, p, cell.gate_type,
+                                     cell.gate_activation, c_scale=S.scan_c_scale(H, W), silu_lo=True,
+                                     silu_hi=True, out_dtype=torch.float32)
     khat = cell.spectral_kernel(p, H, W)
-    mark("gates")
+    mark("in_proj_gates")
     y = S.gated_scan(u.view(B, T, Ci, H, W), z.view(B, T, Ci, H, W), gates, khat)
     mark("scan")
     out = S.proj_out(y.view(F, Ci, HW), p["out_proj"]["kernel"], p["out_proj"]["bias"], out_dtype=x.dtype)

@@ -183,18 +183,22 @@ class GatedCSSM:
         has_conv = self.short_conv_spatial_size > 0 or self.short_conv_size > 0
         # in_proj straight into plane-major x_main and z; SiLU(z) (cssm.py:581) fused here,
         # SiLU(x_main) and ctx too unless the short convolutions come first
-        xm, z, ctx = S.proj_in(x, p["in_proj"]["kernel"], p["in_proj"]["bias"], F, HW,
-                               silu_lo=not has_conv, silu_hi=True, want_ctx=not has_conv, out_dtype=f32)
-        xm = xm.view(B, T, Ci, H, W)
-        z = z.view(B, T, Ci, H, W)
+        c_scale = S.scan_c_scale(H, W)
         if has_conv:
-            u, ctx = S.short_conv(xm, p.get("short_conv_spatial") if self.short_conv_spatial_size > 0 else None,
+            xm, z, _ = S.proj_in(x, p["in_proj"]["kernel"], p["in_proj"]["bias"], F, HW, silu_hi=True,
+                                 out_dtype=f32)
+            u, ctx = S.short_conv(xm.view(B, T, Ci, H, W),
+                                  p.get("short_conv_spatial") if self.short_conv_spatial_size > 0 else None,
                                   p.get("short_conv_temporal") if self.short_conv_size > 0 else None)
             del xm
+            gates = S.gated_gates(ctx.view(B, T, Ci), p, H, W, self.gate_type, self.gate_activation, c_scale=c_scale)
         else:
-            u = xm
-        ctx = ctx.view(B, T, Ci)
-        gates = S.gated_gates(ctx, p, H, W, self.gate_type, self.gate_activation, c_scale=S.scan_c_scale(H, W))
+            # the gates from ctx in the same call (the gate kernel reduces the projection's sums)
+            u, z, _, gates = S.proj_in_gates(x, p["in_proj"]["kernel"], p["in_proj"]["bias"], B, T, H, W, p,
+                                             self.gate_type, self.gate_activation, c_scale=c_scale, silu_lo=True,
+                                             silu_hi=True, out_dtype=f32)
+            u = u.view(B, T, Ci, H, W)
+        z = z.view(B, T, Ci, H, W)
         khat = self.spectral_kernel(p, H, W)
         y = S.gated_scan(u, z, gates, khat)
         out = S.proj_out(y.view(F, Ci, HW), p["out_proj"]["kernel"], p["out_proj"]["bias"],

@@ -91,28 +91,35 @@ int cssm_plane_mean(const void* x, int dtype, long long nplanes, int H, int W, i
                     "cssm_plane_mean");
 }
 
-int cssm_gated_gates(const float* ctx, int B, int T, int C, int H, int W, const cssm_gate_params* p,
-                     float c_scale, float* gates, void* stream) {
-  if (!ctx || !p || !gates) return fail(CSSM_ERR_NULL, "cssm_gated_gates: ctx, params and gates must be non-null");
-  if (B <= 0 || T <= 0 || C <= 0 || H <= 0 || W <= 0)
-    return fail(CSSM_ERR_SHAPE, "cssm_gated_gates: B=%d T=%d C=%d H=%d W=%d", B, T, C, H, W);
+// the gate projections of a cssm_gate_params, checked (0, or the failing status with its message set)
+static int gate_weights(const cssm_gate_params* p, cssm::GateWeights& w, const char* who) {
   if (p->gate_type != CSSM_GATE_DENSE && p->gate_type != CSSM_GATE_FACTORED)
-    return fail(CSSM_ERR_ARG, "cssm_gated_gates: gate_type=%d", p->gate_type);
+    return fail(CSSM_ERR_ARG, "%s: gate_type=%d", who, p->gate_type);
   if (p->activation < CSSM_ACT_SOFTPLUS || p->activation > CSSM_ACT_EXP)
-    return fail(CSSM_ERR_ARG, "cssm_gated_gates: activation=%d", p->activation);
+    return fail(CSSM_ERR_ARG, "%s: activation=%d", who, p->activation);
   const bool fac = p->gate_type == CSSM_GATE_FACTORED;
-  cssm::GateWeights w;
   for (int i = 0; i < 3; ++i) {
     if (!p->kernel[i] || !p->bias[i] || (fac && (!p->kernel_w[i] || !p->bias_w[i])))
-      return fail(CSSM_ERR_NULL, "cssm_gated_gates: gate %d weights missing", i);
+      return fail(CSSM_ERR_NULL, "%s: gate %d weights missing", who, i);
     w.kd[i] = p->kernel[i];
     w.bd[i] = p->bias[i];
     w.kw[i] = fac ? p->kernel_w[i] : nullptr;
     w.bw[i] = fac ? p->bias_w[i] : nullptr;
   }
+  return CSSM_OK;
+}
+
+int cssm_gated_gates(const float* ctx, int B, int T, int C, int H, int W, const cssm_gate_params* p,
+                     float c_scale, float* gates, void* stream) {
+  if (!ctx || !p || !gates) return fail(CSSM_ERR_NULL, "cssm_gated_gates: ctx, params and gates must be non-null");
+  if (B <= 0 || T <= 0 || C <= 0 || H <= 0 || W <= 0)
+    return fail(CSSM_ERR_SHAPE, "cssm_gated_gates: B=%d T=%d C=%d H=%d W=%d", B, T, C, H, W);
+  cssm::GateWeights w;
+  if (const int st = gate_weights(p, w, "cssm_gated_gates")) return st;
   if (!aligned(gates, 16)) return fail(CSSM_ERR_ALIGN, "cssm_gated_gates: gates must be 16-byte aligned");
-  const hipError_t e = cssm::launch_gated_gates(ctx, B * T, C, H, W, fac ? 1 : 0, p->activation, w, c_scale,
-                                                reinterpret_cast<float4*>(gates),
+  const hipError_t e = cssm::launch_gated_gates(ctx, cssm::CtxPartials{nullptr, 0, 0, 0, nullptr}, B * T, C, H, W,
+                                                p->gate_type == CSSM_GATE_FACTORED ? 1 : 0, p->activation, w,
+                                                c_scale, reinterpret_cast<float4*>(gates),
                                                 static_cast<hipStream_t>(stream));
   if (e == hipErrorInvalidValue)
     return fail(CSSM_ERR_UNSUPPORTED, "cssm_gated_gates: C=%d with %dx%d planes exceeds the staging buffer", C, H, W);
@@ -125,22 +132,11 @@ int cssm_gated_gates_bwd(const float* ctx, int B, int T, int C, int H, int W, co
     return fail(CSSM_ERR_NULL, "cssm_gated_gates_bwd: ctx, params, dgates and out must be non-null");
   if (B <= 0 || T <= 0 || C <= 0 || H <= 0 || W <= 0)
     return fail(CSSM_ERR_SHAPE, "cssm_gated_gates_bwd: B=%d T=%d C=%d H=%d W=%d", B, T, C, H, W);
-  if (p->gate_type != CSSM_GATE_DENSE && p->gate_type != CSSM_GATE_FACTORED)
-    return fail(CSSM_ERR_ARG, "cssm_gated_gates_bwd: gate_type=%d", p->gate_type);
-  if (p->activation < CSSM_ACT_SOFTPLUS || p->activation > CSSM_ACT_EXP)
-    return fail(CSSM_ERR_ARG, "cssm_gated_gates_bwd: activation=%d", p->activation);
-  const bool fac = p->gate_type == CSSM_GATE_FACTORED;
   cssm::GateWeights w;
-  for (int i = 0; i < 3; ++i) {
-    if (!p->kernel[i] || !p->bias[i] || (fac && (!p->kernel_w[i] || !p->bias_w[i])))
-      return fail(CSSM_ERR_NULL, "cssm_gated_gates_bwd: gate %d weights missing", i);
-    w.kd[i] = p->kernel[i];
-    w.bd[i] = p->bias[i];
-    w.kw[i] = fac ? p->kernel_w[i] : nullptr;
-    w.bw[i] = fac ? p->bias_w[i] : nullptr;
-  }
+  if (const int st = gate_weights(p, w, "cssm_gated_gates_bwd")) return st;
   if (!aligned(dgates, 16)) return fail(CSSM_ERR_ALIGN, "cssm_gated_gates_bwd: dgates must be 16-byte aligned");
-  const hipError_t e = cssm::launch_gated_gates_bwd(ctx, B * T, C, H, W, fac ? 1 : 0, p->activation, w, c_scale,
+  const hipError_t e = cssm::launch_gated_gates_bwd(ctx, B * T, C, H, W, p->gate_type == CSSM_GATE_FACTORED ? 1 : 0,
+                                                    p->activation, w, c_scale,
                                                     reinterpret_cast<const float4*>(dgates), out,
                                                     static_cast<hipStream_t>(stream));
   if (e == hipErrorInvalidValue)
@@ -226,23 +222,33 @@ size_t cssm_proj_in_workspace_size(int F, int HW, int K, int N) {
   return tiles * slots * (N / 2) * sizeof(float);
 }
 
+// argument checks of the input projection (0, or the failing status with its message set)
+static int proj_in_check(const void* x, int in_dtype, int F, int HW, int K, int N, const float* kernel,
+                         const float* bias, void* out_lo, void* out_hi, int out_dtype, int act_lo, int act_hi,
+                         const char* who) {
+  if (!x || !kernel || !bias || !out_lo || !out_hi)
+    return fail(CSSM_ERR_NULL, "%s: x, kernel, bias, out_lo and out_hi must be non-null", who);
+  if (F <= 0 || HW <= 0 || K <= 0 || N <= 0 || (N % 2) != 0)
+    return fail(CSSM_ERR_SHAPE, "%s: F=%d HW=%d K=%d N=%d (N must be even)", who, F, HW, K, N);
+  if ((long long)F * HW > 0x7fffffffLL) return fail(CSSM_ERR_SHAPE, "%s: F*HW exceeds 2^31", who);
+  if ((in_dtype != CSSM_F32 && in_dtype != CSSM_BF16) || (out_dtype != CSSM_F32 && out_dtype != CSSM_BF16))
+    return fail(CSSM_ERR_ARG, "%s: dtypes %d/%d", who, in_dtype, out_dtype);
+  if ((act_lo != CSSM_LOAD_IDENTITY && act_lo != CSSM_LOAD_SILU && act_lo != CSSM_PROJ_STORE_PRE_CTX_SILU) ||
+      (act_hi != CSSM_LOAD_IDENTITY && act_hi != CSSM_LOAD_SILU))
+    return fail(CSSM_ERR_ARG, "%s: act_lo=%d act_hi=%d", who, act_lo, act_hi);
+  if (!aligned(x, vec_align(in_dtype)))
+    return fail(CSSM_ERR_ALIGN, "%s: x must be %zu-byte aligned", who, vec_align(in_dtype));
+  if (out_dtype == CSSM_F32 && (!aligned(out_lo, 16) || !aligned(out_hi, 16)))
+    return fail(CSSM_ERR_ALIGN, "%s: f32 outputs must be 16-byte aligned", who);
+  return CSSM_OK;
+}
+
 int cssm_proj_in(const void* x, int in_dtype, int F, int HW, int K, int N, const float* kernel, const float* bias,
                  void* out_lo, void* out_hi, int out_dtype, int act_lo, int act_hi, float* ctx, void* workspace,
                  size_t workspace_bytes, void* stream) {
-  if (!x || !kernel || !bias || !out_lo || !out_hi)
-    return fail(CSSM_ERR_NULL, "cssm_proj_in: x, kernel, bias, out_lo and out_hi must be non-null");
-  if (F <= 0 || HW <= 0 || K <= 0 || N <= 0 || (N % 2) != 0)
-    return fail(CSSM_ERR_SHAPE, "cssm_proj_in: F=%d HW=%d K=%d N=%d (N must be even)", F, HW, K, N);
-  if ((long long)F * HW > 0x7fffffffLL) return fail(CSSM_ERR_SHAPE, "cssm_proj_in: F*HW exceeds 2^31");
-  if ((in_dtype != CSSM_F32 && in_dtype != CSSM_BF16) || (out_dtype != CSSM_F32 && out_dtype != CSSM_BF16))
-    return fail(CSSM_ERR_ARG, "cssm_proj_in: dtypes %d/%d", in_dtype, out_dtype);
-  if ((act_lo != CSSM_LOAD_IDENTITY && act_lo != CSSM_LOAD_SILU && act_lo != CSSM_PROJ_STORE_PRE_CTX_SILU) ||
-      (act_hi != CSSM_LOAD_IDENTITY && act_hi != CSSM_LOAD_SILU))
-    return fail(CSSM_ERR_ARG, "cssm_proj_in: act_lo=%d act_hi=%d", act_lo, act_hi);
-  if (!aligned(x, vec_align(in_dtype)))
-    return fail(CSSM_ERR_ALIGN, "cssm_proj_in: x must be %zu-byte aligned", vec_align(in_dtype));
-  if (out_dtype == CSSM_F32 && (!aligned(out_lo, 16) || !aligned(out_hi, 16)))
-    return fail(CSSM_ERR_ALIGN, "cssm_proj_in: f32 outputs must be 16-byte aligned");
+  if (const int st = proj_in_check(x, in_dtype, F, HW, K, N, kernel, bias, out_lo, out_hi, out_dtype, act_lo, act_hi,
+                                   "cssm_proj_in"))
+    return st;
   const hipStream_t s = static_cast<hipStream_t>(stream);
   const int M = F * HW;
   const int tm = cssm::proj_in_tile_rows(K), slots = cssm::proj_in_ctx_slots(K, HW);
@@ -263,6 +269,51 @@ int cssm_proj_in(const void* x, int in_dtype, int F, int HW, int K, int N, const
                                             act_lo == CSSM_PROJ_STORE_PRE_CTX_SILU ? 1 : 0, ctx, s);
   }
   return hip_status(e, "cssm_proj_in");
+}
+
+int cssm_proj_in_gates(const void* x, int in_dtype, int B, int T, int H, int W, int K, int N, const float* kernel,
+                       const float* bias, void* out_lo, void* out_hi, int out_dtype, int act_lo, int act_hi,
+                       float* ctx, const cssm_gate_params* p, float c_scale, float* gates, void* workspace,
+                       size_t workspace_bytes, void* stream) {
+  if (!ctx || !p || !gates) return fail(CSSM_ERR_NULL, "cssm_proj_in_gates: ctx, params and gates must be non-null");
+  if (B <= 0 || T <= 0 || H <= 0 || W <= 0 || (long long)B * T * H * W > 0x7fffffffLL)
+    return fail(CSSM_ERR_SHAPE, "cssm_proj_in_gates: B=%d T=%d H=%d W=%d", B, T, H, W);
+  const int F = B * T, HW = H * W;
+  if (const int st = proj_in_check(x, in_dtype, F, HW, K, N, kernel, bias, out_lo, out_hi, out_dtype, act_lo, act_hi,
+                                   "cssm_proj_in_gates"))
+    return st;
+  cssm::GateWeights w;
+  if (const int st = gate_weights(p, w, "cssm_proj_in_gates")) return st;
+  if (!aligned(gates, 16)) return fail(CSSM_ERR_ALIGN, "cssm_proj_in_gates: gates must be 16-byte aligned");
+  const hipStream_t s = static_cast<hipStream_t>(stream);
+  const int M = F * HW, C = N / 2;
+  const int tm = cssm::proj_in_tile_rows(K), slots = cssm::proj_in_ctx_slots(K, HW);
+  cssm::CtxPartials cp{nullptr, 0, 0, 0, nullptr};
+  float* partial = nullptr;
+  if (slots > 0) {
+    const size_t need = cssm_proj_in_workspace_size(F, HW, K, N);
+    if (!workspace || workspace_bytes < need)
+      return fail(CSSM_ERR_ARG, "cssm_proj_in_gates: a %zu-byte workspace is required (got %zu)", need,
+                  workspace_bytes);
+    partial = static_cast<float*>(workspace);
+    cp = cssm::CtxPartials{partial, HW, tm, slots, ctx};
+  }
+  hipError_t e = cssm::launch_proj_in(x, in_dtype, M, K, N, kernel, bias, HW, out_lo, out_hi, out_dtype, act_lo,
+                                      act_hi, partial, s);
+  if (e != hipSuccess) return hip_status(e, "cssm_proj_in_gates");
+  if (slots == 0) {
+    e = cssm::launch_plane_mean(out_lo, out_dtype, (long long)F * C, HW,
+                                act_lo == CSSM_PROJ_STORE_PRE_CTX_SILU ? 1 : 0, ctx, s);
+    if (e != hipSuccess) return hip_status(e, "cssm_proj_in_gates");
+  }
+  // with the projection's per-tile sums the gate kernel reduces them per frame itself (and writes
+  // ctx) instead of a separate reduction launch
+  e = cssm::launch_gated_gates(slots > 0 ? nullptr : ctx, cp, F, C, H, W, p->gate_type == CSSM_GATE_FACTORED ? 1 : 0,
+                               p->activation, w, c_scale, reinterpret_cast<float4*>(gates), s);
+  if (e == hipErrorInvalidValue)
+    return fail(CSSM_ERR_UNSUPPORTED, "cssm_proj_in_gates: C=%d with %dx%d planes exceeds the staging buffer", C, H,
+                W);
+  return hip_status(e, "cssm_proj_in_gates");
 }
 
 int cssm_proj_out(const void* y, int in_dtype, int F, int HW, int K, int N, const float* kernel, const float* bias,

@@ -39,12 +39,46 @@ struct GateWeights {
   const float* bw[3];
 };
 
+// The projection's per-tile channel sums of ctx (cssm_proj_in's workspace): tile t of TM rows
+// holds, for each of its slots' frames f, partial[(t slots + f - first frame of t) C + c].
+struct CtxPartials {
+  const float* partial;   // nullptr: ctx comes as (F, C) floats instead
+  int HW, TM, slots;
+  float* ctx;             // (F, C) mean written here as well (may be nullptr)
+};
+
+// Sum over the row tiles t0 + gi, t0 + gi + G, ... <= t1 of frame f's partial sums of channel
+// c, in tile order with four loads in flight: one of G strided groups (the ctx reductions add
+// the G group sums in group order, so ctx is deterministic and the same in every kernel that
+// reduces it).
+__device__ __forceinline__ float ctx_tile_sum(const float* __restrict__ partial, int f, int HW, int TM, int slots,
+                                              int C, int c, int gi, int G) {
+  const long long r0 = (long long)f * HW, r1 = r0 + HW - 1;
+  const long long t0 = r0 / TM, t1 = r1 / TM;
+  float s = 0.0f;
+  long long t = t0 + gi;
+  for (; t + 3 * G <= t1; t += 4 * G) {
+    float v[4];
+#pragma unroll
+    for (int u = 0; u < 4; ++u) {
+      const long long tt = t + u * G;
+      v[u] = partial[(size_t(tt) * slots + int(f - (tt * TM) / HW)) * C + c];
+    }
+    s += v[0];
+    s += v[1];
+    s += v[2];
+    s += v[3];
+  }
+  for (; t <= t1; t += G) s += partial[(size_t(t) * slots + int(f - (t * TM) / HW)) * C + c];
+  return s;
+}
+
 hipError_t launch_spectral_kernel(const float* k, int C, int K, int H, int W, float rho, int squash,
                                   int goom_floor, int scan_order, float2* khat, hipStream_t s);
 hipError_t launch_plane_mean(const void* x, int dtype, long long nplanes, int HW, int act, float* out,
                              hipStream_t s);
-hipError_t launch_gated_gates(const float* ctx, int BT, int C, int H, int W, int factored, int act,
-                              const GateWeights& w, float c_scale, float4* gates, hipStream_t s);
+hipError_t launch_gated_gates(const float* ctx, const CtxPartials& cp, int BT, int C, int H, int W, int factored,
+                              int act, const GateWeights& w, float c_scale, float4* gates, hipStream_t s);
 // adjoint of launch_gated_gates: out = dG (BT, 3, H*WF) dense, or the factor gradients (BT, 3, H + WF)
 hipError_t launch_gated_gates_bwd(const float* ctx, int BT, int C, int H, int W, int factored, int act,
                                   const GateWeights& w, float c_scale, const float4* dgates, float* out,

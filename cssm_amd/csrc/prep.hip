@@ -110,69 +110,137 @@ __device__ __forceinline__ float gate_act(float x, int act) {
   return softplus_f(x);
 }
 
-// The 3 (H + WF) factored row / column products of one frame, written to fac
-// (g * (H + WF) + r: rows r < H, columns H + v).  Small planes (few products,
-// long C) split each product over P threads and sum the parts in LDS (part:
-// P * nv floats past fac).  Ends with a barrier.
-__device__ __forceinline__ void gate_factors(const float* cx, int C, int H, int WF, const GateWeights& gw,
-                                             float* fac) {
-  const int nv = 3 * (H + WF);
-  const int P = nv >= int(blockDim.x) ? 1 : int(blockDim.x) / nv;
-  if (P == 1) {
-    for (int idx = threadIdx.x; idx < nv; idx += blockDim.x) {
-      const int g = idx / (H + WF), r = idx % (H + WF);
-      float acc;
-      if (r < H) {
-        acc = gw.bd[g][r];
-#pragma unroll 8
-        for (int c = 0; c < C; ++c) acc = fmaf(cx[c], gw.kd[g][size_t(c) * H + r], acc);
-      } else {
-        const int v = r - H;
-        acc = gw.bw[g][v];
-#pragma unroll 8
-        for (int c = 0; c < C; ++c) acc = fmaf(cx[c], gw.kw[g][size_t(c) * WF + v], acc);
-      }
-      fac[idx] = acc;
-    }
-  } else {
-    float* part = fac + nv;   // P * nv partial sums
-    for (int q = threadIdx.x; q < nv * P; q += blockDim.x) {
-      const int idx = q % nv, pc = q / nv;
-      const int g = idx / (H + WF), r = idx % (H + WF);
-      float acc = 0.0f;
-      // (loads unrolled so several are in flight: the weights come from L2)
-      if (r < H) {
-#pragma unroll 8
-        for (int c = pc; c < C; c += P) acc = fmaf(cx[c], gw.kd[g][size_t(c) * H + r], acc);
-      } else {
-#pragma unroll 8
-        for (int c = pc; c < C; c += P) acc = fmaf(cx[c], gw.kw[g][size_t(c) * WF + (r - H)], acc);
-      }
-      part[pc * nv + idx] = acc;
+// ctx of frame f into cx (LDS): read from ctx (F, C), or reduced from the projection's tile sums
+// (cp.partial; with cp.ctx also written out).  The first 256 threads reduce exactly as
+// ctx_reduce_kernel does, so ctx is the same bit for bit either way.  red: 256 floats of LDS.
+// Ends with a barrier.
+__device__ __forceinline__ void frame_ctx(const float* __restrict__ ctx, const CtxPartials& cp, int f, int C,
+                                          float* cx, float* red) {
+  const int tid = threadIdx.x, nt = blockDim.x;
+  if (!cp.partial) {
+    for (int i = tid; i < C; i += nt) cx[i] = ctx[size_t(f) * C + i];
+    __syncthreads();
+    return;
+  }
+  const float inv = 1.0f / float(cp.HW);
+  const int G = C <= 128 ? 256 / C : 1;
+  if (G > 1) {
+    if (tid < 256) {
+      const int g = tid / C, c = tid % C;
+      red[tid] = g < G ? ctx_tile_sum(cp.partial, f, cp.HW, cp.TM, cp.slots, C, c, g, G) : 0.0f;
     }
     __syncthreads();
-    for (int idx = threadIdx.x; idx < nv; idx += blockDim.x) {
-      const int g = idx / (H + WF), r = idx % (H + WF);
-      float acc = r < H ? gw.bd[g][r] : gw.bw[g][r - H];
-      for (int pc = 0; pc < P; ++pc) acc += part[pc * nv + idx];
-      fac[idx] = acc;
+    if (tid < C) {
+      float sum = 0.0f;
+      for (int q = 0; q < G; ++q) sum += red[q * C + tid];
+      const float v = sum * inv;
+      cx[tid] = v;
+      if (cp.ctx) cp.ctx[size_t(f) * C + tid] = v;
+    }
+  } else {
+    for (int c = tid; c < C; c += nt) {
+      const float v = ctx_tile_sum(cp.partial, f, cp.HW, cp.TM, cp.slots, C, c, 0, 1) * inv;
+      cx[c] = v;
+      if (cp.ctx) cp.ctx[size_t(f) * C + c] = v;
     }
   }
   __syncthreads();
 }
 
-__global__ void __launch_bounds__(1024) gated_gates_kernel(const float* __restrict__ ctx, int C, int H, int W, int factored,
-                                   int act, GateWeights gw, float c_scale, float4* __restrict__ out) {
+// The 3 (H + WF) factored row / column products of one frame, fac[g (H + WF) + r] (rows r < H,
+// columns H + v) = bias + ctx . kernel column.  Small planes (few products, long C) split each
+// product over P threads (channels pc, pc + P, ...) and sum the parts in LDS in order of pc.
+// The first KW weights of a thread are loaded by prefetch(), before ctx is ready (they do not
+// depend on it), so a frame waits for one memory latency, not two; finish() runs after the
+// barrier that publishes cx and ends with one.
+template <int KW>
+struct GateFactors {
+  int nv, P, idx, pc, ws;
+  bool mine;
+  const float* wc;
+  float wr[KW];
+
+  __device__ __forceinline__ void prefetch(const GateWeights& gw, int C, int H, int WF) {
+    const int nt = blockDim.x, q = threadIdx.x;
+    nv = 3 * (H + WF);
+    P = nv >= nt ? 1 : nt / nv;
+    idx = q % nv;
+    pc = q / nv;
+    mine = q < nv * P;
+    const int g = idx / (H + WF), r = idx % (H + WF);
+    wc = r < H ? gw.kd[g] + r : gw.kw[g] + (r - H);
+    ws = r < H ? H : WF;
+#pragma unroll
+    for (int k = 0; k < KW; ++k) {
+      const int c = pc + k * P;
+      wr[k] = mine && c < C ? wc[size_t(c) * ws] : 0.0f;
+    }
+  }
+
+  // part: P * nv floats of LDS (may alias the ctx reduction's scratch)
+  __device__ __forceinline__ void finish(const GateWeights& gw, const float* cx, int C, int H, int WF, float* fac,
+                                         float* part) const {
+    const int nt = blockDim.x, q = threadIdx.x;
+    if (mine) {
+      float acc = 0.0f;
+#pragma unroll
+      for (int k = 0; k < KW; ++k) {
+        const int c = pc + k * P;
+        if (c < C) acc = fmaf(cx[c], wr[k], acc);
+      }
+#pragma unroll 8
+      for (int c = pc + KW * P; c < C; c += P) acc = fmaf(cx[c], wc[size_t(c) * ws], acc);
+      part[pc * nv + idx] = acc;
+    }
+    // products beyond the block's threads (nv > blockDim: one part each, no prefetch)
+    for (int i = q + nt; i < nv; i += nt) {
+      const int g = i / (H + WF), r = i % (H + WF);
+      const float* w = r < H ? gw.kd[g] + r : gw.kw[g] + (r - H);
+      const int s = r < H ? H : WF;
+      float acc = 0.0f;
+#pragma unroll 8
+      for (int c = 0; c < C; ++c) acc = fmaf(cx[c], w[size_t(c) * s], acc);
+      part[i] = acc;
+    }
+    __syncthreads();
+    for (int i = q; i < nv; i += nt) {
+      const int g = i / (H + WF), r = i % (H + WF);
+      float acc = 0.0f;
+      for (int p = 0; p < P; ++p) acc += part[p * nv + i];
+      fac[i] = acc + (r < H ? gw.bd[g][r] : gw.bw[g][r - H]);
+    }
+    __syncthreads();
+  }
+};
+
+// LDS of the gate kernels: cx (C), fac (nv), then max(P nv, 256) floats of scratch
+__host__ __device__ inline int gate_lds_floats(int C, int H, int W, int nt, bool factored) {
+  const int WF = W / 2 + 1, nv = 3 * (H + WF);
+  const int P = nv >= nt ? 1 : nt / nv;
+  const int scratch = factored ? (P * nv > 256 ? P * nv : 256) : 256;
+  return C + (factored ? nv : 0) + scratch;
+}
+
+// 512 threads per frame (two frames per CU at up to 128 VGPRs: a 512-frame batch in one pass),
+// each thread's weights loaded up front (up to 32 of them: 114 VGPRs)
+constexpr int kGateThreads = 512, kGateKW = 32;
+template <bool FACTORED>
+__global__ void __launch_bounds__(kGateThreads, 4) gated_gates_kernel(const float* __restrict__ ctx, CtxPartials cp, int C,
+                                                              int H, int W, int act, GateWeights gw, float c_scale,
+                                                              float4* __restrict__ out) {
+  constexpr bool factored = FACTORED;
   extern __shared__ float sm_f[];
   const int WF = W / 2 + 1;
   const int bt = blockIdx.x;
-  float* cx = sm_f;              // C
-  float* fac = sm_f + C;         // 3 * (H + WF) factored vectors
-  for (int i = threadIdx.x; i < C; i += blockDim.x) cx[i] = ctx[size_t(bt) * C + i];
-  __syncthreads();
   const int nbin = H * WF;
-  if (factored) {
-    gate_factors(cx, C, H, WF, gw, fac);
+  float* cx = sm_f;                                    // C
+  float* fac = sm_f + C;                               // 3 (H + WF) factored vectors
+  float* scratch = fac + (factored ? 3 * (H + WF) : 0);
+  if constexpr (factored) {
+    GateFactors<kGateKW> gf;
+    gf.prefetch(gw, C, H, WF);
+    frame_ctx(ctx, cp, bt, C, cx, scratch);
+    gf.finish(gw, cx, C, H, WF, fac, scratch);
     for (int o = threadIdx.x; o < nbin; o += blockDim.x) {
       const int u = o / WF, v = scan_col(H, W, o % WF);
       float gr[3];
@@ -181,6 +249,7 @@ __global__ void __launch_bounds__(1024) gated_gates_kernel(const float* __restri
       out[size_t(bt) * nbin + o] = make_float4(expf(-d), dd * gr[1], dd * 2e-7f, gr[2] * c_scale);
     }
   } else {
+    frame_ctx(ctx, cp, bt, C, cx, scratch);
     for (int o = threadIdx.x; o < nbin; o += blockDim.x) {
       const int bin = (o / WF) * WF + scan_col(H, W, o % WF);
       float gr[3];
@@ -261,13 +330,16 @@ __global__ void __launch_bounds__(1024) gated_gates_bwd_kernel(const float* __re
     return;
   }
   const int nv = 3 * (H + WF);
-  const int P = nv >= int(blockDim.x) ? 1 : int(blockDim.x) / nv;
   float* cx = sm_f;                                  // C
-  float* fac = cx + C;                               // nv factors (+ P * nv parts while they are built)
-  float* colp = fac + nv + size_t(P) * nv;           // S * WF * 3 column partial sums
-  for (int i = threadIdx.x; i < C; i += blockDim.x) cx[i] = ctx[size_t(bt) * C + i];
-  __syncthreads();
-  gate_factors(cx, C, H, WF, gw, fac);
+  float* fac = cx + C;                               // nv factors
+  float* scratch = fac + nv;                         // parts while the factors are built
+  float* colp = sm_f + gate_lds_floats(C, H, W, int(blockDim.x), true);   // S * WF * 3 column partial sums
+  {
+    GateFactors<16> gf;
+    gf.prefetch(gw, C, H, WF);
+    frame_ctx(ctx, CtxPartials{nullptr, 0, 0, 0, nullptr}, bt, C, cx, scratch);
+    gf.finish(gw, cx, C, H, WF, fac, scratch);
+  }
   float* o3 = out + size_t(bt) * nv;
   // rows: wave w takes rows w, w + nwaves, ...; its lanes walk the row's positions
   const int lane = threadIdx.x & 63, wv = threadIdx.x >> 6, nw = int(blockDim.x) >> 6;
@@ -383,18 +455,18 @@ hipError_t launch_plane_mean(const void* x, int dtype, long long nplanes, int HW
   return hipGetLastError();
 }
 
-hipError_t launch_gated_gates(const float* ctx, int BT, int C, int H, int W, int factored, int act,
-                              const GateWeights& w, float c_scale, float4* gates, hipStream_t s) {
-  const int WF = W / 2 + 1;
-  const int nv = 3 * (H + WF);
-  // 1024 threads per frame: the factored products split over P = 1024 / nv threads each, which
-  // keeps each thread's chain of dependent loads + FMAs at C / P (latency, not arithmetic, bounds it)
-  constexpr int NT = 1024;
-  const int P = nv >= NT ? 1 : NT / nv;   // partial sums per factored product (see the kernel)
-  const size_t shm = (size_t(C) + size_t(nv) * (1 + P)) * sizeof(float);
+hipError_t launch_gated_gates(const float* ctx, const CtxPartials& cp, int BT, int C, int H, int W, int factored,
+                              int act, const GateWeights& w, float c_scale, float4* gates, hipStream_t s) {
+  // the factored products split over P = threads / nv threads each, which keeps each thread's
+  // chain of dependent FMAs at C / P (latency, not arithmetic, bounds it)
+  constexpr int NT = kGateThreads;
+  const size_t shm = size_t(gate_lds_floats(C, H, W, NT, factored != 0)) * sizeof(float);
   if (shm > 64 * 1024) return hipErrorInvalidValue;
-  hipLaunchKernelGGL(gated_gates_kernel, dim3(BT), dim3(NT), shm, s, ctx, C, H, W, factored, act, w,
-                     c_scale, gates);
+  if (factored)
+    hipLaunchKernelGGL(gated_gates_kernel<true>, dim3(BT), dim3(NT), shm, s, ctx, cp, C, H, W, act, w, c_scale, gates);
+  else
+    hipLaunchKernelGGL(gated_gates_kernel<false>, dim3(BT), dim3(NT), shm, s, ctx, cp, C, H, W, act, w, c_scale,
+                       gates);
   return hipGetLastError();
 }
 
@@ -402,13 +474,11 @@ hipError_t launch_gated_gates_bwd(const float* ctx, int BT, int C, int H, int W,
                                   const GateWeights& w, float c_scale, const float4* dgates, float* out,
                                   hipStream_t s) {
   const int WF = W / 2 + 1;
-  const int nv = 3 * (H + WF);
   constexpr int NT = 1024;
   if (factored && WF > NT) return hipErrorInvalidValue;
-  const int P = nv >= NT ? 1 : NT / nv;
   const int S = NT / WF;
-  const size_t shm = factored ? (size_t(C) + size_t(nv) * (1 + P) + size_t(S) * WF * 3) * sizeof(float)
-                              : size_t(C) * sizeof(float);
+  const size_t shm = (size_t(gate_lds_floats(C, H, W, NT, factored != 0)) +
+                      (factored ? size_t(S) * WF * 3 : 0)) * sizeof(float);
   if (shm > 64 * 1024) return hipErrorInvalidValue;
   hipLaunchKernelGGL(gated_gates_bwd_kernel, dim3(BT), dim3(NT), shm, s, ctx, C, H, W, factored, act, w,
                      c_scale, dgates, out);

@@ -215,31 +215,11 @@ __global__ void __launch_bounds__(256) ctx_reduce_kernel(const float* __restrict
                                                          int slots, int C, float* __restrict__ ctx) {
   __shared__ float red[256];
   const int f = blockIdx.x, tid = threadIdx.x;
-  const long long r0 = (long long)f * HW, r1 = r0 + HW - 1;
-  const long long t0 = r0 / TM, t1 = r1 / TM;
   const int G = C <= 128 ? 256 / C : 1;
   const int g = tid / C;   // (C <= 128: tid < G C covers every thread of the block)
-  auto sum_tiles = [&](int c, int gi) {
-    float s = 0.0f;
-    long long t = t0 + gi;
-    for (; t + 3 * G <= t1; t += 4 * G) {
-      float v[4];
-#pragma unroll
-      for (int u = 0; u < 4; ++u) {
-        const long long tt = t + u * G;
-        v[u] = partial[(size_t(tt) * slots + int(f - (tt * TM) / HW)) * C + c];
-      }
-      s += v[0];
-      s += v[1];
-      s += v[2];
-      s += v[3];
-    }
-    for (; t <= t1; t += G) s += partial[(size_t(t) * slots + int(f - (t * TM) / HW)) * C + c];
-    return s;
-  };
   if (G > 1) {
     const int c = tid % C;
-    red[tid] = g < G ? sum_tiles(c, g) : 0.0f;
+    red[tid] = g < G ? ctx_tile_sum(partial, f, HW, TM, slots, C, c, g, G) : 0.0f;
     __syncthreads();
     if (tid < C) {
       float s = 0.0f;
@@ -247,7 +227,8 @@ __global__ void __launch_bounds__(256) ctx_reduce_kernel(const float* __restrict
       ctx[size_t(f) * C + tid] = s * (1.0f / float(HW));
     }
   } else {
-    for (int c = tid; c < C; c += 256) ctx[size_t(f) * C + c] = sum_tiles(c, 0) * (1.0f / float(HW));
+    for (int c = tid; c < C; c += 256)
+      ctx[size_t(f) * C + c] = ctx_tile_sum(partial, f, HW, TM, slots, C, c, 0, 1) * (1.0f / float(HW));
   }
 }
 

@@ -268,6 +268,42 @@ def proj_in(x: torch.Tensor, kernel: torch.Tensor, bias: torch.Tensor, frames: i
     return lo, hi, ctx
 
 
+def proj_in_gates(x: torch.Tensor, kernel: torch.Tensor, bias: torch.Tensor, B: int, T: int, H: int, W: int,
+                  params: Dict, gate_type: str = "dense", activation: str = "softplus", c_scale: float = 1.0,
+                  silu_lo: bool = False, silu_hi: bool = False, out_dtype: Optional[torch.dtype] = None,
+                  ctx_of_silu: bool = False):
+    """:func:`proj_in` with ``want_ctx`` followed by :func:`gated_gates` on its ctx, in one call
+    (cssm_proj_in_gates: the gate kernel reduces the projection's channel sums itself).
+    Returns (lo, hi, ctx, gates) with the shapes of those two functions; the same values."""
+    if ctx_of_silu and silu_lo:
+        raise ValueError("ctx_of_silu stores lo without activation")
+    _dev(x, "x")
+    if x.dtype not in _DTYPES:
+        raise ValueError(f"unsupported dtype {x.dtype}")
+    K = x.shape[-1]
+    F, hw = B * T, H * W
+    if x.numel() != F * hw * K:
+        raise ValueError("x does not hold B * T * H * W rows")
+    _dev(kernel, "kernel", torch.float32)
+    _dev(bias, "bias", torch.float32)
+    Kk, N = kernel.shape
+    if Kk != K or bias.shape != (N,) or N % 2:
+        raise ValueError(f"kernel {tuple(kernel.shape)} / bias {tuple(bias.shape)} do not match K={K}")
+    od = out_dtype or x.dtype
+    lo = torch.empty((F, N // 2, hw), dtype=od, device=x.device)
+    hi = torch.empty_like(lo)
+    ctx = torch.empty((B, T, N // 2), dtype=torch.float32, device=x.device)
+    gates = torch.empty((B, T, H, W // 2 + 1, 4), dtype=torch.float32, device=x.device)
+    nbytes = int(_lib.load().cssm_proj_in_workspace_size(F, hw, K, N))
+    ws = torch.empty(nbytes // 4, dtype=torch.float32, device=x.device) if nbytes else None
+    s = gate_params_struct(params, gate_type, activation)
+    _lib.call("cssm_proj_in_gates", x.data_ptr(), _DTYPES[x.dtype], B, T, H, W, K, N, kernel.data_ptr(),
+              bias.data_ptr(), lo.data_ptr(), hi.data_ptr(), _DTYPES[od], 3 if ctx_of_silu else int(silu_lo),
+              int(silu_hi), ctx.data_ptr(), s, float(c_scale), gates.data_ptr(),
+              ws.data_ptr() if ws is not None else None, nbytes, _stream())
+    return lo, hi, ctx, gates
+
+
 def proj_out(y: torch.Tensor, kernel: torch.Tensor, bias: torch.Tensor,
              out_dtype: Optional[torch.dtype] = None) -> torch.Tensor:
     """Dense(N) from plane-major (frames, K, hw) to channels-last (frames * hw, N) (cssm.py:584)."""

@@ -33,8 +33,9 @@ extern "C" {
  *    (cssm_gated_scan_khat_order).
  * 4: scan_variant arguments of the GDN delta-rule entry points.
  * 5: cssm_im2col_same, cssm_gdn_proj_out_xgate.
- * 6: cssm_gated_gates_bwd. */
-#define CSSM_ABI_VERSION 6
+ * 6: cssm_gated_gates_bwd.
+ * 7: cssm_proj_in_gates. */
+#define CSSM_ABI_VERSION 7
 
 typedef enum cssm_status {
   CSSM_OK = 0,
@@ -233,6 +234,24 @@ int cssm_gated_scan_bwd(const float* uspec, const float* dspec, const float* gat
 int cssm_proj_in(const void* x, int in_dtype, int F, int HW, int K, int N, const float* kernel,
                  const float* bias, void* out_lo, void* out_hi, int out_dtype, int act_lo, int act_hi,
                  float* ctx, void* workspace, size_t workspace_bytes, void* stream);
+
+/*
+ * cssm_proj_in followed by cssm_gated_gates on its ctx, for the gated cell without short
+ * convolutions: replaces cssm.py:480-484 (in_proj), :536 (ctx) and :538-567 (gates) in one
+ * call.  Where the projection kernel takes the frames' channel sums on the way
+ * (cssm_proj_in_workspace_size(B * T, H * W, K, N) > 0), the gate kernel reduces them per
+ * frame itself instead of a separate reduction launch; ctx is written either way.
+ *   x, kernel, bias, out_lo, out_hi, out_dtype, act_lo, act_hi  as cssm_proj_in with
+ *            F = B * T frames of HW = H * W pixels
+ *   ctx      (B, T, N/2) float32 out (required)
+ *   params, c_scale, gates  as cssm_gated_gates with C = N / 2
+ *   workspace  device scratch of cssm_proj_in_workspace_size(B * T, H * W, K, N) bytes
+ * Same results as the two calls, bit for bit.
+ */
+int cssm_proj_in_gates(const void* x, int in_dtype, int B, int T, int H, int W, int K, int N, const float* kernel,
+                       const float* bias, void* out_lo, void* out_hi, int out_dtype, int act_lo, int act_hi,
+                       float* ctx, const cssm_gate_params* params, float c_scale, float* gates, void* workspace,
+                       size_t workspace_bytes, void* stream);
 
 /* Bytes of device workspace cssm_proj_in needs to produce ctx. */
 size_t cssm_proj_in_workspace_size(int F, int HW, int K, int N);

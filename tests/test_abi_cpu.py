@@ -33,7 +33,7 @@ def test_library_exports_every_declared_symbol():
 def test_abi_version_and_errors_without_gpu():
     from cssm_amd import _lib
     lib = _lib.load()
-    assert lib.cssm_abi_version() == _lib.ABI_VERSION == 6
+    assert lib.cssm_abi_version() == _lib.ABI_VERSION == 7
     assert lib.cssm_strerror(-1) == b"null pointer argument"
     # argument validation happens before any GPU work
     st = lib.cssm_gated_scan_fwd(None, None, None, 0, 1, 1, 1, 8, 8, None, None, 0, 0, None)
@@ -94,6 +94,21 @@ def test_abi_version_and_errors_without_gpu():
     gp.gate_type = 7
     st = lib.cssm_gated_gates_bwd(p, 1, 1, 8, 8, 8, ctypes.byref(gp), 1.0, p, p, None)
     assert st == -4 and b"gate_type" in lib.cssm_last_error()
+    # in_proj + gates: ctx, params and gates required; then the projection's and the gates' checks
+    gp.gate_type, gp.bias_w[1] = _lib.GATE_FACTORED, p
+    args = dict(x=p, in_dtype=1, B=2, T=1, H=14, W=14, K=128, N=512, kernel=p, bias=p, lo=p, hi=p, out_dtype=0,
+                act_lo=1, act_hi=1, ctx=p, params=ctypes.byref(gp), c_scale=1.0, gates=p, ws=p, ws_bytes=1 << 30)
+
+    def pig(**kw):
+        a = dict(args, **kw)
+        return lib.cssm_proj_in_gates(*a.values(), None)
+    assert pig(ctx=None) == -1 and b"non-null" in lib.cssm_last_error()
+    assert pig(N=511) == -2
+    assert pig(act_lo=9) == -4
+    assert pig(gates=p + 4) == -5
+    assert pig(ws=None) == -4 and b"workspace" in lib.cssm_last_error()
+    gp.activation = 5
+    assert pig() == -4 and b"activation" in lib.cssm_last_error()
 
 
 @pytest.mark.parametrize("H", [4, 8, 14, 32, 64, 128])

@@ -147,6 +147,49 @@ def test_gated_gates_match_oracle(S, gate_type, act, shape):
     assert rel_err(got[..., 3], 0.5 * gC) < 1e-5
 
 
+# (B, T, H, K, N, dtype): the C5 stages on the K-chunked projection (channel sums per tile,
+# tiles spanning frames), C1 / C2-like planes on the persistent one (one frame per tile), and
+# 7 x 7 at K = 64, where the projection takes no sums and ctx is a plane mean
+PIG_CASES = [(2, 1, 14, 128, 512, torch.bfloat16), (3, 1, 7, 224, 896, torch.bfloat16),
+             (2, 1, 4, 320, 1280, torch.bfloat16), (2, 3, 32, 64, 256, torch.float32),
+             (1, 2, 128, 64, 128, torch.float32), (2, 2, 7, 64, 128, torch.float32)]
+
+
+@pytest.mark.parametrize("gate_type", ["factored", "dense"])
+@pytest.mark.parametrize("B,T,H,K,N,dt", PIG_CASES, ids=[f"{c[2]}x{c[2]}_K{c[3]}_N{c[4]}" for c in PIG_CASES])
+def test_proj_in_gates_matches_separate_calls(S, gate_type, B, T, H, K, N, dt):
+    """cssm_proj_in_gates (the gate kernel reducing the projection's channel sums itself) against
+    cssm_proj_in with ctx followed by cssm_gated_gates: the same planes, ctx and gates, bit for bit;
+    the gates also against the oracle on the projection's own ctx."""
+    print_case(test="proj_in_gates", gate_type=gate_type, shape=(B, T, H, K, N), dtype=dt)
+    rng = np.random.default_rng(12)
+    W, C = H, N // 2
+    cfg = O.GatedConfig(channels=C, gate_type=gate_type, gate_activation="softplus", short_conv_size=0,
+                        short_conv_spatial_size=0, kernel_size=3)
+    p = O.init_params(O.gated_param_shapes(cfg, C, H, W), rng)
+    pd = {k: ({kk: _dev(vv) for kk, vv in v.items()} if isinstance(v, dict) else _dev(v))
+          for k, v in p.items()}
+    x = _dev(rng.standard_normal((B * T * H * W, K)), dt)
+    w_in = _dev(rng.standard_normal((K, N)) / math.sqrt(K))
+    b_in = _dev(0.1 * rng.standard_normal(N))
+    cs = S.scan_c_scale(H, W)
+    lo, hi, ctx = S.proj_in(x, w_in, b_in, B * T, H * W, silu_lo=True, silu_hi=True, want_ctx=True,
+                            out_dtype=torch.float32)
+    gates = S.gated_gates(ctx.view(B, T, C), pd, H, W, gate_type, "softplus", c_scale=cs)
+    lo2, hi2, ctx2, gates2 = S.proj_in_gates(x, w_in, b_in, B, T, H, W, pd, gate_type, "softplus", c_scale=cs,
+                                             silu_lo=True, silu_hi=True, out_dtype=torch.float32)
+    torch.cuda.synchronize()
+    assert torch.equal(lo, lo2) and torch.equal(hi, hi2)
+    assert torch.equal(ctx.view(B, T, C), ctx2)
+    assert torch.equal(gates, gates2)
+    delta, gB, gC = O.gated_gates(to_np(ctx2), p, cfg, H, W)
+    cols = _scan_cols(H, W)
+    d = (delta + 1e-8)[..., cols]
+    got = to_np(gates2)
+    assert rel_err(got[..., 1], d * gB[..., cols]) < 3e-5
+    assert rel_err(got[..., 3], cs * gC[..., cols]) < 1e-5
+
+
 # --------------------------------------------------------------- fused scan
 
 SCAN_CASES = [
