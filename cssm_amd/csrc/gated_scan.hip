@@ -525,6 +525,199 @@ gated_scan_small(const ScanArgs a, long long P) {
   }
 }
 
+// ---------------------------------------------------------------------------
+// Planes of at most 16 samples (3 x 3; 4 x 4 has its own kernel below): one thread per (b, c)
+// plane for all T steps, the whole plane, its spectrum and its state in registers, no LDS and
+// no barriers.  The DFT functions, recurrence and C2R rule are those of gated_scan_small; the
+// plane's u_t and z_t come as 4-element vectors when the plane size allows it and the tensors
+// are aligned (one plane = H W contiguous elements).
+// ---------------------------------------------------------------------------
+template <int H, int W, class IO, bool ONE>
+__global__ void __launch_bounds__(256) gated_scan_plane(const ScanArgs a, long long P) {
+  constexpr int WF = W / 2 + 1, HW = H * W;
+  static_assert(HW <= 16, "one plane per thread in registers");
+  constexpr bool VEC_OK = HW % 4 == 0;
+  using TE = typename IO::T;
+  using V4 = typename IO::V4;
+  const long long pl = (long long)blockIdx.x * blockDim.x + threadIdx.x;
+  if (pl >= P) return;   // (no barriers below)
+  const int T = a.T, C = a.C;
+  const int b = int(pl / C), c = int(pl % C);
+  const TE* __restrict__ up = static_cast<const TE*>(a.u);
+  const TE* __restrict__ zp = static_cast<const TE*>(a.z);
+  TE* __restrict__ yp = static_cast<TE*>(a.y);
+  constexpr unsigned VA = unsigned(sizeof(V4)) - 1u;
+  const bool vec = VEC_OK && ((reinterpret_cast<uintptr_t>(up) | reinterpret_cast<uintptr_t>(zp) |
+                               reinterpret_cast<uintptr_t>(yp)) & VA) == 0;
+  float2 st[ONE ? 1 : H][WF];
+  float2 kh[ONE ? 1 : H][WF];
+  if constexpr (!ONE) {
+    const float2* kp = a.khat + size_t(c) * (H * WF);
+#pragma unroll
+    for (int u = 0; u < H; ++u)
+#pragma unroll
+      for (int v = 0; v < WF; ++v) {
+        kh[u][v] = kp[u * WF + v];
+        st[u][v] = make_float2(0.f, 0.f);
+      }
+  }
+  for (int t = 0; t < T; ++t) {
+    const size_t base = ((size_t(b) * T + t) * C + c) * HW;
+    float x[HW], zg[HW];
+    if (vec) {
+      const V4* u4 = reinterpret_cast<const V4*>(up + base);
+      const V4* z4 = reinterpret_cast<const V4*>(zp + base);
+      V4 uv[HW / 4 > 0 ? HW / 4 : 1], zv[HW / 4 > 0 ? HW / 4 : 1];
+#pragma unroll
+      for (int k = 0; k < HW / 4; ++k) uv[k] = u4[k];
+#pragma unroll
+      for (int k = 0; k < HW / 4; ++k) zv[k] = z4[k];
+#pragma unroll
+      for (int k = 0; k < HW / 4; ++k) {
+        const float4 f = act4(IO::to_f4(uv[k]), a.u_act), g = act4(IO::to_f4(zv[k]), a.z_act);
+        x[4 * k] = 2.0f * f.x;
+        x[4 * k + 1] = 2.0f * f.y;
+        x[4 * k + 2] = 2.0f * f.z;
+        x[4 * k + 3] = 2.0f * f.w;
+        zg[4 * k] = g.x;
+        zg[4 * k + 1] = g.y;
+        zg[4 * k + 2] = g.z;
+        zg[4 * k + 3] = g.w;
+      }
+    } else {
+#pragma unroll
+      for (int e = 0; e < HW; ++e) {
+        const float v = IO::to_f(up[base + e]);
+        x[e] = 2.0f * (a.u_act == 1 ? silu_f(v) : v);
+        const float g = IO::to_f(zp[base + e]);
+        zg[e] = a.z_act == 1 ? silu_f(g) : g;
+      }
+    }
+    // rows, then per column: forward DFT over h, the recurrence, inverse DFT over u
+    float2 R[H][WF];
+#pragma unroll
+    for (int h = 0; h < H; ++h) small_row_r2c<W>(x + h * W, R[h]);
+    const float4* gp = a.gates + (size_t(b) * T + t) * (H * WF);
+#pragma unroll
+    for (int v = 0; v < WF; ++v) {
+      float2 r[H], sv[H];
+#pragma unroll
+      for (int h = 0; h < H; ++h) r[h] = R[h][v];
+      dft_sym<H, false>(r, sv);
+#pragma unroll
+      for (int u = 0; u < H; ++u) {
+        const float4 g = gp[u * WF + v];
+        if constexpr (ONE) {
+          float2 V = make_float2(sv[u].x * g.y, sv[u].y * g.y);
+          if (V.x * V.x + V.y * V.y < g.z * g.z) V = make_float2(g.z, 0.0f);
+          sv[u] = make_float2(V.x * g.w, V.y * g.w);
+        } else {
+          sv[u] = scan_bin(st[u][v], sv[u], g, kh[u][v]);
+        }
+      }
+      dft_sym<H, true>(sv, r);
+#pragma unroll
+      for (int h = 0; h < H; ++h) R[h][v] = r[h];
+    }
+    // C2R rows, x z_gate, store y_t
+    float y[HW];
+#pragma unroll
+    for (int h = 0; h < H; ++h) small_row_c2r<W>(R[h], y + h * W);
+    if (vec) {
+      V4* y4 = reinterpret_cast<V4*>(yp + base);
+#pragma unroll
+      for (int k = 0; k < HW / 4; ++k)
+        y4[k] = IO::from_f4(make_float4(y[4 * k] * zg[4 * k], y[4 * k + 1] * zg[4 * k + 1],
+                                        y[4 * k + 2] * zg[4 * k + 2], y[4 * k + 3] * zg[4 * k + 3]));
+    } else {
+#pragma unroll
+      for (int e = 0; e < HW; ++e) yp[base + e] = IO::from_f(y[e] * zg[e]);
+    }
+  }
+}
+
+// ---------------------------------------------------------------------------
+// 4 x 4 planes: four lanes per (b, c) plane, lane h holding row h.  Each lane takes its row's
+// real DFT; the 4-point column DFTs are two radix-2 stages across the lane quad (DPP quad
+// permutes, no LDS), after which lane h holds spectrum row [0, 2, 1, 3][h]; the recurrence
+// runs on that row's three bins, the inverse column DFT undoes the stages (lane h back on
+// row h) and each lane applies the C2R rule to its row.  Every load and store is one 16-byte
+// row per lane: a wave moves 16 whole planes per instruction.
+// ---------------------------------------------------------------------------
+template <int CTRL>
+__device__ __forceinline__ float2 quad_xch(float2 v) {
+  return make_float2(__int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(v.x), CTRL, 0xf, 0xf, false)),
+                     __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(v.y), CTRL, 0xf, 0xf, false)));
+}
+
+template <class IO, bool ONE>
+__global__ void __launch_bounds__(256) gated_scan_quad4(const ScanArgs a, long long P) {
+  using V4 = typename IO::V4;
+  using TE = typename IO::T;
+  const long long gid = (long long)blockIdx.x * blockDim.x + threadIdx.x;
+  const long long pl = gid >> 2;
+  const int h = int(gid & 3);
+  if (pl >= P) return;   // whole quads leave together (P planes = 4 P lanes); no barriers below
+  const int T = a.T, C = a.C;
+  const int b = int(pl / C), c = int(pl % C);
+  const int uo = ((h & 1) << 1) | (h >> 1);   // the spectrum row this lane holds between the stages
+  const TE* __restrict__ up = static_cast<const TE*>(a.u);
+  const TE* __restrict__ zp = static_cast<const TE*>(a.z);
+  TE* __restrict__ yp = static_cast<TE*>(a.y);
+  float2 st[ONE ? 1 : 3], kh[ONE ? 1 : 3];
+  if constexpr (!ONE) {
+    const float2* kp = a.khat + size_t(c) * 12 + uo * 3;
+#pragma unroll
+    for (int v = 0; v < 3; ++v) {
+      kh[v] = kp[v];
+      st[v] = make_float2(0.f, 0.f);
+    }
+  }
+  const bool lo1 = (h & 1) == 0, lo2 = h < 2;
+  for (int t = 0; t < T; ++t) {
+    const size_t base = ((size_t(b) * T + t) * C + c) * 16 + 4 * h;
+    const float4 xu = act4(IO::to_f4(*reinterpret_cast<const V4*>(up + base)), a.u_act);
+    const float4 g = act4(IO::to_f4(*reinterpret_cast<const V4*>(zp + base)), a.z_act);
+    // row DFT of 2 u (the recurrence runs on 2U, as in the other scan kernels)
+    const float s02 = 2.0f * (xu.x + xu.z), d02 = 2.0f * (xu.x - xu.z);
+    const float s13 = 2.0f * (xu.y + xu.w), d13 = 2.0f * (xu.y - xu.w);
+    float2 R[3] = {make_float2(s02 + s13, 0.f), make_float2(d02, -d13), make_float2(s02 - s13, 0.f)};
+    const float4* gp = a.gates + (size_t(b) * T + t) * 12 + uo * 3;
+#pragma unroll
+    for (int v = 0; v < 3; ++v) {
+      // forward columns: h, h + 2 (sum on lanes 0, 1; difference on 2, 3), then h, h + 1
+      float2 o = quad_xch<0x4e>(R[v]);
+      float2 x = lo2 ? make_float2(R[v].x + o.x, R[v].y + o.y) : make_float2(o.x - R[v].x, o.y - R[v].y);
+      o = quad_xch<0xb1>(x);
+      float2 X;
+      if (h == 0) X = make_float2(x.x + o.x, x.y + o.y);            // X0 = a0 + a1
+      else if (h == 1) X = make_float2(o.x - x.x, o.y - x.y);       // X2 = a0 - a1
+      else if (h == 2) X = make_float2(x.x + o.y, x.y - o.x);       // X1 = s0 - i s1
+      else X = make_float2(o.x - x.y, o.y + x.x);                   // X3 = s0 + i s1
+      const float4 gg = gp[v];
+      if constexpr (ONE) {
+        float2 V = make_float2(X.x * gg.y, X.y * gg.y);
+        if (V.x * V.x + V.y * V.y < gg.z * gg.z) V = make_float2(gg.z, 0.0f);
+        X = make_float2(V.x * gg.w, V.y * gg.w);
+      } else {
+        X = scan_bin(st[v], X, gg, kh[v]);
+      }
+      // inverse columns: rows (0, 2), (1, 3) of the spectrum sit on lanes (0, 1), (2, 3)
+      o = quad_xch<0xb1>(X);
+      x = lo1 ? make_float2(X.x + o.x, X.y + o.y) : make_float2(o.x - X.x, o.y - X.y);
+      o = quad_xch<0x4e>(x);
+      if (h == 0) R[v] = make_float2(x.x + o.x, x.y + o.y);         // y0 = e0 + e1
+      else if (h == 2) R[v] = make_float2(o.x - x.x, o.y - x.y);    // y2 = e0 - e1
+      else if (h == 1) R[v] = make_float2(x.x - o.y, x.y + o.x);    // y1 = d0 + i d1
+      else R[v] = make_float2(o.x + x.y, o.y - x.x);                // y3 = d0 - i d1
+    }
+    // C2R of row h (numpy's rule: the middle bin twice, the Nyquist bin once)
+    const float z0 = R[0].x, zx1 = 2.0f * R[1].x, zy1 = 2.0f * R[1].y, z2 = R[2].x;
+    const float4 y = make_float4(z0 + zx1 + z2, (z0 - z2) - zy1, z0 - zx1 + z2, (z0 - z2) + zy1);
+    *reinterpret_cast<V4*>(yp + base) = IO::from_f4(make_float4(y.x * g.x, y.y * g.y, y.z * g.z, y.w * g.w));
+  }
+}
+
 // ----------------------------------------------------------------- launchers
 
 template <int LH, int LW, int NP, int PPT, class IO>
@@ -543,11 +736,27 @@ template <int H, class IO>
 static hipError_t run_small(const ScanArgs& a, int B, hipStream_t s) {
   using G = SmallGeom<H, H>;
   const long long P = (long long)B * a.C;
-  const dim3 grid(unsigned((P + G::NP - 1) / G::NP));
-  if (a.T == 1)
-    hipLaunchKernelGGL((gated_scan_small<H, H, IO, true>), grid, dim3(G::NT), 0, s, a, P);
-  else
-    hipLaunchKernelGGL((gated_scan_small<H, H, IO, false>), grid, dim3(G::NT), 0, s, a, P);
+  if constexpr (H == 4) {
+    // four lanes per plane
+    const dim3 grid(unsigned((4 * P + 255) / 256));
+    if (a.T == 1)
+      hipLaunchKernelGGL((gated_scan_quad4<IO, true>), grid, dim3(256), 0, s, a, P);
+    else
+      hipLaunchKernelGGL((gated_scan_quad4<IO, false>), grid, dim3(256), 0, s, a, P);
+  } else if constexpr (H * H <= 16) {
+    // one plane per thread
+    const dim3 grid(unsigned((P + 255) / 256));
+    if (a.T == 1)
+      hipLaunchKernelGGL((gated_scan_plane<H, H, IO, true>), grid, dim3(256), 0, s, a, P);
+    else
+      hipLaunchKernelGGL((gated_scan_plane<H, H, IO, false>), grid, dim3(256), 0, s, a, P);
+  } else {
+    const dim3 grid(unsigned((P + G::NP - 1) / G::NP));
+    if (a.T == 1)
+      hipLaunchKernelGGL((gated_scan_small<H, H, IO, true>), grid, dim3(G::NT), 0, s, a, P);
+    else
+      hipLaunchKernelGGL((gated_scan_small<H, H, IO, false>), grid, dim3(G::NT), 0, s, a, P);
+  }
   return hipGetLastError();
 }
 
