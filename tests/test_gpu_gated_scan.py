@@ -205,6 +205,8 @@ SCAN_CASES = [
     # between one batch element and two; at 3 x 3 / C = 301 some groups lie in one batch
     # element but start at an odd element (element path)
     (2, 3, 128, 7, 7), (1, 2, 40, 14, 14), (2, 2, 301, 3, 3),
+    # more even sizes, and groups whose last planes lie past P
+    (2, 3, 10, 10, 10), (1, 1, 7, 14, 14), (1, 4, 9, 12, 12),
 ]
 
 
