@@ -220,15 +220,25 @@ __host__ __device__ inline int gate_lds_floats(int C, int H, int W, int nt, bool
   const int scratch = factored ? (P * nv > 256 ? P * nv : 256) : 256;
   return C + (factored ? nv : 0) + scratch;
 }
+// the weights in LDS (WLDS) start at the next 16-byte boundary and take 3 C (H + WF) floats
+__host__ __device__ inline int gate_wlds_offset(int C, int H, int W, int nt) {
+  return (gate_lds_floats(C, H, W, nt, true) + 3) / 4 * 4;
+}
 
 // 512 threads per frame (two frames per CU at up to 128 VGPRs: a 512-frame batch in one pass),
 // each thread's weights loaded up front (up to 32 of them: 114 VGPRs)
 constexpr int kGateThreads = 512, kGateKW = 32;
-template <bool FACTORED>
+// WLDS (factored, the six weight arrays in 64 KB of LDS with 16-byte rows: C % 4 == 0, host-checked):
+// the workgroup first copies them into LDS as one run of 16-byte pieces, consecutive threads on
+// consecutive pieces, so every load covers whole cache lines; the per-product loads of
+// GateFactors touch a line for every few lanes, and at the CSSM-SHViT stages those line requests,
+// not the arithmetic, set the kernel's time.  The sums run in the same order either way.
+template <bool FACTORED, bool WLDS>
 __global__ void __launch_bounds__(kGateThreads, 4) gated_gates_kernel(const float* __restrict__ ctx, CtxPartials cp, int C,
                                                               int H, int W, int act, GateWeights gw, float c_scale,
                                                               float4* __restrict__ out) {
   constexpr bool factored = FACTORED;
+  static_assert(!WLDS || FACTORED, "weights in LDS for the factored products");
   extern __shared__ float sm_f[];
   const int WF = W / 2 + 1;
   const int bt = blockIdx.x;
@@ -236,7 +246,58 @@ __global__ void __launch_bounds__(kGateThreads, 4) gated_gates_kernel(const floa
   float* cx = sm_f;                                    // C
   float* fac = sm_f + C;                               // 3 (H + WF) factored vectors
   float* scratch = fac + (factored ? 3 * (H + WF) : 0);
-  if constexpr (factored) {
+  if constexpr (WLDS) {
+    const int nt = blockDim.x, tid = threadIdx.x;
+    const int nv = 3 * (H + WF);
+    const int P = nv >= nt ? 1 : nt / nv;
+    // [g][C x H row kernel][C x WF column kernel], 16-byte aligned after the scratch
+    float* Ws = sm_f + gate_wlds_offset(C, H, W, nt);
+    {
+      const int n4h = C * H / 4, n4 = n4h + C * WF / 4;
+      float4* W4 = reinterpret_cast<float4*>(Ws);
+#pragma unroll 4
+      for (int e = tid; e < 3 * n4; e += nt) {
+        const int g = e / n4, r = e % n4;
+        W4[e] = r < n4h ? reinterpret_cast<const float4*>(gw.kd[g])[r]
+                        : reinterpret_cast<const float4*>(gw.kw[g])[r - n4h];
+      }
+    }
+    frame_ctx(ctx, cp, bt, C, cx, scratch);   // (its barrier also publishes the weights)
+    const int idx = tid % nv, pc = tid / nv;
+    if (tid < nv * P) {
+      const int g = idx / (H + WF), r = idx % (H + WF);
+      const float* wl = Ws + g * C * (H + WF) + (r < H ? r : C * H + (r - H));
+      const int ws = r < H ? H : WF;
+      float acc = 0.0f;
+#pragma unroll 8
+      for (int c = pc; c < C; c += P) acc = fmaf(cx[c], wl[c * ws], acc);
+      scratch[pc * nv + idx] = acc;
+    }
+    for (int i = tid + nt; i < nv; i += nt) {   // products beyond the block's threads (P == 1)
+      const int g = i / (H + WF), r = i % (H + WF);
+      const float* wl = Ws + g * C * (H + WF) + (r < H ? r : C * H + (r - H));
+      const int ws = r < H ? H : WF;
+      float acc = 0.0f;
+#pragma unroll 8
+      for (int c = 0; c < C; ++c) acc = fmaf(cx[c], wl[c * ws], acc);
+      scratch[i] = acc;
+    }
+    __syncthreads();
+    for (int i = tid; i < nv; i += nt) {
+      const int g = i / (H + WF), r = i % (H + WF);
+      float acc = 0.0f;
+      for (int p = 0; p < P; ++p) acc += scratch[p * nv + i];
+      fac[i] = acc + (r < H ? gw.bd[g][r] : gw.bw[g][r - H]);
+    }
+    __syncthreads();
+    for (int o = threadIdx.x; o < nbin; o += blockDim.x) {
+      const int u = o / WF, v = scan_col(H, W, o % WF);
+      float gr[3];
+      for (int g = 0; g < 3; ++g) gr[g] = fac[g * (H + WF) + u] * fac[g * (H + WF) + H + v];
+      const float d = gate_act(gr[0], act), dd = d + 1e-8f;
+      out[size_t(bt) * nbin + o] = make_float4(expf(-d), dd * gr[1], dd * 2e-7f, gr[2] * c_scale);
+    }
+  } else if constexpr (factored) {
     GateFactors<kGateKW> gf;
     gf.prefetch(gw, C, H, WF);
     frame_ctx(ctx, cp, bt, C, cx, scratch);
@@ -462,11 +523,23 @@ hipError_t launch_gated_gates(const float* ctx, const CtxPartials& cp, int BT, i
   constexpr int NT = kGateThreads;
   const size_t shm = size_t(gate_lds_floats(C, H, W, NT, factored != 0)) * sizeof(float);
   if (shm > 64 * 1024) return hipErrorInvalidValue;
-  if (factored)
-    hipLaunchKernelGGL(gated_gates_kernel<true>, dim3(BT), dim3(NT), shm, s, ctx, cp, C, H, W, act, w, c_scale, gates);
-  else
-    hipLaunchKernelGGL(gated_gates_kernel<false>, dim3(BT), dim3(NT), shm, s, ctx, cp, C, H, W, act, w, c_scale,
-                       gates);
+  if (factored) {
+    // the weights through LDS where they fit with 16-byte rows
+    const int WF = W / 2 + 1;
+    const size_t shm_w = (size_t(gate_wlds_offset(C, H, W, NT)) + size_t(3) * C * (H + WF)) * sizeof(float);
+    bool wlds = C % 4 == 0 && shm_w <= 64 * 1024;
+    for (int g = 0; g < 3; ++g)
+      wlds = wlds && (reinterpret_cast<uintptr_t>(w.kd[g]) % 16) == 0 && (reinterpret_cast<uintptr_t>(w.kw[g]) % 16) == 0;
+    if (wlds)
+      hipLaunchKernelGGL((gated_gates_kernel<true, true>), dim3(BT), dim3(NT), shm_w, s, ctx, cp, C, H, W, act, w,
+                         c_scale, gates);
+    else
+      hipLaunchKernelGGL((gated_gates_kernel<true, false>), dim3(BT), dim3(NT), shm, s, ctx, cp, C, H, W, act, w,
+                         c_scale, gates);
+  } else {
+    hipLaunchKernelGGL((gated_gates_kernel<false, false>), dim3(BT), dim3(NT), shm, s, ctx, cp, C, H, W, act, w,
+                       c_scale, gates);
+  }
   return hipGetLastError();
 }
 
