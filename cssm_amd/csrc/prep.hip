@@ -155,21 +155,25 @@ __device__ __forceinline__ void frame_ctx(const float* __restrict__ ctx, const C
 // barrier that publishes cx and ends with one.
 template <int KW>
 struct GateFactors {
-  int nv, P, idx, pc, ws;
+  int nv, P, idx, pc, ws, u0, nr;
   bool mine;
   const float* wc;
   float wr[KW];
 
-  __device__ __forceinline__ void prefetch(const GateWeights& gw, int C, int H, int WF) {
+  // the row products of rows u0 .. u0 + nr - 1 and all column products: fac[g (nr + WF) + r]
+  // (rows r < nr, columns nr + v)
+  __device__ __forceinline__ void prefetch(const GateWeights& gw, int C, int H, int WF, int u0_, int nr_) {
     const int nt = blockDim.x, q = threadIdx.x;
-    nv = 3 * (H + WF);
+    u0 = u0_;
+    nr = nr_;
+    nv = 3 * (nr + WF);
     P = nv >= nt ? 1 : nt / nv;
     idx = q % nv;
     pc = q / nv;
     mine = q < nv * P;
-    const int g = idx / (H + WF), r = idx % (H + WF);
-    wc = r < H ? gw.kd[g] + r : gw.kw[g] + (r - H);
-    ws = r < H ? H : WF;
+    const int g = idx / (nr + WF), r = idx % (nr + WF);
+    wc = r < nr ? gw.kd[g] + (u0 + r) : gw.kw[g] + (r - nr);
+    ws = r < nr ? H : WF;
 #pragma unroll
     for (int k = 0; k < KW; ++k) {
       const int c = pc + k * P;
@@ -194,9 +198,9 @@ struct GateFactors {
     }
     // products beyond the block's threads (nv > blockDim: one part each, no prefetch)
     for (int i = q + nt; i < nv; i += nt) {
-      const int g = i / (H + WF), r = i % (H + WF);
-      const float* w = r < H ? gw.kd[g] + r : gw.kw[g] + (r - H);
-      const int s = r < H ? H : WF;
+      const int g = i / (nr + WF), r = i % (nr + WF);
+      const float* w = r < nr ? gw.kd[g] + (u0 + r) : gw.kw[g] + (r - nr);
+      const int s = r < nr ? H : WF;
       float acc = 0.0f;
 #pragma unroll 8
       for (int c = 0; c < C; ++c) acc = fmaf(cx[c], w[size_t(c) * s], acc);
@@ -204,21 +208,22 @@ struct GateFactors {
     }
     __syncthreads();
     for (int i = q; i < nv; i += nt) {
-      const int g = i / (H + WF), r = i % (H + WF);
+      const int g = i / (nr + WF), r = i % (nr + WF);
       float acc = 0.0f;
       for (int p = 0; p < P; ++p) acc += part[p * nv + i];
-      fac[i] = acc + (r < H ? gw.bd[g][r] : gw.bw[g][r - H]);
+      fac[i] = acc + (r < nr ? gw.bd[g][u0 + r] : gw.bw[g][r - nr]);
     }
     __syncthreads();
   }
 };
 
-// LDS of the gate kernels: cx (C), fac (nv), then max(P nv, 256) floats of scratch
+// LDS of the gate kernels: cx (C), fac (nv), then max(nv, threads, 256) floats of scratch (the P nv
+// parts of any row window: P nv <= threads whenever nv < threads)
 __host__ __device__ inline int gate_lds_floats(int C, int H, int W, int nt, bool factored) {
   const int WF = W / 2 + 1, nv = 3 * (H + WF);
-  const int P = nv >= nt ? 1 : nt / nv;
-  const int scratch = factored ? (P * nv > 256 ? P * nv : 256) : 256;
-  return C + (factored ? nv : 0) + scratch;
+  int scratch = nv > nt ? nv : nt;
+  if (scratch < 256) scratch = 256;
+  return C + (factored ? nv : 0) + (factored ? scratch : 256);
 }
 // the weights in LDS (WLDS) start at the next 16-byte boundary and take 3 C (H + WF) floats
 __host__ __device__ inline int gate_wlds_offset(int C, int H, int W, int nt) {
@@ -233,10 +238,13 @@ constexpr int kGateThreads = 512, kGateKW = 32;
 // consecutive pieces, so every load covers whole cache lines; the per-product loads of
 // GateFactors touch a line for every few lanes, and at the CSSM-SHViT stages those line requests,
 // not the arithmetic, set the kernel's time.  The sums run in the same order either way.
+// Few frames (a small batch): each frame's rows are split over gridDim.y workgroups of nr rows
+// (blockIdx.y), each computing its rows' products and all column products (the latter in every
+// workgroup of the frame) and writing its rows' bins; ctx is written by the first of them.
 template <bool FACTORED, bool WLDS>
 __global__ void __launch_bounds__(kGateThreads, 4) gated_gates_kernel(const float* __restrict__ ctx, CtxPartials cp, int C,
                                                               int H, int W, int act, GateWeights gw, float c_scale,
-                                                              float4* __restrict__ out) {
+                                                              float4* __restrict__ out, int nr_split) {
   constexpr bool factored = FACTORED;
   static_assert(!WLDS || FACTORED, "weights in LDS for the factored products");
   extern __shared__ float sm_f[];
@@ -298,14 +306,18 @@ __global__ void __launch_bounds__(kGateThreads, 4) gated_gates_kernel(const floa
       out[size_t(bt) * nbin + o] = make_float4(expf(-d), dd * gr[1], dd * 2e-7f, gr[2] * c_scale);
     }
   } else if constexpr (factored) {
+    const int u0 = int(blockIdx.y) * nr_split;
+    const int nr = H - u0 < nr_split ? H - u0 : nr_split;
+    CtxPartials cpb = cp;
+    if (blockIdx.y != 0) cpb.ctx = nullptr;
     GateFactors<kGateKW> gf;
-    gf.prefetch(gw, C, H, WF);
-    frame_ctx(ctx, cp, bt, C, cx, scratch);
+    gf.prefetch(gw, C, H, WF, u0, nr);
+    frame_ctx(ctx, cpb, bt, C, cx, scratch);
     gf.finish(gw, cx, C, H, WF, fac, scratch);
-    for (int o = threadIdx.x; o < nbin; o += blockDim.x) {
-      const int u = o / WF, v = scan_col(H, W, o % WF);
+    for (int o = u0 * WF + threadIdx.x; o < (u0 + nr) * WF; o += blockDim.x) {
+      const int ur = o / WF - u0, v = scan_col(H, W, o % WF);
       float gr[3];
-      for (int g = 0; g < 3; ++g) gr[g] = fac[g * (H + WF) + u] * fac[g * (H + WF) + H + v];
+      for (int g = 0; g < 3; ++g) gr[g] = fac[g * (nr + WF) + ur] * fac[g * (nr + WF) + nr + v];
       const float d = gate_act(gr[0], act), dd = d + 1e-8f;
       out[size_t(bt) * nbin + o] = make_float4(expf(-d), dd * gr[1], dd * 2e-7f, gr[2] * c_scale);
     }
@@ -397,7 +409,7 @@ __global__ void __launch_bounds__(1024) gated_gates_bwd_kernel(const float* __re
   float* colp = sm_f + gate_lds_floats(C, H, W, int(blockDim.x), true);   // S * WF * 3 column partial sums
   {
     GateFactors<16> gf;
-    gf.prefetch(gw, C, H, WF);
+    gf.prefetch(gw, C, H, WF, 0, H);
     frame_ctx(ctx, CtxPartials{nullptr, 0, 0, 0, nullptr}, bt, C, cx, scratch);
     gf.finish(gw, cx, C, H, WF, fac, scratch);
   }
@@ -530,15 +542,25 @@ hipError_t launch_gated_gates(const float* ctx, const CtxPartials& cp, int BT, i
     bool wlds = C % 4 == 0 && shm_w <= 64 * 1024;
     for (int g = 0; g < 3; ++g)
       wlds = wlds && (reinterpret_cast<uintptr_t>(w.kd[g]) % 16) == 0 && (reinterpret_cast<uintptr_t>(w.kw[g]) % 16) == 0;
-    if (wlds)
+    if (wlds) {
       hipLaunchKernelGGL((gated_gates_kernel<true, true>), dim3(BT), dim3(NT), shm_w, s, ctx, cp, C, H, W, act, w,
-                         c_scale, gates);
-    else
-      hipLaunchKernelGGL((gated_gates_kernel<true, false>), dim3(BT), dim3(NT), shm, s, ctx, cp, C, H, W, act, w,
-                         c_scale, gates);
+                         c_scale, gates, H);
+    } else {
+      // fewer frames than two per CU: split each frame's rows over more workgroups
+      int dev = 0, cus = 256;
+      if (hipGetDevice(&dev) != hipSuccess ||
+          hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess)
+        cus = 256;
+      int splits = BT < 2 * cus ? (2 * cus + BT - 1) / BT : 1;
+      if (splits > H) splits = H;
+      const int nr = (H + splits - 1) / splits;
+      splits = (H + nr - 1) / nr;
+      hipLaunchKernelGGL((gated_gates_kernel<true, false>), dim3(BT, splits), dim3(NT), shm, s, ctx, cp, C, H, W,
+                         act, w, c_scale, gates, nr);
+    }
   } else {
     hipLaunchKernelGGL((gated_gates_kernel<false, false>), dim3(BT), dim3(NT), shm, s, ctx, cp, C, H, W, act, w,
-                       c_scale, gates);
+                       c_scale, gates, H);
   }
   return hipGetLastError();
 }
