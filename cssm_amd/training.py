@@ -275,13 +275,13 @@ class _GatedInScanFn(torch.autograd.Function):
         gates = S.gated_gates(cx.view(B, T, Ci), rebuild(list(gate_params)), H, W, gate_type, activation, c_scale)
         khat = S.spectral_kernel(kernel, H, W, rho, goom_floor=True, scan_order=True)
         y = S.gated_scan(xm.view(B, T, Ci, H, W), z.view(B, T, Ci, H, W), gates, khat, u_silu=True, z_silu=True)
-        ctx.save_for_backward(x2, w_in, xm, z, cx, kernel, *gate_params)
+        ctx.save_for_backward(x2, w_in, xm, z, cx, kernel, khat, *gate_params)
         ctx.meta = meta
         return y
 
     @staticmethod
     def backward(ctx, dy):
-        x2, w_in, xm, z, cx, kernel, *gate_params = ctx.saved_tensors
+        x2, w_in, xm, z, cx, kernel, khat_f, *gate_params = ctx.saved_tensors
         B, T, H, W, Ci, gate_type, activation, rho, rebuild = ctx.meta
         F, HW, Wf = B * T, H * W, W // 2 + 1
         K = x2.shape[1]
@@ -299,8 +299,8 @@ class _GatedInScanFn(torch.autograd.Function):
         sdu = torch.empty_like(uspec)
         dgates = torch.empty_like(gates_c)
         dkh = torch.empty((B, Ci, H, Wf), dtype=torch.complex64, device=dy.device)
-        S.gated_scan_bwd_bins(uspec, dspec, gates_c, khat.detach().contiguous(), B, T, Ci, H, W, c_scale, yspec,
-                              sdu, dgates, dkh)
+        # the reverse recurrence on the forward's own K_hat; torch's construction only differentiates it
+        S.gated_scan_bwd_bins(uspec, dspec, gates_c, khat_f, B, T, Ci, H, W, c_scale, yspec, sdu, dgates, dkh)
         del uspec, dspec, gates_c
         (dk,) = torch.autograd.grad([khat], [k_l], [dkh.sum(dim=0)])
         # the gate pre-activations' gradients (cssm_gated_gates_bwd), then the projections' as GEMMs
