@@ -244,8 +244,8 @@ def gdn_step(cell, variables, x, w, S, mark):
     ab, bkv = S.gdn_gates(ctx, p, H, W, cell.delta_key_dim, cell.gate_type, True, "sinusoid", cell.rope_base)
     mark("gates")
     convs = [p["short_conv_q"], p["short_conv_k"], p["short_conv_v"]]
-    # bf16 input: the output projection computes gate_proj from x itself (no gate planes in HBM)
-    xgate = x.dtype == torch.bfloat16 and S.gdn_proj_out_xgate_supported(C, C, HW)
+    # the output projection computes gate_proj from x itself (no gate planes in HBM)
+    xgate = S.gdn_proj_out_xgate_supported(C, C, HW)
     gv = None
     if cell.qkv_conv_size > 1 or xgate:
         qkv = S.gdn_qkv_proj(xq, p["qkv_proj"]["kernel"], p["qkv_proj"]["bias"], B, T, H, W, convs, 1, bkv,

@@ -10,7 +10,7 @@ import os
 import threading
 
 LIB_PATH = os.path.join(os.path.dirname(os.path.abspath(__file__)), "libcssm_hip.so")
-ABI_VERSION = 7   # CSSM_ABI_VERSION of the include/cssm_amd.h these bindings follow
+ABI_VERSION = 8   # CSSM_ABI_VERSION of the include/cssm_amd.h these bindings follow
 
 CSSM_OK = 0
 F32, BF16 = 0, 1
@@ -111,7 +111,7 @@ SIGNATURES = {
     "cssm_gdn_scan_bins_train": (_I, [_P, _P, _LL, _I, _I, _P, _I, _I, _I, _I, _I, _I, _I, _P, _P, _P]),
     "cssm_gdn_scan_bins_bwd": (_I, [_P, _P, _LL, _I, _I, _P, _P, _P, _I, _I, _I, _I, _I, _I, _I, _P, _P, _P, _P]),
     "cssm_gdn_proj_out": (_I, [_P, _P, _I, _I, _I, _I, _I, _I, _P, _P, _P, _P, _P, _I, _P]),
-    "cssm_gdn_proj_out_xgate": (_I, [_P, _I, _P, _I, _I, _I, _I, _I, _P, _P, _P, _P, _I, _P, _P, _P, _I, _P]),
+    "cssm_gdn_proj_out_xgate": (_I, [_P, _I, _P, _I, _I, _I, _I, _I, _I, _P, _P, _P, _P, _I, _P, _P, _P, _I, _P]),
     "cssm_gdn_proj_out_xgate_supported": (_I, [_I, _I, _I]),
     "cssm_gdn_core_fused": (_I, [_P, _I, _P, _LL, _I, _I, _P, _I, _I, _I, _I, _I, _I, _I, _P, _P]),
     "cssm_gdn_core_fused_supported": (_I, [_I, _I, _I]),

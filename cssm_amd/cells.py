@@ -428,11 +428,11 @@ class GatedDeltaNetCSSM:
         convs = None
         if self.short_conv_size > 0:
             convs = [p["short_conv_q"], p["short_conv_k"], p["short_conv_v"]]
-        # qkv_proj with the short conv, SiLU and input gates in its epilogue.  gate_proj: with a bf16 layer
-        # input the output projection computes it from x (its planes never reach HBM); otherwise, without
+        # qkv_proj with the short conv, SiLU and input gates in its epilogue.  gate_proj: where the widths
+        # allow, the output projection computes it from x (its planes never reach HBM); otherwise, without
         # the qkv conv, as more columns of the qkv launch (x read once), else a projection of its own
         gact = "silu" if self.output_gate_act == "silu" else "sigmoid"
-        xgate = x.dtype == torch.bfloat16 and S.gdn_proj_out_xgate_supported(C, C, HW)
+        xgate = S.gdn_proj_out_xgate_supported(C, C, HW)
         gv = None
         if full_conv:
             # k x k conv with full channel mixing (im2col rows through the projection GEMM), then the

@@ -746,7 +746,7 @@ int cssm_gdn_proj_out(const void* o, const void* gate, int in_dtype, int F, int 
 
 int cssm_gdn_proj_out_xgate_supported(int K, int N, int HW) { return cssm::proj_out_xgate_supported(K, N, HW) ? 1 : 0; }
 
-int cssm_gdn_proj_out_xgate(const void* o, int in_dtype, const void* x, int F, int HW, int K, int N, int norm,
+int cssm_gdn_proj_out_xgate(const void* o, int in_dtype, const void* x, int x_dtype, int F, int HW, int K, int N, int norm,
                             const float* norm_scale, const float* norm_bias, const float* gate_kernel,
                             const float* gate_bias, int gate_act, const float* kernel, const float* bias, void* out,
                             int out_dtype, void* stream) {
@@ -758,16 +758,16 @@ int cssm_gdn_proj_out_xgate(const void* o, int in_dtype, const void* x, int F, i
     return fail(CSSM_ERR_UNSUPPORTED, "cssm_gdn_proj_out_xgate: needs K <= 64, K %% 8 == 0, N <= 64, HW %% 4 == 0 "
                 "(K=%d N=%d HW=%d)", K, N, HW);
   if ((long long)F * HW > 0x7fffffffLL) return fail(CSSM_ERR_SHAPE, "cssm_gdn_proj_out_xgate: F*HW exceeds 2^31");
-  if (!dtype_ok(in_dtype) || !dtype_ok(out_dtype))
-    return fail(CSSM_ERR_ARG, "cssm_gdn_proj_out_xgate: dtypes %d/%d", in_dtype, out_dtype);
+  if (!dtype_ok(in_dtype) || !dtype_ok(out_dtype) || !dtype_ok(x_dtype))
+    return fail(CSSM_ERR_ARG, "cssm_gdn_proj_out_xgate: dtypes %d/%d/%d", in_dtype, x_dtype, out_dtype);
   if (norm < CSSM_NORM_NONE || norm > CSSM_NORM_LAYER) return fail(CSSM_ERR_ARG, "cssm_gdn_proj_out_xgate: norm=%d", norm);
   if (gate_act != 1 && gate_act != 2) return fail(CSSM_ERR_ARG, "cssm_gdn_proj_out_xgate: gate_act=%d", gate_act);
   const size_t va = in_dtype == CSSM_F32 ? 16 : 8;
   if (!aligned(o, va) || !aligned(x, 16) || (out_dtype == CSSM_F32 && !aligned(out, 16)))
     return fail(CSSM_ERR_ALIGN, "cssm_gdn_proj_out_xgate: misaligned o / x / out");
-  return hip_status(cssm::launch_proj_out_norm_xgate(o, in_dtype, static_cast<const uint16_t*>(x), F * HW, K, N, norm,
-                                                     norm_scale, norm_bias, gate_kernel, gate_bias, gate_act, kernel,
-                                                     bias, HW, out, out_dtype, static_cast<hipStream_t>(stream)),
+  return hip_status(cssm::launch_proj_out_norm_xgate(o, in_dtype, x, x_dtype, F * HW, K, N, norm, norm_scale,
+                                                     norm_bias, gate_kernel, gate_bias, gate_act, kernel, bias, HW,
+                                                     out, out_dtype, static_cast<hipStream_t>(stream)),
                     "cssm_gdn_proj_out_xgate");
 }
 

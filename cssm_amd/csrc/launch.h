@@ -108,12 +108,13 @@ hipError_t launch_proj_planes(const void* X, int in_dtype, int M, int K, int N, 
 hipError_t launch_proj_out_norm_gate(const void* Y, const void* G, int in_dtype, int M, int K, int N, int norm,
                                      const float* nscale, const float* nshift, const float* W, const float* b, int HW,
                                      void* out, int out_dtype, hipStream_t s);
-// the same with the gate act(X wg + bg) computed in the kernel from the bf16 layer input X (proj.hip)
+// the same with the gate act(X wg + bg) computed in the kernel from the layer input X (x_dtype 0: f32,
+// 1: bf16) (proj.hip)
 bool proj_out_xgate_supported(int K, int N, int HW);
-hipError_t launch_proj_out_norm_xgate(const void* Y, int in_dtype, const uint16_t* X, int M, int K, int N, int norm,
-                                      const float* nscale, const float* nshift, const float* wg, const float* bg,
-                                      int gact, const float* W, const float* b, int HW, void* out, int out_dtype,
-                                      hipStream_t s);
+hipError_t launch_proj_out_norm_xgate(const void* Y, int in_dtype, const void* X, int x_dtype, int M, int K, int N,
+                                      int norm, const float* nscale, const float* nshift, const float* wg,
+                                      const float* bg, int gact, const float* W, const float* b, int HW, void* out,
+                                      int out_dtype, hipStream_t s);
 hipError_t launch_ctx_reduce(const float* partial, int F, int HW, int tile_rows, int slots, int C, float* ctx,
                              hipStream_t s);
 

@@ -266,7 +266,10 @@ __global__ void __launch_bounds__(256) ctx_reduce_kernel(const float* __restrict
 //   layer input, G = act(X Wg + bg) (gate_proj, cssm.py:4853-4859), X the
 //   tile's channels-last bf16 rows staged in LDS next to A, on bf16 MFMA with
 //   Wg split into three bf16 parts (X is exactly its one part), then applied
-//   with the norm in the MFMA output layout.
+//   with the norm in the MFMA output layout.  XF: fp32 X, each lane's
+//   fragments (8 channels of one row, 32 bytes) loaded straight from the rows
+//   into registers (no LDS: a staged fp32 tile would leave room for one
+//   workgroup per CU) and split into three bf16 parts, six products.
 // ---------------------------------------------------------------------------
 struct NormGate {
   const void* G;        // plane-major (F, K, HW) gate, same dtype as A
@@ -274,6 +277,7 @@ struct NormGate {
   const float* shift;   // (K) or nullptr (LayerNorm bias)
   int kind;             // 0 none, 1 rms, 2 layer
   const uint16_t* X;    // XG: channels-last (M, K) bf16 layer input
+  const float* Xf;      // XG with XF: the same in fp32
   const float* wg;      // XG: (K, K) gate_proj kernel
   const float* bg;      // XG: (K) its bias
   int gact;             // XG: 1 SiLU, 2 sigmoid
@@ -307,7 +311,7 @@ struct QkvPost {
 };
 
 template <int KMAX, bool PLANE_A, bool OUT_SPLIT, int WN, class TI, class TO, bool NORM = false, bool SPLIT = false,
-          int TT = 0, bool CARRY = false, bool PX1 = false, bool XG = false>
+          int TT = 0, bool CARRY = false, bool PX1 = false, bool XG = false, bool XF = false>
 __global__ void __launch_bounds__(256, 2)
 proj_persist_kernel(const TI* __restrict__ A, int M, int K, int N, const float* __restrict__ Wt,
                     const float* __restrict__ bias, int HW, TO* __restrict__ out_lo, TO* __restrict__ out_hi,
@@ -327,6 +331,7 @@ proj_persist_kernel(const TI* __restrict__ A, int M, int K, int N, const float* 
   constexpr bool NSPLIT = NORM && KMAX == 64 && !PX1 && !XG;
   constexpr bool MSPLIT = SPLIT || NSPLIT;   // the product on split-bf16 MFMA, weight fragments in VGPRs
   static_assert(!XG || (NORM && KMAX == 64 && !PX1 && WN == 2), "computed gate: K <= 64 channels, N <= 64 columns");
+  static_assert(!XF || XG, "fp32 x for the computed gate");
   static_assert(!SPLIT || KMAX % 32 == 0, "bf16 MFMA k-blocks of 32");
   constexpr int AP = PLANE_A ? (TM + 16) : (KMAX + 2);   // pitch: rows of A (row-major) or k-rows (plane)
   constexpr int BP = TN + 16;
@@ -348,7 +353,7 @@ proj_persist_kernel(const TI* __restrict__ A, int M, int K, int N, const float* 
   __bf16* const A3 = A2 + TM * KP;
   __shared__ float rowsc[NORM ? 2 * NT : 1];             // per-pixel partial sums, then (scale, mean) of the norm
   __shared__ float nss[NORM ? 2 * KMAX : 1];             // the norm's per-channel scale and shift
-  __shared__ __attribute__((aligned(16))) __bf16 Xs[XG ? TM * KP : 8];   // XG: the tile's X rows [row][k]
+  __shared__ __attribute__((aligned(16))) __bf16 Xs[(XG && !XF) ? TM * KP : 8];   // XG: the tile's X rows [row][k]
   __shared__ float2 gsh[TT > 0 ? TM : 1];                 // qkv epilogue: the tile's input gates
   constexpr int KH = 3;                                   // qkv epilogue: frames carried to the next chunk
   __shared__ float hsh[CARRY ? KH * TN * (TM / 8) : 1];   // their projections, [frame][column][pixel]
@@ -673,10 +678,10 @@ proj_persist_kernel(const TI* __restrict__ A, int M, int K, int N, const float* 
     }
   };
   // XG: the tile's X rows, 16-byte pieces c = i NT + tid: row c / (KMAX / 8), channels 8 (c % (KMAX / 8)) ..
-  constexpr int PX = XG ? TM * KMAX / 8 / NT : 1;
+  constexpr int PX = (XG && !XF) ? TM * KMAX / 8 / NT : 1;
   uint4 px[PX];
   auto fetch_x = [&](int tile) {
-    if constexpr (XG) {
+    if constexpr (XG && !XF) {
       const int m0 = tile * TM;
 #pragma unroll
       for (int i = 0; i < PX; ++i) {
@@ -687,7 +692,7 @@ proj_persist_kernel(const TI* __restrict__ A, int M, int K, int N, const float* 
     }
   };
   auto stash_x = [&]() {
-    if constexpr (XG) {
+    if constexpr (XG && !XF) {
 #pragma unroll
       for (int i = 0; i < PX; ++i) {
         const int c = i * NT + tid, r = c / (KMAX / 8), k8 = (c % (KMAX / 8)) * 8;
@@ -699,8 +704,57 @@ proj_persist_kernel(const TI* __restrict__ A, int M, int K, int N, const float* 
   // (the MFMA output layout), issued before the norm's statistics so the MFMAs run under them; then
   // A <- norm(A) * act(x Wg + bg) for exactly those elements
   floatx4 ag[XG ? MI : 1][2];
-  auto xgate_mma = [&]() {
-    if constexpr (XG) {
+  // XF: this wave's fp32 x fragments of a tile (rows past M and channels past K read as 0; K % 8 == 0,
+  // host-checked), issued at the top of the tile so they land during its stash and barriers
+  float4 xr[XF ? MI : 1][XF ? KB : 1][2];
+  auto xf_fetch = [&](int tile) {
+    if constexpr (XF) {
+#pragma unroll
+      for (int i = 0; i < MI; ++i) {
+        const int row = tile * TM + (wm * MI + i) * 16 + (lane & 15);
+#pragma unroll
+        for (int kb = 0; kb < KB; ++kb) {
+          const int k8 = kb * 32 + (lane >> 4) * 8;
+          const bool ok = row < M && k8 < K;
+          const float4* src = reinterpret_cast<const float4*>(ng.Xf + size_t(ok ? row : 0) * K + (ok ? k8 : 0));
+          xr[i][kb][0] = ok ? src[0] : make_float4(0.f, 0.f, 0.f, 0.f);
+          xr[i][kb][1] = ok ? src[1] : make_float4(0.f, 0.f, 0.f, 0.f);
+        }
+      }
+    }
+  };
+  auto xgate_mma = [&](int tile) {
+    if constexpr (XF) {
+      // fp32 x: each fragment split into three bf16 parts, six products with the gate weights' parts
+      (void)tile;
+#pragma unroll
+      for (int i = 0; i < MI; ++i) {
+        ag[i][0] = ag[i][1] = floatx4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+        for (int kb = 0; kb < KB; ++kb) {
+          if (kb * 32 >= K) break;
+          bf16x8 x1, x2, x3;
+#pragma unroll
+          for (int e = 0; e < 8; ++e) {
+            __bf16 a1, a2, a3;
+            split3_bf16(e < 4 ? (&xr[i][kb][0].x)[e] : (&xr[i][kb][1].x)[e - 4], a1, a2, a3);
+            x1[e] = a1;
+            x2[e] = a2;
+            x3[e] = a3;
+          }
+#pragma unroll
+          for (int j = 0; j < 2; ++j) {
+            floatx4 c = ag[i][j];
+            c = __builtin_amdgcn_mfma_f32_16x16x32_bf16(x3, g1[j][kb], c, 0, 0, 0);   // small terms first
+            c = __builtin_amdgcn_mfma_f32_16x16x32_bf16(x2, g2[j][kb], c, 0, 0, 0);
+            c = __builtin_amdgcn_mfma_f32_16x16x32_bf16(x1, g3[j][kb], c, 0, 0, 0);
+            c = __builtin_amdgcn_mfma_f32_16x16x32_bf16(x2, g1[j][kb], c, 0, 0, 0);
+            c = __builtin_amdgcn_mfma_f32_16x16x32_bf16(x1, g2[j][kb], c, 0, 0, 0);
+            ag[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(x1, g1[j][kb], c, 0, 0, 0);
+          }
+        }
+      }
+    } else if constexpr (XG) {
 #pragma unroll
       for (int i = 0; i < MI; ++i) ag[i][0] = ag[i][1] = floatx4{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
@@ -829,6 +883,7 @@ proj_persist_kernel(const TI* __restrict__ A, int M, int K, int N, const float* 
     else if (NORM) fetch(Gp, tile, pg);
   }
   for (; tile < tiles; tile = tile_of(++kt_)) {
+    xf_fetch(tile);
     __syncthreads();            // previous tile is done with As, Xs, gsh (and Bs is staged)
     stash(pf);
     stash_x();
@@ -837,7 +892,7 @@ proj_persist_kernel(const TI* __restrict__ A, int M, int K, int N, const float* 
     }
     __syncthreads();
     if constexpr (NORM) {
-      xgate_mma();    // XG: x Wg, under the statistics
+      xgate_mma(tile);    // XG: x Wg, under the statistics
       norm_gate(pg);  // the per-pixel statistics (without NSPLIT / XG also the norm x gate in place)
       xgate_norm();   // XG: norm x computed gate in place
       norm_split();   // NSPLIT: norm x gate into the bf16 planes
@@ -2236,30 +2291,38 @@ hipError_t launch_proj_out_norm_gate(const void* Y, const void* G, int in_dtype,
 // kernel (K <= 64, K % 8 == 0, N <= 64, HW % 4 == 0; else invalid value)
 bool proj_out_xgate_supported(int K, int N, int HW) { return K <= 64 && K % 8 == 0 && N <= 64 && HW % 4 == 0; }
 
-template <class TI, class TO>
-static void launch_xgate(const void* Y, const uint16_t* X, int M, int K, int N, const NormGate& ng, const float* W,
-                         const float* b, int HW, void* out, hipStream_t s) {
+template <class TI, class TO, bool XF>
+static void launch_xgate(const void* Y, int M, int K, int N, const NormGate& ng, const float* W, const float* b, int HW,
+                         void* out, hipStream_t s) {
   const int tiles = (M + kPersistTM - 1) / kPersistTM;
   const dim3 grid(unsigned(persistent_grid(tiles)), 1);
-  hipLaunchKernelGGL((proj_persist_kernel<64, true, false, 2, TI, TO, true, false, 0, false, false, true>), grid,
+  hipLaunchKernelGGL((proj_persist_kernel<64, true, false, 2, TI, TO, true, false, 0, false, false, true, XF>), grid,
                      dim3(256), 0, s, static_cast<const TI*>(Y), M, K, N, W, b, HW, static_cast<TO*>(out), nullptr, 0,
                      0, nullptr, N, ng, QkvPost{});
 }
 
-hipError_t launch_proj_out_norm_xgate(const void* Y, int in_dtype, const uint16_t* X, int M, int K, int N, int norm,
-                                      const float* nscale, const float* nshift, const float* wg, const float* bg,
-                                      int gact, const float* W, const float* b, int HW, void* out, int out_dtype,
-                                      hipStream_t s) {
+hipError_t launch_proj_out_norm_xgate(const void* Y, int in_dtype, const void* X, int x_dtype, int M, int K, int N,
+                                      int norm, const float* nscale, const float* nshift, const float* wg,
+                                      const float* bg, int gact, const float* W, const float* b, int HW, void* out,
+                                      int out_dtype, hipStream_t s) {
   if (!proj_out_xgate_supported(K, N, HW)) return hipErrorInvalidValue;
   NormGate ng{nullptr, nscale, nshift, norm};
-  ng.X = X;
+  ng.X = x_dtype == 0 ? nullptr : static_cast<const uint16_t*>(X);
+  ng.Xf = x_dtype == 0 ? static_cast<const float*>(X) : nullptr;
   ng.wg = wg;
   ng.bg = bg;
   ng.gact = gact;
-  if (in_dtype == 0 && out_dtype == 0) launch_xgate<float, float>(Y, X, M, K, N, ng, W, b, HW, out, s);
-  else if (in_dtype == 0) launch_xgate<float, uint16_t>(Y, X, M, K, N, ng, W, b, HW, out, s);
-  else if (out_dtype == 0) launch_xgate<uint16_t, float>(Y, X, M, K, N, ng, W, b, HW, out, s);
-  else launch_xgate<uint16_t, uint16_t>(Y, X, M, K, N, ng, W, b, HW, out, s);
+  if (x_dtype == 0) {
+    if (in_dtype == 0 && out_dtype == 0) launch_xgate<float, float, true>(Y, M, K, N, ng, W, b, HW, out, s);
+    else if (in_dtype == 0) launch_xgate<float, uint16_t, true>(Y, M, K, N, ng, W, b, HW, out, s);
+    else if (out_dtype == 0) launch_xgate<uint16_t, float, true>(Y, M, K, N, ng, W, b, HW, out, s);
+    else launch_xgate<uint16_t, uint16_t, true>(Y, M, K, N, ng, W, b, HW, out, s);
+  } else {
+    if (in_dtype == 0 && out_dtype == 0) launch_xgate<float, float, false>(Y, M, K, N, ng, W, b, HW, out, s);
+    else if (in_dtype == 0) launch_xgate<float, uint16_t, false>(Y, M, K, N, ng, W, b, HW, out, s);
+    else if (out_dtype == 0) launch_xgate<uint16_t, float, false>(Y, M, K, N, ng, W, b, HW, out, s);
+    else launch_xgate<uint16_t, uint16_t, false>(Y, M, K, N, ng, W, b, HW, out, s);
+  }
   return hipGetLastError();
 }
 

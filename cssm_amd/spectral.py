@@ -859,10 +859,13 @@ def gdn_proj_out_xgate(o: torch.Tensor, x: torch.Tensor, norm: str, norm_scale: 
                        norm_bias: Optional[torch.Tensor], gate_kernel: torch.Tensor, gate_bias: torch.Tensor,
                        gate_act: str, kernel: torch.Tensor, bias: torch.Tensor,
                        out_dtype: Optional[torch.dtype] = None) -> torch.Tensor:
-    """:func:`gdn_proj_out` with the gate computed in the kernel from the bf16 layer input x (F hw rows of K
-    channels): gate = SiLU / sigmoid(x gate_kernel + gate_bias) (gate_proj, cssm.py:4853-4859)."""
+    """:func:`gdn_proj_out` with the gate computed in the kernel from the layer input x (F hw rows of K
+    channels, float32 or bfloat16): gate = SiLU / sigmoid(x gate_kernel + gate_bias) (gate_proj,
+    cssm.py:4853-4859)."""
     _dev(o, "o")
-    _dev(x, "x", torch.bfloat16)
+    _dev(x, "x")
+    if x.dtype not in _DTYPES:
+        raise ValueError(f"unsupported x dtype {x.dtype}")
     F, K, hw = o.shape
     if x.numel() != F * hw * K:
         raise ValueError("x does not hold F * hw rows of K channels")
@@ -877,7 +880,8 @@ def gdn_proj_out_xgate(o: torch.Tensor, x: torch.Tensor, norm: str, norm_scale: 
     out = torch.empty((F * hw, N), dtype=od, device=o.device)
     ns = _dev(norm_scale, "norm_scale", torch.float32).data_ptr() if norm_scale is not None else None
     nb = _dev(norm_bias, "norm_bias", torch.float32).data_ptr() if norm_bias is not None else None
-    _lib.call("cssm_gdn_proj_out_xgate", o.data_ptr(), _DTYPES[o.dtype], x.data_ptr(), F, hw, K, N, _NORMS[norm], ns,
+    _lib.call("cssm_gdn_proj_out_xgate", o.data_ptr(), _DTYPES[o.dtype], x.data_ptr(), _DTYPES[x.dtype], F, hw, K, N,
+              _NORMS[norm], ns,
               nb, gate_kernel.data_ptr(), gate_bias.data_ptr(), _ACTS[gate_act], kernel.data_ptr(), bias.data_ptr(),
               out.data_ptr(), _DTYPES[od], _stream())
     return out

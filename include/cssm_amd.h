@@ -34,8 +34,9 @@ extern "C" {
  * 4: scan_variant arguments of the GDN delta-rule entry points.
  * 5: cssm_im2col_same, cssm_gdn_proj_out_xgate.
  * 6: cssm_gated_gates_bwd.
- * 7: cssm_proj_in_gates. */
-#define CSSM_ABI_VERSION 7
+ * 7: cssm_proj_in_gates.
+ * 8: x_dtype argument of cssm_gdn_proj_out_xgate (fp32 layer input). */
+#define CSSM_ABI_VERSION 8
 
 typedef enum cssm_status {
   CSSM_OK = 0,
@@ -642,12 +643,12 @@ int cssm_gdn_proj_out(const void* o, const void* gate, int in_dtype, int F, int 
  * input instead of read: gate = act(x gate_kernel + gate_bias) (gate_proj,
  * cssm.py:4853-4859, act SiLU or sigmoid as output_gate_act), so gate_proj's
  * planes never reach HBM.
- *   x            (F * HW, K) channels-last bf16 layer input, 16-byte aligned
+ *   x, x_dtype   (F * HW, K) channels-last layer input, CSSM_F32 or CSSM_BF16, 16-byte aligned
  *   gate_kernel  (K, K) [gate_proj/kernel], gate_bias (K); gate_act 1 SiLU, 2 sigmoid
  * Other arguments as cssm_gdn_proj_out.  K <= 64, K % 8 == 0, N <= 64 and HW % 4 == 0
  * (cssm_gdn_proj_out_xgate_supported), else CSSM_ERR_UNSUPPORTED.
  */
-int cssm_gdn_proj_out_xgate(const void* o, int in_dtype, const void* x, int F, int HW, int K, int N, int norm,
+int cssm_gdn_proj_out_xgate(const void* o, int in_dtype, const void* x, int x_dtype, int F, int HW, int K, int N, int norm,
                             const float* norm_scale, const float* norm_bias, const float* gate_kernel,
                             const float* gate_bias, int gate_act, const float* kernel, const float* bias, void* out,
                             int out_dtype, void* stream);

@@ -33,7 +33,7 @@ def test_library_exports_every_declared_symbol():
 def test_abi_version_and_errors_without_gpu():
     from cssm_amd import _lib
     lib = _lib.load()
-    assert lib.cssm_abi_version() == _lib.ABI_VERSION == 7
+    assert lib.cssm_abi_version() == _lib.ABI_VERSION == 8
     assert lib.cssm_strerror(-1) == b"null pointer argument"
     # argument validation happens before any GPU work
     st = lib.cssm_gated_scan_fwd(None, None, None, 0, 1, 1, 1, 8, 8, None, None, 0, 0, None)
@@ -69,14 +69,16 @@ def test_abi_version_and_errors_without_gpu():
     assert lib.cssm_gdn_proj_out_xgate_supported(60, 60, 1024) == 0       # K % 8
     assert lib.cssm_gdn_proj_out_xgate_supported(64, 128, 1024) == 0      # N > 64
     assert lib.cssm_gdn_proj_out_xgate_supported(64, 64, 49) == 0         # H W % 4
-    st = lib.cssm_gdn_proj_out_xgate(p, 0, p, 2, 1024, 72, 64, 1, None, None, p, p, 1, p, p, p, 1, None)
+    st = lib.cssm_gdn_proj_out_xgate(p, 0, p, 1, 2, 1024, 72, 64, 1, None, None, p, p, 1, p, p, p, 1, None)
     assert st == -3 and b"K <= 64" in lib.cssm_last_error()
-    st = lib.cssm_gdn_proj_out_xgate(p, 0, p, 2, 1024, 64, 64, 1, None, None, p, p, 0, p, p, p, 1, None)
+    st = lib.cssm_gdn_proj_out_xgate(p, 0, p, 1, 2, 1024, 64, 64, 1, None, None, p, p, 0, p, p, p, 1, None)
     assert st == -4 and b"gate_act" in lib.cssm_last_error()
-    st = lib.cssm_gdn_proj_out_xgate(p, 0, p + 8, 2, 1024, 64, 64, 1, None, None, p, p, 1, p, p, p, 1, None)
+    st = lib.cssm_gdn_proj_out_xgate(p, 0, p + 8, 1, 2, 1024, 64, 64, 1, None, None, p, p, 1, p, p, p, 1, None)
     assert st == -5
-    st = lib.cssm_gdn_proj_out_xgate(p, 0, None, 2, 1024, 64, 64, 1, None, None, p, p, 1, p, p, p, 1, None)
+    st = lib.cssm_gdn_proj_out_xgate(p, 0, None, 1, 2, 1024, 64, 64, 1, None, None, p, p, 1, p, p, p, 1, None)
     assert st == -1
+    st = lib.cssm_gdn_proj_out_xgate(p, 0, p, 5, 2, 1024, 64, 64, 1, None, None, p, p, 1, p, p, p, 1, None)
+    assert st == -4 and b"dtypes" in lib.cssm_last_error()
     # the gates' adjoint: pointers, gate type, weights and alignment checked before any GPU work
     gp = _lib.GateParams()
     gp.gate_type, gp.activation = _lib.GATE_FACTORED, _lib.ACT_SOFTPLUS

@@ -542,27 +542,32 @@ def test_gdn_proj_out_norm_gate(mods):
 
 
 XGATE_CASES = [
-    # F, HW, K, N, norm, gate act, o dtype, out dtype: the C4 widths, narrower ones, a partial last
-    # row tile (F HW not a multiple of 128), LayerNorm and no norm, sigmoid, bf16 o and f32 out
-    (3, 1024, 64, 64, "rms", "silu", torch.float32, torch.bfloat16),
-    (5, 196, 64, 64, "layer", "sigmoid", torch.float32, torch.float32),
-    (2, 1024, 32, 48, "none", "silu", torch.bfloat16, torch.float32),
-    (7, 16, 16, 16, "rms", "sigmoid", torch.float32, torch.float32),
-    (3, 64, 40, 40, "layer", "silu", torch.bfloat16, torch.bfloat16),
+    # F, HW, K, N, norm, gate act, o dtype, out dtype, x dtype: the C4 widths, narrower ones, a partial
+    # last row tile (F HW not a multiple of 128), LayerNorm and no norm, sigmoid, bf16 o and f32 out;
+    # fp32 x (the C3 widths among them), whose fragments come straight from its rows
+    (3, 1024, 64, 64, "rms", "silu", torch.float32, torch.bfloat16, torch.bfloat16),
+    (5, 196, 64, 64, "layer", "sigmoid", torch.float32, torch.float32, torch.bfloat16),
+    (2, 1024, 32, 48, "none", "silu", torch.bfloat16, torch.float32, torch.bfloat16),
+    (7, 16, 16, 16, "rms", "sigmoid", torch.float32, torch.float32, torch.bfloat16),
+    (3, 64, 40, 40, "layer", "silu", torch.bfloat16, torch.bfloat16, torch.bfloat16),
+    (2, 16384, 64, 64, "rms", "silu", torch.float32, torch.float32, torch.float32),
+    (5, 196, 64, 64, "layer", "sigmoid", torch.float32, torch.float32, torch.float32),
+    (3, 64, 40, 40, "none", "silu", torch.float32, torch.bfloat16, torch.float32),
+    (7, 16, 16, 16, "rms", "sigmoid", torch.bfloat16, torch.float32, torch.float32),
 ]
 
 
-@pytest.mark.parametrize("F,HW,K,N,norm,gact,odt,outdt", XGATE_CASES,
-                         ids=[f"F{c[0]}_HW{c[1]}_K{c[2]}_N{c[3]}_{c[4]}_{c[5]}" for c in XGATE_CASES])
-def test_gdn_proj_out_xgate_matches_gate_planes(mods, F, HW, K, N, norm, gact, odt, outdt):
-    """The output projection computing gate_proj from the bf16 layer input against the float64 reference
+@pytest.mark.parametrize("F,HW,K,N,norm,gact,odt,outdt,xdt", XGATE_CASES,
+                         ids=[f"F{c[0]}_HW{c[1]}_K{c[2]}_N{c[3]}_{c[4]}_{c[5]}_x{str(c[8])[6:]}" for c in XGATE_CASES])
+def test_gdn_proj_out_xgate_matches_gate_planes(mods, F, HW, K, N, norm, gact, odt, outdt, xdt):
+    """The output projection computing gate_proj from the layer input against the float64 reference
     of norm(o) * act(x Wg + bg) then output_proj, and against the two-call path (the gate planes from a
     projection, then cssm_gdn_proj_out)."""
     _, S = mods
-    print_case(test="gdn_proj_out_xgate", F=F, HW=HW, K=K, N=N, norm=norm, gact=gact)
+    print_case(test="gdn_proj_out_xgate", F=F, HW=HW, K=K, N=N, norm=norm, gact=gact, x=xdt)
     rng = np.random.default_rng(31)
     o = _dev(rng.standard_normal((F, K, HW)), odt)
-    xb = _dev(rng.standard_normal((F * HW, K)), torch.bfloat16)
+    xb = _dev(rng.standard_normal((F * HW, K)), xdt)
     Wg = rng.standard_normal((K, K)) / np.sqrt(K)
     bg = rng.standard_normal(K) * 0.1
     Wt = rng.standard_normal((K, N)) / np.sqrt(K)
