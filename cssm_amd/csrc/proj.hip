@@ -882,8 +882,8 @@ proj_persist_kernel(const TI* __restrict__ A, int M, int K, int N, const float* 
     else if constexpr (NSPLIT) fetch_gm(tile);
     else if (NORM) fetch(Gp, tile, pg);
   }
+  if (tile < tiles) xf_fetch(tile);
   for (; tile < tiles; tile = tile_of(++kt_)) {
-    xf_fetch(tile);
     __syncthreads();            // previous tile is done with As, Xs, gsh (and Bs is staged)
     stash(pf);
     stash_x();
@@ -902,6 +902,7 @@ proj_persist_kernel(const TI* __restrict__ A, int M, int K, int N, const float* 
     if (next < tiles) {
       fetch(A, next, pf);
       fetch_gates(next);
+      xf_fetch(next);   // XF: the x fragments were consumed by xgate_mma above
       if constexpr (XG) fetch_x(next);
       else if constexpr (NSPLIT) fetch_gm(next);
       else if (NORM) fetch(Gp, next, pg);
