@@ -1847,7 +1847,7 @@ qkv_fseq_kernel(const TI* __restrict__ A, int T, int HW, int K, int N, const flo
   constexpr unsigned kDrop = 0x80000000u;        // a buffer offset past every resource's range
   __shared__ __attribute__((aligned(16))) __bf16 Asm[APL * TM * KP];
   __shared__ __attribute__((aligned(16))) float qcw[CBW * TN * 8];
-  __shared__ float2 gsh[TM];
+  __shared__ __attribute__((aligned(16))) float2 gsh[TM];   // 16-byte reads of 2 pixels' gates
   __bf16* const A1 = Asm;
   __bf16* const A2 = A1 + (APL > 1 ? TM * KP : 0);
   __bf16* const A3 = A2 + (APL > 1 ? TM * KP : 0);
@@ -2073,36 +2073,18 @@ qkv_fseq_kernel(const TI* __restrict__ A, int T, int HW, int K, int N, const flo
           store(i, v);
         }
       } else {
-        const bool gated = blk != 0;
-        // the lane's input gate: component 0 (B_k) of a k column, 1 (B_v) of a v column
-        const float* const gcomp = reinterpret_cast<const float*>(gsh) + (blk == 1 ? 0 : 1);
-#pragma unroll
-        for (int i = 0; i < MI; ++i) {
-          float v[4];
-#pragma unroll
-          for (int r = 0; r < 4; ++r) {
-            const float x = acc[i][j][r] + bv;
-            float y = x;
-            if (qp.kt > 0) {
-              // the tiled epilogue's order: tap 0 and the conv bias, then the taps on t-3, t-2, t-1
-              // (frames before the first are the zero padding, held as zeros)
-              float o = fmaf(w4.x, x, bt);
-              o = fmaf(w4.w, hs[P][i][j][r], o);
-              o = fmaf(w4.z, hs[(P + 1) % 3][i][j][r], o);
-              o = fmaf(w4.y, hs[(P + 2) % 3][i][j][r], o);
-              y = o * __builtin_amdgcn_rcpf(1.0f + __expf(-o));   // SiLU as gdn_qkv_post computes it
-            }
-            hs[P][i][j][r] = x;   // frame t becomes the next phase's t-1
-            v[r] = y;
-          }
+        const bool gated = blk != 0, kcol = blk == 1;
+        // the lane's input gates: component 0 (B_k) for a k column, 1 (B_v) for a v column, none for q.
+        // The (B_k, B_v) pairs of the lane's 4 pixels are two 16-byte LDS reads, issued by every lane and
+        // then selected (no branch around the reads, and no wait between them)
+        auto in_gate = [&](int i, float (&v)[4]) {
           if (tile_gates) {
-            const float* gp = gcomp + 2 * (i * 16 + (lane >> 4) * 4);
+            const float4* gp = reinterpret_cast<const float4*>(gsh + i * 16 + (lane >> 4) * 4);
+            const float4 g01 = gp[0], g23 = gp[1];
+            const float g[4] = {kcol ? g01.x : g01.y, kcol ? g01.z : g01.w, kcol ? g23.x : g23.y,
+                                kcol ? g23.z : g23.w};
 #pragma unroll
-            for (int r = 0; r < 4; ++r) {
-              float g = gp[2 * r];   // loaded for every lane, then selected
-              asm volatile("" : "+v"(g));
-              v[r] *= gated ? g : 1.0f;
-            }
+            for (int r = 0; r < 4; ++r) v[r] *= gated ? g[r] : 1.0f;
           } else if (qp.gate_mode == 3 && gated) {
             const float4 gg = *reinterpret_cast<const float4*>(
                 static_cast<const float*>(qp.gates) + (fr * 2 * C + size_t(egch[j])) * HW + size_t(pb) * TM + i * 16 +
@@ -2112,7 +2094,35 @@ qkv_fseq_kernel(const TI* __restrict__ A, int T, int HW, int K, int N, const flo
             v[2] *= gg.z;
             v[3] *= gg.w;
           }
-          store(i, v);
+        };
+        if (qp.kt > 0) {
+#pragma unroll
+          for (int i = 0; i < MI; ++i) {
+            float v[4];
+#pragma unroll
+            for (int r = 0; r < 4; ++r) {
+              const float x = acc[i][j][r] + bv;
+              // the tiled epilogue's order: tap 0 and the conv bias, then the taps on t-3, t-2, t-1
+              // (frames before the first are the zero padding, held as zeros)
+              float o = fmaf(w4.x, x, bt);
+              o = fmaf(w4.w, hs[P][i][j][r], o);
+              o = fmaf(w4.z, hs[(P + 1) % 3][i][j][r], o);
+              o = fmaf(w4.y, hs[(P + 2) % 3][i][j][r], o);
+              v[r] = o * __builtin_amdgcn_rcpf(1.0f + __expf(-o));   // SiLU as gdn_qkv_post computes it
+              hs[P][i][j][r] = x;   // frame t becomes the next phase's t-1
+            }
+            in_gate(i, v);
+            store(i, v);
+          }
+        } else {
+#pragma unroll
+          for (int i = 0; i < MI; ++i) {
+            float v[4];
+#pragma unroll
+            for (int r = 0; r < 4; ++r) v[r] = acc[i][j][r] + bv;
+            in_gate(i, v);
+            store(i, v);
+          }
         }
       }
     }
