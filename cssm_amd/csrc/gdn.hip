@@ -1556,8 +1556,13 @@ dwconv_cl_blocked(const TI* __restrict__ x, int H, int W, int C, const float* __
       kws[j] = *reinterpret_cast<const float4*>(kw + 4 * j);
     __syncthreads();
   }
-  // frame blockIdx.y; (row group, column quad, channel quad) from 32-bit index arithmetic
-  const int i = int(blockIdx.x) * int(blockDim.x) + int(threadIdx.x);
+  // frame blockIdx.y; (row group, column quad, channel quad) from 32-bit index arithmetic.  The
+  // dispatcher deals the blocks of a launch round-robin over the 8 XCDs (each with its own L2), so with
+  // a multiple of 8 blocks per frame, XCD k runs blocks k, k + 8, ...: they take the contiguous logical
+  // blocks k n / 8 .. (k + 1) n / 8 - 1, whose row groups share their halo rows through that L2
+  const int nb = int(gridDim.x), bx = int(blockIdx.x);
+  const int blk = nb % 8 == 0 ? (bx % 8) * (nb / 8) + bx / 8 : bx;
+  const int i = blk * int(blockDim.x) + int(threadIdx.x);
   if (i >= per_frame) return;
   const int cq = i % CG, c0 = cq * 4;
   const int t1 = i / CG;
@@ -1630,7 +1635,7 @@ dwconv_cl_blocked(const TI* __restrict__ x, int H, int W, int C, const float* __
         sum.z += v.z;
         sum.w += v.w;
       }
-      *reinterpret_cast<float4*>(part + (f * gridDim.x + blockIdx.x) * C + 4 * threadIdx.x) = sum;
+      *reinterpret_cast<float4*>(part + (f * gridDim.x + blk) * C + 4 * threadIdx.x) = sum;
     }
   }
 }
