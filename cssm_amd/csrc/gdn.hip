@@ -182,6 +182,27 @@ struct SpecRegOp {
   }
 };
 
+// inverse policy of the persistent 128 x 128 inverse: interior bins from SpecBins, the DC / Nyquist columns
+// from an LDS stage est[(pl H + u) 2 + (v ? 1 : 0)] that holds them already scaled (see irfft2_planes)
+template <class G>
+struct SpecRegEdgeOp {
+  static constexpr bool kPackedColumnToo = false;
+  static constexpr int H = G::H, H2 = G::H2;
+  const SpecBins<G>& b;
+  float scale;
+  const float2* est;
+  __device__ __forceinline__ void bins(int j, int a2, int, int, int, float2 (&sp)[G::H2]) const {
+#pragma unroll
+    for (int q = 0; q < H2; ++q) sp[q] = make_float2(b.c[j][a2][q].x * scale, b.c[j][a2][q].y * scale);
+  }
+  __device__ __forceinline__ void edge(int, int pl, int uA, int uB, int, float2 (&v4)[4]) const {
+    v4[0] = est[(pl * H + uA) * 2];
+    v4[1] = est[(pl * H + uA) * 2 + 1];
+    v4[2] = est[(pl * H + uB) * 2];
+    v4[3] = est[(pl * H + uB) * 2 + 1];
+  }
+};
+
 // rfft2 of NP planes per group: x (P, H, W) real -> spec (P, H, WF), norms (P) = sum |X|^2 or skipped.
 // The last group may hold fewer than NP planes: the missing ones are neither read nor written.
 // Persistent: workgroup b transforms groups b, b + gridDim.x, ...  Where a wave's rows lie in one
@@ -299,12 +320,42 @@ irfft2_planes(const float2* __restrict__ spec, long long P, void* __restrict__ y
   const int w = __builtin_amdgcn_readfirstlane(int(tid) / 64), l = int(tid) % 64;
   const long long NG = (P + NP - 1) / NP;
   const float scale = 1.0f / float(H * W);
+  auto nvalid_of = [&](long long g) { return int(P - g * NP < NP ? P - g * NP : NP); };
+  // 128 x 128: the next group's DC / Nyquist columns (u, 0) and (u, W/2), 2 H NP values, are loaded one per
+  // lane after the current group's I2 pass and staged (scaled) in LDS at its end. Read in the edge pass
+  // instead, a group after their lines came through L2 with the interior bins, they were fetched from HBM
+  // again (issued with the interior bins, the extra VGPRs cost what the saved traffic gained).
+  constexpr bool EST = PF && LH == 7;
+  constexpr int NEV = 2 * H * NP;
+  static_assert(!EST || NEV <= G::NT, "one staged DC / Nyquist value per lane");
+  __shared__ float2 estage[EST ? NEV : 1];
+  float2 ev = make_float2(0.f, 0.f);
+  auto fetch_edge = [&](long long g) {
+    if constexpr (EST) {
+      const int e = int(tid);
+      if (e < NEV) {
+        const int pl = e / (2 * H), u = (e >> 1) % H;
+        ev = pl < nvalid_of(g) ? spec[(size_t(g) * NP + pl) * H * WF + size_t(u) * WF + ((e & 1) ? WF - 1 : 0)]
+                               : make_float2(0.f, 0.f);
+      }
+    }
+  };
+  auto stage_edge = [&]() {
+    if constexpr (EST) {
+      if (int(tid) < NEV) estage[tid] = make_float2(ev.x * scale, ev.y * scale);
+    }
+  };
   fft.init_twiddles(tid);
+  if constexpr (EST) {
+    if ((long long)blockIdx.x < NG) {
+      fetch_edge(blockIdx.x);
+      stage_edge();
+    }
+  }
   __syncthreads();
   const auto m = G::v4_lane(l);
   const auto col = PlaneFft<G>::v4_col(m.c4);
   SpecBins<G> bins;
-  auto nvalid_of = [&](long long g) { return int(P - g * NP < NP ? P - g * NP : NP); };
   auto group = [&](long long g) {
     const size_t p0 = size_t(g) * NP;
     const int nvalid = nvalid_of(g);
@@ -312,7 +363,14 @@ irfft2_planes(const float2* __restrict__ spec, long long P, void* __restrict__ y
     int ll = l;   // re-derived per group, as in rfft2_planes
     asm volatile("" : "+v"(ll));
     __builtin_assume(ll >= 0 && ll < 64);
-    if constexpr (PF) {
+    if constexpr (EST) {
+      const SpecRegEdgeOp<G> op{bins, scale, estage};
+      fft.template c2<false, true>(w, ll, op);
+      if (g + gridDim.x < NG) {
+        bins.fetch(spec + (g + gridDim.x) * NP * H * WF, nvalid_of(g + gridDim.x), w, l);
+      }
+      fft.template edges<false, true>(w, ll, op);
+    } else if constexpr (PF) {
       const SpecRegOp<G> op{bins, SpecLoadOp<G>{spec + p0 * H * WF, scale, nvalid}};
       fft.template c2<false, true>(w, ll, op);
       if (g + gridDim.x < NG) bins.fetch(spec + (g + gridDim.x) * NP * H * WF, nvalid_of(g + gridDim.x), w, l);
@@ -324,6 +382,7 @@ irfft2_planes(const float2* __restrict__ spec, long long P, void* __restrict__ y
     }
     fft.i1_packed(w, ll);
     fft.i2(w, ll);
+    if (g + gridDim.x < NG) fetch_edge(g + gridDim.x);
     fft.i3(w, ll);
     fft.i4(w, ll);
     V4* dst = reinterpret_cast<V4*>(static_cast<TE*>(y) + p0 * H * W);
@@ -333,6 +392,9 @@ irfft2_planes(const float2* __restrict__ spec, long long P, void* __restrict__ y
       const unsigned f = G::v4_index(row, m);
       if (f < nv4) dst[f] = IO::from_f4(fft.v4_get(row, col));
     }
+    // the next group's DC / Nyquist columns (the edge pass, the only reader, finished before the I2 -> I3
+    // barrier); the last group stages values no group reads
+    stage_edge();
     __syncthreads();   // the stores have read the plane buffer before the next group's C2 writes it
   };
   if constexpr (PF) {
