@@ -1835,7 +1835,8 @@ hipError_t launch_proj_in(const void* X, int in_dtype, int M, int K, int N, cons
 constexpr int kFseqTM = 64;
 // CBW 128-column blocks per workgroup (4 waves each) share one staged A tile: A is read from HBM
 // once for all of them (separate workgroups per column block drift apart and miss in L2)
-template <int CBW, class TI, class TO>
+// GC: the launch has gate_proj columns (qp.ng > 0); false compiles out their stores
+template <int CBW, class TI, class TO, bool GC = true>
 __global__ void __launch_bounds__(256 * CBW, 2 / CBW)
 qkv_fseq_kernel(const TI* __restrict__ A, int T, int HW, int K, int N, const float* __restrict__ Wt,
                 const float* __restrict__ bias, int nseq, TO* __restrict__ out, QkvPost qp) {
@@ -2054,11 +2055,12 @@ qkv_fseq_kernel(const TI* __restrict__ A, int T, int HW, int K, int N, const flo
       const float2 bb2 = *reinterpret_cast<const float2*>(&qcw[cl * 8 + 4]);
       const float bv = bb2.x, bt = bb2.y;
       // every lane issues the same stores: a lane whose column is in neither output has both offsets
-      // at kDrop, and the gv store with no gate columns hits an empty range
+      // at kDrop.  Without gate columns (GC false) the gv store is not compiled: issued to an empty range
+      // it still took its turn in the memory pipeline (C4 qkv 0.96 -> 0.89 ms without it)
       auto store = [&](int i, const float* v) {
         const unsigned po = pxo + unsigned(i * 16) * sizeof(TO);
         bst4(ro, eo[j] + po, v, out);
-        bst4(rg, eg[j] + po, v, out);
+        if constexpr (GC) bst4(rg, eg[j] + po, v, out);
       };
       if (blk == 3) {
 #pragma unroll
@@ -2207,8 +2209,12 @@ static void launch_qkv_fseq(const void* X, int B, int T, int HW, int K, int N, c
   const int cy = (cb + 1) / 2;
   const int slots = cu_count() / cy > 0 ? cu_count() / cy : 1;
   const dim3 grid(unsigned(nseq < slots ? nseq : slots), unsigned(cy));
-  hipLaunchKernelGGL((qkv_fseq_kernel<2, TI, TO>), grid, dim3(512), 0, s, static_cast<const TI*>(X), T, HW, K, N, W,
-                     b, nseq, static_cast<TO*>(out), qp);
+  if (qp.ng > 0)
+    hipLaunchKernelGGL((qkv_fseq_kernel<2, TI, TO>), grid, dim3(512), 0, s, static_cast<const TI*>(X), T, HW, K, N, W,
+                       b, nseq, static_cast<TO*>(out), qp);
+  else
+    hipLaunchKernelGGL((qkv_fseq_kernel<2, TI, TO, false>), grid, dim3(512), 0, s, static_cast<const TI*>(X), T, HW, K,
+                       N, W, b, nseq, static_cast<TO*>(out), qp);
 }
 
 hipError_t launch_gdn_qkv_proj(const void* X, int in_dtype, int B, int T, int HW, int K, int C, const float* W,
